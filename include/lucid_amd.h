@@ -1,0 +1,76 @@
+/*
+ * lucid_amd -- C ABI of the MI355X (gfx950) LUCID attention kernels.
+ *
+ * Plain pointers and sizes only; every buffer is caller-owned device memory
+ * (the library never allocates).  Tensors are bf16 with the last (head_dim)
+ * axis contiguous; the other axes are described by element strides
+ * {batch, head, time}.  All launches go on `stream` (a hipStream_t, NULL =
+ * default stream); calls are asynchronous.  Return value: 0 on success,
+ * LUCID_EINVAL for a rejected argument (text in lucid_last_error()), or
+ * LUCID_EHIP + hipError_t for a HIP launch failure.
+ *
+ * Supported: head_dim D in {64, 128}; T a multiple of 128 (the Python layer
+ * zero-pads the sequence end, which leaves every real row unchanged because
+ * both P and the attention mask are causal); Hq a multiple of Hkv (GQA).
+ */
+#ifndef LUCID_AMD_H
+#define LUCID_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LUCID_OK 0
+#define LUCID_EINVAL 1
+#define LUCID_EHIP 1000
+
+/* ABI version of this header (bumped on any signature change). */
+int lucid_abi_version(void);
+
+/* Text of the last error on the calling thread ("" if none). */
+const char* lucid_last_error(void);
+
+/* Bytes of the forward workspace.  It holds the state the backward reuses
+ * (1/rms of K, K^T and V' in MFMA operand layouts, the inverted 64x64
+ * diagonal blocks of P, chain counters), so keep it alive until
+ * lucid_attn_bwd has been enqueued. */
+size_t lucid_fwd_workspace_bytes(int B, int Hq, int Hkv, int T, int D);
+
+/* Preconditioned values only: vprime = P^-1 V, fp32 [B, Hkv, T, D] contiguous.
+ * Replaces LucidAttention.get_v_prime (modeling_lucid.py:551-574), both its
+ * dense branch (:561-570) and Lucid_Tril_Solver.forward (:284-312). */
+int lucid_get_v_prime(const void* k, const int64_t* k_strides, const void* v, const int64_t* v_strides,
+                      float* vprime, void* fwd_ws, int B, int Hkv, int T, int D, float scale, float eps,
+                      void* stream);
+
+/* Full forward O = softmax(s Q K^T, causal) P^-1 V.
+ * q [B,Hq,T,D], k/v [B,Hkv,T,D] (strided), o [B,T,Hq,D] or any strided layout,
+ * vprime fp32 [B,Hkv,T,D] contiguous (output), lse fp32 [B,Hq,T] (output,
+ * log2-domain row normaliser, needed by the backward).
+ * Replaces get_v_prime + eager_lucid_attention_forward
+ * (modeling_lucid.py:461-496 -> :551-574 and :505-549). */
+int lucid_attn_fwd(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                   const void* v, const int64_t* v_strides, void* o, const int64_t* o_strides, float* vprime,
+                   float* lse, void* fwd_ws, int B, int Hq, int Hkv, int T, int D, float scale, float eps,
+                   void* stream);
+
+/* Bytes of the backward scratch workspace. */
+size_t lucid_bwd_workspace_bytes(int B, int Hq, int Hkv, int T, int D);
+
+/* Gradients of sum(O * dO) w.r.t. q, k, v (bf16, strided outputs).
+ * Replaces the autograd of the dense path and Lucid_Tril_Solver.backward
+ * (modeling_lucid.py:314-382) together with the SDPA backward. */
+int lucid_attn_bwd(const void* dout, const int64_t* do_strides, const void* q, const int64_t* q_strides,
+                   const void* k, const int64_t* k_strides, const void* o, const int64_t* o_strides,
+                   const float* lse, const void* fwd_ws, void* dq, const int64_t* dq_strides, void* dk,
+                   const int64_t* dk_strides, void* dv, const int64_t* dv_strides, void* bwd_ws, int B, int Hq,
+                   int Hkv, int T, int D, float scale, float eps, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LUCID_AMD_H */

@@ -1,0 +1,16 @@
+"""lucid_amd -- LUCID attention and LUCID-Path for AMD MI355X (gfx950) on hand-written HIP kernels.
+
+Operator entry points (drop-ins for the reference seams):
+
+* :func:`lucid_amd.lucid.lucid_attention` / :func:`lucid_amd.lucid.get_v_prime` /
+  :func:`lucid_amd.lucid.eager_lucid_attention_forward` (modeling_lucid.py operator part)
+* :class:`lucid_amd.modeling.LucidAttention` (modeling_lucid.py LucidAttention module)
+"""
+from .lucid import LucidAttentionFunction, eager_lucid_attention_forward, get_v_prime, lucid_attention
+
+__all__ = [
+    "LucidAttentionFunction",
+    "eager_lucid_attention_forward",
+    "get_v_prime",
+    "lucid_attention",
+]

@@ -1,0 +1,83 @@
+"""ctypes binding of ``liblucid_amd.so`` (C ABI declared in include/lucid_amd.h).
+
+The library is loaded after ``torch`` so that it shares torch's HIP runtime.
+There is no fallback: if the library is missing or a call fails, an exception
+is raised.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch  # noqa: F401  (loads the HIP runtime the library links against)
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIBS: dict[str, ctypes.CDLL] = {}
+
+LUCID_EINVAL = 1
+LUCID_EHIP = 1000
+
+_vp = ctypes.c_void_p
+_i64p = ctypes.POINTER(ctypes.c_int64)
+_int = ctypes.c_int
+_flt = ctypes.c_float
+_sz = ctypes.c_size_t
+
+_SIGS = {
+    "liblucid_amd.so": {
+        "lucid_abi_version": ([], _int),
+        "lucid_last_error": ([], ctypes.c_char_p),
+        "lucid_fwd_workspace_bytes": ([_int] * 5, _sz),
+        "lucid_bwd_workspace_bytes": ([_int] * 5, _sz),
+        "lucid_get_v_prime": ([_vp, _i64p, _vp, _i64p, _vp, _vp, _int, _int, _int, _int, _flt, _flt, _vp], _int),
+        "lucid_attn_fwd": ([_vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _vp, _vp,
+                            _int, _int, _int, _int, _int, _flt, _flt, _vp], _int),
+        "lucid_attn_bwd": ([_vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _vp,
+                            _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp,
+                            _int, _int, _int, _int, _int, _flt, _flt, _vp], _int),
+    },
+}
+
+
+def lib_path(name: str = "liblucid_amd.so") -> str:
+    return os.path.join(_HERE, name)
+
+
+def load(name: str = "liblucid_amd.so") -> ctypes.CDLL:
+    """Load (once) and return the named HIP library; raises if it was not built."""
+    if name in _LIBS:
+        return _LIBS[name]
+    path = lib_path(name)
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is missing: build it with `python -m lucid_amd.build` "
+                           "(there is no CPU fallback)")
+    lib = ctypes.CDLL(path)
+    for fn, (args, res) in _SIGS[name].items():
+        f = getattr(lib, fn)
+        f.argtypes = args
+        f.restype = res
+    _LIBS[name] = lib
+    return lib
+
+
+def check(lib: ctypes.CDLL, rc: int, what: str) -> None:
+    if rc == 0:
+        return
+    msg = lib.lucid_last_error().decode(errors="replace") if hasattr(lib, "lucid_last_error") else ""
+    if rc == LUCID_EINVAL:
+        raise ValueError(f"{what}: {msg}")
+    raise RuntimeError(f"{what} failed (code {rc}): {msg}")
+
+
+def strides3(t: torch.Tensor, dims: tuple[int, int, int]):
+    """Element strides of three axes of ``t`` as a ctypes int64[3]."""
+    arr = (ctypes.c_int64 * 3)(*(t.stride(d) for d in dims))
+    return arr
+
+
+def ptr(t: torch.Tensor) -> ctypes.c_void_p:
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def stream_handle(device: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)

@@ -1,0 +1,573 @@
+// LUCID attention backward on CDNA4 (gfx950).
+//
+// Attention part (FlashAttention-2 style, recomputing P from lse):
+//   dV'_j = sum_i P_ij dO_i,  dS = P (dO V'^T - delta),  dK_attn = s dS^T Q,  dQ = s dS K
+// Preconditioner part (modeling_lucid.py:314-382, Lucid_Tril_Solver.backward):
+//   dV  = P^-T dV'                      (chained upper solve, last block first)
+//   M   = tril((dV V'^T) * P)
+//   dK^ = -s (M K^ + M^T K^),  dK = r (dK^ - K^ (K^.dK^)/d) + dK_attn   (RMSNorm backward)
+//
+// Kernels:
+//   lucid_bwd_prep_kernel          delta = rowsum(dO * O), dO^T and Q^T in T-perm layout
+//   lucid_attn_bwd_dkdv_kernel     column sweep: dV' (summed over the GQA group), dK_attn
+//   lucid_attn_bwd_dq_kernel       row sweep: dQ
+//   lucid_precond_bwd_col_kernel   chained transposed solve -> dV, and the M^T K^ column sums
+//   lucid_precond_bwd_row_kernel   M K^ row sums, RMSNorm backward, dK
+#include "lucid_common.h"
+
+namespace lucid {
+
+// grid (T/64, B*Hq)
+template <int D>
+__global__ __launch_bounds__(256) void lucid_bwd_prep_kernel(const bf16* __restrict__ dout, Strides dos,
+                                                             const bf16* __restrict__ o, Strides os,
+                                                             const bf16* __restrict__ q, Strides qs, int Hq, int T,
+                                                             float* __restrict__ delta, bf16* __restrict__ dot,
+                                                             bf16* __restrict__ qt, int* __restrict__ counters,
+                                                             int BH) {
+  constexpr int SEG = D / 4;
+  __shared__ bf16 tdo[D][64 + 8];
+  __shared__ bf16 tq[D][64 + 8];
+  const int blk = blockIdx.x, bhq = blockIdx.y;
+  const int b = bhq / Hq, hq = bhq - b * Hq;
+  const int tid = threadIdx.x;
+  const int row = tid >> 2, seg = tid & 3;
+  const int t = blk * 64 + row;
+  const bf16* dop = dout + b * dos.b + hq * dos.h + (int64_t)t * dos.t;
+  const bf16* opp = o + b * os.b + hq * os.h + (int64_t)t * os.t;
+  const bf16* qp = q + b * qs.b + hq * qs.h + (int64_t)t * qs.t;
+  float acc = 0.f;
+#pragma unroll
+  for (int c = 0; c < SEG; c += 8) {
+    const bf16x8 a = ld8(dop + seg * SEG + c);
+    const bf16x8 bo = ld8(opp + seg * SEG + c);
+    const bf16x8 qq = ld8(qp + seg * SEG + c);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      acc += (float)a[e] * (float)bo[e];
+      tdo[seg * SEG + c + e][row] = a[e];
+      tq[seg * SEG + c + e][row] = qq[e];
+    }
+  }
+  acc += __shfl_xor(acc, 1, 64);
+  acc += __shfl_xor(acc, 2, 64);
+  if (seg == 0) delta[(int64_t)bhq * T + t] = acc;
+  if (blk == 0 && tid == 0 && bhq < BH) counters[bhq] = 0;
+  __syncthreads();
+  for (int idx = tid; idx < D * 8; idx += 256) {
+    const int dd = idx >> 3, c8 = idx & 7;
+    bf16x8 a, bq;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int src = (c8 >> 1) * 16 + jmap((c8 & 1) * 8 + e);
+      a[e] = tdo[dd][src];
+      bq[e] = tq[dd][src];
+    }
+    const int64_t off = ((int64_t)bhq * D + dd) * T + blk * 64 + c8 * 8;
+    *reinterpret_cast<bf16x8*>(dot + off) = a;
+    *reinterpret_cast<bf16x8*>(qt + off) = bq;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Column sweep for the attention part.  WG = 128 keys of one kv head
+// (lane <-> key j), loops over the G query heads of the group and over all
+// 64-row query tiles at or below the diagonal.
+//   S[i][j] = Q_i . K_j (D layout m = i, n = j), P = exp2(c S - lse2_i)
+//   dV'^T[d][j] += dO^T[d][i] P[i][j];  dP[i][j] = dO_i . V'_j
+//   dS = P (dP - delta_i);  dK^T[d][j] += Q^T[d][i] dS[i][j]
+// ---------------------------------------------------------------------------
+template <int D>
+__global__ __launch_bounds__(256) void lucid_attn_bwd_dkdv_kernel(
+    const bf16* __restrict__ q, Strides qs, const bf16* __restrict__ k, Strides ks, const bf16* __restrict__ vpb,
+    const bf16* __restrict__ dout, Strides dos, const bf16* __restrict__ qt, const bf16* __restrict__ dot,
+    const float* __restrict__ lse, const float* __restrict__ delta, float* __restrict__ dvp,
+    float* __restrict__ dka, int Hq, int Hkv, int T, int BH, float scale) {
+  constexpr int NDT = D / 32;
+  constexpr int NKS = D / 16;
+  const int id = blockIdx.x;
+  const int jb = id / BH, bh = id - (id / BH) * BH;
+  const int b = bh / Hkv, h = bh - b * Hkv;
+  const int G = Hq / Hkv;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int g = lane >> 5, l32 = lane & 31;
+  const int jmin = jb * 128 + w * 32;
+  const int jrow = jmin + l32;
+  const bf16* kh = k + b * ks.b + h * ks.h;
+  const float c = scale * LOG2E_F;
+
+  bf16x8 kb[NKS], vb[NKS];
+#pragma unroll
+  for (int s = 0; s < NKS; ++s) {
+    kb[s] = ld8(kh + (int64_t)jrow * ks.t + 16 * s + 8 * g);
+    vb[s] = ld8(vpb + ((int64_t)bh * T + jrow) * D + 16 * s + 8 * g);
+  }
+  f32x16 adv[NDT], adk[NDT];
+#pragma unroll
+  for (int t = 0; t < NDT; ++t) {
+    adv[t] = zero16();
+    adk[t] = zero16();
+  }
+  const int it0 = jmin / 64;
+  const int nt = T / 64;
+  for (int gi = 0; gi < G; ++gi) {
+    const int hq = h * G + gi;
+    const int bhq = b * Hq + hq;
+    const bf16* qh = q + b * qs.b + hq * qs.h;
+    const bf16* doh = dout + b * dos.b + hq * dos.h;
+    const bf16* qth = qt + (int64_t)bhq * D * T;
+    const bf16* doth = dot + (int64_t)bhq * D * T;
+    const float* lh = lse + (int64_t)bhq * T;
+    const float* dh = delta + (int64_t)bhq * T;
+    for (int it = it0; it < nt; ++it) {
+      const int i0 = it * 64;
+      const bool diag = (i0 < jmin + 32);
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        const int ib0 = i0 + mt * 32;
+        f32x16 s = zero16();
+#pragma unroll
+        for (int st = 0; st < NKS; ++st)
+          s = mfma32(ld8(qh + (int64_t)(ib0 + l32) * qs.t + 16 * st + 8 * g), kb[st], s);
+        float lr[16];
+        load_rows16(lh + ib0, g, lr);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          float p = exp2f(s[e] * c - lr[e]);
+          if (diag && (ib0 + drow(e, g) < jrow)) p = 0.f;
+          s[e] = p;
+        }
+        const bf16x8 p0 = pack_b(s, 0), p1 = pack_b(s, 1);
+#pragma unroll
+        for (int t = 0; t < NDT; ++t) {
+          const bf16* ap = doth + (int64_t)(t * 32 + l32) * T + ib0 + 8 * g;
+          adv[t] = mfma32(ld8(ap), p0, adv[t]);
+          adv[t] = mfma32(ld8(ap + 16), p1, adv[t]);
+        }
+        f32x16 dp = zero16();
+#pragma unroll
+        for (int st = 0; st < NKS; ++st)
+          dp = mfma32(ld8(doh + (int64_t)(ib0 + l32) * dos.t + 16 * st + 8 * g), vb[st], dp);
+        load_rows16(dh + ib0, g, lr);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) s[e] = s[e] * (dp[e] - lr[e]);
+        const bf16x8 d0 = pack_b(s, 0), d1 = pack_b(s, 1);
+#pragma unroll
+        for (int t = 0; t < NDT; ++t) {
+          const bf16* ap = qth + (int64_t)(t * 32 + l32) * T + ib0 + 8 * g;
+          adk[t] = mfma32(ld8(ap), d0, adk[t]);
+          adk[t] = mfma32(ld8(ap + 16), d1, adk[t]);
+        }
+      }
+    }
+  }
+  float* ov = dvp + ((int64_t)bh * T + jrow) * D;
+  float* ok = dka + ((int64_t)bh * T + jrow) * D;
+#pragma unroll
+  for (int t = 0; t < NDT; ++t)
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) {
+      f32x4 a, bq;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        a[u] = adv[t][4 * qq + u];
+        bq[u] = adk[t][4 * qq + u] * scale;
+      }
+      *reinterpret_cast<f32x4*>(ov + t * 32 + 8 * qq + 4 * g) = a;
+      *reinterpret_cast<f32x4*>(ok + t * 32 + 8 * qq + 4 * g) = bq;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Row sweep for dQ.  WG = 128 query rows (lane <-> row i), heavy blocks first.
+//   S^T[j][i] = K_j . Q_i, dP^T[j][i] = V'_j . dO_i, dS^T = P^T (dP^T - delta_i)
+//   dQ^T[d][i] += K^T[d][j] dS^T[j][i]
+// ---------------------------------------------------------------------------
+template <int D>
+__global__ __launch_bounds__(256) void lucid_attn_bwd_dq_kernel(
+    const bf16* __restrict__ q, Strides qs, const bf16* __restrict__ k, Strides ks, const bf16* __restrict__ vpb,
+    const bf16* __restrict__ dout, Strides dos, const bf16* __restrict__ kt, const float* __restrict__ lse,
+    const float* __restrict__ delta, bf16* __restrict__ dq, Strides dqs, int Hq, int Hkv, int T, int BHq,
+    float scale) {
+  constexpr int NDT = D / 32;
+  constexpr int NKS = D / 16;
+  const int nblk = T / 128;
+  const int id = blockIdx.x;
+  const int bhq = id % BHq;
+  const int ib = nblk - 1 - id / BHq;
+  const int b = bhq / Hq, hq = bhq - b * Hq;
+  const int h = hq / (Hq / Hkv);
+  const int bh = b * Hkv + h;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int g = lane >> 5, l32 = lane & 31;
+  const int row0 = ib * 128 + w * 32;
+  const int irow = row0 + l32;
+  const bf16* kh = k + b * ks.b + h * ks.h;
+  const bf16* vh = vpb + (int64_t)bh * T * D;
+  const bf16* kth = kt + (int64_t)bh * D * T;
+  const float c = scale * LOG2E_F;
+
+  bf16x8 qb[NKS], db[NKS];
+#pragma unroll
+  for (int s = 0; s < NKS; ++s) {
+    qb[s] = ld8(q + b * qs.b + hq * qs.h + (int64_t)irow * qs.t + 16 * s + 8 * g);
+    db[s] = ld8(dout + b * dos.b + hq * dos.h + (int64_t)irow * dos.t + 16 * s + 8 * g);
+  }
+  const float li = lse[(int64_t)bhq * T + irow];
+  const float di = delta[(int64_t)bhq * T + irow];
+  f32x16 acc[NDT];
+#pragma unroll
+  for (int t = 0; t < NDT; ++t) acc[t] = zero16();
+  const int ntile = (row0 + 32 + 63) / 64;
+  for (int jt = 0; jt < ntile; ++jt) {
+    const int j0 = jt * 64;
+    const bool diag = (j0 + 63 > row0);
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      const int jb0 = j0 + mt * 32;
+      f32x16 s = zero16(), dp = zero16();
+#pragma unroll
+      for (int st = 0; st < NKS; ++st) {
+        s = mfma32(ld8(kh + (int64_t)(jb0 + l32) * ks.t + 16 * st + 8 * g), qb[st], s);
+        dp = mfma32(ld8(vh + (int64_t)(jb0 + l32) * D + 16 * st + 8 * g), db[st], dp);
+      }
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        float p = exp2f(s[e] * c - li);
+        if (diag && (jb0 + drow(e, g) > irow)) p = 0.f;
+        s[e] = p * (dp[e] - di);
+      }
+      const bf16x8 d0 = pack_b(s, 0), d1 = pack_b(s, 1);
+#pragma unroll
+      for (int t = 0; t < NDT; ++t) {
+        const bf16* ap = kth + (int64_t)(t * 32 + l32) * T + jb0 + 8 * g;
+        acc[t] = mfma32(ld8(ap), d0, acc[t]);
+        acc[t] = mfma32(ld8(ap + 16), d1, acc[t]);
+      }
+    }
+  }
+  bf16* op = dq + b * dqs.b + hq * dqs.h + (int64_t)irow * dqs.t;
+#pragma unroll
+  for (int t = 0; t < NDT; ++t)
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) {
+      bf16x4 bb;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) bb[u] = (bf16)(acc[t][4 * qq + u] * scale);
+      *reinterpret_cast<bf16x4*>(op + t * 32 + 8 * qq + 4 * g) = bb;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Chained transposed solve dV = P^-T dV' (Lucid_Tril_Solver.backward :328-334)
+// and the column sums C_J = sum_{I >= J} M_IJ^T K^_I.
+// WG id -> (J = NT-1 - id/BH, bh = id % BH): ids grow as J falls, so block J
+// waits only on later blocks that have lower ids.  Counter value n means
+// blocks NT-1 .. NT-n are published.
+// wave w: ch = w & 1 -> columns J0 + 32ch .. (lane <-> column),
+//         ih = w >> 1 -> rows I0 + 32ih .. of every later 64-row block.
+// ---------------------------------------------------------------------------
+template <int D>
+__global__ __launch_bounds__(256) void lucid_precond_bwd_col_kernel(
+    const bf16* __restrict__ k, Strides ks, int Hkv, int T, int BH, const float* __restrict__ rinv, float scale,
+    const bf16* __restrict__ kt, const bf16* __restrict__ vpb, const float* __restrict__ pinv,
+    const float* __restrict__ dvp, bf16* __restrict__ dvb, bf16* __restrict__ dvt, bf16* __restrict__ dv_out,
+    Strides dvs, float* __restrict__ colsum, int* __restrict__ counters) {
+  constexpr int NDT = D / 32;
+  constexpr int NKS = D / 16;
+  __shared__ __attribute__((aligned(16))) float Ps[64][68];    // P_JJ, lower
+  __shared__ __attribute__((aligned(16))) float Xt[64][68];    // Xt[c][r] = (P_JJ^-1)[r][c]
+  __shared__ __attribute__((aligned(16))) float Rt[D][68];     // reductions, R^T
+  __shared__ __attribute__((aligned(16))) bf16 dvl[64][D + 8]; // dV_J rows (bf16)
+
+  const int NT = T / 64;
+  const int id = blockIdx.x;
+  const int J = NT - 1 - id / BH, bh = id - (id / BH) * BH;
+  const int b = bh / Hkv, h = bh - b * Hkv;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int g = lane >> 5, l32 = lane & 31;
+  const int ch = w & 1, ih = w >> 1;
+  const int J0 = J * 64;
+  const int jcol = J0 + ch * 32 + l32;
+  const bf16* kh = k + b * ks.b + h * ks.h;
+  const float* rv = rinv + (int64_t)bh * T;
+  const bf16* kth = kt + (int64_t)bh * D * T;
+  const bf16* dvth = dvt + (int64_t)bh * D * T;
+  const bf16* dvbh = dvb + (int64_t)bh * T * D;
+  const float sl2 = scale * LOG2E_F;
+  const float c0 = LOG2E_F / scale;
+
+  bf16x8 kbJ[NKS], vbJ[NKS];
+#pragma unroll
+  for (int s = 0; s < NKS; ++s) {
+    kbJ[s] = ld8(kh + (int64_t)jcol * ks.t + 16 * s + 8 * g);
+    vbJ[s] = ld8(vpb + ((int64_t)bh * T + jcol) * D + 16 * s + 8 * g);
+  }
+  const float aJ = sl2 * rv[jcol];
+  {
+    f32x16 sd = zero16();
+#pragma unroll
+    for (int s = 0; s < NKS; ++s)
+      sd = mfma32(ld8(kh + (int64_t)(J0 + ih * 32 + l32) * ks.t + 16 * s + 8 * g), kbJ[s], sd);
+    const int n = ch * 32 + l32;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int m = ih * 32 + drow(e, g);
+      Ps[m][n] = (n <= m) ? exp2f(sd[e] * aJ * rv[J0 + m] - c0) : 0.f;
+    }
+  }
+  {
+    const float* xp = pinv + ((int64_t)bh * NT + J) * 4096;
+    for (int idx = tid; idx < 4096; idx += 256) Xt[idx & 63][idx >> 6] = xp[idx];
+  }
+
+  f32x16 adv[NDT], acs[NDT];
+#pragma unroll
+  for (int t = 0; t < NDT; ++t) {
+    adv[t] = zero16();
+    acs[t] = zero16();
+  }
+  int ready = 0;
+  for (int I = NT - 1; I > J; --I) {
+    const int need = NT - 1 - I;
+    if (need >= ready) ready = wait_counter_gt(counters + bh, need);
+    const int I0 = I * 64 + ih * 32;
+    f32x16 s = zero16(), gg = zero16();
+#pragma unroll
+    for (int st = 0; st < NKS; ++st) {
+      s = mfma32(ld8(kh + (int64_t)(I0 + l32) * ks.t + 16 * st + 8 * g), kbJ[st], s);
+      gg = mfma32(ld8(dvbh + (int64_t)(I0 + l32) * D + 16 * st + 8 * g), vbJ[st], gg);
+    }
+    float rI[16];
+    load_rows16(rv + I0, g, rI);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const float p = exp2f(s[e] * aJ * rI[e] - c0);
+      s[e] = p;
+      gg[e] = gg[e] * p * rI[e];
+    }
+    const bf16x8 p0 = pack_b(s, 0), p1 = pack_b(s, 1);
+    const bf16x8 m0 = pack_b(gg, 0), m1 = pack_b(gg, 1);
+#pragma unroll
+    for (int t = 0; t < NDT; ++t) {
+      const bf16* ap = dvth + (int64_t)(t * 32 + l32) * T + I0 + 8 * g;
+      adv[t] = mfma32(ld8(ap), p0, adv[t]);
+      adv[t] = mfma32(ld8(ap + 16), p1, adv[t]);
+      const bf16* kp = kth + (int64_t)(t * 32 + l32) * T + I0 + 8 * g;
+      acs[t] = mfma32(ld8(kp), m0, acs[t]);
+      acs[t] = mfma32(ld8(kp + 16), m1, acs[t]);
+    }
+  }
+
+  // ---- R_J = dV'_J - sum_{I>J} P_IJ^T dV_I (reduce the two row halves) ----
+  if (ih == 1) {
+#pragma unroll
+    for (int t = 0; t < NDT; ++t)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][ch * 32 + l32] = adv[t][e];
+  }
+  __syncthreads();
+  if (ih == 0) {
+    const float* src = dvp + ((int64_t)bh * T + jcol) * D;
+#pragma unroll
+    for (int t = 0; t < NDT; ++t)
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) {
+        const int d0 = t * 32 + 8 * qq + 4 * g;
+        const f32x4 x = *reinterpret_cast<const f32x4*>(src + d0);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          Rt[d0 + u][ch * 32 + l32] = x[u] - (adv[t][4 * qq + u] + Rt[d0 + u][ch * 32 + l32]);
+      }
+  }
+  __syncthreads();
+
+  // ---- dV^T[d][c] = sum_r R^T[d][r] X[r][c]  (X lower: r >= c) ----
+  for (int tile = w; tile < NDT * 2; tile += 4) {
+    const int dt = tile >> 1, chh = tile & 1;
+    f32x16 o = zero16();
+    for (int s = chh ? 2 : 0; s < 4; ++s) {
+      bf16x8 ah, al, bh8, bl;
+      split8(&Rt[dt * 32 + l32][16 * s + 8 * g], ah, al);
+      split8(&Xt[chh * 32 + l32][16 * s + 8 * g], bh8, bl);
+      o = mfma32(ah, bh8, o);
+      o = mfma32(ah, bl, o);
+      o = mfma32(al, bh8, o);
+    }
+    const int cl = chh * 32 + l32;
+    const int r = J0 + cl;
+    const int slot = (r & ~15) | jmap(r & 15);
+    bf16* ob = dvb + ((int64_t)bh * T + r) * D;
+    bf16* ou = dv_out + b * dvs.b + h * dvs.h + (int64_t)r * dvs.t;
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) {
+      const int d0 = dt * 32 + 8 * qq + 4 * g;
+      bf16x4 bb;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        bb[u] = (bf16)o[4 * qq + u];
+        vpth_w(dvt, bh, D, T, d0 + u, slot, bb[u]);
+        dvl[cl][d0 + u] = bb[u];
+      }
+      *reinterpret_cast<bf16x4*>(ob + d0) = bb;
+      *reinterpret_cast<bf16x4*>(ou + d0) = bb;
+    }
+  }
+  publish_counter(counters + bh, NT - J);
+
+  // ---- diagonal block of the column sums: M_JJ = tril((dV_J V'_J^T) * P_JJ) ----
+  {
+    f32x16 gg = zero16();
+#pragma unroll
+    for (int st = 0; st < NKS; ++st) gg = mfma32(ld8(&dvl[ih * 32 + l32][16 * st + 8 * g]), vbJ[st], gg);
+    float rr[16];
+    load_rows16(rv + J0 + ih * 32, g, rr);
+    const int n = ch * 32 + l32;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) gg[e] = gg[e] * Ps[ih * 32 + drow(e, g)][n] * rr[e];
+    const bf16x8 m0 = pack_b(gg, 0), m1 = pack_b(gg, 1);
+#pragma unroll
+    for (int t = 0; t < NDT; ++t) {
+      const bf16* kp = kth + (int64_t)(t * 32 + l32) * T + J0 + ih * 32 + 8 * g;
+      acs[t] = mfma32(ld8(kp), m0, acs[t]);
+      acs[t] = mfma32(ld8(kp + 16), m1, acs[t]);
+    }
+  }
+  __syncthreads();
+  if (ih == 1) {
+#pragma unroll
+    for (int t = 0; t < NDT; ++t)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][ch * 32 + l32] = acs[t][e];
+  }
+  __syncthreads();
+  if (ih == 0) {
+    float* dst = colsum + ((int64_t)bh * T + jcol) * D;
+#pragma unroll
+    for (int t = 0; t < NDT; ++t)
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) {
+        const int d0 = t * 32 + 8 * qq + 4 * g;
+        f32x4 x;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) x[u] = acs[t][4 * qq + u] + Rt[d0 + u][ch * 32 + l32];
+        *reinterpret_cast<f32x4*>(dst + d0) = x;
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Row sums R_I = sum_{J <= I} M_IJ K^_J, then dK^ = -s (R + C), RMSNorm
+// backward and the attention dK.  No chain: every dV is known.
+// wave w: ih = w & 1 -> rows (lane <-> row I), jh = w >> 1 -> key half.
+// ---------------------------------------------------------------------------
+template <int D>
+__global__ __launch_bounds__(256) void lucid_precond_bwd_row_kernel(
+    const bf16* __restrict__ k, Strides ks, int Hkv, int T, int BH, const float* __restrict__ rinv, float scale,
+    const bf16* __restrict__ kt, const bf16* __restrict__ vpb, const bf16* __restrict__ dvb,
+    const float* __restrict__ colsum, const float* __restrict__ dka, bf16* __restrict__ dk_out, Strides dks) {
+  constexpr int NDT = D / 32;
+  constexpr int NKS = D / 16;
+  __shared__ __attribute__((aligned(16))) float Rt[D][68];
+  const int NT = T / 64;
+  const int id = blockIdx.x;
+  const int I = NT - 1 - id / BH, bh = id - (id / BH) * BH;
+  const int b = bh / Hkv, h = bh - b * Hkv;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int g = lane >> 5, l32 = lane & 31;
+  const int ih = w & 1, jh = w >> 1;
+  const int irow = I * 64 + ih * 32 + l32;
+  const bf16* kh = k + b * ks.b + h * ks.h;
+  const float* rv = rinv + (int64_t)bh * T;
+  const bf16* kth = kt + (int64_t)bh * D * T;
+  const bf16* vh = vpb + (int64_t)bh * T * D;
+  const float sl2 = scale * LOG2E_F;
+  const float c0 = LOG2E_F / scale;
+
+  bf16x8 kbI[NKS], dbI[NKS];
+#pragma unroll
+  for (int s = 0; s < NKS; ++s) {
+    kbI[s] = ld8(kh + (int64_t)irow * ks.t + 16 * s + 8 * g);
+    dbI[s] = ld8(dvb + ((int64_t)bh * T + irow) * D + 16 * s + 8 * g);
+  }
+  const float ri = rv[irow];
+  const float aI = sl2 * ri;
+  f32x16 acc[NDT];
+#pragma unroll
+  for (int t = 0; t < NDT; ++t) acc[t] = zero16();
+  for (int J = 0; J <= I; ++J) {
+    const int J0 = J * 64 + jh * 32;
+    f32x16 s = zero16(), gg = zero16();
+#pragma unroll
+    for (int st = 0; st < NKS; ++st) {
+      s = mfma32(ld8(kh + (int64_t)(J0 + l32) * ks.t + 16 * st + 8 * g), kbI[st], s);
+      gg = mfma32(ld8(vh + (int64_t)(J0 + l32) * D + 16 * st + 8 * g), dbI[st], gg);
+    }
+    float rJ[16];
+    load_rows16(rv + J0, g, rJ);
+    const bool diag = (J == I);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      float p = exp2f(s[e] * aI * rJ[e] - c0);
+      if (diag && (J0 + drow(e, g) > irow)) p = 0.f;
+      gg[e] = gg[e] * p * rJ[e];
+    }
+    const bf16x8 m0 = pack_b(gg, 0), m1 = pack_b(gg, 1);
+#pragma unroll
+    for (int t = 0; t < NDT; ++t) {
+      const bf16* kp = kth + (int64_t)(t * 32 + l32) * T + J0 + 8 * g;
+      acc[t] = mfma32(ld8(kp), m0, acc[t]);
+      acc[t] = mfma32(ld8(kp + 16), m1, acc[t]);
+    }
+  }
+  if (jh == 1) {
+#pragma unroll
+    for (int t = 0; t < NDT; ++t)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][ih * 32 + l32] = acc[t][e];
+  }
+  __syncthreads();
+  if (jh == 0) {
+    const float* cs = colsum + ((int64_t)bh * T + irow) * D;
+    const float* da = dka + ((int64_t)bh * T + irow) * D;
+    const bf16* kr = kh + (int64_t)irow * ks.t;
+    float dkh[NDT][16], khat[NDT][16];
+    float dotp = 0.f;
+#pragma unroll
+    for (int t = 0; t < NDT; ++t)
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) {
+        const int d0 = t * 32 + 8 * qq + 4 * g;
+        const f32x4 cv = *reinterpret_cast<const f32x4*>(cs + d0);
+        const bf16x4 kv = *reinterpret_cast<const bf16x4*>(kr + d0);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int e = 4 * qq + u;
+          const float x = -scale * (acc[t][e] + Rt[d0 + u][ih * 32 + l32] + cv[u]);
+          const float kk = ri * (float)kv[u];
+          dkh[t][e] = x;
+          khat[t][e] = kk;
+          dotp += x * kk;
+        }
+      }
+    dotp += wave_xor32(dotp);
+    const float f = dotp / (float)D;
+    bf16* op = dk_out + b * dks.b + h * dks.h + (int64_t)irow * dks.t;
+#pragma unroll
+    for (int t = 0; t < NDT; ++t)
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) {
+        const int d0 = t * 32 + 8 * qq + 4 * g;
+        const f32x4 av = *reinterpret_cast<const f32x4*>(da + d0);
+        bf16x4 bb;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int e = 4 * qq + u;
+          bb[u] = (bf16)(ri * (dkh[t][e] - khat[t][e] * f) + av[u]);
+        }
+        *reinterpret_cast<bf16x4*>(op + d0) = bb;
+      }
+  }
+}
+
+}  // namespace lucid

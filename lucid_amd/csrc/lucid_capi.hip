@@ -1,0 +1,246 @@
+// C ABI of the LUCID attention kernels (declared in include/lucid_amd.h).
+// One translation unit: the kernel files are included so that every template
+// instantiation lives next to its launcher.
+#include <string>
+
+#include "../../include/lucid_amd.h"
+#include "lucid_bwd.hip"
+#include "lucid_fwd.hip"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(const std::string& msg) {
+  g_last_error = msg;
+  return LUCID_EINVAL;
+}
+
+int hip_status(const char* where) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    g_last_error = std::string(where) + ": " + hipGetErrorString(e);
+    return LUCID_EHIP + (int)e;
+  }
+  return LUCID_OK;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+// Forward workspace carve-out (all offsets 256-byte aligned).
+struct FwdWs {
+  float* rinv;   // [BH][T]
+  bf16* kt;      // [BH][D][T]  K^T, T-perm
+  bf16* vpb;     // [BH][T][D]  V' bf16
+  bf16* vpt;     // [BH][D][T]  V'^T, T-perm
+  float* pinv;   // [BH][T/64][64][64]  inverses of the diagonal blocks of P
+  int* counters; // [BH]
+  size_t bytes;
+};
+
+FwdWs carve_fwd(void* base, int B, int Hkv, int T, int D) {
+  const size_t BH = (size_t)B * Hkv;
+  FwdWs w{};
+  size_t off = 0;
+  char* p = static_cast<char*>(base);
+  auto take = [&](size_t n) {
+    char* r = p ? p + off : nullptr;
+    off += align256(n);
+    return r;
+  };
+  w.rinv = reinterpret_cast<float*>(take(BH * T * 4));
+  w.kt = reinterpret_cast<bf16*>(take(BH * D * T * 2));
+  w.vpb = reinterpret_cast<bf16*>(take(BH * T * D * 2));
+  w.vpt = reinterpret_cast<bf16*>(take(BH * D * T * 2));
+  w.pinv = reinterpret_cast<float*>(take(BH * (T / 64) * 4096 * 4));
+  w.counters = reinterpret_cast<int*>(take(BH * 4));
+  w.bytes = off;
+  return w;
+}
+
+struct BwdWs {
+  float* delta;  // [BHq][T]
+  bf16* dot;     // [BHq][D][T]  dO^T, T-perm
+  bf16* qt;      // [BHq][D][T]  Q^T, T-perm
+  float* dvp;    // [BH][T][D]   dV' (summed over the group)
+  float* dka;    // [BH][T][D]   dK from the softmax part (scaled)
+  bf16* dvb;     // [BH][T][D]   dV bf16
+  bf16* dvt;     // [BH][D][T]   dV^T, T-perm
+  float* colsum; // [BH][T][D]   sum_I M_IJ^T K^_I
+  int* counters; // [BH]
+  size_t bytes;
+};
+
+BwdWs carve_bwd(void* base, int B, int Hq, int Hkv, int T, int D) {
+  const size_t BH = (size_t)B * Hkv, BHq = (size_t)B * Hq;
+  BwdWs w{};
+  size_t off = 0;
+  char* p = static_cast<char*>(base);
+  auto take = [&](size_t n) {
+    char* r = p ? p + off : nullptr;
+    off += align256(n);
+    return r;
+  };
+  w.delta = reinterpret_cast<float*>(take(BHq * T * 4));
+  w.dot = reinterpret_cast<bf16*>(take(BHq * D * T * 2));
+  w.qt = reinterpret_cast<bf16*>(take(BHq * D * T * 2));
+  w.dvp = reinterpret_cast<float*>(take(BH * T * D * 4));
+  w.dka = reinterpret_cast<float*>(take(BH * T * D * 4));
+  w.dvb = reinterpret_cast<bf16*>(take(BH * T * D * 2));
+  w.dvt = reinterpret_cast<bf16*>(take(BH * D * T * 2));
+  w.colsum = reinterpret_cast<float*>(take(BH * T * D * 4));
+  w.counters = reinterpret_cast<int*>(take(BH * 4));
+  w.bytes = off;
+  return w;
+}
+
+int check_dims(int B, int Hq, int Hkv, int T, int D) {
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || T <= 0) return fail("B, Hq, Hkv and T must be positive");
+  if (D != 64 && D != 128) return fail("head_dim must be 64 or 128, got " + std::to_string(D));
+  if (T % 128 != 0) return fail("T must be a multiple of 128, got " + std::to_string(T));
+  if (Hq % Hkv != 0) return fail("Hq must be a multiple of Hkv");
+  if ((int64_t)B * Hq * (T / 128) > (int64_t)0x7fffffff) return fail("grid too large");
+  return LUCID_OK;
+}
+
+int check_tensor(const char* name, const void* p, const int64_t* s) {
+  if (!p) return fail(std::string(name) + " is null");
+  if (!s) return fail(std::string(name) + " strides are null");
+  if (reinterpret_cast<uintptr_t>(p) % 16) return fail(std::string(name) + " must be 16-byte aligned");
+  for (int i = 0; i < 3; ++i)
+    if (s[i] % 8) return fail(std::string(name) + " strides must be multiples of 8 elements");
+  return LUCID_OK;
+}
+
+lucid::Strides S(const int64_t* s) { return lucid::Strides{s[0], s[1], s[2]}; }
+
+template <int D>
+int launch_precond_fwd(const void* k, const int64_t* ks, const void* v, const int64_t* vs, float* vprime,
+                       const FwdWs& w, int B, int Hkv, int T, float scale, float eps, hipStream_t st) {
+  const int BH = B * Hkv;
+  hipLaunchKernelGGL(lucid::lucid_prep_kernel<D>, dim3(T / 64, BH), dim3(256), 0, st, (const bf16*)k, S(ks), Hkv,
+                     T, eps, w.rinv, w.kt, w.counters);
+  if (int rc = hip_status("lucid_prep_kernel")) return rc;
+  hipLaunchKernelGGL(lucid::lucid_precond_fwd_kernel<D>, dim3((T / 64) * BH), dim3(256), 0, st, (const bf16*)k,
+                     S(ks), (const bf16*)v, S(vs), Hkv, T, BH, w.rinv, scale, vprime, w.vpb, w.vpt, w.pinv,
+                     w.counters);
+  return hip_status("lucid_precond_fwd_kernel");
+}
+
+template <int D>
+int launch_fwd(const void* q, const int64_t* qs, const void* k, const int64_t* ks, const void* v, const int64_t* vs,
+               void* o, const int64_t* os, float* vprime, float* lse, const FwdWs& w, int B, int Hq, int Hkv, int T,
+               float scale, float eps, hipStream_t st) {
+  if (int rc = launch_precond_fwd<D>(k, ks, v, vs, vprime, w, B, Hkv, T, scale, eps, st)) return rc;
+  const int BHq = B * Hq;
+  hipLaunchKernelGGL(lucid::lucid_attn_fwd_kernel<D>, dim3((T / 128) * BHq), dim3(256), 0, st, (const bf16*)q,
+                     S(qs), (const bf16*)k, S(ks), w.vpt, (bf16*)o, S(os), lse, Hq, Hkv, T, BHq, scale);
+  return hip_status("lucid_attn_fwd_kernel");
+}
+
+template <int D>
+int launch_bwd(const void* dout, const int64_t* dos, const void* q, const int64_t* qs, const void* k,
+               const int64_t* ks, const void* o, const int64_t* os, const float* lse, const FwdWs& f, void* dq,
+               const int64_t* dqs, void* dk, const int64_t* dks, void* dv, const int64_t* dvs, const BwdWs& w, int B,
+               int Hq, int Hkv, int T, float scale, hipStream_t st) {
+  const int BH = B * Hkv, BHq = B * Hq;
+  hipLaunchKernelGGL(lucid::lucid_bwd_prep_kernel<D>, dim3(T / 64, BHq), dim3(256), 0, st, (const bf16*)dout,
+                     S(dos), (const bf16*)o, S(os), (const bf16*)q, S(qs), Hq, T, w.delta, w.dot, w.qt, w.counters,
+                     BH);
+  if (int rc = hip_status("lucid_bwd_prep_kernel")) return rc;
+  hipLaunchKernelGGL(lucid::lucid_attn_bwd_dkdv_kernel<D>, dim3((T / 128) * BH), dim3(256), 0, st,
+                     (const bf16*)q, S(qs), (const bf16*)k, S(ks), f.vpb, (const bf16*)dout, S(dos), w.qt, w.dot,
+                     lse, w.delta, w.dvp, w.dka, Hq, Hkv, T, BH, scale);
+  if (int rc = hip_status("lucid_attn_bwd_dkdv_kernel")) return rc;
+  hipLaunchKernelGGL(lucid::lucid_attn_bwd_dq_kernel<D>, dim3((T / 128) * BHq), dim3(256), 0, st, (const bf16*)q,
+                     S(qs), (const bf16*)k, S(ks), f.vpb, (const bf16*)dout, S(dos), f.kt, lse, w.delta,
+                     (bf16*)dq, S(dqs), Hq, Hkv, T, BHq, scale);
+  if (int rc = hip_status("lucid_attn_bwd_dq_kernel")) return rc;
+  hipLaunchKernelGGL(lucid::lucid_precond_bwd_col_kernel<D>, dim3((T / 64) * BH), dim3(256), 0, st,
+                     (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, scale, f.kt, f.vpb, f.pinv, w.dvp, w.dvb, w.dvt,
+                     (bf16*)dv, S(dvs), w.colsum, w.counters);
+  if (int rc = hip_status("lucid_precond_bwd_col_kernel")) return rc;
+  hipLaunchKernelGGL(lucid::lucid_precond_bwd_row_kernel<D>, dim3((T / 64) * BH), dim3(256), 0, st,
+                     (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, scale, f.kt, f.vpb, w.dvb, w.colsum, w.dka,
+                     (bf16*)dk, S(dks));
+  return hip_status("lucid_precond_bwd_row_kernel");
+}
+
+}  // namespace
+
+extern "C" {
+
+int lucid_abi_version(void) { return 1; }
+
+const char* lucid_last_error(void) { return g_last_error.c_str(); }
+
+size_t lucid_fwd_workspace_bytes(int B, int Hq, int Hkv, int T, int D) {
+  (void)Hq;
+  return carve_fwd(nullptr, B, Hkv, T, D).bytes;
+}
+
+size_t lucid_bwd_workspace_bytes(int B, int Hq, int Hkv, int T, int D) {
+  return carve_bwd(nullptr, B, Hq, Hkv, T, D).bytes;
+}
+
+int lucid_get_v_prime(const void* k, const int64_t* k_strides, const void* v, const int64_t* v_strides,
+                      float* vprime, void* fwd_ws, int B, int Hkv, int T, int D, float scale, float eps,
+                      void* stream) {
+  g_last_error.clear();
+  if (int rc = check_dims(B, Hkv, Hkv, T, D)) return rc;
+  if (int rc = check_tensor("k", k, k_strides)) return rc;
+  if (int rc = check_tensor("v", v, v_strides)) return rc;
+  if (!vprime || !fwd_ws) return fail("vprime and fwd_ws must be non-null");
+  const FwdWs w = carve_fwd(fwd_ws, B, Hkv, T, D);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (D == 64) return launch_precond_fwd<64>(k, k_strides, v, v_strides, vprime, w, B, Hkv, T, scale, eps, st);
+  return launch_precond_fwd<128>(k, k_strides, v, v_strides, vprime, w, B, Hkv, T, scale, eps, st);
+}
+
+int lucid_attn_fwd(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                   const void* v, const int64_t* v_strides, void* o, const int64_t* o_strides, float* vprime,
+                   float* lse, void* fwd_ws, int B, int Hq, int Hkv, int T, int D, float scale, float eps,
+                   void* stream) {
+  g_last_error.clear();
+  if (int rc = check_dims(B, Hq, Hkv, T, D)) return rc;
+  if (int rc = check_tensor("q", q, q_strides)) return rc;
+  if (int rc = check_tensor("k", k, k_strides)) return rc;
+  if (int rc = check_tensor("v", v, v_strides)) return rc;
+  if (int rc = check_tensor("o", o, o_strides)) return rc;
+  if (!vprime || !lse || !fwd_ws) return fail("vprime, lse and fwd_ws must be non-null");
+  const FwdWs w = carve_fwd(fwd_ws, B, Hkv, T, D);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (D == 64)
+    return launch_fwd<64>(q, q_strides, k, k_strides, v, v_strides, o, o_strides, vprime, lse, w, B, Hq, Hkv, T,
+                          scale, eps, st);
+  return launch_fwd<128>(q, q_strides, k, k_strides, v, v_strides, o, o_strides, vprime, lse, w, B, Hq, Hkv, T,
+                         scale, eps, st);
+}
+
+int lucid_attn_bwd(const void* dout, const int64_t* do_strides, const void* q, const int64_t* q_strides,
+                   const void* k, const int64_t* k_strides, const void* o, const int64_t* o_strides,
+                   const float* lse, const void* fwd_ws, void* dq, const int64_t* dq_strides, void* dk,
+                   const int64_t* dk_strides, void* dv, const int64_t* dv_strides, void* bwd_ws, int B, int Hq,
+                   int Hkv, int T, int D, float scale, float eps, void* stream) {
+  (void)eps;
+  g_last_error.clear();
+  if (int rc = check_dims(B, Hq, Hkv, T, D)) return rc;
+  if (int rc = check_tensor("dout", dout, do_strides)) return rc;
+  if (int rc = check_tensor("q", q, q_strides)) return rc;
+  if (int rc = check_tensor("k", k, k_strides)) return rc;
+  if (int rc = check_tensor("o", o, o_strides)) return rc;
+  if (int rc = check_tensor("dq", dq, dq_strides)) return rc;
+  if (int rc = check_tensor("dk", dk, dk_strides)) return rc;
+  if (int rc = check_tensor("dv", dv, dv_strides)) return rc;
+  if (!lse || !fwd_ws || !bwd_ws) return fail("lse, fwd_ws and bwd_ws must be non-null");
+  const FwdWs f = carve_fwd(const_cast<void*>(fwd_ws), B, Hkv, T, D);
+  const BwdWs w = carve_bwd(bwd_ws, B, Hq, Hkv, T, D);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (D == 64)
+    return launch_bwd<64>(dout, do_strides, q, q_strides, k, k_strides, o, o_strides, lse, f, dq, dq_strides, dk,
+                          dk_strides, dv, dv_strides, w, B, Hq, Hkv, T, scale, st);
+  return launch_bwd<128>(dout, do_strides, q, q_strides, k, k_strides, o, o_strides, lse, f, dq, dq_strides, dk,
+                         dk_strides, dv, dv_strides, w, B, Hq, Hkv, T, scale, st);
+}
+
+}  // extern "C"

@@ -1,0 +1,82 @@
+// Shared device helpers for the LUCID kernels (chain counters, triangular
+// inverse of a 64x64 diagonal block, fp32 -> bf16 hi/lo split).
+#pragma once
+#include "mfma.h"
+
+namespace lucid {
+
+// element strides of a [B, H, T, d] (or [B, T, H, d]) tensor; d is contiguous
+struct Strides {
+  int64_t b, h, t;
+};
+
+// X = P^-1 for a 64x64 lower-triangular fp32 block held in LDS (row-major,
+// row stride 68).  Called by ONE wave: lane c solves column c by forward
+// substitution, x_r = (delta_rc - sum_{k<r} P_rk x_k) / P_rr.  The diagonal of
+// P is exp(s K^_r.K^_r - 1/s) in (0, 1], the off-diagonal entries lie in (0, 1],
+// so plain substitution (no series) is used.  X overwrites P in LDS and is
+// also written to gout[r*64 + c].
+__device__ __forceinline__ void invert_lower64(float (*Ps)[68], int c, float* __restrict__ gout) {
+  float x[64];
+#pragma unroll
+  for (int r = 0; r < 64; ++r) {
+    float acc = (r == c) ? 1.f : 0.f;
+#pragma unroll
+    for (int kk = 0; kk < (r & ~3); kk += 4) {
+      const f32x4 p = *reinterpret_cast<const f32x4*>(&Ps[r][kk]);
+      acc = fmaf(-p[0], x[kk], acc);
+      acc = fmaf(-p[1], x[kk + 1], acc);
+      acc = fmaf(-p[2], x[kk + 2], acc);
+      acc = fmaf(-p[3], x[kk + 3], acc);
+    }
+#pragma unroll
+    for (int kk = (r & ~3); kk < r; ++kk) acc = fmaf(-Ps[r][kk], x[kk], acc);
+    x[r] = acc / Ps[r][r];
+  }
+#pragma unroll
+  for (int r = 0; r < 64; ++r) {
+    Ps[r][c] = x[r];
+    gout[r * 64 + c] = x[r];
+  }
+}
+
+// 8 consecutive fp32 values -> bf16 hi + bf16 lo (x ~= hi + lo to ~2^-17 relative)
+__device__ __forceinline__ void split8(const float* p, bf16x8& hi, bf16x8& lo) {
+  const f32x4 a = *reinterpret_cast<const f32x4*>(p);
+  const f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const bf16 ha = (bf16)a[e], hb = (bf16)b[e];
+    hi[e] = ha;
+    hi[e + 4] = hb;
+    lo[e] = (bf16)(a[e] - (float)ha);
+    lo[e + 4] = (bf16)(b[e] - (float)hb);
+  }
+}
+
+// one element of a T-perm matrix [bh][D][T]
+__device__ __forceinline__ void vpth_w(bf16* base, int bh, int D, int T, int d, int slot, bf16 val) {
+  base[((int64_t)bh * D + d) * T + slot] = val;
+}
+
+// Make this workgroup's global writes visible at agent scope, then advance the
+// head's chain counter to val (release).  Every thread must call it.
+__device__ __forceinline__ void publish_counter(int* cnt, int val) {
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) __hip_atomic_store(cnt, val, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// 16 consecutive-in-D-layout fp32 values of a per-row vector: rows drow(e, g) + base
+__device__ __forceinline__ void load_rows16(const float* __restrict__ p, int g, float out[16]) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const f32x4 t4 = *reinterpret_cast<const f32x4*>(p + 8 * q + 4 * g);
+    out[4 * q] = t4[0];
+    out[4 * q + 1] = t4[1];
+    out[4 * q + 2] = t4[2];
+    out[4 * q + 3] = t4[3];
+  }
+}
+
+}  // namespace lucid

@@ -1,0 +1,71 @@
+// CDNA4 (gfx950) MFMA helpers shared by the LUCID kernels.
+//
+// All contractions use v_mfma_f32_32x32x16_bf16 (one wave64, 32x32 fp32 tile,
+// 16-deep bf16 reduction).  Lane layouts (checked on an MI355X):
+//   A operand [m][k]: lane l holds A[l%32][8*(l/32) + e], e = 0..7
+//   B operand [k][n]: lane l holds B[8*(l/32) + e][l%32], e = 0..7
+//   C/D       [m][n]: lane l holds D[8*(e/4) + 4*(l/32) + e%4][l%32], e = 0..15
+//
+// "Transposed" tiles: a score tile is computed as D[m = key j][n = row i] so
+// that lane <-> row i and the 16 fp32 values of a lane run over keys j.  That
+// D tile, converted to bf16, is directly the B operand [k = j][n = i] of the
+// next MFMA, provided the A operand of that MFMA stores its k index (j) in
+// the order the D layout produces: within every aligned group of 16, logical
+// k slot kappa holds position jmap(kappa), where jmap swaps bits 2 and 3.
+// Operand matrices that are consumed this way are kept in HBM as "T-perm"
+// tiles: [head][d][T] with the T index permuted by jmap inside each 16-group.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+#define LOG2E_F 1.4426950408889634f
+
+__device__ __forceinline__ f32x16 mfma32(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) z[e] = 0.f;
+  return z;
+}
+
+// position of sequence index j inside a T-perm row (involution on the low 4 bits)
+__host__ __device__ __forceinline__ int jmap(int j) {
+  return (j & ~0xC) | ((j & 4) << 1) | ((j & 8) >> 1);
+}
+
+// D-layout row (m) of element e for lane group g = lane/32
+__device__ __forceinline__ int drow(int e, int g) { return 8 * (e >> 2) + 4 * g + (e & 3); }
+
+__device__ __forceinline__ bf16x8 ld8(const bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
+
+// Pack D-layout fp32 values e = 8h .. 8h+7 into a bf16 B operand (k-step h of the tile)
+__device__ __forceinline__ bf16x8 pack_b(const f32x16& x, int h) {
+  bf16x8 r;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r[e] = (bf16)x[8 * h + e];
+  return r;
+}
+
+__device__ __forceinline__ float wave_xor32(float v) {
+  // exchange with lane ^ 32
+  return __shfl_xor(v, 32, 64);
+}
+
+// Agent-scope acquire poll of a chain progress counter; returns the value seen (> target).
+__device__ __forceinline__ int wait_counter_gt(const int* cnt, int target) {
+  int v = __hip_atomic_load(cnt, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+  while (v <= target) {
+    __builtin_amdgcn_s_sleep(1);
+    v = __hip_atomic_load(cnt, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  return v;
+}

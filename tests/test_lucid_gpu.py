@@ -1,0 +1,120 @@
+"""GPU parity of the LUCID attention HIP kernels against the float64 CPU oracle.
+
+Tolerances (bf16 against float64 ground truth computed
+from the same bf16-rounded inputs):
+  * outputs O and V':       max |x - ref| <= 2e-2
+  * gradients dQ, dK, dV:   max |x - ref| <= 2e-2 * max(1, max |ref|)
+Full-size shapes are checked through properties that hold at any size: the
+solve residual ||P V' - V|| (P rebuilt with torch fp32 matmuls) and sampled
+rows of softmax(s q K^T) V' recomputed in fp32.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import lucid_ref as R
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-2
+
+
+def _inputs(B, Hq, Hkv, T, D, seed, scale=None):
+    g = torch.Generator().manual_seed(seed)
+    s = D ** -0.5 if scale is None else scale
+    q = (torch.randn(B, Hq, T, D, generator=g) * s).to(torch.bfloat16)
+    k = (torch.randn(B, Hkv, T, D, generator=g) * s).to(torch.bfloat16)
+    v = (torch.randn(B, Hkv, T, D, generator=g) * s).to(torch.bfloat16)
+    do = torch.randn(B, T, Hq, D, generator=g).to(torch.bfloat16)
+    return q, k, v, do
+
+
+def _np(t):
+    return t.detach().float().cpu().double().numpy()
+
+
+def _maxerr(x, ref):
+    return float(np.abs(_np(x) - ref).max())
+
+
+CASES = [
+    # B, Hq, Hkv, T, D
+    (1, 2, 2, 256, 64),
+    (2, 4, 2, 384, 64),     # GQA, two batches
+    (1, 2, 1, 200, 64),     # ragged T (zero-padded to 256), GQA 2:1
+    (1, 2, 2, 256, 128),
+]
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,T,D", CASES)
+def test_forward_matches_oracle(B, Hq, Hkv, T, D):
+    from lucid_amd import lucid_attention
+    q, k, v, _ = _inputs(B, Hq, Hkv, T, D, seed=T + D)
+    print(f"case fwd B={B} Hq={Hq} Hkv={Hkv} T={T} D={D}", flush=True)
+    o, vp = lucid_attention(q.cuda(), k.cuda(), v.cuda(), return_vprime=True)
+    torch.cuda.synchronize()
+    o_ref, vp_ref = R.lucid_attention(_np(q), _np(k), _np(v), D ** -0.5, 1e-5)
+    assert _maxerr(vp, vp_ref) <= TOL
+    assert _maxerr(o, o_ref) <= TOL
+    # V' is solved with fp32 accumulation: much tighter than the bf16 bar
+    assert _maxerr(vp, vp_ref) <= 2e-3 * max(1.0, np.abs(vp_ref).max())
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,T,D", CASES)
+def test_backward_matches_oracle(B, Hq, Hkv, T, D):
+    from lucid_amd import lucid_attention
+    q, k, v, do = _inputs(B, Hq, Hkv, T, D, seed=7 * T + D)
+    print(f"case bwd B={B} Hq={Hq} Hkv={Hkv} T={T} D={D}", flush=True)
+    qg, kg, vg = (t.cuda().requires_grad_() for t in (q, k, v))
+    o = lucid_attention(qg, kg, vg)
+    o.backward(do.cuda())
+    torch.cuda.synchronize()
+    dq, dk, dv = R.lucid_attention_grads(_np(q), _np(k), _np(v), _np(do), D ** -0.5, 1e-5)
+    for name, got, ref in (("dq", qg.grad, dq), ("dk", kg.grad, dk), ("dv", vg.grad, dv)):
+        err = _maxerr(got, ref)
+        bound = TOL * max(1.0, np.abs(ref).max())
+        assert err <= bound, f"{name}: max err {err:.3e} > {bound:.3e}"
+
+
+def test_identical_keys_first_difference_gpu():
+    # closed form: all keys equal -> V'_0 = V_0/c, V'_i = (V_i - V_{i-1})/c
+    from lucid_amd import get_v_prime
+    T, D = 256, 64
+    g = torch.Generator().manual_seed(3)
+    row = torch.randn(D, generator=g)
+    k = row.expand(1, 1, T, D).to(torch.bfloat16).contiguous()
+    v = (torch.randn(1, 1, T, D, generator=g) / 8).to(torch.bfloat16)
+    vp = get_v_prime(k.cuda(), v.cuda()).cpu().double().numpy()
+    ref = R.vprime_dense(_np(k), _np(v), D ** -0.5, 1e-5)
+    assert np.abs(vp - ref).max() <= 2e-3
+
+
+@pytest.mark.parametrize("T,H", [(8192, 2), (32768, 1)])
+def test_full_size_solve_residual_and_rows(T, H):
+    """Size-independent checks at long T: ||P V' - V|| / ||V|| and sampled attention rows."""
+    from lucid_amd import lucid_attention
+    D = 64
+    q, k, v, _ = _inputs(1, H, H, T, D, seed=T)
+    print(f"case full T={T} H={H}", flush=True)
+    qc, kc, vc = q.cuda(), k.cuda(), v.cuda()
+    o, vp = lucid_attention(qc, kc, vc, return_vprime=True)
+    s = D ** -0.5
+    kf = kc.float()
+    kh = kf * torch.rsqrt(kf.pow(2).mean(-1, keepdim=True) + 1e-5)
+    vf = vc.float()
+    rows = torch.arange(T, device="cuda")
+    for h in range(H):
+        num = 0.0
+        for r0 in range(0, T, 2048):
+            pr = torch.exp(kh[0, h, r0:r0 + 2048] @ kh[0, h].T * s - 1 / s)
+            pr = pr * (rows[None, :] <= rows[r0:r0 + 2048, None])
+            num += float(((pr @ vp[0, h]) - vf[0, h, r0:r0 + 2048]).pow(2).sum())
+        rel = (num ** 0.5) / float(vf[0, h].norm())
+        assert rel < 5e-3, f"head {h}: residual {rel:.3e}"
+        # sampled rows of the attention on V'
+        idx = torch.tensor([0, 1, 63, 64, 1000, T // 2, T - 65, T - 1], device="cuda")
+        sc = (q.cuda().float()[0, h, idx] @ kf[0, h].T) * s
+        sc = sc.masked_fill(rows[None, :] > idx[:, None], float("-inf"))
+        ref = torch.softmax(sc, -1) @ vp[0, h]
+        err = float((o[0, idx, h].float() - ref).abs().max())
+        assert err <= TOL, f"head {h}: sampled-row err {err:.3e}"
