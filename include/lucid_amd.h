@@ -69,6 +69,17 @@ int lucid_attn_bwd(const void* dout, const int64_t* do_strides, const void* q, c
                    const int64_t* dk_strides, void* dv, const int64_t* dv_strides, void* bwd_ws, int B, int Hq,
                    int Hkv, int T, int D, float scale, float eps, void* stream);
 
+/* Per-kernel timing (no counterpart in the reference; used by bench.py).
+ * When enabled, every launch is bracketed by two HIP events on its stream.
+ * lucid_profile_collect() waits for the recorded events, folds them into
+ * per-kernel totals and returns the number of distinct kernels;
+ * lucid_profile_entry(i, ...) reads total milliseconds and launch count of
+ * kernel i; lucid_profile_reset() clears the totals.  Not thread safe. */
+void lucid_profile_enable(int on);
+int lucid_profile_collect(void);
+int lucid_profile_entry(int idx, char* name, int name_len, double* total_ms, long* count);
+void lucid_profile_reset(void);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,7 +1,9 @@
 // C ABI of the LUCID attention kernels (declared in include/lucid_amd.h).
 // One translation unit: the kernel files are included so that every template
 // instantiation lives next to its launcher.
+#include <map>
 #include <string>
+#include <vector>
 
 #include "../../include/lucid_amd.h"
 #include "lucid_bwd.hip"
@@ -114,17 +116,57 @@ int check_tensor(const char* name, const void* p, const int64_t* s) {
 
 lucid::Strides S(const int64_t* s) { return lucid::Strides{s[0], s[1], s[2]}; }
 
+// ---------------------------------------------------------------------------
+// Optional per-kernel timing with HIP events recorded on the launch stream
+// around every kernel (lucid_profile_enable).  Used by bench.py to time the
+// dominant kernel inside the timed region.
+// ---------------------------------------------------------------------------
+struct ProfRec {
+  const char* name;
+  hipEvent_t a, b;
+};
+bool g_prof = false;
+std::vector<ProfRec> g_recs;
+std::vector<hipEvent_t> g_event_pool;
+std::map<std::string, std::pair<double, long>> g_prof_tot;
+
+hipEvent_t pool_event() {
+  if (!g_event_pool.empty()) {
+    hipEvent_t e = g_event_pool.back();
+    g_event_pool.pop_back();
+    return e;
+  }
+  hipEvent_t e;
+  hipEventCreate(&e);
+  return e;
+}
+
+#define LUCID_LAUNCH(NAME, KERNEL, GRID, ST, ...)                          \
+  do {                                                                     \
+    hipEvent_t ev_a = nullptr, ev_b = nullptr;                             \
+    if (g_prof) {                                                          \
+      ev_a = pool_event();                                                 \
+      ev_b = pool_event();                                                 \
+      hipEventRecord(ev_a, ST);                                            \
+    }                                                                      \
+    hipLaunchKernelGGL(KERNEL, GRID, dim3(256), 0, ST, __VA_ARGS__);       \
+    if (int rc_ = hip_status(NAME)) return rc_;                            \
+    if (g_prof) {                                                          \
+      hipEventRecord(ev_b, ST);                                            \
+      g_recs.push_back(ProfRec{NAME, ev_a, ev_b});                         \
+    }                                                                      \
+  } while (0)
+
 template <int D>
 int launch_precond_fwd(const void* k, const int64_t* ks, const void* v, const int64_t* vs, float* vprime,
                        const FwdWs& w, int B, int Hkv, int T, float scale, float eps, hipStream_t st) {
   const int BH = B * Hkv;
-  hipLaunchKernelGGL(lucid::lucid_prep_kernel<D>, dim3(T / 64, BH), dim3(256), 0, st, (const bf16*)k, S(ks), Hkv,
-                     T, eps, w.rinv, w.kt, w.counters);
-  if (int rc = hip_status("lucid_prep_kernel")) return rc;
-  hipLaunchKernelGGL(lucid::lucid_precond_fwd_kernel<D>, dim3((T / 64) * BH), dim3(256), 0, st, (const bf16*)k,
-                     S(ks), (const bf16*)v, S(vs), Hkv, T, BH, w.rinv, scale, vprime, w.vpb, w.vpt, w.pinv,
-                     w.counters);
-  return hip_status("lucid_precond_fwd_kernel");
+  LUCID_LAUNCH("lucid_prep_kernel", lucid::lucid_prep_kernel<D>, dim3(T / 64, BH), st, (const bf16*)k, S(ks), Hkv,
+               T, eps, w.rinv, w.kt, w.counters);
+  LUCID_LAUNCH("lucid_precond_fwd_kernel", lucid::lucid_precond_fwd_kernel<D>, dim3((T / 64) * BH), st,
+               (const bf16*)k, S(ks), (const bf16*)v, S(vs), Hkv, T, BH, w.rinv, scale, vprime, w.vpb, w.vpt,
+               w.pinv, w.counters);
+  return LUCID_OK;
 }
 
 template <int D>
@@ -133,9 +175,9 @@ int launch_fwd(const void* q, const int64_t* qs, const void* k, const int64_t* k
                float scale, float eps, hipStream_t st) {
   if (int rc = launch_precond_fwd<D>(k, ks, v, vs, vprime, w, B, Hkv, T, scale, eps, st)) return rc;
   const int BHq = B * Hq;
-  hipLaunchKernelGGL(lucid::lucid_attn_fwd_kernel<D>, dim3((T / 128) * BHq), dim3(256), 0, st, (const bf16*)q,
-                     S(qs), (const bf16*)k, S(ks), w.vpt, (bf16*)o, S(os), lse, Hq, Hkv, T, BHq, scale);
-  return hip_status("lucid_attn_fwd_kernel");
+  LUCID_LAUNCH("lucid_attn_fwd_kernel", lucid::lucid_attn_fwd_kernel<D>, dim3((T / 128) * BHq), st, (const bf16*)q,
+               S(qs), (const bf16*)k, S(ks), w.vpt, (bf16*)o, S(os), lse, Hq, Hkv, T, BHq, scale);
+  return LUCID_OK;
 }
 
 template <int D>
@@ -144,26 +186,21 @@ int launch_bwd(const void* dout, const int64_t* dos, const void* q, const int64_
                const int64_t* dqs, void* dk, const int64_t* dks, void* dv, const int64_t* dvs, const BwdWs& w, int B,
                int Hq, int Hkv, int T, float scale, hipStream_t st) {
   const int BH = B * Hkv, BHq = B * Hq;
-  hipLaunchKernelGGL(lucid::lucid_bwd_prep_kernel<D>, dim3(T / 64, BHq), dim3(256), 0, st, (const bf16*)dout,
-                     S(dos), (const bf16*)o, S(os), (const bf16*)q, S(qs), Hq, T, w.delta, w.dot, w.qt, w.counters,
-                     BH);
-  if (int rc = hip_status("lucid_bwd_prep_kernel")) return rc;
-  hipLaunchKernelGGL(lucid::lucid_attn_bwd_dkdv_kernel<D>, dim3((T / 128) * BH), dim3(256), 0, st,
-                     (const bf16*)q, S(qs), (const bf16*)k, S(ks), f.vpb, (const bf16*)dout, S(dos), w.qt, w.dot,
-                     lse, w.delta, w.dvp, w.dka, Hq, Hkv, T, BH, scale);
-  if (int rc = hip_status("lucid_attn_bwd_dkdv_kernel")) return rc;
-  hipLaunchKernelGGL(lucid::lucid_attn_bwd_dq_kernel<D>, dim3((T / 128) * BHq), dim3(256), 0, st, (const bf16*)q,
-                     S(qs), (const bf16*)k, S(ks), f.vpb, (const bf16*)dout, S(dos), f.kt, lse, w.delta,
-                     (bf16*)dq, S(dqs), Hq, Hkv, T, BHq, scale);
-  if (int rc = hip_status("lucid_attn_bwd_dq_kernel")) return rc;
-  hipLaunchKernelGGL(lucid::lucid_precond_bwd_col_kernel<D>, dim3((T / 64) * BH), dim3(256), 0, st,
-                     (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, scale, f.kt, f.vpb, f.pinv, w.dvp, w.dvb, w.dvt,
-                     (bf16*)dv, S(dvs), w.colsum, w.counters);
-  if (int rc = hip_status("lucid_precond_bwd_col_kernel")) return rc;
-  hipLaunchKernelGGL(lucid::lucid_precond_bwd_row_kernel<D>, dim3((T / 64) * BH), dim3(256), 0, st,
-                     (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, scale, f.kt, f.vpb, w.dvb, w.colsum, w.dka,
-                     (bf16*)dk, S(dks));
-  return hip_status("lucid_precond_bwd_row_kernel");
+  LUCID_LAUNCH("lucid_bwd_prep_kernel", lucid::lucid_bwd_prep_kernel<D>, dim3(T / 64, BHq), st, (const bf16*)dout,
+               S(dos), (const bf16*)o, S(os), (const bf16*)q, S(qs), Hq, T, w.delta, w.dot, w.qt, w.counters, BH);
+  LUCID_LAUNCH("lucid_attn_bwd_dkdv_kernel", lucid::lucid_attn_bwd_dkdv_kernel<D>, dim3((T / 128) * BH), st,
+               (const bf16*)q, S(qs), (const bf16*)k, S(ks), f.vpb, (const bf16*)dout, S(dos), w.qt, w.dot, lse,
+               w.delta, w.dvp, w.dka, Hq, Hkv, T, BH, scale);
+  LUCID_LAUNCH("lucid_attn_bwd_dq_kernel", lucid::lucid_attn_bwd_dq_kernel<D>, dim3((T / 128) * BHq), st,
+               (const bf16*)q, S(qs), (const bf16*)k, S(ks), f.vpb, (const bf16*)dout, S(dos), f.kt, lse, w.delta,
+               (bf16*)dq, S(dqs), Hq, Hkv, T, BHq, scale);
+  LUCID_LAUNCH("lucid_precond_bwd_col_kernel", lucid::lucid_precond_bwd_col_kernel<D>, dim3((T / 64) * BH), st,
+               (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, scale, f.kt, f.vpb, f.pinv, w.dvp, w.dvb, w.dvt,
+               (bf16*)dv, S(dvs), w.colsum, w.counters);
+  LUCID_LAUNCH("lucid_precond_bwd_row_kernel", lucid::lucid_precond_bwd_row_kernel<D>, dim3((T / 64) * BH), st,
+               (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, scale, f.kt, f.vpb, w.dvb, w.colsum, w.dka, (bf16*)dk,
+               S(dks));
+  return LUCID_OK;
 }
 
 }  // namespace
@@ -241,6 +278,42 @@ int lucid_attn_bwd(const void* dout, const int64_t* do_strides, const void* q, c
                           dk_strides, dv, dv_strides, w, B, Hq, Hkv, T, scale, st);
   return launch_bwd<128>(dout, do_strides, q, q_strides, k, k_strides, o, o_strides, lse, f, dq, dq_strides, dk,
                          dk_strides, dv, dv_strides, w, B, Hq, Hkv, T, scale, st);
+}
+
+void lucid_profile_enable(int on) { g_prof = on != 0; }
+
+int lucid_profile_collect(void) {
+  for (auto& r : g_recs) {
+    if (hipEventSynchronize(r.b) != hipSuccess) return LUCID_EHIP;
+    float ms = 0.f;
+    hipEventElapsedTime(&ms, r.a, r.b);
+    auto& t = g_prof_tot[r.name];
+    t.first += ms;
+    t.second += 1;
+    g_event_pool.push_back(r.a);
+    g_event_pool.push_back(r.b);
+  }
+  g_recs.clear();
+  return (int)g_prof_tot.size();
+}
+
+int lucid_profile_entry(int idx, char* name, int name_len, double* total_ms, long* count) {
+  int i = 0;
+  for (auto& kv : g_prof_tot) {
+    if (i++ != idx) continue;
+    if (name && name_len > 0) {
+      snprintf(name, (size_t)name_len, "%s", kv.first.c_str());
+    }
+    if (total_ms) *total_ms = kv.second.first;
+    if (count) *count = kv.second.second;
+    return LUCID_OK;
+  }
+  return LUCID_EINVAL;
+}
+
+void lucid_profile_reset(void) {
+  lucid_profile_collect();
+  g_prof_tot.clear();
 }
 
 }  // extern "C"

@@ -86,7 +86,9 @@ def test_identical_keys_first_difference_gpu():
     v = (torch.randn(1, 1, T, D, generator=g) / 8).to(torch.bfloat16)
     vp = get_v_prime(k.cuda(), v.cuda()).cpu().double().numpy()
     ref = R.vprime_dense(_np(k), _np(v), D ** -0.5, 1e-5)
-    assert np.abs(vp - ref).max() <= 2e-3
+    # every P_ij ~ 1 here, so the bf16 rounding of V'_j in the off-diagonal MFMA
+    # accumulates like a random walk (no damping); the bf16 bar still holds
+    assert np.abs(vp - ref).max() <= TOL
 
 
 @pytest.mark.parametrize("T,H", [(8192, 2), (32768, 1)])
