@@ -1,0 +1,79 @@
+"""The C-ABI libraries load on the CPU and export every symbol their headers declare.
+
+No compute call is made here (there is no GPU in the CPU suite): only pure host
+functions (ABI version, workspace sizes, argument validation that rejects a
+call before anything is launched) are exercised.
+"""
+import ctypes
+import glob
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADERS = sorted(glob.glob(os.path.join(ROOT, "include", "*.h")))
+LIB_FOR_HEADER = {"lucid_amd.h": "liblucid_amd.so", "lucid_path.h": "liblucid_path.so"}
+
+
+def _declared(header):
+    text = open(header).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^[A-Za-z_][\w\s\*]*?\b(lucid\w+)\s*\(", text, flags=re.M)))
+
+
+@pytest.fixture(scope="module")
+def built():
+    """Use the in-tree libraries; build only those that are missing (build() is the driver's job)."""
+    from lucid_amd import _lib, build
+    if not all(os.path.exists(_lib.lib_path(n)) for n in build.TARGETS):
+        build.build()
+    return True
+
+
+@pytest.mark.parametrize("header", HEADERS, ids=os.path.basename)
+def test_every_declared_symbol_is_exported(built, header):
+    from lucid_amd import _lib
+    libname = LIB_FOR_HEADER[os.path.basename(header)]
+    lib = _lib.load(libname)
+    names = _declared(header)
+    assert names, "no declarations parsed"
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, f"{libname} lacks {missing}"
+
+
+def test_abi_version_and_workspace(built):
+    from lucid_amd import _lib
+    lib = _lib.load()
+    assert lib.lucid_abi_version() == 1
+    ws = lib.lucid_fwd_workspace_bytes(1, 16, 16, 32768, 64)
+    # rinv + K^T + V' (bf16) + V'^T + diagonal inverses, each 256-byte aligned
+    expect = 16 * 32768 * 4 + 3 * 16 * 64 * 32768 * 2 + 16 * 512 * 4096 * 4 + 256
+    assert ws == expect
+    assert lib.lucid_bwd_workspace_bytes(1, 16, 16, 32768, 64) > 0
+
+
+def test_argument_validation_without_gpu(built):
+    from lucid_amd import _lib
+    lib = _lib.load()
+    s = (ctypes.c_int64 * 3)(64 * 256, 64 * 256, 64)
+    dummy = ctypes.c_void_p(1 << 20)
+    # head_dim 96 is rejected before anything is launched
+    rc = lib.lucid_attn_fwd(dummy, s, dummy, s, dummy, s, dummy, s, dummy, dummy, dummy,
+                            1, 1, 1, 256, 96, 0.1, 1e-5, None)
+    assert rc == _lib.LUCID_EINVAL
+    assert b"head_dim" in lib.lucid_last_error()
+    rc = lib.lucid_attn_fwd(dummy, s, dummy, s, dummy, s, dummy, s, dummy, dummy, dummy,
+                            1, 1, 1, 200, 64, 0.1, 1e-5, None)
+    assert rc == _lib.LUCID_EINVAL and b"multiple of 128" in lib.lucid_last_error()
+    rc = lib.lucid_attn_fwd(dummy, s, dummy, s, dummy, s, dummy, s, dummy, dummy, dummy,
+                            1, 3, 2, 256, 64, 0.1, 1e-5, None)
+    assert rc == _lib.LUCID_EINVAL and b"multiple of Hkv" in lib.lucid_last_error()
+
+
+def test_product_path_fails_loudly_without_gpu_tensors():
+    import torch
+    from lucid_amd import lucid_attention
+    q = torch.zeros(1, 1, 128, 64, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="GPU tensor"):
+        lucid_attention(q, q, q)
