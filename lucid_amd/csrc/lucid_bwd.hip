@@ -133,7 +133,7 @@ __global__ __launch_bounds__(256) void lucid_attn_bwd_dkdv_kernel(
         load_rows16(lh + ib0, g, lr);
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-          float p = exp2f(s[e] * c - lr[e]);
+          float p = __builtin_amdgcn_exp2f(s[e] * c - lr[e]);
           if (diag && (ib0 + drow(e, g) < jrow)) p = 0.f;
           s[e] = p;
         }
@@ -233,7 +233,7 @@ __global__ __launch_bounds__(256) void lucid_attn_bwd_dq_kernel(
       }
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        float p = exp2f(s[e] * c - li);
+        float p = __builtin_amdgcn_exp2f(s[e] * c - li);
         if (diag && (jb0 + drow(e, g) > irow)) p = 0.f;
         s[e] = p * (dp[e] - di);
       }
@@ -313,7 +313,7 @@ __global__ __launch_bounds__(256) void lucid_precond_bwd_col_kernel(
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       const int m = ih * 32 + drow(e, g);
-      Ps[m][n] = (n <= m) ? exp2f(sd[e] * aJ * rv[J0 + m] - c0) : 0.f;
+      Ps[m][n] = (n <= m) ? __builtin_amdgcn_exp2f(sd[e] * aJ * rv[J0 + m] - c0) : 0.f;
     }
   }
   {
@@ -342,7 +342,7 @@ __global__ __launch_bounds__(256) void lucid_precond_bwd_col_kernel(
     load_rows16(rv + I0, g, rI);
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-      const float p = exp2f(s[e] * aJ * rI[e] - c0);
+      const float p = __builtin_amdgcn_exp2f(s[e] * aJ * rI[e] - c0);
       s[e] = p;
       gg[e] = gg[e] * p * rI[e];
     }
@@ -508,7 +508,7 @@ __global__ __launch_bounds__(256) void lucid_precond_bwd_row_kernel(
     const bool diag = (J == I);
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-      float p = exp2f(s[e] * aI * rJ[e] - c0);
+      float p = __builtin_amdgcn_exp2f(s[e] * aI * rJ[e] - c0);
       if (diag && (J0 + drow(e, g) > irow)) p = 0.f;
       gg[e] = gg[e] * p * rJ[e];
     }

@@ -175,7 +175,7 @@ int launch_fwd(const void* q, const int64_t* qs, const void* k, const int64_t* k
                float scale, float eps, hipStream_t st) {
   if (int rc = launch_precond_fwd<D>(k, ks, v, vs, vprime, w, B, Hkv, T, scale, eps, st)) return rc;
   const int BHq = B * Hq;
-  LUCID_LAUNCH("lucid_attn_fwd_kernel", lucid::lucid_attn_fwd_kernel<D>, dim3((T / 128) * BHq), st, (const bf16*)q,
+  LUCID_LAUNCH("lucid_attn_fwd_kernel", lucid::lucid_attn_fwd_kernel<D>, dim3(((T + 255) / 256) * BHq), st, (const bf16*)q,
                S(qs), (const bf16*)k, S(ks), w.vpt, (bf16*)o, S(os), lse, Hq, Hkv, T, BHq, scale);
   return LUCID_OK;
 }

@@ -9,7 +9,7 @@
 //   lucid_prep_kernel        per-row 1/rms of K, K^T in T-perm layout, zero chain counters
 //   lucid_precond_fwd_kernel chained solve, one workgroup per (64-row block, kv head);
 //                            block i waits on a per-head progress counter for V'_j, j < i
-//   lucid_attn_fwd_kernel    causal online-softmax attention on V' (128 query rows / WG)
+//   lucid_attn_fwd_kernel    causal online-softmax attention on V' (256 query rows / WG, LDS tiles)
 #include "lucid_common.h"
 
 namespace lucid {
@@ -105,7 +105,7 @@ __global__ __launch_bounds__(256) void lucid_precond_fwd_kernel(
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       const int m = jh * 32 + drow(e, g);
-      Ps[m][n] = (n <= m) ? exp2f(sd[e] * ai * rv[i0 + m] - c0) : 0.f;
+      Ps[m][n] = (n <= m) ? __builtin_amdgcn_exp2f(sd[e] * ai * rv[i0 + m] - c0) : 0.f;
     }
   }
   __syncthreads();
@@ -129,7 +129,7 @@ __global__ __launch_bounds__(256) void lucid_precond_fwd_kernel(
       rj[4 * q] = t4[0]; rj[4 * q + 1] = t4[1]; rj[4 * q + 2] = t4[2]; rj[4 * q + 3] = t4[3];
     }
 #pragma unroll
-    for (int e = 0; e < 16; ++e) s[e] = exp2f(s[e] * ai * rj[e] - c0);
+    for (int e = 0; e < 16; ++e) s[e] = __builtin_amdgcn_exp2f(s[e] * ai * rj[e] - c0);
     const bf16x8 p0 = pack_b(s, 0), p1 = pack_b(s, 1);
 #pragma unroll
     for (int t = 0; t < NDT; ++t) {
@@ -201,12 +201,16 @@ __global__ __launch_bounds__(256) void lucid_precond_fwd_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Causal attention on V'.  Workgroup = 128 query rows of one query head,
-// heavy (late) row blocks first; wave w owns rows 32w..32w+31 (lane <-> row).
-// S^T tile [j][i] = K_j . Q_i, online softmax per lane (max exchanged with
-// lane^32), O^T[d][i] += V'^T[d][j] P^T[j][i].
-// Writes O (bf16, caller layout) and lse2[bhq][i] = log2-sum-exp in units of
-// s*log2(e)*score, so P = exp2(s*log2e*S - lse2).
+// Causal attention on V'.  Workgroup = 256 query rows of one query head
+// (heavy, late row blocks first); wave w owns rows 64w .. 64w+63 as two
+// 32-row n-tiles (lane <-> row).  Every 64-key tile of K and V'^T is staged
+// once per workgroup in LDS (double buffered, loaded one tile ahead with
+// coalesced 16-byte global loads) and read by all four waves.
+//   S^T[j][i] = K_j . Q_i;  online softmax per lane (lazy rescale: the
+//   reference max only moves when a row grows by more than 2^8);
+//   O^T[d][i] += V'^T[d][j] P^T[j][i].
+// Writes O (bf16, caller layout) and lse2[bhq][i] (log2 domain, so that
+// P = exp2(s*log2e*S - lse2)).
 // ---------------------------------------------------------------------------
 template <int D>
 __global__ __launch_bounds__(256) void lucid_attn_fwd_kernel(const bf16* __restrict__ q, Strides qs,
@@ -216,89 +220,160 @@ __global__ __launch_bounds__(256) void lucid_attn_fwd_kernel(const bf16* __restr
                                                              int T, int BHq, float scale) {
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
-  const int nblk = T / 128;
+  constexpr int CH = D / 32;  // 16-byte chunks per thread for each of the K and V'^T tiles
+  __shared__ __attribute__((aligned(16))) bf16 lk[2][64][D + 8];
+  __shared__ __attribute__((aligned(16))) bf16 lv[2][D][64 + 8];
+
+  const int nblk = (T + 255) / 256;
   const int id = blockIdx.x;
   const int bhq = id % BHq;
   const int ib = nblk - 1 - id / BHq;
   const int b = bhq / Hq, hq = bhq - b * Hq;
   const int h = hq / (Hq / Hkv);
   const int bh = b * Hkv + h;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
-  const int row0 = ib * 128 + w * 32;
-  const int irow = row0 + l32;
+  const int r0 = ib * 256;
+  const int row0 = r0 + w * 64;
   const bf16* qh = q + b * qs.b + hq * qs.h;
   const bf16* kh = k + b * ks.b + h * ks.h;
   const bf16* vth = vpt + (int64_t)bh * D * T;
   const float c = scale * LOG2E_F;
 
-  bf16x8 qb[NKS];
+  bf16x8 qb[2][NKS];
 #pragma unroll
-  for (int s = 0; s < NKS; ++s) qb[s] = ld8(qh + (int64_t)irow * qs.t + 16 * s + 8 * g);
-  f32x16 oacc[NDT];
+  for (int nt = 0; nt < 2; ++nt) {
+    const int rq = min(row0 + nt * 32 + l32, T - 1);
 #pragma unroll
-  for (int t = 0; t < NDT; ++t) oacc[t] = zero16();
-  float m = -1e30f, lsum = 0.f;
-  const int ntile = (row0 + 32 + 63) / 64;
-  for (int jt = 0; jt < ntile; ++jt) {
-    const int j0 = jt * 64;
-    f32x16 s[2];
+    for (int st = 0; st < NKS; ++st) qb[nt][st] = ld8(qh + (int64_t)rq * qs.t + 16 * st + 8 * g);
+  }
+  f32x16 oacc[NDT][2];
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      s[mt] = zero16();
+  for (int t = 0; t < NDT; ++t) {
+    oacc[t][0] = zero16();
+    oacc[t][1] = zero16();
+  }
+  float m[2] = {-1e30f, -1e30f}, lsum[2] = {0.f, 0.f};
+
+  const int ntile = (min(r0 + 256, T) + 63) / 64;
+  const int last_w = row0 / 64;  // this wave's diagonal tile
+  bf16x8 stg[2 * CH];
+  auto gload = [&](int j0) {
 #pragma unroll
-      for (int st = 0; st < NKS; ++st)
-        s[mt] = mfma32(ld8(kh + (int64_t)(j0 + mt * 32 + l32) * ks.t + 16 * st + 8 * g), qb[st], s[mt]);
+    for (int u = 0; u < CH; ++u) {
+      const int cidx = tid + 256 * u;
+      const int kr = cidx / (D / 8), kc = cidx % (D / 8);
+      stg[u] = ld8(kh + (int64_t)(j0 + kr) * ks.t + kc * 8);
+      const int vr = cidx >> 3, vc = cidx & 7;
+      stg[CH + u] = ld8(vth + (int64_t)vr * T + j0 + vc * 8);
     }
-    const bool diag = (j0 + 63 > row0);
-    float mx = -1e30f;
+  };
+  auto lstore = [&](int buf) {
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+    for (int u = 0; u < CH; ++u) {
+      const int cidx = tid + 256 * u;
+      const int kr = cidx / (D / 8), kc = cidx % (D / 8);
+      *reinterpret_cast<bf16x8*>(&lk[buf][kr][kc * 8]) = stg[u];
+      const int vr = cidx >> 3, vc = cidx & 7;
+      *reinterpret_cast<bf16x8*>(&lv[buf][vr][vc * 8]) = stg[CH + u];
+    }
+  };
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  for (int jt = 0; jt < ntile; ++jt) {
+    const int buf = jt & 1;
+    const bool more = jt + 1 < ntile;
+    if (more) gload((jt + 1) * 64);
+    if (jt <= last_w && row0 < T) {
+      const int j0 = jt * 64;
+      f32x16 s[2][2];
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        float x = s[mt][e] * c;
-        if (diag && (j0 + mt * 32 + drow(e, g) > irow)) x = -INFINITY;
-        s[mt][e] = x;
-        mx = fmaxf(mx, x);
+      for (int mt = 0; mt < 2; ++mt) {
+        bf16x8 ka[NKS];
+#pragma unroll
+        for (int st = 0; st < NKS; ++st) ka[st] = ld8(&lk[buf][mt * 32 + l32][16 * st + 8 * g]);
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+          s[mt][nt] = zero16();
+#pragma unroll
+          for (int st = 0; st < NKS; ++st) s[mt][nt] = mfma32(ka[st], qb[nt][st], s[mt][nt]);
+        }
       }
-    mx = fmaxf(mx, wave_xor32(mx));
-    const float mnew = fmaxf(m, mx);
-    const float alpha = exp2f(m - mnew);
-    m = mnew;
-    lsum *= alpha;
+      if (jt == last_w) {
 #pragma unroll
-    for (int t = 0; t < NDT; ++t)
+        for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) oacc[t][e] *= alpha;
+          for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const float p = exp2f(s[mt][e] - mnew);
-        lsum += p;
-        s[mt][e] = p;
+            for (int e = 0; e < 16; ++e)
+              if (mt * 32 + drow(e, g) > nt * 32 + l32) s[mt][nt][e] = -INFINITY;
       }
-    bf16x8 pb[4] = {pack_b(s[0], 0), pack_b(s[0], 1), pack_b(s[1], 0), pack_b(s[1], 1)};
+      bf16x8 pb[2][4];
 #pragma unroll
-    for (int t = 0; t < NDT; ++t) {
-      const bf16* ap = vth + (int64_t)(t * 32 + l32) * T + j0 + 8 * g;
+      for (int nt = 0; nt < 2; ++nt) {
+        float mx = -INFINITY;
 #pragma unroll
-      for (int ks2 = 0; ks2 < 4; ++ks2) oacc[t] = mfma32(ld8(ap + 16 * ks2), pb[ks2], oacc[t]);
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[mt][nt][e]);
+        mx = fmaxf(mx, wave_xor32(mx)) * c;
+        if (__builtin_amdgcn_ballot_w64(mx > m[nt] + 8.0f)) {
+          const float mnew = fmaxf(m[nt], mx);
+          const float alpha = __builtin_amdgcn_exp2f(m[nt] - mnew);
+          m[nt] = mnew;
+          lsum[nt] *= alpha;
+#pragma unroll
+          for (int t = 0; t < NDT; ++t)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) oacc[t][nt][e] *= alpha;
+        }
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const float p = __builtin_amdgcn_exp2f(fmaf(s[mt][nt][e], c, -m[nt]));
+            lsum[nt] += p;
+            s[mt][nt][e] = p;
+          }
+        pb[nt][0] = pack_b(s[0][nt], 0);
+        pb[nt][1] = pack_b(s[0][nt], 1);
+        pb[nt][2] = pack_b(s[1][nt], 0);
+        pb[nt][3] = pack_b(s[1][nt], 1);
+      }
+#pragma unroll
+      for (int t = 0; t < NDT; ++t) {
+        bf16x8 va[4];
+#pragma unroll
+        for (int k4 = 0; k4 < 4; ++k4) va[k4] = ld8(&lv[buf][t * 32 + l32][16 * k4 + 8 * g]);
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+          for (int k4 = 0; k4 < 4; ++k4) oacc[t][nt] = mfma32(va[k4], pb[nt][k4], oacc[t][nt]);
+      }
+    }
+    if (more) lstore(buf ^ 1);
+    __syncthreads();
+  }
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    const int irow = row0 + nt * 32 + l32;
+    const float ls = lsum[nt] + wave_xor32(lsum[nt]);
+    if (irow < T) {
+      const float inv = 1.0f / ls;
+      bf16* op = o + b * os.b + hq * os.h + (int64_t)irow * os.t;
+#pragma unroll
+      for (int t = 0; t < NDT; ++t)
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) {
+          bf16x4 bb;
+#pragma unroll
+          for (int u = 0; u < 4; ++u) bb[u] = (bf16)(oacc[t][nt][4 * qq + u] * inv);
+          *reinterpret_cast<bf16x4*>(op + t * 32 + 8 * qq + 4 * g) = bb;
+        }
+      if (g == 0) lse[(int64_t)bhq * T + irow] = m[nt] + log2f(ls);
     }
   }
-  lsum += wave_xor32(lsum);
-  const float inv = 1.0f / lsum;
-  bf16* op = o + b * os.b + hq * os.h + (int64_t)irow * os.t;
-#pragma unroll
-  for (int t = 0; t < NDT; ++t)
-#pragma unroll
-    for (int qq = 0; qq < 4; ++qq) {
-      bf16x4 bb;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) bb[u] = (bf16)(oacc[t][4 * qq + u] * inv);
-      *reinterpret_cast<bf16x4*>(op + t * 32 + 8 * qq + 4 * g) = bb;
-    }
-  if (g == 0) lse[(int64_t)bhq * T + irow] = m + log2f(lsum);
 }
 
 }  // namespace lucid
