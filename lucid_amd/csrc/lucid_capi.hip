@@ -163,7 +163,7 @@ int launch_precond_fwd(const void* k, const int64_t* ks, const void* v, const in
   const int BH = B * Hkv;
   LUCID_LAUNCH("lucid_prep_kernel", lucid::lucid_prep_kernel<D>, dim3(T / 64, BH), st, (const bf16*)k, S(ks), Hkv,
                T, eps, w.rinv, w.kt, w.counters);
-  LUCID_LAUNCH("lucid_precond_fwd_kernel", lucid::lucid_precond_fwd_kernel<D>, dim3((T / 64) * BH), st,
+  LUCID_LAUNCH("lucid_precond_fwd_kernel", lucid::lucid_precond_fwd_kernel<D>, dim3((T / 128) * BH), st,
                (const bf16*)k, S(ks), (const bf16*)v, S(vs), Hkv, T, BH, w.rinv, scale, vprime, w.vpb, w.vpt,
                w.pinv, w.counters);
   return LUCID_OK;

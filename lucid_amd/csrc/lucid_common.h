@@ -62,7 +62,7 @@ __device__ __forceinline__ void vpth_w(bf16* base, int bh, int D, int T, int d, 
 // Make this workgroup's global writes visible at agent scope, then advance the
 // head's chain counter to val (release).  Every thread must call it.
 __device__ __forceinline__ void publish_counter(int* cnt, int val) {
-  __threadfence();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
   __syncthreads();
   if (threadIdx.x == 0) __hip_atomic_store(cnt, val, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
 }

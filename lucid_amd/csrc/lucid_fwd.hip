@@ -7,8 +7,8 @@
 //
 // Kernels (all 256 threads = 4 waves, MFMA 32x32x16 bf16, fp32 accumulate):
 //   lucid_prep_kernel        per-row 1/rms of K, K^T in T-perm layout, zero chain counters
-//   lucid_precond_fwd_kernel chained solve, one workgroup per (64-row block, kv head);
-//                            block i waits on a per-head progress counter for V'_j, j < i
+//   lucid_precond_fwd_kernel chained solve, one workgroup per (128-row block, kv head);
+//                            it waits on a per-head progress counter for V'_j, j < i
 //   lucid_attn_fwd_kernel    causal online-softmax attention on V' (256 query rows / WG, LDS tiles)
 #include "lucid_common.h"
 
@@ -56,148 +56,305 @@ __global__ __launch_bounds__(256) void lucid_prep_kernel(const bf16* __restrict_
 }
 
 // ---------------------------------------------------------------------------
-// Chained preconditioner solve.  Workgroup id -> (i = id / BH, bh = id % BH):
-// ids grow with i, so every wait is on a lower id (in-order dispatch keeps the
-// chain deadlock free) and the blocks of one head share an XCD when BH % 8 == 0.
+// Chained preconditioner solve, 128 rows per workgroup made of two 64-row
+// sub-blocks A (rows i0..i0+63) and B (i0+64..i0+127).
+// Workgroup id -> (i2 = id / BH, bh = id % BH): ids grow with i2, so every
+// wait is on a lower id (in-order dispatch keeps the chain deadlock free) and
+// the blocks of one head share an XCD when BH % 8 == 0.  counters[bh] = number
+// of 64-row blocks of V' already published.
 //
-// wave w: ih = w & 1 selects rows i0 + 32*ih .. +32 (lane <-> row),
-//         jh = w >> 1 selects keys j0 + 32*jh .. +32 of every 64-key tile.
-// acc^T[d][i] = sum_{j < i0} V'^T[d][j] P[i][j]  (MFMA, bf16 operands)
-// V'_i = X (V_i - acc), X = P_ii^-1 computed in fp32 by wave 0 before the wait,
-// applied with a 3-term bf16 split (hi*hi + hi*lo + lo*hi) for ~fp32 accuracy.
+// wave w: ih = w & 1 -> rows i0 + 64*ih .. +64 (two 32-row n-tiles, lane <-> row)
+//         jh = w >> 1 -> keys 32*jh .. +32 of every staged 64-key tile
+// Every earlier 64-key tile (K rows, V'^T in T-perm layout, 1/rms) is staged
+// once per workgroup in LDS, double buffered, with coalesced 16-byte loads:
+//   acc^T[d][i] += V'^T[d][j] P^T[j][i],  P^T[j][i] = exp(s r_i r_j K_j.K_i - 1/s)
+// Then V'_A = X_A (V_A - acc_A); V'_B = X_B (V_B - acc_B - P_BA V'_A), with
+// X = P_diag^-1 computed in fp32 (waves 0/1) and applied through a 3-term bf16
+// split (hi*hi + hi*lo + lo*hi).
 // ---------------------------------------------------------------------------
+template <int D>
+struct PfwdSmem {
+  float X[2][64][68];  // P_AA, P_BB, then their inverses
+  union {
+    struct {
+      bf16 k[2][64][D + 8];
+      bf16 v[2][D][64 + 8];
+      float r[2][64];
+    } st;
+    struct {
+      float Rt[D][132];   // R^T for the 128 rows (cols 0..63 = A, 64..127 = B)
+      bf16 vA[D][64 + 8]; // V'_A^T (bf16, T-perm within the block) for the B correction
+    } fin;
+  } u;
+};
+
 template <int D>
 __global__ __launch_bounds__(256) void lucid_precond_fwd_kernel(
     const bf16* __restrict__ k, Strides ks, const bf16* __restrict__ v, Strides vs, int Hkv, int T, int BH,
     const float* __restrict__ rinv, float scale, float* __restrict__ vp32, bf16* __restrict__ vpb,
     bf16* __restrict__ vpt, float* __restrict__ pinv, int* __restrict__ counters) {
-  constexpr int NDT = D / 32;  // 32-row d tiles
-  constexpr int NKS = D / 16;  // 16-deep k steps over d
-  __shared__ __attribute__((aligned(16))) float Ps[64][68];           // P_ii, then X = P_ii^-1 (row-major [r][c])
-  __shared__ __attribute__((aligned(16))) float Rt[D][68];            // R^T[d][c] (also used for the cross-wave reduction)
+  constexpr int NDT = D / 32;
+  constexpr int NKS = D / 16;
+  constexpr int CH = D / 32;
+  __shared__ __attribute__((aligned(16))) PfwdSmem<D> sm;
 
   const int id = blockIdx.x;
-  const int i = id / BH, bh = id - (id / BH) * BH;
+  const int i2 = id / BH, bh = id - (id / BH) * BH;
   const int b = bh / Hkv, h = bh - b * Hkv;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
   const int ih = w & 1, jh = w >> 1;
-  const int i0 = i * 64;
+  const int i0 = i2 * 128;
+  const int NT = T / 64;
   const bf16* kh = k + b * ks.b + h * ks.h;
   const bf16* vh = v + b * vs.b + h * vs.h;
   const float* rv = rinv + (int64_t)bh * T;
   const bf16* vpth = vpt + (int64_t)bh * D * T;
+  int* cnt = counters + bh;
   const float sl2 = scale * LOG2E_F;
   const float c0 = LOG2E_F / scale;
 
-  bf16x8 kbi[NKS];
-#pragma unroll
-  for (int s = 0; s < NKS; ++s) kbi[s] = ld8(kh + (int64_t)(i0 + ih * 32 + l32) * ks.t + 16 * s + 8 * g);
-  const float ai = sl2 * rv[i0 + ih * 32 + l32];
-
-  // ---- diagonal block P_ii (symmetric S, lower mask) ----
+  // ---- diagonal blocks P_AA, P_BB: each wave computes one 32x32 tile of each ----
   {
-    f32x16 sd = zero16();
+    const int mh = w >> 1, nh = w & 1;
 #pragma unroll
-    for (int s = 0; s < NKS; ++s)
-      sd = mfma32(ld8(kh + (int64_t)(i0 + jh * 32 + l32) * ks.t + 16 * s + 8 * g), kbi[s], sd);
-    const int n = ih * 32 + l32;
+    for (int sb = 0; sb < 2; ++sb) {
+      const int base = i0 + sb * 64;
+      f32x16 sd = zero16();
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int m = jh * 32 + drow(e, g);
-      Ps[m][n] = (n <= m) ? __builtin_amdgcn_exp2f(sd[e] * ai * rv[i0 + m] - c0) : 0.f;
+      for (int st = 0; st < NKS; ++st)
+        sd = mfma32(ld8(kh + (int64_t)(base + mh * 32 + l32) * ks.t + 16 * st + 8 * g),
+                    ld8(kh + (int64_t)(base + nh * 32 + l32) * ks.t + 16 * st + 8 * g), sd);
+      const int n = nh * 32 + l32;
+      const float an = sl2 * rv[base + n];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int m = mh * 32 + drow(e, g);
+        sm.X[sb][m][n] = (n <= m) ? __builtin_amdgcn_exp2f(fmaf(sd[e] * an, rv[base + m], -c0)) : 0.f;
+      }
     }
   }
   __syncthreads();
-  if (w == 0) invert_lower64(Ps, lane, pinv + ((int64_t)bh * (T / 64) + i) * 4096);
+  if (w < 2) invert_lower64(sm.X[w], lane, pinv + ((int64_t)bh * NT + 2 * i2 + w) * 4096);
 
-  // ---- off-diagonal accumulation over all earlier blocks ----
-  f32x16 acc[NDT];
+  bf16x8 kbi[2][NKS];
+  float ai[2];
 #pragma unroll
-  for (int t = 0; t < NDT; ++t) acc[t] = zero16();
-  int ready = 0;
-  for (int j = 0; j < i; ++j) {
-    if (j >= ready) ready = wait_counter_gt(counters + bh, j);
-    const int j0 = j * 64 + jh * 32;
-    f32x16 s = zero16();
+  for (int nt = 0; nt < 2; ++nt) {
+    const int row = i0 + ih * 64 + nt * 32 + l32;
 #pragma unroll
-    for (int st = 0; st < NKS; ++st) s = mfma32(ld8(kh + (int64_t)(j0 + l32) * ks.t + 16 * st + 8 * g), kbi[st], s);
-    float rj[16];
+    for (int st = 0; st < NKS; ++st) kbi[nt][st] = ld8(kh + (int64_t)row * ks.t + 16 * st + 8 * g);
+    ai[nt] = sl2 * rv[row];
+  }
+  f32x16 acc[NDT][2];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      f32x4 t4 = *reinterpret_cast<const f32x4*>(rv + j0 + 8 * q + 4 * g);
-      rj[4 * q] = t4[0]; rj[4 * q + 1] = t4[1]; rj[4 * q + 2] = t4[2]; rj[4 * q + 3] = t4[3];
-    }
-#pragma unroll
-    for (int e = 0; e < 16; ++e) s[e] = __builtin_amdgcn_exp2f(s[e] * ai * rj[e] - c0);
-    const bf16x8 p0 = pack_b(s, 0), p1 = pack_b(s, 1);
-#pragma unroll
-    for (int t = 0; t < NDT; ++t) {
-      const bf16* ap = vpth + (int64_t)(t * 32 + l32) * T + j0 + 8 * g;
-      acc[t] = mfma32(ld8(ap), p0, acc[t]);
-      acc[t] = mfma32(ld8(ap + 16), p1, acc[t]);
-    }
+  for (int t = 0; t < NDT; ++t) {
+    acc[t][0] = zero16();
+    acc[t][1] = zero16();
   }
 
-  // ---- reduce the two key halves: waves jh=1 hand their partials to jh=0 ----
+  // ---- off-diagonal sweep over the 2*i2 earlier 64-key tiles ----
+  const int nj = 2 * i2;
+  int ready = 0;
+  bf16x8 stg[2 * CH];
+  f32x4 rstg;
+  auto gload = [&](int j) {
+    const int j0 = j * 64;
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      const int cidx = tid + 256 * u;
+      const int kr = cidx / (D / 8), kc = cidx % (D / 8);
+      stg[u] = ld8(kh + (int64_t)(j0 + kr) * ks.t + kc * 8);
+      const int vr = cidx >> 3, vc = cidx & 7;
+      stg[CH + u] = ld8(vpth + (int64_t)vr * T + j0 + vc * 8);
+    }
+    if (tid < 16) rstg = *reinterpret_cast<const f32x4*>(rv + j0 + 4 * tid);
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      const int cidx = tid + 256 * u;
+      const int kr = cidx / (D / 8), kc = cidx % (D / 8);
+      *reinterpret_cast<bf16x8*>(&sm.u.st.k[buf][kr][kc * 8]) = stg[u];
+      const int vr = cidx >> 3, vc = cidx & 7;
+      *reinterpret_cast<bf16x8*>(&sm.u.st.v[buf][vr][vc * 8]) = stg[CH + u];
+    }
+    if (tid < 16) *reinterpret_cast<f32x4*>(&sm.u.st.r[buf][4 * tid]) = rstg;
+  };
+  if (nj > 0) {
+    ready = wait_counter_gt(cnt, 0);
+    gload(0);
+    lstore(0);
+  }
+  __syncthreads();
+  for (int j = 0; j < nj; ++j) {
+    const int buf = j & 1;
+    const bool more = j + 1 < nj;
+    bool early = false;
+    if (more) {
+      if (j + 1 >= ready) {
+        const int seen = poll_counter(cnt);
+        if (seen > j + 1) {
+          acquire_agent();
+          ready = seen;
+        }
+      }
+      early = j + 1 < ready;
+      if (early) gload(j + 1);
+    }
+    {
+      bf16x8 ka[NKS];
+#pragma unroll
+      for (int st = 0; st < NKS; ++st) ka[st] = ld8(&sm.u.st.k[buf][jh * 32 + l32][16 * st + 8 * g]);
+      float rj[16];
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd) {
+        const f32x4 t4 = *reinterpret_cast<const f32x4*>(&sm.u.st.r[buf][jh * 32 + 8 * qd + 4 * g]);
+        rj[4 * qd] = t4[0];
+        rj[4 * qd + 1] = t4[1];
+        rj[4 * qd + 2] = t4[2];
+        rj[4 * qd + 3] = t4[3];
+      }
+      bf16x8 pb[2][2];
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        f32x16 sc = zero16();
+#pragma unroll
+        for (int st = 0; st < NKS; ++st) sc = mfma32(ka[st], kbi[nt][st], sc);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sc[e] = __builtin_amdgcn_exp2f(fmaf(sc[e] * ai[nt], rj[e], -c0));
+        pb[nt][0] = pack_b(sc, 0);
+        pb[nt][1] = pack_b(sc, 1);
+      }
+#pragma unroll
+      for (int t = 0; t < NDT; ++t) {
+        const bf16x8 va0 = ld8(&sm.u.st.v[buf][t * 32 + l32][jh * 32 + 8 * g]);
+        const bf16x8 va1 = ld8(&sm.u.st.v[buf][t * 32 + l32][jh * 32 + 16 + 8 * g]);
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+          acc[t][nt] = mfma32(va0, pb[nt][0], acc[t][nt]);
+          acc[t][nt] = mfma32(va1, pb[nt][1], acc[t][nt]);
+        }
+      }
+    }
+    if (more) {
+      if (!early) {
+        ready = wait_counter_gt(cnt, j + 1);
+        gload(j + 1);
+      }
+      lstore(buf ^ 1);
+    }
+    __syncthreads();
+  }
+
+  // ---- reduce the key halves: R^T = V^T - acc^T (Rt columns = rows of this workgroup) ----
+  float(*Rt)[132] = sm.u.fin.Rt;
   if (jh == 1) {
 #pragma unroll
     for (int t = 0; t < NDT; ++t)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][ih * 32 + l32] = acc[t][e];
+      for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][ih * 64 + nt * 32 + l32] = acc[t][nt][e];
   }
-  __syncthreads();  // also orders wave 0's X in Ps before its use below
+  __syncthreads();
   if (jh == 0) {
-    const int r = i0 + ih * 32 + l32;
 #pragma unroll
-    for (int t = 0; t < NDT; ++t)
+    for (int nt = 0; nt < 2; ++nt) {
+      const int col = ih * 64 + nt * 32 + l32;
+      const bf16* vrow = vh + (int64_t)(i0 + col) * vs.t;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int d0 = t * 32 + 8 * q + 4 * g;
-        bf16x4 vv = *reinterpret_cast<const bf16x4*>(vh + (int64_t)r * vs.t + d0);
+      for (int t = 0; t < NDT; ++t)
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int e = 4 * q + u;
-          Rt[d0 + u][ih * 32 + l32] = (float)vv[u] - (acc[t][e] + Rt[d0 + u][ih * 32 + l32]);
+        for (int qd = 0; qd < 4; ++qd) {
+          const int d0 = t * 32 + 8 * qd + 4 * g;
+          const bf16x4 vv = *reinterpret_cast<const bf16x4*>(vrow + d0);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) Rt[d0 + u][col] = (float)vv[u] - (acc[t][nt][4 * qd + u] + Rt[d0 + u][col]);
         }
-      }
+    }
   }
   __syncthreads();
 
-  // ---- diagonal solve V'^T[d][r] = sum_c R^T[d][c] X[r][c] ----
-  for (int tile = w; tile < NDT * 2; tile += 4) {
-    const int dt = tile >> 1, rh = tile & 1;
-    f32x16 o = zero16();
-    const int kmax = rh ? 4 : 2;  // X[r][c] = 0 for c > r
-    for (int s = 0; s < kmax; ++s) {
-      bf16x8 ah, al, bh8, bl;
-      split8(&Rt[dt * 32 + l32][16 * s + 8 * g], ah, al);
-      split8(&Ps[rh * 32 + l32][16 * s + 8 * g], bh8, bl);
-      o = mfma32(ah, bh8, o);
-      o = mfma32(ah, bl, o);
-      o = mfma32(al, bh8, o);
-    }
-    // lane: r = rh*32 + l32; elements: d = dt*32 + drow(e, g)
-    const int r = i0 + rh * 32 + l32;
-    float* out32 = vp32 + ((int64_t)bh * T + r) * D;
-    bf16* outb = vpb + ((int64_t)bh * T + r) * D;
-    const int slot = (r & ~15) | jmap(r & 15);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int d0 = dt * 32 + 8 * q + 4 * g;
-      f32x4 f;
-      bf16x4 bb;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        f[u] = o[4 * q + u];
-        bb[u] = (bf16)o[4 * q + u];
-        vpth_w(vpt, bh, D, T, d0 + u, slot, bb[u]);
+  // V'^T[d][r] = sum_c R^T[d][c] X[r][c] for sub-block sb (X lower triangular)
+  auto diag_solve = [&](int sb) {
+    for (int tile = w; tile < NDT * 2; tile += 4) {
+      const int dt = tile >> 1, rh = tile & 1;
+      f32x16 o = zero16();
+      const int kmax = rh ? 4 : 2;
+      for (int st = 0; st < kmax; ++st) {
+        bf16x8 ah, al, bh8, bl;
+        split8(&Rt[dt * 32 + l32][sb * 64 + 16 * st + 8 * g], ah, al);
+        split8(&sm.X[sb][rh * 32 + l32][16 * st + 8 * g], bh8, bl);
+        o = mfma32(ah, bh8, o);
+        o = mfma32(ah, bl, o);
+        o = mfma32(al, bh8, o);
       }
-      *reinterpret_cast<f32x4*>(out32 + d0) = f;
-      *reinterpret_cast<bf16x4*>(outb + d0) = bb;
+      const int rl = rh * 32 + l32;
+      const int r = i0 + sb * 64 + rl;
+      const int slot = (r & ~15) | jmap(r & 15);
+      const int lslot = (rl & ~15) | jmap(rl & 15);
+      float* out32 = vp32 + ((int64_t)bh * T + r) * D;
+      bf16* outb = vpb + ((int64_t)bh * T + r) * D;
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd) {
+        const int d0 = dt * 32 + 8 * qd + 4 * g;
+        f32x4 f;
+        bf16x4 bb;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          f[u] = o[4 * qd + u];
+          bb[u] = (bf16)o[4 * qd + u];
+          vpth_w(vpt, bh, D, T, d0 + u, slot, bb[u]);
+          if (sb == 0) sm.u.fin.vA[d0 + u][lslot] = bb[u];
+        }
+        *reinterpret_cast<f32x4*>(out32 + d0) = f;
+        *reinterpret_cast<bf16x4*>(outb + d0) = bb;
+      }
     }
+  };
+  diag_solve(0);
+  publish_counter(cnt, 2 * i2 + 1);
+
+  // ---- R_B -= P_BA V'_A: wave -> (B rows half nb, A keys half ka) ----
+  {
+    const int nb = w & 1, ka = w >> 1;
+    const int rowB = i0 + 64 + nb * 32 + l32;
+    f32x16 sc = zero16();
+#pragma unroll
+    for (int st = 0; st < NKS; ++st)
+      sc = mfma32(ld8(kh + (int64_t)(i0 + ka * 32 + l32) * ks.t + 16 * st + 8 * g),
+                  ld8(kh + (int64_t)rowB * ks.t + 16 * st + 8 * g), sc);
+    const float aB = sl2 * rv[rowB];
+    float rA[16];
+    load_rows16(rv + i0 + ka * 32, g, rA);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) sc[e] = __builtin_amdgcn_exp2f(fmaf(sc[e] * aB, rA[e], -c0));
+    const bf16x8 p0 = pack_b(sc, 0), p1 = pack_b(sc, 1);
+    f32x16 cr[NDT];
+#pragma unroll
+    for (int t = 0; t < NDT; ++t) {
+      cr[t] = mfma32(ld8(&sm.u.fin.vA[t * 32 + l32][ka * 32 + 8 * g]), p0, zero16());
+      cr[t] = mfma32(ld8(&sm.u.fin.vA[t * 32 + l32][ka * 32 + 16 + 8 * g]), p1, cr[t]);
+    }
+    const int col = 64 + nb * 32 + l32;
+    if (ka == 1) {
+#pragma unroll
+      for (int t = 0; t < NDT; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][col] -= cr[t][e];
+    }
+    __syncthreads();
+    if (ka == 0) {
+#pragma unroll
+      for (int t = 0; t < NDT; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][col] -= cr[t][e];
+    }
+    __syncthreads();
   }
-  publish_counter(counters + bh, i + 1);
+  diag_solve(1);
+  publish_counter(cnt, 2 * i2 + 2);
 }
 
 // ---------------------------------------------------------------------------

@@ -60,12 +60,23 @@ __device__ __forceinline__ float wave_xor32(float v) {
   return __shfl_xor(v, 32, 64);
 }
 
-// Agent-scope acquire poll of a chain progress counter; returns the value seen (> target).
+// Chain progress counters.  Polls use relaxed agent-scope loads (they read the
+// coherent value without touching the caches); a single agent-scope acquire
+// fence is issued once the awaited progress has been seen, so the data loads
+// that follow observe everything the producer released.
+__device__ __forceinline__ int poll_counter(const int* cnt) {
+  return __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void acquire_agent() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }
+
+// Wait until *cnt > target; returns the value seen (acquire semantics).
 __device__ __forceinline__ int wait_counter_gt(const int* cnt, int target) {
-  int v = __hip_atomic_load(cnt, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+  int v = poll_counter(cnt);
   while (v <= target) {
     __builtin_amdgcn_s_sleep(1);
-    v = __hip_atomic_load(cnt, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+    v = poll_counter(cnt);
   }
+  acquire_agent();
   return v;
 }
