@@ -70,13 +70,25 @@ __global__ __launch_bounds__(256) void lucid_bwd_prep_kernel(const bf16* __restr
 }
 
 // ---------------------------------------------------------------------------
-// Column sweep for the attention part.  WG = 128 keys of one kv head
-// (lane <-> key j), loops over the G query heads of the group and over all
-// 64-row query tiles at or below the diagonal.
-//   S[i][j] = Q_i . K_j (D layout m = i, n = j), P = exp2(c S - lse2_i)
+// Column sweep for the attention part.  Workgroup = 256 keys of one kv head,
+// wave w owns keys 64w..64w+63 as two 32-key n-tiles (lane <-> key j); loops
+// over the G query heads of the group and over every 64-row query tile at or
+// below the diagonal.  Each query tile (Q, dO rows; Q^T, dO^T in T-perm
+// layout; lse2 and delta) is staged once per workgroup in LDS, double buffered.
+//   S[i][j] = Q_i . K_j, P = exp2(c S - lse2_i)
 //   dV'^T[d][j] += dO^T[d][i] P[i][j];  dP[i][j] = dO_i . V'_j
 //   dS = P (dP - delta_i);  dK^T[d][j] += Q^T[d][i] dS[i][j]
 // ---------------------------------------------------------------------------
+template <int D>
+struct DkdvSmem {
+  bf16 q[2][64][D + 8];
+  bf16 dO[2][64][D + 8];
+  bf16 qt[2][D][72];
+  bf16 dot[2][D][72];
+  float lse[2][64];
+  float dl[2][64];
+};
+
 template <int D>
 __global__ __launch_bounds__(256) void lucid_attn_bwd_dkdv_kernel(
     const bf16* __restrict__ q, Strides qs, const bf16* __restrict__ k, Strides ks, const bf16* __restrict__ vpb,
@@ -85,31 +97,39 @@ __global__ __launch_bounds__(256) void lucid_attn_bwd_dkdv_kernel(
     float* __restrict__ dka, int Hq, int Hkv, int T, int BH, float scale) {
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
+  constexpr int CH = D / 32;
+  __shared__ __attribute__((aligned(16))) DkdvSmem<D> sm;
   const int id = blockIdx.x;
   const int jb = id / BH, bh = id - (id / BH) * BH;
   const int b = bh / Hkv, h = bh - b * Hkv;
   const int G = Hq / Hkv;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
-  const int jmin = jb * 128 + w * 32;
-  const int jrow = jmin + l32;
+  const int jw = jb * 256 + w * 64;  // first key of this wave
   const bf16* kh = k + b * ks.b + h * ks.h;
   const float c = scale * LOG2E_F;
 
-  bf16x8 kb[NKS], vb[NKS];
+  bf16x8 kb[2][NKS], vb[2][NKS];
 #pragma unroll
-  for (int s = 0; s < NKS; ++s) {
-    kb[s] = ld8(kh + (int64_t)jrow * ks.t + 16 * s + 8 * g);
-    vb[s] = ld8(vpb + ((int64_t)bh * T + jrow) * D + 16 * s + 8 * g);
-  }
-  f32x16 adv[NDT], adk[NDT];
+  for (int nt = 0; nt < 2; ++nt) {
+    const int jr = min(jw + nt * 32 + l32, T - 1);
 #pragma unroll
-  for (int t = 0; t < NDT; ++t) {
-    adv[t] = zero16();
-    adk[t] = zero16();
+    for (int st = 0; st < NKS; ++st) {
+      kb[nt][st] = ld8(kh + (int64_t)jr * ks.t + 16 * st + 8 * g);
+      vb[nt][st] = ld8(vpb + ((int64_t)bh * T + jr) * D + 16 * st + 8 * g);
+    }
   }
-  const int it0 = jmin / 64;
-  const int nt = T / 64;
+  f32x16 adv[NDT][2], adk[NDT][2];
+#pragma unroll
+  for (int t = 0; t < NDT; ++t)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      adv[t][nt] = zero16();
+      adk[t][nt] = zero16();
+    }
+  const int nt64 = T / 64;
+  const int it_first = jb * 4;  // first query tile any wave needs
+  const int it_w = jw / 64;     // this wave's diagonal tile
   for (int gi = 0; gi < G; ++gi) {
     const int hq = h * G + gi;
     const int bhq = b * Hq + hq;
@@ -119,70 +139,140 @@ __global__ __launch_bounds__(256) void lucid_attn_bwd_dkdv_kernel(
     const bf16* doth = dot + (int64_t)bhq * D * T;
     const float* lh = lse + (int64_t)bhq * T;
     const float* dh = delta + (int64_t)bhq * T;
-    for (int it = it0; it < nt; ++it) {
+    bf16x8 stg[4 * CH];
+    f32x4 fstg;
+    auto gload = [&](int it) {
       const int i0 = it * 64;
-      const bool diag = (i0 < jmin + 32);
+      g2r_rows<D>(qh, qs.t, i0, stg);
+      g2r_rows<D>(doh, dos.t, i0, stg + CH);
+      g2r_tp<D>(qth, T, i0, stg + 2 * CH);
+      g2r_tp<D>(doth, T, i0, stg + 3 * CH);
+      if (tid < 16) fstg = *reinterpret_cast<const f32x4*>(lh + i0 + 4 * tid);
+      else if (tid < 32) fstg = *reinterpret_cast<const f32x4*>(dh + i0 + 4 * (tid - 16));
+    };
+    auto lstore = [&](int buf) {
+      r2l_rows<D>(sm.q[buf], stg);
+      r2l_rows<D>(sm.dO[buf], stg + CH);
+      r2l_tp<D>(sm.qt[buf], stg + 2 * CH);
+      r2l_tp<D>(sm.dot[buf], stg + 3 * CH);
+      if (tid < 16) *reinterpret_cast<f32x4*>(&sm.lse[buf][4 * tid]) = fstg;
+      else if (tid < 32) *reinterpret_cast<f32x4*>(&sm.dl[buf][4 * (tid - 16)]) = fstg;
+    };
+    if (it_first < nt64) {
+      gload(it_first);
+      lstore(0);
+    }
+    __syncthreads();
+    for (int it = it_first; it < nt64; ++it) {
+      const int buf = (it - it_first) & 1;
+      const bool more = it + 1 < nt64;
+      if (more) gload(it + 1);
+      if (it >= it_w) {
+        const bool diag = (it == it_w);
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        const int ib0 = i0 + mt * 32;
-        f32x16 s = zero16();
+        for (int mt = 0; mt < 2; ++mt) {
+          float lr[16];
+          lds_rows16(&sm.lse[buf][mt * 32], g, lr);
+          bf16x8 pb[2][2];
+          f32x16 pv[2];
+          {
+            bf16x8 qa[NKS];
 #pragma unroll
-        for (int st = 0; st < NKS; ++st)
-          s = mfma32(ld8(qh + (int64_t)(ib0 + l32) * qs.t + 16 * st + 8 * g), kb[st], s);
-        float lr[16];
-        load_rows16(lh + ib0, g, lr);
+            for (int st = 0; st < NKS; ++st) qa[st] = ld8(&sm.q[buf][mt * 32 + l32][16 * st + 8 * g]);
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          float p = __builtin_amdgcn_exp2f(s[e] * c - lr[e]);
-          if (diag && (ib0 + drow(e, g) < jrow)) p = 0.f;
-          s[e] = p;
-        }
-        const bf16x8 p0 = pack_b(s, 0), p1 = pack_b(s, 1);
+            for (int nt = 0; nt < 2; ++nt) {
+              f32x16 sc = zero16();
 #pragma unroll
-        for (int t = 0; t < NDT; ++t) {
-          const bf16* ap = doth + (int64_t)(t * 32 + l32) * T + ib0 + 8 * g;
-          adv[t] = mfma32(ld8(ap), p0, adv[t]);
-          adv[t] = mfma32(ld8(ap + 16), p1, adv[t]);
-        }
-        f32x16 dp = zero16();
+              for (int st = 0; st < NKS; ++st) sc = mfma32(qa[st], kb[nt][st], sc);
 #pragma unroll
-        for (int st = 0; st < NKS; ++st)
-          dp = mfma32(ld8(doh + (int64_t)(ib0 + l32) * dos.t + 16 * st + 8 * g), vb[st], dp);
-        load_rows16(dh + ib0, g, lr);
+              for (int e = 0; e < 16; ++e) {
+                float p = __builtin_amdgcn_exp2f(fmaf(sc[e], c, -lr[e]));
+                if (diag && (mt * 32 + drow(e, g) < nt * 32 + l32)) p = 0.f;
+                sc[e] = p;
+              }
+              pv[nt] = sc;
+              pb[nt][0] = pack_b(sc, 0);
+              pb[nt][1] = pack_b(sc, 1);
+            }
+          }
 #pragma unroll
-        for (int e = 0; e < 16; ++e) s[e] = s[e] * (dp[e] - lr[e]);
-        const bf16x8 d0 = pack_b(s, 0), d1 = pack_b(s, 1);
+          for (int t = 0; t < NDT; ++t) {
+            const bf16x8 a0 = ld8(&sm.dot[buf][t * 32 + l32][mt * 32 + 8 * g]);
+            const bf16x8 a1 = ld8(&sm.dot[buf][t * 32 + l32][mt * 32 + 16 + 8 * g]);
 #pragma unroll
-        for (int t = 0; t < NDT; ++t) {
-          const bf16* ap = qth + (int64_t)(t * 32 + l32) * T + ib0 + 8 * g;
-          adk[t] = mfma32(ld8(ap), d0, adk[t]);
-          adk[t] = mfma32(ld8(ap + 16), d1, adk[t]);
+            for (int nt = 0; nt < 2; ++nt) {
+              adv[t][nt] = mfma32(a0, pb[nt][0], adv[t][nt]);
+              adv[t][nt] = mfma32(a1, pb[nt][1], adv[t][nt]);
+            }
+          }
+          lds_rows16(&sm.dl[buf][mt * 32], g, lr);
+          {
+            bf16x8 da[NKS];
+#pragma unroll
+            for (int st = 0; st < NKS; ++st) da[st] = ld8(&sm.dO[buf][mt * 32 + l32][16 * st + 8 * g]);
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+              f32x16 dp = zero16();
+#pragma unroll
+              for (int st = 0; st < NKS; ++st) dp = mfma32(da[st], vb[nt][st], dp);
+#pragma unroll
+              for (int e = 0; e < 16; ++e) dp[e] = pv[nt][e] * (dp[e] - lr[e]);
+              pb[nt][0] = pack_b(dp, 0);
+              pb[nt][1] = pack_b(dp, 1);
+            }
+          }
+#pragma unroll
+          for (int t = 0; t < NDT; ++t) {
+            const bf16x8 a0 = ld8(&sm.qt[buf][t * 32 + l32][mt * 32 + 8 * g]);
+            const bf16x8 a1 = ld8(&sm.qt[buf][t * 32 + l32][mt * 32 + 16 + 8 * g]);
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+              adk[t][nt] = mfma32(a0, pb[nt][0], adk[t][nt]);
+              adk[t][nt] = mfma32(a1, pb[nt][1], adk[t][nt]);
+            }
+          }
         }
       }
+      if (more) lstore(buf ^ 1);
+      __syncthreads();
     }
   }
-  float* ov = dvp + ((int64_t)bh * T + jrow) * D;
-  float* ok = dka + ((int64_t)bh * T + jrow) * D;
 #pragma unroll
-  for (int t = 0; t < NDT; ++t)
+  for (int nt = 0; nt < 2; ++nt) {
+    const int jrow = jw + nt * 32 + l32;
+    if (jrow >= T) continue;
+    float* ov = dvp + ((int64_t)bh * T + jrow) * D;
+    float* ok = dka + ((int64_t)bh * T + jrow) * D;
 #pragma unroll
-    for (int qq = 0; qq < 4; ++qq) {
-      f32x4 a, bq;
+    for (int t = 0; t < NDT; ++t)
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        a[u] = adv[t][4 * qq + u];
-        bq[u] = adk[t][4 * qq + u] * scale;
+      for (int qq = 0; qq < 4; ++qq) {
+        f32x4 a, bq;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          a[u] = adv[t][nt][4 * qq + u];
+          bq[u] = adk[t][nt][4 * qq + u] * scale;
+        }
+        *reinterpret_cast<f32x4*>(ov + t * 32 + 8 * qq + 4 * g) = a;
+        *reinterpret_cast<f32x4*>(ok + t * 32 + 8 * qq + 4 * g) = bq;
       }
-      *reinterpret_cast<f32x4*>(ov + t * 32 + 8 * qq + 4 * g) = a;
-      *reinterpret_cast<f32x4*>(ok + t * 32 + 8 * qq + 4 * g) = bq;
-    }
+  }
 }
 
 // ---------------------------------------------------------------------------
-// Row sweep for dQ.  WG = 128 query rows (lane <-> row i), heavy blocks first.
+// Row sweep for dQ.  Workgroup = 256 query rows (heavy blocks first), wave w
+// owns rows 64w..64w+63 (lane <-> row i).  Every key tile (K rows, V' rows,
+// K^T in T-perm layout) is staged once per workgroup in LDS.
 //   S^T[j][i] = K_j . Q_i, dP^T[j][i] = V'_j . dO_i, dS^T = P^T (dP^T - delta_i)
 //   dQ^T[d][i] += K^T[d][j] dS^T[j][i]
 // ---------------------------------------------------------------------------
+template <int D>
+struct DqSmem {
+  bf16 k[2][64][D + 8];
+  bf16 v[2][64][D + 8];
+  bf16 kt[2][D][72];
+};
+
 template <int D>
 __global__ __launch_bounds__(256) void lucid_attn_bwd_dq_kernel(
     const bf16* __restrict__ q, Strides qs, const bf16* __restrict__ k, Strides ks, const bf16* __restrict__ vpb,
@@ -191,71 +281,122 @@ __global__ __launch_bounds__(256) void lucid_attn_bwd_dq_kernel(
     float scale) {
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
-  const int nblk = T / 128;
+  constexpr int CH = D / 32;
+  __shared__ __attribute__((aligned(16))) DqSmem<D> sm;
+  const int nblk = (T + 255) / 256;
   const int id = blockIdx.x;
   const int bhq = id % BHq;
   const int ib = nblk - 1 - id / BHq;
   const int b = bhq / Hq, hq = bhq - b * Hq;
   const int h = hq / (Hq / Hkv);
   const int bh = b * Hkv + h;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
-  const int row0 = ib * 128 + w * 32;
-  const int irow = row0 + l32;
+  const int r0 = ib * 256;
+  const int row0 = r0 + w * 64;
   const bf16* kh = k + b * ks.b + h * ks.h;
   const bf16* vh = vpb + (int64_t)bh * T * D;
   const bf16* kth = kt + (int64_t)bh * D * T;
   const float c = scale * LOG2E_F;
 
-  bf16x8 qb[NKS], db[NKS];
+  bf16x8 qb[2][NKS], db[2][NKS];
+  float li[2], di[2];
 #pragma unroll
-  for (int s = 0; s < NKS; ++s) {
-    qb[s] = ld8(q + b * qs.b + hq * qs.h + (int64_t)irow * qs.t + 16 * s + 8 * g);
-    db[s] = ld8(dout + b * dos.b + hq * dos.h + (int64_t)irow * dos.t + 16 * s + 8 * g);
+  for (int nt = 0; nt < 2; ++nt) {
+    const int ir = min(row0 + nt * 32 + l32, T - 1);
+#pragma unroll
+    for (int st = 0; st < NKS; ++st) {
+      qb[nt][st] = ld8(q + b * qs.b + hq * qs.h + (int64_t)ir * qs.t + 16 * st + 8 * g);
+      db[nt][st] = ld8(dout + b * dos.b + hq * dos.h + (int64_t)ir * dos.t + 16 * st + 8 * g);
+    }
+    li[nt] = lse[(int64_t)bhq * T + ir];
+    di[nt] = delta[(int64_t)bhq * T + ir];
   }
-  const float li = lse[(int64_t)bhq * T + irow];
-  const float di = delta[(int64_t)bhq * T + irow];
-  f32x16 acc[NDT];
+  f32x16 acc[NDT][2];
 #pragma unroll
-  for (int t = 0; t < NDT; ++t) acc[t] = zero16();
-  const int ntile = (row0 + 32 + 63) / 64;
-  for (int jt = 0; jt < ntile; ++jt) {
+  for (int t = 0; t < NDT; ++t) {
+    acc[t][0] = zero16();
+    acc[t][1] = zero16();
+  }
+  const int ntile = (min(r0 + 256, T) + 63) / 64;
+  const int last_w = row0 / 64;
+  bf16x8 stg[3 * CH];
+  auto gload = [&](int jt) {
     const int j0 = jt * 64;
-    const bool diag = (j0 + 63 > row0);
+    g2r_rows<D>(kh, ks.t, j0, stg);
+    g2r_rows<D>(vh, D, j0, stg + CH);
+    g2r_tp<D>(kth, T, j0, stg + 2 * CH);
+  };
+  auto lstore = [&](int buf) {
+    r2l_rows<D>(sm.k[buf], stg);
+    r2l_rows<D>(sm.v[buf], stg + CH);
+    r2l_tp<D>(sm.kt[buf], stg + 2 * CH);
+  };
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  for (int jt = 0; jt < ntile; ++jt) {
+    const int buf = jt & 1;
+    const bool more = jt + 1 < ntile;
+    if (more) gload(jt + 1);
+    if (jt <= last_w && row0 < T) {
+      const bool diag = (jt == last_w);
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      const int jb0 = j0 + mt * 32;
-      f32x16 s = zero16(), dp = zero16();
+      for (int mt = 0; mt < 2; ++mt) {
+        bf16x8 ka[NKS], va[NKS];
 #pragma unroll
-      for (int st = 0; st < NKS; ++st) {
-        s = mfma32(ld8(kh + (int64_t)(jb0 + l32) * ks.t + 16 * st + 8 * g), qb[st], s);
-        dp = mfma32(ld8(vh + (int64_t)(jb0 + l32) * D + 16 * st + 8 * g), db[st], dp);
-      }
+        for (int st = 0; st < NKS; ++st) {
+          ka[st] = ld8(&sm.k[buf][mt * 32 + l32][16 * st + 8 * g]);
+          va[st] = ld8(&sm.v[buf][mt * 32 + l32][16 * st + 8 * g]);
+        }
+        bf16x8 dsb[2][2];
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        float p = __builtin_amdgcn_exp2f(s[e] * c - li);
-        if (diag && (jb0 + drow(e, g) > irow)) p = 0.f;
-        s[e] = p * (dp[e] - di);
-      }
-      const bf16x8 d0 = pack_b(s, 0), d1 = pack_b(s, 1);
+        for (int nt = 0; nt < 2; ++nt) {
+          f32x16 sc = zero16(), dp = zero16();
 #pragma unroll
-      for (int t = 0; t < NDT; ++t) {
-        const bf16* ap = kth + (int64_t)(t * 32 + l32) * T + jb0 + 8 * g;
-        acc[t] = mfma32(ld8(ap), d0, acc[t]);
-        acc[t] = mfma32(ld8(ap + 16), d1, acc[t]);
+          for (int st = 0; st < NKS; ++st) {
+            sc = mfma32(ka[st], qb[nt][st], sc);
+            dp = mfma32(va[st], db[nt][st], dp);
+          }
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            float p = __builtin_amdgcn_exp2f(fmaf(sc[e], c, -li[nt]));
+            if (diag && (mt * 32 + drow(e, g) > nt * 32 + l32)) p = 0.f;
+            sc[e] = p * (dp[e] - di[nt]);
+          }
+          dsb[nt][0] = pack_b(sc, 0);
+          dsb[nt][1] = pack_b(sc, 1);
+        }
+#pragma unroll
+        for (int t = 0; t < NDT; ++t) {
+          const bf16x8 a0 = ld8(&sm.kt[buf][t * 32 + l32][mt * 32 + 8 * g]);
+          const bf16x8 a1 = ld8(&sm.kt[buf][t * 32 + l32][mt * 32 + 16 + 8 * g]);
+#pragma unroll
+          for (int nt = 0; nt < 2; ++nt) {
+            acc[t][nt] = mfma32(a0, dsb[nt][0], acc[t][nt]);
+            acc[t][nt] = mfma32(a1, dsb[nt][1], acc[t][nt]);
+          }
+        }
       }
     }
+    if (more) lstore(buf ^ 1);
+    __syncthreads();
   }
-  bf16* op = dq + b * dqs.b + hq * dqs.h + (int64_t)irow * dqs.t;
 #pragma unroll
-  for (int t = 0; t < NDT; ++t)
+  for (int nt = 0; nt < 2; ++nt) {
+    const int irow = row0 + nt * 32 + l32;
+    if (irow >= T) continue;
+    bf16* op = dq + b * dqs.b + hq * dqs.h + (int64_t)irow * dqs.t;
 #pragma unroll
-    for (int qq = 0; qq < 4; ++qq) {
-      bf16x4 bb;
+    for (int t = 0; t < NDT; ++t)
 #pragma unroll
-      for (int u = 0; u < 4; ++u) bb[u] = (bf16)(acc[t][4 * qq + u] * scale);
-      *reinterpret_cast<bf16x4*>(op + t * 32 + 8 * qq + 4 * g) = bb;
-    }
+      for (int qq = 0; qq < 4; ++qq) {
+        bf16x4 bb;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) bb[u] = (bf16)(acc[t][nt][4 * qq + u] * scale);
+        *reinterpret_cast<bf16x4*>(op + t * 32 + 8 * qq + 4 * g) = bb;
+      }
+  }
 }
 
 // ---------------------------------------------------------------------------

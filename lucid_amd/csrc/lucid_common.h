@@ -79,4 +79,56 @@ __device__ __forceinline__ void load_rows16(const float* __restrict__ p, int g, 
   }
 }
 
+// ---------------------------------------------------------------------------
+// Cooperative LDS staging of 64-wide tiles by a 256-thread workgroup with
+// coalesced 16-byte global loads (D/32 chunks per thread per tile).
+//   row tile:    [64 rows][D]   from rows j0.. of a [T][D]-strided source
+//   T-perm tile: [D][64 slots]  from a [D][T] T-perm source (slots j0..)
+// g2r_* loads into registers (issued early, overlapping compute), r2l_* stores
+// the registers to LDS.
+// ---------------------------------------------------------------------------
+template <int D>
+__device__ __forceinline__ void g2r_rows(const bf16* __restrict__ src, int64_t st, int j0, bf16x8* stg) {
+#pragma unroll
+  for (int u = 0; u < D / 32; ++u) {
+    const int c = threadIdx.x + 256 * u;
+    stg[u] = ld8(src + (int64_t)(j0 + c / (D / 8)) * st + (c % (D / 8)) * 8);
+  }
+}
+template <int D>
+__device__ __forceinline__ void r2l_rows(bf16 (*dst)[D + 8], const bf16x8* stg) {
+#pragma unroll
+  for (int u = 0; u < D / 32; ++u) {
+    const int c = threadIdx.x + 256 * u;
+    *reinterpret_cast<bf16x8*>(&dst[c / (D / 8)][(c % (D / 8)) * 8]) = stg[u];
+  }
+}
+template <int D>
+__device__ __forceinline__ void g2r_tp(const bf16* __restrict__ src, int T, int j0, bf16x8* stg) {
+#pragma unroll
+  for (int u = 0; u < D / 32; ++u) {
+    const int c = threadIdx.x + 256 * u;
+    stg[u] = ld8(src + (int64_t)(c >> 3) * T + j0 + (c & 7) * 8);
+  }
+}
+template <int D>
+__device__ __forceinline__ void r2l_tp(bf16 (*dst)[72], const bf16x8* stg) {
+#pragma unroll
+  for (int u = 0; u < D / 32; ++u) {
+    const int c = threadIdx.x + 256 * u;
+    *reinterpret_cast<bf16x8*>(&dst[c >> 3][(c & 7) * 8]) = stg[u];
+  }
+}
+// 16 fp32 values of a staged per-row vector for D-layout rows base + drow(e, g)
+__device__ __forceinline__ void lds_rows16(const float* p, int g, float out[16]) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const f32x4 t4 = *reinterpret_cast<const f32x4*>(p + 8 * q + 4 * g);
+    out[4 * q] = t4[0];
+    out[4 * q + 1] = t4[1];
+    out[4 * q + 2] = t4[2];
+    out[4 * q + 3] = t4[3];
+  }
+}
+
 }  // namespace lucid
