@@ -401,13 +401,39 @@ __global__ __launch_bounds__(256) void lucid_attn_bwd_dq_kernel(
 
 // ---------------------------------------------------------------------------
 // Chained transposed solve dV = P^-T dV' (Lucid_Tril_Solver.backward :328-334)
-// and the column sums C_J = sum_{I >= J} M_IJ^T K^_I.
-// WG id -> (J = NT-1 - id/BH, bh = id % BH): ids grow as J falls, so block J
-// waits only on later blocks that have lower ids.  Counter value n means
-// blocks NT-1 .. NT-n are published.
-// wave w: ch = w & 1 -> columns J0 + 32ch .. (lane <-> column),
-//         ih = w >> 1 -> rows I0 + 32ih .. of every later 64-row block.
+// and the column sums C_J = sum_{I >= J} M_IJ^T K^_I, M = (dV V'^T) * P.
+// Workgroup = 128 columns: sub-blocks A = J0..J0+63 and B = J0+64..J0+127.
+// id -> (p = NP-1 - id/BH, bh = id % BH): ids grow as p falls, so a workgroup
+// waits only on later blocks held by lower ids.  counters[bh] = n means the
+// last n 64-blocks of dV are published.
+// wave w: cb = w & 1 -> columns J0 + 64*cb .. +64 (two n-tiles, lane <-> column)
+//         ih = w >> 1 -> rows 32*ih .. +32 of every staged 64-row tile I
+// Each later row tile (K rows, dV rows, dV^T and K^T in T-perm layout, 1/rms)
+// is staged once in LDS (double buffered):
+//   S[I][J] = K_I . K_J, P = exp(s r_I r_J S - 1/s), G[I][J] = dV_I . V'_J
+//   acc^T[d][J] += dV^T[d][I] P[I][J];  C^T[d][J] += K^T[d][I] (r_I G P)[I][J]
+// Then dV_B = X_B^T (dV'_B - acc_B), dV_A = X_A^T (dV'_A - acc_A - P_BA^T dV_B),
+// and the diagonal-block terms of C.
 // ---------------------------------------------------------------------------
+template <int D>
+struct PcolSmem {
+  union {
+    struct {
+      bf16 k[2][64][D + 8];
+      bf16 dv[2][64][D + 8];
+      bf16 dvt[2][D][72];
+      bf16 kt[2][D][72];
+      float r[2][64];
+    } st;
+    struct {
+      float Rt[D][132];       // R^T for the 128 columns (0..63 = A, 64..127 = B), reductions
+      float Xt[2][64][68];    // Xt[sb][c][r] = (P_diag^-1)[r][c]
+      bf16 dvl[2][64][D + 8]; // dV rows of A and B (bf16)
+      bf16 dvtB[D][72];       // dV_B^T, T-perm within the block
+    } fin;
+  } u;
+};
+
 template <int D>
 __global__ __launch_bounds__(256) void lucid_precond_bwd_col_kernel(
     const bf16* __restrict__ k, Strides ks, int Hkv, int T, int BH, const float* __restrict__ rinv, float scale,
@@ -416,192 +442,350 @@ __global__ __launch_bounds__(256) void lucid_precond_bwd_col_kernel(
     Strides dvs, float* __restrict__ colsum, int* __restrict__ counters) {
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
-  __shared__ __attribute__((aligned(16))) float Ps[64][68];    // P_JJ, lower
-  __shared__ __attribute__((aligned(16))) float Xt[64][68];    // Xt[c][r] = (P_JJ^-1)[r][c]
-  __shared__ __attribute__((aligned(16))) float Rt[D][68];     // reductions, R^T
-  __shared__ __attribute__((aligned(16))) bf16 dvl[64][D + 8]; // dV_J rows (bf16)
+  constexpr int CH = D / 32;
+  __shared__ __attribute__((aligned(16))) PcolSmem<D> sm;
 
-  const int NT = T / 64;
+  const int NT = T / 64, NP = T / 128;
   const int id = blockIdx.x;
-  const int J = NT - 1 - id / BH, bh = id - (id / BH) * BH;
+  const int p = NP - 1 - id / BH, bh = id - (id / BH) * BH;
   const int b = bh / Hkv, h = bh - b * Hkv;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
-  const int ch = w & 1, ih = w >> 1;
-  const int J0 = J * 64;
-  const int jcol = J0 + ch * 32 + l32;
+  const int cb = w & 1, ih = w >> 1;
+  const int J0 = p * 128;
   const bf16* kh = k + b * ks.b + h * ks.h;
   const float* rv = rinv + (int64_t)bh * T;
   const bf16* kth = kt + (int64_t)bh * D * T;
   const bf16* dvth = dvt + (int64_t)bh * D * T;
   const bf16* dvbh = dvb + (int64_t)bh * T * D;
+  const bf16* vph = vpb + (int64_t)bh * T * D;
+  int* cnt = counters + bh;
   const float sl2 = scale * LOG2E_F;
   const float c0 = LOG2E_F / scale;
 
-  bf16x8 kbJ[NKS], vbJ[NKS];
+  bf16x8 kbJ[2][NKS], vbJ[2][NKS];
+  float aJ[2];
 #pragma unroll
-  for (int s = 0; s < NKS; ++s) {
-    kbJ[s] = ld8(kh + (int64_t)jcol * ks.t + 16 * s + 8 * g);
-    vbJ[s] = ld8(vpb + ((int64_t)bh * T + jcol) * D + 16 * s + 8 * g);
-  }
-  const float aJ = sl2 * rv[jcol];
-  {
-    f32x16 sd = zero16();
-#pragma unroll
-    for (int s = 0; s < NKS; ++s)
-      sd = mfma32(ld8(kh + (int64_t)(J0 + ih * 32 + l32) * ks.t + 16 * s + 8 * g), kbJ[s], sd);
-    const int n = ch * 32 + l32;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int m = ih * 32 + drow(e, g);
-      Ps[m][n] = (n <= m) ? __builtin_amdgcn_exp2f(sd[e] * aJ * rv[J0 + m] - c0) : 0.f;
-    }
-  }
-  {
-    const float* xp = pinv + ((int64_t)bh * NT + J) * 4096;
-    for (int idx = tid; idx < 4096; idx += 256) Xt[idx & 63][idx >> 6] = xp[idx];
-  }
-
-  f32x16 adv[NDT], acs[NDT];
-#pragma unroll
-  for (int t = 0; t < NDT; ++t) {
-    adv[t] = zero16();
-    acs[t] = zero16();
-  }
-  int ready = 0;
-  for (int I = NT - 1; I > J; --I) {
-    const int need = NT - 1 - I;
-    if (need >= ready) ready = wait_counter_gt(counters + bh, need);
-    const int I0 = I * 64 + ih * 32;
-    f32x16 s = zero16(), gg = zero16();
+  for (int nt = 0; nt < 2; ++nt) {
+    const int jc = J0 + cb * 64 + nt * 32 + l32;
 #pragma unroll
     for (int st = 0; st < NKS; ++st) {
-      s = mfma32(ld8(kh + (int64_t)(I0 + l32) * ks.t + 16 * st + 8 * g), kbJ[st], s);
-      gg = mfma32(ld8(dvbh + (int64_t)(I0 + l32) * D + 16 * st + 8 * g), vbJ[st], gg);
+      kbJ[nt][st] = ld8(kh + (int64_t)jc * ks.t + 16 * st + 8 * g);
+      vbJ[nt][st] = ld8(vph + (int64_t)jc * D + 16 * st + 8 * g);
     }
-    float rI[16];
-    load_rows16(rv + I0, g, rI);
+    aJ[nt] = sl2 * rv[jc];
+  }
+  f32x16 adv[NDT][2], acs[NDT][2];
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const float p = __builtin_amdgcn_exp2f(s[e] * aJ * rI[e] - c0);
-      s[e] = p;
-      gg[e] = gg[e] * p * rI[e];
-    }
-    const bf16x8 p0 = pack_b(s, 0), p1 = pack_b(s, 1);
-    const bf16x8 m0 = pack_b(gg, 0), m1 = pack_b(gg, 1);
+  for (int t = 0; t < NDT; ++t)
 #pragma unroll
-    for (int t = 0; t < NDT; ++t) {
-      const bf16* ap = dvth + (int64_t)(t * 32 + l32) * T + I0 + 8 * g;
-      adv[t] = mfma32(ld8(ap), p0, adv[t]);
-      adv[t] = mfma32(ld8(ap + 16), p1, adv[t]);
-      const bf16* kp = kth + (int64_t)(t * 32 + l32) * T + I0 + 8 * g;
-      acs[t] = mfma32(ld8(kp), m0, acs[t]);
-      acs[t] = mfma32(ld8(kp + 16), m1, acs[t]);
+    for (int nt = 0; nt < 2; ++nt) {
+      adv[t][nt] = zero16();
+      acs[t][nt] = zero16();
     }
+
+  // ---- sweep over the later 64-row tiles, far (published first) to near ----
+  const int first = NT - 1, last = 2 * p + 2;  // tiles first, first-1, ..., last
+  int ready = 0;
+  bf16x8 stg[4 * CH];
+  f32x4 rstg;
+  auto gload = [&](int I) {
+    const int i0 = I * 64;
+    g2r_rows<D>(kh, ks.t, i0, stg);
+    g2r_rows<D>(dvbh, D, i0, stg + CH);
+    g2r_tp<D>(dvth, T, i0, stg + 2 * CH);
+    g2r_tp<D>(kth, T, i0, stg + 3 * CH);
+    if (tid < 16) rstg = *reinterpret_cast<const f32x4*>(rv + i0 + 4 * tid);
+  };
+  auto lstore = [&](int buf) {
+    r2l_rows<D>(sm.u.st.k[buf], stg);
+    r2l_rows<D>(sm.u.st.dv[buf], stg + CH);
+    r2l_tp<D>(sm.u.st.dvt[buf], stg + 2 * CH);
+    r2l_tp<D>(sm.u.st.kt[buf], stg + 3 * CH);
+    if (tid < 16) *reinterpret_cast<f32x4*>(&sm.u.st.r[buf][4 * tid]) = rstg;
+  };
+  // tile I is published once the counter exceeds NT-1-I
+  if (first >= last) {
+    ready = wait_counter_gt(cnt, NT - 1 - first);
+    gload(first);
+    lstore(0);
+  }
+  __syncthreads();
+  for (int I = first; I >= last; --I) {
+    const int buf = (first - I) & 1;
+    const bool more = I - 1 >= last;
+    bool early = false;
+    if (more) {
+      const int need = NT - 1 - (I - 1);
+      if (need >= ready) {
+        const int seen = poll_counter(cnt);
+        if (seen > need) {
+          acquire_agent();
+          ready = seen;
+        }
+      }
+      early = need < ready;
+      if (early) gload(I - 1);
+    }
+    {
+      bf16x8 ka[NKS], da[NKS];
+#pragma unroll
+      for (int st = 0; st < NKS; ++st) {
+        ka[st] = ld8(&sm.u.st.k[buf][ih * 32 + l32][16 * st + 8 * g]);
+        da[st] = ld8(&sm.u.st.dv[buf][ih * 32 + l32][16 * st + 8 * g]);
+      }
+      float rI[16];
+      lds_rows16(&sm.u.st.r[buf][ih * 32], g, rI);
+      bf16x8 pb[2][2], mb[2][2];
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        f32x16 sc = zero16(), gg = zero16();
+#pragma unroll
+        for (int st = 0; st < NKS; ++st) {
+          sc = mfma32(ka[st], kbJ[nt][st], sc);
+          gg = mfma32(da[st], vbJ[nt][st], gg);
+        }
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const float pe = __builtin_amdgcn_exp2f(fmaf(sc[e] * aJ[nt], rI[e], -c0));
+          sc[e] = pe;
+          gg[e] = gg[e] * pe * rI[e];
+        }
+        pb[nt][0] = pack_b(sc, 0);
+        pb[nt][1] = pack_b(sc, 1);
+        mb[nt][0] = pack_b(gg, 0);
+        mb[nt][1] = pack_b(gg, 1);
+      }
+#pragma unroll
+      for (int t = 0; t < NDT; ++t) {
+        const bf16x8 a0 = ld8(&sm.u.st.dvt[buf][t * 32 + l32][ih * 32 + 8 * g]);
+        const bf16x8 a1 = ld8(&sm.u.st.dvt[buf][t * 32 + l32][ih * 32 + 16 + 8 * g]);
+        const bf16x8 k0 = ld8(&sm.u.st.kt[buf][t * 32 + l32][ih * 32 + 8 * g]);
+        const bf16x8 k1 = ld8(&sm.u.st.kt[buf][t * 32 + l32][ih * 32 + 16 + 8 * g]);
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+          adv[t][nt] = mfma32(a0, pb[nt][0], adv[t][nt]);
+          adv[t][nt] = mfma32(a1, pb[nt][1], adv[t][nt]);
+          acs[t][nt] = mfma32(k0, mb[nt][0], acs[t][nt]);
+          acs[t][nt] = mfma32(k1, mb[nt][1], acs[t][nt]);
+        }
+      }
+    }
+    if (more) {
+      if (!early) {
+        ready = wait_counter_gt(cnt, NT - 1 - (I - 1));
+        gload(I - 1);
+      }
+      lstore(buf ^ 1);
+    }
+    __syncthreads();
   }
 
-  // ---- R_J = dV'_J - sum_{I>J} P_IJ^T dV_I (reduce the two row halves) ----
+  // ---- R = dV' - acc (reduce the two row halves), load X^T of both sub-blocks ----
+  float(*Rt)[132] = sm.u.fin.Rt;
   if (ih == 1) {
 #pragma unroll
     for (int t = 0; t < NDT; ++t)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][ch * 32 + l32] = adv[t][e];
+      for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][cb * 64 + nt * 32 + l32] = adv[t][nt][e];
+  }
+  for (int idx = tid; idx < 2 * 4096; idx += 256) {
+    const int sb = idx >> 12, r = (idx >> 6) & 63, cc = idx & 63;
+    sm.u.fin.Xt[sb][cc][r] = pinv[((int64_t)bh * NT + 2 * p + sb) * 4096 + r * 64 + cc];
   }
   __syncthreads();
   if (ih == 0) {
-    const float* src = dvp + ((int64_t)bh * T + jcol) * D;
 #pragma unroll
-    for (int t = 0; t < NDT; ++t)
+    for (int nt = 0; nt < 2; ++nt) {
+      const int col = cb * 64 + nt * 32 + l32;
+      const float* src = dvp + ((int64_t)bh * T + J0 + col) * D;
 #pragma unroll
-      for (int qq = 0; qq < 4; ++qq) {
-        const int d0 = t * 32 + 8 * qq + 4 * g;
-        const f32x4 x = *reinterpret_cast<const f32x4*>(src + d0);
+      for (int t = 0; t < NDT; ++t)
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
-          Rt[d0 + u][ch * 32 + l32] = x[u] - (adv[t][4 * qq + u] + Rt[d0 + u][ch * 32 + l32]);
-      }
+        for (int qq = 0; qq < 4; ++qq) {
+          const int d0 = t * 32 + 8 * qq + 4 * g;
+          const f32x4 x = *reinterpret_cast<const f32x4*>(src + d0);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) Rt[d0 + u][col] = x[u] - (adv[t][nt][4 * qq + u] + Rt[d0 + u][col]);
+        }
+    }
   }
   __syncthreads();
 
-  // ---- dV^T[d][c] = sum_r R^T[d][r] X[r][c]  (X lower: r >= c) ----
-  for (int tile = w; tile < NDT * 2; tile += 4) {
-    const int dt = tile >> 1, chh = tile & 1;
-    f32x16 o = zero16();
-    for (int s = chh ? 2 : 0; s < 4; ++s) {
-      bf16x8 ah, al, bh8, bl;
-      split8(&Rt[dt * 32 + l32][16 * s + 8 * g], ah, al);
-      split8(&Xt[chh * 32 + l32][16 * s + 8 * g], bh8, bl);
-      o = mfma32(ah, bh8, o);
-      o = mfma32(ah, bl, o);
-      o = mfma32(al, bh8, o);
-    }
-    const int cl = chh * 32 + l32;
-    const int r = J0 + cl;
-    const int slot = (r & ~15) | jmap(r & 15);
-    bf16* ob = dvb + ((int64_t)bh * T + r) * D;
-    bf16* ou = dv_out + b * dvs.b + h * dvs.h + (int64_t)r * dvs.t;
-#pragma unroll
-    for (int qq = 0; qq < 4; ++qq) {
-      const int d0 = dt * 32 + 8 * qq + 4 * g;
-      bf16x4 bb;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        bb[u] = (bf16)o[4 * qq + u];
-        vpth_w(dvt, bh, D, T, d0 + u, slot, bb[u]);
-        dvl[cl][d0 + u] = bb[u];
+  // dV^T[d][c] = sum_r R^T[d][r] X[r][c] for sub-block sb (X lower: r >= c)
+  auto diag_solve = [&](int sb) {
+    for (int tile = w; tile < NDT * 2; tile += 4) {
+      const int dt = tile >> 1, chh = tile & 1;
+      f32x16 o = zero16();
+      for (int st = chh ? 2 : 0; st < 4; ++st) {
+        bf16x8 ah, al, bh8, bl;
+        split8(&Rt[dt * 32 + l32][sb * 64 + 16 * st + 8 * g], ah, al);
+        split8(&sm.u.fin.Xt[sb][chh * 32 + l32][16 * st + 8 * g], bh8, bl);
+        o = mfma32(ah, bh8, o);
+        o = mfma32(ah, bl, o);
+        o = mfma32(al, bh8, o);
       }
-      *reinterpret_cast<bf16x4*>(ob + d0) = bb;
-      *reinterpret_cast<bf16x4*>(ou + d0) = bb;
+      const int cl = chh * 32 + l32;
+      const int r = J0 + sb * 64 + cl;
+      const int slot = (r & ~15) | jmap(r & 15);
+      const int lslot = (cl & ~15) | jmap(cl & 15);
+      bf16* ob = dvb + ((int64_t)bh * T + r) * D;
+      bf16* ou = dv_out + b * dvs.b + h * dvs.h + (int64_t)r * dvs.t;
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) {
+        const int d0 = dt * 32 + 8 * qq + 4 * g;
+        bf16x4 bb;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          bb[u] = (bf16)o[4 * qq + u];
+          vpth_w(dvt, bh, D, T, d0 + u, slot, bb[u]);
+          sm.u.fin.dvl[sb][cl][d0 + u] = bb[u];
+          if (sb == 1) sm.u.fin.dvtB[d0 + u][lslot] = bb[u];
+        }
+        *reinterpret_cast<bf16x4*>(ob + d0) = bb;
+        *reinterpret_cast<bf16x4*>(ou + d0) = bb;
+      }
     }
-  }
-  publish_counter(counters + bh, NT - J);
+  };
+  diag_solve(1);
+  publish_counter(cnt, NT - (2 * p + 1));
 
-  // ---- diagonal block of the column sums: M_JJ = tril((dV_J V'_J^T) * P_JJ) ----
+  // ---- R_A -= P_BA^T dV_B: wave -> (A columns half na, B rows half kb) ----
   {
-    f32x16 gg = zero16();
+    const int na = w & 1, kb = w >> 1;
+    const int colA = J0 + na * 32 + l32;
+    f32x16 sc = zero16();
 #pragma unroll
-    for (int st = 0; st < NKS; ++st) gg = mfma32(ld8(&dvl[ih * 32 + l32][16 * st + 8 * g]), vbJ[st], gg);
-    float rr[16];
-    load_rows16(rv + J0 + ih * 32, g, rr);
-    const int n = ch * 32 + l32;
+    for (int st = 0; st < NKS; ++st)
+      sc = mfma32(ld8(kh + (int64_t)(J0 + 64 + kb * 32 + l32) * ks.t + 16 * st + 8 * g),
+                  ld8(kh + (int64_t)colA * ks.t + 16 * st + 8 * g), sc);
+    const float aA = sl2 * rv[colA];
+    float rB[16];
+    load_rows16(rv + J0 + 64 + kb * 32, g, rB);
 #pragma unroll
-    for (int e = 0; e < 16; ++e) gg[e] = gg[e] * Ps[ih * 32 + drow(e, g)][n] * rr[e];
-    const bf16x8 m0 = pack_b(gg, 0), m1 = pack_b(gg, 1);
+    for (int e = 0; e < 16; ++e) sc[e] = __builtin_amdgcn_exp2f(fmaf(sc[e] * aA, rB[e], -c0));
+    const bf16x8 p0 = pack_b(sc, 0), p1 = pack_b(sc, 1);
+    f32x16 cr[NDT];
 #pragma unroll
     for (int t = 0; t < NDT; ++t) {
-      const bf16* kp = kth + (int64_t)(t * 32 + l32) * T + J0 + ih * 32 + 8 * g;
-      acs[t] = mfma32(ld8(kp), m0, acs[t]);
-      acs[t] = mfma32(ld8(kp + 16), m1, acs[t]);
+      cr[t] = mfma32(ld8(&sm.u.fin.dvtB[t * 32 + l32][kb * 32 + 8 * g]), p0, zero16());
+      cr[t] = mfma32(ld8(&sm.u.fin.dvtB[t * 32 + l32][kb * 32 + 16 + 8 * g]), p1, cr[t]);
+    }
+    const int col = na * 32 + l32;
+    if (kb == 1) {
+#pragma unroll
+      for (int t = 0; t < NDT; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][col] -= cr[t][e];
+    }
+    __syncthreads();
+    if (kb == 0) {
+#pragma unroll
+      for (int t = 0; t < NDT; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][col] -= cr[t][e];
+    }
+    __syncthreads();
+  }
+  diag_solve(0);
+  publish_counter(cnt, NT - 2 * p);
+
+  // ---- diagonal-block terms of the column sums (rows r >= columns c inside the workgroup) ----
+  // wave (cb, ih): columns of sub-block cb; rows of sub-block rb = cb..1, half ih
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) {
+    if (rb < cb) continue;
+    const int rbase = J0 + rb * 64 + ih * 32;  // 32 rows handled by this wave
+    bf16x8 ka[NKS], da[NKS];
+#pragma unroll
+    for (int st = 0; st < NKS; ++st) {
+      ka[st] = ld8(kh + (int64_t)(rbase + l32) * ks.t + 16 * st + 8 * g);
+      da[st] = ld8(&sm.u.fin.dvl[rb][ih * 32 + l32][16 * st + 8 * g]);
+    }
+    float rr[16];
+    load_rows16(rv + rbase, g, rr);
+    bf16x8 mb[2][2];
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      f32x16 sc = zero16(), gg = zero16();
+#pragma unroll
+      for (int st = 0; st < NKS; ++st) {
+        sc = mfma32(ka[st], kbJ[nt][st], sc);
+        gg = mfma32(da[st], vbJ[nt][st], gg);
+      }
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int rloc = rb * 64 + ih * 32 + drow(e, g), cloc = cb * 64 + nt * 32 + l32;
+        const float pe = (rloc >= cloc) ? __builtin_amdgcn_exp2f(fmaf(sc[e] * aJ[nt], rr[e], -c0)) : 0.f;
+        gg[e] = gg[e] * pe * rr[e];
+      }
+      mb[nt][0] = pack_b(gg, 0);
+      mb[nt][1] = pack_b(gg, 1);
+    }
+#pragma unroll
+    for (int t = 0; t < NDT; ++t) {
+      const bf16* kp = kth + (int64_t)(t * 32 + l32) * T + rbase + 8 * g;
+      const bf16x8 k0 = ld8(kp), k1 = ld8(kp + 16);
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        acs[t][nt] = mfma32(k0, mb[nt][0], acs[t][nt]);
+        acs[t][nt] = mfma32(k1, mb[nt][1], acs[t][nt]);
+      }
     }
   }
+  // ---- reduce the two row halves of the column sums and store ----
   __syncthreads();
   if (ih == 1) {
 #pragma unroll
     for (int t = 0; t < NDT; ++t)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][ch * 32 + l32] = acs[t][e];
+      for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][cb * 64 + nt * 32 + l32] = acs[t][nt][e];
   }
   __syncthreads();
   if (ih == 0) {
-    float* dst = colsum + ((int64_t)bh * T + jcol) * D;
 #pragma unroll
-    for (int t = 0; t < NDT; ++t)
+    for (int nt = 0; nt < 2; ++nt) {
+      const int col = cb * 64 + nt * 32 + l32;
+      float* dst = colsum + ((int64_t)bh * T + J0 + col) * D;
 #pragma unroll
-      for (int qq = 0; qq < 4; ++qq) {
-        const int d0 = t * 32 + 8 * qq + 4 * g;
-        f32x4 x;
+      for (int t = 0; t < NDT; ++t)
 #pragma unroll
-        for (int u = 0; u < 4; ++u) x[u] = acs[t][4 * qq + u] + Rt[d0 + u][ch * 32 + l32];
-        *reinterpret_cast<f32x4*>(dst + d0) = x;
-      }
+        for (int qq = 0; qq < 4; ++qq) {
+          const int d0 = t * 32 + 8 * qq + 4 * g;
+          f32x4 x;
+#pragma unroll
+          for (int u = 0; u < 4; ++u) x[u] = acs[t][nt][4 * qq + u] + Rt[d0 + u][col];
+          *reinterpret_cast<f32x4*>(dst + d0) = x;
+        }
+    }
   }
 }
 
 // ---------------------------------------------------------------------------
-// Row sums R_I = sum_{J <= I} M_IJ K^_J, then dK^ = -s (R + C), RMSNorm
+// Row sums R_I = sum_{J <= I} M_IJ K^_J, then dK^ = -s (R + C), the RMSNorm
 // backward and the attention dK.  No chain: every dV is known.
-// wave w: ih = w & 1 -> rows (lane <-> row I), jh = w >> 1 -> key half.
+// Workgroup = 128 rows; wave w: ih = w & 1 -> rows 64*ih .. +64 (lane <-> row),
+// jh = w >> 1 -> keys 32*jh .. +32 of every staged 64-key tile J
+// (K rows, V' rows, K^T in T-perm layout, 1/rms), double buffered in LDS:
+//   S^T[J][I] = K_J . K_I, G^T[J][I] = V'_J . dV_I, R^T[d][I] += K^T[d][J] (r_J G P)^T[J][I]
 // ---------------------------------------------------------------------------
+template <int D>
+struct ProwSmem {
+  union {
+    struct {
+      bf16 k[2][64][D + 8];
+      bf16 v[2][64][D + 8];
+      bf16 kt[2][D][72];
+      float r[2][64];
+    } st;
+    float Rt[D][132];
+  } u;
+};
+
 template <int D>
 __global__ __launch_bounds__(256) void lucid_precond_bwd_row_kernel(
     const bf16* __restrict__ k, Strides ks, int Hkv, int T, int BH, const float* __restrict__ rinv, float scale,
@@ -609,15 +793,16 @@ __global__ __launch_bounds__(256) void lucid_precond_bwd_row_kernel(
     const float* __restrict__ colsum, const float* __restrict__ dka, bf16* __restrict__ dk_out, Strides dks) {
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
-  __shared__ __attribute__((aligned(16))) float Rt[D][68];
-  const int NT = T / 64;
+  constexpr int CH = D / 32;
+  __shared__ __attribute__((aligned(16))) ProwSmem<D> sm;
+  const int NP = T / 128;
   const int id = blockIdx.x;
-  const int I = NT - 1 - id / BH, bh = id - (id / BH) * BH;
+  const int p = NP - 1 - id / BH, bh = id - (id / BH) * BH;  // heavy (late) blocks first
   const int b = bh / Hkv, h = bh - b * Hkv;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
   const int ih = w & 1, jh = w >> 1;
-  const int irow = I * 64 + ih * 32 + l32;
+  const int I0 = p * 128;
   const bf16* kh = k + b * ks.b + h * ks.h;
   const float* rv = rinv + (int64_t)bh * T;
   const bf16* kth = kt + (int64_t)bh * D * T;
@@ -625,89 +810,147 @@ __global__ __launch_bounds__(256) void lucid_precond_bwd_row_kernel(
   const float sl2 = scale * LOG2E_F;
   const float c0 = LOG2E_F / scale;
 
-  bf16x8 kbI[NKS], dbI[NKS];
+  bf16x8 kbI[2][NKS], dbI[2][NKS];
+  float aI[2];
 #pragma unroll
-  for (int s = 0; s < NKS; ++s) {
-    kbI[s] = ld8(kh + (int64_t)irow * ks.t + 16 * s + 8 * g);
-    dbI[s] = ld8(dvb + ((int64_t)bh * T + irow) * D + 16 * s + 8 * g);
-  }
-  const float ri = rv[irow];
-  const float aI = sl2 * ri;
-  f32x16 acc[NDT];
-#pragma unroll
-  for (int t = 0; t < NDT; ++t) acc[t] = zero16();
-  for (int J = 0; J <= I; ++J) {
-    const int J0 = J * 64 + jh * 32;
-    f32x16 s = zero16(), gg = zero16();
+  for (int nt = 0; nt < 2; ++nt) {
+    const int ir = I0 + ih * 64 + nt * 32 + l32;
 #pragma unroll
     for (int st = 0; st < NKS; ++st) {
-      s = mfma32(ld8(kh + (int64_t)(J0 + l32) * ks.t + 16 * st + 8 * g), kbI[st], s);
-      gg = mfma32(ld8(vh + (int64_t)(J0 + l32) * D + 16 * st + 8 * g), dbI[st], gg);
+      kbI[nt][st] = ld8(kh + (int64_t)ir * ks.t + 16 * st + 8 * g);
+      dbI[nt][st] = ld8(dvb + ((int64_t)bh * T + ir) * D + 16 * st + 8 * g);
     }
-    float rJ[16];
-    load_rows16(rv + J0, g, rJ);
-    const bool diag = (J == I);
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      float p = __builtin_amdgcn_exp2f(s[e] * aI * rJ[e] - c0);
-      if (diag && (J0 + drow(e, g) > irow)) p = 0.f;
-      gg[e] = gg[e] * p * rJ[e];
-    }
-    const bf16x8 m0 = pack_b(gg, 0), m1 = pack_b(gg, 1);
-#pragma unroll
-    for (int t = 0; t < NDT; ++t) {
-      const bf16* kp = kth + (int64_t)(t * 32 + l32) * T + J0 + 8 * g;
-      acc[t] = mfma32(ld8(kp), m0, acc[t]);
-      acc[t] = mfma32(ld8(kp + 16), m1, acc[t]);
-    }
+    aI[nt] = sl2 * rv[ir];
   }
+  f32x16 acc[NDT][2];
+#pragma unroll
+  for (int t = 0; t < NDT; ++t) {
+    acc[t][0] = zero16();
+    acc[t][1] = zero16();
+  }
+  const int ntile = 2 * p + 2;  // key tiles 0 .. 2p+1 (the last two are this workgroup's own blocks)
+  bf16x8 stg[3 * CH];
+  f32x4 rstg;
+  auto gload = [&](int J) {
+    const int j0 = J * 64;
+    g2r_rows<D>(kh, ks.t, j0, stg);
+    g2r_rows<D>(vh, D, j0, stg + CH);
+    g2r_tp<D>(kth, T, j0, stg + 2 * CH);
+    if (tid < 16) rstg = *reinterpret_cast<const f32x4*>(rv + j0 + 4 * tid);
+  };
+  auto lstore = [&](int buf) {
+    r2l_rows<D>(sm.u.st.k[buf], stg);
+    r2l_rows<D>(sm.u.st.v[buf], stg + CH);
+    r2l_tp<D>(sm.u.st.kt[buf], stg + 2 * CH);
+    if (tid < 16) *reinterpret_cast<f32x4*>(&sm.u.st.r[buf][4 * tid]) = rstg;
+  };
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  // this wave's rows start at 64-block index 2p + ih; key tiles after it are fully masked
+  const int last_w = 2 * p + ih;
+  for (int J = 0; J < ntile; ++J) {
+    const int buf = J & 1;
+    const bool more = J + 1 < ntile;
+    if (more) gload(J + 1);
+    if (J <= last_w) {
+      const bool diag = (J == last_w);
+      bf16x8 ka[NKS], va[NKS];
+#pragma unroll
+      for (int st = 0; st < NKS; ++st) {
+        ka[st] = ld8(&sm.u.st.k[buf][jh * 32 + l32][16 * st + 8 * g]);
+        va[st] = ld8(&sm.u.st.v[buf][jh * 32 + l32][16 * st + 8 * g]);
+      }
+      float rJ[16];
+      lds_rows16(&sm.u.st.r[buf][jh * 32], g, rJ);
+      bf16x8 mb[2][2];
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        f32x16 sc = zero16(), gg = zero16();
+#pragma unroll
+        for (int st = 0; st < NKS; ++st) {
+          sc = mfma32(ka[st], kbI[nt][st], sc);
+          gg = mfma32(va[st], dbI[nt][st], gg);
+        }
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          float pe = __builtin_amdgcn_exp2f(fmaf(sc[e] * aI[nt], rJ[e], -c0));
+          if (diag && (jh * 32 + drow(e, g) > nt * 32 + l32)) pe = 0.f;
+          gg[e] = gg[e] * pe * rJ[e];
+        }
+        mb[nt][0] = pack_b(gg, 0);
+        mb[nt][1] = pack_b(gg, 1);
+      }
+#pragma unroll
+      for (int t = 0; t < NDT; ++t) {
+        const bf16x8 k0 = ld8(&sm.u.st.kt[buf][t * 32 + l32][jh * 32 + 8 * g]);
+        const bf16x8 k1 = ld8(&sm.u.st.kt[buf][t * 32 + l32][jh * 32 + 16 + 8 * g]);
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+          acc[t][nt] = mfma32(k0, mb[nt][0], acc[t][nt]);
+          acc[t][nt] = mfma32(k1, mb[nt][1], acc[t][nt]);
+        }
+      }
+    }
+    if (more) lstore(buf ^ 1);
+    __syncthreads();
+  }
+  float(*Rt)[132] = sm.u.Rt;
   if (jh == 1) {
 #pragma unroll
     for (int t = 0; t < NDT; ++t)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][ih * 32 + l32] = acc[t][e];
+      for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][ih * 64 + nt * 32 + l32] = acc[t][nt][e];
   }
   __syncthreads();
   if (jh == 0) {
-    const float* cs = colsum + ((int64_t)bh * T + irow) * D;
-    const float* da = dka + ((int64_t)bh * T + irow) * D;
-    const bf16* kr = kh + (int64_t)irow * ks.t;
-    float dkh[NDT][16], khat[NDT][16];
-    float dotp = 0.f;
 #pragma unroll
-    for (int t = 0; t < NDT; ++t)
+    for (int nt = 0; nt < 2; ++nt) {
+      const int col = ih * 64 + nt * 32 + l32;
+      const int irow = I0 + col;
+      const float ri = rv[irow];
+      const float* cs = colsum + ((int64_t)bh * T + irow) * D;
+      const float* da = dka + ((int64_t)bh * T + irow) * D;
+      const bf16* kr = kh + (int64_t)irow * ks.t;
+      float dkh[NDT][16], khat[NDT][16];
+      float dotp = 0.f;
 #pragma unroll
-      for (int qq = 0; qq < 4; ++qq) {
-        const int d0 = t * 32 + 8 * qq + 4 * g;
-        const f32x4 cv = *reinterpret_cast<const f32x4*>(cs + d0);
-        const bf16x4 kv = *reinterpret_cast<const bf16x4*>(kr + d0);
+      for (int t = 0; t < NDT; ++t)
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int e = 4 * qq + u;
-          const float x = -scale * (acc[t][e] + Rt[d0 + u][ih * 32 + l32] + cv[u]);
-          const float kk = ri * (float)kv[u];
-          dkh[t][e] = x;
-          khat[t][e] = kk;
-          dotp += x * kk;
+        for (int qq = 0; qq < 4; ++qq) {
+          const int d0 = t * 32 + 8 * qq + 4 * g;
+          const f32x4 cv = *reinterpret_cast<const f32x4*>(cs + d0);
+          const bf16x4 kv = *reinterpret_cast<const bf16x4*>(kr + d0);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int e = 4 * qq + u;
+            const float x = -scale * (acc[t][nt][e] + Rt[d0 + u][col] + cv[u]);
+            const float kk = ri * (float)kv[u];
+            dkh[t][e] = x;
+            khat[t][e] = kk;
+            dotp += x * kk;
+          }
         }
-      }
-    dotp += wave_xor32(dotp);
-    const float f = dotp / (float)D;
-    bf16* op = dk_out + b * dks.b + h * dks.h + (int64_t)irow * dks.t;
+      dotp += wave_xor32(dotp);
+      const float f = dotp / (float)D;
+      bf16* op = dk_out + b * dks.b + h * dks.h + (int64_t)irow * dks.t;
 #pragma unroll
-    for (int t = 0; t < NDT; ++t)
+      for (int t = 0; t < NDT; ++t)
 #pragma unroll
-      for (int qq = 0; qq < 4; ++qq) {
-        const int d0 = t * 32 + 8 * qq + 4 * g;
-        const f32x4 av = *reinterpret_cast<const f32x4*>(da + d0);
-        bf16x4 bb;
+        for (int qq = 0; qq < 4; ++qq) {
+          const int d0 = t * 32 + 8 * qq + 4 * g;
+          const f32x4 av = *reinterpret_cast<const f32x4*>(da + d0);
+          bf16x4 bb;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int e = 4 * qq + u;
-          bb[u] = (bf16)(ri * (dkh[t][e] - khat[t][e] * f) + av[u]);
+          for (int u = 0; u < 4; ++u) {
+            const int e = 4 * qq + u;
+            bb[u] = (bf16)(ri * (dkh[t][e] - khat[t][e] * f) + av[u]);
+          }
+          *reinterpret_cast<bf16x4*>(op + d0) = bb;
         }
-        *reinterpret_cast<bf16x4*>(op + d0) = bb;
-      }
+    }
   }
 }
 

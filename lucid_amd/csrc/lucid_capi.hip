@@ -194,10 +194,10 @@ int launch_bwd(const void* dout, const int64_t* dos, const void* q, const int64_
   LUCID_LAUNCH("lucid_attn_bwd_dq_kernel", lucid::lucid_attn_bwd_dq_kernel<D>, dim3(((T + 255) / 256) * BHq), st,
                (const bf16*)q, S(qs), (const bf16*)k, S(ks), f.vpb, (const bf16*)dout, S(dos), f.kt, lse, w.delta,
                (bf16*)dq, S(dqs), Hq, Hkv, T, BHq, scale);
-  LUCID_LAUNCH("lucid_precond_bwd_col_kernel", lucid::lucid_precond_bwd_col_kernel<D>, dim3((T / 64) * BH), st,
+  LUCID_LAUNCH("lucid_precond_bwd_col_kernel", lucid::lucid_precond_bwd_col_kernel<D>, dim3((T / 128) * BH), st,
                (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, scale, f.kt, f.vpb, f.pinv, w.dvp, w.dvb, w.dvt,
                (bf16*)dv, S(dvs), w.colsum, w.counters);
-  LUCID_LAUNCH("lucid_precond_bwd_row_kernel", lucid::lucid_precond_bwd_row_kernel<D>, dim3((T / 64) * BH), st,
+  LUCID_LAUNCH("lucid_precond_bwd_row_kernel", lucid::lucid_precond_bwd_row_kernel<D>, dim3((T / 128) * BH), st,
                (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, scale, f.kt, f.vpb, w.dvb, w.colsum, w.dka, (bf16*)dk,
                S(dks));
   return LUCID_OK;
