@@ -1,0 +1,48 @@
+/*
+ * lucid_path -- C ABI of the MI355X (gfx950) LUCID-Path kernels.
+ *
+ * LUCID-Path (lucid_path/triton_code/parallel.py:180-241):
+ *   O = (I + L)^-1 V,  L_ij = exp(s A_ij - 1/s) for j < i,
+ *   A_ij = q_i^T H_i ... H_{j+1} k_j,  H_t = I - beta_t w_t w_t^T.
+ * Layouts as the reference: q [B,T,HQ,K], k/w [B,T,H,K], v [B,T,H,V], beta [B,T,H],
+ * o [B,T,HQ,V]; element strides {batch, head, time}, last axis contiguous.
+ * bf16 tensors; K = V = 64; T a multiple of 64 (the Python layer zero-pads the
+ * sequence end, exact for every real row since L is strictly lower triangular).
+ * Buffers are caller-owned (the library never allocates); launches go on `stream`.
+ * Return codes as in lucid_amd.h (0 ok, 1 bad argument, 1000 + hipError_t).
+ */
+#ifndef LUCID_PATH_H
+#define LUCID_PATH_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ABI version of this header. */
+int lucid_path_abi_version(void);
+
+/* Text of the last error on the calling thread. */
+const char* lucid_path_last_error(void);
+
+/* Bytes of the forward workspace (kept alive for lucid_path_bwd). */
+size_t lucid_path_fwd_workspace_bytes(int B, int T, int H, int HQ, int K);
+
+/* Forward: o = (I + L)^-1 v; if kcache is non-null also the decode key cache
+ * [B,T,H,K] (keys carried through every later Householder).
+ * Replaces ParallelLUCIDPathAttentionFunction.forward (parallel.py:27-76): the
+ * kkt + solve_tril WY step (:39-51), triangular_solve_fwd_fn (:54-65) and
+ * prepare_k_cache_fn (:68). */
+int lucid_path_fwd(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                   const void* v, const int64_t* v_strides, const void* w, const int64_t* w_strides,
+                   const void* beta, const int64_t* beta_strides, void* o, const int64_t* o_strides,
+                   void* kcache, const int64_t* kcache_strides, void* fwd_ws, int B, int T, int H, int HQ,
+                   int K, float scale, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LUCID_PATH_H */

@@ -41,6 +41,13 @@ _SIGS = {
                                  ctypes.POINTER(ctypes.c_long)], _int),
         "lucid_profile_reset": ([], None),
     },
+    "liblucid_path.so": {
+        "lucid_path_abi_version": ([], _int),
+        "lucid_path_last_error": ([], ctypes.c_char_p),
+        "lucid_path_fwd_workspace_bytes": ([_int] * 5, _sz),
+        "lucid_path_fwd": ([_vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p,
+                            _vp, _i64p, _vp, _int, _int, _int, _int, _int, _flt, _vp], _int),
+    },
 }
 
 
@@ -82,7 +89,8 @@ def load(name: str = "liblucid_amd.so") -> ctypes.CDLL:
 def check(lib: ctypes.CDLL, rc: int, what: str) -> None:
     if rc == 0:
         return
-    msg = lib.lucid_last_error().decode(errors="replace") if hasattr(lib, "lucid_last_error") else ""
+    getter = getattr(lib, "lucid_last_error", None) or getattr(lib, "lucid_path_last_error", None)
+    msg = getter().decode(errors="replace") if getter else ""
     if rc == LUCID_EINVAL:
         raise ValueError(f"{what}: {msg}")
     raise RuntimeError(f"{what} failed (code {rc}): {msg}")

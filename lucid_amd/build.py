@@ -20,6 +20,7 @@ HIPCC_FLAGS = [
 
 TARGETS = {
     "liblucid_amd.so": ["lucid_capi.hip"],
+    "liblucid_path.so": ["path_capi.hip"],
 }
 
 

@@ -1,0 +1,132 @@
+// C ABI of the LUCID-Path kernels (declared in include/lucid_path.h).
+#include <string>
+
+#include "../../include/lucid_path.h"
+#include "path_fwd.hip"
+
+namespace {
+
+thread_local std::string g_path_error;
+
+int pfail(const std::string& msg) {
+  g_path_error = msg;
+  return 1;
+}
+
+int phip(const char* where) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    g_path_error = std::string(where) + ": " + hipGetErrorString(e);
+    return 1000 + (int)e;
+  }
+  return 0;
+}
+
+size_t a256(size_t x) { return (x + 255) & ~size_t(255); }
+
+lucid::PathFwdWs carve_path_fwd(void* base, int B, int T, int H, int HQ, size_t* bytes) {
+  const size_t BH = (size_t)B * H, BHq = (size_t)B * HQ;
+  const size_t NT = T / 64, NS = (NT + 7) / 8;
+  lucid::PathFwdWs w{};
+  size_t off = 0;
+  char* p = static_cast<char*>(base);
+  auto take = [&](size_t n) {
+    char* r = p ? p + off : nullptr;
+    off += a256(n);
+    return r;
+  };
+  w.w2 = reinterpret_cast<float*>(take(BH * T * 64 * 4));
+  w.hc = reinterpret_cast<float*>(take(BH * NT * 4096 * 4));
+  w.kt = reinterpret_cast<bf16*>(take(BH * T * 64 * 2));
+  w.ktT = reinterpret_cast<bf16*>(take(BH * T * 64 * 2));
+  w.suf = reinterpret_cast<float*>(take(BH * NT * 4096 * 4));
+  w.hl = reinterpret_cast<float*>(take(BH * NS * 4096 * 4));
+  w.kl = reinterpret_cast<bf16*>(take(BH * T * 64 * 2));
+  w.klT = reinterpret_cast<bf16*>(take(BH * T * 64 * 2));
+  w.qt = reinterpret_cast<float*>(take(BHq * T * 64 * 4));
+  w.ld = reinterpret_cast<float*>(take(BHq * NT * 4096 * 4));
+  w.y = reinterpret_cast<float*>(take(BHq * NT * 4096 * 4));
+  w.qs = reinterpret_cast<bf16*>(take(BHq * 8 * T * 64 * 2));
+  w.qsT = reinterpret_cast<bf16*>(take(BHq * 8 * T * 64 * 2));
+  w.qb = reinterpret_cast<bf16*>(take(BHq * NS * T * 64 * 2));
+  w.qbT = reinterpret_cast<bf16*>(take(BHq * NS * T * 64 * 2));
+  w.oT = reinterpret_cast<bf16*>(take(BHq * T * 64 * 2));
+  w.counters = reinterpret_cast<int*>(take(BHq * 4));
+  if (bytes) *bytes = off;
+  return w;
+}
+
+int pcheck(const char* name, const void* p, const int64_t* s) {
+  if (!p) return pfail(std::string(name) + " is null");
+  if (!s) return pfail(std::string(name) + " strides are null");
+  if (reinterpret_cast<uintptr_t>(p) % 16) return pfail(std::string(name) + " must be 16-byte aligned");
+  return 0;
+}
+
+int pcheck_vec(const char* name, const void* p, const int64_t* s) {
+  if (int rc = pcheck(name, p, s)) return rc;
+  for (int i = 0; i < 3; ++i)
+    if (s[i] % 8) return pfail(std::string(name) + " strides must be multiples of 8 elements");
+  return 0;
+}
+
+lucid::Strides PS(const int64_t* s) { return lucid::Strides{s[0], s[1], s[2]}; }
+
+}  // namespace
+
+extern "C" {
+
+int lucid_path_abi_version(void) { return 1; }
+
+const char* lucid_path_last_error(void) { return g_path_error.c_str(); }
+
+size_t lucid_path_fwd_workspace_bytes(int B, int T, int H, int HQ, int K) {
+  (void)K;
+  size_t n = 0;
+  carve_path_fwd(nullptr, B, T, H, HQ, &n);
+  return n;
+}
+
+int lucid_path_fwd(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                   const void* v, const int64_t* v_strides, const void* w, const int64_t* w_strides,
+                   const void* beta, const int64_t* beta_strides, void* o, const int64_t* o_strides,
+                   void* kcache, const int64_t* kcache_strides, void* fwd_ws, int B, int T, int H, int HQ,
+                   int K, float scale, void* stream) {
+  g_path_error.clear();
+  if (B <= 0 || T <= 0 || H <= 0 || HQ <= 0) return pfail("B, T, H and HQ must be positive");
+  if (K != 64) return pfail("head_dim must be 64, got " + std::to_string(K));
+  if (T % 64) return pfail("T must be a multiple of 64, got " + std::to_string(T));
+  if (HQ % H) return pfail("the number of query heads must be a multiple of the key heads");
+  if (int rc = pcheck_vec("q", q, q_strides)) return rc;
+  if (int rc = pcheck_vec("k", k, k_strides)) return rc;
+  if (int rc = pcheck_vec("v", v, v_strides)) return rc;
+  if (int rc = pcheck_vec("w", w, w_strides)) return rc;
+  if (int rc = pcheck("beta", beta, beta_strides)) return rc;
+  if (int rc = pcheck_vec("o", o, o_strides)) return rc;
+  if (kcache)
+    if (int rc = pcheck_vec("kcache", kcache, kcache_strides)) return rc;
+  if (!fwd_ws) return pfail("fwd_ws is null");
+  const lucid::PathFwdWs ws = carve_path_fwd(fwd_ws, B, T, H, HQ, nullptr);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int NT = T / 64, NS = (NT + 7) / 8;
+  const int BH = B * H, BHq = B * HQ;
+  hipLaunchKernelGGL(lucid::path_chunk_kernel, dim3(NT, BHq), dim3(256), 0, st, (const bf16*)q, PS(q_strides),
+                     (const bf16*)k, PS(k_strides), (const bf16*)w, PS(w_strides), (const bf16*)beta,
+                     PS(beta_strides), HQ, H, T, scale, ws);
+  if (int rc = phip("path_chunk_kernel")) return rc;
+  hipLaunchKernelGGL(lucid::path_large_kernel, dim3(NS, BH), dim3(256), 0, st, T, ws);
+  if (int rc = phip("path_large_kernel")) return rc;
+  hipLaunchKernelGGL(lucid::path_transport_kernel, dim3(NT, BHq), dim3(256), 0, st, HQ, H, T, ws);
+  if (int rc = phip("path_transport_kernel")) return rc;
+  hipLaunchKernelGGL(lucid::path_solve_fwd_kernel, dim3(NT * BHq), dim3(256), 0, st, (const bf16*)v,
+                     PS(v_strides), (bf16*)o, PS(o_strides), HQ, H, T, BHq, scale, ws);
+  if (int rc = phip("path_solve_fwd_kernel")) return rc;
+  if (kcache) {
+    hipLaunchKernelGGL(lucid::path_kcache_kernel, dim3(NT, BH), dim3(256), 0, st, T, (bf16*)kcache,
+                       PS(kcache_strides), H, ws);
+    if (int rc = phip("path_kcache_kernel")) return rc;
+  }
+  return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,507 @@
+// LUCID-Path forward on CDNA4 (gfx950): O = (I + L)^-1 V,
+//   L_ij = exp(s A_ij - 1/s) (j < i),  A_ij = q_i^T H_i ... H_{j+1} k_j,  H_t = I - beta_t w_t w_t^T
+// (lucid_path/triton_code/parallel.py:27-76, triangular_solve_fwd.py:19-225).
+//
+// Two-level chunking (small chunk 64, large chunk 512): every inter-chunk logit block
+// is ONE GEMM of a query carried down and a key carried up to a common boundary:
+//   A_IJ = QB_I^(sJ) KL_J^T   (J in an earlier large chunk)
+//   A_IJ = QS_I^(J)  k~_J^T   (J earlier in the same large chunk)
+// so the chained solve has no per-pair Householder propagation (the reference
+// propagates the query through every chunk pair, triangular_solve_fwd.py:170-196).
+//
+// Kernels (256 threads):
+//   path_chunk_kernel      per (chunk, query head): WY form T_inv, W2, Hc = I - W^T W2,
+//                          q~, k~, L_diag and Y = (I + L_diag)^-1   (fp32, LDS)
+//   path_large_kernel      per (large chunk, kv head): SUF_c, HL_s and KL = k~ SUF^T
+//   path_transport_kernel  per (chunk, query head): QS and QB (MFMA, 3-term bf16 split)
+//   path_solve_fwd_kernel  chained solve per query head (chain counters as in LUCID)
+//   path_kcache_kernel     k_cache = keys carried to the sequence end (use_cache)
+#include "path_common.h"
+
+namespace lucid {
+
+struct PathFwdWs {
+  float* w2;    // [BH][T][64]        W2 = T_inv (beta W)
+  float* hc;    // [BH][NT][64][64]   Hc = I - W^T W2
+  bf16* kt;     // [BH][T][64]        k~ rows
+  bf16* ktT;    // [BH][64][T]        k~^T, T-perm
+  float* suf;   // [BH][NT][64][64]   SUF_c
+  float* hl;    // [BH][NS][64][64]   HL_s
+  bf16* kl;     // [BH][T][64]        KL rows
+  bf16* klT;    // [BH][64][T]        KL^T, T-perm
+  float* qt;    // [BHq][T][64]       q~
+  float* ld;    // [BHq][NT][64][64]  L_diag (strictly lower)
+  float* y;     // [BHq][NT][64][64]  (I + L_diag)^-1
+  bf16* qs;     // [BHq][8][T][64]    QS rows, slot = c - (first chunk of I's large chunk)
+  bf16* qsT;    // [BHq][8][64][T]    QS^T, T-perm
+  bf16* qb;     // [BHq][NS][T][64]   QB rows
+  bf16* qbT;    // [BHq][NS][64][T]   QB^T, T-perm
+  bf16* oT;     // [BHq][64][T]       O^T, T-perm (chain operand)
+  int* counters;  // [BHq]
+};
+
+// ---------------------------------------------------------------------------
+// WY form and in-chunk transforms (triangular_solve_fwd.py:118-148, parallel.py:39-51)
+// grid (NT, B*HQ).  kv-head outputs are written by the first query head of each group.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void path_chunk_kernel(const bf16* __restrict__ q, Strides qs,
+                                                         const bf16* __restrict__ k, Strides ks,
+                                                         const bf16* __restrict__ w, Strides wst,
+                                                         const bf16* __restrict__ beta, Strides bst, int HQ, int H,
+                                                         int T, float scale, PathFwdWs ws) {
+  __shared__ __attribute__((aligned(16))) float Wm[64][68];
+  __shared__ __attribute__((aligned(16))) float Wb[64][68];
+  __shared__ __attribute__((aligned(16))) float Tm[64][68];
+  __shared__ __attribute__((aligned(16))) float W2s[64][68];
+  __shared__ __attribute__((aligned(16))) float Qs[64][68];
+  __shared__ __attribute__((aligned(16))) float Ks[64][68];
+  __shared__ __attribute__((aligned(16))) float X[64][68];
+  const int c = blockIdx.x, bhq = blockIdx.y;
+  const int NT = T / PC;
+  const int G = HQ / H;
+  const int b = bhq / HQ, hq = bhq - b * HQ, h = hq / G;
+  const int bh = b * H + h;
+  const bool kvw = (hq % G) == 0;
+  const int tid = threadIdx.x, w_ = tid >> 6, lane = tid & 63;
+  const int r0 = (tid >> 4) * 4, c0 = (tid & 15) * 4;
+  const int t0 = c * PC;
+  if (c == 0 && tid == 0) ws.counters[bhq] = 0;
+
+  load_rows64_f32(Wm, w + b * wst.b + h * wst.h + (int64_t)t0 * wst.t, wst.t);
+  load_rows64_f32(Qs, q + b * qs.b + hq * qs.h + (int64_t)t0 * qs.t, qs.t);
+  load_rows64_f32(Ks, k + b * ks.b + h * ks.h + (int64_t)t0 * ks.t, ks.t);
+  __syncthreads();
+  {
+    const int r = tid >> 2, cc = (tid & 3) * 16;
+    const float bt = (float)beta[b * bst.b + h * bst.h + (int64_t)(t0 + r) * bst.t];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) Wb[r][cc + e] = bt * Wm[r][cc + e];
+  }
+  __syncthreads();
+  float acc[4][4];
+  // a = stril(beta W W^T) -> Tm, then T_inv = (I + a)^-1 in place
+  zero44(acc);
+  lds_gemm64<false, true>(Wb, Wm, acc);
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) Tm[r0 + i][c0 + j] = (c0 + j < r0 + i) ? acc[i][j] : 0.f;
+  __syncthreads();
+  if (w_ == 0) invert_unit_lower64(Tm, lane);
+  __syncthreads();
+  // W2 = T_inv (beta W)
+  zero44(acc);
+  lds_gemm64<false, false>(Tm, Wb, acc);
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) W2s[r0 + i][c0 + j] = acc[i][j];
+  if (kvw) {
+    float* dst = ws.w2 + ((int64_t)bh * T + t0) * 64;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f32x4 v;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] = acc[i][j];
+      *reinterpret_cast<f32x4*>(dst + (r0 + i) * 64 + c0) = v;
+    }
+  }
+  __syncthreads();
+  // Hc = I - W^T W2
+  if (kvw) {
+    zero44(acc);
+    lds_gemm64<true, false>(Wm, W2s, acc);
+    float* dst = ws.hc + ((int64_t)bh * NT + c) * 4096;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f32x4 v;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] = ((r0 + i) == (c0 + j) ? 1.f : 0.f) - acc[i][j];
+      *reinterpret_cast<f32x4*>(dst + (r0 + i) * 64 + c0) = v;
+    }
+  }
+  // WBK = stril(beta W K^T) -> X
+  zero44(acc);
+  lds_gemm64<false, true>(Wb, Ks, acc);
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) X[r0 + i][c0 + j] = (c0 + j < r0 + i) ? acc[i][j] : 0.f;
+  __syncthreads();
+  // TW = T_inv WBK -> Wb (beta W is no longer needed)
+  zero44(acc);
+  lds_gemm64<false, false>(Tm, X, acc);
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) Wb[r0 + i][c0 + j] = acc[i][j];
+  __syncthreads();
+  // k~ = K - TW^T W
+  if (kvw) {
+    zero44(acc);
+    lds_gemm64<true, false>(Wb, Wm, acc);
+    bf16* dst = ws.kt + ((int64_t)bh * T + t0) * 64;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      bf16x4 v;
+      const int t = t0 + r0 + i;
+      const int slot = (t & ~15) | jmap(t & 15);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[j] = (bf16)(Ks[r0 + i][c0 + j] - acc[i][j]);
+        ws.ktT[((int64_t)bh * 64 + c0 + j) * T + slot] = v[j];
+      }
+      *reinterpret_cast<bf16x4*>(dst + (r0 + i) * 64 + c0) = v;
+    }
+  }
+  // QW = tril(Q W^T) -> X
+  zero44(acc);
+  lds_gemm64<false, true>(Qs, Wm, acc);
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) X[r0 + i][c0 + j] = (c0 + j <= r0 + i) ? acc[i][j] : 0.f;
+  __syncthreads();
+  // q~ = Q - QW W2
+  zero44(acc);
+  lds_gemm64<false, false>(X, W2s, acc);
+  {
+    float* dst = ws.qt + ((int64_t)bhq * T + t0) * 64;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f32x4 v;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] = Qs[r0 + i][c0 + j] - acc[i][j];
+      *reinterpret_cast<f32x4*>(dst + (r0 + i) * 64 + c0) = v;
+    }
+  }
+  // A_diag = tril(Q K^T - QW TW); L_diag = stril(exp(s A - 1/s)) -> W2s, global
+  float acc2[4][4];
+  zero44(acc);
+  zero44(acc2);
+  lds_gemm64<false, true>(Qs, Ks, acc);
+  lds_gemm64<false, false>(X, Wb, acc2);
+  __syncthreads();
+  {
+    const float sl2 = scale * LOG2E_F, cc0 = LOG2E_F / scale;
+    float* dst = ws.ld + ((int64_t)bhq * NT + c) * 4096;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f32x4 v;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float a = acc[i][j] - acc2[i][j];
+        v[j] = (c0 + j < r0 + i) ? __builtin_amdgcn_exp2f(fmaf(a, sl2, -cc0)) : 0.f;
+        W2s[r0 + i][c0 + j] = v[j];
+      }
+      *reinterpret_cast<f32x4*>(dst + (r0 + i) * 64 + c0) = v;
+    }
+  }
+  __syncthreads();
+  if (w_ == 0) invert_unit_lower64(W2s, lane);
+  __syncthreads();
+  {
+    float* dst = ws.y + ((int64_t)bhq * NT + c) * 4096;
+    for (int idx = tid; idx < 4096; idx += 256) dst[idx] = W2s[idx >> 6][idx & 63];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Per large chunk: SUF_c (c from the top down), HL_s, KL = k~ SUF^T
+// (cumprod_householder_fwd.py:13-79).  grid (NS, B*H)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void path_large_kernel(int T, PathFwdWs ws) {
+  __shared__ __attribute__((aligned(16))) float Sf[64][68];
+  __shared__ __attribute__((aligned(16))) float Hs[64][68];
+  __shared__ __attribute__((aligned(16))) float Kt[64][68];
+  const int s = blockIdx.x, bh = blockIdx.y;
+  const int NT = T / PC;
+  const int tid = threadIdx.x;
+  const int r0 = (tid >> 4) * 4, c0 = (tid & 15) * 4;
+  const int cb = s * PR, ce = min(cb + PR, NT) - 1;
+  for (int idx = tid; idx < 4096; idx += 256) Sf[idx >> 6][idx & 63] = ((idx >> 6) == (idx & 63)) ? 1.f : 0.f;
+  float acc[4][4];
+  for (int c = ce; c >= cb; --c) {
+    load_rows64_f32(Kt, ws.kt + ((int64_t)bh * T + c * PC) * 64, 64);
+    load_mat64<false>(Hs, ws.hc + ((int64_t)bh * NT + c) * 4096);
+    __syncthreads();
+    {
+      float* dst = ws.suf + ((int64_t)bh * NT + c) * 4096;
+      for (int idx = tid; idx < 4096; idx += 256) dst[idx] = Sf[idx >> 6][idx & 63];
+    }
+    // KL_c = k~_c SUF_c^T
+    zero44(acc);
+    lds_gemm64<false, true>(Kt, Sf, acc);
+    {
+      bf16* dst = ws.kl + ((int64_t)bh * T + c * PC) * 64;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        bf16x4 v;
+        const int t = c * PC + r0 + i;
+        const int slot = (t & ~15) | jmap(t & 15);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          v[j] = (bf16)acc[i][j];
+          ws.klT[((int64_t)bh * 64 + c0 + j) * T + slot] = v[j];
+        }
+        *reinterpret_cast<bf16x4*>(dst + (r0 + i) * 64 + c0) = v;
+      }
+    }
+    // SUF_{c-1} = SUF_c Hc_c
+    zero44(acc);
+    lds_gemm64<false, false>(Sf, Hs, acc);
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) Sf[r0 + i][c0 + j] = acc[i][j];
+    __syncthreads();
+  }
+  float* dst = ws.hl + ((int64_t)bh * ((NT + PR - 1) / PR) + s) * 4096;
+  for (int idx = tid; idx < 4096; idx += 256) dst[idx] = Sf[idx >> 6][idx & 63];
+}
+
+// ---------------------------------------------------------------------------
+// Query transport (transform_q.py:15-61): x = q~_I; QS slots for chunks of I's large
+// chunk below I, then QB for every earlier large chunk.  grid (NT, B*HQ)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void path_transport_kernel(int HQ, int H, int T, PathFwdWs ws) {
+  __shared__ __attribute__((aligned(16))) float X[64][68];
+  __shared__ __attribute__((aligned(16))) float MT[64][68];
+  const int I = blockIdx.x, bhq = blockIdx.y;
+  const int NT = T / PC, NS = (NT + PR - 1) / PR;
+  const int G = HQ / H;
+  const int b = bhq / HQ, hq = bhq - b * HQ, bh = b * H + hq / G;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 5, l32 = lane & 31;
+  const int sI = I / PR, cb = sI * PR;
+  {
+    const float* src = ws.qt + ((int64_t)bhq * T + I * PC) * 64;
+    for (int idx = tid; idx < 4096; idx += 256) X[idx >> 6][idx & 63] = src[idx];
+  }
+  __syncthreads();
+  // rows of X -> bf16 rows at dst (row stride 64) and T-perm rows at dstT (row stride T)
+  auto emit = [&](bf16* dst, bf16* dstT) {
+    const int r = tid >> 2, cc = (tid & 3) * 16;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      bf16x8 v;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = (bf16)X[r][cc + 8 * hh + e];
+      *reinterpret_cast<bf16x8*>(dst + (int64_t)r * 64 + cc + 8 * hh) = v;
+    }
+    const int d = tid >> 2, sc = (tid & 3) * 16;  // T-perm row d, slots sc .. sc+15
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      bf16x8 v;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = (bf16)X[sc + jmap(8 * hh + e)][d];
+      *reinterpret_cast<bf16x8*>(dstT + (int64_t)d * T + I * PC + sc + 8 * hh) = v;
+    }
+  };
+  auto step = [&](const float* M) {
+    load_mat64<true>(MT, M);
+    __syncthreads();
+    const int dt = w >> 1, rt = w & 1;
+    const f32x16 o = mat_xM_tile(X, MT, dt, rt);
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < 16; ++e) X[rt * 32 + l32][dt * 32 + drow(e, g)] = o[e];
+    __syncthreads();
+  };
+  for (int c = I - 1; c >= cb; --c) {
+    const int slot = c - cb;
+    emit(ws.qs + (((int64_t)bhq * PR + slot) * T + I * PC) * 64, ws.qsT + ((int64_t)bhq * PR + slot) * 64 * T);
+    step(ws.hc + ((int64_t)bh * NT + c) * 4096);
+  }
+  for (int s = sI - 1; s >= 0; --s) {
+    emit(ws.qb + (((int64_t)bhq * NS + s) * T + I * PC) * 64, ws.qbT + ((int64_t)bhq * NS + s) * 64 * T);
+    step(ws.hl + ((int64_t)bh * NS + s) * 4096);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Chained solve (triangular_solve_fwd.py:99-225) per query head; one workgroup per
+// 64-row chunk I; ids grow with I.  wave w: ih = w & 1 -> rows 32*ih (lane <-> row),
+// jh = w >> 1 -> keys 32*jh of every staged 64-key tile.
+//   S^T[j][i] = Kop_J . Qop_I, P = exp(s S - 1/s), acc^T[d][i] += O^T[d][j] P^T[j][i]
+//   O_I = Y_I (V_I - acc)   (3-term bf16 split)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void path_solve_fwd_kernel(const bf16* __restrict__ v, Strides vs,
+                                                             bf16* __restrict__ o, Strides os, int HQ, int H,
+                                                             int T, int BHq, float scale, PathFwdWs ws) {
+  __shared__ __attribute__((aligned(16))) float Ys[64][68];
+  __shared__ __attribute__((aligned(16))) float Rt[64][68];
+  __shared__ __attribute__((aligned(16))) bf16 lk[2][64][72];
+  __shared__ __attribute__((aligned(16))) bf16 lo[2][64][72];
+  const int NT = T / PC, NS = (NT + PR - 1) / PR;
+  const int id = blockIdx.x;
+  const int I = id / BHq, bhq = id - (id / BHq) * BHq;
+  const int G = HQ / H;
+  const int b = bhq / HQ, hq = bhq - b * HQ, h = hq / G, bh = b * H + h;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
+  const int ih = w & 1, jh = w >> 1;
+  const int sI = I / PR, cb = sI * PR;
+  const int i0 = I * PC;
+  int* cnt = ws.counters + bhq;
+  const float sl2 = scale * LOG2E_F, cc0 = LOG2E_F / scale;
+  const bf16* oTh = ws.oT + (int64_t)bhq * 64 * T;
+
+  load_mat64<false>(Ys, ws.y + ((int64_t)bhq * NT + I) * 4096);
+
+  f32x16 acc[2] = {zero16(), zero16()};
+  bf16x8 qb[4];
+  int qsrc = -1;  // current Qop source: s (QB) or PR*NS + slot (QS)
+  auto load_q = [&](int J) {
+    const int src = (J < cb) ? (J / PR) : (PR * NS + (J - cb));
+    if (src == qsrc) return;
+    qsrc = src;
+    const bf16* base = (J < cb) ? ws.qb + ((int64_t)bhq * NS + J / PR) * T * 64
+                                : ws.qs + ((int64_t)bhq * PR + (J - cb)) * T * 64;
+#pragma unroll
+    for (int st = 0; st < 4; ++st) qb[st] = ld8(base + (int64_t)(i0 + ih * 32 + l32) * 64 + 16 * st + 8 * g);
+  };
+  bf16x8 stg[4];
+  auto gload = [&](int J) {
+    const bf16* ksrc = ((J < cb) ? ws.kl : ws.kt) + (int64_t)bh * T * 64;
+    g2r_rows<64>(ksrc, 64, J * PC, stg);
+    g2r_tp<64>(oTh, T, J * PC, stg + 2);
+  };
+  auto lstore = [&](int buf) {
+    r2l_rows<64>(lk[buf], stg);
+    r2l_tp<64>(lo[buf], stg + 2);
+  };
+  int ready = 0;
+  if (I > 0) {
+    ready = wait_counter_gt(cnt, 0);
+    gload(0);
+    lstore(0);
+  }
+  __syncthreads();
+  for (int J = 0; J < I; ++J) {
+    const int buf = J & 1;
+    const bool more = J + 1 < I;
+    bool early = false;
+    if (more) {
+      if (J + 1 >= ready) {
+        const int seen = poll_counter(cnt);
+        if (seen > J + 1) {
+          acquire_agent();
+          ready = seen;
+        }
+      }
+      early = J + 1 < ready;
+      if (early) gload(J + 1);
+    }
+    load_q(J);
+    {
+      f32x16 sc = zero16();
+#pragma unroll
+      for (int st = 0; st < 4; ++st) sc = mfma32(ld8(&lk[buf][jh * 32 + l32][16 * st + 8 * g]), qb[st], sc);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sc[e] = __builtin_amdgcn_exp2f(fmaf(sc[e], sl2, -cc0));
+      const bf16x8 p0 = pack_b(sc, 0), p1 = pack_b(sc, 1);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        acc[t] = mfma32(ld8(&lo[buf][t * 32 + l32][jh * 32 + 8 * g]), p0, acc[t]);
+        acc[t] = mfma32(ld8(&lo[buf][t * 32 + l32][jh * 32 + 16 + 8 * g]), p1, acc[t]);
+      }
+    }
+    if (more) {
+      if (!early) {
+        ready = wait_counter_gt(cnt, J + 1);
+        gload(J + 1);
+      }
+      lstore(buf ^ 1);
+    }
+    __syncthreads();
+  }
+  // ---- R = V - acc (reduce key halves) ----
+  if (jh == 1) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][ih * 32 + l32] = acc[t][e];
+  }
+  __syncthreads();
+  if (jh == 0) {
+    const bf16* vrow = v + b * vs.b + h * vs.h + (int64_t)(i0 + ih * 32 + l32) * vs.t;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) {
+        const int d0 = t * 32 + 8 * qq + 4 * g;
+        const bf16x4 vv = *reinterpret_cast<const bf16x4*>(vrow + d0);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          Rt[d0 + u][ih * 32 + l32] = (float)vv[u] - (acc[t][4 * qq + u] + Rt[d0 + u][ih * 32 + l32]);
+      }
+  }
+  __syncthreads();
+  // ---- O^T[d][r] = sum_c R^T[d][c] Y[r][c] ----
+  {
+    const int dt = w >> 1, rh = w & 1;
+    f32x16 oo = zero16();
+    for (int st = 0; st < (rh ? 4 : 2); ++st) {
+      bf16x8 ah, al, bh8, bl;
+      split8(&Rt[dt * 32 + l32][16 * st + 8 * g], ah, al);
+      split8(&Ys[rh * 32 + l32][16 * st + 8 * g], bh8, bl);
+      oo = mfma32(ah, bh8, oo);
+      oo = mfma32(ah, bl, oo);
+      oo = mfma32(al, bh8, oo);
+    }
+    const int r = i0 + rh * 32 + l32;
+    const int slot = (r & ~15) | jmap(r & 15);
+    bf16* orow = o + b * os.b + hq * os.h + (int64_t)r * os.t;
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) {
+      const int d0 = dt * 32 + 8 * qq + 4 * g;
+      bf16x4 bb;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        bb[u] = (bf16)oo[4 * qq + u];
+        ws.oT[((int64_t)bhq * 64 + d0 + u) * T + slot] = bb[u];
+      }
+      *reinterpret_cast<bf16x4*>(orow + d0) = bb;
+    }
+  }
+  publish_counter(cnt, I + 1);
+}
+
+// ---------------------------------------------------------------------------
+// k_cache_j = keys carried to the sequence end (prepare_k_cache.py:12-74):
+// x = KL_J; x <- x HL_s^T for every later large chunk.  grid (NT, B*H)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void path_kcache_kernel(int T, bf16* __restrict__ kc, Strides kcs, int H,
+                                                          PathFwdWs ws) {
+  __shared__ __attribute__((aligned(16))) float X[64][68];
+  __shared__ __attribute__((aligned(16))) float MT[64][68];
+  const int J = blockIdx.x, bh = blockIdx.y;
+  const int b = bh / H, h = bh - b * H;
+  const int NT = T / PC, NS = (NT + PR - 1) / PR;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 5, l32 = lane & 31;
+  load_rows64_f32(X, ws.kl + ((int64_t)bh * T + J * PC) * 64, 64);
+  __syncthreads();
+  for (int s = J / PR + 1; s < NS; ++s) {
+    load_mat64<false>(MT, ws.hl + ((int64_t)bh * NS + s) * 4096);  // (HL^T)^T = HL
+    __syncthreads();
+    const int dt = w >> 1, rt = w & 1;
+    const f32x16 oo = mat_xM_tile(X, MT, dt, rt);
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < 16; ++e) X[rt * 32 + l32][dt * 32 + drow(e, g)] = oo[e];
+    __syncthreads();
+  }
+  const int r = tid >> 2, cc = (tid & 3) * 16;
+  bf16* dst = kc + b * kcs.b + h * kcs.h + (int64_t)(J * PC + r) * kcs.t + cc;
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+    bf16x8 vv;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) vv[e] = (bf16)X[r][cc + 8 * hh + e];
+    *reinterpret_cast<bf16x8*>(dst + 8 * hh) = vv;
+  }
+}
+
+}  // namespace lucid

@@ -1,0 +1,127 @@
+"""LUCID-Path attention on the HIP kernels (MI355X / gfx950).
+
+Python mirror of ``fla.ops.lucid_path`` (reference ``lucid_path/triton_code/parallel.py``):
+:func:`parallel_lucid_path_attention` keeps the reference signature, defaults and
+asserts (parallel.py:180-241) and returns ``(o, k_cache)``.
+
+    O = (I + L)^-1 V,  L_ij = exp(s A_ij - 1/s) (j < i),  A_ij = q_i^T H_i ... H_{j+1} k_j,
+    H_t = I - beta_t w_t w_t^T
+
+Tensors are bf16 GPU tensors in the reference layout ``[B, T, H, K]``; K = V = 64.
+There is no CPU or Triton fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional
+
+import torch
+import torch.nn.functional as F
+
+from . import _lib
+
+_LIB = "liblucid_path.so"
+
+
+def _pad_t(x: torch.Tensor, tp: int) -> torch.Tensor:
+    t = x.shape[1]
+    if t == tp:
+        return x
+    pad = [0, 0] * (x.dim() - 2) + [0, tp - t]
+    return F.pad(x, pad)
+
+
+def _ready(x: torch.Tensor) -> torch.Tensor:
+    if x.stride(-1) != 1 or x.data_ptr() % 16 or any(s % 8 for s in x.stride()[:-1]):
+        x = x.contiguous()
+    return x
+
+
+def _fwd(q, k, v, w, beta, scale, use_cache):
+    lib = _lib.load(_LIB)
+    B, T, HQ, K = q.shape
+    H = k.shape[2]
+    dev = q.device
+    o = torch.empty(B, T, HQ, v.shape[-1], dtype=torch.bfloat16, device=dev)
+    kc = torch.empty(B, T, H, K, dtype=torch.bfloat16, device=dev) if use_cache else None
+    ws = torch.empty(lib.lucid_path_fwd_workspace_bytes(B, T, H, HQ, K), dtype=torch.uint8, device=dev)
+    beta = beta.contiguous()
+    st3 = lambda t: _lib.strides3(t, (0, 2, 1))  # noqa: E731  (batch, head, time)
+    beta_strides = (ctypes.c_int64 * 3)(beta.stride(0), beta.stride(2), beta.stride(1))
+    rc = lib.lucid_path_fwd(
+        _lib.ptr(q), st3(q), _lib.ptr(k), st3(k), _lib.ptr(v), st3(v), _lib.ptr(w), st3(w),
+        _lib.ptr(beta), beta_strides, _lib.ptr(o), st3(o),
+        _lib.ptr(kc) if kc is not None else None, st3(kc) if kc is not None else None,
+        _lib.ptr(ws), B, T, H, HQ, K, float(scale), _lib.stream_handle(dev))
+    _lib.check(lib, rc, "lucid_path_fwd")
+    return o, kc, ws
+
+
+class ParallelLUCIDPathAttentionFunction(torch.autograd.Function):
+    """Forward/backward of LUCID-Path (ParallelLUCIDPathAttentionFunction, parallel.py:27-177)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, w, beta, g, scale, cu_seqlens, use_cache=False):
+        t = q.shape[1]
+        tp = (t + 63) // 64 * 64
+        q, k, v, w, beta = (_ready(_pad_t(x, tp)) for x in (q, k, v, w, beta))
+        o, kc, ws = _fwd(q, k, v, w, beta, scale, use_cache)
+        ctx.save_for_backward(q, k, v, w, beta, o, ws)
+        ctx.scale, ctx.t = scale, t
+        if kc is not None:
+            kc = kc[:, :t]
+            ctx.mark_non_differentiable(kc)
+        return o[:, :t], kc
+
+    @staticmethod
+    def backward(ctx, do, dk_cache):
+        raise NotImplementedError("LUCID-Path backward kernels are not built yet")
+
+
+@torch.compiler.disable
+def parallel_lucid_path_attention(
+    k: torch.Tensor,
+    v: torch.Tensor,
+    w: torch.Tensor,
+    beta: torch.Tensor,
+    q: Optional[torch.Tensor] = None,
+    g: Optional[torch.Tensor] = None,
+    scale: float = None,
+    cu_seqlens: Optional[torch.Tensor] = None,
+    use_cache: bool = False,
+):
+    """LUCID Path attention: solves (I + L) O = V with L = stril(exp(A * scale - 1/scale)).
+
+    Same arguments, defaults and asserts as the reference (parallel.py:180-241);
+    returns ``(o [B,T,HQ,V], k_cache [B,T,H,K] or None)``.
+    """
+    if q is None:
+        q = k
+    if scale is None:
+        scale = k.shape[-1] ** -0.5
+    assert q.shape[-1] in [16, 32, 64, 128], "only support head_dim in [16, 32, 64, 128] for now. Stay tuned!"
+    assert v.shape[-1] in [16, 32, 64, 128], "only support head_dim in [16, 32, 64, 128] for now. Stay tuned!"
+    assert q.shape[-1] == k.shape[-1], 'q, k should have the same head_dim.'
+    assert k.shape == w.shape, 'k, w should have the same shape.'
+    assert beta.shape[:3] == k.shape[:3], 'beta should have the same number of heads as k'
+    assert g is None, 'g is not supported'
+    assert q.shape[-2] % k.shape[-2] == 0, 'the number of query heads should be divisible by the number of key heads'
+    if q.shape[-1] != 64 or v.shape[-1] != 64:
+        raise NotImplementedError("lucid_amd LUCID-Path kernels support head_dim 64")
+    for name, x in (("q", q), ("k", k), ("v", v), ("w", w), ("beta", beta)):
+        if not x.is_cuda:
+            raise RuntimeError(f"lucid_amd: {name} must be a GPU tensor (no CPU path)")
+        if x.dtype != torch.bfloat16:
+            raise TypeError(f"lucid_amd: {name} must be bfloat16, got {x.dtype}")
+    if cu_seqlens is not None:
+        if q.shape[0] != 1:
+            raise ValueError("cu_seqlens requires batch size 1 (packed sequences)")
+        outs, caches = [], []
+        bounds = cu_seqlens.tolist()
+        for s0, s1 in zip(bounds[:-1], bounds[1:]):
+            o_i, kc_i = ParallelLUCIDPathAttentionFunction.apply(
+                q[:, s0:s1], k[:, s0:s1], v[:, s0:s1], w[:, s0:s1], beta[:, s0:s1], g, scale, None, use_cache)
+            outs.append(o_i)
+            caches.append(kc_i)
+        return torch.cat(outs, 1), (torch.cat(caches, 1) if use_cache else None)
+    return ParallelLUCIDPathAttentionFunction.apply(q, k, v, w, beta, g, scale, cu_seqlens, use_cache)
