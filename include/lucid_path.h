@@ -41,6 +41,22 @@ int lucid_path_fwd(const void* q, const int64_t* q_strides, const void* k, const
                    void* kcache, const int64_t* kcache_strides, void* fwd_ws, int B, int T, int H, int HQ,
                    int K, float scale, void* stream);
 
+/* Bytes of the backward scratch workspace. */
+size_t lucid_path_bwd_workspace_bytes(int B, int T, int H, int HQ, int K);
+
+/* Backward of sum(o * dout) w.r.t. q [B,T,HQ,K], k, v, w [B,T,H,*] and beta [B,T,H]
+ * (bf16 outputs, GQA sums applied).  `o` and `fwd_ws` are those of the forward call.
+ * Replaces ParallelLUCIDPathAttentionFunction.backward (parallel.py:78-177): the dv
+ * solve (:103-114), bwd_prepare (:116-127), the Householder products, transform_q and
+ * the inter/intra-chunk gradient kernels (:129-163) and the GQA reduction (:165-171). */
+int lucid_path_bwd(const void* dout, const int64_t* do_strides, const void* q, const int64_t* q_strides,
+                   const void* k, const int64_t* k_strides, const void* w, const int64_t* w_strides,
+                   const void* beta, const int64_t* beta_strides, const void* o, const int64_t* o_strides,
+                   const void* fwd_ws, void* dq, const int64_t* dq_strides, void* dk, const int64_t* dk_strides,
+                   void* dv, const int64_t* dv_strides, void* dw, const int64_t* dw_strides, void* dbeta,
+                   const int64_t* dbeta_strides, void* bwd_ws, int B, int T, int H, int HQ, int K, float scale,
+                   void* stream);
+
 #ifdef __cplusplus
 }
 #endif

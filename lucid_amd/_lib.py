@@ -47,6 +47,10 @@ _SIGS = {
         "lucid_path_fwd_workspace_bytes": ([_int] * 5, _sz),
         "lucid_path_fwd": ([_vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p,
                             _vp, _i64p, _vp, _int, _int, _int, _int, _int, _flt, _vp], _int),
+        "lucid_path_bwd_workspace_bytes": ([_int] * 5, _sz),
+        "lucid_path_bwd": ([_vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp,
+                            _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp,
+                            _int, _int, _int, _int, _int, _flt, _vp], _int),
     },
 }
 

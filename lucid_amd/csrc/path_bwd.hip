@@ -1,0 +1,827 @@
+// LUCID-Path backward on CDNA4 (gfx950) (parallel.py:78-177).
+//
+//   dV  = (I + L)^-T dO                       chained, last chunk first
+//   dA  = -s (dV O^T) * L                     (strictly lower)
+// and the path-attention backward driven by dA through the two-level transport
+// (row sweep: queries carried down; column sweep: keys carried up; the d x d
+// chunk products; the WY form), then the GQA reduction.
+//
+// Kernels (256 threads):
+//   path_bwd_zero_kernel   zero chain counters and the atomic dHL / dHc accumulators
+//   path_dv_kernel         chained transposed solve dV_J = Y_J^T (dO_J - sum_{I>J} L_IJ^T dV_I),
+//                          plus the in-chunk dA_diag = -s (dV_J O_J^T) * L_diag
+//   path_bwd_row_kernel    per query chunk: G scan over key chunks -> dq~, dHL, dHc
+//   path_bwd_col_kernel    per key chunk: dk~ (same large chunk), dKL -> dk~, dSUF
+//   path_products_bwd_kernel  per large chunk: dHc += SUF^T F, F <- F Hc^T + dSUF
+//   path_wy_bwd_kernel     per chunk: backward of the WY form -> dq, dk, dw, dbeta
+//   path_reduce_kernel     GQA sums and casts to the caller's bf16 gradients
+#include "path_common.h"
+
+namespace lucid {
+
+struct PathBwdWs {
+  float* dvf;   // [BHq][T][64]       dV (fp32)
+  bf16* dvb;    // [BHq][T][64]       dV rows (bf16)
+  bf16* dvT;    // [BHq][64][T]       dV^T, T-perm (chain operand)
+  float* dad;   // [BHq][NT][64][64]  dA_diag
+  float* dqt;   // [BHq][T][64]       d q~
+  float* dkt;   // [BHq][T][64]       d k~
+  float* dsuf;  // [BHq][NT][64][64]  d SUF
+  float* dhl;   // [BHq][NS][64][64]  d HL  (atomics)
+  float* dhc;   // [BHq][NT][64][64]  d Hc  (atomics + products backward)
+  float* dq;    // [BHq][T][64]
+  float* dk;    // [BHq][T][64]       per query head, summed over the group at the end
+  float* dw;    // [BHq][T][64]
+  float* db;    // [BHq][T]
+  int* counters;  // [BHq]
+};
+
+__global__ __launch_bounds__(256) void path_bwd_zero_kernel(int64_t n_hl, int64_t n_hc, int n_cnt, PathBwdWs bw) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t j = i; j < n_hl; j += stride) bw.dhl[j] = 0.f;
+  for (int64_t j = i; j < n_hc; j += stride) bw.dhc[j] = 0.f;
+  if (i < n_cnt) bw.counters[i] = 0;
+}
+
+// ---------------------------------------------------------------------------
+// Chained transposed solve (triangular_solve_bwd_dv_reuse.py:113-205), one
+// workgroup per 64-column chunk J of one query head, ids grow as J falls.
+// wave w: ch = w & 1 -> columns 32*ch (lane <-> column j), ih = w >> 1 -> rows 32*ih
+// of every staged 64-row tile I > J.
+//   S[I][J] = Qop_I . Kop_J, L = exp(s S - 1/s), acc^T[d][j] += dV^T[d][i] L[i][j]
+// counters[bhq] = number of chunks of dV published from the end.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void path_dv_kernel(const bf16* __restrict__ dout, Strides dos,
+                                                      const bf16* __restrict__ o, Strides os, int HQ, int H, int T,
+                                                      int BHq, float scale, PathFwdWs ws, PathBwdWs bw) {
+  __shared__ __attribute__((aligned(16))) float Yt[64][68];  // Yt[c][r] = Y[r][c]
+  __shared__ __attribute__((aligned(16))) float Rt[64][68];
+  __shared__ __attribute__((aligned(16))) bf16 lq[2][64][72];
+  __shared__ __attribute__((aligned(16))) bf16 ld_[2][64][72];
+  const int NT = T / PC, NS = (NT + PR - 1) / PR;
+  const int id = blockIdx.x;
+  const int J = NT - 1 - id / BHq, bhq = id - (id / BHq) * BHq;
+  const int G = HQ / H;
+  const int b = bhq / HQ, hq = bhq - b * HQ, bh = b * H + hq / G;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
+  const int ch = w & 1, ih = w >> 1;
+  const int sJ = J / PR, ceJ = min(sJ * PR + PR, NT) - 1;  // last chunk of J's large chunk
+  const int j0 = J * PC;
+  int* cnt = bw.counters + bhq;
+  const float sl2 = scale * LOG2E_F, cc0 = LOG2E_F / scale;
+
+  load_mat64<true>(Yt, ws.y + ((int64_t)bhq * NT + J) * 4096);
+  bf16x8 kbs[4], kbf[4];
+#pragma unroll
+  for (int st = 0; st < 4; ++st) {
+    kbs[st] = ld8(ws.kt + ((int64_t)bh * T + j0 + ch * 32 + l32) * 64 + 16 * st + 8 * g);
+    kbf[st] = ld8(ws.kl + ((int64_t)bh * T + j0 + ch * 32 + l32) * 64 + 16 * st + 8 * g);
+  }
+  f32x16 acc[2] = {zero16(), zero16()};
+  bf16x8 stg[4];
+  auto gload = [&](int I) {
+    const bf16* qsrc = (I <= ceJ) ? ws.qs + (((int64_t)bhq * PR + (J - (I / PR) * PR)) * T) * 64
+                                  : ws.qb + (((int64_t)bhq * NS + sJ) * T) * 64;
+    g2r_rows<64>(qsrc, 64, I * PC, stg);
+    g2r_tp<64>(bw.dvT + (int64_t)bhq * 64 * T, T, I * PC, stg + 2);
+  };
+  auto lstore = [&](int buf) {
+    r2l_rows<64>(lq[buf], stg);
+    r2l_tp<64>(ld_[buf], stg + 2);
+  };
+  const int first = NT - 1;
+  int ready = 0;
+  if (first > J) {
+    ready = wait_counter_gt(cnt, 0);
+    gload(first);
+    lstore(0);
+  }
+  __syncthreads();
+  for (int I = first; I > J; --I) {
+    const int buf = (first - I) & 1;
+    const bool more = I - 1 > J;
+    bool early = false;
+    if (more) {
+      const int need = NT - I;  // chunk I-1 is published once the counter exceeds NT-1-(I-1)
+      if (need >= ready) {
+        const int seen = poll_counter(cnt);
+        if (seen > need) {
+          acquire_agent();
+          ready = seen;
+        }
+      }
+      early = need < ready;
+      if (early) gload(I - 1);
+    }
+    {
+      const bool same = (I <= ceJ);
+      f32x16 sc = zero16();
+#pragma unroll
+      for (int st = 0; st < 4; ++st)
+        sc = mfma32(ld8(&lq[buf][ih * 32 + l32][16 * st + 8 * g]), same ? kbs[st] : kbf[st], sc);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sc[e] = __builtin_amdgcn_exp2f(fmaf(sc[e], sl2, -cc0));
+      const bf16x8 p0 = pack_b(sc, 0), p1 = pack_b(sc, 1);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        acc[t] = mfma32(ld8(&ld_[buf][t * 32 + l32][ih * 32 + 8 * g]), p0, acc[t]);
+        acc[t] = mfma32(ld8(&ld_[buf][t * 32 + l32][ih * 32 + 16 + 8 * g]), p1, acc[t]);
+      }
+    }
+    if (more) {
+      if (!early) {
+        ready = wait_counter_gt(cnt, NT - I);
+        gload(I - 1);
+      }
+      lstore(buf ^ 1);
+    }
+    __syncthreads();
+  }
+  // ---- R = dO_J - acc ----
+  if (ih == 1) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][ch * 32 + l32] = acc[t][e];
+  }
+  __syncthreads();
+  if (ih == 0) {
+    const bf16* drow_ = dout + b * dos.b + hq * dos.h + (int64_t)(j0 + ch * 32 + l32) * dos.t;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) {
+        const int d0 = t * 32 + 8 * qq + 4 * g;
+        const bf16x4 x = *reinterpret_cast<const bf16x4*>(drow_ + d0);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          Rt[d0 + u][ch * 32 + l32] = (float)x[u] - (acc[t][4 * qq + u] + Rt[d0 + u][ch * 32 + l32]);
+      }
+  }
+  __syncthreads();
+  // ---- dV^T[d][c] = sum_r R^T[d][r] Y[r][c]  (Y lower: r >= c) ----
+  f32x16 dvo;
+  const int dt = w >> 1, chh = w & 1;
+  {
+    dvo = zero16();
+    for (int st = chh ? 2 : 0; st < 4; ++st) {
+      bf16x8 ah, al, bh8, bl;
+      split8(&Rt[dt * 32 + l32][16 * st + 8 * g], ah, al);
+      split8(&Yt[chh * 32 + l32][16 * st + 8 * g], bh8, bl);
+      dvo = mfma32(ah, bh8, dvo);
+      dvo = mfma32(ah, bl, dvo);
+      dvo = mfma32(al, bh8, dvo);
+    }
+    const int cl = chh * 32 + l32;
+    const int r = j0 + cl;
+    const int slot = (r & ~15) | jmap(r & 15);
+    float* of = bw.dvf + ((int64_t)bhq * T + r) * 64;
+    bf16* ob = bw.dvb + ((int64_t)bhq * T + r) * 64;
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) {
+      const int d0 = dt * 32 + 8 * qq + 4 * g;
+      f32x4 f;
+      bf16x4 bb;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        f[u] = dvo[4 * qq + u];
+        bb[u] = (bf16)f[u];
+        bw.dvT[((int64_t)bhq * 64 + d0 + u) * T + slot] = bb[u];
+      }
+      *reinterpret_cast<f32x4*>(of + d0) = f;
+      *reinterpret_cast<bf16x4*>(ob + d0) = bb;
+    }
+  }
+  publish_counter(cnt, NT - J);
+  // ---- dA_diag = -s (dV_J O_J^T) * L_diag  (fp32, in LDS) ----
+#pragma unroll
+  for (int e = 0; e < 16; ++e) Rt[chh * 32 + l32][dt * 32 + drow(e, g)] = dvo[e];  // Rt <- dV rows
+  load_rows64_f32(Yt, o + b * os.b + hq * os.h + (int64_t)j0 * os.t, os.t);       // Yt <- O rows
+  __syncthreads();
+  float a4[4][4];
+  zero44(a4);
+  lds_gemm64<false, true>(Rt, Yt, a4);
+  {
+    const int r0 = (tid >> 4) * 4, c0 = (tid & 15) * 4;
+    const float* ldp = ws.ld + ((int64_t)bhq * NT + J) * 4096;
+    float* dst = bw.dad + ((int64_t)bhq * NT + J) * 4096;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f32x4 lv = *reinterpret_cast<const f32x4*>(ldp + (r0 + i) * 64 + c0);
+      f32x4 v;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] = -scale * a4[i][j] * lv[j];
+      *reinterpret_cast<f32x4*>(dst + (r0 + i) * 64 + c0) = v;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Row sweep (parallel_path_bwd_inter_dqh.py, parallel_path_bwd_intra.py): per query
+// chunk I, key chunks J ascending.  G accumulates d(query operand):
+//   G^T[d][i] += Kop^T[d][j] dA^T[j][i]
+// and at every change of query operand X (large-chunk boundary: X = QB^(s), M = HL_s;
+// inside I's large chunk: X = QS^(c), M = Hc_c):  dM += X^T G,  G <- G M^T.
+// Finally d q~_I = G.  wave w: ih = w & 1 -> rows 32*ih (lane <-> row i),
+// jh = w >> 1 -> keys 32*jh; partial G of the two key halves is summed in LDS at
+// every transport step.  grid (NT, B*HQ)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void path_bwd_row_kernel(const bf16* __restrict__ o, Strides os, int HQ, int H,
+                                                           int T, float scale, PathFwdWs ws, PathBwdWs bw) {
+  __shared__ __attribute__((aligned(16))) bf16 lk[64][72];
+  __shared__ __attribute__((aligned(16))) bf16 lo[64][72];
+  __shared__ __attribute__((aligned(16))) bf16 lkt[64][72];
+  __shared__ __attribute__((aligned(16))) float Gs[64][68];  // full G (rows i, cols d)
+  __shared__ __attribute__((aligned(16))) float Ms[64][68];  // transport matrix M (rows)
+  const int NT = T / PC, NS = (NT + PR - 1) / PR;
+  const int I = blockIdx.x, bhq = blockIdx.y;
+  const int G_ = HQ / H;
+  const int b = bhq / HQ, hq = bhq - b * HQ, bh = b * H + hq / G_;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
+  const int ih = w & 1, jh = w >> 1;
+  const int sI = I / PR, cb = sI * PR;
+  const int i0 = I * PC;
+  const float sl2 = scale * LOG2E_F, cc0 = LOG2E_F / scale;
+
+  bf16x8 dvr[4];
+#pragma unroll
+  for (int st = 0; st < 4; ++st) dvr[st] = ld8(bw.dvb + ((int64_t)bhq * T + i0 + ih * 32 + l32) * 64 + 16 * st + 8 * g);
+  f32x16 acc[2] = {zero16(), zero16()};
+
+  // ---- G (sum of the two key halves) -> Gs ----
+  auto gather_G = [&]() {
+    if (jh == 1) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) Gs[ih * 32 + l32][t * 32 + drow(e, g)] = acc[t][e];
+    }
+    __syncthreads();
+    if (jh == 0) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) Gs[ih * 32 + l32][t * 32 + drow(e, g)] += acc[t][e];
+    }
+    __syncthreads();
+  };
+  // ---- dM += X^T G (atomic) and G <- G M^T ----
+  auto transition = [&](const bf16* XT, const float* M, float* dM) {
+    gather_G();
+    load_mat64<false>(Ms, M);
+    {
+      const int at = w >> 1, bt = w & 1;  // dM tile (a rows, b cols)
+      f32x16 dm = zero16();
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const bf16x8 xa = ld8(XT + (int64_t)(at * 32 + l32) * T + i0 + 16 * ks + 8 * g);
+        bf16x8 gh, gl;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float x = Gs[16 * ks + jmap(8 * g + e)][bt * 32 + l32];
+          gh[e] = (bf16)x;
+          gl[e] = (bf16)(x - (float)gh[e]);
+        }
+        dm = mfma32(xa, gh, dm);
+        dm = mfma32(xa, gl, dm);
+      }
+#pragma unroll
+      for (int e = 0; e < 16; ++e) unsafeAtomicAdd(dM + (at * 32 + drow(e, g)) * 64 + bt * 32 + l32, dm[e]);
+    }
+    __syncthreads();
+    f32x16 gn;
+    {
+      const int bt = w >> 1, it = w & 1;  // new G^T tile (b rows, i cols)
+      gn = zero16();
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        bf16x8 ah, al, bh8, bl;
+        split8(&Ms[bt * 32 + l32][16 * ks + 8 * g], ah, al);
+        split8(&Gs[it * 32 + l32][16 * ks + 8 * g], bh8, bl);
+        gn = mfma32(ah, bh8, gn);
+        gn = mfma32(ah, bl, gn);
+        gn = mfma32(al, bh8, gn);
+      }
+    }
+    __syncthreads();
+    {
+      const int bt = w >> 1, it = w & 1;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) Gs[it * 32 + l32][bt * 32 + drow(e, g)] = gn[e];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[t][e] = (jh == 0) ? Gs[ih * 32 + l32][t * 32 + drow(e, g)] : 0.f;
+  };
+
+  bf16x8 qb[4];
+  bf16x8 stg[6];
+  auto gload = [&](int J) {
+    const bool far = J < cb;
+    const bf16* kr = (far ? ws.kl : ws.kt) + (int64_t)bh * T * 64;
+    const bf16* ktp = (far ? ws.klT : ws.ktT) + (int64_t)bh * 64 * T;
+    g2r_rows<64>(kr, 64, J * PC, stg);
+    g2r_rows<64>(o + b * os.b + hq * os.h, os.t, J * PC, stg + 2);
+    g2r_tp<64>(ktp, T, J * PC, stg + 4);
+  };
+  if (I > 0) gload(0);
+  for (int J = 0; J < I; ++J) {
+    // transport step before the first tile that uses a new query operand
+    if (J < cb) {
+      if (J % PR == 0 && J > 0) {
+        const int s = J / PR;
+        transition(ws.qbT + ((int64_t)bhq * NS + s) * 64 * T, ws.hl + ((int64_t)bh * NS + s) * 4096,
+                   bw.dhl + ((int64_t)bhq * NS + s) * 4096);
+      }
+    } else if (sI > 0 || J > cb) {
+      transition(ws.qsT + ((int64_t)bhq * PR + (J - cb)) * 64 * T, ws.hc + ((int64_t)bh * NT + J) * 4096,
+                 bw.dhc + ((int64_t)bhq * NT + J) * 4096);
+    }
+    r2l_rows<64>(lk, stg);
+    r2l_rows<64>(lo, stg + 2);
+    r2l_tp<64>(lkt, stg + 4);
+    {
+      const bf16* qsrc = (J < cb) ? ws.qb + ((int64_t)bhq * NS + J / PR) * T * 64
+                                  : ws.qs + ((int64_t)bhq * PR + (J - cb)) * T * 64;
+#pragma unroll
+      for (int st = 0; st < 4; ++st) qb[st] = ld8(qsrc + (int64_t)(i0 + ih * 32 + l32) * 64 + 16 * st + 8 * g);
+    }
+    __syncthreads();
+    if (J + 1 < I) gload(J + 1);
+    {
+      f32x16 sc = zero16(), dp = zero16();
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        sc = mfma32(ld8(&lk[jh * 32 + l32][16 * st + 8 * g]), qb[st], sc);
+        dp = mfma32(ld8(&lo[jh * 32 + l32][16 * st + 8 * g]), dvr[st], dp);
+      }
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sc[e] = -scale * dp[e] * __builtin_amdgcn_exp2f(fmaf(sc[e], sl2, -cc0));
+      const bf16x8 d0 = pack_b(sc, 0), d1 = pack_b(sc, 1);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        acc[t] = mfma32(ld8(&lkt[t * 32 + l32][jh * 32 + 8 * g]), d0, acc[t]);
+        acc[t] = mfma32(ld8(&lkt[t * 32 + l32][jh * 32 + 16 + 8 * g]), d1, acc[t]);
+      }
+    }
+    __syncthreads();
+  }
+  gather_G();
+  {
+    float* dst = bw.dqt + ((int64_t)bhq * T + i0) * 64;
+    for (int idx = tid; idx < 4096; idx += 256) dst[idx] = Gs[idx >> 6][idx & 63];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Column sweep (parallel_path_bwd_inter_dkv.py, parallel_path_bwd_intra.py): per key
+// chunk J, query chunks I > J.  wave w: ch = w & 1 -> keys 32*ch (lane <-> key j),
+// ih = w >> 1 -> rows 32*ih of each staged query tile.
+//   S[i][j] = Qop_I . Kop_J, dP[i][j] = dV_I . O_J, dA = -s dP * exp(s S - 1/s)
+//   dKop^T[d][j] += Qop^T[d][i] dA[i][j]   (Kop = k~_J for I in J's large chunk, else KL_J)
+// Then d k~_J = dk~(same) + dKL SUF_J and dSUF_J = dKL^T k~_J.  grid (NT, B*HQ)
+// ---------------------------------------------------------------------------
+struct ColSmem {
+  union {
+    struct {
+      bf16 q[64][72];
+      bf16 dv[64][72];
+      bf16 qt[64][72];
+    } st;
+    struct {
+      float a[64][68];  // d k~ (same large chunk), then the result
+      float f[64][68];  // dKL
+      float m[64][68];  // SUF_J, then k~_J
+    } fin;
+  } u;
+};
+
+__global__ __launch_bounds__(256) void path_bwd_col_kernel(const bf16* __restrict__ o, Strides os, int HQ, int H,
+                                                           int T, float scale, PathFwdWs ws, PathBwdWs bw) {
+  __shared__ __attribute__((aligned(16))) ColSmem sm;
+  const int NT = T / PC, NS = (NT + PR - 1) / PR;
+  const int J = blockIdx.x, bhq = blockIdx.y;
+  const int G_ = HQ / H;
+  const int b = bhq / HQ, hq = bhq - b * HQ, bh = b * H + hq / G_;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
+  const int ch = w & 1, ih = w >> 1;
+  const int sJ = J / PR, ceJ = min(sJ * PR + PR, NT) - 1;
+  const int j0 = J * PC;
+  const float sl2 = scale * LOG2E_F, cc0 = LOG2E_F / scale;
+
+  bf16x8 kbs[4], kbf[4], ob[4];
+#pragma unroll
+  for (int st = 0; st < 4; ++st) {
+    const int jr = j0 + ch * 32 + l32;
+    kbs[st] = ld8(ws.kt + ((int64_t)bh * T + jr) * 64 + 16 * st + 8 * g);
+    kbf[st] = ld8(ws.kl + ((int64_t)bh * T + jr) * 64 + 16 * st + 8 * g);
+    ob[st] = ld8(o + b * os.b + hq * os.h + (int64_t)jr * os.t + 16 * st + 8 * g);
+  }
+  f32x16 as_[2] = {zero16(), zero16()}, af[2] = {zero16(), zero16()};
+  bf16x8 stg[6];
+  auto gload = [&](int I) {
+    const bool same = I <= ceJ;
+    const bf16* qr = same ? ws.qs + ((int64_t)bhq * PR + (J - sJ * PR)) * T * 64
+                          : ws.qb + ((int64_t)bhq * NS + sJ) * T * 64;
+    const bf16* qtp = same ? ws.qsT + ((int64_t)bhq * PR + (J - sJ * PR)) * 64 * T
+                           : ws.qbT + ((int64_t)bhq * NS + sJ) * 64 * T;
+    g2r_rows<64>(qr, 64, I * PC, stg);
+    g2r_rows<64>(bw.dvb + (int64_t)bhq * T * 64, 64, I * PC, stg + 2);
+    g2r_tp<64>(qtp, T, I * PC, stg + 4);
+  };
+  if (J + 1 < NT) gload(J + 1);
+  for (int I = J + 1; I < NT; ++I) {
+    r2l_rows<64>(sm.u.st.q, stg);
+    r2l_rows<64>(sm.u.st.dv, stg + 2);
+    r2l_tp<64>(sm.u.st.qt, stg + 4);
+    __syncthreads();
+    if (I + 1 < NT) gload(I + 1);
+    const bool same = I <= ceJ;
+    f32x16 sc = zero16(), dp = zero16();
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      sc = mfma32(ld8(&sm.u.st.q[ih * 32 + l32][16 * st + 8 * g]), same ? kbs[st] : kbf[st], sc);
+      dp = mfma32(ld8(&sm.u.st.dv[ih * 32 + l32][16 * st + 8 * g]), ob[st], dp);
+    }
+#pragma unroll
+    for (int e = 0; e < 16; ++e) sc[e] = -scale * dp[e] * __builtin_amdgcn_exp2f(fmaf(sc[e], sl2, -cc0));
+    const bf16x8 d0 = pack_b(sc, 0), d1 = pack_b(sc, 1);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const bf16x8 a0 = ld8(&sm.u.st.qt[t * 32 + l32][ih * 32 + 8 * g]);
+      const bf16x8 a1 = ld8(&sm.u.st.qt[t * 32 + l32][ih * 32 + 16 + 8 * g]);
+      if (same) {
+        as_[t] = mfma32(a0, d0, as_[t]);
+        as_[t] = mfma32(a1, d1, as_[t]);
+      } else {
+        af[t] = mfma32(a0, d0, af[t]);
+        af[t] = mfma32(a1, d1, af[t]);
+      }
+    }
+    __syncthreads();
+  }
+  // ---- reduce the two row halves: fin.a = dk~(same), fin.f = dKL (rows j, cols d) ----
+  if (ih == 1) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        sm.u.fin.a[ch * 32 + l32][t * 32 + drow(e, g)] = as_[t][e];
+        sm.u.fin.f[ch * 32 + l32][t * 32 + drow(e, g)] = af[t][e];
+      }
+  }
+  __syncthreads();
+  if (ih == 0) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        sm.u.fin.a[ch * 32 + l32][t * 32 + drow(e, g)] += as_[t][e];
+        sm.u.fin.f[ch * 32 + l32][t * 32 + drow(e, g)] += af[t][e];
+      }
+  }
+  load_mat64<false>(sm.u.fin.m, ws.suf + ((int64_t)bh * NT + J) * 4096);
+  __syncthreads();
+  const int r0 = (tid >> 4) * 4, c0 = (tid & 15) * 4;
+  float acc4[4][4];
+  zero44(acc4);
+  lds_gemm64<false, false>(sm.u.fin.f, sm.u.fin.m, acc4);  // dKL SUF
+  {
+    float* dst = bw.dkt + ((int64_t)bhq * T + j0) * 64;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f32x4 v;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] = acc4[i][j] + sm.u.fin.a[r0 + i][c0 + j];
+      *reinterpret_cast<f32x4*>(dst + (r0 + i) * 64 + c0) = v;
+    }
+  }
+  __syncthreads();
+  load_rows64_f32(sm.u.fin.m, ws.kt + ((int64_t)bh * T + j0) * 64, 64);
+  __syncthreads();
+  zero44(acc4);
+  lds_gemm64<true, false>(sm.u.fin.f, sm.u.fin.m, acc4);  // dSUF = dKL^T k~
+  {
+    float* dst = bw.dsuf + ((int64_t)bhq * NT + J) * 4096;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f32x4 v;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] = acc4[i][j];
+      *reinterpret_cast<f32x4*>(dst + (r0 + i) * 64 + c0) = v;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Products backward inside one large chunk (cumprod_householder_bwd.py:13-95):
+//   F = dHL_s; for c from the bottom up: dHc_c += SUF_c^T F; F <- F Hc_c^T + dSUF_c
+// grid (NS, B*HQ)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void path_products_bwd_kernel(int HQ, int H, int T, PathFwdWs ws, PathBwdWs bw) {
+  __shared__ __attribute__((aligned(16))) float F[64][68];
+  __shared__ __attribute__((aligned(16))) float S[64][68];
+  __shared__ __attribute__((aligned(16))) float Hs[64][68];
+  const int NT = T / PC, NS = (NT + PR - 1) / PR;
+  const int s = blockIdx.x, bhq = blockIdx.y;
+  const int G_ = HQ / H;
+  const int b = bhq / HQ, hq = bhq - b * HQ, bh = b * H + hq / G_;
+  const int tid = threadIdx.x;
+  const int r0 = (tid >> 4) * 4, c0 = (tid & 15) * 4;
+  const int cb = s * PR, ce = min(cb + PR, NT) - 1;
+  load_mat64<false>(F, bw.dhl + ((int64_t)bhq * NS + s) * 4096);
+  float acc[4][4];
+  for (int c = cb; c <= ce; ++c) {
+    load_mat64<false>(S, ws.suf + ((int64_t)bh * NT + c) * 4096);
+    load_mat64<false>(Hs, ws.hc + ((int64_t)bh * NT + c) * 4096);
+    __syncthreads();
+    zero44(acc);
+    lds_gemm64<true, false>(S, F, acc);
+    {
+      float* dst = bw.dhc + ((int64_t)bhq * NT + c) * 4096;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        f32x4 v = *reinterpret_cast<f32x4*>(dst + (r0 + i) * 64 + c0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] += acc[i][j];
+        *reinterpret_cast<f32x4*>(dst + (r0 + i) * 64 + c0) = v;
+      }
+    }
+    zero44(acc);
+    lds_gemm64<false, true>(F, Hs, acc);
+    __syncthreads();
+    {
+      const float* ds = bw.dsuf + ((int64_t)bhq * NT + c) * 4096;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(ds + (r0 + i) * 64 + c0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) F[r0 + i][c0 + j] = acc[i][j] + v[j];
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward of the WY form of one chunk (intra_chunk_preprocess_bwd.py:14-110):
+//   Wb = beta W, Tm = (I + stril(Wb W^T))^-1, W2 = Tm Wb, Hc = I - W^T W2,
+//   q~ = q - QW W2 (QW = tril(q W^T)), k~ = k - TW^T W (TW = Tm stril(Wb k^T)),
+//   A_diag = tril(q k^T - QW TW).
+// Inputs d q~, d k~, dA_diag, dHc; outputs dq, dk, dw, dbeta (per query head, fp32).
+// All 64x64 products in fp32 on LDS (9 buffers).  grid (NT, B*HQ)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void path_wy_bwd_kernel(const bf16* __restrict__ q, Strides qs,
+                                                          const bf16* __restrict__ k, Strides ks,
+                                                          const bf16* __restrict__ w, Strides wst,
+                                                          const bf16* __restrict__ beta, Strides bst, int HQ, int H,
+                                                          int T, PathFwdWs ws, PathBwdWs bw) {
+  __shared__ __attribute__((aligned(16))) float W[64][68];
+  __shared__ __attribute__((aligned(16))) float Wb[64][68];
+  __shared__ __attribute__((aligned(16))) float Q[64][68];
+  __shared__ __attribute__((aligned(16))) float K[64][68];
+  __shared__ __attribute__((aligned(16))) float Tm[64][68];
+  __shared__ __attribute__((aligned(16))) float S1[64][68];
+  __shared__ __attribute__((aligned(16))) float S2[64][68];
+  __shared__ __attribute__((aligned(16))) float S3[64][68];
+  __shared__ __attribute__((aligned(16))) float S4[64][68];
+  const int NT = T / PC;
+  const int c = blockIdx.x, bhq = blockIdx.y;
+  const int G_ = HQ / H;
+  const int b = bhq / HQ, hq = bhq - b * HQ, h = hq / G_, bh = b * H + h;
+  const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
+  const int r0 = (tid >> 4) * 4, c0 = (tid & 15) * 4;
+  const int t0 = c * PC;
+  float bt4[4];
+
+  load_rows64_f32(W, w + b * wst.b + h * wst.h + (int64_t)t0 * wst.t, wst.t);
+  load_rows64_f32(Q, q + b * qs.b + hq * qs.h + (int64_t)t0 * qs.t, qs.t);
+  load_rows64_f32(K, k + b * ks.b + h * ks.h + (int64_t)t0 * ks.t, ks.t);
+  __syncthreads();
+  {
+    const int r = tid >> 2, cc = (tid & 3) * 16;
+    const float bt = (float)beta[b * bst.b + h * bst.h + (int64_t)(t0 + r) * bst.t];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) Wb[r][cc + e] = bt * W[r][cc + e];
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) bt4[i] = (float)beta[b * bst.b + h * bst.h + (int64_t)(t0 + r0 + i) * bst.t];
+  __syncthreads();
+  float t4[4][4];
+  zero44(t4);
+  lds_gemm64<false, true>(Wb, W, t4);
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) Tm[r0 + i][c0 + j] = (c0 + j < r0 + i) ? t4[i][j] : 0.f;
+  __syncthreads();
+  if (wv == 0) invert_unit_lower64(Tm, lane);
+  load_mat64<false>(S1, ws.w2 + ((int64_t)bh * T + t0) * 64);          // W2
+  load_mat64<false>(S2, bw.dhc + ((int64_t)bhq * NT + c) * 4096);      // dHc
+  __syncthreads();
+  float aW[4][4], aW2[4][4], aq[4][4], ak[4][4], aWb[4][4], dQW[4][4], dTW[4][4], dTm[4][4];
+  zero44(aW);
+  zero44(aW2);
+  zero44(aWb);
+  zero44(dQW);
+  zero44(dTW);
+  zero44(dTm);
+  lds_gemm64<false, true>(S1, S2, aW);   // W2 dHc^T
+  lds_gemm64<false, false>(W, S2, aW2);  // W dHc
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      aW[i][j] = -aW[i][j];
+      aW2[i][j] = -aW2[i][j];
+    }
+  zero44(t4);
+  lds_gemm64<false, true>(Q, W, t4);  // QW
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) S3[r0 + i][c0 + j] = (c0 + j <= r0 + i) ? t4[i][j] : 0.f;
+  __syncthreads();
+  load_mat64<false>(S2, bw.dqt + ((int64_t)bhq * T + t0) * 64);  // d q~
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) aq[i][j] = S2[r0 + i][c0 + j];
+  lds_gemm64<false, true>(S2, S1, dQW);  // dq~ W2^T   (negated below)
+  zero44(t4);
+  lds_gemm64<true, false>(S3, S2, t4);   // QW^T dq~
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      dQW[i][j] = -dQW[i][j];
+      aW2[i][j] -= t4[i][j];
+    }
+  zero44(t4);
+  lds_gemm64<false, true>(Wb, K, t4);    // WBK
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) S4[r0 + i][c0 + j] = (c0 + j < r0 + i) ? t4[i][j] : 0.f;
+  __syncthreads();
+  zero44(t4);
+  lds_gemm64<false, false>(Tm, S4, t4);  // TW
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) S1[r0 + i][c0 + j] = t4[i][j];
+  load_mat64<false>(S2, bw.dkt + ((int64_t)bhq * T + t0) * 64);  // d k~
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ak[i][j] = S2[r0 + i][c0 + j];
+  lds_gemm64<false, true>(W, S2, dTW);   // W dk~^T (negated below)
+  zero44(t4);
+  lds_gemm64<false, false>(S1, S2, t4);  // TW dk~
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      dTW[i][j] = -dTW[i][j];
+      aW[i][j] -= t4[i][j];
+    }
+  __syncthreads();
+  load_mat64<false>(S2, bw.dad + ((int64_t)bhq * NT + c) * 4096);  // dA_diag
+  __syncthreads();
+  lds_gemm64<false, false>(S2, K, aq);   // dq += dA K
+  lds_gemm64<true, false>(S2, Q, ak);    // dk += dA^T Q
+  zero44(t4);
+  lds_gemm64<false, true>(S2, S1, t4);   // dA TW^T
+  float t5[4][4];
+  zero44(t5);
+  lds_gemm64<true, false>(S3, S2, t5);   // QW^T dA
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      dQW[i][j] -= t4[i][j];
+      dTW[i][j] -= t5[i][j];
+    }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) S2[r0 + i][c0 + j] = (c0 + j <= r0 + i) ? dQW[i][j] : 0.f;
+  __syncthreads();
+  lds_gemm64<false, false>(S2, W, aq);   // dq += tril(dQW) W
+  lds_gemm64<true, false>(S2, Q, aW);    // dW += tril(dQW)^T q
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) S2[r0 + i][c0 + j] = dTW[i][j];
+  __syncthreads();
+  lds_gemm64<false, true>(S2, S4, dTm);  // dTm = dTW WBK^T
+  zero44(t4);
+  lds_gemm64<true, false>(Tm, S2, t4);   // Tm^T dTW
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) S3[r0 + i][c0 + j] = (c0 + j < r0 + i) ? t4[i][j] : 0.f;  // dWBK
+  __syncthreads();
+  lds_gemm64<false, false>(S3, K, aWb);  // dWb = dWBK k
+  lds_gemm64<true, false>(S3, Wb, ak);   // dk += dWBK^T Wb
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) S1[r0 + i][c0 + j] = aW2[i][j];  // dW2
+  __syncthreads();
+  lds_gemm64<false, true>(S1, Wb, dTm);  // dTm += dW2 Wb^T
+  lds_gemm64<true, false>(Tm, S1, aWb);  // dWb += Tm^T dW2
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) S2[r0 + i][c0 + j] = dTm[i][j];
+  __syncthreads();
+  zero44(t4);
+  lds_gemm64<true, false>(Tm, S2, t4);   // Tm^T dTm
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) S3[r0 + i][c0 + j] = t4[i][j];
+  __syncthreads();
+  zero44(t4);
+  lds_gemm64<false, true>(S3, Tm, t4);   // (Tm^T dTm) Tm^T
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) S4[r0 + i][c0 + j] = (c0 + j < r0 + i) ? -t4[i][j] : 0.f;  // da
+  __syncthreads();
+  lds_gemm64<false, false>(S4, W, aWb);  // dWb += da W
+  lds_gemm64<true, false>(S4, Wb, aW);   // dW += da^T Wb
+  float dbp[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    dbp[i] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      aW[i][j] += bt4[i] * aWb[i][j];
+      dbp[i] += aWb[i][j] * W[r0 + i][c0 + j];
+    }
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) dbp[i] += __shfl_xor(dbp[i], m, 64);
+  }
+  const int64_t rowbase = ((int64_t)bhq * T + t0) * 64;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f32x4 vq, vk, vw;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      vq[j] = aq[i][j];
+      vk[j] = ak[i][j];
+      vw[j] = aW[i][j];
+    }
+    *reinterpret_cast<f32x4*>(bw.dq + rowbase + (r0 + i) * 64 + c0) = vq;
+    *reinterpret_cast<f32x4*>(bw.dk + rowbase + (r0 + i) * 64 + c0) = vk;
+    *reinterpret_cast<f32x4*>(bw.dw + rowbase + (r0 + i) * 64 + c0) = vw;
+    if ((tid & 15) == 0) bw.db[(int64_t)bhq * T + t0 + r0 + i] = dbp[i];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// GQA sums over the query heads of each kv head (parallel.py:165-171) and casts
+// to the caller's bf16 gradients.  grid (T/4, B*H), thread = (row, column)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void path_reduce_kernel(int HQ, int H, int T, PathBwdWs bw, bf16* __restrict__ dq,
+                                                          Strides dqs, bf16* __restrict__ dk, Strides dks,
+                                                          bf16* __restrict__ dv, Strides dvs, bf16* __restrict__ dw,
+                                                          Strides dws, bf16* __restrict__ db, Strides dbs) {
+  const int bh = blockIdx.y;
+  const int b = bh / H, h = bh - b * H;
+  const int G_ = HQ / H;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6), col = threadIdx.x & 63;
+  if (t >= T) return;
+  float sk = 0.f, sv = 0.f, sw = 0.f, sb = 0.f;
+  for (int gi = 0; gi < G_; ++gi) {
+    const int hq = h * G_ + gi;
+    const int64_t bhq = (int64_t)b * HQ + hq;
+    const int64_t off = (bhq * T + t) * 64 + col;
+    sk += bw.dk[off];
+    sv += bw.dvf[off];
+    sw += bw.dw[off];
+    if (col == 0) sb += bw.db[bhq * T + t];
+    dq[b * dqs.b + hq * dqs.h + (int64_t)t * dqs.t + col] = (bf16)bw.dq[off];
+  }
+  dk[b * dks.b + h * dks.h + (int64_t)t * dks.t + col] = (bf16)sk;
+  dv[b * dvs.b + h * dvs.h + (int64_t)t * dvs.t + col] = (bf16)sv;
+  dw[b * dws.b + h * dws.h + (int64_t)t * dws.t + col] = (bf16)sw;
+  if (col == 0) db[b * dbs.b + h * dbs.h + (int64_t)t * dbs.t] = (bf16)sb;
+}
+
+}  // namespace lucid

@@ -3,6 +3,7 @@
 
 #include "../../include/lucid_path.h"
 #include "path_fwd.hip"
+#include "path_bwd.hip"
 
 namespace {
 
@@ -72,6 +73,35 @@ int pcheck_vec(const char* name, const void* p, const int64_t* s) {
 
 lucid::Strides PS(const int64_t* s) { return lucid::Strides{s[0], s[1], s[2]}; }
 
+lucid::PathBwdWs carve_path_bwd(void* base, int B, int T, int HQ, size_t* bytes) {
+  const size_t BHq = (size_t)B * HQ;
+  const size_t NT = T / 64, NS = (NT + 7) / 8;
+  lucid::PathBwdWs w{};
+  size_t off = 0;
+  char* p = static_cast<char*>(base);
+  auto take = [&](size_t n) {
+    char* r = p ? p + off : nullptr;
+    off += a256(n);
+    return r;
+  };
+  w.dvf = reinterpret_cast<float*>(take(BHq * T * 64 * 4));
+  w.dvb = reinterpret_cast<bf16*>(take(BHq * T * 64 * 2));
+  w.dvT = reinterpret_cast<bf16*>(take(BHq * T * 64 * 2));
+  w.dad = reinterpret_cast<float*>(take(BHq * NT * 4096 * 4));
+  w.dqt = reinterpret_cast<float*>(take(BHq * T * 64 * 4));
+  w.dkt = reinterpret_cast<float*>(take(BHq * T * 64 * 4));
+  w.dsuf = reinterpret_cast<float*>(take(BHq * NT * 4096 * 4));
+  w.dhl = reinterpret_cast<float*>(take(BHq * NS * 4096 * 4));
+  w.dhc = reinterpret_cast<float*>(take(BHq * NT * 4096 * 4));
+  w.dq = reinterpret_cast<float*>(take(BHq * T * 64 * 4));
+  w.dk = reinterpret_cast<float*>(take(BHq * T * 64 * 4));
+  w.dw = reinterpret_cast<float*>(take(BHq * T * 64 * 4));
+  w.db = reinterpret_cast<float*>(take(BHq * T * 4));
+  w.counters = reinterpret_cast<int*>(take(BHq * 4));
+  if (bytes) *bytes = off;
+  return w;
+}
+
 }  // namespace
 
 extern "C" {
@@ -127,6 +157,67 @@ int lucid_path_fwd(const void* q, const int64_t* q_strides, const void* k, const
     if (int rc = phip("path_kcache_kernel")) return rc;
   }
   return 0;
+}
+
+size_t lucid_path_bwd_workspace_bytes(int B, int T, int H, int HQ, int K) {
+  (void)H;
+  (void)K;
+  size_t n = 0;
+  carve_path_bwd(nullptr, B, T, HQ, &n);
+  return n;
+}
+
+int lucid_path_bwd(const void* dout, const int64_t* do_strides, const void* q, const int64_t* q_strides,
+                   const void* k, const int64_t* k_strides, const void* w, const int64_t* w_strides,
+                   const void* beta, const int64_t* beta_strides, const void* o, const int64_t* o_strides,
+                   const void* fwd_ws, void* dq, const int64_t* dq_strides, void* dk, const int64_t* dk_strides,
+                   void* dv, const int64_t* dv_strides, void* dw, const int64_t* dw_strides, void* dbeta,
+                   const int64_t* dbeta_strides, void* bwd_ws, int B, int T, int H, int HQ, int K, float scale,
+                   void* stream) {
+  g_path_error.clear();
+  if (B <= 0 || T <= 0 || H <= 0 || HQ <= 0) return pfail("B, T, H and HQ must be positive");
+  if (K != 64) return pfail("head_dim must be 64, got " + std::to_string(K));
+  if (T % 64) return pfail("T must be a multiple of 64, got " + std::to_string(T));
+  if (HQ % H) return pfail("the number of query heads must be a multiple of the key heads");
+  if (int rc = pcheck_vec("dout", dout, do_strides)) return rc;
+  if (int rc = pcheck_vec("q", q, q_strides)) return rc;
+  if (int rc = pcheck_vec("k", k, k_strides)) return rc;
+  if (int rc = pcheck_vec("w", w, w_strides)) return rc;
+  if (int rc = pcheck("beta", beta, beta_strides)) return rc;
+  if (int rc = pcheck_vec("o", o, o_strides)) return rc;
+  if (int rc = pcheck("dq", dq, dq_strides)) return rc;
+  if (int rc = pcheck("dk", dk, dk_strides)) return rc;
+  if (int rc = pcheck("dv", dv, dv_strides)) return rc;
+  if (int rc = pcheck("dw", dw, dw_strides)) return rc;
+  if (int rc = pcheck("dbeta", dbeta, dbeta_strides)) return rc;
+  if (!fwd_ws || !bwd_ws) return pfail("fwd_ws and bwd_ws must be non-null");
+  const lucid::PathFwdWs ws = carve_path_fwd(const_cast<void*>(fwd_ws), B, T, H, HQ, nullptr);
+  const lucid::PathBwdWs bw = carve_path_bwd(bwd_ws, B, T, HQ, nullptr);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int NT = T / 64, NS = (NT + 7) / 8;
+  const int BH = B * H, BHq = B * HQ;
+  const int64_t n_hl = (int64_t)BHq * NS * 4096, n_hc = (int64_t)BHq * NT * 4096;
+  hipLaunchKernelGGL(lucid::path_bwd_zero_kernel, dim3(1024), dim3(256), 0, st, n_hl, n_hc, BHq, bw);
+  if (int rc = phip("path_bwd_zero_kernel")) return rc;
+  hipLaunchKernelGGL(lucid::path_dv_kernel, dim3(NT * BHq), dim3(256), 0, st, (const bf16*)dout, PS(do_strides),
+                     (const bf16*)o, PS(o_strides), HQ, H, T, BHq, scale, ws, bw);
+  if (int rc = phip("path_dv_kernel")) return rc;
+  hipLaunchKernelGGL(lucid::path_bwd_row_kernel, dim3(NT, BHq), dim3(256), 0, st, (const bf16*)o, PS(o_strides),
+                     HQ, H, T, scale, ws, bw);
+  if (int rc = phip("path_bwd_row_kernel")) return rc;
+  hipLaunchKernelGGL(lucid::path_bwd_col_kernel, dim3(NT, BHq), dim3(256), 0, st, (const bf16*)o, PS(o_strides),
+                     HQ, H, T, scale, ws, bw);
+  if (int rc = phip("path_bwd_col_kernel")) return rc;
+  hipLaunchKernelGGL(lucid::path_products_bwd_kernel, dim3(NS, BHq), dim3(256), 0, st, HQ, H, T, ws, bw);
+  if (int rc = phip("path_products_bwd_kernel")) return rc;
+  hipLaunchKernelGGL(lucid::path_wy_bwd_kernel, dim3(NT, BHq), dim3(256), 0, st, (const bf16*)q, PS(q_strides),
+                     (const bf16*)k, PS(k_strides), (const bf16*)w, PS(w_strides), (const bf16*)beta,
+                     PS(beta_strides), HQ, H, T, ws, bw);
+  if (int rc = phip("path_wy_bwd_kernel")) return rc;
+  hipLaunchKernelGGL(lucid::path_reduce_kernel, dim3((T + 3) / 4, BH), dim3(256), 0, st, HQ, H, T, bw, (bf16*)dq,
+                     PS(dq_strides), (bf16*)dk, PS(dk_strides), (bf16*)dv, PS(dv_strides), (bf16*)dw,
+                     PS(dw_strides), (bf16*)dbeta, PS(dbeta_strides));
+  return phip("path_reduce_kernel");
 }
 
 }  // extern "C"

@@ -75,7 +75,27 @@ class ParallelLUCIDPathAttentionFunction(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, do, dk_cache):
-        raise NotImplementedError("LUCID-Path backward kernels are not built yet")
+        # the k_cache output carries no gradient (parallel.py:78-81 ignores dk_new)
+        q, k, v, w, beta, o, ws = ctx.saved_tensors
+        t, tp = ctx.t, q.shape[1]
+        if do.dtype != torch.bfloat16:
+            do = do.to(torch.bfloat16)
+        do = _ready(_pad_t(do, tp))
+        lib = _lib.load(_LIB)
+        B, T, HQ, K = q.shape
+        H = k.shape[2]
+        dq, dk, dv, dw = (torch.empty_like(x) for x in (q, k, v, w))
+        db = torch.empty(B, T, H, dtype=torch.bfloat16, device=q.device)
+        bws = torch.empty(lib.lucid_path_bwd_workspace_bytes(B, T, H, HQ, K), dtype=torch.uint8, device=q.device)
+        st3 = lambda x: _lib.strides3(x, (0, 2, 1))  # noqa: E731
+        bst = lambda x: (ctypes.c_int64 * 3)(x.stride(0), x.stride(2), x.stride(1))  # noqa: E731
+        rc = lib.lucid_path_bwd(
+            _lib.ptr(do), st3(do), _lib.ptr(q), st3(q), _lib.ptr(k), st3(k), _lib.ptr(w), st3(w),
+            _lib.ptr(beta), bst(beta), _lib.ptr(o), st3(o), _lib.ptr(ws),
+            _lib.ptr(dq), st3(dq), _lib.ptr(dk), st3(dk), _lib.ptr(dv), st3(dv), _lib.ptr(dw), st3(dw),
+            _lib.ptr(db), bst(db), _lib.ptr(bws), B, T, H, HQ, K, float(ctx.scale), _lib.stream_handle(q.device))
+        _lib.check(lib, rc, "lucid_path_bwd")
+        return (dq[:, :t], dk[:, :t], dv[:, :t], dw[:, :t], db[:, :t], None, None, None, None)
 
 
 @torch.compiler.disable

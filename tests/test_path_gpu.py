@@ -81,3 +81,22 @@ def test_path_full_size_residual():
         lrow = torch.exp(row * s - 1 / s)
         res = of[i] + lrow @ of[:i] - vc[0, i, 0].float()
         assert res.abs().max().item() <= 5 * TOL, f"row {i}: residual {res.abs().max().item():.3e}"
+
+
+@pytest.mark.parametrize("B,T,H,G", [(1, 256, 2, 1), (1, 1024, 1, 2), (2, 640, 1, 1), (1, 200, 1, 1)])
+def test_path_backward_matches_oracle(B, T, H, G):
+    from lucid_amd.lucid_path import parallel_lucid_path_attention
+    q, k, v, w, beta, do = _inputs(B, T, H, G, seed=3 * T + G)
+    print(f"case path bwd B={B} T={T} H={H} G={G}", flush=True)
+    leaves = [x.cuda().requires_grad_() for x in (q, k, v, w, beta)]
+    o, _ = parallel_lucid_path_attention(leaves[1], leaves[2], leaves[3], leaves[4], q=leaves[0])
+    o.backward(do.cuda())
+    torch.cuda.synchronize()
+    Tp = (T + 63) // 64 * 64
+    pad = lambda x: torch.nn.functional.pad(_f64(x), [0, 0] * (x.dim() - 2) + [0, Tp - T])  # noqa: E731
+    ref = P.path_attention_grads(*(pad(x) for x in (q, k, v, w, beta)), pad(do), scale=64 ** -0.5, C=64)
+    for name, got, r in zip(("dq", "dk", "dv", "dw", "dbeta"), leaves, ref):
+        r = r[:, :T]
+        err = (got.grad.cpu().double() - r).abs().max().item()
+        bound = TOL * max(1.0, r.abs().max().item())
+        assert err <= bound, f"{name}: max err {err:.3e} > {bound:.3e}"
