@@ -85,16 +85,51 @@ def cpu_baseline(T_sample=16384, T_full=32768, H_full=16, D=64):
     }
 
 
+def _bench_inputs(B, Hq, Hkv, T, D, dev, grad=True):
+    import torch
+    g = torch.Generator().manual_seed(0)
+    mk = lambda *shape: (torch.randn(*shape, generator=g) / D ** 0.5).to(torch.bfloat16).to(dev)  # noqa: E731
+    q, k, v = mk(B, Hq, T, D), mk(B, Hkv, T, D), mk(B, Hkv, T, D)
+    if grad:
+        for x in (q, k, v):
+            x.requires_grad_()
+    do = torch.randn(B, T, Hq, D, generator=g).to(torch.bfloat16).to(dev)
+    return q, k, v, do
+
+
+def _path_inputs(B, H, T, D, dev):
+    import torch
+    g = torch.Generator().manual_seed(0)
+    q, k, v = (torch.randn(B, T, H, D, generator=g) for _ in range(3))
+    w = torch.randn(B, T, H, D, generator=g)
+    w = w / w.norm(dim=-1, keepdim=True)
+    beta = 2 * torch.sigmoid(torch.randn(B, T, H, generator=g))
+    do = torch.randn(B, T, H, D, generator=g)
+    xs = [x.to(torch.bfloat16).to(dev) for x in (q, k, v, w, beta, do)]
+    for x in xs[:5]:
+        x.requires_grad_()
+    return xs
+
+
+# LUCID-Path kernel FLOPs of this implementation's algorithm (per query head, in T^2 d,
+# causal halves): the two-level transport makes every inter-chunk logit block one GEMM.
+PATH_KERNEL_FLOPS = {
+    "path_solve_fwd_kernel": 2.0,  # A = Q K^T, L O
+    "path_dv_kernel": 2.0,         # A, L^T dV
+    "path_bwd_row_kernel": 3.0,    # A, dV O^T, dA K
+    "path_bwd_col_kernel": 3.0,    # A, dV O^T, dA^T Q
+}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--B", type=int, default=1)
-    ap.add_argument("--H", type=int, default=16)
-    ap.add_argument("--Hkv", type=int, default=None)
-    ap.add_argument("--T", type=int, default=32768)
-    ap.add_argument("--D", type=int, default=64)
+    ap.add_argument("--workload", default="lucid", choices=["lucid", "c2", "c5", "path"],
+                    help="lucid: north star B1 H16 T32768 d64 fwd+bwd (default); c2: B4 H16 T4096 d64 "
+                         "fwd+bwd; c5: B1 T131072 Hq32/Hkv8 d128 forward only; path: LUCID-Path "
+                         "B1 H16 T32768 d64 fwd+bwd")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-causal", action="store_true")
     args = ap.parse_args()
@@ -109,49 +144,75 @@ def main():
 
     from lucid_amd import _lib, lucid_attention
 
-    B, Hq, T, D = args.B, args.H, args.T, args.D
-    Hkv = args.Hkv or Hq
     dev = torch.device("cuda:0")
-    g = torch.Generator().manual_seed(0)
-    q = (torch.randn(B, Hq, T, D, generator=g) / D ** 0.5).to(torch.bfloat16).to(dev).requires_grad_()
-    k = (torch.randn(B, Hkv, T, D, generator=g) / D ** 0.5).to(torch.bfloat16).to(dev).requires_grad_()
-    v = (torch.randn(B, Hkv, T, D, generator=g) / D ** 0.5).to(torch.bfloat16).to(dev).requires_grad_()
-    do = torch.randn(B, T, Hq, D, generator=g).to(torch.bfloat16).to(dev)
+    wl = args.workload
+    fwd_only = wl == "c5"
+    if wl == "path":
+        from lucid_amd.lucid_path import parallel_lucid_path_attention
+        B, Hq, Hkv, T, D = 1, 16, 16, 32768, 64
+        q, k, v, w, beta, do = _path_inputs(B, Hq, T, D, dev)
+        lib, prefix = _lib.load("liblucid_path.so"), "lucid_path_"
 
-    def step():
-        q.grad = k.grad = v.grad = None
-        o = lucid_attention(q, k, v)
-        o.backward(do)
+        def step():
+            for x in (q, k, v, w, beta):
+                x.grad = None
+            o, _ = parallel_lucid_path_attention(k, v, w, beta, q=q)
+            o.backward(do)
+        # count of the reference algorithm (query propagated through every chunk pair):
+        # fwd 4 T^2 d (A, L O, 2x propagation) + bwd 12 T^2 d per query head
+        flops = 16.0 * T * T * D * B * Hq
+        kflops = {n: f * T * T * D * B * Hq for n, f in PATH_KERNEL_FLOPS.items()}
+        metric = "LUCID-Path fwd+bwd tokens/s & TFLOP/s at T=32K bf16 (config 4)"
+    else:
+        B, Hq, Hkv, T, D = {"lucid": (1, 16, 16, 32768, 64), "c2": (4, 16, 16, 4096, 64),
+                            "c5": (1, 32, 8, 131072, 128)}[wl]
+        q, k, v, do = _bench_inputs(B, Hq, Hkv, T, D, dev, grad=not fwd_only)
+        lib, prefix = _lib.load(), "lucid_"
+
+        def step():
+            if fwd_only:
+                with torch.no_grad():
+                    lucid_attention(q, k, v)
+                return
+            q.grad = k.grad = v.grad = None
+            o = lucid_attention(q, k, v)
+            o.backward(do)
+        if fwd_only:
+            flops = 2.0 * T * T * D * B * (Hq + Hkv)
+            kflops = {"lucid_precond_fwd_kernel": KERNEL_FLOPS["lucid_precond_fwd_kernel"](B, Hq, Hkv, T, D),
+                      "lucid_attn_fwd_kernel": KERNEL_FLOPS["lucid_attn_fwd_kernel"](B, Hq, Hkv, T, D)}
+        else:
+            flops = lucid_flops(B, Hq, Hkv, T, D)
+            kflops = {n: f(B, Hq, Hkv, T, D) for n, f in KERNEL_FLOPS.items()}
+        metric = "LUCID attn fwd+bwd tokens/s & TFLOP/s at T=32K bf16; % MFMA peak; vs CPU ref"
+        if wl != "lucid":
+            metric = f"LUCID attention {'forward' if fwd_only else 'fwd+bwd'} tokens/s & TFLOP/s ({wl})"
 
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    lib = _lib.load()
-    lib.lucid_profile_reset()
-    lib.lucid_profile_enable(1)
+    getattr(lib, prefix + "profile_reset")()
+    getattr(lib, prefix + "profile_enable")(1)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
         step()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    lib.lucid_profile_enable(0)
-    totals = _lib.profile_totals(lib)
+    getattr(lib, prefix + "profile_enable")(0)
+    totals = _lib.profile_totals(lib, prefix)
     ms = (t1 - t0) / args.steps * 1e3
     tokens_s = B * T / (ms / 1e3)
-    flops = lucid_flops(B, Hq, Hkv, T, D)
 
     kernels = {}
     for name, (tot, cnt) in sorted(totals.items(), key=lambda kv: -kv[1][0]):
         avg = tot / cnt
-        f = KERNEL_FLOPS.get(name)
-        kf = f(B, Hq, Hkv, T, D) if f else 0.0
+        kf = kflops.get(name, 0.0)
         kernels[name] = {"avg_ms": round(avg, 4), "launches": cnt,
                          "tflops": round(kf / (avg / 1e3) / 1e12, 1) if kf else None}
     dom = max(totals.items(), key=lambda kv: kv[1][0])[0]
     dom_avg = totals[dom][0] / totals[dom][1]
-    dom_flops = KERNEL_FLOPS[dom](B, Hq, Hkv, T, D)
-    achieved = dom_flops / (dom_avg / 1e3) / 1e12
+    achieved = kflops.get(dom, 0.0) / (dom_avg / 1e3) / 1e12
     traffic = None
     tfile = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
     if os.path.exists(tfile):
@@ -159,7 +220,7 @@ def main():
             traffic = json.load(fh).get(dom)
 
     causal = None
-    if not args.no_causal:
+    if not args.no_causal and wl in ("lucid", "c2"):
         import torch.nn.functional as F
         qc, kc, vc = (t.detach().clone().requires_grad_() for t in (q, k, v))
         doc = do.transpose(1, 2)
@@ -181,10 +242,12 @@ def main():
                   "tflops": round(causal_flops(B, Hq, T, D) / (cms / 1e3) / 1e12, 1),
                   "lucid_over_causal": round(ms / cms, 3)}
 
-    cpu = None if args.no_cpu_baseline else cpu_baseline(T_full=T, H_full=B * Hq, D=D)
+    cpu = None
+    if not args.no_cpu_baseline and wl == "lucid":
+        cpu = cpu_baseline(T_full=T, H_full=B * Hq, D=D)
 
     out = {
-        "metric": "LUCID attn fwd+bwd tokens/s & TFLOP/s at T=32K bf16; % MFMA peak; vs CPU ref",
+        "metric": metric,
         "value": round(tokens_s, 1),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -195,9 +258,12 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (seeded N(0,1)/sqrt(d) q,k,v; N(0,1) dO)",
-        "config": {"workload": "lucid_attention_fwd_bwd", "B": B, "Hq": Hq, "Hkv": Hkv, "T": T, "head_dim": D,
-                   "causal": True, "solve_block": 64, "parallelism": "single GPU"},
+        "data": "synthetic (seeded N(0,1)/sqrt(d) q,k,v; N(0,1) dO)" if wl != "path"
+                else "synthetic (seeded N(0,1) q,k,v,w; w L2-normalised; beta=2 sigmoid(N(0,1)); N(0,1) dO)",
+        "config": {"workload": {"lucid": "lucid_attention_fwd_bwd", "c2": "lucid_attention_fwd_bwd",
+                                "c5": "lucid_attention_fwd", "path": "lucid_path_fwd_bwd"}[wl],
+                   "B": B, "Hq": Hq, "Hkv": Hkv, "T": T, "head_dim": D, "causal": True,
+                   "parallelism": "single GPU"},
         "tflops": round(flops / (ms / 1e3) / 1e12, 1),
         "frac_mfma_peak": round(flops / (ms / 1e3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
         "roofline": {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 1), "peak": MFMA_BF16_PEAK_TFLOPS,

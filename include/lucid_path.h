@@ -57,6 +57,13 @@ int lucid_path_bwd(const void* dout, const int64_t* do_strides, const void* q, c
                    const int64_t* dbeta_strides, void* bwd_ws, int B, int T, int H, int HQ, int K, float scale,
                    void* stream);
 
+/* Per-kernel timing with HIP events (no counterpart in the reference; used by
+ * bench.py), same contract as lucid_profile_* in lucid_amd.h. */
+void lucid_path_profile_enable(int on);
+int lucid_path_profile_collect(void);
+int lucid_path_profile_entry(int idx, char* name, int name_len, double* total_ms, long* count);
+void lucid_path_profile_reset(void);
+
 #ifdef __cplusplus
 }
 #endif

@@ -51,20 +51,28 @@ _SIGS = {
         "lucid_path_bwd": ([_vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp,
                             _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp,
                             _int, _int, _int, _int, _int, _flt, _vp], _int),
+        "lucid_path_profile_enable": ([_int], None),
+        "lucid_path_profile_collect": ([], _int),
+        "lucid_path_profile_entry": ([_int, ctypes.c_char_p, _int, ctypes.POINTER(ctypes.c_double),
+                                      ctypes.POINTER(ctypes.c_long)], _int),
+        "lucid_path_profile_reset": ([], None),
     },
 }
 
 
-def profile_totals(lib: ctypes.CDLL) -> dict[str, tuple[float, int]]:
-    """Collect the per-kernel event timings recorded so far: {name: (total_ms, launches)}."""
-    n = lib.lucid_profile_collect()
+def profile_totals(lib: ctypes.CDLL, prefix: str = "lucid_") -> dict[str, tuple[float, int]]:
+    """Collect the per-kernel event timings recorded so far: {name: (total_ms, launches)}.
+
+    ``prefix`` selects the library's profile API ("lucid_" or "lucid_path_")."""
+    n = getattr(lib, prefix + "profile_collect")()
     if n < 0:
-        raise RuntimeError("lucid_profile_collect failed")
+        raise RuntimeError("profile collect failed")
     out = {}
     buf = ctypes.create_string_buffer(128)
+    entry = getattr(lib, prefix + "profile_entry")
     for i in range(n):
         ms, cnt = ctypes.c_double(), ctypes.c_long()
-        if lib.lucid_profile_entry(i, buf, 128, ctypes.byref(ms), ctypes.byref(cnt)) == 0:
+        if entry(i, buf, 128, ctypes.byref(ms), ctypes.byref(cnt)) == 0:
             out[buf.value.decode()] = (ms.value, cnt.value)
     return out
 

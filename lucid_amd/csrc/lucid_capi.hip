@@ -8,6 +8,7 @@
 #include "../../include/lucid_amd.h"
 #include "lucid_bwd.hip"
 #include "lucid_fwd.hip"
+#include "profiling.h"
 
 namespace {
 
@@ -116,46 +117,7 @@ int check_tensor(const char* name, const void* p, const int64_t* s) {
 
 lucid::Strides S(const int64_t* s) { return lucid::Strides{s[0], s[1], s[2]}; }
 
-// ---------------------------------------------------------------------------
-// Optional per-kernel timing with HIP events recorded on the launch stream
-// around every kernel (lucid_profile_enable).  Used by bench.py to time the
-// dominant kernel inside the timed region.
-// ---------------------------------------------------------------------------
-struct ProfRec {
-  const char* name;
-  hipEvent_t a, b;
-};
-bool g_prof = false;
-std::vector<ProfRec> g_recs;
-std::vector<hipEvent_t> g_event_pool;
-std::map<std::string, std::pair<double, long>> g_prof_tot;
-
-hipEvent_t pool_event() {
-  if (!g_event_pool.empty()) {
-    hipEvent_t e = g_event_pool.back();
-    g_event_pool.pop_back();
-    return e;
-  }
-  hipEvent_t e;
-  hipEventCreate(&e);
-  return e;
-}
-
-#define LUCID_LAUNCH(NAME, KERNEL, GRID, ST, ...)                          \
-  do {                                                                     \
-    hipEvent_t ev_a = nullptr, ev_b = nullptr;                             \
-    if (g_prof) {                                                          \
-      ev_a = pool_event();                                                 \
-      ev_b = pool_event();                                                 \
-      hipEventRecord(ev_a, ST);                                            \
-    }                                                                      \
-    hipLaunchKernelGGL(KERNEL, GRID, dim3(256), 0, ST, __VA_ARGS__);       \
-    if (int rc_ = hip_status(NAME)) return rc_;                            \
-    if (g_prof) {                                                          \
-      hipEventRecord(ev_b, ST);                                            \
-      g_recs.push_back(ProfRec{NAME, ev_a, ev_b});                         \
-    }                                                                      \
-  } while (0)
+#define LUCID_LAUNCH(NAME, KERNEL, GRID, ST, ...) LUCID_TIMED_LAUNCH(hip_status, NAME, KERNEL, GRID, ST, __VA_ARGS__)
 
 template <int D>
 int launch_precond_fwd(const void* k, const int64_t* ks, const void* v, const int64_t* vs, float* vprime,
@@ -280,40 +242,14 @@ int lucid_attn_bwd(const void* dout, const int64_t* do_strides, const void* q, c
                          dk_strides, dv, dv_strides, w, B, Hq, Hkv, T, scale, st);
 }
 
-void lucid_profile_enable(int on) { g_prof = on != 0; }
+void lucid_profile_enable(int on) { lucid_prof::enabled() = on != 0; }
 
-int lucid_profile_collect(void) {
-  for (auto& r : g_recs) {
-    if (hipEventSynchronize(r.b) != hipSuccess) return LUCID_EHIP;
-    float ms = 0.f;
-    hipEventElapsedTime(&ms, r.a, r.b);
-    auto& t = g_prof_tot[r.name];
-    t.first += ms;
-    t.second += 1;
-    g_event_pool.push_back(r.a);
-    g_event_pool.push_back(r.b);
-  }
-  g_recs.clear();
-  return (int)g_prof_tot.size();
-}
+int lucid_profile_collect(void) { return lucid_prof::collect(); }
 
 int lucid_profile_entry(int idx, char* name, int name_len, double* total_ms, long* count) {
-  int i = 0;
-  for (auto& kv : g_prof_tot) {
-    if (i++ != idx) continue;
-    if (name && name_len > 0) {
-      snprintf(name, (size_t)name_len, "%s", kv.first.c_str());
-    }
-    if (total_ms) *total_ms = kv.second.first;
-    if (count) *count = kv.second.second;
-    return LUCID_OK;
-  }
-  return LUCID_EINVAL;
+  return lucid_prof::entry(idx, name, name_len, total_ms, count);
 }
 
-void lucid_profile_reset(void) {
-  lucid_profile_collect();
-  g_prof_tot.clear();
-}
+void lucid_profile_reset(void) { lucid_prof::reset(); }
 
 }  // extern "C"

@@ -4,6 +4,7 @@
 #include "../../include/lucid_path.h"
 #include "path_fwd.hip"
 #include "path_bwd.hip"
+#include "profiling.h"
 
 namespace {
 
@@ -140,21 +141,16 @@ int lucid_path_fwd(const void* q, const int64_t* q_strides, const void* k, const
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int NT = T / 64, NS = (NT + 7) / 8;
   const int BH = B * H, BHq = B * HQ;
-  hipLaunchKernelGGL(lucid::path_chunk_kernel, dim3(NT, BHq), dim3(256), 0, st, (const bf16*)q, PS(q_strides),
+  LUCID_TIMED_LAUNCH(phip, "path_chunk_kernel", lucid::path_chunk_kernel, dim3(NT, BHq), st, (const bf16*)q, PS(q_strides),
                      (const bf16*)k, PS(k_strides), (const bf16*)w, PS(w_strides), (const bf16*)beta,
                      PS(beta_strides), HQ, H, T, scale, ws);
-  if (int rc = phip("path_chunk_kernel")) return rc;
-  hipLaunchKernelGGL(lucid::path_large_kernel, dim3(NS, BH), dim3(256), 0, st, T, ws);
-  if (int rc = phip("path_large_kernel")) return rc;
-  hipLaunchKernelGGL(lucid::path_transport_kernel, dim3(NT, BHq), dim3(256), 0, st, HQ, H, T, ws);
-  if (int rc = phip("path_transport_kernel")) return rc;
-  hipLaunchKernelGGL(lucid::path_solve_fwd_kernel, dim3(NT * BHq), dim3(256), 0, st, (const bf16*)v,
+  LUCID_TIMED_LAUNCH(phip, "path_large_kernel", lucid::path_large_kernel, dim3(NS, BH), st, T, ws);
+  LUCID_TIMED_LAUNCH(phip, "path_transport_kernel", lucid::path_transport_kernel, dim3(NT, BHq), st, HQ, H, T, ws);
+  LUCID_TIMED_LAUNCH(phip, "path_solve_fwd_kernel", lucid::path_solve_fwd_kernel, dim3(NT * BHq), st, (const bf16*)v,
                      PS(v_strides), (bf16*)o, PS(o_strides), HQ, H, T, BHq, scale, ws);
-  if (int rc = phip("path_solve_fwd_kernel")) return rc;
   if (kcache) {
-    hipLaunchKernelGGL(lucid::path_kcache_kernel, dim3(NT, BH), dim3(256), 0, st, T, (bf16*)kcache,
+    LUCID_TIMED_LAUNCH(phip, "path_kcache_kernel", lucid::path_kcache_kernel, dim3(NT, BH), st, T, (bf16*)kcache,
                        PS(kcache_strides), H, ws);
-    if (int rc = phip("path_kcache_kernel")) return rc;
   }
   return 0;
 }
@@ -197,27 +193,31 @@ int lucid_path_bwd(const void* dout, const int64_t* do_strides, const void* q, c
   const int NT = T / 64, NS = (NT + 7) / 8;
   const int BH = B * H, BHq = B * HQ;
   const int64_t n_hl = (int64_t)BHq * NS * 4096, n_hc = (int64_t)BHq * NT * 4096;
-  hipLaunchKernelGGL(lucid::path_bwd_zero_kernel, dim3(1024), dim3(256), 0, st, n_hl, n_hc, BHq, bw);
-  if (int rc = phip("path_bwd_zero_kernel")) return rc;
-  hipLaunchKernelGGL(lucid::path_dv_kernel, dim3(NT * BHq), dim3(256), 0, st, (const bf16*)dout, PS(do_strides),
+  LUCID_TIMED_LAUNCH(phip, "path_bwd_zero_kernel", lucid::path_bwd_zero_kernel, dim3(1024), st, n_hl, n_hc, BHq, bw);
+  LUCID_TIMED_LAUNCH(phip, "path_dv_kernel", lucid::path_dv_kernel, dim3(NT * BHq), st, (const bf16*)dout, PS(do_strides),
                      (const bf16*)o, PS(o_strides), HQ, H, T, BHq, scale, ws, bw);
-  if (int rc = phip("path_dv_kernel")) return rc;
-  hipLaunchKernelGGL(lucid::path_bwd_row_kernel, dim3(NT, BHq), dim3(256), 0, st, (const bf16*)o, PS(o_strides),
+  LUCID_TIMED_LAUNCH(phip, "path_bwd_row_kernel", lucid::path_bwd_row_kernel, dim3(NT, BHq), st, (const bf16*)o, PS(o_strides),
                      HQ, H, T, scale, ws, bw);
-  if (int rc = phip("path_bwd_row_kernel")) return rc;
-  hipLaunchKernelGGL(lucid::path_bwd_col_kernel, dim3(NT, BHq), dim3(256), 0, st, (const bf16*)o, PS(o_strides),
+  LUCID_TIMED_LAUNCH(phip, "path_bwd_col_kernel", lucid::path_bwd_col_kernel, dim3(NT, BHq), st, (const bf16*)o, PS(o_strides),
                      HQ, H, T, scale, ws, bw);
-  if (int rc = phip("path_bwd_col_kernel")) return rc;
-  hipLaunchKernelGGL(lucid::path_products_bwd_kernel, dim3(NS, BHq), dim3(256), 0, st, HQ, H, T, ws, bw);
-  if (int rc = phip("path_products_bwd_kernel")) return rc;
-  hipLaunchKernelGGL(lucid::path_wy_bwd_kernel, dim3(NT, BHq), dim3(256), 0, st, (const bf16*)q, PS(q_strides),
+  LUCID_TIMED_LAUNCH(phip, "path_products_bwd_kernel", lucid::path_products_bwd_kernel, dim3(NS, BHq), st, HQ, H, T, ws, bw);
+  LUCID_TIMED_LAUNCH(phip, "path_wy_bwd_kernel", lucid::path_wy_bwd_kernel, dim3(NT, BHq), st, (const bf16*)q, PS(q_strides),
                      (const bf16*)k, PS(k_strides), (const bf16*)w, PS(w_strides), (const bf16*)beta,
                      PS(beta_strides), HQ, H, T, ws, bw);
-  if (int rc = phip("path_wy_bwd_kernel")) return rc;
-  hipLaunchKernelGGL(lucid::path_reduce_kernel, dim3((T + 3) / 4, BH), dim3(256), 0, st, HQ, H, T, bw, (bf16*)dq,
-                     PS(dq_strides), (bf16*)dk, PS(dk_strides), (bf16*)dv, PS(dv_strides), (bf16*)dw,
+  LUCID_TIMED_LAUNCH(phip, "path_reduce_kernel", lucid::path_reduce_kernel, dim3((T + 3) / 4, BH), st, HQ, H, T, bw,
+                     (bf16*)dq, PS(dq_strides), (bf16*)dk, PS(dk_strides), (bf16*)dv, PS(dv_strides), (bf16*)dw,
                      PS(dw_strides), (bf16*)dbeta, PS(dbeta_strides));
-  return phip("path_reduce_kernel");
+  return 0;
 }
+
+void lucid_path_profile_enable(int on) { lucid_prof::enabled() = on != 0; }
+
+int lucid_path_profile_collect(void) { return lucid_prof::collect(); }
+
+int lucid_path_profile_entry(int idx, char* name, int name_len, double* total_ms, long* count) {
+  return lucid_prof::entry(idx, name, name_len, total_ms, count);
+}
+
+void lucid_path_profile_reset(void) { lucid_prof::reset(); }
 
 }  // extern "C"
