@@ -131,4 +131,38 @@ __device__ __forceinline__ void lds_rows16(const float* p, int g, float out[16])
   }
 }
 
+// Generalised staging: a [ROWS][D] row tile and a [D][SLOTS] T-perm tile.
+template <int D, int ROWS>
+__device__ __forceinline__ void g2r_rows_n(const bf16* __restrict__ src, int64_t st, int j0, bf16x8* stg) {
+#pragma unroll
+  for (int u = 0; u < ROWS * D / 2048; ++u) {
+    const int c = threadIdx.x + 256 * u;
+    stg[u] = ld8(src + (int64_t)(j0 + c / (D / 8)) * st + (c % (D / 8)) * 8);
+  }
+}
+template <int D, int ROWS>
+__device__ __forceinline__ void r2l_rows_n(bf16 (*dst)[D + 8], const bf16x8* stg) {
+#pragma unroll
+  for (int u = 0; u < ROWS * D / 2048; ++u) {
+    const int c = threadIdx.x + 256 * u;
+    *reinterpret_cast<bf16x8*>(&dst[c / (D / 8)][(c % (D / 8)) * 8]) = stg[u];
+  }
+}
+template <int D, int SLOTS>
+__device__ __forceinline__ void g2r_tp_n(const bf16* __restrict__ src, int T, int j0, bf16x8* stg) {
+#pragma unroll
+  for (int u = 0; u < D * SLOTS / 2048; ++u) {
+    const int c = threadIdx.x + 256 * u;
+    stg[u] = ld8(src + (int64_t)(c / (SLOTS / 8)) * T + j0 + (c % (SLOTS / 8)) * 8);
+  }
+}
+template <int D, int SLOTS>
+__device__ __forceinline__ void r2l_tp_n(bf16 (*dst)[SLOTS + 8], const bf16x8* stg) {
+#pragma unroll
+  for (int u = 0; u < D * SLOTS / 2048; ++u) {
+    const int c = threadIdx.x + 256 * u;
+    *reinterpret_cast<bf16x8*>(&dst[c / (SLOTS / 8)][(c % (SLOTS / 8)) * 8]) = stg[u];
+  }
+}
+
 }  // namespace lucid

@@ -41,8 +41,8 @@ inline hipEvent_t pool_event() {
     p.pop_back();
     return e;
   }
-  hipEvent_t e;
-  hipEventCreate(&e);
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
   return e;
 }
 
@@ -51,7 +51,7 @@ inline int collect() {
   for (auto& r : records()) {
     if (hipEventSynchronize(r.b) != hipSuccess) return -1;
     float ms = 0.f;
-    hipEventElapsedTime(&ms, r.a, r.b);
+    if (hipEventElapsedTime(&ms, r.a, r.b) != hipSuccess) return -1;
     auto& t = totals()[r.name];
     t.first += ms;
     t.second += 1;
@@ -89,12 +89,11 @@ inline void reset() {
     if (lucid_prof::enabled()) {                                           \
       ev_a = lucid_prof::pool_event();                                     \
       ev_b = lucid_prof::pool_event();                                     \
-      hipEventRecord(ev_a, ST);                                            \
+      if (!ev_a || !ev_b || hipEventRecord(ev_a, ST) != hipSuccess)        \
+        ev_a = nullptr;                                                    \
     }                                                                      \
     hipLaunchKernelGGL(KERNEL, GRID, dim3(256), 0, ST, __VA_ARGS__);       \
     if (int rc_ = STATUS_FN(NAME)) return rc_;                             \
-    if (lucid_prof::enabled()) {                                           \
-      hipEventRecord(ev_b, ST);                                            \
+    if (ev_a && hipEventRecord(ev_b, ST) == hipSuccess)                    \
       lucid_prof::records().push_back(lucid_prof::Rec{NAME, ev_a, ev_b});  \
-    }                                                                      \
   } while (0)
