@@ -274,7 +274,7 @@ struct DqSmem {
 };
 
 template <int D>
-__global__ __launch_bounds__(256) void lucid_attn_bwd_dq_kernel(
+__global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_bwd_dq_kernel(
     const bf16* __restrict__ q, Strides qs, const bf16* __restrict__ k, Strides ks, const bf16* __restrict__ vpb,
     const bf16* __restrict__ dout, Strides dos, const bf16* __restrict__ kt, const float* __restrict__ lse,
     const float* __restrict__ delta, bf16* __restrict__ dq, Strides dqs, int Hq, int Hkv, int T, int BHq,
@@ -787,7 +787,7 @@ struct ProwSmem {
 };
 
 template <int D>
-__global__ __launch_bounds__(256) void lucid_precond_bwd_row_kernel(
+__global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond_bwd_row_kernel(
     const bf16* __restrict__ k, Strides ks, int Hkv, int T, int BH, const float* __restrict__ rinv, float scale,
     const bf16* __restrict__ kt, const bf16* __restrict__ vpb, const bf16* __restrict__ dvb,
     const float* __restrict__ colsum, const float* __restrict__ dka, bf16* __restrict__ dk_out, Strides dks) {
@@ -852,7 +852,6 @@ __global__ __launch_bounds__(256) void lucid_precond_bwd_row_kernel(
   for (int J = 0; J < ntile; ++J) {
     const int buf = J & 1;
     const bool more = J + 1 < ntile;
-    if (more) gload(J + 1);
     if (J <= last_w) {
       const bool diag = (J == last_w);
       bf16x8 ka[NKS], va[NKS];
@@ -892,7 +891,10 @@ __global__ __launch_bounds__(256) void lucid_precond_bwd_row_kernel(
         }
       }
     }
-    if (more) lstore(buf ^ 1);
+    if (more) {
+      gload(J + 1);
+      lstore(buf ^ 1);
+    }
     __syncthreads();
   }
   float(*Rt)[132] = sm.u.Rt;

@@ -370,7 +370,7 @@ __global__ __launch_bounds__(256) void lucid_precond_fwd_kernel(
 // P = exp2(s*log2e*S - lse2)).
 // ---------------------------------------------------------------------------
 template <int D>
-__global__ __launch_bounds__(256) void lucid_attn_fwd_kernel(const bf16* __restrict__ q, Strides qs,
+__global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_fwd_kernel(const bf16* __restrict__ q, Strides qs,
                                                              const bf16* __restrict__ k, Strides ks,
                                                              const bf16* __restrict__ vpt, bf16* __restrict__ o,
                                                              Strides os, float* __restrict__ lse, int Hq, int Hkv,

@@ -26,6 +26,11 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 #define LOG2E_F 1.4426950408889634f
 
+// Two waves per SIMD: caps a kernel at 256 VGPR+AGPR per lane so that the MFMA
+// work of one wave overlaps the exp/VALU work of the other (one wave per SIMD
+// leaves the matrix core idle while its own softmax-style VALU code runs).
+#define LUCID_TWO_WAVES_IF(COND) __attribute__((amdgpu_waves_per_eu((COND) ? 2 : 1)))
+
 __device__ __forceinline__ f32x16 mfma32(const bf16x8& a, const bf16x8& b, const f32x16& c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
