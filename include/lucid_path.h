@@ -27,7 +27,8 @@ int lucid_path_abi_version(void);
 /* Text of the last error on the calling thread. */
 const char* lucid_path_last_error(void);
 
-/* Bytes of the forward workspace (kept alive for lucid_path_bwd). */
+/* Bytes of the forward workspace (kept alive for lucid_path_bwd).  Both
+ * workspaces must be 256-byte aligned. */
 size_t lucid_path_fwd_workspace_bytes(int B, int T, int H, int HQ, int K);
 
 /* Forward: o = (I + L)^-1 v; if kcache is non-null also the decode key cache

@@ -520,7 +520,7 @@ __global__ __launch_bounds__(256) void lucid_precond_bwd_col_kernel(
       if (need >= ready) {
         const int seen = poll_counter(cnt);
         if (seen > need) {
-          acquire_agent();
+          chain_acquire();
           ready = seen;
         }
       }

@@ -106,6 +106,12 @@ int check_dims(int B, int Hq, int Hkv, int T, int D) {
   return LUCID_OK;
 }
 
+// Workspaces hold the chain operands; their 64-row blocks must fill whole cache lines.
+int check_ws(const char* name, const void* p) {
+  if (reinterpret_cast<uintptr_t>(p) % 256) return fail(std::string(name) + " must be 256-byte aligned");
+  return LUCID_OK;
+}
+
 int check_tensor(const char* name, const void* p, const int64_t* s) {
   if (!p) return fail(std::string(name) + " is null");
   if (!s) return fail(std::string(name) + " strides are null");
@@ -124,7 +130,7 @@ int launch_precond_fwd(const void* k, const int64_t* ks, const void* v, const in
                        const FwdWs& w, int B, int Hkv, int T, float scale, float eps, hipStream_t st) {
   const int BH = B * Hkv;
   LUCID_LAUNCH("lucid_prep_kernel", lucid::lucid_prep_kernel<D>, dim3(T / 64, BH), st, (const bf16*)k, S(ks), Hkv,
-               T, eps, w.rinv, w.kt, w.counters);
+               T, eps, scale, w.rinv, w.kt, w.pinv, w.counters);
   LUCID_LAUNCH("lucid_precond_fwd_kernel", lucid::lucid_precond_fwd_kernel<D>, dim3((T / 128) * BH), st,
                (const bf16*)k, S(ks), (const bf16*)v, S(vs), Hkv, T, BH, w.rinv, scale, vprime, w.vpb, w.vpt,
                w.pinv, w.counters);
@@ -190,6 +196,7 @@ int lucid_get_v_prime(const void* k, const int64_t* k_strides, const void* v, co
   if (int rc = check_tensor("k", k, k_strides)) return rc;
   if (int rc = check_tensor("v", v, v_strides)) return rc;
   if (!vprime || !fwd_ws) return fail("vprime and fwd_ws must be non-null");
+  if (int rc = check_ws("fwd_ws", fwd_ws)) return rc;
   const FwdWs w = carve_fwd(fwd_ws, B, Hkv, T, D);
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (D == 64) return launch_precond_fwd<64>(k, k_strides, v, v_strides, vprime, w, B, Hkv, T, scale, eps, st);
@@ -207,6 +214,7 @@ int lucid_attn_fwd(const void* q, const int64_t* q_strides, const void* k, const
   if (int rc = check_tensor("v", v, v_strides)) return rc;
   if (int rc = check_tensor("o", o, o_strides)) return rc;
   if (!vprime || !lse || !fwd_ws) return fail("vprime, lse and fwd_ws must be non-null");
+  if (int rc = check_ws("fwd_ws", fwd_ws)) return rc;
   const FwdWs w = carve_fwd(fwd_ws, B, Hkv, T, D);
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (D == 64)
@@ -232,6 +240,8 @@ int lucid_attn_bwd(const void* dout, const int64_t* do_strides, const void* q, c
   if (int rc = check_tensor("dk", dk, dk_strides)) return rc;
   if (int rc = check_tensor("dv", dv, dv_strides)) return rc;
   if (!lse || !fwd_ws || !bwd_ws) return fail("lse, fwd_ws and bwd_ws must be non-null");
+  if (int rc = check_ws("fwd_ws", fwd_ws)) return rc;
+  if (int rc = check_ws("bwd_ws", bwd_ws)) return rc;
   const FwdWs f = carve_fwd(const_cast<void*>(fwd_ws), B, Hkv, T, D);
   const BwdWs w = carve_bwd(bwd_ws, B, Hq, Hkv, T, D);
   hipStream_t st = static_cast<hipStream_t>(stream);

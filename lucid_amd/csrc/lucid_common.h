@@ -60,11 +60,18 @@ __device__ __forceinline__ void vpth_w(bf16* base, int bh, int D, int T, int d, 
 }
 
 // Make this workgroup's global writes visible at agent scope, then advance the
-// head's chain counter to val (release).  Every thread must call it.
+// head's chain counter to val.  Every wave first waits until its own stores
+// have reached the L2 (s_waitcnt 0), the barrier orders that before wave 0,
+// whose agent-scope release writes the XCD's L2 back once for the whole
+// workgroup before the counter store.  Every thread must call it.
 __device__ __forceinline__ void publish_counter(int* cnt, int val) {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (threadIdx.x == 0) __hip_atomic_store(cnt, val, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x < 64) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __builtin_amdgcn_s_waitcnt(0);  // the write-back has completed
+    if (threadIdx.x == 0) __hip_atomic_store(cnt, val, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 // 16 consecutive-in-D-layout fp32 values of a per-row vector: rows drow(e, g) + base

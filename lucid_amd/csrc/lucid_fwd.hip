@@ -6,27 +6,35 @@
 //   O   = softmax(s Q K^T, causal) V'                     (:520-530)
 //
 // Kernels (all 256 threads = 4 waves, MFMA 32x32x16 bf16, fp32 accumulate):
-//   lucid_prep_kernel        per-row 1/rms of K, K^T in T-perm layout, zero chain counters
+//   lucid_prep_kernel        per-row 1/rms of K, K^T in T-perm layout, inverses of the 64x64
+//                            diagonal blocks of P, zero chain counters
 //   lucid_precond_fwd_kernel chained solve, one workgroup per (128-row block, kv head);
-//                            it waits on a per-head progress counter for V'_j, j < i
+//                            it waits on a per-head progress counter for V'_j, j < i and
+//                            sweeps the earlier keys 128 at a time
 //   lucid_attn_fwd_kernel    causal online-softmax attention on V' (256 query rows / WG, LDS tiles)
 #include "lucid_common.h"
 
 namespace lucid {
 
 // ---------------------------------------------------------------------------
-// prep: rinv[bh][t] = 1/sqrt(mean K^2 + eps); kt[bh][d][perm(t)] = K[t][d]
-// grid (T/64, B*Hkv)
+// prep: rinv[bh][t] = 1/sqrt(mean K^2 + eps); kt[bh][d][perm(t)] = K[t][d];
+// pinv[bh][blk] = inverse of the 64x64 diagonal block of P (fp32 forward
+// substitution by wave 0); zero the chain counter.  grid (T/64, B*Hkv)
 // ---------------------------------------------------------------------------
 template <int D>
 __global__ __launch_bounds__(256) void lucid_prep_kernel(const bf16* __restrict__ k, Strides ks, int Hkv, int T,
-                                                         float eps, float* __restrict__ rinv,
-                                                         bf16* __restrict__ kt, int* __restrict__ counters) {
+                                                         float eps, float scale, float* __restrict__ rinv,
+                                                         bf16* __restrict__ kt, float* __restrict__ pinv,
+                                                         int* __restrict__ counters) {
   constexpr int SEG = D / 4;
+  constexpr int NKS = D / 16;
   __shared__ bf16 tile[D][64 + 8];
+  __shared__ float rr[64];
+  __shared__ __attribute__((aligned(16))) float Pd[64][68];
   const int blk = blockIdx.x, bh = blockIdx.y;
   const int b = bh / Hkv, h = bh - b * Hkv;
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int g = lane >> 5, l32 = lane & 31;
   const bf16* kp = k + b * ks.b + h * ks.h + (int64_t)blk * 64 * ks.t;
   const int row = tid >> 2, seg = tid & 3;
   float ss = 0.f;
@@ -42,7 +50,11 @@ __global__ __launch_bounds__(256) void lucid_prep_kernel(const bf16* __restrict_
   }
   ss += __shfl_xor(ss, 1, 64);
   ss += __shfl_xor(ss, 2, 64);
-  if (seg == 0) rinv[(int64_t)bh * T + blk * 64 + row] = 1.0f / sqrtf(ss / (float)D + eps);
+  if (seg == 0) {
+    const float ri = 1.0f / sqrtf(ss / (float)D + eps);
+    rinv[(int64_t)bh * T + blk * 64 + row] = ri;
+    rr[row] = ri;
+  }
   if (blk == 0 && tid == 0) counters[bh] = 0;
   __syncthreads();
   // T-perm rows: kt[bh][d][blk*64 + slot], slot kappa holds t = jmap(kappa)
@@ -53,6 +65,28 @@ __global__ __launch_bounds__(256) void lucid_prep_kernel(const bf16* __restrict_
     for (int e = 0; e < 8; ++e) out[e] = tile[dd][(c8 >> 1) * 16 + jmap((c8 & 1) * 8 + e)];
     *reinterpret_cast<bf16x8*>(kt + ((int64_t)bh * D + dd) * T + blk * 64 + c8 * 8) = out;
   }
+  // diagonal block P[m][n] = exp(s r_m r_n K_m.K_n - 1/s) (n <= m); wave -> 32x32 quadrant
+  {
+    const float sl2 = scale * LOG2E_F;
+    const float c0 = LOG2E_F / scale;
+    const int mh = w >> 1, nh = w & 1;
+    f32x16 sd = zero16();
+    if (nh <= mh) {
+#pragma unroll
+      for (int st = 0; st < NKS; ++st)
+        sd = mfma32(ld8(kp + (int64_t)(mh * 32 + l32) * ks.t + 16 * st + 8 * g),
+                    ld8(kp + (int64_t)(nh * 32 + l32) * ks.t + 16 * st + 8 * g), sd);
+    }
+    const int n = nh * 32 + l32;
+    const float an = sl2 * rr[n];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int m = mh * 32 + drow(e, g);
+      Pd[m][n] = (n <= m) ? __builtin_amdgcn_exp2f(fmaf(sd[e] * an, rr[m], -c0)) : 0.f;
+    }
+  }
+  __syncthreads();
+  if (w == 0) invert_lower64(Pd, lane, pinv + ((int64_t)bh * (T / 64) + blk) * 4096);
 }
 
 // ---------------------------------------------------------------------------
@@ -63,39 +97,42 @@ __global__ __launch_bounds__(256) void lucid_prep_kernel(const bf16* __restrict_
 // the blocks of one head share an XCD when BH % 8 == 0.  counters[bh] = number
 // of 64-row blocks of V' already published.
 //
+// The earlier keys are swept in pairs of 64-key tiles (128 keys per barrier):
+// K rows, V'^T (T-perm) and 1/rms of the pair are staged once per workgroup in
+// LDS, double buffered, with coalesced 16-byte loads.
 // wave w: ih = w & 1 -> rows i0 + 64*ih .. +64 (two 32-row n-tiles, lane <-> row)
-//         jh = w >> 1 -> keys 32*jh .. +32 of every staged 64-key tile
-// Every earlier 64-key tile (K rows, V'^T in T-perm layout, 1/rms) is staged
-// once per workgroup in LDS, double buffered, with coalesced 16-byte loads:
+//         kh = w >> 1 -> the 64-key tile 2*pair + kh of every staged pair
 //   acc^T[d][i] += V'^T[d][j] P^T[j][i],  P^T[j][i] = exp(s r_i r_j K_j.K_i - 1/s)
 // Then V'_A = X_A (V_A - acc_A); V'_B = X_B (V_B - acc_B - P_BA V'_A), with
-// X = P_diag^-1 computed in fp32 (waves 0/1) and applied through a 3-term bf16
-// split (hi*hi + hi*lo + lo*hi).
+// X = P_diag^-1 (fp32, computed by lucid_prep_kernel into pinv) applied through
+// a 3-term bf16 split (hi*hi + hi*lo + lo*hi).  At d = 64 two workgroups share a CU (LDS <= 80 KB,
+// <= 256 registers per lane) so that one's MFMA work overlaps the other's exp.
 // ---------------------------------------------------------------------------
 template <int D>
 struct PfwdSmem {
-  float X[2][64][68];  // P_AA, P_BB, then their inverses
   union {
     struct {
-      bf16 k[2][64][D + 8];
-      bf16 v[2][D][64 + 8];
-      float r[2][64];
+      bf16 k[2][128][D + 8];
+      bf16 v[2][D][128 + 8];
+      float r[2][128];
     } st;
     struct {
-      float Rt[D][132];   // R^T for the 128 rows (cols 0..63 = A, 64..127 = B)
-      bf16 vA[D][64 + 8]; // V'_A^T (bf16, T-perm within the block) for the B correction
+      float Rt[D][132];    // R^T for the 128 rows (cols 0..63 = A, 64..127 = B)
+      float X[64][68];     // inverse of the diagonal block being solved
+      bf16 vA[D][64 + 8];  // V'_A^T (bf16, T-perm within the block) for the B correction
     } fin;
   } u;
 };
 
 template <int D>
-__global__ __launch_bounds__(256) void lucid_precond_fwd_kernel(
+__global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond_fwd_kernel(
     const bf16* __restrict__ k, Strides ks, const bf16* __restrict__ v, Strides vs, int Hkv, int T, int BH,
     const float* __restrict__ rinv, float scale, float* __restrict__ vp32, bf16* __restrict__ vpb,
     bf16* __restrict__ vpt, float* __restrict__ pinv, int* __restrict__ counters) {
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
-  constexpr int CH = D / 32;
+  constexpr int SK = 128 * D / 2048;  // 16-byte chunks per thread of a staged 128-key K tile
+  constexpr int SV = D * 128 / 2048;  // ... and of the V'^T tile
   __shared__ __attribute__((aligned(16))) PfwdSmem<D> sm;
 
   const int id = blockIdx.x;
@@ -103,39 +140,17 @@ __global__ __launch_bounds__(256) void lucid_precond_fwd_kernel(
   const int b = bh / Hkv, h = bh - b * Hkv;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
-  const int ih = w & 1, jh = w >> 1;
+  const int ih = w & 1, kh = w >> 1;
   const int i0 = i2 * 128;
   const int NT = T / 64;
-  const bf16* kh = k + b * ks.b + h * ks.h;
+  const bf16* kp = k + b * ks.b + h * ks.h;
   const bf16* vh = v + b * vs.b + h * vs.h;
   const float* rv = rinv + (int64_t)bh * T;
   const bf16* vpth = vpt + (int64_t)bh * D * T;
+  float* pinv_blk = pinv + ((int64_t)bh * NT + 2 * i2) * 4096;
   int* cnt = counters + bh;
   const float sl2 = scale * LOG2E_F;
   const float c0 = LOG2E_F / scale;
-
-  // ---- diagonal blocks P_AA, P_BB: each wave computes one 32x32 tile of each ----
-  {
-    const int mh = w >> 1, nh = w & 1;
-#pragma unroll
-    for (int sb = 0; sb < 2; ++sb) {
-      const int base = i0 + sb * 64;
-      f32x16 sd = zero16();
-#pragma unroll
-      for (int st = 0; st < NKS; ++st)
-        sd = mfma32(ld8(kh + (int64_t)(base + mh * 32 + l32) * ks.t + 16 * st + 8 * g),
-                    ld8(kh + (int64_t)(base + nh * 32 + l32) * ks.t + 16 * st + 8 * g), sd);
-      const int n = nh * 32 + l32;
-      const float an = sl2 * rv[base + n];
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int m = mh * 32 + drow(e, g);
-        sm.X[sb][m][n] = (n <= m) ? __builtin_amdgcn_exp2f(fmaf(sd[e] * an, rv[base + m], -c0)) : 0.f;
-      }
-    }
-  }
-  __syncthreads();
-  if (w < 2) invert_lower64(sm.X[w], lane, pinv + ((int64_t)bh * NT + 2 * i2 + w) * 4096);
 
   bf16x8 kbi[2][NKS];
   float ai[2];
@@ -143,7 +158,7 @@ __global__ __launch_bounds__(256) void lucid_precond_fwd_kernel(
   for (int nt = 0; nt < 2; ++nt) {
     const int row = i0 + ih * 64 + nt * 32 + l32;
 #pragma unroll
-    for (int st = 0; st < NKS; ++st) kbi[nt][st] = ld8(kh + (int64_t)row * ks.t + 16 * st + 8 * g);
+    for (int st = 0; st < NKS; ++st) kbi[nt][st] = ld8(kp + (int64_t)row * ks.t + 16 * st + 8 * g);
     ai[nt] = sl2 * rv[row];
   }
   f32x16 acc[NDT][2];
@@ -153,68 +168,52 @@ __global__ __launch_bounds__(256) void lucid_precond_fwd_kernel(
     acc[t][1] = zero16();
   }
 
-  // ---- off-diagonal sweep over the 2*i2 earlier 64-key tiles ----
-  const int nj = 2 * i2;
+  // ---- off-diagonal sweep over the i2 earlier pairs of 64-key tiles ----
+  // pair pp (keys 128pp .. 128pp+127) is complete once the counter exceeds 2pp+1
+  const int npair = i2;
   int ready = 0;
-  bf16x8 stg[2 * CH];
+  bf16x8 stg[SK + SV];
   f32x4 rstg;
-  auto gload = [&](int j) {
-    const int j0 = j * 64;
-#pragma unroll
-    for (int u = 0; u < CH; ++u) {
-      const int cidx = tid + 256 * u;
-      const int kr = cidx / (D / 8), kc = cidx % (D / 8);
-      stg[u] = ld8(kh + (int64_t)(j0 + kr) * ks.t + kc * 8);
-      const int vr = cidx >> 3, vc = cidx & 7;
-      stg[CH + u] = ld8(vpth + (int64_t)vr * T + j0 + vc * 8);
-    }
-    if (tid < 16) rstg = *reinterpret_cast<const f32x4*>(rv + j0 + 4 * tid);
+  auto gload = [&](int pp) {
+    g2r_rows_n<D, 128>(kp, ks.t, pp * 128, stg);
+    g2r_tp_n<D, 128>(vpth, T, pp * 128, stg + SK);
+    if (tid < 32) rstg = *reinterpret_cast<const f32x4*>(rv + pp * 128 + 4 * tid);
   };
   auto lstore = [&](int buf) {
-#pragma unroll
-    for (int u = 0; u < CH; ++u) {
-      const int cidx = tid + 256 * u;
-      const int kr = cidx / (D / 8), kc = cidx % (D / 8);
-      *reinterpret_cast<bf16x8*>(&sm.u.st.k[buf][kr][kc * 8]) = stg[u];
-      const int vr = cidx >> 3, vc = cidx & 7;
-      *reinterpret_cast<bf16x8*>(&sm.u.st.v[buf][vr][vc * 8]) = stg[CH + u];
-    }
-    if (tid < 16) *reinterpret_cast<f32x4*>(&sm.u.st.r[buf][4 * tid]) = rstg;
+    r2l_rows_n<D, 128>(sm.u.st.k[buf], stg);
+    r2l_tp_n<D, 128>(sm.u.st.v[buf], stg + SK);
+    if (tid < 32) *reinterpret_cast<f32x4*>(&sm.u.st.r[buf][4 * tid]) = rstg;
   };
-  if (nj > 0) {
-    ready = wait_counter_gt(cnt, 0);
+  if (npair > 0) {
+    ready = wait_counter_gt(cnt, 1);
     gload(0);
     lstore(0);
   }
   __syncthreads();
-  for (int j = 0; j < nj; ++j) {
-    const int buf = j & 1;
-    const bool more = j + 1 < nj;
+  for (int pp = 0; pp < npair; ++pp) {
+    const int buf = pp & 1;
+    const bool more = pp + 1 < npair;
     bool early = false;
     if (more) {
-      if (j + 1 >= ready) {
+      const int need = 2 * pp + 3;
+      if (need >= ready) {
         const int seen = poll_counter(cnt);
-        if (seen > j + 1) {
-          acquire_agent();
+        if (seen > need) {
+          chain_acquire();
           ready = seen;
         }
       }
-      early = j + 1 < ready;
-      if (early) gload(j + 1);
+      early = need < ready;
+      if (early) gload(pp + 1);
     }
-    {
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      const int key0 = kh * 64 + mt * 32;
       bf16x8 ka[NKS];
 #pragma unroll
-      for (int st = 0; st < NKS; ++st) ka[st] = ld8(&sm.u.st.k[buf][jh * 32 + l32][16 * st + 8 * g]);
+      for (int st = 0; st < NKS; ++st) ka[st] = ld8(&sm.u.st.k[buf][key0 + l32][16 * st + 8 * g]);
       float rj[16];
-#pragma unroll
-      for (int qd = 0; qd < 4; ++qd) {
-        const f32x4 t4 = *reinterpret_cast<const f32x4*>(&sm.u.st.r[buf][jh * 32 + 8 * qd + 4 * g]);
-        rj[4 * qd] = t4[0];
-        rj[4 * qd + 1] = t4[1];
-        rj[4 * qd + 2] = t4[2];
-        rj[4 * qd + 3] = t4[3];
-      }
+      lds_rows16(&sm.u.st.r[buf][key0], g, rj);
       bf16x8 pb[2][2];
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt) {
@@ -228,8 +227,8 @@ __global__ __launch_bounds__(256) void lucid_precond_fwd_kernel(
       }
 #pragma unroll
       for (int t = 0; t < NDT; ++t) {
-        const bf16x8 va0 = ld8(&sm.u.st.v[buf][t * 32 + l32][jh * 32 + 8 * g]);
-        const bf16x8 va1 = ld8(&sm.u.st.v[buf][t * 32 + l32][jh * 32 + 16 + 8 * g]);
+        const bf16x8 va0 = ld8(&sm.u.st.v[buf][t * 32 + l32][key0 + 8 * g]);
+        const bf16x8 va1 = ld8(&sm.u.st.v[buf][t * 32 + l32][key0 + 16 + 8 * g]);
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) {
           acc[t][nt] = mfma32(va0, pb[nt][0], acc[t][nt]);
@@ -239,8 +238,8 @@ __global__ __launch_bounds__(256) void lucid_precond_fwd_kernel(
     }
     if (more) {
       if (!early) {
-        ready = wait_counter_gt(cnt, j + 1);
-        gload(j + 1);
+        ready = wait_counter_gt(cnt, 2 * pp + 3);
+        gload(pp + 1);
       }
       lstore(buf ^ 1);
     }
@@ -249,7 +248,14 @@ __global__ __launch_bounds__(256) void lucid_precond_fwd_kernel(
 
   // ---- reduce the key halves: R^T = V^T - acc^T (Rt columns = rows of this workgroup) ----
   float(*Rt)[132] = sm.u.fin.Rt;
-  if (jh == 1) {
+  auto load_x = [&](int sb) {
+    const float* src = pinv_blk + sb * 4096;
+    for (int idx = tid; idx < 1024; idx += 256) {
+      const int r = idx >> 4, c4 = (idx & 15) * 4;
+      *reinterpret_cast<f32x4*>(&sm.u.fin.X[r][c4]) = *reinterpret_cast<const f32x4*>(src + r * 64 + c4);
+    }
+  };
+  if (kh == 1) {
 #pragma unroll
     for (int t = 0; t < NDT; ++t)
 #pragma unroll
@@ -257,8 +263,9 @@ __global__ __launch_bounds__(256) void lucid_precond_fwd_kernel(
 #pragma unroll
         for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][ih * 64 + nt * 32 + l32] = acc[t][nt][e];
   }
+  load_x(0);
   __syncthreads();
-  if (jh == 0) {
+  if (kh == 0) {
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
       const int col = ih * 64 + nt * 32 + l32;
@@ -285,7 +292,7 @@ __global__ __launch_bounds__(256) void lucid_precond_fwd_kernel(
       for (int st = 0; st < kmax; ++st) {
         bf16x8 ah, al, bh8, bl;
         split8(&Rt[dt * 32 + l32][sb * 64 + 16 * st + 8 * g], ah, al);
-        split8(&sm.X[sb][rh * 32 + l32][16 * st + 8 * g], bh8, bl);
+        split8(&sm.u.fin.X[rh * 32 + l32][16 * st + 8 * g], bh8, bl);
         o = mfma32(ah, bh8, o);
         o = mfma32(ah, bl, o);
         o = mfma32(al, bh8, o);
@@ -314,7 +321,7 @@ __global__ __launch_bounds__(256) void lucid_precond_fwd_kernel(
     }
   };
   diag_solve(0);
-  publish_counter(cnt, 2 * i2 + 1);
+  __syncthreads();  // consumers wait for whole 128-row blocks: V'_A is published with V'_B
 
   // ---- R_B -= P_BA V'_A: wave -> (B rows half nb, A keys half ka) ----
   {
@@ -323,8 +330,8 @@ __global__ __launch_bounds__(256) void lucid_precond_fwd_kernel(
     f32x16 sc = zero16();
 #pragma unroll
     for (int st = 0; st < NKS; ++st)
-      sc = mfma32(ld8(kh + (int64_t)(i0 + ka * 32 + l32) * ks.t + 16 * st + 8 * g),
-                  ld8(kh + (int64_t)rowB * ks.t + 16 * st + 8 * g), sc);
+      sc = mfma32(ld8(kp + (int64_t)(i0 + ka * 32 + l32) * ks.t + 16 * st + 8 * g),
+                  ld8(kp + (int64_t)rowB * ks.t + 16 * st + 8 * g), sc);
     const float aB = sl2 * rv[rowB];
     float rA[16];
     load_rows16(rv + i0 + ka * 32, g, rA);
@@ -344,6 +351,7 @@ __global__ __launch_bounds__(256) void lucid_precond_fwd_kernel(
 #pragma unroll
         for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][col] -= cr[t][e];
     }
+    load_x(1);
     __syncthreads();
     if (ka == 0) {
 #pragma unroll

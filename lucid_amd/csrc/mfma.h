@@ -65,23 +65,32 @@ __device__ __forceinline__ float wave_xor32(float v) {
   return __shfl_xor(v, 32, 64);
 }
 
-// Chain progress counters.  Polls use relaxed agent-scope loads (they read the
-// coherent value without touching the caches); a single agent-scope acquire
-// fence is issued once the awaited progress has been seen, so the data loads
-// that follow observe everything the producer released.
+// Chain progress counters.  A producer writes a finished block, makes it
+// visible at agent scope (release fence: the L2 of its XCD is written back) and
+// then stores its progress counter.  Consumers poll the counter with relaxed
+// agent-scope loads (they read the coherent value without cache maintenance).
+//
+// Once the awaited progress has been seen a consumer needs only an ordering
+// fence, not an agent-scope acquire (which would invalidate the whole L2 of the
+// XCD for every other workgroup on it): the chain operands are laid out so that
+// one 64-row block fills whole 128-byte cache lines, no line of a block is read
+// by anyone before the block is published within the kernel, and the caches
+// are invalidated at kernel start, so neither this CU's L1 nor this XCD's L2 can
+// hold a stale copy of the lines read after the wait.  Workspaces must
+// therefore be 256-byte aligned (checked at the C ABI).
 __device__ __forceinline__ int poll_counter(const int* cnt) {
   return __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ __forceinline__ void acquire_agent() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }
+__device__ __forceinline__ void chain_acquire() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup"); }
 
-// Wait until *cnt > target; returns the value seen (acquire semantics).
+// Wait until *cnt > target; returns the value seen.
 __device__ __forceinline__ int wait_counter_gt(const int* cnt, int target) {
   int v = poll_counter(cnt);
   while (v <= target) {
     __builtin_amdgcn_s_sleep(1);
     v = poll_counter(cnt);
   }
-  acquire_agent();
+  chain_acquire();
   return v;
 }

@@ -107,7 +107,7 @@ __global__ __launch_bounds__(256) void path_dv_kernel(const bf16* __restrict__ d
       if (need >= ready) {
         const int seen = poll_counter(cnt);
         if (seen > need) {
-          acquire_agent();
+          chain_acquire();
           ready = seen;
         }
       }

@@ -137,6 +137,7 @@ int lucid_path_fwd(const void* q, const int64_t* q_strides, const void* k, const
   if (kcache)
     if (int rc = pcheck_vec("kcache", kcache, kcache_strides)) return rc;
   if (!fwd_ws) return pfail("fwd_ws is null");
+  if (reinterpret_cast<uintptr_t>(fwd_ws) % 256) return pfail("fwd_ws must be 256-byte aligned");
   const lucid::PathFwdWs ws = carve_path_fwd(fwd_ws, B, T, H, HQ, nullptr);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int NT = T / 64, NS = (NT + 7) / 8;
@@ -187,6 +188,8 @@ int lucid_path_bwd(const void* dout, const int64_t* do_strides, const void* q, c
   if (int rc = pcheck("dw", dw, dw_strides)) return rc;
   if (int rc = pcheck("dbeta", dbeta, dbeta_strides)) return rc;
   if (!fwd_ws || !bwd_ws) return pfail("fwd_ws and bwd_ws must be non-null");
+  if (reinterpret_cast<uintptr_t>(fwd_ws) % 256 || reinterpret_cast<uintptr_t>(bwd_ws) % 256)
+    return pfail("fwd_ws and bwd_ws must be 256-byte aligned");
   const lucid::PathFwdWs ws = carve_path_fwd(const_cast<void*>(fwd_ws), B, T, H, HQ, nullptr);
   const lucid::PathBwdWs bw = carve_path_bwd(bwd_ws, B, T, HQ, nullptr);
   hipStream_t st = static_cast<hipStream_t>(stream);

@@ -387,7 +387,7 @@ __global__ __launch_bounds__(256) void path_solve_fwd_kernel(const bf16* __restr
       if (J + 1 >= ready) {
         const int seen = poll_counter(cnt);
         if (seen > J + 1) {
-          acquire_agent();
+          chain_acquire();
           ready = seen;
         }
       }

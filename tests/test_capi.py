@@ -69,6 +69,17 @@ def test_argument_validation_without_gpu(built):
     rc = lib.lucid_attn_fwd(dummy, s, dummy, s, dummy, s, dummy, s, dummy, dummy, dummy,
                             1, 3, 2, 256, 64, 0.1, 1e-5, None)
     assert rc == _lib.LUCID_EINVAL and b"multiple of Hkv" in lib.lucid_last_error()
+    # workspaces must be 256-byte aligned (chain blocks fill whole cache lines)
+    misaligned = ctypes.c_void_p((1 << 20) + 128)
+    rc = lib.lucid_attn_fwd(dummy, s, dummy, s, dummy, s, dummy, s, dummy, dummy, misaligned,
+                            1, 1, 1, 256, 64, 0.1, 1e-5, None)
+    assert rc == _lib.LUCID_EINVAL and b"256-byte aligned" in lib.lucid_last_error()
+    plib = _lib.load("liblucid_path.so")
+    s4 = (ctypes.c_int64 * 3)(64 * 256, 64, 64)
+    sb = (ctypes.c_int64 * 3)(256, 1, 1)
+    rc = plib.lucid_path_fwd(dummy, s4, dummy, s4, dummy, s4, dummy, s4, dummy, sb, dummy, s4, None, None,
+                             misaligned, 1, 256, 1, 1, 64, 0.125, None)
+    assert rc == _lib.LUCID_EINVAL and b"256-byte aligned" in plib.lucid_path_last_error()
 
 
 def test_product_path_fails_loudly_without_gpu_tensors():
