@@ -406,14 +406,15 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_bw
 // id -> (p = NP-1 - id/BH, bh = id % BH): ids grow as p falls, so a workgroup
 // waits only on later blocks held by lower ids.  counters[bh] = n means the
 // last n 64-blocks of dV are published.
-// wave w: cb = w & 1 -> columns J0 + 64*cb .. +64 (two n-tiles, lane <-> column)
-//         ih = w >> 1 -> rows 32*ih .. +32 of every staged 64-row tile I
-// Each later row tile (K rows, dV rows, dV^T and K^T in T-perm layout, 1/rms)
-// is staged once in LDS (double buffered):
+// wave w owns columns J0 + 32w .. +32 (one n-tile, lane <-> column) and sweeps
+// all 64 rows of every later row tile I, so its column accumulators need no
+// cross-wave reduction.  Each later row tile (K rows, dV rows, dV^T and K^T in
+// T-perm layout, 1/rms) is staged once in LDS (double buffered):
 //   S[I][J] = K_I . K_J, P = exp(s r_I r_J S - 1/s), G[I][J] = dV_I . V'_J
 //   acc^T[d][J] += dV^T[d][I] P[I][J];  C^T[d][J] += K^T[d][I] (r_I G P)[I][J]
 // Then dV_B = X_B^T (dV'_B - acc_B), dV_A = X_A^T (dV'_A - acc_A - P_BA^T dV_B),
-// and the diagonal-block terms of C.
+// and the diagonal-block terms of C.  At d = 64 two workgroups share a CU
+// (LDS <= 80 KB, <= 256 registers per lane).
 // ---------------------------------------------------------------------------
 template <int D>
 struct PcolSmem {
@@ -426,16 +427,16 @@ struct PcolSmem {
       float r[2][64];
     } st;
     struct {
-      float Rt[D][132];       // R^T for the 128 columns (0..63 = A, 64..127 = B), reductions
-      float Xt[2][64][68];    // Xt[sb][c][r] = (P_diag^-1)[r][c]
-      bf16 dvl[2][64][D + 8]; // dV rows of A and B (bf16)
-      bf16 dvtB[D][72];       // dV_B^T, T-perm within the block
+      float Rt[D][132];        // R^T for the 128 columns (0..63 = A, 64..127 = B), reductions
+      float Xt[64][68];        // Xt[c][r] = (P_diag^-1)[r][c] of the sub-block being solved
+      bf16 dvl[2][64][D + 8];  // dV rows of A and B (bf16)
+      bf16 dvtB[D][72];        // dV_B^T, T-perm within the block
     } fin;
   } u;
 };
 
 template <int D>
-__global__ __launch_bounds__(256) void lucid_precond_bwd_col_kernel(
+__global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond_bwd_col_kernel(
     const bf16* __restrict__ k, Strides ks, int Hkv, int T, int BH, const float* __restrict__ rinv, float scale,
     const bf16* __restrict__ kt, const bf16* __restrict__ vpb, const float* __restrict__ pinv,
     const float* __restrict__ dvp, bf16* __restrict__ dvb, bf16* __restrict__ dvt, bf16* __restrict__ dv_out,
@@ -451,7 +452,7 @@ __global__ __launch_bounds__(256) void lucid_precond_bwd_col_kernel(
   const int b = bh / Hkv, h = bh - b * Hkv;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
-  const int cb = w & 1, ih = w >> 1;
+  const int cw = w * 32;  // this wave's columns J0 + cw .. +32
   const int J0 = p * 128;
   const bf16* kh = k + b * ks.b + h * ks.h;
   const float* rv = rinv + (int64_t)bh * T;
@@ -463,26 +464,20 @@ __global__ __launch_bounds__(256) void lucid_precond_bwd_col_kernel(
   const float sl2 = scale * LOG2E_F;
   const float c0 = LOG2E_F / scale;
 
-  bf16x8 kbJ[2][NKS], vbJ[2][NKS];
-  float aJ[2];
+  bf16x8 kbJ[NKS], vbJ[NKS];
+  const int jc = J0 + cw + l32;
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
-    const int jc = J0 + cb * 64 + nt * 32 + l32;
-#pragma unroll
-    for (int st = 0; st < NKS; ++st) {
-      kbJ[nt][st] = ld8(kh + (int64_t)jc * ks.t + 16 * st + 8 * g);
-      vbJ[nt][st] = ld8(vph + (int64_t)jc * D + 16 * st + 8 * g);
-    }
-    aJ[nt] = sl2 * rv[jc];
+  for (int st = 0; st < NKS; ++st) {
+    kbJ[st] = ld8(kh + (int64_t)jc * ks.t + 16 * st + 8 * g);
+    vbJ[st] = ld8(vph + (int64_t)jc * D + 16 * st + 8 * g);
   }
-  f32x16 adv[NDT][2], acs[NDT][2];
+  const float aJ = sl2 * rv[jc];
+  f32x16 adv[NDT], acs[NDT];
 #pragma unroll
-  for (int t = 0; t < NDT; ++t)
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      adv[t][nt] = zero16();
-      acs[t][nt] = zero16();
-    }
+  for (int t = 0; t < NDT; ++t) {
+    adv[t] = zero16();
+    acs[t] = zero16();
+  }
 
   // ---- sweep over the later 64-row tiles, far (published first) to near ----
   const int first = NT - 1, last = 2 * p + 2;  // tiles first, first-1, ..., last
@@ -527,48 +522,40 @@ __global__ __launch_bounds__(256) void lucid_precond_bwd_col_kernel(
       early = need < ready;
       if (early) gload(I - 1);
     }
-    {
+#pragma unroll
+    for (int rh = 0; rh < 2; ++rh) {
       bf16x8 ka[NKS], da[NKS];
 #pragma unroll
       for (int st = 0; st < NKS; ++st) {
-        ka[st] = ld8(&sm.u.st.k[buf][ih * 32 + l32][16 * st + 8 * g]);
-        da[st] = ld8(&sm.u.st.dv[buf][ih * 32 + l32][16 * st + 8 * g]);
+        ka[st] = ld8(&sm.u.st.k[buf][rh * 32 + l32][16 * st + 8 * g]);
+        da[st] = ld8(&sm.u.st.dv[buf][rh * 32 + l32][16 * st + 8 * g]);
       }
       float rI[16];
-      lds_rows16(&sm.u.st.r[buf][ih * 32], g, rI);
-      bf16x8 pb[2][2], mb[2][2];
+      lds_rows16(&sm.u.st.r[buf][rh * 32], g, rI);
+      f32x16 sc = zero16(), gg = zero16();
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        f32x16 sc = zero16(), gg = zero16();
-#pragma unroll
-        for (int st = 0; st < NKS; ++st) {
-          sc = mfma32(ka[st], kbJ[nt][st], sc);
-          gg = mfma32(da[st], vbJ[nt][st], gg);
-        }
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const float pe = __builtin_amdgcn_exp2f(fmaf(sc[e] * aJ[nt], rI[e], -c0));
-          sc[e] = pe;
-          gg[e] = gg[e] * pe * rI[e];
-        }
-        pb[nt][0] = pack_b(sc, 0);
-        pb[nt][1] = pack_b(sc, 1);
-        mb[nt][0] = pack_b(gg, 0);
-        mb[nt][1] = pack_b(gg, 1);
+      for (int st = 0; st < NKS; ++st) {
+        sc = mfma32(ka[st], kbJ[st], sc);
+        gg = mfma32(da[st], vbJ[st], gg);
       }
 #pragma unroll
-      for (int t = 0; t < NDT; ++t) {
-        const bf16x8 a0 = ld8(&sm.u.st.dvt[buf][t * 32 + l32][ih * 32 + 8 * g]);
-        const bf16x8 a1 = ld8(&sm.u.st.dvt[buf][t * 32 + l32][ih * 32 + 16 + 8 * g]);
-        const bf16x8 k0 = ld8(&sm.u.st.kt[buf][t * 32 + l32][ih * 32 + 8 * g]);
-        const bf16x8 k1 = ld8(&sm.u.st.kt[buf][t * 32 + l32][ih * 32 + 16 + 8 * g]);
+      for (int e = 0; e < 16; ++e) {
+        const float pe = __builtin_amdgcn_exp2f(fmaf(sc[e] * aJ, rI[e], -c0));
+        sc[e] = pe;
+        gg[e] = gg[e] * pe * rI[e];
+      }
+      const bf16x8 pb0 = pack_b(sc, 0), pb1 = pack_b(sc, 1);
+      const bf16x8 mb0 = pack_b(gg, 0), mb1 = pack_b(gg, 1);
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
-          adv[t][nt] = mfma32(a0, pb[nt][0], adv[t][nt]);
-          adv[t][nt] = mfma32(a1, pb[nt][1], adv[t][nt]);
-          acs[t][nt] = mfma32(k0, mb[nt][0], acs[t][nt]);
-          acs[t][nt] = mfma32(k1, mb[nt][1], acs[t][nt]);
-        }
+      for (int t = 0; t < NDT; ++t) {
+        const bf16x8 a0 = ld8(&sm.u.st.dvt[buf][t * 32 + l32][rh * 32 + 8 * g]);
+        const bf16x8 a1 = ld8(&sm.u.st.dvt[buf][t * 32 + l32][rh * 32 + 16 + 8 * g]);
+        const bf16x8 k0 = ld8(&sm.u.st.kt[buf][t * 32 + l32][rh * 32 + 8 * g]);
+        const bf16x8 k1 = ld8(&sm.u.st.kt[buf][t * 32 + l32][rh * 32 + 16 + 8 * g]);
+        adv[t] = mfma32(a0, pb0, adv[t]);
+        adv[t] = mfma32(a1, pb1, adv[t]);
+        acs[t] = mfma32(k0, mb0, acs[t]);
+        acs[t] = mfma32(k1, mb1, acs[t]);
       }
     }
     if (more) {
@@ -581,37 +568,26 @@ __global__ __launch_bounds__(256) void lucid_precond_bwd_col_kernel(
     __syncthreads();
   }
 
-  // ---- R = dV' - acc (reduce the two row halves), load X^T of both sub-blocks ----
+  // ---- R = dV' - acc for this wave's columns; X^T of sub-block B ----
   float(*Rt)[132] = sm.u.fin.Rt;
-  if (ih == 1) {
+  auto load_xt = [&](int sb) {
+    const float* src = pinv + ((int64_t)bh * NT + 2 * p + sb) * 4096;
+    for (int idx = tid; idx < 4096; idx += 256) sm.u.fin.Xt[idx & 63][idx >> 6] = src[idx];
+  };
+  {
+    const int col = cw + l32;
+    const float* src = dvp + ((int64_t)bh * T + J0 + col) * D;
 #pragma unroll
     for (int t = 0; t < NDT; ++t)
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt)
+      for (int qq = 0; qq < 4; ++qq) {
+        const int d0 = t * 32 + 8 * qq + 4 * g;
+        const f32x4 x = *reinterpret_cast<const f32x4*>(src + d0);
 #pragma unroll
-        for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][cb * 64 + nt * 32 + l32] = adv[t][nt][e];
+        for (int u = 0; u < 4; ++u) Rt[d0 + u][col] = x[u] - adv[t][4 * qq + u];
+      }
   }
-  for (int idx = tid; idx < 2 * 4096; idx += 256) {
-    const int sb = idx >> 12, r = (idx >> 6) & 63, cc = idx & 63;
-    sm.u.fin.Xt[sb][cc][r] = pinv[((int64_t)bh * NT + 2 * p + sb) * 4096 + r * 64 + cc];
-  }
-  __syncthreads();
-  if (ih == 0) {
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      const int col = cb * 64 + nt * 32 + l32;
-      const float* src = dvp + ((int64_t)bh * T + J0 + col) * D;
-#pragma unroll
-      for (int t = 0; t < NDT; ++t)
-#pragma unroll
-        for (int qq = 0; qq < 4; ++qq) {
-          const int d0 = t * 32 + 8 * qq + 4 * g;
-          const f32x4 x = *reinterpret_cast<const f32x4*>(src + d0);
-#pragma unroll
-          for (int u = 0; u < 4; ++u) Rt[d0 + u][col] = x[u] - (adv[t][nt][4 * qq + u] + Rt[d0 + u][col]);
-        }
-    }
-  }
+  load_xt(1);
   __syncthreads();
 
   // dV^T[d][c] = sum_r R^T[d][r] X[r][c] for sub-block sb (X lower: r >= c)
@@ -622,7 +598,7 @@ __global__ __launch_bounds__(256) void lucid_precond_bwd_col_kernel(
       for (int st = chh ? 2 : 0; st < 4; ++st) {
         bf16x8 ah, al, bh8, bl;
         split8(&Rt[dt * 32 + l32][sb * 64 + 16 * st + 8 * g], ah, al);
-        split8(&sm.u.fin.Xt[sb][chh * 32 + l32][16 * st + 8 * g], bh8, bl);
+        split8(&sm.u.fin.Xt[chh * 32 + l32][16 * st + 8 * g], bh8, bl);
         o = mfma32(ah, bh8, o);
         o = mfma32(ah, bl, o);
         o = mfma32(al, bh8, o);
@@ -680,6 +656,7 @@ __global__ __launch_bounds__(256) void lucid_precond_bwd_col_kernel(
 #pragma unroll
         for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][col] -= cr[t][e];
     }
+    load_xt(0);
     __syncthreads();
     if (kb == 0) {
 #pragma unroll
@@ -693,75 +670,55 @@ __global__ __launch_bounds__(256) void lucid_precond_bwd_col_kernel(
   publish_counter(cnt, NT - 2 * p);
 
   // ---- diagonal-block terms of the column sums (rows r >= columns c inside the workgroup) ----
-  // wave (cb, ih): columns of sub-block cb; rows of sub-block rb = cb..1, half ih
+  // wave w: its 32 columns (sub-block w >> 1) against rows of sub-blocks rb = w >> 1 .. 1
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb) {
-    if (rb < cb) continue;
-    const int rbase = J0 + rb * 64 + ih * 32;  // 32 rows handled by this wave
-    bf16x8 ka[NKS], da[NKS];
+    if (rb < (w >> 1)) continue;
 #pragma unroll
-    for (int st = 0; st < NKS; ++st) {
-      ka[st] = ld8(kh + (int64_t)(rbase + l32) * ks.t + 16 * st + 8 * g);
-      da[st] = ld8(&sm.u.fin.dvl[rb][ih * 32 + l32][16 * st + 8 * g]);
-    }
-    float rr[16];
-    load_rows16(rv + rbase, g, rr);
-    bf16x8 mb[2][2];
+    for (int rh = 0; rh < 2; ++rh) {
+      if (rb * 64 + rh * 32 + 31 < cw) continue;  // rows all above this wave's columns
+      const int rbase = J0 + rb * 64 + rh * 32;
+      bf16x8 ka[NKS], da[NKS];
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
+      for (int st = 0; st < NKS; ++st) {
+        ka[st] = ld8(kh + (int64_t)(rbase + l32) * ks.t + 16 * st + 8 * g);
+        da[st] = ld8(&sm.u.fin.dvl[rb][rh * 32 + l32][16 * st + 8 * g]);
+      }
+      float rr[16];
+      load_rows16(rv + rbase, g, rr);
       f32x16 sc = zero16(), gg = zero16();
 #pragma unroll
       for (int st = 0; st < NKS; ++st) {
-        sc = mfma32(ka[st], kbJ[nt][st], sc);
-        gg = mfma32(da[st], vbJ[nt][st], gg);
+        sc = mfma32(ka[st], kbJ[st], sc);
+        gg = mfma32(da[st], vbJ[st], gg);
       }
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const int rloc = rb * 64 + ih * 32 + drow(e, g), cloc = cb * 64 + nt * 32 + l32;
-        const float pe = (rloc >= cloc) ? __builtin_amdgcn_exp2f(fmaf(sc[e] * aJ[nt], rr[e], -c0)) : 0.f;
+        const int rloc = rb * 64 + rh * 32 + drow(e, g), cloc = cw + l32;
+        const float pe = (rloc >= cloc) ? __builtin_amdgcn_exp2f(fmaf(sc[e] * aJ, rr[e], -c0)) : 0.f;
         gg[e] = gg[e] * pe * rr[e];
       }
-      mb[nt][0] = pack_b(gg, 0);
-      mb[nt][1] = pack_b(gg, 1);
-    }
+      const bf16x8 mb0 = pack_b(gg, 0), mb1 = pack_b(gg, 1);
 #pragma unroll
-    for (int t = 0; t < NDT; ++t) {
-      const bf16* kp = kth + (int64_t)(t * 32 + l32) * T + rbase + 8 * g;
-      const bf16x8 k0 = ld8(kp), k1 = ld8(kp + 16);
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        acs[t][nt] = mfma32(k0, mb[nt][0], acs[t][nt]);
-        acs[t][nt] = mfma32(k1, mb[nt][1], acs[t][nt]);
+      for (int t = 0; t < NDT; ++t) {
+        const bf16* kp = kth + (int64_t)(t * 32 + l32) * T + rbase + 8 * g;
+        acs[t] = mfma32(ld8(kp), mb0, acs[t]);
+        acs[t] = mfma32(ld8(kp + 16), mb1, acs[t]);
       }
     }
   }
-  // ---- reduce the two row halves of the column sums and store ----
-  __syncthreads();
-  if (ih == 1) {
+  // ---- store the column sums of this wave's columns ----
+  {
+    float* dst = colsum + ((int64_t)bh * T + jc) * D;
 #pragma unroll
     for (int t = 0; t < NDT; ++t)
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt)
+      for (int qq = 0; qq < 4; ++qq) {
+        f32x4 x;
 #pragma unroll
-        for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][cb * 64 + nt * 32 + l32] = acs[t][nt][e];
-  }
-  __syncthreads();
-  if (ih == 0) {
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      const int col = cb * 64 + nt * 32 + l32;
-      float* dst = colsum + ((int64_t)bh * T + J0 + col) * D;
-#pragma unroll
-      for (int t = 0; t < NDT; ++t)
-#pragma unroll
-        for (int qq = 0; qq < 4; ++qq) {
-          const int d0 = t * 32 + 8 * qq + 4 * g;
-          f32x4 x;
-#pragma unroll
-          for (int u = 0; u < 4; ++u) x[u] = acs[t][nt][4 * qq + u] + Rt[d0 + u][col];
-          *reinterpret_cast<f32x4*>(dst + d0) = x;
-        }
-    }
+        for (int u = 0; u < 4; ++u) x[u] = acs[t][4 * qq + u];
+        *reinterpret_cast<f32x4*>(dst + t * 32 + 8 * qq + 4 * g) = x;
+      }
   }
 }
 
