@@ -70,14 +70,15 @@ __global__ __launch_bounds__(256) void lucid_bwd_prep_kernel(const bf16* __restr
 }
 
 // ---------------------------------------------------------------------------
-// Column sweep for the attention part.  Workgroup = 256 keys of one kv head,
-// wave w owns keys 64w..64w+63 as two 32-key n-tiles (lane <-> key j); loops
-// over the G query heads of the group and over every 64-row query tile at or
-// below the diagonal.  Each query tile (Q, dO rows; Q^T, dO^T in T-perm
-// layout; lse2 and delta) is staged once per workgroup in LDS, double buffered.
+// Column sweep for the attention part.  Workgroup = 128 keys of one kv head,
+// wave w owns keys 32w..32w+31 (one n-tile, lane <-> key j); loops over the G
+// query heads of the group and over every 64-row query tile at or below the
+// diagonal.  Each query tile (Q, dO rows; Q^T, dO^T in T-perm layout; lse2 and
+// delta) is staged once per workgroup in LDS, double buffered.
 //   S[i][j] = Q_i . K_j, P = exp2(c S - lse2_i)
 //   dV'^T[d][j] += dO^T[d][i] P[i][j];  dP[i][j] = dO_i . V'_j
 //   dS = P (dP - delta_i);  dK^T[d][j] += Q^T[d][i] dS[i][j]
+// At d = 64 two workgroups share a CU (<= 256 registers per lane).
 // ---------------------------------------------------------------------------
 template <int D>
 struct DkdvSmem {
@@ -90,7 +91,7 @@ struct DkdvSmem {
 };
 
 template <int D>
-__global__ __launch_bounds__(256) void lucid_attn_bwd_dkdv_kernel(
+__global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_bwd_dkdv_kernel(
     const bf16* __restrict__ q, Strides qs, const bf16* __restrict__ k, Strides ks, const bf16* __restrict__ vpb,
     const bf16* __restrict__ dout, Strides dos, const bf16* __restrict__ qt, const bf16* __restrict__ dot,
     const float* __restrict__ lse, const float* __restrict__ delta, float* __restrict__ dvp,
@@ -105,31 +106,27 @@ __global__ __launch_bounds__(256) void lucid_attn_bwd_dkdv_kernel(
   const int G = Hq / Hkv;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
-  const int jw = jb * 256 + w * 64;  // first key of this wave
+  const int jw = jb * 128 + w * 32;  // first key of this wave
+  const int jrow = jw + l32;
   const bf16* kh = k + b * ks.b + h * ks.h;
   const float c = scale * LOG2E_F;
 
-  bf16x8 kb[2][NKS], vb[2][NKS];
+  bf16x8 kb[NKS], vb[NKS];
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
-    const int jr = min(jw + nt * 32 + l32, T - 1);
-#pragma unroll
-    for (int st = 0; st < NKS; ++st) {
-      kb[nt][st] = ld8(kh + (int64_t)jr * ks.t + 16 * st + 8 * g);
-      vb[nt][st] = ld8(vpb + ((int64_t)bh * T + jr) * D + 16 * st + 8 * g);
-    }
+  for (int st = 0; st < NKS; ++st) {
+    kb[st] = ld8(kh + (int64_t)jrow * ks.t + 16 * st + 8 * g);
+    vb[st] = ld8(vpb + ((int64_t)bh * T + jrow) * D + 16 * st + 8 * g);
   }
-  f32x16 adv[NDT][2], adk[NDT][2];
+  f32x16 adv[NDT], adk[NDT];
 #pragma unroll
-  for (int t = 0; t < NDT; ++t)
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      adv[t][nt] = zero16();
-      adk[t][nt] = zero16();
-    }
+  for (int t = 0; t < NDT; ++t) {
+    adv[t] = zero16();
+    adk[t] = zero16();
+  }
   const int nt64 = T / 64;
-  const int it_first = jb * 4;  // first query tile any wave needs
+  const int it_first = jb * 2;  // first query tile any wave needs
   const int it_w = jw / 64;     // this wave's diagonal tile
+  const int kloc = jw - it_w * 64 + l32;  // this lane's key inside its diagonal tile
   for (int gi = 0; gi < G; ++gi) {
     const int hq = h * G + gi;
     const int bhq = b * Hq + hq;
@@ -158,10 +155,8 @@ __global__ __launch_bounds__(256) void lucid_attn_bwd_dkdv_kernel(
       if (tid < 16) *reinterpret_cast<f32x4*>(&sm.lse[buf][4 * tid]) = fstg;
       else if (tid < 32) *reinterpret_cast<f32x4*>(&sm.dl[buf][4 * (tid - 16)]) = fstg;
     };
-    if (it_first < nt64) {
-      gload(it_first);
-      lstore(0);
-    }
+    gload(it_first);
+    lstore(0);
     __syncthreads();
     for (int it = it_first; it < nt64; ++it) {
       const int buf = (it - it_first) & 1;
@@ -171,65 +166,49 @@ __global__ __launch_bounds__(256) void lucid_attn_bwd_dkdv_kernel(
         const bool diag = (it == it_w);
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
+          if (diag && mt * 32 + 31 < kloc - l32) continue;  // rows all above this wave's keys
           float lr[16];
           lds_rows16(&sm.lse[buf][mt * 32], g, lr);
-          bf16x8 pb[2][2];
-          f32x16 pv[2];
+          f32x16 pv;
+          bf16x8 pb0, pb1;
           {
             bf16x8 qa[NKS];
 #pragma unroll
             for (int st = 0; st < NKS; ++st) qa[st] = ld8(&sm.q[buf][mt * 32 + l32][16 * st + 8 * g]);
+            f32x16 sc = zero16();
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt) {
-              f32x16 sc = zero16();
+            for (int st = 0; st < NKS; ++st) sc = mfma32(qa[st], kb[st], sc);
 #pragma unroll
-              for (int st = 0; st < NKS; ++st) sc = mfma32(qa[st], kb[nt][st], sc);
-#pragma unroll
-              for (int e = 0; e < 16; ++e) {
-                float p = __builtin_amdgcn_exp2f(fmaf(sc[e], c, -lr[e]));
-                if (diag && (mt * 32 + drow(e, g) < nt * 32 + l32)) p = 0.f;
-                sc[e] = p;
-              }
-              pv[nt] = sc;
-              pb[nt][0] = pack_b(sc, 0);
-              pb[nt][1] = pack_b(sc, 1);
+            for (int e = 0; e < 16; ++e) {
+              float p = __builtin_amdgcn_exp2f(fmaf(sc[e], c, -lr[e]));
+              if (diag && (mt * 32 + drow(e, g) < kloc)) p = 0.f;
+              pv[e] = p;
             }
+            pb0 = pack_b(pv, 0);
+            pb1 = pack_b(pv, 1);
           }
 #pragma unroll
           for (int t = 0; t < NDT; ++t) {
-            const bf16x8 a0 = ld8(&sm.dot[buf][t * 32 + l32][mt * 32 + 8 * g]);
-            const bf16x8 a1 = ld8(&sm.dot[buf][t * 32 + l32][mt * 32 + 16 + 8 * g]);
-#pragma unroll
-            for (int nt = 0; nt < 2; ++nt) {
-              adv[t][nt] = mfma32(a0, pb[nt][0], adv[t][nt]);
-              adv[t][nt] = mfma32(a1, pb[nt][1], adv[t][nt]);
-            }
+            adv[t] = mfma32(ld8(&sm.dot[buf][t * 32 + l32][mt * 32 + 8 * g]), pb0, adv[t]);
+            adv[t] = mfma32(ld8(&sm.dot[buf][t * 32 + l32][mt * 32 + 16 + 8 * g]), pb1, adv[t]);
           }
           lds_rows16(&sm.dl[buf][mt * 32], g, lr);
           {
             bf16x8 da[NKS];
 #pragma unroll
             for (int st = 0; st < NKS; ++st) da[st] = ld8(&sm.dO[buf][mt * 32 + l32][16 * st + 8 * g]);
+            f32x16 dp = zero16();
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt) {
-              f32x16 dp = zero16();
+            for (int st = 0; st < NKS; ++st) dp = mfma32(da[st], vb[st], dp);
 #pragma unroll
-              for (int st = 0; st < NKS; ++st) dp = mfma32(da[st], vb[nt][st], dp);
-#pragma unroll
-              for (int e = 0; e < 16; ++e) dp[e] = pv[nt][e] * (dp[e] - lr[e]);
-              pb[nt][0] = pack_b(dp, 0);
-              pb[nt][1] = pack_b(dp, 1);
-            }
+            for (int e = 0; e < 16; ++e) dp[e] = pv[e] * (dp[e] - lr[e]);
+            pb0 = pack_b(dp, 0);
+            pb1 = pack_b(dp, 1);
           }
 #pragma unroll
           for (int t = 0; t < NDT; ++t) {
-            const bf16x8 a0 = ld8(&sm.qt[buf][t * 32 + l32][mt * 32 + 8 * g]);
-            const bf16x8 a1 = ld8(&sm.qt[buf][t * 32 + l32][mt * 32 + 16 + 8 * g]);
-#pragma unroll
-            for (int nt = 0; nt < 2; ++nt) {
-              adk[t][nt] = mfma32(a0, pb[nt][0], adk[t][nt]);
-              adk[t][nt] = mfma32(a1, pb[nt][1], adk[t][nt]);
-            }
+            adk[t] = mfma32(ld8(&sm.qt[buf][t * 32 + l32][mt * 32 + 8 * g]), pb0, adk[t]);
+            adk[t] = mfma32(ld8(&sm.qt[buf][t * 32 + l32][mt * 32 + 16 + 8 * g]), pb1, adk[t]);
           }
         }
       }
@@ -237,26 +216,21 @@ __global__ __launch_bounds__(256) void lucid_attn_bwd_dkdv_kernel(
       __syncthreads();
     }
   }
+  float* ov = dvp + ((int64_t)bh * T + jrow) * D;
+  float* ok = dka + ((int64_t)bh * T + jrow) * D;
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
-    const int jrow = jw + nt * 32 + l32;
-    if (jrow >= T) continue;
-    float* ov = dvp + ((int64_t)bh * T + jrow) * D;
-    float* ok = dka + ((int64_t)bh * T + jrow) * D;
+  for (int t = 0; t < NDT; ++t)
 #pragma unroll
-    for (int t = 0; t < NDT; ++t)
+    for (int qq = 0; qq < 4; ++qq) {
+      f32x4 a, bq;
 #pragma unroll
-      for (int qq = 0; qq < 4; ++qq) {
-        f32x4 a, bq;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          a[u] = adv[t][nt][4 * qq + u];
-          bq[u] = adk[t][nt][4 * qq + u] * scale;
-        }
-        *reinterpret_cast<f32x4*>(ov + t * 32 + 8 * qq + 4 * g) = a;
-        *reinterpret_cast<f32x4*>(ok + t * 32 + 8 * qq + 4 * g) = bq;
+      for (int u = 0; u < 4; ++u) {
+        a[u] = adv[t][4 * qq + u];
+        bq[u] = adk[t][4 * qq + u] * scale;
       }
-  }
+      *reinterpret_cast<f32x4*>(ov + t * 32 + 8 * qq + 4 * g) = a;
+      *reinterpret_cast<f32x4*>(ok + t * 32 + 8 * qq + 4 * g) = bq;
+    }
 }
 
 // ---------------------------------------------------------------------------
