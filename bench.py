@@ -121,6 +121,22 @@ PATH_KERNEL_FLOPS = {
 }
 
 
+def copy_calibration(nbytes: int, reps: int = 3) -> None:
+    """A plain copy of ``nbytes`` (reads nbytes, writes nbytes) so that per-dispatch
+    HBM counters can be scaled to bytes: factor = nbytes / counter reading."""
+    import torch
+    x = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+    y = torch.empty_like(x)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / reps * 1e3
+    print(json.dumps({"copy_bytes": nbytes, "ms": round(ms, 4), "GB/s": round(2 * nbytes / ms / 1e6, 1)}),
+          flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -132,8 +148,14 @@ def main():
                          "B1 H16 T32768 d64 fwd+bwd")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-causal", action="store_true")
+    ap.add_argument("--copy-bytes", type=int, default=0,
+                    help="calibration only: time a plain device copy of this many bytes (the reference kernel "
+                         "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings) and exit")
     args = ap.parse_args()
 
+    if args.copy_bytes:
+        copy_calibration(args.copy_bytes)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not supported "
               "(heads shard across GPUs with no exchange; no multi-GPU run is part of this build)",

@@ -95,7 +95,7 @@ __global__ __launch_bounds__(256) void lucid_prep_kernel(const bf16* __restrict_
 // Workgroup id -> (i2 = id / BH, bh = id % BH): ids grow with i2, so every
 // wait is on a lower id (in-order dispatch keeps the chain deadlock free) and
 // the blocks of one head share an XCD when BH % 8 == 0.  counters[bh] = number
-// of 64-row blocks of V' already published.
+// of 64-row blocks of V' already published (whole 128-row blocks at a time).
 //
 // The earlier keys are swept in pairs of 64-key tiles (128 keys per barrier):
 // K rows, V'^T (T-perm) and 1/rms of the pair are staged once per workgroup in
@@ -103,9 +103,12 @@ __global__ __launch_bounds__(256) void lucid_prep_kernel(const bf16* __restrict_
 // wave w: ih = w & 1 -> rows i0 + 64*ih .. +64 (two 32-row n-tiles, lane <-> row)
 //         kh = w >> 1 -> the 64-key tile 2*pair + kh of every staged pair
 //   acc^T[d][i] += V'^T[d][j] P^T[j][i],  P^T[j][i] = exp(s r_i r_j K_j.K_i - 1/s)
-// Then V'_A = X_A (V_A - acc_A); V'_B = X_B (V_B - acc_B - P_BA V'_A), with
-// X = P_diag^-1 (fp32, computed by lucid_prep_kernel into pinv) applied through
-// a 3-term bf16 split (hi*hi + hi*lo + lo*hi).  At d = 64 two workgroups share a CU (LDS <= 80 KB,
+// (the kh = 0 accumulators start at -V^T).  Then V'_A = X_A R_A,
+// V'_B = X_B (R_B - P_BA V'_A), R = V - acc, with X = P_diag^-1 (fp32, from
+// lucid_prep_kernel) applied through a 3-term bf16 split (hi*hi + hi*lo + lo*hi).
+// The chain's critical path is the work after the last pair becomes visible, so
+// everything that does not depend on it (V, P_BA, the two inverses) is loaded
+// or computed earlier.  At d = 64 two workgroups share a CU (LDS <= 80 KB,
 // <= 256 registers per lane) so that one's MFMA work overlaps the other's exp.
 // ---------------------------------------------------------------------------
 template <int D>
@@ -117,11 +120,12 @@ struct PfwdSmem {
       float r[2][128];
     } st;
     struct {
-      float Rt[D][132];    // R^T for the 128 rows (cols 0..63 = A, 64..127 = B)
-      float X[64][68];     // inverse of the diagonal block being solved
-      bf16 vA[D][64 + 8];  // V'_A^T (bf16, T-perm within the block) for the B correction
+      float Rt[D][132];     // R^T for the 128 rows (cols 0..63 = A, 64..127 = B)
+      float X[64][68];      // inverse of the diagonal block being solved
+      bf16 vT[D][128 + 8];  // V'^T of the block (bf16, T-perm within 16-groups)
     } fin;
   } u;
+  bf16x8 pba[4][64][2];  // P_BA as MFMA B operands, per wave and lane
 };
 
 template <int D>
@@ -133,6 +137,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
   constexpr int NKS = D / 16;
   constexpr int SK = 128 * D / 2048;  // 16-byte chunks per thread of a staged 128-key K tile
   constexpr int SV = D * 128 / 2048;  // ... and of the V'^T tile
+  static_assert(SK + SV >= 8, "the staging registers also carry the two 64x64 fp32 inverses");
   __shared__ __attribute__((aligned(16))) PfwdSmem<D> sm;
 
   const int id = blockIdx.x;
@@ -147,7 +152,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
   const bf16* vh = v + b * vs.b + h * vs.h;
   const float* rv = rinv + (int64_t)bh * T;
   const bf16* vpth = vpt + (int64_t)bh * D * T;
-  float* pinv_blk = pinv + ((int64_t)bh * NT + 2 * i2) * 4096;
+  const float* pinv_blk = pinv + ((int64_t)bh * NT + 2 * i2) * 4096;
   int* cnt = counters + bh;
   const float sl2 = scale * LOG2E_F;
   const float c0 = LOG2E_F / scale;
@@ -161,11 +166,36 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
     for (int st = 0; st < NKS; ++st) kbi[nt][st] = ld8(kp + (int64_t)row * ks.t + 16 * st + 8 * g);
     ai[nt] = sl2 * rv[row];
   }
+  // accumulators: -V^T for the kh = 0 waves, zero for the others
   f32x16 acc[NDT][2];
 #pragma unroll
-  for (int t = 0; t < NDT; ++t) {
-    acc[t][0] = zero16();
-    acc[t][1] = zero16();
+  for (int nt = 0; nt < 2; ++nt) {
+    const bf16* vrow = vh + (int64_t)(i0 + ih * 64 + nt * 32 + l32) * vs.t;
+#pragma unroll
+    for (int t = 0; t < NDT; ++t)
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd) {
+        const bf16x4 vv = *reinterpret_cast<const bf16x4*>(vrow + t * 32 + 8 * qd + 4 * g);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc[t][nt][4 * qd + u] = kh ? 0.f : -(float)vv[u];
+      }
+  }
+  // P_BA for the B correction (keys of A half ka, rows of B half nb): depends on K only
+  {
+    const int nb = w & 1, ka = w >> 1;
+    const int rowB = i0 + 64 + nb * 32 + l32;
+    f32x16 sc = zero16();
+#pragma unroll
+    for (int st = 0; st < NKS; ++st)
+      sc = mfma32(ld8(kp + (int64_t)(i0 + ka * 32 + l32) * ks.t + 16 * st + 8 * g),
+                  ld8(kp + (int64_t)rowB * ks.t + 16 * st + 8 * g), sc);
+    const float aB = sl2 * rv[rowB];
+    float rA[16];
+    load_rows16(rv + i0 + ka * 32, g, rA);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) sc[e] = __builtin_amdgcn_exp2f(fmaf(sc[e] * aB, rA[e], -c0));
+    sm.pba[w][lane][0] = pack_b(sc, 0);
+    sm.pba[w][lane][1] = pack_b(sc, 1);
   }
 
   // ---- off-diagonal sweep over the i2 earlier pairs of 64-key tiles ----
@@ -184,10 +214,29 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
     r2l_tp_n<D, 128>(sm.u.st.v[buf], stg + SK);
     if (tid < 32) *reinterpret_cast<f32x4*>(&sm.u.st.r[buf][4 * tid]) = rstg;
   };
+  // the two inverses X_A, X_B (2 x 64 x 64 fp32) into stg[0..7]: chunk u -> sub-block u >> 2
+  auto xload = [&]() {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int idx = tid + 256 * u;
+      const int sb = idx >> 10, r = (idx >> 4) & 63, c4 = (idx & 15) * 4;
+      stg[u] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const f32x4*>(pinv_blk + sb * 4096 + r * 64 + c4));
+    }
+  };
+  auto xstore = [&](int sb) {
+#pragma unroll
+    for (int u = 4 * sb; u < 4 * sb + 4; ++u) {
+      const int idx = tid + 256 * u;
+      const int r = (idx >> 4) & 63, c4 = (idx & 15) * 4;
+      *reinterpret_cast<f32x4*>(&sm.u.fin.X[r][c4]) = __builtin_bit_cast(f32x4, stg[u]);
+    }
+  };
   if (npair > 0) {
     ready = wait_counter_gt(cnt, 1);
     gload(0);
     lstore(0);
+  } else {
+    xload();
   }
   __syncthreads();
   for (int pp = 0; pp < npair; ++pp) {
@@ -205,6 +254,8 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
       }
       early = need < ready;
       if (early) gload(pp + 1);
+    } else {
+      xload();  // last pair: fetch the inverses while it is processed
     }
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
@@ -246,15 +297,8 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
     __syncthreads();
   }
 
-  // ---- reduce the key halves: R^T = V^T - acc^T (Rt columns = rows of this workgroup) ----
+  // ---- reduce the key halves: R^T = -(acc_0 + acc_1) (Rt columns = rows of this workgroup) ----
   float(*Rt)[132] = sm.u.fin.Rt;
-  auto load_x = [&](int sb) {
-    const float* src = pinv_blk + sb * 4096;
-    for (int idx = tid; idx < 1024; idx += 256) {
-      const int r = idx >> 4, c4 = (idx & 15) * 4;
-      *reinterpret_cast<f32x4*>(&sm.u.fin.X[r][c4]) = *reinterpret_cast<const f32x4*>(src + r * 64 + c4);
-    }
-  };
   if (kh == 1) {
 #pragma unroll
     for (int t = 0; t < NDT; ++t)
@@ -263,23 +307,18 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
 #pragma unroll
         for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][ih * 64 + nt * 32 + l32] = acc[t][nt][e];
   }
-  load_x(0);
+  xstore(0);
   __syncthreads();
   if (kh == 0) {
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      const int col = ih * 64 + nt * 32 + l32;
-      const bf16* vrow = vh + (int64_t)(i0 + col) * vs.t;
+    for (int t = 0; t < NDT; ++t)
 #pragma unroll
-      for (int t = 0; t < NDT; ++t)
+      for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
-        for (int qd = 0; qd < 4; ++qd) {
-          const int d0 = t * 32 + 8 * qd + 4 * g;
-          const bf16x4 vv = *reinterpret_cast<const bf16x4*>(vrow + d0);
-#pragma unroll
-          for (int u = 0; u < 4; ++u) Rt[d0 + u][col] = (float)vv[u] - (acc[t][nt][4 * qd + u] + Rt[d0 + u][col]);
+        for (int e = 0; e < 16; ++e) {
+          float& x = Rt[t * 32 + drow(e, g)][ih * 64 + nt * 32 + l32];
+          x = -(acc[t][nt][e] + x);
         }
-    }
   }
   __syncthreads();
 
@@ -299,8 +338,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
       }
       const int rl = rh * 32 + l32;
       const int r = i0 + sb * 64 + rl;
-      const int slot = (r & ~15) | jmap(r & 15);
-      const int lslot = (rl & ~15) | jmap(rl & 15);
+      const int lslot = sb * 64 + ((rl & ~15) | jmap(rl & 15));
       float* out32 = vp32 + ((int64_t)bh * T + r) * D;
       bf16* outb = vpb + ((int64_t)bh * T + r) * D;
 #pragma unroll
@@ -312,8 +350,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
         for (int u = 0; u < 4; ++u) {
           f[u] = o[4 * qd + u];
           bb[u] = (bf16)o[4 * qd + u];
-          vpth_w(vpt, bh, D, T, d0 + u, slot, bb[u]);
-          if (sb == 0) sm.u.fin.vA[d0 + u][lslot] = bb[u];
+          sm.u.fin.vT[d0 + u][lslot] = bb[u];
         }
         *reinterpret_cast<f32x4*>(out32 + d0) = f;
         *reinterpret_cast<bf16x4*>(outb + d0) = bb;
@@ -321,28 +358,18 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
     }
   };
   diag_solve(0);
-  __syncthreads();  // consumers wait for whole 128-row blocks: V'_A is published with V'_B
+  __syncthreads();
+  xstore(1);
 
   // ---- R_B -= P_BA V'_A: wave -> (B rows half nb, A keys half ka) ----
   {
     const int nb = w & 1, ka = w >> 1;
-    const int rowB = i0 + 64 + nb * 32 + l32;
-    f32x16 sc = zero16();
-#pragma unroll
-    for (int st = 0; st < NKS; ++st)
-      sc = mfma32(ld8(kp + (int64_t)(i0 + ka * 32 + l32) * ks.t + 16 * st + 8 * g),
-                  ld8(kp + (int64_t)rowB * ks.t + 16 * st + 8 * g), sc);
-    const float aB = sl2 * rv[rowB];
-    float rA[16];
-    load_rows16(rv + i0 + ka * 32, g, rA);
-#pragma unroll
-    for (int e = 0; e < 16; ++e) sc[e] = __builtin_amdgcn_exp2f(fmaf(sc[e] * aB, rA[e], -c0));
-    const bf16x8 p0 = pack_b(sc, 0), p1 = pack_b(sc, 1);
+    const bf16x8 pba0 = sm.pba[w][lane][0], pba1 = sm.pba[w][lane][1];
     f32x16 cr[NDT];
 #pragma unroll
     for (int t = 0; t < NDT; ++t) {
-      cr[t] = mfma32(ld8(&sm.u.fin.vA[t * 32 + l32][ka * 32 + 8 * g]), p0, zero16());
-      cr[t] = mfma32(ld8(&sm.u.fin.vA[t * 32 + l32][ka * 32 + 16 + 8 * g]), p1, cr[t]);
+      cr[t] = mfma32(ld8(&sm.u.fin.vT[t * 32 + l32][ka * 32 + 8 * g]), pba0, zero16());
+      cr[t] = mfma32(ld8(&sm.u.fin.vT[t * 32 + l32][ka * 32 + 16 + 8 * g]), pba1, cr[t]);
     }
     const int col = 64 + nb * 32 + l32;
     if (ka == 1) {
@@ -351,7 +378,6 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
 #pragma unroll
         for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][col] -= cr[t][e];
     }
-    load_x(1);
     __syncthreads();
     if (ka == 0) {
 #pragma unroll
@@ -362,6 +388,12 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
     __syncthreads();
   }
   diag_solve(1);
+  __syncthreads();
+  // V'^T of the whole block to the T-perm operand copy: 16-byte stores
+  for (int c = tid; c < D * 16; c += 256) {
+    const int dd = c >> 4, s8 = (c & 15) * 8;
+    *reinterpret_cast<bf16x8*>(vpt + ((int64_t)bh * D + dd) * T + i0 + s8) = ld8(&sm.u.fin.vT[dd][s8]);
+  }
   publish_counter(cnt, 2 * i2 + 2);
 }
 
