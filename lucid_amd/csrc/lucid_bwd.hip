@@ -386,9 +386,11 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_bw
 // T-perm layout, 1/rms) is staged once in LDS (double buffered):
 //   S[I][J] = K_I . K_J, P = exp(s r_I r_J S - 1/s), G[I][J] = dV_I . V'_J
 //   acc^T[d][J] += dV^T[d][I] P[I][J];  C^T[d][J] += K^T[d][I] (r_I G P)[I][J]
-// Then dV_B = X_B^T (dV'_B - acc_B), dV_A = X_A^T (dV'_A - acc_A - P_BA^T dV_B),
-// and the diagonal-block terms of C.  At d = 64 two workgroups share a CU
-// (LDS <= 80 KB, <= 256 registers per lane).
+// (acc starts at -dV'^T).  Then dV_B = X_B^T R_B, dV_A = X_A^T (R_A - P_BA^T dV_B),
+// R = dV' - acc, and the diagonal-block terms of C.  The chain's critical path
+// is the work after the last tile becomes visible, so dV' and both inverses
+// are loaded earlier and dV^T is stored with coalesced 16-byte writes.  At
+// d = 64 two workgroups share a CU (LDS <= 80 KB, <= 256 registers per lane).
 // ---------------------------------------------------------------------------
 template <int D>
 struct PcolSmem {
@@ -401,10 +403,9 @@ struct PcolSmem {
       float r[2][64];
     } st;
     struct {
-      float Rt[D][132];        // R^T for the 128 columns (0..63 = A, 64..127 = B), reductions
-      float Xt[64][68];        // Xt[c][r] = (P_diag^-1)[r][c] of the sub-block being solved
-      bf16 dvl[2][64][D + 8];  // dV rows of A and B (bf16)
-      bf16 dvtB[D][72];        // dV_B^T, T-perm within the block
+      float Rt[D][132];     // R^T for the 128 columns (0..63 = A, 64..127 = B), reductions
+      float Xt[64][68];     // Xt[c][r] = (P_diag^-1)[r][c] of the sub-block being solved
+      bf16 vT[D][128 + 8];  // dV^T of the block (bf16, T-perm within 16-groups)
     } fin;
   } u;
 };
@@ -447,10 +448,18 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
   }
   const float aJ = sl2 * rv[jc];
   f32x16 adv[NDT], acs[NDT];
+  {
+    const float* src = dvp + ((int64_t)bh * T + jc) * D;
 #pragma unroll
-  for (int t = 0; t < NDT; ++t) {
-    adv[t] = zero16();
-    acs[t] = zero16();
+    for (int t = 0; t < NDT; ++t) {
+      acs[t] = zero16();
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) {
+        const f32x4 x = *reinterpret_cast<const f32x4*>(src + t * 32 + 8 * qq + 4 * g);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) adv[t][4 * qq + u] = -x[u];
+      }
+    }
   }
 
   // ---- sweep over the later 64-row tiles, far (published first) to near ----
@@ -473,11 +482,34 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
     r2l_tp<D>(sm.u.st.kt[buf], stg + 3 * CH);
     if (tid < 16) *reinterpret_cast<f32x4*>(&sm.u.st.r[buf][4 * tid]) = rstg;
   };
+  // the two inverses X_A, X_B (2 x 64 x 64 fp32) into stg[0..7]: chunk u -> sub-block u >> 2
+  static_assert(4 * CH >= 8, "the staging registers also carry the two inverses");
+  const float* pinv_blk = pinv + ((int64_t)bh * NT + 2 * p) * 4096;
+  auto xload = [&]() {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int idx = tid + 256 * u;
+      const int sb = idx >> 10, r = (idx >> 4) & 63, c4 = (idx & 15) * 4;
+      stg[u] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const f32x4*>(pinv_blk + sb * 4096 + r * 64 + c4));
+    }
+  };
+  auto xstore_t = [&](int sb) {
+#pragma unroll
+    for (int u = 4 * sb; u < 4 * sb + 4; ++u) {
+      const int idx = tid + 256 * u;
+      const int r = (idx >> 4) & 63, c4 = (idx & 15) * 4;
+      const f32x4 x = __builtin_bit_cast(f32x4, stg[u]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sm.u.fin.Xt[c4 + e][r] = x[e];
+    }
+  };
   // tile I is published once the counter exceeds NT-1-I
   if (first >= last) {
     ready = wait_counter_gt(cnt, NT - 1 - first);
     gload(first);
     lstore(0);
+  } else {
+    xload();
   }
   __syncthreads();
   for (int I = first; I >= last; --I) {
@@ -495,6 +527,8 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
       }
       early = need < ready;
       if (early) gload(I - 1);
+    } else {
+      xload();  // last tile: fetch the inverses while it is processed
     }
 #pragma unroll
     for (int rh = 0; rh < 2; ++rh) {
@@ -542,26 +576,13 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
     __syncthreads();
   }
 
-  // ---- R = dV' - acc for this wave's columns; X^T of sub-block B ----
+  // ---- R = dV' - acc = -adv for this wave's columns; X^T of sub-block B ----
   float(*Rt)[132] = sm.u.fin.Rt;
-  auto load_xt = [&](int sb) {
-    const float* src = pinv + ((int64_t)bh * NT + 2 * p + sb) * 4096;
-    for (int idx = tid; idx < 4096; idx += 256) sm.u.fin.Xt[idx & 63][idx >> 6] = src[idx];
-  };
-  {
-    const int col = cw + l32;
-    const float* src = dvp + ((int64_t)bh * T + J0 + col) * D;
 #pragma unroll
-    for (int t = 0; t < NDT; ++t)
+  for (int t = 0; t < NDT; ++t)
 #pragma unroll
-      for (int qq = 0; qq < 4; ++qq) {
-        const int d0 = t * 32 + 8 * qq + 4 * g;
-        const f32x4 x = *reinterpret_cast<const f32x4*>(src + d0);
-#pragma unroll
-        for (int u = 0; u < 4; ++u) Rt[d0 + u][col] = x[u] - adv[t][4 * qq + u];
-      }
-  }
-  load_xt(1);
+    for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][cw + l32] = -adv[t][e];
+  xstore_t(1);
   __syncthreads();
 
   // dV^T[d][c] = sum_r R^T[d][r] X[r][c] for sub-block sb (X lower: r >= c)
@@ -579,8 +600,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
       }
       const int cl = chh * 32 + l32;
       const int r = J0 + sb * 64 + cl;
-      const int slot = (r & ~15) | jmap(r & 15);
-      const int lslot = (cl & ~15) | jmap(cl & 15);
+      const int lslot = sb * 64 + ((cl & ~15) | jmap(cl & 15));
       bf16* ob = dvb + ((int64_t)bh * T + r) * D;
       bf16* ou = dv_out + b * dvs.b + h * dvs.h + (int64_t)r * dvs.t;
 #pragma unroll
@@ -590,16 +610,23 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           bb[u] = (bf16)o[4 * qq + u];
-          vpth_w(dvt, bh, D, T, d0 + u, slot, bb[u]);
-          sm.u.fin.dvl[sb][cl][d0 + u] = bb[u];
-          if (sb == 1) sm.u.fin.dvtB[d0 + u][lslot] = bb[u];
+          sm.u.fin.vT[d0 + u][lslot] = bb[u];
         }
         *reinterpret_cast<bf16x4*>(ob + d0) = bb;
         *reinterpret_cast<bf16x4*>(ou + d0) = bb;
       }
     }
   };
+  // dV^T of sub-block sb to the T-perm operand copy: 16-byte stores
+  auto store_dvt = [&](int sb) {
+    for (int c = tid; c < D * 8; c += 256) {
+      const int dd = c >> 3, s8 = sb * 64 + (c & 7) * 8;
+      *reinterpret_cast<bf16x8*>(dvt + ((int64_t)bh * D + dd) * T + J0 + s8) = ld8(&sm.u.fin.vT[dd][s8]);
+    }
+  };
   diag_solve(1);
+  __syncthreads();
+  store_dvt(1);
   publish_counter(cnt, NT - (2 * p + 1));
 
   // ---- R_A -= P_BA^T dV_B: wave -> (A columns half na, B rows half kb) ----
@@ -620,8 +647,8 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
     f32x16 cr[NDT];
 #pragma unroll
     for (int t = 0; t < NDT; ++t) {
-      cr[t] = mfma32(ld8(&sm.u.fin.dvtB[t * 32 + l32][kb * 32 + 8 * g]), p0, zero16());
-      cr[t] = mfma32(ld8(&sm.u.fin.dvtB[t * 32 + l32][kb * 32 + 16 + 8 * g]), p1, cr[t]);
+      cr[t] = mfma32(ld8(&sm.u.fin.vT[t * 32 + l32][64 + kb * 32 + 8 * g]), p0, zero16());
+      cr[t] = mfma32(ld8(&sm.u.fin.vT[t * 32 + l32][64 + kb * 32 + 16 + 8 * g]), p1, cr[t]);
     }
     const int col = na * 32 + l32;
     if (kb == 1) {
@@ -630,7 +657,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
 #pragma unroll
         for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][col] -= cr[t][e];
     }
-    load_xt(0);
+    xstore_t(0);
     __syncthreads();
     if (kb == 0) {
 #pragma unroll
@@ -641,6 +668,8 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
     __syncthreads();
   }
   diag_solve(0);
+  __syncthreads();
+  store_dvt(0);
   publish_counter(cnt, NT - 2 * p);
 
   // ---- diagonal-block terms of the column sums (rows r >= columns c inside the workgroup) ----
@@ -656,7 +685,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
 #pragma unroll
       for (int st = 0; st < NKS; ++st) {
         ka[st] = ld8(kh + (int64_t)(rbase + l32) * ks.t + 16 * st + 8 * g);
-        da[st] = ld8(&sm.u.fin.dvl[rb][rh * 32 + l32][16 * st + 8 * g]);
+        da[st] = ld8(dvbh + (int64_t)(rbase + l32) * D + 16 * st + 8 * g);
       }
       float rr[16];
       load_rows16(rv + rbase, g, rr);
