@@ -382,8 +382,10 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_bw
 // last n 64-blocks of dV are published.
 // wave w owns columns J0 + 32w .. +32 (one n-tile, lane <-> column) and sweeps
 // all 64 rows of every later row tile I, so its column accumulators need no
-// cross-wave reduction.  Each later row tile (K rows, dV rows, dV^T and K^T in
-// T-perm layout, 1/rms) is staged once in LDS (double buffered):
+// cross-wave reduction.  Each later row tile (K rows, dV rows, 1/rms) is
+// staged once in LDS by direct global->LDS loads (double buffered, swizzled,
+// no registers); the transposed operands dV^T and K^T are read from the same
+// tiles with transposing LDS loads:
 //   S[I][J] = K_I . K_J, P = exp(s r_I r_J S - 1/s), G[I][J] = dV_I . V'_J
 //   acc^T[d][J] += dV^T[d][I] P[I][J];  C^T[d][J] += K^T[d][I] (r_I G P)[I][J]
 // (acc starts at -dV'^T).  Then dV_B = X_B^T R_B, dV_A = X_A^T (R_A - P_BA^T dV_B),
@@ -396,10 +398,8 @@ template <int D>
 struct PcolSmem {
   union {
     struct {
-      bf16 k[2][64][D + 8];
-      bf16 dv[2][64][D + 8];
-      bf16 dvt[2][D][72];
-      bf16 kt[2][D][72];
+      bf16 k[2][64 * D];   // swizzled tiles (chunk c of row r at c ^ (r & 7))
+      bf16 dv[2][64 * D];
       float r[2][64];
     } st;
     struct {
@@ -465,32 +465,21 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
   // ---- sweep over the later 64-row tiles, far (published first) to near ----
   const int first = NT - 1, last = 2 * p + 2;  // tiles first, first-1, ..., last
   int ready = 0;
-  bf16x8 stg[4 * CH];
-  f32x4 rstg;
-  auto gload = [&](int I) {
+  auto stage = [&](int I, int buf) {
     const int i0 = I * 64;
-    g2r_rows<D>(kh, ks.t, i0, stg);
-    g2r_rows<D>(dvbh, D, i0, stg + CH);
-    g2r_tp<D>(dvth, T, i0, stg + 2 * CH);
-    g2r_tp<D>(kth, T, i0, stg + 3 * CH);
-    if (tid < 16) rstg = *reinterpret_cast<const f32x4*>(rv + i0 + 4 * tid);
-  };
-  auto lstore = [&](int buf) {
-    r2l_rows<D>(sm.u.st.k[buf], stg);
-    r2l_rows<D>(sm.u.st.dv[buf], stg + CH);
-    r2l_tp<D>(sm.u.st.dvt[buf], stg + 2 * CH);
-    r2l_tp<D>(sm.u.st.kt[buf], stg + 3 * CH);
-    if (tid < 16) *reinterpret_cast<f32x4*>(&sm.u.st.r[buf][4 * tid]) = rstg;
+    dma_tile<64, D / 8>(kh + (int64_t)i0 * ks.t, ks.t, sm.u.st.k[buf]);
+    dma_tile<64, D / 8>(dvbh + (int64_t)i0 * D, D, sm.u.st.dv[buf]);
+    if (w == 0) dma_f32x64(rv + i0, sm.u.st.r[buf]);
   };
   // the two inverses X_A, X_B (2 x 64 x 64 fp32) into stg[0..7]: chunk u -> sub-block u >> 2
-  static_assert(4 * CH >= 8, "the staging registers also carry the two inverses");
   const float* pinv_blk = pinv + ((int64_t)bh * NT + 2 * p) * 4096;
+  f32x4 xr[8];
   auto xload = [&]() {
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int idx = tid + 256 * u;
       const int sb = idx >> 10, r = (idx >> 4) & 63, c4 = (idx & 15) * 4;
-      stg[u] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const f32x4*>(pinv_blk + sb * 4096 + r * 64 + c4));
+      xr[u] = *reinterpret_cast<const f32x4*>(pinv_blk + sb * 4096 + r * 64 + c4);
     }
   };
   auto xstore_t = [&](int sb) {
@@ -498,7 +487,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
     for (int u = 4 * sb; u < 4 * sb + 4; ++u) {
       const int idx = tid + 256 * u;
       const int r = (idx >> 4) & 63, c4 = (idx & 15) * 4;
-      const f32x4 x = __builtin_bit_cast(f32x4, stg[u]);
+      const f32x4 x = xr[u];
 #pragma unroll
       for (int e = 0; e < 4; ++e) sm.u.fin.Xt[c4 + e][r] = x[e];
     }
@@ -506,11 +495,11 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
   // tile I is published once the counter exceeds NT-1-I
   if (first >= last) {
     ready = wait_counter_gt(cnt, NT - 1 - first);
-    gload(first);
-    lstore(0);
+    stage(first, 0);
   } else {
     xload();
   }
+  dma_wait();
   __syncthreads();
   for (int I = first; I >= last; --I) {
     const int buf = (first - I) & 1;
@@ -526,7 +515,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
         }
       }
       early = need < ready;
-      if (early) gload(I - 1);
+      if (early) stage(I - 1, buf ^ 1);
     } else {
       xload();  // last tile: fetch the inverses while it is processed
     }
@@ -535,8 +524,8 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
       bf16x8 ka[NKS], da[NKS];
 #pragma unroll
       for (int st = 0; st < NKS; ++st) {
-        ka[st] = ld8(&sm.u.st.k[buf][rh * 32 + l32][16 * st + 8 * g]);
-        da[st] = ld8(&sm.u.st.dv[buf][rh * 32 + l32][16 * st + 8 * g]);
+        ka[st] = ld8(swz<D / 8>(sm.u.st.k[buf], rh * 32 + l32, 2 * st + g));
+        da[st] = ld8(swz<D / 8>(sm.u.st.dv[buf], rh * 32 + l32, 2 * st + g));
       }
       float rI[16];
       lds_rows16(&sm.u.st.r[buf][rh * 32], g, rI);
@@ -556,23 +545,21 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
       const bf16x8 mb0 = pack_b(gg, 0), mb1 = pack_b(gg, 1);
 #pragma unroll
       for (int t = 0; t < NDT; ++t) {
-        const bf16x8 a0 = ld8(&sm.u.st.dvt[buf][t * 32 + l32][rh * 32 + 8 * g]);
-        const bf16x8 a1 = ld8(&sm.u.st.dvt[buf][t * 32 + l32][rh * 32 + 16 + 8 * g]);
-        const bf16x8 k0 = ld8(&sm.u.st.kt[buf][t * 32 + l32][rh * 32 + 8 * g]);
-        const bf16x8 k1 = ld8(&sm.u.st.kt[buf][t * 32 + l32][rh * 32 + 16 + 8 * g]);
+        const bf16x8 a0 = lds_tr_a<D / 8>(sm.u.st.dv[buf], rh * 32, t * 32);
+        const bf16x8 a1 = lds_tr_a<D / 8>(sm.u.st.dv[buf], rh * 32 + 16, t * 32);
+        const bf16x8 k0 = lds_tr_a<D / 8>(sm.u.st.k[buf], rh * 32, t * 32);
+        const bf16x8 k1 = lds_tr_a<D / 8>(sm.u.st.k[buf], rh * 32 + 16, t * 32);
         adv[t] = mfma32(a0, pb0, adv[t]);
         adv[t] = mfma32(a1, pb1, adv[t]);
         acs[t] = mfma32(k0, mb0, acs[t]);
         acs[t] = mfma32(k1, mb1, acs[t]);
       }
     }
-    if (more) {
-      if (!early) {
-        ready = wait_counter_gt(cnt, NT - 1 - (I - 1));
-        gload(I - 1);
-      }
-      lstore(buf ^ 1);
+    if (more && !early) {
+      ready = wait_counter_gt(cnt, NT - 1 - (I - 1));
+      stage(I - 1, buf ^ 1);
     }
+    dma_wait();
     __syncthreads();
   }
 

@@ -172,4 +172,60 @@ __device__ __forceinline__ void r2l_tp_n(bf16 (*dst)[SLOTS + 8], const bf16x8* s
   }
 }
 
+// ---------------------------------------------------------------------------
+// Direct global -> LDS staging (gfx950 global_load_lds_dwordx4: every lane
+// fetches 16 bytes from its own address and the 64 lanes of one instruction
+// fill 1 KB of LDS contiguously from a wave-uniform base), so staged tiles
+// cost no registers and no LDS store instructions.  Tiles are unpadded; the
+// 16-byte chunk c of row r is stored at chunk c ^ (r & 7) of that row, so that
+// 16-byte reads of one chunk by 8 consecutive rows hit distinct banks.
+// All 256 threads call dma_tile; the data may be read after dma_wait() and a
+// barrier.
+// ---------------------------------------------------------------------------
+template <int ROWS, int CPR>  // CPR: 16-byte chunks per row
+__device__ __forceinline__ void dma_tile(const bf16* __restrict__ src, int64_t stride, bf16* lds) {
+  constexpr int PER_WAVE = ROWS * CPR / 256;
+  static_assert(PER_WAVE * 256 == ROWS * CPR, "tile must be a whole number of 1 KB pieces per wave");
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+  for (int i = 0; i < PER_WAVE; ++i) {
+    const int q = (w * PER_WAVE + i) * 64 + lane;
+    const int r = q / CPR, c = (q % CPR) ^ (r & 7);
+    __builtin_amdgcn_global_load_lds(src + (int64_t)r * stride + c * 8, lds + (w * PER_WAVE + i) * 512, 16, 0, 0);
+  }
+}
+// 64 consecutive fp32 values into LDS by one wave (call from a single wave)
+__device__ __forceinline__ void dma_f32x64(const float* __restrict__ src, float* lds) {
+  __builtin_amdgcn_global_load_lds(src + (threadIdx.x & 63), lds, 4, 0, 0);
+}
+// Wait until this wave's staging loads have landed in LDS.
+__device__ __forceinline__ void dma_wait() { __builtin_amdgcn_s_waitcnt(0); }
+// Address of logical chunk c (8 bf16) of row r in a swizzled tile with CPR chunks per row.
+template <int CPR>
+__device__ __forceinline__ const bf16* swz(const bf16* tile, int r, int c) {
+  return tile + r * (CPR * 8) + ((c ^ (r & 7)) << 3);
+}
+
+// MFMA A operand [m = col0 + lane%32][k = 16 rows from row0] read from a
+// swizzled row-major LDS tile (CPR 16-byte chunks per row) with two gfx950
+// transposing loads (ds_read_b64_tr_b16).  In each group of 16 lanes, source
+// lane s addresses 4 consecutive elements of row row0 + 4g + s/4 (+8 for the
+// second load) at column col0 + 16*((lane>>4)&1) + 4*(s&3); result lane j then
+// receives element j%4 of source lanes 4e + j/4, e = 0..3 (checked on an
+// MI355X), i.e. column col0 + lane%32 of rows row0 + 4g + e (+8).  Operand
+// slot 8g + e therefore holds row jmap(8g + e) -- the order in which the D
+// layout of a score tile delivers its keys -- so the result pairs with
+// pack_b() exactly like a 16-byte read from a T-perm tile.
+template <int CPR>
+__device__ __forceinline__ bf16x8 lds_tr_a(const bf16* tile, int row0, int col0) {
+  typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+  const int lane = threadIdx.x & 63, s = lane & 15;
+  const int col = col0 + 16 * ((lane >> 4) & 1) + 4 * (s & 3);
+  const int r1 = row0 + 4 * (lane >> 5) + (s >> 2);
+  const int off = (((col >> 3) ^ (r1 & 7)) << 3) | (col & 7);  // rows r1 and r1 + 8 share the swizzle
+  const bf16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(tile + r1 * (CPR * 8) + off));
+  const bf16x4 v2 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(tile + (r1 + 8) * (CPR * 8) + off));
+  return bf16x8{v1[0], v1[1], v1[2], v1[3], v2[0], v2[1], v2[2], v2[3]};
+}
+
 }  // namespace lucid
