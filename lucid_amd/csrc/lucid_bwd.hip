@@ -383,9 +383,9 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_bw
 // wave w owns columns J0 + 32w .. +32 (one n-tile, lane <-> column) and sweeps
 // all 64 rows of every later row tile I, so its column accumulators need no
 // cross-wave reduction.  Each later row tile (K rows, dV rows, 1/rms) is
-// staged once in LDS by direct global->LDS loads (double buffered, swizzled,
-// no registers); the transposed operands dV^T and K^T are read from the same
-// tiles with transposing LDS loads:
+// staged once in LDS by direct global->LDS loads (three buffers, two tiles
+// ahead, swizzled, no registers); the transposed operands dV^T and K^T are read
+// from the same tiles with transposing LDS loads:
 //   S[I][J] = K_I . K_J, P = exp(s r_I r_J S - 1/s), G[I][J] = dV_I . V'_J
 //   acc^T[d][J] += dV^T[d][I] P[I][J];  C^T[d][J] += K^T[d][I] (r_I G P)[I][J]
 // (acc starts at -dV'^T).  Then dV_B = X_B^T R_B, dV_A = X_A^T (R_A - P_BA^T dV_B),
@@ -398,9 +398,9 @@ template <int D>
 struct PcolSmem {
   union {
     struct {
-      bf16 k[2][64 * D];   // swizzled tiles (chunk c of row r at c ^ (r & 7))
-      bf16 dv[2][64 * D];
-      float r[2][64];
+      bf16 k[3][64 * D];   // swizzled tiles (chunk c of row r at c ^ (r & 7))
+      bf16 dv[3][64 * D];
+      float r[3][64];
     } st;
     struct {
       float Rt[D][132];     // R^T for the 128 columns (0..63 = A, 64..127 = B), reductions
@@ -465,11 +465,34 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
   // ---- sweep over the later 64-row tiles, far (published first) to near ----
   const int first = NT - 1, last = 2 * p + 2;  // tiles first, first-1, ..., last
   int ready = 0;
-  auto stage = [&](int I, int buf) {
-    const int i0 = I * 64;
+  // step k of the sweep stages tile first - k into buffer k % 3; the newest
+  // STAGE_OPS vector memory operations of a wave are the two tiles of a step
+  constexpr int STAGE_OPS = 2 * (64 * (D / 8) / 256);
+  const int nsteps = first - last + 1;
+  auto stage = [&](int k) {
+    const int i0 = (first - k) * 64, buf = k % 3;
+    if (w == 0) dma_f32x64(rv + i0, sm.u.st.r[buf]);
     dma_tile<64, D / 8>(kh + (int64_t)i0 * ks.t, ks.t, sm.u.st.k[buf]);
     dma_tile<64, D / 8>(dvbh + (int64_t)i0 * D, D, sm.u.st.dv[buf]);
-    if (w == 0) dma_f32x64(rv + i0, sm.u.st.r[buf]);
+  };
+  // issue the steps up to `upto` whose tiles are already published (tile I is
+  // published once the counter exceeds NT-1-I); never blocks
+  int issued = 0;
+  auto try_issue = [&](int upto) {
+    if (issued <= upto && issued < nsteps) {
+      const int need = NT - 1 - (first - issued);
+      if (need >= ready) {
+        const int seen = poll_counter(cnt);
+        if (seen > need) {
+          chain_acquire();
+          ready = seen;
+        }
+      }
+      if (need < ready) {
+        stage(issued);
+        ++issued;
+      }
+    }
   };
   // the two inverses X_A, X_B (2 x 64 x 64 fp32) into stg[0..7]: chunk u -> sub-block u >> 2
   const float* pinv_blk = pinv + ((int64_t)bh * NT + 2 * p) * 4096;
@@ -492,33 +515,19 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
       for (int e = 0; e < 4; ++e) sm.u.fin.Xt[c4 + e][r] = x[e];
     }
   };
-  // tile I is published once the counter exceeds NT-1-I
-  if (first >= last) {
+  if (nsteps > 0) {
     ready = wait_counter_gt(cnt, NT - 1 - first);
-    stage(first, 0);
+    stage(0);
+    issued = 1;
+    try_issue(1);
+    if (issued > 1) dma_wait_but<STAGE_OPS>();
+    else dma_wait();
   } else {
     xload();
   }
-  dma_wait();
   __syncthreads();
-  for (int I = first; I >= last; --I) {
-    const int buf = (first - I) & 1;
-    const bool more = I - 1 >= last;
-    bool early = false;
-    if (more) {
-      const int need = NT - 1 - (I - 1);
-      if (need >= ready) {
-        const int seen = poll_counter(cnt);
-        if (seen > need) {
-          chain_acquire();
-          ready = seen;
-        }
-      }
-      early = need < ready;
-      if (early) stage(I - 1, buf ^ 1);
-    } else {
-      xload();  // last tile: fetch the inverses while it is processed
-    }
+
+  auto sweep_tile = [&](int buf) {
 #pragma unroll
     for (int rh = 0; rh < 2; ++rh) {
       bf16x8 ka[NKS], da[NKS];
@@ -555,10 +564,24 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
         acs[t] = mfma32(k1, mb1, acs[t]);
       }
     }
-    if (more && !early) {
-      ready = wait_counter_gt(cnt, NT - 1 - (I - 1));
-      stage(I - 1, buf ^ 1);
+  };
+  // all steps but the last; the last one is peeled so that the inverses it
+  // prefetches do not hold registers through the loop
+  for (int ks_ = 0; ks_ + 1 < nsteps; ++ks_) {
+    try_issue(ks_ + 2);
+    sweep_tile(ks_ % 3);
+    if (issued == ks_ + 1) {  // the next tile was not published yet: wait for it
+      ready = wait_counter_gt(cnt, NT - 1 - (first - issued));
+      stage(issued);
+      ++issued;
     }
+    if (issued > ks_ + 2) dma_wait_but<STAGE_OPS>();  // the step after next may stay in flight
+    else dma_wait();
+    __syncthreads();
+  }
+  if (nsteps > 0) {
+    xload();  // fetch the inverses while the last tile is processed
+    sweep_tile((nsteps - 1) % 3);
     dma_wait();
     __syncthreads();
   }

@@ -200,6 +200,13 @@ __device__ __forceinline__ void dma_f32x64(const float* __restrict__ src, float*
 }
 // Wait until this wave's staging loads have landed in LDS.
 __device__ __forceinline__ void dma_wait() { __builtin_amdgcn_s_waitcnt(0); }
+// Wait until at most N of this wave's vector memory operations are outstanding
+// (the newest N may still be in flight; s_waitcnt vmcnt(N), gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void dma_wait_but() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
 // Address of logical chunk c (8 bf16) of row r in a swizzled tile with CPR chunks per row.
 template <int CPR>
 __device__ __forceinline__ const bf16* swz(const bf16* tile, int r, int c) {
