@@ -71,10 +71,11 @@ __global__ __launch_bounds__(256) void lucid_bwd_prep_kernel(const bf16* __restr
 
 // ---------------------------------------------------------------------------
 // Column sweep for the attention part.  Workgroup = 128 keys of one kv head,
-// wave w owns keys 32w..32w+31 (one n-tile, lane <-> key j); loops over the G
-// query heads of the group and over every 64-row query tile at or below the
-// diagonal.  Each query tile (Q, dO rows; Q^T, dO^T in T-perm layout; lse2 and
-// delta) is staged once per workgroup in LDS, double buffered.
+// wave w owns keys 32w..32w+31 (one n-tile, lane <-> key j); sweeps the G query
+// heads of the group and every 64-row query tile at or below the diagonal.
+// Each query tile (Q and dO rows, lse2, delta) is staged once per workgroup in
+// LDS by direct global->LDS loads (three buffers, two tiles ahead, swizzled);
+// Q^T and dO^T operands come from the same tiles through transposing LDS loads.
 //   S[i][j] = Q_i . K_j, P = exp2(c S - lse2_i)
 //   dV'^T[d][j] += dO^T[d][i] P[i][j];  dP[i][j] = dO_i . V'_j
 //   dS = P (dP - delta_i);  dK^T[d][j] += Q^T[d][i] dS[i][j]
@@ -82,23 +83,20 @@ __global__ __launch_bounds__(256) void lucid_bwd_prep_kernel(const bf16* __restr
 // ---------------------------------------------------------------------------
 template <int D>
 struct DkdvSmem {
-  bf16 q[2][64][D + 8];
-  bf16 dO[2][64][D + 8];
-  bf16 qt[2][D][72];
-  bf16 dot[2][D][72];
-  float lse[2][64];
-  float dl[2][64];
+  bf16 q[3][64 * D];   // swizzled tiles (chunk c of row r at c ^ (r & 7))
+  bf16 dO[3][64 * D];
+  float lse[3][64];
+  float dl[3][64];
 };
 
 template <int D>
 __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_bwd_dkdv_kernel(
     const bf16* __restrict__ q, Strides qs, const bf16* __restrict__ k, Strides ks, const bf16* __restrict__ vpb,
-    const bf16* __restrict__ dout, Strides dos, const bf16* __restrict__ qt, const bf16* __restrict__ dot,
-    const float* __restrict__ lse, const float* __restrict__ delta, float* __restrict__ dvp,
-    float* __restrict__ dka, int Hq, int Hkv, int T, int BH, float scale) {
+    const bf16* __restrict__ dout, Strides dos, const float* __restrict__ lse, const float* __restrict__ delta,
+    float* __restrict__ dvp, float* __restrict__ dka, int Hq, int Hkv, int T, int BH, float scale) {
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
-  constexpr int CH = D / 32;
+  constexpr int STAGE_OPS = 2 * (64 * (D / 8) / 256);  // newest vector-memory ops of a step, per wave
   __shared__ __attribute__((aligned(16))) DkdvSmem<D> sm;
   const int id = blockIdx.x;
   const int jb = id / BH, bh = id - (id / BH) * BH;
@@ -124,97 +122,84 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_bw
     adk[t] = zero16();
   }
   const int nt64 = T / 64;
-  const int it_first = jb * 2;  // first query tile any wave needs
-  const int it_w = jw / 64;     // this wave's diagonal tile
+  const int it_first = jb * 2;            // first query tile any wave needs
+  const int ntile = nt64 - it_first;      // query tiles per query head
+  const int nsteps = G * ntile;           // step s: query head s / ntile, tile it_first + s % ntile
+  const int it_w = jw / 64;               // this wave's diagonal tile
   const int kloc = jw - it_w * 64 + l32;  // this lane's key inside its diagonal tile
-  for (int gi = 0; gi < G; ++gi) {
-    const int hq = h * G + gi;
-    const int bhq = b * Hq + hq;
-    const bf16* qh = q + b * qs.b + hq * qs.h;
-    const bf16* doh = dout + b * dos.b + hq * dos.h;
-    const bf16* qth = qt + (int64_t)bhq * D * T;
-    const bf16* doth = dot + (int64_t)bhq * D * T;
-    const float* lh = lse + (int64_t)bhq * T;
-    const float* dh = delta + (int64_t)bhq * T;
-    bf16x8 stg[4 * CH];
-    f32x4 fstg;
-    auto gload = [&](int it) {
-      const int i0 = it * 64;
-      g2r_rows<D>(qh, qs.t, i0, stg);
-      g2r_rows<D>(doh, dos.t, i0, stg + CH);
-      g2r_tp<D>(qth, T, i0, stg + 2 * CH);
-      g2r_tp<D>(doth, T, i0, stg + 3 * CH);
-      if (tid < 16) fstg = *reinterpret_cast<const f32x4*>(lh + i0 + 4 * tid);
-      else if (tid < 32) fstg = *reinterpret_cast<const f32x4*>(dh + i0 + 4 * (tid - 16));
-    };
-    auto lstore = [&](int buf) {
-      r2l_rows<D>(sm.q[buf], stg);
-      r2l_rows<D>(sm.dO[buf], stg + CH);
-      r2l_tp<D>(sm.qt[buf], stg + 2 * CH);
-      r2l_tp<D>(sm.dot[buf], stg + 3 * CH);
-      if (tid < 16) *reinterpret_cast<f32x4*>(&sm.lse[buf][4 * tid]) = fstg;
-      else if (tid < 32) *reinterpret_cast<f32x4*>(&sm.dl[buf][4 * (tid - 16)]) = fstg;
-    };
-    gload(it_first);
-    lstore(0);
-    __syncthreads();
-    for (int it = it_first; it < nt64; ++it) {
-      const int buf = (it - it_first) & 1;
-      const bool more = it + 1 < nt64;
-      if (more) gload(it + 1);
-      if (it >= it_w) {
-        const bool diag = (it == it_w);
+  auto stage = [&](int s) {
+    const int gi = s / ntile, it = it_first + s - gi * ntile, buf = s % 3;
+    const int hq = h * G + gi, bhq = b * Hq + hq, i0 = it * 64;
+    if (w == 0) dma_f32x64(lse + (int64_t)bhq * T + i0, sm.lse[buf]);
+    if (w == 1) dma_f32x64(delta + (int64_t)bhq * T + i0, sm.dl[buf]);
+    dma_tile<64, D / 8>(q + b * qs.b + hq * qs.h + (int64_t)i0 * qs.t, qs.t, sm.q[buf]);
+    dma_tile<64, D / 8>(dout + b * dos.b + hq * dos.h + (int64_t)i0 * dos.t, dos.t, sm.dO[buf]);
+  };
+  stage(0);
+  if (nsteps > 1) {
+    stage(1);
+    dma_wait_but<STAGE_OPS>();
+  } else {
+    dma_wait();
+  }
+  __syncthreads();
+  for (int s = 0; s < nsteps; ++s) {
+    const int buf = s % 3;
+    if (s + 2 < nsteps) stage(s + 2);
+    const int it = it_first + s % ntile;
+    if (it >= it_w) {
+      const bool diag = (it == it_w);
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
-          if (diag && mt * 32 + 31 < kloc - l32) continue;  // rows all above this wave's keys
-          float lr[16];
-          lds_rows16(&sm.lse[buf][mt * 32], g, lr);
-          f32x16 pv;
-          bf16x8 pb0, pb1;
-          {
-            bf16x8 qa[NKS];
+      for (int mt = 0; mt < 2; ++mt) {
+        if (diag && mt * 32 + 31 < kloc - l32) continue;  // rows all above this wave's keys
+        float lr[16];
+        lds_rows16(&sm.lse[buf][mt * 32], g, lr);
+        f32x16 pv;
+        bf16x8 pb0, pb1;
+        {
+          bf16x8 qa[NKS];
 #pragma unroll
-            for (int st = 0; st < NKS; ++st) qa[st] = ld8(&sm.q[buf][mt * 32 + l32][16 * st + 8 * g]);
-            f32x16 sc = zero16();
+          for (int st = 0; st < NKS; ++st) qa[st] = ld8(swz<D / 8>(sm.q[buf], mt * 32 + l32, 2 * st + g));
+          f32x16 sc = zero16();
 #pragma unroll
-            for (int st = 0; st < NKS; ++st) sc = mfma32(qa[st], kb[st], sc);
+          for (int st = 0; st < NKS; ++st) sc = mfma32(qa[st], kb[st], sc);
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-              float p = __builtin_amdgcn_exp2f(fmaf(sc[e], c, -lr[e]));
-              if (diag && (mt * 32 + drow(e, g) < kloc)) p = 0.f;
-              pv[e] = p;
-            }
-            pb0 = pack_b(pv, 0);
-            pb1 = pack_b(pv, 1);
+          for (int e = 0; e < 16; ++e) {
+            float p = __builtin_amdgcn_exp2f(fmaf(sc[e], c, -lr[e]));
+            if (diag && (mt * 32 + drow(e, g) < kloc)) p = 0.f;
+            pv[e] = p;
           }
+          pb0 = pack_b(pv, 0);
+          pb1 = pack_b(pv, 1);
+        }
 #pragma unroll
-          for (int t = 0; t < NDT; ++t) {
-            adv[t] = mfma32(ld8(&sm.dot[buf][t * 32 + l32][mt * 32 + 8 * g]), pb0, adv[t]);
-            adv[t] = mfma32(ld8(&sm.dot[buf][t * 32 + l32][mt * 32 + 16 + 8 * g]), pb1, adv[t]);
-          }
-          lds_rows16(&sm.dl[buf][mt * 32], g, lr);
-          {
-            bf16x8 da[NKS];
+        for (int t = 0; t < NDT; ++t) {
+          adv[t] = mfma32(lds_tr_a<D / 8>(sm.dO[buf], mt * 32, t * 32), pb0, adv[t]);
+          adv[t] = mfma32(lds_tr_a<D / 8>(sm.dO[buf], mt * 32 + 16, t * 32), pb1, adv[t]);
+        }
+        lds_rows16(&sm.dl[buf][mt * 32], g, lr);
+        {
+          bf16x8 da[NKS];
 #pragma unroll
-            for (int st = 0; st < NKS; ++st) da[st] = ld8(&sm.dO[buf][mt * 32 + l32][16 * st + 8 * g]);
-            f32x16 dp = zero16();
+          for (int st = 0; st < NKS; ++st) da[st] = ld8(swz<D / 8>(sm.dO[buf], mt * 32 + l32, 2 * st + g));
+          f32x16 dp = zero16();
 #pragma unroll
-            for (int st = 0; st < NKS; ++st) dp = mfma32(da[st], vb[st], dp);
+          for (int st = 0; st < NKS; ++st) dp = mfma32(da[st], vb[st], dp);
 #pragma unroll
-            for (int e = 0; e < 16; ++e) dp[e] = pv[e] * (dp[e] - lr[e]);
-            pb0 = pack_b(dp, 0);
-            pb1 = pack_b(dp, 1);
-          }
+          for (int e = 0; e < 16; ++e) dp[e] = pv[e] * (dp[e] - lr[e]);
+          pb0 = pack_b(dp, 0);
+          pb1 = pack_b(dp, 1);
+        }
 #pragma unroll
-          for (int t = 0; t < NDT; ++t) {
-            adk[t] = mfma32(ld8(&sm.qt[buf][t * 32 + l32][mt * 32 + 8 * g]), pb0, adk[t]);
-            adk[t] = mfma32(ld8(&sm.qt[buf][t * 32 + l32][mt * 32 + 16 + 8 * g]), pb1, adk[t]);
-          }
+        for (int t = 0; t < NDT; ++t) {
+          adk[t] = mfma32(lds_tr_a<D / 8>(sm.q[buf], mt * 32, t * 32), pb0, adk[t]);
+          adk[t] = mfma32(lds_tr_a<D / 8>(sm.q[buf], mt * 32 + 16, t * 32), pb1, adk[t]);
         }
       }
-      if (more) lstore(buf ^ 1);
-      __syncthreads();
     }
+    if (s + 2 < nsteps) dma_wait_but<STAGE_OPS>();  // the step after next may stay in flight
+    else dma_wait();
+    __syncthreads();
   }
   float* ov = dvp + ((int64_t)bh * T + jrow) * D;
   float* ok = dka + ((int64_t)bh * T + jrow) * D;

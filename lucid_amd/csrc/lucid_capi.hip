@@ -157,7 +157,7 @@ int launch_bwd(const void* dout, const int64_t* dos, const void* q, const int64_
   LUCID_LAUNCH("lucid_bwd_prep_kernel", lucid::lucid_bwd_prep_kernel<D>, dim3(T / 64, BHq), st, (const bf16*)dout,
                S(dos), (const bf16*)o, S(os), (const bf16*)q, S(qs), Hq, T, w.delta, w.dot, w.qt, w.counters, BH);
   LUCID_LAUNCH("lucid_attn_bwd_dkdv_kernel", lucid::lucid_attn_bwd_dkdv_kernel<D>, dim3((T / 128) * BH), st,
-               (const bf16*)q, S(qs), (const bf16*)k, S(ks), f.vpb, (const bf16*)dout, S(dos), w.qt, w.dot, lse,
+               (const bf16*)q, S(qs), (const bf16*)k, S(ks), f.vpb, (const bf16*)dout, S(dos), lse,
                w.delta, w.dvp, w.dka, Hq, Hkv, T, BH, scale);
   LUCID_LAUNCH("lucid_attn_bwd_dq_kernel", lucid::lucid_attn_bwd_dq_kernel<D>, dim3(((T + 255) / 256) * BHq), st,
                (const bf16*)q, S(qs), (const bf16*)k, S(ks), f.vpb, (const bf16*)dout, S(dos), f.kt, lse, w.delta,
