@@ -99,7 +99,7 @@ __global__ __launch_bounds__(256) void lucid_prep_kernel(const bf16* __restrict_
 //
 // The earlier keys are swept in pairs of 64-key tiles (128 keys per barrier):
 // K rows, V'^T (T-perm) and 1/rms of the pair are staged once per workgroup in
-// LDS, double buffered, with coalesced 16-byte loads.
+// LDS by direct global->LDS loads (double buffered, swizzled, no registers).
 // wave w: ih = w & 1 -> rows i0 + 64*ih .. +64 (two 32-row n-tiles, lane <-> row)
 //         kh = w >> 1 -> the 64-key tile 2*pair + kh of every staged pair
 //   acc^T[d][i] += V'^T[d][j] P^T[j][i],  P^T[j][i] = exp(s r_i r_j K_j.K_i - 1/s)
@@ -115,8 +115,8 @@ template <int D>
 struct PfwdSmem {
   union {
     struct {
-      bf16 k[2][128][D + 8];
-      bf16 v[2][D][128 + 8];
+      bf16 k[2][128 * D];  // swizzled tiles (chunk c of row r at c ^ (r & 7))
+      bf16 v[2][D * 128];
       float r[2][128];
     } st;
     struct {
@@ -135,9 +135,6 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
     bf16* __restrict__ vpt, float* __restrict__ pinv, int* __restrict__ counters) {
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
-  constexpr int SK = 128 * D / 2048;  // 16-byte chunks per thread of a staged 128-key K tile
-  constexpr int SV = D * 128 / 2048;  // ... and of the V'^T tile
-  static_assert(SK + SV >= 8, "the staging registers also carry the two 64x64 fp32 inverses");
   __shared__ __attribute__((aligned(16))) PfwdSmem<D> sm;
 
   const int id = blockIdx.x;
@@ -199,28 +196,24 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
   }
 
   // ---- off-diagonal sweep over the i2 earlier pairs of 64-key tiles ----
-  // pair pp (keys 128pp .. 128pp+127) is complete once the counter exceeds 2pp+1
+  // pair pp (keys 128pp .. 128pp+127) is complete once the counter exceeds 2pp+1;
+  // it is staged into buffer pp & 1 by direct global->LDS loads
   const int npair = i2;
   int ready = 0;
-  bf16x8 stg[SK + SV];
-  f32x4 rstg;
-  auto gload = [&](int pp) {
-    g2r_rows_n<D, 128>(kp, ks.t, pp * 128, stg);
-    g2r_tp_n<D, 128>(vpth, T, pp * 128, stg + SK);
-    if (tid < 32) rstg = *reinterpret_cast<const f32x4*>(rv + pp * 128 + 4 * tid);
+  auto stage = [&](int pp) {
+    const int buf = pp & 1;
+    if (w < 2) dma_f32x64(rv + pp * 128 + 64 * w, &sm.u.st.r[buf][64 * w]);
+    dma_tile<128, D / 8>(kp + (int64_t)pp * 128 * ks.t, ks.t, sm.u.st.k[buf]);
+    dma_tile<D, 16>(vpth + pp * 128, T, sm.u.st.v[buf]);
   };
-  auto lstore = [&](int buf) {
-    r2l_rows_n<D, 128>(sm.u.st.k[buf], stg);
-    r2l_tp_n<D, 128>(sm.u.st.v[buf], stg + SK);
-    if (tid < 32) *reinterpret_cast<f32x4*>(&sm.u.st.r[buf][4 * tid]) = rstg;
-  };
-  // the two inverses X_A, X_B (2 x 64 x 64 fp32) into stg[0..7]: chunk u -> sub-block u >> 2
+  // the two inverses X_A, X_B (2 x 64 x 64 fp32): chunk u -> sub-block u >> 2
+  f32x4 xr[8];
   auto xload = [&]() {
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int idx = tid + 256 * u;
       const int sb = idx >> 10, r = (idx >> 4) & 63, c4 = (idx & 15) * 4;
-      stg[u] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const f32x4*>(pinv_blk + sb * 4096 + r * 64 + c4));
+      xr[u] = *reinterpret_cast<const f32x4*>(pinv_blk + sb * 4096 + r * 64 + c4);
     }
   };
   auto xstore = [&](int sb) {
@@ -228,41 +221,16 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
     for (int u = 4 * sb; u < 4 * sb + 4; ++u) {
       const int idx = tid + 256 * u;
       const int r = (idx >> 4) & 63, c4 = (idx & 15) * 4;
-      *reinterpret_cast<f32x4*>(&sm.u.fin.X[r][c4]) = __builtin_bit_cast(f32x4, stg[u]);
+      *reinterpret_cast<f32x4*>(&sm.u.fin.X[r][c4]) = xr[u];
     }
   };
-  if (npair > 0) {
-    ready = wait_counter_gt(cnt, 1);
-    gload(0);
-    lstore(0);
-  } else {
-    xload();
-  }
-  __syncthreads();
-  for (int pp = 0; pp < npair; ++pp) {
-    const int buf = pp & 1;
-    const bool more = pp + 1 < npair;
-    bool early = false;
-    if (more) {
-      const int need = 2 * pp + 3;
-      if (need >= ready) {
-        const int seen = poll_counter(cnt);
-        if (seen > need) {
-          chain_acquire();
-          ready = seen;
-        }
-      }
-      early = need < ready;
-      if (early) gload(pp + 1);
-    } else {
-      xload();  // last pair: fetch the inverses while it is processed
-    }
+  auto sweep_pair = [&](int buf) {
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
       const int key0 = kh * 64 + mt * 32;
       bf16x8 ka[NKS];
 #pragma unroll
-      for (int st = 0; st < NKS; ++st) ka[st] = ld8(&sm.u.st.k[buf][key0 + l32][16 * st + 8 * g]);
+      for (int st = 0; st < NKS; ++st) ka[st] = ld8(swz<D / 8>(sm.u.st.k[buf], key0 + l32, 2 * st + g));
       float rj[16];
       lds_rows16(&sm.u.st.r[buf][key0], g, rj);
       bf16x8 pb[2][2];
@@ -278,8 +246,8 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
       }
 #pragma unroll
       for (int t = 0; t < NDT; ++t) {
-        const bf16x8 va0 = ld8(&sm.u.st.v[buf][t * 32 + l32][key0 + 8 * g]);
-        const bf16x8 va1 = ld8(&sm.u.st.v[buf][t * 32 + l32][key0 + 16 + 8 * g]);
+        const bf16x8 va0 = ld8(swz<16>(sm.u.st.v[buf], t * 32 + l32, key0 / 8 + g));
+        const bf16x8 va1 = ld8(swz<16>(sm.u.st.v[buf], t * 32 + l32, key0 / 8 + 2 + g));
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) {
           acc[t][nt] = mfma32(va0, pb[nt][0], acc[t][nt]);
@@ -287,13 +255,39 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
         }
       }
     }
-    if (more) {
-      if (!early) {
-        ready = wait_counter_gt(cnt, 2 * pp + 3);
-        gload(pp + 1);
+  };
+  if (npair > 0) {
+    ready = wait_counter_gt(cnt, 1);
+    stage(0);
+    dma_wait();
+  } else {
+    xload();
+  }
+  __syncthreads();
+  // all pairs but the last; the last one is peeled so that the inverses it
+  // prefetches do not hold registers through the loop
+  for (int pp = 0; pp + 1 < npair; ++pp) {
+    const int need = 2 * pp + 3;  // pair pp + 1 is complete once the counter exceeds this
+    if (need >= ready) {
+      const int seen = poll_counter(cnt);
+      if (seen > need) {
+        chain_acquire();
+        ready = seen;
       }
-      lstore(buf ^ 1);
     }
+    const bool early = need < ready;
+    if (early) stage(pp + 1);
+    sweep_pair(pp & 1);
+    if (!early) {
+      ready = wait_counter_gt(cnt, need);
+      stage(pp + 1);
+    }
+    dma_wait();
+    __syncthreads();
+  }
+  if (npair > 0) {
+    xload();  // fetch the inverses while the last pair is processed
+    sweep_pair((npair - 1) & 1);
     __syncthreads();
   }
 
