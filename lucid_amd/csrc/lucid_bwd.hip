@@ -725,17 +725,17 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
 // backward and the attention dK.  No chain: every dV is known.
 // Workgroup = 128 rows; wave w: ih = w & 1 -> rows 64*ih .. +64 (lane <-> row),
 // jh = w >> 1 -> keys 32*jh .. +32 of every staged 64-key tile J
-// (K rows, V' rows, K^T in T-perm layout, 1/rms), double buffered in LDS:
+// (K rows, V' rows, 1/rms; direct global->LDS loads, three buffers, two tiles
+// ahead; K^T operands through transposing LDS loads):
 //   S^T[J][I] = K_J . K_I, G^T[J][I] = V'_J . dV_I, R^T[d][I] += K^T[d][J] (r_J G P)^T[J][I]
 // ---------------------------------------------------------------------------
 template <int D>
 struct ProwSmem {
   union {
     struct {
-      bf16 k[2][64][D + 8];
-      bf16 v[2][64][D + 8];
-      bf16 kt[2][D][72];
-      float r[2][64];
+      bf16 k[3][64 * D];  // swizzled tiles (chunk c of row r at c ^ (r & 7))
+      bf16 v[3][64 * D];
+      float r[3][64];
     } st;
     float Rt[D][132];
   } u;
@@ -784,36 +784,29 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
     acc[t][1] = zero16();
   }
   const int ntile = 2 * p + 2;  // key tiles 0 .. 2p+1 (the last two are this workgroup's own blocks)
-  bf16x8 stg[3 * CH];
-  f32x4 rstg;
-  auto gload = [&](int J) {
-    const int j0 = J * 64;
-    g2r_rows<D>(kh, ks.t, j0, stg);
-    g2r_rows<D>(vh, D, j0, stg + CH);
-    g2r_tp<D>(kth, T, j0, stg + 2 * CH);
-    if (tid < 16) rstg = *reinterpret_cast<const f32x4*>(rv + j0 + 4 * tid);
+  constexpr int STAGE_OPS = 2 * (64 * (D / 8) / 256);  // newest vector-memory ops of a step, per wave
+  auto stage = [&](int J) {
+    const int j0 = J * 64, buf = J % 3;
+    if (w == 0) dma_f32x64(rv + j0, sm.u.st.r[buf]);
+    dma_tile<64, D / 8>(kh + (int64_t)j0 * ks.t, ks.t, sm.u.st.k[buf]);
+    dma_tile<64, D / 8>(vh + (int64_t)j0 * D, D, sm.u.st.v[buf]);
   };
-  auto lstore = [&](int buf) {
-    r2l_rows<D>(sm.u.st.k[buf], stg);
-    r2l_rows<D>(sm.u.st.v[buf], stg + CH);
-    r2l_tp<D>(sm.u.st.kt[buf], stg + 2 * CH);
-    if (tid < 16) *reinterpret_cast<f32x4*>(&sm.u.st.r[buf][4 * tid]) = rstg;
-  };
-  gload(0);
-  lstore(0);
+  stage(0);
+  stage(1);  // ntile >= 2
+  dma_wait_but<STAGE_OPS>();
   __syncthreads();
   // this wave's rows start at 64-block index 2p + ih; key tiles after it are fully masked
   const int last_w = 2 * p + ih;
   for (int J = 0; J < ntile; ++J) {
-    const int buf = J & 1;
-    const bool more = J + 1 < ntile;
+    const int buf = J % 3;
+    if (J + 2 < ntile) stage(J + 2);
     if (J <= last_w) {
       const bool diag = (J == last_w);
       bf16x8 ka[NKS], va[NKS];
 #pragma unroll
       for (int st = 0; st < NKS; ++st) {
-        ka[st] = ld8(&sm.u.st.k[buf][jh * 32 + l32][16 * st + 8 * g]);
-        va[st] = ld8(&sm.u.st.v[buf][jh * 32 + l32][16 * st + 8 * g]);
+        ka[st] = ld8(swz<D / 8>(sm.u.st.k[buf], jh * 32 + l32, 2 * st + g));
+        va[st] = ld8(swz<D / 8>(sm.u.st.v[buf], jh * 32 + l32, 2 * st + g));
       }
       float rJ[16];
       lds_rows16(&sm.u.st.r[buf][jh * 32], g, rJ);
@@ -837,8 +830,8 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
       }
 #pragma unroll
       for (int t = 0; t < NDT; ++t) {
-        const bf16x8 k0 = ld8(&sm.u.st.kt[buf][t * 32 + l32][jh * 32 + 8 * g]);
-        const bf16x8 k1 = ld8(&sm.u.st.kt[buf][t * 32 + l32][jh * 32 + 16 + 8 * g]);
+        const bf16x8 k0 = lds_tr_a<D / 8>(sm.u.st.k[buf], jh * 32, t * 32);
+        const bf16x8 k1 = lds_tr_a<D / 8>(sm.u.st.k[buf], jh * 32 + 16, t * 32);
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) {
           acc[t][nt] = mfma32(k0, mb[nt][0], acc[t][nt]);
@@ -846,10 +839,8 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
         }
       }
     }
-    if (more) {
-      gload(J + 1);
-      lstore(buf ^ 1);
-    }
+    if (J + 2 < ntile) dma_wait_but<STAGE_OPS>();  // the step after next may stay in flight
+    else dma_wait();
     __syncthreads();
   }
   float(*Rt)[132] = sm.u.Rt;
