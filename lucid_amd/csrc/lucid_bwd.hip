@@ -127,13 +127,16 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_bw
   const int nsteps = G * ntile;           // step s: query head s / ntile, tile it_first + s % ntile
   const int it_w = jw / 64;               // this wave's diagonal tile
   const int kloc = jw - it_w * 64 + l32;  // this lane's key inside its diagonal tile
+  int plan_q[64 * (D / 8) / 256], plan_o[64 * (D / 8) / 256];
+  dma_plan<64, D / 8>(qs.t, plan_q);
+  dma_plan<64, D / 8>(dos.t, plan_o);
   auto stage = [&](int s) {
     const int gi = s / ntile, it = it_first + s - gi * ntile, buf = s % 3;
     const int hq = h * G + gi, bhq = b * Hq + hq, i0 = it * 64;
     if (w == 0) dma_f32x64(lse + (int64_t)bhq * T + i0, sm.lse[buf]);
     if (w == 1) dma_f32x64(delta + (int64_t)bhq * T + i0, sm.dl[buf]);
-    dma_tile<64, D / 8>(q + b * qs.b + hq * qs.h + (int64_t)i0 * qs.t, qs.t, sm.q[buf]);
-    dma_tile<64, D / 8>(dout + b * dos.b + hq * dos.h + (int64_t)i0 * dos.t, dos.t, sm.dO[buf]);
+    dma_stage<64, D / 8>(plan_q, q + b * qs.b + hq * qs.h + (int64_t)i0 * qs.t, sm.q[buf]);
+    dma_stage<64, D / 8>(plan_o, dout + b * dos.b + hq * dos.h + (int64_t)i0 * dos.t, sm.dO[buf]);
   };
   stage(0);
   if (nsteps > 1) {
@@ -220,16 +223,16 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_bw
 
 // ---------------------------------------------------------------------------
 // Row sweep for dQ.  Workgroup = 256 query rows (heavy blocks first), wave w
-// owns rows 64w..64w+63 (lane <-> row i).  Every key tile (K rows, V' rows,
-// K^T in T-perm layout) is staged once per workgroup in LDS.
+// owns rows 64w..64w+63 (lane <-> row i).  Every key tile (K rows, V' rows) is
+// staged once per workgroup in LDS by direct global->LDS loads (three buffers,
+// two tiles ahead); K^T operands come through transposing LDS loads.
 //   S^T[j][i] = K_j . Q_i, dP^T[j][i] = V'_j . dO_i, dS^T = P^T (dP^T - delta_i)
 //   dQ^T[d][i] += K^T[d][j] dS^T[j][i]
 // ---------------------------------------------------------------------------
 template <int D>
 struct DqSmem {
-  bf16 k[2][64][D + 8];
-  bf16 v[2][64][D + 8];
-  bf16 kt[2][D][72];
+  bf16 k[3][64 * D];  // swizzled tiles (chunk c of row r at c ^ (r & 7))
+  bf16 v[3][64 * D];
 };
 
 template <int D>
@@ -279,25 +282,26 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_bw
   }
   const int ntile = (min(r0 + 256, T) + 63) / 64;
   const int last_w = row0 / 64;
-  bf16x8 stg[3 * CH];
-  auto gload = [&](int jt) {
-    const int j0 = jt * 64;
-    g2r_rows<D>(kh, ks.t, j0, stg);
-    g2r_rows<D>(vh, D, j0, stg + CH);
-    g2r_tp<D>(kth, T, j0, stg + 2 * CH);
+  constexpr int STAGE_OPS = 2 * (64 * (D / 8) / 256);  // newest vector-memory ops of a step, per wave
+  int plan_k[64 * (D / 8) / 256], plan_v[64 * (D / 8) / 256];
+  dma_plan<64, D / 8>(ks.t, plan_k);
+  dma_plan<64, D / 8>(D, plan_v);
+  auto stage = [&](int jt) {
+    const int j0 = jt * 64, buf = jt % 3;
+    dma_stage<64, D / 8>(plan_k, kh + (int64_t)j0 * ks.t, sm.k[buf]);
+    dma_stage<64, D / 8>(plan_v, vh + (int64_t)j0 * D, sm.v[buf]);
   };
-  auto lstore = [&](int buf) {
-    r2l_rows<D>(sm.k[buf], stg);
-    r2l_rows<D>(sm.v[buf], stg + CH);
-    r2l_tp<D>(sm.kt[buf], stg + 2 * CH);
-  };
-  gload(0);
-  lstore(0);
+  stage(0);
+  if (ntile > 1) {
+    stage(1);
+    dma_wait_but<STAGE_OPS>();
+  } else {
+    dma_wait();
+  }
   __syncthreads();
   for (int jt = 0; jt < ntile; ++jt) {
-    const int buf = jt & 1;
-    const bool more = jt + 1 < ntile;
-    if (more) gload(jt + 1);
+    const int buf = jt % 3;
+    if (jt + 2 < ntile) stage(jt + 2);
     if (jt <= last_w && row0 < T) {
       const bool diag = (jt == last_w);
 #pragma unroll
@@ -305,8 +309,8 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_bw
         bf16x8 ka[NKS], va[NKS];
 #pragma unroll
         for (int st = 0; st < NKS; ++st) {
-          ka[st] = ld8(&sm.k[buf][mt * 32 + l32][16 * st + 8 * g]);
-          va[st] = ld8(&sm.v[buf][mt * 32 + l32][16 * st + 8 * g]);
+          ka[st] = ld8(swz<D / 8>(sm.k[buf], mt * 32 + l32, 2 * st + g));
+          va[st] = ld8(swz<D / 8>(sm.v[buf], mt * 32 + l32, 2 * st + g));
         }
         bf16x8 dsb[2][2];
 #pragma unroll
@@ -328,8 +332,8 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_bw
         }
 #pragma unroll
         for (int t = 0; t < NDT; ++t) {
-          const bf16x8 a0 = ld8(&sm.kt[buf][t * 32 + l32][mt * 32 + 8 * g]);
-          const bf16x8 a1 = ld8(&sm.kt[buf][t * 32 + l32][mt * 32 + 16 + 8 * g]);
+          const bf16x8 a0 = lds_tr_a<D / 8>(sm.k[buf], mt * 32, t * 32);
+          const bf16x8 a1 = lds_tr_a<D / 8>(sm.k[buf], mt * 32 + 16, t * 32);
 #pragma unroll
           for (int nt = 0; nt < 2; ++nt) {
             acc[t][nt] = mfma32(a0, dsb[nt][0], acc[t][nt]);
@@ -338,7 +342,8 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_bw
         }
       }
     }
-    if (more) lstore(buf ^ 1);
+    if (jt + 2 < ntile) dma_wait_but<STAGE_OPS>();  // the step after next may stay in flight
+    else dma_wait();
     __syncthreads();
   }
 #pragma unroll
@@ -454,11 +459,14 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
   // STAGE_OPS vector memory operations of a wave are the two tiles of a step
   constexpr int STAGE_OPS = 2 * (64 * (D / 8) / 256);
   const int nsteps = first - last + 1;
+  int plan_k[64 * (D / 8) / 256], plan_d[64 * (D / 8) / 256];
+  dma_plan<64, D / 8>(ks.t, plan_k);
+  dma_plan<64, D / 8>(D, plan_d);
   auto stage = [&](int k) {
     const int i0 = (first - k) * 64, buf = k % 3;
     if (w == 0) dma_f32x64(rv + i0, sm.u.st.r[buf]);
-    dma_tile<64, D / 8>(kh + (int64_t)i0 * ks.t, ks.t, sm.u.st.k[buf]);
-    dma_tile<64, D / 8>(dvbh + (int64_t)i0 * D, D, sm.u.st.dv[buf]);
+    dma_stage<64, D / 8>(plan_k, kh + (int64_t)i0 * ks.t, sm.u.st.k[buf]);
+    dma_stage<64, D / 8>(plan_d, dvbh + (int64_t)i0 * D, sm.u.st.dv[buf]);
   };
   // issue the steps up to `upto` whose tiles are already published (tile I is
   // published once the counter exceeds NT-1-I); never blocks
@@ -785,11 +793,14 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
   }
   const int ntile = 2 * p + 2;  // key tiles 0 .. 2p+1 (the last two are this workgroup's own blocks)
   constexpr int STAGE_OPS = 2 * (64 * (D / 8) / 256);  // newest vector-memory ops of a step, per wave
+  int plan_k[64 * (D / 8) / 256], plan_v[64 * (D / 8) / 256];
+  dma_plan<64, D / 8>(ks.t, plan_k);
+  dma_plan<64, D / 8>(D, plan_v);
   auto stage = [&](int J) {
     const int j0 = J * 64, buf = J % 3;
     if (w == 0) dma_f32x64(rv + j0, sm.u.st.r[buf]);
-    dma_tile<64, D / 8>(kh + (int64_t)j0 * ks.t, ks.t, sm.u.st.k[buf]);
-    dma_tile<64, D / 8>(vh + (int64_t)j0 * D, D, sm.u.st.v[buf]);
+    dma_stage<64, D / 8>(plan_k, kh + (int64_t)j0 * ks.t, sm.u.st.k[buf]);
+    dma_stage<64, D / 8>(plan_v, vh + (int64_t)j0 * D, sm.u.st.v[buf]);
   };
   stage(0);
   stage(1);  // ntile >= 2

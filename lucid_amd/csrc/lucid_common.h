@@ -194,6 +194,28 @@ __device__ __forceinline__ void dma_tile(const bf16* __restrict__ src, int64_t s
     __builtin_amdgcn_global_load_lds(src + (int64_t)r * stride + c * 8, lds + (w * PER_WAVE + i) * 512, 16, 0, 0);
   }
 }
+// dma_tile split in two: the per-lane element offsets for a fixed row stride
+// (dma_plan, once per kernel) and the loads of one tile (dma_stage).
+template <int ROWS, int CPR>
+__device__ __forceinline__ void dma_plan(int64_t stride, int* off) {
+  constexpr int PER_WAVE = ROWS * CPR / 256;
+  static_assert(PER_WAVE * 256 == ROWS * CPR, "tile must be a whole number of 1 KB pieces per wave");
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+  for (int i = 0; i < PER_WAVE; ++i) {
+    const int q = (w * PER_WAVE + i) * 64 + lane;
+    const int r = q / CPR, c = (q % CPR) ^ (r & 7);
+    off[i] = (int)(r * stride) + c * 8;
+  }
+}
+template <int ROWS, int CPR>
+__device__ __forceinline__ void dma_stage(const int* off, const bf16* __restrict__ src, bf16* lds) {
+  constexpr int PER_WAVE = ROWS * CPR / 256;
+  const int w = threadIdx.x >> 6;
+#pragma unroll
+  for (int i = 0; i < PER_WAVE; ++i)
+    __builtin_amdgcn_global_load_lds(src + off[i], lds + (w * PER_WAVE + i) * 512, 16, 0, 0);
+}
 // 64 consecutive fp32 values into LDS by one wave (call from a single wave)
 __device__ __forceinline__ void dma_f32x64(const float* __restrict__ src, float* lds) {
   __builtin_amdgcn_global_load_lds(src + (threadIdx.x & 63), lds, 4, 0, 0);

@@ -200,11 +200,14 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
   // it is staged into buffer pp & 1 by direct global->LDS loads
   const int npair = i2;
   int ready = 0;
+  int plan_k[128 * (D / 8) / 256], plan_v[D * 16 / 256];
+  dma_plan<128, D / 8>(ks.t, plan_k);
+  dma_plan<D, 16>(T, plan_v);
   auto stage = [&](int pp) {
     const int buf = pp & 1;
     if (w < 2) dma_f32x64(rv + pp * 128 + 64 * w, &sm.u.st.r[buf][64 * w]);
-    dma_tile<128, D / 8>(kp + (int64_t)pp * 128 * ks.t, ks.t, sm.u.st.k[buf]);
-    dma_tile<D, 16>(vpth + pp * 128, T, sm.u.st.v[buf]);
+    dma_stage<128, D / 8>(plan_k, kp + (int64_t)pp * 128 * ks.t, sm.u.st.k[buf]);
+    dma_stage<D, 16>(plan_v, vpth + pp * 128, sm.u.st.v[buf]);
   };
   // the two inverses X_A, X_B (2 x 64 x 64 fp32): chunk u -> sub-block u >> 2
   f32x4 xr[8];
