@@ -8,7 +8,7 @@
 //   dK^ = -s (M K^ + M^T K^),  dK = r (dK^ - K^ (K^.dK^)/d) + dK_attn   (RMSNorm backward)
 //
 // Kernels:
-//   lucid_bwd_prep_kernel          delta = rowsum(dO * O), dO^T and Q^T in T-perm layout
+//   lucid_bwd_prep_kernel          delta = rowsum(dO * O), zero the chain counters
 //   lucid_attn_bwd_dkdv_kernel     column sweep: dV' (summed over the GQA group), dK_attn
 //   lucid_attn_bwd_dq_kernel       row sweep: dQ
 //   lucid_precond_bwd_col_kernel   chained transposed solve -> dV, and the M^T K^ column sums
@@ -17,17 +17,13 @@
 
 namespace lucid {
 
-// grid (T/64, B*Hq)
+// delta[bhq][t] = dO_t . O_t; zero the chain counters.  grid (T/64, B*Hq)
 template <int D>
 __global__ __launch_bounds__(256) void lucid_bwd_prep_kernel(const bf16* __restrict__ dout, Strides dos,
-                                                             const bf16* __restrict__ o, Strides os,
-                                                             const bf16* __restrict__ q, Strides qs, int Hq, int T,
-                                                             float* __restrict__ delta, bf16* __restrict__ dot,
-                                                             bf16* __restrict__ qt, int* __restrict__ counters,
+                                                             const bf16* __restrict__ o, Strides os, int Hq, int T,
+                                                             float* __restrict__ delta, int* __restrict__ counters,
                                                              int BH) {
   constexpr int SEG = D / 4;
-  __shared__ bf16 tdo[D][64 + 8];
-  __shared__ bf16 tq[D][64 + 8];
   const int blk = blockIdx.x, bhq = blockIdx.y;
   const int b = bhq / Hq, hq = bhq - b * Hq;
   const int tid = threadIdx.x;
@@ -35,38 +31,18 @@ __global__ __launch_bounds__(256) void lucid_bwd_prep_kernel(const bf16* __restr
   const int t = blk * 64 + row;
   const bf16* dop = dout + b * dos.b + hq * dos.h + (int64_t)t * dos.t;
   const bf16* opp = o + b * os.b + hq * os.h + (int64_t)t * os.t;
-  const bf16* qp = q + b * qs.b + hq * qs.h + (int64_t)t * qs.t;
   float acc = 0.f;
 #pragma unroll
   for (int c = 0; c < SEG; c += 8) {
     const bf16x8 a = ld8(dop + seg * SEG + c);
     const bf16x8 bo = ld8(opp + seg * SEG + c);
-    const bf16x8 qq = ld8(qp + seg * SEG + c);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      acc += (float)a[e] * (float)bo[e];
-      tdo[seg * SEG + c + e][row] = a[e];
-      tq[seg * SEG + c + e][row] = qq[e];
-    }
+    for (int e = 0; e < 8; ++e) acc += (float)a[e] * (float)bo[e];
   }
   acc += __shfl_xor(acc, 1, 64);
   acc += __shfl_xor(acc, 2, 64);
   if (seg == 0) delta[(int64_t)bhq * T + t] = acc;
   if (blk == 0 && tid == 0 && bhq < BH) counters[bhq] = 0;
-  __syncthreads();
-  for (int idx = tid; idx < D * 8; idx += 256) {
-    const int dd = idx >> 3, c8 = idx & 7;
-    bf16x8 a, bq;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int src = (c8 >> 1) * 16 + jmap((c8 & 1) * 8 + e);
-      a[e] = tdo[dd][src];
-      bq[e] = tq[dd][src];
-    }
-    const int64_t off = ((int64_t)bhq * D + dd) * T + blk * 64 + c8 * 8;
-    *reinterpret_cast<bf16x8*>(dot + off) = a;
-    *reinterpret_cast<bf16x8*>(qt + off) = bq;
-  }
 }
 
 // ---------------------------------------------------------------------------
@@ -238,7 +214,7 @@ struct DqSmem {
 template <int D>
 __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_bwd_dq_kernel(
     const bf16* __restrict__ q, Strides qs, const bf16* __restrict__ k, Strides ks, const bf16* __restrict__ vpb,
-    const bf16* __restrict__ dout, Strides dos, const bf16* __restrict__ kt, const float* __restrict__ lse,
+    const bf16* __restrict__ dout, Strides dos, const float* __restrict__ lse,
     const float* __restrict__ delta, bf16* __restrict__ dq, Strides dqs, int Hq, int Hkv, int T, int BHq,
     float scale) {
   constexpr int NDT = D / 32;
@@ -258,8 +234,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_bw
   const int row0 = r0 + w * 64;
   const bf16* kh = k + b * ks.b + h * ks.h;
   const bf16* vh = vpb + (int64_t)bh * T * D;
-  const bf16* kth = kt + (int64_t)bh * D * T;
-  const float c = scale * LOG2E_F;
+    const float c = scale * LOG2E_F;
 
   bf16x8 qb[2][NKS], db[2][NKS];
   float li[2], di[2];
@@ -381,7 +356,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_bw
 // (acc starts at -dV'^T).  Then dV_B = X_B^T R_B, dV_A = X_A^T (R_A - P_BA^T dV_B),
 // R = dV' - acc, and the diagonal-block terms of C.  The chain's critical path
 // is the work after the last tile becomes visible, so dV' and both inverses
-// are loaded earlier and dV^T is stored with coalesced 16-byte writes.  At
+// are loaded earlier.  At
 // d = 64 two workgroups share a CU (LDS <= 80 KB, <= 256 registers per lane).
 // ---------------------------------------------------------------------------
 template <int D>
@@ -404,7 +379,7 @@ template <int D>
 __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond_bwd_col_kernel(
     const bf16* __restrict__ k, Strides ks, int Hkv, int T, int BH, const float* __restrict__ rinv, float scale,
     const bf16* __restrict__ kt, const bf16* __restrict__ vpb, const float* __restrict__ pinv,
-    const float* __restrict__ dvp, bf16* __restrict__ dvb, bf16* __restrict__ dvt, bf16* __restrict__ dv_out,
+    const float* __restrict__ dvp, bf16* __restrict__ dvb, bf16* __restrict__ dv_out,
     Strides dvs, float* __restrict__ colsum, int* __restrict__ counters) {
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
@@ -422,7 +397,6 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
   const bf16* kh = k + b * ks.b + h * ks.h;
   const float* rv = rinv + (int64_t)bh * T;
   const bf16* kth = kt + (int64_t)bh * D * T;
-  const bf16* dvth = dvt + (int64_t)bh * D * T;
   const bf16* dvbh = dvb + (int64_t)bh * T * D;
   const bf16* vph = vpb + (int64_t)bh * T * D;
   int* cnt = counters + bh;
@@ -620,16 +594,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
       }
     }
   };
-  // dV^T of sub-block sb to the T-perm operand copy: 16-byte stores
-  auto store_dvt = [&](int sb) {
-    for (int c = tid; c < D * 8; c += 256) {
-      const int dd = c >> 3, s8 = sb * 64 + (c & 7) * 8;
-      *reinterpret_cast<bf16x8*>(dvt + ((int64_t)bh * D + dd) * T + J0 + s8) = ld8(&sm.u.fin.vT[dd][s8]);
-    }
-  };
   diag_solve(1);
-  __syncthreads();
-  store_dvt(1);
   publish_counter(cnt, NT - (2 * p + 1));
 
   // ---- R_A -= P_BA^T dV_B: wave -> (A columns half na, B rows half kb) ----
@@ -671,8 +636,6 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
     __syncthreads();
   }
   diag_solve(0);
-  __syncthreads();
-  store_dvt(0);
   publish_counter(cnt, NT - 2 * p);
 
   // ---- diagonal-block terms of the column sums (rows r >= columns c inside the workgroup) ----
@@ -752,7 +715,7 @@ struct ProwSmem {
 template <int D>
 __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond_bwd_row_kernel(
     const bf16* __restrict__ k, Strides ks, int Hkv, int T, int BH, const float* __restrict__ rinv, float scale,
-    const bf16* __restrict__ kt, const bf16* __restrict__ vpb, const bf16* __restrict__ dvb,
+    const bf16* __restrict__ vpb, const bf16* __restrict__ dvb,
     const float* __restrict__ colsum, const float* __restrict__ dka, bf16* __restrict__ dk_out, Strides dks) {
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
@@ -768,7 +731,6 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
   const int I0 = p * 128;
   const bf16* kh = k + b * ks.b + h * ks.h;
   const float* rv = rinv + (int64_t)bh * T;
-  const bf16* kth = kt + (int64_t)bh * D * T;
   const bf16* vh = vpb + (int64_t)bh * T * D;
   const float sl2 = scale * LOG2E_F;
   const float c0 = LOG2E_F / scale;

@@ -63,12 +63,9 @@ FwdWs carve_fwd(void* base, int B, int Hkv, int T, int D) {
 
 struct BwdWs {
   float* delta;  // [BHq][T]
-  bf16* dot;     // [BHq][D][T]  dO^T, T-perm
-  bf16* qt;      // [BHq][D][T]  Q^T, T-perm
   float* dvp;    // [BH][T][D]   dV' (summed over the group)
   float* dka;    // [BH][T][D]   dK from the softmax part (scaled)
   bf16* dvb;     // [BH][T][D]   dV bf16
-  bf16* dvt;     // [BH][D][T]   dV^T, T-perm
   float* colsum; // [BH][T][D]   sum_I M_IJ^T K^_I
   int* counters; // [BH]
   size_t bytes;
@@ -85,12 +82,9 @@ BwdWs carve_bwd(void* base, int B, int Hq, int Hkv, int T, int D) {
     return r;
   };
   w.delta = reinterpret_cast<float*>(take(BHq * T * 4));
-  w.dot = reinterpret_cast<bf16*>(take(BHq * D * T * 2));
-  w.qt = reinterpret_cast<bf16*>(take(BHq * D * T * 2));
   w.dvp = reinterpret_cast<float*>(take(BH * T * D * 4));
   w.dka = reinterpret_cast<float*>(take(BH * T * D * 4));
   w.dvb = reinterpret_cast<bf16*>(take(BH * T * D * 2));
-  w.dvt = reinterpret_cast<bf16*>(take(BH * D * T * 2));
   w.colsum = reinterpret_cast<float*>(take(BH * T * D * 4));
   w.counters = reinterpret_cast<int*>(take(BH * 4));
   w.bytes = off;
@@ -155,18 +149,18 @@ int launch_bwd(const void* dout, const int64_t* dos, const void* q, const int64_
                int Hq, int Hkv, int T, float scale, hipStream_t st) {
   const int BH = B * Hkv, BHq = B * Hq;
   LUCID_LAUNCH("lucid_bwd_prep_kernel", lucid::lucid_bwd_prep_kernel<D>, dim3(T / 64, BHq), st, (const bf16*)dout,
-               S(dos), (const bf16*)o, S(os), (const bf16*)q, S(qs), Hq, T, w.delta, w.dot, w.qt, w.counters, BH);
+               S(dos), (const bf16*)o, S(os), Hq, T, w.delta, w.counters, BH);
   LUCID_LAUNCH("lucid_attn_bwd_dkdv_kernel", lucid::lucid_attn_bwd_dkdv_kernel<D>, dim3((T / 128) * BH), st,
                (const bf16*)q, S(qs), (const bf16*)k, S(ks), f.vpb, (const bf16*)dout, S(dos), lse,
                w.delta, w.dvp, w.dka, Hq, Hkv, T, BH, scale);
   LUCID_LAUNCH("lucid_attn_bwd_dq_kernel", lucid::lucid_attn_bwd_dq_kernel<D>, dim3(((T + 255) / 256) * BHq), st,
-               (const bf16*)q, S(qs), (const bf16*)k, S(ks), f.vpb, (const bf16*)dout, S(dos), f.kt, lse, w.delta,
+               (const bf16*)q, S(qs), (const bf16*)k, S(ks), f.vpb, (const bf16*)dout, S(dos), lse, w.delta,
                (bf16*)dq, S(dqs), Hq, Hkv, T, BHq, scale);
   LUCID_LAUNCH("lucid_precond_bwd_col_kernel", lucid::lucid_precond_bwd_col_kernel<D>, dim3((T / 128) * BH), st,
-               (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, scale, f.kt, f.vpb, f.pinv, w.dvp, w.dvb, w.dvt,
+               (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, scale, f.kt, f.vpb, f.pinv, w.dvp, w.dvb,
                (bf16*)dv, S(dvs), w.colsum, w.counters);
   LUCID_LAUNCH("lucid_precond_bwd_row_kernel", lucid::lucid_precond_bwd_row_kernel<D>, dim3((T / 128) * BH), st,
-               (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, scale, f.kt, f.vpb, w.dvb, w.colsum, w.dka, (bf16*)dk,
+               (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, scale, f.vpb, w.dvb, w.colsum, w.dka, (bf16*)dk,
                S(dks));
   return LUCID_OK;
 }
