@@ -377,19 +377,24 @@ __global__ __launch_bounds__(256) void path_bwd_row_kernel(const bf16* __restric
 }
 
 // ---------------------------------------------------------------------------
-// Column sweep (parallel_path_bwd_inter_dkv.py, parallel_path_bwd_intra.py): per key
-// chunk J, query chunks I > J.  wave w: ch = w & 1 -> keys 32*ch (lane <-> key j),
-// ih = w >> 1 -> rows 32*ih of each staged query tile.
+// Column sweep (parallel_path_bwd_inter_dkv.py, parallel_path_bwd_intra.py): per
+// pair of key chunks J1 = 2*blockIdx.x, J2 = J1 + 1 (one large chunk), query chunks
+// I > J.  Wave w owns keys 32w .. 32w+31 of the pair (chunk Jw = J1 + w/2, lane <->
+// key j) and sweeps all 64 rows of every query tile, so its accumulators need no
+// cross-wave reduction.
 //   S[i][j] = Qop_I . Kop_J, dP[i][j] = dV_I . O_J, dA = -s dP * exp(s S - 1/s)
 //   dKop^T[d][j] += Qop^T[d][i] dA[i][j]   (Kop = k~_J for I in J's large chunk, else KL_J)
-// Then d k~_J = dk~(same) + dKL SUF_J and dSUF_J = dKL^T k~_J.  grid (NT, B*HQ)
+// Query tiles (the shared QB^(s) rows for later large chunks, or QS^(J1), QS^(J2)
+// rows inside the large chunk) and dV rows are staged by direct global->LDS loads
+// (three buffers, two tiles ahead); Qop^T comes through transposing LDS reads.
+// Then d k~_J = dk~(same) + dKL SUF_J and dSUF_J = dKL^T k~_J.  grid (ceil(NT/2), B*HQ)
 // ---------------------------------------------------------------------------
 struct ColSmem {
   union {
     struct {
-      bf16 q[64][72];
-      bf16 dv[64][72];
-      bf16 qt[64][72];
+      bf16 qa[3][64 * 64];  // swizzled (chunk c of row r at c ^ (r & 7))
+      bf16 qb[3][64 * 64];
+      bf16 dv[3][64 * 64];
     } st;
     struct {
       float a[64][68];  // d k~ (same large chunk), then the result
@@ -399,120 +404,144 @@ struct ColSmem {
   } u;
 };
 
-__global__ __launch_bounds__(256) void path_bwd_col_kernel(const bf16* __restrict__ o, Strides os, int HQ, int H,
-                                                           int T, float scale, PathFwdWs ws, PathBwdWs bw) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void path_bwd_col_kernel(
+    const bf16* __restrict__ o, Strides os, int HQ, int H, int T, float scale, PathFwdWs ws, PathBwdWs bw) {
   __shared__ __attribute__((aligned(16))) ColSmem sm;
   const int NT = T / PC, NS = (NT + PR - 1) / PR;
-  const int J = blockIdx.x, bhq = blockIdx.y;
+  const int J1 = 2 * blockIdx.x, bhq = blockIdx.y;
   const int G_ = HQ / H;
   const int b = bhq / HQ, hq = bhq - b * HQ, bh = b * H + hq / G_;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
-  const int ch = w & 1, ih = w >> 1;
-  const int sJ = J / PR, ceJ = min(sJ * PR + PR, NT) - 1;
-  const int j0 = J * PC;
+  const int Jw = J1 + (w >> 1);        // this wave's key chunk
+  const bool live = Jw < NT;           // NT odd: the last pair has one chunk
+  const int sJ = J1 / PR, cb = sJ * PR, ceJ = min(cb + PR, NT) - 1;
   const float sl2 = scale * LOG2E_F, cc0 = LOG2E_F / scale;
 
   bf16x8 kbs[4], kbf[4], ob[4];
-#pragma unroll
-  for (int st = 0; st < 4; ++st) {
-    const int jr = j0 + ch * 32 + l32;
-    kbs[st] = ld8(ws.kt + ((int64_t)bh * T + jr) * 64 + 16 * st + 8 * g);
-    kbf[st] = ld8(ws.kl + ((int64_t)bh * T + jr) * 64 + 16 * st + 8 * g);
-    ob[st] = ld8(o + b * os.b + hq * os.h + (int64_t)jr * os.t + 16 * st + 8 * g);
-  }
-  f32x16 as_[2] = {zero16(), zero16()}, af[2] = {zero16(), zero16()};
-  bf16x8 stg[6];
-  auto gload = [&](int I) {
-    const bool same = I <= ceJ;
-    const bf16* qr = same ? ws.qs + ((int64_t)bhq * PR + (J - sJ * PR)) * T * 64
-                          : ws.qb + ((int64_t)bhq * NS + sJ) * T * 64;
-    const bf16* qtp = same ? ws.qsT + ((int64_t)bhq * PR + (J - sJ * PR)) * 64 * T
-                           : ws.qbT + ((int64_t)bhq * NS + sJ) * 64 * T;
-    g2r_rows<64>(qr, 64, I * PC, stg);
-    g2r_rows<64>(bw.dvb + (int64_t)bhq * T * 64, 64, I * PC, stg + 2);
-    g2r_tp<64>(qtp, T, I * PC, stg + 4);
-  };
-  if (J + 1 < NT) gload(J + 1);
-  for (int I = J + 1; I < NT; ++I) {
-    r2l_rows<64>(sm.u.st.q, stg);
-    r2l_rows<64>(sm.u.st.dv, stg + 2);
-    r2l_tp<64>(sm.u.st.qt, stg + 4);
-    __syncthreads();
-    if (I + 1 < NT) gload(I + 1);
-    const bool same = I <= ceJ;
-    f32x16 sc = zero16(), dp = zero16();
+  {
+    const int jr = min(J1 * PC + 32 * w + l32, T - 1);
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
-      sc = mfma32(ld8(&sm.u.st.q[ih * 32 + l32][16 * st + 8 * g]), same ? kbs[st] : kbf[st], sc);
-      dp = mfma32(ld8(&sm.u.st.dv[ih * 32 + l32][16 * st + 8 * g]), ob[st], dp);
+      kbs[st] = ld8(ws.kt + ((int64_t)bh * T + jr) * 64 + 16 * st + 8 * g);
+      kbf[st] = ld8(ws.kl + ((int64_t)bh * T + jr) * 64 + 16 * st + 8 * g);
+      ob[st] = ld8(o + b * os.b + hq * os.h + (int64_t)jr * os.t + 16 * st + 8 * g);
     }
+  }
+  f32x16 as_[2] = {zero16(), zero16()}, af[2] = {zero16(), zero16()};
+
+  // step k stages query tile I = J1 + 1 + k
+  const int nsteps = NT - 1 - J1;
+  // newest vector-memory ops of a step, per wave: 3 tiles inside J's large chunk, 2 beyond
+  auto near = [&](int k) { return J1 + 1 + k <= ceJ; };
+  int plan_r[2];
+  dma_plan<64, 8>(64, plan_r);
+  auto stage = [&](int k) {
+    const int I = J1 + 1 + k, buf = k % 3;
+    const bool same = I <= ceJ;
+    const bf16* q1 = same ? ws.qs + ((int64_t)bhq * PR + (J1 - cb)) * T * 64
+                          : ws.qb + ((int64_t)bhq * NS + sJ) * T * 64;
+    dma_stage<64, 8>(plan_r, q1 + (int64_t)I * PC * 64, sm.u.st.qa[buf]);
+    dma_stage<64, 8>(plan_r, bw.dvb + ((int64_t)bhq * T + I * PC) * 64, sm.u.st.dv[buf]);
+    if (same)  // the second chunk of the pair has its own query operand inside the large chunk
+      dma_stage<64, 8>(plan_r, ws.qs + ((int64_t)bhq * PR + (J1 + 1 - cb)) * T * 64 + (int64_t)I * PC * 64,
+                       sm.u.st.qb[buf]);
+  };
+  if (nsteps > 0) {
+    stage(0);
+    if (nsteps > 1) {
+      stage(1);
+      if (near(1)) dma_wait_but<6>();
+      else dma_wait_but<4>();
+    } else {
+      dma_wait();
+    }
+  }
+  __syncthreads();
+  for (int k = 0; k < nsteps; ++k) {
+    const int buf = k % 3;
+    if (k + 2 < nsteps) stage(k + 2);
+    const int I = J1 + 1 + k;
+    if (live && I > Jw) {
+      const bool same = I <= ceJ;
+      const bf16* qt = (w >= 2 && same) ? sm.u.st.qb[buf] : sm.u.st.qa[buf];
 #pragma unroll
-    for (int e = 0; e < 16; ++e) sc[e] = -scale * dp[e] * __builtin_amdgcn_exp2f(fmaf(sc[e], sl2, -cc0));
-    const bf16x8 d0 = pack_b(sc, 0), d1 = pack_b(sc, 1);
+      for (int rh = 0; rh < 2; ++rh) {
+        f32x16 sc = zero16(), dp = zero16();
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const bf16x8 a0 = ld8(&sm.u.st.qt[t * 32 + l32][ih * 32 + 8 * g]);
-      const bf16x8 a1 = ld8(&sm.u.st.qt[t * 32 + l32][ih * 32 + 16 + 8 * g]);
-      if (same) {
-        as_[t] = mfma32(a0, d0, as_[t]);
-        as_[t] = mfma32(a1, d1, as_[t]);
-      } else {
-        af[t] = mfma32(a0, d0, af[t]);
-        af[t] = mfma32(a1, d1, af[t]);
+        for (int st = 0; st < 4; ++st) {
+          sc = mfma32(ld8(swz<8>(qt, rh * 32 + l32, 2 * st + g)), same ? kbs[st] : kbf[st], sc);
+          dp = mfma32(ld8(swz<8>(sm.u.st.dv[buf], rh * 32 + l32, 2 * st + g)), ob[st], dp);
+        }
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sc[e] = -scale * dp[e] * __builtin_amdgcn_exp2f(fmaf(sc[e], sl2, -cc0));
+        const bf16x8 d0 = pack_b(sc, 0), d1 = pack_b(sc, 1);
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const bf16x8 a0 = lds_tr_a<8>(qt, rh * 32, t * 32);
+          const bf16x8 a1 = lds_tr_a<8>(qt, rh * 32 + 16, t * 32);
+          if (same) {
+            as_[t] = mfma32(a0, d0, as_[t]);
+            as_[t] = mfma32(a1, d1, as_[t]);
+          } else {
+            af[t] = mfma32(a0, d0, af[t]);
+            af[t] = mfma32(a1, d1, af[t]);
+          }
+        }
       }
+    }
+    if (k + 2 < nsteps) {  // the step after next may stay in flight
+      if (near(k + 2)) dma_wait_but<6>();
+      else dma_wait_but<4>();
+    } else {
+      dma_wait();
     }
     __syncthreads();
   }
-  // ---- reduce the two row halves: fin.a = dk~(same), fin.f = dKL (rows j, cols d) ----
-  if (ih == 1) {
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        sm.u.fin.a[ch * 32 + l32][t * 32 + drow(e, g)] = as_[t][e];
-        sm.u.fin.f[ch * 32 + l32][t * 32 + drow(e, g)] = af[t][e];
-      }
-  }
-  __syncthreads();
-  if (ih == 0) {
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        sm.u.fin.a[ch * 32 + l32][t * 32 + drow(e, g)] += as_[t][e];
-        sm.u.fin.f[ch * 32 + l32][t * 32 + drow(e, g)] += af[t][e];
-      }
-  }
-  load_mat64<false>(sm.u.fin.m, ws.suf + ((int64_t)bh * NT + J) * 4096);
-  __syncthreads();
+  // ---- per chunk of the pair: d k~_J = dk~(same) + dKL SUF_J, dSUF_J = dKL^T k~_J ----
   const int r0 = (tid >> 4) * 4, c0 = (tid & 15) * 4;
-  float acc4[4][4];
-  zero44(acc4);
-  lds_gemm64<false, false>(sm.u.fin.f, sm.u.fin.m, acc4);  // dKL SUF
-  {
-    float* dst = bw.dkt + ((int64_t)bhq * T + j0) * 64;
+  for (int half = 0; half < 2; ++half) {
+    const int J = J1 + half;
+    if (J >= NT) break;
+    if ((w >> 1) == half) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      f32x4 v;
+      for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) v[j] = acc4[i][j] + sm.u.fin.a[r0 + i][c0 + j];
-      *reinterpret_cast<f32x4*>(dst + (r0 + i) * 64 + c0) = v;
+        for (int e = 0; e < 16; ++e) {
+          sm.u.fin.a[(w & 1) * 32 + l32][t * 32 + drow(e, g)] = as_[t][e];
+          sm.u.fin.f[(w & 1) * 32 + l32][t * 32 + drow(e, g)] = af[t][e];
+        }
     }
-  }
-  __syncthreads();
-  load_rows64_f32(sm.u.fin.m, ws.kt + ((int64_t)bh * T + j0) * 64, 64);
-  __syncthreads();
-  zero44(acc4);
-  lds_gemm64<true, false>(sm.u.fin.f, sm.u.fin.m, acc4);  // dSUF = dKL^T k~
-  {
-    float* dst = bw.dsuf + ((int64_t)bhq * NT + J) * 4096;
+    load_mat64<false>(sm.u.fin.m, ws.suf + ((int64_t)bh * NT + J) * 4096);
+    __syncthreads();
+    float acc4[4][4];
+    zero44(acc4);
+    lds_gemm64<false, false>(sm.u.fin.f, sm.u.fin.m, acc4);  // dKL SUF
+    {
+      float* dst = bw.dkt + ((int64_t)bhq * T + J * PC) * 64;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      f32x4 v;
+      for (int i = 0; i < 4; ++i) {
+        f32x4 v;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) v[j] = acc4[i][j];
-      *reinterpret_cast<f32x4*>(dst + (r0 + i) * 64 + c0) = v;
+        for (int j = 0; j < 4; ++j) v[j] = acc4[i][j] + sm.u.fin.a[r0 + i][c0 + j];
+        *reinterpret_cast<f32x4*>(dst + (r0 + i) * 64 + c0) = v;
+      }
     }
+    __syncthreads();
+    load_rows64_f32(sm.u.fin.m, ws.kt + ((int64_t)bh * T + J * PC) * 64, 64);
+    __syncthreads();
+    zero44(acc4);
+    lds_gemm64<true, false>(sm.u.fin.f, sm.u.fin.m, acc4);  // dSUF = dKL^T k~
+    {
+      float* dst = bw.dsuf + ((int64_t)bhq * NT + J) * 4096;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        f32x4 v;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = acc4[i][j];
+        *reinterpret_cast<f32x4*>(dst + (r0 + i) * 64 + c0) = v;
+      }
+    }
+    __syncthreads();
   }
 }
 

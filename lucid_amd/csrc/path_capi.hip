@@ -201,7 +201,7 @@ int lucid_path_bwd(const void* dout, const int64_t* do_strides, const void* q, c
                      (const bf16*)o, PS(o_strides), HQ, H, T, BHq, scale, ws, bw);
   LUCID_TIMED_LAUNCH(phip, "path_bwd_row_kernel", lucid::path_bwd_row_kernel, dim3(NT, BHq), st, (const bf16*)o, PS(o_strides),
                      HQ, H, T, scale, ws, bw);
-  LUCID_TIMED_LAUNCH(phip, "path_bwd_col_kernel", lucid::path_bwd_col_kernel, dim3(NT, BHq), st, (const bf16*)o, PS(o_strides),
+  LUCID_TIMED_LAUNCH(phip, "path_bwd_col_kernel", lucid::path_bwd_col_kernel, dim3((NT + 1) / 2, BHq), st, (const bf16*)o, PS(o_strides),
                      HQ, H, T, scale, ws, bw);
   LUCID_TIMED_LAUNCH(phip, "path_products_bwd_kernel", lucid::path_products_bwd_kernel, dim3(NS, BHq), st, HQ, H, T, ws, bw);
   LUCID_TIMED_LAUNCH(phip, "path_wy_bwd_kernel", lucid::path_wy_bwd_kernel, dim3(NT, BHq), st, (const bf16*)q, PS(q_strides),

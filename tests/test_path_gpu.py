@@ -83,7 +83,8 @@ def test_path_full_size_residual():
         assert res.abs().max().item() <= 5 * TOL, f"row {i}: residual {res.abs().max().item():.3e}"
 
 
-@pytest.mark.parametrize("B,T,H,G", [(1, 256, 2, 1), (1, 1024, 1, 2), (2, 640, 1, 1), (1, 200, 1, 1)])
+@pytest.mark.parametrize("B,T,H,G", [(1, 256, 2, 1), (1, 1024, 1, 2), (2, 640, 1, 1), (1, 200, 1, 1),
+                                     (1, 576, 1, 1)])  # 9 chunks: an odd chunk count spanning two large chunks
 def test_path_backward_matches_oracle(B, T, H, G):
     from lucid_amd.lucid_path import parallel_lucid_path_attention
     q, k, v, w, beta, do = _inputs(B, T, H, G, seed=3 * T + G)
