@@ -218,68 +218,63 @@ __global__ __launch_bounds__(256) void path_dv_kernel(const bf16* __restrict__ d
 }
 
 // ---------------------------------------------------------------------------
-// Row sweep (parallel_path_bwd_inter_dqh.py, parallel_path_bwd_intra.py): per query
-// chunk I, key chunks J ascending.  G accumulates d(query operand):
+// Row sweep (parallel_path_bwd_inter_dqh.py, parallel_path_bwd_intra.py): per pair
+// of query chunks I1 = 2*blockIdx.x, I2 = I1 + 1 (one large chunk), key chunks J
+// ascending.  G accumulates d(query operand):
 //   G^T[d][i] += Kop^T[d][j] dA^T[j][i]
 // and at every change of query operand X (large-chunk boundary: X = QB^(s), M = HL_s;
-// inside I's large chunk: X = QS^(c), M = Hc_c):  dM += X^T G,  G <- G M^T.
-// Finally d q~_I = G.  wave w: ih = w & 1 -> rows 32*ih (lane <-> row i),
-// jh = w >> 1 -> keys 32*jh; partial G of the two key halves is summed in LDS at
-// every transport step.  grid (NT, B*HQ)
+// inside the large chunk: X = QS^(c), M = Hc_c):  dM += X^T G,  G <- G M^T.
+// Finally d q~ = G.  Wave w owns rows 32w..32w+31 of the pair (chunk I1 + w/2,
+// lane <-> row i) and all 64 keys of every key tile; key-operand and O rows are
+// staged by direct global->LDS loads (double buffered), Kop^T comes through
+// transposing LDS reads.  The pair's dM contributions are summed over its 128 rows
+// before the atomic adds.  grid (ceil(NT/2), B*HQ)
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void path_bwd_row_kernel(const bf16* __restrict__ o, Strides os, int HQ, int H,
-                                                           int T, float scale, PathFwdWs ws, PathBwdWs bw) {
-  __shared__ __attribute__((aligned(16))) bf16 lk[64][72];
-  __shared__ __attribute__((aligned(16))) bf16 lo[64][72];
-  __shared__ __attribute__((aligned(16))) bf16 lkt[64][72];
-  __shared__ __attribute__((aligned(16))) float Gs[64][68];  // full G (rows i, cols d)
-  __shared__ __attribute__((aligned(16))) float Ms[64][68];  // transport matrix M (rows)
+struct RowSmem {
+  bf16 k[2][64 * 64];  // swizzled (chunk c of row r at c ^ (r & 7))
+  bf16 o[2][64 * 64];
+  float g[128][68];    // G rows of the pair at a transport step
+};
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void path_bwd_row_kernel(
+    const bf16* __restrict__ o, Strides os, int HQ, int H, int T, float scale, PathFwdWs ws, PathBwdWs bw) {
+  __shared__ __attribute__((aligned(16))) RowSmem sm;
   const int NT = T / PC, NS = (NT + PR - 1) / PR;
-  const int I = blockIdx.x, bhq = blockIdx.y;
+  const int I1 = 2 * blockIdx.x, bhq = blockIdx.y;
   const int G_ = HQ / H;
   const int b = bhq / HQ, hq = bhq - b * HQ, bh = b * H + hq / G_;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
-  const int ih = w & 1, jh = w >> 1;
-  const int sI = I / PR, cb = sI * PR;
-  const int i0 = I * PC;
+  const int Iw = I1 + (w >> 1);                     // this wave's query chunk
+  const bool pair = I1 + 1 < NT;                    // NT odd: the last pair has one chunk
+  const int sI = I1 / PR, cb = sI * PR;
+  const int iw0 = min(Iw, NT - 1) * PC + (w & 1) * 32;  // first row of this wave
+  const int nJ = pair ? I1 + 1 : I1;                // key tiles needed by the pair
   const float sl2 = scale * LOG2E_F, cc0 = LOG2E_F / scale;
 
   bf16x8 dvr[4];
 #pragma unroll
-  for (int st = 0; st < 4; ++st) dvr[st] = ld8(bw.dvb + ((int64_t)bhq * T + i0 + ih * 32 + l32) * 64 + 16 * st + 8 * g);
+  for (int st = 0; st < 4; ++st) dvr[st] = ld8(bw.dvb + ((int64_t)bhq * T + iw0 + l32) * 64 + 16 * st + 8 * g);
   f32x16 acc[2] = {zero16(), zero16()};
 
-  // ---- G (sum of the two key halves) -> Gs ----
-  auto gather_G = [&]() {
-    if (jh == 1) {
+  // ---- dM += X^T G over the pair's rows (atomic) and G <- G M^T for each wave's rows ----
+  auto transition = [&](int J, const bf16* XT, const float* M, float* dM) {
+    const bool act = Iw < NT && J < Iw;
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) Gs[ih * 32 + l32][t * 32 + drow(e, g)] = acc[t][e];
-    }
+      for (int e = 0; e < 16; ++e) sm.g[32 * w + l32][t * 32 + drow(e, g)] = act ? acc[t][e] : 0.f;
     __syncthreads();
-    if (jh == 0) {
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) Gs[ih * 32 + l32][t * 32 + drow(e, g)] += acc[t][e];
-    }
-    __syncthreads();
-  };
-  // ---- dM += X^T G (atomic) and G <- G M^T ----
-  auto transition = [&](const bf16* XT, const float* M, float* dM) {
-    gather_G();
-    load_mat64<false>(Ms, M);
     {
       const int at = w >> 1, bt = w & 1;  // dM tile (a rows, b cols)
       f32x16 dm = zero16();
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const bf16x8 xa = ld8(XT + (int64_t)(at * 32 + l32) * T + i0 + 16 * ks + 8 * g);
+      // rows of a chunk that has left the sweep are skipped: its X rows may be undefined
+      const int ks0 = (J < I1) ? 0 : 4, ks1 = (pair && J < I1 + 1) ? 8 : 4;
+      for (int ks = ks0; ks < ks1; ++ks) {
+        const bf16x8 xa = ld8(XT + (int64_t)(at * 32 + l32) * T + I1 * PC + 16 * ks + 8 * g);
         bf16x8 gh, gl;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const float x = Gs[16 * ks + jmap(8 * g + e)][bt * 32 + l32];
+          const float x = sm.g[16 * ks + jmap(8 * g + e)][bt * 32 + l32];
           gh[e] = (bf16)x;
           gl[e] = (bf16)(x - (float)gh[e]);
         }
@@ -289,90 +284,91 @@ __global__ __launch_bounds__(256) void path_bwd_row_kernel(const bf16* __restric
 #pragma unroll
       for (int e = 0; e < 16; ++e) unsafeAtomicAdd(dM + (at * 32 + drow(e, g)) * 64 + bt * 32 + l32, dm[e]);
     }
-    __syncthreads();
-    f32x16 gn;
-    {
-      const int bt = w >> 1, it = w & 1;  // new G^T tile (b rows, i cols)
-      gn = zero16();
+    if (act) {
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        bf16x8 ah, al, bh8, bl;
-        split8(&Ms[bt * 32 + l32][16 * ks + 8 * g], ah, al);
-        split8(&Gs[it * 32 + l32][16 * ks + 8 * g], bh8, bl);
-        gn = mfma32(ah, bh8, gn);
-        gn = mfma32(ah, bl, gn);
-        gn = mfma32(al, bh8, gn);
+      for (int bt = 0; bt < 2; ++bt) {
+        f32x16 gn = zero16();
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          bf16x8 ah, al, bh8, bl;
+          split8(M + (bt * 32 + l32) * 64 + 16 * ks + 8 * g, ah, al);
+          split8(&sm.g[32 * w + l32][16 * ks + 8 * g], bh8, bl);
+          gn = mfma32(ah, bh8, gn);
+          gn = mfma32(ah, bl, gn);
+          gn = mfma32(al, bh8, gn);
+        }
+        acc[bt] = gn;
       }
     }
     __syncthreads();
-    {
-      const int bt = w >> 1, it = w & 1;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) Gs[it * 32 + l32][bt * 32 + drow(e, g)] = gn[e];
-    }
-    __syncthreads();
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[t][e] = (jh == 0) ? Gs[ih * 32 + l32][t * 32 + drow(e, g)] : 0.f;
   };
 
-  bf16x8 qb[4];
-  bf16x8 stg[6];
-  auto gload = [&](int J) {
-    const bool far = J < cb;
-    const bf16* kr = (far ? ws.kl : ws.kt) + (int64_t)bh * T * 64;
-    const bf16* ktp = (far ? ws.klT : ws.ktT) + (int64_t)bh * 64 * T;
-    g2r_rows<64>(kr, 64, J * PC, stg);
-    g2r_rows<64>(o + b * os.b + hq * os.h, os.t, J * PC, stg + 2);
-    g2r_tp<64>(ktp, T, J * PC, stg + 4);
+  int plan_k[2], plan_o[2];
+  dma_plan<64, 8>(64, plan_k);
+  dma_plan<64, 8>(os.t, plan_o);
+  auto stage = [&](int J) {
+    const int buf = J & 1;
+    const bf16* kr = ((J < cb) ? ws.kl : ws.kt) + ((int64_t)bh * T + J * PC) * 64;
+    dma_stage<64, 8>(plan_k, kr, sm.k[buf]);
+    dma_stage<64, 8>(plan_o, o + b * os.b + hq * os.h + (int64_t)J * PC * os.t, sm.o[buf]);
   };
-  if (I > 0) gload(0);
-  for (int J = 0; J < I; ++J) {
+  if (nJ > 0) stage(0);
+  dma_wait();
+  __syncthreads();
+  bf16x8 qb[4];
+  for (int J = 0; J < nJ; ++J) {
+    const int buf = J & 1;
     // transport step before the first tile that uses a new query operand
     if (J < cb) {
       if (J % PR == 0 && J > 0) {
         const int s = J / PR;
-        transition(ws.qbT + ((int64_t)bhq * NS + s) * 64 * T, ws.hl + ((int64_t)bh * NS + s) * 4096,
+        transition(J, ws.qbT + ((int64_t)bhq * NS + s) * 64 * T, ws.hl + ((int64_t)bh * NS + s) * 4096,
                    bw.dhl + ((int64_t)bhq * NS + s) * 4096);
       }
     } else if (sI > 0 || J > cb) {
-      transition(ws.qsT + ((int64_t)bhq * PR + (J - cb)) * 64 * T, ws.hc + ((int64_t)bh * NT + J) * 4096,
+      transition(J, ws.qsT + ((int64_t)bhq * PR + (J - cb)) * 64 * T, ws.hc + ((int64_t)bh * NT + J) * 4096,
                  bw.dhc + ((int64_t)bhq * NT + J) * 4096);
     }
-    r2l_rows<64>(lk, stg);
-    r2l_rows<64>(lo, stg + 2);
-    r2l_tp<64>(lkt, stg + 4);
-    {
+    if (J + 1 < nJ) stage(J + 1);
+    if (J >= cb || J % PR == 0) {  // the query operand changes
       const bf16* qsrc = (J < cb) ? ws.qb + ((int64_t)bhq * NS + J / PR) * T * 64
                                   : ws.qs + ((int64_t)bhq * PR + (J - cb)) * T * 64;
 #pragma unroll
-      for (int st = 0; st < 4; ++st) qb[st] = ld8(qsrc + (int64_t)(i0 + ih * 32 + l32) * 64 + 16 * st + 8 * g);
+      for (int st = 0; st < 4; ++st) qb[st] = ld8(qsrc + (int64_t)(iw0 + l32) * 64 + 16 * st + 8 * g);
     }
-    __syncthreads();
-    if (J + 1 < I) gload(J + 1);
-    {
-      f32x16 sc = zero16(), dp = zero16();
+    if (Iw < NT && J < Iw) {
 #pragma unroll
-      for (int st = 0; st < 4; ++st) {
-        sc = mfma32(ld8(&lk[jh * 32 + l32][16 * st + 8 * g]), qb[st], sc);
-        dp = mfma32(ld8(&lo[jh * 32 + l32][16 * st + 8 * g]), dvr[st], dp);
-      }
+      for (int jh = 0; jh < 2; ++jh) {
+        f32x16 sc = zero16(), dp = zero16();
 #pragma unroll
-      for (int e = 0; e < 16; ++e) sc[e] = -scale * dp[e] * __builtin_amdgcn_exp2f(fmaf(sc[e], sl2, -cc0));
-      const bf16x8 d0 = pack_b(sc, 0), d1 = pack_b(sc, 1);
+        for (int st = 0; st < 4; ++st) {
+          sc = mfma32(ld8(swz<8>(sm.k[buf], jh * 32 + l32, 2 * st + g)), qb[st], sc);
+          dp = mfma32(ld8(swz<8>(sm.o[buf], jh * 32 + l32, 2 * st + g)), dvr[st], dp);
+        }
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        acc[t] = mfma32(ld8(&lkt[t * 32 + l32][jh * 32 + 8 * g]), d0, acc[t]);
-        acc[t] = mfma32(ld8(&lkt[t * 32 + l32][jh * 32 + 16 + 8 * g]), d1, acc[t]);
+        for (int e = 0; e < 16; ++e) sc[e] = -scale * dp[e] * __builtin_amdgcn_exp2f(fmaf(sc[e], sl2, -cc0));
+        const bf16x8 d0 = pack_b(sc, 0), d1 = pack_b(sc, 1);
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          acc[t] = mfma32(lds_tr_a<8>(sm.k[buf], jh * 32, t * 32), d0, acc[t]);
+          acc[t] = mfma32(lds_tr_a<8>(sm.k[buf], jh * 32 + 16, t * 32), d1, acc[t]);
+        }
       }
     }
+    dma_wait();
     __syncthreads();
   }
-  gather_G();
-  {
-    float* dst = bw.dqt + ((int64_t)bhq * T + i0) * 64;
-    for (int idx = tid; idx < 4096; idx += 256) dst[idx] = Gs[idx >> 6][idx & 63];
+  if (Iw < NT) {
+    float* dst = bw.dqt + ((int64_t)bhq * T + iw0 + l32) * 64;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) {
+        f32x4 v;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = acc[t][4 * qq + u];
+        *reinterpret_cast<f32x4*>(dst + t * 32 + 8 * qq + 4 * g) = v;
+      }
   }
 }
 
