@@ -57,8 +57,8 @@ __global__ __launch_bounds__(256) void path_dv_kernel(const bf16* __restrict__ d
                                                       int BHq, float scale, PathFwdWs ws, PathBwdWs bw) {
   __shared__ __attribute__((aligned(16))) float Yt[64][68];  // Yt[c][r] = Y[r][c]
   __shared__ __attribute__((aligned(16))) float Rt[64][68];
-  __shared__ __attribute__((aligned(16))) bf16 lq[2][64][72];
-  __shared__ __attribute__((aligned(16))) bf16 ld_[2][64][72];
+  __shared__ __attribute__((aligned(16))) bf16 lq[2][64 * 64];  // swizzled (chunk c of row r at c ^ (r & 7))
+  __shared__ __attribute__((aligned(16))) bf16 ld_[2][64 * 64];
   const int NT = T / PC, NS = (NT + PR - 1) / PR;
   const int id = blockIdx.x;
   const int J = NT - 1 - id / BHq, bhq = id - (id / BHq) * BHq;
@@ -78,24 +78,35 @@ __global__ __launch_bounds__(256) void path_dv_kernel(const bf16* __restrict__ d
     kbs[st] = ld8(ws.kt + ((int64_t)bh * T + j0 + ch * 32 + l32) * 64 + 16 * st + 8 * g);
     kbf[st] = ld8(ws.kl + ((int64_t)bh * T + j0 + ch * 32 + l32) * 64 + 16 * st + 8 * g);
   }
-  f32x16 acc[2] = {zero16(), zero16()};
-  bf16x8 stg[4];
-  auto gload = [&](int I) {
+  // accumulators: -dO^T for the ih = 0 waves (R = dO - acc = -(acc_0 + acc_1)), zero for the others
+  f32x16 acc[2];
+  {
+    const bf16* drow_ = dout + b * dos.b + hq * dos.h + (int64_t)(j0 + ch * 32 + l32) * dos.t;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) {
+        const bf16x4 x = *reinterpret_cast<const bf16x4*>(drow_ + t * 32 + 8 * qq + 4 * g);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc[t][4 * qq + u] = ih ? 0.f : -(float)x[u];
+      }
+  }
+  int plan_q[2], plan_t[2];
+  dma_plan<64, 8>(64, plan_q);
+  dma_plan<64, 8>(T, plan_t);
+  const int first = NT - 1;
+  auto stage = [&](int I) {  // direct global->LDS staging of query chunk I into buffer (first - I) & 1
+    const int buf = (first - I) & 1;
     const bf16* qsrc = (I <= ceJ) ? ws.qs + (((int64_t)bhq * PR + (J - (I / PR) * PR)) * T) * 64
                                   : ws.qb + (((int64_t)bhq * NS + sJ) * T) * 64;
-    g2r_rows<64>(qsrc, 64, I * PC, stg);
-    g2r_tp<64>(bw.dvT + (int64_t)bhq * 64 * T, T, I * PC, stg + 2);
+    dma_stage<64, 8>(plan_q, qsrc + (int64_t)I * PC * 64, lq[buf]);
+    dma_stage<64, 8>(plan_t, bw.dvT + (int64_t)bhq * 64 * T + I * PC, ld_[buf]);
   };
-  auto lstore = [&](int buf) {
-    r2l_rows<64>(lq[buf], stg);
-    r2l_tp<64>(ld_[buf], stg + 2);
-  };
-  const int first = NT - 1;
   int ready = 0;
   if (first > J) {
     ready = wait_counter_gt(cnt, 0);
-    gload(first);
-    lstore(0);
+    stage(first);
+    dma_wait();
   }
   __syncthreads();
   for (int I = first; I > J; --I) {
@@ -112,30 +123,28 @@ __global__ __launch_bounds__(256) void path_dv_kernel(const bf16* __restrict__ d
         }
       }
       early = need < ready;
-      if (early) gload(I - 1);
+      if (early) stage(I - 1);
     }
     {
       const bool same = (I <= ceJ);
       f32x16 sc = zero16();
 #pragma unroll
       for (int st = 0; st < 4; ++st)
-        sc = mfma32(ld8(&lq[buf][ih * 32 + l32][16 * st + 8 * g]), same ? kbs[st] : kbf[st], sc);
+        sc = mfma32(ld8(swz<8>(lq[buf], ih * 32 + l32, 2 * st + g)), same ? kbs[st] : kbf[st], sc);
 #pragma unroll
       for (int e = 0; e < 16; ++e) sc[e] = __builtin_amdgcn_exp2f(fmaf(sc[e], sl2, -cc0));
       const bf16x8 p0 = pack_b(sc, 0), p1 = pack_b(sc, 1);
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        acc[t] = mfma32(ld8(&ld_[buf][t * 32 + l32][ih * 32 + 8 * g]), p0, acc[t]);
-        acc[t] = mfma32(ld8(&ld_[buf][t * 32 + l32][ih * 32 + 16 + 8 * g]), p1, acc[t]);
+        acc[t] = mfma32(ld8(swz<8>(ld_[buf], t * 32 + l32, 4 * ih + g)), p0, acc[t]);
+        acc[t] = mfma32(ld8(swz<8>(ld_[buf], t * 32 + l32, 4 * ih + 2 + g)), p1, acc[t]);
       }
     }
-    if (more) {
-      if (!early) {
-        ready = wait_counter_gt(cnt, NT - I);
-        gload(I - 1);
-      }
-      lstore(buf ^ 1);
+    if (more && !early) {
+      ready = wait_counter_gt(cnt, NT - I);
+      stage(I - 1);
     }
+    dma_wait();
     __syncthreads();
   }
   // ---- R = dO_J - acc ----
@@ -147,16 +156,12 @@ __global__ __launch_bounds__(256) void path_dv_kernel(const bf16* __restrict__ d
   }
   __syncthreads();
   if (ih == 0) {
-    const bf16* drow_ = dout + b * dos.b + hq * dos.h + (int64_t)(j0 + ch * 32 + l32) * dos.t;
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int qq = 0; qq < 4; ++qq) {
-        const int d0 = t * 32 + 8 * qq + 4 * g;
-        const bf16x4 x = *reinterpret_cast<const bf16x4*>(drow_ + d0);
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-          Rt[d0 + u][ch * 32 + l32] = (float)x[u] - (acc[t][4 * qq + u] + Rt[d0 + u][ch * 32 + l32]);
+      for (int e = 0; e < 16; ++e) {
+        float& x = Rt[t * 32 + drow(e, g)][ch * 32 + l32];
+        x = -(acc[t][e] + x);
       }
   }
   __syncthreads();
@@ -175,9 +180,10 @@ __global__ __launch_bounds__(256) void path_dv_kernel(const bf16* __restrict__ d
     }
     const int cl = chh * 32 + l32;
     const int r = j0 + cl;
-    const int slot = (r & ~15) | jmap(r & 15);
+    const int lslot = (cl & ~15) | jmap(cl & 15);
     float* of = bw.dvf + ((int64_t)bhq * T + r) * 64;
     bf16* ob = bw.dvb + ((int64_t)bhq * T + r) * 64;
+    bf16* dt_l = ld_[0];  // dV^T of the chunk, T-perm within 16-groups (plain [64][64])
 #pragma unroll
     for (int qq = 0; qq < 4; ++qq) {
       const int d0 = dt * 32 + 8 * qq + 4 * g;
@@ -187,11 +193,16 @@ __global__ __launch_bounds__(256) void path_dv_kernel(const bf16* __restrict__ d
       for (int u = 0; u < 4; ++u) {
         f[u] = dvo[4 * qq + u];
         bb[u] = (bf16)f[u];
-        bw.dvT[((int64_t)bhq * 64 + d0 + u) * T + slot] = bb[u];
+        dt_l[(d0 + u) * 64 + lslot] = bb[u];
       }
       *reinterpret_cast<f32x4*>(of + d0) = f;
       *reinterpret_cast<bf16x4*>(ob + d0) = bb;
     }
+  }
+  __syncthreads();
+  for (int c = tid; c < 64 * 8; c += 256) {  // dV^T to the chain operand with 16-byte stores
+    const int dd = c >> 3, s8 = (c & 7) * 8;
+    *reinterpret_cast<bf16x8*>(bw.dvT + ((int64_t)bhq * 64 + dd) * T + j0 + s8) = ld8(ld_[0] + dd * 64 + s8);
   }
   publish_counter(cnt, NT - J);
   // ---- dA_diag = -s (dV_J O_J^T) * L_diag  (fp32, in LDS) ----

@@ -333,8 +333,8 @@ __global__ __launch_bounds__(256) void path_solve_fwd_kernel(const bf16* __restr
                                                              int T, int BHq, float scale, PathFwdWs ws) {
   __shared__ __attribute__((aligned(16))) float Ys[64][68];
   __shared__ __attribute__((aligned(16))) float Rt[64][68];
-  __shared__ __attribute__((aligned(16))) bf16 lk[2][64][72];
-  __shared__ __attribute__((aligned(16))) bf16 lo[2][64][72];
+  __shared__ __attribute__((aligned(16))) bf16 lk[2][64 * 64];  // swizzled (chunk c of row r at c ^ (r & 7))
+  __shared__ __attribute__((aligned(16))) bf16 lo[2][64 * 64];
   const int NT = T / PC, NS = (NT + PR - 1) / PR;
   const int id = blockIdx.x;
   const int I = id / BHq, bhq = id - (id / BHq) * BHq;
@@ -350,7 +350,19 @@ __global__ __launch_bounds__(256) void path_solve_fwd_kernel(const bf16* __restr
 
   load_mat64<false>(Ys, ws.y + ((int64_t)bhq * NT + I) * 4096);
 
-  f32x16 acc[2] = {zero16(), zero16()};
+  // accumulators: -V^T for the jh = 0 waves (R = V - acc = -(acc_0 + acc_1)), zero for the others
+  f32x16 acc[2];
+  {
+    const bf16* vrow = v + b * vs.b + h * vs.h + (int64_t)(i0 + ih * 32 + l32) * vs.t;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) {
+        const bf16x4 vv = *reinterpret_cast<const bf16x4*>(vrow + t * 32 + 8 * qq + 4 * g);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc[t][4 * qq + u] = jh ? 0.f : -(float)vv[u];
+      }
+  }
   bf16x8 qb[4];
   int qsrc = -1;  // current Qop source: s (QB) or PR*NS + slot (QS)
   auto load_q = [&](int J) {
@@ -362,21 +374,19 @@ __global__ __launch_bounds__(256) void path_solve_fwd_kernel(const bf16* __restr
 #pragma unroll
     for (int st = 0; st < 4; ++st) qb[st] = ld8(base + (int64_t)(i0 + ih * 32 + l32) * 64 + 16 * st + 8 * g);
   };
-  bf16x8 stg[4];
-  auto gload = [&](int J) {
-    const bf16* ksrc = ((J < cb) ? ws.kl : ws.kt) + (int64_t)bh * T * 64;
-    g2r_rows<64>(ksrc, 64, J * PC, stg);
-    g2r_tp<64>(oTh, T, J * PC, stg + 2);
-  };
-  auto lstore = [&](int buf) {
-    r2l_rows<64>(lk[buf], stg);
-    r2l_tp<64>(lo[buf], stg + 2);
+  int plan_k[2], plan_t[2];
+  dma_plan<64, 8>(64, plan_k);
+  dma_plan<64, 8>(T, plan_t);
+  auto stage = [&](int J) {  // direct global->LDS staging of key chunk J into buffer J & 1
+    const int buf = J & 1;
+    dma_stage<64, 8>(plan_k, ((J < cb) ? ws.kl : ws.kt) + ((int64_t)bh * T + J * PC) * 64, lk[buf]);
+    dma_stage<64, 8>(plan_t, oTh + J * PC, lo[buf]);
   };
   int ready = 0;
   if (I > 0) {
     ready = wait_counter_gt(cnt, 0);
-    gload(0);
-    lstore(0);
+    stage(0);
+    dma_wait();
   }
   __syncthreads();
   for (int J = 0; J < I; ++J) {
@@ -392,29 +402,27 @@ __global__ __launch_bounds__(256) void path_solve_fwd_kernel(const bf16* __restr
         }
       }
       early = J + 1 < ready;
-      if (early) gload(J + 1);
+      if (early) stage(J + 1);
     }
     load_q(J);
     {
       f32x16 sc = zero16();
 #pragma unroll
-      for (int st = 0; st < 4; ++st) sc = mfma32(ld8(&lk[buf][jh * 32 + l32][16 * st + 8 * g]), qb[st], sc);
+      for (int st = 0; st < 4; ++st) sc = mfma32(ld8(swz<8>(lk[buf], jh * 32 + l32, 2 * st + g)), qb[st], sc);
 #pragma unroll
       for (int e = 0; e < 16; ++e) sc[e] = __builtin_amdgcn_exp2f(fmaf(sc[e], sl2, -cc0));
       const bf16x8 p0 = pack_b(sc, 0), p1 = pack_b(sc, 1);
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        acc[t] = mfma32(ld8(&lo[buf][t * 32 + l32][jh * 32 + 8 * g]), p0, acc[t]);
-        acc[t] = mfma32(ld8(&lo[buf][t * 32 + l32][jh * 32 + 16 + 8 * g]), p1, acc[t]);
+        acc[t] = mfma32(ld8(swz<8>(lo[buf], t * 32 + l32, 4 * jh + g)), p0, acc[t]);
+        acc[t] = mfma32(ld8(swz<8>(lo[buf], t * 32 + l32, 4 * jh + 2 + g)), p1, acc[t]);
       }
     }
-    if (more) {
-      if (!early) {
-        ready = wait_counter_gt(cnt, J + 1);
-        gload(J + 1);
-      }
-      lstore(buf ^ 1);
+    if (more && !early) {
+      ready = wait_counter_gt(cnt, J + 1);
+      stage(J + 1);
     }
+    dma_wait();
     __syncthreads();
   }
   // ---- R = V - acc (reduce key halves) ----
@@ -426,16 +434,12 @@ __global__ __launch_bounds__(256) void path_solve_fwd_kernel(const bf16* __restr
   }
   __syncthreads();
   if (jh == 0) {
-    const bf16* vrow = v + b * vs.b + h * vs.h + (int64_t)(i0 + ih * 32 + l32) * vs.t;
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int qq = 0; qq < 4; ++qq) {
-        const int d0 = t * 32 + 8 * qq + 4 * g;
-        const bf16x4 vv = *reinterpret_cast<const bf16x4*>(vrow + d0);
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-          Rt[d0 + u][ih * 32 + l32] = (float)vv[u] - (acc[t][4 * qq + u] + Rt[d0 + u][ih * 32 + l32]);
+      for (int e = 0; e < 16; ++e) {
+        float& x = Rt[t * 32 + drow(e, g)][ih * 32 + l32];
+        x = -(acc[t][e] + x);
       }
   }
   __syncthreads();
@@ -451,9 +455,10 @@ __global__ __launch_bounds__(256) void path_solve_fwd_kernel(const bf16* __restr
       oo = mfma32(ah, bl, oo);
       oo = mfma32(al, bh8, oo);
     }
-    const int r = i0 + rh * 32 + l32;
-    const int slot = (r & ~15) | jmap(r & 15);
-    bf16* orow = o + b * os.b + hq * os.h + (int64_t)r * os.t;
+    const int rl = rh * 32 + l32;
+    const int lslot = (rl & ~15) | jmap(rl & 15);
+    bf16* orow = o + b * os.b + hq * os.h + (int64_t)(i0 + rl) * os.t;
+    bf16* ot = lo[0];  // O^T of the chunk, T-perm within 16-groups (plain [64][64])
 #pragma unroll
     for (int qq = 0; qq < 4; ++qq) {
       const int d0 = dt * 32 + 8 * qq + 4 * g;
@@ -461,10 +466,15 @@ __global__ __launch_bounds__(256) void path_solve_fwd_kernel(const bf16* __restr
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         bb[u] = (bf16)oo[4 * qq + u];
-        ws.oT[((int64_t)bhq * 64 + d0 + u) * T + slot] = bb[u];
+        ot[(d0 + u) * 64 + lslot] = bb[u];
       }
       *reinterpret_cast<bf16x4*>(orow + d0) = bb;
     }
+  }
+  __syncthreads();
+  for (int c = tid; c < 64 * 8; c += 256) {  // O^T to the chain operand with 16-byte stores
+    const int dd = c >> 3, s8 = (c & 7) * 8;
+    *reinterpret_cast<bf16x8*>(ws.oT + ((int64_t)bhq * 64 + dd) * T + i0 + s8) = ld8(lo[0] + dd * 64 + s8);
   }
   publish_counter(cnt, I + 1);
 }
