@@ -1,0 +1,115 @@
+"""Llama-LUCID decoder (lucid_amd.modeling_lucid): module tree, decode rows, and on the
+GPU a tiny model against a float32 PyTorch reference whose attention core is the
+oracle's restatement of the reference dense path.
+
+Decode parity is defined mathematically: the V' row of a decoded token equals the row
+of the same token in a prefill (P's diagonal is not 1, modeling_lucid.py:565-569)."""
+import numpy as np
+import pytest
+import torch
+
+from lucid_amd import modeling_lucid as M
+from oracle import lucid_ref as R
+
+
+def _tiny(hkv=2):
+    return M.LucidConfig(vocab_size=512, hidden_size=128, intermediate_size=256, num_hidden_layers=2,
+                         num_attention_heads=2, num_key_value_heads=hkv, head_dim=64)
+
+
+def test_module_tree_follows_reference_names():
+    torch.manual_seed(0)
+    model = M.LlamaForCausalLM(_tiny())
+    names = {n for n, _ in model.named_parameters()}
+    for n in ("model.embed_tokens.weight", "model.layers.0.self_attn.q_proj.weight",
+              "model.layers.0.self_attn.k_proj.weight", "model.layers.0.self_attn.v_proj.weight",
+              "model.layers.0.self_attn.o_proj.weight", "model.layers.1.mlp.gate_proj.weight",
+              "model.layers.1.mlp.up_proj.weight", "model.layers.1.mlp.down_proj.weight",
+              "model.layers.1.input_layernorm.weight", "model.layers.1.post_attention_layernorm.weight",
+              "model.norm.weight", "lm_head.weight"):
+        assert n in names, n
+    c3 = M.c3_config()
+    assert (c3.num_hidden_layers, c3.hidden_size, c3.num_attention_heads, c3.head_dim, c3.intermediate_size,
+            c3.vocab_size, c3.rope_theta) == (16, 2048, 32, 64, 5632, 32000, 10000.0)
+
+
+@pytest.mark.parametrize("n_new", [1, 3])
+def test_decode_rows_equal_prefill_rows(n_new):
+    rng = np.random.default_rng(4 + n_new)
+    B, H, T, d = 1, 2, 12, 16
+    k = rng.standard_normal((B, H, T, d))
+    v = rng.standard_normal((B, H, T, d))
+    s, eps = d ** -0.5, 1e-5
+    vp = R.vprime_dense(k, v, s, eps)  # prefill rows (float64 oracle)
+    attn = M.LucidAttention(M.LucidConfig(hidden_size=2 * d, num_attention_heads=2, head_dim=d, rms_norm_eps=eps), 0)
+    t0 = T - n_new
+    kt, vt = torch.from_numpy(k), torch.from_numpy(v)
+    new = attn.get_new_v_prime(kt[:, :, t0:], vt[:, :, t0:], kt[:, :, :t0], torch.from_numpy(vp[:, :, :t0]))
+    np.testing.assert_allclose(new.numpy(), vp[:, :, t0:], rtol=1e-10, atol=1e-10)
+
+
+def _reference_forward(model, ids, labels):
+    """Run `model` with the attention core replaced by the oracle's torch restatement."""
+    saved = M.lucid_attention
+
+    def core(q, k, v, scaling=None, eps=1e-5, return_vprime=False):
+        o, vp = R.lucid_attention_torch(q, k, v, scaling, eps)
+        return (o, vp) if return_vprime else o
+
+    M.lucid_attention = core
+    try:
+        return model(ids, labels=labels)
+    finally:
+        M.lucid_attention = saved
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("hkv", [2, 1])
+def test_tiny_model_matches_float32_reference(hkv):
+    torch.manual_seed(1)
+    cfg = _tiny(hkv)
+    ref = M.LlamaForCausalLM(cfg)  # float32, CPU
+    ours = M.LlamaForCausalLM(cfg)
+    ours.load_state_dict(ref.state_dict())
+    ours = ours.to("cuda", torch.bfloat16)
+    T = 200
+    ids = torch.randint(0, cfg.vocab_size, (1, T), generator=torch.Generator().manual_seed(2))
+    print(f"case tiny model hkv={hkv} T={T}", flush=True)
+    loss_ref, _ = _reference_forward(ref, ids, ids)
+    loss_ref.backward()
+    loss, _ = ours(ids.cuda(), labels=ids.cuda())
+    loss.backward()
+    torch.cuda.synchronize()
+    assert abs(loss.item() - loss_ref.item()) <= 1e-2 * abs(loss_ref.item()), (loss.item(), loss_ref.item())
+    assert abs(loss_ref.item() - np.log(cfg.vocab_size)) < 0.5  # random init: loss ~ ln V
+    for name in ("model.layers.0.self_attn.k_proj.weight", "model.layers.1.self_attn.q_proj.weight",
+                 "model.layers.0.self_attn.v_proj.weight", "model.embed_tokens.weight"):
+        gr = dict(ref.named_parameters())[name].grad.double()
+        go = dict(ours.named_parameters())[name].grad.double().cpu()
+        cos = torch.nn.functional.cosine_similarity(gr.flatten(), go.flatten(), dim=0).item()
+        rel = ((go - gr).norm() / gr.norm()).item()
+        assert cos > 0.99 and rel < 0.1, (name, cos, rel)
+
+
+@pytest.mark.gpu
+def test_decode_matches_prefill_logits():
+    torch.manual_seed(3)
+    cfg = _tiny(1)
+    model = M.LlamaForCausalLM(cfg).to("cuda", torch.bfloat16).eval()
+    T, n_new = 130, 2
+    ids = torch.randint(0, cfg.vocab_size, (1, T + n_new), generator=torch.Generator().manual_seed(5)).cuda()
+    print(f"case decode T={T} new={n_new}", flush=True)
+    with torch.no_grad():
+        _, full = model(ids)
+        cache = M.LucidCache()
+        _, pre = model(ids[:, :T], past_key_values=cache)
+        steps = []
+        for t in range(T, T + n_new):
+            _, lg = model(ids[:, t:t + 1], past_key_values=cache)
+            steps.append(lg)
+    torch.cuda.synchronize()
+    dec = torch.cat(steps, dim=1).float()
+    ref = full[:, T:].float()
+    err = (dec - ref).abs().max().item()
+    assert err <= 2e-2 * max(1.0, ref.abs().max().item()), err
+    assert cache.get_seq_length() == T + n_new
