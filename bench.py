@@ -118,6 +118,10 @@ PATH_KERNEL_FLOPS = {
     "path_dv_kernel": 2.0,         # A, L^T dV
     "path_bwd_row_kernel": 3.0,    # A, dV O^T, dA K
     "path_bwd_col_kernel": 3.0,    # A, dV O^T, dA^T Q
+    # PaTH softmax attention
+    "path_softmax_fwd_kernel": 2.0,      # A, P V
+    "path_softmax_bwd_row_kernel": 3.0,  # A, dO V^T, dA K
+    "path_softmax_bwd_col_kernel": 4.0,  # A, dO V^T, dA^T Q, P^T dO
 }
 
 
@@ -244,11 +248,12 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="lucid", choices=["lucid", "c2", "c3", "c5", "path"],
+    ap.add_argument("--workload", default="lucid", choices=["lucid", "c2", "c3", "c5", "path", "path_softmax"],
                     help="lucid: north star B1 H16 T32768 d64 fwd+bwd (default); c2: B4 H16 T4096 d64 "
                          "fwd+bwd; c3: 16-layer Llama-LUCID decoder, one training step (fwd+bwd+AdamW) "
                          "on B1 x T8192; c5: B1 T131072 Hq32/Hkv8 d128 forward only; path: LUCID-Path "
-                         "B1 H16 T32768 d64 fwd+bwd")
+                         "B1 H16 T32768 d64 fwd+bwd; path_softmax: PaTH softmax attention on the config-4 "
+                         "shape, fwd+bwd")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-causal", action="store_true")
     ap.add_argument("--copy-bytes", type=int, default=0,
@@ -275,8 +280,8 @@ def main():
         bench_c3(args, dev)
         return
     fwd_only = wl == "c5"
-    if wl == "path":
-        from lucid_amd.lucid_path import parallel_lucid_path_attention
+    if wl in ("path", "path_softmax"):
+        from lucid_amd.lucid_path import parallel_lucid_path_attention, parallel_path_attention
         B, Hq, Hkv, T, D = 1, 16, 16, 32768, 64
         q, k, v, w, beta, do = _path_inputs(B, Hq, T, D, dev)
         lib, prefix = _lib.load("liblucid_path.so"), "lucid_path_"
@@ -284,13 +289,18 @@ def main():
         def step():
             for x in (q, k, v, w, beta):
                 x.grad = None
-            o, _ = parallel_lucid_path_attention(k, v, w, beta, q=q)
+            if wl == "path":
+                o, _ = parallel_lucid_path_attention(k, v, w, beta, q=q)
+            else:
+                o, _ = parallel_path_attention(q, k, v, w, beta)
             o.backward(do)
         # count of the reference algorithm (query propagated through every chunk pair):
         # fwd 4 T^2 d (A, L O, 2x propagation) + bwd 12 T^2 d per query head
         flops = 16.0 * T * T * D * B * Hq
         kflops = {n: f * T * T * D * B * Hq for n, f in PATH_KERNEL_FLOPS.items()}
         metric = "LUCID-Path fwd+bwd tokens/s & TFLOP/s at T=32K bf16 (config 4)"
+        if wl == "path_softmax":
+            metric = "PaTH softmax attention fwd+bwd tokens/s & TFLOP/s at T=32K bf16 (config-4 shape)"
     else:
         B, Hq, Hkv, T, D = {"lucid": (1, 16, 16, 32768, 64), "c2": (4, 16, 16, 4096, 64),
                             "c5": (1, 32, 8, 131072, 128)}[wl]
@@ -348,10 +358,14 @@ def main():
             traffic = json.load(fh).get(dom)
 
     causal = None
-    if not args.no_causal and wl in ("lucid", "c2"):
+    if not args.no_causal and wl in ("lucid", "c2", "path_softmax"):
         import torch.nn.functional as F
-        qc, kc, vc = (t.detach().clone().requires_grad_() for t in (q, k, v))
-        doc = do.transpose(1, 2)
+        if wl == "path_softmax":  # [B, T, H, D] inputs
+            qc, kc, vc = (t.detach().transpose(1, 2).contiguous().requires_grad_() for t in (q, k, v))
+            doc = do.transpose(1, 2).contiguous()
+        else:
+            qc, kc, vc = (t.detach().clone().requires_grad_() for t in (q, k, v))
+            doc = do.transpose(1, 2)
 
         def cstep():
             qc.grad = kc.grad = vc.grad = None
@@ -386,10 +400,11 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (seeded N(0,1)/sqrt(d) q,k,v; N(0,1) dO)" if wl != "path"
+        "data": "synthetic (seeded N(0,1)/sqrt(d) q,k,v; N(0,1) dO)" if wl not in ("path", "path_softmax")
                 else "synthetic (seeded N(0,1) q,k,v,w; w L2-normalised; beta=2 sigmoid(N(0,1)); N(0,1) dO)",
         "config": {"workload": {"lucid": "lucid_attention_fwd_bwd", "c2": "lucid_attention_fwd_bwd",
-                                "c5": "lucid_attention_fwd", "path": "lucid_path_fwd_bwd"}[wl],
+                                "c5": "lucid_attention_fwd", "path": "lucid_path_fwd_bwd",
+                                "path_softmax": "path_softmax_attention_fwd_bwd"}[wl],
                    "B": B, "Hq": Hq, "Hkv": Hkv, "T": T, "head_dim": D, "causal": True,
                    "parallelism": "single GPU"},
         "tflops": round(flops / (ms / 1e3) / 1e12, 1),

@@ -58,6 +58,42 @@ int lucid_path_bwd(const void* dout, const int64_t* do_strides, const void* q, c
                    const int64_t* dbeta_strides, void* bwd_ws, int B, int T, int H, int HQ, int K, float scale,
                    void* stream);
 
+/*
+ * PaTH softmax attention, the softmax half of a LUCID-Path layer, on the same path
+ * logits (diagonal included, A_ii = q_i . k_i):
+ *   o_i = sum_{j<=i} softmax_j(s A_ij) v_j.
+ * The reference ships only its forward kernels (intra_chunk_preprocess_fwd.py:14-168,
+ * parallel_path_fwd.py:13-170, not called by parallel.py); their backward lives in the
+ * unvendored flash-linear-attention package.  Same layouts, dtypes and constraints as
+ * lucid_path_fwd / lucid_path_bwd (the forward workspace layout differs: size it with
+ * lucid_path_softmax_fwd_workspace_bytes).
+ */
+size_t lucid_path_softmax_fwd_workspace_bytes(int B, int T, int H, int HQ, int K);
+
+/* Forward: o = softmax(s A) v; the row log-sum-exp is kept in fwd_ws for the backward;
+ * kcache as in lucid_path_fwd.  Replaces intra_chunk_preprocess_fwd_fn followed by
+ * parallel_path_fwd_fn (intra_chunk_preprocess_fwd.py:124-168, parallel_path_fwd.py:127-170). */
+int lucid_path_softmax_fwd(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                           const void* v, const int64_t* v_strides, const void* w, const int64_t* w_strides,
+                           const void* beta, const int64_t* beta_strides, void* o, const int64_t* o_strides,
+                           void* kcache, const int64_t* kcache_strides, void* fwd_ws, int B, int T, int H, int HQ,
+                           int K, float scale, void* stream);
+
+size_t lucid_path_softmax_bwd_workspace_bytes(int B, int T, int H, int HQ, int K);
+
+/* Backward of sum(o * dout) w.r.t. q, k, v, w and beta (bf16, GQA sums applied); `o`
+ * and `fwd_ws` are those of lucid_path_softmax_fwd.  No counterpart in the reference
+ * (its PaTH softmax backward is in the unvendored fla package); the gradients equal
+ * float64 autograd of the definition. */
+int lucid_path_softmax_bwd(const void* dout, const int64_t* do_strides, const void* q, const int64_t* q_strides,
+                           const void* k, const int64_t* k_strides, const void* v, const int64_t* v_strides,
+                           const void* w, const int64_t* w_strides, const void* beta, const int64_t* beta_strides,
+                           const void* o, const int64_t* o_strides, const void* fwd_ws, void* dq,
+                           const int64_t* dq_strides, void* dk, const int64_t* dk_strides, void* dv,
+                           const int64_t* dv_strides, void* dw, const int64_t* dw_strides, void* dbeta,
+                           const int64_t* dbeta_strides, void* bwd_ws, int B, int T, int H, int HQ, int K,
+                           float scale, void* stream);
+
 /* Per-kernel timing with HIP events (no counterpart in the reference; used by
  * bench.py), same contract as lucid_profile_* in lucid_amd.h. */
 void lucid_path_profile_enable(int on);

@@ -34,6 +34,7 @@ struct PathBwdWs {
   float* dw;    // [BHq][T][64]
   float* db;    // [BHq][T]
   int* counters;  // [BHq]
+  float* delta; // [BHq][T]           PaTH softmax only: rowsum(dO * O)
 };
 
 __global__ __launch_bounds__(256) void path_bwd_zero_kernel(int64_t n_hl, int64_t n_hc, int n_cnt, PathBwdWs bw) {
@@ -240,6 +241,9 @@ __global__ __launch_bounds__(256) void path_dv_kernel(const bf16* __restrict__ d
 // staged by direct global->LDS loads (double buffered), Kop^T comes through
 // transposing LDS reads.  The pair's dM contributions are summed over its 128 rows
 // before the atomic adds.  grid (ceil(NT/2), B*HQ)
+// The dA rule is the template argument: LUCID-Path (SM = false) dA = -s (X_I Y_J^T) L
+// with X = dV, Y = O (rows of the same query head); PaTH softmax (SM = true)
+// dA = s P (X_I Y_J^T - delta_i), P = exp2(s' S - lse_i), X = dO, Y = V (kv head).
 // ---------------------------------------------------------------------------
 struct RowSmem {
   bf16 k[2][64 * 64];  // swizzled (chunk c of row r at c ^ (r & 7))
@@ -247,13 +251,16 @@ struct RowSmem {
   float g[128][68];    // G rows of the pair at a transport step
 };
 
+template <bool SM>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void path_bwd_row_kernel(
-    const bf16* __restrict__ o, Strides os, int HQ, int H, int T, float scale, PathFwdWs ws, PathBwdWs bw) {
+    const bf16* __restrict__ xsrc, Strides xs, const bf16* __restrict__ ysrc, Strides ys, int HQ, int H, int T,
+    float scale, PathFwdWs ws, PathBwdWs bw) {
   __shared__ __attribute__((aligned(16))) RowSmem sm;
   const int NT = T / PC, NS = (NT + PR - 1) / PR;
   const int I1 = 2 * blockIdx.x, bhq = blockIdx.y;
   const int G_ = HQ / H;
   const int b = bhq / HQ, hq = bhq - b * HQ, bh = b * H + hq / G_;
+  const bf16* yh = ysrc + b * ys.b + (SM ? hq / G_ : hq) * ys.h;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
   const int Iw = I1 + (w >> 1);                     // this wave's query chunk
   const bool pair = I1 + 1 < NT;                    // NT odd: the last pair has one chunk
@@ -263,8 +270,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
   const float sl2 = scale * LOG2E_F, cc0 = LOG2E_F / scale;
 
   bf16x8 dvr[4];
+  {
+    const bf16* xrow = xsrc + b * xs.b + hq * xs.h + (int64_t)(iw0 + l32) * xs.t;
 #pragma unroll
-  for (int st = 0; st < 4; ++st) dvr[st] = ld8(bw.dvb + ((int64_t)bhq * T + iw0 + l32) * 64 + 16 * st + 8 * g);
+    for (int st = 0; st < 4; ++st) dvr[st] = ld8(xrow + 16 * st + 8 * g);
+  }
+  // exponent offset and delta of this lane's row (LUCID-Path: the constant 1/s, no delta)
+  const float ci = SM ? ws.lse[(int64_t)bhq * T + iw0 + l32] : cc0;
+  const float di = SM ? bw.delta[(int64_t)bhq * T + iw0 + l32] : 0.f;
   f32x16 acc[2] = {zero16(), zero16()};
 
   // ---- dM += X^T G over the pair's rows (atomic) and G <- G M^T for each wave's rows ----
@@ -316,12 +329,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
 
   int plan_k[2], plan_o[2];
   dma_plan<64, 8>(64, plan_k);
-  dma_plan<64, 8>(os.t, plan_o);
+  dma_plan<64, 8>(ys.t, plan_o);
   auto stage = [&](int J) {
     const int buf = J & 1;
     const bf16* kr = ((J < cb) ? ws.kl : ws.kt) + ((int64_t)bh * T + J * PC) * 64;
     dma_stage<64, 8>(plan_k, kr, sm.k[buf]);
-    dma_stage<64, 8>(plan_o, o + b * os.b + hq * os.h + (int64_t)J * PC * os.t, sm.o[buf]);
+    dma_stage<64, 8>(plan_o, yh + (int64_t)J * PC * ys.t, sm.o[buf]);
   };
   if (nJ > 0) stage(0);
   dma_wait();
@@ -357,7 +370,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
           dp = mfma32(ld8(swz<8>(sm.o[buf], jh * 32 + l32, 2 * st + g)), dvr[st], dp);
         }
 #pragma unroll
-        for (int e = 0; e < 16; ++e) sc[e] = -scale * dp[e] * __builtin_amdgcn_exp2f(fmaf(sc[e], sl2, -cc0));
+        for (int e = 0; e < 16; ++e) {
+          const float ex = __builtin_amdgcn_exp2f(fmaf(sc[e], sl2, -ci));
+          sc[e] = SM ? scale * ex * (dp[e] - di) : -scale * dp[e] * ex;
+        }
         const bf16x8 d0 = pack_b(sc, 0), d1 = pack_b(sc, 1);
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
@@ -395,7 +411,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
 // rows inside the large chunk) and dV rows are staged by direct global->LDS loads
 // (three buffers, two tiles ahead); Qop^T comes through transposing LDS reads.
 // Then d k~_J = dk~(same) + dKL SUF_J and dSUF_J = dKL^T k~_J.  grid (ceil(NT/2), B*HQ)
+// Template argument SM as in the row sweep; in PaTH softmax mode the rows' lse and
+// delta are staged beside each query tile, and dV_J^T[d][j] += dO_I^T[d][i] P[i][j]
+// is accumulated too and added to the diagonal block's part in dvf.
 // ---------------------------------------------------------------------------
+template <bool SM>
 struct ColSmem {
   union {
     struct {
@@ -409,15 +429,20 @@ struct ColSmem {
       float m[64][68];  // SUF_J, then k~_J
     } fin;
   } u;
+  float lse[SM ? 3 : 1][64];  // softmax: lse and delta of the staged query rows
+  float dl[SM ? 3 : 1][64];
 };
 
+template <bool SM>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void path_bwd_col_kernel(
-    const bf16* __restrict__ o, Strides os, int HQ, int H, int T, float scale, PathFwdWs ws, PathBwdWs bw) {
-  __shared__ __attribute__((aligned(16))) ColSmem sm;
+    const bf16* __restrict__ xsrc, Strides xs, const bf16* __restrict__ ysrc, Strides ys, int HQ, int H, int T,
+    float scale, PathFwdWs ws, PathBwdWs bw) {
+  __shared__ __attribute__((aligned(16))) ColSmem<SM> sm;
   const int NT = T / PC, NS = (NT + PR - 1) / PR;
   const int J1 = 2 * blockIdx.x, bhq = blockIdx.y;
   const int G_ = HQ / H;
   const int b = bhq / HQ, hq = bhq - b * HQ, bh = b * H + hq / G_;
+  const bf16* xh = xsrc + b * xs.b + hq * xs.h;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
   const int Jw = J1 + (w >> 1);        // this wave's key chunk
   const bool live = Jw < NT;           // NT odd: the last pair has one chunk
@@ -427,47 +452,84 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
   bf16x8 kbs[4], kbf[4], ob[4];
   {
     const int jr = min(J1 * PC + 32 * w + l32, T - 1);
+    const bf16* yrow = ysrc + b * ys.b + (SM ? hq / G_ : hq) * ys.h + (int64_t)jr * ys.t;
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
       kbs[st] = ld8(ws.kt + ((int64_t)bh * T + jr) * 64 + 16 * st + 8 * g);
       kbf[st] = ld8(ws.kl + ((int64_t)bh * T + jr) * 64 + 16 * st + 8 * g);
-      ob[st] = ld8(o + b * os.b + hq * os.h + (int64_t)jr * os.t + 16 * st + 8 * g);
+      ob[st] = ld8(yrow + 16 * st + 8 * g);
     }
   }
   f32x16 as_[2] = {zero16(), zero16()}, af[2] = {zero16(), zero16()};
+  f32x16 dva[2] = {zero16(), zero16()};  // softmax: dV^T of this wave's keys
 
   // step k stages query tile I = J1 + 1 + k
   const int nsteps = NT - 1 - J1;
   // newest vector-memory ops of a step, per wave: 3 tiles inside J's large chunk, 2 beyond
   auto near = [&](int k) { return J1 + 1 + k <= ceJ; };
-  int plan_r[2];
+  int plan_r[2], plan_x[2];
   dma_plan<64, 8>(64, plan_r);
+  if (SM) dma_plan<64, 8>(xs.t, plan_x);
   auto stage = [&](int k) {
     const int I = J1 + 1 + k, buf = k % 3;
     const bool same = I <= ceJ;
     const bf16* q1 = same ? ws.qs + ((int64_t)bhq * PR + (J1 - cb)) * T * 64
                           : ws.qb + ((int64_t)bhq * NS + sJ) * T * 64;
     dma_stage<64, 8>(plan_r, q1 + (int64_t)I * PC * 64, sm.u.st.qa[buf]);
-    dma_stage<64, 8>(plan_r, bw.dvb + ((int64_t)bhq * T + I * PC) * 64, sm.u.st.dv[buf]);
+    dma_stage<64, 8>(SM ? plan_x : plan_r, xh + (int64_t)I * PC * xs.t, sm.u.st.dv[buf]);
     if (same)  // the second chunk of the pair has its own query operand inside the large chunk
       dma_stage<64, 8>(plan_r, ws.qs + ((int64_t)bhq * PR + (J1 + 1 - cb)) * T * 64 + (int64_t)I * PC * 64,
                        sm.u.st.qb[buf]);
+    if (SM) {  // one more load for waves 0 and 1
+      if (w == 0) dma_f32x64(ws.lse + (int64_t)bhq * T + I * PC, sm.lse[buf]);
+      if (w == 1) dma_f32x64(bw.delta + (int64_t)bhq * T + I * PC, sm.dl[buf]);
+    }
+  };
+  // wait until the step after the next one is the only one in flight
+  auto wait_next = [&](bool nr) {
+    if (SM && w < 2) {
+      if (nr) dma_wait_but<7>();
+      else dma_wait_but<5>();
+    } else {
+      if (nr) dma_wait_but<6>();
+      else dma_wait_but<4>();
+    }
   };
   if (nsteps > 0) {
     stage(0);
     if (nsteps > 1) {
       stage(1);
-      if (near(1)) dma_wait_but<6>();
-      else dma_wait_but<4>();
+      wait_next(near(1));
     } else {
       dma_wait();
     }
   }
   __syncthreads();
+  // softmax (register budget): as_ holds d k~ (same large chunk) until the sweep leaves
+  // J's large chunk, then it is parked in dkt and as_ collects dKL
+  bool parked = false;
+  auto park = [&]() {
+    if (live) {
+      float* dst = bw.dkt + ((int64_t)bhq * T + Jw * PC + (w & 1) * 32 + l32) * 64;
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) {
+          f32x4 x;
+#pragma unroll
+          for (int u = 0; u < 4; ++u) x[u] = as_[t][4 * qq + u];
+          *reinterpret_cast<f32x4*>(dst + t * 32 + 8 * qq + 4 * g) = x;
+        }
+      as_[0] = zero16();
+      as_[1] = zero16();
+    }
+    parked = true;
+  };
   for (int k = 0; k < nsteps; ++k) {
     const int buf = k % 3;
     if (k + 2 < nsteps) stage(k + 2);
     const int I = J1 + 1 + k;
+    if (SM && I == ceJ + 1) park();
     if (live && I > Jw) {
       const bool same = I <= ceJ;
       const bf16* qt = (w >= 2 && same) ? sm.u.st.qb[buf] : sm.u.st.qa[buf];
@@ -479,14 +541,36 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
           sc = mfma32(ld8(swz<8>(qt, rh * 32 + l32, 2 * st + g)), same ? kbs[st] : kbf[st], sc);
           dp = mfma32(ld8(swz<8>(sm.u.st.dv[buf], rh * 32 + l32, 2 * st + g)), ob[st], dp);
         }
+        if (SM) {
 #pragma unroll
-        for (int e = 0; e < 16; ++e) sc[e] = -scale * dp[e] * __builtin_amdgcn_exp2f(fmaf(sc[e], sl2, -cc0));
+          for (int qq = 0; qq < 4; ++qq) {  // rows rh*32 + drow(4qq + u, g)
+            const f32x4 c4 = *reinterpret_cast<const f32x4*>(sm.lse[buf] + rh * 32 + 8 * qq + 4 * g);
+            const f32x4 d4 = *reinterpret_cast<const f32x4*>(sm.dl[buf] + rh * 32 + 8 * qq + 4 * g);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              const int e = 4 * qq + u;
+              sc[e] = __builtin_amdgcn_exp2f(fmaf(sc[e], sl2, -c4[u]));  // P
+              dp[e] = scale * sc[e] * (dp[e] - d4[u]);                   // dA
+            }
+          }
+          const bf16x8 p0 = pack_b(sc, 0), p1 = pack_b(sc, 1);
+#pragma unroll
+          for (int t = 0; t < 2; ++t) {
+            dva[t] = mfma32(lds_tr_a<8>(sm.u.st.dv[buf], rh * 32, t * 32), p0, dva[t]);
+            dva[t] = mfma32(lds_tr_a<8>(sm.u.st.dv[buf], rh * 32 + 16, t * 32), p1, dva[t]);
+          }
+#pragma unroll
+          for (int e = 0; e < 16; ++e) sc[e] = dp[e];
+        } else {
+#pragma unroll
+          for (int e = 0; e < 16; ++e) sc[e] = -scale * dp[e] * __builtin_amdgcn_exp2f(fmaf(sc[e], sl2, -cc0));
+        }
         const bf16x8 d0 = pack_b(sc, 0), d1 = pack_b(sc, 1);
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
           const bf16x8 a0 = lds_tr_a<8>(qt, rh * 32, t * 32);
           const bf16x8 a1 = lds_tr_a<8>(qt, rh * 32 + 16, t * 32);
-          if (same) {
+          if (same || SM) {  // softmax: one accumulator, the same-chunk part is parked in dkt
             as_[t] = mfma32(a0, d0, as_[t]);
             as_[t] = mfma32(a1, d1, as_[t]);
           } else {
@@ -497,12 +581,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
       }
     }
     if (k + 2 < nsteps) {  // the step after next may stay in flight
-      if (near(k + 2)) dma_wait_but<6>();
-      else dma_wait_but<4>();
+      wait_next(near(k + 2));
     } else {
       dma_wait();
     }
     __syncthreads();
+  }
+  if (SM && !parked) park();
+  if (SM && live) {  // dV_J rows: the diagonal block's part is already in dvf
+    float* dst = bw.dvf + ((int64_t)bhq * T + Jw * PC + (w & 1) * 32 + l32) * 64;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) {
+        f32x4* p = reinterpret_cast<f32x4*>(dst + t * 32 + 8 * qq + 4 * g);
+        f32x4 x = *p;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) x[u] += dva[t][4 * qq + u];
+        *p = x;
+      }
   }
   // ---- per chunk of the pair: d k~_J = dk~(same) + dKL SUF_J, dSUF_J = dKL^T k~_J ----
   const int r0 = (tid >> 4) * 4, c0 = (tid & 15) * 4;
@@ -514,8 +611,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-          sm.u.fin.a[(w & 1) * 32 + l32][t * 32 + drow(e, g)] = as_[t][e];
-          sm.u.fin.f[(w & 1) * 32 + l32][t * 32 + drow(e, g)] = af[t][e];
+          if (!SM) sm.u.fin.a[(w & 1) * 32 + l32][t * 32 + drow(e, g)] = as_[t][e];
+          sm.u.fin.f[(w & 1) * 32 + l32][t * 32 + drow(e, g)] = SM ? as_[t][e] : af[t][e];
         }
     }
     load_mat64<false>(sm.u.fin.m, ws.suf + ((int64_t)bh * NT + J) * 4096);
@@ -528,8 +625,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         f32x4 v;
+        if (SM) v = *reinterpret_cast<const f32x4*>(dst + (r0 + i) * 64 + c0);  // parked part
 #pragma unroll
-        for (int j = 0; j < 4; ++j) v[j] = acc4[i][j] + sm.u.fin.a[r0 + i][c0 + j];
+        for (int j = 0; j < 4; ++j) v[j] = acc4[i][j] + (SM ? v[j] : sm.u.fin.a[r0 + i][c0 + j]);
         *reinterpret_cast<f32x4*>(dst + (r0 + i) * 64 + c0) = v;
       }
     }
@@ -549,6 +647,89 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
       }
     }
     __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// PaTH softmax backward of the diagonal blocks, per (chunk c, query head):
+//   delta_i = dO_i . O_i,  P = exp2(s' A_diag - lse_i) (j <= i),
+//   dA_diag = s P (dO V^T - delta_i),  dV_c = P^T dO_c   (the column sweep adds the rest)
+// fp32 on LDS.  grid (NT, B*HQ)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void path_softmax_diag_bwd_kernel(const bf16* __restrict__ dout, Strides dos,
+                                                                    const bf16* __restrict__ o, Strides os,
+                                                                    const bf16* __restrict__ v, Strides vs, int HQ,
+                                                                    int H, int T, float scale, PathFwdWs ws,
+                                                                    PathBwdWs bw) {
+  __shared__ __attribute__((aligned(16))) float Dm[64][68];
+  __shared__ __attribute__((aligned(16))) float Vm[64][68];
+  __shared__ __attribute__((aligned(16))) float Pm[64][68];
+  __shared__ float dls[64], lss[64];
+  const int NT = T / PC;
+  const int c = blockIdx.x, bhq = blockIdx.y;
+  const int G_ = HQ / H;
+  const int b = bhq / HQ, hq = bhq - b * HQ, h = hq / G_;
+  const int tid = threadIdx.x;
+  const int r0 = (tid >> 4) * 4, c0 = (tid & 15) * 4;
+  const int t0 = c * PC;
+  load_rows64_f32(Dm, dout + b * dos.b + hq * dos.h + (int64_t)t0 * dos.t, dos.t);
+  load_rows64_f32(Vm, v + b * vs.b + h * vs.h + (int64_t)t0 * vs.t, vs.t);
+  {  // delta of row r: 4 threads x 16 columns
+    const int r = tid >> 2, cc = (tid & 3) * 16;
+    const bf16* orow = o + b * os.b + hq * os.h + (int64_t)(t0 + r) * os.t + cc;
+    const bf16* drow_ = dout + b * dos.b + hq * dos.h + (int64_t)(t0 + r) * dos.t + cc;
+    float acc = 0.f;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const bf16x8 x = ld8(orow + 8 * hh), y = ld8(drow_ + 8 * hh);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc = fmaf((float)x[e], (float)y[e], acc);
+    }
+    acc += __shfl_xor(acc, 1, 64);
+    acc += __shfl_xor(acc, 2, 64);
+    if ((tid & 3) == 0) {
+      dls[r] = acc;
+      bw.delta[(int64_t)bhq * T + t0 + r] = acc;
+      lss[r] = ws.lse[(int64_t)bhq * T + t0 + r];
+    }
+  }
+  __syncthreads();
+  const float sl2 = scale * LOG2E_F;
+  {
+    const float* ad = ws.ld + ((int64_t)bhq * NT + c) * 4096;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f32x4 x = *reinterpret_cast<const f32x4*>(ad + (r0 + i) * 64 + c0);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        Pm[r0 + i][c0 + j] = (c0 + j <= r0 + i) ? __builtin_amdgcn_exp2f(fmaf(x[j], sl2, -lss[r0 + i])) : 0.f;
+    }
+  }
+  __syncthreads();
+  float acc[4][4];
+  zero44(acc);
+  lds_gemm64<false, true>(Dm, Vm, acc);  // dP = dO V^T
+  {
+    float* dst = bw.dad + ((int64_t)bhq * NT + c) * 4096;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f32x4 x;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x[j] = scale * Pm[r0 + i][c0 + j] * (acc[i][j] - dls[r0 + i]);
+      *reinterpret_cast<f32x4*>(dst + (r0 + i) * 64 + c0) = x;
+    }
+  }
+  zero44(acc);
+  lds_gemm64<true, false>(Pm, Dm, acc);  // dV_c = P^T dO
+  {
+    float* dst = bw.dvf + ((int64_t)bhq * T + t0) * 64;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f32x4 x;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x[j] = acc[i][j];
+      *reinterpret_cast<f32x4*>(dst + (r0 + i) * 64 + c0) = x;
+    }
   }
 }
 

@@ -26,7 +26,9 @@ int phip(const char* where) {
 
 size_t a256(size_t x) { return (x + 255) & ~size_t(255); }
 
-lucid::PathFwdWs carve_path_fwd(void* base, int B, int T, int H, int HQ, size_t* bytes) {
+// softmax = true: the PaTH softmax layout (row log-sum-exp instead of the solve's
+// diagonal inverses and O^T chain operand)
+lucid::PathFwdWs carve_path_fwd(void* base, int B, int T, int H, int HQ, size_t* bytes, bool softmax = false) {
   const size_t BH = (size_t)B * H, BHq = (size_t)B * HQ;
   const size_t NT = T / 64, NS = (NT + 7) / 8;
   lucid::PathFwdWs w{};
@@ -47,13 +49,14 @@ lucid::PathFwdWs carve_path_fwd(void* base, int B, int T, int H, int HQ, size_t*
   w.klT = reinterpret_cast<bf16*>(take(BH * T * 64 * 2));
   w.qt = reinterpret_cast<float*>(take(BHq * T * 64 * 4));
   w.ld = reinterpret_cast<float*>(take(BHq * NT * 4096 * 4));
-  w.y = reinterpret_cast<float*>(take(BHq * NT * 4096 * 4));
+  if (!softmax) w.y = reinterpret_cast<float*>(take(BHq * NT * 4096 * 4));
   w.qs = reinterpret_cast<bf16*>(take(BHq * 8 * T * 64 * 2));
   w.qsT = reinterpret_cast<bf16*>(take(BHq * 8 * T * 64 * 2));
   w.qb = reinterpret_cast<bf16*>(take(BHq * NS * T * 64 * 2));
   w.qbT = reinterpret_cast<bf16*>(take(BHq * NS * T * 64 * 2));
-  w.oT = reinterpret_cast<bf16*>(take(BHq * T * 64 * 2));
+  if (!softmax) w.oT = reinterpret_cast<bf16*>(take(BHq * T * 64 * 2));
   w.counters = reinterpret_cast<int*>(take(BHq * 4));
+  if (softmax) w.lse = reinterpret_cast<float*>(take(BHq * T * 4));
   if (bytes) *bytes = off;
   return w;
 }
@@ -74,7 +77,7 @@ int pcheck_vec(const char* name, const void* p, const int64_t* s) {
 
 lucid::Strides PS(const int64_t* s) { return lucid::Strides{s[0], s[1], s[2]}; }
 
-lucid::PathBwdWs carve_path_bwd(void* base, int B, int T, int HQ, size_t* bytes) {
+lucid::PathBwdWs carve_path_bwd(void* base, int B, int T, int HQ, size_t* bytes, bool softmax = false) {
   const size_t BHq = (size_t)B * HQ;
   const size_t NT = T / 64, NS = (NT + 7) / 8;
   lucid::PathBwdWs w{};
@@ -86,8 +89,10 @@ lucid::PathBwdWs carve_path_bwd(void* base, int B, int T, int HQ, size_t* bytes)
     return r;
   };
   w.dvf = reinterpret_cast<float*>(take(BHq * T * 64 * 4));
-  w.dvb = reinterpret_cast<bf16*>(take(BHq * T * 64 * 2));
-  w.dvT = reinterpret_cast<bf16*>(take(BHq * T * 64 * 2));
+  if (!softmax) {
+    w.dvb = reinterpret_cast<bf16*>(take(BHq * T * 64 * 2));
+    w.dvT = reinterpret_cast<bf16*>(take(BHq * T * 64 * 2));
+  }
   w.dad = reinterpret_cast<float*>(take(BHq * NT * 4096 * 4));
   w.dqt = reinterpret_cast<float*>(take(BHq * T * 64 * 4));
   w.dkt = reinterpret_cast<float*>(take(BHq * T * 64 * 4));
@@ -99,8 +104,59 @@ lucid::PathBwdWs carve_path_bwd(void* base, int B, int T, int HQ, size_t* bytes)
   w.dw = reinterpret_cast<float*>(take(BHq * T * 64 * 4));
   w.db = reinterpret_cast<float*>(take(BHq * T * 4));
   w.counters = reinterpret_cast<int*>(take(BHq * 4));
+  if (softmax) w.delta = reinterpret_cast<float*>(take(BHq * T * 4));
   if (bytes) *bytes = off;
   return w;
+}
+
+int check_shapes(int B, int T, int H, int HQ, int K) {
+  if (B <= 0 || T <= 0 || H <= 0 || HQ <= 0) return pfail("B, T, H and HQ must be positive");
+  if (K != 64) return pfail("head_dim must be 64, got " + std::to_string(K));
+  if (T % 64) return pfail("T must be a multiple of 64, got " + std::to_string(T));
+  if (HQ % H) return pfail("the number of query heads must be a multiple of the key heads");
+  return 0;
+}
+
+// shared by both forwards: WY form, large-chunk products, query transport, and the
+// decode key cache
+int launch_front(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                 const void* w, const int64_t* w_strides, const void* beta, const int64_t* beta_strides,
+                 int B, int T, int H, int HQ, float scale, int softmax, const lucid::PathFwdWs& ws, hipStream_t st) {
+  const int NT = T / 64, NS = (NT + 7) / 8;
+  const int BH = B * H, BHq = B * HQ;
+  LUCID_TIMED_LAUNCH(phip, "path_chunk_kernel", lucid::path_chunk_kernel, dim3(NT, BHq), st, (const bf16*)q, PS(q_strides),
+                     (const bf16*)k, PS(k_strides), (const bf16*)w, PS(w_strides), (const bf16*)beta,
+                     PS(beta_strides), HQ, H, T, scale, softmax, ws);
+  LUCID_TIMED_LAUNCH(phip, "path_large_kernel", lucid::path_large_kernel, dim3(NS, BH), st, T, ws);
+  LUCID_TIMED_LAUNCH(phip, "path_transport_kernel", lucid::path_transport_kernel, dim3(NT, BHq), st, HQ, H, T, ws);
+  return 0;
+}
+
+int launch_kcache(void* kcache, const int64_t* kcache_strides, int B, int T, int H, const lucid::PathFwdWs& ws,
+                  hipStream_t st) {
+  const int NT = T / 64;
+  LUCID_TIMED_LAUNCH(phip, "path_kcache_kernel", lucid::path_kcache_kernel, dim3(NT, B * H), st, T, (bf16*)kcache,
+                     PS(kcache_strides), H, ws);
+  return 0;
+}
+
+// the logit-gradient stages shared by both backwards (after dV, dA and the row/column
+// sweeps): products, WY backward, GQA reduction
+int launch_back(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides, const void* w,
+                const int64_t* w_strides, const void* beta, const int64_t* beta_strides, void* dq,
+                const int64_t* dq_strides, void* dk, const int64_t* dk_strides, void* dv, const int64_t* dv_strides,
+                void* dw, const int64_t* dw_strides, void* dbeta, const int64_t* dbeta_strides, int B, int T, int H,
+                int HQ, const lucid::PathFwdWs& ws, const lucid::PathBwdWs& bw, hipStream_t st) {
+  const int NT = T / 64, NS = (NT + 7) / 8;
+  const int BH = B * H, BHq = B * HQ;
+  LUCID_TIMED_LAUNCH(phip, "path_products_bwd_kernel", lucid::path_products_bwd_kernel, dim3(NS, BHq), st, HQ, H, T, ws, bw);
+  LUCID_TIMED_LAUNCH(phip, "path_wy_bwd_kernel", lucid::path_wy_bwd_kernel, dim3(NT, BHq), st, (const bf16*)q, PS(q_strides),
+                     (const bf16*)k, PS(k_strides), (const bf16*)w, PS(w_strides), (const bf16*)beta,
+                     PS(beta_strides), HQ, H, T, ws, bw);
+  LUCID_TIMED_LAUNCH(phip, "path_reduce_kernel", lucid::path_reduce_kernel, dim3((T + 3) / 4, BH), st, HQ, H, T, bw,
+                     (bf16*)dq, PS(dq_strides), (bf16*)dk, PS(dk_strides), (bf16*)dv, PS(dv_strides), (bf16*)dw,
+                     PS(dw_strides), (bf16*)dbeta, PS(dbeta_strides));
+  return 0;
 }
 
 }  // namespace
@@ -124,10 +180,7 @@ int lucid_path_fwd(const void* q, const int64_t* q_strides, const void* k, const
                    void* kcache, const int64_t* kcache_strides, void* fwd_ws, int B, int T, int H, int HQ,
                    int K, float scale, void* stream) {
   g_path_error.clear();
-  if (B <= 0 || T <= 0 || H <= 0 || HQ <= 0) return pfail("B, T, H and HQ must be positive");
-  if (K != 64) return pfail("head_dim must be 64, got " + std::to_string(K));
-  if (T % 64) return pfail("T must be a multiple of 64, got " + std::to_string(T));
-  if (HQ % H) return pfail("the number of query heads must be a multiple of the key heads");
+  if (int rc = check_shapes(B, T, H, HQ, K)) return rc;
   if (int rc = pcheck_vec("q", q, q_strides)) return rc;
   if (int rc = pcheck_vec("k", k, k_strides)) return rc;
   if (int rc = pcheck_vec("v", v, v_strides)) return rc;
@@ -140,19 +193,14 @@ int lucid_path_fwd(const void* q, const int64_t* q_strides, const void* k, const
   if (reinterpret_cast<uintptr_t>(fwd_ws) % 256) return pfail("fwd_ws must be 256-byte aligned");
   const lucid::PathFwdWs ws = carve_path_fwd(fwd_ws, B, T, H, HQ, nullptr);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const int NT = T / 64, NS = (NT + 7) / 8;
-  const int BH = B * H, BHq = B * HQ;
-  LUCID_TIMED_LAUNCH(phip, "path_chunk_kernel", lucid::path_chunk_kernel, dim3(NT, BHq), st, (const bf16*)q, PS(q_strides),
-                     (const bf16*)k, PS(k_strides), (const bf16*)w, PS(w_strides), (const bf16*)beta,
-                     PS(beta_strides), HQ, H, T, scale, ws);
-  LUCID_TIMED_LAUNCH(phip, "path_large_kernel", lucid::path_large_kernel, dim3(NS, BH), st, T, ws);
-  LUCID_TIMED_LAUNCH(phip, "path_transport_kernel", lucid::path_transport_kernel, dim3(NT, BHq), st, HQ, H, T, ws);
+  const int NT = T / 64;
+  const int BHq = B * HQ;
+  if (int rc = launch_front(q, q_strides, k, k_strides, w, w_strides, beta, beta_strides, B, T, H, HQ, scale, 0, ws, st))
+    return rc;
   LUCID_TIMED_LAUNCH(phip, "path_solve_fwd_kernel", lucid::path_solve_fwd_kernel, dim3(NT * BHq), st, (const bf16*)v,
                      PS(v_strides), (bf16*)o, PS(o_strides), HQ, H, T, BHq, scale, ws);
-  if (kcache) {
-    LUCID_TIMED_LAUNCH(phip, "path_kcache_kernel", lucid::path_kcache_kernel, dim3(NT, BH), st, T, (bf16*)kcache,
-                       PS(kcache_strides), H, ws);
-  }
+  if (kcache)
+    if (int rc = launch_kcache(kcache, kcache_strides, B, T, H, ws, st)) return rc;
   return 0;
 }
 
@@ -172,10 +220,7 @@ int lucid_path_bwd(const void* dout, const int64_t* do_strides, const void* q, c
                    const int64_t* dbeta_strides, void* bwd_ws, int B, int T, int H, int HQ, int K, float scale,
                    void* stream) {
   g_path_error.clear();
-  if (B <= 0 || T <= 0 || H <= 0 || HQ <= 0) return pfail("B, T, H and HQ must be positive");
-  if (K != 64) return pfail("head_dim must be 64, got " + std::to_string(K));
-  if (T % 64) return pfail("T must be a multiple of 64, got " + std::to_string(T));
-  if (HQ % H) return pfail("the number of query heads must be a multiple of the key heads");
+  if (int rc = check_shapes(B, T, H, HQ, K)) return rc;
   if (int rc = pcheck_vec("dout", dout, do_strides)) return rc;
   if (int rc = pcheck_vec("q", q, q_strides)) return rc;
   if (int rc = pcheck_vec("k", k, k_strides)) return rc;
@@ -194,23 +239,105 @@ int lucid_path_bwd(const void* dout, const int64_t* do_strides, const void* q, c
   const lucid::PathBwdWs bw = carve_path_bwd(bwd_ws, B, T, HQ, nullptr);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int NT = T / 64, NS = (NT + 7) / 8;
-  const int BH = B * H, BHq = B * HQ;
+  const int BHq = B * HQ;
   const int64_t n_hl = (int64_t)BHq * NS * 4096, n_hc = (int64_t)BHq * NT * 4096;
+  const lucid::Strides dvs{(int64_t)HQ * T * 64, (int64_t)T * 64, 64};  // dV rows [B][HQ][T][64]
   LUCID_TIMED_LAUNCH(phip, "path_bwd_zero_kernel", lucid::path_bwd_zero_kernel, dim3(1024), st, n_hl, n_hc, BHq, bw);
   LUCID_TIMED_LAUNCH(phip, "path_dv_kernel", lucid::path_dv_kernel, dim3(NT * BHq), st, (const bf16*)dout, PS(do_strides),
                      (const bf16*)o, PS(o_strides), HQ, H, T, BHq, scale, ws, bw);
-  LUCID_TIMED_LAUNCH(phip, "path_bwd_row_kernel", lucid::path_bwd_row_kernel, dim3((NT + 1) / 2, BHq), st, (const bf16*)o, PS(o_strides),
-                     HQ, H, T, scale, ws, bw);
-  LUCID_TIMED_LAUNCH(phip, "path_bwd_col_kernel", lucid::path_bwd_col_kernel, dim3((NT + 1) / 2, BHq), st, (const bf16*)o, PS(o_strides),
-                     HQ, H, T, scale, ws, bw);
-  LUCID_TIMED_LAUNCH(phip, "path_products_bwd_kernel", lucid::path_products_bwd_kernel, dim3(NS, BHq), st, HQ, H, T, ws, bw);
-  LUCID_TIMED_LAUNCH(phip, "path_wy_bwd_kernel", lucid::path_wy_bwd_kernel, dim3(NT, BHq), st, (const bf16*)q, PS(q_strides),
-                     (const bf16*)k, PS(k_strides), (const bf16*)w, PS(w_strides), (const bf16*)beta,
-                     PS(beta_strides), HQ, H, T, ws, bw);
-  LUCID_TIMED_LAUNCH(phip, "path_reduce_kernel", lucid::path_reduce_kernel, dim3((T + 3) / 4, BH), st, HQ, H, T, bw,
-                     (bf16*)dq, PS(dq_strides), (bf16*)dk, PS(dk_strides), (bf16*)dv, PS(dv_strides), (bf16*)dw,
-                     PS(dw_strides), (bf16*)dbeta, PS(dbeta_strides));
+  LUCID_TIMED_LAUNCH(phip, "path_bwd_row_kernel", lucid::path_bwd_row_kernel<false>, dim3((NT + 1) / 2, BHq), st,
+                     (const bf16*)bw.dvb, dvs, (const bf16*)o, PS(o_strides), HQ, H, T, scale, ws, bw);
+  LUCID_TIMED_LAUNCH(phip, "path_bwd_col_kernel", lucid::path_bwd_col_kernel<false>, dim3((NT + 1) / 2, BHq), st,
+                     (const bf16*)bw.dvb, dvs, (const bf16*)o, PS(o_strides), HQ, H, T, scale, ws, bw);
+  return launch_back(q, q_strides, k, k_strides, w, w_strides, beta, beta_strides, dq, dq_strides, dk, dk_strides, dv,
+                     dv_strides, dw, dw_strides, dbeta, dbeta_strides, B, T, H, HQ, ws, bw, st);
+}
+
+size_t lucid_path_softmax_fwd_workspace_bytes(int B, int T, int H, int HQ, int K) {
+  (void)K;
+  size_t n = 0;
+  carve_path_fwd(nullptr, B, T, H, HQ, &n, true);
+  return n;
+}
+
+int lucid_path_softmax_fwd(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                           const void* v, const int64_t* v_strides, const void* w, const int64_t* w_strides,
+                           const void* beta, const int64_t* beta_strides, void* o, const int64_t* o_strides,
+                           void* kcache, const int64_t* kcache_strides, void* fwd_ws, int B, int T, int H, int HQ,
+                           int K, float scale, void* stream) {
+  g_path_error.clear();
+  if (int rc = check_shapes(B, T, H, HQ, K)) return rc;
+  if (int rc = pcheck_vec("q", q, q_strides)) return rc;
+  if (int rc = pcheck_vec("k", k, k_strides)) return rc;
+  if (int rc = pcheck_vec("v", v, v_strides)) return rc;
+  if (int rc = pcheck_vec("w", w, w_strides)) return rc;
+  if (int rc = pcheck("beta", beta, beta_strides)) return rc;
+  if (int rc = pcheck_vec("o", o, o_strides)) return rc;
+  if (kcache)
+    if (int rc = pcheck_vec("kcache", kcache, kcache_strides)) return rc;
+  if (!fwd_ws) return pfail("fwd_ws is null");
+  if (reinterpret_cast<uintptr_t>(fwd_ws) % 256) return pfail("fwd_ws must be 256-byte aligned");
+  const lucid::PathFwdWs ws = carve_path_fwd(fwd_ws, B, T, H, HQ, nullptr, true);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int NT = T / 64;
+  if (int rc = launch_front(q, q_strides, k, k_strides, w, w_strides, beta, beta_strides, B, T, H, HQ, scale, 1, ws, st))
+    return rc;
+  LUCID_TIMED_LAUNCH(phip, "path_softmax_fwd_kernel", lucid::path_softmax_fwd_kernel, dim3((NT + 1) / 2, B * HQ), st,
+                     (const bf16*)v, PS(v_strides), (bf16*)o, PS(o_strides), HQ, H, T, scale, ws);
+  if (kcache)
+    if (int rc = launch_kcache(kcache, kcache_strides, B, T, H, ws, st)) return rc;
   return 0;
+}
+
+size_t lucid_path_softmax_bwd_workspace_bytes(int B, int T, int H, int HQ, int K) {
+  (void)H;
+  (void)K;
+  size_t n = 0;
+  carve_path_bwd(nullptr, B, T, HQ, &n, true);
+  return n;
+}
+
+int lucid_path_softmax_bwd(const void* dout, const int64_t* do_strides, const void* q, const int64_t* q_strides,
+                           const void* k, const int64_t* k_strides, const void* v, const int64_t* v_strides,
+                           const void* w, const int64_t* w_strides, const void* beta, const int64_t* beta_strides,
+                           const void* o, const int64_t* o_strides, const void* fwd_ws, void* dq,
+                           const int64_t* dq_strides, void* dk, const int64_t* dk_strides, void* dv,
+                           const int64_t* dv_strides, void* dw, const int64_t* dw_strides, void* dbeta,
+                           const int64_t* dbeta_strides, void* bwd_ws, int B, int T, int H, int HQ, int K,
+                           float scale, void* stream) {
+  g_path_error.clear();
+  if (int rc = check_shapes(B, T, H, HQ, K)) return rc;
+  if (int rc = pcheck_vec("dout", dout, do_strides)) return rc;
+  if (int rc = pcheck_vec("q", q, q_strides)) return rc;
+  if (int rc = pcheck_vec("k", k, k_strides)) return rc;
+  if (int rc = pcheck_vec("v", v, v_strides)) return rc;
+  if (int rc = pcheck_vec("w", w, w_strides)) return rc;
+  if (int rc = pcheck("beta", beta, beta_strides)) return rc;
+  if (int rc = pcheck_vec("o", o, o_strides)) return rc;
+  if (int rc = pcheck("dq", dq, dq_strides)) return rc;
+  if (int rc = pcheck("dk", dk, dk_strides)) return rc;
+  if (int rc = pcheck("dv", dv, dv_strides)) return rc;
+  if (int rc = pcheck("dw", dw, dw_strides)) return rc;
+  if (int rc = pcheck("dbeta", dbeta, dbeta_strides)) return rc;
+  if (!fwd_ws || !bwd_ws) return pfail("fwd_ws and bwd_ws must be non-null");
+  if (reinterpret_cast<uintptr_t>(fwd_ws) % 256 || reinterpret_cast<uintptr_t>(bwd_ws) % 256)
+    return pfail("fwd_ws and bwd_ws must be 256-byte aligned");
+  const lucid::PathFwdWs ws = carve_path_fwd(const_cast<void*>(fwd_ws), B, T, H, HQ, nullptr, true);
+  const lucid::PathBwdWs bw = carve_path_bwd(bwd_ws, B, T, HQ, nullptr, true);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int NT = T / 64, NS = (NT + 7) / 8;
+  const int BHq = B * HQ;
+  const int64_t n_hl = (int64_t)BHq * NS * 4096, n_hc = (int64_t)BHq * NT * 4096;
+  LUCID_TIMED_LAUNCH(phip, "path_bwd_zero_kernel", lucid::path_bwd_zero_kernel, dim3(1024), st, n_hl, n_hc, BHq, bw);
+  LUCID_TIMED_LAUNCH(phip, "path_softmax_diag_bwd_kernel", lucid::path_softmax_diag_bwd_kernel, dim3(NT, BHq), st,
+                     (const bf16*)dout, PS(do_strides), (const bf16*)o, PS(o_strides), (const bf16*)v, PS(v_strides),
+                     HQ, H, T, scale, ws, bw);
+  LUCID_TIMED_LAUNCH(phip, "path_softmax_bwd_row_kernel", lucid::path_bwd_row_kernel<true>, dim3((NT + 1) / 2, BHq), st,
+                     (const bf16*)dout, PS(do_strides), (const bf16*)v, PS(v_strides), HQ, H, T, scale, ws, bw);
+  LUCID_TIMED_LAUNCH(phip, "path_softmax_bwd_col_kernel", lucid::path_bwd_col_kernel<true>, dim3((NT + 1) / 2, BHq), st,
+                     (const bf16*)dout, PS(do_strides), (const bf16*)v, PS(v_strides), HQ, H, T, scale, ws, bw);
+  return launch_back(q, q_strides, k, k_strides, w, w_strides, beta, beta_strides, dq, dq_strides, dk, dk_strides, dv,
+                     dv_strides, dw, dw_strides, dbeta, dbeta_strides, B, T, H, HQ, ws, bw, st);
 }
 
 void lucid_path_profile_enable(int on) { lucid_prof::enabled() = on != 0; }

@@ -38,6 +38,7 @@ struct PathFwdWs {
   bf16* qbT;    // [BHq][NS][64][T]   QB^T, T-perm
   bf16* oT;     // [BHq][64][T]       O^T, T-perm (chain operand)
   int* counters;  // [BHq]
+  float* lse;   // [BHq][T]           PaTH softmax only: row log-sum-exp, exp2 domain (log2(l) + m)
 };
 
 // ---------------------------------------------------------------------------
@@ -48,7 +49,7 @@ __global__ __launch_bounds__(256) void path_chunk_kernel(const bf16* __restrict_
                                                          const bf16* __restrict__ k, Strides ks,
                                                          const bf16* __restrict__ w, Strides wst,
                                                          const bf16* __restrict__ beta, Strides bst, int HQ, int H,
-                                                         int T, float scale, PathFwdWs ws) {
+                                                         int T, float scale, int softmax, PathFwdWs ws) {
   __shared__ __attribute__((aligned(16))) float Wm[64][68];
   __shared__ __attribute__((aligned(16))) float Wb[64][68];
   __shared__ __attribute__((aligned(16))) float Tm[64][68];
@@ -178,12 +179,24 @@ __global__ __launch_bounds__(256) void path_chunk_kernel(const bf16* __restrict_
     }
   }
   // A_diag = tril(Q K^T - QW TW); L_diag = stril(exp(s A - 1/s)) -> W2s, global
+  // (PaTH softmax: the logits themselves, diagonal included; no inverse)
   float acc2[4][4];
   zero44(acc);
   zero44(acc2);
   lds_gemm64<false, true>(Qs, Ks, acc);
   lds_gemm64<false, false>(X, Wb, acc2);
   __syncthreads();
+  if (softmax) {
+    float* dst = ws.ld + ((int64_t)bhq * NT + c) * 4096;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f32x4 v;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] = (c0 + j <= r0 + i) ? acc[i][j] - acc2[i][j] : 0.f;
+      *reinterpret_cast<f32x4*>(dst + (r0 + i) * 64 + c0) = v;
+    }
+    return;
+  }
   {
     const float sl2 = scale * LOG2E_F, cc0 = LOG2E_F / scale;
     float* dst = ws.ld + ((int64_t)bhq * NT + c) * 4096;
@@ -477,6 +490,167 @@ __global__ __launch_bounds__(256) void path_solve_fwd_kernel(const bf16* __restr
     *reinterpret_cast<bf16x8*>(ws.oT + ((int64_t)bhq * 64 + dd) * T + i0 + s8) = ld8(lo[0] + dd * 64 + s8);
   }
   publish_counter(cnt, I + 1);
+}
+
+// ---------------------------------------------------------------------------
+// PaTH softmax attention forward: the in-chunk pass of intra_chunk_preprocess_fwd.py:71-115
+// and the inter-chunk online softmax of parallel_path_fwd.py:54-124 in one kernel, on the
+// same two-level logit blocks as the solve above:
+//   O_i = sum_{j <= i} exp2(s' A_ij - lse_i) v_j,  s' = s log2(e)
+// Per pair of query chunks I1 = 2p, I1 + 1 (one large chunk); wave w owns rows 32w ..
+// of the pair (chunk Iw = I1 + w/2, lane <-> row, both lane halves hold the same row
+// and half of the keys).  The diagonal block reads the in-chunk logits; key chunks
+// J < Iw give S^T[j][i] = Kop_J . Qop_I^(J).  O^T[d][i] += V^T[d][j] P^T[j][i] with V^T
+// from transposing LDS reads.  Key-operand and V rows are staged by direct
+// global->LDS loads (double buffered).  The row log-sum-exp (exp2 domain) is kept
+// for the backward.  grid ((NT+1)/2, B*HQ), pairs with the most key chunks first.
+// ---------------------------------------------------------------------------
+struct SoftmaxFwdSmem {
+  bf16 k[2][64 * 64];   // swizzled (chunk c of row r at c ^ (r & 7))
+  bf16 v[2][64 * 64];
+  bf16 vd[2][64 * 64];  // V rows of the pair's own chunks (diagonal blocks)
+};
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void path_softmax_fwd_kernel(
+    const bf16* __restrict__ v, Strides vs, bf16* __restrict__ o, Strides os, int HQ, int H, int T, float scale,
+    PathFwdWs ws) {
+  __shared__ __attribute__((aligned(16))) SoftmaxFwdSmem sm;
+  const int NT = T / PC, NS = (NT + PR - 1) / PR, NP = (NT + 1) / 2;
+  const int I1 = 2 * (NP - 1 - (int)blockIdx.x), bhq = blockIdx.y;
+  const int G_ = HQ / H;
+  const int b = bhq / HQ, hq = bhq - b * HQ, h = hq / G_, bh = b * H + h;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
+  const int Iw = I1 + (w >> 1);
+  const bool pair = I1 + 1 < NT;  // NT odd: the last pair has one chunk
+  const bool live = Iw < NT;
+  const int sI = I1 / PR, cb = sI * PR;
+  const int rl = (w & 1) * 32 + l32;                   // this lane's row inside its chunk
+  const int iw0 = min(Iw, NT - 1) * PC + (w & 1) * 32;  // first row of this wave
+  const int nJ = pair ? I1 + 1 : I1;                   // key tiles needed by the pair
+  const float sl2 = scale * LOG2E_F;
+  const bf16* vh = v + b * vs.b + h * vs.h;
+
+  int plan_k[2], plan_v[2];
+  dma_plan<64, 8>(64, plan_k);
+  dma_plan<64, 8>(vs.t, plan_v);
+  auto stage = [&](int J) {
+    const int buf = J & 1;
+    dma_stage<64, 8>(plan_k, ((J < cb) ? ws.kl : ws.kt) + ((int64_t)bh * T + J * PC) * 64, sm.k[buf]);
+    dma_stage<64, 8>(plan_v, vh + (int64_t)J * PC * vs.t, sm.v[buf]);
+  };
+  dma_stage<64, 8>(plan_v, vh + (int64_t)I1 * PC * vs.t, sm.vd[0]);
+  if (pair) dma_stage<64, 8>(plan_v, vh + (int64_t)(I1 + 1) * PC * vs.t, sm.vd[1]);
+  if (nJ > 0) stage(0);
+
+  f32x16 acc[2] = {zero16(), zero16()};
+  float m = 0.f, l = 0.f;
+  f32x16 sc[2];
+  if (live) {  // in-chunk logits of row rl, keys j = 32 jh + drow(e, g); keys j > rl are masked
+    const float* ad = ws.ld + ((int64_t)bhq * NT + Iw) * 4096 + rl * 64;
+#pragma unroll
+    for (int jh = 0; jh < 2; ++jh)
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) {
+        const f32x4 x = *reinterpret_cast<const f32x4*>(ad + jh * 32 + 8 * qq + 4 * g);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int j = jh * 32 + 8 * qq + 4 * g + u;
+          sc[jh][4 * qq + u] = (j <= rl) ? x[u] * sl2 : -INFINITY;
+        }
+      }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int jh = 0; jh < 2; ++jh)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sc[jh][e]);
+    m = fmaxf(mx, wave_xor32(mx));  // finite: the diagonal key is always present
+#pragma unroll
+    for (int jh = 0; jh < 2; ++jh)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        sc[jh][e] = __builtin_amdgcn_exp2f(sc[jh][e] - m);
+        l += sc[jh][e];
+      }
+  }
+  dma_wait();
+  __syncthreads();
+  if (live) {
+    const bf16* vt = sm.vd[w >> 1];
+#pragma unroll
+    for (int jh = 0; jh < 2; ++jh) {
+      const bf16x8 p0 = pack_b(sc[jh], 0), p1 = pack_b(sc[jh], 1);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        acc[t] = mfma32(lds_tr_a<8>(vt, jh * 32, t * 32), p0, acc[t]);
+        acc[t] = mfma32(lds_tr_a<8>(vt, jh * 32 + 16, t * 32), p1, acc[t]);
+      }
+    }
+  }
+  bf16x8 qb[4];
+  for (int J = 0; J < nJ; ++J) {
+    const int buf = J & 1;
+    if (J + 1 < nJ) stage(J + 1);
+    if (J >= cb || J % PR == 0) {  // the query operand changes
+      const bf16* qsrc = (J < cb) ? ws.qb + ((int64_t)bhq * NS + J / PR) * T * 64
+                                  : ws.qs + ((int64_t)bhq * PR + (J - cb)) * T * 64;
+#pragma unroll
+      for (int st = 0; st < 4; ++st) qb[st] = ld8(qsrc + (int64_t)(iw0 + l32) * 64 + 16 * st + 8 * g);
+    }
+    if (live && J < Iw) {
+#pragma unroll
+      for (int jh = 0; jh < 2; ++jh) {
+        sc[jh] = zero16();
+#pragma unroll
+        for (int st = 0; st < 4; ++st) sc[jh] = mfma32(ld8(swz<8>(sm.k[buf], jh * 32 + l32, 2 * st + g)), qb[st], sc[jh]);
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int jh = 0; jh < 2; ++jh)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sc[jh][e]);
+      mx = fmaxf(mx, wave_xor32(mx));
+      const float mn = fmaxf(m, mx * sl2);
+      const float alpha = __builtin_amdgcn_exp2f(m - mn);
+      m = mn;
+      l *= alpha;
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[t][e] *= alpha;
+#pragma unroll
+      for (int jh = 0; jh < 2; ++jh) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          sc[jh][e] = __builtin_amdgcn_exp2f(fmaf(sc[jh][e], sl2, -mn));
+          l += sc[jh][e];
+        }
+        const bf16x8 p0 = pack_b(sc[jh], 0), p1 = pack_b(sc[jh], 1);
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          acc[t] = mfma32(lds_tr_a<8>(sm.v[buf], jh * 32, t * 32), p0, acc[t]);
+          acc[t] = mfma32(lds_tr_a<8>(sm.v[buf], jh * 32 + 16, t * 32), p1, acc[t]);
+        }
+      }
+    }
+    dma_wait();
+    __syncthreads();
+  }
+  if (live) {
+    l += wave_xor32(l);
+    const float inv = 1.f / l;
+    const int i = iw0 + l32;
+    bf16* orow = o + b * os.b + hq * os.h + (int64_t)i * os.t;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) {
+        bf16x4 bb;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) bb[u] = (bf16)(acc[t][4 * qq + u] * inv);
+        *reinterpret_cast<bf16x4*>(orow + t * 32 + 8 * qq + 4 * g) = bb;
+      }
+    if (g == 0) ws.lse[(int64_t)bhq * T + i] = m + log2f(l);
+  }
 }
 
 // ---------------------------------------------------------------------------

@@ -7,6 +7,13 @@ asserts (parallel.py:180-241) and returns ``(o, k_cache)``.
     O = (I + L)^-1 V,  L_ij = exp(s A_ij - 1/s) (j < i),  A_ij = q_i^T H_i ... H_{j+1} k_j,
     H_t = I - beta_t w_t w_t^T
 
+:func:`parallel_path_attention` is PaTH softmax attention on the same path logits
+(diagonal included), the softmax half of a LUCID-Path layer, whose forward the
+reference ships as the kernels ``intra_chunk_preprocess_fwd.py`` and
+``parallel_path_fwd.py`` (entry point and backward in the unvendored fla package):
+
+    O_i = sum_{j <= i} softmax_j(s A_ij) v_j
+
 Tensors are bf16 GPU tensors in the reference layout ``[B, T, H, K]``; K = V = 64.
 There is no CPU or Triton fallback.
 """
@@ -37,23 +44,24 @@ def _ready(x: torch.Tensor) -> torch.Tensor:
     return x
 
 
-def _fwd(q, k, v, w, beta, scale, use_cache):
+def _fwd(q, k, v, w, beta, scale, use_cache, softmax=False):
     lib = _lib.load(_LIB)
+    pre = "lucid_path_softmax_" if softmax else "lucid_path_"
     B, T, HQ, K = q.shape
     H = k.shape[2]
     dev = q.device
     o = torch.empty(B, T, HQ, v.shape[-1], dtype=torch.bfloat16, device=dev)
     kc = torch.empty(B, T, H, K, dtype=torch.bfloat16, device=dev) if use_cache else None
-    ws = torch.empty(lib.lucid_path_fwd_workspace_bytes(B, T, H, HQ, K), dtype=torch.uint8, device=dev)
+    ws = torch.empty(getattr(lib, pre + "fwd_workspace_bytes")(B, T, H, HQ, K), dtype=torch.uint8, device=dev)
     beta = beta.contiguous()
     st3 = lambda t: _lib.strides3(t, (0, 2, 1))  # noqa: E731  (batch, head, time)
     beta_strides = (ctypes.c_int64 * 3)(beta.stride(0), beta.stride(2), beta.stride(1))
-    rc = lib.lucid_path_fwd(
+    rc = getattr(lib, pre + "fwd")(
         _lib.ptr(q), st3(q), _lib.ptr(k), st3(k), _lib.ptr(v), st3(v), _lib.ptr(w), st3(w),
         _lib.ptr(beta), beta_strides, _lib.ptr(o), st3(o),
         _lib.ptr(kc) if kc is not None else None, st3(kc) if kc is not None else None,
         _lib.ptr(ws), B, T, H, HQ, K, float(scale), _lib.stream_handle(dev))
-    _lib.check(lib, rc, "lucid_path_fwd")
+    _lib.check(lib, rc, pre + "fwd")
     return o, kc, ws
 
 
@@ -98,6 +106,104 @@ class ParallelLUCIDPathAttentionFunction(torch.autograd.Function):
         return (dq[:, :t], dk[:, :t], dv[:, :t], dw[:, :t], db[:, :t], None, None, None, None)
 
 
+class ParallelPathAttentionFunction(torch.autograd.Function):
+    """Forward/backward of PaTH softmax attention (forward: intra_chunk_preprocess_fwd.py:14-168
+    then parallel_path_fwd.py:13-170; backward: softmax gradient of the same logits)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, w, beta, g, scale, cu_seqlens, use_cache=False):
+        t = q.shape[1]
+        tp = (t + 63) // 64 * 64
+        q, k, v, w, beta = (_ready(_pad_t(x, tp)) for x in (q, k, v, w, beta))
+        o, kc, ws = _fwd(q, k, v, w, beta, scale, use_cache, softmax=True)
+        ctx.save_for_backward(q, k, v, w, beta, o, ws)
+        ctx.scale, ctx.t = scale, t
+        if kc is not None:
+            kc = kc[:, :t]
+            ctx.mark_non_differentiable(kc)
+        return o[:, :t], kc
+
+    @staticmethod
+    def backward(ctx, do, dk_cache):
+        q, k, v, w, beta, o, ws = ctx.saved_tensors
+        t, tp = ctx.t, q.shape[1]
+        if do.dtype != torch.bfloat16:
+            do = do.to(torch.bfloat16)
+        do = _ready(_pad_t(do, tp))
+        lib = _lib.load(_LIB)
+        B, T, HQ, K = q.shape
+        H = k.shape[2]
+        dq, dk, dv, dw = (torch.empty_like(x) for x in (q, k, v, w))
+        db = torch.empty(B, T, H, dtype=torch.bfloat16, device=q.device)
+        bws = torch.empty(lib.lucid_path_softmax_bwd_workspace_bytes(B, T, H, HQ, K), dtype=torch.uint8,
+                          device=q.device)
+        st3 = lambda x: _lib.strides3(x, (0, 2, 1))  # noqa: E731
+        bst = lambda x: (ctypes.c_int64 * 3)(x.stride(0), x.stride(2), x.stride(1))  # noqa: E731
+        rc = lib.lucid_path_softmax_bwd(
+            _lib.ptr(do), st3(do), _lib.ptr(q), st3(q), _lib.ptr(k), st3(k), _lib.ptr(v), st3(v),
+            _lib.ptr(w), st3(w), _lib.ptr(beta), bst(beta), _lib.ptr(o), st3(o), _lib.ptr(ws),
+            _lib.ptr(dq), st3(dq), _lib.ptr(dk), st3(dk), _lib.ptr(dv), st3(dv), _lib.ptr(dw), st3(dw),
+            _lib.ptr(db), bst(db), _lib.ptr(bws), B, T, H, HQ, K, float(ctx.scale), _lib.stream_handle(q.device))
+        _lib.check(lib, rc, "lucid_path_softmax_bwd")
+        return (dq[:, :t], dk[:, :t], dv[:, :t], dw[:, :t], db[:, :t], None, None, None, None)
+
+
+def _check(q, k, v, w, beta, g):
+    assert q.shape[-1] in [16, 32, 64, 128], "only support head_dim in [16, 32, 64, 128] for now. Stay tuned!"
+    assert v.shape[-1] in [16, 32, 64, 128], "only support head_dim in [16, 32, 64, 128] for now. Stay tuned!"
+    assert q.shape[-1] == k.shape[-1], 'q, k should have the same head_dim.'
+    assert k.shape == w.shape, 'k, w should have the same shape.'
+    assert beta.shape[:3] == k.shape[:3], 'beta should have the same number of heads as k'
+    assert g is None, 'g is not supported'
+    assert q.shape[-2] % k.shape[-2] == 0, 'the number of query heads should be divisible by the number of key heads'
+    if q.shape[-1] != 64 or v.shape[-1] != 64:
+        raise NotImplementedError("lucid_amd LUCID-Path kernels support head_dim 64")
+    for name, x in (("q", q), ("k", k), ("v", v), ("w", w), ("beta", beta)):
+        if not x.is_cuda:
+            raise RuntimeError(f"lucid_amd: {name} must be a GPU tensor (no CPU path)")
+        if x.dtype != torch.bfloat16:
+            raise TypeError(f"lucid_amd: {name} must be bfloat16, got {x.dtype}")
+
+
+def _apply(fn, q, k, v, w, beta, g, scale, cu_seqlens, use_cache):
+    if cu_seqlens is not None:
+        if q.shape[0] != 1:
+            raise ValueError("cu_seqlens requires batch size 1 (packed sequences)")
+        outs, caches = [], []
+        bounds = cu_seqlens.tolist()
+        for s0, s1 in zip(bounds[:-1], bounds[1:]):
+            o_i, kc_i = fn.apply(q[:, s0:s1], k[:, s0:s1], v[:, s0:s1], w[:, s0:s1], beta[:, s0:s1], g, scale,
+                                 None, use_cache)
+            outs.append(o_i)
+            caches.append(kc_i)
+        return torch.cat(outs, 1), (torch.cat(caches, 1) if use_cache else None)
+    return fn.apply(q, k, v, w, beta, g, scale, cu_seqlens, use_cache)
+
+
+@torch.compiler.disable
+def parallel_path_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    w: torch.Tensor,
+    beta: torch.Tensor,
+    g: Optional[torch.Tensor] = None,
+    scale: float = None,
+    cu_seqlens: Optional[torch.Tensor] = None,
+    use_cache: bool = False,
+):
+    """PaTH softmax attention: O = softmax(s A) V over the path logits A (j <= i).
+
+    q [B,T,HQ,K], k/w [B,T,H,K], v [B,T,H,V], beta [B,T,H]; returns
+    ``(o [B,T,HQ,V], k_cache [B,T,H,K] or None)``.  Gating (``g``) is not supported,
+    as in the LUCID-Path entry point.
+    """
+    if scale is None:
+        scale = k.shape[-1] ** -0.5
+    _check(q, k, v, w, beta, g)
+    return _apply(ParallelPathAttentionFunction, q, k, v, w, beta, g, scale, cu_seqlens, use_cache)
+
+
 @torch.compiler.disable
 def parallel_lucid_path_attention(
     k: torch.Tensor,
@@ -119,29 +225,14 @@ def parallel_lucid_path_attention(
         q = k
     if scale is None:
         scale = k.shape[-1] ** -0.5
-    assert q.shape[-1] in [16, 32, 64, 128], "only support head_dim in [16, 32, 64, 128] for now. Stay tuned!"
-    assert v.shape[-1] in [16, 32, 64, 128], "only support head_dim in [16, 32, 64, 128] for now. Stay tuned!"
-    assert q.shape[-1] == k.shape[-1], 'q, k should have the same head_dim.'
-    assert k.shape == w.shape, 'k, w should have the same shape.'
-    assert beta.shape[:3] == k.shape[:3], 'beta should have the same number of heads as k'
-    assert g is None, 'g is not supported'
-    assert q.shape[-2] % k.shape[-2] == 0, 'the number of query heads should be divisible by the number of key heads'
-    if q.shape[-1] != 64 or v.shape[-1] != 64:
-        raise NotImplementedError("lucid_amd LUCID-Path kernels support head_dim 64")
-    for name, x in (("q", q), ("k", k), ("v", v), ("w", w), ("beta", beta)):
-        if not x.is_cuda:
-            raise RuntimeError(f"lucid_amd: {name} must be a GPU tensor (no CPU path)")
-        if x.dtype != torch.bfloat16:
-            raise TypeError(f"lucid_amd: {name} must be bfloat16, got {x.dtype}")
-    if cu_seqlens is not None:
-        if q.shape[0] != 1:
-            raise ValueError("cu_seqlens requires batch size 1 (packed sequences)")
-        outs, caches = [], []
-        bounds = cu_seqlens.tolist()
-        for s0, s1 in zip(bounds[:-1], bounds[1:]):
-            o_i, kc_i = ParallelLUCIDPathAttentionFunction.apply(
-                q[:, s0:s1], k[:, s0:s1], v[:, s0:s1], w[:, s0:s1], beta[:, s0:s1], g, scale, None, use_cache)
-            outs.append(o_i)
-            caches.append(kc_i)
-        return torch.cat(outs, 1), (torch.cat(caches, 1) if use_cache else None)
-    return ParallelLUCIDPathAttentionFunction.apply(q, k, v, w, beta, g, scale, cu_seqlens, use_cache)
+    _check(q, k, v, w, beta, g)
+    return _apply(ParallelLUCIDPathAttentionFunction, q, k, v, w, beta, g, scale, cu_seqlens, use_cache)
+
+
+def lucid_path_layer_attention(q, k, v, w, beta, scale=None):
+    """One LUCID-Path layer's attention: V' = (I + L)^-1 V with the key-key path
+    preconditioner (``parallel_lucid_path_attention`` with q = k), then PaTH softmax
+    attention of the queries over (k, V')."""
+    vp, _ = parallel_lucid_path_attention(k, v, w, beta, q=None, scale=scale)  # [B, T, H, V]
+    o, _ = parallel_path_attention(q, k, vp, w, beta, scale=scale)
+    return o

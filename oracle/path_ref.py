@@ -157,3 +157,110 @@ def path_attention_grads(q, k, v, w, beta, do, scale=None, C=64):
     o = path_attention_chunked(*leaves, scale=scale, C=C)
     (o * do).sum().backward()
     return tuple(t.grad for t in leaves)
+
+
+# ---------------------------------------------------------------------------
+# PaTH softmax attention (the softmax half of a LUCID-Path layer)
+#
+#   O_i = sum_{j<=i} softmax_j(s A_ij) v_j,  A_ij = q_i^T H_i ... H_{j+1} k_j  (A_ii = q_i . k_i)
+#
+# Reference: the forward kernels intra_chunk_preprocess_fwd.py:14-121 (in-chunk
+# logits including the diagonal, o, row sum L and row max M in the exp2 domain)
+# and parallel_path_fwd.py:13-124 (online-softmax continuation over earlier
+# chunks with the query carried down by q <- q - (q W^T) W2, output o and
+# L_new = log2(l) + m).  Their backward lives in the unvendored fla package, so
+# gradients are pinned by float64 autograd of the brute-force definition.
+# ---------------------------------------------------------------------------
+
+
+def path_softmax_logits_bruteforce(q, k, w, beta):
+    """A[b, hq, i, j] for j <= i (the diagonal is q_i . k_i, no reflection applies)."""
+    A = path_logits_bruteforce(q, k, w, beta)
+    G = q.shape[2] // k.shape[2]
+    kk = k.repeat_interleave(G, dim=2)
+    diag = (q * kk).sum(-1).permute(0, 2, 1)  # [B, HQ, T]
+    return A + torch.diag_embed(diag)
+
+
+def path_softmax_bruteforce(q, k, v, w, beta, scale=None, return_lse=False):
+    """O [B,T,HQ,V] = causal softmax(s A) V from the definition (small T only);
+    with ``return_lse`` also the natural log-sum-exp [B,HQ,T] of each row."""
+    K = k.shape[-1]
+    scale = K ** -0.5 if scale is None else scale
+    G = q.shape[2] // k.shape[2]
+    A = path_softmax_logits_bruteforce(q, k, w, beta) * scale
+    T = A.shape[-1]
+    mask = torch.ones(T, T, dtype=torch.bool).tril()
+    A = A.masked_fill(~mask, float("-inf"))
+    vv = v.permute(0, 2, 1, 3).repeat_interleave(G, dim=1)
+    o = (torch.softmax(A, dim=-1) @ vv).permute(0, 2, 1, 3).contiguous()
+    return (o, torch.logsumexp(A, dim=-1)) if return_lse else o
+
+
+def path_softmax_chunked(q, k, v, w, beta, scale=None, C=64):
+    """Chunk restatement of the two PaTH softmax forward kernels (differentiable).
+
+    In-chunk (intra_chunk_preprocess_fwd.py:71-115): with T_inv the WY matrix of the
+    chunk, ``A = tril(q k^T - tril(q W^T) T_inv stril(beta W k^T))`` (diagonal
+    included), row max m, l = sum exp2(s' A - m), o = exp2(...) V, s' = s log2(e).
+    Inter-chunk (parallel_path_fwd.py:77-117): for earlier chunks J descending,
+    S = q_new k_new_J^T, online-softmax update of (m, l, o), then
+    ``q_new <- q_new - (q_new W_J^T) W2_J``.  Returns (o, L_new) with
+    ``L_new = log2(l) + m`` [B,T,HQ] as the reference's second kernel stores it.
+    """
+    B, T, HQ, K = q.shape
+    H = k.shape[2]
+    G = HQ // H
+    scale = K ** -0.5 if scale is None else scale
+    if T % C:
+        raise ValueError("T must be a multiple of the chunk size")
+    sm = scale * 1.4426950408889634
+    NT = T // C
+    outs, lses = [], []
+    for b in range(B):
+        for hq in range(HQ):
+            h = hq // G
+            qn, kn, w2s, ad = [], [], [], []
+            for c in range(NT):
+                sl = slice(c * C, (c + 1) * C)
+                wc, bc, qc, kc = w[b, sl, h], beta[b, sl, h], q[b, sl, hq], k[b, sl, h]
+                t_inv, w2 = wy_chunk(wc, bc)
+                qw = torch.tril(qc @ wc.T)
+                wbk = torch.tril((wc * bc[:, None]) @ kc.T, -1)
+                qn.append(qc - qw @ w2)
+                kn.append(kc - (wc.T @ (t_inv @ wbk)).T)
+                ad.append(qc @ kc.T - qw @ t_inv @ wbk)
+                w2s.append(w2)
+            mask = torch.ones(C, C, dtype=torch.bool).tril()
+            rows_o, rows_l = [], []
+            for i in range(NT):
+                s_ii = (ad[i] * sm).masked_fill(~mask, float("-inf"))
+                m = s_ii.max(-1).values
+                p = torch.exp2(s_ii - m[:, None])
+                l = p.sum(-1)
+                o = p @ v[b, i * C:(i + 1) * C, h]
+                qq = qn[i]
+                for j in range(i - 1, -1, -1):
+                    s = (qq @ kn[j].T) * sm
+                    m_new = torch.maximum(m, s.max(-1).values)
+                    alpha = torch.exp2(m - m_new)
+                    p = torch.exp2(s - m_new[:, None])
+                    o = o * alpha[:, None] + p @ v[b, j * C:(j + 1) * C, h]
+                    l = l * alpha + p.sum(-1)
+                    m = m_new
+                    qq = qq - (qq @ w[b, j * C:(j + 1) * C, h].T) @ w2s[j]
+                rows_o.append(o / l[:, None])
+                rows_l.append(torch.log2(l) + m)
+            outs.append(torch.cat(rows_o, 0))
+            lses.append(torch.cat(rows_l, 0))
+    o = torch.stack(outs).reshape(B, HQ, T, -1).permute(0, 2, 1, 3).contiguous()
+    lse2 = torch.stack(lses).reshape(B, HQ, T).permute(0, 2, 1).contiguous()
+    return o, lse2
+
+
+def path_softmax_grads(q, k, v, w, beta, do, scale=None):
+    """(dq, dk, dv, dw, dbeta) of sum(O * dO) by float64 autograd of the brute force."""
+    leaves = [t.detach().clone().requires_grad_() for t in (q, k, v, w, beta)]
+    o = path_softmax_bruteforce(*leaves, scale=scale)
+    (o * do).sum().backward()
+    return tuple(t.grad for t in leaves)

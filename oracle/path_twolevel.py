@@ -45,7 +45,7 @@ def chunk_prep(q, k, w, beta, scale, C):
         adiag = torch.tril(qc @ kc.T - qw @ tw)
         ld = torch.tril(torch.exp(adiag * scale - 1.0 / scale), -1)
         out.append(dict(W=W, b=b, Wb=Wb, tm=tm, w2=w2, Hc=torch.eye(d, dtype=k.dtype) - W.T @ w2,
-                        qw=qw, wbk=wbk, tw=tw, qt=qc - qw @ w2, kt=kc - tw.T @ W, ld=ld,
+                        qw=qw, wbk=wbk, tw=tw, qt=qc - qw @ w2, kt=kc - tw.T @ W, ld=ld, adiag=adiag,
                         Y=_ltri_inv_unit(ld)))
     return out
 
@@ -86,8 +86,13 @@ def query_transport(ch, HL, R):
     return QS, QB
 
 
-def forward(q, k, v, w, beta, scale, C=64, S=512):
-    """O for one query head (kv tensors of its kv head); returns (O, state for backward)."""
+def forward(q, k, v, w, beta, scale, C=64, S=512, softmax=False):
+    """O for one query head (kv tensors of its kv head); returns (O, state for backward).
+
+    ``softmax=False``: LUCID-Path, the chained solve (I + L) O = V.
+    ``softmax=True``: PaTH softmax attention over the same logits, diagonal included:
+    O_I = sum_{J<=I} P_IJ V_J with P = exp(s A - lse) (row-wise log-sum-exp).
+    """
     T = k.shape[0]
     R = S // C
     NT = T // C
@@ -102,13 +107,30 @@ def forward(q, k, v, w, beta, scale, C=64, S=512):
 
     L = {}
     O = []
+    st = dict(ch=ch, SUF=SUF, PRE=PRE, HL=HL, KL=KL, QS=QS, QB=QB, L=L, O=O, R=R, C=C, scale=scale,
+              softmax=softmax)
+    if softmax:
+        mask = torch.ones(C, C, dtype=torch.bool).tril()
+        Vb = [v[J * C:(J + 1) * C] for J in range(NT)]
+        Pd, lse = [], []
+        for I in range(NT):
+            blocks = [logits(I, J) * scale for J in range(I)]
+            blocks.append((ch[I]["adiag"] * scale).masked_fill(~mask, float("-inf")))
+            full = torch.cat(blocks, 1)
+            ls = torch.logsumexp(full, dim=-1)
+            for J in range(I):
+                L[(I, J)] = torch.exp(blocks[J] - ls[:, None])
+            Pd.append(torch.exp(blocks[I] - ls[:, None]))
+            O.append(sum(L[(I, J)] @ Vb[J] for J in range(I)) + Pd[I] @ Vb[I])
+            lse.append(ls)
+        st.update(Pd=Pd, V=Vb, lse=torch.cat(lse))
+        return torch.cat(O, 0), st
     for I in range(NT):
         r = v[I * C:(I + 1) * C].clone()
         for J in range(I):
             L[(I, J)] = torch.exp(logits(I, J) * scale - 1.0 / scale)
             r -= L[(I, J)] @ O[J]
         O.append(ch[I]["Y"] @ r)
-    st = dict(ch=ch, SUF=SUF, PRE=PRE, HL=HL, KL=KL, QS=QS, QB=QB, L=L, O=O, R=R, C=C, scale=scale)
     return torch.cat(O, 0), st
 
 
@@ -119,6 +141,16 @@ def backward(st, do):
     NT = len(ch)
     d = ch[0]["Hc"].shape[0]
     z = lambda *s: torch.zeros(*s, dtype=do.dtype)  # noqa: E731
+    if st["softmax"]:
+        # ---- softmax: dP = dO V^T, dA = s P (dP - delta), dV_J = sum_{I>=J} P_IJ^T dO_I ----
+        Vb, Pd = st["V"], st["Pd"]
+        dOb = [do[I * C:(I + 1) * C] for I in range(NT)]
+        delta = [(dOb[I] * O[I]).sum(-1, keepdim=True) for I in range(NT)]
+        dA = {(I, J): scale * L[(I, J)] * (dOb[I] @ Vb[J].T - delta[I]) for (I, J) in L}
+        dAd = [scale * Pd[c] * (dOb[c] @ Vb[c].T - delta[c]) for c in range(NT)]
+        dV = [Pd[J].T @ dOb[J] + sum((L[(I, J)].T @ dOb[I] for I in range(J + 1, NT)), z(C, d))
+              for J in range(NT)]
+        return _logit_backward(st, dA, dAd, dV, z)
     # ---- dV = (I + L)^-T dO, last block first ----
     dV = [None] * NT
     for J in range(NT - 1, -1, -1):
@@ -128,6 +160,16 @@ def backward(st, do):
         dV[J] = ch[J]["Y"].T @ r
     dA = {(I, J): -scale * (dV[I] @ O[J].T) * L[(I, J)] for (I, J) in L}
     dAd = [-scale * (dV[c] @ O[c].T) * ch[c]["ld"] for c in range(NT)]
+    return _logit_backward(st, dA, dAd, dV, z)
+
+
+def _logit_backward(st, dA, dAd, dV, z):
+    """Gradients of the inputs given dA (inter-chunk blocks), dAd (in-chunk, lower incl. the
+    diagonal) and dV: the row sweep, the column sweep, the products and the WY backward."""
+    ch, SUF, HL, KL, QS, QB = (st[x] for x in ("ch", "SUF", "HL", "KL", "QS", "QB"))
+    R, C = st["R"], st["C"]
+    NT = len(ch)
+    d = ch[0]["Hc"].shape[0]
     # ---- row sweep: gradient of the query transports ----
     dHL = [z(d, d) for _ in HL]
     dHc = [z(d, d) for _ in range(NT)]
@@ -183,7 +225,7 @@ def backward(st, do):
         dkc = dkt[c].clone()
         dTW = -W @ dkt[c].T
         dW = dW - tw @ dkt[c]
-        # A_diag (strictly lower part used)
+        # A_diag (lower part incl. the diagonal; LUCID-Path's dAd vanishes on the diagonal)
         qrows, krows = st_rows(st, c)
         dqc += dAd[c] @ krows
         dkc += dAd[c].T @ qrows
@@ -219,7 +261,7 @@ def st_rows(st, c):
     return st["q"][c * C:(c + 1) * C], st["k"][c * C:(c + 1) * C]
 
 
-def path_attention_twolevel(q, k, v, w, beta, do=None, scale=None, C=64, S=512):
+def path_attention_twolevel(q, k, v, w, beta, do=None, scale=None, C=64, S=512, softmax=False):
     """Forward (and backward if ``do`` is given) over [B,T,H*,K] tensors, looping over heads.
 
     Returns O [B,T,HQ,V] and, with ``do``, (dq, dk, dv, dw, dbeta) with the GQA sums applied.
@@ -236,7 +278,7 @@ def path_attention_twolevel(q, k, v, w, beta, do=None, scale=None, C=64, S=512):
     for b in range(B):
         for hq in range(HQ):
             h = hq // G
-            ob, st = forward(q[b, :, hq], k[b, :, h], v[b, :, h], w[b, :, h], beta[b, :, h], scale, C, S)
+            ob, st = forward(q[b, :, hq], k[b, :, h], v[b, :, h], w[b, :, h], beta[b, :, h], scale, C, S, softmax)
             o[b, :, hq] = ob
             if do is not None:
                 st["q"], st["k"] = q[b, :, hq], k[b, :, h]

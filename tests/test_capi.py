@@ -80,6 +80,16 @@ def test_argument_validation_without_gpu(built):
     rc = plib.lucid_path_fwd(dummy, s4, dummy, s4, dummy, s4, dummy, s4, dummy, sb, dummy, s4, None, None,
                              misaligned, 1, 256, 1, 1, 64, 0.125, None)
     assert rc == _lib.LUCID_EINVAL and b"256-byte aligned" in plib.lucid_path_last_error()
+    rc = plib.lucid_path_softmax_fwd(dummy, s4, dummy, s4, dummy, s4, dummy, s4, dummy, sb, dummy, s4, None, None,
+                                     misaligned, 1, 256, 1, 1, 64, 0.125, None)
+    assert rc == _lib.LUCID_EINVAL and b"256-byte aligned" in plib.lucid_path_last_error()
+    rc = plib.lucid_path_softmax_fwd(dummy, s4, dummy, s4, dummy, s4, dummy, s4, dummy, sb, dummy, s4, None, None,
+                                     dummy, 1, 256, 1, 1, 128, 0.125, None)
+    assert rc == _lib.LUCID_EINVAL and b"head_dim" in plib.lucid_path_last_error()
+    # the softmax forward workspace drops the solve's inverses and O^T and adds the row lse
+    B, T, H, HQ = 1, 4096, 2, 4
+    d = plib.lucid_path_fwd_workspace_bytes(B, T, H, HQ, 64) - plib.lucid_path_softmax_fwd_workspace_bytes(B, T, H, HQ, 64)
+    assert d == B * HQ * (T // 64) * 4096 * 4 + B * HQ * T * 64 * 2 - B * HQ * T * 4
 
 
 def test_product_path_fails_loudly_without_gpu_tensors():

@@ -115,3 +115,48 @@ def test_chunked_grads_match_bruteforce_grads():
     (P.path_attention_bruteforce(*leaves, scale=0.6) * do).sum().backward()
     for a, b in zip(g_ch, leaves):
         torch.testing.assert_close(a, b.grad, rtol=1e-9, atol=1e-10)
+
+
+# ---- PaTH softmax attention (softmax over the same path logits, diagonal included) ----
+
+def test_softmax_logits_diagonal_and_beta_zero():
+    q, k, v, w, beta = _inputs(1, 9, 1, 2, 4, 20)
+    A = P.path_softmax_logits_bruteforce(q, k, w, beta)
+    for hq in range(2):
+        torch.testing.assert_close(torch.diagonal(A[0, hq]), (q[0, :, hq] * k[0, :, 0]).sum(-1))
+        assert torch.equal(torch.tril(A[0, hq], -1), P.path_logits_bruteforce(q, k, w, beta)[0, hq])
+    A0 = P.path_softmax_logits_bruteforce(q, k, w, torch.zeros_like(beta))
+    torch.testing.assert_close(A0[0, 1], torch.tril(q[0, :, 1] @ k[0, :, 0].T))
+
+
+@pytest.mark.parametrize("G", [1, 2])
+def test_softmax_beta_zero_is_causal_sdpa(G):
+    # no reflections: plain causal softmax attention, checked against torch's SDPA (float64)
+    q, k, v, w, beta = _inputs(2, 14, 2, G, 8, 21 + G)
+    o = P.path_softmax_bruteforce(q, k, v, w, torch.zeros_like(beta), scale=0.3)
+    kk, vv = (x.repeat_interleave(G, dim=2).transpose(1, 2) for x in (k, v))
+    ref = torch.nn.functional.scaled_dot_product_attention(q.transpose(1, 2), kk, vv, is_causal=True, scale=0.3)
+    torch.testing.assert_close(o, ref.transpose(1, 2), rtol=1e-12, atol=1e-12)
+
+
+def test_softmax_first_row_is_v0():
+    q, k, v, w, beta = _inputs(1, 6, 1, 1, 4, 23)
+    o = P.path_softmax_bruteforce(q, k, v, w, beta)
+    torch.testing.assert_close(o[0, 0, 0], v[0, 0, 0])
+
+
+@pytest.mark.parametrize("T,C,G", [(16, 4, 1), (24, 8, 2), (32, 16, 1), (64, 16, 2)])
+def test_softmax_chunked_equals_bruteforce(T, C, G):
+    q, k, v, w, beta = _inputs(2, T, 2, G, 8, 30 + T + C)
+    scale = 8 ** -0.5
+    o_bf, lse = P.path_softmax_bruteforce(q, k, v, w, beta, scale, return_lse=True)
+    o_ch, lse2 = P.path_softmax_chunked(q, k, v, w, beta, scale, C=C)
+    torch.testing.assert_close(o_ch, o_bf, rtol=1e-10, atol=1e-10)
+    # the reference's L_new is log2(l) + m in the exp2 domain = lse / ln 2
+    torch.testing.assert_close(lse2 * math.log(2.0), lse.permute(0, 2, 1), rtol=1e-10, atol=1e-10)
+
+
+def test_softmax_gradcheck_bruteforce():
+    q, k, v, w, beta = _inputs(1, 5, 1, 1, 3, 24)
+    leaves = [t.clone().requires_grad_() for t in (q, k, v, w, beta)]
+    assert torch.autograd.gradcheck(lambda *a: P.path_softmax_bruteforce(*a, scale=0.7), leaves)

@@ -30,3 +30,15 @@ def test_twolevel_matches_autograd(T, C, S, G):
     ref = P.path_attention_grads(q, k, v, w, beta, do, scale=scale, C=C)
     for name, a, b in zip(("dq", "dk", "dv", "dw", "dbeta"), grads, ref):
         torch.testing.assert_close(a, b, rtol=1e-8, atol=1e-9, msg=name)
+
+
+@pytest.mark.parametrize("T,C,S,G", [(64, 4, 16, 1), (48, 8, 16, 2), (40, 4, 16, 1)])
+def test_twolevel_softmax_matches_bruteforce_autograd(T, C, S, G):
+    # PaTH softmax attention: same decomposition, dA from the softmax backward
+    q, k, v, w, beta, do = _inputs(1, T, 2, G, 8, 100 + T + C + S)
+    scale = 8 ** -0.5
+    o, grads = TL.path_attention_twolevel(q, k, v, w, beta, do, scale=scale, C=C, S=S, softmax=True)
+    torch.testing.assert_close(o, P.path_softmax_bruteforce(q, k, v, w, beta, scale), rtol=1e-10, atol=1e-10)
+    ref = P.path_softmax_grads(q, k, v, w, beta, do, scale=scale)
+    for name, a, b in zip(("dq", "dk", "dv", "dw", "dbeta"), grads, ref):
+        torch.testing.assert_close(a, b, rtol=1e-8, atol=1e-9, msg=name)
