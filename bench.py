@@ -141,6 +141,69 @@ def copy_calibration(nbytes: int, reps: int = 3) -> None:
           flush=True)
 
 
+def bench_decode(args, dev):
+    """One LUCID decoding step (one layer's attention for one new token per sequence) against
+    a full cache at the long-context shape of config 5: B=1, Hq=32 over Hkv=8, d=128,
+    T=131072 cached rows.  HBM-bound: the K and V' caches are read once per step."""
+    import torch
+
+    from lucid_amd import _lib, lucid_decode
+
+    B, Hq, Hkv, T, D = 1, 32, 8, 131072, 128
+    g = torch.Generator().manual_seed(0)
+    s = D ** -0.5
+    kc = (torch.randn(B, Hkv, T + 1, D, generator=g) * s).to(torch.bfloat16).to(dev)
+    vc = (torch.randn(B, Hkv, T + 1, D, generator=g) * s).to(torch.bfloat16).to(dev)
+    q = (torch.randn(B, Hq, 1, D, generator=g) * s).to(torch.bfloat16).to(dev)
+    k = (torch.randn(B, Hkv, 1, D, generator=g) * s).to(torch.bfloat16).to(dev)
+    v = (torch.randn(B, Hkv, 1, D, generator=g) * s).to(torch.bfloat16).to(dev)
+    lib = _lib.load()
+
+    def step():  # every step decodes row T against rows [0, T) (same work each time)
+        lucid_decode(q, k, v, kc, vc, T)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    lib.lucid_profile_reset()
+    lib.lucid_profile_enable(1)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / args.steps * 1e3
+    lib.lucid_profile_enable(0)
+    totals = _lib.profile_totals(lib, "lucid_")
+    kernels = {n: {"avg_ms": round(tot / cnt, 4), "launches": cnt} for n, (tot, cnt) in
+               sorted(totals.items(), key=lambda kv: -kv[1][0])}
+    dom = "lucid_decode_split_kernel"
+    dom_avg = totals[dom][0] / totals[dom][1]
+    nbytes = 2.0 * B * Hkv * T * D * 2  # K and V' caches, bf16, read once
+    achieved = nbytes / (dom_avg / 1e3) / 1e9
+    out = {
+        "metric": "LUCID decode step (one layer, one new token) tokens/s at T=128K cache (config-5 shape)",
+        "value": round(B / (ms / 1e3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1)/sqrt(d) caches and token)",
+        "config": {"workload": "lucid_decode_step", "B": B, "Hq": Hq, "Hkv": Hkv, "T_cache": T, "head_dim": D,
+                   "parallelism": "single GPU"},
+        "roofline": {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+        "kernels": kernels,
+        "cpu_baseline": None,
+    }
+    print(json.dumps(out), flush=True)
+
+
 def bench_c3(args, dev):
     """Decoder training step: 16 layers, hidden 2048, 32 x 64 heads, SwiGLU 5632, vocab 32000,
     bf16 weights, random init N(0, 0.02); tokens uniform over the vocabulary, labels = tokens.
@@ -248,12 +311,13 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="lucid", choices=["lucid", "c2", "c3", "c5", "path", "path_softmax"],
+    ap.add_argument("--workload", default="lucid",
+                    choices=["lucid", "c2", "c3", "c5", "path", "path_softmax", "decode"],
                     help="lucid: north star B1 H16 T32768 d64 fwd+bwd (default); c2: B4 H16 T4096 d64 "
                          "fwd+bwd; c3: 16-layer Llama-LUCID decoder, one training step (fwd+bwd+AdamW) "
                          "on B1 x T8192; c5: B1 T131072 Hq32/Hkv8 d128 forward only; path: LUCID-Path "
                          "B1 H16 T32768 d64 fwd+bwd; path_softmax: PaTH softmax attention on the config-4 "
-                         "shape, fwd+bwd")
+                         "shape, fwd+bwd; decode: one decoding step against a 128K cache (config-5 heads)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-causal", action="store_true")
     ap.add_argument("--copy-bytes", type=int, default=0,
@@ -278,6 +342,9 @@ def main():
     wl = args.workload
     if wl == "c3":
         bench_c3(args, dev)
+        return
+    if wl == "decode":
+        bench_decode(args, dev)
         return
     fwd_only = wl == "c5"
     if wl in ("path", "path_softmax"):

@@ -70,6 +70,26 @@ int lucid_attn_bwd(const void* dout, const int64_t* do_strides, const void* q, c
                    const int64_t* dk_strides, void* dv, const int64_t* dv_strides, void* bwd_ws, int B, int Hq,
                    int Hkv, int T, int D, float scale, float eps, void* stream);
 
+/* Bytes of the decoding workspace for caches of capacity T_cap (0 on bad sizes). */
+size_t lucid_decode_workspace_bytes(int B, int Hq, int Hkv, int T_cap, int D);
+
+/* One decoding step: a new token per sequence (q [B,Hq,1,D], k and v [B,Hkv,1,D])
+ * against the caches k_cache (keys with RoPE applied, as the attention saw them) and
+ * vp_cache (V' rows, bf16), both [B,Hkv,T_cap,D] with rows [0, T_past) valid.
+ * Computes the token's V' row with the exact diagonal,
+ *   v'_t = (v_t - sum_{j<t} P_tj v'_j) / P_tt,
+ * writes it to vp_new (fp32 [B,Hkv,D]) and appends (k_t, v'_t) at row T_past of the
+ * caches, then o (strides {batch, head, -}, [B,1,Hq,D] in the reference layout) =
+ * softmax over j <= t of s q.k_j times v'_j.  Hq / Hkv in {1, 2, 4, 8}.
+ * Replaces LucidAttention.get_new_v_prime (modeling_lucid.py:576-598, which omits the
+ * division by P_tt) and the cached attention call of LucidAttention.forward
+ * (:475-496); a decoded row equals the same row of lucid_attn_fwd on the whole
+ * sequence. */
+int lucid_decode(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides, const void* v,
+                 const int64_t* v_strides, void* k_cache, const int64_t* k_cache_strides, void* vp_cache,
+                 const int64_t* vp_cache_strides, void* o, const int64_t* o_strides, float* vp_new, void* ws, int B,
+                 int Hq, int Hkv, int T_past, int T_cap, int D, float scale, float eps, void* stream);
+
 /* Per-kernel timing (no counterpart in the reference; used by bench.py).
  * When enabled, every launch is bracketed by two HIP events on its stream.
  * lucid_profile_collect() waits for the recorded events, folds them into

@@ -4,13 +4,16 @@ Operator entry points (drop-ins for the reference seams):
 
 * :func:`lucid_amd.lucid.lucid_attention` / :func:`lucid_amd.lucid.get_v_prime` /
   :func:`lucid_amd.lucid.eager_lucid_attention_forward` (modeling_lucid.py operator part)
-* :class:`lucid_amd.modeling.LucidAttention` (modeling_lucid.py LucidAttention module)
+* :func:`lucid_amd.lucid.lucid_decode` (one decoding step against a (K, V') cache)
+* :mod:`lucid_amd.modeling_lucid` (the reference model file's classes on these operators)
+* :mod:`lucid_amd.lucid_path` (LUCID-Path and PaTH softmax attention)
 """
-from .lucid import LucidAttentionFunction, eager_lucid_attention_forward, get_v_prime, lucid_attention
+from .lucid import LucidAttentionFunction, eager_lucid_attention_forward, get_v_prime, lucid_attention, lucid_decode
 
 __all__ = [
     "LucidAttentionFunction",
     "eager_lucid_attention_forward",
     "get_v_prime",
     "lucid_attention",
+    "lucid_decode",
 ]

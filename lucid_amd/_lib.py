@@ -35,6 +35,9 @@ _SIGS = {
         "lucid_attn_bwd": ([_vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _vp,
                             _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp,
                             _int, _int, _int, _int, _int, _flt, _flt, _vp], _int),
+        "lucid_decode_workspace_bytes": ([_int] * 5, _sz),
+        "lucid_decode": ([_vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _vp,
+                          _int, _int, _int, _int, _int, _int, _flt, _flt, _vp], _int),
         "lucid_profile_enable": ([_int], None),
         "lucid_profile_collect": ([], _int),
         "lucid_profile_entry": ([_int, ctypes.c_char_p, _int, ctypes.POINTER(ctypes.c_double),

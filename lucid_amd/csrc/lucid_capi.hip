@@ -7,6 +7,7 @@
 
 #include "../../include/lucid_amd.h"
 #include "lucid_bwd.hip"
+#include "lucid_decode.hip"
 #include "lucid_fwd.hip"
 #include "profiling.h"
 
@@ -165,9 +166,108 @@ int launch_bwd(const void* dout, const int64_t* dos, const void* q, const int64_
   return LUCID_OK;
 }
 
+// Decoding: split the cached sequence so that about LUCID_DECODE_WGS workgroups run (at least 64
+// keys per split).  Monotone in Tp, so the workspace sized for the capacity covers
+// every call.
+#ifndef LUCID_DECODE_WGS
+#define LUCID_DECODE_WGS 1024
+#endif
+int decode_splits(int BH, int Tp) {
+  if (Tp <= 0) return 0;
+  const int want = (LUCID_DECODE_WGS + BH - 1) / BH, most = (Tp + 63) / 64;
+  return want < most ? want : most;
+}
+
+lucid::DecodePartials carve_decode(void* base, int BH, int G, int nsplit, int D, size_t* bytes) {
+  lucid::DecodePartials w{};
+  size_t off = 0;
+  char* p = static_cast<char*>(base);
+  auto take = [&](size_t n) {
+    char* r = p ? p + off : nullptr;
+    off += align256(n);
+    return r;
+  };
+  const size_t ns = nsplit > 0 ? nsplit : 1;
+  w.a = reinterpret_cast<float*>(take(ns * BH * D * 4));
+  w.m = reinterpret_cast<float*>(take(ns * BH * G * 4));
+  w.l = reinterpret_cast<float*>(take(ns * BH * G * 4));
+  w.o = reinterpret_cast<float*>(take(ns * BH * G * D * 4));
+  if (bytes) *bytes = off;
+  return w;
+}
+
+template <int D, int G>
+int launch_decode(const void* q, const int64_t* qs, const void* k, const int64_t* ks, const void* v,
+                  const int64_t* vs, void* kc, const int64_t* kcs, void* vc, const int64_t* vcs, void* o,
+                  const int64_t* os, float* vp_new, const lucid::DecodePartials& part, int B, int Hkv, int Tp,
+                  float scale, float eps, hipStream_t st) {
+  const int BH = B * Hkv;
+  const int ns = decode_splits(BH, Tp);
+  if (ns > 0) {
+    const int KS = (Tp + ns - 1) / ns;
+    LUCID_LAUNCH("lucid_decode_split_kernel", (lucid::lucid_decode_split_kernel<D, G>), dim3(ns, BH), st,
+                 (const bf16*)q, S(qs), (const bf16*)k, S(ks), (const bf16*)kc, S(kcs), (const bf16*)vc, S(vcs), Hkv,
+                 Tp, KS, scale, eps, part);
+  }
+  LUCID_LAUNCH("lucid_decode_combine_kernel", (lucid::lucid_decode_combine_kernel<D, G>), dim3(BH, G), st, ns,
+               (const bf16*)q, S(qs), (const bf16*)k, S(ks), (const bf16*)v, S(vs), (bf16*)kc, S(kcs), (bf16*)vc,
+               S(vcs), (bf16*)o, S(os), vp_new, Hkv, Tp, scale, eps, part);
+  return LUCID_OK;
+}
+
+template <int D>
+int decode_dispatch_g(int G, const void* q, const int64_t* qs, const void* k, const int64_t* ks, const void* v,
+                      const int64_t* vs, void* kc, const int64_t* kcs, void* vc, const int64_t* vcs, void* o,
+                      const int64_t* os, float* vp_new, const lucid::DecodePartials& part, int B, int Hkv, int Tp,
+                      float scale, float eps, hipStream_t st) {
+  switch (G) {
+    case 1: return launch_decode<D, 1>(q, qs, k, ks, v, vs, kc, kcs, vc, vcs, o, os, vp_new, part, B, Hkv, Tp, scale, eps, st);
+    case 2: return launch_decode<D, 2>(q, qs, k, ks, v, vs, kc, kcs, vc, vcs, o, os, vp_new, part, B, Hkv, Tp, scale, eps, st);
+    case 4: return launch_decode<D, 4>(q, qs, k, ks, v, vs, kc, kcs, vc, vcs, o, os, vp_new, part, B, Hkv, Tp, scale, eps, st);
+    case 8: return launch_decode<D, 8>(q, qs, k, ks, v, vs, kc, kcs, vc, vcs, o, os, vp_new, part, B, Hkv, Tp, scale, eps, st);
+    default: return fail("decode supports Hq / Hkv in {1, 2, 4, 8}, got " + std::to_string(G));
+  }
+}
+
 }  // namespace
 
 extern "C" {
+
+size_t lucid_decode_workspace_bytes(int B, int Hq, int Hkv, int T_cap, int D) {
+  if (B <= 0 || Hkv <= 0 || Hq <= 0 || Hq % Hkv || T_cap < 0) return 0;
+  size_t n = 0;
+  carve_decode(nullptr, B * Hkv, Hq / Hkv, decode_splits(B * Hkv, T_cap), D, &n);
+  return n;
+}
+
+int lucid_decode(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides, const void* v,
+                 const int64_t* v_strides, void* k_cache, const int64_t* k_cache_strides, void* vp_cache,
+                 const int64_t* vp_cache_strides, void* o, const int64_t* o_strides, float* vp_new, void* ws, int B,
+                 int Hq, int Hkv, int T_past, int T_cap, int D, float scale, float eps, void* stream) {
+  g_last_error.clear();
+  if (B <= 0 || Hq <= 0 || Hkv <= 0) return fail("B, Hq and Hkv must be positive");
+  if (D != 64 && D != 128) return fail("head_dim must be 64 or 128, got " + std::to_string(D));
+  if (Hq % Hkv != 0) return fail("Hq must be a multiple of Hkv");
+  if (T_past < 0 || T_past >= T_cap) return fail("the cache is full: T_past must be in [0, T_cap)");
+  if (int rc = check_tensor("q", q, q_strides)) return rc;
+  if (int rc = check_tensor("k", k, k_strides)) return rc;
+  if (int rc = check_tensor("v", v, v_strides)) return rc;
+  if (int rc = check_tensor("k_cache", k_cache, k_cache_strides)) return rc;
+  if (int rc = check_tensor("vp_cache", vp_cache, vp_cache_strides)) return rc;
+  if (int rc = check_tensor("o", o, o_strides)) return rc;
+  if (!vp_new || !ws) return fail("vp_new and ws must be non-null");
+  if (int rc = check_ws("ws", ws)) return rc;
+  const lucid::DecodePartials part =
+      carve_decode(ws, B * Hkv, Hq / Hkv, decode_splits(B * Hkv, T_past), D, nullptr);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (D == 64)
+    return decode_dispatch_g<64>(Hq / Hkv, q, q_strides, k, k_strides, v, v_strides, k_cache, k_cache_strides,
+                                 vp_cache, vp_cache_strides, o, o_strides, vp_new, part, B, Hkv, T_past, scale, eps,
+                                 st);
+  return decode_dispatch_g<128>(Hq / Hkv, q, q_strides, k, k_strides, v, v_strides, k_cache, k_cache_strides,
+                                vp_cache, vp_cache_strides, o, o_strides, vp_new, part, B, Hkv, T_past, scale, eps,
+                                st);
+}
 
 int lucid_abi_version(void) { return 1; }
 

@@ -160,3 +160,43 @@ def get_v_prime(key, value, scaling=None, eps=1e-5):
 def eager_lucid_attention_forward(query, key, value, scaling=None, eps=1e-5):
     """Drop-in for ``get_v_prime`` followed by ``eager_lucid_attention_forward``: returns ``(O, None)``."""
     return lucid_attention(query, key, value, scaling, eps), None
+
+
+def lucid_decode(query, key, value, key_cache, vprime_cache, cache_len, scaling=None, eps=1e-5):
+    """One decoding step for one new token per sequence (``get_new_v_prime`` and the cached
+    attention of LucidAttention.forward, modeling_lucid.py:475-496, 576-598).
+
+    ``query [B, Hq, 1, d]``, ``key/value [B, Hkv, 1, d]`` (bf16; keys with RoPE applied);
+    ``key_cache`` / ``vprime_cache`` are bf16 buffers ``[B, Hkv, T_cap, d]`` whose first
+    ``cache_len`` rows are valid.  The token's V' row (exact diagonal:
+    ``v'_t = (v_t - sum_j P_tj v'_j) / P_tt``) and its key are written at row ``cache_len``
+    of the caches in place.  Returns ``(O [B, 1, Hq, d], v'_t fp32 [B, Hkv, 1, d])``.
+    """
+    _check_inputs(None, key, value)
+    for name, t in (("query", query), ("key_cache", key_cache), ("vprime_cache", vprime_cache)):
+        if not t.is_cuda or t.dtype != torch.bfloat16 or t.dim() != 4:
+            raise TypeError(f"lucid_amd: {name} must be a 4-D bfloat16 GPU tensor")
+        if t.stride(-1) != 1 or any(s % 8 for s in t.stride()[:3]) or t.data_ptr() % 16:
+            raise ValueError(f"lucid_amd: {name} needs a contiguous last axis and 8-element aligned strides")
+    B, Hkv, tn, D = key.shape
+    Hq = query.shape[1]
+    if tn != 1 or query.shape[2] != 1:
+        raise ValueError("lucid_amd: lucid_decode takes one new token per sequence")
+    if key_cache.shape[:2] != (B, Hkv) or vprime_cache.shape != key_cache.shape or key_cache.shape[3] != D:
+        raise ValueError("lucid_amd: cache shapes disagree with the new key")
+    lib = _lib.load()
+    cap = key_cache.shape[2]
+    q, k, v = (_prep(t, 1) for t in (query, key, value))
+    o = torch.empty(B, 1, Hq, D, dtype=torch.bfloat16, device=q.device)
+    vp_new = torch.empty(B, Hkv, 1, D, dtype=torch.float32, device=q.device)
+    ws = torch.empty(max(lib.lucid_decode_workspace_bytes(B, Hq, Hkv, cap, D), 256), dtype=torch.uint8,
+                     device=q.device)
+    scale = D ** -0.5 if scaling is None else float(scaling)
+    rc = lib.lucid_decode(
+        _lib.ptr(q), _lib.strides3(q, (0, 1, 2)), _lib.ptr(k), _lib.strides3(k, (0, 1, 2)),
+        _lib.ptr(v), _lib.strides3(v, (0, 1, 2)), _lib.ptr(key_cache), _lib.strides3(key_cache, (0, 1, 2)),
+        _lib.ptr(vprime_cache), _lib.strides3(vprime_cache, (0, 1, 2)), _lib.ptr(o), _lib.strides3(o, (0, 2, 1)),
+        _lib.ptr(vp_new), _lib.ptr(ws), B, Hq, Hkv, int(cache_len), cap, D, scale, float(eps),
+        _lib.stream_handle(q.device))
+    _lib.check(lib, rc, "lucid_decode")
+    return o, vp_new

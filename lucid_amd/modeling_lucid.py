@@ -9,7 +9,8 @@ preconditioner solve V' = P^-1 V and causal softmax attention on V' -- runs in
 the LM head are plain PyTorch (hipBLASLt GEMMs).
 
 Decoding with a cache (``get_new_v_prime``, ``modeling_lucid.py:576-598``) keeps
-(K, V') per layer.  The new rows of V' follow the prefill definition exactly:
+(K, V') per layer and runs the HIP decoding step ``lucid_decode``.  The new rows of V'
+follow the prefill definition exactly:
 v'_t = (v_t - sum_{j<t} P_tj v'_j) / P_tt with the non-unit diagonal
 P_tt = exp(s |K^_t|^2 - 1/s), so a decoded token gets the same V' row as the same
 token inside a prefill (the reference's decode path drops the division by P_tt).
@@ -23,7 +24,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from .lucid import lucid_attention
+from .lucid import lucid_attention, lucid_decode
 
 
 @dataclass
@@ -107,23 +108,64 @@ class LlamaMLP(nn.Module):
 
 
 class LucidCache:
-    """Per-layer (K with RoPE applied, V') cache for decoding; shapes [B, Hkv, T, d]."""
+    """Per-layer (K with RoPE applied, V') cache for decoding (the reference keeps the same
+    pair in a DynamicCache, modeling_lucid.py:479-481).  Rows live in preallocated bf16
+    buffers [B, Hkv, capacity, d] that grow by doubling, so a decoding step appends in
+    place instead of concatenating the whole cache; ``key_cache`` / ``value_cache`` give
+    the valid rows [B, Hkv, T, d]."""
 
-    def __init__(self):
-        self.key_cache: list[torch.Tensor] = []
-        self.value_cache: list[torch.Tensor] = []
+    def __init__(self, min_capacity: int = 256):
+        self._k: list[torch.Tensor] = []
+        self._v: list[torch.Tensor] = []
+        self._len: list[int] = []
+        self.min_capacity = min_capacity
+
+    @property
+    def key_cache(self) -> list[torch.Tensor]:
+        return [k[:, :, :n] for k, n in zip(self._k, self._len)]
+
+    @property
+    def value_cache(self) -> list[torch.Tensor]:
+        return [v[:, :, :n] for v, n in zip(self._v, self._len)]
 
     def get_seq_length(self, layer_idx: int = 0) -> int:
-        return self.key_cache[layer_idx].shape[-2] if layer_idx < len(self.key_cache) else 0
+        return self._len[layer_idx] if layer_idx < len(self._len) else 0
+
+    def reserve(self, layer_idx: int, like: torch.Tensor, extra: int) -> None:
+        """Make room for ``extra`` more rows of layer ``layer_idx`` (``like``: [B, Hkv, *, d])."""
+        n = self.get_seq_length(layer_idx)
+        if layer_idx == len(self._k):
+            cap = max(self.min_capacity, -(-extra // 256) * 256)
+            shape = (like.shape[0], like.shape[1], cap, like.shape[3])
+            self._k.append(torch.empty(shape, dtype=torch.bfloat16, device=like.device))
+            self._v.append(torch.empty(shape, dtype=torch.bfloat16, device=like.device))
+            self._len.append(0)
+            return
+        cap = self._k[layer_idx].shape[2]
+        if n + extra <= cap:
+            return
+        new_cap = max(2 * cap, -(-(n + extra) // 256) * 256)
+        for bufs in (self._k, self._v):
+            old = bufs[layer_idx]
+            grown = torch.empty(old.shape[0], old.shape[1], new_cap, old.shape[3], dtype=old.dtype, device=old.device)
+            grown[:, :, :n] = old[:, :, :n]
+            bufs[layer_idx] = grown
+
+    def buffers(self, layer_idx: int):
+        return self._k[layer_idx], self._v[layer_idx], self._len[layer_idx]
+
+    def advance(self, layer_idx: int, n: int = 1) -> None:
+        self._len[layer_idx] += n
 
     def update(self, key: torch.Tensor, v_prime: torch.Tensor, layer_idx: int):
-        if layer_idx == len(self.key_cache):
-            self.key_cache.append(key)
-            self.value_cache.append(v_prime)
-        else:
-            self.key_cache[layer_idx] = torch.cat([self.key_cache[layer_idx], key], dim=-2)
-            self.value_cache[layer_idx] = torch.cat([self.value_cache[layer_idx], v_prime], dim=-2)
-        return self.key_cache[layer_idx], self.value_cache[layer_idx]
+        """Append rows (prefill); returns the valid (K, V') of the layer."""
+        self.reserve(layer_idx, key, key.shape[2])
+        k, v, n = self.buffers(layer_idx)
+        t = key.shape[2]
+        k[:, :, n:n + t] = key
+        v[:, :, n:n + t] = v_prime
+        self._len[layer_idx] = n + t
+        return k[:, :, :n + t], v[:, :, :n + t]
 
 
 class LucidAttention(nn.Module):
@@ -193,18 +235,18 @@ class LucidAttention(nn.Module):
         return torch.cat(outs, dim=-2)
 
     def _decode(self, q, k, v, cache: LucidCache) -> torch.Tensor:
-        past_k, past_vp = cache.key_cache[self.layer_idx], cache.value_cache[self.layer_idx]
-        v_new = self.get_new_v_prime(k, v, past_k, past_vp)
-        keys, v_prime = cache.update(k, v_new.to(past_vp.dtype), self.layer_idx)
-        G = self.num_key_value_groups
-        kq = keys.repeat_interleave(G, dim=1).float() if G > 1 else keys.float()
-        vq = v_prime.repeat_interleave(G, dim=1).float() if G > 1 else v_prime.float()
-        Tn, Tk = q.shape[-2], keys.shape[-2]
-        scores = (q.float() @ kq.transpose(-1, -2)) * self.scaling
-        mask = torch.ones(Tn, Tk, dtype=torch.bool, device=q.device).tril(Tk - Tn)
-        scores = scores.masked_fill(~mask, float("-inf"))
-        out = torch.softmax(scores, dim=-1) @ vq
-        return out.transpose(1, 2).to(q.dtype)
+        """New tokens one at a time through the HIP decoding step (``lucid_decode``), which
+        computes the V' row exactly as ``get_new_v_prime`` and appends (k_t, v'_t) to the
+        cache in place; returns [B, Tn, Hq, d]."""
+        outs = []
+        for t in range(q.shape[2]):
+            cache.reserve(self.layer_idx, k, 1)
+            kb, vb, n = cache.buffers(self.layer_idx)
+            o, _ = lucid_decode(q[:, :, t:t + 1], k[:, :, t:t + 1], v[:, :, t:t + 1], kb, vb, n,
+                                scaling=self.scaling, eps=self.config.rms_norm_eps)
+            cache.advance(self.layer_idx, 1)
+            outs.append(o)
+        return outs[0] if len(outs) == 1 else torch.cat(outs, dim=1)
 
 
 class LlamaDecoderLayer(nn.Module):

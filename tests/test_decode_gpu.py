@@ -1,0 +1,91 @@
+"""GPU parity of the LUCID decoding step (lucid_amd.lucid.lucid_decode).
+
+Decode parity is defined mathematically: a token decoded against the (K, V') cache of
+the earlier tokens must reproduce the same row of the full-sequence forward (P has a
+non-unit diagonal, modeling_lucid.py:565-569, which the step keeps).  Each case checks
+the decoded O and V' rows against the float64 oracle of the whole sequence
+(``oracle.lucid_ref.lucid_attention``) and against the HIP prefill of the whole sequence.
+Tolerance: max |x - ref| <= 2e-2 (bf16 against float64 on the same bf16 inputs).
+"""
+import pytest
+import torch
+
+from oracle import lucid_ref as R
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-2
+
+
+def _inputs(B, Hq, Hkv, T, D, seed):
+    g = torch.Generator().manual_seed(seed)
+    s = D ** -0.5
+    q = (torch.randn(B, Hq, T, D, generator=g) * s).to(torch.bfloat16)
+    k = (torch.randn(B, Hkv, T, D, generator=g) * s).to(torch.bfloat16)
+    v = (torch.randn(B, Hkv, T, D, generator=g) * s).to(torch.bfloat16)
+    return q, k, v
+
+
+def _decode_tail(q, k, v, t0, cap):
+    """Prefill rows [0, t0) with the fused op, then decode rows t0.. one at a time."""
+    from lucid_amd import lucid_attention, lucid_decode
+    B, Hkv, T, D = k.shape
+    kc = torch.zeros(B, Hkv, cap, D, dtype=torch.bfloat16, device="cuda")
+    vc = torch.zeros_like(kc)
+    if t0 > 0:
+        _, vp0 = lucid_attention(q[:, :, :t0], k[:, :, :t0], v[:, :, :t0], return_vprime=True)
+        kc[:, :, :t0] = k[:, :, :t0]
+        vc[:, :, :t0] = vp0.to(torch.bfloat16)
+    outs, vps = [], []
+    for t in range(t0, T):
+        o, vp = lucid_decode(q[:, :, t:t + 1], k[:, :, t:t + 1], v[:, :, t:t + 1], kc, vc, t)
+        outs.append(o)
+        vps.append(vp)
+    torch.cuda.synchronize()
+    return torch.cat(outs, 1), torch.cat(vps, 2), kc, vc
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,T0,n,D", [(2, 4, 2, 300, 3, 64), (1, 8, 1, 1000, 2, 128), (1, 2, 2, 0, 5, 64),
+                                            (1, 4, 4, 130, 2, 64), (2, 4, 1, 77, 2, 128)])
+def test_decode_rows_match_oracle_and_prefill(B, Hq, Hkv, T0, n, D):
+    from lucid_amd import lucid_attention
+    T = T0 + n
+    q, k, v = _inputs(B, Hq, Hkv, T, D, seed=T0 + n + D)
+    print(f"case decode B={B} Hq={Hq} Hkv={Hkv} T0={T0} n={n} D={D}", flush=True)
+    qc, kc_, vc_ = q.cuda(), k.cuda(), v.cuda()
+    o_dec, vp_dec, kcache, vcache = _decode_tail(qc, kc_, vc_, T0, T + 7)
+    o_ref, vp_ref = R.lucid_attention(q.double().numpy(), k.double().numpy(), v.double().numpy())
+    o_ref, vp_ref = torch.from_numpy(o_ref), torch.from_numpy(vp_ref)
+    err_o = (o_dec.cpu().double() - o_ref[:, T0:]).abs().max().item()
+    err_v = (vp_dec.cpu().double() - vp_ref[:, :, T0:]).abs().max().item()
+    assert err_o <= TOL and err_v <= TOL, f"O err {err_o:.3e}, V' err {err_v:.3e}"
+    # against the HIP prefill of the whole sequence, and the cache holds the appended rows
+    o_full, vp_full = lucid_attention(qc, kc_, vc_, return_vprime=True)
+    torch.cuda.synchronize()
+    assert (o_dec.float() - o_full[:, T0:].float()).abs().max().item() <= TOL
+    assert (vp_dec - vp_full[:, :, T0:]).abs().max().item() <= TOL
+    assert torch.equal(kcache[:, :, :T], kc_)
+    assert (vcache[:, :, T0:T].float() - vp_dec).abs().max().item() <= 1e-2 * max(1.0, vp_dec.abs().max().item())
+
+
+def test_decode_long_cache_matches_prefill():
+    """T = 20000 cached rows (the split path with many splits): decoded rows against the
+    HIP prefill of the whole sequence."""
+    from lucid_amd import lucid_attention
+    B, Hq, Hkv, T0, n, D = 1, 4, 2, 20000, 2, 64
+    q, k, v = _inputs(B, Hq, Hkv, T0 + n, D, seed=9)
+    print(f"case decode long T0={T0}", flush=True)
+    qc, kc_, vc_ = q.cuda(), k.cuda(), v.cuda()
+    o_dec, vp_dec, _, _ = _decode_tail(qc, kc_, vc_, T0, T0 + n)
+    o_full, vp_full = lucid_attention(qc, kc_, vc_, return_vprime=True)
+    torch.cuda.synchronize()
+    assert (o_dec.float() - o_full[:, T0:].float()).abs().max().item() <= TOL
+    assert (vp_dec - vp_full[:, :, T0:]).abs().max().item() <= TOL
+
+
+def test_decode_rejects_full_cache():
+    from lucid_amd import lucid_decode
+    q, k, v = (x.cuda() for x in _inputs(1, 2, 2, 1, 64, seed=1))
+    kc = torch.zeros(1, 2, 4, 64, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ValueError, match="cache is full"):
+        lucid_decode(q, k, v, kc, kc.clone(), 4)

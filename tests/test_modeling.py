@@ -113,3 +113,20 @@ def test_decode_matches_prefill_logits():
     err = (dec - ref).abs().max().item()
     assert err <= 2e-2 * max(1.0, ref.abs().max().item()), err
     assert cache.get_seq_length() == T + n_new
+
+
+def test_cache_grows_in_place_and_keeps_rows():
+    cache = M.LucidCache(min_capacity=256)
+    g = torch.Generator().manual_seed(7)
+    k = torch.randn(2, 3, 200, 64, generator=g).to(torch.bfloat16)
+    v = torch.randn(2, 3, 200, 64, generator=g).to(torch.bfloat16)
+    kk, vv = cache.update(k, v, 0)
+    assert cache.get_seq_length(0) == 200 and torch.equal(kk, k) and torch.equal(vv, v)
+    kb, _, n = cache.buffers(0)
+    assert kb.shape[2] == 256 and n == 200
+    cache.reserve(0, k, 100)  # 300 rows > 256: doubles to 512, keeps the valid rows
+    kb2, vb2, n2 = cache.buffers(0)
+    assert kb2.shape[2] == 512 and n2 == 200 and torch.equal(kb2[:, :, :200], k)
+    kb2[:, :, 200] = 1.0
+    cache.advance(0, 1)
+    assert cache.key_cache[0].shape[2] == 201 and torch.equal(cache.value_cache[0][:, :, :200], v)
