@@ -166,18 +166,33 @@ def _check(q, k, v, w, beta, g):
 
 
 def _apply(fn, q, k, v, w, beta, g, scale, cu_seqlens, use_cache):
-    if cu_seqlens is not None:
-        if q.shape[0] != 1:
-            raise ValueError("cu_seqlens requires batch size 1 (packed sequences)")
-        outs, caches = [], []
-        bounds = cu_seqlens.tolist()
-        for s0, s1 in zip(bounds[:-1], bounds[1:]):
-            o_i, kc_i = fn.apply(q[:, s0:s1], k[:, s0:s1], v[:, s0:s1], w[:, s0:s1], beta[:, s0:s1], g, scale,
-                                 None, use_cache)
-            outs.append(o_i)
-            caches.append(kc_i)
-        return torch.cat(outs, 1), (torch.cat(caches, 1) if use_cache else None)
-    return fn.apply(q, k, v, w, beta, g, scale, cu_seqlens, use_cache)
+    if cu_seqlens is None:
+        return fn.apply(q, k, v, w, beta, g, scale, None, use_cache)
+    # packed sequences [1, sum T_i, ...] (the reference's varlen mode, parallel.py:189,214-216):
+    # sequences are bucketed by their length rounded up to the 64-position chunk, and each
+    # bucket runs as one batched call on zero-padded sequences (exact: padding only follows
+    # the real positions, and every operator here is causal)
+    if q.shape[0] != 1:
+        raise ValueError("cu_seqlens requires batch size 1 (packed sequences)")
+    bounds = [int(x) for x in cu_seqlens.tolist()]
+    if bounds[0] != 0 or bounds[-1] != q.shape[1] or any(b1 < b0 for b0, b1 in zip(bounds[:-1], bounds[1:])):
+        raise ValueError("cu_seqlens must rise from 0 to the packed length")
+    spans = [(b0, b1) for b0, b1 in zip(bounds[:-1], bounds[1:]) if b1 > b0]
+    buckets: dict[int, list[int]] = {}
+    for i, (b0, b1) in enumerate(spans):
+        buckets.setdefault((b1 - b0 + 63) // 64 * 64, []).append(i)
+    outs: list = [None] * len(spans)
+    caches: list = [None] * len(spans)
+    for tp, members in buckets.items():
+        def stack(x):
+            return torch.cat([_pad_t(x[:, spans[i][0]:spans[i][1]], tp) for i in members], 0)
+        o_b, kc_b = fn.apply(stack(q), stack(k), stack(v), stack(w), stack(beta), g, scale, None, use_cache)
+        for r, i in enumerate(members):
+            n = spans[i][1] - spans[i][0]
+            outs[i] = o_b[r:r + 1, :n]
+            if use_cache:
+                caches[i] = kc_b[r:r + 1, :n]
+    return torch.cat(outs, 1), (torch.cat(caches, 1) if use_cache else None)
 
 
 @torch.compiler.disable

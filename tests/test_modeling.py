@@ -130,3 +130,33 @@ def test_cache_grows_in_place_and_keeps_rows():
     kb2[:, :, 200] = 1.0
     cache.advance(0, 1)
     assert cache.key_cache[0].shape[2] == 201 and torch.equal(cache.value_cache[0][:, :, :200], v)
+
+
+@pytest.mark.gpu
+def test_right_padded_batch_matches_unpadded_sequences():
+    """Padded batches as the reference's data pipeline builds them (run_clm_chunk.py:517-610:
+    right padding, labels -100 on padding): the real rows' logits equal those of each
+    sequence alone, and the loss ignores the padding."""
+    torch.manual_seed(11)
+    cfg = _tiny(2)
+    model = M.LlamaForCausalLM(cfg).to("cuda", torch.bfloat16).eval()
+    lens, T = (70, 200), 200
+    gen = torch.Generator().manual_seed(12)
+    ids = torch.randint(0, cfg.vocab_size, (2, T), generator=gen)
+    labels = ids.clone()
+    ids[0, lens[0]:] = 0
+    labels[0, lens[0]:] = -100
+    print("case right-padded batch", flush=True)
+    with torch.no_grad():
+        loss, logits = model(ids.cuda(), labels=labels.cuda())
+        for b, n in enumerate(lens):
+            _, alone = model(ids[b:b + 1, :n].cuda())
+            err = (logits[b, :n].float() - alone[0].float()).abs().max().item()
+            assert err <= 2e-2 * max(1.0, alone.abs().max().item()), (b, err)
+        # loss over the real next-token targets only
+        lf = logits[:, :-1].float().reshape(-1, cfg.vocab_size)
+        tgt = labels[:, 1:].reshape(-1).cuda()
+        keep = tgt != -100
+        ref = torch.nn.functional.cross_entropy(lf[keep], tgt[keep])
+    torch.cuda.synchronize()
+    assert abs(loss.item() - ref.item()) < 1e-4

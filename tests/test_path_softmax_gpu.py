@@ -118,3 +118,41 @@ def test_path_softmax_long_sequence_sampled_rows():
         ref = torch.softmax(row * 0.125, dim=0) @ vf[: i + 1]
         err = (o[0, i, 0].float() - ref).abs().max().item()
         assert err <= TOL, f"row {i}: max err {err:.3e}"
+
+
+@pytest.mark.parametrize("softmax", [False, True])
+def test_varlen_packed_sequences(softmax):
+    """cu_seqlens (packed sequences, B = 1): each sequence independent; outputs and gradients
+    against the float64 oracle of every sequence on its own (lengths span several buckets)."""
+    from lucid_amd.lucid_path import parallel_lucid_path_attention, parallel_path_attention
+    bounds = [0, 100, 228, 740, 800, 864]
+    T = bounds[-1]
+    q, k, v, w, beta, do = _inputs(1, T, 2, 1, seed=81 + softmax)
+    print(f"case varlen softmax={softmax} bounds={bounds}", flush=True)
+    leaves = [x.cuda().requires_grad_() for x in (q, k, v, w, beta)]
+    cu = torch.tensor(bounds, dtype=torch.int32, device="cuda")
+    if softmax:
+        o, kc = parallel_path_attention(*leaves, cu_seqlens=cu, use_cache=True)
+    else:
+        qq, kk, vv, ww, bb = leaves
+        o, kc = parallel_lucid_path_attention(kk, vv, ww, bb, q=qq, cu_seqlens=cu, use_cache=True)
+    o.backward(do.cuda())
+    torch.cuda.synchronize()
+    assert o.shape == (1, T, 2, 64) and kc.shape == (1, T, 2, 64)
+    for s0, s1 in zip(bounds[:-1], bounds[1:]):
+        n = s1 - s0
+        tp = (n + 63) // 64 * 64
+        seg = [_padded(x[:, s0:s1], tp) for x in (q, k, v, w, beta)]
+        o_ref, g_ref = TL.path_attention_twolevel(*seg, do=_padded(do[:, s0:s1], tp), scale=0.125, C=64, S=512,
+                                                  softmax=softmax)
+        err = (o[:, s0:s1].detach().cpu().double() - o_ref[:, :n]).abs().max().item()
+        assert err <= TOL, f"seq [{s0},{s1}) O err {err:.3e}"
+        for name, x, r in zip(("dq", "dk", "dv", "dw", "dbeta"), leaves, g_ref):
+            r = r[:, :n]
+            e = (x.grad[:, s0:s1].cpu().double() - r).abs().max().item()
+            assert e <= TOL * max(1.0, r.abs().max().item()), f"seq [{s0},{s1}) {name} err {e:.3e}"
+        kc_ref = P.path_kcache_bruteforce(_f64(k[:, s0:s1]), _f64(w[:, s0:s1]), _f64(beta[:, s0:s1])) if n <= 128 \
+            else None
+        if kc_ref is not None:
+            e = (kc[:, s0:s1].cpu().double() - kc_ref).abs().max().item()
+            assert e <= TOL * max(1.0, kc_ref.abs().max().item()), f"seq [{s0},{s1}) k_cache err {e:.3e}"
