@@ -181,6 +181,11 @@ def bench_decode(args, dev):
     dom_avg = totals[dom][0] / totals[dom][1]
     nbytes = 2.0 * B * Hkv * T * D * 2  # K and V' caches, bf16, read once
     achieved = nbytes / (dom_avg / 1e3) / 1e9
+    traffic = None
+    tfile = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
+    if os.path.exists(tfile):
+        with open(tfile) as fh:
+            traffic = json.load(fh).get(dom)
     out = {
         "metric": "LUCID decode step (one layer, one new token) tokens/s at T=128K cache (config-5 shape)",
         "value": round(B / (ms / 1e3), 1),
@@ -197,7 +202,8 @@ def bench_decode(args, dev):
         "config": {"workload": "lucid_decode_step", "B": B, "Hq": Hq, "Hkv": Hkv, "T_cache": T, "head_dim": D,
                    "parallelism": "single GPU"},
         "roofline": {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "algorithmic_bytes": nbytes},
         "kernels": kernels,
         "cpu_baseline": None,
     }
