@@ -235,7 +235,8 @@ __global__ __launch_bounds__(256) void path_dv_kernel(const bf16* __restrict__ d
 // ascending.  G accumulates d(query operand):
 //   G^T[d][i] += Kop^T[d][j] dA^T[j][i]
 // and at every change of query operand X (large-chunk boundary: X = QB^(s), M = HL_s;
-// inside the large chunk: X = QS^(c), M = Hc_c):  dM += X^T G,  G <- G M^T.
+// inside the large chunk: X = QS^(c), M = Hc_c):  dM += X^T G,  G <- G M^T
+// (X^T from transposing LDS reads of the staged X rows).
 // Finally d q~ = G.  Wave w owns rows 32w..32w+31 of the pair (chunk I1 + w/2,
 // lane <-> row i) and all 64 keys of every key tile; key-operand and O rows are
 // staged by direct global->LDS loads (double buffered), Kop^T comes through
@@ -280,13 +281,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
   const float di = SM ? bw.delta[(int64_t)bhq * T + iw0 + l32] : 0.f;
   f32x16 acc[2] = {zero16(), zero16()};
 
+  int plan_k[2], plan_o[2];
+  dma_plan<64, 8>(64, plan_k);
+  dma_plan<64, 8>(ys.t, plan_o);
   // ---- dM += X^T G over the pair's rows (atomic) and G <- G M^T for each wave's rows ----
-  auto transition = [&](int J, const bf16* XT, const float* M, float* dM) {
+  // X (rows of the query operand, row-major) is staged into the idle half of the double
+  // buffer (tile J+1 is staged only after the transition); X^T comes from transposing reads
+  auto transition = [&](int J, const bf16* X, const float* M, float* dM) {
     const bool act = Iw < NT && J < Iw;
+    bf16* xa_t = sm.k[(J + 1) & 1];  // X rows of chunk I1
+    bf16* xb_t = sm.o[(J + 1) & 1];  // X rows of chunk I1 + 1
+    dma_stage<64, 8>(plan_k, X + (int64_t)I1 * PC * 64, xa_t);
+    if (pair) dma_stage<64, 8>(plan_k, X + (int64_t)(I1 + 1) * PC * 64, xb_t);
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int e = 0; e < 16; ++e) sm.g[32 * w + l32][t * 32 + drow(e, g)] = act ? acc[t][e] : 0.f;
+    dma_wait();
     __syncthreads();
     {
       const int at = w >> 1, bt = w & 1;  // dM tile (a rows, b cols)
@@ -294,7 +305,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
       // rows of a chunk that has left the sweep are skipped: its X rows may be undefined
       const int ks0 = (J < I1) ? 0 : 4, ks1 = (pair && J < I1 + 1) ? 8 : 4;
       for (int ks = ks0; ks < ks1; ++ks) {
-        const bf16x8 xa = ld8(XT + (int64_t)(at * 32 + l32) * T + I1 * PC + 16 * ks + 8 * g);
+        const bf16x8 xa = lds_tr_a<8>(ks < 4 ? xa_t : xb_t, 16 * (ks & 3), at * 32);
         bf16x8 gh, gl;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -327,9 +338,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
     __syncthreads();
   };
 
-  int plan_k[2], plan_o[2];
-  dma_plan<64, 8>(64, plan_k);
-  dma_plan<64, 8>(ys.t, plan_o);
   auto stage = [&](int J) {
     const int buf = J & 1;
     const bf16* kr = ((J < cb) ? ws.kl : ws.kt) + ((int64_t)bh * T + J * PC) * 64;
@@ -346,11 +354,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
     if (J < cb) {
       if (J % PR == 0 && J > 0) {
         const int s = J / PR;
-        transition(J, ws.qbT + ((int64_t)bhq * NS + s) * 64 * T, ws.hl + ((int64_t)bh * NS + s) * 4096,
+        transition(J, ws.qb + ((int64_t)bhq * NS + s) * T * 64, ws.hl + ((int64_t)bh * NS + s) * 4096,
                    bw.dhl + ((int64_t)bhq * NS + s) * 4096);
       }
     } else if (sI > 0 || J > cb) {
-      transition(J, ws.qsT + ((int64_t)bhq * PR + (J - cb)) * 64 * T, ws.hc + ((int64_t)bh * NT + J) * 4096,
+      transition(J, ws.qs + ((int64_t)bhq * PR + (J - cb)) * T * 64, ws.hc + ((int64_t)bh * NT + J) * 4096,
                  bw.dhc + ((int64_t)bhq * NT + J) * 4096);
     }
     if (J + 1 < nJ) stage(J + 1);

@@ -42,18 +42,14 @@ lucid::PathFwdWs carve_path_fwd(void* base, int B, int T, int H, int HQ, size_t*
   w.w2 = reinterpret_cast<float*>(take(BH * T * 64 * 4));
   w.hc = reinterpret_cast<float*>(take(BH * NT * 4096 * 4));
   w.kt = reinterpret_cast<bf16*>(take(BH * T * 64 * 2));
-  w.ktT = reinterpret_cast<bf16*>(take(BH * T * 64 * 2));
   w.suf = reinterpret_cast<float*>(take(BH * NT * 4096 * 4));
   w.hl = reinterpret_cast<float*>(take(BH * NS * 4096 * 4));
   w.kl = reinterpret_cast<bf16*>(take(BH * T * 64 * 2));
-  w.klT = reinterpret_cast<bf16*>(take(BH * T * 64 * 2));
   w.qt = reinterpret_cast<float*>(take(BHq * T * 64 * 4));
   w.ld = reinterpret_cast<float*>(take(BHq * NT * 4096 * 4));
   if (!softmax) w.y = reinterpret_cast<float*>(take(BHq * NT * 4096 * 4));
   w.qs = reinterpret_cast<bf16*>(take(BHq * 8 * T * 64 * 2));
-  w.qsT = reinterpret_cast<bf16*>(take(BHq * 8 * T * 64 * 2));
   w.qb = reinterpret_cast<bf16*>(take(BHq * NS * T * 64 * 2));
-  w.qbT = reinterpret_cast<bf16*>(take(BHq * NS * T * 64 * 2));
   if (!softmax) w.oT = reinterpret_cast<bf16*>(take(BHq * T * 64 * 2));
   w.counters = reinterpret_cast<int*>(take(BHq * 4));
   if (softmax) w.lse = reinterpret_cast<float*>(take(BHq * T * 4));

@@ -24,18 +24,14 @@ struct PathFwdWs {
   float* w2;    // [BH][T][64]        W2 = T_inv (beta W)
   float* hc;    // [BH][NT][64][64]   Hc = I - W^T W2
   bf16* kt;     // [BH][T][64]        k~ rows
-  bf16* ktT;    // [BH][64][T]        k~^T, T-perm
   float* suf;   // [BH][NT][64][64]   SUF_c
   float* hl;    // [BH][NS][64][64]   HL_s
   bf16* kl;     // [BH][T][64]        KL rows
-  bf16* klT;    // [BH][64][T]        KL^T, T-perm
   float* qt;    // [BHq][T][64]       q~
   float* ld;    // [BHq][NT][64][64]  L_diag (strictly lower)
   float* y;     // [BHq][NT][64][64]  (I + L_diag)^-1
   bf16* qs;     // [BHq][8][T][64]    QS rows, slot = c - (first chunk of I's large chunk)
-  bf16* qsT;    // [BHq][8][64][T]    QS^T, T-perm
   bf16* qb;     // [BHq][NS][T][64]   QB rows
-  bf16* qbT;    // [BHq][NS][64][T]   QB^T, T-perm
   bf16* oT;     // [BHq][64][T]       O^T, T-perm (chain operand)
   int* counters;  // [BHq]
   float* lse;   // [BHq][T]           PaTH softmax only: row log-sum-exp, exp2 domain (log2(l) + m)
@@ -146,13 +142,8 @@ __global__ __launch_bounds__(256) void path_chunk_kernel(const bf16* __restrict_
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       bf16x4 v;
-      const int t = t0 + r0 + i;
-      const int slot = (t & ~15) | jmap(t & 15);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        v[j] = (bf16)(Ks[r0 + i][c0 + j] - acc[i][j]);
-        ws.ktT[((int64_t)bh * 64 + c0 + j) * T + slot] = v[j];
-      }
+      for (int j = 0; j < 4; ++j) v[j] = (bf16)(Ks[r0 + i][c0 + j] - acc[i][j]);
       *reinterpret_cast<bf16x4*>(dst + (r0 + i) * 64 + c0) = v;
     }
   }
@@ -252,13 +243,8 @@ __global__ __launch_bounds__(256) void path_large_kernel(int T, PathFwdWs ws) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         bf16x4 v;
-        const int t = c * PC + r0 + i;
-        const int slot = (t & ~15) | jmap(t & 15);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          v[j] = (bf16)acc[i][j];
-          ws.klT[((int64_t)bh * 64 + c0 + j) * T + slot] = v[j];
-        }
+        for (int j = 0; j < 4; ++j) v[j] = (bf16)acc[i][j];
         *reinterpret_cast<bf16x4*>(dst + (r0 + i) * 64 + c0) = v;
       }
     }
@@ -294,8 +280,8 @@ __global__ __launch_bounds__(256) void path_transport_kernel(int HQ, int H, int 
     for (int idx = tid; idx < 4096; idx += 256) X[idx >> 6][idx & 63] = src[idx];
   }
   __syncthreads();
-  // rows of X -> bf16 rows at dst (row stride 64) and T-perm rows at dstT (row stride T)
-  auto emit = [&](bf16* dst, bf16* dstT) {
+  // rows of X -> bf16 rows at dst (row stride 64)
+  auto emit = [&](bf16* dst) {
     const int r = tid >> 2, cc = (tid & 3) * 16;
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
@@ -303,14 +289,6 @@ __global__ __launch_bounds__(256) void path_transport_kernel(int HQ, int H, int 
 #pragma unroll
       for (int e = 0; e < 8; ++e) v[e] = (bf16)X[r][cc + 8 * hh + e];
       *reinterpret_cast<bf16x8*>(dst + (int64_t)r * 64 + cc + 8 * hh) = v;
-    }
-    const int d = tid >> 2, sc = (tid & 3) * 16;  // T-perm row d, slots sc .. sc+15
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-      bf16x8 v;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = (bf16)X[sc + jmap(8 * hh + e)][d];
-      *reinterpret_cast<bf16x8*>(dstT + (int64_t)d * T + I * PC + sc + 8 * hh) = v;
     }
   };
   auto step = [&](const float* M) {
@@ -325,11 +303,11 @@ __global__ __launch_bounds__(256) void path_transport_kernel(int HQ, int H, int 
   };
   for (int c = I - 1; c >= cb; --c) {
     const int slot = c - cb;
-    emit(ws.qs + (((int64_t)bhq * PR + slot) * T + I * PC) * 64, ws.qsT + ((int64_t)bhq * PR + slot) * 64 * T);
+    emit(ws.qs + (((int64_t)bhq * PR + slot) * T + I * PC) * 64);
     step(ws.hc + ((int64_t)bh * NT + c) * 4096);
   }
   for (int s = sI - 1; s >= 0; --s) {
-    emit(ws.qb + (((int64_t)bhq * NS + s) * T + I * PC) * 64, ws.qbT + ((int64_t)bhq * NS + s) * 64 * T);
+    emit(ws.qb + (((int64_t)bhq * NS + s) * T + I * PC) * 64);
     step(ws.hl + ((int64_t)bh * NS + s) * 4096);
   }
 }
