@@ -8,7 +8,7 @@
 //   dK^ = -s (M K^ + M^T K^),  dK = r (dK^ - K^ (K^.dK^)/d) + dK_attn   (RMSNorm backward)
 //
 // Kernels:
-//   lucid_bwd_prep_kernel          delta = rowsum(dO * O), zero the chain counters
+//   lucid_bwd_prep_kernel          ndelta = -rowsum(dO * O), zero the chain counters
 //   lucid_attn_bwd_dkdv_kernel     column sweep: dV' (summed over the GQA group), dK_attn
 //   lucid_attn_bwd_dq_kernel       row sweep: dQ
 //   lucid_precond_bwd_col_kernel   chained transposed solve -> dV, and the M^T K^ column sums
@@ -17,7 +17,8 @@
 
 namespace lucid {
 
-// delta[bhq][t] = dO_t . O_t; zero the chain counters.  grid (T/64, B*Hq)
+// delta[bhq][t] = -(dO_t . O_t) (stored negated: it seeds the dP accumulators of the
+// column sweep); zero the chain counters.  grid (T/64, B*Hq)
 template <int D>
 __global__ __launch_bounds__(256) void lucid_bwd_prep_kernel(const bf16* __restrict__ dout, Strides dos,
                                                              const bf16* __restrict__ o, Strides os, int Hq, int T,
@@ -41,7 +42,7 @@ __global__ __launch_bounds__(256) void lucid_bwd_prep_kernel(const bf16* __restr
   }
   acc += __shfl_xor(acc, 1, 64);
   acc += __shfl_xor(acc, 2, 64);
-  if (seg == 0) delta[(int64_t)bhq * T + t] = acc;
+  if (seg == 0) delta[(int64_t)bhq * T + t] = -acc;
   if (blk == 0 && tid == 0 && bhq < BH) counters[bhq] = 0;
 }
 
@@ -122,60 +123,69 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_bw
     dma_wait();
   }
   __syncthreads();
+  int tro[NDT], rdo[NKS];  // lane offsets of the transposing and the row reads
+#pragma unroll
+  for (int t = 0; t < NDT; ++t) tro[t] = lds_tr_lane_off<D / 8>(t * 32);
+#pragma unroll
+  for (int st = 0; st < NKS; ++st) rdo[st] = static_cast<int>(swz<D / 8>(nullptr, l32, 2 * st + g) - (const bf16*)nullptr);
+  // one 64-row query tile; DIAG: the tile holding this wave's keys (causal mask)
+  auto tile = [&](const int buf, const bool DIAG) {
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      if (DIAG && mt * 32 + 31 < kloc - l32) continue;  // rows all above this wave's keys
+      float lr[16];
+      lds_rows16(&sm.lse[buf][mt * 32], g, lr);
+      f32x16 pv;
+      bf16x8 pb0, pb1;
+      {
+        bf16x8 qa[NKS];
+#pragma unroll
+        for (int st = 0; st < NKS; ++st) qa[st] = ld8(sm.q[buf] + rdo[st] + mt * 32 * D);
+        f32x16 sc = zero16();
+#pragma unroll
+        for (int st = 0; st < NKS; ++st) sc = mfma32(qa[st], kb[st], sc);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          float p = __builtin_amdgcn_exp2f(fmaf(sc[e], c, -lr[e]));
+          if (DIAG && (mt * 32 + drow(e, g) < kloc)) p = 0.f;
+          pv[e] = p;
+        }
+        pb0 = pack_b(pv, 0);
+        pb1 = pack_b(pv, 1);
+      }
+#pragma unroll
+      for (int t = 0; t < NDT; ++t) {
+        adv[t] = mfma32(lds_tr_a_at<D / 8>(sm.dO[buf] + tro[t], mt * 32), pb0, adv[t]);
+        adv[t] = mfma32(lds_tr_a_at<D / 8>(sm.dO[buf] + tro[t], mt * 32 + 16), pb1, adv[t]);
+      }
+      lds_rows16(&sm.dl[buf][mt * 32], g, lr);
+      {
+        bf16x8 da[NKS];
+#pragma unroll
+        for (int st = 0; st < NKS; ++st) da[st] = ld8(sm.dO[buf] + rdo[st] + mt * 32 * D);
+        f32x16 dp;  // dP - delta: the accumulator starts at -delta (stored negated)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) dp[e] = lr[e];
+#pragma unroll
+        for (int st = 0; st < NKS; ++st) dp = mfma32(da[st], vb[st], dp);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) dp[e] = pv[e] * dp[e];
+        pb0 = pack_b(dp, 0);
+        pb1 = pack_b(dp, 1);
+      }
+#pragma unroll
+      for (int t = 0; t < NDT; ++t) {
+        adk[t] = mfma32(lds_tr_a_at<D / 8>(sm.q[buf] + tro[t], mt * 32), pb0, adk[t]);
+        adk[t] = mfma32(lds_tr_a_at<D / 8>(sm.q[buf] + tro[t], mt * 32 + 16), pb1, adk[t]);
+      }
+    }
+  };
   for (int s = 0; s < nsteps; ++s) {
     const int buf = s % 3;
     if (s + 2 < nsteps) stage(s + 2);
     const int it = it_first + s % ntile;
-    if (it >= it_w) {
-      const bool diag = (it == it_w);
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        if (diag && mt * 32 + 31 < kloc - l32) continue;  // rows all above this wave's keys
-        float lr[16];
-        lds_rows16(&sm.lse[buf][mt * 32], g, lr);
-        f32x16 pv;
-        bf16x8 pb0, pb1;
-        {
-          bf16x8 qa[NKS];
-#pragma unroll
-          for (int st = 0; st < NKS; ++st) qa[st] = ld8(swz<D / 8>(sm.q[buf], mt * 32 + l32, 2 * st + g));
-          f32x16 sc = zero16();
-#pragma unroll
-          for (int st = 0; st < NKS; ++st) sc = mfma32(qa[st], kb[st], sc);
-#pragma unroll
-          for (int e = 0; e < 16; ++e) {
-            float p = __builtin_amdgcn_exp2f(fmaf(sc[e], c, -lr[e]));
-            if (diag && (mt * 32 + drow(e, g) < kloc)) p = 0.f;
-            pv[e] = p;
-          }
-          pb0 = pack_b(pv, 0);
-          pb1 = pack_b(pv, 1);
-        }
-#pragma unroll
-        for (int t = 0; t < NDT; ++t) {
-          adv[t] = mfma32(lds_tr_a<D / 8>(sm.dO[buf], mt * 32, t * 32), pb0, adv[t]);
-          adv[t] = mfma32(lds_tr_a<D / 8>(sm.dO[buf], mt * 32 + 16, t * 32), pb1, adv[t]);
-        }
-        lds_rows16(&sm.dl[buf][mt * 32], g, lr);
-        {
-          bf16x8 da[NKS];
-#pragma unroll
-          for (int st = 0; st < NKS; ++st) da[st] = ld8(swz<D / 8>(sm.dO[buf], mt * 32 + l32, 2 * st + g));
-          f32x16 dp = zero16();
-#pragma unroll
-          for (int st = 0; st < NKS; ++st) dp = mfma32(da[st], vb[st], dp);
-#pragma unroll
-          for (int e = 0; e < 16; ++e) dp[e] = pv[e] * (dp[e] - lr[e]);
-          pb0 = pack_b(dp, 0);
-          pb1 = pack_b(dp, 1);
-        }
-#pragma unroll
-        for (int t = 0; t < NDT; ++t) {
-          adk[t] = mfma32(lds_tr_a<D / 8>(sm.q[buf], mt * 32, t * 32), pb0, adk[t]);
-          adk[t] = mfma32(lds_tr_a<D / 8>(sm.q[buf], mt * 32 + 16, t * 32), pb1, adk[t]);
-        }
-      }
-    }
+    if (it > it_w) tile(buf, false);
+    else if (it == it_w) tile(buf, true);
     if (s + 2 < nsteps) dma_wait_but<STAGE_OPS>();  // the step after next may stay in flight
     else dma_wait();
     __syncthreads();
@@ -300,7 +310,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_bw
           for (int e = 0; e < 16; ++e) {
             float p = __builtin_amdgcn_exp2f(fmaf(sc[e], c, -li[nt]));
             if (diag && (mt * 32 + drow(e, g) > nt * 32 + l32)) p = 0.f;
-            sc[e] = p * (dp[e] - di[nt]);
+            sc[e] = p * (dp[e] + di[nt]);  // di holds -delta
           }
           dsb[nt][0] = pack_b(sc, 0);
           dsb[nt][1] = pack_b(sc, 1);

@@ -15,23 +15,24 @@ struct Strides {
 // substitution, x_r = (delta_rc - sum_{k<r} P_rk x_k) / P_rr.  The diagonal of
 // P is exp(s K^_r.K^_r - 1/s) in (0, 1], the off-diagonal entries lie in (0, 1],
 // so plain substitution (no series) is used.  X overwrites P in LDS and is
-// also written to gout[r*64 + c].
+// also written to gout[r*64 + c].  Each sum runs over four independent accumulators
+// to shorten the dependent chain.
 __device__ __forceinline__ void invert_lower64(float (*Ps)[68], int c, float* __restrict__ gout) {
   float x[64];
 #pragma unroll
   for (int r = 0; r < 64; ++r) {
-    float acc = (r == c) ? 1.f : 0.f;
+    float a0 = (r == c) ? 1.f : 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
 #pragma unroll
     for (int kk = 0; kk < (r & ~3); kk += 4) {
       const f32x4 p = *reinterpret_cast<const f32x4*>(&Ps[r][kk]);
-      acc = fmaf(-p[0], x[kk], acc);
-      acc = fmaf(-p[1], x[kk + 1], acc);
-      acc = fmaf(-p[2], x[kk + 2], acc);
-      acc = fmaf(-p[3], x[kk + 3], acc);
+      a0 = fmaf(-p[0], x[kk], a0);
+      a1 = fmaf(-p[1], x[kk + 1], a1);
+      a2 = fmaf(-p[2], x[kk + 2], a2);
+      a3 = fmaf(-p[3], x[kk + 3], a3);
     }
 #pragma unroll
-    for (int kk = (r & ~3); kk < r; ++kk) acc = fmaf(-Ps[r][kk], x[kk], acc);
-    x[r] = acc / Ps[r][r];
+    for (int kk = (r & ~3); kk < r; ++kk) a0 = fmaf(-Ps[r][kk], x[kk], a0);
+    x[r] = ((a0 + a1) + (a2 + a3)) / Ps[r][r];
   }
 #pragma unroll
   for (int r = 0; r < 64; ++r) {
@@ -254,6 +255,25 @@ __device__ __forceinline__ bf16x8 lds_tr_a(const bf16* tile, int row0, int col0)
   const int off = (((col >> 3) ^ (r1 & 7)) << 3) | (col & 7);  // rows r1 and r1 + 8 share the swizzle
   const bf16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(tile + r1 * (CPR * 8) + off));
   const bf16x4 v2 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(tile + (r1 + 8) * (CPR * 8) + off));
+  return bf16x8{v1[0], v1[1], v1[2], v1[3], v2[0], v2[1], v2[2], v2[3]};
+}
+
+// lds_tr_a split into its lane part (once per kernel) and its tile part: the lane
+// offset (elements) of the transposing read for column block col0 (a multiple of 32)
+// at row0 = 0; rows row0 (a multiple of 16) then add row0 * CPR * 8, a constant that
+// the compiler folds into the instruction's offset field.
+template <int CPR>
+__device__ __forceinline__ int lds_tr_lane_off(int col0) {
+  const int lane = threadIdx.x & 63, s = lane & 15;
+  const int col = col0 + 16 * ((lane >> 4) & 1) + 4 * (s & 3);
+  const int r1 = 4 * (lane >> 5) + (s >> 2);
+  return r1 * (CPR * 8) + ((((col >> 3) ^ (r1 & 7)) << 3) | (col & 7));
+}
+template <int CPR>
+__device__ __forceinline__ bf16x8 lds_tr_a_at(const bf16* tile_lane, int row0) {
+  typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+  const bf16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(tile_lane + row0 * (CPR * 8)));
+  const bf16x4 v2 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(tile_lane + (row0 + 8) * (CPR * 8)));
   return bf16x8{v1[0], v1[1], v1[2], v1[3], v2[0], v2[1], v2[2], v2[3]};
 }
 

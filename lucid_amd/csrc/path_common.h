@@ -10,31 +10,42 @@ constexpr int PR = 8;   // small chunks per large chunk
 
 // acc[i][j] += sum_k opA(A)[r0+i][k] * opB(B)[k][c0+j] for 64x64 fp32 LDS matrices
 // (row stride 68); thread t owns the 4x4 block r0 = 4*(t/16), c0 = 4*(t%16).
+// Four k-steps per iteration: every operand is read as 16-byte vectors (along k for
+// the row-indexed operands, along the block for the others), 8 reads per 64 FMAs.
 template <bool TA, bool TB>
 __device__ __forceinline__ void lds_gemm64(const float (*A)[68], const float (*B)[68], float acc[4][4]) {
   const int tid = threadIdx.x;
   const int r0 = (tid >> 4) * 4, c0 = (tid & 15) * 4;
-#pragma unroll 4
-  for (int k = 0; k < 64; ++k) {
-    float a[4], b[4];
-    if (TA) {
-      const f32x4 t4 = *reinterpret_cast<const f32x4*>(&A[k][r0]);
-      a[0] = t4[0]; a[1] = t4[1]; a[2] = t4[2]; a[3] = t4[3];
-    } else {
+#pragma unroll 2
+  for (int k = 0; k < 64; k += 4) {
+    float a[4][4], b[4][4];  // a[kk][i] = opA[r0+i][k+kk], b[kk][j] = opB[k+kk][c0+j]
 #pragma unroll
-      for (int i = 0; i < 4; ++i) a[i] = A[r0 + i][k];
+    for (int q = 0; q < 4; ++q) {
+      if (TA) {
+        const f32x4 t4 = *reinterpret_cast<const f32x4*>(&A[k + q][r0]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a[q][i] = t4[i];
+      } else {
+        const f32x4 t4 = *reinterpret_cast<const f32x4*>(&A[r0 + q][k]);
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) a[kk][q] = t4[kk];
+      }
+      if (TB) {
+        const f32x4 t4 = *reinterpret_cast<const f32x4*>(&B[c0 + q][k]);
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) b[kk][q] = t4[kk];
+      } else {
+        const f32x4 t4 = *reinterpret_cast<const f32x4*>(&B[k + q][c0]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) b[q][j] = t4[j];
+      }
     }
-    if (TB) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) b[j] = B[c0 + j][k];
-    } else {
-      const f32x4 t4 = *reinterpret_cast<const f32x4*>(&B[k][c0]);
-      b[0] = t4[0]; b[1] = t4[1]; b[2] = t4[2]; b[3] = t4[3];
-    }
+    for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
+        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(a[kk][i], b[kk][j], acc[i][j]);
   }
 }
 
@@ -47,23 +58,24 @@ __device__ __forceinline__ void zero44(float acc[4][4]) {
 
 // (I + M)^-1 in place for the strictly lower part of a 64x64 fp32 LDS matrix (the
 // diagonal and upper part of M are ignored).  Called by ONE wave: lane c solves
-// column c by forward substitution x_r = delta_rc - sum_{k<r} M_rk x_k.
+// column c by forward substitution x_r = delta_rc - sum_{k<r} M_rk x_k, each sum
+// split over four independent accumulators to shorten the dependent chain.
 __device__ __forceinline__ void invert_unit_lower64(float (*M)[68], int c) {
   float x[64];
 #pragma unroll
   for (int r = 0; r < 64; ++r) {
-    float acc = (r == c) ? 1.f : 0.f;
+    float a0 = (r == c) ? 1.f : 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
 #pragma unroll
     for (int kk = 0; kk < (r & ~3); kk += 4) {
       const f32x4 p = *reinterpret_cast<const f32x4*>(&M[r][kk]);
-      acc = fmaf(-p[0], x[kk], acc);
-      acc = fmaf(-p[1], x[kk + 1], acc);
-      acc = fmaf(-p[2], x[kk + 2], acc);
-      acc = fmaf(-p[3], x[kk + 3], acc);
+      a0 = fmaf(-p[0], x[kk], a0);
+      a1 = fmaf(-p[1], x[kk + 1], a1);
+      a2 = fmaf(-p[2], x[kk + 2], a2);
+      a3 = fmaf(-p[3], x[kk + 3], a3);
     }
 #pragma unroll
-    for (int kk = (r & ~3); kk < r; ++kk) acc = fmaf(-M[r][kk], x[kk], acc);
-    x[r] = acc;
+    for (int kk = (r & ~3); kk < r; ++kk) a0 = fmaf(-M[r][kk], x[kk], a0);
+    x[r] = (a0 + a1) + (a2 + a3);
   }
 #pragma unroll
   for (int r = 0; r < 64; ++r) M[r][c] = x[r];
