@@ -127,7 +127,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_bw
 #pragma unroll
   for (int t = 0; t < NDT; ++t) tro[t] = lds_tr_lane_off<D / 8>(t * 32);
 #pragma unroll
-  for (int st = 0; st < NKS; ++st) rdo[st] = static_cast<int>(swz<D / 8>(nullptr, l32, 2 * st + g) - (const bf16*)nullptr);
+  for (int st = 0; st < NKS; ++st) rdo[st] = swz_off<D / 8>(l32, 2 * st + g);
   // one 64-row query tile; DIAG: the tile holding this wave's keys (causal mask)
   auto tile = [&](const int buf, const bool DIAG) {
 #pragma unroll
@@ -284,48 +284,58 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_bw
     dma_wait();
   }
   __syncthreads();
+  // lane offsets of the row reads (the transposing reads keep their per-read address
+  // arithmetic here: with precomputed offsets the register-bound D = 128 instance of
+  // this kernel returned NaN in dQ, unlike the same helper in the dK/dV sweep)
+  int rdo[NKS];
+#pragma unroll
+  for (int st = 0; st < NKS; ++st) rdo[st] = swz_off<D / 8>(l32, 2 * st + g);
+  // one 64-key tile; DIAG: the tile holding this wave's rows (causal mask)
+  auto tile = [&](const int buf, const bool DIAG) {
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      bf16x8 ka[NKS], va[NKS];
+#pragma unroll
+      for (int st = 0; st < NKS; ++st) {
+        ka[st] = ld8(sm.k[buf] + rdo[st] + mt * 32 * D);
+        va[st] = ld8(sm.v[buf] + rdo[st] + mt * 32 * D);
+      }
+      bf16x8 dsb[2][2];
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        f32x16 sc = zero16(), dp = zero16();
+#pragma unroll
+        for (int st = 0; st < NKS; ++st) {
+          sc = mfma32(ka[st], qb[nt][st], sc);
+          dp = mfma32(va[st], db[nt][st], dp);
+        }
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          float p = __builtin_amdgcn_exp2f(fmaf(sc[e], c, -li[nt]));
+          if (DIAG && (mt * 32 + drow(e, g) > nt * 32 + l32)) p = 0.f;
+          sc[e] = p * (dp[e] + di[nt]);  // di holds -delta
+        }
+        dsb[nt][0] = pack_b(sc, 0);
+        dsb[nt][1] = pack_b(sc, 1);
+      }
+#pragma unroll
+      for (int t = 0; t < NDT; ++t) {
+        const bf16x8 a0 = lds_tr_a<D / 8>(sm.k[buf], mt * 32, t * 32);
+        const bf16x8 a1 = lds_tr_a<D / 8>(sm.k[buf], mt * 32 + 16, t * 32);
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+          acc[t][nt] = mfma32(a0, dsb[nt][0], acc[t][nt]);
+          acc[t][nt] = mfma32(a1, dsb[nt][1], acc[t][nt]);
+        }
+      }
+    }
+  };
   for (int jt = 0; jt < ntile; ++jt) {
     const int buf = jt % 3;
     if (jt + 2 < ntile) stage(jt + 2);
-    if (jt <= last_w && row0 < T) {
-      const bool diag = (jt == last_w);
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        bf16x8 ka[NKS], va[NKS];
-#pragma unroll
-        for (int st = 0; st < NKS; ++st) {
-          ka[st] = ld8(swz<D / 8>(sm.k[buf], mt * 32 + l32, 2 * st + g));
-          va[st] = ld8(swz<D / 8>(sm.v[buf], mt * 32 + l32, 2 * st + g));
-        }
-        bf16x8 dsb[2][2];
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
-          f32x16 sc = zero16(), dp = zero16();
-#pragma unroll
-          for (int st = 0; st < NKS; ++st) {
-            sc = mfma32(ka[st], qb[nt][st], sc);
-            dp = mfma32(va[st], db[nt][st], dp);
-          }
-#pragma unroll
-          for (int e = 0; e < 16; ++e) {
-            float p = __builtin_amdgcn_exp2f(fmaf(sc[e], c, -li[nt]));
-            if (diag && (mt * 32 + drow(e, g) > nt * 32 + l32)) p = 0.f;
-            sc[e] = p * (dp[e] + di[nt]);  // di holds -delta
-          }
-          dsb[nt][0] = pack_b(sc, 0);
-          dsb[nt][1] = pack_b(sc, 1);
-        }
-#pragma unroll
-        for (int t = 0; t < NDT; ++t) {
-          const bf16x8 a0 = lds_tr_a<D / 8>(sm.k[buf], mt * 32, t * 32);
-          const bf16x8 a1 = lds_tr_a<D / 8>(sm.k[buf], mt * 32 + 16, t * 32);
-#pragma unroll
-          for (int nt = 0; nt < 2; ++nt) {
-            acc[t][nt] = mfma32(a0, dsb[nt][0], acc[t][nt]);
-            acc[t][nt] = mfma32(a1, dsb[nt][1], acc[t][nt]);
-          }
-        }
-      }
+    if (row0 < T) {
+      if (jt < last_w) tile(buf, false);
+      else if (jt == last_w) tile(buf, true);
     }
     if (jt + 2 < ntile) dma_wait_but<STAGE_OPS>();  // the step after next may stay in flight
     else dma_wait();

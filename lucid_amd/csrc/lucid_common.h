@@ -230,10 +230,15 @@ __device__ __forceinline__ void dma_wait_but() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
-// Address of logical chunk c (8 bf16) of row r in a swizzled tile with CPR chunks per row.
+// Element offset of logical chunk c (8 bf16) of row r in a swizzled tile with CPR
+// chunks per row, and its address.
+template <int CPR>
+__device__ __forceinline__ int swz_off(int r, int c) {
+  return r * (CPR * 8) + ((c ^ (r & 7)) << 3);
+}
 template <int CPR>
 __device__ __forceinline__ const bf16* swz(const bf16* tile, int r, int c) {
-  return tile + r * (CPR * 8) + ((c ^ (r & 7)) << 3);
+  return tile + swz_off<CPR>(r, c);
 }
 
 // MFMA A operand [m = col0 + lane%32][k = 16 rows from row0] read from a
