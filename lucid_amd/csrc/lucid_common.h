@@ -15,24 +15,23 @@ struct Strides {
 // substitution, x_r = (delta_rc - sum_{k<r} P_rk x_k) / P_rr.  The diagonal of
 // P is exp(s K^_r.K^_r - 1/s) in (0, 1], the off-diagonal entries lie in (0, 1],
 // so plain substitution (no series) is used.  X overwrites P in LDS and is
-// also written to gout[r*64 + c].  Each sum runs over four independent accumulators
-// to shorten the dependent chain.
+// also written to gout[r*64 + c].
 __device__ __forceinline__ void invert_lower64(float (*Ps)[68], int c, float* __restrict__ gout) {
   float x[64];
 #pragma unroll
   for (int r = 0; r < 64; ++r) {
-    float a0 = (r == c) ? 1.f : 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+    float acc = (r == c) ? 1.f : 0.f;
 #pragma unroll
     for (int kk = 0; kk < (r & ~3); kk += 4) {
       const f32x4 p = *reinterpret_cast<const f32x4*>(&Ps[r][kk]);
-      a0 = fmaf(-p[0], x[kk], a0);
-      a1 = fmaf(-p[1], x[kk + 1], a1);
-      a2 = fmaf(-p[2], x[kk + 2], a2);
-      a3 = fmaf(-p[3], x[kk + 3], a3);
+      acc = fmaf(-p[0], x[kk], acc);
+      acc = fmaf(-p[1], x[kk + 1], acc);
+      acc = fmaf(-p[2], x[kk + 2], acc);
+      acc = fmaf(-p[3], x[kk + 3], acc);
     }
 #pragma unroll
-    for (int kk = (r & ~3); kk < r; ++kk) a0 = fmaf(-Ps[r][kk], x[kk], a0);
-    x[r] = ((a0 + a1) + (a2 + a3)) / Ps[r][r];
+    for (int kk = (r & ~3); kk < r; ++kk) acc = fmaf(-Ps[r][kk], x[kk], acc);
+    x[r] = acc / Ps[r][r];
   }
 #pragma unroll
   for (int r = 0; r < 64; ++r) {
