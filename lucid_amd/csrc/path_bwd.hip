@@ -53,7 +53,7 @@ __global__ __launch_bounds__(256) void path_bwd_zero_kernel(int64_t n_hl, int64_
 //   S[I][J] = Qop_I . Kop_J, L = exp(s S - 1/s), acc^T[d][j] += dV^T[d][i] L[i][j]
 // counters[bhq] = number of chunks of dV published from the end.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void path_dv_kernel(const bf16* __restrict__ dout, Strides dos,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void path_dv_kernel(const bf16* __restrict__ dout, Strides dos,
                                                       const bf16* __restrict__ o, Strides os, int HQ, int H, int T,
                                                       int BHq, float scale, PathFwdWs ws, PathBwdWs bw) {
   __shared__ __attribute__((aligned(16))) float Yt[64][68];  // Yt[c][r] = Y[r][c]

@@ -319,7 +319,7 @@ __global__ __launch_bounds__(256) void path_transport_kernel(int HQ, int H, int 
 //   S^T[j][i] = Kop_J . Qop_I, P = exp(s S - 1/s), acc^T[d][i] += O^T[d][j] P^T[j][i]
 //   O_I = Y_I (V_I - acc)   (3-term bf16 split)
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void path_solve_fwd_kernel(const bf16* __restrict__ v, Strides vs,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void path_solve_fwd_kernel(const bf16* __restrict__ v, Strides vs,
                                                              bf16* __restrict__ o, Strides os, int HQ, int H,
                                                              int T, int BHq, float scale, PathFwdWs ws) {
   __shared__ __attribute__((aligned(16))) float Ys[64][68];
