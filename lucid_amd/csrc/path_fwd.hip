@@ -291,24 +291,44 @@ __global__ __launch_bounds__(256) void path_transport_kernel(int HQ, int H, int 
       *reinterpret_cast<bf16x8*>(dst + (int64_t)r * 64 + cc + 8 * hh) = v;
     }
   };
-  auto step = [&](const float* M) {
-    load_mat64<true>(MT, M);
-    __syncthreads();
+  // steps k = 0 .. nq-1 carry X through Hc_{I-1} .. Hc_cb (emitting QS), steps nq .. nq+sI-1
+  // through HL_{sI-1} .. HL_0 (emitting QB).  The transition matrix of step k+1 is loaded
+  // into registers while step k computes, so no step waits for its operand.
+  const int nq = I - cb, nsteps = nq + sI;
+  auto mat = [&](int k) {
+    return (k < nq) ? ws.hc + ((int64_t)bh * NT + (I - 1 - k)) * 4096
+                    : ws.hl + ((int64_t)bh * NS + (sI - 1 - (k - nq))) * 4096;
+  };
+  f32x4 mr[4];  // thread t holds M[r][c4 .. c4+3], r = (t + 256 u) / 16, c4 = 4 ((t + 256 u) % 16)
+  auto mload = [&](int k) {
+    const float* M = mat(k);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) mr[u] = *reinterpret_cast<const f32x4*>(M + 4 * (tid + 256 * u));
+  };
+  auto mstore_t = [&]() {  // MT[c][r] = M[r][c]
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int idx = tid + 256 * u, r = idx >> 4, c4 = (idx & 15) * 4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) MT[c4 + e][r] = mr[u][e];
+    }
+  };
+  if (nsteps > 0) {
+    mload(0);
+    mstore_t();
+  }
+  __syncthreads();
+  for (int k = 0; k < nsteps; ++k) {
+    if (k + 1 < nsteps) mload(k + 1);
+    emit(k < nq ? ws.qs + (((int64_t)bhq * PR + (I - 1 - k - cb)) * T + I * PC) * 64
+                : ws.qb + (((int64_t)bhq * NS + (sI - 1 - (k - nq))) * T + I * PC) * 64);
     const int dt = w >> 1, rt = w & 1;
     const f32x16 o = mat_xM_tile(X, MT, dt, rt);
     __syncthreads();
 #pragma unroll
     for (int e = 0; e < 16; ++e) X[rt * 32 + l32][dt * 32 + drow(e, g)] = o[e];
+    if (k + 1 < nsteps) mstore_t();
     __syncthreads();
-  };
-  for (int c = I - 1; c >= cb; --c) {
-    const int slot = c - cb;
-    emit(ws.qs + (((int64_t)bhq * PR + slot) * T + I * PC) * 64);
-    step(ws.hc + ((int64_t)bh * NT + c) * 4096);
-  }
-  for (int s = sI - 1; s >= 0; --s) {
-    emit(ws.qb + (((int64_t)bhq * NS + s) * T + I * PC) * 64);
-    step(ws.hl + ((int64_t)bh * NS + s) * 4096);
   }
 }
 
