@@ -107,6 +107,12 @@ class LucidAttentionFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, scale, eps):
         t = q.shape[2]
+        ctx.empty = t == 0 or q.numel() == 0
+        ctx.shapes = (q.shape, k.shape)
+        if ctx.empty:  # the reference's torch ops return empty results (no kernel launch)
+            B, Hq, _, D = q.shape
+            return (q.new_empty(B, t, Hq, D),
+                    torch.empty(B, k.shape[1], t, D, dtype=torch.float32, device=q.device))
         tp = _padded_len(t)
         qp, kp, vp_ = _prep(q, tp), _prep(k, tp), _prep(v, tp)
         o, vprime, lse, ws = _fwd(qp, kp, vp_, scale, eps)
@@ -117,6 +123,8 @@ class LucidAttentionFunction(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, do, _dvprime):
+        if ctx.empty:
+            return do.new_zeros(ctx.shapes[0]), do.new_zeros(ctx.shapes[1]), do.new_zeros(ctx.shapes[1]), None, None
         qp, kp, o, lse, ws = ctx.saved_tensors
         t, tp = ctx.t, qp.shape[2]
         if do.dtype != torch.bfloat16:
@@ -143,8 +151,10 @@ def lucid_attention(query, key, value, scaling=None, eps=1e-5, return_vprime=Fal
 def get_v_prime(key, value, scaling=None, eps=1e-5):
     """``V' = P^-1 V`` (forward only), fp32 ``[B, Hkv, T, d]`` -- get_v_prime, modeling_lucid.py:551-574."""
     _check_inputs(None, key, value)
-    lib = _lib.load()
     B, Hkv, T, D = key.shape
+    if T == 0 or key.numel() == 0:
+        return torch.empty(B, Hkv, T, D, dtype=torch.float32, device=key.device)
+    lib = _lib.load()
     tp = _padded_len(T)
     k, v = _prep(key, tp), _prep(value, tp)
     scale = D ** -0.5 if scaling is None else float(scaling)

@@ -166,6 +166,9 @@ def _check(q, k, v, w, beta, g):
 
 
 def _apply(fn, q, k, v, w, beta, g, scale, cu_seqlens, use_cache):
+    if q.shape[1] == 0 or q.numel() == 0:  # empty: empty results, as the reference's ops give
+        o = q.new_zeros(*q.shape[:3], v.shape[-1]) + 0 * (q.sum() + k.sum() + v.sum() + w.sum() + beta.sum())
+        return o, (k.new_empty(k.shape) if use_cache else None)
     if cu_seqlens is None:
         return fn.apply(q, k, v, w, beta, g, scale, None, use_cache)
     # packed sequences [1, sum T_i, ...] (the reference's varlen mode, parallel.py:189,214-216):

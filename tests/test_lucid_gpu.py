@@ -120,3 +120,49 @@ def test_full_size_solve_residual_and_rows(T, H):
         ref = torch.softmax(sc, -1) @ vp[0, h]
         err = float((o[0, idx, h].float() - ref).abs().max())
         assert err <= TOL, f"head {h}: sampled-row err {err:.3e}"
+
+
+def test_config5_long_context_gqa_d128_rows():
+    """Config 5 shape (T = 131072, 32 query heads over 8 kv heads, d = 128), forward only:
+    sampled rows of the solve residual (P V')_i = V_i for two kv heads and sampled rows of
+    the attention output for query heads of different groups, in fp32 on the GPU."""
+    from lucid_amd import lucid_attention
+    T, Hq, Hkv, D = 131072, 32, 8, 128
+    q, k, v, _ = _inputs(1, Hq, Hkv, T, D, seed=5)
+    print(f"case config5 T={T} Hq={Hq} Hkv={Hkv} D={D}", flush=True)
+    qc, kc, vc = q.cuda(), k.cuda(), v.cuda()
+    del q, k, v
+    with torch.no_grad():
+        o, vp = lucid_attention(qc, kc, vc, return_vprime=True)
+        torch.cuda.synchronize()
+        s = D ** -0.5
+        rows = torch.arange(T, device="cuda")
+        idx = torch.tensor([0, 1, 127, 128, 5000, T // 2, T - 129, T - 1], device="cuda")
+        for h in (0, Hkv - 1):
+            kf = kc[0, h].float()
+            kh = kf * torch.rsqrt(kf.pow(2).mean(-1, keepdim=True) + 1e-5)
+            pr = torch.exp(kh[idx] @ kh.T * s - 1 / s) * (rows[None, :] <= idx[:, None])
+            res = (pr @ vp[0, h]) - vc[0, h, idx].float()
+            rel = float(res.norm() / vc[0, h, idx].float().norm())
+            assert rel < 5e-3, f"kv head {h}: sampled residual {rel:.3e}"
+        for hq in (0, 5, Hq - 1):
+            h = hq // (Hq // Hkv)
+            sc = (qc[0, hq, idx].float() @ kc[0, h].float().T) * s
+            sc = sc.masked_fill(rows[None, :] > idx[:, None], float("-inf"))
+            ref = torch.softmax(sc, -1) @ vp[0, h]
+            err = float((o[0, idx, hq].float() - ref).abs().max())
+            assert err <= TOL, f"query head {hq}: sampled-row err {err:.3e}"
+
+
+def test_empty_sequence_returns_empty_like_the_reference():
+    """T = 0: the reference's dense path (einsum, solve_triangular, SDPA) returns empty
+    tensors; so do the operators here, gradients included."""
+    from lucid_amd import get_v_prime, lucid_attention
+    q = torch.zeros(2, 4, 0, 64, dtype=torch.bfloat16, device="cuda", requires_grad=True)
+    k = torch.zeros(2, 2, 0, 64, dtype=torch.bfloat16, device="cuda", requires_grad=True)
+    v = torch.zeros(2, 2, 0, 64, dtype=torch.bfloat16, device="cuda", requires_grad=True)
+    o, vp = lucid_attention(q, k, v, return_vprime=True)
+    assert o.shape == (2, 0, 4, 64) and vp.shape == (2, 2, 0, 64)
+    o.sum().backward()
+    assert q.grad.shape == q.shape and k.grad.shape == k.shape and v.grad.shape == v.shape
+    assert get_v_prime(k.detach(), v.detach()).shape == (2, 2, 0, 64)

@@ -156,3 +156,15 @@ def test_varlen_packed_sequences(softmax):
         if kc_ref is not None:
             e = (kc[:, s0:s1].cpu().double() - kc_ref).abs().max().item()
             assert e <= TOL * max(1.0, kc_ref.abs().max().item()), f"seq [{s0},{s1}) k_cache err {e:.3e}"
+
+
+def test_empty_sequence_returns_empty():
+    from lucid_amd.lucid_path import parallel_lucid_path_attention, parallel_path_attention
+    q, k, v, w, beta, _ = _inputs(1, 0, 2, 1, seed=1)
+    leaves = [x.cuda().requires_grad_() for x in (q, k, v, w, beta)]
+    o, kc = parallel_path_attention(*leaves, use_cache=True)
+    assert o.shape == (1, 0, 2, 64) and kc.shape == (1, 0, 2, 64)
+    o.sum().backward()
+    assert all(x.grad is not None and x.grad.shape == x.shape for x in leaves)
+    o2, kc2 = parallel_lucid_path_attention(*leaves[1:], q=leaves[0])
+    assert o2.shape == (1, 0, 2, 64) and kc2 is None
