@@ -797,8 +797,45 @@ __global__ __launch_bounds__(256) void path_products_bwd_kernel(int HQ, int H, i
 //   q~ = q - QW W2 (QW = tril(q W^T)), k~ = k - TW^T W (TW = Tm stril(Wb k^T)),
 //   A_diag = tril(q k^T - QW TW).
 // Inputs d q~, d k~, dA_diag, dHc; outputs dq, dk, dw, dbeta (per query head, fp32).
-// All 64x64 products in fp32 on LDS (9 buffers).  grid (NT, B*HQ)
+// The 64x64 products run on the matrix cores (mgemm64, 3-term bf16 split, ~fp32
+// accuracy); every wave keeps its 32x32 tile of each running result in MFMA D layout
+// (rows dl_row(e), column dl_col()).  Operands live in 9 fp32 LDS buffers.
+// grid (NT, B*HQ)
 // ---------------------------------------------------------------------------
+// D-layout tile element helpers: S[row][col] <- x (masked), x <- S[row][col]
+#define WY_FOR_E _Pragma("unroll") for (int e = 0; e < 16; ++e)
+__device__ __forceinline__ void wy_store(float (*S)[68], const f32x16& x, int mode) {
+  // mode 0: all, 1: col <= row (tril), 2: col < row (strictly lower)
+  const int cl = dl_col();
+  WY_FOR_E {
+    const int r = dl_row(e);
+    const bool keep = mode == 0 || (mode == 1 ? cl <= r : cl < r);
+    S[r][cl] = keep ? x[e] : 0.f;
+  }
+}
+__device__ __forceinline__ f32x16 wy_load(const float (*S)[68]) {
+  const int cl = dl_col();
+  f32x16 x;
+  WY_FOR_E x[e] = S[dl_row(e)][cl];
+  return x;
+}
+// 64x64 fp32 row-major matrix: thread t holds rows (t + 256 i) / 16, 4 columns each
+__device__ __forceinline__ void wy_fetch(f32x4 v[4], const float* __restrict__ src) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = *reinterpret_cast<const f32x4*>(src + 4 * (threadIdx.x + 256 * i));
+}
+__device__ __forceinline__ void wy_put(float (*S)[68], const f32x4 v[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int f = 4 * (threadIdx.x + 256 * i);
+    *reinterpret_cast<f32x4*>(&S[f >> 6][f & 63]) = v[i];
+  }
+}
+__device__ __forceinline__ f32x16 wy_neg(f32x16 x) {
+  WY_FOR_E x[e] = -x[e];
+  return x;
+}
+
 __global__ __launch_bounds__(256) void path_wy_bwd_kernel(const bf16* __restrict__ q, Strides qs,
                                                           const bf16* __restrict__ k, Strides ks,
                                                           const bf16* __restrict__ w, Strides wst,
@@ -813,15 +850,23 @@ __global__ __launch_bounds__(256) void path_wy_bwd_kernel(const bf16* __restrict
   __shared__ __attribute__((aligned(16))) float S2[64][68];
   __shared__ __attribute__((aligned(16))) float S3[64][68];
   __shared__ __attribute__((aligned(16))) float S4[64][68];
+  __shared__ float bsh[64];
   const int NT = T / PC;
   const int c = blockIdx.x, bhq = blockIdx.y;
   const int G_ = HQ / H;
   const int b = bhq / HQ, hq = bhq - b * HQ, h = hq / G_, bh = b * H + h;
   const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
-  const int r0 = (tid >> 4) * 4, c0 = (tid & 15) * 4;
   const int t0 = c * PC;
-  float bt4[4];
+  const f32x16 z = zero16();
 
+  // The fp32 inputs go to registers first (16 values per thread each) so their
+  // latency overlaps the WY recomputation; each is stored to LDS when its buffer frees.
+  f32x4 pw2[4], pdh[4], pdq[4], pdk[4], pda[4];
+  wy_fetch(pw2, ws.w2 + ((int64_t)bh * T + t0) * 64);
+  wy_fetch(pdh, bw.dhc + ((int64_t)bhq * NT + c) * 4096);
+  wy_fetch(pdq, bw.dqt + ((int64_t)bhq * T + t0) * 64);
+  wy_fetch(pdk, bw.dkt + ((int64_t)bhq * T + t0) * 64);
+  wy_fetch(pda, bw.dad + ((int64_t)bhq * NT + c) * 4096);
   load_rows64_f32(W, w + b * wst.b + h * wst.h + (int64_t)t0 * wst.t, wst.t);
   load_rows64_f32(Q, q + b * qs.b + hq * qs.h + (int64_t)t0 * qs.t, qs.t);
   load_rows64_f32(K, k + b * ks.b + h * ks.h + (int64_t)t0 * ks.t, ks.t);
@@ -829,195 +874,105 @@ __global__ __launch_bounds__(256) void path_wy_bwd_kernel(const bf16* __restrict
   {
     const int r = tid >> 2, cc = (tid & 3) * 16;
     const float bt = (float)beta[b * bst.b + h * bst.h + (int64_t)(t0 + r) * bst.t];
+    if ((tid & 3) == 0) bsh[r] = bt;
 #pragma unroll
     for (int e = 0; e < 16; ++e) Wb[r][cc + e] = bt * W[r][cc + e];
   }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) bt4[i] = (float)beta[b * bst.b + h * bst.h + (int64_t)(t0 + r0 + i) * bst.t];
+  wy_put(S1, pw2);  // W2
+  wy_put(S2, pdh);  // dHc
   __syncthreads();
-  float t4[4][4];
-  zero44(t4);
-  lds_gemm64<false, true>(Wb, W, t4);
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) Tm[r0 + i][c0 + j] = (c0 + j < r0 + i) ? t4[i][j] : 0.f;
+  wy_store(Tm, mgemm64<false, true>(Wb, W, z), 2);
   __syncthreads();
+  // Wave 0 inverts Tm while the others start on the products that do not need it.
   if (wv == 0) invert_unit_lower64(Tm, lane);
-  load_mat64<false>(S1, ws.w2 + ((int64_t)bh * T + t0) * 64);          // W2
-  load_mat64<false>(S2, bw.dhc + ((int64_t)bhq * NT + c) * 4096);      // dHc
+  f32x16 aW = wy_neg(mgemm64<false, true>(S1, S2, z));   // -W2 dHc^T
+  f32x16 aW2 = wy_neg(mgemm64<false, false>(W, S2, z));  // -W dHc
+  wy_store(S3, mgemm64<false, true>(Q, W, z), 1);        // QW
   __syncthreads();
-  float aW[4][4], aW2[4][4], aq[4][4], ak[4][4], aWb[4][4], dQW[4][4], dTW[4][4], dTm[4][4];
-  zero44(aW);
-  zero44(aW2);
-  zero44(aWb);
-  zero44(dQW);
-  zero44(dTW);
-  zero44(dTm);
-  lds_gemm64<false, true>(S1, S2, aW);   // W2 dHc^T
-  lds_gemm64<false, false>(W, S2, aW2);  // W dHc
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      aW[i][j] = -aW[i][j];
-      aW2[i][j] = -aW2[i][j];
+  wy_put(S2, pdq);  // d q~
+  __syncthreads();
+  f32x16 aq = wy_load(S2);
+  f32x16 dQW = wy_neg(mgemm64<false, true>(S2, S1, z));  // -dq~ W2^T
+  {
+    const f32x16 t = mgemm64<true, false>(S3, S2, z);    // QW^T dq~
+    WY_FOR_E aW2[e] -= t[e];
+  }
+  wy_store(S4, mgemm64<false, true>(Wb, K, z), 2);       // WBK
+  __syncthreads();
+  wy_store(S1, mgemm64<false, false>(Tm, S4, z), 0);     // TW
+  wy_put(S2, pdk);                                       // d k~
+  __syncthreads();
+  f32x16 ak = wy_load(S2);
+  f32x16 dTW = wy_neg(mgemm64<false, true>(W, S2, z));   // -W dk~^T
+  {
+    const f32x16 t = mgemm64<false, false>(S1, S2, z);   // TW dk~
+    WY_FOR_E aW[e] -= t[e];
+  }
+  __syncthreads();
+  wy_put(S2, pda);  // dA_diag
+  __syncthreads();
+  aq = mgemm64<false, false>(S2, K, aq);  // dq += dA K
+  ak = mgemm64<true, false>(S2, Q, ak);   // dk += dA^T Q
+  {
+    const f32x16 t = mgemm64<false, true>(S2, S1, z);   // dA TW^T
+    const f32x16 t5 = mgemm64<true, false>(S3, S2, z);  // QW^T dA
+    WY_FOR_E {
+      dQW[e] -= t[e];
+      dTW[e] -= t5[e];
     }
-  zero44(t4);
-  lds_gemm64<false, true>(Q, W, t4);  // QW
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) S3[r0 + i][c0 + j] = (c0 + j <= r0 + i) ? t4[i][j] : 0.f;
+  }
   __syncthreads();
-  load_mat64<false>(S2, bw.dqt + ((int64_t)bhq * T + t0) * 64);  // d q~
+  wy_store(S2, dQW, 1);
+  wy_store(S1, dTW, 0);
   __syncthreads();
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) aq[i][j] = S2[r0 + i][c0 + j];
-  lds_gemm64<false, true>(S2, S1, dQW);  // dq~ W2^T   (negated below)
-  zero44(t4);
-  lds_gemm64<true, false>(S3, S2, t4);   // QW^T dq~
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      dQW[i][j] = -dQW[i][j];
-      aW2[i][j] -= t4[i][j];
-    }
-  zero44(t4);
-  lds_gemm64<false, true>(Wb, K, t4);    // WBK
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) S4[r0 + i][c0 + j] = (c0 + j < r0 + i) ? t4[i][j] : 0.f;
+  aq = mgemm64<false, false>(S2, W, aq);         // dq += tril(dQW) W
+  aW = mgemm64<true, false>(S2, Q, aW);          // dW += tril(dQW)^T q
+  f32x16 dTm = mgemm64<false, true>(S1, S4, z);  // dTm = dTW WBK^T
+  wy_store(S3, mgemm64<true, false>(Tm, S1, z), 2);  // dWBK = stril(Tm^T dTW)
   __syncthreads();
-  zero44(t4);
-  lds_gemm64<false, false>(Tm, S4, t4);  // TW
+  f32x16 aWb = mgemm64<false, false>(S3, K, z);  // dWb = dWBK k
+  ak = mgemm64<true, false>(S3, Wb, ak);         // dk += dWBK^T Wb
+  wy_store(S2, aW2, 0);                          // dW2
   __syncthreads();
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) S1[r0 + i][c0 + j] = t4[i][j];
-  load_mat64<false>(S2, bw.dkt + ((int64_t)bhq * T + t0) * 64);  // d k~
+  dTm = mgemm64<false, true>(S2, Wb, dTm);  // dTm += dW2 Wb^T
+  aWb = mgemm64<true, false>(Tm, S2, aWb);  // dWb += Tm^T dW2
+  wy_store(S1, dTm, 0);
   __syncthreads();
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) ak[i][j] = S2[r0 + i][c0 + j];
-  lds_gemm64<false, true>(W, S2, dTW);   // W dk~^T (negated below)
-  zero44(t4);
-  lds_gemm64<false, false>(S1, S2, t4);  // TW dk~
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      dTW[i][j] = -dTW[i][j];
-      aW[i][j] -= t4[i][j];
-    }
+  wy_store(S3, mgemm64<true, false>(Tm, S1, z), 0);  // Tm^T dTm
   __syncthreads();
-  load_mat64<false>(S2, bw.dad + ((int64_t)bhq * NT + c) * 4096);  // dA_diag
+  wy_store(S4, wy_neg(mgemm64<false, true>(S3, Tm, z)), 2);  // da = -stril((Tm^T dTm) Tm^T)
   __syncthreads();
-  lds_gemm64<false, false>(S2, K, aq);   // dq += dA K
-  lds_gemm64<true, false>(S2, Q, ak);    // dk += dA^T Q
-  zero44(t4);
-  lds_gemm64<false, true>(S2, S1, t4);   // dA TW^T
-  float t5[4][4];
-  zero44(t5);
-  lds_gemm64<true, false>(S3, S2, t5);   // QW^T dA
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      dQW[i][j] -= t4[i][j];
-      dTW[i][j] -= t5[i][j];
-    }
-  __syncthreads();
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) S2[r0 + i][c0 + j] = (c0 + j <= r0 + i) ? dQW[i][j] : 0.f;
-  __syncthreads();
-  lds_gemm64<false, false>(S2, W, aq);   // dq += tril(dQW) W
-  lds_gemm64<true, false>(S2, Q, aW);    // dW += tril(dQW)^T q
-  __syncthreads();
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) S2[r0 + i][c0 + j] = dTW[i][j];
-  __syncthreads();
-  lds_gemm64<false, true>(S2, S4, dTm);  // dTm = dTW WBK^T
-  zero44(t4);
-  lds_gemm64<true, false>(Tm, S2, t4);   // Tm^T dTW
-  __syncthreads();
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) S3[r0 + i][c0 + j] = (c0 + j < r0 + i) ? t4[i][j] : 0.f;  // dWBK
-  __syncthreads();
-  lds_gemm64<false, false>(S3, K, aWb);  // dWb = dWBK k
-  lds_gemm64<true, false>(S3, Wb, ak);   // dk += dWBK^T Wb
-  __syncthreads();
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) S1[r0 + i][c0 + j] = aW2[i][j];  // dW2
-  __syncthreads();
-  lds_gemm64<false, true>(S1, Wb, dTm);  // dTm += dW2 Wb^T
-  lds_gemm64<true, false>(Tm, S1, aWb);  // dWb += Tm^T dW2
-  __syncthreads();
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) S2[r0 + i][c0 + j] = dTm[i][j];
-  __syncthreads();
-  zero44(t4);
-  lds_gemm64<true, false>(Tm, S2, t4);   // Tm^T dTm
-  __syncthreads();
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) S3[r0 + i][c0 + j] = t4[i][j];
-  __syncthreads();
-  zero44(t4);
-  lds_gemm64<false, true>(S3, Tm, t4);   // (Tm^T dTm) Tm^T
-  __syncthreads();
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) S4[r0 + i][c0 + j] = (c0 + j < r0 + i) ? -t4[i][j] : 0.f;  // da
-  __syncthreads();
-  lds_gemm64<false, false>(S4, W, aWb);  // dWb += da W
-  lds_gemm64<true, false>(S4, Wb, aW);   // dW += da^T Wb
-  float dbp[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    dbp[i] = 0.f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      aW[i][j] += bt4[i] * aWb[i][j];
-      dbp[i] += aWb[i][j] * W[r0 + i][c0 + j];
-    }
-#pragma unroll
-    for (int m = 1; m < 16; m <<= 1) dbp[i] += __shfl_xor(dbp[i], m, 64);
+  aWb = mgemm64<false, false>(S4, W, aWb);  // dWb += da W
+  aW = mgemm64<true, false>(S4, Wb, aW);    // dW += da^T Wb
+  // dW += beta dWb; dbeta_r = sum_c dWb[r][c] W[r][c] (row sums through S2)
+  const int cl = dl_col();
+  WY_FOR_E {
+    const int r = dl_row(e);
+    aW[e] += bsh[r] * aWb[e];
+    S2[r][cl] = aWb[e] * W[r][cl];
   }
   const int64_t rowbase = ((int64_t)bhq * T + t0) * 64;
+  WY_FOR_E {
+    const int64_t off = rowbase + dl_row(e) * 64 + cl;
+    bw.dq[off] = aq[e];
+    bw.dk[off] = ak[e];
+    bw.dw[off] = aW[e];
+  }
+  __syncthreads();
+  {
+    const int r = tid >> 2, cc = (tid & 3) * 16;
+    float s = 0.f;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    f32x4 vq, vk, vw;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      vq[j] = aq[i][j];
-      vk[j] = ak[i][j];
-      vw[j] = aW[i][j];
+    for (int i = 0; i < 16; i += 4) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(&S2[r][cc + i]);
+      s += (v[0] + v[1]) + (v[2] + v[3]);
     }
-    *reinterpret_cast<f32x4*>(bw.dq + rowbase + (r0 + i) * 64 + c0) = vq;
-    *reinterpret_cast<f32x4*>(bw.dk + rowbase + (r0 + i) * 64 + c0) = vk;
-    *reinterpret_cast<f32x4*>(bw.dw + rowbase + (r0 + i) * 64 + c0) = vw;
-    if ((tid & 15) == 0) bw.db[(int64_t)bhq * T + t0 + r0 + i] = dbp[i];
+    s += __shfl_xor(s, 1, 64);
+    s += __shfl_xor(s, 2, 64);
+    if ((tid & 3) == 0) bw.db[(int64_t)bhq * T + t0 + r] = s;
   }
 }
+#undef WY_FOR_E
 
 // ---------------------------------------------------------------------------
 // GQA sums over the query heads of each kv head (parallel.py:165-171) and casts

@@ -124,4 +124,68 @@ __device__ __forceinline__ f32x16 mat_xM_tile(const float (*X)[68], const float 
   return o;
 }
 
+// ---------------------------------------------------------------------------
+// 64x64 fp32 LDS matrix products on the matrix cores.  Wave w owns the 32x32 output
+// tile (tm = w >> 1, tn = w & 1) in MFMA D layout: element e of lane l is
+// C[32 tm + drow(e, l / 32)][32 tn + l % 32] (dl_row / dl_col below).
+// acc += opA(A) opB(B) with a 3-term bf16 split (hi.hi + hi.lo + lo.hi, ~fp32
+// accuracy); operands are read along k as 16-byte vectors where the layout allows
+// (A not transposed, B transposed) and gathered otherwise.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int dl_row(int e) {
+  return 32 * ((int)threadIdx.x >> 7) + drow(e, ((int)threadIdx.x >> 5) & 1);
+}
+__device__ __forceinline__ int dl_col() { return 32 * (((int)threadIdx.x >> 6) & 1) + ((int)threadIdx.x & 31); }
+
+__device__ __forceinline__ void split_vals(const float v[8], bf16x8& hi, bf16x8& lo) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const bf16 h = (bf16)v[e];
+    hi[e] = h;
+    lo[e] = (bf16)(v[e] - (float)h);
+  }
+}
+
+template <bool TA, bool TB>
+__device__ __forceinline__ f32x16 mgemm64(const float (*A)[68], const float (*B)[68], f32x16 acc) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 5, l32 = lane & 31;
+  const int m = 32 * (w >> 1) + l32, n = 32 * (w & 1) + l32;
+#pragma unroll
+  for (int st = 0; st < 4; ++st) {
+    const int k0 = 16 * st + 8 * g;
+    float a[8], b[8];
+    if (TA) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) a[i] = A[k0 + i][m];
+    } else {
+      const f32x4 x = *reinterpret_cast<const f32x4*>(&A[m][k0]);
+      const f32x4 y = *reinterpret_cast<const f32x4*>(&A[m][k0 + 4]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        a[i] = x[i];
+        a[4 + i] = y[i];
+      }
+    }
+    if (TB) {
+      const f32x4 x = *reinterpret_cast<const f32x4*>(&B[n][k0]);
+      const f32x4 y = *reinterpret_cast<const f32x4*>(&B[n][k0 + 4]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        b[i] = x[i];
+        b[4 + i] = y[i];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) b[i] = B[k0 + i][n];
+    }
+    bf16x8 ah, al, bh, bl;
+    split_vals(a, ah, al);
+    split_vals(b, bh, bl);
+    acc = mfma32(ah, bh, acc);
+    acc = mfma32(ah, bl, acc);
+    acc = mfma32(al, bh, acc);
+  }
+  return acc;
+}
+
 }  // namespace lucid
