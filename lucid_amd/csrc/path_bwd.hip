@@ -802,40 +802,6 @@ __global__ __launch_bounds__(256) void path_products_bwd_kernel(int HQ, int H, i
 // (rows dl_row(e), column dl_col()).  Operands live in 9 fp32 LDS buffers.
 // grid (NT, B*HQ)
 // ---------------------------------------------------------------------------
-// D-layout tile element helpers: S[row][col] <- x (masked), x <- S[row][col]
-#define WY_FOR_E _Pragma("unroll") for (int e = 0; e < 16; ++e)
-__device__ __forceinline__ void wy_store(float (*S)[68], const f32x16& x, int mode) {
-  // mode 0: all, 1: col <= row (tril), 2: col < row (strictly lower)
-  const int cl = dl_col();
-  WY_FOR_E {
-    const int r = dl_row(e);
-    const bool keep = mode == 0 || (mode == 1 ? cl <= r : cl < r);
-    S[r][cl] = keep ? x[e] : 0.f;
-  }
-}
-__device__ __forceinline__ f32x16 wy_load(const float (*S)[68]) {
-  const int cl = dl_col();
-  f32x16 x;
-  WY_FOR_E x[e] = S[dl_row(e)][cl];
-  return x;
-}
-// 64x64 fp32 row-major matrix: thread t holds rows (t + 256 i) / 16, 4 columns each
-__device__ __forceinline__ void wy_fetch(f32x4 v[4], const float* __restrict__ src) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) v[i] = *reinterpret_cast<const f32x4*>(src + 4 * (threadIdx.x + 256 * i));
-}
-__device__ __forceinline__ void wy_put(float (*S)[68], const f32x4 v[4]) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int f = 4 * (threadIdx.x + 256 * i);
-    *reinterpret_cast<f32x4*>(&S[f >> 6][f & 63]) = v[i];
-  }
-}
-__device__ __forceinline__ f32x16 wy_neg(f32x16 x) {
-  WY_FOR_E x[e] = -x[e];
-  return x;
-}
-
 __global__ __launch_bounds__(256) void path_wy_bwd_kernel(const bf16* __restrict__ q, Strides qs,
                                                           const bf16* __restrict__ k, Strides ks,
                                                           const bf16* __restrict__ w, Strides wst,
@@ -855,18 +821,18 @@ __global__ __launch_bounds__(256) void path_wy_bwd_kernel(const bf16* __restrict
   const int c = blockIdx.x, bhq = blockIdx.y;
   const int G_ = HQ / H;
   const int b = bhq / HQ, hq = bhq - b * HQ, h = hq / G_, bh = b * H + h;
-  const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x;
   const int t0 = c * PC;
   const f32x16 z = zero16();
 
   // The fp32 inputs go to registers first (16 values per thread each) so their
   // latency overlaps the WY recomputation; each is stored to LDS when its buffer frees.
   f32x4 pw2[4], pdh[4], pdq[4], pdk[4], pda[4];
-  wy_fetch(pw2, ws.w2 + ((int64_t)bh * T + t0) * 64);
-  wy_fetch(pdh, bw.dhc + ((int64_t)bhq * NT + c) * 4096);
-  wy_fetch(pdq, bw.dqt + ((int64_t)bhq * T + t0) * 64);
-  wy_fetch(pdk, bw.dkt + ((int64_t)bhq * T + t0) * 64);
-  wy_fetch(pda, bw.dad + ((int64_t)bhq * NT + c) * 4096);
+  mat_fetch(pw2, ws.w2 + ((int64_t)bh * T + t0) * 64);
+  mat_fetch(pdh, bw.dhc + ((int64_t)bhq * NT + c) * 4096);
+  mat_fetch(pdq, bw.dqt + ((int64_t)bhq * T + t0) * 64);
+  mat_fetch(pdk, bw.dkt + ((int64_t)bhq * T + t0) * 64);
+  mat_fetch(pda, bw.dad + ((int64_t)bhq * NT + c) * 4096);
   load_rows64_f32(W, w + b * wst.b + h * wst.h + (int64_t)t0 * wst.t, wst.t);
   load_rows64_f32(Q, q + b * qs.b + hq * qs.h + (int64_t)t0 * qs.t, qs.t);
   load_rows64_f32(K, k + b * ks.b + h * ks.h + (int64_t)t0 * ks.t, ks.t);
@@ -878,81 +844,80 @@ __global__ __launch_bounds__(256) void path_wy_bwd_kernel(const bf16* __restrict
 #pragma unroll
     for (int e = 0; e < 16; ++e) Wb[r][cc + e] = bt * W[r][cc + e];
   }
-  wy_put(S1, pw2);  // W2
-  wy_put(S2, pdh);  // dHc
+  mat_put(S1, pw2);  // W2
+  mat_put(S2, pdh);  // dHc
   __syncthreads();
-  wy_store(Tm, mgemm64<false, true>(Wb, W, z), 2);
+  dl_store(Tm, mgemm64<false, true>(Wb, W, z), 2);
   __syncthreads();
-  // Wave 0 inverts Tm while the others start on the products that do not need it.
-  if (wv == 0) invert_unit_lower64(Tm, lane);
-  f32x16 aW = wy_neg(mgemm64<false, true>(S1, S2, z));   // -W2 dHc^T
-  f32x16 aW2 = wy_neg(mgemm64<false, false>(W, S2, z));  // -W dHc
-  wy_store(S3, mgemm64<false, true>(Q, W, z), 1);        // QW
+  invert_unit_lower64(Tm);
+  f32x16 aW = dl_neg(mgemm64<false, true>(S1, S2, z));   // -W2 dHc^T
+  f32x16 aW2 = dl_neg(mgemm64<false, false>(W, S2, z));  // -W dHc
+  dl_store(S3, mgemm64<false, true>(Q, W, z), 1);        // QW
   __syncthreads();
-  wy_put(S2, pdq);  // d q~
+  mat_put(S2, pdq);  // d q~
   __syncthreads();
-  f32x16 aq = wy_load(S2);
-  f32x16 dQW = wy_neg(mgemm64<false, true>(S2, S1, z));  // -dq~ W2^T
+  f32x16 aq = dl_load(S2);
+  f32x16 dQW = dl_neg(mgemm64<false, true>(S2, S1, z));  // -dq~ W2^T
   {
     const f32x16 t = mgemm64<true, false>(S3, S2, z);    // QW^T dq~
-    WY_FOR_E aW2[e] -= t[e];
+    DL_FOR_E aW2[e] -= t[e];
   }
-  wy_store(S4, mgemm64<false, true>(Wb, K, z), 2);       // WBK
+  dl_store(S4, mgemm64<false, true>(Wb, K, z), 2);       // WBK
   __syncthreads();
-  wy_store(S1, mgemm64<false, false>(Tm, S4, z), 0);     // TW
-  wy_put(S2, pdk);                                       // d k~
+  dl_store(S1, mgemm64<false, false>(Tm, S4, z), 0);     // TW
+  mat_put(S2, pdk);                                       // d k~
   __syncthreads();
-  f32x16 ak = wy_load(S2);
-  f32x16 dTW = wy_neg(mgemm64<false, true>(W, S2, z));   // -W dk~^T
+  f32x16 ak = dl_load(S2);
+  f32x16 dTW = dl_neg(mgemm64<false, true>(W, S2, z));   // -W dk~^T
   {
     const f32x16 t = mgemm64<false, false>(S1, S2, z);   // TW dk~
-    WY_FOR_E aW[e] -= t[e];
+    DL_FOR_E aW[e] -= t[e];
   }
   __syncthreads();
-  wy_put(S2, pda);  // dA_diag
+  mat_put(S2, pda);  // dA_diag
   __syncthreads();
   aq = mgemm64<false, false>(S2, K, aq);  // dq += dA K
   ak = mgemm64<true, false>(S2, Q, ak);   // dk += dA^T Q
   {
     const f32x16 t = mgemm64<false, true>(S2, S1, z);   // dA TW^T
     const f32x16 t5 = mgemm64<true, false>(S3, S2, z);  // QW^T dA
-    WY_FOR_E {
+    DL_FOR_E {
       dQW[e] -= t[e];
       dTW[e] -= t5[e];
     }
   }
   __syncthreads();
-  wy_store(S2, dQW, 1);
-  wy_store(S1, dTW, 0);
+  dl_store(S2, dQW, 1);
+  dl_store(S1, dTW, 0);
   __syncthreads();
   aq = mgemm64<false, false>(S2, W, aq);         // dq += tril(dQW) W
   aW = mgemm64<true, false>(S2, Q, aW);          // dW += tril(dQW)^T q
   f32x16 dTm = mgemm64<false, true>(S1, S4, z);  // dTm = dTW WBK^T
-  wy_store(S3, mgemm64<true, false>(Tm, S1, z), 2);  // dWBK = stril(Tm^T dTW)
+  dl_store(S3, mgemm64<true, false>(Tm, S1, z), 2);  // dWBK = stril(Tm^T dTW)
   __syncthreads();
   f32x16 aWb = mgemm64<false, false>(S3, K, z);  // dWb = dWBK k
   ak = mgemm64<true, false>(S3, Wb, ak);         // dk += dWBK^T Wb
-  wy_store(S2, aW2, 0);                          // dW2
+  dl_store(S2, aW2, 0);                          // dW2
   __syncthreads();
   dTm = mgemm64<false, true>(S2, Wb, dTm);  // dTm += dW2 Wb^T
   aWb = mgemm64<true, false>(Tm, S2, aWb);  // dWb += Tm^T dW2
-  wy_store(S1, dTm, 0);
+  dl_store(S1, dTm, 0);
   __syncthreads();
-  wy_store(S3, mgemm64<true, false>(Tm, S1, z), 0);  // Tm^T dTm
+  dl_store(S3, mgemm64<true, false>(Tm, S1, z), 0);  // Tm^T dTm
   __syncthreads();
-  wy_store(S4, wy_neg(mgemm64<false, true>(S3, Tm, z)), 2);  // da = -stril((Tm^T dTm) Tm^T)
+  dl_store(S4, dl_neg(mgemm64<false, true>(S3, Tm, z)), 2);  // da = -stril((Tm^T dTm) Tm^T)
   __syncthreads();
   aWb = mgemm64<false, false>(S4, W, aWb);  // dWb += da W
   aW = mgemm64<true, false>(S4, Wb, aW);    // dW += da^T Wb
   // dW += beta dWb; dbeta_r = sum_c dWb[r][c] W[r][c] (row sums through S2)
   const int cl = dl_col();
-  WY_FOR_E {
+  DL_FOR_E {
     const int r = dl_row(e);
     aW[e] += bsh[r] * aWb[e];
     S2[r][cl] = aWb[e] * W[r][cl];
   }
   const int64_t rowbase = ((int64_t)bhq * T + t0) * 64;
-  WY_FOR_E {
+  DL_FOR_E {
     const int64_t off = rowbase + dl_row(e) * 64 + cl;
     bw.dq[off] = aq[e];
     bw.dk[off] = ak[e];
@@ -972,7 +937,6 @@ __global__ __launch_bounds__(256) void path_wy_bwd_kernel(const bf16* __restrict
     if ((tid & 3) == 0) bw.db[(int64_t)bhq * T + t0 + r] = s;
   }
 }
-#undef WY_FOR_E
 
 // ---------------------------------------------------------------------------
 // GQA sums over the query heads of each kv head (parallel.py:165-171) and casts

@@ -56,29 +56,80 @@ __device__ __forceinline__ void zero44(float acc[4][4]) {
     for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
 }
 
-// (I + M)^-1 in place for the strictly lower part of a 64x64 fp32 LDS matrix (the
-// diagonal and upper part of M are ignored).  Called by ONE wave: lane c solves
-// column c by forward substitution x_r = delta_rc - sum_{k<r} M_rk x_k, each sum
-// split over four independent accumulators to shorten the dependent chain.
-__device__ __forceinline__ void invert_unit_lower64(float (*M)[68], int c) {
-  float x[64];
+// One merge of two inverted s x s diagonal blocks A = [a, a+s), B = [a+s, a+2s) of a
+// unit lower matrix (I + N): X_BA = -X_B (N_BA X_A), computed in place in the N_BA block
+// in two products; each thread owns 4 consecutive columns of one row of a pair.
+template <int S>
+__device__ __forceinline__ void merge_lower_blocks(float (*M)[68]) {
+  constexpr int QPP = S * S / 4;         // column quads per pair
+  constexpr int NQ = (64 / (2 * S)) * QPP;  // quads of all pairs
+  const int qd = threadIdx.x;
+  const bool act = qd < NQ;
+  const int p = qd / QPP, rem = qd - p * QPP;
+  const int i = rem / (S / 4), j0 = 4 * (rem - i * (S / 4));
+  const int ao = 2 * p * S, bo = ao + S;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  if (act) {  // Y = N_BA X_A
 #pragma unroll
-  for (int r = 0; r < 64; ++r) {
-    float a0 = (r == c) ? 1.f : 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+    for (int kk = 0; kk < S; ++kk) {
+      const float a = M[bo + i][ao + kk];
+      const f32x4 x = *reinterpret_cast<const f32x4*>(&M[ao + kk][ao + j0]);
 #pragma unroll
-    for (int kk = 0; kk < (r & ~3); kk += 4) {
-      const f32x4 p = *reinterpret_cast<const f32x4*>(&M[r][kk]);
-      a0 = fmaf(-p[0], x[kk], a0);
-      a1 = fmaf(-p[1], x[kk + 1], a1);
-      a2 = fmaf(-p[2], x[kk + 2], a2);
-      a3 = fmaf(-p[3], x[kk + 3], a3);
+      for (int e = 0; e < 4; ++e) acc[e] = fmaf(a, x[e], acc[e]);
     }
-#pragma unroll
-    for (int kk = (r & ~3); kk < r; ++kk) a0 = fmaf(-M[r][kk], x[kk], a0);
-    x[r] = (a0 + a1) + (a2 + a3);
   }
+  __syncthreads();
+  if (act) *reinterpret_cast<f32x4*>(&M[bo + i][ao + j0]) = acc;
+  __syncthreads();
+  if (act) {  // X_BA = -X_B Y
+    acc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int r = 0; r < 64; ++r) M[r][c] = x[r];
+    for (int kk = 0; kk < S; ++kk) {
+      const float a = M[bo + i][bo + kk];
+      const f32x4 y = *reinterpret_cast<const f32x4*>(&M[bo + kk][ao + j0]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[e] = fmaf(a, y[e], acc[e]);
+    }
+  }
+  __syncthreads();
+  if (act) *reinterpret_cast<f32x4*>(&M[bo + i][ao + j0]) = -acc;
+  __syncthreads();
+}
+
+// (I + M)^-1 in place for a strictly lower 64x64 fp32 LDS matrix M (its diagonal and
+// strictly upper part must hold zeros; the result has a unit diagonal and zeros above).
+// Called by all 256 threads of the block; the caller syncs before, the function syncs
+// before returning.  Wave w inverts the 16x16 diagonal block w by forward substitution
+// (lane c < 16 solves column c: x_r = delta_rc - sum_{k<r} M_rk x_k); the blocks are
+// then merged 16 -> 32 -> 64 through X_BA = -X_B N_BA X_A.  A 64-deep solve in one
+// wave has four times the dependent work and leaves three waves idle.
+__device__ __forceinline__ void invert_unit_lower64(float (*M)[68]) {
+  const int w = threadIdx.x >> 6, c = threadIdx.x & 63;
+  if (c < 16) {
+    const int o = 16 * w;
+    float x[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      float a0 = (r == c) ? 1.f : 0.f, a1 = 0.f;
+#pragma unroll
+      for (int kk = 0; kk < (r & ~3); kk += 4) {
+        const f32x4 m4 = *reinterpret_cast<const f32x4*>(&M[o + r][o + kk]);
+        a0 = fmaf(-m4[0], x[kk], a0);
+        a1 = fmaf(-m4[1], x[kk + 1], a1);
+        a0 = fmaf(-m4[2], x[kk + 2], a0);
+        a1 = fmaf(-m4[3], x[kk + 3], a1);
+      }
+#pragma unroll
+      for (int kk = (r & ~3); kk < r; ++kk) a0 = fmaf(-M[o + r][o + kk], x[kk], a0);
+      x[r] = a0 + a1;
+    }
+    // only this wave reads its diagonal block, so it may write it back right away
+#pragma unroll
+    for (int r = 0; r < 16; ++r) M[o + r][o + c] = x[r];
+  }
+  __syncthreads();
+  merge_lower_blocks<16>(M);
+  merge_lower_blocks<32>(M);
 }
 
 // Load a 64x64 block of bf16 rows (row stride st elements) into an fp32 LDS matrix.
@@ -187,5 +238,40 @@ __device__ __forceinline__ f32x16 mgemm64(const float (*A)[68], const float (*B)
   }
   return acc;
 }
+
+// D-layout tile helpers for mgemm64 results: S[row][col] <- x (masked), x <- S[row][col]
+#define DL_FOR_E _Pragma("unroll") for (int e = 0; e < 16; ++e)
+__device__ __forceinline__ void dl_store(float (*S)[68], const f32x16& x, int mode) {
+  // mode 0: all, 1: col <= row (tril), 2: col < row (strictly lower)
+  const int cl = dl_col();
+  DL_FOR_E {
+    const int r = dl_row(e);
+    const bool keep = mode == 0 || (mode == 1 ? cl <= r : cl < r);
+    S[r][cl] = keep ? x[e] : 0.f;
+  }
+}
+__device__ __forceinline__ f32x16 dl_load(const float (*S)[68]) {
+  const int cl = dl_col();
+  f32x16 x;
+  DL_FOR_E x[e] = S[dl_row(e)][cl];
+  return x;
+}
+// 64x64 fp32 row-major matrix: thread t holds rows (t + 256 i) / 16, 4 columns each
+__device__ __forceinline__ void mat_fetch(f32x4 v[4], const float* __restrict__ src) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = *reinterpret_cast<const f32x4*>(src + 4 * (threadIdx.x + 256 * i));
+}
+__device__ __forceinline__ void mat_put(float (*S)[68], const f32x4 v[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int f = 4 * (threadIdx.x + 256 * i);
+    *reinterpret_cast<f32x4*>(&S[f >> 6][f & 63]) = v[i];
+  }
+}
+__device__ __forceinline__ f32x16 dl_neg(f32x16 x) {
+  DL_FOR_E x[e] = -x[e];
+  return x;
+}
+
 
 }  // namespace lucid

@@ -59,9 +59,10 @@ __global__ __launch_bounds__(256) void path_chunk_kernel(const bf16* __restrict_
   const int b = bhq / HQ, hq = bhq - b * HQ, h = hq / G;
   const int bh = b * H + h;
   const bool kvw = (hq % G) == 0;
-  const int tid = threadIdx.x, w_ = tid >> 6, lane = tid & 63;
-  const int r0 = (tid >> 4) * 4, c0 = (tid & 15) * 4;
+  const int tid = threadIdx.x;
   const int t0 = c * PC;
+  const f32x16 z = zero16();
+  const int cl = dl_col();
   if (c == 0 && tid == 0) ws.counters[bhq] = 0;
 
   load_rows64_f32(Wm, w + b * wst.b + h * wst.h + (int64_t)t0 * wst.t, wst.t);
@@ -75,140 +76,87 @@ __global__ __launch_bounds__(256) void path_chunk_kernel(const bf16* __restrict_
     for (int e = 0; e < 16; ++e) Wb[r][cc + e] = bt * Wm[r][cc + e];
   }
   __syncthreads();
-  float acc[4][4];
+  // Products on the matrix cores (mgemm64); each wave keeps its 32x32 tile in D layout.
   // a = stril(beta W W^T) -> Tm, then T_inv = (I + a)^-1 in place
-  zero44(acc);
-  lds_gemm64<false, true>(Wb, Wm, acc);
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) Tm[r0 + i][c0 + j] = (c0 + j < r0 + i) ? acc[i][j] : 0.f;
+  dl_store(Tm, mgemm64<false, true>(Wb, Wm, z), 2);
   __syncthreads();
-  if (w_ == 0) invert_unit_lower64(Tm, lane);
-  __syncthreads();
+  invert_unit_lower64(Tm);
   // W2 = T_inv (beta W)
-  zero44(acc);
-  lds_gemm64<false, false>(Tm, Wb, acc);
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) W2s[r0 + i][c0 + j] = acc[i][j];
-  if (kvw) {
-    float* dst = ws.w2 + ((int64_t)bh * T + t0) * 64;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      f32x4 v;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) v[j] = acc[i][j];
-      *reinterpret_cast<f32x4*>(dst + (r0 + i) * 64 + c0) = v;
+  {
+    const f32x16 acc = mgemm64<false, false>(Tm, Wb, z);
+    dl_store(W2s, acc, 0);
+    if (kvw) {
+      float* dst = ws.w2 + ((int64_t)bh * T + t0) * 64;
+      DL_FOR_E dst[dl_row(e) * 64 + cl] = acc[e];
     }
   }
   __syncthreads();
   // Hc = I - W^T W2
   if (kvw) {
-    zero44(acc);
-    lds_gemm64<true, false>(Wm, W2s, acc);
+    const f32x16 acc = mgemm64<true, false>(Wm, W2s, z);
     float* dst = ws.hc + ((int64_t)bh * NT + c) * 4096;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      f32x4 v;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) v[j] = ((r0 + i) == (c0 + j) ? 1.f : 0.f) - acc[i][j];
-      *reinterpret_cast<f32x4*>(dst + (r0 + i) * 64 + c0) = v;
+    DL_FOR_E {
+      const int r = dl_row(e);
+      dst[r * 64 + cl] = (r == cl ? 1.f : 0.f) - acc[e];
     }
   }
   // WBK = stril(beta W K^T) -> X
-  zero44(acc);
-  lds_gemm64<false, true>(Wb, Ks, acc);
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) X[r0 + i][c0 + j] = (c0 + j < r0 + i) ? acc[i][j] : 0.f;
+  dl_store(X, mgemm64<false, true>(Wb, Ks, z), 2);
   __syncthreads();
-  // TW = T_inv WBK -> Wb (beta W is no longer needed)
-  zero44(acc);
-  lds_gemm64<false, false>(Tm, X, acc);
-  __syncthreads();
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) Wb[r0 + i][c0 + j] = acc[i][j];
+  // TW = T_inv WBK -> Wb (every read of beta W came before the last barrier)
+  dl_store(Wb, mgemm64<false, false>(Tm, X, z), 0);
   __syncthreads();
   // k~ = K - TW^T W
   if (kvw) {
-    zero44(acc);
-    lds_gemm64<true, false>(Wb, Wm, acc);
+    const f32x16 acc = mgemm64<true, false>(Wb, Wm, z);
     bf16* dst = ws.kt + ((int64_t)bh * T + t0) * 64;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      bf16x4 v;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) v[j] = (bf16)(Ks[r0 + i][c0 + j] - acc[i][j]);
-      *reinterpret_cast<bf16x4*>(dst + (r0 + i) * 64 + c0) = v;
+    DL_FOR_E {
+      const int r = dl_row(e);
+      dst[r * 64 + cl] = (bf16)(Ks[r][cl] - acc[e]);
     }
   }
-  // QW = tril(Q W^T) -> X
-  zero44(acc);
-  lds_gemm64<false, true>(Qs, Wm, acc);
-  __syncthreads();
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) X[r0 + i][c0 + j] = (c0 + j <= r0 + i) ? acc[i][j] : 0.f;
+  // QW = tril(Q W^T) -> X (every read of WBK came before the last barrier)
+  dl_store(X, mgemm64<false, true>(Qs, Wm, z), 1);
   __syncthreads();
   // q~ = Q - QW W2
-  zero44(acc);
-  lds_gemm64<false, false>(X, W2s, acc);
   {
+    const f32x16 acc = mgemm64<false, false>(X, W2s, z);
     float* dst = ws.qt + ((int64_t)bhq * T + t0) * 64;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      f32x4 v;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) v[j] = Qs[r0 + i][c0 + j] - acc[i][j];
-      *reinterpret_cast<f32x4*>(dst + (r0 + i) * 64 + c0) = v;
+    DL_FOR_E {
+      const int r = dl_row(e);
+      dst[r * 64 + cl] = Qs[r][cl] - acc[e];
     }
   }
   // A_diag = tril(Q K^T - QW TW); L_diag = stril(exp(s A - 1/s)) -> W2s, global
   // (PaTH softmax: the logits themselves, diagonal included; no inverse)
-  float acc2[4][4];
-  zero44(acc);
-  zero44(acc2);
-  lds_gemm64<false, true>(Qs, Ks, acc);
-  lds_gemm64<false, false>(X, Wb, acc2);
-  __syncthreads();
+  const f32x16 qk = mgemm64<false, true>(Qs, Ks, z);
+  const f32x16 qt = mgemm64<false, false>(X, Wb, z);
+  float* dst = ws.ld + ((int64_t)bhq * NT + c) * 4096;
   if (softmax) {
-    float* dst = ws.ld + ((int64_t)bhq * NT + c) * 4096;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      f32x4 v;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) v[j] = (c0 + j <= r0 + i) ? acc[i][j] - acc2[i][j] : 0.f;
-      *reinterpret_cast<f32x4*>(dst + (r0 + i) * 64 + c0) = v;
+    DL_FOR_E {
+      const int r = dl_row(e);
+      dst[r * 64 + cl] = cl <= r ? qk[e] - qt[e] : 0.f;
     }
     return;
   }
+  __syncthreads();  // the q~ product above still reads W2s
   {
     const float sl2 = scale * LOG2E_F, cc0 = LOG2E_F / scale;
-    float* dst = ws.ld + ((int64_t)bhq * NT + c) * 4096;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      f32x4 v;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float a = acc[i][j] - acc2[i][j];
-        v[j] = (c0 + j < r0 + i) ? __builtin_amdgcn_exp2f(fmaf(a, sl2, -cc0)) : 0.f;
-        W2s[r0 + i][c0 + j] = v[j];
-      }
-      *reinterpret_cast<f32x4*>(dst + (r0 + i) * 64 + c0) = v;
+    DL_FOR_E {
+      const int r = dl_row(e);
+      const float v = cl < r ? __builtin_amdgcn_exp2f(fmaf(qk[e] - qt[e], sl2, -cc0)) : 0.f;
+      W2s[r][cl] = v;
+      dst[r * 64 + cl] = v;
     }
   }
   __syncthreads();
-  if (w_ == 0) invert_unit_lower64(W2s, lane);
-  __syncthreads();
+  invert_unit_lower64(W2s);
   {
-    float* dst = ws.y + ((int64_t)bhq * NT + c) * 4096;
-    for (int idx = tid; idx < 4096; idx += 256) dst[idx] = W2s[idx >> 6][idx & 63];
+    float* dy = ws.y + ((int64_t)bhq * NT + c) * 4096;
+    for (int i = 0; i < 4; ++i) {
+      const int f = 4 * (tid + 256 * i);
+      *reinterpret_cast<f32x4*>(dy + f) = *reinterpret_cast<const f32x4*>(&W2s[f >> 6][f & 63]);
+    }
   }
 }
 
