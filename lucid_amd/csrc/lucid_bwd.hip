@@ -874,7 +874,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
             dotp += x * kk;
           }
         }
-      dotp += wave_xor32(dotp);
+      dotp = wave_sum32(dotp);
       const float f = dotp / (float)D;
       bf16* op = dk_out + b * dks.b + h * dks.h + (int64_t)irow * dks.t;
 #pragma unroll

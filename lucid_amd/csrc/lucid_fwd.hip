@@ -511,7 +511,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_fw
         for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
           for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[mt][nt][e]);
-        mx = fmaxf(mx, wave_xor32(mx)) * c;
+        mx = wave_max32(mx) * c;
         if (__builtin_amdgcn_ballot_w64(mx > m[nt] + 8.0f)) {
           const float mnew = fmaxf(m[nt], mx);
           const float alpha = __builtin_amdgcn_exp2f(m[nt] - mnew);
@@ -552,7 +552,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_fw
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
     const int irow = row0 + nt * 32 + l32;
-    const float ls = lsum[nt] + wave_xor32(lsum[nt]);
+    const float ls = wave_sum32(lsum[nt]);
     if (irow < T) {
       const float inv = 1.0f / ls;
       bf16* op = o + b * os.b + hq * os.h + (int64_t)irow * os.t;

@@ -60,9 +60,19 @@ __device__ __forceinline__ bf16x8 pack_b(const f32x16& x, int h) {
   return r;
 }
 
-__device__ __forceinline__ float wave_xor32(float v) {
-  // exchange with lane ^ 32
-  return __shfl_xor(v, 32, 64);
+// Reductions of a value over lane pairs (l, l ^ 32), the two halves of a D-layout row.
+// v_permlane32_swap exchanges the lane halves in the VALU (no LDS round trip): of the
+// two results, one holds this lane's value and the other its partner's, so the
+// symmetric reduction of the pair is the same on both lanes.
+__device__ __forceinline__ float wave_max32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, v), __builtin_bit_cast(unsigned, v),
+                                                  false, false);
+  return fmaxf(__builtin_bit_cast(float, (unsigned)r[0]), __builtin_bit_cast(float, (unsigned)r[1]));
+}
+__device__ __forceinline__ float wave_sum32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, v), __builtin_bit_cast(unsigned, v),
+                                                  false, false);
+  return __builtin_bit_cast(float, (unsigned)r[0]) + __builtin_bit_cast(float, (unsigned)r[1]);
 }
 
 // Chain progress counters.  A producer writes a finished block, makes it

@@ -509,7 +509,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
     for (int jh = 0; jh < 2; ++jh)
 #pragma unroll
       for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sc[jh][e]);
-    m = fmaxf(mx, wave_xor32(mx));  // finite: the diagonal key is always present
+    m = wave_max32(mx);  // finite: the diagonal key is always present
 #pragma unroll
     for (int jh = 0; jh < 2; ++jh)
 #pragma unroll
@@ -554,7 +554,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
       for (int jh = 0; jh < 2; ++jh)
 #pragma unroll
         for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sc[jh][e]);
-      mx = fmaxf(mx, wave_xor32(mx));
+      mx = wave_max32(mx);
       const float mn = fmaxf(m, mx * sl2);
       const float alpha = __builtin_amdgcn_exp2f(m - mn);
       m = mn;
@@ -582,7 +582,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
     __syncthreads();
   }
   if (live) {
-    l += wave_xor32(l);
+    l = wave_sum32(l);
     const float inv = 1.f / l;
     const int i = iw0 + l32;
     bf16* orow = o + b * os.b + hq * os.h + (int64_t)i * os.t;
