@@ -212,12 +212,13 @@ __global__ __launch_bounds__(256) void path_large_kernel(int T, PathFwdWs ws) {
 
 // ---------------------------------------------------------------------------
 // Query transport (transform_q.py:15-61): x = q~_I; QS slots for chunks of I's large
-// chunk below I, then QB for every earlier large chunk.  grid (NT, B*HQ)
+// chunk below I, then QB for every earlier large chunk.  grid (B*HQ, NT): the work of a
+// chunk grows with I, so the late chunks of every head are dispatched first.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void path_transport_kernel(int HQ, int H, int T, PathFwdWs ws) {
   __shared__ __attribute__((aligned(16))) float X[64][68];
   __shared__ __attribute__((aligned(16))) float MT[64][68];
-  const int I = blockIdx.x, bhq = blockIdx.y;
+  const int I = (int)gridDim.y - 1 - (int)blockIdx.y, bhq = blockIdx.x;
   const int NT = T / PC, NS = (NT + PR - 1) / PR;
   const int G = HQ / H;
   const int b = bhq / HQ, hq = bhq - b * HQ, bh = b * H + hq / G;
