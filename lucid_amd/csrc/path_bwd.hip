@@ -241,7 +241,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
 // lane <-> row i) and all 64 keys of every key tile; key-operand and O rows are
 // staged by direct global->LDS loads (double buffered), Kop^T comes through
 // transposing LDS reads.  The pair's dM contributions are summed over its 128 rows
-// before the atomic adds.  grid (ceil(NT/2), B*HQ)
+// before the atomic adds.  grid (B*HQ, ceil(NT/2)), late (long) pairs first
 // The dA rule is the template argument: LUCID-Path (SM = false) dA = -s (X_I Y_J^T) L
 // with X = dV, Y = O (rows of the same query head); PaTH softmax (SM = true)
 // dA = s P (X_I Y_J^T - delta_i), P = exp2(s' S - lse_i), X = dO, Y = V (kv head).
@@ -258,7 +258,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
     float scale, PathFwdWs ws, PathBwdWs bw) {
   __shared__ __attribute__((aligned(16))) RowSmem sm;
   const int NT = T / PC, NS = (NT + PR - 1) / PR;
-  const int I1 = 2 * blockIdx.x, bhq = blockIdx.y;
+  const int I1 = 2 * ((int)gridDim.y - 1 - (int)blockIdx.y), bhq = blockIdx.x;  // heaviest pairs of all heads first
   const int G_ = HQ / H;
   const int b = bhq / HQ, hq = bhq - b * HQ, bh = b * H + hq / G_;
   const bf16* yh = ysrc + b * ys.b + (SM ? hq / G_ : hq) * ys.h;
@@ -418,7 +418,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
 // Query tiles (the shared QB^(s) rows for later large chunks, or QS^(J1), QS^(J2)
 // rows inside the large chunk) and dV rows are staged by direct global->LDS loads
 // (three buffers, two tiles ahead); Qop^T comes through transposing LDS reads.
-// Then d k~_J = dk~(same) + dKL SUF_J and dSUF_J = dKL^T k~_J.  grid (ceil(NT/2), B*HQ)
+// Then d k~_J = dk~(same) + dKL SUF_J and dSUF_J = dKL^T k~_J.  grid (B*HQ, ceil(NT/2)),
+// early (long) pairs first
 // Template argument SM as in the row sweep; in PaTH softmax mode the rows' lse and
 // delta are staged beside each query tile, and dV_J^T[d][j] += dO_I^T[d][i] P[i][j]
 // is accumulated too and added to the diagonal block's part in dvf.
@@ -447,7 +448,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
     float scale, PathFwdWs ws, PathBwdWs bw) {
   __shared__ __attribute__((aligned(16))) ColSmem<SM> sm;
   const int NT = T / PC, NS = (NT + PR - 1) / PR;
-  const int J1 = 2 * blockIdx.x, bhq = blockIdx.y;
+  const int J1 = 2 * blockIdx.y, bhq = blockIdx.x;  // heaviest (earliest) key pairs of all heads first
   const int G_ = HQ / H;
   const int b = bhq / HQ, hq = bhq - b * HQ, bh = b * H + hq / G_;
   const bf16* xh = xsrc + b * xs.b + hq * xs.h;

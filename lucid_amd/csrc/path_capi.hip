@@ -241,9 +241,9 @@ int lucid_path_bwd(const void* dout, const int64_t* do_strides, const void* q, c
   LUCID_TIMED_LAUNCH(phip, "path_bwd_zero_kernel", lucid::path_bwd_zero_kernel, dim3(1024), st, n_hl, n_hc, BHq, bw);
   LUCID_TIMED_LAUNCH(phip, "path_dv_kernel", lucid::path_dv_kernel, dim3(NT * BHq), st, (const bf16*)dout, PS(do_strides),
                      (const bf16*)o, PS(o_strides), HQ, H, T, BHq, scale, ws, bw);
-  LUCID_TIMED_LAUNCH(phip, "path_bwd_row_kernel", lucid::path_bwd_row_kernel<false>, dim3((NT + 1) / 2, BHq), st,
+  LUCID_TIMED_LAUNCH(phip, "path_bwd_row_kernel", lucid::path_bwd_row_kernel<false>, dim3(BHq, (NT + 1) / 2), st,
                      (const bf16*)bw.dvb, dvs, (const bf16*)o, PS(o_strides), HQ, H, T, scale, ws, bw);
-  LUCID_TIMED_LAUNCH(phip, "path_bwd_col_kernel", lucid::path_bwd_col_kernel<false>, dim3((NT + 1) / 2, BHq), st,
+  LUCID_TIMED_LAUNCH(phip, "path_bwd_col_kernel", lucid::path_bwd_col_kernel<false>, dim3(BHq, (NT + 1) / 2), st,
                      (const bf16*)bw.dvb, dvs, (const bf16*)o, PS(o_strides), HQ, H, T, scale, ws, bw);
   return launch_back(q, q_strides, k, k_strides, w, w_strides, beta, beta_strides, dq, dq_strides, dk, dk_strides, dv,
                      dv_strides, dw, dw_strides, dbeta, dbeta_strides, B, T, H, HQ, ws, bw, st);
@@ -278,7 +278,7 @@ int lucid_path_softmax_fwd(const void* q, const int64_t* q_strides, const void* 
   const int NT = T / 64;
   if (int rc = launch_front(q, q_strides, k, k_strides, w, w_strides, beta, beta_strides, B, T, H, HQ, scale, 1, ws, st))
     return rc;
-  LUCID_TIMED_LAUNCH(phip, "path_softmax_fwd_kernel", lucid::path_softmax_fwd_kernel, dim3((NT + 1) / 2, B * HQ), st,
+  LUCID_TIMED_LAUNCH(phip, "path_softmax_fwd_kernel", lucid::path_softmax_fwd_kernel, dim3(B * HQ, (NT + 1) / 2), st,
                      (const bf16*)v, PS(v_strides), (bf16*)o, PS(o_strides), HQ, H, T, scale, ws);
   if (kcache)
     if (int rc = launch_kcache(kcache, kcache_strides, B, T, H, ws, st)) return rc;
@@ -328,9 +328,9 @@ int lucid_path_softmax_bwd(const void* dout, const int64_t* do_strides, const vo
   LUCID_TIMED_LAUNCH(phip, "path_softmax_diag_bwd_kernel", lucid::path_softmax_diag_bwd_kernel, dim3(NT, BHq), st,
                      (const bf16*)dout, PS(do_strides), (const bf16*)o, PS(o_strides), (const bf16*)v, PS(v_strides),
                      HQ, H, T, scale, ws, bw);
-  LUCID_TIMED_LAUNCH(phip, "path_softmax_bwd_row_kernel", lucid::path_bwd_row_kernel<true>, dim3((NT + 1) / 2, BHq), st,
+  LUCID_TIMED_LAUNCH(phip, "path_softmax_bwd_row_kernel", lucid::path_bwd_row_kernel<true>, dim3(BHq, (NT + 1) / 2), st,
                      (const bf16*)dout, PS(do_strides), (const bf16*)v, PS(v_strides), HQ, H, T, scale, ws, bw);
-  LUCID_TIMED_LAUNCH(phip, "path_softmax_bwd_col_kernel", lucid::path_bwd_col_kernel<true>, dim3((NT + 1) / 2, BHq), st,
+  LUCID_TIMED_LAUNCH(phip, "path_softmax_bwd_col_kernel", lucid::path_bwd_col_kernel<true>, dim3(BHq, (NT + 1) / 2), st,
                      (const bf16*)dout, PS(do_strides), (const bf16*)v, PS(v_strides), HQ, H, T, scale, ws, bw);
   return launch_back(q, q_strides, k, k_strides, w, w_strides, beta, beta_strides, dq, dq_strides, dk, dk_strides, dv,
                      dv_strides, dw, dw_strides, dbeta, dbeta_strides, B, T, H, HQ, ws, bw, st);

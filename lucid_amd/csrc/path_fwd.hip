@@ -450,7 +450,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
 // J < Iw give S^T[j][i] = Kop_J . Qop_I^(J).  O^T[d][i] += V^T[d][j] P^T[j][i] with V^T
 // from transposing LDS reads.  Key-operand and V rows are staged by direct
 // global->LDS loads (double buffered).  The row log-sum-exp (exp2 domain) is kept
-// for the backward.  grid ((NT+1)/2, B*HQ), pairs with the most key chunks first.
+// for the backward.  grid (B*HQ, (NT+1)/2), the pairs with the most key chunks (of all heads) first.
 // ---------------------------------------------------------------------------
 struct SoftmaxFwdSmem {
   bf16 k[2][64 * 64];   // swizzled (chunk c of row r at c ^ (r & 7))
@@ -463,7 +463,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
     PathFwdWs ws) {
   __shared__ __attribute__((aligned(16))) SoftmaxFwdSmem sm;
   const int NT = T / PC, NS = (NT + PR - 1) / PR, NP = (NT + 1) / 2;
-  const int I1 = 2 * (NP - 1 - (int)blockIdx.x), bhq = blockIdx.y;
+  const int I1 = 2 * (NP - 1 - (int)blockIdx.y), bhq = blockIdx.x;  // heaviest pairs of all heads first
   const int G_ = HQ / H;
   const int b = bhq / HQ, hq = bhq - b * HQ, h = hq / G_, bh = b * H + h;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
