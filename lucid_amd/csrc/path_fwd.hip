@@ -287,14 +287,28 @@ __global__ __launch_bounds__(256) void path_transport_kernel(int HQ, int H, int 
 // jh = w >> 1 -> keys 32*jh of every staged 64-key tile.
 //   S^T[j][i] = Kop_J . Qop_I, P = exp(s S - 1/s), acc^T[d][i] += O^T[d][j] P^T[j][i]
 //   O_I = Y_I (V_I - acc)   (3-term bf16 split)
+// The key chunks are swept in pairs (J = 2pp, 2pp + 1; both in one large chunk), one
+// barrier per pair, the next pair staged by direct global->LDS loads while this one
+// is processed.  The fp32 buffers of the final step (R^T, Y) reuse the staging space.
 // ---------------------------------------------------------------------------
+struct SolveFwdSmem {
+  union {
+    struct {
+      bf16 k[2][2][64 * 64];  // [buffer][tile of the pair], swizzled (chunk c of row r at c ^ (r & 7))
+      bf16 o[2][2][64 * 64];
+    } st;
+    struct {
+      float Ys[64][68];
+      float Rt[64][68];
+      bf16 ot[64 * 64];  // O^T of the chunk, T-perm within 16-groups
+    } fin;
+  } u;
+};
+
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void path_solve_fwd_kernel(const bf16* __restrict__ v, Strides vs,
                                                              bf16* __restrict__ o, Strides os, int HQ, int H,
                                                              int T, int BHq, float scale, PathFwdWs ws) {
-  __shared__ __attribute__((aligned(16))) float Ys[64][68];
-  __shared__ __attribute__((aligned(16))) float Rt[64][68];
-  __shared__ __attribute__((aligned(16))) bf16 lk[2][64 * 64];  // swizzled (chunk c of row r at c ^ (r & 7))
-  __shared__ __attribute__((aligned(16))) bf16 lo[2][64 * 64];
+  __shared__ __attribute__((aligned(16))) SolveFwdSmem sm;
   const int NT = T / PC, NS = (NT + PR - 1) / PR;
   const int id = blockIdx.x;
   const int I = id / BHq, bhq = id - (id / BHq) * BHq;
@@ -307,8 +321,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
   int* cnt = ws.counters + bhq;
   const float sl2 = scale * LOG2E_F, cc0 = LOG2E_F / scale;
   const bf16* oTh = ws.oT + (int64_t)bhq * 64 * T;
-
-  load_mat64<false>(Ys, ws.y + ((int64_t)bhq * NT + I) * 4096);
+  const int npair = (I + 1) / 2;
 
   // accumulators: -V^T for the jh = 0 waves (R = V - acc = -(acc_0 + acc_1)), zero for the others
   f32x16 acc[2];
@@ -323,74 +336,112 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
         for (int u = 0; u < 4; ++u) acc[t][4 * qq + u] = jh ? 0.f : -(float)vv[u];
       }
   }
-  bf16x8 qb[4];
-  int qsrc = -1;  // current Qop source: s (QB) or PR*NS + slot (QS)
-  auto load_q = [&](int J) {
-    const int src = (J < cb) ? (J / PR) : (PR * NS + (J - cb));
-    if (src == qsrc) return;
-    qsrc = src;
+  // query operand of key chunk J for this lane's row: QB^(J/PR) below I's large chunk,
+  // QS slot J - cb inside it
+  auto load_q = [&](int J, bf16x8 q[4]) {
     const bf16* base = (J < cb) ? ws.qb + ((int64_t)bhq * NS + J / PR) * T * 64
                                 : ws.qs + ((int64_t)bhq * PR + (J - cb)) * T * 64;
 #pragma unroll
-    for (int st = 0; st < 4; ++st) qb[st] = ld8(base + (int64_t)(i0 + ih * 32 + l32) * 64 + 16 * st + 8 * g);
+    for (int st = 0; st < 4; ++st) q[st] = ld8(base + (int64_t)(i0 + ih * 32 + l32) * 64 + 16 * st + 8 * g);
   };
+  // below I's large chunk the operand changes only every PR key chunks (both chunks of
+  // a pair share it), so it stays in registers; inside it every chunk has its own slot
+  bf16x8 q0[4], q1[4];
+  int qsrc = -1;
   int plan_k[2], plan_t[2];
   dma_plan<64, 8>(64, plan_k);
   dma_plan<64, 8>(T, plan_t);
-  auto stage = [&](int J) {  // direct global->LDS staging of key chunk J into buffer J & 1
-    const int buf = J & 1;
-    dma_stage<64, 8>(plan_k, ((J < cb) ? ws.kl : ws.kt) + ((int64_t)bh * T + J * PC) * 64, lk[buf]);
-    dma_stage<64, 8>(plan_t, oTh + J * PC, lo[buf]);
+  auto stage = [&](int pp) {  // key chunks 2pp (and 2pp + 1 if below I) into buffer pp & 1
+    const int buf = pp & 1;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int J = 2 * pp + u;
+      if (J < I) {
+        dma_stage<64, 8>(plan_k, ((J < cb) ? ws.kl : ws.kt) + ((int64_t)bh * T + J * PC) * 64, sm.u.st.k[buf][u]);
+        dma_stage<64, 8>(plan_t, oTh + J * PC, sm.u.st.o[buf][u]);
+      }
+    }
+  };
+  // pair pp is complete once the counter exceeds its last chunk
+  auto need = [&](int pp) { return min(2 * pp + 1, I - 1); };
+  // Y_I (fp32) is fetched into registers during the last pair
+  f32x4 yr[4];
+  auto yload = [&]() {
+    const float* src = ws.y + ((int64_t)bhq * NT + I) * 4096;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) yr[u] = *reinterpret_cast<const f32x4*>(src + 4 * (tid + 256 * u));
+  };
+  auto tile = [&](int buf, int u, const bf16x8 q[4]) {
+    f32x16 sc = zero16();
+#pragma unroll
+    for (int st = 0; st < 4; ++st) sc = mfma32(ld8(swz<8>(sm.u.st.k[buf][u], jh * 32 + l32, 2 * st + g)), q[st], sc);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) sc[e] = __builtin_amdgcn_exp2f(fmaf(sc[e], sl2, -cc0));
+    const bf16x8 p0 = pack_b(sc, 0), p1 = pack_b(sc, 1);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      acc[t] = mfma32(ld8(swz<8>(sm.u.st.o[buf][u], t * 32 + l32, 4 * jh + g)), p0, acc[t]);
+      acc[t] = mfma32(ld8(swz<8>(sm.u.st.o[buf][u], t * 32 + l32, 4 * jh + 2 + g)), p1, acc[t]);
+    }
   };
   int ready = 0;
-  if (I > 0) {
-    ready = wait_counter_gt(cnt, 0);
+  if (npair > 0) {
+    ready = wait_counter_gt(cnt, need(0));
     stage(0);
     dma_wait();
+  } else {
+    yload();
   }
   __syncthreads();
-  for (int J = 0; J < I; ++J) {
-    const int buf = J & 1;
-    const bool more = J + 1 < I;
+  for (int pp = 0; pp < npair; ++pp) {
+    const int buf = pp & 1;
+    const bool more = pp + 1 < npair;
+    const bool two = 2 * pp + 1 < I;
+    // the query operands are loaded before the next pair's staging so that waiting
+    // for them does not wait for the staging loads
+    const int J0 = 2 * pp;
+    const bool below = J0 < cb;
+    if (!below || J0 / PR != qsrc) {
+      load_q(J0, q0);
+      qsrc = below ? J0 / PR : -1;
+    }
+    if (two && !below) load_q(J0 + 1, q1);
     bool early = false;
     if (more) {
-      if (J + 1 >= ready) {
+      const int nd = need(pp + 1);
+      if (nd >= ready) {
         const int seen = poll_counter(cnt);
-        if (seen > J + 1) {
+        if (seen > nd) {
           chain_acquire();
           ready = seen;
         }
       }
-      early = J + 1 < ready;
-      if (early) stage(J + 1);
+      early = nd < ready;
+      if (early) stage(pp + 1);
+    } else {
+      yload();
     }
-    load_q(J);
-    {
-      f32x16 sc = zero16();
-#pragma unroll
-      for (int st = 0; st < 4; ++st) sc = mfma32(ld8(swz<8>(lk[buf], jh * 32 + l32, 2 * st + g)), qb[st], sc);
-#pragma unroll
-      for (int e = 0; e < 16; ++e) sc[e] = __builtin_amdgcn_exp2f(fmaf(sc[e], sl2, -cc0));
-      const bf16x8 p0 = pack_b(sc, 0), p1 = pack_b(sc, 1);
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        acc[t] = mfma32(ld8(swz<8>(lo[buf], t * 32 + l32, 4 * jh + g)), p0, acc[t]);
-        acc[t] = mfma32(ld8(swz<8>(lo[buf], t * 32 + l32, 4 * jh + 2 + g)), p1, acc[t]);
-      }
-    }
+    tile(buf, 0, q0);
+    if (two) tile(buf, 1, below ? q0 : q1);
     if (more && !early) {
-      ready = wait_counter_gt(cnt, J + 1);
-      stage(J + 1);
+      ready = wait_counter_gt(cnt, need(pp + 1));
+      stage(pp + 1);
     }
     dma_wait();
     __syncthreads();
   }
-  // ---- R = V - acc (reduce key halves) ----
+  // ---- R = V - acc (reduce key halves); the staging space is free from here ----
+  float(*Rt)[68] = sm.u.fin.Rt;
   if (jh == 1) {
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][ih * 32 + l32] = acc[t][e];
+  }
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int f = 4 * (tid + 256 * u);
+    *reinterpret_cast<f32x4*>(&sm.u.fin.Ys[f >> 6][f & 63]) = yr[u];
   }
   __syncthreads();
   if (jh == 0) {
@@ -410,7 +461,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
     for (int st = 0; st < (rh ? 4 : 2); ++st) {
       bf16x8 ah, al, bh8, bl;
       split8(&Rt[dt * 32 + l32][16 * st + 8 * g], ah, al);
-      split8(&Ys[rh * 32 + l32][16 * st + 8 * g], bh8, bl);
+      split8(&sm.u.fin.Ys[rh * 32 + l32][16 * st + 8 * g], bh8, bl);
       oo = mfma32(ah, bh8, oo);
       oo = mfma32(ah, bl, oo);
       oo = mfma32(al, bh8, oo);
@@ -418,7 +469,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
     const int rl = rh * 32 + l32;
     const int lslot = (rl & ~15) | jmap(rl & 15);
     bf16* orow = o + b * os.b + hq * os.h + (int64_t)(i0 + rl) * os.t;
-    bf16* ot = lo[0];  // O^T of the chunk, T-perm within 16-groups (plain [64][64])
+    bf16* ot = sm.u.fin.ot;
 #pragma unroll
     for (int qq = 0; qq < 4; ++qq) {
       const int d0 = dt * 32 + 8 * qq + 4 * g;
@@ -434,7 +485,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
   __syncthreads();
   for (int c = tid; c < 64 * 8; c += 256) {  // O^T to the chain operand with 16-byte stores
     const int dd = c >> 3, s8 = (c & 7) * 8;
-    *reinterpret_cast<bf16x8*>(ws.oT + ((int64_t)bhq * 64 + dd) * T + i0 + s8) = ld8(lo[0] + dd * 64 + s8);
+    *reinterpret_cast<bf16x8*>(ws.oT + ((int64_t)bhq * 64 + dd) * T + i0 + s8) = ld8(sm.u.fin.ot + dd * 64 + s8);
   }
   publish_counter(cnt, I + 1);
 }
