@@ -51,15 +51,29 @@ __global__ __launch_bounds__(256) void path_bwd_zero_kernel(int64_t n_hl, int64_
 // wave w: ch = w & 1 -> columns 32*ch (lane <-> column j), ih = w >> 1 -> rows 32*ih
 // of every staged 64-row tile I > J.
 //   S[I][J] = Qop_I . Kop_J, L = exp(s S - 1/s), acc^T[d][j] += dV^T[d][i] L[i][j]
-// counters[bhq] = number of chunks of dV published from the end.
+// counters[bhq] = number of chunks of dV published from the end.  The row tiles are
+// swept in pairs (I = NT-1-2pp, NT-2-2pp), one barrier and one staging round per pair;
+// the fp32 buffers of the final step reuse the staging space.  Finally
+// dA_diag = -s (dV_J O_J^T) * L_diag on the matrix cores.
 // ---------------------------------------------------------------------------
+struct DvSmem {
+  union {
+    struct {
+      bf16 q[2][2][64 * 64];  // [buffer][tile of the pair], swizzled (chunk c of row r at c ^ (r & 7))
+      bf16 d[2][2][64 * 64];
+    } st;
+    struct {
+      float Yt[64][68];  // Yt[c][r] = Y[r][c], then O rows
+      float Rt[64][68];  // R^T, then dV rows
+      bf16 dt[64 * 64];  // dV^T of the chunk, T-perm within 16-groups
+    } fin;
+  } u;
+};
+
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void path_dv_kernel(const bf16* __restrict__ dout, Strides dos,
                                                       const bf16* __restrict__ o, Strides os, int HQ, int H, int T,
                                                       int BHq, float scale, PathFwdWs ws, PathBwdWs bw) {
-  __shared__ __attribute__((aligned(16))) float Yt[64][68];  // Yt[c][r] = Y[r][c]
-  __shared__ __attribute__((aligned(16))) float Rt[64][68];
-  __shared__ __attribute__((aligned(16))) bf16 lq[2][64 * 64];  // swizzled (chunk c of row r at c ^ (r & 7))
-  __shared__ __attribute__((aligned(16))) bf16 ld_[2][64 * 64];
+  __shared__ __attribute__((aligned(16))) DvSmem sm;
   const int NT = T / PC, NS = (NT + PR - 1) / PR;
   const int id = blockIdx.x;
   const int J = NT - 1 - id / BHq, bhq = id - (id / BHq) * BHq;
@@ -72,7 +86,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
   int* cnt = bw.counters + bhq;
   const float sl2 = scale * LOG2E_F, cc0 = LOG2E_F / scale;
 
-  load_mat64<true>(Yt, ws.y + ((int64_t)bhq * NT + J) * 4096);
   bf16x8 kbs[4], kbf[4];
 #pragma unroll
   for (int st = 0; st < 4; ++st) {
@@ -92,68 +105,98 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
         for (int u = 0; u < 4; ++u) acc[t][4 * qq + u] = ih ? 0.f : -(float)x[u];
       }
   }
+  // row tile k (k = 0 .. n-1) is chunk I = NT-1-k; it is published once the counter exceeds k
+  const int n = NT - 1 - J, npair = (n + 1) / 2;
   int plan_q[2], plan_t[2];
   dma_plan<64, 8>(64, plan_q);
   dma_plan<64, 8>(T, plan_t);
-  const int first = NT - 1;
-  auto stage = [&](int I) {  // direct global->LDS staging of query chunk I into buffer (first - I) & 1
-    const int buf = (first - I) & 1;
-    const bf16* qsrc = (I <= ceJ) ? ws.qs + (((int64_t)bhq * PR + (J - (I / PR) * PR)) * T) * 64
-                                  : ws.qb + (((int64_t)bhq * NS + sJ) * T) * 64;
-    dma_stage<64, 8>(plan_q, qsrc + (int64_t)I * PC * 64, lq[buf]);
-    dma_stage<64, 8>(plan_t, bw.dvT + (int64_t)bhq * 64 * T + I * PC, ld_[buf]);
+  auto stage = [&](int pp) {  // tiles 2pp (and 2pp + 1 if below n) into buffer pp & 1
+    const int buf = pp & 1;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int k = 2 * pp + u;
+      if (k < n) {
+        const int I = NT - 1 - k;
+        const bf16* qsrc = (I <= ceJ) ? ws.qs + (((int64_t)bhq * PR + (J - (I / PR) * PR)) * T) * 64
+                                      : ws.qb + (((int64_t)bhq * NS + sJ) * T) * 64;
+        dma_stage<64, 8>(plan_q, qsrc + (int64_t)I * PC * 64, sm.u.st.q[buf][u]);
+        dma_stage<64, 8>(plan_t, bw.dvT + (int64_t)bhq * 64 * T + I * PC, sm.u.st.d[buf][u]);
+      }
+    }
+  };
+  auto need = [&](int pp) { return min(2 * pp + 1, n - 1); };
+  // Y_J (fp32) is fetched into registers during the last pair
+  f32x4 yr[4];
+  auto yload = [&]() {
+    const float* src = ws.y + ((int64_t)bhq * NT + J) * 4096;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) yr[u] = *reinterpret_cast<const f32x4*>(src + 4 * (tid + 256 * u));
+  };
+  auto tile = [&](int buf, int u, bool same) {
+    f32x16 sc = zero16();
+#pragma unroll
+    for (int st = 0; st < 4; ++st)
+      sc = mfma32(ld8(swz<8>(sm.u.st.q[buf][u], ih * 32 + l32, 2 * st + g)), same ? kbs[st] : kbf[st], sc);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) sc[e] = __builtin_amdgcn_exp2f(fmaf(sc[e], sl2, -cc0));
+    const bf16x8 p0 = pack_b(sc, 0), p1 = pack_b(sc, 1);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      acc[t] = mfma32(ld8(swz<8>(sm.u.st.d[buf][u], t * 32 + l32, 4 * ih + g)), p0, acc[t]);
+      acc[t] = mfma32(ld8(swz<8>(sm.u.st.d[buf][u], t * 32 + l32, 4 * ih + 2 + g)), p1, acc[t]);
+    }
   };
   int ready = 0;
-  if (first > J) {
-    ready = wait_counter_gt(cnt, 0);
-    stage(first);
+  if (npair > 0) {
+    ready = wait_counter_gt(cnt, need(0));
+    stage(0);
     dma_wait();
+  } else {
+    yload();
   }
   __syncthreads();
-  for (int I = first; I > J; --I) {
-    const int buf = (first - I) & 1;
-    const bool more = I - 1 > J;
+  for (int pp = 0; pp < npair; ++pp) {
+    const int buf = pp & 1;
+    const bool more = pp + 1 < npair;
+    const bool two = 2 * pp + 1 < n;
     bool early = false;
     if (more) {
-      const int need = NT - I;  // chunk I-1 is published once the counter exceeds NT-1-(I-1)
-      if (need >= ready) {
+      const int nd = need(pp + 1);
+      if (nd >= ready) {
         const int seen = poll_counter(cnt);
-        if (seen > need) {
+        if (seen > nd) {
           chain_acquire();
           ready = seen;
         }
       }
-      early = need < ready;
-      if (early) stage(I - 1);
+      early = nd < ready;
+      if (early) stage(pp + 1);
+    } else {
+      yload();
     }
-    {
-      const bool same = (I <= ceJ);
-      f32x16 sc = zero16();
-#pragma unroll
-      for (int st = 0; st < 4; ++st)
-        sc = mfma32(ld8(swz<8>(lq[buf], ih * 32 + l32, 2 * st + g)), same ? kbs[st] : kbf[st], sc);
-#pragma unroll
-      for (int e = 0; e < 16; ++e) sc[e] = __builtin_amdgcn_exp2f(fmaf(sc[e], sl2, -cc0));
-      const bf16x8 p0 = pack_b(sc, 0), p1 = pack_b(sc, 1);
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        acc[t] = mfma32(ld8(swz<8>(ld_[buf], t * 32 + l32, 4 * ih + g)), p0, acc[t]);
-        acc[t] = mfma32(ld8(swz<8>(ld_[buf], t * 32 + l32, 4 * ih + 2 + g)), p1, acc[t]);
-      }
-    }
+    tile(buf, 0, NT - 1 - 2 * pp <= ceJ);
+    if (two) tile(buf, 1, NT - 2 - 2 * pp <= ceJ);
     if (more && !early) {
-      ready = wait_counter_gt(cnt, NT - I);
-      stage(I - 1);
+      ready = wait_counter_gt(cnt, need(pp + 1));
+      stage(pp + 1);
     }
     dma_wait();
     __syncthreads();
   }
-  // ---- R = dO_J - acc ----
+  // ---- R = dO_J - acc; Y^T to LDS (the staging space is free from here) ----
+  float(*Rt)[68] = sm.u.fin.Rt;
+  float(*Yt)[68] = sm.u.fin.Yt;
   if (ih == 1) {
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][ch * 32 + l32] = acc[t][e];
+  }
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int f = 4 * (tid + 256 * u), r = f >> 6, c4 = f & 63;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) Yt[c4 + e][r] = yr[u][e];
   }
   __syncthreads();
   if (ih == 0) {
@@ -184,7 +227,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
     const int lslot = (cl & ~15) | jmap(cl & 15);
     float* of = bw.dvf + ((int64_t)bhq * T + r) * 64;
     bf16* ob = bw.dvb + ((int64_t)bhq * T + r) * 64;
-    bf16* dt_l = ld_[0];  // dV^T of the chunk, T-perm within 16-groups (plain [64][64])
+    bf16* dt_l = sm.u.fin.dt;
 #pragma unroll
     for (int qq = 0; qq < 4; ++qq) {
       const int d0 = dt * 32 + 8 * qq + 4 * g;
@@ -203,28 +246,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
   __syncthreads();
   for (int c = tid; c < 64 * 8; c += 256) {  // dV^T to the chain operand with 16-byte stores
     const int dd = c >> 3, s8 = (c & 7) * 8;
-    *reinterpret_cast<bf16x8*>(bw.dvT + ((int64_t)bhq * 64 + dd) * T + j0 + s8) = ld8(ld_[0] + dd * 64 + s8);
+    *reinterpret_cast<bf16x8*>(bw.dvT + ((int64_t)bhq * 64 + dd) * T + j0 + s8) = ld8(sm.u.fin.dt + dd * 64 + s8);
   }
   publish_counter(cnt, NT - J);
-  // ---- dA_diag = -s (dV_J O_J^T) * L_diag  (fp32, in LDS) ----
+  // ---- dA_diag = -s (dV_J O_J^T) * L_diag  (every read of Rt / Yt came before the last barrier) ----
 #pragma unroll
   for (int e = 0; e < 16; ++e) Rt[chh * 32 + l32][dt * 32 + drow(e, g)] = dvo[e];  // Rt <- dV rows
   load_rows64_f32(Yt, o + b * os.b + hq * os.h + (int64_t)j0 * os.t, os.t);       // Yt <- O rows
   __syncthreads();
-  float a4[4][4];
-  zero44(a4);
-  lds_gemm64<false, true>(Rt, Yt, a4);
   {
-    const int r0 = (tid >> 4) * 4, c0 = (tid & 15) * 4;
+    const f32x16 a = mgemm64<false, true>(Rt, Yt, zero16());
     const float* ldp = ws.ld + ((int64_t)bhq * NT + J) * 4096;
     float* dst = bw.dad + ((int64_t)bhq * NT + J) * 4096;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const f32x4 lv = *reinterpret_cast<const f32x4*>(ldp + (r0 + i) * 64 + c0);
-      f32x4 v;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) v[j] = -scale * a4[i][j] * lv[j];
-      *reinterpret_cast<f32x4*>(dst + (r0 + i) * 64 + c0) = v;
+    const int cl = dl_col();
+    DL_FOR_E {
+      const int rr = dl_row(e);
+      dst[rr * 64 + cl] = -scale * a[e] * ldp[rr * 64 + cl];
     }
   }
 }
