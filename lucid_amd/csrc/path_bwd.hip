@@ -792,40 +792,36 @@ __global__ __launch_bounds__(256) void path_products_bwd_kernel(int HQ, int H, i
   const int s = blockIdx.x, bhq = blockIdx.y;
   const int G_ = HQ / H;
   const int b = bhq / HQ, hq = bhq - b * HQ, bh = b * H + hq / G_;
-  const int tid = threadIdx.x;
-  const int r0 = (tid >> 4) * 4, c0 = (tid & 15) * 4;
   const int cb = s * PR, ce = min(cb + PR, NT) - 1;
+  const int cl = dl_col();
+  // products on the matrix cores (mgemm64, D layout); SUF_c and Hc_c of the next chunk
+  // are fetched into registers while the current one is processed
+  f32x4 ps[4], ph[4];
+  mat_fetch(ps, ws.suf + ((int64_t)bh * NT + cb) * 4096);
+  mat_fetch(ph, ws.hc + ((int64_t)bh * NT + cb) * 4096);
   load_mat64<false>(F, bw.dhl + ((int64_t)bhq * NS + s) * 4096);
-  float acc[4][4];
   for (int c = cb; c <= ce; ++c) {
-    load_mat64<false>(S, ws.suf + ((int64_t)bh * NT + c) * 4096);
-    load_mat64<false>(Hs, ws.hc + ((int64_t)bh * NT + c) * 4096);
+    mat_put(S, ps);
+    mat_put(Hs, ph);
     __syncthreads();
-    zero44(acc);
-    lds_gemm64<true, false>(S, F, acc);
-    {
-      float* dst = bw.dhc + ((int64_t)bhq * NT + c) * 4096;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        f32x4 v = *reinterpret_cast<f32x4*>(dst + (r0 + i) * 64 + c0);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) v[j] += acc[i][j];
-        *reinterpret_cast<f32x4*>(dst + (r0 + i) * 64 + c0) = v;
-      }
+    if (c < ce) {
+      mat_fetch(ps, ws.suf + ((int64_t)bh * NT + c + 1) * 4096);
+      mat_fetch(ph, ws.hc + ((int64_t)bh * NT + c + 1) * 4096);
     }
-    zero44(acc);
-    lds_gemm64<false, true>(F, Hs, acc);
+    {
+      const f32x16 a = mgemm64<true, false>(S, F, zero16());  // dHc_c += SUF_c^T F
+      float* dst = bw.dhc + ((int64_t)bhq * NT + c) * 4096;
+      DL_FOR_E dst[dl_row(e) * 64 + cl] += a[e];
+    }
+    const f32x16 f = mgemm64<false, true>(F, Hs, zero16());  // F <- F Hc_c^T + dSUF_c
     __syncthreads();
     {
       const float* ds = bw.dsuf + ((int64_t)bhq * NT + c) * 4096;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const f32x4 v = *reinterpret_cast<const f32x4*>(ds + (r0 + i) * 64 + c0);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) F[r0 + i][c0 + j] = acc[i][j] + v[j];
+      DL_FOR_E {
+        const int r = dl_row(e);
+        F[r][cl] = f[e] + ds[r * 64 + cl];
       }
     }
-    __syncthreads();
   }
 }
 

@@ -171,43 +171,53 @@ __global__ __launch_bounds__(256) void path_large_kernel(int T, PathFwdWs ws) {
   const int s = blockIdx.x, bh = blockIdx.y;
   const int NT = T / PC;
   const int tid = threadIdx.x;
-  const int r0 = (tid >> 4) * 4, c0 = (tid & 15) * 4;
   const int cb = s * PR, ce = min(cb + PR, NT) - 1;
+  const int cl = dl_col();
   for (int idx = tid; idx < 4096; idx += 256) Sf[idx >> 6][idx & 63] = ((idx >> 6) == (idx & 63)) ? 1.f : 0.f;
-  float acc[4][4];
+  // products on the matrix cores (mgemm64, D layout); k~_c and Hc_c of the next chunk
+  // are fetched into registers while the current one is processed
+  const int kr = tid >> 2, kc = (tid & 3) * 16;
+  bf16x8 pk[2];
+  f32x4 ph[4];
+  auto fetch = [&](int c) {
+    const bf16* src = ws.kt + ((int64_t)bh * T + c * PC + kr) * 64 + kc;
+    pk[0] = ld8(src);
+    pk[1] = ld8(src + 8);
+    mat_fetch(ph, ws.hc + ((int64_t)bh * NT + c) * 4096);
+  };
+  fetch(ce);
   for (int c = ce; c >= cb; --c) {
-    load_rows64_f32(Kt, ws.kt + ((int64_t)bh * T + c * PC) * 64, 64);
-    load_mat64<false>(Hs, ws.hc + ((int64_t)bh * NT + c) * 4096);
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) Kt[kr][kc + 8 * hh + e] = (float)pk[hh][e];
+    mat_put(Hs, ph);
     __syncthreads();
+    if (c > cb) fetch(c - 1);
     {
       float* dst = ws.suf + ((int64_t)bh * NT + c) * 4096;
-      for (int idx = tid; idx < 4096; idx += 256) dst[idx] = Sf[idx >> 6][idx & 63];
-    }
-    // KL_c = k~_c SUF_c^T
-    zero44(acc);
-    lds_gemm64<false, true>(Kt, Sf, acc);
-    {
-      bf16* dst = ws.kl + ((int64_t)bh * T + c * PC) * 64;
-#pragma unroll
       for (int i = 0; i < 4; ++i) {
-        bf16x4 v;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) v[j] = (bf16)acc[i][j];
-        *reinterpret_cast<bf16x4*>(dst + (r0 + i) * 64 + c0) = v;
+        const int f = 4 * (tid + 256 * i);
+        *reinterpret_cast<f32x4*>(dst + f) = *reinterpret_cast<const f32x4*>(&Sf[f >> 6][f & 63]);
       }
     }
+    // KL_c = k~_c SUF_c^T
+    {
+      const f32x16 a = mgemm64<false, true>(Kt, Sf, zero16());
+      bf16* dst = ws.kl + ((int64_t)bh * T + c * PC) * 64;
+      DL_FOR_E dst[dl_row(e) * 64 + cl] = (bf16)a[e];
+    }
     // SUF_{c-1} = SUF_c Hc_c
-    zero44(acc);
-    lds_gemm64<false, false>(Sf, Hs, acc);
+    const f32x16 sn = mgemm64<false, false>(Sf, Hs, zero16());
     __syncthreads();
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) Sf[r0 + i][c0 + j] = acc[i][j];
-    __syncthreads();
+    dl_store(Sf, sn, 0);
   }
+  __syncthreads();
   float* dst = ws.hl + ((int64_t)bh * ((NT + PR - 1) / PR) + s) * 4096;
-  for (int idx = tid; idx < 4096; idx += 256) dst[idx] = Sf[idx >> 6][idx & 63];
+  for (int i = 0; i < 4; ++i) {
+    const int f = 4 * (tid + 256 * i);
+    *reinterpret_cast<f32x4*>(dst + f) = *reinterpret_cast<const f32x4*>(&Sf[f >> 6][f & 63]);
+  }
 }
 
 // ---------------------------------------------------------------------------
