@@ -480,70 +480,154 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_fw
     const bool more = jt + 1 < ntile;
     if (more) gload((jt + 1) * 64);
     if (jt <= last_w && row0 < T) {
-      const int j0 = jt * 64;
-      f32x16 s[2][2];
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        bf16x8 ka[NKS];
-#pragma unroll
-        for (int st = 0; st < NKS; ++st) ka[st] = ld8(&lk[buf][mt * 32 + l32][16 * st + 8 * g]);
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
-          s[mt][nt] = zero16();
-#pragma unroll
-          for (int st = 0; st < NKS; ++st) s[mt][nt] = mfma32(ka[st], qb[nt][st], s[mt][nt]);
-        }
-      }
-      if (jt == last_w) {
+      if constexpr (D == 64) {
+        // Two 32-row halves (nt) per 64-key tile, staggered so that each half's softmax
+        // VALU work overlaps the other half's MFMA work inside this wave:
+        //   S(nt 0) | max(0) | S(nt 1) + exp(0) | max(1) | PV(nt 0) + exp(1) | PV(nt 1)
+        const bool diag = jt == last_w;
+        bf16x8 ka[2][NKS];
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-          for (int nt = 0; nt < 2; ++nt)
+          for (int st = 0; st < NKS; ++st) ka[mt][st] = ld8(&lk[buf][mt * 32 + l32][16 * st + 8 * g]);
+        f32x16 s[2][2];  // [nt][mt]
+        auto sgemm = [&](int nt) {
 #pragma unroll
-            for (int e = 0; e < 16; ++e)
-              if (mt * 32 + drow(e, g) > nt * 32 + l32) s[mt][nt][e] = -INFINITY;
-      }
-      bf16x8 pb[2][4];
+          for (int mt = 0; mt < 2; ++mt) {
+            s[nt][mt] = zero16();
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        float mx = -INFINITY;
+            for (int st = 0; st < NKS; ++st) s[nt][mt] = mfma32(ka[mt][st], qb[nt][st], s[nt][mt]);
+          }
+        };
+        // causal mask, row max and (lazy) rescale of half nt
+        auto rowmax = [&](int nt) {
+          if (diag) {
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
+            for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-          for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[mt][nt][e]);
-        mx = wave_max32(mx) * c;
-        if (__builtin_amdgcn_ballot_w64(mx > m[nt] + 8.0f)) {
-          const float mnew = fmaxf(m[nt], mx);
-          const float alpha = __builtin_amdgcn_exp2f(m[nt] - mnew);
-          m[nt] = mnew;
-          lsum[nt] *= alpha;
+              for (int e = 0; e < 16; ++e)
+                if (mt * 32 + drow(e, g) > nt * 32 + l32) s[nt][mt][e] = -INFINITY;
+          }
+          float mx = -INFINITY;
+#pragma unroll
+          for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[nt][mt][e]);
+          mx = wave_max32(mx) * c;
+          if (__builtin_amdgcn_ballot_w64(mx > m[nt] + 8.0f)) {
+            const float mnew = fmaxf(m[nt], mx);
+            const float alpha = __builtin_amdgcn_exp2f(m[nt] - mnew);
+            m[nt] = mnew;
+            lsum[nt] *= alpha;
+#pragma unroll
+            for (int t = 0; t < NDT; ++t)
+#pragma unroll
+              for (int e = 0; e < 16; ++e) oacc[t][nt][e] *= alpha;
+          }
+        };
+        bf16x8 pb[2][4];
+        auto softmax = [&](int nt) {
+#pragma unroll
+          for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+              const float p = __builtin_amdgcn_exp2f(fmaf(s[nt][mt][e], c, -m[nt]));
+              lsum[nt] += p;
+              s[nt][mt][e] = p;
+            }
+          pb[nt][0] = pack_b(s[nt][0], 0);
+          pb[nt][1] = pack_b(s[nt][0], 1);
+          pb[nt][2] = pack_b(s[nt][1], 0);
+          pb[nt][3] = pack_b(s[nt][1], 1);
+        };
+        auto pv = [&](int nt) {
 #pragma unroll
           for (int t = 0; t < NDT; ++t)
 #pragma unroll
-            for (int e = 0; e < 16; ++e) oacc[t][nt][e] *= alpha;
+            for (int k4 = 0; k4 < 4; ++k4)
+              oacc[t][nt] = mfma32(ld8(&lv[buf][t * 32 + l32][16 * k4 + 8 * g]), pb[nt][k4], oacc[t][nt]);
+        };
+        sgemm(0);
+        rowmax(0);
+        sgemm(1);
+        softmax(0);
+        // half 0's P must be formed here, beside half 1's S products, and not sunk past
+        // half 1's rescale branch into the block of its only use
+#pragma unroll
+        for (int k4 = 0; k4 < 4; ++k4) {
+          const u32x4 pw = __builtin_bit_cast(u32x4, pb[0][k4]);
+          asm volatile("" ::"v"(pw[0]), "v"(pw[1]), "v"(pw[2]), "v"(pw[3]));
+        }
+        rowmax(1);
+        pv(0);
+        softmax(1);
+        pv(1);
+      } else {  // D = 128: both halves' products first (the staggered order spills here)
+        const int j0 = jt * 64;
+        f32x16 s[2][2];
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+          bf16x8 ka[NKS];
+#pragma unroll
+          for (int st = 0; st < NKS; ++st) ka[st] = ld8(&lk[buf][mt * 32 + l32][16 * st + 8 * g]);
+#pragma unroll
+          for (int nt = 0; nt < 2; ++nt) {
+            s[mt][nt] = zero16();
+#pragma unroll
+            for (int st = 0; st < NKS; ++st) s[mt][nt] = mfma32(ka[st], qb[nt][st], s[mt][nt]);
+          }
+        }
+        if (jt == last_w) {
+#pragma unroll
+          for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+              for (int e = 0; e < 16; ++e)
+                if (mt * 32 + drow(e, g) > nt * 32 + l32) s[mt][nt][e] = -INFINITY;
+        }
+        bf16x8 pb[2][4];
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+          float mx = -INFINITY;
+#pragma unroll
+          for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[mt][nt][e]);
+          mx = wave_max32(mx) * c;
+          if (__builtin_amdgcn_ballot_w64(mx > m[nt] + 8.0f)) {
+            const float mnew = fmaxf(m[nt], mx);
+            const float alpha = __builtin_amdgcn_exp2f(m[nt] - mnew);
+            m[nt] = mnew;
+            lsum[nt] *= alpha;
+#pragma unroll
+            for (int t = 0; t < NDT; ++t)
+#pragma unroll
+              for (int e = 0; e < 16; ++e) oacc[t][nt][e] *= alpha;
+          }
+#pragma unroll
+          for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+              const float p = __builtin_amdgcn_exp2f(fmaf(s[mt][nt][e], c, -m[nt]));
+              lsum[nt] += p;
+              s[mt][nt][e] = p;
+            }
+          pb[nt][0] = pack_b(s[0][nt], 0);
+          pb[nt][1] = pack_b(s[0][nt], 1);
+          pb[nt][2] = pack_b(s[1][nt], 0);
+          pb[nt][3] = pack_b(s[1][nt], 1);
         }
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
+        for (int t = 0; t < NDT; ++t) {
+          bf16x8 va[4];
 #pragma unroll
-          for (int e = 0; e < 16; ++e) {
-            const float p = __builtin_amdgcn_exp2f(fmaf(s[mt][nt][e], c, -m[nt]));
-            lsum[nt] += p;
-            s[mt][nt][e] = p;
-          }
-        pb[nt][0] = pack_b(s[0][nt], 0);
-        pb[nt][1] = pack_b(s[0][nt], 1);
-        pb[nt][2] = pack_b(s[1][nt], 0);
-        pb[nt][3] = pack_b(s[1][nt], 1);
-      }
+          for (int k4 = 0; k4 < 4; ++k4) va[k4] = ld8(&lv[buf][t * 32 + l32][16 * k4 + 8 * g]);
 #pragma unroll
-      for (int t = 0; t < NDT; ++t) {
-        bf16x8 va[4];
+          for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
-        for (int k4 = 0; k4 < 4; ++k4) va[k4] = ld8(&lv[buf][t * 32 + l32][16 * k4 + 8 * g]);
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-          for (int k4 = 0; k4 < 4; ++k4) oacc[t][nt] = mfma32(va[k4], pb[nt][k4], oacc[t][nt]);
+            for (int k4 = 0; k4 < 4; ++k4) oacc[t][nt] = mfma32(va[k4], pb[nt][k4], oacc[t][nt]);
+        }
       }
     }
     if (more) lstore(buf ^ 1);
