@@ -167,10 +167,11 @@ int launch_bwd(const void* dout, const int64_t* dos, const void* q, const int64_
 }
 
 // Decoding: split the cached sequence so that about LUCID_DECODE_WGS workgroups run (at least 64
-// keys per split).  Monotone in Tp, so the workspace sized for the capacity covers
-// every call.
+// keys per split): 768 = one round of the split kernel at three waves per SIMD on 256 CUs
+// (1024 left a second round a third full).  Monotone in Tp, so the workspace sized for the
+// capacity covers every call.
 #ifndef LUCID_DECODE_WGS
-#define LUCID_DECODE_WGS 1024
+#define LUCID_DECODE_WGS 768
 #endif
 int decode_splits(int BH, int Tp) {
   if (Tp <= 0) return 0;
