@@ -166,16 +166,14 @@ int launch_bwd(const void* dout, const int64_t* dos, const void* q, const int64_
   return LUCID_OK;
 }
 
-// Decoding: split the cached sequence so that about LUCID_DECODE_WGS workgroups run (at least 64
-// keys per split): 768 = one round of the split kernel at three waves per SIMD on 256 CUs
-// (1024 left a second round a third full).  Monotone in Tp, so the workspace sized for the
-// capacity covers every call.
-#ifndef LUCID_DECODE_WGS
-#define LUCID_DECODE_WGS 768
-#endif
-int decode_splits(int BH, int Tp) {
+// Decoding: split the cached sequence so that one resident round of split workgroups
+// runs (at least 64 keys per split): the split kernel holds two workgroups per CU at
+// head dim 128 (66 KB of LDS each) and four at 64, on 256 CUs.  Monotone in Tp, so the
+// workspace sized for the capacity covers every call.
+int decode_splits(int BH, int Tp, int D) {
   if (Tp <= 0) return 0;
-  const int want = (LUCID_DECODE_WGS + BH - 1) / BH, most = (Tp + 63) / 64;
+  const int wgs = D == 128 ? 512 : 1024;
+  const int want = (wgs + BH - 1) / BH, most = (Tp + 63) / 64;
   return want < most ? want : most;
 }
 
@@ -203,7 +201,7 @@ int launch_decode(const void* q, const int64_t* qs, const void* k, const int64_t
                   const int64_t* os, float* vp_new, const lucid::DecodePartials& part, int B, int Hkv, int Tp,
                   float scale, float eps, hipStream_t st) {
   const int BH = B * Hkv;
-  const int ns = decode_splits(BH, Tp);
+  const int ns = decode_splits(BH, Tp, D);
   if (ns > 0) {
     const int KS = (Tp + ns - 1) / ns;
     LUCID_LAUNCH("lucid_decode_split_kernel", (lucid::lucid_decode_split_kernel<D, G>), dim3(ns, BH), st,
@@ -237,7 +235,7 @@ extern "C" {
 size_t lucid_decode_workspace_bytes(int B, int Hq, int Hkv, int T_cap, int D) {
   if (B <= 0 || Hkv <= 0 || Hq <= 0 || Hq % Hkv || T_cap < 0) return 0;
   size_t n = 0;
-  carve_decode(nullptr, B * Hkv, Hq / Hkv, decode_splits(B * Hkv, T_cap), D, &n);
+  carve_decode(nullptr, B * Hkv, Hq / Hkv, decode_splits(B * Hkv, T_cap, D), D, &n);
   return n;
 }
 
@@ -259,7 +257,7 @@ int lucid_decode(const void* q, const int64_t* q_strides, const void* k, const i
   if (!vp_new || !ws) return fail("vp_new and ws must be non-null");
   if (int rc = check_ws("ws", ws)) return rc;
   const lucid::DecodePartials part =
-      carve_decode(ws, B * Hkv, Hq / Hkv, decode_splits(B * Hkv, T_past), D, nullptr);
+      carve_decode(ws, B * Hkv, Hq / Hkv, decode_splits(B * Hkv, T_past, D), D, nullptr);
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (D == 64)
     return decode_dispatch_g<64>(Hq / Hkv, q, q_strides, k, k_strides, v, v_strides, k_cache, k_cache_strides,

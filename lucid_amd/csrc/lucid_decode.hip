@@ -8,7 +8,9 @@
 // Both sums read every cached row once (memory bound), so one pass over the cache
 // computes them together, split over the sequence (flash-decoding):
 //   lucid_decode_split_kernel    per (split, kv head): partial sum_j P_tj v'_j and the
-//                                online-softmax state (m, l, O) of every query head
+//                                online-softmax state (m, l, O) of every query head, as
+//                                MFMA tiles (the G query heads and the token's key are
+//                                the columns of one score tile)
 //   lucid_decode_combine_kernel  per (kv head, query head): v'_t, the token's own
 //                                softmax term, the output, and the append of (k_t, v'_t)
 //                                to the cache
@@ -18,13 +20,6 @@ namespace lucid {
 
 constexpr float DEC_NEG = -1e30f;  // finite "minus infinity" for empty softmax states
 
-#ifndef LUCID_DECODE_KB
-#define LUCID_DECODE_KB 4  // keys per lane group and step of the split kernel
-#endif
-#ifndef LUCID_DECODE_EPL
-#define LUCID_DECODE_EPL 8  // elements of a key row per lane (8 or 16)
-#endif
-
 struct DecodePartials {
   float* a;  // [nsplit][BH][D]     sum_j P_tj v'_j
   float* m;  // [nsplit][BH][G]     running max (log2 domain)
@@ -32,170 +27,184 @@ struct DecodePartials {
   float* o;  // [nsplit][BH][G][D]  unnormalised output
 };
 
-// Each key row is read by LPK = D/EPL lanes (EPL elements each); a wave covers 64/LPK
-// keys per step and each group of LPK lanes keeps its own partial state.
+// Split pass on the matrix cores.  Each wave sweeps its own 32-key tiles of the split
+// (tiles w, w+4, ...) and computes, per tile, one MFMA score tile
+//   S^T[j][c] = K_j . X_c,  X_c = q_{hG+c} (c < G),  X_G = k_t,  other columns zero,
+// so the G query heads and the preconditioner row of the new token share one product.
+// Column c < G takes the online softmax p = exp2(s' S - m_c); column G takes
+// p = exp2(s' r_t r_j S - 1/s log2 e), with 1/rms r_j of the cached key from the key
+// registers.  O^T[d][c] += V'^T[d][j] p^T[j][c] (V' rows staged per wave into LDS by
+// direct loads and read transposed) accumulates the G outputs and, in column G, the
+// sum_j P_tj v'_j.  Keys reach registers one tile ahead; no barrier in the sweep.
 template <int D, int G>
-__global__ __launch_bounds__(256) void lucid_decode_split_kernel(
+struct DecodeMfmaSmem {
+  union {
+    bf16 v[4][2][32 * D];  // per wave, double buffered, swizzled (chunk c of row r at c ^ (r & 7))
+    struct {
+      float so[4][G + 1][D];  // per wave: columns 0..G of O^T
+      float m[4][G], l[4][G];
+    } fin;
+  } u;
+  float nn[4][32];  // per wave: squared norms of the tile's keys
+};
+
+template <int D, int G>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void lucid_decode_split_kernel(
     const bf16* __restrict__ q, Strides qs, const bf16* __restrict__ kn, Strides kns,
     const bf16* __restrict__ kc, Strides kcs, const bf16* __restrict__ vc, Strides vcs, int Hkv, int Tp, int KS,
     float scale, float eps, DecodePartials part) {
-  constexpr int EPL = LUCID_DECODE_EPL, NV = EPL / 8;  // 16-byte loads per lane and row
-  constexpr int LPK = D / EPL, NG = 256 / LPK;
-  __shared__ float sa[4][D], so[4][G][D], sm_[4][G], sl[4][G];
+  constexpr int NKS = D / 16, NDT = D / 32, CPR = D / 8, NST = 32 * CPR / 64;  // NST: staging loads per tile
+  static_assert(G + 1 <= 32, "query heads + the preconditioner row must fit one 32-column tile");
+  __shared__ __attribute__((aligned(16))) DecodeMfmaSmem<D, G> sm;
   const int s = blockIdx.x, bh = blockIdx.y, BH = gridDim.y;
   const int b = bh / Hkv, h = bh - b * Hkv;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int sub = lane % LPK, grp = tid / LPK;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
+  const int col = l32;  // score / output column of this lane
   const int j0 = s * KS, j1 = min(Tp, j0 + KS);
 
-  float kt[EPL], qv[G][EPL];
-#pragma unroll
-  for (int c = 0; c < NV; ++c) {
-    const bf16x8 x = ld8(kn + b * kns.b + h * kns.h + EPL * sub + 8 * c);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) kt[8 * c + e] = (float)x[e];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const bf16x8 y = ld8(q + b * qs.b + (h * G + g) * qs.h + EPL * sub + 8 * c);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) qv[g][8 * c + e] = (float)y[e];
-    }
-  }
+  // B operand: column col of X^T (k = d), zero for the padding columns
+  bf16x8 xb[NKS];
   float nt = 0.f;
 #pragma unroll
-  for (int e = 0; e < EPL; ++e) nt = fmaf(kt[e], kt[e], nt);
+  for (int st = 0; st < NKS; ++st) {
+    bf16x8 x;
+    if (col < G) {
+      x = ld8(q + b * qs.b + (h * G + col) * qs.h + 16 * st + 8 * g);
+    } else if (col == G) {
+      x = ld8(kn + b * kns.b + h * kns.h + 16 * st + 8 * g);
 #pragma unroll
-  for (int off = 1; off < LPK; off <<= 1) nt += __shfl_xor(nt, off, 64);
-  const float rt = rsqrtf(nt / D + eps);
-  const float c1 = scale * rt * LOG2E_F, c0 = LOG2E_F / scale, sl2 = scale * LOG2E_F;
+      for (int e = 0; e < 8; ++e) nt = fmaf((float)x[e], (float)x[e], nt);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = (bf16)0.f;
+    }
+    xb[st] = x;
+  }
+  nt = wave_sum32(nt);
+  const float rt = rsqrtf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, nt), G)) / D + eps);
+  const float sl2 = scale * LOG2E_F, c1 = sl2 * rt, c0 = LOG2E_F / scale;
 
-  float acc[EPL], oo[G][EPL], m[G], l[G];
+  f32x16 oacc[NDT];
 #pragma unroll
-  for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
+  for (int t = 0; t < NDT; ++t) oacc[t] = zero16();
+  float m = DEC_NEG, l = 0.f;
+
+  const bf16* kbase = kc + b * kcs.b + h * kcs.h;
+  const bf16* vbase = vc + b * vcs.b + h * vcs.h;
+  const int ntile = (j1 - j0 + 31) / 32;  // 32-key tiles of the split; wave w takes w, w+4, ...
+  bf16x8 kcur[NKS], knx[NKS];  // this tile's and the next tile's key rows
+  auto kload = [&](int t, bf16x8* dst) {  // A operand: key row j (lane row l32), clamped into the split
+    const int jr = min(j0 + 32 * t + l32, j1 - 1);
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    m[g] = DEC_NEG;
-    l[g] = 0.f;
+    for (int st = 0; st < NKS; ++st) dst[st] = ld8(kbase + (int64_t)jr * kcs.t + 16 * st + 8 * g);
+  };
+  auto vstage = [&](int t, bf16* dst) {  // 32 V' rows of tile t into this wave's buffer
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) oo[g][e] = 0.f;
+    for (int i = 0; i < NST; ++i) {
+      const int qq = i * 64 + lane, r = qq / CPR, c = (qq % CPR) ^ (r & 7);
+      const int jr = min(j0 + 32 * t + r, j1 - 1);
+      __builtin_amdgcn_global_load_lds(vbase + (int64_t)jr * vcs.t + c * 8, dst + i * 512, 16, 0, 0);
+    }
+  };
+  int it = 0;
+  if (w < ntile) {
+    kload(w, kcur);
+    vstage(w, sm.u.v[w][0]);
   }
-  const bf16* kbase = kc + b * kcs.b + h * kcs.h + EPL * sub;
-  const bf16* vbase = vc + b * vcs.b + h * vcs.h + EPL * sub;
-  // KB keys per group and step, all loads issued before the arithmetic (HBM latency);
-  // a key past the split's end is loaded clamped and contributes nothing
-  constexpr int KB = LUCID_DECODE_KB;
-  for (int j = j0 + grp; j < j1; j += KB * NG) {
-    bf16x8 kx[KB][NV], vx[KB][NV];
-#pragma unroll
-    for (int u = 0; u < KB; ++u) {
-      const int jj = min(j + u * NG, j1 - 1);
-#pragma unroll
-      for (int c = 0; c < NV; ++c) {
-        kx[u][c] = ld8(kbase + (int64_t)jj * kcs.t + 8 * c);
-        vx[u][c] = ld8(vbase + (int64_t)jj * vcs.t + 8 * c);
-      }
+  for (int t = w; t < ntile; t += 4, ++it) {
+    const int cur = it & 1;
+    const bool more = t + 4 < ntile;
+    if (more) {
+      kload(t + 4, knx);
+      vstage(t + 4, sm.u.v[w][cur ^ 1]);
     }
-    // scores of the KB keys, then one running-max update and rescale per query head
-    float pk[KB], sg[KB][G];
+    const int jb = j0 + 32 * t;
+    // scores and the squared norms of the tile's keys
+    f32x16 sc = zero16();
+    float nn = 0.f;
 #pragma unroll
-    for (int u = 0; u < KB; ++u) {
-      const bool ok = j + u * NG < j1;
-      float kk = 0.f, nn = 0.f, qk[G];
+    for (int st = 0; st < NKS; ++st) {
+      sc = mfma32(kcur[st], xb[st], sc);
 #pragma unroll
-      for (int g = 0; g < G; ++g) qk[g] = 0.f;
+      for (int e = 0; e < 8; ++e) nn = fmaf((float)kcur[st][e], (float)kcur[st][e], nn);
+    }
+    nn = wave_sum32(nn);
+    if (g == 0) sm.nn[w][l32] = nn;
+    float nr[16];
+    lds_rows16(&sm.nn[w][0], g, nr);
+    // online max of the query columns (lazy: rescale only when a row grows by 2^8)
+    float mx = DEC_NEG;
 #pragma unroll
-      for (int e = 0; e < EPL; ++e) {
-        const float x = (float)kx[u][e >> 3][e & 7];
-        kk = fmaf(kt[e], x, kk);
-        nn = fmaf(x, x, nn);
+    for (int e = 0; e < 16; ++e)
+      if (jb + drow(e, g) < j1) mx = fmaxf(mx, sc[e]);
+    mx = (col < G) ? wave_max32(mx) * sl2 : DEC_NEG;
+    if (__builtin_amdgcn_ballot_w64(mx > m + 8.0f)) {
+      const float mnew = fmaxf(m, mx);
+      const float al = __builtin_amdgcn_exp2f(m - mnew);
+      m = mnew;
+      l *= al;
 #pragma unroll
-        for (int g = 0; g < G; ++g) qk[g] = fmaf(qv[g][e], x, qk[g]);
-      }
+      for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-      for (int off = 1; off < LPK; off <<= 1) {
-        kk += __shfl_xor(kk, off, 64);
-        nn += __shfl_xor(nn, off, 64);
-#pragma unroll
-        for (int g = 0; g < G; ++g) qk[g] += __shfl_xor(qk[g], off, 64);
-      }
-      pk[u] = ok ? __builtin_amdgcn_exp2f(fmaf(c1 * rsqrtf(nn / D + eps), kk, -c0)) : 0.f;
-#pragma unroll
-      for (int g = 0; g < G; ++g) sg[u][g] = ok ? qk[g] * sl2 : 3.f * DEC_NEG;  // below any running max
+        for (int e = 0; e < 16; ++e) oacc[dt][e] *= (col < G) ? al : 1.f;
     }
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float mn = m[g];
-#pragma unroll
-      for (int u = 0; u < KB; ++u) mn = fmaxf(mn, sg[u][g]);
-      const float al = __builtin_amdgcn_exp2f(m[g] - mn);
-      m[g] = mn;
-      l[g] *= al;
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) oo[g][e] *= al;
-#pragma unroll
-      for (int u = 0; u < KB; ++u) sg[u][g] = __builtin_amdgcn_exp2f(sg[u][g] - mn);
+    for (int e = 0; e < 16; ++e) {
+      const bool ok = jb + drow(e, g) < j1 && col <= G;
+      const float arg = (col < G) ? fmaf(sc[e], sl2, -m) : fmaf(c1 * rsqrtf(nr[e] / D + eps), sc[e], -c0);
+      const float p = ok ? __builtin_amdgcn_exp2f(arg) : 0.f;
+      if (col < G) l += p;
+      sc[e] = p;
     }
+    const bf16x8 p0 = pack_b(sc, 0), p1 = pack_b(sc, 1);
+    // this tile's V' rows have landed once at most the next tile's loads are in flight
+    if (more)
+      dma_wait_but<NKS + NST>();
+    else
+      dma_wait();
+    const bf16* vt = sm.u.v[w][cur];
 #pragma unroll
-    for (int u = 0; u < KB; ++u) {
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) {
-        const float vv = (float)vx[u][e >> 3][e & 7];
-        acc[e] = fmaf(pk[u], vv, acc[e]);
-#pragma unroll
-        for (int g = 0; g < G; ++g) oo[g][e] = fmaf(sg[u][g], vv, oo[g][e]);
-      }
-#pragma unroll
-      for (int g = 0; g < G; ++g) l[g] += sg[u][g];
+    for (int dt = 0; dt < NDT; ++dt) {
+      oacc[dt] = mfma32(lds_tr_a<CPR>(vt, 0, dt * 32), p0, oacc[dt]);
+      oacc[dt] = mfma32(lds_tr_a<CPR>(vt, 16, dt * 32), p1, oacc[dt]);
     }
-  }
-  // combine the groups of a wave (lanes with the same sub)
+    if (more) {
 #pragma unroll
-  for (int off = LPK; off < 64; off <<= 1) {
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) acc[e] += __shfl_xor(acc[e], off, 64);
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float mp = __shfl_xor(m[g], off, 64), lp = __shfl_xor(l[g], off, 64);
-      const float mn = fmaxf(m[g], mp);
-      const float a0 = __builtin_amdgcn_exp2f(m[g] - mn), a1 = __builtin_amdgcn_exp2f(mp - mn);
-      l[g] = l[g] * a0 + lp * a1;
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) oo[g][e] = oo[g][e] * a0 + __shfl_xor(oo[g][e], off, 64) * a1;
-      m[g] = mn;
+      for (int st = 0; st < NKS; ++st) kcur[st] = knx[st];
     }
   }
-  if (lane < LPK) {
+  l = wave_sum32(l);
+  __syncthreads();  // every wave is done with its staging buffers (aliased below)
+  if (col <= G) {
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) sa[w][EPL * sub + e] = acc[e];
+    for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) so[w][g][EPL * sub + e] = oo[g][e];
-      if (sub == 0) {
-        sm_[w][g] = m[g];
-        sl[w][g] = l[g];
-      }
+      for (int e = 0; e < 16; ++e) sm.u.fin.so[w][col][dt * 32 + drow(e, g)] = oacc[dt][e];
+    if (col < G && g == 0) {
+      sm.u.fin.m[w][col] = m;
+      sm.u.fin.l[w][col] = l;
     }
   }
   __syncthreads();
   // combine the 4 waves: thread d of the first D threads owns column d
   if (tid < D) {
     const int d = tid;
-    part.a[((int64_t)s * BH + bh) * D + d] = sa[0][d] + sa[1][d] + sa[2][d] + sa[3][d];
+    part.a[((int64_t)s * BH + bh) * D + d] =
+        sm.u.fin.so[0][G][d] + sm.u.fin.so[1][G][d] + sm.u.fin.so[2][G][d] + sm.u.fin.so[3][G][d];
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float mn = fmaxf(fmaxf(sm_[0][g], sm_[1][g]), fmaxf(sm_[2][g], sm_[3][g]));
+    for (int gg = 0; gg < G; ++gg) {
+      const float mn = fmaxf(fmaxf(sm.u.fin.m[0][gg], sm.u.fin.m[1][gg]), fmaxf(sm.u.fin.m[2][gg], sm.u.fin.m[3][gg]));
       float lt = 0.f, ot = 0.f;
 #pragma unroll
       for (int ww = 0; ww < 4; ++ww) {
-        const float al = __builtin_amdgcn_exp2f(sm_[ww][g] - mn);
-        lt = fmaf(sl[ww][g], al, lt);
-        ot = fmaf(so[ww][g][d], al, ot);
+        const float al = __builtin_amdgcn_exp2f(sm.u.fin.m[ww][gg] - mn);
+        lt = fmaf(sm.u.fin.l[ww][gg], al, lt);
+        ot = fmaf(sm.u.fin.so[ww][gg][d], al, ot);
       }
-      part.o[(((int64_t)s * BH + bh) * G + g) * D + d] = ot;
+      part.o[(((int64_t)s * BH + bh) * G + gg) * D + d] = ot;
       if (d == 0) {
-        part.m[((int64_t)s * BH + bh) * G + g] = mn;
-        part.l[((int64_t)s * BH + bh) * G + g] = lt;
+        part.m[((int64_t)s * BH + bh) * G + gg] = mn;
+        part.l[((int64_t)s * BH + bh) * G + gg] = lt;
       }
     }
   }
