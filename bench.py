@@ -141,6 +141,16 @@ def copy_calibration(nbytes: int, reps: int = 3) -> None:
           flush=True)
 
 
+def measured_traffic(workload, kernel):
+    """Calibrated HBM bytes per launch of `kernel` at `workload`'s shape, from
+    profiles/traffic.json (rocprofv3 FETCH_SIZE + WRITE_SIZE runs); None if not measured."""
+    tfile = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
+    if not os.path.exists(tfile):
+        return None
+    with open(tfile) as fh:
+        return json.load(fh).get(workload, {}).get(kernel)
+
+
 def bench_decode(args, dev):
     """One LUCID decoding step (one layer's attention for one new token per sequence) against
     a full cache at the long-context shape of config 5: B=1, Hq=32 over Hkv=8, d=128,
@@ -181,11 +191,7 @@ def bench_decode(args, dev):
     dom_avg = totals[dom][0] / totals[dom][1]
     nbytes = 2.0 * B * Hkv * T * D * 2  # K and V' caches, bf16, read once
     achieved = nbytes / (dom_avg / 1e3) / 1e9
-    traffic = None
-    tfile = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
-    if os.path.exists(tfile):
-        with open(tfile) as fh:
-            traffic = json.load(fh).get(dom)
+    traffic = measured_traffic("decode", dom)
     out = {
         "metric": "LUCID decode step (one layer, one new token) tokens/s at T=128K cache (config-5 shape)",
         "value": round(B / (ms / 1e3), 1),
@@ -424,11 +430,7 @@ def main():
     dom = max(totals.items(), key=lambda kv: kv[1][0])[0]
     dom_avg = totals[dom][0] / totals[dom][1]
     achieved = kflops.get(dom, 0.0) / (dom_avg / 1e3) / 1e12
-    traffic = None
-    tfile = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
-    if os.path.exists(tfile):
-        with open(tfile) as fh:
-            traffic = json.load(fh).get(dom)
+    traffic = measured_traffic(wl, dom)
 
     causal = None
     if not args.no_causal and wl in ("lucid", "c2", "path_softmax"):
