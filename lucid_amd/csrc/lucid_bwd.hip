@@ -229,7 +229,6 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_bw
     float scale) {
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
-  constexpr int CH = D / 32;
   __shared__ __attribute__((aligned(16))) DqSmem<D> sm;
   const int nblk = (T + 255) / 256;
   const int id = blockIdx.x;
@@ -403,7 +402,6 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
     Strides dvs, float* __restrict__ colsum, int* __restrict__ counters) {
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
-  constexpr int CH = D / 32;
   __shared__ __attribute__((aligned(16))) PcolSmem<D> sm;
 
   const int NT = T / 64, NP = T / 128;
@@ -739,7 +737,6 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
     const float* __restrict__ colsum, const float* __restrict__ dka, bf16* __restrict__ dk_out, Strides dks) {
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
-  constexpr int CH = D / 32;
   __shared__ __attribute__((aligned(16))) ProwSmem<D> sm;
   const int NP = T / 128;
   const int id = blockIdx.x;
