@@ -563,7 +563,6 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_fw
         softmax(1);
         pv(1);
       } else {  // D = 128: both halves' products first (the staggered order spills here)
-        const int j0 = jt * 64;
         f32x16 s[2][2];
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
