@@ -128,25 +128,28 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_bw
   for (int t = 0; t < NDT; ++t) tro[t] = lds_tr_lane_off<D / 8>(t * 32);
 #pragma unroll
   for (int st = 0; st < NKS; ++st) rdo[st] = swz_off<D / 8>(l32, 2 * st + g);
+  const bf16x8 ones = seed_ones(g);
+  const float cinv = 1.f / c;
   // one 64-row query tile; DIAG: the tile holding this wave's keys (causal mask)
   auto tile = [&](const int buf, const bool DIAG) {
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
       if (DIAG && mt * 32 + 31 < kloc - l32) continue;  // rows all above this wave's keys
-      float lr[16];
-      lds_rows16(&sm.lse[buf][mt * 32], g, lr);
+      // the per-row terms enter through the matrix cores: a rank-3 product with `ones`
+      // seeds the score accumulator with -lse_i / c and the dP accumulator with -delta_i,
+      // from the one value of this lane's own row (no per-element row reads)
       f32x16 pv;
       bf16x8 pb0, pb1;
       {
         bf16x8 qa[NKS];
 #pragma unroll
         for (int st = 0; st < NKS; ++st) qa[st] = ld8(sm.q[buf] + rdo[st] + mt * 32 * D);
-        f32x16 sc = zero16();
+        f32x16 sc = mfma32(seed_a(-sm.lse[buf][mt * 32 + l32] * cinv, g), ones, zero16());
 #pragma unroll
         for (int st = 0; st < NKS; ++st) sc = mfma32(qa[st], kb[st], sc);
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-          float p = __builtin_amdgcn_exp2f(fmaf(sc[e], c, -lr[e]));
+          float p = __builtin_amdgcn_exp2f(sc[e] * c);
           if (DIAG && (mt * 32 + drow(e, g) < kloc)) p = 0.f;
           pv[e] = p;
         }
@@ -158,14 +161,12 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_bw
         adv[t] = mfma32(lds_tr_a_at<D / 8>(sm.dO[buf] + tro[t], mt * 32), pb0, adv[t]);
         adv[t] = mfma32(lds_tr_a_at<D / 8>(sm.dO[buf] + tro[t], mt * 32 + 16), pb1, adv[t]);
       }
-      lds_rows16(&sm.dl[buf][mt * 32], g, lr);
       {
         bf16x8 da[NKS];
 #pragma unroll
         for (int st = 0; st < NKS; ++st) da[st] = ld8(sm.dO[buf] + rdo[st] + mt * 32 * D);
-        f32x16 dp;  // dP - delta: the accumulator starts at -delta (stored negated)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) dp[e] = lr[e];
+        // dP - delta: the accumulator starts at -delta (stored negated)
+        f32x16 dp = mfma32(seed_a(sm.dl[buf][mt * 32 + l32], g), ones, zero16());
 #pragma unroll
         for (int st = 0; st < NKS; ++st) dp = mfma32(da[st], vb[st], dp);
 #pragma unroll

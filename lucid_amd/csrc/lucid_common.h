@@ -54,6 +54,30 @@ __device__ __forceinline__ void split8(const float* p, bf16x8& hi, bf16x8& lo) {
   }
 }
 
+// Per-row seed of an MFMA accumulator: mfma32(seed_a(x_m, g), seed_ones(g), 0) gives
+// D[m][n] = x_m for every column n (m = the lane's row, lane % 32).  x is split into
+// three bf16 terms at k = 0, 1, 2 (exact to ~2^-24 relative); the other k are zero.
+__device__ __forceinline__ bf16x8 seed_a(float x, int g) {
+  bf16x8 a;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) a[e] = (bf16)0.f;
+  if (g == 0) {
+    const bf16 h = (bf16)x;
+    const float r1 = x - (float)h;
+    const bf16 m = (bf16)r1;
+    a[0] = h;
+    a[1] = m;
+    a[2] = (bf16)(r1 - (float)m);
+  }
+  return a;
+}
+__device__ __forceinline__ bf16x8 seed_ones(int g) {
+  bf16x8 b;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) b[e] = (bf16)((g == 0 && e < 3) ? 1.f : 0.f);
+  return b;
+}
+
 // one element of a T-perm matrix [bh][D][T]
 __device__ __forceinline__ void vpth_w(bf16* base, int bh, int D, int T, int d, int slot, bf16 val) {
   base[((int64_t)bh * D + d) * T + slot] = val;
