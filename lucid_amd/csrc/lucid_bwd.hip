@@ -713,22 +713,18 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
 // ---------------------------------------------------------------------------
 // Row sums R_I = sum_{J <= I} M_IJ K^_J, then dK^ = -s (R + C), the RMSNorm
 // backward and the attention dK.  No chain: every dV is known.
-// Workgroup = 128 rows; wave w: ih = w & 1 -> rows 64*ih .. +64 (lane <-> row),
-// jh = w >> 1 -> keys 32*jh .. +32 of every staged 64-key tile J
-// (K rows, V' rows, 1/rms; direct global->LDS loads, three buffers, two tiles
-// ahead; K^T operands through transposing LDS loads):
+// Workgroup = 256 rows (heavy, late blocks first); wave w owns rows 64w .. +64
+// (two 32-row n-tiles, lane <-> row) and sweeps both 32-key halves of every
+// staged 64-key tile J (K rows, V' rows, 1/rms; direct global->LDS loads, three
+// buffers, two tiles ahead; K^T operands through transposing LDS loads):
 //   S^T[J][I] = K_J . K_I, G^T[J][I] = V'_J . dV_I, R^T[d][I] += K^T[d][J] (r_J G P)^T[J][I]
+// Each wave finishes its own rows, so no cross-wave reduction is needed.
 // ---------------------------------------------------------------------------
 template <int D>
 struct ProwSmem {
-  union {
-    struct {
-      bf16 k[3][64 * D];  // swizzled tiles (chunk c of row r at c ^ (r & 7))
-      bf16 v[3][64 * D];
-      float r[3][64];
-    } st;
-    float Rt[D][132];
-  } u;
+  bf16 k[3][64 * D];  // swizzled tiles (chunk c of row r at c ^ (r & 7))
+  bf16 v[3][64 * D];
+  float r[3][64];
 };
 
 template <int D>
@@ -739,14 +735,14 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
   __shared__ __attribute__((aligned(16))) ProwSmem<D> sm;
-  const int NP = T / 128;
+  const int nblk = (T + 255) / 256;
   const int id = blockIdx.x;
-  const int p = NP - 1 - id / BH, bh = id - (id / BH) * BH;  // heavy (late) blocks first
+  const int ib = nblk - 1 - id / BH, bh = id - (id / BH) * BH;  // heavy (late) blocks first
   const int b = bh / Hkv, h = bh - b * Hkv;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
-  const int ih = w & 1, jh = w >> 1;
-  const int I0 = p * 128;
+  const int row0 = ib * 256 + w * 64;  // this wave's rows (T is a multiple of 128, so all 64 or none are < T)
+  const bool active = row0 < T;
   const bf16* kh = k + b * ks.b + h * ks.h;
   const float* rv = rinv + (int64_t)bh * T;
   const bf16* vh = vpb + (int64_t)bh * T * D;
@@ -757,7 +753,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
   float aI[2];
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
-    const int ir = I0 + ih * 64 + nt * 32 + l32;
+    const int ir = active ? row0 + nt * 32 + l32 : 0;
 #pragma unroll
     for (int st = 0; st < NKS; ++st) {
       kbI[nt][st] = ld8(kh + (int64_t)ir * ks.t + 16 * st + 8 * g);
@@ -771,36 +767,34 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
     acc[t][0] = zero16();
     acc[t][1] = zero16();
   }
-  const int ntile = 2 * p + 2;  // key tiles 0 .. 2p+1 (the last two are this workgroup's own blocks)
+  const int ntile = min(4 * ib + 4, T / 64);  // key tiles 0 .. ntile-1 (>= 2 since T >= 128)
   constexpr int STAGE_OPS = 2 * (64 * (D / 8) / 256);  // newest vector-memory ops of a step, per wave
   int plan_k[64 * (D / 8) / 256], plan_v[64 * (D / 8) / 256];
   dma_plan<64, D / 8>(ks.t, plan_k);
   dma_plan<64, D / 8>(D, plan_v);
   auto stage = [&](int J) {
     const int j0 = J * 64, buf = J % 3;
-    if (w == 0) dma_f32x64(rv + j0, sm.u.st.r[buf]);
-    dma_stage<64, D / 8>(plan_k, kh + (int64_t)j0 * ks.t, sm.u.st.k[buf]);
-    dma_stage<64, D / 8>(plan_v, vh + (int64_t)j0 * D, sm.u.st.v[buf]);
+    if (w == 0) dma_f32x64(rv + j0, sm.r[buf]);
+    dma_stage<64, D / 8>(plan_k, kh + (int64_t)j0 * ks.t, sm.k[buf]);
+    dma_stage<64, D / 8>(plan_v, vh + (int64_t)j0 * D, sm.v[buf]);
   };
   stage(0);
-  stage(1);  // ntile >= 2
+  stage(1);
   dma_wait_but<STAGE_OPS>();
   __syncthreads();
-  // this wave's rows start at 64-block index 2p + ih; key tiles after it are fully masked
-  const int last_w = 2 * p + ih;
-  for (int J = 0; J < ntile; ++J) {
-    const int buf = J % 3;
-    if (J + 2 < ntile) stage(J + 2);
-    if (J <= last_w) {
-      const bool diag = (J == last_w);
+  // this wave's rows are the 64-block row0 / 64; key tiles after it are fully masked
+  const int last_w = row0 / 64;
+  auto tile = [&](int buf, bool diag) {
+#pragma unroll 1
+    for (int jh = 0; jh < 2; ++jh) {
       bf16x8 ka[NKS], va[NKS];
 #pragma unroll
       for (int st = 0; st < NKS; ++st) {
-        ka[st] = ld8(swz<D / 8>(sm.u.st.k[buf], jh * 32 + l32, 2 * st + g));
-        va[st] = ld8(swz<D / 8>(sm.u.st.v[buf], jh * 32 + l32, 2 * st + g));
+        ka[st] = ld8(swz<D / 8>(sm.k[buf], jh * 32 + l32, 2 * st + g));
+        va[st] = ld8(swz<D / 8>(sm.v[buf], jh * 32 + l32, 2 * st + g));
       }
       float rJ[16];
-      lds_rows16(&sm.u.st.r[buf][jh * 32], g, rJ);
+      lds_rows16(&sm.r[buf][jh * 32], g, rJ);
       bf16x8 mb[2][2];
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt) {
@@ -821,8 +815,8 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
       }
 #pragma unroll
       for (int t = 0; t < NDT; ++t) {
-        const bf16x8 k0 = lds_tr_a<D / 8>(sm.u.st.k[buf], jh * 32, t * 32);
-        const bf16x8 k1 = lds_tr_a<D / 8>(sm.u.st.k[buf], jh * 32 + 16, t * 32);
+        const bf16x8 k0 = lds_tr_a<D / 8>(sm.k[buf], jh * 32, t * 32);
+        const bf16x8 k1 = lds_tr_a<D / 8>(sm.k[buf], jh * 32 + 16, t * 32);
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) {
           acc[t][nt] = mfma32(k0, mb[nt][0], acc[t][nt]);
@@ -830,66 +824,62 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
         }
       }
     }
+  };
+  for (int J = 0; J < ntile; ++J) {
+    const int buf = J % 3;
+    if (J + 2 < ntile) stage(J + 2);
+    if (active) {
+      if (J < last_w) tile(buf, false);
+      else if (J == last_w) tile(buf, true);
+    }
     if (J + 2 < ntile) dma_wait_but<STAGE_OPS>();  // the step after next may stay in flight
     else dma_wait();
     __syncthreads();
   }
-  float(*Rt)[132] = sm.u.Rt;
-  if (jh == 1) {
+  if (!active) return;
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    const int irow = row0 + nt * 32 + l32;
+    const float ri = rv[irow];
+    const float* cs = colsum + ((int64_t)bh * T + irow) * D;
+    const float* da = dka + ((int64_t)bh * T + irow) * D;
+    const bf16* kr = kh + (int64_t)irow * ks.t;
+    float dkh[NDT][16], khat[NDT][16];
+    float dotp = 0.f;
 #pragma unroll
     for (int t = 0; t < NDT; ++t)
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt)
+      for (int qq = 0; qq < 4; ++qq) {
+        const int d0 = t * 32 + 8 * qq + 4 * g;
+        const f32x4 cv = *reinterpret_cast<const f32x4*>(cs + d0);
+        const bf16x4 kv = *reinterpret_cast<const bf16x4*>(kr + d0);
 #pragma unroll
-        for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][ih * 64 + nt * 32 + l32] = acc[t][nt][e];
-  }
-  __syncthreads();
-  if (jh == 0) {
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      const int col = ih * 64 + nt * 32 + l32;
-      const int irow = I0 + col;
-      const float ri = rv[irow];
-      const float* cs = colsum + ((int64_t)bh * T + irow) * D;
-      const float* da = dka + ((int64_t)bh * T + irow) * D;
-      const bf16* kr = kh + (int64_t)irow * ks.t;
-      float dkh[NDT][16], khat[NDT][16];
-      float dotp = 0.f;
-#pragma unroll
-      for (int t = 0; t < NDT; ++t)
-#pragma unroll
-        for (int qq = 0; qq < 4; ++qq) {
-          const int d0 = t * 32 + 8 * qq + 4 * g;
-          const f32x4 cv = *reinterpret_cast<const f32x4*>(cs + d0);
-          const bf16x4 kv = *reinterpret_cast<const bf16x4*>(kr + d0);
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const int e = 4 * qq + u;
-            const float x = -scale * (acc[t][nt][e] + Rt[d0 + u][col] + cv[u]);
-            const float kk = ri * (float)kv[u];
-            dkh[t][e] = x;
-            khat[t][e] = kk;
-            dotp += x * kk;
-          }
+        for (int u = 0; u < 4; ++u) {
+          const int e = 4 * qq + u;
+          const float x = -scale * (acc[t][nt][e] + cv[u]);
+          const float kk = ri * (float)kv[u];
+          dkh[t][e] = x;
+          khat[t][e] = kk;
+          dotp += x * kk;
         }
-      dotp = wave_sum32(dotp);
-      const float f = dotp / (float)D;
-      bf16* op = dk_out + b * dks.b + h * dks.h + (int64_t)irow * dks.t;
+      }
+    dotp = wave_sum32(dotp);
+    const float f = dotp / (float)D;
+    bf16* op = dk_out + b * dks.b + h * dks.h + (int64_t)irow * dks.t;
 #pragma unroll
-      for (int t = 0; t < NDT; ++t)
+    for (int t = 0; t < NDT; ++t)
 #pragma unroll
-        for (int qq = 0; qq < 4; ++qq) {
-          const int d0 = t * 32 + 8 * qq + 4 * g;
-          const f32x4 av = *reinterpret_cast<const f32x4*>(da + d0);
-          bf16x4 bb;
+      for (int qq = 0; qq < 4; ++qq) {
+        const int d0 = t * 32 + 8 * qq + 4 * g;
+        const f32x4 av = *reinterpret_cast<const f32x4*>(da + d0);
+        bf16x4 bb;
 #pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const int e = 4 * qq + u;
-            bb[u] = (bf16)(ri * (dkh[t][e] - khat[t][e] * f) + av[u]);
-          }
-          *reinterpret_cast<bf16x4*>(op + d0) = bb;
+        for (int u = 0; u < 4; ++u) {
+          const int e = 4 * qq + u;
+          bb[u] = (bf16)(ri * (dkh[t][e] - khat[t][e] * f) + av[u]);
         }
-    }
+        *reinterpret_cast<bf16x4*>(op + d0) = bb;
+      }
   }
 }
 

@@ -160,7 +160,7 @@ int launch_bwd(const void* dout, const int64_t* dos, const void* q, const int64_
   LUCID_LAUNCH("lucid_precond_bwd_col_kernel", lucid::lucid_precond_bwd_col_kernel<D>, dim3((T / 128) * BH), st,
                (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, scale, f.kt, f.vpb, f.pinv, w.dvp, w.dvb,
                (bf16*)dv, S(dvs), w.colsum, w.counters);
-  LUCID_LAUNCH("lucid_precond_bwd_row_kernel", lucid::lucid_precond_bwd_row_kernel<D>, dim3((T / 128) * BH), st,
+  LUCID_LAUNCH("lucid_precond_bwd_row_kernel", lucid::lucid_precond_bwd_row_kernel<D>, dim3(((T + 255) / 256) * BH), st,
                (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, scale, f.vpb, w.dvb, w.colsum, w.dka, (bf16*)dk,
                S(dks));
   return LUCID_OK;
