@@ -193,7 +193,7 @@ int lucid_path_fwd(const void* q, const int64_t* q_strides, const void* k, const
   const int BHq = B * HQ;
   if (int rc = launch_front(q, q_strides, k, k_strides, w, w_strides, beta, beta_strides, B, T, H, HQ, scale, 0, ws, st))
     return rc;
-  LUCID_TIMED_LAUNCH(phip, "path_solve_fwd_kernel", lucid::path_solve_fwd_kernel, dim3(NT * BHq), st, (const bf16*)v,
+  LUCID_TIMED_LAUNCH(phip, "path_solve_fwd_kernel", lucid::path_solve_fwd_kernel, dim3(((NT + 1) / 2) * BHq), st, (const bf16*)v,
                      PS(v_strides), (bf16*)o, PS(o_strides), HQ, H, T, BHq, scale, ws);
   if (kcache)
     if (int rc = launch_kcache(kcache, kcache_strides, B, T, H, ws, st)) return rc;

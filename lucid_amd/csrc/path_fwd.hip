@@ -293,26 +293,32 @@ __global__ __launch_bounds__(256) void path_transport_kernel(int HQ, int H, int 
 
 // ---------------------------------------------------------------------------
 // Chained solve (triangular_solve_fwd.py:99-225) per query head; one workgroup per
-// 64-row chunk I; ids grow with I.  wave w: ih = w & 1 -> rows 32*ih (lane <-> row),
-// jh = w >> 1 -> keys 32*jh of every staged 64-key tile.
-//   S^T[j][i] = Kop_J . Qop_I, P = exp(s S - 1/s), acc^T[d][i] += O^T[d][j] P^T[j][i]
-//   O_I = Y_I (V_I - acc)   (3-term bf16 split)
-// The key chunks are swept in pairs (J = 2pp, 2pp + 1; both in one large chunk), one
+// pair of 64-row chunks A = 2p, B = 2p + 1 (one large chunk holds both); ids grow
+// with p, so every wait is on a lower id.  counters[bhq] = number of chunks of O
+// published (two at a time).
+// The earlier key chunks are swept in pairs (J = 2pp, 2pp + 1, one large chunk), one
 // barrier per pair, the next pair staged by direct global->LDS loads while this one
-// is processed.  The fp32 buffers of the final step (R^T, Y) reuse the staging space.
+// is processed.  wave w: ih = w & 1 -> the rows of chunk A (ih = 0) or B (two 32-row
+// n-tiles, lane <-> row), kh = w >> 1 -> key chunk 2pp + kh of every staged pair:
+//   S^T[j][i] = Kop_J . Qop_I, L = exp(s S - 1/s), acc^T[d][i] += O^T[d][j] L^T[j][i]
+// (the kh = 0 accumulators start at -V^T).  Then O_A = Y_A R_A and
+// O_B = Y_B (R_B - L_BA O_A), R = V - acc, Y = (I + L_diag)^-1 applied through a 3-term
+// bf16 split.  L_BA depends on the key operands only and is computed before the sweep.
+// The fp32 buffers of the final step reuse the staging space.
 // ---------------------------------------------------------------------------
 struct SolveFwdSmem {
   union {
     struct {
-      bf16 k[2][2][64 * 64];  // [buffer][tile of the pair], swizzled (chunk c of row r at c ^ (r & 7))
+      bf16 k[2][2][64 * 64];  // [buffer][chunk of the pair], swizzled (chunk c of row r at c ^ (r & 7))
       bf16 o[2][2][64 * 64];
     } st;
     struct {
-      float Ys[64][68];
-      float Rt[64][68];
-      bf16 ot[64 * 64];  // O^T of the chunk, T-perm within 16-groups
+      float Rt[64][132];    // R^T for the 128 rows (0..63 = A, 64..127 = B)
+      float Ys[64][68];     // Y of the chunk being solved
+      bf16 ot[64][128 + 8];  // O^T of both chunks, T-perm within 16-groups
     } fin;
   } u;
+  bf16x8 lba[4][64][2];  // L_BA as MFMA B operands, per wave and lane
 };
 
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void path_solve_fwd_kernel(const bf16* __restrict__ v, Strides vs,
@@ -321,82 +327,130 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
   __shared__ __attribute__((aligned(16))) SolveFwdSmem sm;
   const int NT = T / PC, NS = (NT + PR - 1) / PR;
   const int id = blockIdx.x;
-  const int I = id / BHq, bhq = id - (id / BHq) * BHq;
+  const int p = id / BHq, bhq = id - (id / BHq) * BHq;
   const int G = HQ / H;
   const int b = bhq / HQ, hq = bhq - b * HQ, h = hq / G, bh = b * H + h;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
-  const int ih = w & 1, jh = w >> 1;
-  const int sI = I / PR, cb = sI * PR;
-  const int i0 = I * PC;
+  const int ih = w & 1, kh = w >> 1;
+  const int A = 2 * p;
+  const bool hasB = A + 1 < NT;
+  const int cb = (A / PR) * PR;  // first chunk of the large chunk holding A and B
+  const int i0 = A * PC;
   int* cnt = ws.counters + bhq;
   const float sl2 = scale * LOG2E_F, cc0 = LOG2E_F / scale;
   const bf16* oTh = ws.oT + (int64_t)bhq * 64 * T;
-  const int npair = (I + 1) / 2;
+  const int npair = p;  // key chunks 0 .. A - 1
+  // this wave's rows (chunk A or B); a missing chunk B reads chunk A's rows, unused
+  const bool myrows = ih == 0 || hasB;
+  const int r0 = i0 + (myrows ? ih * 64 : 0);
 
-  // accumulators: -V^T for the jh = 0 waves (R = V - acc = -(acc_0 + acc_1)), zero for the others
-  f32x16 acc[2];
-  {
-    const bf16* vrow = v + b * vs.b + h * vs.h + (int64_t)(i0 + ih * 32 + l32) * vs.t;
+  // accumulators: -V^T for the kh = 0 waves (R = V - acc = -(acc_0 + acc_1)), zero for the others
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    const bf16* vrow = v + b * vs.b + h * vs.h + (int64_t)(r0 + nt * 32 + l32) * vs.t;
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int qq = 0; qq < 4; ++qq) {
         const bf16x4 vv = *reinterpret_cast<const bf16x4*>(vrow + t * 32 + 8 * qq + 4 * g);
 #pragma unroll
-        for (int u = 0; u < 4; ++u) acc[t][4 * qq + u] = jh ? 0.f : -(float)vv[u];
+        for (int u = 0; u < 4; ++u) acc[t][nt][4 * qq + u] = kh ? 0.f : -(float)vv[u];
       }
   }
-  // query operand of key chunk J for this lane's row: QB^(J/PR) below I's large chunk,
+  // query operand of key chunk J for this wave's rows: QB^(J/PR) below the large chunk,
   // QS slot J - cb inside it
-  auto load_q = [&](int J, bf16x8 q[4]) {
-    const bf16* base = (J < cb) ? ws.qb + ((int64_t)bhq * NS + J / PR) * T * 64
-                                : ws.qs + ((int64_t)bhq * PR + (J - cb)) * T * 64;
-#pragma unroll
-    for (int st = 0; st < 4; ++st) q[st] = ld8(base + (int64_t)(i0 + ih * 32 + l32) * 64 + 16 * st + 8 * g);
+  auto qbase = [&](int J) {
+    return (J < cb) ? ws.qb + ((int64_t)bhq * NS + J / PR) * T * 64 : ws.qs + ((int64_t)bhq * PR + (J - cb)) * T * 64;
   };
-  // below I's large chunk the operand changes only every PR key chunks (both chunks of
-  // a pair share it), so it stays in registers; inside it every chunk has its own slot
-  bf16x8 q0[4], q1[4];
+  // L_BA (rows of B half nb, keys of A half ka): Kop_A = k~_A, Qop = QS slot A - cb of B's rows
+  if (hasB) {
+    const int nb = w & 1, ka = w >> 1;
+    const bf16* kr = ws.kt + ((int64_t)bh * T + i0 + ka * 32 + l32) * 64;
+    const bf16* qr = qbase(A) + (int64_t)(i0 + 64 + nb * 32 + l32) * 64;
+    f32x16 sc = zero16();
+#pragma unroll
+    for (int st = 0; st < 4; ++st) sc = mfma32(ld8(kr + 16 * st + 8 * g), ld8(qr + 16 * st + 8 * g), sc);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) sc[e] = __builtin_amdgcn_exp2f(fmaf(sc[e], sl2, -cc0));
+    sm.lba[w][lane][0] = pack_b(sc, 0);
+    sm.lba[w][lane][1] = pack_b(sc, 1);
+  }
+  // below the large chunk the operand changes only every PR key chunks, so it stays in
+  // registers across pairs; inside it every chunk has its own slot
+  bf16x8 qop[2][4];
   int qsrc = -1;
+  auto load_q = [&](int J) {
+    const int src = (J < cb) ? J / PR : NS + J;
+    if (src == qsrc) return;
+    qsrc = src;
+    const bf16* base = qbase(J);
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+      for (int st = 0; st < 4; ++st) qop[nt][st] = ld8(base + (int64_t)(r0 + nt * 32 + l32) * 64 + 16 * st + 8 * g);
+  };
   int plan_k[2], plan_t[2];
   dma_plan<64, 8>(64, plan_k);
   dma_plan<64, 8>(T, plan_t);
-  auto stage = [&](int pp) {  // key chunks 2pp (and 2pp + 1 if below I) into buffer pp & 1
+  auto stage = [&](int pp) {  // key chunks 2pp, 2pp + 1 into buffer pp & 1
     const int buf = pp & 1;
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int J = 2 * pp + u;
-      if (J < I) {
-        dma_stage<64, 8>(plan_k, ((J < cb) ? ws.kl : ws.kt) + ((int64_t)bh * T + J * PC) * 64, sm.u.st.k[buf][u]);
-        dma_stage<64, 8>(plan_t, oTh + J * PC, sm.u.st.o[buf][u]);
-      }
+      dma_stage<64, 8>(plan_k, ((J < cb) ? ws.kl : ws.kt) + ((int64_t)bh * T + J * PC) * 64, sm.u.st.k[buf][u]);
+      dma_stage<64, 8>(plan_t, oTh + J * PC, sm.u.st.o[buf][u]);
     }
   };
-  // pair pp is complete once the counter exceeds its last chunk
-  auto need = [&](int pp) { return min(2 * pp + 1, I - 1); };
-  // Y_I (fp32) is fetched into registers during the last pair
-  f32x4 yr[4];
+  // Y_A, Y_B (fp32) are fetched into registers during the last pair
+  f32x4 yr[8];
   auto yload = [&]() {
-    const float* src = ws.y + ((int64_t)bhq * NT + I) * 4096;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) yr[u] = *reinterpret_cast<const f32x4*>(src + 4 * (tid + 256 * u));
+    for (int u = 0; u < 8; ++u) {
+      const int c = u >> 2;
+      if (c == 0 || hasB)
+        yr[u] = *reinterpret_cast<const f32x4*>(ws.y + ((int64_t)bhq * NT + A + c) * 4096 + 4 * (tid + 256 * (u & 3)));
+    }
   };
-  auto tile = [&](int buf, int u, const bf16x8 q[4]) {
-    f32x16 sc = zero16();
+  auto ystore = [&](int c) {
 #pragma unroll
-    for (int st = 0; st < 4; ++st) sc = mfma32(ld8(swz<8>(sm.u.st.k[buf][u], jh * 32 + l32, 2 * st + g)), q[st], sc);
+    for (int u = 4 * c; u < 4 * c + 4; ++u) {
+      const int f = 4 * (tid + 256 * (u & 3));
+      *reinterpret_cast<f32x4*>(&sm.u.fin.Ys[f >> 6][f & 63]) = yr[u];
+    }
+  };
+  auto sweep_pair = [&](int buf) {
 #pragma unroll
-    for (int e = 0; e < 16; ++e) sc[e] = __builtin_amdgcn_exp2f(fmaf(sc[e], sl2, -cc0));
-    const bf16x8 p0 = pack_b(sc, 0), p1 = pack_b(sc, 1);
+    for (int mt = 0; mt < 2; ++mt) {
+      bf16x8 ka[4];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      acc[t] = mfma32(ld8(swz<8>(sm.u.st.o[buf][u], t * 32 + l32, 4 * jh + g)), p0, acc[t]);
-      acc[t] = mfma32(ld8(swz<8>(sm.u.st.o[buf][u], t * 32 + l32, 4 * jh + 2 + g)), p1, acc[t]);
+      for (int st = 0; st < 4; ++st) ka[st] = ld8(swz<8>(sm.u.st.k[buf][kh], mt * 32 + l32, 2 * st + g));
+      bf16x8 pb[2][2];
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        f32x16 sc = zero16();
+#pragma unroll
+        for (int st = 0; st < 4; ++st) sc = mfma32(ka[st], qop[nt][st], sc);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sc[e] = __builtin_amdgcn_exp2f(fmaf(sc[e], sl2, -cc0));
+        pb[nt][0] = pack_b(sc, 0);
+        pb[nt][1] = pack_b(sc, 1);
+      }
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const bf16x8 va0 = ld8(swz<8>(sm.u.st.o[buf][kh], t * 32 + l32, 4 * mt + g));
+        const bf16x8 va1 = ld8(swz<8>(sm.u.st.o[buf][kh], t * 32 + l32, 4 * mt + 2 + g));
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+          acc[t][nt] = mfma32(va0, pb[nt][0], acc[t][nt]);
+          acc[t][nt] = mfma32(va1, pb[nt][1], acc[t][nt]);
+        }
+      }
     }
   };
   int ready = 0;
   if (npair > 0) {
-    ready = wait_counter_gt(cnt, need(0));
+    ready = wait_counter_gt(cnt, 1);
     stage(0);
     dma_wait();
   } else {
@@ -404,21 +458,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
   }
   __syncthreads();
   for (int pp = 0; pp < npair; ++pp) {
-    const int buf = pp & 1;
     const bool more = pp + 1 < npair;
-    const bool two = 2 * pp + 1 < I;
-    // the query operands are loaded before the next pair's staging so that waiting
-    // for them does not wait for the staging loads
-    const int J0 = 2 * pp;
-    const bool below = J0 < cb;
-    if (!below || J0 / PR != qsrc) {
-      load_q(J0, q0);
-      qsrc = below ? J0 / PR : -1;
-    }
-    if (two && !below) load_q(J0 + 1, q1);
+    // the query operand is loaded before the next pair's staging so that waiting for
+    // it does not wait for the staging loads
+    load_q(2 * pp + kh);
     bool early = false;
     if (more) {
-      const int nd = need(pp + 1);
+      const int nd = 2 * pp + 3;  // pair pp + 1 is complete once the counter exceeds this
       if (nd >= ready) {
         const int seen = poll_counter(cnt);
         if (seen > nd) {
@@ -429,57 +475,55 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
       early = nd < ready;
       if (early) stage(pp + 1);
     } else {
-      yload();
+      yload();  // fetch Y_A, Y_B while the last pair is processed
     }
-    tile(buf, 0, q0);
-    if (two) tile(buf, 1, below ? q0 : q1);
+    sweep_pair(pp & 1);
     if (more && !early) {
-      ready = wait_counter_gt(cnt, need(pp + 1));
+      ready = wait_counter_gt(cnt, 2 * pp + 3);
       stage(pp + 1);
     }
     dma_wait();
     __syncthreads();
   }
-  // ---- R = V - acc (reduce key halves); the staging space is free from here ----
-  float(*Rt)[68] = sm.u.fin.Rt;
-  if (jh == 1) {
+  // ---- R^T = -(acc_0 + acc_1) (Rt columns = rows of the workgroup); Y_A to LDS ----
+  float(*Rt)[132] = sm.u.fin.Rt;
+  if (kh == 1 && myrows) {
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][ih * 32 + l32] = acc[t][e];
-  }
+      for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int f = 4 * (tid + 256 * u);
-    *reinterpret_cast<f32x4*>(&sm.u.fin.Ys[f >> 6][f & 63]) = yr[u];
+        for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][ih * 64 + nt * 32 + l32] = acc[t][nt][e];
   }
+  ystore(0);
   __syncthreads();
-  if (jh == 0) {
+  if (kh == 0 && myrows) {
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        float& x = Rt[t * 32 + drow(e, g)][ih * 32 + l32];
-        x = -(acc[t][e] + x);
-      }
+      for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          float& x = Rt[t * 32 + drow(e, g)][ih * 64 + nt * 32 + l32];
+          x = -(acc[t][nt][e] + x);
+        }
   }
   __syncthreads();
-  // ---- O^T[d][r] = sum_c R^T[d][c] Y[r][c] ----
-  {
+  // O^T[d][r] = sum_c R^T[d][c] Y[r][c] for chunk c (Y lower triangular)
+  auto diag_solve = [&](int c) {
     const int dt = w >> 1, rh = w & 1;
     f32x16 oo = zero16();
     for (int st = 0; st < (rh ? 4 : 2); ++st) {
       bf16x8 ah, al, bh8, bl;
-      split8(&Rt[dt * 32 + l32][16 * st + 8 * g], ah, al);
+      split8(&Rt[dt * 32 + l32][c * 64 + 16 * st + 8 * g], ah, al);
       split8(&sm.u.fin.Ys[rh * 32 + l32][16 * st + 8 * g], bh8, bl);
       oo = mfma32(ah, bh8, oo);
       oo = mfma32(ah, bl, oo);
       oo = mfma32(al, bh8, oo);
     }
     const int rl = rh * 32 + l32;
-    const int lslot = (rl & ~15) | jmap(rl & 15);
-    bf16* orow = o + b * os.b + hq * os.h + (int64_t)(i0 + rl) * os.t;
-    bf16* ot = sm.u.fin.ot;
+    const int lslot = c * 64 + ((rl & ~15) | jmap(rl & 15));
+    bf16* orow = o + b * os.b + hq * os.h + (int64_t)(i0 + c * 64 + rl) * os.t;
 #pragma unroll
     for (int qq = 0; qq < 4; ++qq) {
       const int d0 = dt * 32 + 8 * qq + 4 * g;
@@ -487,17 +531,49 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         bb[u] = (bf16)oo[4 * qq + u];
-        ot[(d0 + u) * 64 + lslot] = bb[u];
+        sm.u.fin.ot[d0 + u][lslot] = bb[u];
       }
       *reinterpret_cast<bf16x4*>(orow + d0) = bb;
     }
-  }
+  };
+  diag_solve(0);
   __syncthreads();
-  for (int c = tid; c < 64 * 8; c += 256) {  // O^T to the chain operand with 16-byte stores
-    const int dd = c >> 3, s8 = (c & 7) * 8;
-    *reinterpret_cast<bf16x8*>(ws.oT + ((int64_t)bhq * 64 + dd) * T + i0 + s8) = ld8(sm.u.fin.ot + dd * 64 + s8);
+  if (hasB) {
+    ystore(1);
+    // ---- R_B -= L_BA O_A: wave -> (B rows half nb, A keys half ka) ----
+    const int nb = w & 1, ka = w >> 1;
+    const bf16x8 l0 = sm.lba[w][lane][0], l1 = sm.lba[w][lane][1];
+    f32x16 cr[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      cr[t] = mfma32(ld8(&sm.u.fin.ot[t * 32 + l32][ka * 32 + 8 * g]), l0, zero16());
+      cr[t] = mfma32(ld8(&sm.u.fin.ot[t * 32 + l32][ka * 32 + 16 + 8 * g]), l1, cr[t]);
+    }
+    const int col = 64 + nb * 32 + l32;
+    if (ka == 1) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][col] -= cr[t][e];
+    }
+    __syncthreads();
+    if (ka == 0) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][col] -= cr[t][e];
+    }
+    __syncthreads();
+    diag_solve(1);
+    __syncthreads();
   }
-  publish_counter(cnt, I + 1);
+  // O^T of the workgroup's chunks to the chain operand with 16-byte stores
+  const int nch = hasB ? 2 : 1;
+  for (int c = tid; c < 64 * 8 * nch; c += 256) {
+    const int dd = c / (8 * nch), s8 = (c - dd * 8 * nch) * 8;
+    *reinterpret_cast<bf16x8*>(ws.oT + ((int64_t)bhq * 64 + dd) * T + i0 + s8) = ld8(&sm.u.fin.ot[dd][s8]);
+  }
+  publish_counter(cnt, A + nch);
 }
 
 // ---------------------------------------------------------------------------
