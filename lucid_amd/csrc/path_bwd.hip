@@ -47,107 +47,158 @@ __global__ __launch_bounds__(256) void path_bwd_zero_kernel(int64_t n_hl, int64_
 
 // ---------------------------------------------------------------------------
 // Chained transposed solve (triangular_solve_bwd_dv_reuse.py:113-205), one
-// workgroup per 64-column chunk J of one query head, ids grow as J falls.
-// wave w: ch = w & 1 -> columns 32*ch (lane <-> column j), ih = w >> 1 -> rows 32*ih
-// of every staged 64-row tile I > J.
+// workgroup per pair of 64-column chunks A = 2q, B = 2q + 1 (one large chunk holds
+// both) of one query head; ids grow as q falls, so every wait is on a lower id.
+// counters[bhq] = number of chunks of dV published from the end (B, then A).
+// wave w owns columns 32w .. +32 of the pair (chunk A for w < 2, lane <-> column j)
+// and all 64 rows of every later row tile I > B, so its sums need no cross-wave
+// reduction:
 //   S[I][J] = Qop_I . Kop_J, L = exp(s S - 1/s), acc^T[d][j] += dV^T[d][i] L[i][j]
-// counters[bhq] = number of chunks of dV published from the end.  The row tiles are
-// swept in pairs (I = NT-1-2pp, NT-2-2pp), one barrier and one staging round per pair;
-// the fp32 buffers of the final step reuse the staging space.  Finally
-// dA_diag = -s (dV_J O_J^T) * L_diag on the matrix cores.
+// Row tiles beyond the large chunk share one query operand (QB) for both chunks and
+// are swept in pairs, one barrier and one staging round per pair; the (at most six)
+// row tiles inside the large chunk need a query slot per column chunk (QS) and are
+// swept one per step with both slots staged.  Then dV_B = Y_B^T R_B (published),
+// R_A -= L_BA^T dV_B, dV_A = Y_A^T R_A (published), R = dO - acc, and
+// dA_diag = -s (dV_J O_J^T) * L_diag for both chunks on the matrix cores.  L_BA
+// depends on the operands only and is computed before the sweep; the fp32 buffers
+// of the final step reuse the staging space.
 // ---------------------------------------------------------------------------
 struct DvSmem {
   union {
     struct {
-      bf16 q[2][2][64 * 64];  // [buffer][tile of the pair], swizzled (chunk c of row r at c ^ (r & 7))
+      bf16 q[2][2][64 * 64];  // [buffer][tile of the pair, or column chunk], swizzled (chunk c of row r at c ^ (r & 7))
       bf16 d[2][2][64 * 64];
     } st;
     struct {
-      float Yt[64][68];  // Yt[c][r] = Y[r][c], then O rows
-      float Rt[64][68];  // R^T, then dV rows
-      bf16 dt[64 * 64];  // dV^T of the chunk, T-perm within 16-groups
+      float Rt[64][132];    // R^T for the 128 columns (0..63 = A), then dV rows of one chunk
+      float Yt[64][68];     // Yt[c][r] = Y[r][c] of the chunk being solved, then O rows
+      bf16 dt[64][128 + 8];  // dV^T of both chunks, T-perm within 16-groups
     } fin;
   } u;
+  bf16x8 lba[4][64][2];  // L_BA as MFMA B operands, per wave and lane
 };
 
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void path_dv_kernel(const bf16* __restrict__ dout, Strides dos,
                                                       const bf16* __restrict__ o, Strides os, int HQ, int H, int T,
                                                       int BHq, float scale, PathFwdWs ws, PathBwdWs bw) {
   __shared__ __attribute__((aligned(16))) DvSmem sm;
-  const int NT = T / PC, NS = (NT + PR - 1) / PR;
+  const int NT = T / PC, NS = (NT + PR - 1) / PR, NQ = (NT + 1) / 2;
   const int id = blockIdx.x;
-  const int J = NT - 1 - id / BHq, bhq = id - (id / BHq) * BHq;
+  const int q = NQ - 1 - id / BHq, bhq = id - (id / BHq) * BHq;
   const int G = HQ / H;
   const int b = bhq / HQ, hq = bhq - b * HQ, bh = b * H + hq / G;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
-  const int ch = w & 1, ih = w >> 1;
-  const int sJ = J / PR, ceJ = min(sJ * PR + PR, NT) - 1;  // last chunk of J's large chunk
-  const int j0 = J * PC;
+  const int A = 2 * q;
+  const bool hasB = A + 1 < NT;
+  const int last = hasB ? A + 1 : A;                     // last chunk of the workgroup
+  const int sJ = A / PR, cb = sJ * PR, ceJ = min(cb + PR, NT) - 1;  // the large chunk holding A and B
+  const int j0 = A * PC;
+  const int wc = w >> 1;                                 // this wave's column chunk (0 = A, 1 = B)
+  const bool mycols = wc == 0 || hasB;
+  const int jc = j0 + (mycols ? w * 32 : (w & 1) * 32) + l32;  // this lane's column (a missing B reuses A's)
   int* cnt = bw.counters + bhq;
   const float sl2 = scale * LOG2E_F, cc0 = LOG2E_F / scale;
 
   bf16x8 kbs[4], kbf[4];
 #pragma unroll
   for (int st = 0; st < 4; ++st) {
-    kbs[st] = ld8(ws.kt + ((int64_t)bh * T + j0 + ch * 32 + l32) * 64 + 16 * st + 8 * g);
-    kbf[st] = ld8(ws.kl + ((int64_t)bh * T + j0 + ch * 32 + l32) * 64 + 16 * st + 8 * g);
+    kbs[st] = ld8(ws.kt + ((int64_t)bh * T + jc) * 64 + 16 * st + 8 * g);
+    kbf[st] = ld8(ws.kl + ((int64_t)bh * T + jc) * 64 + 16 * st + 8 * g);
   }
-  // accumulators: -dO^T for the ih = 0 waves (R = dO - acc = -(acc_0 + acc_1)), zero for the others
+  // accumulators start at -dO^T (R = dO - acc = -acc)
   f32x16 acc[2];
   {
-    const bf16* drow_ = dout + b * dos.b + hq * dos.h + (int64_t)(j0 + ch * 32 + l32) * dos.t;
+    const bf16* drow_ = dout + b * dos.b + hq * dos.h + (int64_t)jc * dos.t;
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int qq = 0; qq < 4; ++qq) {
         const bf16x4 x = *reinterpret_cast<const bf16x4*>(drow_ + t * 32 + 8 * qq + 4 * g);
 #pragma unroll
-        for (int u = 0; u < 4; ++u) acc[t][4 * qq + u] = ih ? 0.f : -(float)x[u];
+        for (int u = 0; u < 4; ++u) acc[t][4 * qq + u] = -(float)x[u];
       }
   }
-  // row tile k (k = 0 .. n-1) is chunk I = NT-1-k; it is published once the counter exceeds k
-  const int n = NT - 1 - J, npair = (n + 1) / 2;
+  // QS slot of column chunk c (relative to the large chunk) for row chunk I inside it
+  auto qs_slot = [&](int c) { return ws.qs + ((int64_t)bhq * PR + (A + c - cb)) * T * 64; };
+  // L_BA (rows of B half kb, columns of A half na): Qop = QS slot A - cb of B's rows, Kop_A = k~_A
+  if (hasB) {
+    const int na = w & 1, kb = w >> 1;
+    const bf16* qr = qs_slot(0) + (int64_t)((A + 1) * PC + kb * 32 + l32) * 64;
+    const bf16* kr = ws.kt + ((int64_t)bh * T + j0 + na * 32 + l32) * 64;
+    f32x16 sc = zero16();
+#pragma unroll
+    for (int st = 0; st < 4; ++st) sc = mfma32(ld8(qr + 16 * st + 8 * g), ld8(kr + 16 * st + 8 * g), sc);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) sc[e] = __builtin_amdgcn_exp2f(fmaf(sc[e], sl2, -cc0));
+    sm.lba[w][lane][0] = pack_b(sc, 0);
+    sm.lba[w][lane][1] = pack_b(sc, 1);
+  }
+  // row tile k (k = 0 .. n-1) is chunk I = NT-1-k, published once the counter exceeds k.
+  // Tiles k < nfar lie beyond the large chunk (swept in pairs); the rest one per step.
+  const int n = NT - 1 - last, nfar = min(n, NT - 1 - ceJ);
+  const int nfs = (nfar + 1) / 2, nsteps = nfs + (n - nfar);
+  auto first_tile = [&](int s) { return s < nfs ? 2 * s : nfar + (s - nfs); };
+  auto need = [&](int s) { return s < nfs ? min(2 * s + 1, nfar - 1) : first_tile(s); };
   int plan_q[2], plan_t[2];
   dma_plan<64, 8>(64, plan_q);
   dma_plan<64, 8>(T, plan_t);
-  auto stage = [&](int pp) {  // tiles 2pp (and 2pp + 1 if below n) into buffer pp & 1
-    const int buf = pp & 1;
+  auto stage = [&](int s) {
+    const int buf = s & 1, k0 = first_tile(s);
+    if (s < nfs) {
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int k = 2 * pp + u;
-      if (k < n) {
-        const int I = NT - 1 - k;
-        const bf16* qsrc = (I <= ceJ) ? ws.qs + (((int64_t)bhq * PR + (J - (I / PR) * PR)) * T) * 64
-                                      : ws.qb + (((int64_t)bhq * NS + sJ) * T) * 64;
-        dma_stage<64, 8>(plan_q, qsrc + (int64_t)I * PC * 64, sm.u.st.q[buf][u]);
-        dma_stage<64, 8>(plan_t, bw.dvT + (int64_t)bhq * 64 * T + I * PC, sm.u.st.d[buf][u]);
+      for (int u = 0; u < 2; ++u) {
+        const int k = k0 + u;
+        if (k < nfar) {
+          const int I = NT - 1 - k;
+          dma_stage<64, 8>(plan_q, ws.qb + (((int64_t)bhq * NS + sJ) * T + (int64_t)I * PC) * 64, sm.u.st.q[buf][u]);
+          dma_stage<64, 8>(plan_t, bw.dvT + (int64_t)bhq * 64 * T + I * PC, sm.u.st.d[buf][u]);
+        }
+      }
+    } else {
+      const int I = NT - 1 - k0;
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+        if (c == 0 || hasB) dma_stage<64, 8>(plan_q, qs_slot(c) + (int64_t)I * PC * 64, sm.u.st.q[buf][c]);
+      dma_stage<64, 8>(plan_t, bw.dvT + (int64_t)bhq * 64 * T + I * PC, sm.u.st.d[buf][0]);
+    }
+  };
+  // Y_A, Y_B (fp32) are fetched into registers during the last step
+  f32x4 yr[8];
+  auto yload = [&]() {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int c = u >> 2;
+      if (c == 0 || hasB)
+        yr[u] = *reinterpret_cast<const f32x4*>(ws.y + ((int64_t)bhq * NT + A + c) * 4096 + 4 * (tid + 256 * (u & 3)));
+    }
+  };
+  auto ystore_t = [&](int c) {
+#pragma unroll
+    for (int u = 4 * c; u < 4 * c + 4; ++u) {
+      const int f = 4 * (tid + 256 * (u & 3)), r = f >> 6, c4 = f & 63;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sm.u.fin.Yt[c4 + e][r] = yr[u][e];
+    }
+  };
+  // one staged 64-row tile against this wave's 32 columns
+  auto tile = [&](const bf16* qt, const bf16* dtl, bool same) {
+#pragma unroll
+    for (int rh = 0; rh < 2; ++rh) {
+      f32x16 sc = zero16();
+#pragma unroll
+      for (int st = 0; st < 4; ++st) sc = mfma32(ld8(swz<8>(qt, rh * 32 + l32, 2 * st + g)), same ? kbs[st] : kbf[st], sc);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sc[e] = __builtin_amdgcn_exp2f(fmaf(sc[e], sl2, -cc0));
+      const bf16x8 p0 = pack_b(sc, 0), p1 = pack_b(sc, 1);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        acc[t] = mfma32(ld8(swz<8>(dtl, t * 32 + l32, 4 * rh + g)), p0, acc[t]);
+        acc[t] = mfma32(ld8(swz<8>(dtl, t * 32 + l32, 4 * rh + 2 + g)), p1, acc[t]);
       }
     }
   };
-  auto need = [&](int pp) { return min(2 * pp + 1, n - 1); };
-  // Y_J (fp32) is fetched into registers during the last pair
-  f32x4 yr[4];
-  auto yload = [&]() {
-    const float* src = ws.y + ((int64_t)bhq * NT + J) * 4096;
-#pragma unroll
-    for (int u = 0; u < 4; ++u) yr[u] = *reinterpret_cast<const f32x4*>(src + 4 * (tid + 256 * u));
-  };
-  auto tile = [&](int buf, int u, bool same) {
-    f32x16 sc = zero16();
-#pragma unroll
-    for (int st = 0; st < 4; ++st)
-      sc = mfma32(ld8(swz<8>(sm.u.st.q[buf][u], ih * 32 + l32, 2 * st + g)), same ? kbs[st] : kbf[st], sc);
-#pragma unroll
-    for (int e = 0; e < 16; ++e) sc[e] = __builtin_amdgcn_exp2f(fmaf(sc[e], sl2, -cc0));
-    const bf16x8 p0 = pack_b(sc, 0), p1 = pack_b(sc, 1);
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      acc[t] = mfma32(ld8(swz<8>(sm.u.st.d[buf][u], t * 32 + l32, 4 * ih + g)), p0, acc[t]);
-      acc[t] = mfma32(ld8(swz<8>(sm.u.st.d[buf][u], t * 32 + l32, 4 * ih + 2 + g)), p1, acc[t]);
-    }
-  };
   int ready = 0;
-  if (npair > 0) {
+  if (nsteps > 0) {
     ready = wait_counter_gt(cnt, need(0));
     stage(0);
     dma_wait();
@@ -155,13 +206,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
     yload();
   }
   __syncthreads();
-  for (int pp = 0; pp < npair; ++pp) {
-    const int buf = pp & 1;
-    const bool more = pp + 1 < npair;
-    const bool two = 2 * pp + 1 < n;
+  for (int s = 0; s < nsteps; ++s) {
+    const int buf = s & 1;
+    const bool more = s + 1 < nsteps;
     bool early = false;
     if (more) {
-      const int nd = need(pp + 1);
+      const int nd = need(s + 1);
       if (nd >= ready) {
         const int seen = poll_counter(cnt);
         if (seen > nd) {
@@ -170,64 +220,51 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
         }
       }
       early = nd < ready;
-      if (early) stage(pp + 1);
+      if (early) stage(s + 1);
     } else {
       yload();
     }
-    tile(buf, 0, NT - 1 - 2 * pp <= ceJ);
-    if (two) tile(buf, 1, NT - 2 - 2 * pp <= ceJ);
+    if (s < nfs) {
+      tile(sm.u.st.q[buf][0], sm.u.st.d[buf][0], false);
+      if (2 * s + 1 < nfar) tile(sm.u.st.q[buf][1], sm.u.st.d[buf][1], false);
+    } else {
+      tile(sm.u.st.q[buf][mycols ? wc : 0], sm.u.st.d[buf][0], true);
+    }
     if (more && !early) {
-      ready = wait_counter_gt(cnt, need(pp + 1));
-      stage(pp + 1);
+      ready = wait_counter_gt(cnt, need(s + 1));
+      stage(s + 1);
     }
     dma_wait();
     __syncthreads();
   }
-  // ---- R = dO_J - acc; Y^T to LDS (the staging space is free from here) ----
-  float(*Rt)[68] = sm.u.fin.Rt;
+  // ---- R^T = -acc (Rt columns = columns of the workgroup); Y_B^T to LDS ----
+  float(*Rt)[132] = sm.u.fin.Rt;
   float(*Yt)[68] = sm.u.fin.Yt;
-  if (ih == 1) {
+  if (mycols) {
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][ch * 32 + l32] = acc[t][e];
+      for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][w * 32 + l32] = -acc[t][e];
   }
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int f = 4 * (tid + 256 * u), r = f >> 6, c4 = f & 63;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) Yt[c4 + e][r] = yr[u][e];
-  }
+  ystore_t(hasB ? 1 : 0);
   __syncthreads();
-  if (ih == 0) {
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        float& x = Rt[t * 32 + drow(e, g)][ch * 32 + l32];
-        x = -(acc[t][e] + x);
-      }
-  }
-  __syncthreads();
-  // ---- dV^T[d][c] = sum_r R^T[d][r] Y[r][c]  (Y lower: r >= c) ----
-  f32x16 dvo;
+  // dV^T[d][c] = sum_r R^T[d][r] Y[r][c] for chunk cc (Y lower: r >= c); wave -> (d tile, column half)
   const int dt = w >> 1, chh = w & 1;
-  {
-    dvo = zero16();
+  auto diag_solve = [&](int cc) {
+    f32x16 dvo = zero16();
     for (int st = chh ? 2 : 0; st < 4; ++st) {
       bf16x8 ah, al, bh8, bl;
-      split8(&Rt[dt * 32 + l32][16 * st + 8 * g], ah, al);
+      split8(&Rt[dt * 32 + l32][cc * 64 + 16 * st + 8 * g], ah, al);
       split8(&Yt[chh * 32 + l32][16 * st + 8 * g], bh8, bl);
       dvo = mfma32(ah, bh8, dvo);
       dvo = mfma32(ah, bl, dvo);
       dvo = mfma32(al, bh8, dvo);
     }
     const int cl = chh * 32 + l32;
-    const int r = j0 + cl;
-    const int lslot = (cl & ~15) | jmap(cl & 15);
+    const int r = j0 + cc * 64 + cl;
+    const int lslot = cc * 64 + ((cl & ~15) | jmap(cl & 15));
     float* of = bw.dvf + ((int64_t)bhq * T + r) * 64;
     bf16* ob = bw.dvb + ((int64_t)bhq * T + r) * 64;
-    bf16* dt_l = sm.u.fin.dt;
 #pragma unroll
     for (int qq = 0; qq < 4; ++qq) {
       const int d0 = dt * 32 + 8 * qq + 4 * g;
@@ -237,32 +274,72 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
       for (int u = 0; u < 4; ++u) {
         f[u] = dvo[4 * qq + u];
         bb[u] = (bf16)f[u];
-        dt_l[(d0 + u) * 64 + lslot] = bb[u];
+        sm.u.fin.dt[d0 + u][lslot] = bb[u];
       }
       *reinterpret_cast<f32x4*>(of + d0) = f;
       *reinterpret_cast<bf16x4*>(ob + d0) = bb;
     }
-  }
-  __syncthreads();
-  for (int c = tid; c < 64 * 8; c += 256) {  // dV^T to the chain operand with 16-byte stores
-    const int dd = c >> 3, s8 = (c & 7) * 8;
-    *reinterpret_cast<bf16x8*>(bw.dvT + ((int64_t)bhq * 64 + dd) * T + j0 + s8) = ld8(sm.u.fin.dt + dd * 64 + s8);
-  }
-  publish_counter(cnt, NT - J);
-  // ---- dA_diag = -s (dV_J O_J^T) * L_diag  (every read of Rt / Yt came before the last barrier) ----
+    return dvo;
+  };
+  // dV^T of chunk cc to the chain operand with 16-byte stores, then publish it
+  auto publish_chunk = [&](int cc) {
+    __syncthreads();
+    for (int c = tid; c < 64 * 8; c += 256) {
+      const int dd = c >> 3, s8 = (c & 7) * 8;
+      *reinterpret_cast<bf16x8*>(bw.dvT + ((int64_t)bhq * 64 + dd) * T + j0 + cc * 64 + s8) =
+          ld8(&sm.u.fin.dt[dd][cc * 64 + s8]);
+    }
+    publish_counter(cnt, NT - (A + cc));
+  };
+  f32x16 dvoB = zero16();
+  if (hasB) {
+    dvoB = diag_solve(1);
+    publish_chunk(1);
+    // ---- R_A -= L_BA^T dV_B: wave -> (A columns half na, B rows half kb); Y_A^T to LDS ----
+    const int na = w & 1, kb = w >> 1;
+    const bf16x8 l0 = sm.lba[w][lane][0], l1 = sm.lba[w][lane][1];
+    f32x16 cr[2];
 #pragma unroll
-  for (int e = 0; e < 16; ++e) Rt[chh * 32 + l32][dt * 32 + drow(e, g)] = dvo[e];  // Rt <- dV rows
-  load_rows64_f32(Yt, o + b * os.b + hq * os.h + (int64_t)j0 * os.t, os.t);       // Yt <- O rows
-  __syncthreads();
-  {
-    const f32x16 a = mgemm64<false, true>(Rt, Yt, zero16());
-    const float* ldp = ws.ld + ((int64_t)bhq * NT + J) * 4096;
-    float* dst = bw.dad + ((int64_t)bhq * NT + J) * 4096;
+    for (int t = 0; t < 2; ++t) {
+      cr[t] = mfma32(ld8(&sm.u.fin.dt[t * 32 + l32][64 + kb * 32 + 8 * g]), l0, zero16());
+      cr[t] = mfma32(ld8(&sm.u.fin.dt[t * 32 + l32][64 + kb * 32 + 16 + 8 * g]), l1, cr[t]);
+    }
+    const int col = na * 32 + l32;
+    if (kb == 1) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][col] -= cr[t][e];
+    }
+    ystore_t(0);
+    __syncthreads();
+    if (kb == 0) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][col] -= cr[t][e];
+    }
+    __syncthreads();
+  }
+  const f32x16 dvoA = diag_solve(0);
+  publish_chunk(0);
+  // ---- dA_diag = -s (dV_J O_J^T) * L_diag per chunk (every read of Rt / Yt came before the last barrier) ----
+  float(*Dr)[68] = reinterpret_cast<float(*)[68]>(&sm.u.fin.Rt[0][0]);  // dV rows of the chunk
+  for (int cc = 0; cc < (hasB ? 2 : 1); ++cc) {
+    const f32x16 dvo = cc ? dvoB : dvoA;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) Dr[chh * 32 + l32][dt * 32 + drow(e, g)] = dvo[e];
+    load_rows64_f32(Yt, o + b * os.b + hq * os.h + (int64_t)(j0 + cc * 64) * os.t, os.t);  // Yt <- O rows
+    __syncthreads();
+    const f32x16 a = mgemm64<false, true>(Dr, Yt, zero16());
+    const float* ldp = ws.ld + ((int64_t)bhq * NT + A + cc) * 4096;
+    float* dst = bw.dad + ((int64_t)bhq * NT + A + cc) * 4096;
     const int cl = dl_col();
     DL_FOR_E {
       const int rr = dl_row(e);
       dst[rr * 64 + cl] = -scale * a[e] * ldp[rr * 64 + cl];
     }
+    __syncthreads();
   }
 }
 

@@ -239,7 +239,7 @@ int lucid_path_bwd(const void* dout, const int64_t* do_strides, const void* q, c
   const int64_t n_hl = (int64_t)BHq * NS * 4096, n_hc = (int64_t)BHq * NT * 4096;
   const lucid::Strides dvs{(int64_t)HQ * T * 64, (int64_t)T * 64, 64};  // dV rows [B][HQ][T][64]
   LUCID_TIMED_LAUNCH(phip, "path_bwd_zero_kernel", lucid::path_bwd_zero_kernel, dim3(1024), st, n_hl, n_hc, BHq, bw);
-  LUCID_TIMED_LAUNCH(phip, "path_dv_kernel", lucid::path_dv_kernel, dim3(NT * BHq), st, (const bf16*)dout, PS(do_strides),
+  LUCID_TIMED_LAUNCH(phip, "path_dv_kernel", lucid::path_dv_kernel, dim3(((NT + 1) / 2) * BHq), st, (const bf16*)dout, PS(do_strides),
                      (const bf16*)o, PS(o_strides), HQ, H, T, BHq, scale, ws, bw);
   LUCID_TIMED_LAUNCH(phip, "path_bwd_row_kernel", lucid::path_bwd_row_kernel<false>, dim3(BHq, (NT + 1) / 2), st,
                      (const bf16*)bw.dvb, dvs, (const bf16*)o, PS(o_strides), HQ, H, T, scale, ws, bw);
