@@ -32,7 +32,9 @@ def _f64(x):
     return x.detach().cpu().double()
 
 
-@pytest.mark.parametrize("B,T,H,G", [(1, 256, 2, 1), (1, 1024, 1, 2), (2, 640, 1, 1), (1, 200, 1, 1)])
+@pytest.mark.parametrize("B,T,H,G", [(1, 256, 2, 1), (1, 1024, 1, 2), (2, 640, 1, 1), (1, 200, 1, 1),
+                                     (1, 64, 1, 1),    # one chunk: a chain workgroup with no earlier keys
+                                     (1, 576, 1, 2)])  # 9 chunks: the last workgroup holds one chunk
 def test_path_forward_matches_oracle(B, T, H, G):
     from lucid_amd.lucid_path import parallel_lucid_path_attention
     q, k, v, w, beta, _ = _inputs(B, T, H, G, seed=T + G)
@@ -84,7 +86,9 @@ def test_path_full_size_residual():
 
 
 @pytest.mark.parametrize("B,T,H,G", [(1, 256, 2, 1), (1, 1024, 1, 2), (2, 640, 1, 1), (1, 200, 1, 1),
-                                     (1, 576, 1, 1)])  # 9 chunks: an odd chunk count spanning two large chunks
+                                     (1, 576, 1, 1),   # 9 chunks: an odd chunk count spanning two large chunks
+                                     (1, 64, 1, 1),    # one chunk: nothing to sweep in either chain
+                                     (1, 192, 1, 1)])  # 3 chunks: a one-chunk chain tail, one in-chunk row tile
 def test_path_backward_matches_oracle(B, T, H, G):
     from lucid_amd.lucid_path import parallel_lucid_path_attention
     q, k, v, w, beta, do = _inputs(B, T, H, G, seed=3 * T + G)
