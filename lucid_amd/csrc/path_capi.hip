@@ -124,7 +124,7 @@ int launch_front(const void* q, const int64_t* q_strides, const void* k, const i
                      (const bf16*)k, PS(k_strides), (const bf16*)w, PS(w_strides), (const bf16*)beta,
                      PS(beta_strides), HQ, H, T, scale, softmax, ws);
   LUCID_TIMED_LAUNCH(phip, "path_large_kernel", lucid::path_large_kernel, dim3(NS, BH), st, T, ws);
-  LUCID_TIMED_LAUNCH(phip, "path_transport_kernel", lucid::path_transport_kernel, dim3(BHq, NT), st, HQ, H, T, ws);
+  LUCID_TIMED_LAUNCH(phip, "path_transport_kernel", lucid::path_transport_kernel, dim3(BHq, (NT + 1) / 2), st, HQ, H, T, ws);
   return 0;
 }
 

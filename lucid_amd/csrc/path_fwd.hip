@@ -13,7 +13,7 @@
 //   path_chunk_kernel      per (chunk, query head): WY form T_inv, W2, Hc = I - W^T W2,
 //                          q~, k~, L_diag and Y = (I + L_diag)^-1   (fp32, LDS)
 //   path_large_kernel      per (large chunk, kv head): SUF_c, HL_s and KL = k~ SUF^T
-//   path_transport_kernel  per (chunk, query head): QS and QB (MFMA, 3-term bf16 split)
+//   path_transport_kernel  per (pair of chunks, query head): QS and QB (MFMA, 3-term bf16 split)
 //   path_solve_fwd_kernel  chained solve per query head (chain counters as in LUCID)
 //   path_kcache_kernel     k_cache = keys carried to the sequence end (use_cache)
 #include "path_common.h"
@@ -222,45 +222,58 @@ __global__ __launch_bounds__(256) void path_large_kernel(int T, PathFwdWs ws) {
 
 // ---------------------------------------------------------------------------
 // Query transport (transform_q.py:15-61): x = q~_I; QS slots for chunks of I's large
-// chunk below I, then QB for every earlier large chunk.  grid (B*HQ, NT): the work of a
-// chunk grows with I, so the late chunks of every head are dispatched first.
+// chunk below I, then QB for every earlier large chunk.  One workgroup per pair of
+// chunks A = 2p, B = 2p + 1 (one large chunk holds both) of one query head: B's
+// sequence of transition matrices is A's with Hc_A in front, so after that one step
+// the two 64-row blocks are carried together, each matrix loaded, transposed and
+// synchronised once for 128 rows, and both blocks' rows (adjacent in T) emitted to
+// the same slot.  grid (B*HQ, ceil(NT/2)): the work of a pair grows with p, so the
+// late pairs of every head are dispatched first.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void path_transport_kernel(int HQ, int H, int T, PathFwdWs ws) {
-  __shared__ __attribute__((aligned(16))) float X[64][68];
+  __shared__ __attribute__((aligned(16))) float X[128][68];  // rows 0..63 = chunk A, 64..127 = chunk B
   __shared__ __attribute__((aligned(16))) float MT[64][68];
-  const int I = (int)gridDim.y - 1 - (int)blockIdx.y, bhq = blockIdx.x;
+  const int p = (int)gridDim.y - 1 - (int)blockIdx.y, bhq = blockIdx.x;
   const int NT = T / PC, NS = (NT + PR - 1) / PR;
   const int G = HQ / H;
   const int b = bhq / HQ, hq = bhq - b * HQ, bh = b * H + hq / G;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 5, l32 = lane & 31;
-  const int sI = I / PR, cb = sI * PR;
+  const int A = 2 * p;
+  const bool hasB = A + 1 < NT;
+  const int sI = A / PR, cb = sI * PR;
   {
-    const float* src = ws.qt + ((int64_t)bhq * T + I * PC) * 64;
-    for (int idx = tid; idx < 4096; idx += 256) X[idx >> 6][idx & 63] = src[idx];
+    const float* src = ws.qt + ((int64_t)bhq * T + A * PC) * 64;  // A's and B's rows are adjacent
+    for (int idx = tid; idx < (hasB ? 8192 : 4096); idx += 256) X[idx >> 6][idx & 63] = src[idx];
   }
-  __syncthreads();
-  // rows of X -> bf16 rows at dst (row stride 64)
-  auto emit = [&](bf16* dst) {
-    const int r = tid >> 2, cc = (tid & 3) * 16;
+  // rows r0 .. r0 + 64 * nblk of X -> bf16 rows at dst (row stride 64)
+  auto emit = [&](bf16* dst, int r0, int nblk) {
+    const int cc = (tid & 3) * 16;
+    for (int r = r0 + (tid >> 2); r < r0 + 64 * nblk; r += 64) {
 #pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-      bf16x8 v;
+      for (int hh = 0; hh < 2; ++hh) {
+        bf16x8 v;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = (bf16)X[r][cc + 8 * hh + e];
-      *reinterpret_cast<bf16x8*>(dst + (int64_t)r * 64 + cc + 8 * hh) = v;
+        for (int e = 0; e < 8; ++e) v[e] = (bf16)X[r][cc + 8 * hh + e];
+        *reinterpret_cast<bf16x8*>(dst + (int64_t)r * 64 + cc + 8 * hh) = v;
+      }
     }
   };
-  // steps k = 0 .. nq-1 carry X through Hc_{I-1} .. Hc_cb (emitting QS), steps nq .. nq+sI-1
-  // through HL_{sI-1} .. HL_0 (emitting QB).  The transition matrix of step k+1 is loaded
-  // into registers while step k computes, so no step waits for its operand.
-  const int nq = I - cb, nsteps = nq + sI;
-  auto mat = [&](int k) {
-    return (k < nq) ? ws.hc + ((int64_t)bh * NT + (I - 1 - k)) * 4096
-                    : ws.hl + ((int64_t)bh * NS + (sI - 1 - (k - nq))) * 4096;
+  // joint steps j = 0 .. nq-1 carry X through Hc_{A-1} .. Hc_cb (emitting QS), steps
+  // nq .. nq+sI-1 through HL_{sI-1} .. HL_0 (emitting QB).  The transition matrix of the
+  // next step is loaded into registers while a step computes, so no step waits for it.
+  const int nq = A - cb, nsteps = nq + sI;
+  auto mat = [&](int j) {  // j = -1: Hc_A, B's own first step
+    return (j < nq) ? ws.hc + ((int64_t)bh * NT + (A - 1 - j)) * 4096
+                    : ws.hl + ((int64_t)bh * NS + (sI - 1 - (j - nq))) * 4096;
+  };
+  auto slot = [&](int j) {  // destination of the rows emitted before step j (row 0 = chunk A's first row)
+    return ((j < nq) ? ws.qs + (((int64_t)bhq * PR + (A - 1 - j - cb)) * T) * 64
+                     : ws.qb + (((int64_t)bhq * NS + (sI - 1 - (j - nq))) * T) * 64) +
+           (int64_t)A * PC * 64;
   };
   f32x4 mr[4];  // thread t holds M[r][c4 .. c4+3], r = (t + 256 u) / 16, c4 = 4 ((t + 256 u) % 16)
-  auto mload = [&](int k) {
-    const float* M = mat(k);
+  auto mload = [&](int j) {
+    const float* M = mat(j);
 #pragma unroll
     for (int u = 0; u < 4; ++u) mr[u] = *reinterpret_cast<const f32x4*>(M + 4 * (tid + 256 * u));
   };
@@ -272,21 +285,40 @@ __global__ __launch_bounds__(256) void path_transport_kernel(int HQ, int H, int 
       for (int e = 0; e < 4; ++e) MT[c4 + e][r] = mr[u][e];
     }
   };
-  if (nsteps > 0) {
-    mload(0);
+  const int dt = w >> 1, rt = w & 1;  // this wave's output tiles: (dt, rt) of A and (dt, rt + 2) of B
+  if (hasB) {
+    // B's own first step: emit to QS slot A - cb, then X_B <- X_B Hc_A
+    mload(-1);
     mstore_t();
-  }
-  __syncthreads();
-  for (int k = 0; k < nsteps; ++k) {
-    if (k + 1 < nsteps) mload(k + 1);
-    emit(k < nq ? ws.qs + (((int64_t)bhq * PR + (I - 1 - k - cb)) * T + I * PC) * 64
-                : ws.qb + (((int64_t)bhq * NS + (sI - 1 - (k - nq))) * T + I * PC) * 64);
-    const int dt = w >> 1, rt = w & 1;
-    const f32x16 o = mat_xM_tile(X, MT, dt, rt);
+    __syncthreads();
+    emit(ws.qs + (((int64_t)bhq * PR + (A - cb)) * T) * 64 + (int64_t)A * PC * 64, 64, 1);
+    if (nsteps > 0) mload(0);
+    const f32x16 o = mat_xM_tile(X, MT, dt, rt + 2);
     __syncthreads();
 #pragma unroll
-    for (int e = 0; e < 16; ++e) X[rt * 32 + l32][dt * 32 + drow(e, g)] = o[e];
-    if (k + 1 < nsteps) mstore_t();
+    for (int e = 0; e < 16; ++e) X[(rt + 2) * 32 + l32][dt * 32 + drow(e, g)] = o[e];
+    if (nsteps > 0) mstore_t();
+    __syncthreads();
+  } else if (nsteps > 0) {
+    mload(0);
+    mstore_t();
+    __syncthreads();
+  }
+  const int nblk = hasB ? 2 : 1;
+  for (int j = 0; j < nsteps; ++j) {
+    if (j + 1 < nsteps) mload(j + 1);
+    emit(slot(j), 0, nblk);
+    const f32x16 o0 = mat_xM_tile(X, MT, dt, rt);
+    f32x16 o1 = zero16();
+    if (hasB) o1 = mat_xM_tile(X, MT, dt, rt + 2);
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < 16; ++e) X[rt * 32 + l32][dt * 32 + drow(e, g)] = o0[e];
+    if (hasB) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) X[(rt + 2) * 32 + l32][dt * 32 + drow(e, g)] = o1[e];
+    }
+    if (j + 1 < nsteps) mstore_t();
     __syncthreads();
   }
 }
