@@ -38,6 +38,7 @@ struct FwdWs {
   bf16* vpb;     // [BH][T][D]  V' bf16
   bf16* vpt;     // [BH][D][T]  V'^T, T-perm
   float* pinv;   // [BH][T/64][64][64]  inverses of the diagonal blocks of P
+  float* zx;     // [BH][T/128][64][64] -(X_B P_BA) per 128-row block, columns T-perm
   int* counters; // [BH]
   size_t bytes;
 };
@@ -57,6 +58,7 @@ FwdWs carve_fwd(void* base, int B, int Hkv, int T, int D) {
   w.vpb = reinterpret_cast<bf16*>(take(BH * T * D * 2));
   w.vpt = reinterpret_cast<bf16*>(take(BH * D * T * 2));
   w.pinv = reinterpret_cast<float*>(take(BH * (T / 64) * 4096 * 4));
+  w.zx = reinterpret_cast<float*>(take(BH * (T / 128) * 4096 * 4));
   w.counters = reinterpret_cast<int*>(take(BH * 4));
   w.bytes = off;
   return w;
@@ -126,9 +128,11 @@ int launch_precond_fwd(const void* k, const int64_t* ks, const void* v, const in
   const int BH = B * Hkv;
   LUCID_LAUNCH("lucid_prep_kernel", lucid::lucid_prep_kernel<D>, dim3(T / 64, BH), st, (const bf16*)k, S(ks), Hkv,
                T, eps, scale, w.rinv, w.kt, w.pinv, w.counters);
+  LUCID_LAUNCH("lucid_zx_kernel", lucid::lucid_zx_kernel<D>, dim3(T / 128, BH), st, (const bf16*)k, S(ks), Hkv, T,
+               w.rinv, scale, w.pinv, w.zx);
   LUCID_LAUNCH("lucid_precond_fwd_kernel", lucid::lucid_precond_fwd_kernel<D>, dim3((T / 128) * BH), st,
                (const bf16*)k, S(ks), (const bf16*)v, S(vs), Hkv, T, BH, w.rinv, scale, vprime, w.vpb, w.vpt,
-               w.pinv, w.counters);
+               w.pinv, w.zx, w.counters);
   return LUCID_OK;
 }
 

@@ -90,6 +90,65 @@ __global__ __launch_bounds__(256) void lucid_prep_kernel(const bf16* __restrict_
 }
 
 // ---------------------------------------------------------------------------
+// zx = -(X_B P_BA) for every 128-row chain block (A = its first 64 rows, B = the
+// last 64; X_B = the inverse of P's diagonal block B from lucid_prep_kernel,
+// P_BA[m][c] = exp(s r_m r_c K_m.K_c - 1/s)), 3-term bf16 split products, columns in
+// T-perm order so that the chain can add zx V'_A straight from its bf16 V'_A tile.
+// wave -> 32x32 quadrant.  grid (T/128, B*Hkv)
+// ---------------------------------------------------------------------------
+template <int D>
+__global__ __launch_bounds__(256) void lucid_zx_kernel(const bf16* __restrict__ k, Strides ks, int Hkv, int T,
+                                                       const float* __restrict__ rinv, float scale,
+                                                       const float* __restrict__ pinv, float* __restrict__ zx) {
+  constexpr int NKS = D / 16;
+  __shared__ __attribute__((aligned(16))) float Xb[64][68];
+  __shared__ __attribute__((aligned(16))) float PT[64][68];  // PT[c][m] = P_BA[m][c]
+  const int blk = blockIdx.x, bh = blockIdx.y;
+  const int b = bh / Hkv, h = bh - b * Hkv;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int g = lane >> 5, l32 = lane & 31;
+  const int tm = w >> 1, tn = w & 1;
+  const bf16* kp = k + b * ks.b + h * ks.h + (int64_t)blk * 128 * ks.t;  // A rows; B rows from 64 on
+  const float* rv = rinv + (int64_t)bh * T + blk * 128;
+  const float* xb = pinv + ((int64_t)bh * (T / 64) + 2 * blk + 1) * 4096;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int f = 4 * (tid + 256 * u);
+    *reinterpret_cast<f32x4*>(&Xb[f >> 6][f & 63]) = *reinterpret_cast<const f32x4*>(xb + f);
+  }
+  {
+    const float sl2 = scale * LOG2E_F;
+    const float c0 = LOG2E_F / scale;
+    f32x16 sd = zero16();
+#pragma unroll
+    for (int st = 0; st < NKS; ++st)
+      sd = mfma32(ld8(kp + (int64_t)(64 + tm * 32 + l32) * ks.t + 16 * st + 8 * g),
+                  ld8(kp + (int64_t)(tn * 32 + l32) * ks.t + 16 * st + 8 * g), sd);
+    const int cc = tn * 32 + l32;
+    const float ac = sl2 * rv[cc];
+    float rm[16];
+    load_rows16(rv + 64 + tm * 32, g, rm);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) PT[cc][tm * 32 + drow(e, g)] = __builtin_amdgcn_exp2f(fmaf(sd[e] * ac, rm[e], -c0));
+  }
+  __syncthreads();
+  f32x16 z = zero16();
+#pragma unroll
+  for (int st = 0; st < 4; ++st) {
+    bf16x8 ah, al, bh8, bl;
+    split8(&Xb[tm * 32 + l32][16 * st + 8 * g], ah, al);
+    split8(&PT[tn * 32 + l32][16 * st + 8 * g], bh8, bl);
+    z = mfma32(ah, bh8, z);
+    z = mfma32(ah, bl, z);
+    z = mfma32(al, bh8, z);
+  }
+  const int cc = tn * 32 + l32, slot = (cc & ~15) | jmap(cc & 15);
+  float* zo = zx + ((int64_t)bh * (T / 128) + blk) * 4096 + slot;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) zo[(tm * 32 + drow(e, g)) * 64] = -z[e];
+}
+
+// ---------------------------------------------------------------------------
 // Chained preconditioner solve, 128 rows per workgroup made of two 64-row
 // sub-blocks A (rows i0..i0+63) and B (i0+64..i0+127).
 // Workgroup id -> (i2 = id / BH, bh = id % BH): ids grow with i2, so every
@@ -103,12 +162,12 @@ __global__ __launch_bounds__(256) void lucid_prep_kernel(const bf16* __restrict_
 // wave w: ih = w & 1 -> rows i0 + 64*ih .. +64 (two 32-row n-tiles, lane <-> row)
 //         kh = w >> 1 -> the 64-key tile 2*pair + kh of every staged pair
 //   acc^T[d][i] += V'^T[d][j] P^T[j][i],  P^T[j][i] = exp(s r_i r_j K_j.K_i - 1/s)
-// (the kh = 0 accumulators start at -V^T).  Then V'_A = X_A R_A,
-// V'_B = X_B (R_B - P_BA V'_A), R = V - acc, with X = P_diag^-1 (fp32, from
-// lucid_prep_kernel) applied through a 3-term bf16 split (hi*hi + hi*lo + lo*hi).
-// The chain's critical path is the work after the last pair becomes visible, so
-// everything that does not depend on it (V, P_BA, the two inverses) is loaded
-// or computed earlier.  At d = 64 two workgroups share a CU (LDS <= 80 KB,
+// (the kh = 0 accumulators start at -V^T).  Then V'_A = X_A R_A and
+// V'_B = X_B R_B + Z V'_A with Z = -(X_B P_BA), R = V - acc, X = P_diag^-1 (fp32, both
+// from lucid_prep_kernel) applied through a 3-term bf16 split (hi*hi + hi*lo + lo*hi),
+// Z through a 2-term split against bf16 V'_A.  The chain's critical path is the work
+// after the last pair becomes visible, so everything that does not depend on it (V,
+// the two inverses, Z) is loaded earlier.  At d = 64 two workgroups share a CU (LDS <= 80 KB,
 // <= 256 registers per lane) so that one's MFMA work overlaps the other's exp.
 // ---------------------------------------------------------------------------
 template <int D>
@@ -125,14 +184,13 @@ struct PfwdSmem {
       bf16 vT[D][128 + 8];  // V'^T of the block (bf16, T-perm within 16-groups)
     } fin;
   } u;
-  bf16x8 pba[4][64][2];  // P_BA as MFMA B operands, per wave and lane
 };
 
 template <int D>
 __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond_fwd_kernel(
     const bf16* __restrict__ k, Strides ks, const bf16* __restrict__ v, Strides vs, int Hkv, int T, int BH,
     const float* __restrict__ rinv, float scale, float* __restrict__ vp32, bf16* __restrict__ vpb,
-    bf16* __restrict__ vpt, float* __restrict__ pinv, int* __restrict__ counters) {
+    bf16* __restrict__ vpt, float* __restrict__ pinv, const float* __restrict__ zx, int* __restrict__ counters) {
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
   __shared__ __attribute__((aligned(16))) PfwdSmem<D> sm;
@@ -176,23 +234,6 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
 #pragma unroll
         for (int u = 0; u < 4; ++u) acc[t][nt][4 * qd + u] = kh ? 0.f : -(float)vv[u];
       }
-  }
-  // P_BA for the B correction (keys of A half ka, rows of B half nb): depends on K only
-  {
-    const int nb = w & 1, ka = w >> 1;
-    const int rowB = i0 + 64 + nb * 32 + l32;
-    f32x16 sc = zero16();
-#pragma unroll
-    for (int st = 0; st < NKS; ++st)
-      sc = mfma32(ld8(kp + (int64_t)(i0 + ka * 32 + l32) * ks.t + 16 * st + 8 * g),
-                  ld8(kp + (int64_t)rowB * ks.t + 16 * st + 8 * g), sc);
-    const float aB = sl2 * rv[rowB];
-    float rA[16];
-    load_rows16(rv + i0 + ka * 32, g, rA);
-#pragma unroll
-    for (int e = 0; e < 16; ++e) sc[e] = __builtin_amdgcn_exp2f(fmaf(sc[e] * aB, rA[e], -c0));
-    sm.pba[w][lane][0] = pack_b(sc, 0);
-    sm.pba[w][lane][1] = pack_b(sc, 1);
   }
 
   // ---- off-diagonal sweep over the i2 earlier pairs of 64-key tiles ----
@@ -317,6 +358,17 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
           x = -(acc[t][nt][e] + x);
         }
   }
+  // Z rows of this wave's B output tiles (row half rh = w & 1), 8 columns per lane half and
+  // 16-column step, fetched while sub-block A is solved
+  f32x4 zr[4][2];
+  {
+    const float* zrow = zx + ((int64_t)bh * (T / 128) + i2) * 4096 + ((w & 1) * 32 + l32) * 64 + 8 * g;
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      zr[st][0] = *reinterpret_cast<const f32x4*>(zrow + 16 * st);
+      zr[st][1] = *reinterpret_cast<const f32x4*>(zrow + 16 * st + 4);
+    }
+  }
   __syncthreads();
 
   // V'^T[d][r] = sum_c R^T[d][c] X[r][c] for sub-block sb (X lower triangular)
@@ -332,6 +384,21 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
         o = mfma32(ah, bh8, o);
         o = mfma32(ah, bl, o);
         o = mfma32(al, bh8, o);
+      }
+      if (sb == 1) {  // + Z V'_A: V'_A^T from the bf16 T-perm tile, Z split into hi + lo
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+          bf16x8 zh, zl;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float x = zr[st][e >> 2][e & 3];
+            zh[e] = (bf16)x;
+            zl[e] = (bf16)(x - (float)zh[e]);
+          }
+          const bf16x8 va = ld8(&sm.u.fin.vT[dt * 32 + l32][16 * st + 8 * g]);
+          o = mfma32(va, zh, o);
+          o = mfma32(va, zl, o);
+        }
       }
       const int rl = rh * 32 + l32;
       const int r = i0 + sb * 64 + rl;
@@ -357,33 +424,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
   diag_solve(0);
   __syncthreads();
   xstore(1);
-
-  // ---- R_B -= P_BA V'_A: wave -> (B rows half nb, A keys half ka) ----
-  {
-    const int nb = w & 1, ka = w >> 1;
-    const bf16x8 pba0 = sm.pba[w][lane][0], pba1 = sm.pba[w][lane][1];
-    f32x16 cr[NDT];
-#pragma unroll
-    for (int t = 0; t < NDT; ++t) {
-      cr[t] = mfma32(ld8(&sm.u.fin.vT[t * 32 + l32][ka * 32 + 8 * g]), pba0, zero16());
-      cr[t] = mfma32(ld8(&sm.u.fin.vT[t * 32 + l32][ka * 32 + 16 + 8 * g]), pba1, cr[t]);
-    }
-    const int col = 64 + nb * 32 + l32;
-    if (ka == 1) {
-#pragma unroll
-      for (int t = 0; t < NDT; ++t)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][col] -= cr[t][e];
-    }
-    __syncthreads();
-    if (ka == 0) {
-#pragma unroll
-      for (int t = 0; t < NDT; ++t)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][col] -= cr[t][e];
-    }
-    __syncthreads();
-  }
+  __syncthreads();
   diag_solve(1);
   __syncthreads();
   // V'^T of the whole block to the T-perm operand copy: 16-byte stores

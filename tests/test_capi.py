@@ -47,8 +47,9 @@ def test_abi_version_and_workspace(built):
     lib = _lib.load()
     assert lib.lucid_abi_version() == 1
     ws = lib.lucid_fwd_workspace_bytes(1, 16, 16, 32768, 64)
-    # rinv + K^T + V' (bf16) + V'^T + diagonal inverses, each 256-byte aligned
-    expect = 16 * 32768 * 4 + 3 * 16 * 64 * 32768 * 2 + 16 * 512 * 4096 * 4 + 256
+    # rinv + K^T + V' (bf16) + V'^T + diagonal inverses + -(X_B P_BA) per 128-row block,
+    # each 256-byte aligned
+    expect = 16 * 32768 * 4 + 3 * 16 * 64 * 32768 * 2 + 16 * 512 * 4096 * 4 + 16 * 256 * 4096 * 4 + 256
     assert ws == expect
     assert lib.lucid_bwd_workspace_bytes(1, 16, 16, 32768, 64) > 0
 
