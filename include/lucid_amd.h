@@ -35,7 +35,8 @@ const char* lucid_last_error(void);
 
 /* Bytes of the forward workspace.  It holds the state the backward reuses
  * (1/rms of K, K^T and V' in MFMA operand layouts, the inverted 64x64
- * diagonal blocks of P, chain counters), so keep it alive until
+ * diagonal blocks of P, the in-block coupling of each 128-row chain block,
+ * chain counters), so keep it alive until
  * lucid_attn_bwd has been enqueued.  Workspaces must be 256-byte aligned
  * (hipMalloc and the torch allocator return such pointers). */
 size_t lucid_fwd_workspace_bytes(int B, int Hq, int Hkv, int T, int D);
