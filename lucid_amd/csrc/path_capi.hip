@@ -278,7 +278,7 @@ int lucid_path_softmax_fwd(const void* q, const int64_t* q_strides, const void* 
   const int NT = T / 64;
   if (int rc = launch_front(q, q_strides, k, k_strides, w, w_strides, beta, beta_strides, B, T, H, HQ, scale, 1, ws, st))
     return rc;
-  LUCID_TIMED_LAUNCH(phip, "path_softmax_fwd_kernel", lucid::path_softmax_fwd_kernel, dim3(B * HQ, (NT + 1) / 2), st,
+  LUCID_TIMED_LAUNCH(phip, "path_softmax_fwd_kernel", lucid::path_softmax_fwd_kernel, dim3(B * HQ, (NT + 3) / 4), st,
                      (const bf16*)v, PS(v_strides), (bf16*)o, PS(o_strides), HQ, H, T, scale, ws);
   if (kcache)
     if (int rc = launch_kcache(kcache, kcache_strides, B, T, H, ws, st)) return rc;

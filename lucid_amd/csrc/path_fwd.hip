@@ -613,36 +613,35 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
 // and the inter-chunk online softmax of parallel_path_fwd.py:54-124 in one kernel, on the
 // same two-level logit blocks as the solve above:
 //   O_i = sum_{j <= i} exp2(s' A_ij - lse_i) v_j,  s' = s log2(e)
-// Per pair of query chunks I1 = 2p, I1 + 1 (one large chunk); wave w owns rows 32w ..
-// of the pair (chunk Iw = I1 + w/2, lane <-> row, both lane halves hold the same row
-// and half of the keys).  The diagonal block reads the in-chunk logits; key chunks
-// J < Iw give S^T[j][i] = Kop_J . Qop_I^(J).  O^T[d][i] += V^T[d][j] P^T[j][i] with V^T
-// from transposing LDS reads.  Key-operand and V rows are staged by direct
-// global->LDS loads (double buffered).  The row log-sum-exp (exp2 domain) is kept
-// for the backward.  grid (B*HQ, (NT+1)/2), the pairs with the most key chunks (of all heads) first.
+// Per group of four query chunks I1 = 4p .. I1 + 3 (one large chunk); wave w owns chunk
+// Iw = I1 + w (two 32-row n-tiles, lane <-> row, both lane halves hold the same row and
+// half of the keys), so every staged key tile serves 256 rows.  The diagonal block reads
+// the in-chunk logits; key chunks J < Iw give S^T[j][i] = Kop_J . Qop_I^(J).
+// O^T[d][i] += V^T[d][j] P^T[j][i] with V^T from transposing LDS reads.  Key-operand and V
+// rows are staged by direct global->LDS loads (double buffered).  The row log-sum-exp
+// (exp2 domain) is kept for the backward.  grid (B*HQ, ceil(NT/4)), the groups with the
+// most key chunks (of all heads) first.
 // ---------------------------------------------------------------------------
 struct SoftmaxFwdSmem {
   bf16 k[2][64 * 64];   // swizzled (chunk c of row r at c ^ (r & 7))
   bf16 v[2][64 * 64];
-  bf16 vd[2][64 * 64];  // V rows of the pair's own chunks (diagonal blocks)
+  bf16 vd[4][64 * 64];  // V rows of the group's own chunks (diagonal blocks)
 };
 
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void path_softmax_fwd_kernel(
     const bf16* __restrict__ v, Strides vs, bf16* __restrict__ o, Strides os, int HQ, int H, int T, float scale,
     PathFwdWs ws) {
   __shared__ __attribute__((aligned(16))) SoftmaxFwdSmem sm;
-  const int NT = T / PC, NS = (NT + PR - 1) / PR, NP = (NT + 1) / 2;
-  const int I1 = 2 * (NP - 1 - (int)blockIdx.y), bhq = blockIdx.x;  // heaviest pairs of all heads first
+  const int NT = T / PC, NS = (NT + PR - 1) / PR, NQ = (NT + 3) / 4;
+  const int I1 = 4 * (NQ - 1 - (int)blockIdx.y), bhq = blockIdx.x;  // heaviest groups of all heads first
   const int G_ = HQ / H;
   const int b = bhq / HQ, hq = bhq - b * HQ, h = hq / G_, bh = b * H + h;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
-  const int Iw = I1 + (w >> 1);
-  const bool pair = I1 + 1 < NT;  // NT odd: the last pair has one chunk
+  const int Iw = I1 + w;
   const bool live = Iw < NT;
   const int sI = I1 / PR, cb = sI * PR;
-  const int rl = (w & 1) * 32 + l32;                   // this lane's row inside its chunk
-  const int iw0 = min(Iw, NT - 1) * PC + (w & 1) * 32;  // first row of this wave
-  const int nJ = pair ? I1 + 1 : I1;                   // key tiles needed by the pair
+  const int iw0 = min(Iw, NT - 1) * PC;         // first row of this wave
+  const int nJ = min(I1 + 3, NT - 1);           // key tiles needed by the group
   const float sl2 = scale * LOG2E_F;
   const bf16* vh = v + b * vs.b + h * vs.h;
 
@@ -654,15 +653,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
     dma_stage<64, 8>(plan_k, ((J < cb) ? ws.kl : ws.kt) + ((int64_t)bh * T + J * PC) * 64, sm.k[buf]);
     dma_stage<64, 8>(plan_v, vh + (int64_t)J * PC * vs.t, sm.v[buf]);
   };
-  dma_stage<64, 8>(plan_v, vh + (int64_t)I1 * PC * vs.t, sm.vd[0]);
-  if (pair) dma_stage<64, 8>(plan_v, vh + (int64_t)(I1 + 1) * PC * vs.t, sm.vd[1]);
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+    if (I1 + c < NT) dma_stage<64, 8>(plan_v, vh + (int64_t)(I1 + c) * PC * vs.t, sm.vd[c]);
   if (nJ > 0) stage(0);
 
-  f32x16 acc[2] = {zero16(), zero16()};
-  float m = 0.f, l = 0.f;
-  f32x16 sc[2];
-  if (live) {  // in-chunk logits of row rl, keys j = 32 jh + drow(e, g); keys j > rl are masked
+  f32x16 acc[2][2];
+  float m[2] = {0.f, 0.f}, l[2] = {0.f, 0.f};
+  dma_wait();
+  __syncthreads();
+  // the diagonal block first, one n-tile at a time: in-chunk logits of row rl, keys
+  // j = 32 jh + drow(e, g); keys j > rl are masked
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    acc[nt][0] = zero16();
+    acc[nt][1] = zero16();
+    if (!live) continue;
+    const int rl = nt * 32 + l32;
     const float* ad = ws.ld + ((int64_t)bhq * NT + Iw) * 4096 + rl * 64;
+    f32x16 sd[2];
 #pragma unroll
     for (int jh = 0; jh < 2; ++jh)
 #pragma unroll
@@ -671,38 +680,32 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           const int j = jh * 32 + 8 * qq + 4 * g + u;
-          sc[jh][4 * qq + u] = (j <= rl) ? x[u] * sl2 : -INFINITY;
+          sd[jh][4 * qq + u] = (j <= rl) ? x[u] * sl2 : -INFINITY;
         }
       }
     float mx = -INFINITY;
 #pragma unroll
     for (int jh = 0; jh < 2; ++jh)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sc[jh][e]);
-    m = wave_max32(mx);  // finite: the diagonal key is always present
-#pragma unroll
-    for (int jh = 0; jh < 2; ++jh)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        sc[jh][e] = __builtin_amdgcn_exp2f(sc[jh][e] - m);
-        l += sc[jh][e];
-      }
-  }
-  dma_wait();
-  __syncthreads();
-  if (live) {
-    const bf16* vt = sm.vd[w >> 1];
+      for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sd[jh][e]);
+    m[nt] = wave_max32(mx);  // finite: the diagonal key is always present
+    const bf16* vt = sm.vd[w];
 #pragma unroll
     for (int jh = 0; jh < 2; ++jh) {
-      const bf16x8 p0 = pack_b(sc[jh], 0), p1 = pack_b(sc[jh], 1);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        sd[jh][e] = __builtin_amdgcn_exp2f(sd[jh][e] - m[nt]);
+        l[nt] += sd[jh][e];
+      }
+      const bf16x8 p0 = pack_b(sd[jh], 0), p1 = pack_b(sd[jh], 1);
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        acc[t] = mfma32(lds_tr_a<8>(vt, jh * 32, t * 32), p0, acc[t]);
-        acc[t] = mfma32(lds_tr_a<8>(vt, jh * 32 + 16, t * 32), p1, acc[t]);
+        acc[nt][t] = mfma32(lds_tr_a<8>(vt, jh * 32, t * 32), p0, acc[nt][t]);
+        acc[nt][t] = mfma32(lds_tr_a<8>(vt, jh * 32 + 16, t * 32), p1, acc[nt][t]);
       }
     }
   }
-  bf16x8 qb[4];
+  bf16x8 qb[2][4];
   for (int J = 0; J < nJ; ++J) {
     const int buf = J & 1;
     if (J + 1 < nJ) stage(J + 1);
@@ -710,41 +713,48 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
       const bf16* qsrc = (J < cb) ? ws.qb + ((int64_t)bhq * NS + J / PR) * T * 64
                                   : ws.qs + ((int64_t)bhq * PR + (J - cb)) * T * 64;
 #pragma unroll
-      for (int st = 0; st < 4; ++st) qb[st] = ld8(qsrc + (int64_t)(iw0 + l32) * 64 + 16 * st + 8 * g);
+      for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+        for (int st = 0; st < 4; ++st) qb[nt][st] = ld8(qsrc + (int64_t)(iw0 + nt * 32 + l32) * 64 + 16 * st + 8 * g);
     }
     if (live && J < Iw) {
 #pragma unroll
-      for (int jh = 0; jh < 2; ++jh) {
-        sc[jh] = zero16();
+      for (int nt = 0; nt < 2; ++nt) {
+        f32x16 sc[2];
 #pragma unroll
-        for (int st = 0; st < 4; ++st) sc[jh] = mfma32(ld8(swz<8>(sm.k[buf], jh * 32 + l32, 2 * st + g)), qb[st], sc[jh]);
-      }
-      float mx = -INFINITY;
+        for (int jh = 0; jh < 2; ++jh) {
+          sc[jh] = zero16();
 #pragma unroll
-      for (int jh = 0; jh < 2; ++jh)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sc[jh][e]);
-      mx = wave_max32(mx);
-      const float mn = fmaxf(m, mx * sl2);
-      const float alpha = __builtin_amdgcn_exp2f(m - mn);
-      m = mn;
-      l *= alpha;
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) acc[t][e] *= alpha;
-#pragma unroll
-      for (int jh = 0; jh < 2; ++jh) {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          sc[jh][e] = __builtin_amdgcn_exp2f(fmaf(sc[jh][e], sl2, -mn));
-          l += sc[jh][e];
+          for (int st = 0; st < 4; ++st)
+            sc[jh] = mfma32(ld8(swz<8>(sm.k[buf], jh * 32 + l32, 2 * st + g)), qb[nt][st], sc[jh]);
         }
-        const bf16x8 p0 = pack_b(sc[jh], 0), p1 = pack_b(sc[jh], 1);
+        float mx = -INFINITY;
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          acc[t] = mfma32(lds_tr_a<8>(sm.v[buf], jh * 32, t * 32), p0, acc[t]);
-          acc[t] = mfma32(lds_tr_a<8>(sm.v[buf], jh * 32 + 16, t * 32), p1, acc[t]);
+        for (int jh = 0; jh < 2; ++jh)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sc[jh][e]);
+        mx = wave_max32(mx);
+        const float mn = fmaxf(m[nt], mx * sl2);
+        const float alpha = __builtin_amdgcn_exp2f(m[nt] - mn);
+        m[nt] = mn;
+        l[nt] *= alpha;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) acc[nt][t][e] *= alpha;
+#pragma unroll
+        for (int jh = 0; jh < 2; ++jh) {
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            sc[jh][e] = __builtin_amdgcn_exp2f(fmaf(sc[jh][e], sl2, -mn));
+            l[nt] += sc[jh][e];
+          }
+          const bf16x8 p0 = pack_b(sc[jh], 0), p1 = pack_b(sc[jh], 1);
+#pragma unroll
+          for (int t = 0; t < 2; ++t) {
+            acc[nt][t] = mfma32(lds_tr_a<8>(sm.v[buf], jh * 32, t * 32), p0, acc[nt][t]);
+            acc[nt][t] = mfma32(lds_tr_a<8>(sm.v[buf], jh * 32 + 16, t * 32), p1, acc[nt][t]);
+          }
         }
       }
     }
@@ -752,20 +762,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
     __syncthreads();
   }
   if (live) {
-    l = wave_sum32(l);
-    const float inv = 1.f / l;
-    const int i = iw0 + l32;
-    bf16* orow = o + b * os.b + hq * os.h + (int64_t)i * os.t;
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int nt = 0; nt < 2; ++nt) {
+      const float ls = wave_sum32(l[nt]);
+      const float inv = 1.f / ls;
+      const int i = iw0 + nt * 32 + l32;
+      bf16* orow = o + b * os.b + hq * os.h + (int64_t)i * os.t;
 #pragma unroll
-      for (int qq = 0; qq < 4; ++qq) {
-        bf16x4 bb;
+      for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int u = 0; u < 4; ++u) bb[u] = (bf16)(acc[t][4 * qq + u] * inv);
-        *reinterpret_cast<bf16x4*>(orow + t * 32 + 8 * qq + 4 * g) = bb;
-      }
-    if (g == 0) ws.lse[(int64_t)bhq * T + i] = m + log2f(l);
+        for (int qq = 0; qq < 4; ++qq) {
+          bf16x4 bb;
+#pragma unroll
+          for (int u = 0; u < 4; ++u) bb[u] = (bf16)(acc[nt][t][4 * qq + u] * inv);
+          *reinterpret_cast<bf16x4*>(orow + t * 32 + 8 * qq + 4 * g) = bb;
+        }
+      if (g == 0) ws.lse[(int64_t)bhq * T + i] = m[nt] + log2f(ls);
+    }
   }
 }
 
