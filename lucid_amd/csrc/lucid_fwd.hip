@@ -8,6 +8,7 @@
 // Kernels (all 256 threads = 4 waves, MFMA 32x32x16 bf16, fp32 accumulate):
 //   lucid_prep_kernel        per-row 1/rms of K, K^T in T-perm layout, inverses of the 64x64
 //                            diagonal blocks of P, zero chain counters
+//   lucid_zx_kernel          the in-block coupling -X_B P_BA of every 128-row chain block
 //   lucid_precond_fwd_kernel chained solve, one workgroup per (128-row block, kv head);
 //                            it waits on a per-head progress counter for V'_j, j < i and
 //                            sweeps the earlier keys 128 at a time
