@@ -181,3 +181,30 @@ def test_rmsnorm_backward_matches_autograd():
     (kh * torch.from_numpy(dkh)).sum().backward()
     np.testing.assert_allclose(R.rmsnorm_backward(k.detach().numpy(), dkh, 1e-5), k.grad.numpy(),
                                rtol=1e-11, atol=1e-13)
+
+
+def test_chain_block_coupling_identity():
+    """The forward chain solves each 128-row block as V'_A = X_A R_A and
+    V'_B = X_B R_B + Z V'_A with Z = -(X_B P_BA) precomputed (X = inverse of a 64x64
+    diagonal block of P).  This pins that identity against a direct triangular solve of
+    P's real 128x128 diagonal block, and its transpose form (dV_A = X_A^T R_A + W dV_B,
+    W = -(X_A^T P_BA^T)) used by the backward column chain; a wrong sign, block or
+    transpose fails it."""
+    t, d, eps = 128, 64, 1e-5
+    k = _rand((1, 1, t, d), 21, 0.125)[0, 0]
+    r = _rand((1, 1, t, d), 22, 1.0)[0, 0]
+    s = d ** -0.5
+    p = R.precond_matrix(R.k_hat(k[None, None], eps)[0, 0], s)
+    pa, pb, pba = p[:64, :64], p[64:, 64:], p[64:, :64]
+    xa, xb = np.linalg.inv(pa), np.linalg.inv(pb)
+    direct = sla.solve_triangular(p, r, lower=True)
+    va = xa @ r[:64]
+    z = -(xb @ pba)
+    vb = xb @ r[64:] + z @ va
+    np.testing.assert_allclose(np.concatenate([va, vb]), direct, rtol=1e-10, atol=1e-12)
+    # the transposed (backward) solve P^T dV = R, last block first
+    direct_t = sla.solve_triangular(p.T, r, lower=False)
+    dvb = xb.T @ r[64:]
+    w = -(xa.T @ pba.T)
+    dva = xa.T @ r[:64] + w @ dvb
+    np.testing.assert_allclose(np.concatenate([dva, dvb]), direct_t, rtol=1e-10, atol=1e-12)
