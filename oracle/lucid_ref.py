@@ -214,6 +214,59 @@ def lucid_attention_grads(q, k, v, do, scale=None, eps=1e-5):
 # float32 CPU baseline, which follows the reference's own op sequence.
 # ---------------------------------------------------------------------------
 
+def lucid_group_torch(q, k, v, do=None, scale=None, eps=1e-5):
+    """One kv head and its G query heads in float64 torch, on whatever device the inputs are on.
+
+    ``q [G, T, d]``, ``k, v [T, d]``, ``do [G, T, d]`` (or None).  Returns a dict with
+    ``o [G, T, d]`` and ``vp [T, d]`` and, when ``do`` is given, ``dq [G, T, d]``, ``dk`` and
+    ``dv [T, d]``.  The same closed forms as :func:`lucid_attention` and
+    :func:`lucid_attention_grads` (modeling_lucid.py:551-574, :505-549 forward;
+    :314-382 backward) written so that the T x T temporaries of one query head at a time
+    are the only large allocations: this is the full-size ground truth of the GPU parity
+    tests (T = 32768 needs ~40 GB of device memory in float64).
+    """
+    import torch
+
+    q, k, v = q.double(), k.double(), v.double()
+    G, T, d = q.shape
+    scale = d ** -0.5 if scale is None else scale
+    r = torch.rsqrt(k.pow(2).mean(-1, keepdim=True) + eps)
+    kh = k * r
+    causal = torch.ones(T, T, dtype=torch.bool, device=k.device).tril_()
+    p = (kh @ kh.T).mul_(scale).sub_(1.0 / scale).masked_fill_(~causal, float("-inf")).exp_()
+    vp = torch.linalg.solve_triangular(p, v, upper=False)
+    out = {"vp": vp, "o": torch.empty_like(q)}
+    if do is not None:
+        do = do.double()
+        dvp = torch.zeros_like(v)
+        dk_attn = torch.zeros_like(k)
+        out["dq"] = torch.empty_like(q)
+    for gi in range(G):
+        a = (q[gi] @ k.T).mul_(scale).masked_fill_(~causal, float("-inf"))
+        a = torch.softmax(a, dim=-1)
+        out["o"][gi] = a @ vp
+        if do is None:
+            continue
+        dvp += a.T @ do[gi]
+        ds = do[gi] @ vp.T
+        ds -= (ds * a).sum(-1, keepdim=True)
+        ds *= a
+        del a
+        out["dq"][gi] = scale * (ds @ k)
+        dk_attn += scale * (ds.T @ q[gi])
+        del ds
+    if do is None:
+        return out
+    dv = torch.linalg.solve_triangular(p.T, dvp, upper=True)
+    m = (dv @ vp.T).mul_(p)  # p is zero above the diagonal, so m is lower triangular
+    del p
+    dkh = -scale * (m @ kh + m.T @ kh)
+    del m
+    dk = r * (dkh - kh * (kh * dkh).sum(-1, keepdim=True) / d) + dk_attn
+    out["dk"], out["dv"] = dk, dv
+    return out
+
+
 def lucid_attention_torch(q, k, v, scale=None, eps=1e-5):
     """Differentiable torch restatement of get_v_prime + eager_lucid_attention_forward.
 

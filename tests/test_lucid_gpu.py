@@ -1,9 +1,9 @@
 """GPU parity of the LUCID attention HIP kernels against the float64 CPU oracle.
 
-Tolerances (bf16 against float64 ground truth computed
-from the same bf16-rounded inputs):
-  * outputs O and V':       max |x - ref| <= 2e-2
-  * gradients dQ, dK, dV:   max |x - ref| <= 2e-2 * max(1, max |ref|)
+Tolerances (tests/bars.py; BASELINE north star, bf16 against float64 ground truth
+computed from the same bf16-rounded inputs): max |x - ref| <= 2e-2 * max |ref| for
+every tensor, and <= 2e-2 absolute where max |ref| <= 4.  Every-head checks at the
+full north-star and config-2 shapes are in tests/test_lucid_fullsize_gpu.py; here
 Full-size shapes are checked through properties that hold at any size: the
 solve residual ||P V' - V|| (P rebuilt with torch fp32 matmuls) and sampled
 rows of softmax(s q K^T) V' recomputed in fp32.
@@ -14,16 +14,21 @@ import torch
 
 from oracle import lucid_ref as R
 
+from bars import check  # noqa: E402
+
 pytestmark = pytest.mark.gpu
 
 TOL = 2e-2
 
 
-def _inputs(B, Hq, Hkv, T, D, seed, scale=None):
+def _inputs(B, Hq, Hkv, T, D, seed, qk_std=None):
+    """q, k ~ N(0, qk_std^2) (default 1/sqrt(d), the BASELINE configs; 1.0 puts s q.k at O(1)),
+    v ~ N(0, 1/d), dO ~ N(0, 1)."""
     g = torch.Generator().manual_seed(seed)
-    s = D ** -0.5 if scale is None else scale
-    q = (torch.randn(B, Hq, T, D, generator=g) * s).to(torch.bfloat16)
-    k = (torch.randn(B, Hkv, T, D, generator=g) * s).to(torch.bfloat16)
+    s = D ** -0.5
+    qs = s if qk_std is None else qk_std
+    q = (torch.randn(B, Hq, T, D, generator=g) * qs).to(torch.bfloat16)
+    k = (torch.randn(B, Hkv, T, D, generator=g) * qs).to(torch.bfloat16)
     v = (torch.randn(B, Hkv, T, D, generator=g) * s).to(torch.bfloat16)
     do = torch.randn(B, T, Hq, D, generator=g).to(torch.bfloat16)
     return q, k, v, do
@@ -38,33 +43,36 @@ def _maxerr(x, ref):
 
 
 CASES = [
-    # B, Hq, Hkv, T, D
-    (1, 2, 2, 256, 64),
-    (2, 4, 2, 384, 64),     # GQA, two batches
-    (1, 2, 1, 200, 64),     # ragged T (zero-padded to 256), GQA 2:1
-    (1, 2, 2, 256, 128),
+    # B, Hq, Hkv, T, D, q/k std (None: 1/sqrt(d); 1.0: O(1) scores, a sharp softmax)
+    (1, 2, 2, 256, 64, None),
+    (2, 4, 2, 384, 64, None),     # GQA, two batches
+    (1, 2, 1, 200, 64, None),     # ragged T (zero-padded to 256), GQA 2:1
+    (1, 2, 2, 256, 128, None),
+    (1, 2, 2, 256, 64, 1.0),
+    (2, 4, 2, 384, 64, 1.0),
+    (1, 2, 1, 200, 128, 1.0),
 ]
 
 
-@pytest.mark.parametrize("B,Hq,Hkv,T,D", CASES)
-def test_forward_matches_oracle(B, Hq, Hkv, T, D):
+@pytest.mark.parametrize("B,Hq,Hkv,T,D,qk_std", CASES)
+def test_forward_matches_oracle(B, Hq, Hkv, T, D, qk_std):
     from lucid_amd import lucid_attention
-    q, k, v, _ = _inputs(B, Hq, Hkv, T, D, seed=T + D)
-    print(f"case fwd B={B} Hq={Hq} Hkv={Hkv} T={T} D={D}", flush=True)
+    q, k, v, _ = _inputs(B, Hq, Hkv, T, D, seed=T + D, qk_std=qk_std)
+    print(f"case fwd B={B} Hq={Hq} Hkv={Hkv} T={T} D={D} qk_std={qk_std}", flush=True)
     o, vp = lucid_attention(q.cuda(), k.cuda(), v.cuda(), return_vprime=True)
     torch.cuda.synchronize()
     o_ref, vp_ref = R.lucid_attention(_np(q), _np(k), _np(v), D ** -0.5, 1e-5)
-    assert _maxerr(vp, vp_ref) <= TOL
-    assert _maxerr(o, o_ref) <= TOL
+    check("vprime", _maxerr(vp, vp_ref), float(np.abs(vp_ref).max()))
+    check("o", _maxerr(o, o_ref), float(np.abs(o_ref).max()))
     # V' is solved with fp32 accumulation: much tighter than the bf16 bar
     assert _maxerr(vp, vp_ref) <= 2e-3 * max(1.0, np.abs(vp_ref).max())
 
 
-@pytest.mark.parametrize("B,Hq,Hkv,T,D", CASES)
-def test_backward_matches_oracle(B, Hq, Hkv, T, D):
+@pytest.mark.parametrize("B,Hq,Hkv,T,D,qk_std", CASES)
+def test_backward_matches_oracle(B, Hq, Hkv, T, D, qk_std):
     from lucid_amd import lucid_attention
-    q, k, v, do = _inputs(B, Hq, Hkv, T, D, seed=7 * T + D)
-    print(f"case bwd B={B} Hq={Hq} Hkv={Hkv} T={T} D={D}", flush=True)
+    q, k, v, do = _inputs(B, Hq, Hkv, T, D, seed=7 * T + D, qk_std=qk_std)
+    print(f"case bwd B={B} Hq={Hq} Hkv={Hkv} T={T} D={D} qk_std={qk_std}", flush=True)
     qg, kg, vg = (t.cuda().requires_grad_() for t in (q, k, v))
     o = lucid_attention(qg, kg, vg)
     o.backward(do.cuda())
@@ -72,8 +80,7 @@ def test_backward_matches_oracle(B, Hq, Hkv, T, D):
     dq, dk, dv = R.lucid_attention_grads(_np(q), _np(k), _np(v), _np(do), D ** -0.5, 1e-5)
     for name, got, ref in (("dq", qg.grad, dq), ("dk", kg.grad, dk), ("dv", vg.grad, dv)):
         err = _maxerr(got, ref)
-        bound = TOL * max(1.0, np.abs(ref).max())
-        assert err <= bound, f"{name}: max err {err:.3e} > {bound:.3e}"
+        check(name, err, float(np.abs(ref).max()))
 
 
 def test_identical_keys_first_difference_gpu():

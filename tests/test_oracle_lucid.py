@@ -208,3 +208,47 @@ def test_chain_block_coupling_identity():
     w = -(xa.T @ pba.T)
     dva = xa.T @ r[:64] + w @ dvb
     np.testing.assert_allclose(np.concatenate([dva, dvb]), direct_t, rtol=1e-10, atol=1e-12)
+
+
+@pytest.mark.parametrize("t,g", [(48, 1), (40, 3)])
+def test_group_torch_matches_numpy_closed_forms(t, g):
+    """lucid_group_torch (the full-size GPU ground truth) equals the numpy oracle, forward and
+    gradients, for one kv head with g query heads; a missing GQA sum or transposed solve fails."""
+    d = 16
+    q = _rand((1, g, t, d), 26)
+    k = _rand((1, 1, t, d), 27, 0.7)
+    v = _rand((1, 1, t, d), 28)
+    do = _rand((1, t, g, d), 29)
+    o, vp = R.lucid_attention(q, k, v)
+    dq, dk, dv = R.lucid_attention_grads(q, k, v, do)
+    out = R.lucid_group_torch(torch.from_numpy(q[0]), torch.from_numpy(k[0, 0]), torch.from_numpy(v[0, 0]),
+                              torch.from_numpy(do[0].transpose(1, 0, 2).copy()))
+    np.testing.assert_allclose(out["vp"].numpy(), vp[0, 0], rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(out["o"].numpy(), o[0].transpose(1, 0, 2), rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(out["dq"].numpy(), dq[0], rtol=1e-9, atol=1e-11)
+    np.testing.assert_allclose(out["dk"].numpy(), dk[0, 0], rtol=1e-9, atol=1e-11)
+    np.testing.assert_allclose(out["dv"].numpy(), dv[0, 0], rtol=1e-9, atol=1e-11)
+
+
+def test_unit_variance_inputs_reject_scale_and_gradient_mistakes():
+    """The GPU parity cases with unit-variance q and k put s q.k at O(1), so the softmax is far
+    from uniform: there a doubled softmax scale moves O, and a halved dQ or dK misses, by more
+    than the relative bar (2e-2 of max |ref|) -- unlike N(0,1)/sqrt(d) inputs, whose near-uniform
+    softmax hides such mistakes."""
+    t, d = 256, 64
+    q = _rand((1, 1, t, d), 30)
+    k = _rand((1, 1, t, d), 31)
+    v = _rand((1, 1, t, d), 32, 0.125)
+    do = _rand((1, t, 1, d), 33)
+    s = d ** -0.5
+    o, vp = R.lucid_attention(q, k, v, s)
+    o2, _ = R.causal_attention(q, k, vp, 2 * s)
+    assert np.abs(o2 - o).max() > 2e-2 * np.abs(o).max()
+    dq, dk, _ = R.lucid_attention_grads(q, k, v, do, s)
+    for ref in (dq, dk):
+        assert np.abs(0.5 * ref - ref).max() > 2e-2 * np.abs(ref).max()
+    # the same mistake hides under the small-score inputs at the absolute bar
+    qs, ks = q / 8, k / 8
+    o_s, vp_s = R.lucid_attention(qs, ks, v, s)
+    o2_s, _ = R.causal_attention(qs, ks, vp_s, 2 * s)
+    assert np.abs(o2_s - o_s).max() < 2e-2
