@@ -85,11 +85,14 @@ def cpu_baseline(T_sample=16384, T_full=32768, H_full=16, D=64):
     }
 
 
-def _bench_inputs(B, Hq, Hkv, T, D, dev, grad=True):
+def _bench_inputs(B, Hq, Hkv, T, D, dev, grad=True, keys="iid"):
     import torch
     g = torch.Generator().manual_seed(0)
     mk = lambda *shape: (torch.randn(*shape, generator=g) / D ** 0.5).to(torch.bfloat16).to(dev)  # noqa: E731
     q, k, v = mk(B, Hq, T, D), mk(B, Hkv, T, D), mk(B, Hkv, T, D)
+    if keys == "correlated":  # a shared direction per head + 0.1 N(0,1) noise
+        base = torch.randn(B, Hkv, 1, D, generator=g)
+        k = ((base + 0.1 * torch.randn(B, Hkv, T, D, generator=g)) / D ** 0.5).to(torch.bfloat16).to(dev)
     if grad:
         for x in (q, k, v):
             x.requires_grad_()
@@ -330,6 +333,12 @@ def main():
                          "on B1 x T8192; c5: B1 T131072 Hq32/Hkv8 d128 forward only; path: LUCID-Path "
                          "B1 H16 T32768 d64 fwd+bwd; path_softmax: PaTH softmax attention on the config-4 "
                          "shape, fwd+bwd; decode: one decoding step against a 128K cache (config-5 heads)")
+    ap.add_argument("--precision", default="auto", choices=["auto", "fast", "exact"],
+                    help="LUCID chain precision (lucid_amd.set_precision): auto picks per head from the row "
+                         "mass; exact forces the hi/lo split chains for every head")
+    ap.add_argument("--keys", default="iid", choices=["iid", "correlated"],
+                    help="iid: the BASELINE inputs; correlated: every key = a shared direction + 0.1 N(0,1) "
+                         "(row mass ~T, the exact chains under --precision auto)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-causal", action="store_true")
     ap.add_argument("--copy-bytes", type=int, default=0,
@@ -348,10 +357,11 @@ def main():
 
     import torch
 
-    from lucid_amd import _lib, lucid_attention
+    from lucid_amd import _lib, lucid_attention, set_precision
 
     dev = torch.device("cuda:0")
     wl = args.workload
+    set_precision(args.precision)
     if wl == "c3":
         bench_c3(args, dev)
         return
@@ -383,7 +393,7 @@ def main():
     else:
         B, Hq, Hkv, T, D = {"lucid": (1, 16, 16, 32768, 64), "c2": (4, 16, 16, 4096, 64),
                             "c5": (1, 32, 8, 131072, 128)}[wl]
-        q, k, v, do = _bench_inputs(B, Hq, Hkv, T, D, dev, grad=not fwd_only)
+        q, k, v, do = _bench_inputs(B, Hq, Hkv, T, D, dev, grad=not fwd_only, keys=args.keys)
         lib, prefix = _lib.load(), "lucid_"
 
         def step():
@@ -477,6 +487,7 @@ def main():
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1)/sqrt(d) q,k,v; N(0,1) dO)" if wl not in ("path", "path_softmax")
                 else "synthetic (seeded N(0,1) q,k,v,w; w L2-normalised; beta=2 sigmoid(N(0,1)); N(0,1) dO)",
+        "precision": args.precision, "keys": args.keys,
         "config": {"workload": {"lucid": "lucid_attention_fwd_bwd", "c2": "lucid_attention_fwd_bwd",
                                 "c5": "lucid_attention_fwd", "path": "lucid_path_fwd_bwd",
                                 "path_softmax": "path_softmax_attention_fwd_bwd"}[wl],

@@ -27,11 +27,34 @@ extern "C" {
 #define LUCID_EINVAL 1
 #define LUCID_EHIP 1000
 
+/* Precision of the preconditioner chains (lucid_set_precision). */
+#define LUCID_PRECISION_AUTO 0  /* per head, from the head's row mass (default) */
+#define LUCID_PRECISION_FAST 1  /* bf16 products everywhere */
+#define LUCID_PRECISION_EXACT 2 /* hi/lo split products for every head */
+
 /* ABI version of this header (bumped on any signature change). */
 int lucid_abi_version(void);
 
 /* Text of the last error on the calling thread ("" if none). */
 const char* lucid_last_error(void);
+
+/* Chain precision for the forward calls that follow (process-wide; the backward uses the
+ * choice recorded in the forward workspace).  The off-diagonal products of the chained
+ * solves (P V', P^T dV, (dV V'^T) * P and its sums with K) accumulate over every earlier
+ * key of a row; with bf16 operands their error grows like 2^-8 |V'| sqrt(m), m = the
+ * row mass sum_{j<i} P_ij^2, which is ~1e-2 for keys with no common direction but ~T for
+ * keys along a shared direction (the reference's fp32 TRSM carries those at fp32
+ * accuracy).  AUTO measures m per head (sampled) and runs heads with m > 4 through
+ * kernels that split every such product into bf16 hi*hi + hi*lo + lo*hi terms (~fp32
+ * accuracy); FAST and EXACT force one kind for every head (testing, benchmarking).
+ * Returns LUCID_EINVAL for an unknown mode.  No counterpart in the reference, whose
+ * torch solve_triangular works in the input dtype (modeling_lucid.py:570). */
+int lucid_set_precision(int mode);
+int lucid_get_precision(void);
+
+/* Byte offset, inside the forward workspace, of the per-head row masses (float [B*Hkv]);
+ * a head ran the exact chain kernels when its mass exceeds 4 (testing aid). */
+size_t lucid_fwd_workspace_mass_offset(int B, int Hq, int Hkv, int T, int D);
 
 /* Bytes of the forward workspace.  It holds the state the backward reuses
  * (1/rms of K, K^T and V' in MFMA operand layouts, the inverted 64x64
@@ -70,6 +93,50 @@ int lucid_attn_bwd(const void* dout, const int64_t* do_strides, const void* q, c
                    const float* lse, const void* fwd_ws, void* dq, const int64_t* dq_strides, void* dk,
                    const int64_t* dk_strides, void* dv, const int64_t* dv_strides, void* bwd_ws, int B, int Hq,
                    int Hkv, int T, int D, float scale, float eps, void* stream);
+
+/* ---- The two operator seams of LucidAttention.forward, separately ----
+ * get_v_prime (modeling_lucid.py:551-574) is lucid_get_v_prime above; its gradient is
+ * lucid_precond_bwd.  eager_lucid_attention_forward (:505-549: causal SDPA of q and the
+ * repeat_kv'd key and v_prime, output [B,T,Hq,D]) is lucid_attn_vp_fwd and its gradient
+ * lucid_attn_vp_bwd.  Composed as LucidAttention.forward composes them (:461-496) they give
+ * the same result as lucid_attn_fwd / lucid_attn_bwd.  With v_prime = value they are plain
+ * causal softmax attention. */
+
+/* Bytes of the workspace of lucid_attn_vp_fwd, kept alive until lucid_attn_vp_bwd. */
+size_t lucid_attn_vp_fwd_workspace_bytes(int B, int Hq, int Hkv, int T, int D);
+
+/* O = softmax(s Q K^T, causal) V' for a caller's V' (bf16, or fp32 when vprime_f32 != 0;
+ * [B,Hkv,T,D] strided), o [B,T,Hq,D] (strided), lse fp32 [B,Hq,T] (output).  eps is the
+ * k_norm epsilon, used to measure each head's row mass (lucid_set_precision). */
+int lucid_attn_vp_fwd(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                      const void* vprime, const int64_t* vprime_strides, int vprime_f32, void* o,
+                      const int64_t* o_strides, float* lse, void* ws, int B, int Hq, int Hkv, int T, int D,
+                      float scale, float eps, void* stream);
+
+/* Bytes of the backward scratch of lucid_attn_vp_bwd. */
+size_t lucid_attn_vp_bwd_workspace_bytes(int B, int Hq, int Hkv, int T, int D);
+
+/* Gradients of sum(O * dO) w.r.t. q, k (the softmax part only; bf16) and v_prime (bf16 or
+ * fp32 when dvprime_f32 != 0), GQA groups summed.  fwd_ws is lucid_attn_vp_fwd's. */
+int lucid_attn_vp_bwd(const void* dout, const int64_t* do_strides, const void* q, const int64_t* q_strides,
+                      const void* k, const int64_t* k_strides, const void* o, const int64_t* o_strides,
+                      const float* lse, const void* fwd_ws, void* dq, const int64_t* dq_strides, void* dk,
+                      const int64_t* dk_strides, void* dvprime, const int64_t* dvprime_strides, int dvprime_f32,
+                      void* bwd_ws, int B, int Hq, int Hkv, int T, int D, float scale, void* stream);
+
+/* Bytes of the backward scratch of lucid_precond_bwd. */
+size_t lucid_precond_bwd_workspace_bytes(int B, int Hkv, int T, int D);
+
+/* Gradient of V' = P(K^)^-1 V alone: given dV' (bf16, or fp32 when dvprime_f32 != 0;
+ * strided), dv = P^-T dV' and dk = RMSNorm backward of dK^ = -s (M K^ + M^T K^),
+ * M = tril((dV V'^T) * P) (bf16 outputs).  fwd_ws is the workspace of the lucid_get_v_prime
+ * call that produced V' (kept alive until this call is enqueued).  Replaces
+ * Lucid_Tril_Solver.backward (modeling_lucid.py:314-382) and the autograd of the dense
+ * branch of get_v_prime (:561-570), k_norm (:409) included. */
+int lucid_precond_bwd(const void* k, const int64_t* k_strides, const void* dvprime, const int64_t* dvprime_strides,
+                      int dvprime_f32, const void* fwd_ws, void* dk, const int64_t* dk_strides, void* dv,
+                      const int64_t* dv_strides, void* bwd_ws, int B, int Hkv, int T, int D, float scale,
+                      void* stream);
 
 /* Bytes of the decoding workspace for caches of capacity T_cap (0 on bad sizes). */
 size_t lucid_decode_workspace_bytes(int B, int Hq, int Hkv, int T_cap, int D);

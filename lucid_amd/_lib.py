@@ -28,6 +28,9 @@ _SIGS = {
         "lucid_abi_version": ([], _int),
         "lucid_last_error": ([], ctypes.c_char_p),
         "lucid_fwd_workspace_bytes": ([_int] * 5, _sz),
+        "lucid_set_precision": ([_int], _int),
+        "lucid_get_precision": ([], _int),
+        "lucid_fwd_workspace_mass_offset": ([_int] * 5, _sz),
         "lucid_bwd_workspace_bytes": ([_int] * 5, _sz),
         "lucid_get_v_prime": ([_vp, _i64p, _vp, _i64p, _vp, _vp, _int, _int, _int, _int, _flt, _flt, _vp], _int),
         "lucid_attn_fwd": ([_vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _vp, _vp,
@@ -35,6 +38,16 @@ _SIGS = {
         "lucid_attn_bwd": ([_vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _vp,
                             _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp,
                             _int, _int, _int, _int, _int, _flt, _flt, _vp], _int),
+        "lucid_attn_vp_fwd_workspace_bytes": ([_int] * 5, _sz),
+        "lucid_attn_vp_fwd": ([_vp, _i64p, _vp, _i64p, _vp, _i64p, _int, _vp, _i64p, _vp, _vp,
+                               _int, _int, _int, _int, _int, _flt, _flt, _vp], _int),
+        "lucid_attn_vp_bwd_workspace_bytes": ([_int] * 5, _sz),
+        "lucid_attn_vp_bwd": ([_vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _vp,
+                               _vp, _i64p, _vp, _i64p, _vp, _i64p, _int, _vp,
+                               _int, _int, _int, _int, _int, _flt, _vp], _int),
+        "lucid_precond_bwd_workspace_bytes": ([_int] * 4, _sz),
+        "lucid_precond_bwd": ([_vp, _i64p, _vp, _i64p, _int, _vp, _vp, _i64p, _vp, _i64p, _vp,
+                               _int, _int, _int, _int, _flt, _vp], _int),
         "lucid_decode_workspace_bytes": ([_int] * 5, _sz),
         "lucid_decode": ([_vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _vp,
                           _int, _int, _int, _int, _int, _int, _flt, _flt, _vp], _int),

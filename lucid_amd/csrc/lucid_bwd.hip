@@ -18,20 +18,26 @@
 namespace lucid {
 
 // delta[bhq][t] = -(dO_t . O_t) (stored negated: it seeds the dP accumulators of the
-// column sweep); zero the chain counters.  grid (T/64, B*Hq)
+// column sweep); zero the chain counters.  Heads of the exact chains (row mass above
+// kExactMass) take O as its bf16 pair O + olo (written by the attention forward).
+// grid (T/64, B*Hq)
 template <int D>
 __global__ __launch_bounds__(256) void lucid_bwd_prep_kernel(const bf16* __restrict__ dout, Strides dos,
-                                                             const bf16* __restrict__ o, Strides os, int Hq, int T,
+                                                             const bf16* __restrict__ o, Strides os,
+                                                             const bf16* __restrict__ olo,
+                                                             const float* __restrict__ mass, int Hq, int Hkv, int T,
                                                              float* __restrict__ delta, int* __restrict__ counters,
                                                              int BH) {
   constexpr int SEG = D / 4;
   const int blk = blockIdx.x, bhq = blockIdx.y;
   const int b = bhq / Hq, hq = bhq - b * Hq;
+  const bool exact = mass[b * Hkv + hq / (Hq / Hkv)] > kExactMass;
   const int tid = threadIdx.x;
   const int row = tid >> 2, seg = tid & 3;
   const int t = blk * 64 + row;
   const bf16* dop = dout + b * dos.b + hq * dos.h + (int64_t)t * dos.t;
   const bf16* opp = o + b * os.b + hq * os.h + (int64_t)t * os.t;
+  const bf16* olp = olo + ((int64_t)bhq * T + t) * D;
   float acc = 0.f;
 #pragma unroll
   for (int c = 0; c < SEG; c += 8) {
@@ -39,6 +45,11 @@ __global__ __launch_bounds__(256) void lucid_bwd_prep_kernel(const bf16* __restr
     const bf16x8 bo = ld8(opp + seg * SEG + c);
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc += (float)a[e] * (float)bo[e];
+    if (exact) {
+      const bf16x8 bl = ld8(olp + seg * SEG + c);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc += (float)a[e] * (float)bl[e];
+    }
   }
   acc += __shfl_xor(acc, 1, 64);
   acc += __shfl_xor(acc, 2, 64);
@@ -215,6 +226,12 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_bw
 // two tiles ahead); K^T operands come through transposing LDS loads.
 //   S^T[j][i] = K_j . Q_i, dP^T[j][i] = V'_j . dO_i, dS^T = P^T (dP^T - delta_i)
 //   dQ^T[d][i] += K^T[d][j] dS^T[j][i]
+// EXACT (heads whose row mass exceeds kExactMass, i.e. keys along a shared direction; each
+// instance returns at once for the other heads): every row of dS sums to zero, so the
+// shared key direction cancels out of dQ_i = s sum_j dS_ij K_j and the bf16 rounding of
+// dS would leave it behind; dS enters as a hi/lo pair (K is exact in bf16).  dP = dO V'^T
+// keeps the bf16 V' of the forward: delta_i = dO_i . O_i equals sum_j P_ij dP_ij only when
+// both use the same V', and that identity is what cancels the shared direction.
 // ---------------------------------------------------------------------------
 template <int D>
 struct DqSmem {
@@ -222,12 +239,12 @@ struct DqSmem {
   bf16 v[3][64 * D];
 };
 
-template <int D>
-__global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_bwd_dq_kernel(
+template <int D, bool EXACT>
+__global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void lucid_attn_bwd_dq_kernel(
     const bf16* __restrict__ q, Strides qs, const bf16* __restrict__ k, Strides ks, const bf16* __restrict__ vpb,
     const bf16* __restrict__ dout, Strides dos, const float* __restrict__ lse,
-    const float* __restrict__ delta, bf16* __restrict__ dq, Strides dqs, int Hq, int Hkv, int T, int BHq,
-    float scale) {
+    const float* __restrict__ delta, const float* __restrict__ mass, bf16* __restrict__ dq, Strides dqs, int Hq,
+    int Hkv, int T, int BHq, float scale) {
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
   __shared__ __attribute__((aligned(16))) DqSmem<D> sm;
@@ -238,13 +255,14 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_bw
   const int b = bhq / Hq, hq = bhq - b * Hq;
   const int h = hq / (Hq / Hkv);
   const int bh = b * Hkv + h;
+  if ((mass[bh] > kExactMass) != EXACT) return;  // the other instance handles this head
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
   const int r0 = ib * 256;
   const int row0 = r0 + w * 64;
   const bf16* kh = k + b * ks.b + h * ks.h;
   const bf16* vh = vpb + (int64_t)bh * T * D;
-    const float c = scale * LOG2E_F;
+  const float c = scale * LOG2E_F;
 
   bf16x8 qb[2][NKS], db[2][NKS];
   float li[2], di[2];
@@ -300,7 +318,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_bw
         ka[st] = ld8(sm.k[buf] + rdo[st] + mt * 32 * D);
         va[st] = ld8(sm.v[buf] + rdo[st] + mt * 32 * D);
       }
-      bf16x8 dsb[2][2];
+      bf16x8 dsb[2][2], dsl[2][2];
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt) {
         f32x16 sc = zero16(), dp = zero16();
@@ -317,6 +335,10 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_bw
         }
         dsb[nt][0] = pack_b(sc, 0);
         dsb[nt][1] = pack_b(sc, 1);
+        if constexpr (EXACT) {
+          dsl[nt][0] = pack_lo(sc, 0, dsb[nt][0]);
+          dsl[nt][1] = pack_lo(sc, 1, dsb[nt][1]);
+        }
       }
 #pragma unroll
       for (int t = 0; t < NDT; ++t) {
@@ -326,6 +348,10 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_bw
         for (int nt = 0; nt < 2; ++nt) {
           acc[t][nt] = mfma32(a0, dsb[nt][0], acc[t][nt]);
           acc[t][nt] = mfma32(a1, dsb[nt][1], acc[t][nt]);
+          if constexpr (EXACT) {
+            acc[t][nt] = mfma32(a0, dsl[nt][0], acc[t][nt]);
+            acc[t][nt] = mfma32(a1, dsl[nt][1], acc[t][nt]);
+          }
         }
       }
     }
@@ -378,9 +404,17 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_bw
 // is the work after the last tile becomes visible, so dV' and both inverses
 // are loaded earlier.  At
 // d = 64 two workgroups share a CU (LDS <= 80 KB, <= 256 registers per lane).
+//
+// EXACT (heads whose row mass exceeds kExactMass; each instance returns at once for the
+// other heads): dV is also kept as its bf16 residual (dvbl), the staged row tiles carry
+// it, V'_J's residual (vpbl) is held beside V'_J, and every product that sums over rows
+// is split into hi*hi + hi*lo + lo*hi: P^T dV, G = dV V'^T, M^T K (K is exact in bf16,
+// so two terms) and the in-block P_BA^T dV_B.  One workgroup per CU.
 // ---------------------------------------------------------------------------
+template <int D, bool EXACT>
+struct PcolSmem;
 template <int D>
-struct PcolSmem {
+struct PcolSmem<D, false> {
   union {
     struct {
       bf16 k[3][64 * D];   // swizzled tiles (chunk c of row r at c ^ (r & 7))
@@ -394,20 +428,39 @@ struct PcolSmem {
     } fin;
   } u;
 };
-
 template <int D>
-__global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond_bwd_col_kernel(
+struct PcolSmem<D, true> {
+  union {
+    struct {
+      bf16 k[3][64 * D];
+      bf16 dv[3][64 * D];
+      bf16 dvl[3][64 * D];  // lo part of dV
+      float r[3][64];
+    } st;
+    struct {
+      float Rt[D][132];
+      float Xt[64][68];
+      bf16 vT[D][128 + 8];
+      bf16 vTl[D][128 + 8];  // lo part of dV^T of the block
+    } fin;
+  } u;
+};
+
+template <int D, bool EXACT>
+__global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void lucid_precond_bwd_col_kernel(
     const bf16* __restrict__ k, Strides ks, int Hkv, int T, int BH, const float* __restrict__ rinv, float scale,
-    const bf16* __restrict__ kt, const bf16* __restrict__ vpb, const float* __restrict__ pinv,
-    const float* __restrict__ dvp, bf16* __restrict__ dvb, bf16* __restrict__ dv_out,
-    Strides dvs, float* __restrict__ colsum, int* __restrict__ counters) {
+    const bf16* __restrict__ kt, const bf16* __restrict__ vpb, const bf16* __restrict__ vpbl,
+    const float* __restrict__ pinv, const float* __restrict__ mass, const float* __restrict__ dvp,
+    bf16* __restrict__ dvb, bf16* __restrict__ dvbl, bf16* __restrict__ dv_out, Strides dvs,
+    float* __restrict__ colsum, int* __restrict__ counters) {
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
-  __shared__ __attribute__((aligned(16))) PcolSmem<D> sm;
+  __shared__ __attribute__((aligned(16))) PcolSmem<D, EXACT> sm;
 
   const int NT = T / 64, NP = T / 128;
   const int id = blockIdx.x;
   const int p = NP - 1 - id / BH, bh = id - (id / BH) * BH;
+  if ((mass[bh] > kExactMass) != EXACT) return;  // the other instance solves this head
   const int b = bh / Hkv, h = bh - b * Hkv;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
@@ -417,17 +470,19 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
   const float* rv = rinv + (int64_t)bh * T;
   const bf16* kth = kt + (int64_t)bh * D * T;
   const bf16* dvbh = dvb + (int64_t)bh * T * D;
+  const bf16* dvblh = dvbl + (int64_t)bh * T * D;
   const bf16* vph = vpb + (int64_t)bh * T * D;
   int* cnt = counters + bh;
   const float sl2 = scale * LOG2E_F;
   const float c0 = LOG2E_F / scale;
 
-  bf16x8 kbJ[NKS], vbJ[NKS];
+  bf16x8 kbJ[NKS], vbJ[NKS], vbJl[NKS];
   const int jc = J0 + cw + l32;
 #pragma unroll
   for (int st = 0; st < NKS; ++st) {
     kbJ[st] = ld8(kh + (int64_t)jc * ks.t + 16 * st + 8 * g);
     vbJ[st] = ld8(vph + (int64_t)jc * D + 16 * st + 8 * g);
+    if constexpr (EXACT) vbJl[st] = ld8(vpbl + ((int64_t)bh * T + jc) * D + 16 * st + 8 * g);
   }
   const float aJ = sl2 * rv[jc];
   f32x16 adv[NDT], acs[NDT];
@@ -449,8 +504,8 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
   const int first = NT - 1, last = 2 * p + 2;  // tiles first, first-1, ..., last
   int ready = 0;
   // step k of the sweep stages tile first - k into buffer k % 3; the newest
-  // STAGE_OPS vector memory operations of a wave are the two tiles of a step
-  constexpr int STAGE_OPS = 2 * (64 * (D / 8) / 256);
+  // STAGE_OPS vector memory operations of a wave are the tiles of a step
+  constexpr int STAGE_OPS = (EXACT ? 3 : 2) * (64 * (D / 8) / 256);
   const int nsteps = first - last + 1;
   int plan_k[64 * (D / 8) / 256], plan_d[64 * (D / 8) / 256];
   dma_plan<64, D / 8>(ks.t, plan_k);
@@ -460,6 +515,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
     if (w == 0) dma_f32x64(rv + i0, sm.u.st.r[buf]);
     dma_stage<64, D / 8>(plan_k, kh + (int64_t)i0 * ks.t, sm.u.st.k[buf]);
     dma_stage<64, D / 8>(plan_d, dvbh + (int64_t)i0 * D, sm.u.st.dv[buf]);
+    if constexpr (EXACT) dma_stage<64, D / 8>(plan_d, dvblh + (int64_t)i0 * D, sm.u.st.dvl[buf]);
   };
   // issue the steps up to `upto` whose tiles are already published (tile I is
   // published once the counter exceeds NT-1-I); never blocks
@@ -530,6 +586,13 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
         sc = mfma32(ka[st], kbJ[st], sc);
         gg = mfma32(da[st], vbJ[st], gg);
       }
+      if constexpr (EXACT) {
+#pragma unroll
+        for (int st = 0; st < NKS; ++st) {
+          gg = mfma32(da[st], vbJl[st], gg);
+          gg = mfma32(ld8(swz<D / 8>(sm.u.st.dvl[buf], rh * 32 + l32, 2 * st + g)), vbJ[st], gg);
+        }
+      }
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const float pe = __builtin_amdgcn_exp2f(fmaf(sc[e] * aJ, rI[e], -c0));
@@ -538,6 +601,13 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
       }
       const bf16x8 pb0 = pack_b(sc, 0), pb1 = pack_b(sc, 1);
       const bf16x8 mb0 = pack_b(gg, 0), mb1 = pack_b(gg, 1);
+      bf16x8 pl0, pl1, ml0, ml1;  // lo parts (EXACT)
+      if constexpr (EXACT) {
+        pl0 = pack_lo(sc, 0, pb0);
+        pl1 = pack_lo(sc, 1, pb1);
+        ml0 = pack_lo(gg, 0, mb0);
+        ml1 = pack_lo(gg, 1, mb1);
+      }
 #pragma unroll
       for (int t = 0; t < NDT; ++t) {
         const bf16x8 a0 = lds_tr_a<D / 8>(sm.u.st.dv[buf], rh * 32, t * 32);
@@ -548,6 +618,14 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
         adv[t] = mfma32(a1, pb1, adv[t]);
         acs[t] = mfma32(k0, mb0, acs[t]);
         acs[t] = mfma32(k1, mb1, acs[t]);
+        if constexpr (EXACT) {
+          adv[t] = mfma32(a0, pl0, adv[t]);
+          adv[t] = mfma32(a1, pl1, adv[t]);
+          adv[t] = mfma32(lds_tr_a<D / 8>(sm.u.st.dvl[buf], rh * 32, t * 32), pb0, adv[t]);
+          adv[t] = mfma32(lds_tr_a<D / 8>(sm.u.st.dvl[buf], rh * 32 + 16, t * 32), pb1, adv[t]);
+          acs[t] = mfma32(k0, ml0, acs[t]);
+          acs[t] = mfma32(k1, ml1, acs[t]);
+        }
       }
     }
   };
@@ -602,14 +680,19 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
 #pragma unroll
       for (int qq = 0; qq < 4; ++qq) {
         const int d0 = dt * 32 + 8 * qq + 4 * g;
-        bf16x4 bb;
+        bf16x4 bb, bl;
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           bb[u] = (bf16)o[4 * qq + u];
           sm.u.fin.vT[d0 + u][lslot] = bb[u];
+          if constexpr (EXACT) {
+            bl[u] = (bf16)(o[4 * qq + u] - (float)bb[u]);
+            sm.u.fin.vTl[d0 + u][lslot] = bl[u];
+          }
         }
         *reinterpret_cast<bf16x4*>(ob + d0) = bb;
         *reinterpret_cast<bf16x4*>(ou + d0) = bb;
+        if constexpr (EXACT) *reinterpret_cast<bf16x4*>(dvbl + ((int64_t)bh * T + r) * D + d0) = bl;
       }
     }
   };
@@ -634,8 +717,16 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
     f32x16 cr[NDT];
 #pragma unroll
     for (int t = 0; t < NDT; ++t) {
-      cr[t] = mfma32(ld8(&sm.u.fin.vT[t * 32 + l32][64 + kb * 32 + 8 * g]), p0, zero16());
-      cr[t] = mfma32(ld8(&sm.u.fin.vT[t * 32 + l32][64 + kb * 32 + 16 + 8 * g]), p1, cr[t]);
+      const bf16x8 v0 = ld8(&sm.u.fin.vT[t * 32 + l32][64 + kb * 32 + 8 * g]);
+      const bf16x8 v1 = ld8(&sm.u.fin.vT[t * 32 + l32][64 + kb * 32 + 16 + 8 * g]);
+      cr[t] = mfma32(v0, p0, zero16());
+      cr[t] = mfma32(v1, p1, cr[t]);
+      if constexpr (EXACT) {
+        cr[t] = mfma32(v0, pack_lo(sc, 0, p0), cr[t]);
+        cr[t] = mfma32(v1, pack_lo(sc, 1, p1), cr[t]);
+        cr[t] = mfma32(ld8(&sm.u.fin.vTl[t * 32 + l32][64 + kb * 32 + 8 * g]), p0, cr[t]);
+        cr[t] = mfma32(ld8(&sm.u.fin.vTl[t * 32 + l32][64 + kb * 32 + 16 + 8 * g]), p1, cr[t]);
+      }
     }
     const int col = na * 32 + l32;
     if (kb == 1) {
@@ -680,6 +771,13 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
         sc = mfma32(ka[st], kbJ[st], sc);
         gg = mfma32(da[st], vbJ[st], gg);
       }
+      if constexpr (EXACT) {
+#pragma unroll
+        for (int st = 0; st < NKS; ++st) {
+          gg = mfma32(da[st], vbJl[st], gg);
+          gg = mfma32(ld8(dvblh + (int64_t)(rbase + l32) * D + 16 * st + 8 * g), vbJ[st], gg);
+        }
+      }
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int rloc = rb * 64 + rh * 32 + drow(e, g), cloc = cw + l32;
@@ -692,6 +790,10 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
         const bf16* kp = kth + (int64_t)(t * 32 + l32) * T + rbase + 8 * g;
         acs[t] = mfma32(ld8(kp), mb0, acs[t]);
         acs[t] = mfma32(ld8(kp + 16), mb1, acs[t]);
+        if constexpr (EXACT) {
+          acs[t] = mfma32(ld8(kp), pack_lo(gg, 0, mb0), acs[t]);
+          acs[t] = mfma32(ld8(kp + 16), pack_lo(gg, 1, mb1), acs[t]);
+        }
       }
     }
   }
@@ -712,32 +814,45 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
 
 // ---------------------------------------------------------------------------
 // Row sums R_I = sum_{J <= I} M_IJ K^_J, then dK^ = -s (R + C), the RMSNorm
-// backward and the attention dK.  No chain: every dV is known.
+// backward and the attention dK (dka; null for the preconditioner-only backward).
+// No chain: every dV is known.
 // Workgroup = 256 rows (heavy, late blocks first); wave w owns rows 64w .. +64
 // (two 32-row n-tiles, lane <-> row) and sweeps both 32-key halves of every
 // staged 64-key tile J (K rows, V' rows, 1/rms; direct global->LDS loads, three
 // buffers, two tiles ahead; K^T operands through transposing LDS loads):
 //   S^T[J][I] = K_J . K_I, G^T[J][I] = V'_J . dV_I, R^T[d][I] += K^T[d][J] (r_J G P)^T[J][I]
 // Each wave finishes its own rows, so no cross-wave reduction is needed.
+// EXACT (heads whose row mass exceeds kExactMass; each instance returns at once for the
+// other heads): G = V' dV^T and M K are split into hi*hi + hi*lo + lo*hi with the lo
+// parts of V' (staged beside V') and dV (held beside dV); one workgroup per CU.
 // ---------------------------------------------------------------------------
-template <int D>
+template <int D, bool EXACT>
 struct ProwSmem {
   bf16 k[3][64 * D];  // swizzled tiles (chunk c of row r at c ^ (r & 7))
   bf16 v[3][64 * D];
   float r[3][64];
 };
-
 template <int D>
-__global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond_bwd_row_kernel(
+struct ProwSmem<D, true> {
+  bf16 k[3][64 * D];
+  bf16 v[3][64 * D];
+  bf16 vl[3][64 * D];  // lo part of V'
+  float r[3][64];
+};
+
+template <int D, bool EXACT>
+__global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void lucid_precond_bwd_row_kernel(
     const bf16* __restrict__ k, Strides ks, int Hkv, int T, int BH, const float* __restrict__ rinv, float scale,
-    const bf16* __restrict__ vpb, const bf16* __restrict__ dvb,
-    const float* __restrict__ colsum, const float* __restrict__ dka, bf16* __restrict__ dk_out, Strides dks) {
+    const bf16* __restrict__ vpb, const bf16* __restrict__ vpbl, const bf16* __restrict__ dvb,
+    const bf16* __restrict__ dvbl, const float* __restrict__ mass, const float* __restrict__ colsum,
+    const float* __restrict__ dka, bf16* __restrict__ dk_out, Strides dks) {
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
-  __shared__ __attribute__((aligned(16))) ProwSmem<D> sm;
+  __shared__ __attribute__((aligned(16))) ProwSmem<D, EXACT> sm;
   const int nblk = (T + 255) / 256;
   const int id = blockIdx.x;
   const int ib = nblk - 1 - id / BH, bh = id - (id / BH) * BH;  // heavy (late) blocks first
+  if ((mass[bh] > kExactMass) != EXACT) return;  // the other instance handles this head
   const int b = bh / Hkv, h = bh - b * Hkv;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
@@ -749,7 +864,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
   const float sl2 = scale * LOG2E_F;
   const float c0 = LOG2E_F / scale;
 
-  bf16x8 kbI[2][NKS], dbI[2][NKS];
+  bf16x8 kbI[2][NKS], dbI[2][NKS], dbIl[2][NKS];
   float aI[2];
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
@@ -758,6 +873,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
     for (int st = 0; st < NKS; ++st) {
       kbI[nt][st] = ld8(kh + (int64_t)ir * ks.t + 16 * st + 8 * g);
       dbI[nt][st] = ld8(dvb + ((int64_t)bh * T + ir) * D + 16 * st + 8 * g);
+      if constexpr (EXACT) dbIl[nt][st] = ld8(dvbl + ((int64_t)bh * T + ir) * D + 16 * st + 8 * g);
     }
     aI[nt] = sl2 * rv[ir];
   }
@@ -768,7 +884,8 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
     acc[t][1] = zero16();
   }
   const int ntile = min(4 * ib + 4, T / 64);  // key tiles 0 .. ntile-1 (>= 2 since T >= 128)
-  constexpr int STAGE_OPS = 2 * (64 * (D / 8) / 256);  // newest vector-memory ops of a step, per wave
+  // newest vector-memory ops of a step, per wave
+  constexpr int STAGE_OPS = (EXACT ? 3 : 2) * (64 * (D / 8) / 256);
   int plan_k[64 * (D / 8) / 256], plan_v[64 * (D / 8) / 256];
   dma_plan<64, D / 8>(ks.t, plan_k);
   dma_plan<64, D / 8>(D, plan_v);
@@ -777,6 +894,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
     if (w == 0) dma_f32x64(rv + j0, sm.r[buf]);
     dma_stage<64, D / 8>(plan_k, kh + (int64_t)j0 * ks.t, sm.k[buf]);
     dma_stage<64, D / 8>(plan_v, vh + (int64_t)j0 * D, sm.v[buf]);
+    if constexpr (EXACT) dma_stage<64, D / 8>(plan_v, vpbl + (int64_t)bh * T * D + (int64_t)j0 * D, sm.vl[buf]);
   };
   stage(0);
   stage(1);
@@ -795,7 +913,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
       }
       float rJ[16];
       lds_rows16(&sm.r[buf][jh * 32], g, rJ);
-      bf16x8 mb[2][2];
+      bf16x8 mb[2][2], ml[2][2];
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt) {
         f32x16 sc = zero16(), gg = zero16();
@@ -803,6 +921,13 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
         for (int st = 0; st < NKS; ++st) {
           sc = mfma32(ka[st], kbI[nt][st], sc);
           gg = mfma32(va[st], dbI[nt][st], gg);
+        }
+        if constexpr (EXACT) {
+#pragma unroll
+          for (int st = 0; st < NKS; ++st) {
+            gg = mfma32(va[st], dbIl[nt][st], gg);
+            gg = mfma32(ld8(swz<D / 8>(sm.vl[buf], jh * 32 + l32, 2 * st + g)), dbI[nt][st], gg);
+          }
         }
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
@@ -812,6 +937,10 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
         }
         mb[nt][0] = pack_b(gg, 0);
         mb[nt][1] = pack_b(gg, 1);
+        if constexpr (EXACT) {
+          ml[nt][0] = pack_lo(gg, 0, mb[nt][0]);
+          ml[nt][1] = pack_lo(gg, 1, mb[nt][1]);
+        }
       }
 #pragma unroll
       for (int t = 0; t < NDT; ++t) {
@@ -821,6 +950,10 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
         for (int nt = 0; nt < 2; ++nt) {
           acc[t][nt] = mfma32(k0, mb[nt][0], acc[t][nt]);
           acc[t][nt] = mfma32(k1, mb[nt][1], acc[t][nt]);
+          if constexpr (EXACT) {
+            acc[t][nt] = mfma32(k0, ml[nt][0], acc[t][nt]);
+            acc[t][nt] = mfma32(k1, ml[nt][1], acc[t][nt]);
+          }
         }
       }
     }
@@ -871,7 +1004,8 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
 #pragma unroll
       for (int qq = 0; qq < 4; ++qq) {
         const int d0 = t * 32 + 8 * qq + 4 * g;
-        const f32x4 av = *reinterpret_cast<const f32x4*>(da + d0);
+        f32x4 av = {0.f, 0.f, 0.f, 0.f};  // no attention part (preconditioner-only backward)
+        if (dka) av = *reinterpret_cast<const f32x4*>(da + d0);
         bf16x4 bb;
 #pragma unroll
         for (int u = 0; u < 4; ++u) {

@@ -15,6 +15,10 @@ namespace {
 
 thread_local std::string g_last_error;
 
+// Precision of the preconditioner chains (lucid_set_precision): LUCID_PRECISION_AUTO picks
+// per head from its row mass (lucid_mass_kernel, kExactMass); the others force one kind.
+int g_precision = LUCID_PRECISION_AUTO;
+
 int fail(const std::string& msg) {
   g_last_error = msg;
   return LUCID_EINVAL;
@@ -39,12 +43,16 @@ struct FwdWs {
   bf16* vpt;     // [BH][D][T]  V'^T, T-perm
   float* pinv;   // [BH][T/64][64][64]  inverses of the diagonal blocks of P
   float* zx;     // [BH][T/128][64][64] -(X_B P_BA) per 128-row block, columns T-perm
+  bf16* vpbl;    // [BH][T][D]  lo part of V' (exact heads)
+  bf16* vptl;    // [BH][D][T]  lo part of V'^T, T-perm (exact heads)
+  float* mass;   // [BH]        largest row mass sum_{j<i} P_ij^2 (sampled; selects the chain precision)
+  bf16* olo;     // [BHq][T][D] lo part of O (exact heads)
   int* counters; // [BH]
   size_t bytes;
 };
 
-FwdWs carve_fwd(void* base, int B, int Hkv, int T, int D) {
-  const size_t BH = (size_t)B * Hkv;
+FwdWs carve_fwd(void* base, int B, int Hq, int Hkv, int T, int D) {
+  const size_t BH = (size_t)B * Hkv, BHq = (size_t)B * Hq;
   FwdWs w{};
   size_t off = 0;
   char* p = static_cast<char*>(base);
@@ -59,6 +67,10 @@ FwdWs carve_fwd(void* base, int B, int Hkv, int T, int D) {
   w.vpt = reinterpret_cast<bf16*>(take(BH * D * T * 2));
   w.pinv = reinterpret_cast<float*>(take(BH * (T / 64) * 4096 * 4));
   w.zx = reinterpret_cast<float*>(take(BH * (T / 128) * 4096 * 4));
+  w.vpbl = reinterpret_cast<bf16*>(take(BH * T * D * 2));
+  w.vptl = reinterpret_cast<bf16*>(take(BH * D * T * 2));
+  w.mass = reinterpret_cast<float*>(take(BH * 4));
+  w.olo = reinterpret_cast<bf16*>(take(BHq * T * D * 2));
   w.counters = reinterpret_cast<int*>(take(BH * 4));
   w.bytes = off;
   return w;
@@ -69,6 +81,7 @@ struct BwdWs {
   float* dvp;    // [BH][T][D]   dV' (summed over the group)
   float* dka;    // [BH][T][D]   dK from the softmax part (scaled)
   bf16* dvb;     // [BH][T][D]   dV bf16
+  bf16* dvbl;    // [BH][T][D]   lo part of dV (exact heads)
   float* colsum; // [BH][T][D]   sum_I M_IJ^T K^_I
   int* counters; // [BH]
   size_t bytes;
@@ -88,6 +101,7 @@ BwdWs carve_bwd(void* base, int B, int Hq, int Hkv, int T, int D) {
   w.dvp = reinterpret_cast<float*>(take(BH * T * D * 4));
   w.dka = reinterpret_cast<float*>(take(BH * T * D * 4));
   w.dvb = reinterpret_cast<bf16*>(take(BH * T * D * 2));
+  w.dvbl = reinterpret_cast<bf16*>(take(BH * T * D * 2));
   w.colsum = reinterpret_cast<float*>(take(BH * T * D * 4));
   w.counters = reinterpret_cast<int*>(take(BH * 4));
   w.bytes = off;
@@ -126,13 +140,25 @@ template <int D>
 int launch_precond_fwd(const void* k, const int64_t* ks, const void* v, const int64_t* vs, float* vprime,
                        const FwdWs& w, int B, int Hkv, int T, float scale, float eps, hipStream_t st) {
   const int BH = B * Hkv;
+  // a forced precision is written straight into the head masses (no mass pass)
+  const float mass_init = g_precision == LUCID_PRECISION_EXACT ? 1e30f : 0.f;
   LUCID_LAUNCH("lucid_prep_kernel", lucid::lucid_prep_kernel<D>, dim3(T / 64, BH), st, (const bf16*)k, S(ks), Hkv,
-               T, eps, scale, w.rinv, w.kt, w.pinv, w.counters);
+               T, eps, scale, w.rinv, w.kt, w.pinv, w.counters, w.mass, mass_init);
+  if (g_precision == LUCID_PRECISION_AUTO)
+    LUCID_LAUNCH("lucid_mass_kernel", lucid::lucid_mass_kernel<D>, dim3(T / 64, BH), st, (const bf16*)k, S(ks),
+                 Hkv, T, w.rinv, scale, w.mass);
   LUCID_LAUNCH("lucid_zx_kernel", lucid::lucid_zx_kernel<D>, dim3(T / 128, BH), st, (const bf16*)k, S(ks), Hkv, T,
                w.rinv, scale, w.pinv, w.zx);
-  LUCID_LAUNCH("lucid_precond_fwd_kernel", lucid::lucid_precond_fwd_kernel<D>, dim3((T / 128) * BH), st,
-               (const bf16*)k, S(ks), (const bf16*)v, S(vs), Hkv, T, BH, w.rinv, scale, vprime, w.vpb, w.vpt,
-               w.pinv, w.zx, w.counters);
+  // both instances of the chain: each solves the heads of its precision and returns at
+  // once for the others
+  if (g_precision != LUCID_PRECISION_EXACT)
+    LUCID_LAUNCH("lucid_precond_fwd_kernel", (lucid::lucid_precond_fwd_kernel<D, false>), dim3((T / 128) * BH),
+                 st, (const bf16*)k, S(ks), (const bf16*)v, S(vs), Hkv, T, BH, w.rinv, scale, vprime, w.vpb,
+                 w.vpt, w.vpbl, w.vptl, w.pinv, w.zx, w.mass, w.counters);
+  if (g_precision != LUCID_PRECISION_FAST)
+    LUCID_LAUNCH("lucid_precond_fwd_exact_kernel", (lucid::lucid_precond_fwd_kernel<D, true>),
+                 dim3((T / 128) * BH), st, (const bf16*)k, S(ks), (const bf16*)v, S(vs), Hkv, T, BH, w.rinv,
+                 scale, vprime, w.vpb, w.vpt, w.vpbl, w.vptl, w.pinv, w.zx, w.mass, w.counters);
   return LUCID_OK;
 }
 
@@ -143,7 +169,52 @@ int launch_fwd(const void* q, const int64_t* qs, const void* k, const int64_t* k
   if (int rc = launch_precond_fwd<D>(k, ks, v, vs, vprime, w, B, Hkv, T, scale, eps, st)) return rc;
   const int BHq = B * Hq;
   LUCID_LAUNCH("lucid_attn_fwd_kernel", lucid::lucid_attn_fwd_kernel<D>, dim3(((T + 255) / 256) * BHq), st, (const bf16*)q,
-               S(qs), (const bf16*)k, S(ks), w.vpt, (bf16*)o, S(os), lse, Hq, Hkv, T, BHq, scale);
+               S(qs), (const bf16*)k, S(ks), w.vpt, (bf16*)o, S(os), lse, w.mass, w.olo, Hq, Hkv, T, BHq, scale);
+  return LUCID_OK;
+}
+
+// The attention part of the backward: delta, dV' and the softmax dK (into w.dvp, w.dka)
+// and dQ.  Reads f.vpb, f.olo and f.mass.
+template <int D>
+int launch_attn_bwd(const void* dout, const int64_t* dos, const void* q, const int64_t* qs, const void* k,
+                    const int64_t* ks, const void* o, const int64_t* os, const float* lse, const FwdWs& f, void* dq,
+                    const int64_t* dqs, const BwdWs& w, int B, int Hq, int Hkv, int T, float scale, hipStream_t st) {
+  const int BH = B * Hkv, BHq = B * Hq;
+  LUCID_LAUNCH("lucid_bwd_prep_kernel", lucid::lucid_bwd_prep_kernel<D>, dim3(T / 64, BHq), st, (const bf16*)dout,
+               S(dos), (const bf16*)o, S(os), f.olo, f.mass, Hq, Hkv, T, w.delta, w.counters, BH);
+  LUCID_LAUNCH("lucid_attn_bwd_dkdv_kernel", lucid::lucid_attn_bwd_dkdv_kernel<D>, dim3((T / 128) * BH), st,
+               (const bf16*)q, S(qs), (const bf16*)k, S(ks), f.vpb, (const bf16*)dout, S(dos), lse,
+               w.delta, w.dvp, w.dka, Hq, Hkv, T, BH, scale);
+  LUCID_LAUNCH("lucid_attn_bwd_dq_kernel", (lucid::lucid_attn_bwd_dq_kernel<D, false>),
+               dim3(((T + 255) / 256) * BHq), st, (const bf16*)q, S(qs), (const bf16*)k, S(ks), f.vpb,
+               (const bf16*)dout, S(dos), lse, w.delta, f.mass, (bf16*)dq, S(dqs), Hq, Hkv, T, BHq, scale);
+  LUCID_LAUNCH("lucid_attn_bwd_dq_exact_kernel", (lucid::lucid_attn_bwd_dq_kernel<D, true>),
+               dim3(((T + 255) / 256) * BHq), st, (const bf16*)q, S(qs), (const bf16*)k, S(ks), f.vpb,
+               (const bf16*)dout, S(dos), lse, w.delta, f.mass, (bf16*)dq, S(dqs), Hq, Hkv, T, BHq, scale);
+  return LUCID_OK;
+}
+
+// The preconditioner part: dV = P^-T dV' (w.dvp, counters zeroed), then dK with the softmax
+// part w.dka added (null: none).  Reads the forward's K operands, V' and row masses.
+template <int D>
+int launch_precond_bwd(const void* k, const int64_t* ks, const FwdWs& f, void* dk, const int64_t* dks, void* dv,
+                       const int64_t* dvs, const BwdWs& w, const float* dka, int B, int Hkv, int T, float scale,
+                       hipStream_t st) {
+  const int BH = B * Hkv;
+  // each chain kernel in two instances (bf16 and exact), selected per head by the forward's
+  // row mass; the precision forced at the forward call is recorded there
+  LUCID_LAUNCH("lucid_precond_bwd_col_kernel", (lucid::lucid_precond_bwd_col_kernel<D, false>),
+               dim3((T / 128) * BH), st, (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, scale, f.kt, f.vpb, f.vpbl,
+               f.pinv, f.mass, w.dvp, w.dvb, w.dvbl, (bf16*)dv, S(dvs), w.colsum, w.counters);
+  LUCID_LAUNCH("lucid_precond_bwd_col_exact_kernel", (lucid::lucid_precond_bwd_col_kernel<D, true>),
+               dim3((T / 128) * BH), st, (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, scale, f.kt, f.vpb, f.vpbl,
+               f.pinv, f.mass, w.dvp, w.dvb, w.dvbl, (bf16*)dv, S(dvs), w.colsum, w.counters);
+  LUCID_LAUNCH("lucid_precond_bwd_row_kernel", (lucid::lucid_precond_bwd_row_kernel<D, false>),
+               dim3(((T + 255) / 256) * BH), st, (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, scale, f.vpb, f.vpbl,
+               w.dvb, w.dvbl, f.mass, w.colsum, dka, (bf16*)dk, S(dks));
+  LUCID_LAUNCH("lucid_precond_bwd_row_exact_kernel", (lucid::lucid_precond_bwd_row_kernel<D, true>),
+               dim3(((T + 255) / 256) * BH), st, (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, scale, f.vpb, f.vpbl,
+               w.dvb, w.dvbl, f.mass, w.colsum, dka, (bf16*)dk, S(dks));
   return LUCID_OK;
 }
 
@@ -152,22 +223,114 @@ int launch_bwd(const void* dout, const int64_t* dos, const void* q, const int64_
                const int64_t* ks, const void* o, const int64_t* os, const float* lse, const FwdWs& f, void* dq,
                const int64_t* dqs, void* dk, const int64_t* dks, void* dv, const int64_t* dvs, const BwdWs& w, int B,
                int Hq, int Hkv, int T, float scale, hipStream_t st) {
+  if (int rc = launch_attn_bwd<D>(dout, dos, q, qs, k, ks, o, os, lse, f, dq, dqs, w, B, Hq, Hkv, T, scale, st))
+    return rc;
+  return launch_precond_bwd<D>(k, ks, f, dk, dks, dv, dvs, w, w.dka, B, Hkv, T, scale, st);
+}
+
+// ---- the two operator seams (get_v_prime / eager_lucid_attention_forward) ----
+
+// Workspace of the attention on a caller's V': the operand copies of V', 1/rms of K,
+// the row masses and O's lo part (the FwdWs fields the attention kernels read).
+FwdWs carve_attn_vp(void* base, int B, int Hq, int Hkv, int T, int D) {
+  const size_t BH = (size_t)B * Hkv, BHq = (size_t)B * Hq;
+  FwdWs w{};
+  size_t off = 0;
+  char* p = static_cast<char*>(base);
+  auto take = [&](size_t n) {
+    char* r = p ? p + off : nullptr;
+    off += align256(n);
+    return r;
+  };
+  w.rinv = reinterpret_cast<float*>(take(BH * T * 4));
+  w.vpb = reinterpret_cast<bf16*>(take(BH * T * D * 2));
+  w.vpt = reinterpret_cast<bf16*>(take(BH * D * T * 2));
+  w.mass = reinterpret_cast<float*>(take(BH * 4));
+  w.olo = reinterpret_cast<bf16*>(take(BHq * T * D * 2));
+  w.bytes = off;
+  return w;
+}
+
+// Backward scratch of one seam: the attention part needs delta, dV' and the softmax dK, the
+// preconditioner part dV' (as fp32), dV and its lo part, the column sums and counters.
+BwdWs carve_seam_bwd(void* base, int B, int Hq, int Hkv, int T, int D, bool attn) {
+  const size_t BH = (size_t)B * Hkv, BHq = (size_t)B * Hq;
+  BwdWs w{};
+  size_t off = 0;
+  char* p = static_cast<char*>(base);
+  auto take = [&](size_t n) {
+    char* r = p ? p + off : nullptr;
+    off += align256(n);
+    return r;
+  };
+  w.dvp = reinterpret_cast<float*>(take(BH * T * D * 4));
+  if (attn) {
+    w.delta = reinterpret_cast<float*>(take(BHq * T * 4));
+    w.dka = reinterpret_cast<float*>(take(BH * T * D * 4));
+  } else {
+    w.dvb = reinterpret_cast<bf16*>(take(BH * T * D * 2));
+    w.dvbl = reinterpret_cast<bf16*>(take(BH * T * D * 2));
+    w.colsum = reinterpret_cast<float*>(take(BH * T * D * 4));
+  }
+  w.counters = reinterpret_cast<int*>(take(BH * 4));
+  w.bytes = off;
+  return w;
+}
+
+template <int D>
+int launch_attn_vp_fwd(const void* q, const int64_t* qs, const void* k, const int64_t* ks, const void* vp,
+                       const int64_t* vs, int vp_f32, void* o, const int64_t* os, float* lse, const FwdWs& w, int B,
+                       int Hq, int Hkv, int T, float scale, float eps, hipStream_t st) {
   const int BH = B * Hkv, BHq = B * Hq;
-  LUCID_LAUNCH("lucid_bwd_prep_kernel", lucid::lucid_bwd_prep_kernel<D>, dim3(T / 64, BHq), st, (const bf16*)dout,
-               S(dos), (const bf16*)o, S(os), Hq, T, w.delta, w.counters, BH);
-  LUCID_LAUNCH("lucid_attn_bwd_dkdv_kernel", lucid::lucid_attn_bwd_dkdv_kernel<D>, dim3((T / 128) * BH), st,
-               (const bf16*)q, S(qs), (const bf16*)k, S(ks), f.vpb, (const bf16*)dout, S(dos), lse,
-               w.delta, w.dvp, w.dka, Hq, Hkv, T, BH, scale);
-  LUCID_LAUNCH("lucid_attn_bwd_dq_kernel", lucid::lucid_attn_bwd_dq_kernel<D>, dim3(((T + 255) / 256) * BHq), st,
-               (const bf16*)q, S(qs), (const bf16*)k, S(ks), f.vpb, (const bf16*)dout, S(dos), lse, w.delta,
-               (bf16*)dq, S(dqs), Hq, Hkv, T, BHq, scale);
-  LUCID_LAUNCH("lucid_precond_bwd_col_kernel", lucid::lucid_precond_bwd_col_kernel<D>, dim3((T / 128) * BH), st,
-               (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, scale, f.kt, f.vpb, f.pinv, w.dvp, w.dvb,
-               (bf16*)dv, S(dvs), w.colsum, w.counters);
-  LUCID_LAUNCH("lucid_precond_bwd_row_kernel", lucid::lucid_precond_bwd_row_kernel<D>, dim3(((T + 255) / 256) * BH), st,
-               (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, scale, f.vpb, w.dvb, w.colsum, w.dka, (bf16*)dk,
-               S(dks));
+  const float mass_init = g_precision == LUCID_PRECISION_EXACT ? 1e30f : 0.f;
+  if (vp_f32)
+    LUCID_LAUNCH("lucid_vp_layout_kernel", (lucid::lucid_vp_layout_kernel<D, float>), dim3(T / 64, BH), st,
+                 (const bf16*)k, S(ks), (const float*)vp, S(vs), Hkv, T, eps, w.rinv, w.vpb, w.vpt, w.mass,
+                 mass_init);
+  else
+    LUCID_LAUNCH("lucid_vp_layout_kernel", (lucid::lucid_vp_layout_kernel<D, bf16>), dim3(T / 64, BH), st,
+                 (const bf16*)k, S(ks), (const bf16*)vp, S(vs), Hkv, T, eps, w.rinv, w.vpb, w.vpt, w.mass,
+                 mass_init);
+  if (g_precision == LUCID_PRECISION_AUTO)
+    LUCID_LAUNCH("lucid_mass_kernel", lucid::lucid_mass_kernel<D>, dim3(T / 64, BH), st, (const bf16*)k, S(ks),
+                 Hkv, T, w.rinv, scale, w.mass);
+  LUCID_LAUNCH("lucid_attn_fwd_kernel", lucid::lucid_attn_fwd_kernel<D>, dim3(((T + 255) / 256) * BHq), st,
+               (const bf16*)q, S(qs), (const bf16*)k, S(ks), w.vpt, (bf16*)o, S(os), lse, w.mass, w.olo, Hq, Hkv, T,
+               BHq, scale);
   return LUCID_OK;
+}
+
+template <int D>
+int launch_attn_vp_bwd(const void* dout, const int64_t* dos, const void* q, const int64_t* qs, const void* k,
+                       const int64_t* ks, const void* o, const int64_t* os, const float* lse, const FwdWs& f,
+                       void* dq, const int64_t* dqs, void* dk, const int64_t* dks, void* dvp, const int64_t* dvps,
+                       int dvp_f32, const BwdWs& w, int B, int Hq, int Hkv, int T, float scale, hipStream_t st) {
+  const int BH = B * Hkv;
+  if (int rc = launch_attn_bwd<D>(dout, dos, q, qs, k, ks, o, os, lse, f, dq, dqs, w, B, Hq, Hkv, T, scale, st))
+    return rc;
+  LUCID_LAUNCH("lucid_rows_out_kernel", (lucid::lucid_rows_out_kernel<D, bf16>), dim3(T / 64, BH), st, w.dka,
+               (bf16*)dk, S(dks), Hkv, T, 1.f);
+  if (dvp_f32)
+    LUCID_LAUNCH("lucid_rows_out_kernel", (lucid::lucid_rows_out_kernel<D, float>), dim3(T / 64, BH), st, w.dvp,
+                 (float*)dvp, S(dvps), Hkv, T, 1.f);
+  else
+    LUCID_LAUNCH("lucid_rows_out_kernel", (lucid::lucid_rows_out_kernel<D, bf16>), dim3(T / 64, BH), st, w.dvp,
+                 (bf16*)dvp, S(dvps), Hkv, T, 1.f);
+  return LUCID_OK;
+}
+
+template <int D>
+int launch_precond_only_bwd(const void* k, const int64_t* ks, const void* dvp, const int64_t* dvps, int dvp_f32,
+                            const FwdWs& f, void* dk, const int64_t* dks, void* dv, const int64_t* dvs,
+                            const BwdWs& w, int B, int Hkv, int T, float scale, hipStream_t st) {
+  const int BH = B * Hkv;
+  if (dvp_f32)
+    LUCID_LAUNCH("lucid_rows_in_kernel", (lucid::lucid_rows_in_kernel<D, float>), dim3(T / 64, BH), st,
+                 (const float*)dvp, S(dvps), w.dvp, Hkv, T, w.counters);
+  else
+    LUCID_LAUNCH("lucid_rows_in_kernel", (lucid::lucid_rows_in_kernel<D, bf16>), dim3(T / 64, BH), st,
+                 (const bf16*)dvp, S(dvps), w.dvp, Hkv, T, w.counters);
+  return launch_precond_bwd<D>(k, ks, f, dk, dks, dv, dvs, w, nullptr, B, Hkv, T, scale, st);
 }
 
 // Decoding: split the cached sequence so that one resident round of split workgroups
@@ -272,13 +435,27 @@ int lucid_decode(const void* q, const int64_t* q_strides, const void* k, const i
                                 st);
 }
 
-int lucid_abi_version(void) { return 1; }
+int lucid_abi_version(void) { return 2; }
+
+int lucid_set_precision(int mode) {
+  g_last_error.clear();
+  if (mode != LUCID_PRECISION_AUTO && mode != LUCID_PRECISION_FAST && mode != LUCID_PRECISION_EXACT)
+    return fail("precision mode must be LUCID_PRECISION_AUTO, _FAST or _EXACT, got " + std::to_string(mode));
+  g_precision = mode;
+  return LUCID_OK;
+}
+
+int lucid_get_precision(void) { return g_precision; }
+
+size_t lucid_fwd_workspace_mass_offset(int B, int Hq, int Hkv, int T, int D) {
+  char* base = reinterpret_cast<char*>(size_t(256));  // any non-null 256-aligned base
+  return static_cast<size_t>(reinterpret_cast<char*>(carve_fwd(base, B, Hq, Hkv, T, D).mass) - base);
+}
 
 const char* lucid_last_error(void) { return g_last_error.c_str(); }
 
 size_t lucid_fwd_workspace_bytes(int B, int Hq, int Hkv, int T, int D) {
-  (void)Hq;
-  return carve_fwd(nullptr, B, Hkv, T, D).bytes;
+  return carve_fwd(nullptr, B, Hq, Hkv, T, D).bytes;
 }
 
 size_t lucid_bwd_workspace_bytes(int B, int Hq, int Hkv, int T, int D) {
@@ -294,7 +471,7 @@ int lucid_get_v_prime(const void* k, const int64_t* k_strides, const void* v, co
   if (int rc = check_tensor("v", v, v_strides)) return rc;
   if (!vprime || !fwd_ws) return fail("vprime and fwd_ws must be non-null");
   if (int rc = check_ws("fwd_ws", fwd_ws)) return rc;
-  const FwdWs w = carve_fwd(fwd_ws, B, Hkv, T, D);
+  const FwdWs w = carve_fwd(fwd_ws, B, Hkv, Hkv, T, D);
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (D == 64) return launch_precond_fwd<64>(k, k_strides, v, v_strides, vprime, w, B, Hkv, T, scale, eps, st);
   return launch_precond_fwd<128>(k, k_strides, v, v_strides, vprime, w, B, Hkv, T, scale, eps, st);
@@ -312,7 +489,7 @@ int lucid_attn_fwd(const void* q, const int64_t* q_strides, const void* k, const
   if (int rc = check_tensor("o", o, o_strides)) return rc;
   if (!vprime || !lse || !fwd_ws) return fail("vprime, lse and fwd_ws must be non-null");
   if (int rc = check_ws("fwd_ws", fwd_ws)) return rc;
-  const FwdWs w = carve_fwd(fwd_ws, B, Hkv, T, D);
+  const FwdWs w = carve_fwd(fwd_ws, B, Hq, Hkv, T, D);
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (D == 64)
     return launch_fwd<64>(q, q_strides, k, k_strides, v, v_strides, o, o_strides, vprime, lse, w, B, Hq, Hkv, T,
@@ -339,7 +516,7 @@ int lucid_attn_bwd(const void* dout, const int64_t* do_strides, const void* q, c
   if (!lse || !fwd_ws || !bwd_ws) return fail("lse, fwd_ws and bwd_ws must be non-null");
   if (int rc = check_ws("fwd_ws", fwd_ws)) return rc;
   if (int rc = check_ws("bwd_ws", bwd_ws)) return rc;
-  const FwdWs f = carve_fwd(const_cast<void*>(fwd_ws), B, Hkv, T, D);
+  const FwdWs f = carve_fwd(const_cast<void*>(fwd_ws), B, Hq, Hkv, T, D);
   const BwdWs w = carve_bwd(bwd_ws, B, Hq, Hkv, T, D);
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (D == 64)
@@ -347,6 +524,90 @@ int lucid_attn_bwd(const void* dout, const int64_t* do_strides, const void* q, c
                           dk_strides, dv, dv_strides, w, B, Hq, Hkv, T, scale, st);
   return launch_bwd<128>(dout, do_strides, q, q_strides, k, k_strides, o, o_strides, lse, f, dq, dq_strides, dk,
                          dk_strides, dv, dv_strides, w, B, Hq, Hkv, T, scale, st);
+}
+
+size_t lucid_attn_vp_fwd_workspace_bytes(int B, int Hq, int Hkv, int T, int D) {
+  return carve_attn_vp(nullptr, B, Hq, Hkv, T, D).bytes;
+}
+
+int lucid_attn_vp_fwd(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                      const void* vprime, const int64_t* vprime_strides, int vprime_f32, void* o,
+                      const int64_t* o_strides, float* lse, void* ws, int B, int Hq, int Hkv, int T, int D,
+                      float scale, float eps, void* stream) {
+  g_last_error.clear();
+  if (int rc = check_dims(B, Hq, Hkv, T, D)) return rc;
+  if (int rc = check_tensor("q", q, q_strides)) return rc;
+  if (int rc = check_tensor("k", k, k_strides)) return rc;
+  if (int rc = check_tensor("vprime", vprime, vprime_strides)) return rc;
+  if (int rc = check_tensor("o", o, o_strides)) return rc;
+  if (!lse || !ws) return fail("lse and ws must be non-null");
+  if (int rc = check_ws("ws", ws)) return rc;
+  const FwdWs w = carve_attn_vp(ws, B, Hq, Hkv, T, D);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (D == 64)
+    return launch_attn_vp_fwd<64>(q, q_strides, k, k_strides, vprime, vprime_strides, vprime_f32, o, o_strides, lse,
+                                  w, B, Hq, Hkv, T, scale, eps, st);
+  return launch_attn_vp_fwd<128>(q, q_strides, k, k_strides, vprime, vprime_strides, vprime_f32, o, o_strides, lse,
+                                 w, B, Hq, Hkv, T, scale, eps, st);
+}
+
+size_t lucid_attn_vp_bwd_workspace_bytes(int B, int Hq, int Hkv, int T, int D) {
+  return carve_seam_bwd(nullptr, B, Hq, Hkv, T, D, true).bytes;
+}
+
+int lucid_attn_vp_bwd(const void* dout, const int64_t* do_strides, const void* q, const int64_t* q_strides,
+                      const void* k, const int64_t* k_strides, const void* o, const int64_t* o_strides,
+                      const float* lse, const void* fwd_ws, void* dq, const int64_t* dq_strides, void* dk,
+                      const int64_t* dk_strides, void* dvprime, const int64_t* dvprime_strides, int dvprime_f32,
+                      void* bwd_ws, int B, int Hq, int Hkv, int T, int D, float scale, void* stream) {
+  g_last_error.clear();
+  if (int rc = check_dims(B, Hq, Hkv, T, D)) return rc;
+  if (int rc = check_tensor("dout", dout, do_strides)) return rc;
+  if (int rc = check_tensor("q", q, q_strides)) return rc;
+  if (int rc = check_tensor("k", k, k_strides)) return rc;
+  if (int rc = check_tensor("o", o, o_strides)) return rc;
+  if (int rc = check_tensor("dq", dq, dq_strides)) return rc;
+  if (int rc = check_tensor("dk", dk, dk_strides)) return rc;
+  if (int rc = check_tensor("dvprime", dvprime, dvprime_strides)) return rc;
+  if (!lse || !fwd_ws || !bwd_ws) return fail("lse, fwd_ws and bwd_ws must be non-null");
+  if (int rc = check_ws("fwd_ws", fwd_ws)) return rc;
+  if (int rc = check_ws("bwd_ws", bwd_ws)) return rc;
+  const FwdWs f = carve_attn_vp(const_cast<void*>(fwd_ws), B, Hq, Hkv, T, D);
+  const BwdWs w = carve_seam_bwd(bwd_ws, B, Hq, Hkv, T, D, true);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (D == 64)
+    return launch_attn_vp_bwd<64>(dout, do_strides, q, q_strides, k, k_strides, o, o_strides, lse, f, dq,
+                                  dq_strides, dk, dk_strides, dvprime, dvprime_strides, dvprime_f32, w, B, Hq, Hkv,
+                                  T, scale, st);
+  return launch_attn_vp_bwd<128>(dout, do_strides, q, q_strides, k, k_strides, o, o_strides, lse, f, dq, dq_strides,
+                                 dk, dk_strides, dvprime, dvprime_strides, dvprime_f32, w, B, Hq, Hkv, T, scale, st);
+}
+
+size_t lucid_precond_bwd_workspace_bytes(int B, int Hkv, int T, int D) {
+  return carve_seam_bwd(nullptr, B, Hkv, Hkv, T, D, false).bytes;
+}
+
+int lucid_precond_bwd(const void* k, const int64_t* k_strides, const void* dvprime, const int64_t* dvprime_strides,
+                      int dvprime_f32, const void* fwd_ws, void* dk, const int64_t* dk_strides, void* dv,
+                      const int64_t* dv_strides, void* bwd_ws, int B, int Hkv, int T, int D, float scale,
+                      void* stream) {
+  g_last_error.clear();
+  if (int rc = check_dims(B, Hkv, Hkv, T, D)) return rc;
+  if (int rc = check_tensor("k", k, k_strides)) return rc;
+  if (int rc = check_tensor("dvprime", dvprime, dvprime_strides)) return rc;
+  if (int rc = check_tensor("dk", dk, dk_strides)) return rc;
+  if (int rc = check_tensor("dv", dv, dv_strides)) return rc;
+  if (!fwd_ws || !bwd_ws) return fail("fwd_ws and bwd_ws must be non-null");
+  if (int rc = check_ws("fwd_ws", fwd_ws)) return rc;
+  if (int rc = check_ws("bwd_ws", bwd_ws)) return rc;
+  const FwdWs f = carve_fwd(const_cast<void*>(fwd_ws), B, Hkv, Hkv, T, D);
+  const BwdWs w = carve_seam_bwd(bwd_ws, B, Hkv, Hkv, T, D, false);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (D == 64)
+    return launch_precond_only_bwd<64>(k, k_strides, dvprime, dvprime_strides, dvprime_f32, f, dk, dk_strides, dv,
+                                       dv_strides, w, B, Hkv, T, scale, st);
+  return launch_precond_only_bwd<128>(k, k_strides, dvprime, dvprime_strides, dvprime_f32, f, dk, dk_strides, dv,
+                                      dv_strides, w, B, Hkv, T, scale, st);
 }
 
 void lucid_profile_enable(int on) { lucid_prof::enabled() = on != 0; }

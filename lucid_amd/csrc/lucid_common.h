@@ -10,6 +10,26 @@ struct Strides {
   int64_t b, h, t;
 };
 
+// Precision of the preconditioner chains, chosen per head.  The off-diagonal products
+// P_ij V'_j (forward), P_ij dV_i (transposed solve) and the M = (dV V'^T) * P sums of the
+// backward accumulate over every earlier (later) key of a row, and with bf16 operands
+// their rounding error grows like 2^-8 |V'| sqrt(m_i), m_i = sum_{j<i} P_ij^2 (measured
+// on CPU emulations of the kernels: ~1e-3 sqrt(m) relative for V' and dV).  A head whose
+// largest row mass exceeds kExactMass runs the exact chain kernels, which carry V' and
+// dV as bf16 hi/lo pairs and split every such product into hi*hi + hi*lo + lo*hi (~fp32
+// accuracy); the others run the bf16 kernels.  Keys with no common direction
+// (N(0,1)-like) give m ~ 1e-2; keys along a shared direction give m ~ T.
+constexpr float kExactMass = 4.0f;
+
+// bf16 of the residual x - hi for D-layout values e = 8h .. 8h+7 (hi = pack_b(x, h)):
+// the lo term of a two-term bf16 split (x ~= hi + lo to ~2^-17 relative)
+__device__ __forceinline__ bf16x8 pack_lo(const f32x16& x, int h, const bf16x8& hi) {
+  bf16x8 r;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r[e] = (bf16)(x[8 * h + e] - (float)hi[e]);
+  return r;
+}
+
 // X = P^-1 for a 64x64 lower-triangular fp32 block held in LDS (row-major,
 // row stride 68).  Called by ONE wave: lane c solves column c by forward
 // substitution, x_r = (delta_rc - sum_{k<r} P_rk x_k) / P_rr.  The diagonal of

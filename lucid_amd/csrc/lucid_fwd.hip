@@ -20,13 +20,16 @@ namespace lucid {
 // ---------------------------------------------------------------------------
 // prep: rinv[bh][t] = 1/sqrt(mean K^2 + eps); kt[bh][d][perm(t)] = K[t][d];
 // pinv[bh][blk] = inverse of the 64x64 diagonal block of P (fp32 forward
-// substitution by wave 0); zero the chain counter.  grid (T/64, B*Hkv)
+// substitution by wave 0); zero the chain counter and set the head's row mass
+// to mass_init (0 before lucid_mass_kernel; a forced precision sets it directly).
+// grid (T/64, B*Hkv)
 // ---------------------------------------------------------------------------
 template <int D>
 __global__ __launch_bounds__(256) void lucid_prep_kernel(const bf16* __restrict__ k, Strides ks, int Hkv, int T,
                                                          float eps, float scale, float* __restrict__ rinv,
                                                          bf16* __restrict__ kt, float* __restrict__ pinv,
-                                                         int* __restrict__ counters) {
+                                                         int* __restrict__ counters, float* __restrict__ mass,
+                                                         float mass_init) {
   constexpr int SEG = D / 4;
   constexpr int NKS = D / 16;
   __shared__ bf16 tile[D][64 + 8];
@@ -56,7 +59,10 @@ __global__ __launch_bounds__(256) void lucid_prep_kernel(const bf16* __restrict_
     rinv[(int64_t)bh * T + blk * 64 + row] = ri;
     rr[row] = ri;
   }
-  if (blk == 0 && tid == 0) counters[bh] = 0;
+  if (blk == 0 && tid == 0) {
+    counters[bh] = 0;
+    mass[bh] = mass_init;
+  }
   __syncthreads();
   // T-perm rows: kt[bh][d][blk*64 + slot], slot kappa holds t = jmap(kappa)
   for (int idx = tid; idx < D * 8; idx += 256) {
@@ -88,6 +94,179 @@ __global__ __launch_bounds__(256) void lucid_prep_kernel(const bf16* __restrict_
   }
   __syncthreads();
   if (w == 0) invert_lower64(Pd, lane, pinv + ((int64_t)bh * (T / 64) + blk) * 4096);
+}
+
+// ---------------------------------------------------------------------------
+// Operands of the attention on a caller's V' (eager_lucid_attention_forward): V' rows
+// (bf16 or fp32, strided) to the bf16 row-major copy vpb and the T-perm copy vpt the
+// attention kernels read, 1/rms of K for the row-mass pass, and the head's row mass
+// initialised to mass_init.  grid (T/64, B*Hkv)
+// ---------------------------------------------------------------------------
+template <int D, typename VT>
+__global__ __launch_bounds__(256) void lucid_vp_layout_kernel(const bf16* __restrict__ k, Strides ks,
+                                                              const VT* __restrict__ vp, Strides vs, int Hkv, int T,
+                                                              float eps, float* __restrict__ rinv,
+                                                              bf16* __restrict__ vpb, bf16* __restrict__ vpt,
+                                                              float* __restrict__ mass, float mass_init) {
+  constexpr int SEG = D / 4;
+  __shared__ bf16 tile[D][64 + 8];
+  const int blk = blockIdx.x, bh = blockIdx.y;
+  const int b = bh / Hkv, h = bh - b * Hkv;
+  const int tid = threadIdx.x;
+  const int row = tid >> 2, seg = tid & 3;
+  const int t = blk * 64 + row;
+  const bf16* kr = k + b * ks.b + h * ks.h + (int64_t)t * ks.t;
+  const VT* vr = vp + b * vs.b + h * vs.h + (int64_t)t * vs.t;
+  bf16* ob = vpb + ((int64_t)bh * T + t) * D;
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < SEG; c += 8) {
+    const bf16x8 x = ld8(kr + seg * SEG + c);
+    bf16x8 y;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float f = (float)x[e];
+      ss += f * f;
+      y[e] = (bf16)vr[seg * SEG + c + e];
+      tile[seg * SEG + c + e][row] = y[e];
+    }
+    *reinterpret_cast<bf16x8*>(ob + seg * SEG + c) = y;
+  }
+  ss += __shfl_xor(ss, 1, 64);
+  ss += __shfl_xor(ss, 2, 64);
+  if (seg == 0) rinv[(int64_t)bh * T + t] = 1.0f / sqrtf(ss / (float)D + eps);
+  if (blk == 0 && tid == 0) mass[bh] = mass_init;
+  __syncthreads();
+  for (int idx = tid; idx < D * 8; idx += 256) {
+    const int dd = idx >> 3, c8 = idx & 7;
+    bf16x8 out;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out[e] = tile[dd][(c8 >> 1) * 16 + jmap((c8 & 1) * 8 + e)];
+    *reinterpret_cast<bf16x8*>(vpt + ((int64_t)bh * D + dd) * T + blk * 64 + c8 * 8) = out;
+  }
+}
+
+// Rows of an fp32 [BH][T][D] buffer to a strided bf16 or fp32 tensor (the attention
+// seam's dK and dV' outputs), scaled by `mul`.  grid (T/64, B*H)
+template <int D, typename OT>
+__global__ __launch_bounds__(256) void lucid_rows_out_kernel(const float* __restrict__ src, OT* __restrict__ dst,
+                                                             Strides ds, int H, int T, float mul) {
+  const int blk = blockIdx.x, bh = blockIdx.y;
+  const int b = bh / H, h = bh - b * H;
+  for (int idx = threadIdx.x; idx < 64 * D / 4; idx += 256) {
+    const int r = idx / (D / 4), c4 = (idx % (D / 4)) * 4;
+    const int t = blk * 64 + r;
+    const f32x4 x = *reinterpret_cast<const f32x4*>(src + ((int64_t)bh * T + t) * D + c4);
+    OT* o = dst + b * ds.b + h * ds.h + (int64_t)t * ds.t + c4;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) o[u] = (OT)(x[u] * mul);
+  }
+}
+
+// dV' of the preconditioner-only backward (bf16 or fp32, strided) to the fp32
+// [BH][T][D] buffer the column chain reads; zero the chain counters.  grid (T/64, B*Hkv)
+template <int D, typename IT>
+__global__ __launch_bounds__(256) void lucid_rows_in_kernel(const IT* __restrict__ src, Strides ss,
+                                                            float* __restrict__ dst, int H, int T,
+                                                            int* __restrict__ counters) {
+  const int blk = blockIdx.x, bh = blockIdx.y;
+  const int b = bh / H, h = bh - b * H;
+  if (blk == 0 && threadIdx.x == 0) counters[bh] = 0;
+  for (int idx = threadIdx.x; idx < 64 * D / 4; idx += 256) {
+    const int r = idx / (D / 4), c4 = (idx % (D / 4)) * 4;
+    const int t = blk * 64 + r;
+    const IT* i = src + b * ss.b + h * ss.h + (int64_t)t * ss.t + c4;
+    f32x4 x;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) x[u] = (float)i[u];
+    *reinterpret_cast<f32x4*>(dst + ((int64_t)bh * T + t) * D + c4) = x;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Largest row mass m_i = sum_{j<i} P_ij^2 of a head (the quantity that sets the bf16
+// error of the chain products, see kExactMass).  A workgroup covers the 64 rows of one
+// block: the keys of its own block are summed exactly (j < i), the earlier keys are
+// sampled, at most 128 keys spread evenly over the earlier 64-blocks (one key per block
+// at a row offset that varies with the row block), each weighted by the number of
+// earlier keys it stands for.  Each wave takes 32-key chunks:
+//   S[i][j] = K_i . K_j (lane <-> key j, rows i in the D layout), P = exp(s r_i r_j S - 1/s)
+// The block's largest row total goes to mass[bh] by an integer max of the (non-negative)
+// float bits.  grid (T/64, B*Hkv), after lucid_prep_kernel (1/rms, mass[bh] = 0).
+// ---------------------------------------------------------------------------
+template <int D>
+__global__ __launch_bounds__(256) void lucid_mass_kernel(const bf16* __restrict__ k, Strides ks, int Hkv, int T,
+                                                         const float* __restrict__ rinv, float scale,
+                                                         float* __restrict__ mass) {
+  constexpr int NKS = D / 16;
+  __shared__ float part[4][64];
+  const int blk = blockIdx.x, bh = blockIdx.y;
+  const int b = bh / Hkv, h = bh - b * Hkv;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int g = lane >> 5, l32 = lane & 31;
+  const bf16* kp = k + b * ks.b + h * ks.h;
+  const float* rv = rinv + (int64_t)bh * T;
+  const int i0 = blk * 64;
+  const float c0 = LOG2E_F / scale;
+  bf16x8 ka[2][NKS];  // A operand: the block's rows (m-tiles of 32)
+  float ri[2][16];    // s log2e / rms of the D-layout rows
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+    for (int st = 0; st < NKS; ++st) ka[mt][st] = ld8(kp + (int64_t)(i0 + mt * 32 + l32) * ks.t + 16 * st + 8 * g);
+    load_rows16(rv + i0 + mt * 32, g, ri[mt]);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) ri[mt][e] *= scale * LOG2E_F;
+  }
+  float acc[2][16];
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[mt][e] = 0.f;
+  const int off = (blk * 29) & 63;           // sampled row inside a sampled block
+  const int ns = min(blk, 128);              // sampled keys
+  const int nchunk = 2 + (ns + 31) / 32;     // chunks 0, 1: own block; 2..: sampled
+  const float wsample = ns ? 64.f * (float)blk / (float)ns : 0.f;
+  for (int c = w; c < nchunk; c += 4) {
+    const bool own = c < 2;
+    const int n = 32 * (c - 2) + l32;        // this lane's sample
+    const bool valid = own || n < ns;
+    const int key = own ? i0 + 32 * c + l32 : (valid ? (int)(((int64_t)n * blk) / ns) : 0) * 64 + off;
+    const float wgt = own ? 1.f : (valid ? wsample : 0.f);
+    bf16x8 kb[NKS];
+#pragma unroll
+    for (int st = 0; st < NKS; ++st) kb[st] = ld8(kp + (int64_t)key * ks.t + 16 * st + 8 * g);
+    const float rj = rv[key];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      f32x16 sd = zero16();
+#pragma unroll
+      for (int st = 0; st < NKS; ++st) sd = mfma32(ka[mt][st], kb[st], sd);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        float p = __builtin_amdgcn_exp2f(fmaf(sd[e] * ri[mt][e], rj, -c0));
+        if (own && 32 * c + l32 >= mt * 32 + drow(e, g)) p = 0.f;  // keys j < i only
+        acc[mt][e] = fmaf(wgt * p, p, acc[mt][e]);
+      }
+    }
+  }
+  // sum over the 32 keys of a lane half, then over the waves
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      float x = acc[mt][e];
+#pragma unroll
+      for (int m = 16; m >= 1; m >>= 1) x += __shfl_xor(x, m, 32);
+      if (l32 == 0) part[w][mt * 32 + drow(e, g)] = x;
+    }
+  __syncthreads();
+  if (tid < 64) {
+    float x = part[0][tid] + part[1][tid] + part[2][tid] + part[3][tid];
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) x = fmaxf(x, __shfl_xor(x, m, 64));
+    if (tid == 0) atomicMax(reinterpret_cast<int*>(mass) + bh, __float_as_int(x));
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -170,9 +349,18 @@ __global__ __launch_bounds__(256) void lucid_zx_kernel(const bf16* __restrict__ 
 // after the last pair becomes visible, so everything that does not depend on it (V,
 // the two inverses, Z) is loaded earlier.  At d = 64 two workgroups share a CU (LDS <= 80 KB,
 // <= 256 registers per lane) so that one's MFMA work overlaps the other's exp.
+//
+// EXACT (heads whose row mass exceeds kExactMass; the other instance returns at once for
+// them and vice versa): V' is also kept as its bf16 residual lo = bf16(V' - bf16(V'))
+// (vpbl row-major, vptl T-perm), the staged pairs carry the lo tile too, and every
+// off-diagonal product is split: P V' ~= Ph Vh + Pl Vh + Ph Vl, as is Z V'_A.  The
+// extra tile and registers allow one workgroup per CU; at d = 128 the staged pairs are
+// single-buffered (three 32 KB tiles), each pair staged after the previous one's sweep.
 // ---------------------------------------------------------------------------
+template <int D, bool EXACT>
+struct PfwdSmem;
 template <int D>
-struct PfwdSmem {
+struct PfwdSmem<D, false> {
   union {
     struct {
       bf16 k[2][128 * D];  // swizzled tiles (chunk c of row r at c ^ (r & 7))
@@ -186,18 +374,39 @@ struct PfwdSmem {
     } fin;
   } u;
 };
-
 template <int D>
-__global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond_fwd_kernel(
+struct PfwdSmem<D, true> {
+  static constexpr int NBUF = D == 128 ? 1 : 2;
+  union {
+    struct {
+      bf16 k[NBUF][128 * D];
+      bf16 v[NBUF][D * 128];
+      bf16 vl[NBUF][D * 128];  // lo part of V'^T
+      float r[NBUF][128];
+    } st;
+    struct {
+      float Rt[D][132];
+      float X[64][68];
+      bf16 vT[D][128 + 8];
+      bf16 vTl[D][128 + 8];  // lo part of V'^T of the block
+    } fin;
+  } u;
+};
+
+template <int D, bool EXACT>
+__global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void lucid_precond_fwd_kernel(
     const bf16* __restrict__ k, Strides ks, const bf16* __restrict__ v, Strides vs, int Hkv, int T, int BH,
     const float* __restrict__ rinv, float scale, float* __restrict__ vp32, bf16* __restrict__ vpb,
-    bf16* __restrict__ vpt, float* __restrict__ pinv, const float* __restrict__ zx, int* __restrict__ counters) {
+    bf16* __restrict__ vpt, bf16* __restrict__ vpbl, bf16* __restrict__ vptl, float* __restrict__ pinv,
+    const float* __restrict__ zx, const float* __restrict__ mass, int* __restrict__ counters) {
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
-  __shared__ __attribute__((aligned(16))) PfwdSmem<D> sm;
+  constexpr bool SINGLE = EXACT && D == 128;  // one staging buffer
+  __shared__ __attribute__((aligned(16))) PfwdSmem<D, EXACT> sm;
 
   const int id = blockIdx.x;
   const int i2 = id / BH, bh = id - (id / BH) * BH;
+  if ((mass[bh] > kExactMass) != EXACT) return;  // the other instance solves this head
   const int b = bh / Hkv, h = bh - b * Hkv;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
@@ -208,6 +417,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
   const bf16* vh = v + b * vs.b + h * vs.h;
   const float* rv = rinv + (int64_t)bh * T;
   const bf16* vpth = vpt + (int64_t)bh * D * T;
+  const bf16* vptlh = vptl + (int64_t)bh * D * T;
   const float* pinv_blk = pinv + ((int64_t)bh * NT + 2 * i2) * 4096;
   int* cnt = counters + bh;
   const float sl2 = scale * LOG2E_F;
@@ -246,10 +456,11 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
   dma_plan<128, D / 8>(ks.t, plan_k);
   dma_plan<D, 16>(T, plan_v);
   auto stage = [&](int pp) {
-    const int buf = pp & 1;
+    const int buf = SINGLE ? 0 : pp & 1;
     if (w < 2) dma_f32x64(rv + pp * 128 + 64 * w, &sm.u.st.r[buf][64 * w]);
     dma_stage<128, D / 8>(plan_k, kp + (int64_t)pp * 128 * ks.t, sm.u.st.k[buf]);
     dma_stage<D, 16>(plan_v, vpth + pp * 128, sm.u.st.v[buf]);
+    if constexpr (EXACT) dma_stage<D, 16>(plan_v, vptlh + pp * 128, sm.u.st.vl[buf]);
   };
   // the two inverses X_A, X_B (2 x 64 x 64 fp32): chunk u -> sub-block u >> 2
   f32x4 xr[8];
@@ -278,7 +489,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
       for (int st = 0; st < NKS; ++st) ka[st] = ld8(swz<D / 8>(sm.u.st.k[buf], key0 + l32, 2 * st + g));
       float rj[16];
       lds_rows16(&sm.u.st.r[buf][key0], g, rj);
-      bf16x8 pb[2][2];
+      bf16x8 pb[2][2], pbl[2][2];
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt) {
         f32x16 sc = zero16();
@@ -288,6 +499,10 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
         for (int e = 0; e < 16; ++e) sc[e] = __builtin_amdgcn_exp2f(fmaf(sc[e] * ai[nt], rj[e], -c0));
         pb[nt][0] = pack_b(sc, 0);
         pb[nt][1] = pack_b(sc, 1);
+        if constexpr (EXACT) {
+          pbl[nt][0] = pack_lo(sc, 0, pb[nt][0]);
+          pbl[nt][1] = pack_lo(sc, 1, pb[nt][1]);
+        }
       }
 #pragma unroll
       for (int t = 0; t < NDT; ++t) {
@@ -297,6 +512,17 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
         for (int nt = 0; nt < 2; ++nt) {
           acc[t][nt] = mfma32(va0, pb[nt][0], acc[t][nt]);
           acc[t][nt] = mfma32(va1, pb[nt][1], acc[t][nt]);
+        }
+        if constexpr (EXACT) {
+          const bf16x8 vl0 = ld8(swz<16>(sm.u.st.vl[buf], t * 32 + l32, key0 / 8 + g));
+          const bf16x8 vl1 = ld8(swz<16>(sm.u.st.vl[buf], t * 32 + l32, key0 / 8 + 2 + g));
+#pragma unroll
+          for (int nt = 0; nt < 2; ++nt) {
+            acc[t][nt] = mfma32(va0, pbl[nt][0], acc[t][nt]);
+            acc[t][nt] = mfma32(va1, pbl[nt][1], acc[t][nt]);
+            acc[t][nt] = mfma32(vl0, pb[nt][0], acc[t][nt]);
+            acc[t][nt] = mfma32(vl1, pb[nt][1], acc[t][nt]);
+          }
         }
       }
     }
@@ -313,6 +539,15 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
   // prefetches do not hold registers through the loop
   for (int pp = 0; pp + 1 < npair; ++pp) {
     const int need = 2 * pp + 3;  // pair pp + 1 is complete once the counter exceeds this
+    if constexpr (SINGLE) {
+      sweep_pair(0);
+      __syncthreads();  // every wave is done with the buffer
+      if (need >= ready) ready = wait_counter_gt(cnt, need);
+      stage(pp + 1);
+      dma_wait();
+      __syncthreads();
+      continue;
+    }
     if (need >= ready) {
       const int seen = poll_counter(cnt);
       if (seen > need) {
@@ -332,7 +567,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
   }
   if (npair > 0) {
     xload();  // fetch the inverses while the last pair is processed
-    sweep_pair((npair - 1) & 1);
+    sweep_pair(SINGLE ? 0 : (npair - 1) & 1);
     __syncthreads();
   }
 
@@ -399,6 +634,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
           const bf16x8 va = ld8(&sm.u.fin.vT[dt * 32 + l32][16 * st + 8 * g]);
           o = mfma32(va, zh, o);
           o = mfma32(va, zl, o);
+          if constexpr (EXACT) o = mfma32(ld8(&sm.u.fin.vTl[dt * 32 + l32][16 * st + 8 * g]), zh, o);
         }
       }
       const int rl = rh * 32 + l32;
@@ -410,15 +646,20 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
       for (int qd = 0; qd < 4; ++qd) {
         const int d0 = dt * 32 + 8 * qd + 4 * g;
         f32x4 f;
-        bf16x4 bb;
+        bf16x4 bb, bl;
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           f[u] = o[4 * qd + u];
           bb[u] = (bf16)o[4 * qd + u];
           sm.u.fin.vT[d0 + u][lslot] = bb[u];
+          if constexpr (EXACT) {
+            bl[u] = (bf16)(o[4 * qd + u] - (float)bb[u]);
+            sm.u.fin.vTl[d0 + u][lslot] = bl[u];
+          }
         }
         *reinterpret_cast<f32x4*>(out32 + d0) = f;
         *reinterpret_cast<bf16x4*>(outb + d0) = bb;
+        if constexpr (EXACT) *reinterpret_cast<bf16x4*>(vpbl + ((int64_t)bh * T + r) * D + d0) = bl;
       }
     }
   };
@@ -432,6 +673,8 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
   for (int c = tid; c < D * 16; c += 256) {
     const int dd = c >> 4, s8 = (c & 15) * 8;
     *reinterpret_cast<bf16x8*>(vpt + ((int64_t)bh * D + dd) * T + i0 + s8) = ld8(&sm.u.fin.vT[dd][s8]);
+    if constexpr (EXACT)
+      *reinterpret_cast<bf16x8*>(vptl + ((int64_t)bh * D + dd) * T + i0 + s8) = ld8(&sm.u.fin.vTl[dd][s8]);
   }
   publish_counter(cnt, 2 * i2 + 2);
 }
@@ -446,14 +689,18 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_precond
 //   reference max only moves when a row grows by more than 2^8);
 //   O^T[d][i] += V'^T[d][j] P^T[j][i].
 // Writes O (bf16, caller layout) and lse2[bhq][i] (log2 domain, so that
-// P = exp2(s*log2e*S - lse2)).
+// P = exp2(s*log2e*S - lse2)).  For heads that run the exact chains (row mass above
+// kExactMass) it also writes O's bf16 residual olo[bhq][i][d] = bf16(O - bf16(O)): the
+// backward's delta_i = dO_i . O_i enters dQ_i = s sum_j dS_ij K_j multiplied by the
+// attention-weighted mean key, which is large when keys share a direction.
 // ---------------------------------------------------------------------------
 template <int D>
 __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_fwd_kernel(const bf16* __restrict__ q, Strides qs,
                                                              const bf16* __restrict__ k, Strides ks,
                                                              const bf16* __restrict__ vpt, bf16* __restrict__ o,
-                                                             Strides os, float* __restrict__ lse, int Hq, int Hkv,
-                                                             int T, int BHq, float scale) {
+                                                             Strides os, float* __restrict__ lse,
+                                                             const float* __restrict__ mass, bf16* __restrict__ olo,
+                                                             int Hq, int Hkv, int T, int BHq, float scale) {
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
   constexpr int CH = D / 32;  // 16-byte chunks per thread for each of the K and V'^T tiles
@@ -674,6 +921,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_fw
     if (more) lstore(buf ^ 1);
     __syncthreads();
   }
+  const bool exact = mass[bh] > kExactMass;
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
     const int irow = row0 + nt * 32 + l32;
@@ -681,14 +929,20 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_fw
     if (irow < T) {
       const float inv = 1.0f / ls;
       bf16* op = o + b * os.b + hq * os.h + (int64_t)irow * os.t;
+      bf16* ol = olo + ((int64_t)bhq * T + irow) * D;
 #pragma unroll
       for (int t = 0; t < NDT; ++t)
 #pragma unroll
         for (int qq = 0; qq < 4; ++qq) {
-          bf16x4 bb;
+          bf16x4 bb, bl;
 #pragma unroll
-          for (int u = 0; u < 4; ++u) bb[u] = (bf16)(oacc[t][nt][4 * qq + u] * inv);
+          for (int u = 0; u < 4; ++u) {
+            const float x = oacc[t][nt][4 * qq + u] * inv;
+            bb[u] = (bf16)x;
+            bl[u] = (bf16)(x - (float)bb[u]);
+          }
           *reinterpret_cast<bf16x4*>(op + t * 32 + 8 * qq + 4 * g) = bb;
+          if (exact) *reinterpret_cast<bf16x4*>(ol + t * 32 + 8 * qq + 4 * g) = bl;
         }
       if (g == 0) lse[(int64_t)bhq * T + irow] = m[nt] + log2f(ls);
     }

@@ -2,10 +2,13 @@
 
 Python mirror of the reference operator seams in ``modeling_lucid.py``:
 
-* :func:`get_v_prime`      -- ``LucidAttention.get_v_prime`` (:551-574): V' = P^-1 V
+* :func:`get_v_prime`      -- ``LucidAttention.get_v_prime`` (:551-574): V' = P^-1 V,
+  differentiable (its backward is Lucid_Tril_Solver.backward, :314-382, and k_norm's)
 * :func:`eager_lucid_attention_forward` -- ``LucidAttention.eager_lucid_attention_forward``
-  (:505-549) fused with the solve: O = softmax(s Q K^T, causal) V'
-* :func:`lucid_attention`  -- both in one differentiable call (forward + backward kernels)
+  (:505-549): O = softmax(s Q K^T, causal) V' for a given V', differentiable
+* :func:`lucid_attention`  -- both in one call on the fused kernel sequence (the path
+  LucidAttention.forward takes, :461-496)
+* :func:`causal_attention` -- the same attention kernels with V' = V (plain causal attention)
 
 Layouts follow the reference: ``query [B, Hq, T, d]``, ``key/value [B, Hkv, T, d]``
 (any strides with a contiguous last axis, e.g. the ``.view(...).transpose(1, 2)``
@@ -35,7 +38,7 @@ def _check_inputs(q, k, v):
             raise TypeError(f"lucid_amd: {name} must be bfloat16, got {t.dtype}")
         if t.dim() != 4:
             raise ValueError(f"lucid_amd: {name} must be 4-D [B, H, T, d]")
-    if k.shape != v.shape:
+    if v is not None and k.shape != v.shape:
         raise ValueError(f"lucid_amd: key {tuple(k.shape)} and value {tuple(v.shape)} must match")
     d = k.shape[-1]
     if d not in _SUPPORTED_D:
@@ -137,6 +140,37 @@ class LucidAttentionFunction(torch.autograd.Function):
         return dq[:, :, :t], dk[:, :, :t], dv[:, :, :t], None, None
 
 
+_PRECISIONS = {"auto": 0, "fast": 1, "exact": 2}
+
+
+def set_precision(mode: str = "auto") -> None:
+    """Precision of the preconditioner chains for the calls that follow (process-wide).
+
+    ``"auto"`` (default) measures each head's row mass ``max_i sum_{j<i} P_ij^2`` (sampled)
+    and runs heads above 4 -- keys along a shared direction, where the chain products
+    cancel heavily -- through kernels that carry V' and dV as bf16 hi/lo pairs and split
+    every product into three bf16 terms (~fp32 accuracy), the other heads through the bf16
+    kernels.  ``"fast"`` and ``"exact"`` force one kind for every head.
+    """
+    if mode not in _PRECISIONS:
+        raise ValueError(f"lucid_amd: precision must be one of {sorted(_PRECISIONS)}, got {mode!r}")
+    lib = _lib.load()
+    _lib.check(lib, lib.lucid_set_precision(_PRECISIONS[mode]), "lucid_set_precision")
+
+
+def get_precision() -> str:
+    code = _lib.load().lucid_get_precision()
+    return {v: k for k, v in _PRECISIONS.items()}[code]
+
+
+def head_row_mass(ws: torch.Tensor, B: int, Hq: int, Hkv: int, T: int, D: int) -> torch.Tensor:
+    """Per-head row mass recorded in a forward workspace (float [B*Hkv]); heads above 4 ran the
+    exact chain kernels.  ``T`` is the padded length the forward ran at."""
+    lib = _lib.load()
+    off = lib.lucid_fwd_workspace_mass_offset(B, Hq, Hkv, T, D)
+    return ws[off:off + 4 * B * Hkv].view(torch.float32).clone()
+
+
 def lucid_attention(query, key, value, scaling=None, eps=1e-5, return_vprime=False):
     """LUCID attention: ``softmax(s Q K^T, causal) P^-1 V``; returns O ``[B, T, Hq, d]``.
 
@@ -148,28 +182,171 @@ def lucid_attention(query, key, value, scaling=None, eps=1e-5, return_vprime=Fal
     return (o, vprime) if return_vprime else o
 
 
-def get_v_prime(key, value, scaling=None, eps=1e-5):
-    """``V' = P^-1 V`` (forward only), fp32 ``[B, Hkv, T, d]`` -- get_v_prime, modeling_lucid.py:551-574."""
+def _check_causal_mask(mask, lq, lk):
+    """The reference's only mask is the causal one (create_causal_mask, modeling_lucid.py:600-618:
+    bool, True where key j <= query i of the last ``lq`` rows); its training path ignores the mask
+    and runs is_causal=True (:520-530).  The kernels are causal by construction, so a mask is
+    accepted only if it is that one; anything else raises instead of being ignored silently."""
+    if mask is None:
+        return
+    if not torch.is_tensor(mask) or mask.dtype != torch.bool or mask.dim() < 2:
+        raise NotImplementedError("lucid_amd: attention_mask must be None or the causal bool mask")
+    m = mask[..., -lq:, :lk]
+    if m.shape[-2:] != (lq, lk):
+        raise ValueError(f"lucid_amd: attention_mask {tuple(mask.shape)} does not cover {lq} x {lk}")
+    causal = torch.ones(lq, lk, dtype=torch.bool, device=mask.device).tril_(lk - lq)
+    if not bool((m == causal).all()):
+        raise NotImplementedError("lucid_amd: only the causal attention mask is supported")
+
+
+class GetVPrimeFunction(torch.autograd.Function):
+    """``V' = P(K^)^-1 V`` with its own backward (Lucid_Tril_Solver.backward,
+    modeling_lucid.py:314-382, and the k_norm backward): C ``lucid_get_v_prime`` /
+    ``lucid_precond_bwd``.  V' is returned in the dtype of ``value`` like the reference's
+    ``solve_triangular``; the backward uses the forward's fp32 solve state."""
+
+    @staticmethod
+    def forward(ctx, key, value, scale, eps):
+        B, Hkv, T, D = key.shape
+        ctx.shape, ctx.t = key.shape, T
+        if T == 0 or key.numel() == 0:
+            ctx.empty = True
+            return value.new_empty(B, Hkv, T, D)
+        ctx.empty = False
+        lib = _lib.load()
+        tp = _padded_len(T)
+        k, v = _prep(key, tp), _prep(value, tp)
+        vprime = torch.empty(B, Hkv, tp, D, dtype=torch.float32, device=key.device)
+        ws = torch.empty(lib.lucid_fwd_workspace_bytes(B, Hkv, Hkv, tp, D), dtype=torch.uint8, device=key.device)
+        rc = lib.lucid_get_v_prime(_lib.ptr(k), _lib.strides3(k, (0, 1, 2)), _lib.ptr(v), _lib.strides3(v, (0, 1, 2)),
+                                   _lib.ptr(vprime), _lib.ptr(ws), B, Hkv, tp, D, scale, float(eps),
+                                   _lib.stream_handle(key.device))
+        _lib.check(lib, rc, "lucid_get_v_prime")
+        ctx.save_for_backward(k, ws)
+        ctx.scale = scale
+        return vprime[:, :, :T].to(value.dtype)
+
+    @staticmethod
+    def backward(ctx, dvp):
+        if ctx.empty:
+            return dvp.new_zeros(ctx.shape), dvp.new_zeros(ctx.shape), None, None
+        k, ws = ctx.saved_tensors
+        lib = _lib.load()
+        B, Hkv, tp, D = k.shape
+        t = ctx.t
+        f32 = dvp.dtype == torch.float32
+        if not f32 and dvp.dtype != torch.bfloat16:
+            dvp = dvp.to(torch.bfloat16)
+        dvp = _prep(dvp, tp)
+        dk = torch.empty(B, Hkv, tp, D, dtype=torch.bfloat16, device=k.device)
+        dv = torch.empty_like(dk)
+        bws = torch.empty(lib.lucid_precond_bwd_workspace_bytes(B, Hkv, tp, D), dtype=torch.uint8, device=k.device)
+        rc = lib.lucid_precond_bwd(_lib.ptr(k), _lib.strides3(k, (0, 1, 2)), _lib.ptr(dvp), _lib.strides3(dvp, (0, 1, 2)),
+                                   int(f32), _lib.ptr(ws), _lib.ptr(dk), _lib.strides3(dk, (0, 1, 2)), _lib.ptr(dv),
+                                   _lib.strides3(dv, (0, 1, 2)), _lib.ptr(bws), B, Hkv, tp, D, ctx.scale,
+                                   _lib.stream_handle(k.device))
+        _lib.check(lib, rc, "lucid_precond_bwd")
+        return dk[:, :, :t], dv[:, :, :t], None, None
+
+
+class AttentionOnVPrimeFunction(torch.autograd.Function):
+    """``O = softmax(s Q K^T, causal) V'`` for a given V' (eager_lucid_attention_forward,
+    modeling_lucid.py:505-549), with dV' in the backward: C ``lucid_attn_vp_fwd`` /
+    ``lucid_attn_vp_bwd``."""
+
+    @staticmethod
+    def forward(ctx, q, k, vp, scale, eps):
+        B, Hq, T, D = q.shape
+        Hkv = k.shape[1]
+        ctx.shapes, ctx.t, ctx.vdtype = (q.shape, k.shape, vp.shape), T, vp.dtype
+        if T == 0 or q.numel() == 0:
+            ctx.empty = True
+            return q.new_empty(B, T, Hq, D)
+        ctx.empty = False
+        lib = _lib.load()
+        tp = _padded_len(T)
+        qp, kp = _prep(q, tp), _prep(k, tp)
+        f32 = vp.dtype == torch.float32
+        vpp = _prep(vp if f32 else vp.to(torch.bfloat16), tp)
+        dev = q.device
+        o = torch.empty(B, tp, Hq, D, dtype=torch.bfloat16, device=dev)
+        lse = torch.empty(B, Hq, tp, dtype=torch.float32, device=dev)
+        ws = torch.empty(lib.lucid_attn_vp_fwd_workspace_bytes(B, Hq, Hkv, tp, D), dtype=torch.uint8, device=dev)
+        rc = lib.lucid_attn_vp_fwd(_lib.ptr(qp), _lib.strides3(qp, (0, 1, 2)), _lib.ptr(kp), _lib.strides3(kp, (0, 1, 2)),
+                                   _lib.ptr(vpp), _lib.strides3(vpp, (0, 1, 2)), int(f32), _lib.ptr(o),
+                                   _lib.strides3(o, (0, 2, 1)), _lib.ptr(lse), _lib.ptr(ws), B, Hq, Hkv, tp, D, scale,
+                                   float(eps), _lib.stream_handle(dev))
+        _lib.check(lib, rc, "lucid_attn_vp_fwd")
+        ctx.save_for_backward(qp, kp, o, lse, ws)
+        ctx.scale = scale
+        return o[:, :T]
+
+    @staticmethod
+    def backward(ctx, do):
+        qs, ks, vs = ctx.shapes
+        if ctx.empty:
+            return do.new_zeros(qs), do.new_zeros(ks), torch.zeros(vs, dtype=ctx.vdtype, device=do.device), None, None
+        qp, kp, o, lse, ws = ctx.saved_tensors
+        lib = _lib.load()
+        B, Hq, tp, D = qp.shape
+        Hkv, t = kp.shape[1], ctx.t
+        if do.dtype != torch.bfloat16:
+            do = do.to(torch.bfloat16)
+        if t != tp:
+            do = F.pad(do, (0, 0, 0, 0, 0, tp - t))
+        if do.stride(-1) != 1 or any(s % 8 for s in do.stride()) or do.data_ptr() % 16:
+            do = do.contiguous()
+        dev = qp.device
+        f32 = ctx.vdtype == torch.float32
+        dq = torch.empty(B, Hq, tp, D, dtype=torch.bfloat16, device=dev)
+        dk = torch.empty(B, Hkv, tp, D, dtype=torch.bfloat16, device=dev)
+        dvp = torch.empty(B, Hkv, tp, D, dtype=torch.float32 if f32 else torch.bfloat16, device=dev)
+        bws = torch.empty(lib.lucid_attn_vp_bwd_workspace_bytes(B, Hq, Hkv, tp, D), dtype=torch.uint8, device=dev)
+        rc = lib.lucid_attn_vp_bwd(_lib.ptr(do), _lib.strides3(do, (0, 2, 1)), _lib.ptr(qp), _lib.strides3(qp, (0, 1, 2)),
+                                   _lib.ptr(kp), _lib.strides3(kp, (0, 1, 2)), _lib.ptr(o), _lib.strides3(o, (0, 2, 1)),
+                                   _lib.ptr(lse), _lib.ptr(ws), _lib.ptr(dq), _lib.strides3(dq, (0, 1, 2)), _lib.ptr(dk),
+                                   _lib.strides3(dk, (0, 1, 2)), _lib.ptr(dvp), _lib.strides3(dvp, (0, 1, 2)), int(f32),
+                                   _lib.ptr(bws), B, Hq, Hkv, tp, D, ctx.scale, _lib.stream_handle(dev))
+        _lib.check(lib, rc, "lucid_attn_vp_bwd")
+        dvp = dvp[:, :, :t]
+        if dvp.dtype != ctx.vdtype:
+            dvp = dvp.to(ctx.vdtype)
+        return dq[:, :, :t], dk[:, :, :t], dvp, None, None
+
+
+def get_v_prime(key, value, scaling=None, attention_mask=None, eps=1e-5):
+    """``V' = P^-1 V`` -- ``LucidAttention.get_v_prime(key, value, scaling, attention_mask)``
+    (modeling_lucid.py:551-574), differentiable w.r.t. ``key`` and ``value``.
+
+    ``key, value [B, Hkv, T, d]``; returns V' in ``value``'s dtype.  ``eps`` is k_norm's
+    epsilon (``config.rms_norm_eps``).  ``attention_mask``: None or the causal mask."""
     _check_inputs(None, key, value)
-    B, Hkv, T, D = key.shape
-    if T == 0 or key.numel() == 0:
-        return torch.empty(B, Hkv, T, D, dtype=torch.float32, device=key.device)
-    lib = _lib.load()
-    tp = _padded_len(T)
-    k, v = _prep(key, tp), _prep(value, tp)
-    scale = D ** -0.5 if scaling is None else float(scaling)
-    vprime = torch.empty(B, Hkv, tp, D, dtype=torch.float32, device=key.device)
-    ws = torch.empty(lib.lucid_fwd_workspace_bytes(B, Hkv, Hkv, tp, D), dtype=torch.uint8, device=key.device)
-    rc = lib.lucid_get_v_prime(_lib.ptr(k), _lib.strides3(k, (0, 1, 2)), _lib.ptr(v), _lib.strides3(v, (0, 1, 2)),
-                               _lib.ptr(vprime), _lib.ptr(ws), B, Hkv, tp, D, scale, float(eps),
-                               _lib.stream_handle(key.device))
-    _lib.check(lib, rc, "lucid_get_v_prime")
-    return vprime[:, :, :T]
+    _check_causal_mask(attention_mask, key.shape[2], key.shape[2])
+    scale = key.shape[-1] ** -0.5 if scaling is None else float(scaling)
+    return GetVPrimeFunction.apply(key, value, scale, eps)
 
 
-def eager_lucid_attention_forward(query, key, value, scaling=None, eps=1e-5):
-    """Drop-in for ``get_v_prime`` followed by ``eager_lucid_attention_forward``: returns ``(O, None)``."""
-    return lucid_attention(query, key, value, scaling, eps), None
+def eager_lucid_attention_forward(query, key, v_prime, scaling=None, attention_mask=None, eps=1e-5, **kwargs):
+    """``LucidAttention.eager_lucid_attention_forward(query, key, v_prime, scaling, attention_mask)``
+    (modeling_lucid.py:505-549): causal softmax attention of ``query [B, Hq, T, d]`` and
+    ``key [B, Hkv, T, d]`` on a given ``v_prime [B, Hkv, T, d]`` (bf16 or fp32; GQA by index,
+    no repeat_kv copy).  Returns ``(O [B, T, Hq, d], None)``, differentiable w.r.t. all three.
+    ``attention_mask``: None or the causal mask.  ``eps`` (k_norm's) only serves the per-head
+    precision choice (:func:`set_precision`)."""
+    _check_inputs(query, key, None)
+    if v_prime.shape != key.shape or not v_prime.is_cuda or v_prime.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError("lucid_amd: v_prime must be a bf16 or fp32 GPU tensor shaped like key")
+    _check_causal_mask(attention_mask, query.shape[2], key.shape[2])
+    scale = query.shape[-1] ** -0.5 if scaling is None else float(scaling)
+    return AttentionOnVPrimeFunction.apply(query, key, v_prime, scale, eps), None
+
+
+def causal_attention(query, key, value, scaling=None):
+    """Plain causal softmax attention on the same HIP kernels (V' = V): ``O [B, T, Hq, d]``.
+
+    The build's own comparator for the cost of the preconditioner (no counterpart in the
+    reference, which calls SDPA)."""
+    return eager_lucid_attention_forward(query, key, value, scaling)[0]
 
 
 def lucid_decode(query, key, value, key_cache, vprime_cache, cache_len, scaling=None, eps=1e-5):

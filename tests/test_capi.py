@@ -45,13 +45,25 @@ def test_every_declared_symbol_is_exported(built, header):
 def test_abi_version_and_workspace(built):
     from lucid_amd import _lib
     lib = _lib.load()
-    assert lib.lucid_abi_version() == 1
+    assert lib.lucid_abi_version() == 2
     ws = lib.lucid_fwd_workspace_bytes(1, 16, 16, 32768, 64)
-    # rinv + K^T + V' (bf16) + V'^T + diagonal inverses + -(X_B P_BA) per 128-row block,
-    # each 256-byte aligned
-    expect = 16 * 32768 * 4 + 3 * 16 * 64 * 32768 * 2 + 16 * 512 * 4096 * 4 + 16 * 256 * 4096 * 4 + 256
+    # rinv + K^T + V' (bf16) + V'^T + diagonal inverses + -(X_B P_BA) per 128-row block
+    # + lo parts of V' and V'^T + row masses + lo part of O + counters, each 256-byte aligned
+    expect = (16 * 32768 * 4 + 3 * 16 * 64 * 32768 * 2 + 16 * 512 * 4096 * 4 + 16 * 256 * 4096 * 4
+              + 2 * 16 * 64 * 32768 * 2 + 256 + 16 * 32768 * 64 * 2 + 256)
     assert ws == expect
+    assert lib.lucid_fwd_workspace_mass_offset(1, 16, 16, 32768, 64) == expect - 512 - 16 * 32768 * 64 * 2
     assert lib.lucid_bwd_workspace_bytes(1, 16, 16, 32768, 64) > 0
+
+
+def test_precision_mode_roundtrip_and_validation(built):
+    from lucid_amd import _lib
+    lib = _lib.load()
+    assert lib.lucid_get_precision() == 0
+    for mode in (2, 1, 0):
+        assert lib.lucid_set_precision(mode) == 0 and lib.lucid_get_precision() == mode
+    assert lib.lucid_set_precision(7) == _lib.LUCID_EINVAL
+    assert b"precision" in lib.lucid_last_error() and lib.lucid_get_precision() == 0
 
 
 def test_argument_validation_without_gpu(built):

@@ -19,7 +19,7 @@ Inputs:
 import pytest
 import torch
 
-from bars import check
+from bars import bar, check
 from oracle import lucid_ref as R
 
 pytestmark = pytest.mark.gpu
@@ -41,10 +41,13 @@ def _inputs(B, Hq, Hkv, T, D, seed, kind):
 
 
 def _check(name, got, ref, report):
-    err = float((got.double() - ref).abs().max())
+    """Record the worst error per tensor over the checked heads (asserted after all heads)."""
+    err = float((got.detach().double() - ref).abs().max())
     scale = float(ref.abs().max())
-    report[name] = max(report.get(name, (0.0, 0.0))[0], err), max(report.get(name, (0.0, 0.0))[1], scale)
-    check(name, err, scale)
+    e0, s0 = report.get(name, (0.0, 0.0))
+    bad = err > bar(scale)
+    if bad or e0 / max(bar(s0), 1e-30) <= err / max(bar(scale), 1e-30):
+        report[name] = (err, scale)
 
 
 def _run(B, Hq, Hkv, T, D, seed, kind, heads=None, backward=True):
@@ -75,7 +78,9 @@ def _run(B, Hq, Hkv, T, D, seed, kind, heads=None, backward=True):
             _check("dk", kc.grad[b, h], ref["dk"], report)
             _check("dv", vc.grad[b, h], ref["dv"], report)
         del ref
-    print("max errors (err, max|ref|):", {n: (f"{e:.2e}", f"{s:.2e}") for n, (e, s) in report.items()}, flush=True)
+    print("worst errors (err, max|ref|):", {n: (f"{e:.2e}", f"{s:.2e}") for n, (e, s) in report.items()}, flush=True)
+    for name, (err, scale) in report.items():
+        check(name, err, scale)
 
 
 def test_north_star_every_head():

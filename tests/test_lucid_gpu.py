@@ -173,3 +173,60 @@ def test_empty_sequence_returns_empty_like_the_reference():
     o.sum().backward()
     assert q.grad.shape == q.shape and k.grad.shape == k.shape and v.grad.shape == v.shape
     assert get_v_prime(k.detach(), v.detach()).shape == (2, 2, 0, 64)
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,T,D,qk_std", CASES)
+def test_exact_chains_match_oracle(B, Hq, Hkv, T, D, qk_std):
+    """The exact (hi/lo split) chain kernels, forced for every head, on the same cases as the
+    bf16 ones: O, V' and every gradient against the float64 oracle; V' to 1e-4 of its scale."""
+    from lucid_amd import lucid_attention, set_precision
+    q, k, v, do = _inputs(B, Hq, Hkv, T, D, seed=11 * T + D, qk_std=qk_std)
+    print(f"case exact B={B} Hq={Hq} Hkv={Hkv} T={T} D={D} qk_std={qk_std}", flush=True)
+    qg, kg, vg = (t.cuda().requires_grad_() for t in (q, k, v))
+    set_precision("exact")
+    try:
+        o, vp = lucid_attention(qg, kg, vg, return_vprime=True)
+    finally:
+        set_precision("auto")
+    o.backward(do.cuda())
+    torch.cuda.synchronize()
+    o_ref, vp_ref = R.lucid_attention(_np(q), _np(k), _np(v), D ** -0.5, 1e-5)
+    dq, dk, dv = R.lucid_attention_grads(_np(q), _np(k), _np(v), _np(do), D ** -0.5, 1e-5)
+    vscale = float(np.abs(vp_ref).max())
+    assert _maxerr(vp, vp_ref) <= 1e-4 * vscale, f"V' err {_maxerr(vp, vp_ref):.3e}"
+    check("o", _maxerr(o, o_ref), float(np.abs(o_ref).max()))
+    for name, got, ref in (("dq", qg.grad, dq), ("dk", kg.grad, dk), ("dv", vg.grad, dv)):
+        check(name, _maxerr(got, ref), float(np.abs(ref).max()))
+
+
+def _correlated_keys(T, D, g, noise=0.1):
+    base = torch.randn(D, generator=g)
+    return base + noise * torch.randn(T, D, generator=g)
+
+
+def test_auto_precision_picks_exact_for_correlated_heads():
+    """AUTO: a head whose keys share a direction (row mass ~T) runs the exact chains, a head of
+    N(0,1)-like keys the bf16 ones; the sampled mass agrees with the exact row mass
+    max_i sum_{j<i} P_ij^2 of the float64 oracle, and both heads meet the parity bars."""
+    from lucid_amd import lucid
+    B, Hq, Hkv, T, D = 1, 2, 2, 1024, 64
+    g = torch.Generator().manual_seed(21)
+    q = torch.randn(B, Hq, T, D, generator=g).to(torch.bfloat16)
+    k = torch.stack([torch.randn(T, D, generator=g), _correlated_keys(T, D, g)])[None].to(torch.bfloat16)
+    v = (torch.randn(B, Hkv, T, D, generator=g) / 8).to(torch.bfloat16)
+    print("case auto precision", flush=True)
+    assert lucid.get_precision() == "auto"
+    o, vp, lse, ws = lucid._fwd(q.cuda(), k.cuda(), v.cuda(), D ** -0.5, 1e-5)
+    torch.cuda.synchronize()
+    mass = lucid.head_row_mass(ws, B, Hq, Hkv, T, D).cpu().numpy()
+    kh = R.k_hat(_np(k), 1e-5)
+    exact = [float((np.tril(R.precond_matrix(kh[0, h], D ** -0.5), -1) ** 2).sum(1).max()) for h in range(Hkv)]
+    print("sampled mass", mass, "exact", exact, flush=True)
+    assert exact[0] < 0.5 and mass[0] < 0.5            # N(0,1) keys: bf16 chains
+    assert exact[1] > 100 and mass[1] > 4.0            # shared direction: exact chains
+    assert abs(mass[1] - exact[1]) <= 0.25 * exact[1]  # the sample tracks the bulk mass
+    o_ref, vp_ref = R.lucid_attention(_np(q), _np(k), _np(v), D ** -0.5, 1e-5)
+    for h in range(Hkv):
+        scale = float(np.abs(vp_ref[:, h]).max())
+        assert _maxerr(vp[:, h], vp_ref[:, h]) <= 2e-3 * scale
+    check("o", _maxerr(o, o_ref), float(np.abs(o_ref).max()))
