@@ -158,6 +158,22 @@ int lucid_decode(const void* q, const int64_t* q_strides, const void* k, const i
                  const int64_t* vp_cache_strides, void* o, const int64_t* o_strides, float* vp_new, void* ws, int B,
                  int Hq, int Hkv, int T_past, int T_cap, int D, float scale, float eps, void* stream);
 
+/* lucid_decode without a workspace argument: the same decoding step, with its split
+ * partials in a static 4 MiB (4194304-byte) device array of the library instead of `ws`,
+ * so that it calls no allocator (hipMalloc, hipFree or an allocating library routine).
+ * No counterpart in the reference: for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid allocation).  Sizes whose partials
+ * exceed 4 MiB (B*Hkv above about 900 at head dim 128 with 8 query heads per kv head) are
+ * rejected with LUCID_EINVAL and a message before anything runs; use lucid_decode for them.  Each GPU
+ * holds its own array until the process ends, found on a device's first call; every
+ * call on one GPU shares it, so calls that overlap on one GPU (other streams, other
+ * threads) race. */
+int lucid_decode_noalloc(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                         const void* v, const int64_t* v_strides, void* k_cache, const int64_t* k_cache_strides,
+                         void* vp_cache, const int64_t* vp_cache_strides, void* o, const int64_t* o_strides,
+                         float* vp_new, int B, int Hq, int Hkv, int T_past, int T_cap, int D, float scale, float eps,
+                         void* stream);
+
 /* Per-kernel timing (no counterpart in the reference; used by bench.py).
  * When enabled, every launch is bracketed by two HIP events on its stream.
  * lucid_profile_collect() waits for the recorded events, folds them into

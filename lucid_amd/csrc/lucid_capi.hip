@@ -2,6 +2,7 @@
 // One translation unit: the kernel files are included so that every template
 // instantiation lives next to its launcher.
 #include <map>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -395,6 +396,77 @@ int decode_dispatch_g(int G, const void* q, const int64_t* qs, const void* k, co
   }
 }
 
+int check_decode_args(const void* q, const int64_t* qs, const void* k, const int64_t* ks, const void* v,
+                      const int64_t* vs, const void* kc, const int64_t* kcs, const void* vc, const int64_t* vcs,
+                      const void* o, const int64_t* os, const float* vp_new, int B, int Hq, int Hkv, int T_past,
+                      int T_cap, int D) {
+  if (B <= 0 || Hq <= 0 || Hkv <= 0) return fail("B, Hq and Hkv must be positive");
+  if (D != 64 && D != 128) return fail("head_dim must be 64 or 128, got " + std::to_string(D));
+  if (Hq % Hkv != 0) return fail("Hq must be a multiple of Hkv");
+  if (T_past < 0 || T_past >= T_cap) return fail("the cache is full: T_past must be in [0, T_cap)");
+  if (int rc = check_tensor("q", q, qs)) return rc;
+  if (int rc = check_tensor("k", k, ks)) return rc;
+  if (int rc = check_tensor("v", v, vs)) return rc;
+  if (int rc = check_tensor("k_cache", kc, kcs)) return rc;
+  if (int rc = check_tensor("vp_cache", vc, vcs)) return rc;
+  if (int rc = check_tensor("o", o, os)) return rc;
+  if (!vp_new) return fail("vp_new must be non-null");
+  return LUCID_OK;
+}
+
+// ---- allocation-free decoding (lucid_decode_noalloc) ----
+// The split partials live in this file-scope device array instead of a caller workspace.
+// Each GPU the library runs on holds its own copy until the process ends; host code must
+// use the address hipGetSymbolAddress returns for the current device, never the array's
+// name (a host-side stand-in).  Every call on a GPU shares that GPU's array: calls that
+// overlap on one GPU race.  The split pass writes every partial it combines, so nothing
+// has to start at zero.
+constexpr size_t kDecodeScratchBytes = size_t(4) << 20;
+static __device__ __align__(256) unsigned char scratch[kDecodeScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device, looked up once per device.
+int decode_scratch(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    g_last_error = std::string("hipGetDevice: ") + hipGetErrorString(e);
+    return LUCID_EHIP + (int)e;
+  }
+  if (dev < 0 || dev >= kMaxDevices) return fail("device index " + std::to_string(dev) + " out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      g_last_error = std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e);
+      return LUCID_EHIP + (int)e;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return LUCID_OK;
+}
+
+int decode_impl(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides, const void* v,
+                const int64_t* v_strides, void* k_cache, const int64_t* k_cache_strides, void* vp_cache,
+                const int64_t* vp_cache_strides, void* o, const int64_t* o_strides, float* vp_new, void* ws, int B,
+                int Hq, int Hkv, int T_past, int D, float scale, float eps, void* stream) {
+  const lucid::DecodePartials part =
+      carve_decode(ws, B * Hkv, Hq / Hkv, decode_splits(B * Hkv, T_past, D), D, nullptr);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (D == 64)
+    return decode_dispatch_g<64>(Hq / Hkv, q, q_strides, k, k_strides, v, v_strides, k_cache, k_cache_strides,
+                                 vp_cache, vp_cache_strides, o, o_strides, vp_new, part, B, Hkv, T_past, scale, eps,
+                                 st);
+  return decode_dispatch_g<128>(Hq / Hkv, q, q_strides, k, k_strides, v, v_strides, k_cache, k_cache_strides,
+                                vp_cache, vp_cache_strides, o, o_strides, vp_new, part, B, Hkv, T_past, scale, eps,
+                                st);
+}
+
 }  // namespace
 
 extern "C" {
@@ -411,29 +483,35 @@ int lucid_decode(const void* q, const int64_t* q_strides, const void* k, const i
                  const int64_t* vp_cache_strides, void* o, const int64_t* o_strides, float* vp_new, void* ws, int B,
                  int Hq, int Hkv, int T_past, int T_cap, int D, float scale, float eps, void* stream) {
   g_last_error.clear();
-  if (B <= 0 || Hq <= 0 || Hkv <= 0) return fail("B, Hq and Hkv must be positive");
-  if (D != 64 && D != 128) return fail("head_dim must be 64 or 128, got " + std::to_string(D));
-  if (Hq % Hkv != 0) return fail("Hq must be a multiple of Hkv");
-  if (T_past < 0 || T_past >= T_cap) return fail("the cache is full: T_past must be in [0, T_cap)");
-  if (int rc = check_tensor("q", q, q_strides)) return rc;
-  if (int rc = check_tensor("k", k, k_strides)) return rc;
-  if (int rc = check_tensor("v", v, v_strides)) return rc;
-  if (int rc = check_tensor("k_cache", k_cache, k_cache_strides)) return rc;
-  if (int rc = check_tensor("vp_cache", vp_cache, vp_cache_strides)) return rc;
-  if (int rc = check_tensor("o", o, o_strides)) return rc;
-  if (!vp_new || !ws) return fail("vp_new and ws must be non-null");
+  if (int rc = check_decode_args(q, q_strides, k, k_strides, v, v_strides, k_cache, k_cache_strides, vp_cache,
+                                 vp_cache_strides, o, o_strides, vp_new, B, Hq, Hkv, T_past, T_cap, D))
+    return rc;
+  if (!ws) return fail("ws must be non-null");
   if (int rc = check_ws("ws", ws)) return rc;
-  const lucid::DecodePartials part =
-      carve_decode(ws, B * Hkv, Hq / Hkv, decode_splits(B * Hkv, T_past, D), D, nullptr);
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  if (D == 64)
-    return decode_dispatch_g<64>(Hq / Hkv, q, q_strides, k, k_strides, v, v_strides, k_cache, k_cache_strides,
-                                 vp_cache, vp_cache_strides, o, o_strides, vp_new, part, B, Hkv, T_past, scale, eps,
-                                 st);
-  return decode_dispatch_g<128>(Hq / Hkv, q, q_strides, k, k_strides, v, v_strides, k_cache, k_cache_strides,
-                                vp_cache, vp_cache_strides, o, o_strides, vp_new, part, B, Hkv, T_past, scale, eps,
-                                st);
+  return decode_impl(q, q_strides, k, k_strides, v, v_strides, k_cache, k_cache_strides, vp_cache, vp_cache_strides,
+                     o, o_strides, vp_new, ws, B, Hq, Hkv, T_past, D, scale, eps, stream);
 }
+
+int lucid_decode_noalloc(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                         const void* v, const int64_t* v_strides, void* k_cache, const int64_t* k_cache_strides,
+                         void* vp_cache, const int64_t* vp_cache_strides, void* o, const int64_t* o_strides,
+                         float* vp_new, int B, int Hq, int Hkv, int T_past, int T_cap, int D, float scale, float eps,
+                         void* stream) {
+  g_last_error.clear();
+  if (int rc = check_decode_args(q, q_strides, k, k_strides, v, v_strides, k_cache, k_cache_strides, vp_cache,
+                                 vp_cache_strides, o, o_strides, vp_new, B, Hq, Hkv, T_past, T_cap, D))
+    return rc;
+  size_t need = 0;
+  carve_decode(nullptr, B * Hkv, Hq / Hkv, decode_splits(B * Hkv, T_past, D), D, &need);
+  if (need > kDecodeScratchBytes)
+    return fail("lucid_decode_noalloc needs " + std::to_string(need) + " bytes of scratch for these sizes, above its " +
+                std::to_string(kDecodeScratchBytes) + "-byte static scratch; call lucid_decode with a workspace");
+  void* ws = nullptr;
+  if (int rc = decode_scratch(&ws)) return rc;
+  return decode_impl(q, q_strides, k, k_strides, v, v_strides, k_cache, k_cache_strides, vp_cache, vp_cache_strides,
+                     o, o_strides, vp_new, ws, B, Hq, Hkv, T_past, D, scale, eps, stream);
+}
+
 
 int lucid_abi_version(void) { return 2; }
 

@@ -105,6 +105,19 @@ def test_argument_validation_without_gpu(built):
     assert d == B * HQ * (T // 64) * 4096 * 4 + B * HQ * T * 64 * 2 - B * HQ * T * 4
 
 
+def test_noalloc_decode_rejects_sizes_beyond_its_scratch_without_gpu(built):
+    """lucid_decode_noalloc checks the size of its partials against its 4 MiB static scratch
+    before any GPU call: 2048 kv heads of head dim 128 with 8 query heads each need more."""
+    from lucid_amd import _lib
+    lib = _lib.load()
+    dummy = ctypes.c_void_p(1 << 20)
+    s = (ctypes.c_int64 * 3)(64 * 256, 64 * 256, 128)
+    rc = lib.lucid_decode_noalloc(dummy, s, dummy, s, dummy, s, dummy, s, dummy, s, dummy, s, dummy,
+                                  1, 8 * 2048, 2048, 100, 256, 128, 0.088, 1e-5, None)
+    assert rc == _lib.LUCID_EINVAL
+    assert b"static scratch" in lib.lucid_last_error()
+
+
 def test_product_path_fails_loudly_without_gpu_tensors():
     import torch
     from lucid_amd import lucid_attention
