@@ -10,9 +10,10 @@ Reported: tokens/s (whole job), TFLOP/s by the frozen algorithmic count
 7*T^2*d*B*(Hq+Hkv) (causal halves, 1 FMA = 2 flop; exp, RMSNorm and the
 diagonal-block inverses excluded), the roofline of the dominant kernel timed
 with HIP events on its launch stream inside the timed region, plain causal
-attention (torch SDPA) at the same shape as a comparator, and a CPU baseline
-(the float32 torch restatement of the reference's dense path) on a bounded
-sample.
+attention at the same shape as a comparator (this build's own attention kernels
+with V' = V, and torch SDPA; the ratio is taken against the faster), and a CPU
+baseline (the float32 torch restatement of the reference's dense path, one head
+at the full length, on every core the process may use).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
 """
@@ -49,39 +50,68 @@ KERNEL_FLOPS = {
 }
 
 
-def cpu_baseline(T_sample=16384, T_full=32768, H_full=16, D=64):
+def _cpu_info():
+    """Host CPU facts for the record: model name (lscpu), os.cpu_count(), the cores this process
+    may run on (sched affinity) and the thread cap of the environment (OMP_NUM_THREADS)."""
+    import subprocess
+    model = None
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                model = line.split(":", 1)[1].strip()
+    except Exception:  # lscpu missing: the record says so
+        model = None
+    affinity = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    omp = os.environ.get("OMP_NUM_THREADS")
+    return {"model": model, "cpu_count": os.cpu_count(), "affinity": affinity,
+            "omp_num_threads": int(omp) if omp and omp.isdigit() else None}
+
+
+def cpu_baseline(T=32768, H_full=16, D=64):
     """Time the float32 torch restatement of the reference dense path on the host cores.
 
-    Sample: one head at T_sample, fwd+bwd; scaled to the full workload by
-    (T_full/T_sample)^2 (every term is O(T^2 d)) and by the head count.
+    One head at the full sequence length (fwd + bwd through autograd: dense P,
+    solve_triangular, SDPA), times the head count -- all 16 heads at once need 64 GiB of
+    fp32 P alone.  Threads: every core this process may run on, capped by OMP_NUM_THREADS
+    where the host sets it (the GPU box's CPU share).  One untimed warm-up at T=1024; the
+    median of three runs, or one run when it takes over 20 s.
     """
+    import statistics
+
     import torch
 
     from oracle.lucid_ref import lucid_attention_torch
 
-    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
-    cores = min(cores, 16)
-    torch.set_num_threads(cores)
+    info = _cpu_info()
+    threads = info["affinity"]
+    if info["omp_num_threads"]:
+        threads = min(threads, info["omp_num_threads"])
+    torch.set_num_threads(threads)
 
-    def run(T):
+    def run(T_):
         g = torch.Generator().manual_seed(0)
-        q, k, v = ((torch.randn(1, 1, T, D, generator=g) / D ** 0.5).requires_grad_() for _ in range(3))
-        do = torch.randn(1, T, 1, D, generator=g)
+        q, k, v = ((torch.randn(1, 1, T_, D, generator=g) / D ** 0.5).requires_grad_() for _ in range(3))
+        do = torch.randn(1, T_, 1, D, generator=g)
         t0 = time.perf_counter()
         o, _ = lucid_attention_torch(q, k, v)
         o.backward(do)
         return time.perf_counter() - t0
 
     run(1024)  # warm-up
-    t = run(T_sample)
-    t_full = t * (T_full / T_sample) ** 2 * H_full
+    times = [run(T)]
+    if times[0] < 20.0:
+        times += [run(T), run(T)]
+    t = statistics.median(times)
     return {
-        "value": T_full / t_full,
+        "value": T / (t * H_full),
         "unit": "tokens/s",
-        "cores": cores,
+        "cores": threads,
         "kind": "port",
-        "sample": (f"1 head, T={T_sample}, d={D}, fp32, torch CPU dense P + solve_triangular + SDPA "
-                   f"fwd+bwd in {t:.2f}s; scaled x(T{T_full}/T{T_sample})^2 x {H_full} heads"),
+        "sample": (f"1 head of the workload (B1 H1 T{T} d{D}), fp32, torch CPU dense P + solve_triangular + SDPA, "
+                   f"fwd+bwd: {'median of 3' if len(times) == 3 else 'one run'} {t:.2f} s "
+                   f"({', '.join(f'{x:.2f}' for x in times)}); x {H_full} heads"),
+        "host": info,
     }
 
 
@@ -445,6 +475,8 @@ def main():
     causal = None
     if not args.no_causal and wl in ("lucid", "c2", "path_softmax"):
         import torch.nn.functional as F
+
+        from lucid_amd import causal_attention
         if wl == "path_softmax":  # [B, T, H, D] inputs
             qc, kc, vc = (t.detach().transpose(1, 2).contiguous().requires_grad_() for t in (q, k, v))
             doc = do.transpose(1, 2).contiguous()
@@ -452,26 +484,42 @@ def main():
             qc, kc, vc = (t.detach().clone().requires_grad_() for t in (q, k, v))
             doc = do.transpose(1, 2)
 
-        def cstep():
+        def sdpa_step():
             qc.grad = kc.grad = vc.grad = None
-            oc = F.scaled_dot_product_attention(qc, kc, vc, is_causal=True)
-            oc.backward(doc)
+            F.scaled_dot_product_attention(qc, kc, vc, is_causal=True).backward(doc)
 
-        for _ in range(max(1, args.warmup)):
-            cstep()
-        torch.cuda.synchronize()
-        c0 = time.perf_counter()
-        for _ in range(args.steps):
-            cstep()
-        torch.cuda.synchronize()
-        cms = (time.perf_counter() - c0) / args.steps * 1e3
-        causal = {"impl": "torch.nn.functional.scaled_dot_product_attention (ROCm)", "ms_per_step": round(cms, 3),
-                  "tflops": round(causal_flops(B, Hq, T, D) / (cms / 1e3) / 1e12, 1),
-                  "lucid_over_causal": round(ms / cms, 3)}
+        def own_step():  # the build's attention kernels with V' = V (outputs [B, T, H, D])
+            qc.grad = kc.grad = vc.grad = None
+            causal_attention(qc, kc, vc).backward(do)
+
+        def timed(fn):
+            for _ in range(max(1, args.warmup)):
+                fn()
+            torch.cuda.synchronize()
+            c0 = time.perf_counter()
+            for _ in range(args.steps):
+                fn()
+            torch.cuda.synchronize()
+            return (time.perf_counter() - c0) / args.steps * 1e3
+
+        sdpa_ms = timed(sdpa_step)
+        set_precision("fast")  # plain attention has no preconditioner: skip the row-mass pass
+        try:
+            own_ms = timed(own_step)
+        finally:
+            set_precision(args.precision)
+        best = min(sdpa_ms, own_ms)
+        cf = causal_flops(B, Hq, T, D)
+        causal = {"sdpa": {"impl": "torch.nn.functional.scaled_dot_product_attention (ROCm)",
+                           "ms_per_step": round(sdpa_ms, 3), "tflops": round(cf / (sdpa_ms / 1e3) / 1e12, 1)},
+                  "own": {"impl": "lucid_amd.causal_attention (this build's attention kernels, V' = V)",
+                          "ms_per_step": round(own_ms, 3), "tflops": round(cf / (own_ms / 1e3) / 1e12, 1)},
+                  "faster": "own" if own_ms <= sdpa_ms else "sdpa",
+                  "lucid_over_causal": round(ms / best, 3)}
 
     cpu = None
     if not args.no_cpu_baseline and wl == "lucid":
-        cpu = cpu_baseline(T_full=T, H_full=B * Hq, D=D)
+        cpu = cpu_baseline(T=T, H_full=B * Hq, D=D)
 
     out = {
         "metric": metric,

@@ -25,6 +25,7 @@ extern "C" {
 
 #define LUCID_OK 0
 #define LUCID_EINVAL 1
+#define LUCID_ECHAIN 2 /* a chain wait gave up in an earlier launch (lucid_chain_status) */
 #define LUCID_EHIP 1000
 
 /* Precision of the preconditioner chains (lucid_set_precision). */
@@ -51,6 +52,19 @@ const char* lucid_last_error(void);
  * torch solve_triangular works in the input dtype (modeling_lucid.py:570). */
 int lucid_set_precision(int mode);
 int lucid_get_precision(void);
+
+/* Bounded chain waits (no counterpart in the reference, which has no cross-workgroup
+ * waits).  The chained solves hand blocks between workgroups through per-head progress
+ * counters; a wait that sees no progress for the wait limit (default 2 s, against waits of
+ * microseconds) gives up so that the kernel still finishes, and records it in a word of
+ * pinned host memory (4 bytes, allocated once on the first chain call).  Every entry point
+ * that launches a chain kernel first reports such an earlier give-up as LUCID_ECHAIN (the
+ * results of the launch that gave up are invalid).  lucid_chain_status() makes the same
+ * check on its own (synchronize the stream first to cover the launches in flight).
+ * lucid_set_chain_wait_limit(seconds) changes the limit for the calls that follow
+ * (testing aid: a tiny limit forces the give-up path with every kernel still exiting). */
+int lucid_chain_status(void);
+int lucid_set_chain_wait_limit(double seconds);
 
 /* Byte offset, inside the forward workspace, of the per-head row masses (float [B*Hkv]);
  * a head ran the exact chain kernels when its mass exceeds 4 (testing aid). */

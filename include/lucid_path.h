@@ -27,6 +27,13 @@ int lucid_path_abi_version(void);
 /* Text of the last error on the calling thread. */
 const char* lucid_path_last_error(void);
 
+/* Bounded chain waits of this library (the forward solve and the dV chain hand blocks
+ * between workgroups through progress counters): as lucid_chain_status /
+ * lucid_set_chain_wait_limit in lucid_amd.h; an earlier give-up is reported as 2 by the
+ * next lucid_path_fwd / lucid_path_bwd call.  No counterpart in the reference. */
+int lucid_path_chain_status(void);
+int lucid_path_set_chain_wait_limit(double seconds);
+
 /* Bytes of the forward workspace (kept alive for lucid_path_bwd).  Both
  * workspaces must be 256-byte aligned. */
 size_t lucid_path_fwd_workspace_bytes(int B, int T, int H, int HQ, int K);

@@ -15,6 +15,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIBS: dict[str, ctypes.CDLL] = {}
 
 LUCID_EINVAL = 1
+LUCID_ECHAIN = 2
 LUCID_EHIP = 1000
 
 _vp = ctypes.c_void_p
@@ -29,6 +30,8 @@ _SIGS = {
         "lucid_last_error": ([], ctypes.c_char_p),
         "lucid_fwd_workspace_bytes": ([_int] * 5, _sz),
         "lucid_set_precision": ([_int], _int),
+        "lucid_chain_status": ([], _int),
+        "lucid_set_chain_wait_limit": ([ctypes.c_double], _int),
         "lucid_get_precision": ([], _int),
         "lucid_fwd_workspace_mass_offset": ([_int] * 5, _sz),
         "lucid_bwd_workspace_bytes": ([_int] * 5, _sz),
@@ -62,6 +65,8 @@ _SIGS = {
     "liblucid_path.so": {
         "lucid_path_abi_version": ([], _int),
         "lucid_path_last_error": ([], ctypes.c_char_p),
+        "lucid_path_chain_status": ([], _int),
+        "lucid_path_set_chain_wait_limit": ([ctypes.c_double], _int),
         "lucid_path_fwd_workspace_bytes": ([_int] * 5, _sz),
         "lucid_path_fwd": ([_vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p,
                             _vp, _i64p, _vp, _int, _int, _int, _int, _int, _flt, _vp], _int),
@@ -121,6 +126,17 @@ def load(name: str = "liblucid_amd.so") -> ctypes.CDLL:
         f.restype = res
     _LIBS[name] = lib
     return lib
+
+
+def chain_status(synchronize: bool = True) -> None:
+    """Raise RuntimeError if a chain wait of either library gave up (no progress within the
+    wait bound) in a launch since the last check; ``synchronize`` first waits for the
+    launches in flight so that they are covered."""
+    if synchronize:
+        torch.cuda.synchronize()
+    for name, fn in (("liblucid_amd.so", "lucid_chain_status"), ("liblucid_path.so", "lucid_path_chain_status")):
+        lib = load(name)
+        check(lib, getattr(lib, fn)(), fn)
 
 
 def check(lib: ctypes.CDLL, rc: int, what: str) -> None:

@@ -10,6 +10,7 @@
 #include "lucid_bwd.hip"
 #include "lucid_decode.hip"
 #include "lucid_fwd.hip"
+#include "chain_guard.h"
 #include "profiling.h"
 
 namespace {
@@ -35,6 +36,22 @@ int hip_status(const char* where) {
 }
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+// First step of every entry point that launches a chain kernel: set up the bounded waits on
+// this device and report a wait that gave up in an earlier launch.
+int chain_check() {
+  std::string what;
+  if (int e = chain_guard::setup(&what)) {
+    g_last_error = what + ": " + hipGetErrorString((hipError_t)e);
+    return LUCID_EHIP + e;
+  }
+  if (chain_guard::take_flag()) {
+    g_last_error = "a chain wait gave up in an earlier launch (no progress within the wait bound); "
+                   "the results of that launch are invalid";
+    return LUCID_ECHAIN;
+  }
+  return LUCID_OK;
+}
 
 // Forward workspace carve-out (all offsets 256-byte aligned).
 struct FwdWs {
@@ -525,6 +542,18 @@ int lucid_set_precision(int mode) {
 
 int lucid_get_precision(void) { return g_precision; }
 
+int lucid_chain_status(void) {
+  g_last_error.clear();
+  return chain_check();
+}
+
+int lucid_set_chain_wait_limit(double seconds) {
+  g_last_error.clear();
+  if (!(seconds > 0.0)) return fail("the chain wait limit must be positive");
+  chain_guard::set_limit(seconds);
+  return LUCID_OK;
+}
+
 size_t lucid_fwd_workspace_mass_offset(int B, int Hq, int Hkv, int T, int D) {
   char* base = reinterpret_cast<char*>(size_t(256));  // any non-null 256-aligned base
   return static_cast<size_t>(reinterpret_cast<char*>(carve_fwd(base, B, Hq, Hkv, T, D).mass) - base);
@@ -549,6 +578,7 @@ int lucid_get_v_prime(const void* k, const int64_t* k_strides, const void* v, co
   if (int rc = check_tensor("v", v, v_strides)) return rc;
   if (!vprime || !fwd_ws) return fail("vprime and fwd_ws must be non-null");
   if (int rc = check_ws("fwd_ws", fwd_ws)) return rc;
+  if (int rc = chain_check()) return rc;
   const FwdWs w = carve_fwd(fwd_ws, B, Hkv, Hkv, T, D);
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (D == 64) return launch_precond_fwd<64>(k, k_strides, v, v_strides, vprime, w, B, Hkv, T, scale, eps, st);
@@ -567,6 +597,7 @@ int lucid_attn_fwd(const void* q, const int64_t* q_strides, const void* k, const
   if (int rc = check_tensor("o", o, o_strides)) return rc;
   if (!vprime || !lse || !fwd_ws) return fail("vprime, lse and fwd_ws must be non-null");
   if (int rc = check_ws("fwd_ws", fwd_ws)) return rc;
+  if (int rc = chain_check()) return rc;
   const FwdWs w = carve_fwd(fwd_ws, B, Hq, Hkv, T, D);
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (D == 64)
@@ -594,6 +625,7 @@ int lucid_attn_bwd(const void* dout, const int64_t* do_strides, const void* q, c
   if (!lse || !fwd_ws || !bwd_ws) return fail("lse, fwd_ws and bwd_ws must be non-null");
   if (int rc = check_ws("fwd_ws", fwd_ws)) return rc;
   if (int rc = check_ws("bwd_ws", bwd_ws)) return rc;
+  if (int rc = chain_check()) return rc;
   const FwdWs f = carve_fwd(const_cast<void*>(fwd_ws), B, Hq, Hkv, T, D);
   const BwdWs w = carve_bwd(bwd_ws, B, Hq, Hkv, T, D);
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -678,6 +710,7 @@ int lucid_precond_bwd(const void* k, const int64_t* k_strides, const void* dvpri
   if (!fwd_ws || !bwd_ws) return fail("fwd_ws and bwd_ws must be non-null");
   if (int rc = check_ws("fwd_ws", fwd_ws)) return rc;
   if (int rc = check_ws("bwd_ws", bwd_ws)) return rc;
+  if (int rc = chain_check()) return rc;
   const FwdWs f = carve_fwd(const_cast<void*>(fwd_ws), B, Hkv, Hkv, T, D);
   const BwdWs w = carve_seam_bwd(bwd_ws, B, Hkv, Hkv, T, D, false);
   hipStream_t st = static_cast<hipStream_t>(stream);

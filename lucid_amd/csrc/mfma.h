@@ -95,12 +95,31 @@ __device__ __forceinline__ int poll_counter(const int* cnt) {
 
 __device__ __forceinline__ void chain_acquire() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup"); }
 
-// Wait until *cnt > target; returns the value seen.
+// Bounded waits.  In-order dispatch makes every wait end (a workgroup waits only on
+// blocks of lower ids, which are running or done), so a wait that lasts longer than
+// chain_wait_ticks of the constant-rate wall clock means that the protocol broke: it
+// stores 1 to *chain_error (pinned host memory set up by the library's C ABI, which
+// reports it on the next call) and returns, so that every wave of the kernel still
+// finishes -- the results of that launch are then invalid.  Each library (translation
+// unit) has its own pair, set per device by chain_guard.h.
+static __device__ long long chain_wait_ticks = 200000000LL;  // 2 s at the 100 MHz wall clock
+static __device__ int* chain_error = nullptr;
+
+// Wait until *cnt > target (or the bound above); returns the value seen.
 __device__ __forceinline__ int wait_counter_gt(const int* cnt, int target) {
   int v = poll_counter(cnt);
-  while (v <= target) {
-    __builtin_amdgcn_s_sleep(1);
-    v = poll_counter(cnt);
+  if (v <= target) {
+    const long long t0 = wall_clock64();
+    const long long limit = chain_wait_ticks;
+    while (v <= target) {
+      __builtin_amdgcn_s_sleep(1);
+      v = poll_counter(cnt);
+      if (v <= target && wall_clock64() - t0 > limit) {
+        int* err = chain_error;
+        if (err) __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        break;
+      }
+    }
   }
   chain_acquire();
   return v;

@@ -4,6 +4,7 @@
 #include "../../include/lucid_path.h"
 #include "path_fwd.hip"
 #include "path_bwd.hip"
+#include "chain_guard.h"
 #include "profiling.h"
 
 namespace {
@@ -25,6 +26,22 @@ int phip(const char* where) {
 }
 
 size_t a256(size_t x) { return (x + 255) & ~size_t(255); }
+
+// First step of the entry points that launch a chain kernel (lucid_path_fwd, lucid_path_bwd):
+// set up the bounded waits on this device, report a wait that gave up in an earlier launch.
+int pchain_check() {
+  std::string what;
+  if (int e = chain_guard::setup(&what)) {
+    g_path_error = what + ": " + hipGetErrorString((hipError_t)e);
+    return 1000 + e;
+  }
+  if (chain_guard::take_flag()) {
+    g_path_error = "a chain wait gave up in an earlier launch (no progress within the wait bound); "
+                   "the results of that launch are invalid";
+    return 2;
+  }
+  return 0;
+}
 
 // softmax = true: the PaTH softmax layout (row log-sum-exp instead of the solve's
 // diagonal inverses and O^T chain operand)
@@ -163,6 +180,18 @@ int lucid_path_abi_version(void) { return 1; }
 
 const char* lucid_path_last_error(void) { return g_path_error.c_str(); }
 
+int lucid_path_chain_status(void) {
+  g_path_error.clear();
+  return pchain_check();
+}
+
+int lucid_path_set_chain_wait_limit(double seconds) {
+  g_path_error.clear();
+  if (!(seconds > 0.0)) return pfail("the chain wait limit must be positive");
+  chain_guard::set_limit(seconds);
+  return 0;
+}
+
 size_t lucid_path_fwd_workspace_bytes(int B, int T, int H, int HQ, int K) {
   (void)K;
   size_t n = 0;
@@ -187,6 +216,7 @@ int lucid_path_fwd(const void* q, const int64_t* q_strides, const void* k, const
     if (int rc = pcheck_vec("kcache", kcache, kcache_strides)) return rc;
   if (!fwd_ws) return pfail("fwd_ws is null");
   if (reinterpret_cast<uintptr_t>(fwd_ws) % 256) return pfail("fwd_ws must be 256-byte aligned");
+  if (int rc = pchain_check()) return rc;
   const lucid::PathFwdWs ws = carve_path_fwd(fwd_ws, B, T, H, HQ, nullptr);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int NT = T / 64;
@@ -231,6 +261,7 @@ int lucid_path_bwd(const void* dout, const int64_t* do_strides, const void* q, c
   if (!fwd_ws || !bwd_ws) return pfail("fwd_ws and bwd_ws must be non-null");
   if (reinterpret_cast<uintptr_t>(fwd_ws) % 256 || reinterpret_cast<uintptr_t>(bwd_ws) % 256)
     return pfail("fwd_ws and bwd_ws must be 256-byte aligned");
+  if (int rc = pchain_check()) return rc;
   const lucid::PathFwdWs ws = carve_path_fwd(const_cast<void*>(fwd_ws), B, T, H, HQ, nullptr);
   const lucid::PathBwdWs bw = carve_path_bwd(bwd_ws, B, T, HQ, nullptr);
   hipStream_t st = static_cast<hipStream_t>(stream);

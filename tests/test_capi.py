@@ -118,6 +118,15 @@ def test_noalloc_decode_rejects_sizes_beyond_its_scratch_without_gpu(built):
     assert b"static scratch" in lib.lucid_last_error()
 
 
+def test_chain_wait_limit_validation_without_gpu(built):
+    from lucid_amd import _lib
+    lib = _lib.load()
+    assert lib.lucid_set_chain_wait_limit(0.0) == _lib.LUCID_EINVAL
+    assert b"positive" in lib.lucid_last_error()
+    plib = _lib.load("liblucid_path.so")
+    assert plib.lucid_path_set_chain_wait_limit(-1.0) == _lib.LUCID_EINVAL
+
+
 def test_product_path_fails_loudly_without_gpu_tensors():
     import torch
     from lucid_amd import lucid_attention
