@@ -2,8 +2,8 @@
  * lucid_amd -- C ABI of the MI355X (gfx950) LUCID attention kernels.
  *
  * Plain pointers and sizes only; every buffer is caller-owned device memory
- * (the library never allocates).  Tensors are bf16 with the last (head_dim)
- * axis contiguous; the other axes are described by element strides
+ * (the library never allocates).  Tensors are bf16 (fp32 for the _f32 entry
+ * points) with the last (head_dim) axis contiguous; the other axes are described by element strides
  * {batch, head, time}.  All launches go on `stream` (a hipStream_t, NULL =
  * default stream); calls are asynchronous.  Return value: 0 on success,
  * LUCID_EINVAL for a rejected argument (text in lucid_last_error()), or
@@ -107,6 +107,49 @@ int lucid_attn_bwd(const void* dout, const int64_t* do_strides, const void* q, c
                    const float* lse, const void* fwd_ws, void* dq, const int64_t* dq_strides, void* dk,
                    const int64_t* dk_strides, void* dv, const int64_t* dv_strides, void* bwd_ws, int B, int Hq,
                    int Hkv, int T, int D, float scale, float eps, void* stream);
+
+/* ---- fp32 inputs (head dim 64) ----
+ * The reference computes in the dtype of its inputs (modeling_lucid.py:461-496, :284-382 run
+ * on whatever q/k/v hold); these are lucid_attn_fwd / lucid_attn_bwd for fp32 tensors, with
+ * fp32 outputs (o, dq, dk, dv) and the same layouts and strides.  Q, K and dO are carried as
+ * bf16 pairs (hi + lo) through split MFMA products and every head runs the exact chain
+ * instances, so the results are within ~1e-4 relative of an fp64 evaluation.  The forward
+ * workspace (lucid_fwd_f32_workspace_bytes) holds the split copies of Q and K and must stay
+ * alive until lucid_attn_bwd_f32; the backward reads o as written by the forward. */
+size_t lucid_fwd_f32_workspace_bytes(int B, int Hq, int Hkv, int T, int D);
+size_t lucid_bwd_f32_workspace_bytes(int B, int Hq, int Hkv, int T, int D);
+int lucid_attn_fwd_f32(const float* q, const int64_t* q_strides, const float* k, const int64_t* k_strides,
+                       const float* v, const int64_t* v_strides, float* o, const int64_t* o_strides, float* vprime,
+                       float* lse, void* fwd_ws, int B, int Hq, int Hkv, int T, int D, float scale, float eps,
+                       void* stream);
+int lucid_attn_bwd_f32(const float* dout, const int64_t* do_strides, const float* o, const int64_t* o_strides,
+                       const float* lse, const void* fwd_ws, float* dq, const int64_t* dq_strides, float* dk,
+                       const int64_t* dk_strides, float* dv, const int64_t* dv_strides, void* bwd_ws, int B, int Hq,
+                       int Hkv, int T, int D, float scale, void* stream);
+
+/* The two seams below (get_v_prime and eager_lucid_attention_forward) on fp32 tensors, head
+ * dim 64: the same contracts as lucid_get_v_prime / lucid_precond_bwd and lucid_attn_vp_fwd /
+ * lucid_attn_vp_bwd, with fp32 inputs (v_prime included) and fp32 outputs.  Workspaces:
+ * lucid_v_prime_f32_workspace_bytes for lucid_get_v_prime_f32 (kept until
+ * lucid_precond_bwd_f32, whose own workspace is lucid_precond_bwd_workspace_bytes), and the
+ * two _f32 sizes of the attention seam. */
+size_t lucid_v_prime_f32_workspace_bytes(int B, int Hkv, int T, int D);
+int lucid_get_v_prime_f32(const float* k, const int64_t* k_strides, const float* v, const int64_t* v_strides,
+                          float* vprime, void* fwd_ws, int B, int Hkv, int T, int D, float scale, float eps,
+                          void* stream);
+int lucid_precond_bwd_f32(const float* dvprime, const int64_t* dvprime_strides, const void* fwd_ws, float* dk,
+                          const int64_t* dk_strides, float* dv, const int64_t* dv_strides, void* bwd_ws, int B,
+                          int Hkv, int T, int D, float scale, void* stream);
+size_t lucid_attn_vp_fwd_f32_workspace_bytes(int B, int Hq, int Hkv, int T, int D);
+int lucid_attn_vp_fwd_f32(const float* q, const int64_t* q_strides, const float* k, const int64_t* k_strides,
+                          const float* vprime, const int64_t* vprime_strides, float* o, const int64_t* o_strides,
+                          float* lse, void* ws, int B, int Hq, int Hkv, int T, int D, float scale, float eps,
+                          void* stream);
+size_t lucid_attn_vp_bwd_f32_workspace_bytes(int B, int Hq, int Hkv, int T, int D);
+int lucid_attn_vp_bwd_f32(const float* dout, const int64_t* do_strides, const float* o, const int64_t* o_strides,
+                          const float* lse, const void* fwd_ws, float* dq, const int64_t* dq_strides, float* dk,
+                          const int64_t* dk_strides, float* dvprime, const int64_t* dvprime_strides, void* bwd_ws,
+                          int B, int Hq, int Hkv, int T, int D, float scale, void* stream);
 
 /* ---- The two operator seams of LucidAttention.forward, separately ----
  * get_v_prime (modeling_lucid.py:551-574) is lucid_get_v_prime above; its gradient is

@@ -41,6 +41,22 @@ _SIGS = {
         "lucid_attn_bwd": ([_vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _vp,
                             _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp,
                             _int, _int, _int, _int, _int, _flt, _flt, _vp], _int),
+        "lucid_fwd_f32_workspace_bytes": ([_int] * 5, _sz),
+        "lucid_bwd_f32_workspace_bytes": ([_int] * 5, _sz),
+        "lucid_attn_fwd_f32": ([_vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _vp, _vp,
+                                _int, _int, _int, _int, _int, _flt, _flt, _vp], _int),
+        "lucid_attn_bwd_f32": ([_vp, _i64p, _vp, _i64p, _vp, _vp, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp,
+                                _int, _int, _int, _int, _int, _flt, _vp], _int),
+        "lucid_v_prime_f32_workspace_bytes": ([_int] * 4, _sz),
+        "lucid_get_v_prime_f32": ([_vp, _i64p, _vp, _i64p, _vp, _vp, _int, _int, _int, _int, _flt, _flt, _vp], _int),
+        "lucid_precond_bwd_f32": ([_vp, _i64p, _vp, _vp, _i64p, _vp, _i64p, _vp, _int, _int, _int, _int, _flt, _vp],
+                                  _int),
+        "lucid_attn_vp_fwd_f32_workspace_bytes": ([_int] * 5, _sz),
+        "lucid_attn_vp_fwd_f32": ([_vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _vp,
+                                   _int, _int, _int, _int, _int, _flt, _flt, _vp], _int),
+        "lucid_attn_vp_bwd_f32_workspace_bytes": ([_int] * 5, _sz),
+        "lucid_attn_vp_bwd_f32": ([_vp, _i64p, _vp, _i64p, _vp, _vp, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp,
+                                   _int, _int, _int, _int, _int, _flt, _vp], _int),
         "lucid_attn_vp_fwd_workspace_bytes": ([_int] * 5, _sz),
         "lucid_attn_vp_fwd": ([_vp, _i64p, _vp, _i64p, _vp, _i64p, _int, _vp, _i64p, _vp, _vp,
                                _int, _int, _int, _int, _int, _flt, _flt, _vp], _int),

@@ -13,6 +13,8 @@
 //   lucid_attn_bwd_dq_kernel       row sweep: dQ
 //   lucid_precond_bwd_col_kernel   chained transposed solve -> dV, and the M^T K^ column sums
 //   lucid_precond_bwd_row_kernel   M K^ row sums, RMSNorm backward, dK
+#include <type_traits>
+
 #include "lucid_common.h"
 
 namespace lucid {
@@ -21,13 +23,13 @@ namespace lucid {
 // column sweep); zero the chain counters.  Heads of the exact chains (row mass above
 // kExactMass) take O as its bf16 pair O + olo (written by the attention forward).
 // grid (T/64, B*Hq)
-template <int D>
+template <int D, bool F32 = false>
 __global__ __launch_bounds__(256) void lucid_bwd_prep_kernel(const bf16* __restrict__ dout, Strides dos,
                                                              const bf16* __restrict__ o, Strides os,
                                                              const bf16* __restrict__ olo,
                                                              const float* __restrict__ mass, int Hq, int Hkv, int T,
                                                              float* __restrict__ delta, int* __restrict__ counters,
-                                                             int BH) {
+                                                             int BH, Lo lo) {
   constexpr int SEG = D / 4;
   const int blk = blockIdx.x, bhq = blockIdx.y;
   const int b = bhq / Hq, hq = bhq - b * Hq;
@@ -39,16 +41,28 @@ __global__ __launch_bounds__(256) void lucid_bwd_prep_kernel(const bf16* __restr
   const bf16* opp = o + b * os.b + hq * os.h + (int64_t)t * os.t;
   const bf16* olp = olo + ((int64_t)bhq * T + t) * D;
   float acc = 0.f;
+  if constexpr (F32) {  // fp32 dO and O themselves
+    const float* df = lo.dof + b * dos.b + hq * dos.h + (int64_t)t * dos.t + seg * SEG;
+    const float* of = lo.o + b * os.b + hq * os.h + (int64_t)t * os.t + seg * SEG;
 #pragma unroll
-  for (int c = 0; c < SEG; c += 8) {
-    const bf16x8 a = ld8(dop + seg * SEG + c);
-    const bf16x8 bo = ld8(opp + seg * SEG + c);
+    for (int c = 0; c < SEG; c += 4) {
+      const f32x4 a = *reinterpret_cast<const f32x4*>(df + c);
+      const f32x4 x = *reinterpret_cast<const f32x4*>(of + c);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc += (float)a[e] * (float)bo[e];
-    if (exact) {
-      const bf16x8 bl = ld8(olp + seg * SEG + c);
+      for (int e = 0; e < 4; ++e) acc = fmaf(a[e], x[e], acc);
+    }
+  } else {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc += (float)a[e] * (float)bl[e];
+    for (int c = 0; c < SEG; c += 8) {
+      const bf16x8 a = ld8(dop + seg * SEG + c);
+      const bf16x8 bo = ld8(opp + seg * SEG + c);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc += (float)a[e] * (float)bo[e];
+      if (exact) {
+        const bf16x8 bl = ld8(olp + seg * SEG + c);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc += (float)a[e] * (float)bl[e];
+      }
     }
   }
   acc += __shfl_xor(acc, 1, 64);
@@ -69,23 +83,31 @@ __global__ __launch_bounds__(256) void lucid_bwd_prep_kernel(const bf16* __restr
 //   dS = P (dP - delta_i);  dK^T[d][j] += Q^T[d][i] dS[i][j]
 // At d = 64 two workgroups share a CU (<= 256 registers per lane).
 // ---------------------------------------------------------------------------
-template <int D>
+template <int D, bool F32 = false>
 struct DkdvSmem {
   bf16 q[3][64 * D];   // swizzled tiles (chunk c of row r at c ^ (r & 7))
   bf16 dO[3][64 * D];
+  bf16 ql[F32 ? 3 : 1][F32 ? 64 * D : 8];   // lo tiles (fp32 inputs)
+  bf16 dOl[F32 ? 3 : 1][F32 ? 64 * D : 8];
   float lse[3][64];
   float dl[3][64];
 };
 
-template <int D>
-__global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_bwd_dkdv_kernel(
+// F32 (fp32 inputs, head dim 64): the lo tiles of Q and dO are staged beside the hi tiles,
+// K and V' carry their lo parts in registers, and every product (dV', dP, dK) takes
+// three MFMAs (S = Q.K four, lo*lo included); P and dS are split into hi and lo.
+template <int D, bool F32 = false>
+__global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid_attn_bwd_dkdv_kernel(
     const bf16* __restrict__ q, Strides qs, const bf16* __restrict__ k, Strides ks, const bf16* __restrict__ vpb,
     const bf16* __restrict__ dout, Strides dos, const float* __restrict__ lse, const float* __restrict__ delta,
-    float* __restrict__ dvp, float* __restrict__ dka, int Hq, int Hkv, int T, int BH, float scale) {
+    float* __restrict__ dvp, float* __restrict__ dka, int Hq, int Hkv, int T, int BH, float scale, Lo lo,
+    const bf16* __restrict__ vpbl) {
+  static_assert(!F32 || D == 64, "fp32 inputs: head dim 64");
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
-  constexpr int STAGE_OPS = 2 * (64 * (D / 8) / 256);  // newest vector-memory ops of a step, per wave
-  __shared__ __attribute__((aligned(16))) DkdvSmem<D> sm;
+  // newest vector-memory ops of a step, per wave
+  constexpr int STAGE_OPS = (F32 ? 4 : 2) * (64 * (D / 8) / 256);
+  __shared__ __attribute__((aligned(16))) DkdvSmem<D, F32> sm;
   const int id = blockIdx.x;
   const int jb = id / BH, bh = id - (id / BH) * BH;
   const int b = bh / Hkv, h = bh - b * Hkv;
@@ -97,11 +119,15 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_bw
   const bf16* kh = k + b * ks.b + h * ks.h;
   const float c = scale * LOG2E_F;
 
-  bf16x8 kb[NKS], vb[NKS];
+  bf16x8 kb[NKS], vb[NKS], kbl[NKS], vbl[NKS];
 #pragma unroll
   for (int st = 0; st < NKS; ++st) {
     kb[st] = ld8(kh + (int64_t)jrow * ks.t + 16 * st + 8 * g);
     vb[st] = ld8(vpb + ((int64_t)bh * T + jrow) * D + 16 * st + 8 * g);
+    if constexpr (F32) {
+      kbl[st] = ld8(lo.k + b * ks.b + h * ks.h + (int64_t)jrow * ks.t + 16 * st + 8 * g);
+      vbl[st] = ld8(vpbl + ((int64_t)bh * T + jrow) * D + 16 * st + 8 * g);
+    }
   }
   f32x16 adv[NDT], adk[NDT];
 #pragma unroll
@@ -125,6 +151,10 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_bw
     if (w == 1) dma_f32x64(delta + (int64_t)bhq * T + i0, sm.dl[buf]);
     dma_stage<64, D / 8>(plan_q, q + b * qs.b + hq * qs.h + (int64_t)i0 * qs.t, sm.q[buf]);
     dma_stage<64, D / 8>(plan_o, dout + b * dos.b + hq * dos.h + (int64_t)i0 * dos.t, sm.dO[buf]);
+    if constexpr (F32) {
+      dma_stage<64, D / 8>(plan_q, lo.q + b * qs.b + hq * qs.h + (int64_t)i0 * qs.t, sm.ql[buf]);
+      dma_stage<64, D / 8>(plan_o, lo.dout + b * dos.b + hq * dos.h + (int64_t)i0 * dos.t, sm.dOl[buf]);
+    }
   };
   stage(0);
   if (nsteps > 1) {
@@ -158,6 +188,15 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_bw
         f32x16 sc = mfma32(seed_a(-sm.lse[buf][mt * 32 + l32] * cinv, g), ones, zero16());
 #pragma unroll
         for (int st = 0; st < NKS; ++st) sc = mfma32(qa[st], kb[st], sc);
+        if constexpr (F32) {
+#pragma unroll
+          for (int st = 0; st < NKS; ++st) {
+            const bf16x8 qal = ld8(sm.ql[buf] + rdo[st] + mt * 32 * D);
+            sc = mfma32(qa[st], kbl[st], sc);
+            sc = mfma32(qal, kb[st], sc);
+            sc = mfma32(qal, kbl[st], sc);
+          }
+        }
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           float p = __builtin_amdgcn_exp2f(sc[e] * c);
@@ -169,9 +208,18 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_bw
       }
 #pragma unroll
       for (int t = 0; t < NDT; ++t) {
-        adv[t] = mfma32(lds_tr_a_at<D / 8>(sm.dO[buf] + tro[t], mt * 32), pb0, adv[t]);
-        adv[t] = mfma32(lds_tr_a_at<D / 8>(sm.dO[buf] + tro[t], mt * 32 + 16), pb1, adv[t]);
+        const bf16x8 o0 = lds_tr_a_at<D / 8>(sm.dO[buf] + tro[t], mt * 32);
+        const bf16x8 o1 = lds_tr_a_at<D / 8>(sm.dO[buf] + tro[t], mt * 32 + 16);
+        adv[t] = mfma32(o0, pb0, adv[t]);
+        adv[t] = mfma32(o1, pb1, adv[t]);
+        if constexpr (F32) {
+          adv[t] = mfma32(o0, pack_lo(pv, 0, pb0), adv[t]);
+          adv[t] = mfma32(o1, pack_lo(pv, 1, pb1), adv[t]);
+          adv[t] = mfma32(lds_tr_a_at<D / 8>(sm.dOl[buf] + tro[t], mt * 32), pb0, adv[t]);
+          adv[t] = mfma32(lds_tr_a_at<D / 8>(sm.dOl[buf] + tro[t], mt * 32 + 16), pb1, adv[t]);
+        }
       }
+      f32x16 ds;
       {
         bf16x8 da[NKS];
 #pragma unroll
@@ -180,15 +228,30 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_bw
         f32x16 dp = mfma32(seed_a(sm.dl[buf][mt * 32 + l32], g), ones, zero16());
 #pragma unroll
         for (int st = 0; st < NKS; ++st) dp = mfma32(da[st], vb[st], dp);
+        if constexpr (F32) {
 #pragma unroll
-        for (int e = 0; e < 16; ++e) dp[e] = pv[e] * dp[e];
-        pb0 = pack_b(dp, 0);
-        pb1 = pack_b(dp, 1);
+          for (int st = 0; st < NKS; ++st) {
+            dp = mfma32(da[st], vbl[st], dp);
+            dp = mfma32(ld8(sm.dOl[buf] + rdo[st] + mt * 32 * D), vb[st], dp);
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < 16; ++e) ds[e] = pv[e] * dp[e];
+        pb0 = pack_b(ds, 0);
+        pb1 = pack_b(ds, 1);
       }
 #pragma unroll
       for (int t = 0; t < NDT; ++t) {
-        adk[t] = mfma32(lds_tr_a_at<D / 8>(sm.q[buf] + tro[t], mt * 32), pb0, adk[t]);
-        adk[t] = mfma32(lds_tr_a_at<D / 8>(sm.q[buf] + tro[t], mt * 32 + 16), pb1, adk[t]);
+        const bf16x8 q0 = lds_tr_a_at<D / 8>(sm.q[buf] + tro[t], mt * 32);
+        const bf16x8 q1 = lds_tr_a_at<D / 8>(sm.q[buf] + tro[t], mt * 32 + 16);
+        adk[t] = mfma32(q0, pb0, adk[t]);
+        adk[t] = mfma32(q1, pb1, adk[t]);
+        if constexpr (F32) {
+          adk[t] = mfma32(q0, pack_lo(ds, 0, pb0), adk[t]);
+          adk[t] = mfma32(q1, pack_lo(ds, 1, pb1), adk[t]);
+          adk[t] = mfma32(lds_tr_a_at<D / 8>(sm.ql[buf] + tro[t], mt * 32), pb0, adk[t]);
+          adk[t] = mfma32(lds_tr_a_at<D / 8>(sm.ql[buf] + tro[t], mt * 32 + 16), pb1, adk[t]);
+        }
       }
     }
   };
@@ -238,16 +301,25 @@ struct DqSmem {
   bf16 k[3][64 * D];  // swizzled tiles (chunk c of row r at c ^ (r & 7))
   bf16 v[3][64 * D];
 };
+template <int D>
+struct DqSmemF32 {  // fp32 inputs: the lo tiles of K and V' beside the hi tiles
+  bf16 k[3][64 * D];
+  bf16 v[3][64 * D];
+  bf16 kl[3][64 * D];
+  bf16 vl[3][64 * D];
+};
 
-template <int D, bool EXACT>
+template <int D, bool EXACT, bool F32 = false>
 __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void lucid_attn_bwd_dq_kernel(
     const bf16* __restrict__ q, Strides qs, const bf16* __restrict__ k, Strides ks, const bf16* __restrict__ vpb,
     const bf16* __restrict__ dout, Strides dos, const float* __restrict__ lse,
-    const float* __restrict__ delta, const float* __restrict__ mass, bf16* __restrict__ dq, Strides dqs, int Hq,
-    int Hkv, int T, int BHq, float scale) {
+    const float* __restrict__ delta, const float* __restrict__ mass,
+    std::conditional_t<F32, float, bf16>* __restrict__ dq, Strides dqs, int Hq, int Hkv, int T, int BHq,
+    float scale, Lo lo, const bf16* __restrict__ vpbl) {
+  static_assert(!F32 || (EXACT && D == 64), "fp32 inputs: exact instance, head dim 64");
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
-  __shared__ __attribute__((aligned(16))) DqSmem<D> sm;
+  __shared__ __attribute__((aligned(16))) std::conditional_t<F32, DqSmemF32<D>, DqSmem<D>> sm;
   const int nblk = (T + 255) / 256;
   const int id = blockIdx.x;
   const int bhq = id % BHq;
@@ -264,7 +336,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
   const bf16* vh = vpb + (int64_t)bh * T * D;
   const float c = scale * LOG2E_F;
 
-  bf16x8 qb[2][NKS], db[2][NKS];
+  bf16x8 qb[2][NKS], db[2][NKS], qbl[2][NKS], dbl[2][NKS];
   float li[2], di[2];
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
@@ -273,6 +345,10 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
     for (int st = 0; st < NKS; ++st) {
       qb[nt][st] = ld8(q + b * qs.b + hq * qs.h + (int64_t)ir * qs.t + 16 * st + 8 * g);
       db[nt][st] = ld8(dout + b * dos.b + hq * dos.h + (int64_t)ir * dos.t + 16 * st + 8 * g);
+      if constexpr (F32) {
+        qbl[nt][st] = ld8(lo.q + b * qs.b + hq * qs.h + (int64_t)ir * qs.t + 16 * st + 8 * g);
+        dbl[nt][st] = ld8(lo.dout + b * dos.b + hq * dos.h + (int64_t)ir * dos.t + 16 * st + 8 * g);
+      }
     }
     li[nt] = lse[(int64_t)bhq * T + ir];
     di[nt] = delta[(int64_t)bhq * T + ir];
@@ -285,7 +361,8 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
   }
   const int ntile = (min(r0 + 256, T) + 63) / 64;
   const int last_w = row0 / 64;
-  constexpr int STAGE_OPS = 2 * (64 * (D / 8) / 256);  // newest vector-memory ops of a step, per wave
+  // newest vector-memory ops of a step, per wave
+  constexpr int STAGE_OPS = (F32 ? 4 : 2) * (64 * (D / 8) / 256);
   int plan_k[64 * (D / 8) / 256], plan_v[64 * (D / 8) / 256];
   dma_plan<64, D / 8>(ks.t, plan_k);
   dma_plan<64, D / 8>(D, plan_v);
@@ -293,6 +370,10 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
     const int j0 = jt * 64, buf = jt % 3;
     dma_stage<64, D / 8>(plan_k, kh + (int64_t)j0 * ks.t, sm.k[buf]);
     dma_stage<64, D / 8>(plan_v, vh + (int64_t)j0 * D, sm.v[buf]);
+    if constexpr (F32) {
+      dma_stage<64, D / 8>(plan_k, lo.k + b * ks.b + h * ks.h + (int64_t)j0 * ks.t, sm.kl[buf]);
+      dma_stage<64, D / 8>(plan_v, vpbl + (int64_t)bh * T * D + (int64_t)j0 * D, sm.vl[buf]);
+    }
   };
   stage(0);
   if (ntile > 1) {
@@ -327,6 +408,18 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
           sc = mfma32(ka[st], qb[nt][st], sc);
           dp = mfma32(va[st], db[nt][st], dp);
         }
+        if constexpr (F32) {
+#pragma unroll
+          for (int st = 0; st < NKS; ++st) {
+            const bf16x8 kl8 = ld8(sm.kl[buf] + rdo[st] + mt * 32 * D);
+            const bf16x8 vl8 = ld8(sm.vl[buf] + rdo[st] + mt * 32 * D);
+            sc = mfma32(ka[st], qbl[nt][st], sc);
+            sc = mfma32(kl8, qb[nt][st], sc);
+            sc = mfma32(kl8, qbl[nt][st], sc);
+            dp = mfma32(va[st], dbl[nt][st], dp);
+            dp = mfma32(vl8, db[nt][st], dp);
+          }
+        }
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           float p = __builtin_amdgcn_exp2f(fmaf(sc[e], c, -li[nt]));
@@ -352,6 +445,10 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
             acc[t][nt] = mfma32(a0, dsl[nt][0], acc[t][nt]);
             acc[t][nt] = mfma32(a1, dsl[nt][1], acc[t][nt]);
           }
+          if constexpr (F32) {
+            acc[t][nt] = mfma32(lds_tr_a<D / 8>(sm.kl[buf], mt * 32, t * 32), dsb[nt][0], acc[t][nt]);
+            acc[t][nt] = mfma32(lds_tr_a<D / 8>(sm.kl[buf], mt * 32 + 16, t * 32), dsb[nt][1], acc[t][nt]);
+          }
         }
       }
     }
@@ -371,7 +468,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
   for (int nt = 0; nt < 2; ++nt) {
     const int irow = row0 + nt * 32 + l32;
     if (irow >= T) continue;
-    bf16* op = dq + b * dqs.b + hq * dqs.h + (int64_t)irow * dqs.t;
+    auto* op = dq + b * dqs.b + hq * dqs.h + (int64_t)irow * dqs.t;
 #pragma unroll
     for (int t = 0; t < NDT; ++t)
 #pragma unroll
@@ -379,7 +476,14 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
         bf16x4 bb;
 #pragma unroll
         for (int u = 0; u < 4; ++u) bb[u] = (bf16)(acc[t][nt][4 * qq + u] * scale);
-        *reinterpret_cast<bf16x4*>(op + t * 32 + 8 * qq + 4 * g) = bb;
+        if constexpr (F32) {
+          f32x4 x;
+#pragma unroll
+          for (int u = 0; u < 4; ++u) x[u] = acc[t][nt][4 * qq + u] * scale;
+          *reinterpret_cast<f32x4*>(op + t * 32 + 8 * qq + 4 * g) = x;
+        } else {
+          *reinterpret_cast<bf16x4*>(op + t * 32 + 8 * qq + 4 * g) = bb;
+        }
       }
   }
 }
@@ -410,11 +514,14 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
 // it, V'_J's residual (vpbl) is held beside V'_J, and every product that sums over rows
 // is split into hi*hi + hi*lo + lo*hi: P^T dV, G = dV V'^T, M^T K (K is exact in bf16,
 // so two terms) and the in-block P_BA^T dV_B.  One workgroup per CU.
+// F32 (fp32 inputs, exact, head dim 64): K also comes as hi + lo (the lo row tiles staged
+// beside the others, K_J's lo part in registers, K^T's lo copy ktl), so every product with
+// K takes three terms as well (four for the K.K of P); dV is written in fp32.
 // ---------------------------------------------------------------------------
-template <int D, bool EXACT>
+template <int D, bool EXACT, bool F32 = false>
 struct PcolSmem;
 template <int D>
-struct PcolSmem<D, false> {
+struct PcolSmem<D, false, false> {
   union {
     struct {
       bf16 k[3][64 * D];   // swizzled tiles (chunk c of row r at c ^ (r & 7))
@@ -428,13 +535,14 @@ struct PcolSmem<D, false> {
     } fin;
   } u;
 };
-template <int D>
-struct PcolSmem<D, true> {
+template <int D, bool F32>
+struct PcolSmem<D, true, F32> {
   union {
     struct {
       bf16 k[3][64 * D];
       bf16 dv[3][64 * D];
       bf16 dvl[3][64 * D];  // lo part of dV
+      bf16 kl[F32 ? 3 : 1][F32 ? 64 * D : 8];  // lo part of K (fp32 inputs)
       float r[3][64];
     } st;
     struct {
@@ -446,16 +554,17 @@ struct PcolSmem<D, true> {
   } u;
 };
 
-template <int D, bool EXACT>
+template <int D, bool EXACT, bool F32 = false>
 __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void lucid_precond_bwd_col_kernel(
     const bf16* __restrict__ k, Strides ks, int Hkv, int T, int BH, const float* __restrict__ rinv, float scale,
     const bf16* __restrict__ kt, const bf16* __restrict__ vpb, const bf16* __restrict__ vpbl,
     const float* __restrict__ pinv, const float* __restrict__ mass, const float* __restrict__ dvp,
-    bf16* __restrict__ dvb, bf16* __restrict__ dvbl, bf16* __restrict__ dv_out, Strides dvs,
-    float* __restrict__ colsum, int* __restrict__ counters) {
+    bf16* __restrict__ dvb, bf16* __restrict__ dvbl, std::conditional_t<F32, float, bf16>* __restrict__ dv_out,
+    Strides dvs, float* __restrict__ colsum, int* __restrict__ counters, Lo lo) {
+  static_assert(!F32 || (EXACT && D == 64), "fp32 inputs: exact instance, head dim 64");
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
-  __shared__ __attribute__((aligned(16))) PcolSmem<D, EXACT> sm;
+  __shared__ __attribute__((aligned(16))) PcolSmem<D, EXACT, F32> sm;
 
   const int NT = T / 64, NP = T / 128;
   const int id = blockIdx.x;
@@ -476,13 +585,16 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
   const float sl2 = scale * LOG2E_F;
   const float c0 = LOG2E_F / scale;
 
-  bf16x8 kbJ[NKS], vbJ[NKS], vbJl[NKS];
+  const bf16* klh = F32 ? lo.k + b * ks.b + h * ks.h : nullptr;
+  const bf16* ktlh = F32 ? lo.kt + (int64_t)bh * D * T : nullptr;
+  bf16x8 kbJ[NKS], vbJ[NKS], vbJl[NKS], kbJl[NKS];
   const int jc = J0 + cw + l32;
 #pragma unroll
   for (int st = 0; st < NKS; ++st) {
     kbJ[st] = ld8(kh + (int64_t)jc * ks.t + 16 * st + 8 * g);
     vbJ[st] = ld8(vph + (int64_t)jc * D + 16 * st + 8 * g);
     if constexpr (EXACT) vbJl[st] = ld8(vpbl + ((int64_t)bh * T + jc) * D + 16 * st + 8 * g);
+    if constexpr (F32) kbJl[st] = ld8(klh + (int64_t)jc * ks.t + 16 * st + 8 * g);
   }
   const float aJ = sl2 * rv[jc];
   f32x16 adv[NDT], acs[NDT];
@@ -505,7 +617,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
   int ready = 0;
   // step k of the sweep stages tile first - k into buffer k % 3; the newest
   // STAGE_OPS vector memory operations of a wave are the tiles of a step
-  constexpr int STAGE_OPS = (EXACT ? 3 : 2) * (64 * (D / 8) / 256);
+  constexpr int STAGE_OPS = (F32 ? 4 : EXACT ? 3 : 2) * (64 * (D / 8) / 256);
   const int nsteps = first - last + 1;
   int plan_k[64 * (D / 8) / 256], plan_d[64 * (D / 8) / 256];
   dma_plan<64, D / 8>(ks.t, plan_k);
@@ -516,6 +628,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
     dma_stage<64, D / 8>(plan_k, kh + (int64_t)i0 * ks.t, sm.u.st.k[buf]);
     dma_stage<64, D / 8>(plan_d, dvbh + (int64_t)i0 * D, sm.u.st.dv[buf]);
     if constexpr (EXACT) dma_stage<64, D / 8>(plan_d, dvblh + (int64_t)i0 * D, sm.u.st.dvl[buf]);
+    if constexpr (F32) dma_stage<64, D / 8>(plan_k, klh + (int64_t)i0 * ks.t, sm.u.st.kl[buf]);
   };
   // issue the steps up to `upto` whose tiles are already published (tile I is
   // published once the counter exceeds NT-1-I); never blocks
@@ -593,6 +706,15 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
           gg = mfma32(ld8(swz<D / 8>(sm.u.st.dvl[buf], rh * 32 + l32, 2 * st + g)), vbJ[st], gg);
         }
       }
+      if constexpr (F32) {
+#pragma unroll
+        for (int st = 0; st < NKS; ++st) {
+          const bf16x8 kal = ld8(swz<D / 8>(sm.u.st.kl[buf], rh * 32 + l32, 2 * st + g));
+          sc = mfma32(ka[st], kbJl[st], sc);
+          sc = mfma32(kal, kbJ[st], sc);
+          sc = mfma32(kal, kbJl[st], sc);
+        }
+      }
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const float pe = __builtin_amdgcn_exp2f(fmaf(sc[e] * aJ, rI[e], -c0));
@@ -625,6 +747,10 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
           adv[t] = mfma32(lds_tr_a<D / 8>(sm.u.st.dvl[buf], rh * 32 + 16, t * 32), pb1, adv[t]);
           acs[t] = mfma32(k0, ml0, acs[t]);
           acs[t] = mfma32(k1, ml1, acs[t]);
+        }
+        if constexpr (F32) {
+          acs[t] = mfma32(lds_tr_a<D / 8>(sm.u.st.kl[buf], rh * 32, t * 32), mb0, acs[t]);
+          acs[t] = mfma32(lds_tr_a<D / 8>(sm.u.st.kl[buf], rh * 32 + 16, t * 32), mb1, acs[t]);
         }
       }
     }
@@ -676,7 +802,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
       const int r = J0 + sb * 64 + cl;
       const int lslot = sb * 64 + ((cl & ~15) | jmap(cl & 15));
       bf16* ob = dvb + ((int64_t)bh * T + r) * D;
-      bf16* ou = dv_out + b * dvs.b + h * dvs.h + (int64_t)r * dvs.t;
+      auto* ou = dv_out + b * dvs.b + h * dvs.h + (int64_t)r * dvs.t;
 #pragma unroll
       for (int qq = 0; qq < 4; ++qq) {
         const int d0 = dt * 32 + 8 * qq + 4 * g;
@@ -691,7 +817,14 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
           }
         }
         *reinterpret_cast<bf16x4*>(ob + d0) = bb;
-        *reinterpret_cast<bf16x4*>(ou + d0) = bb;
+        if constexpr (F32) {
+          f32x4 x;
+#pragma unroll
+          for (int u = 0; u < 4; ++u) x[u] = o[4 * qq + u];
+          *reinterpret_cast<f32x4*>(ou + d0) = x;
+        } else {
+          *reinterpret_cast<bf16x4*>(ou + d0) = bb;
+        }
         if constexpr (EXACT) *reinterpret_cast<bf16x4*>(dvbl + ((int64_t)bh * T + r) * D + d0) = bl;
       }
     }
@@ -705,9 +838,15 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
     const int colA = J0 + na * 32 + l32;
     f32x16 sc = zero16();
 #pragma unroll
-    for (int st = 0; st < NKS; ++st)
-      sc = mfma32(ld8(kh + (int64_t)(J0 + 64 + kb * 32 + l32) * ks.t + 16 * st + 8 * g),
-                  ld8(kh + (int64_t)colA * ks.t + 16 * st + 8 * g), sc);
+    for (int st = 0; st < NKS; ++st) {
+      const int64_t om = (int64_t)(J0 + 64 + kb * 32 + l32) * ks.t + 16 * st + 8 * g;
+      const int64_t on = (int64_t)colA * ks.t + 16 * st + 8 * g;
+      sc = mfma32(ld8(kh + om), ld8(kh + on), sc);
+      if constexpr (F32) {
+        sc = mfma32(ld8(kh + om), ld8(klh + on), sc);
+        sc = mfma32(ld8(klh + om), ld8(kh + on), sc);
+      }
+    }
     const float aA = sl2 * rv[colA];
     float rB[16];
     load_rows16(rv + J0 + 64 + kb * 32, g, rB);
@@ -778,10 +917,21 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
           gg = mfma32(ld8(dvblh + (int64_t)(rbase + l32) * D + 16 * st + 8 * g), vbJ[st], gg);
         }
       }
+      if constexpr (F32) {
+#pragma unroll
+        for (int st = 0; st < NKS; ++st) {
+          const bf16x8 kal = ld8(klh + (int64_t)(rbase + l32) * ks.t + 16 * st + 8 * g);
+          sc = mfma32(ka[st], kbJl[st], sc);
+          sc = mfma32(kal, kbJ[st], sc);
+          sc = mfma32(kal, kbJl[st], sc);
+        }
+      }
+      // strictly below the diagonal: the diagonal terms M_jj K^_j lie along K^_j and are
+      // added by the row kernel in closed form (they cancel in the RMSNorm backward)
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int rloc = rb * 64 + rh * 32 + drow(e, g), cloc = cw + l32;
-        const float pe = (rloc >= cloc) ? __builtin_amdgcn_exp2f(fmaf(sc[e] * aJ, rr[e], -c0)) : 0.f;
+        const float pe = (rloc > cloc) ? __builtin_amdgcn_exp2f(fmaf(sc[e] * aJ, rr[e], -c0)) : 0.f;
         gg[e] = gg[e] * pe * rr[e];
       }
       const bf16x8 mb0 = pack_b(gg, 0), mb1 = pack_b(gg, 1);
@@ -793,6 +943,11 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
         if constexpr (EXACT) {
           acs[t] = mfma32(ld8(kp), pack_lo(gg, 0, mb0), acs[t]);
           acs[t] = mfma32(ld8(kp + 16), pack_lo(gg, 1, mb1), acs[t]);
+        }
+        if constexpr (F32) {
+          const bf16* kpl = ktlh + (int64_t)(t * 32 + l32) * T + rbase + 8 * g;
+          acs[t] = mfma32(ld8(kpl), mb0, acs[t]);
+          acs[t] = mfma32(ld8(kpl + 16), mb1, acs[t]);
         }
       }
     }
@@ -826,29 +981,31 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
 // other heads): G = V' dV^T and M K are split into hi*hi + hi*lo + lo*hi with the lo
 // parts of V' (staged beside V') and dV (held beside dV); one workgroup per CU.
 // ---------------------------------------------------------------------------
-template <int D, bool EXACT>
+template <int D, bool EXACT, bool F32 = false>
 struct ProwSmem {
   bf16 k[3][64 * D];  // swizzled tiles (chunk c of row r at c ^ (r & 7))
   bf16 v[3][64 * D];
   float r[3][64];
 };
-template <int D>
-struct ProwSmem<D, true> {
+template <int D, bool F32>
+struct ProwSmem<D, true, F32> {
   bf16 k[3][64 * D];
   bf16 v[3][64 * D];
   bf16 vl[3][64 * D];  // lo part of V'
+  bf16 kl[F32 ? 3 : 1][F32 ? 64 * D : 8];  // lo part of K (fp32 inputs)
   float r[3][64];
 };
 
-template <int D, bool EXACT>
+template <int D, bool EXACT, bool F32 = false>
 __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void lucid_precond_bwd_row_kernel(
     const bf16* __restrict__ k, Strides ks, int Hkv, int T, int BH, const float* __restrict__ rinv, float scale,
     const bf16* __restrict__ vpb, const bf16* __restrict__ vpbl, const bf16* __restrict__ dvb,
     const bf16* __restrict__ dvbl, const float* __restrict__ mass, const float* __restrict__ colsum,
-    const float* __restrict__ dka, bf16* __restrict__ dk_out, Strides dks) {
+    const float* __restrict__ dka, std::conditional_t<F32, float, bf16>* __restrict__ dk_out, Strides dks, Lo lo) {
+  static_assert(!F32 || (EXACT && D == 64), "fp32 inputs: exact instance, head dim 64");
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
-  __shared__ __attribute__((aligned(16))) ProwSmem<D, EXACT> sm;
+  __shared__ __attribute__((aligned(16))) ProwSmem<D, EXACT, F32> sm;
   const int nblk = (T + 255) / 256;
   const int id = blockIdx.x;
   const int ib = nblk - 1 - id / BH, bh = id - (id / BH) * BH;  // heavy (late) blocks first
@@ -864,7 +1021,8 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
   const float sl2 = scale * LOG2E_F;
   const float c0 = LOG2E_F / scale;
 
-  bf16x8 kbI[2][NKS], dbI[2][NKS], dbIl[2][NKS];
+  const bf16* klh = F32 ? lo.k + b * ks.b + h * ks.h : nullptr;
+  bf16x8 kbI[2][NKS], dbI[2][NKS], dbIl[2][NKS], kbIl[2][NKS];
   float aI[2];
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
@@ -872,6 +1030,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
 #pragma unroll
     for (int st = 0; st < NKS; ++st) {
       kbI[nt][st] = ld8(kh + (int64_t)ir * ks.t + 16 * st + 8 * g);
+      if constexpr (F32) kbIl[nt][st] = ld8(klh + (int64_t)ir * ks.t + 16 * st + 8 * g);
       dbI[nt][st] = ld8(dvb + ((int64_t)bh * T + ir) * D + 16 * st + 8 * g);
       if constexpr (EXACT) dbIl[nt][st] = ld8(dvbl + ((int64_t)bh * T + ir) * D + 16 * st + 8 * g);
     }
@@ -885,7 +1044,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
   }
   const int ntile = min(4 * ib + 4, T / 64);  // key tiles 0 .. ntile-1 (>= 2 since T >= 128)
   // newest vector-memory ops of a step, per wave
-  constexpr int STAGE_OPS = (EXACT ? 3 : 2) * (64 * (D / 8) / 256);
+  constexpr int STAGE_OPS = (F32 ? 4 : EXACT ? 3 : 2) * (64 * (D / 8) / 256);
   int plan_k[64 * (D / 8) / 256], plan_v[64 * (D / 8) / 256];
   dma_plan<64, D / 8>(ks.t, plan_k);
   dma_plan<64, D / 8>(D, plan_v);
@@ -895,6 +1054,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
     dma_stage<64, D / 8>(plan_k, kh + (int64_t)j0 * ks.t, sm.k[buf]);
     dma_stage<64, D / 8>(plan_v, vh + (int64_t)j0 * D, sm.v[buf]);
     if constexpr (EXACT) dma_stage<64, D / 8>(plan_v, vpbl + (int64_t)bh * T * D + (int64_t)j0 * D, sm.vl[buf]);
+    if constexpr (F32) dma_stage<64, D / 8>(plan_k, klh + (int64_t)j0 * ks.t, sm.kl[buf]);
   };
   stage(0);
   stage(1);
@@ -929,10 +1089,20 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
             gg = mfma32(ld8(swz<D / 8>(sm.vl[buf], jh * 32 + l32, 2 * st + g)), dbI[nt][st], gg);
           }
         }
+        if constexpr (F32) {
+#pragma unroll
+          for (int st = 0; st < NKS; ++st) {
+            const bf16x8 kal = ld8(swz<D / 8>(sm.kl[buf], jh * 32 + l32, 2 * st + g));
+            sc = mfma32(ka[st], kbIl[nt][st], sc);
+            sc = mfma32(kal, kbI[nt][st], sc);
+            sc = mfma32(kal, kbIl[nt][st], sc);
+          }
+        }
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           float pe = __builtin_amdgcn_exp2f(fmaf(sc[e] * aI[nt], rJ[e], -c0));
-          if (diag && (jh * 32 + drow(e, g) > nt * 32 + l32)) pe = 0.f;
+          // j >= i masked: the diagonal term is added in closed form after the sweep
+          if (diag && jh * 32 + drow(e, g) >= nt * 32 + l32) pe = 0.f;
           gg[e] = gg[e] * pe * rJ[e];
         }
         mb[nt][0] = pack_b(gg, 0);
@@ -953,6 +1123,10 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
           if constexpr (EXACT) {
             acc[t][nt] = mfma32(k0, ml[nt][0], acc[t][nt]);
             acc[t][nt] = mfma32(k1, ml[nt][1], acc[t][nt]);
+          }
+          if constexpr (F32) {
+            acc[t][nt] = mfma32(lds_tr_a<D / 8>(sm.kl[buf], jh * 32, t * 32), mb[nt][0], acc[t][nt]);
+            acc[t][nt] = mfma32(lds_tr_a<D / 8>(sm.kl[buf], jh * 32 + 16, t * 32), mb[nt][1], acc[t][nt]);
           }
         }
       }
@@ -977,8 +1151,10 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
     const float* cs = colsum + ((int64_t)bh * T + irow) * D;
     const float* da = dka + ((int64_t)bh * T + irow) * D;
     const bf16* kr = kh + (int64_t)irow * ks.t;
+    const bf16* dvr = dvb + ((int64_t)bh * T + irow) * D;
+    const bf16* vpr = vh + (int64_t)irow * D;
     float dkh[NDT][16], khat[NDT][16];
-    float dotp = 0.f;
+    float dotp = 0.f, kss = 0.f, gdot = 0.f;
 #pragma unroll
     for (int t = 0; t < NDT; ++t)
 #pragma unroll
@@ -986,19 +1162,39 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
         const int d0 = t * 32 + 8 * qq + 4 * g;
         const f32x4 cv = *reinterpret_cast<const f32x4*>(cs + d0);
         const bf16x4 kv = *reinterpret_cast<const bf16x4*>(kr + d0);
+        bf16x4 kvl;
+        if constexpr (F32) kvl = *reinterpret_cast<const bf16x4*>(klh + (int64_t)irow * ks.t + d0);
+        const bf16x4 dv4 = *reinterpret_cast<const bf16x4*>(dvr + d0);
+        const bf16x4 vp4 = *reinterpret_cast<const bf16x4*>(vpr + d0);
+        bf16x4 dv4l, vp4l;
+        if constexpr (EXACT) {
+          dv4l = *reinterpret_cast<const bf16x4*>(dvbl + ((int64_t)bh * T + irow) * D + d0);
+          vp4l = *reinterpret_cast<const bf16x4*>(vpbl + ((int64_t)bh * T + irow) * D + d0);
+        }
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           const int e = 4 * qq + u;
           const float x = -scale * (acc[t][nt][e] + cv[u]);
-          const float kk = ri * (float)kv[u];
+          const float kk = ri * ((float)kv[u] + (F32 ? (float)kvl[u] : 0.f));
           dkh[t][e] = x;
           khat[t][e] = kk;
           dotp += x * kk;
+          kss += kk * kk;
+          const float dvv = (float)dv4[u] + (EXACT ? (float)dv4l[u] : 0.f);
+          const float vpv = (float)vp4[u] + (EXACT ? (float)vp4l[u] : 0.f);
+          gdot = fmaf(dvv, vpv, gdot);
         }
       }
     dotp = wave_sum32(dotp);
+    kss = wave_sum32(kss);
+    gdot = wave_sum32(gdot);
     const float f = dotp / (float)D;
-    bf16* op = dk_out + b * dks.b + h * dks.h + (int64_t)irow * dks.t;
+    // The diagonal terms of M K^ + M^T K^ (excluded from both sums), -2 s M_ii K^_i with
+    // M_ii = (dV_i . V'_i) P_ii, P_ii = exp(s |K^_i|^2 - 1/s), lie along K^_i, which the
+    // RMSNorm backward keeps only to the fraction 1 - |K^_i|^2 / D (= eps r_i^2): added here
+    // as fd * K^_i rather than as two large terms that cancel down to that fraction.
+    const float fd = -2.f * scale * gdot * __builtin_amdgcn_exp2f(fmaf(sl2, kss, -c0)) * (1.f - kss / (float)D);
+    auto* op = dk_out + b * dks.b + h * dks.h + (int64_t)irow * dks.t;
 #pragma unroll
     for (int t = 0; t < NDT; ++t)
 #pragma unroll
@@ -1006,13 +1202,20 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
         const int d0 = t * 32 + 8 * qq + 4 * g;
         f32x4 av = {0.f, 0.f, 0.f, 0.f};  // no attention part (preconditioner-only backward)
         if (dka) av = *reinterpret_cast<const f32x4*>(da + d0);
-        bf16x4 bb;
+        f32x4 x;
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           const int e = 4 * qq + u;
-          bb[u] = (bf16)(ri * (dkh[t][e] - khat[t][e] * f) + av[u]);
+          x[u] = ri * (dkh[t][e] - khat[t][e] * f + khat[t][e] * fd) + av[u];
         }
-        *reinterpret_cast<bf16x4*>(op + d0) = bb;
+        if constexpr (F32) {
+          *reinterpret_cast<f32x4*>(op + d0) = x;
+        } else {
+          bf16x4 bb;
+#pragma unroll
+          for (int u = 0; u < 4; ++u) bb[u] = (bf16)x[u];
+          *reinterpret_cast<bf16x4*>(op + d0) = bb;
+        }
       }
   }
 }

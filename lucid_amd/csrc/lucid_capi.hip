@@ -66,10 +66,16 @@ struct FwdWs {
   float* mass;   // [BH]        largest row mass sum_{j<i} P_ij^2 (sampled; selects the chain precision)
   bf16* olo;     // [BHq][T][D] lo part of O (exact heads)
   int* counters; // [BH]
+  // fp32 inputs only: the bf16 pairs of Q and K ([BH][T][D] rows), K^T's lo part, the
+  // mean key of each head (fp32 [BH][D]) and the pair of K - mean (the attention's keys)
+  bf16 *qh, *ql, *kh, *kl, *ktl;
+  float* kmean;
+  bf16 *kch, *kcl;
   size_t bytes;
 };
 
-FwdWs carve_fwd(void* base, int B, int Hq, int Hkv, int T, int D) {
+// f32: the fp32-input copies as well (with_q: also those of Q and the attention's keys)
+FwdWs carve_fwd(void* base, int B, int Hq, int Hkv, int T, int D, bool f32 = false, bool with_q = true) {
   const size_t BH = (size_t)B * Hkv, BHq = (size_t)B * Hq;
   FwdWs w{};
   size_t off = 0;
@@ -90,6 +96,20 @@ FwdWs carve_fwd(void* base, int B, int Hq, int Hkv, int T, int D) {
   w.mass = reinterpret_cast<float*>(take(BH * 4));
   w.olo = reinterpret_cast<bf16*>(take(BHq * T * D * 2));
   w.counters = reinterpret_cast<int*>(take(BH * 4));
+  if (f32) {
+    if (with_q) {
+      w.qh = reinterpret_cast<bf16*>(take(BHq * T * D * 2));
+      w.ql = reinterpret_cast<bf16*>(take(BHq * T * D * 2));
+    }
+    w.kh = reinterpret_cast<bf16*>(take(BH * T * D * 2));
+    w.kl = reinterpret_cast<bf16*>(take(BH * T * D * 2));
+    w.ktl = reinterpret_cast<bf16*>(take(BH * D * T * 2));
+    if (with_q) {
+      w.kmean = reinterpret_cast<float*>(take(BH * D * 4));
+      w.kch = reinterpret_cast<bf16*>(take(BH * T * D * 2));
+      w.kcl = reinterpret_cast<bf16*>(take(BH * T * D * 2));
+    }
+  }
   w.bytes = off;
   return w;
 }
@@ -102,10 +122,11 @@ struct BwdWs {
   bf16* dvbl;    // [BH][T][D]   lo part of dV (exact heads)
   float* colsum; // [BH][T][D]   sum_I M_IJ^T K^_I
   int* counters; // [BH]
+  bf16 *doh, *dol; // fp32 inputs only: the bf16 pair of dO ([BHq][T][D] rows)
   size_t bytes;
 };
 
-BwdWs carve_bwd(void* base, int B, int Hq, int Hkv, int T, int D) {
+BwdWs carve_bwd(void* base, int B, int Hq, int Hkv, int T, int D, bool f32 = false) {
   const size_t BH = (size_t)B * Hkv, BHq = (size_t)B * Hq;
   BwdWs w{};
   size_t off = 0;
@@ -122,6 +143,10 @@ BwdWs carve_bwd(void* base, int B, int Hq, int Hkv, int T, int D) {
   w.dvbl = reinterpret_cast<bf16*>(take(BH * T * D * 2));
   w.colsum = reinterpret_cast<float*>(take(BH * T * D * 4));
   w.counters = reinterpret_cast<int*>(take(BH * 4));
+  if (f32) {
+    w.doh = reinterpret_cast<bf16*>(take(BHq * T * D * 2));
+    w.dol = reinterpret_cast<bf16*>(take(BHq * T * D * 2));
+  }
   w.bytes = off;
   return w;
 }
@@ -161,22 +186,22 @@ int launch_precond_fwd(const void* k, const int64_t* ks, const void* v, const in
   // a forced precision is written straight into the head masses (no mass pass)
   const float mass_init = g_precision == LUCID_PRECISION_EXACT ? 1e30f : 0.f;
   LUCID_LAUNCH("lucid_prep_kernel", lucid::lucid_prep_kernel<D>, dim3(T / 64, BH), st, (const bf16*)k, S(ks), Hkv,
-               T, eps, scale, w.rinv, w.kt, w.pinv, w.counters, w.mass, mass_init);
+               T, eps, scale, w.rinv, w.kt, w.pinv, w.counters, w.mass, mass_init, lucid::Lo{}, nullptr);
   if (g_precision == LUCID_PRECISION_AUTO)
     LUCID_LAUNCH("lucid_mass_kernel", lucid::lucid_mass_kernel<D>, dim3(T / 64, BH), st, (const bf16*)k, S(ks),
                  Hkv, T, w.rinv, scale, w.mass);
   LUCID_LAUNCH("lucid_zx_kernel", lucid::lucid_zx_kernel<D>, dim3(T / 128, BH), st, (const bf16*)k, S(ks), Hkv, T,
-               w.rinv, scale, w.pinv, w.zx);
+               w.rinv, scale, w.pinv, w.zx, lucid::Lo{});
   // both instances of the chain: each solves the heads of its precision and returns at
   // once for the others
   if (g_precision != LUCID_PRECISION_EXACT)
     LUCID_LAUNCH("lucid_precond_fwd_kernel", (lucid::lucid_precond_fwd_kernel<D, false>), dim3((T / 128) * BH),
                  st, (const bf16*)k, S(ks), (const bf16*)v, S(vs), Hkv, T, BH, w.rinv, scale, vprime, w.vpb,
-                 w.vpt, w.vpbl, w.vptl, w.pinv, w.zx, w.mass, w.counters);
+                 w.vpt, w.vpbl, w.vptl, w.pinv, w.zx, w.mass, w.counters, lucid::Lo{});
   if (g_precision != LUCID_PRECISION_FAST)
     LUCID_LAUNCH("lucid_precond_fwd_exact_kernel", (lucid::lucid_precond_fwd_kernel<D, true>),
                  dim3((T / 128) * BH), st, (const bf16*)k, S(ks), (const bf16*)v, S(vs), Hkv, T, BH, w.rinv,
-                 scale, vprime, w.vpb, w.vpt, w.vpbl, w.vptl, w.pinv, w.zx, w.mass, w.counters);
+                 scale, vprime, w.vpb, w.vpt, w.vpbl, w.vptl, w.pinv, w.zx, w.mass, w.counters, lucid::Lo{});
   return LUCID_OK;
 }
 
@@ -187,7 +212,8 @@ int launch_fwd(const void* q, const int64_t* qs, const void* k, const int64_t* k
   if (int rc = launch_precond_fwd<D>(k, ks, v, vs, vprime, w, B, Hkv, T, scale, eps, st)) return rc;
   const int BHq = B * Hq;
   LUCID_LAUNCH("lucid_attn_fwd_kernel", lucid::lucid_attn_fwd_kernel<D>, dim3(((T + 255) / 256) * BHq), st, (const bf16*)q,
-               S(qs), (const bf16*)k, S(ks), w.vpt, (bf16*)o, S(os), lse, w.mass, w.olo, Hq, Hkv, T, BHq, scale);
+               S(qs), (const bf16*)k, S(ks), w.vpt, (bf16*)o, S(os), lse, w.mass, w.olo, Hq, Hkv, T, BHq, scale,
+               lucid::Lo{}, nullptr);
   return LUCID_OK;
 }
 
@@ -199,16 +225,18 @@ int launch_attn_bwd(const void* dout, const int64_t* dos, const void* q, const i
                     const int64_t* dqs, const BwdWs& w, int B, int Hq, int Hkv, int T, float scale, hipStream_t st) {
   const int BH = B * Hkv, BHq = B * Hq;
   LUCID_LAUNCH("lucid_bwd_prep_kernel", lucid::lucid_bwd_prep_kernel<D>, dim3(T / 64, BHq), st, (const bf16*)dout,
-               S(dos), (const bf16*)o, S(os), f.olo, f.mass, Hq, Hkv, T, w.delta, w.counters, BH);
+               S(dos), (const bf16*)o, S(os), f.olo, f.mass, Hq, Hkv, T, w.delta, w.counters, BH, lucid::Lo{});
   LUCID_LAUNCH("lucid_attn_bwd_dkdv_kernel", lucid::lucid_attn_bwd_dkdv_kernel<D>, dim3((T / 128) * BH), st,
                (const bf16*)q, S(qs), (const bf16*)k, S(ks), f.vpb, (const bf16*)dout, S(dos), lse,
-               w.delta, w.dvp, w.dka, Hq, Hkv, T, BH, scale);
+               w.delta, w.dvp, w.dka, Hq, Hkv, T, BH, scale, lucid::Lo{}, nullptr);
   LUCID_LAUNCH("lucid_attn_bwd_dq_kernel", (lucid::lucid_attn_bwd_dq_kernel<D, false>),
                dim3(((T + 255) / 256) * BHq), st, (const bf16*)q, S(qs), (const bf16*)k, S(ks), f.vpb,
-               (const bf16*)dout, S(dos), lse, w.delta, f.mass, (bf16*)dq, S(dqs), Hq, Hkv, T, BHq, scale);
+               (const bf16*)dout, S(dos), lse, w.delta, f.mass, (bf16*)dq, S(dqs), Hq, Hkv, T, BHq, scale,
+               lucid::Lo{}, nullptr);
   LUCID_LAUNCH("lucid_attn_bwd_dq_exact_kernel", (lucid::lucid_attn_bwd_dq_kernel<D, true>),
                dim3(((T + 255) / 256) * BHq), st, (const bf16*)q, S(qs), (const bf16*)k, S(ks), f.vpb,
-               (const bf16*)dout, S(dos), lse, w.delta, f.mass, (bf16*)dq, S(dqs), Hq, Hkv, T, BHq, scale);
+               (const bf16*)dout, S(dos), lse, w.delta, f.mass, (bf16*)dq, S(dqs), Hq, Hkv, T, BHq, scale,
+               lucid::Lo{}, nullptr);
   return LUCID_OK;
 }
 
@@ -223,16 +251,16 @@ int launch_precond_bwd(const void* k, const int64_t* ks, const FwdWs& f, void* d
   // row mass; the precision forced at the forward call is recorded there
   LUCID_LAUNCH("lucid_precond_bwd_col_kernel", (lucid::lucid_precond_bwd_col_kernel<D, false>),
                dim3((T / 128) * BH), st, (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, scale, f.kt, f.vpb, f.vpbl,
-               f.pinv, f.mass, w.dvp, w.dvb, w.dvbl, (bf16*)dv, S(dvs), w.colsum, w.counters);
+               f.pinv, f.mass, w.dvp, w.dvb, w.dvbl, (bf16*)dv, S(dvs), w.colsum, w.counters, lucid::Lo{});
   LUCID_LAUNCH("lucid_precond_bwd_col_exact_kernel", (lucid::lucid_precond_bwd_col_kernel<D, true>),
                dim3((T / 128) * BH), st, (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, scale, f.kt, f.vpb, f.vpbl,
-               f.pinv, f.mass, w.dvp, w.dvb, w.dvbl, (bf16*)dv, S(dvs), w.colsum, w.counters);
+               f.pinv, f.mass, w.dvp, w.dvb, w.dvbl, (bf16*)dv, S(dvs), w.colsum, w.counters, lucid::Lo{});
   LUCID_LAUNCH("lucid_precond_bwd_row_kernel", (lucid::lucid_precond_bwd_row_kernel<D, false>),
                dim3(((T + 255) / 256) * BH), st, (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, scale, f.vpb, f.vpbl,
-               w.dvb, w.dvbl, f.mass, w.colsum, dka, (bf16*)dk, S(dks));
+               w.dvb, w.dvbl, f.mass, w.colsum, dka, (bf16*)dk, S(dks), lucid::Lo{});
   LUCID_LAUNCH("lucid_precond_bwd_row_exact_kernel", (lucid::lucid_precond_bwd_row_kernel<D, true>),
                dim3(((T + 255) / 256) * BH), st, (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, scale, f.vpb, f.vpbl,
-               w.dvb, w.dvbl, f.mass, w.colsum, dka, (bf16*)dk, S(dks));
+               w.dvb, w.dvbl, f.mass, w.colsum, dka, (bf16*)dk, S(dks), lucid::Lo{});
   return LUCID_OK;
 }
 
@@ -250,7 +278,8 @@ int launch_bwd(const void* dout, const int64_t* dos, const void* q, const int64_
 
 // Workspace of the attention on a caller's V': the operand copies of V', 1/rms of K,
 // the row masses and O's lo part (the FwdWs fields the attention kernels read).
-FwdWs carve_attn_vp(void* base, int B, int Hq, int Hkv, int T, int D) {
+// (f32: the bf16 pairs of Q, K - mean and V' as well.)
+FwdWs carve_attn_vp(void* base, int B, int Hq, int Hkv, int T, int D, bool f32 = false) {
   const size_t BH = (size_t)B * Hkv, BHq = (size_t)B * Hq;
   FwdWs w{};
   size_t off = 0;
@@ -265,13 +294,23 @@ FwdWs carve_attn_vp(void* base, int B, int Hq, int Hkv, int T, int D) {
   w.vpt = reinterpret_cast<bf16*>(take(BH * D * T * 2));
   w.mass = reinterpret_cast<float*>(take(BH * 4));
   w.olo = reinterpret_cast<bf16*>(take(BHq * T * D * 2));
+  if (f32) {
+    w.qh = reinterpret_cast<bf16*>(take(BHq * T * D * 2));
+    w.ql = reinterpret_cast<bf16*>(take(BHq * T * D * 2));
+    w.kmean = reinterpret_cast<float*>(take(BH * D * 4));
+    w.kch = reinterpret_cast<bf16*>(take(BH * T * D * 2));
+    w.kcl = reinterpret_cast<bf16*>(take(BH * T * D * 2));
+    w.vpbl = reinterpret_cast<bf16*>(take(BH * T * D * 2));
+    w.vptl = reinterpret_cast<bf16*>(take(BH * D * T * 2));
+  }
   w.bytes = off;
   return w;
 }
 
 // Backward scratch of one seam: the attention part needs delta, dV' and the softmax dK, the
 // preconditioner part dV' (as fp32), dV and its lo part, the column sums and counters.
-BwdWs carve_seam_bwd(void* base, int B, int Hq, int Hkv, int T, int D, bool attn) {
+// (f32 with attn: the bf16 pair of dO as well.)
+BwdWs carve_seam_bwd(void* base, int B, int Hq, int Hkv, int T, int D, bool attn, bool f32 = false) {
   const size_t BH = (size_t)B * Hkv, BHq = (size_t)B * Hq;
   BwdWs w{};
   size_t off = 0;
@@ -285,6 +324,10 @@ BwdWs carve_seam_bwd(void* base, int B, int Hq, int Hkv, int T, int D, bool attn
   if (attn) {
     w.delta = reinterpret_cast<float*>(take(BHq * T * 4));
     w.dka = reinterpret_cast<float*>(take(BH * T * D * 4));
+    if (f32) {
+      w.doh = reinterpret_cast<bf16*>(take(BHq * T * D * 2));
+      w.dol = reinterpret_cast<bf16*>(take(BHq * T * D * 2));
+    }
   } else {
     w.dvb = reinterpret_cast<bf16*>(take(BH * T * D * 2));
     w.dvbl = reinterpret_cast<bf16*>(take(BH * T * D * 2));
@@ -304,17 +347,17 @@ int launch_attn_vp_fwd(const void* q, const int64_t* qs, const void* k, const in
   if (vp_f32)
     LUCID_LAUNCH("lucid_vp_layout_kernel", (lucid::lucid_vp_layout_kernel<D, float>), dim3(T / 64, BH), st,
                  (const bf16*)k, S(ks), (const float*)vp, S(vs), Hkv, T, eps, w.rinv, w.vpb, w.vpt, w.mass,
-                 mass_init);
+                 mass_init, nullptr, nullptr);
   else
     LUCID_LAUNCH("lucid_vp_layout_kernel", (lucid::lucid_vp_layout_kernel<D, bf16>), dim3(T / 64, BH), st,
                  (const bf16*)k, S(ks), (const bf16*)vp, S(vs), Hkv, T, eps, w.rinv, w.vpb, w.vpt, w.mass,
-                 mass_init);
+                 mass_init, nullptr, nullptr);
   if (g_precision == LUCID_PRECISION_AUTO)
     LUCID_LAUNCH("lucid_mass_kernel", lucid::lucid_mass_kernel<D>, dim3(T / 64, BH), st, (const bf16*)k, S(ks),
                  Hkv, T, w.rinv, scale, w.mass);
   LUCID_LAUNCH("lucid_attn_fwd_kernel", lucid::lucid_attn_fwd_kernel<D>, dim3(((T + 255) / 256) * BHq), st,
                (const bf16*)q, S(qs), (const bf16*)k, S(ks), w.vpt, (bf16*)o, S(os), lse, w.mass, w.olo, Hq, Hkv, T,
-               BHq, scale);
+               BHq, scale, lucid::Lo{}, nullptr);
   return LUCID_OK;
 }
 
@@ -349,6 +392,174 @@ int launch_precond_only_bwd(const void* k, const int64_t* ks, const void* dvp, c
     LUCID_LAUNCH("lucid_rows_in_kernel", (lucid::lucid_rows_in_kernel<D, bf16>), dim3(T / 64, BH), st,
                  (const bf16*)dvp, S(dvps), w.dvp, Hkv, T, w.counters);
   return launch_precond_bwd<D>(k, ks, f, dk, dks, dv, dvs, w, nullptr, B, Hkv, T, scale, st);
+}
+
+// ---- fp32 inputs (head dim 64) ----
+// Q, K, dO (and a caller's V') are split into bf16 pairs (lucid_split_kernel) and every
+// product of the path is taken on the pairs (lucid_common.h, struct Lo); V, O and dO enter
+// as fp32 where they are summed directly (the chain's right-hand side, delta).  All heads
+// run the exact chain instances (their row mass is forced above kExactMass); outputs are
+// fp32.  The launchers mirror the bf16 ones above piece by piece.
+
+constexpr int kF32D = 64;
+constexpr float kForceExact = 1e30f;
+
+// Element strides of the contiguous [B][H][T][D] rows of a split copy.
+lucid::Strides rows_strides(int H, int T, int D) {
+  return lucid::Strides{(int64_t)H * T * D, (int64_t)T * D, (int64_t)D};
+}
+
+int launch_split(const void* x, const int64_t* xs, int B, int H, int T, bf16* hi, bf16* lo, hipStream_t st,
+                 const float* center = nullptr) {
+  LUCID_LAUNCH("lucid_split_kernel", lucid::lucid_split_kernel<kF32D>, dim3(T / 64, B * H), st, (const float*)x,
+               S(xs), H, T, hi, lo, center);
+  return LUCID_OK;
+}
+
+// The attention's keys: K - (mean key of the head) as a bf16 pair in w.kch / w.kcl.
+int launch_centered_keys(const void* k, const int64_t* ks, const FwdWs& w, int B, int Hkv, int T, hipStream_t st) {
+  LUCID_LAUNCH("lucid_key_mean_kernel", lucid::lucid_key_mean_kernel<kF32D>, dim3(B * Hkv), st, (const float*)k,
+               S(ks), Hkv, T, w.kmean);
+  return launch_split(k, ks, B, Hkv, T, w.kch, w.kcl, st, w.kmean);
+}
+
+// V' = P^-1 V from fp32 K and V (K split into w.kh / w.kl).
+int launch_precond_fwd_f32(const void* k, const int64_t* ks, const void* v, const int64_t* vs, float* vprime,
+                           const FwdWs& w, int B, int Hkv, int T, float scale, float eps, hipStream_t st) {
+  constexpr int D = kF32D;
+  const int BH = B * Hkv;
+  const lucid::Strides ck = rows_strides(Hkv, T, D);
+  if (int rc = launch_split(k, ks, B, Hkv, T, w.kh, w.kl, st)) return rc;
+  lucid::Lo lo{};
+  lo.k = w.kl;
+  lo.kt = w.ktl;
+  lo.v = static_cast<const float*>(v);
+  LUCID_LAUNCH("lucid_prep_f32_kernel", (lucid::lucid_prep_kernel<D, true>), dim3(T / 64, BH), st, w.kh, ck, Hkv,
+               T, eps, scale, w.rinv, w.kt, w.pinv, w.counters, w.mass, kForceExact, lo, w.ktl);
+  LUCID_LAUNCH("lucid_zx_f32_kernel", (lucid::lucid_zx_kernel<D, true>), dim3(T / 128, BH), st, w.kh, ck, Hkv, T,
+               w.rinv, scale, w.pinv, w.zx, lo);
+  // the chain reads V as fp32 through lo.v with V's own strides (its bf16 operand is unused)
+  LUCID_LAUNCH("lucid_precond_fwd_f32_kernel", (lucid::lucid_precond_fwd_kernel<D, true, true>),
+               dim3((T / 128) * BH), st, w.kh, ck, (const bf16*)v, S(vs), Hkv, T, BH, w.rinv, scale, vprime, w.vpb,
+               w.vpt, w.vpbl, w.vptl, w.pinv, w.zx, w.mass, w.counters, lo);
+  return LUCID_OK;
+}
+
+// O = softmax(s Q K^T, causal) V' on the split Q (split here), the centred keys and V' in
+// w.  lse is the row normaliser of the scores against the centred keys.
+int launch_attn_fwd_f32(const void* q, const int64_t* qs, void* o, const int64_t* os, float* lse, const FwdWs& w,
+                        int B, int Hq, int Hkv, int T, float scale, hipStream_t st) {
+  constexpr int D = kF32D;
+  const int BHq = B * Hq;
+  if (int rc = launch_split(q, qs, B, Hq, T, w.qh, w.ql, st)) return rc;
+  lucid::Lo lo{};
+  lo.q = w.ql;
+  lo.k = w.kcl;
+  LUCID_LAUNCH("lucid_attn_fwd_f32_kernel", (lucid::lucid_attn_fwd_kernel<D, true>), dim3(((T + 255) / 256) * BHq),
+               st, w.qh, rows_strides(Hq, T, D), w.kch, rows_strides(Hkv, T, D), w.vpt, (float*)o, S(os), lse,
+               w.mass, w.olo, Hq, Hkv, T, BHq, scale, lo, w.vptl);
+  return LUCID_OK;
+}
+
+int launch_fwd_f32(const void* q, const int64_t* qs, const void* k, const int64_t* ks, const void* v,
+                   const int64_t* vs, void* o, const int64_t* os, float* vprime, float* lse, const FwdWs& w, int B,
+                   int Hq, int Hkv, int T, float scale, float eps, hipStream_t st) {
+  if (int rc = launch_precond_fwd_f32(k, ks, v, vs, vprime, w, B, Hkv, T, scale, eps, st)) return rc;
+  if (int rc = launch_centered_keys(k, ks, w, B, Hkv, T, st)) return rc;
+  return launch_attn_fwd_f32(q, qs, o, os, lse, w, B, Hq, Hkv, T, scale, st);
+}
+
+// The attention part of the backward: delta (from fp32 dO and O), dV' and the softmax dK
+// (into w.dvp, w.dka) and dQ (fp32).  Reads the split Q, centred K and V' of the forward.
+int launch_attn_bwd_f32(const void* dout, const int64_t* dos, const void* o, const int64_t* os, const float* lse,
+                        const FwdWs& f, void* dq, const int64_t* dqs, const BwdWs& w, int B, int Hq, int Hkv, int T,
+                        float scale, hipStream_t st) {
+  constexpr int D = kF32D;
+  const int BH = B * Hkv, BHq = B * Hq;
+  const lucid::Strides cq = rows_strides(Hq, T, D), ck = rows_strides(Hkv, T, D);
+  if (int rc = launch_split(dout, dos, B, Hq, T, w.doh, w.dol, st)) return rc;
+  lucid::Lo lo{};
+  lo.q = f.ql;
+  lo.k = f.kcl;
+  lo.dout = w.dol;
+  lo.o = static_cast<const float*>(o);
+  lo.dof = static_cast<const float*>(dout);
+  // delta reads fp32 dO and O with their own strides (the bf16 operands are unused)
+  LUCID_LAUNCH("lucid_bwd_prep_f32_kernel", (lucid::lucid_bwd_prep_kernel<D, true>), dim3(T / 64, BHq), st,
+               (const bf16*)dout, S(dos), (const bf16*)o, S(os), f.olo, f.mass, Hq, Hkv, T, w.delta, w.counters, BH,
+               lo);
+  LUCID_LAUNCH("lucid_attn_bwd_dkdv_f32_kernel", (lucid::lucid_attn_bwd_dkdv_kernel<D, true>), dim3((T / 128) * BH),
+               st, f.qh, cq, f.kch, ck, f.vpb, w.doh, cq, lse, w.delta, w.dvp, w.dka, Hq, Hkv, T, BH, scale, lo,
+               f.vpbl);
+  LUCID_LAUNCH("lucid_attn_bwd_dq_f32_kernel", (lucid::lucid_attn_bwd_dq_kernel<D, true, true>),
+               dim3(((T + 255) / 256) * BHq), st, f.qh, cq, f.kch, ck, f.vpb, w.doh, cq, lse, w.delta, f.mass,
+               (float*)dq, S(dqs), Hq, Hkv, T, BHq, scale, lo, f.vpbl);
+  return LUCID_OK;
+}
+
+// The preconditioner part: dV = P^-T dV' (w.dvp, counters zeroed), then dK (fp32) with the
+// softmax part dka added (null: none).
+int launch_precond_bwd_f32(const FwdWs& f, void* dk, const int64_t* dks, void* dv, const int64_t* dvs,
+                           const BwdWs& w, const float* dka, int B, int Hkv, int T, float scale, hipStream_t st) {
+  constexpr int D = kF32D;
+  const int BH = B * Hkv;
+  const lucid::Strides ck = rows_strides(Hkv, T, D);
+  lucid::Lo lo{};
+  lo.k = f.kl;
+  lo.kt = f.ktl;
+  LUCID_LAUNCH("lucid_precond_bwd_col_f32_kernel", (lucid::lucid_precond_bwd_col_kernel<D, true, true>),
+               dim3((T / 128) * BH), st, f.kh, ck, Hkv, T, BH, f.rinv, scale, f.kt, f.vpb, f.vpbl, f.pinv, f.mass,
+               w.dvp, w.dvb, w.dvbl, (float*)dv, S(dvs), w.colsum, w.counters, lo);
+  LUCID_LAUNCH("lucid_precond_bwd_row_f32_kernel", (lucid::lucid_precond_bwd_row_kernel<D, true, true>),
+               dim3(((T + 255) / 256) * BH), st, f.kh, ck, Hkv, T, BH, f.rinv, scale, f.vpb, f.vpbl, w.dvb, w.dvbl,
+               f.mass, w.colsum, dka, (float*)dk, S(dks), lo);
+  return LUCID_OK;
+}
+
+int launch_bwd_f32(const void* dout, const int64_t* dos, const void* o, const int64_t* os, const float* lse,
+                   const FwdWs& f, void* dq, const int64_t* dqs, void* dk, const int64_t* dks, void* dv,
+                   const int64_t* dvs, const BwdWs& w, int B, int Hq, int Hkv, int T, float scale, hipStream_t st) {
+  if (int rc = launch_attn_bwd_f32(dout, dos, o, os, lse, f, dq, dqs, w, B, Hq, Hkv, T, scale, st)) return rc;
+  return launch_precond_bwd_f32(f, dk, dks, dv, dvs, w, w.dka, B, Hkv, T, scale, st);
+}
+
+// eager_lucid_attention_forward on fp32 Q, K and V': the centred keys, the V' pair and
+// layouts, then the attention (the layout pass's 1/rms, read only by the row-mass pass,
+// which the forced precision skips, comes from the centred keys).
+int launch_attn_vp_fwd_f32(const void* q, const int64_t* qs, const void* k, const int64_t* ks, const void* vp,
+                           const int64_t* vs, void* o, const int64_t* os, float* lse, const FwdWs& w, int B, int Hq,
+                           int Hkv, int T, float eps, float scale, hipStream_t st) {
+  constexpr int D = kF32D;
+  const int BH = B * Hkv;
+  if (int rc = launch_centered_keys(k, ks, w, B, Hkv, T, st)) return rc;
+  LUCID_LAUNCH("lucid_vp_layout_f32_kernel", (lucid::lucid_vp_layout_kernel<D, float, true>), dim3(T / 64, BH), st,
+               w.kch, rows_strides(Hkv, T, D), (const float*)vp, S(vs), Hkv, T, eps, w.rinv, w.vpb, w.vpt, w.mass,
+               kForceExact, w.vpbl, w.vptl);
+  return launch_attn_fwd_f32(q, qs, o, os, lse, w, B, Hq, Hkv, T, scale, st);
+}
+
+int launch_attn_vp_bwd_f32(const void* dout, const int64_t* dos, const void* o, const int64_t* os, const float* lse,
+                           const FwdWs& f, void* dq, const int64_t* dqs, void* dk, const int64_t* dks, void* dvp,
+                           const int64_t* dvps, const BwdWs& w, int B, int Hq, int Hkv, int T, float scale,
+                           hipStream_t st) {
+  constexpr int D = kF32D;
+  const int BH = B * Hkv;
+  if (int rc = launch_attn_bwd_f32(dout, dos, o, os, lse, f, dq, dqs, w, B, Hq, Hkv, T, scale, st)) return rc;
+  LUCID_LAUNCH("lucid_rows_out_kernel", (lucid::lucid_rows_out_kernel<D, float>), dim3(T / 64, BH), st, w.dka,
+               (float*)dk, S(dks), Hkv, T, 1.f);
+  LUCID_LAUNCH("lucid_rows_out_kernel", (lucid::lucid_rows_out_kernel<D, float>), dim3(T / 64, BH), st, w.dvp,
+               (float*)dvp, S(dvps), Hkv, T, 1.f);
+  return LUCID_OK;
+}
+
+// Gradient of get_v_prime on fp32 inputs: dV' (fp32, strided) in, fp32 dK and dV out.
+int launch_precond_only_bwd_f32(const void* dvp, const int64_t* dvps, const FwdWs& f, void* dk, const int64_t* dks,
+                                void* dv, const int64_t* dvs, const BwdWs& w, int B, int Hkv, int T, float scale,
+                                hipStream_t st) {
+  constexpr int D = kF32D;
+  LUCID_LAUNCH("lucid_rows_in_kernel", (lucid::lucid_rows_in_kernel<D, float>), dim3(T / 64, B * Hkv), st,
+               (const float*)dvp, S(dvps), w.dvp, Hkv, T, w.counters);
+  return launch_precond_bwd_f32(f, dk, dks, dv, dvs, w, nullptr, B, Hkv, T, scale, st);
 }
 
 // Decoding: split the cached sequence so that one resident round of split workgroups
@@ -530,7 +741,7 @@ int lucid_decode_noalloc(const void* q, const int64_t* q_strides, const void* k,
 }
 
 
-int lucid_abi_version(void) { return 2; }
+int lucid_abi_version(void) { return 3; }
 
 int lucid_set_precision(int mode) {
   g_last_error.clear();
@@ -634,6 +845,141 @@ int lucid_attn_bwd(const void* dout, const int64_t* do_strides, const void* q, c
                           dk_strides, dv, dv_strides, w, B, Hq, Hkv, T, scale, st);
   return launch_bwd<128>(dout, do_strides, q, q_strides, k, k_strides, o, o_strides, lse, f, dq, dq_strides, dk,
                          dk_strides, dv, dv_strides, w, B, Hq, Hkv, T, scale, st);
+}
+
+size_t lucid_fwd_f32_workspace_bytes(int B, int Hq, int Hkv, int T, int D) {
+  return carve_fwd(nullptr, B, Hq, Hkv, T, D, true).bytes;
+}
+
+size_t lucid_bwd_f32_workspace_bytes(int B, int Hq, int Hkv, int T, int D) {
+  return carve_bwd(nullptr, B, Hq, Hkv, T, D, true).bytes;
+}
+
+int lucid_attn_fwd_f32(const float* q, const int64_t* q_strides, const float* k, const int64_t* k_strides,
+                       const float* v, const int64_t* v_strides, float* o, const int64_t* o_strides, float* vprime,
+                       float* lse, void* fwd_ws, int B, int Hq, int Hkv, int T, int D, float scale, float eps,
+                       void* stream) {
+  g_last_error.clear();
+  if (int rc = check_dims(B, Hq, Hkv, T, D)) return rc;
+  if (D != 64) return fail("fp32 inputs are supported at head_dim 64, got " + std::to_string(D));
+  if (int rc = check_tensor("q", q, q_strides)) return rc;
+  if (int rc = check_tensor("k", k, k_strides)) return rc;
+  if (int rc = check_tensor("v", v, v_strides)) return rc;
+  if (int rc = check_tensor("o", o, o_strides)) return rc;
+  if (!vprime || !lse || !fwd_ws) return fail("vprime, lse and fwd_ws must be non-null");
+  if (int rc = check_ws("fwd_ws", fwd_ws)) return rc;
+  if (int rc = chain_check()) return rc;
+  const FwdWs w = carve_fwd(fwd_ws, B, Hq, Hkv, T, D, true);
+  return launch_fwd_f32(q, q_strides, k, k_strides, v, v_strides, o, o_strides, vprime, lse, w, B, Hq, Hkv, T,
+                        scale, eps, static_cast<hipStream_t>(stream));
+}
+
+int lucid_attn_bwd_f32(const float* dout, const int64_t* do_strides, const float* o, const int64_t* o_strides,
+                       const float* lse, const void* fwd_ws, float* dq, const int64_t* dq_strides, float* dk,
+                       const int64_t* dk_strides, float* dv, const int64_t* dv_strides, void* bwd_ws, int B, int Hq,
+                       int Hkv, int T, int D, float scale, void* stream) {
+  g_last_error.clear();
+  if (int rc = check_dims(B, Hq, Hkv, T, D)) return rc;
+  if (D != 64) return fail("fp32 inputs are supported at head_dim 64, got " + std::to_string(D));
+  if (int rc = check_tensor("dout", dout, do_strides)) return rc;
+  if (int rc = check_tensor("o", o, o_strides)) return rc;
+  if (int rc = check_tensor("dq", dq, dq_strides)) return rc;
+  if (int rc = check_tensor("dk", dk, dk_strides)) return rc;
+  if (int rc = check_tensor("dv", dv, dv_strides)) return rc;
+  if (!lse || !fwd_ws || !bwd_ws) return fail("lse, fwd_ws and bwd_ws must be non-null");
+  if (int rc = check_ws("fwd_ws", fwd_ws)) return rc;
+  if (int rc = check_ws("bwd_ws", bwd_ws)) return rc;
+  if (int rc = chain_check()) return rc;
+  const FwdWs f = carve_fwd(const_cast<void*>(fwd_ws), B, Hq, Hkv, T, D, true);
+  const BwdWs w = carve_bwd(bwd_ws, B, Hq, Hkv, T, D, true);
+  return launch_bwd_f32(dout, do_strides, o, o_strides, lse, f, dq, dq_strides, dk, dk_strides, dv, dv_strides, w,
+                        B, Hq, Hkv, T, scale, static_cast<hipStream_t>(stream));
+}
+
+size_t lucid_v_prime_f32_workspace_bytes(int B, int Hkv, int T, int D) {
+  return carve_fwd(nullptr, B, Hkv, Hkv, T, D, true, false).bytes;
+}
+
+int lucid_get_v_prime_f32(const float* k, const int64_t* k_strides, const float* v, const int64_t* v_strides,
+                          float* vprime, void* fwd_ws, int B, int Hkv, int T, int D, float scale, float eps,
+                          void* stream) {
+  g_last_error.clear();
+  if (int rc = check_dims(B, Hkv, Hkv, T, D)) return rc;
+  if (D != kF32D) return fail("fp32 inputs are supported at head_dim 64, got " + std::to_string(D));
+  if (int rc = check_tensor("k", k, k_strides)) return rc;
+  if (int rc = check_tensor("v", v, v_strides)) return rc;
+  if (!vprime || !fwd_ws) return fail("vprime and fwd_ws must be non-null");
+  if (int rc = check_ws("fwd_ws", fwd_ws)) return rc;
+  if (int rc = chain_check()) return rc;
+  const FwdWs w = carve_fwd(fwd_ws, B, Hkv, Hkv, T, D, true, false);
+  return launch_precond_fwd_f32(k, k_strides, v, v_strides, vprime, w, B, Hkv, T, scale, eps,
+                                static_cast<hipStream_t>(stream));
+}
+
+int lucid_precond_bwd_f32(const float* dvprime, const int64_t* dvprime_strides, const void* fwd_ws, float* dk,
+                          const int64_t* dk_strides, float* dv, const int64_t* dv_strides, void* bwd_ws, int B,
+                          int Hkv, int T, int D, float scale, void* stream) {
+  g_last_error.clear();
+  if (int rc = check_dims(B, Hkv, Hkv, T, D)) return rc;
+  if (D != kF32D) return fail("fp32 inputs are supported at head_dim 64, got " + std::to_string(D));
+  if (int rc = check_tensor("dvprime", dvprime, dvprime_strides)) return rc;
+  if (int rc = check_tensor("dk", dk, dk_strides)) return rc;
+  if (int rc = check_tensor("dv", dv, dv_strides)) return rc;
+  if (!fwd_ws || !bwd_ws) return fail("fwd_ws and bwd_ws must be non-null");
+  if (int rc = check_ws("fwd_ws", fwd_ws)) return rc;
+  if (int rc = check_ws("bwd_ws", bwd_ws)) return rc;
+  if (int rc = chain_check()) return rc;
+  const FwdWs f = carve_fwd(const_cast<void*>(fwd_ws), B, Hkv, Hkv, T, D, true, false);
+  const BwdWs w = carve_seam_bwd(bwd_ws, B, Hkv, Hkv, T, D, false);
+  return launch_precond_only_bwd_f32(dvprime, dvprime_strides, f, dk, dk_strides, dv, dv_strides, w, B, Hkv, T,
+                                     scale, static_cast<hipStream_t>(stream));
+}
+
+size_t lucid_attn_vp_fwd_f32_workspace_bytes(int B, int Hq, int Hkv, int T, int D) {
+  return carve_attn_vp(nullptr, B, Hq, Hkv, T, D, true).bytes;
+}
+
+int lucid_attn_vp_fwd_f32(const float* q, const int64_t* q_strides, const float* k, const int64_t* k_strides,
+                          const float* vprime, const int64_t* vprime_strides, float* o, const int64_t* o_strides,
+                          float* lse, void* ws, int B, int Hq, int Hkv, int T, int D, float scale, float eps,
+                          void* stream) {
+  g_last_error.clear();
+  if (int rc = check_dims(B, Hq, Hkv, T, D)) return rc;
+  if (D != kF32D) return fail("fp32 inputs are supported at head_dim 64, got " + std::to_string(D));
+  if (int rc = check_tensor("q", q, q_strides)) return rc;
+  if (int rc = check_tensor("k", k, k_strides)) return rc;
+  if (int rc = check_tensor("vprime", vprime, vprime_strides)) return rc;
+  if (int rc = check_tensor("o", o, o_strides)) return rc;
+  if (!lse || !ws) return fail("lse and ws must be non-null");
+  if (int rc = check_ws("ws", ws)) return rc;
+  const FwdWs w = carve_attn_vp(ws, B, Hq, Hkv, T, D, true);
+  return launch_attn_vp_fwd_f32(q, q_strides, k, k_strides, vprime, vprime_strides, o, o_strides, lse, w, B, Hq, Hkv,
+                                T, eps, scale, static_cast<hipStream_t>(stream));
+}
+
+size_t lucid_attn_vp_bwd_f32_workspace_bytes(int B, int Hq, int Hkv, int T, int D) {
+  return carve_seam_bwd(nullptr, B, Hq, Hkv, T, D, true, true).bytes;
+}
+
+int lucid_attn_vp_bwd_f32(const float* dout, const int64_t* do_strides, const float* o, const int64_t* o_strides,
+                          const float* lse, const void* fwd_ws, float* dq, const int64_t* dq_strides, float* dk,
+                          const int64_t* dk_strides, float* dvprime, const int64_t* dvprime_strides, void* bwd_ws,
+                          int B, int Hq, int Hkv, int T, int D, float scale, void* stream) {
+  g_last_error.clear();
+  if (int rc = check_dims(B, Hq, Hkv, T, D)) return rc;
+  if (D != kF32D) return fail("fp32 inputs are supported at head_dim 64, got " + std::to_string(D));
+  if (int rc = check_tensor("dout", dout, do_strides)) return rc;
+  if (int rc = check_tensor("o", o, o_strides)) return rc;
+  if (int rc = check_tensor("dq", dq, dq_strides)) return rc;
+  if (int rc = check_tensor("dk", dk, dk_strides)) return rc;
+  if (int rc = check_tensor("dvprime", dvprime, dvprime_strides)) return rc;
+  if (!lse || !fwd_ws || !bwd_ws) return fail("lse, fwd_ws and bwd_ws must be non-null");
+  if (int rc = check_ws("fwd_ws", fwd_ws)) return rc;
+  if (int rc = check_ws("bwd_ws", bwd_ws)) return rc;
+  const FwdWs f = carve_attn_vp(const_cast<void*>(fwd_ws), B, Hq, Hkv, T, D, true);
+  const BwdWs w = carve_seam_bwd(bwd_ws, B, Hq, Hkv, T, D, true, true);
+  return launch_attn_vp_bwd_f32(dout, do_strides, o, o_strides, lse, f, dq, dq_strides, dk, dk_strides, dvprime,
+                                dvprime_strides, w, B, Hq, Hkv, T, scale, static_cast<hipStream_t>(stream));
 }
 
 size_t lucid_attn_vp_fwd_workspace_bytes(int B, int Hq, int Hkv, int T, int D) {

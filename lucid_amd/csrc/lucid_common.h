@@ -21,6 +21,27 @@ struct Strides {
 // (N(0,1)-like) give m ~ 1e-2; keys along a shared direction give m ~ T.
 constexpr float kExactMass = 4.0f;
 
+// fp32 inputs (F32 kernel instances): each fp32 input X reaches the kernels as two bf16
+// tensors, X ~= X_hi + X_lo (lucid_split_kernel: 16 significant bits), and every product
+// with an input operand takes three MFMAs (hi*hi + hi*lo + lo*hi).  The score products
+// (K.K of P, Q.K of the softmax) take the fourth, lo*lo, as well: where the two operands
+// share a direction (a key with itself or its neighbours, keys along a common direction)
+// the lo parts are correlated and the dropped lo*lo terms add up instead of cancelling,
+// a bias of ~2^-18 |k|^2 in the exponent's argument (a 2e-4 relative V' error at
+// correlated keys, T = 1024, against 1.5e-5 with it).  The hi copies are passed in
+// the kernels' ordinary bf16 arguments; this struct carries the lo copies (same layouts,
+// same strides) and the fp32 values themselves where a kernel reads them directly.
+// Null members in the bf16 instances.
+struct Lo {
+  const bf16* q;     // query lo, strides as the kernel's q
+  const bf16* k;     // key lo, strides as the kernel's k
+  const bf16* dout;  // dO lo, strides as the kernel's dout
+  const bf16* kt;    // K^T lo, T-perm [bh][D][T]
+  const float* v;    // fp32 V [B, H, T, D], strides vs (the chain's right-hand side)
+  const float* o;    // fp32 O, strides as the kernel's o (delta of the backward)
+  const float* dof;  // fp32 dO, strides as the kernel's dout (delta of the backward)
+};
+
 // bf16 of the residual x - hi for D-layout values e = 8h .. 8h+7 (hi = pack_b(x, h)):
 // the lo term of a two-term bf16 split (x ~= hi + lo to ~2^-17 relative)
 __device__ __forceinline__ bf16x8 pack_lo(const f32x16& x, int h, const bf16x8& hi) {

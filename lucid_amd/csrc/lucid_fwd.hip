@@ -13,6 +13,8 @@
 //                            it waits on a per-head progress counter for V'_j, j < i and
 //                            sweeps the earlier keys 128 at a time
 //   lucid_attn_fwd_kernel    causal online-softmax attention on V' (256 query rows / WG, LDS tiles)
+#include <type_traits>
+
 #include "lucid_common.h"
 
 namespace lucid {
@@ -24,15 +26,15 @@ namespace lucid {
 // to mass_init (0 before lucid_mass_kernel; a forced precision sets it directly).
 // grid (T/64, B*Hkv)
 // ---------------------------------------------------------------------------
-template <int D>
+template <int D, bool F32 = false>
 __global__ __launch_bounds__(256) void lucid_prep_kernel(const bf16* __restrict__ k, Strides ks, int Hkv, int T,
                                                          float eps, float scale, float* __restrict__ rinv,
                                                          bf16* __restrict__ kt, float* __restrict__ pinv,
                                                          int* __restrict__ counters, float* __restrict__ mass,
-                                                         float mass_init) {
+                                                         float mass_init, Lo lo, bf16* __restrict__ ktl) {
   constexpr int SEG = D / 4;
   constexpr int NKS = D / 16;
-  __shared__ bf16 tile[D][64 + 8];
+  __shared__ bf16 tile[F32 ? 2 : 1][D][64 + 8];
   __shared__ float rr[64];
   __shared__ __attribute__((aligned(16))) float Pd[64][68];
   const int blk = blockIdx.x, bh = blockIdx.y;
@@ -40,16 +42,23 @@ __global__ __launch_bounds__(256) void lucid_prep_kernel(const bf16* __restrict_
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
   const bf16* kp = k + b * ks.b + h * ks.h + (int64_t)blk * 64 * ks.t;
+  const bf16* klp = F32 ? lo.k + b * ks.b + h * ks.h + (int64_t)blk * 64 * ks.t : nullptr;
   const int row = tid >> 2, seg = tid & 3;
   float ss = 0.f;
 #pragma unroll
   for (int c = 0; c < SEG; c += 8) {
     bf16x8 x = ld8(kp + row * ks.t + seg * SEG + c);
+    bf16x8 xl;
+    if constexpr (F32) xl = ld8(klp + row * ks.t + seg * SEG + c);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       float f = (float)x[e];
+      if constexpr (F32) {
+        f += (float)xl[e];
+        tile[1][seg * SEG + c + e][row] = xl[e];
+      }
       ss += f * f;
-      tile[seg * SEG + c + e][row] = x[e];
+      tile[0][seg * SEG + c + e][row] = x[e];
     }
   }
   ss += __shfl_xor(ss, 1, 64);
@@ -69,8 +78,13 @@ __global__ __launch_bounds__(256) void lucid_prep_kernel(const bf16* __restrict_
     const int dd = idx >> 3, c8 = idx & 7;
     bf16x8 out;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) out[e] = tile[dd][(c8 >> 1) * 16 + jmap((c8 & 1) * 8 + e)];
+    for (int e = 0; e < 8; ++e) out[e] = tile[0][dd][(c8 >> 1) * 16 + jmap((c8 & 1) * 8 + e)];
     *reinterpret_cast<bf16x8*>(kt + ((int64_t)bh * D + dd) * T + blk * 64 + c8 * 8) = out;
+    if constexpr (F32) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) out[e] = tile[1][dd][(c8 >> 1) * 16 + jmap((c8 & 1) * 8 + e)];
+      *reinterpret_cast<bf16x8*>(ktl + ((int64_t)bh * D + dd) * T + blk * 64 + c8 * 8) = out;
+    }
   }
   // diagonal block P[m][n] = exp(s r_m r_n K_m.K_n - 1/s) (n <= m); wave -> 32x32 quadrant
   {
@@ -80,9 +94,15 @@ __global__ __launch_bounds__(256) void lucid_prep_kernel(const bf16* __restrict_
     f32x16 sd = zero16();
     if (nh <= mh) {
 #pragma unroll
-      for (int st = 0; st < NKS; ++st)
-        sd = mfma32(ld8(kp + (int64_t)(mh * 32 + l32) * ks.t + 16 * st + 8 * g),
-                    ld8(kp + (int64_t)(nh * 32 + l32) * ks.t + 16 * st + 8 * g), sd);
+      for (int st = 0; st < NKS; ++st) {
+        const int64_t om = (mh * 32 + l32) * ks.t + 16 * st + 8 * g, on = (nh * 32 + l32) * ks.t + 16 * st + 8 * g;
+        sd = mfma32(ld8(kp + om), ld8(kp + on), sd);
+        if constexpr (F32) {
+          sd = mfma32(ld8(kp + om), ld8(klp + on), sd);
+          sd = mfma32(ld8(klp + om), ld8(kp + on), sd);
+          sd = mfma32(ld8(klp + om), ld8(klp + on), sd);
+        }
+      }
     }
     const int n = nh * 32 + l32;
     const float an = sl2 * rr[n];
@@ -100,16 +120,19 @@ __global__ __launch_bounds__(256) void lucid_prep_kernel(const bf16* __restrict_
 // Operands of the attention on a caller's V' (eager_lucid_attention_forward): V' rows
 // (bf16 or fp32, strided) to the bf16 row-major copy vpb and the T-perm copy vpt the
 // attention kernels read, 1/rms of K for the row-mass pass, and the head's row mass
-// initialised to mass_init.  grid (T/64, B*Hkv)
+// initialised to mass_init.  LO (fp32 V', fp32-input kernels): V' also as its bf16 lo
+// parts vpbl (row-major) and vptl (T-perm), V' ~= hi + lo.  grid (T/64, B*Hkv)
 // ---------------------------------------------------------------------------
-template <int D, typename VT>
+template <int D, typename VT, bool LO = false>
 __global__ __launch_bounds__(256) void lucid_vp_layout_kernel(const bf16* __restrict__ k, Strides ks,
                                                               const VT* __restrict__ vp, Strides vs, int Hkv, int T,
                                                               float eps, float* __restrict__ rinv,
                                                               bf16* __restrict__ vpb, bf16* __restrict__ vpt,
-                                                              float* __restrict__ mass, float mass_init) {
+                                                              float* __restrict__ mass, float mass_init,
+                                                              bf16* __restrict__ vpbl, bf16* __restrict__ vptl) {
+  static_assert(!LO || std::is_same<VT, float>::value, "lo parts of an fp32 V' only");
   constexpr int SEG = D / 4;
-  __shared__ bf16 tile[D][64 + 8];
+  __shared__ bf16 tile[LO ? 2 : 1][D][64 + 8];
   const int blk = blockIdx.x, bh = blockIdx.y;
   const int b = bh / Hkv, h = bh - b * Hkv;
   const int tid = threadIdx.x;
@@ -122,15 +145,21 @@ __global__ __launch_bounds__(256) void lucid_vp_layout_kernel(const bf16* __rest
 #pragma unroll
   for (int c = 0; c < SEG; c += 8) {
     const bf16x8 x = ld8(kr + seg * SEG + c);
-    bf16x8 y;
+    bf16x8 y, yl;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float f = (float)x[e];
       ss += f * f;
-      y[e] = (bf16)vr[seg * SEG + c + e];
-      tile[seg * SEG + c + e][row] = y[e];
+      const float vv = (float)vr[seg * SEG + c + e];
+      y[e] = (bf16)vv;
+      tile[0][seg * SEG + c + e][row] = y[e];
+      if constexpr (LO) {
+        yl[e] = (bf16)(vv - (float)y[e]);
+        tile[1][seg * SEG + c + e][row] = yl[e];
+      }
     }
     *reinterpret_cast<bf16x8*>(ob + seg * SEG + c) = y;
+    if constexpr (LO) *reinterpret_cast<bf16x8*>(vpbl + ((int64_t)bh * T + t) * D + seg * SEG + c) = yl;
   }
   ss += __shfl_xor(ss, 1, 64);
   ss += __shfl_xor(ss, 2, 64);
@@ -141,8 +170,13 @@ __global__ __launch_bounds__(256) void lucid_vp_layout_kernel(const bf16* __rest
     const int dd = idx >> 3, c8 = idx & 7;
     bf16x8 out;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) out[e] = tile[dd][(c8 >> 1) * 16 + jmap((c8 & 1) * 8 + e)];
+    for (int e = 0; e < 8; ++e) out[e] = tile[0][dd][(c8 >> 1) * 16 + jmap((c8 & 1) * 8 + e)];
     *reinterpret_cast<bf16x8*>(vpt + ((int64_t)bh * D + dd) * T + blk * 64 + c8 * 8) = out;
+    if constexpr (LO) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) out[e] = tile[1][dd][(c8 >> 1) * 16 + jmap((c8 & 1) * 8 + e)];
+      *reinterpret_cast<bf16x8*>(vptl + ((int64_t)bh * D + dd) * T + blk * 64 + c8 * 8) = out;
+    }
   }
 }
 
@@ -160,6 +194,82 @@ __global__ __launch_bounds__(256) void lucid_rows_out_kernel(const float* __rest
     OT* o = dst + b * ds.b + h * ds.h + (int64_t)t * ds.t + c4;
 #pragma unroll
     for (int u = 0; u < 4; ++u) o[u] = (OT)(x[u] * mul);
+  }
+}
+
+// fp32 inputs: a strided fp32 [B][H][T][D] tensor to the bf16 pair the MFMA operands are
+// built from, hi = bf16(x) and lo = bf16(x - hi) (x = hi + lo to ~2^-16 relative), both
+// written as contiguous [BH][T][D] rows.  center (fp32 [BH][D], or null): x - center[bh]
+// is split instead.  grid (T/64, B*H)
+template <int D>
+__global__ __launch_bounds__(256) void lucid_split_kernel(const float* __restrict__ src, Strides ss, int H, int T,
+                                                          bf16* __restrict__ hi, bf16* __restrict__ lo,
+                                                          const float* __restrict__ center) {
+  constexpr int SEG = D / 4;
+  const int bh = blockIdx.y, b = bh / H, h = bh - b * H;
+  const int row = threadIdx.x >> 2, seg = threadIdx.x & 3;
+  const int t = blockIdx.x * 64 + row;
+  const float* s = src + b * ss.b + h * ss.h + (int64_t)t * ss.t + seg * SEG;
+  const float* cen = center ? center + (int64_t)bh * D + seg * SEG : nullptr;
+  const int64_t off = ((int64_t)bh * T + t) * D + seg * SEG;
+#pragma unroll
+  for (int c = 0; c < SEG; c += 8) {
+    f32x4 x0 = *reinterpret_cast<const f32x4*>(s + c);
+    f32x4 x1 = *reinterpret_cast<const f32x4*>(s + c + 4);
+    if (cen) {
+      const f32x4 c0 = *reinterpret_cast<const f32x4*>(cen + c);
+      const f32x4 c1 = *reinterpret_cast<const f32x4*>(cen + c + 4);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        x0[u] -= c0[u];
+        x1[u] -= c1[u];
+      }
+    }
+    bf16x8 a, r;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      a[u] = (bf16)x0[u];
+      a[u + 4] = (bf16)x1[u];
+      r[u] = (bf16)(x0[u] - (float)a[u]);
+      r[u + 4] = (bf16)(x1[u] - (float)a[u + 4]);
+    }
+    *reinterpret_cast<bf16x8*>(hi + off + c) = a;
+    *reinterpret_cast<bf16x8*>(lo + off + c) = r;
+  }
+}
+
+// Mean key of each head, mean[bh][d] = (1/T) sum_t K[t][d] (fp32 inputs).  The attention's
+// scores are taken against K - mean: the softmax is unchanged (a per-row constant Q.mean
+// leaves it as it is), dQ = s dS (K - mean) exactly because every row of dS sums to zero,
+// and dK does not involve K.  Keys along a shared direction then reach the split products
+// as their small deviations, so the 16-bit rounding of dS, dP and the scores no longer
+// multiplies the shared part (a ~6-10x smaller dQ error there).  One workgroup per head:
+// 16 row phases x 16 four-column groups, fixed summation order.  grid (B*H), D == 64
+template <int D>
+__global__ __launch_bounds__(256) void lucid_key_mean_kernel(const float* __restrict__ k, Strides ks, int H, int T,
+                                                             float* __restrict__ mean) {
+  static_assert(D == 64, "16 four-column groups");
+  __shared__ f32x4 part[16][16];
+  const int bh = blockIdx.x, b = bh / H, h = bh - b * H;
+  const int ph = threadIdx.x >> 4, c4 = threadIdx.x & 15;
+  const float* kp = k + b * ks.b + h * ks.h + 4 * c4;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+  for (int t = ph; t < T; t += 16) {
+    const f32x4 x = *reinterpret_cast<const f32x4*>(kp + (int64_t)t * ks.t);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc[u] += x[u];
+  }
+  part[ph][c4] = acc;
+  __syncthreads();
+  if (ph == 0) {
+    f32x4 tot = part[0][c4];
+    for (int r = 1; r < 16; ++r)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) tot[u] += part[r][c4][u];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) tot[u] /= (float)T;
+    *reinterpret_cast<f32x4*>(mean + (int64_t)bh * D + 4 * c4) = tot;
   }
 }
 
@@ -272,14 +382,15 @@ __global__ __launch_bounds__(256) void lucid_mass_kernel(const bf16* __restrict_
 // ---------------------------------------------------------------------------
 // zx = -(X_B P_BA) for every 128-row chain block (A = its first 64 rows, B = the
 // last 64; X_B = the inverse of P's diagonal block B from lucid_prep_kernel,
-// P_BA[m][c] = exp(s r_m r_c K_m.K_c - 1/s)), 3-term bf16 split products, columns in
+// P_BA[m][c] = exp(s r_m r_c K_m.K_c - 1/s)) (fp32 inputs: K.K over hi/lo with all four
+// terms), columns in
 // T-perm order so that the chain can add zx V'_A straight from its bf16 V'_A tile.
 // wave -> 32x32 quadrant.  grid (T/128, B*Hkv)
 // ---------------------------------------------------------------------------
-template <int D>
+template <int D, bool F32 = false>
 __global__ __launch_bounds__(256) void lucid_zx_kernel(const bf16* __restrict__ k, Strides ks, int Hkv, int T,
                                                        const float* __restrict__ rinv, float scale,
-                                                       const float* __restrict__ pinv, float* __restrict__ zx) {
+                                                       const float* __restrict__ pinv, float* __restrict__ zx, Lo lo) {
   constexpr int NKS = D / 16;
   __shared__ __attribute__((aligned(16))) float Xb[64][68];
   __shared__ __attribute__((aligned(16))) float PT[64][68];  // PT[c][m] = P_BA[m][c]
@@ -300,10 +411,18 @@ __global__ __launch_bounds__(256) void lucid_zx_kernel(const bf16* __restrict__ 
     const float sl2 = scale * LOG2E_F;
     const float c0 = LOG2E_F / scale;
     f32x16 sd = zero16();
+    const bf16* klp = F32 ? lo.k + b * ks.b + h * ks.h + (int64_t)blk * 128 * ks.t : nullptr;
 #pragma unroll
-    for (int st = 0; st < NKS; ++st)
-      sd = mfma32(ld8(kp + (int64_t)(64 + tm * 32 + l32) * ks.t + 16 * st + 8 * g),
-                  ld8(kp + (int64_t)(tn * 32 + l32) * ks.t + 16 * st + 8 * g), sd);
+    for (int st = 0; st < NKS; ++st) {
+      const int64_t om = (int64_t)(64 + tm * 32 + l32) * ks.t + 16 * st + 8 * g;
+      const int64_t on = (int64_t)(tn * 32 + l32) * ks.t + 16 * st + 8 * g;
+      sd = mfma32(ld8(kp + om), ld8(kp + on), sd);
+      if constexpr (F32) {
+        sd = mfma32(ld8(kp + om), ld8(klp + on), sd);
+        sd = mfma32(ld8(klp + om), ld8(kp + on), sd);
+        sd = mfma32(ld8(klp + om), ld8(klp + on), sd);
+      }
+    }
     const int cc = tn * 32 + l32;
     const float ac = sl2 * rv[cc];
     float rm[16];
@@ -357,10 +476,10 @@ __global__ __launch_bounds__(256) void lucid_zx_kernel(const bf16* __restrict__ 
 // extra tile and registers allow one workgroup per CU; at d = 128 the staged pairs are
 // single-buffered (three 32 KB tiles), each pair staged after the previous one's sweep.
 // ---------------------------------------------------------------------------
-template <int D, bool EXACT>
+template <int D, bool EXACT, bool F32 = false>
 struct PfwdSmem;
 template <int D>
-struct PfwdSmem<D, false> {
+struct PfwdSmem<D, false, false> {
   union {
     struct {
       bf16 k[2][128 * D];  // swizzled tiles (chunk c of row r at c ^ (r & 7))
@@ -374,12 +493,13 @@ struct PfwdSmem<D, false> {
     } fin;
   } u;
 };
-template <int D>
-struct PfwdSmem<D, true> {
+template <int D, bool F32>
+struct PfwdSmem<D, true, F32> {
   static constexpr int NBUF = D == 128 ? 1 : 2;
   union {
     struct {
       bf16 k[NBUF][128 * D];
+      bf16 kl[F32 ? NBUF : 1][F32 ? 128 * D : 8];  // lo part of K (fp32 inputs)
       bf16 v[NBUF][D * 128];
       bf16 vl[NBUF][D * 128];  // lo part of V'^T
       float r[NBUF][128];
@@ -393,16 +513,17 @@ struct PfwdSmem<D, true> {
   } u;
 };
 
-template <int D, bool EXACT>
+template <int D, bool EXACT, bool F32 = false>
 __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void lucid_precond_fwd_kernel(
     const bf16* __restrict__ k, Strides ks, const bf16* __restrict__ v, Strides vs, int Hkv, int T, int BH,
     const float* __restrict__ rinv, float scale, float* __restrict__ vp32, bf16* __restrict__ vpb,
     bf16* __restrict__ vpt, bf16* __restrict__ vpbl, bf16* __restrict__ vptl, float* __restrict__ pinv,
-    const float* __restrict__ zx, const float* __restrict__ mass, int* __restrict__ counters) {
+    const float* __restrict__ zx, const float* __restrict__ mass, int* __restrict__ counters, Lo lo) {
+  static_assert(EXACT || !F32, "fp32 inputs run the exact chains");
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
   constexpr bool SINGLE = EXACT && D == 128;  // one staging buffer
-  __shared__ __attribute__((aligned(16))) PfwdSmem<D, EXACT> sm;
+  __shared__ __attribute__((aligned(16))) PfwdSmem<D, EXACT, F32> sm;
 
   const int id = blockIdx.x;
   const int i2 = id / BH, bh = id - (id / BH) * BH;
@@ -423,27 +544,41 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
   const float sl2 = scale * LOG2E_F;
   const float c0 = LOG2E_F / scale;
 
-  bf16x8 kbi[2][NKS];
+  const bf16* klh = F32 ? lo.k + b * ks.b + h * ks.h : nullptr;
+  bf16x8 kbi[2][NKS], kbil[2][NKS];
   float ai[2];
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
     const int row = i0 + ih * 64 + nt * 32 + l32;
 #pragma unroll
-    for (int st = 0; st < NKS; ++st) kbi[nt][st] = ld8(kp + (int64_t)row * ks.t + 16 * st + 8 * g);
+    for (int st = 0; st < NKS; ++st) {
+      kbi[nt][st] = ld8(kp + (int64_t)row * ks.t + 16 * st + 8 * g);
+      if constexpr (F32) kbil[nt][st] = ld8(klh + (int64_t)row * ks.t + 16 * st + 8 * g);
+    }
     ai[nt] = sl2 * rv[row];
   }
   // accumulators: -V^T for the kh = 0 waves, zero for the others
   f32x16 acc[NDT][2];
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
-    const bf16* vrow = vh + (int64_t)(i0 + ih * 64 + nt * 32 + l32) * vs.t;
+    const int64_t roff = (int64_t)(i0 + ih * 64 + nt * 32 + l32) * vs.t;
+    const bf16* vrow = vh + roff;
 #pragma unroll
     for (int t = 0; t < NDT; ++t)
 #pragma unroll
       for (int qd = 0; qd < 4; ++qd) {
-        const bf16x4 vv = *reinterpret_cast<const bf16x4*>(vrow + t * 32 + 8 * qd + 4 * g);
+        float vv[4];
+        if constexpr (F32) {  // the fp32 right-hand side itself
+          const f32x4 x = *reinterpret_cast<const f32x4*>(lo.v + b * vs.b + h * vs.h + roff + t * 32 + 8 * qd + 4 * g);
 #pragma unroll
-        for (int u = 0; u < 4; ++u) acc[t][nt][4 * qd + u] = kh ? 0.f : -(float)vv[u];
+          for (int u = 0; u < 4; ++u) vv[u] = x[u];
+        } else {
+          const bf16x4 x = *reinterpret_cast<const bf16x4*>(vrow + t * 32 + 8 * qd + 4 * g);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) vv[u] = (float)x[u];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc[t][nt][4 * qd + u] = kh ? 0.f : -vv[u];
       }
   }
 
@@ -459,6 +594,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
     const int buf = SINGLE ? 0 : pp & 1;
     if (w < 2) dma_f32x64(rv + pp * 128 + 64 * w, &sm.u.st.r[buf][64 * w]);
     dma_stage<128, D / 8>(plan_k, kp + (int64_t)pp * 128 * ks.t, sm.u.st.k[buf]);
+    if constexpr (F32) dma_stage<128, D / 8>(plan_k, klh + (int64_t)pp * 128 * ks.t, sm.u.st.kl[buf]);
     dma_stage<D, 16>(plan_v, vpth + pp * 128, sm.u.st.v[buf]);
     if constexpr (EXACT) dma_stage<D, 16>(plan_v, vptlh + pp * 128, sm.u.st.vl[buf]);
   };
@@ -495,6 +631,15 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
         f32x16 sc = zero16();
 #pragma unroll
         for (int st = 0; st < NKS; ++st) sc = mfma32(ka[st], kbi[nt][st], sc);
+        if constexpr (F32) {
+#pragma unroll
+          for (int st = 0; st < NKS; ++st) {
+            const bf16x8 kal = ld8(swz<D / 8>(sm.u.st.kl[buf], key0 + l32, 2 * st + g));
+            sc = mfma32(ka[st], kbil[nt][st], sc);
+            sc = mfma32(kal, kbi[nt][st], sc);
+            sc = mfma32(kal, kbil[nt][st], sc);
+          }
+        }
 #pragma unroll
         for (int e = 0; e < 16; ++e) sc[e] = __builtin_amdgcn_exp2f(fmaf(sc[e] * ai[nt], rj[e], -c0));
         pb[nt][0] = pack_b(sc, 0);
@@ -694,18 +839,20 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
 // backward's delta_i = dO_i . O_i enters dQ_i = s sum_j dS_ij K_j multiplied by the
 // attention-weighted mean key, which is large when keys share a direction.
 // ---------------------------------------------------------------------------
-template <int D>
-__global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_fwd_kernel(const bf16* __restrict__ q, Strides qs,
-                                                             const bf16* __restrict__ k, Strides ks,
-                                                             const bf16* __restrict__ vpt, bf16* __restrict__ o,
-                                                             Strides os, float* __restrict__ lse,
-                                                             const float* __restrict__ mass, bf16* __restrict__ olo,
-                                                             int Hq, int Hkv, int T, int BHq, float scale) {
+template <int D, bool F32 = false>
+__global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid_attn_fwd_kernel(
+    const bf16* __restrict__ q, Strides qs, const bf16* __restrict__ k, Strides ks, const bf16* __restrict__ vpt,
+    std::conditional_t<F32, float, bf16>* __restrict__ o, Strides os, float* __restrict__ lse,
+    const float* __restrict__ mass, bf16* __restrict__ olo, int Hq, int Hkv, int T, int BHq, float scale, Lo lo,
+    const bf16* __restrict__ vptl) {
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
   constexpr int CH = D / 32;  // 16-byte chunks per thread for each of the K and V'^T tiles
+  constexpr int NST = F32 ? 4 * CH : 2 * CH;  // staging registers (fp32 inputs: hi and lo tiles)
   __shared__ __attribute__((aligned(16))) bf16 lk[2][64][D + 8];
   __shared__ __attribute__((aligned(16))) bf16 lv[2][D][64 + 8];
+  __shared__ __attribute__((aligned(16))) bf16 lkl[F32 ? 2 : 1][F32 ? 64 : 1][D + 8];  // lo tiles (fp32 inputs)
+  __shared__ __attribute__((aligned(16))) bf16 lvl[F32 ? 2 : 1][F32 ? D : 1][64 + 8];
 
   const int nblk = (T + 255) / 256;
   const int id = blockIdx.x;
@@ -721,14 +868,20 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_fw
   const bf16* qh = q + b * qs.b + hq * qs.h;
   const bf16* kh = k + b * ks.b + h * ks.h;
   const bf16* vth = vpt + (int64_t)bh * D * T;
+  const bf16* qlh = F32 ? lo.q + b * qs.b + hq * qs.h : nullptr;
+  const bf16* klh = F32 ? lo.k + b * ks.b + h * ks.h : nullptr;
+  const bf16* vtlh = F32 ? vptl + (int64_t)bh * D * T : nullptr;
   const float c = scale * LOG2E_F;
 
-  bf16x8 qb[2][NKS];
+  bf16x8 qb[2][NKS], qbl[2][NKS];
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
     const int rq = min(row0 + nt * 32 + l32, T - 1);
 #pragma unroll
-    for (int st = 0; st < NKS; ++st) qb[nt][st] = ld8(qh + (int64_t)rq * qs.t + 16 * st + 8 * g);
+    for (int st = 0; st < NKS; ++st) {
+      qb[nt][st] = ld8(qh + (int64_t)rq * qs.t + 16 * st + 8 * g);
+      if constexpr (F32) qbl[nt][st] = ld8(qlh + (int64_t)rq * qs.t + 16 * st + 8 * g);
+    }
   }
   f32x16 oacc[NDT][2];
 #pragma unroll
@@ -740,7 +893,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_fw
 
   const int ntile = (min(r0 + 256, T) + 63) / 64;
   const int last_w = row0 / 64;  // this wave's diagonal tile
-  bf16x8 stg[2 * CH];
+  bf16x8 stg[NST];
   auto gload = [&](int j0) {
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
@@ -749,6 +902,10 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_fw
       stg[u] = ld8(kh + (int64_t)(j0 + kr) * ks.t + kc * 8);
       const int vr = cidx >> 3, vc = cidx & 7;
       stg[CH + u] = ld8(vth + (int64_t)vr * T + j0 + vc * 8);
+      if constexpr (F32) {
+        stg[2 * CH + u] = ld8(klh + (int64_t)(j0 + kr) * ks.t + kc * 8);
+        stg[3 * CH + u] = ld8(vtlh + (int64_t)vr * T + j0 + vc * 8);
+      }
     }
   };
   auto lstore = [&](int buf) {
@@ -759,6 +916,10 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_fw
       *reinterpret_cast<bf16x8*>(&lk[buf][kr][kc * 8]) = stg[u];
       const int vr = cidx >> 3, vc = cidx & 7;
       *reinterpret_cast<bf16x8*>(&lv[buf][vr][vc * 8]) = stg[CH + u];
+      if constexpr (F32) {
+        *reinterpret_cast<bf16x8*>(&lkl[buf][kr][kc * 8]) = stg[2 * CH + u];
+        *reinterpret_cast<bf16x8*>(&lvl[buf][vr][vc * 8]) = stg[3 * CH + u];
+      }
     }
   };
   gload(0);
@@ -769,7 +930,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_fw
     const bool more = jt + 1 < ntile;
     if (more) gload((jt + 1) * 64);
     if (jt <= last_w && row0 < T) {
-      if constexpr (D == 64) {
+      if constexpr (D == 64 && !F32) {
         // Two 32-row halves (nt) per 64-key tile, staggered so that each half's softmax
         // VALU work overlaps the other half's MFMA work inside this wave:
         //   S(nt 0) | max(0) | S(nt 1) + exp(0) | max(1) | PV(nt 0) + exp(1) | PV(nt 1)
@@ -851,18 +1012,28 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_fw
         pv(0);
         softmax(1);
         pv(1);
-      } else {  // D = 128: both halves' products first (the staggered order spills here)
+      } else {  // D = 128 and fp32 inputs: both halves' products first (the staggered order spills)
         f32x16 s[2][2];
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
-          bf16x8 ka[NKS];
+          bf16x8 ka[NKS], kal[NKS];
 #pragma unroll
-          for (int st = 0; st < NKS; ++st) ka[st] = ld8(&lk[buf][mt * 32 + l32][16 * st + 8 * g]);
+          for (int st = 0; st < NKS; ++st) {
+            ka[st] = ld8(&lk[buf][mt * 32 + l32][16 * st + 8 * g]);
+            if constexpr (F32) kal[st] = ld8(&lkl[buf][mt * 32 + l32][16 * st + 8 * g]);
+          }
 #pragma unroll
           for (int nt = 0; nt < 2; ++nt) {
             s[mt][nt] = zero16();
 #pragma unroll
-            for (int st = 0; st < NKS; ++st) s[mt][nt] = mfma32(ka[st], qb[nt][st], s[mt][nt]);
+            for (int st = 0; st < NKS; ++st) {
+              s[mt][nt] = mfma32(ka[st], qb[nt][st], s[mt][nt]);
+              if constexpr (F32) {
+                s[mt][nt] = mfma32(ka[st], qbl[nt][st], s[mt][nt]);
+                s[mt][nt] = mfma32(kal[st], qb[nt][st], s[mt][nt]);
+                s[mt][nt] = mfma32(kal[st], qbl[nt][st], s[mt][nt]);
+              }
+            }
           }
         }
         if (jt == last_w) {
@@ -874,7 +1045,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_fw
               for (int e = 0; e < 16; ++e)
                 if (mt * 32 + drow(e, g) > nt * 32 + l32) s[mt][nt][e] = -INFINITY;
         }
-        bf16x8 pb[2][4];
+        bf16x8 pb[2][4], pbl[2][4];
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) {
           float mx = -INFINITY;
@@ -905,6 +1076,12 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_fw
           pb[nt][1] = pack_b(s[0][nt], 1);
           pb[nt][2] = pack_b(s[1][nt], 0);
           pb[nt][3] = pack_b(s[1][nt], 1);
+          if constexpr (F32) {
+            pbl[nt][0] = pack_lo(s[0][nt], 0, pb[nt][0]);
+            pbl[nt][1] = pack_lo(s[0][nt], 1, pb[nt][1]);
+            pbl[nt][2] = pack_lo(s[1][nt], 0, pb[nt][2]);
+            pbl[nt][3] = pack_lo(s[1][nt], 1, pb[nt][3]);
+          }
         }
 #pragma unroll
         for (int t = 0; t < NDT; ++t) {
@@ -915,34 +1092,52 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64) void lucid_attn_fw
           for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
             for (int k4 = 0; k4 < 4; ++k4) oacc[t][nt] = mfma32(va[k4], pb[nt][k4], oacc[t][nt]);
+          if constexpr (F32) {
+#pragma unroll
+            for (int k4 = 0; k4 < 4; ++k4) {
+              const bf16x8 val = ld8(&lvl[buf][t * 32 + l32][16 * k4 + 8 * g]);
+#pragma unroll
+              for (int nt = 0; nt < 2; ++nt) {
+                oacc[t][nt] = mfma32(va[k4], pbl[nt][k4], oacc[t][nt]);
+                oacc[t][nt] = mfma32(val, pb[nt][k4], oacc[t][nt]);
+              }
+            }
+          }
         }
       }
     }
     if (more) lstore(buf ^ 1);
     __syncthreads();
   }
-  const bool exact = mass[bh] > kExactMass;
+  const bool exact = !F32 && mass[bh] > kExactMass;  // fp32 O needs no lo part
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
     const int irow = row0 + nt * 32 + l32;
     const float ls = wave_sum32(lsum[nt]);
     if (irow < T) {
       const float inv = 1.0f / ls;
-      bf16* op = o + b * os.b + hq * os.h + (int64_t)irow * os.t;
+      auto* op = o + b * os.b + hq * os.h + (int64_t)irow * os.t;
       bf16* ol = olo + ((int64_t)bhq * T + irow) * D;
 #pragma unroll
       for (int t = 0; t < NDT; ++t)
 #pragma unroll
         for (int qq = 0; qq < 4; ++qq) {
-          bf16x4 bb, bl;
+          if constexpr (F32) {
+            f32x4 x;
 #pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const float x = oacc[t][nt][4 * qq + u] * inv;
-            bb[u] = (bf16)x;
-            bl[u] = (bf16)(x - (float)bb[u]);
+            for (int u = 0; u < 4; ++u) x[u] = oacc[t][nt][4 * qq + u] * inv;
+            *reinterpret_cast<f32x4*>(op + t * 32 + 8 * qq + 4 * g) = x;
+          } else {
+            bf16x4 bb, bl;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              const float x = oacc[t][nt][4 * qq + u] * inv;
+              bb[u] = (bf16)x;
+              bl[u] = (bf16)(x - (float)bb[u]);
+            }
+            *reinterpret_cast<bf16x4*>(op + t * 32 + 8 * qq + 4 * g) = bb;
+            if (exact) *reinterpret_cast<bf16x4*>(ol + t * 32 + 8 * qq + 4 * g) = bl;
           }
-          *reinterpret_cast<bf16x4*>(op + t * 32 + 8 * qq + 4 * g) = bb;
-          if (exact) *reinterpret_cast<bf16x4*>(ol + t * 32 + 8 * qq + 4 * g) = bl;
         }
       if (g == 0) lse[(int64_t)bhq * T + irow] = m[nt] + log2f(ls);
     }

@@ -13,7 +13,8 @@ Python mirror of the reference operator seams in ``modeling_lucid.py``:
 Layouts follow the reference: ``query [B, Hq, T, d]``, ``key/value [B, Hkv, T, d]``
 (any strides with a contiguous last axis, e.g. the ``.view(...).transpose(1, 2)``
 views LucidAttention builds), output ``[B, T, Hq, d]``.  Inputs must be bf16
-CUDA(HIP) tensors with d in {64, 128}; anything else raises (there is no CPU or
+CUDA(HIP) tensors with d in {64, 128}, or fp32 tensors with d = 64 (computed on bf16
+hi/lo pairs to ~1e-4 relative, fp32 outputs); anything else raises (there is no CPU or
 eager fallback).  T that is not a multiple of 128 is zero-padded at the end,
 which is exact for every real row because P and the attention mask are causal.
 """
@@ -26,23 +27,30 @@ from . import _lib
 
 _T_ALIGN = 128
 _SUPPORTED_D = (64, 128)
+_F32_D = 64  # head dim of the fp32-input kernels
 
 
-def _check_inputs(q, k, v):
+def _check_inputs(q, k, v, f32_ok=False):
+    """Shapes, device and dtype of the operands; ``f32_ok``: fp32 operands (head dim 64) are
+    accepted, all of one dtype."""
     for name, t in (("query", q), ("key", k), ("value", v)):
         if t is None:
             continue
         if not t.is_cuda:
             raise RuntimeError(f"lucid_amd: {name} must be a GPU tensor (no CPU path)")
-        if t.dtype != torch.bfloat16:
-            raise TypeError(f"lucid_amd: {name} must be bfloat16, got {t.dtype}")
+        if t.dtype != torch.bfloat16 and not (f32_ok and t.dtype == torch.float32):
+            raise TypeError(f"lucid_amd: {name} must be bfloat16{' or float32' if f32_ok else ''}, got {t.dtype}")
         if t.dim() != 4:
             raise ValueError(f"lucid_amd: {name} must be 4-D [B, H, T, d]")
+    if len({t.dtype for t in (q, k, v) if t is not None}) > 1:
+        raise TypeError("lucid_amd: query, key and value must share one dtype")
     if v is not None and k.shape != v.shape:
         raise ValueError(f"lucid_amd: key {tuple(k.shape)} and value {tuple(v.shape)} must match")
     d = k.shape[-1]
     if d not in _SUPPORTED_D:
         raise ValueError(f"lucid_amd: head_dim {d} not supported (supported: {_SUPPORTED_D})")
+    if k.dtype == torch.float32 and d != _F32_D:
+        raise ValueError(f"lucid_amd: fp32 inputs are supported at head_dim {_F32_D}, got {d} (use bf16)")
     if q is not None:
         if q.shape[0] != k.shape[0] or q.shape[2] != k.shape[2] or q.shape[3] != d:
             raise ValueError("lucid_amd: query/key shapes disagree")
@@ -79,6 +87,42 @@ def _fwd(q, k, v, scale, eps):
         _lib.stream_handle(dev))
     _lib.check(lib, rc, "lucid_attn_fwd")
     return o, vprime, lse, ws
+
+
+def _fwd_f32(q, k, v, scale, eps):
+    lib = _lib.load()
+    B, Hq, T, D = q.shape
+    Hkv = k.shape[1]
+    dev = q.device
+    o = torch.empty(B, T, Hq, D, dtype=torch.float32, device=dev)
+    vprime = torch.empty(B, Hkv, T, D, dtype=torch.float32, device=dev)
+    lse = torch.empty(B, Hq, T, dtype=torch.float32, device=dev)
+    ws = torch.empty(lib.lucid_fwd_f32_workspace_bytes(B, Hq, Hkv, T, D), dtype=torch.uint8, device=dev)
+    rc = lib.lucid_attn_fwd_f32(
+        _lib.ptr(q), _lib.strides3(q, (0, 1, 2)), _lib.ptr(k), _lib.strides3(k, (0, 1, 2)),
+        _lib.ptr(v), _lib.strides3(v, (0, 1, 2)), _lib.ptr(o), _lib.strides3(o, (0, 2, 1)),
+        _lib.ptr(vprime), _lib.ptr(lse), _lib.ptr(ws), B, Hq, Hkv, T, D, float(scale), float(eps),
+        _lib.stream_handle(dev))
+    _lib.check(lib, rc, "lucid_attn_fwd_f32")
+    return o, vprime, lse, ws
+
+
+def _bwd_f32(do, q, k, o, lse, ws, scale):
+    lib = _lib.load()
+    B, Hq, T, D = q.shape
+    Hkv = k.shape[1]
+    dev = q.device
+    dq = torch.empty(B, Hq, T, D, dtype=torch.float32, device=dev)
+    dk = torch.empty(B, Hkv, T, D, dtype=torch.float32, device=dev)
+    dv = torch.empty(B, Hkv, T, D, dtype=torch.float32, device=dev)
+    bws = torch.empty(lib.lucid_bwd_f32_workspace_bytes(B, Hq, Hkv, T, D), dtype=torch.uint8, device=dev)
+    rc = lib.lucid_attn_bwd_f32(
+        _lib.ptr(do), _lib.strides3(do, (0, 2, 1)), _lib.ptr(o), _lib.strides3(o, (0, 2, 1)),
+        _lib.ptr(lse), _lib.ptr(ws), _lib.ptr(dq), _lib.strides3(dq, (0, 1, 2)),
+        _lib.ptr(dk), _lib.strides3(dk, (0, 1, 2)), _lib.ptr(dv), _lib.strides3(dv, (0, 1, 2)),
+        _lib.ptr(bws), B, Hq, Hkv, T, D, float(scale), _lib.stream_handle(dev))
+    _lib.check(lib, rc, "lucid_attn_bwd_f32")
+    return dq, dk, dv
 
 
 def _bwd(do, q, k, o, lse, ws, scale, eps):
@@ -118,7 +162,8 @@ class LucidAttentionFunction(torch.autograd.Function):
                     torch.empty(B, k.shape[1], t, D, dtype=torch.float32, device=q.device))
         tp = _padded_len(t)
         qp, kp, vp_ = _prep(q, tp), _prep(k, tp), _prep(v, tp)
-        o, vprime, lse, ws = _fwd(qp, kp, vp_, scale, eps)
+        ctx.f32 = q.dtype == torch.float32
+        o, vprime, lse, ws = (_fwd_f32 if ctx.f32 else _fwd)(qp, kp, vp_, scale, eps)
         ctx.save_for_backward(qp, kp, o, lse, ws)
         ctx.scale, ctx.eps, ctx.t = scale, eps, t
         ctx.mark_non_differentiable(vprime)
@@ -130,13 +175,17 @@ class LucidAttentionFunction(torch.autograd.Function):
             return do.new_zeros(ctx.shapes[0]), do.new_zeros(ctx.shapes[1]), do.new_zeros(ctx.shapes[1]), None, None
         qp, kp, o, lse, ws = ctx.saved_tensors
         t, tp = ctx.t, qp.shape[2]
-        if do.dtype != torch.bfloat16:
-            do = do.to(torch.bfloat16)
+        dt = torch.float32 if ctx.f32 else torch.bfloat16
+        if do.dtype != dt:
+            do = do.to(dt)
         if t != tp:
             do = F.pad(do, (0, 0, 0, 0, 0, tp - t))
         if do.stride(-1) != 1 or any(s % 8 for s in do.stride()) or do.data_ptr() % 16:
             do = do.contiguous()
-        dq, dk, dv = _bwd(do, qp, kp, o, lse, ws, ctx.scale, ctx.eps)
+        if ctx.f32:
+            dq, dk, dv = _bwd_f32(do, qp, kp, o, lse, ws, ctx.scale)
+        else:
+            dq, dk, dv = _bwd(do, qp, kp, o, lse, ws, ctx.scale, ctx.eps)
         return dq[:, :, :t], dk[:, :, :t], dv[:, :, :t], None, None
 
 
@@ -175,8 +224,9 @@ def lucid_attention(query, key, value, scaling=None, eps=1e-5, return_vprime=Fal
     """LUCID attention: ``softmax(s Q K^T, causal) P^-1 V``; returns O ``[B, T, Hq, d]``.
 
     ``eps`` is the k_norm epsilon (``config.rms_norm_eps``, modeling_lucid.py:409).
+    bf16 inputs give bf16 O; fp32 inputs (head dim 64) give fp32 O and gradients.
     """
-    _check_inputs(query, key, value)
+    _check_inputs(query, key, value, f32_ok=True)
     scale = query.shape[-1] ** -0.5 if scaling is None else float(scaling)
     o, vprime = LucidAttentionFunction.apply(query, key, value, scale, eps)
     return (o, vprime) if return_vprime else o
@@ -216,12 +266,18 @@ class GetVPrimeFunction(torch.autograd.Function):
         lib = _lib.load()
         tp = _padded_len(T)
         k, v = _prep(key, tp), _prep(value, tp)
+        ctx.f32 = key.dtype == torch.float32
         vprime = torch.empty(B, Hkv, tp, D, dtype=torch.float32, device=key.device)
-        ws = torch.empty(lib.lucid_fwd_workspace_bytes(B, Hkv, Hkv, tp, D), dtype=torch.uint8, device=key.device)
-        rc = lib.lucid_get_v_prime(_lib.ptr(k), _lib.strides3(k, (0, 1, 2)), _lib.ptr(v), _lib.strides3(v, (0, 1, 2)),
-                                   _lib.ptr(vprime), _lib.ptr(ws), B, Hkv, tp, D, scale, float(eps),
-                                   _lib.stream_handle(key.device))
-        _lib.check(lib, rc, "lucid_get_v_prime")
+        if ctx.f32:
+            ws = torch.empty(lib.lucid_v_prime_f32_workspace_bytes(B, Hkv, tp, D), dtype=torch.uint8,
+                             device=key.device)
+            fn, name = lib.lucid_get_v_prime_f32, "lucid_get_v_prime_f32"
+        else:
+            ws = torch.empty(lib.lucid_fwd_workspace_bytes(B, Hkv, Hkv, tp, D), dtype=torch.uint8, device=key.device)
+            fn, name = lib.lucid_get_v_prime, "lucid_get_v_prime"
+        rc = fn(_lib.ptr(k), _lib.strides3(k, (0, 1, 2)), _lib.ptr(v), _lib.strides3(v, (0, 1, 2)),
+                _lib.ptr(vprime), _lib.ptr(ws), B, Hkv, tp, D, scale, float(eps), _lib.stream_handle(key.device))
+        _lib.check(lib, rc, name)
         ctx.save_for_backward(k, ws)
         ctx.scale = scale
         return vprime[:, :, :T].to(value.dtype)
@@ -234,13 +290,22 @@ class GetVPrimeFunction(torch.autograd.Function):
         lib = _lib.load()
         B, Hkv, tp, D = k.shape
         t = ctx.t
+        bws = torch.empty(lib.lucid_precond_bwd_workspace_bytes(B, Hkv, tp, D), dtype=torch.uint8, device=k.device)
+        if ctx.f32:  # fp32 inputs: fp32 dV' in, fp32 dK and dV out
+            dvp = _prep(dvp.float(), tp)
+            dk = torch.empty(B, Hkv, tp, D, dtype=torch.float32, device=k.device)
+            dv = torch.empty_like(dk)
+            rc = lib.lucid_precond_bwd_f32(_lib.ptr(dvp), _lib.strides3(dvp, (0, 1, 2)), _lib.ptr(ws), _lib.ptr(dk),
+                                           _lib.strides3(dk, (0, 1, 2)), _lib.ptr(dv), _lib.strides3(dv, (0, 1, 2)),
+                                           _lib.ptr(bws), B, Hkv, tp, D, ctx.scale, _lib.stream_handle(k.device))
+            _lib.check(lib, rc, "lucid_precond_bwd_f32")
+            return dk[:, :, :t], dv[:, :, :t], None, None
         f32 = dvp.dtype == torch.float32
         if not f32 and dvp.dtype != torch.bfloat16:
             dvp = dvp.to(torch.bfloat16)
         dvp = _prep(dvp, tp)
         dk = torch.empty(B, Hkv, tp, D, dtype=torch.bfloat16, device=k.device)
         dv = torch.empty_like(dk)
-        bws = torch.empty(lib.lucid_precond_bwd_workspace_bytes(B, Hkv, tp, D), dtype=torch.uint8, device=k.device)
         rc = lib.lucid_precond_bwd(_lib.ptr(k), _lib.strides3(k, (0, 1, 2)), _lib.ptr(dvp), _lib.strides3(dvp, (0, 1, 2)),
                                    int(f32), _lib.ptr(ws), _lib.ptr(dk), _lib.strides3(dk, (0, 1, 2)), _lib.ptr(dv),
                                    _lib.strides3(dv, (0, 1, 2)), _lib.ptr(bws), B, Hkv, tp, D, ctx.scale,
@@ -266,9 +331,24 @@ class AttentionOnVPrimeFunction(torch.autograd.Function):
         lib = _lib.load()
         tp = _padded_len(T)
         qp, kp = _prep(q, tp), _prep(k, tp)
+        dev = q.device
+        ctx.f32in = q.dtype == torch.float32
+        if ctx.f32in:  # fp32 q and k: the fp32 kernels, V' in fp32
+            vpp = _prep(vp.float(), tp)
+            o = torch.empty(B, tp, Hq, D, dtype=torch.float32, device=dev)
+            lse = torch.empty(B, Hq, tp, dtype=torch.float32, device=dev)
+            ws = torch.empty(lib.lucid_attn_vp_fwd_f32_workspace_bytes(B, Hq, Hkv, tp, D), dtype=torch.uint8,
+                             device=dev)
+            rc = lib.lucid_attn_vp_fwd_f32(_lib.ptr(qp), _lib.strides3(qp, (0, 1, 2)), _lib.ptr(kp),
+                                           _lib.strides3(kp, (0, 1, 2)), _lib.ptr(vpp), _lib.strides3(vpp, (0, 1, 2)),
+                                           _lib.ptr(o), _lib.strides3(o, (0, 2, 1)), _lib.ptr(lse), _lib.ptr(ws),
+                                           B, Hq, Hkv, tp, D, scale, float(eps), _lib.stream_handle(dev))
+            _lib.check(lib, rc, "lucid_attn_vp_fwd_f32")
+            ctx.save_for_backward(qp, kp, o, lse, ws)
+            ctx.scale = scale
+            return o[:, :T]
         f32 = vp.dtype == torch.float32
         vpp = _prep(vp if f32 else vp.to(torch.bfloat16), tp)
-        dev = q.device
         o = torch.empty(B, tp, Hq, D, dtype=torch.bfloat16, device=dev)
         lse = torch.empty(B, Hq, tp, dtype=torch.float32, device=dev)
         ws = torch.empty(lib.lucid_attn_vp_fwd_workspace_bytes(B, Hq, Hkv, tp, D), dtype=torch.uint8, device=dev)
@@ -290,13 +370,27 @@ class AttentionOnVPrimeFunction(torch.autograd.Function):
         lib = _lib.load()
         B, Hq, tp, D = qp.shape
         Hkv, t = kp.shape[1], ctx.t
-        if do.dtype != torch.bfloat16:
-            do = do.to(torch.bfloat16)
+        dt = torch.float32 if ctx.f32in else torch.bfloat16
+        if do.dtype != dt:
+            do = do.to(dt)
         if t != tp:
             do = F.pad(do, (0, 0, 0, 0, 0, tp - t))
         if do.stride(-1) != 1 or any(s % 8 for s in do.stride()) or do.data_ptr() % 16:
             do = do.contiguous()
         dev = qp.device
+        if ctx.f32in:
+            dq = torch.empty(B, Hq, tp, D, dtype=torch.float32, device=dev)
+            dk = torch.empty(B, Hkv, tp, D, dtype=torch.float32, device=dev)
+            dvp = torch.empty(B, Hkv, tp, D, dtype=torch.float32, device=dev)
+            bws = torch.empty(lib.lucid_attn_vp_bwd_f32_workspace_bytes(B, Hq, Hkv, tp, D), dtype=torch.uint8,
+                              device=dev)
+            rc = lib.lucid_attn_vp_bwd_f32(_lib.ptr(do), _lib.strides3(do, (0, 2, 1)), _lib.ptr(o),
+                                           _lib.strides3(o, (0, 2, 1)), _lib.ptr(lse), _lib.ptr(ws), _lib.ptr(dq),
+                                           _lib.strides3(dq, (0, 1, 2)), _lib.ptr(dk), _lib.strides3(dk, (0, 1, 2)),
+                                           _lib.ptr(dvp), _lib.strides3(dvp, (0, 1, 2)), _lib.ptr(bws),
+                                           B, Hq, Hkv, tp, D, ctx.scale, _lib.stream_handle(dev))
+            _lib.check(lib, rc, "lucid_attn_vp_bwd_f32")
+            return dq[:, :, :t], dk[:, :, :t], dvp[:, :, :t].to(ctx.vdtype), None, None
         f32 = ctx.vdtype == torch.float32
         dq = torch.empty(B, Hq, tp, D, dtype=torch.bfloat16, device=dev)
         dk = torch.empty(B, Hkv, tp, D, dtype=torch.bfloat16, device=dev)
@@ -318,9 +412,10 @@ def get_v_prime(key, value, scaling=None, attention_mask=None, eps=1e-5):
     """``V' = P^-1 V`` -- ``LucidAttention.get_v_prime(key, value, scaling, attention_mask)``
     (modeling_lucid.py:551-574), differentiable w.r.t. ``key`` and ``value``.
 
-    ``key, value [B, Hkv, T, d]``; returns V' in ``value``'s dtype.  ``eps`` is k_norm's
-    epsilon (``config.rms_norm_eps``).  ``attention_mask``: None or the causal mask."""
-    _check_inputs(None, key, value)
+    ``key, value [B, Hkv, T, d]`` (bf16, or fp32 at d = 64); returns V' in ``value``'s dtype.
+    ``eps`` is k_norm's epsilon (``config.rms_norm_eps``).  ``attention_mask``: None or the
+    causal mask."""
+    _check_inputs(None, key, value, f32_ok=True)
     _check_causal_mask(attention_mask, key.shape[2], key.shape[2])
     scale = key.shape[-1] ** -0.5 if scaling is None else float(scaling)
     return GetVPrimeFunction.apply(key, value, scale, eps)
@@ -330,10 +425,10 @@ def eager_lucid_attention_forward(query, key, v_prime, scaling=None, attention_m
     """``LucidAttention.eager_lucid_attention_forward(query, key, v_prime, scaling, attention_mask)``
     (modeling_lucid.py:505-549): causal softmax attention of ``query [B, Hq, T, d]`` and
     ``key [B, Hkv, T, d]`` on a given ``v_prime [B, Hkv, T, d]`` (bf16 or fp32; GQA by index,
-    no repeat_kv copy).  Returns ``(O [B, T, Hq, d], None)``, differentiable w.r.t. all three.
+    no repeat_kv copy).  fp32 query and key (d = 64) run the fp32 kernels (fp32 O).  Returns ``(O [B, T, Hq, d], None)``, differentiable w.r.t. all three.
     ``attention_mask``: None or the causal mask.  ``eps`` (k_norm's) only serves the per-head
     precision choice (:func:`set_precision`)."""
-    _check_inputs(query, key, None)
+    _check_inputs(query, key, None, f32_ok=True)
     if v_prime.shape != key.shape or not v_prime.is_cuda or v_prime.dtype not in (torch.bfloat16, torch.float32):
         raise ValueError("lucid_amd: v_prime must be a bf16 or fp32 GPU tensor shaped like key")
     _check_causal_mask(attention_mask, query.shape[2], key.shape[2])

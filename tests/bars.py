@@ -16,3 +16,10 @@ def bar(scale: float) -> float:
 
 def check(name: str, err: float, scale: float) -> None:
     assert err <= bar(scale), f"{name}: max err {err:.3e} > bar {bar(scale):.3e} (max|ref| {scale:.3e})"
+
+# fp32 inputs (north star: rel 1e-4): max |x - ref| <= 1e-4 * max |ref| for every tensor
+TOL_F32 = 1e-4
+
+
+def check_f32(name: str, err: float, scale: float) -> None:
+    assert err <= TOL_F32 * scale, f"{name}: max err {err:.3e} > {TOL_F32:.0e} * max|ref| {scale:.3e}"
