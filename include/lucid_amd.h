@@ -9,9 +9,15 @@
  * LUCID_EINVAL for a rejected argument (text in lucid_last_error()), or
  * LUCID_EHIP + hipError_t for a HIP launch failure.
  *
- * Supported: head_dim D in {64, 128}; T a multiple of 128 (the Python layer
- * zero-pads the sequence end, which leaves every real row unchanged because
- * both P and the attention mask are causal); Hq a multiple of Hkv (GQA).
+ * Supported: head_dim D in [1, 128] (fp32 entry points: [1, 64]); T a multiple of
+ * 128 (the Python layer zero-pads the sequence end, which leaves every real row
+ * unchanged because both P and the attention mask are causal); Hq a multiple of
+ * Hkv (GQA).  Head dims other than 64 and 128 (the reference model's is 68,
+ * lucid/config/config.json:9) run on zero-padded rows: every [.., D] operand then
+ * has Dp = 64 (D <= 64) or 128 (D > 64) elements per row, columns D .. Dp-1 zero in
+ * the inputs (dout included) and written zero in the outputs; the dot products are
+ * unchanged and the RMS of k_norm divides by D itself.  Workspace sizes take D and
+ * are those of Dp.
  */
 #ifndef LUCID_AMD_H
 #define LUCID_AMD_H
@@ -200,7 +206,8 @@ size_t lucid_decode_workspace_bytes(int B, int Hq, int Hkv, int T_cap, int D);
 
 /* One decoding step: a new token per sequence (q [B,Hq,1,D], k and v [B,Hkv,1,D])
  * against the caches k_cache (keys with RoPE applied, as the attention saw them) and
- * vp_cache (V' rows, bf16), both [B,Hkv,T_cap,D] with rows [0, T_past) valid.
+ * vp_cache (V' rows, bf16), both [B,Hkv,T_cap,D] (padded rows of Dp columns for
+ * other head dims) with rows [0, T_past) valid.
  * Computes the token's V' row with the exact diagonal,
  *   v'_t = (v_t - sum_{j<t} P_tj v'_j) / P_tt,
  * writes it to vp_new (fp32 [B,Hkv,D]) and appends (k_t, v'_t) at row T_past of the

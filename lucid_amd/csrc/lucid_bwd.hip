@@ -999,7 +999,7 @@ struct ProwSmem<D, true, F32> {
 template <int D, bool EXACT, bool F32 = false>
 __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void lucid_precond_bwd_row_kernel(
     const bf16* __restrict__ k, Strides ks, int Hkv, int T, int BH, const float* __restrict__ rinv, float scale,
-    const bf16* __restrict__ vpb, const bf16* __restrict__ vpbl, const bf16* __restrict__ dvb,
+    float dn, const bf16* __restrict__ vpb, const bf16* __restrict__ vpbl, const bf16* __restrict__ dvb,
     const bf16* __restrict__ dvbl, const float* __restrict__ mass, const float* __restrict__ colsum,
     const float* __restrict__ dka, std::conditional_t<F32, float, bf16>* __restrict__ dk_out, Strides dks, Lo lo) {
   static_assert(!F32 || (EXACT && D == 64), "fp32 inputs: exact instance, head dim 64");
@@ -1188,12 +1188,12 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
     dotp = wave_sum32(dotp);
     kss = wave_sum32(kss);
     gdot = wave_sum32(gdot);
-    const float f = dotp / (float)D;
+    const float f = dotp / dn;
     // The diagonal terms of M K^ + M^T K^ (excluded from both sums), -2 s M_ii K^_i with
     // M_ii = (dV_i . V'_i) P_ii, P_ii = exp(s |K^_i|^2 - 1/s), lie along K^_i, which the
-    // RMSNorm backward keeps only to the fraction 1 - |K^_i|^2 / D (= eps r_i^2): added here
+    // RMSNorm backward keeps only to the fraction 1 - |K^_i|^2 / dn (= eps r_i^2): added here
     // as fd * K^_i rather than as two large terms that cancel down to that fraction.
-    const float fd = -2.f * scale * gdot * __builtin_amdgcn_exp2f(fmaf(sl2, kss, -c0)) * (1.f - kss / (float)D);
+    const float fd = -2.f * scale * gdot * __builtin_amdgcn_exp2f(fmaf(sl2, kss, -c0)) * (1.f - kss / dn);
     auto* op = dk_out + b * dks.b + h * dks.h + (int64_t)irow * dks.t;
 #pragma unroll
     for (int t = 0; t < NDT; ++t)

@@ -74,8 +74,14 @@ struct FwdWs {
   size_t bytes;
 };
 
+// Head dims other than 64 and 128 run on rows zero-padded to the next of the two (every
+// [.., d] operand has padded_dim(D) columns, columns D.. zero in the inputs and written
+// zero in the outputs); the RMS of K divides by D itself.
+int padded_dim(int D) { return D <= 64 ? 64 : 128; }
+
 // f32: the fp32-input copies as well (with_q: also those of Q and the attention's keys)
 FwdWs carve_fwd(void* base, int B, int Hq, int Hkv, int T, int D, bool f32 = false, bool with_q = true) {
+  D = padded_dim(D);
   const size_t BH = (size_t)B * Hkv, BHq = (size_t)B * Hq;
   FwdWs w{};
   size_t off = 0;
@@ -127,6 +133,7 @@ struct BwdWs {
 };
 
 BwdWs carve_bwd(void* base, int B, int Hq, int Hkv, int T, int D, bool f32 = false) {
+  D = padded_dim(D);
   const size_t BH = (size_t)B * Hkv, BHq = (size_t)B * Hq;
   BwdWs w{};
   size_t off = 0;
@@ -153,7 +160,7 @@ BwdWs carve_bwd(void* base, int B, int Hq, int Hkv, int T, int D, bool f32 = fal
 
 int check_dims(int B, int Hq, int Hkv, int T, int D) {
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || T <= 0) return fail("B, Hq, Hkv and T must be positive");
-  if (D != 64 && D != 128) return fail("head_dim must be 64 or 128, got " + std::to_string(D));
+  if (D < 1 || D > 128) return fail("head_dim must be in [1, 128], got " + std::to_string(D));
   if (T % 128 != 0) return fail("T must be a multiple of 128, got " + std::to_string(T));
   if (Hq % Hkv != 0) return fail("Hq must be a multiple of Hkv");
   if ((int64_t)B * Hq * (T / 128) > (int64_t)0x7fffffff) return fail("grid too large");
@@ -181,12 +188,12 @@ lucid::Strides S(const int64_t* s) { return lucid::Strides{s[0], s[1], s[2]}; }
 
 template <int D>
 int launch_precond_fwd(const void* k, const int64_t* ks, const void* v, const int64_t* vs, float* vprime,
-                       const FwdWs& w, int B, int Hkv, int T, float scale, float eps, hipStream_t st) {
+                       const FwdWs& w, int B, int Hkv, int T, float scale, float eps, float dn, hipStream_t st) {
   const int BH = B * Hkv;
   // a forced precision is written straight into the head masses (no mass pass)
   const float mass_init = g_precision == LUCID_PRECISION_EXACT ? 1e30f : 0.f;
   LUCID_LAUNCH("lucid_prep_kernel", lucid::lucid_prep_kernel<D>, dim3(T / 64, BH), st, (const bf16*)k, S(ks), Hkv,
-               T, eps, scale, w.rinv, w.kt, w.pinv, w.counters, w.mass, mass_init, lucid::Lo{}, nullptr);
+               T, eps, dn, scale, w.rinv, w.kt, w.pinv, w.counters, w.mass, mass_init, lucid::Lo{}, nullptr);
   if (g_precision == LUCID_PRECISION_AUTO)
     LUCID_LAUNCH("lucid_mass_kernel", lucid::lucid_mass_kernel<D>, dim3(T / 64, BH), st, (const bf16*)k, S(ks),
                  Hkv, T, w.rinv, scale, w.mass);
@@ -208,8 +215,8 @@ int launch_precond_fwd(const void* k, const int64_t* ks, const void* v, const in
 template <int D>
 int launch_fwd(const void* q, const int64_t* qs, const void* k, const int64_t* ks, const void* v, const int64_t* vs,
                void* o, const int64_t* os, float* vprime, float* lse, const FwdWs& w, int B, int Hq, int Hkv, int T,
-               float scale, float eps, hipStream_t st) {
-  if (int rc = launch_precond_fwd<D>(k, ks, v, vs, vprime, w, B, Hkv, T, scale, eps, st)) return rc;
+               float scale, float eps, float dn, hipStream_t st) {
+  if (int rc = launch_precond_fwd<D>(k, ks, v, vs, vprime, w, B, Hkv, T, scale, eps, dn, st)) return rc;
   const int BHq = B * Hq;
   LUCID_LAUNCH("lucid_attn_fwd_kernel", lucid::lucid_attn_fwd_kernel<D>, dim3(((T + 255) / 256) * BHq), st, (const bf16*)q,
                S(qs), (const bf16*)k, S(ks), w.vpt, (bf16*)o, S(os), lse, w.mass, w.olo, Hq, Hkv, T, BHq, scale,
@@ -245,7 +252,7 @@ int launch_attn_bwd(const void* dout, const int64_t* dos, const void* q, const i
 template <int D>
 int launch_precond_bwd(const void* k, const int64_t* ks, const FwdWs& f, void* dk, const int64_t* dks, void* dv,
                        const int64_t* dvs, const BwdWs& w, const float* dka, int B, int Hkv, int T, float scale,
-                       hipStream_t st) {
+                       float dn, hipStream_t st) {
   const int BH = B * Hkv;
   // each chain kernel in two instances (bf16 and exact), selected per head by the forward's
   // row mass; the precision forced at the forward call is recorded there
@@ -256,10 +263,10 @@ int launch_precond_bwd(const void* k, const int64_t* ks, const FwdWs& f, void* d
                dim3((T / 128) * BH), st, (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, scale, f.kt, f.vpb, f.vpbl,
                f.pinv, f.mass, w.dvp, w.dvb, w.dvbl, (bf16*)dv, S(dvs), w.colsum, w.counters, lucid::Lo{});
   LUCID_LAUNCH("lucid_precond_bwd_row_kernel", (lucid::lucid_precond_bwd_row_kernel<D, false>),
-               dim3(((T + 255) / 256) * BH), st, (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, scale, f.vpb, f.vpbl,
+               dim3(((T + 255) / 256) * BH), st, (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, scale, dn, f.vpb, f.vpbl,
                w.dvb, w.dvbl, f.mass, w.colsum, dka, (bf16*)dk, S(dks), lucid::Lo{});
   LUCID_LAUNCH("lucid_precond_bwd_row_exact_kernel", (lucid::lucid_precond_bwd_row_kernel<D, true>),
-               dim3(((T + 255) / 256) * BH), st, (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, scale, f.vpb, f.vpbl,
+               dim3(((T + 255) / 256) * BH), st, (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, scale, dn, f.vpb, f.vpbl,
                w.dvb, w.dvbl, f.mass, w.colsum, dka, (bf16*)dk, S(dks), lucid::Lo{});
   return LUCID_OK;
 }
@@ -268,10 +275,10 @@ template <int D>
 int launch_bwd(const void* dout, const int64_t* dos, const void* q, const int64_t* qs, const void* k,
                const int64_t* ks, const void* o, const int64_t* os, const float* lse, const FwdWs& f, void* dq,
                const int64_t* dqs, void* dk, const int64_t* dks, void* dv, const int64_t* dvs, const BwdWs& w, int B,
-               int Hq, int Hkv, int T, float scale, hipStream_t st) {
+               int Hq, int Hkv, int T, float scale, float dn, hipStream_t st) {
   if (int rc = launch_attn_bwd<D>(dout, dos, q, qs, k, ks, o, os, lse, f, dq, dqs, w, B, Hq, Hkv, T, scale, st))
     return rc;
-  return launch_precond_bwd<D>(k, ks, f, dk, dks, dv, dvs, w, w.dka, B, Hkv, T, scale, st);
+  return launch_precond_bwd<D>(k, ks, f, dk, dks, dv, dvs, w, w.dka, B, Hkv, T, scale, dn, st);
 }
 
 // ---- the two operator seams (get_v_prime / eager_lucid_attention_forward) ----
@@ -280,6 +287,7 @@ int launch_bwd(const void* dout, const int64_t* dos, const void* q, const int64_
 // the row masses and O's lo part (the FwdWs fields the attention kernels read).
 // (f32: the bf16 pairs of Q, K - mean and V' as well.)
 FwdWs carve_attn_vp(void* base, int B, int Hq, int Hkv, int T, int D, bool f32 = false) {
+  D = padded_dim(D);
   const size_t BH = (size_t)B * Hkv, BHq = (size_t)B * Hq;
   FwdWs w{};
   size_t off = 0;
@@ -311,6 +319,7 @@ FwdWs carve_attn_vp(void* base, int B, int Hq, int Hkv, int T, int D, bool f32 =
 // preconditioner part dV' (as fp32), dV and its lo part, the column sums and counters.
 // (f32 with attn: the bf16 pair of dO as well.)
 BwdWs carve_seam_bwd(void* base, int B, int Hq, int Hkv, int T, int D, bool attn, bool f32 = false) {
+  D = padded_dim(D);
   const size_t BH = (size_t)B * Hkv, BHq = (size_t)B * Hq;
   BwdWs w{};
   size_t off = 0;
@@ -341,16 +350,16 @@ BwdWs carve_seam_bwd(void* base, int B, int Hq, int Hkv, int T, int D, bool attn
 template <int D>
 int launch_attn_vp_fwd(const void* q, const int64_t* qs, const void* k, const int64_t* ks, const void* vp,
                        const int64_t* vs, int vp_f32, void* o, const int64_t* os, float* lse, const FwdWs& w, int B,
-                       int Hq, int Hkv, int T, float scale, float eps, hipStream_t st) {
+                       int Hq, int Hkv, int T, float scale, float eps, float dn, hipStream_t st) {
   const int BH = B * Hkv, BHq = B * Hq;
   const float mass_init = g_precision == LUCID_PRECISION_EXACT ? 1e30f : 0.f;
   if (vp_f32)
     LUCID_LAUNCH("lucid_vp_layout_kernel", (lucid::lucid_vp_layout_kernel<D, float>), dim3(T / 64, BH), st,
-                 (const bf16*)k, S(ks), (const float*)vp, S(vs), Hkv, T, eps, w.rinv, w.vpb, w.vpt, w.mass,
+                 (const bf16*)k, S(ks), (const float*)vp, S(vs), Hkv, T, eps, dn, w.rinv, w.vpb, w.vpt, w.mass,
                  mass_init, nullptr, nullptr);
   else
     LUCID_LAUNCH("lucid_vp_layout_kernel", (lucid::lucid_vp_layout_kernel<D, bf16>), dim3(T / 64, BH), st,
-                 (const bf16*)k, S(ks), (const bf16*)vp, S(vs), Hkv, T, eps, w.rinv, w.vpb, w.vpt, w.mass,
+                 (const bf16*)k, S(ks), (const bf16*)vp, S(vs), Hkv, T, eps, dn, w.rinv, w.vpb, w.vpt, w.mass,
                  mass_init, nullptr, nullptr);
   if (g_precision == LUCID_PRECISION_AUTO)
     LUCID_LAUNCH("lucid_mass_kernel", lucid::lucid_mass_kernel<D>, dim3(T / 64, BH), st, (const bf16*)k, S(ks),
@@ -383,7 +392,7 @@ int launch_attn_vp_bwd(const void* dout, const int64_t* dos, const void* q, cons
 template <int D>
 int launch_precond_only_bwd(const void* k, const int64_t* ks, const void* dvp, const int64_t* dvps, int dvp_f32,
                             const FwdWs& f, void* dk, const int64_t* dks, void* dv, const int64_t* dvs,
-                            const BwdWs& w, int B, int Hkv, int T, float scale, hipStream_t st) {
+                            const BwdWs& w, int B, int Hkv, int T, float scale, float dn, hipStream_t st) {
   const int BH = B * Hkv;
   if (dvp_f32)
     LUCID_LAUNCH("lucid_rows_in_kernel", (lucid::lucid_rows_in_kernel<D, float>), dim3(T / 64, BH), st,
@@ -391,7 +400,7 @@ int launch_precond_only_bwd(const void* k, const int64_t* ks, const void* dvp, c
   else
     LUCID_LAUNCH("lucid_rows_in_kernel", (lucid::lucid_rows_in_kernel<D, bf16>), dim3(T / 64, BH), st,
                  (const bf16*)dvp, S(dvps), w.dvp, Hkv, T, w.counters);
-  return launch_precond_bwd<D>(k, ks, f, dk, dks, dv, dvs, w, nullptr, B, Hkv, T, scale, st);
+  return launch_precond_bwd<D>(k, ks, f, dk, dks, dv, dvs, w, nullptr, B, Hkv, T, scale, dn, st);
 }
 
 // ---- fp32 inputs (head dim 64) ----
@@ -425,7 +434,8 @@ int launch_centered_keys(const void* k, const int64_t* ks, const FwdWs& w, int B
 
 // V' = P^-1 V from fp32 K and V (K split into w.kh / w.kl).
 int launch_precond_fwd_f32(const void* k, const int64_t* ks, const void* v, const int64_t* vs, float* vprime,
-                           const FwdWs& w, int B, int Hkv, int T, float scale, float eps, hipStream_t st) {
+                           const FwdWs& w, int B, int Hkv, int T, float scale, float eps, float dn,
+                           hipStream_t st) {
   constexpr int D = kF32D;
   const int BH = B * Hkv;
   const lucid::Strides ck = rows_strides(Hkv, T, D);
@@ -435,7 +445,7 @@ int launch_precond_fwd_f32(const void* k, const int64_t* ks, const void* v, cons
   lo.kt = w.ktl;
   lo.v = static_cast<const float*>(v);
   LUCID_LAUNCH("lucid_prep_f32_kernel", (lucid::lucid_prep_kernel<D, true>), dim3(T / 64, BH), st, w.kh, ck, Hkv,
-               T, eps, scale, w.rinv, w.kt, w.pinv, w.counters, w.mass, kForceExact, lo, w.ktl);
+               T, eps, dn, scale, w.rinv, w.kt, w.pinv, w.counters, w.mass, kForceExact, lo, w.ktl);
   LUCID_LAUNCH("lucid_zx_f32_kernel", (lucid::lucid_zx_kernel<D, true>), dim3(T / 128, BH), st, w.kh, ck, Hkv, T,
                w.rinv, scale, w.pinv, w.zx, lo);
   // the chain reads V as fp32 through lo.v with V's own strides (its bf16 operand is unused)
@@ -463,8 +473,8 @@ int launch_attn_fwd_f32(const void* q, const int64_t* qs, void* o, const int64_t
 
 int launch_fwd_f32(const void* q, const int64_t* qs, const void* k, const int64_t* ks, const void* v,
                    const int64_t* vs, void* o, const int64_t* os, float* vprime, float* lse, const FwdWs& w, int B,
-                   int Hq, int Hkv, int T, float scale, float eps, hipStream_t st) {
-  if (int rc = launch_precond_fwd_f32(k, ks, v, vs, vprime, w, B, Hkv, T, scale, eps, st)) return rc;
+                   int Hq, int Hkv, int T, float scale, float eps, float dn, hipStream_t st) {
+  if (int rc = launch_precond_fwd_f32(k, ks, v, vs, vprime, w, B, Hkv, T, scale, eps, dn, st)) return rc;
   if (int rc = launch_centered_keys(k, ks, w, B, Hkv, T, st)) return rc;
   return launch_attn_fwd_f32(q, qs, o, os, lse, w, B, Hq, Hkv, T, scale, st);
 }
@@ -500,7 +510,8 @@ int launch_attn_bwd_f32(const void* dout, const int64_t* dos, const void* o, con
 // The preconditioner part: dV = P^-T dV' (w.dvp, counters zeroed), then dK (fp32) with the
 // softmax part dka added (null: none).
 int launch_precond_bwd_f32(const FwdWs& f, void* dk, const int64_t* dks, void* dv, const int64_t* dvs,
-                           const BwdWs& w, const float* dka, int B, int Hkv, int T, float scale, hipStream_t st) {
+                           const BwdWs& w, const float* dka, int B, int Hkv, int T, float scale, float dn,
+                           hipStream_t st) {
   constexpr int D = kF32D;
   const int BH = B * Hkv;
   const lucid::Strides ck = rows_strides(Hkv, T, D);
@@ -511,16 +522,17 @@ int launch_precond_bwd_f32(const FwdWs& f, void* dk, const int64_t* dks, void* d
                dim3((T / 128) * BH), st, f.kh, ck, Hkv, T, BH, f.rinv, scale, f.kt, f.vpb, f.vpbl, f.pinv, f.mass,
                w.dvp, w.dvb, w.dvbl, (float*)dv, S(dvs), w.colsum, w.counters, lo);
   LUCID_LAUNCH("lucid_precond_bwd_row_f32_kernel", (lucid::lucid_precond_bwd_row_kernel<D, true, true>),
-               dim3(((T + 255) / 256) * BH), st, f.kh, ck, Hkv, T, BH, f.rinv, scale, f.vpb, f.vpbl, w.dvb, w.dvbl,
+               dim3(((T + 255) / 256) * BH), st, f.kh, ck, Hkv, T, BH, f.rinv, scale, dn, f.vpb, f.vpbl, w.dvb, w.dvbl,
                f.mass, w.colsum, dka, (float*)dk, S(dks), lo);
   return LUCID_OK;
 }
 
 int launch_bwd_f32(const void* dout, const int64_t* dos, const void* o, const int64_t* os, const float* lse,
                    const FwdWs& f, void* dq, const int64_t* dqs, void* dk, const int64_t* dks, void* dv,
-                   const int64_t* dvs, const BwdWs& w, int B, int Hq, int Hkv, int T, float scale, hipStream_t st) {
+                   const int64_t* dvs, const BwdWs& w, int B, int Hq, int Hkv, int T, float scale, float dn,
+                   hipStream_t st) {
   if (int rc = launch_attn_bwd_f32(dout, dos, o, os, lse, f, dq, dqs, w, B, Hq, Hkv, T, scale, st)) return rc;
-  return launch_precond_bwd_f32(f, dk, dks, dv, dvs, w, w.dka, B, Hkv, T, scale, st);
+  return launch_precond_bwd_f32(f, dk, dks, dv, dvs, w, w.dka, B, Hkv, T, scale, dn, st);
 }
 
 // eager_lucid_attention_forward on fp32 Q, K and V': the centred keys, the V' pair and
@@ -528,12 +540,12 @@ int launch_bwd_f32(const void* dout, const int64_t* dos, const void* o, const in
 // which the forced precision skips, comes from the centred keys).
 int launch_attn_vp_fwd_f32(const void* q, const int64_t* qs, const void* k, const int64_t* ks, const void* vp,
                            const int64_t* vs, void* o, const int64_t* os, float* lse, const FwdWs& w, int B, int Hq,
-                           int Hkv, int T, float eps, float scale, hipStream_t st) {
+                           int Hkv, int T, float eps, float scale, float dn, hipStream_t st) {
   constexpr int D = kF32D;
   const int BH = B * Hkv;
   if (int rc = launch_centered_keys(k, ks, w, B, Hkv, T, st)) return rc;
   LUCID_LAUNCH("lucid_vp_layout_f32_kernel", (lucid::lucid_vp_layout_kernel<D, float, true>), dim3(T / 64, BH), st,
-               w.kch, rows_strides(Hkv, T, D), (const float*)vp, S(vs), Hkv, T, eps, w.rinv, w.vpb, w.vpt, w.mass,
+               w.kch, rows_strides(Hkv, T, D), (const float*)vp, S(vs), Hkv, T, eps, dn, w.rinv, w.vpb, w.vpt, w.mass,
                kForceExact, w.vpbl, w.vptl);
   return launch_attn_fwd_f32(q, qs, o, os, lse, w, B, Hq, Hkv, T, scale, st);
 }
@@ -555,11 +567,11 @@ int launch_attn_vp_bwd_f32(const void* dout, const int64_t* dos, const void* o, 
 // Gradient of get_v_prime on fp32 inputs: dV' (fp32, strided) in, fp32 dK and dV out.
 int launch_precond_only_bwd_f32(const void* dvp, const int64_t* dvps, const FwdWs& f, void* dk, const int64_t* dks,
                                 void* dv, const int64_t* dvs, const BwdWs& w, int B, int Hkv, int T, float scale,
-                                hipStream_t st) {
+                                float dn, hipStream_t st) {
   constexpr int D = kF32D;
   LUCID_LAUNCH("lucid_rows_in_kernel", (lucid::lucid_rows_in_kernel<D, float>), dim3(T / 64, B * Hkv), st,
                (const float*)dvp, S(dvps), w.dvp, Hkv, T, w.counters);
-  return launch_precond_bwd_f32(f, dk, dks, dv, dvs, w, nullptr, B, Hkv, T, scale, st);
+  return launch_precond_bwd_f32(f, dk, dks, dv, dvs, w, nullptr, B, Hkv, T, scale, dn, st);
 }
 
 // Decoding: split the cached sequence so that one resident round of split workgroups
@@ -568,12 +580,13 @@ int launch_precond_only_bwd_f32(const void* dvp, const int64_t* dvps, const FwdW
 // workspace sized for the capacity covers every call.
 int decode_splits(int BH, int Tp, int D) {
   if (Tp <= 0) return 0;
-  const int wgs = D == 128 ? 512 : 1024;
+  const int wgs = padded_dim(D) == 128 ? 512 : 1024;
   const int want = (wgs + BH - 1) / BH, most = (Tp + 63) / 64;
   return want < most ? want : most;
 }
 
 lucid::DecodePartials carve_decode(void* base, int BH, int G, int nsplit, int D, size_t* bytes) {
+  D = padded_dim(D);
   lucid::DecodePartials w{};
   size_t off = 0;
   char* p = static_cast<char*>(base);
@@ -595,18 +608,18 @@ template <int D, int G>
 int launch_decode(const void* q, const int64_t* qs, const void* k, const int64_t* ks, const void* v,
                   const int64_t* vs, void* kc, const int64_t* kcs, void* vc, const int64_t* vcs, void* o,
                   const int64_t* os, float* vp_new, const lucid::DecodePartials& part, int B, int Hkv, int Tp,
-                  float scale, float eps, hipStream_t st) {
+                  float scale, float eps, float dn, hipStream_t st) {
   const int BH = B * Hkv;
   const int ns = decode_splits(BH, Tp, D);
   if (ns > 0) {
     const int KS = (Tp + ns - 1) / ns;
     LUCID_LAUNCH("lucid_decode_split_kernel", (lucid::lucid_decode_split_kernel<D, G>), dim3(ns, BH), st,
                  (const bf16*)q, S(qs), (const bf16*)k, S(ks), (const bf16*)kc, S(kcs), (const bf16*)vc, S(vcs), Hkv,
-                 Tp, KS, scale, eps, part);
+                 Tp, KS, scale, eps, dn, part);
   }
   LUCID_LAUNCH("lucid_decode_combine_kernel", (lucid::lucid_decode_combine_kernel<D, G>), dim3(BH, G), st, ns,
                (const bf16*)q, S(qs), (const bf16*)k, S(ks), (const bf16*)v, S(vs), (bf16*)kc, S(kcs), (bf16*)vc,
-               S(vcs), (bf16*)o, S(os), vp_new, Hkv, Tp, scale, eps, part);
+               S(vcs), (bf16*)o, S(os), vp_new, Hkv, Tp, scale, eps, dn, part);
   return LUCID_OK;
 }
 
@@ -614,12 +627,12 @@ template <int D>
 int decode_dispatch_g(int G, const void* q, const int64_t* qs, const void* k, const int64_t* ks, const void* v,
                       const int64_t* vs, void* kc, const int64_t* kcs, void* vc, const int64_t* vcs, void* o,
                       const int64_t* os, float* vp_new, const lucid::DecodePartials& part, int B, int Hkv, int Tp,
-                      float scale, float eps, hipStream_t st) {
+                      float scale, float eps, float dn, hipStream_t st) {
   switch (G) {
-    case 1: return launch_decode<D, 1>(q, qs, k, ks, v, vs, kc, kcs, vc, vcs, o, os, vp_new, part, B, Hkv, Tp, scale, eps, st);
-    case 2: return launch_decode<D, 2>(q, qs, k, ks, v, vs, kc, kcs, vc, vcs, o, os, vp_new, part, B, Hkv, Tp, scale, eps, st);
-    case 4: return launch_decode<D, 4>(q, qs, k, ks, v, vs, kc, kcs, vc, vcs, o, os, vp_new, part, B, Hkv, Tp, scale, eps, st);
-    case 8: return launch_decode<D, 8>(q, qs, k, ks, v, vs, kc, kcs, vc, vcs, o, os, vp_new, part, B, Hkv, Tp, scale, eps, st);
+    case 1: return launch_decode<D, 1>(q, qs, k, ks, v, vs, kc, kcs, vc, vcs, o, os, vp_new, part, B, Hkv, Tp, scale, eps, dn, st);
+    case 2: return launch_decode<D, 2>(q, qs, k, ks, v, vs, kc, kcs, vc, vcs, o, os, vp_new, part, B, Hkv, Tp, scale, eps, dn, st);
+    case 4: return launch_decode<D, 4>(q, qs, k, ks, v, vs, kc, kcs, vc, vcs, o, os, vp_new, part, B, Hkv, Tp, scale, eps, dn, st);
+    case 8: return launch_decode<D, 8>(q, qs, k, ks, v, vs, kc, kcs, vc, vcs, o, os, vp_new, part, B, Hkv, Tp, scale, eps, dn, st);
     default: return fail("decode supports Hq / Hkv in {1, 2, 4, 8}, got " + std::to_string(G));
   }
 }
@@ -629,7 +642,7 @@ int check_decode_args(const void* q, const int64_t* qs, const void* k, const int
                       const void* o, const int64_t* os, const float* vp_new, int B, int Hq, int Hkv, int T_past,
                       int T_cap, int D) {
   if (B <= 0 || Hq <= 0 || Hkv <= 0) return fail("B, Hq and Hkv must be positive");
-  if (D != 64 && D != 128) return fail("head_dim must be 64 or 128, got " + std::to_string(D));
+  if (D < 1 || D > 128) return fail("head_dim must be in [1, 128], got " + std::to_string(D));
   if (Hq % Hkv != 0) return fail("Hq must be a multiple of Hkv");
   if (T_past < 0 || T_past >= T_cap) return fail("the cache is full: T_past must be in [0, T_cap)");
   if (int rc = check_tensor("q", q, qs)) return rc;
@@ -686,13 +699,13 @@ int decode_impl(const void* q, const int64_t* q_strides, const void* k, const in
   const lucid::DecodePartials part =
       carve_decode(ws, B * Hkv, Hq / Hkv, decode_splits(B * Hkv, T_past, D), D, nullptr);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (D == 64)
+  if (padded_dim(D) == 64)
     return decode_dispatch_g<64>(Hq / Hkv, q, q_strides, k, k_strides, v, v_strides, k_cache, k_cache_strides,
                                  vp_cache, vp_cache_strides, o, o_strides, vp_new, part, B, Hkv, T_past, scale, eps,
-                                 st);
+                                 (float)D, st);
   return decode_dispatch_g<128>(Hq / Hkv, q, q_strides, k, k_strides, v, v_strides, k_cache, k_cache_strides,
                                 vp_cache, vp_cache_strides, o, o_strides, vp_new, part, B, Hkv, T_past, scale, eps,
-                                st);
+                                (float)D, st);
 }
 
 }  // namespace
@@ -792,8 +805,8 @@ int lucid_get_v_prime(const void* k, const int64_t* k_strides, const void* v, co
   if (int rc = chain_check()) return rc;
   const FwdWs w = carve_fwd(fwd_ws, B, Hkv, Hkv, T, D);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (D == 64) return launch_precond_fwd<64>(k, k_strides, v, v_strides, vprime, w, B, Hkv, T, scale, eps, st);
-  return launch_precond_fwd<128>(k, k_strides, v, v_strides, vprime, w, B, Hkv, T, scale, eps, st);
+  if (padded_dim(D) == 64) return launch_precond_fwd<64>(k, k_strides, v, v_strides, vprime, w, B, Hkv, T, scale, eps, (float)D, st);
+  return launch_precond_fwd<128>(k, k_strides, v, v_strides, vprime, w, B, Hkv, T, scale, eps, (float)D, st);
 }
 
 int lucid_attn_fwd(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
@@ -811,11 +824,11 @@ int lucid_attn_fwd(const void* q, const int64_t* q_strides, const void* k, const
   if (int rc = chain_check()) return rc;
   const FwdWs w = carve_fwd(fwd_ws, B, Hq, Hkv, T, D);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (D == 64)
+  if (padded_dim(D) == 64)
     return launch_fwd<64>(q, q_strides, k, k_strides, v, v_strides, o, o_strides, vprime, lse, w, B, Hq, Hkv, T,
-                          scale, eps, st);
+                          scale, eps, (float)D, st);
   return launch_fwd<128>(q, q_strides, k, k_strides, v, v_strides, o, o_strides, vprime, lse, w, B, Hq, Hkv, T,
-                         scale, eps, st);
+                         scale, eps, (float)D, st);
 }
 
 int lucid_attn_bwd(const void* dout, const int64_t* do_strides, const void* q, const int64_t* q_strides,
@@ -840,11 +853,11 @@ int lucid_attn_bwd(const void* dout, const int64_t* do_strides, const void* q, c
   const FwdWs f = carve_fwd(const_cast<void*>(fwd_ws), B, Hq, Hkv, T, D);
   const BwdWs w = carve_bwd(bwd_ws, B, Hq, Hkv, T, D);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (D == 64)
+  if (padded_dim(D) == 64)
     return launch_bwd<64>(dout, do_strides, q, q_strides, k, k_strides, o, o_strides, lse, f, dq, dq_strides, dk,
-                          dk_strides, dv, dv_strides, w, B, Hq, Hkv, T, scale, st);
+                          dk_strides, dv, dv_strides, w, B, Hq, Hkv, T, scale, (float)D, st);
   return launch_bwd<128>(dout, do_strides, q, q_strides, k, k_strides, o, o_strides, lse, f, dq, dq_strides, dk,
-                         dk_strides, dv, dv_strides, w, B, Hq, Hkv, T, scale, st);
+                         dk_strides, dv, dv_strides, w, B, Hq, Hkv, T, scale, (float)D, st);
 }
 
 size_t lucid_fwd_f32_workspace_bytes(int B, int Hq, int Hkv, int T, int D) {
@@ -861,7 +874,7 @@ int lucid_attn_fwd_f32(const float* q, const int64_t* q_strides, const float* k,
                        void* stream) {
   g_last_error.clear();
   if (int rc = check_dims(B, Hq, Hkv, T, D)) return rc;
-  if (D != 64) return fail("fp32 inputs are supported at head_dim 64, got " + std::to_string(D));
+  if (padded_dim(D) != kF32D) return fail("fp32 inputs are supported at head_dim <= 64, got " + std::to_string(D));
   if (int rc = check_tensor("q", q, q_strides)) return rc;
   if (int rc = check_tensor("k", k, k_strides)) return rc;
   if (int rc = check_tensor("v", v, v_strides)) return rc;
@@ -871,7 +884,7 @@ int lucid_attn_fwd_f32(const float* q, const int64_t* q_strides, const float* k,
   if (int rc = chain_check()) return rc;
   const FwdWs w = carve_fwd(fwd_ws, B, Hq, Hkv, T, D, true);
   return launch_fwd_f32(q, q_strides, k, k_strides, v, v_strides, o, o_strides, vprime, lse, w, B, Hq, Hkv, T,
-                        scale, eps, static_cast<hipStream_t>(stream));
+                        scale, eps, (float)D, static_cast<hipStream_t>(stream));
 }
 
 int lucid_attn_bwd_f32(const float* dout, const int64_t* do_strides, const float* o, const int64_t* o_strides,
@@ -880,7 +893,7 @@ int lucid_attn_bwd_f32(const float* dout, const int64_t* do_strides, const float
                        int Hkv, int T, int D, float scale, void* stream) {
   g_last_error.clear();
   if (int rc = check_dims(B, Hq, Hkv, T, D)) return rc;
-  if (D != 64) return fail("fp32 inputs are supported at head_dim 64, got " + std::to_string(D));
+  if (padded_dim(D) != kF32D) return fail("fp32 inputs are supported at head_dim <= 64, got " + std::to_string(D));
   if (int rc = check_tensor("dout", dout, do_strides)) return rc;
   if (int rc = check_tensor("o", o, o_strides)) return rc;
   if (int rc = check_tensor("dq", dq, dq_strides)) return rc;
@@ -893,7 +906,7 @@ int lucid_attn_bwd_f32(const float* dout, const int64_t* do_strides, const float
   const FwdWs f = carve_fwd(const_cast<void*>(fwd_ws), B, Hq, Hkv, T, D, true);
   const BwdWs w = carve_bwd(bwd_ws, B, Hq, Hkv, T, D, true);
   return launch_bwd_f32(dout, do_strides, o, o_strides, lse, f, dq, dq_strides, dk, dk_strides, dv, dv_strides, w,
-                        B, Hq, Hkv, T, scale, static_cast<hipStream_t>(stream));
+                        B, Hq, Hkv, T, scale, (float)D, static_cast<hipStream_t>(stream));
 }
 
 size_t lucid_v_prime_f32_workspace_bytes(int B, int Hkv, int T, int D) {
@@ -905,7 +918,7 @@ int lucid_get_v_prime_f32(const float* k, const int64_t* k_strides, const float*
                           void* stream) {
   g_last_error.clear();
   if (int rc = check_dims(B, Hkv, Hkv, T, D)) return rc;
-  if (D != kF32D) return fail("fp32 inputs are supported at head_dim 64, got " + std::to_string(D));
+  if (padded_dim(D) != kF32D) return fail("fp32 inputs are supported at head_dim <= 64, got " + std::to_string(D));
   if (int rc = check_tensor("k", k, k_strides)) return rc;
   if (int rc = check_tensor("v", v, v_strides)) return rc;
   if (!vprime || !fwd_ws) return fail("vprime and fwd_ws must be non-null");
@@ -913,7 +926,7 @@ int lucid_get_v_prime_f32(const float* k, const int64_t* k_strides, const float*
   if (int rc = chain_check()) return rc;
   const FwdWs w = carve_fwd(fwd_ws, B, Hkv, Hkv, T, D, true, false);
   return launch_precond_fwd_f32(k, k_strides, v, v_strides, vprime, w, B, Hkv, T, scale, eps,
-                                static_cast<hipStream_t>(stream));
+                                (float)D, static_cast<hipStream_t>(stream));
 }
 
 int lucid_precond_bwd_f32(const float* dvprime, const int64_t* dvprime_strides, const void* fwd_ws, float* dk,
@@ -921,7 +934,7 @@ int lucid_precond_bwd_f32(const float* dvprime, const int64_t* dvprime_strides, 
                           int Hkv, int T, int D, float scale, void* stream) {
   g_last_error.clear();
   if (int rc = check_dims(B, Hkv, Hkv, T, D)) return rc;
-  if (D != kF32D) return fail("fp32 inputs are supported at head_dim 64, got " + std::to_string(D));
+  if (padded_dim(D) != kF32D) return fail("fp32 inputs are supported at head_dim <= 64, got " + std::to_string(D));
   if (int rc = check_tensor("dvprime", dvprime, dvprime_strides)) return rc;
   if (int rc = check_tensor("dk", dk, dk_strides)) return rc;
   if (int rc = check_tensor("dv", dv, dv_strides)) return rc;
@@ -932,7 +945,7 @@ int lucid_precond_bwd_f32(const float* dvprime, const int64_t* dvprime_strides, 
   const FwdWs f = carve_fwd(const_cast<void*>(fwd_ws), B, Hkv, Hkv, T, D, true, false);
   const BwdWs w = carve_seam_bwd(bwd_ws, B, Hkv, Hkv, T, D, false);
   return launch_precond_only_bwd_f32(dvprime, dvprime_strides, f, dk, dk_strides, dv, dv_strides, w, B, Hkv, T,
-                                     scale, static_cast<hipStream_t>(stream));
+                                     scale, (float)D, static_cast<hipStream_t>(stream));
 }
 
 size_t lucid_attn_vp_fwd_f32_workspace_bytes(int B, int Hq, int Hkv, int T, int D) {
@@ -945,7 +958,7 @@ int lucid_attn_vp_fwd_f32(const float* q, const int64_t* q_strides, const float*
                           void* stream) {
   g_last_error.clear();
   if (int rc = check_dims(B, Hq, Hkv, T, D)) return rc;
-  if (D != kF32D) return fail("fp32 inputs are supported at head_dim 64, got " + std::to_string(D));
+  if (padded_dim(D) != kF32D) return fail("fp32 inputs are supported at head_dim <= 64, got " + std::to_string(D));
   if (int rc = check_tensor("q", q, q_strides)) return rc;
   if (int rc = check_tensor("k", k, k_strides)) return rc;
   if (int rc = check_tensor("vprime", vprime, vprime_strides)) return rc;
@@ -954,7 +967,7 @@ int lucid_attn_vp_fwd_f32(const float* q, const int64_t* q_strides, const float*
   if (int rc = check_ws("ws", ws)) return rc;
   const FwdWs w = carve_attn_vp(ws, B, Hq, Hkv, T, D, true);
   return launch_attn_vp_fwd_f32(q, q_strides, k, k_strides, vprime, vprime_strides, o, o_strides, lse, w, B, Hq, Hkv,
-                                T, eps, scale, static_cast<hipStream_t>(stream));
+                                T, eps, scale, (float)D, static_cast<hipStream_t>(stream));
 }
 
 size_t lucid_attn_vp_bwd_f32_workspace_bytes(int B, int Hq, int Hkv, int T, int D) {
@@ -967,7 +980,7 @@ int lucid_attn_vp_bwd_f32(const float* dout, const int64_t* do_strides, const fl
                           int B, int Hq, int Hkv, int T, int D, float scale, void* stream) {
   g_last_error.clear();
   if (int rc = check_dims(B, Hq, Hkv, T, D)) return rc;
-  if (D != kF32D) return fail("fp32 inputs are supported at head_dim 64, got " + std::to_string(D));
+  if (padded_dim(D) != kF32D) return fail("fp32 inputs are supported at head_dim <= 64, got " + std::to_string(D));
   if (int rc = check_tensor("dout", dout, do_strides)) return rc;
   if (int rc = check_tensor("o", o, o_strides)) return rc;
   if (int rc = check_tensor("dq", dq, dq_strides)) return rc;
@@ -1000,11 +1013,11 @@ int lucid_attn_vp_fwd(const void* q, const int64_t* q_strides, const void* k, co
   if (int rc = check_ws("ws", ws)) return rc;
   const FwdWs w = carve_attn_vp(ws, B, Hq, Hkv, T, D);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (D == 64)
+  if (padded_dim(D) == 64)
     return launch_attn_vp_fwd<64>(q, q_strides, k, k_strides, vprime, vprime_strides, vprime_f32, o, o_strides, lse,
-                                  w, B, Hq, Hkv, T, scale, eps, st);
+                                  w, B, Hq, Hkv, T, scale, eps, (float)D, st);
   return launch_attn_vp_fwd<128>(q, q_strides, k, k_strides, vprime, vprime_strides, vprime_f32, o, o_strides, lse,
-                                 w, B, Hq, Hkv, T, scale, eps, st);
+                                 w, B, Hq, Hkv, T, scale, eps, (float)D, st);
 }
 
 size_t lucid_attn_vp_bwd_workspace_bytes(int B, int Hq, int Hkv, int T, int D) {
@@ -1031,7 +1044,7 @@ int lucid_attn_vp_bwd(const void* dout, const int64_t* do_strides, const void* q
   const FwdWs f = carve_attn_vp(const_cast<void*>(fwd_ws), B, Hq, Hkv, T, D);
   const BwdWs w = carve_seam_bwd(bwd_ws, B, Hq, Hkv, T, D, true);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (D == 64)
+  if (padded_dim(D) == 64)
     return launch_attn_vp_bwd<64>(dout, do_strides, q, q_strides, k, k_strides, o, o_strides, lse, f, dq,
                                   dq_strides, dk, dk_strides, dvprime, dvprime_strides, dvprime_f32, w, B, Hq, Hkv,
                                   T, scale, st);
@@ -1060,11 +1073,11 @@ int lucid_precond_bwd(const void* k, const int64_t* k_strides, const void* dvpri
   const FwdWs f = carve_fwd(const_cast<void*>(fwd_ws), B, Hkv, Hkv, T, D);
   const BwdWs w = carve_seam_bwd(bwd_ws, B, Hkv, Hkv, T, D, false);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (D == 64)
+  if (padded_dim(D) == 64)
     return launch_precond_only_bwd<64>(k, k_strides, dvprime, dvprime_strides, dvprime_f32, f, dk, dk_strides, dv,
-                                       dv_strides, w, B, Hkv, T, scale, st);
+                                       dv_strides, w, B, Hkv, T, scale, (float)D, st);
   return launch_precond_only_bwd<128>(k, k_strides, dvprime, dvprime_strides, dvprime_f32, f, dk, dk_strides, dv,
-                                      dv_strides, w, B, Hkv, T, scale, st);
+                                      dv_strides, w, B, Hkv, T, scale, (float)D, st);
 }
 
 void lucid_profile_enable(int on) { lucid_prof::enabled() = on != 0; }

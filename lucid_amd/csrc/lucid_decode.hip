@@ -3,7 +3,8 @@
 // the reference seam; its V' update drops the division by the diagonal P_tt, kept
 // here so that a decoded row equals the same row of a prefill):
 //   P_tj = exp(s r_t r_j (k_t . k_j) - 1/s),  r = 1 / rms(k)  (j < t)
-//   v'_t = (v_t - sum_{j<t} P_tj v'_j) / P_tt,  P_tt = exp(s d ms_t / (ms_t + eps) - 1/s)
+//   v'_t = (v_t - sum_{j<t} P_tj v'_j) / P_tt,  P_tt = exp(s dn ms_t / (ms_t + eps) - 1/s)
+// (dn: the head dim; rows may be zero-padded beyond it, ms = sum k^2 / dn)
 //   o_g  = softmax_j(s q_g . k_j) v'_j over j <= t, for the G query heads of the kv head
 // Both sums read every cached row once (memory bound), so one pass over the cache
 // computes them together, split over the sequence (flash-decoding):
@@ -52,7 +53,7 @@ template <int D, int G>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void lucid_decode_split_kernel(
     const bf16* __restrict__ q, Strides qs, const bf16* __restrict__ kn, Strides kns,
     const bf16* __restrict__ kc, Strides kcs, const bf16* __restrict__ vc, Strides vcs, int Hkv, int Tp, int KS,
-    float scale, float eps, DecodePartials part) {
+    float scale, float eps, float dn, DecodePartials part) {
   constexpr int NKS = D / 16, NDT = D / 32, CPR = D / 8, NST = 32 * CPR / 64;  // NST: staging loads per tile
   static_assert(G + 1 <= 32, "query heads + the preconditioner row must fit one 32-column tile");
   __shared__ __attribute__((aligned(16))) DecodeMfmaSmem<D, G> sm;
@@ -81,7 +82,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void l
     xb[st] = x;
   }
   nt = wave_sum32(nt);
-  const float rt = rsqrtf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, nt), G)) / D + eps);
+  const float rt = rsqrtf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, nt), G)) / dn + eps);
   const float sl2 = scale * LOG2E_F, c1 = sl2 * rt, c0 = LOG2E_F / scale;
 
   f32x16 oacc[NDT];
@@ -151,7 +152,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void l
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       const bool ok = jb + drow(e, g) < j1 && col <= G;
-      const float arg = (col < G) ? fmaf(sc[e], sl2, -m) : fmaf(c1 * rsqrtf(nr[e] / D + eps), sc[e], -c0);
+      const float arg = (col < G) ? fmaf(sc[e], sl2, -m) : fmaf(c1 * rsqrtf(nr[e] / dn + eps), sc[e], -c0);
       const float p = ok ? __builtin_amdgcn_exp2f(arg) : 0.f;
       if (col < G) l += p;
       sc[e] = p;
@@ -218,7 +219,7 @@ template <int D, int G>
 __global__ __launch_bounds__(256) void lucid_decode_combine_kernel(
     int nsplit, const bf16* __restrict__ q, Strides qs, const bf16* __restrict__ kn, Strides kns,
     const bf16* __restrict__ vn, Strides vns, bf16* __restrict__ kc, Strides kcs, bf16* __restrict__ vc, Strides vcs,
-    bf16* __restrict__ o, Strides os, float* __restrict__ vp_new, int Hkv, int Tp, float scale, float eps,
+    bf16* __restrict__ o, Strides os, float* __restrict__ vp_new, int Hkv, int Tp, float scale, float eps, float dn,
     DecodePartials part) {
   constexpr int NSL = 256 / D;
   __shared__ float ra[NSL][D], ro[NSL][D], rm[NSL], rl[NSL], dots[2][D];
@@ -267,9 +268,9 @@ __global__ __launch_bounds__(256) void lucid_decode_combine_kernel(
   lt = 0.f;
 #pragma unroll
   for (int i = 0; i < NSL; ++i) lt += rl[i];
-  const float ms = nk / D;
-  // P_tt = exp(s |K^_t|^2 - 1/s), |K^_t|^2 = D ms / (ms + eps)
-  const float ptt = __builtin_amdgcn_exp2f(LOG2E_F * (scale * D * ms / (ms + eps) - 1.f / scale));
+  const float ms = nk / dn;
+  // P_tt = exp(s |K^_t|^2 - 1/s), |K^_t|^2 = dn ms / (ms + eps)
+  const float ptt = __builtin_amdgcn_exp2f(LOG2E_F * (scale * dn * ms / (ms + eps) - 1.f / scale));
   const float vpt = ((float)vn[b * vns.b + h * vns.h + d] - a) / ptt;
   const bf16 vpb = (bf16)vpt;
   if (g == 0) {

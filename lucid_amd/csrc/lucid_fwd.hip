@@ -20,7 +20,7 @@
 namespace lucid {
 
 // ---------------------------------------------------------------------------
-// prep: rinv[bh][t] = 1/sqrt(mean K^2 + eps); kt[bh][d][perm(t)] = K[t][d];
+// prep: rinv[bh][t] = 1/sqrt(sum K^2 / dn + eps) (dn: the head dim, rows zero-padded beyond it); kt[bh][d][perm(t)] = K[t][d];
 // pinv[bh][blk] = inverse of the 64x64 diagonal block of P (fp32 forward
 // substitution by wave 0); zero the chain counter and set the head's row mass
 // to mass_init (0 before lucid_mass_kernel; a forced precision sets it directly).
@@ -28,7 +28,7 @@ namespace lucid {
 // ---------------------------------------------------------------------------
 template <int D, bool F32 = false>
 __global__ __launch_bounds__(256) void lucid_prep_kernel(const bf16* __restrict__ k, Strides ks, int Hkv, int T,
-                                                         float eps, float scale, float* __restrict__ rinv,
+                                                         float eps, float dn, float scale, float* __restrict__ rinv,
                                                          bf16* __restrict__ kt, float* __restrict__ pinv,
                                                          int* __restrict__ counters, float* __restrict__ mass,
                                                          float mass_init, Lo lo, bf16* __restrict__ ktl) {
@@ -64,7 +64,7 @@ __global__ __launch_bounds__(256) void lucid_prep_kernel(const bf16* __restrict_
   ss += __shfl_xor(ss, 1, 64);
   ss += __shfl_xor(ss, 2, 64);
   if (seg == 0) {
-    const float ri = 1.0f / sqrtf(ss / (float)D + eps);
+    const float ri = 1.0f / sqrtf(ss / dn + eps);
     rinv[(int64_t)bh * T + blk * 64 + row] = ri;
     rr[row] = ri;
   }
@@ -126,7 +126,7 @@ __global__ __launch_bounds__(256) void lucid_prep_kernel(const bf16* __restrict_
 template <int D, typename VT, bool LO = false>
 __global__ __launch_bounds__(256) void lucid_vp_layout_kernel(const bf16* __restrict__ k, Strides ks,
                                                               const VT* __restrict__ vp, Strides vs, int Hkv, int T,
-                                                              float eps, float* __restrict__ rinv,
+                                                              float eps, float dn, float* __restrict__ rinv,
                                                               bf16* __restrict__ vpb, bf16* __restrict__ vpt,
                                                               float* __restrict__ mass, float mass_init,
                                                               bf16* __restrict__ vpbl, bf16* __restrict__ vptl) {
@@ -163,7 +163,7 @@ __global__ __launch_bounds__(256) void lucid_vp_layout_kernel(const bf16* __rest
   }
   ss += __shfl_xor(ss, 1, 64);
   ss += __shfl_xor(ss, 2, 64);
-  if (seg == 0) rinv[(int64_t)bh * T + t] = 1.0f / sqrtf(ss / (float)D + eps);
+  if (seg == 0) rinv[(int64_t)bh * T + t] = 1.0f / sqrtf(ss / dn + eps);
   if (blk == 0 && tid == 0) mass[bh] = mass_init;
   __syncthreads();
   for (int idx = tid; idx < D * 8; idx += 256) {

@@ -13,10 +13,12 @@ Python mirror of the reference operator seams in ``modeling_lucid.py``:
 Layouts follow the reference: ``query [B, Hq, T, d]``, ``key/value [B, Hkv, T, d]``
 (any strides with a contiguous last axis, e.g. the ``.view(...).transpose(1, 2)``
 views LucidAttention builds), output ``[B, T, Hq, d]``.  Inputs must be bf16
-CUDA(HIP) tensors with d in {64, 128}, or fp32 tensors with d = 64 (computed on bf16
-hi/lo pairs to ~1e-4 relative, fp32 outputs); anything else raises (there is no CPU or
-eager fallback).  T that is not a multiple of 128 is zero-padded at the end,
-which is exact for every real row because P and the attention mask are causal.
+CUDA(HIP) tensors with d <= 128, or fp32 tensors with d <= 64 (computed on bf16 hi/lo
+pairs to ~1e-4 relative, fp32 outputs); anything else raises (there is no CPU or eager
+fallback).  T that is not a multiple of 128 is zero-padded at the end, which is exact for
+every real row because P and the attention mask are causal.  Head dims other than 64 and
+128 (the reference model's is 68) run on rows zero-padded to the next of the two, which
+leaves every dot product unchanged; the RMS of k_norm divides by the true d.
 """
 from __future__ import annotations
 
@@ -26,8 +28,17 @@ import torch.nn.functional as F
 from . import _lib
 
 _T_ALIGN = 128
-_SUPPORTED_D = (64, 128)
-_F32_D = 64  # head dim of the fp32-input kernels
+_MAX_D = 128  # head dims up to 128: rows are zero-padded to 64 or 128 columns
+_F32_MAX_D = 64  # the fp32-input kernels run at 64 columns
+
+
+def _padded_dim(d: int) -> int:
+    return 64 if d <= 64 else 128
+
+
+def _pad_d(t: torch.Tensor, dp: int) -> torch.Tensor:
+    """Zero-pad the head axis (last) to ``dp`` columns (differentiable; a no-op at dp)."""
+    return t if t.shape[-1] == dp else F.pad(t, (0, dp - t.shape[-1]))
 
 
 def _check_inputs(q, k, v, f32_ok=False):
@@ -47,10 +58,10 @@ def _check_inputs(q, k, v, f32_ok=False):
     if v is not None and k.shape != v.shape:
         raise ValueError(f"lucid_amd: key {tuple(k.shape)} and value {tuple(v.shape)} must match")
     d = k.shape[-1]
-    if d not in _SUPPORTED_D:
-        raise ValueError(f"lucid_amd: head_dim {d} not supported (supported: {_SUPPORTED_D})")
-    if k.dtype == torch.float32 and d != _F32_D:
-        raise ValueError(f"lucid_amd: fp32 inputs are supported at head_dim {_F32_D}, got {d} (use bf16)")
+    if not 1 <= d <= _MAX_D:
+        raise ValueError(f"lucid_amd: head_dim {d} not supported (supported: 1 .. {_MAX_D})")
+    if k.dtype == torch.float32 and d > _F32_MAX_D:
+        raise ValueError(f"lucid_amd: fp32 inputs are supported at head_dim <= {_F32_MAX_D}, got {d} (use bf16)")
     if q is not None:
         if q.shape[0] != k.shape[0] or q.shape[2] != k.shape[2] or q.shape[3] != d:
             raise ValueError("lucid_amd: query/key shapes disagree")
@@ -71,7 +82,7 @@ def _padded_len(t: int) -> int:
     return (t + _T_ALIGN - 1) // _T_ALIGN * _T_ALIGN
 
 
-def _fwd(q, k, v, scale, eps):
+def _fwd(q, k, v, scale, eps, dn):
     lib = _lib.load()
     B, Hq, T, D = q.shape
     Hkv = k.shape[1]
@@ -79,17 +90,17 @@ def _fwd(q, k, v, scale, eps):
     o = torch.empty(B, T, Hq, D, dtype=torch.bfloat16, device=dev)
     vprime = torch.empty(B, Hkv, T, D, dtype=torch.float32, device=dev)
     lse = torch.empty(B, Hq, T, dtype=torch.float32, device=dev)
-    ws = torch.empty(lib.lucid_fwd_workspace_bytes(B, Hq, Hkv, T, D), dtype=torch.uint8, device=dev)
+    ws = torch.empty(lib.lucid_fwd_workspace_bytes(B, Hq, Hkv, T, dn), dtype=torch.uint8, device=dev)
     rc = lib.lucid_attn_fwd(
         _lib.ptr(q), _lib.strides3(q, (0, 1, 2)), _lib.ptr(k), _lib.strides3(k, (0, 1, 2)),
         _lib.ptr(v), _lib.strides3(v, (0, 1, 2)), _lib.ptr(o), _lib.strides3(o, (0, 2, 1)),
-        _lib.ptr(vprime), _lib.ptr(lse), _lib.ptr(ws), B, Hq, Hkv, T, D, float(scale), float(eps),
+        _lib.ptr(vprime), _lib.ptr(lse), _lib.ptr(ws), B, Hq, Hkv, T, dn, float(scale), float(eps),
         _lib.stream_handle(dev))
     _lib.check(lib, rc, "lucid_attn_fwd")
     return o, vprime, lse, ws
 
 
-def _fwd_f32(q, k, v, scale, eps):
+def _fwd_f32(q, k, v, scale, eps, dn):
     lib = _lib.load()
     B, Hq, T, D = q.shape
     Hkv = k.shape[1]
@@ -97,17 +108,17 @@ def _fwd_f32(q, k, v, scale, eps):
     o = torch.empty(B, T, Hq, D, dtype=torch.float32, device=dev)
     vprime = torch.empty(B, Hkv, T, D, dtype=torch.float32, device=dev)
     lse = torch.empty(B, Hq, T, dtype=torch.float32, device=dev)
-    ws = torch.empty(lib.lucid_fwd_f32_workspace_bytes(B, Hq, Hkv, T, D), dtype=torch.uint8, device=dev)
+    ws = torch.empty(lib.lucid_fwd_f32_workspace_bytes(B, Hq, Hkv, T, dn), dtype=torch.uint8, device=dev)
     rc = lib.lucid_attn_fwd_f32(
         _lib.ptr(q), _lib.strides3(q, (0, 1, 2)), _lib.ptr(k), _lib.strides3(k, (0, 1, 2)),
         _lib.ptr(v), _lib.strides3(v, (0, 1, 2)), _lib.ptr(o), _lib.strides3(o, (0, 2, 1)),
-        _lib.ptr(vprime), _lib.ptr(lse), _lib.ptr(ws), B, Hq, Hkv, T, D, float(scale), float(eps),
+        _lib.ptr(vprime), _lib.ptr(lse), _lib.ptr(ws), B, Hq, Hkv, T, dn, float(scale), float(eps),
         _lib.stream_handle(dev))
     _lib.check(lib, rc, "lucid_attn_fwd_f32")
     return o, vprime, lse, ws
 
 
-def _bwd_f32(do, q, k, o, lse, ws, scale):
+def _bwd_f32(do, q, k, o, lse, ws, scale, dn):
     lib = _lib.load()
     B, Hq, T, D = q.shape
     Hkv = k.shape[1]
@@ -115,17 +126,17 @@ def _bwd_f32(do, q, k, o, lse, ws, scale):
     dq = torch.empty(B, Hq, T, D, dtype=torch.float32, device=dev)
     dk = torch.empty(B, Hkv, T, D, dtype=torch.float32, device=dev)
     dv = torch.empty(B, Hkv, T, D, dtype=torch.float32, device=dev)
-    bws = torch.empty(lib.lucid_bwd_f32_workspace_bytes(B, Hq, Hkv, T, D), dtype=torch.uint8, device=dev)
+    bws = torch.empty(lib.lucid_bwd_f32_workspace_bytes(B, Hq, Hkv, T, dn), dtype=torch.uint8, device=dev)
     rc = lib.lucid_attn_bwd_f32(
         _lib.ptr(do), _lib.strides3(do, (0, 2, 1)), _lib.ptr(o), _lib.strides3(o, (0, 2, 1)),
         _lib.ptr(lse), _lib.ptr(ws), _lib.ptr(dq), _lib.strides3(dq, (0, 1, 2)),
         _lib.ptr(dk), _lib.strides3(dk, (0, 1, 2)), _lib.ptr(dv), _lib.strides3(dv, (0, 1, 2)),
-        _lib.ptr(bws), B, Hq, Hkv, T, D, float(scale), _lib.stream_handle(dev))
+        _lib.ptr(bws), B, Hq, Hkv, T, dn, float(scale), _lib.stream_handle(dev))
     _lib.check(lib, rc, "lucid_attn_bwd_f32")
     return dq, dk, dv
 
 
-def _bwd(do, q, k, o, lse, ws, scale, eps):
+def _bwd(do, q, k, o, lse, ws, scale, eps, dn):
     lib = _lib.load()
     B, Hq, T, D = q.shape
     Hkv = k.shape[1]
@@ -133,13 +144,13 @@ def _bwd(do, q, k, o, lse, ws, scale, eps):
     dq = torch.empty(B, Hq, T, D, dtype=torch.bfloat16, device=dev)
     dk = torch.empty(B, Hkv, T, D, dtype=torch.bfloat16, device=dev)
     dv = torch.empty(B, Hkv, T, D, dtype=torch.bfloat16, device=dev)
-    bws = torch.empty(lib.lucid_bwd_workspace_bytes(B, Hq, Hkv, T, D), dtype=torch.uint8, device=dev)
+    bws = torch.empty(lib.lucid_bwd_workspace_bytes(B, Hq, Hkv, T, dn), dtype=torch.uint8, device=dev)
     rc = lib.lucid_attn_bwd(
         _lib.ptr(do), _lib.strides3(do, (0, 2, 1)), _lib.ptr(q), _lib.strides3(q, (0, 1, 2)),
         _lib.ptr(k), _lib.strides3(k, (0, 1, 2)), _lib.ptr(o), _lib.strides3(o, (0, 2, 1)),
         _lib.ptr(lse), _lib.ptr(ws), _lib.ptr(dq), _lib.strides3(dq, (0, 1, 2)),
         _lib.ptr(dk), _lib.strides3(dk, (0, 1, 2)), _lib.ptr(dv), _lib.strides3(dv, (0, 1, 2)),
-        _lib.ptr(bws), B, Hq, Hkv, T, D, float(scale), float(eps), _lib.stream_handle(dev))
+        _lib.ptr(bws), B, Hq, Hkv, T, dn, float(scale), float(eps), _lib.stream_handle(dev))
     _lib.check(lib, rc, "lucid_attn_bwd")
     return dq, dk, dv
 
@@ -152,7 +163,7 @@ class LucidAttentionFunction(torch.autograd.Function):
     """
 
     @staticmethod
-    def forward(ctx, q, k, v, scale, eps):
+    def forward(ctx, q, k, v, scale, eps, dn):
         t = q.shape[2]
         ctx.empty = t == 0 or q.numel() == 0
         ctx.shapes = (q.shape, k.shape)
@@ -163,16 +174,17 @@ class LucidAttentionFunction(torch.autograd.Function):
         tp = _padded_len(t)
         qp, kp, vp_ = _prep(q, tp), _prep(k, tp), _prep(v, tp)
         ctx.f32 = q.dtype == torch.float32
-        o, vprime, lse, ws = (_fwd_f32 if ctx.f32 else _fwd)(qp, kp, vp_, scale, eps)
+        o, vprime, lse, ws = (_fwd_f32 if ctx.f32 else _fwd)(qp, kp, vp_, scale, eps, dn)
         ctx.save_for_backward(qp, kp, o, lse, ws)
-        ctx.scale, ctx.eps, ctx.t = scale, eps, t
+        ctx.scale, ctx.eps, ctx.t, ctx.dn = scale, eps, t, dn
         ctx.mark_non_differentiable(vprime)
         return o[:, :t], vprime[:, :, :t]
 
     @staticmethod
     def backward(ctx, do, _dvprime):
         if ctx.empty:
-            return do.new_zeros(ctx.shapes[0]), do.new_zeros(ctx.shapes[1]), do.new_zeros(ctx.shapes[1]), None, None
+            return (do.new_zeros(ctx.shapes[0]), do.new_zeros(ctx.shapes[1]), do.new_zeros(ctx.shapes[1]),
+                    None, None, None)
         qp, kp, o, lse, ws = ctx.saved_tensors
         t, tp = ctx.t, qp.shape[2]
         dt = torch.float32 if ctx.f32 else torch.bfloat16
@@ -183,10 +195,10 @@ class LucidAttentionFunction(torch.autograd.Function):
         if do.stride(-1) != 1 or any(s % 8 for s in do.stride()) or do.data_ptr() % 16:
             do = do.contiguous()
         if ctx.f32:
-            dq, dk, dv = _bwd_f32(do, qp, kp, o, lse, ws, ctx.scale)
+            dq, dk, dv = _bwd_f32(do, qp, kp, o, lse, ws, ctx.scale, ctx.dn)
         else:
-            dq, dk, dv = _bwd(do, qp, kp, o, lse, ws, ctx.scale, ctx.eps)
-        return dq[:, :, :t], dk[:, :, :t], dv[:, :, :t], None, None
+            dq, dk, dv = _bwd(do, qp, kp, o, lse, ws, ctx.scale, ctx.eps, ctx.dn)
+        return dq[:, :, :t], dk[:, :, :t], dv[:, :, :t], None, None, None
 
 
 _PRECISIONS = {"auto": 0, "fast": 1, "exact": 2}
@@ -224,11 +236,16 @@ def lucid_attention(query, key, value, scaling=None, eps=1e-5, return_vprime=Fal
     """LUCID attention: ``softmax(s Q K^T, causal) P^-1 V``; returns O ``[B, T, Hq, d]``.
 
     ``eps`` is the k_norm epsilon (``config.rms_norm_eps``, modeling_lucid.py:409).
-    bf16 inputs give bf16 O; fp32 inputs (head dim 64) give fp32 O and gradients.
+    bf16 inputs give bf16 O; fp32 inputs (head dim <= 64) give fp32 O and gradients.
     """
     _check_inputs(query, key, value, f32_ok=True)
-    scale = query.shape[-1] ** -0.5 if scaling is None else float(scaling)
-    o, vprime = LucidAttentionFunction.apply(query, key, value, scale, eps)
+    d = query.shape[-1]
+    scale = d ** -0.5 if scaling is None else float(scaling)
+    dp = _padded_dim(d)
+    q, k, v = (_pad_d(t, dp) for t in (query, key, value))
+    o, vprime = LucidAttentionFunction.apply(q, k, v, scale, eps, d)
+    if dp != d:
+        o, vprime = o[..., :d], vprime[..., :d]
     return (o, vprime) if return_vprime else o
 
 
@@ -256,7 +273,7 @@ class GetVPrimeFunction(torch.autograd.Function):
     ``solve_triangular``; the backward uses the forward's fp32 solve state."""
 
     @staticmethod
-    def forward(ctx, key, value, scale, eps):
+    def forward(ctx, key, value, scale, eps, dn):
         B, Hkv, T, D = key.shape
         ctx.shape, ctx.t = key.shape, T
         if T == 0 or key.numel() == 0:
@@ -269,37 +286,37 @@ class GetVPrimeFunction(torch.autograd.Function):
         ctx.f32 = key.dtype == torch.float32
         vprime = torch.empty(B, Hkv, tp, D, dtype=torch.float32, device=key.device)
         if ctx.f32:
-            ws = torch.empty(lib.lucid_v_prime_f32_workspace_bytes(B, Hkv, tp, D), dtype=torch.uint8,
+            ws = torch.empty(lib.lucid_v_prime_f32_workspace_bytes(B, Hkv, tp, dn), dtype=torch.uint8,
                              device=key.device)
             fn, name = lib.lucid_get_v_prime_f32, "lucid_get_v_prime_f32"
         else:
-            ws = torch.empty(lib.lucid_fwd_workspace_bytes(B, Hkv, Hkv, tp, D), dtype=torch.uint8, device=key.device)
+            ws = torch.empty(lib.lucid_fwd_workspace_bytes(B, Hkv, Hkv, tp, dn), dtype=torch.uint8, device=key.device)
             fn, name = lib.lucid_get_v_prime, "lucid_get_v_prime"
         rc = fn(_lib.ptr(k), _lib.strides3(k, (0, 1, 2)), _lib.ptr(v), _lib.strides3(v, (0, 1, 2)),
-                _lib.ptr(vprime), _lib.ptr(ws), B, Hkv, tp, D, scale, float(eps), _lib.stream_handle(key.device))
+                _lib.ptr(vprime), _lib.ptr(ws), B, Hkv, tp, dn, scale, float(eps), _lib.stream_handle(key.device))
         _lib.check(lib, rc, name)
         ctx.save_for_backward(k, ws)
-        ctx.scale = scale
+        ctx.scale, ctx.dn = scale, dn
         return vprime[:, :, :T].to(value.dtype)
 
     @staticmethod
     def backward(ctx, dvp):
         if ctx.empty:
-            return dvp.new_zeros(ctx.shape), dvp.new_zeros(ctx.shape), None, None
+            return dvp.new_zeros(ctx.shape), dvp.new_zeros(ctx.shape), None, None, None
         k, ws = ctx.saved_tensors
         lib = _lib.load()
         B, Hkv, tp, D = k.shape
-        t = ctx.t
-        bws = torch.empty(lib.lucid_precond_bwd_workspace_bytes(B, Hkv, tp, D), dtype=torch.uint8, device=k.device)
+        t, dn = ctx.t, ctx.dn
+        bws = torch.empty(lib.lucid_precond_bwd_workspace_bytes(B, Hkv, tp, dn), dtype=torch.uint8, device=k.device)
         if ctx.f32:  # fp32 inputs: fp32 dV' in, fp32 dK and dV out
             dvp = _prep(dvp.float(), tp)
             dk = torch.empty(B, Hkv, tp, D, dtype=torch.float32, device=k.device)
             dv = torch.empty_like(dk)
             rc = lib.lucid_precond_bwd_f32(_lib.ptr(dvp), _lib.strides3(dvp, (0, 1, 2)), _lib.ptr(ws), _lib.ptr(dk),
                                            _lib.strides3(dk, (0, 1, 2)), _lib.ptr(dv), _lib.strides3(dv, (0, 1, 2)),
-                                           _lib.ptr(bws), B, Hkv, tp, D, ctx.scale, _lib.stream_handle(k.device))
+                                           _lib.ptr(bws), B, Hkv, tp, dn, ctx.scale, _lib.stream_handle(k.device))
             _lib.check(lib, rc, "lucid_precond_bwd_f32")
-            return dk[:, :, :t], dv[:, :, :t], None, None
+            return dk[:, :, :t], dv[:, :, :t], None, None, None
         f32 = dvp.dtype == torch.float32
         if not f32 and dvp.dtype != torch.bfloat16:
             dvp = dvp.to(torch.bfloat16)
@@ -308,10 +325,10 @@ class GetVPrimeFunction(torch.autograd.Function):
         dv = torch.empty_like(dk)
         rc = lib.lucid_precond_bwd(_lib.ptr(k), _lib.strides3(k, (0, 1, 2)), _lib.ptr(dvp), _lib.strides3(dvp, (0, 1, 2)),
                                    int(f32), _lib.ptr(ws), _lib.ptr(dk), _lib.strides3(dk, (0, 1, 2)), _lib.ptr(dv),
-                                   _lib.strides3(dv, (0, 1, 2)), _lib.ptr(bws), B, Hkv, tp, D, ctx.scale,
+                                   _lib.strides3(dv, (0, 1, 2)), _lib.ptr(bws), B, Hkv, tp, dn, ctx.scale,
                                    _lib.stream_handle(k.device))
         _lib.check(lib, rc, "lucid_precond_bwd")
-        return dk[:, :, :t], dv[:, :, :t], None, None
+        return dk[:, :, :t], dv[:, :, :t], None, None, None
 
 
 class AttentionOnVPrimeFunction(torch.autograd.Function):
@@ -320,7 +337,7 @@ class AttentionOnVPrimeFunction(torch.autograd.Function):
     ``lucid_attn_vp_bwd``."""
 
     @staticmethod
-    def forward(ctx, q, k, vp, scale, eps):
+    def forward(ctx, q, k, vp, scale, eps, dn):
         B, Hq, T, D = q.shape
         Hkv = k.shape[1]
         ctx.shapes, ctx.t, ctx.vdtype = (q.shape, k.shape, vp.shape), T, vp.dtype
@@ -337,39 +354,40 @@ class AttentionOnVPrimeFunction(torch.autograd.Function):
             vpp = _prep(vp.float(), tp)
             o = torch.empty(B, tp, Hq, D, dtype=torch.float32, device=dev)
             lse = torch.empty(B, Hq, tp, dtype=torch.float32, device=dev)
-            ws = torch.empty(lib.lucid_attn_vp_fwd_f32_workspace_bytes(B, Hq, Hkv, tp, D), dtype=torch.uint8,
+            ws = torch.empty(lib.lucid_attn_vp_fwd_f32_workspace_bytes(B, Hq, Hkv, tp, dn), dtype=torch.uint8,
                              device=dev)
             rc = lib.lucid_attn_vp_fwd_f32(_lib.ptr(qp), _lib.strides3(qp, (0, 1, 2)), _lib.ptr(kp),
                                            _lib.strides3(kp, (0, 1, 2)), _lib.ptr(vpp), _lib.strides3(vpp, (0, 1, 2)),
                                            _lib.ptr(o), _lib.strides3(o, (0, 2, 1)), _lib.ptr(lse), _lib.ptr(ws),
-                                           B, Hq, Hkv, tp, D, scale, float(eps), _lib.stream_handle(dev))
+                                           B, Hq, Hkv, tp, dn, scale, float(eps), _lib.stream_handle(dev))
             _lib.check(lib, rc, "lucid_attn_vp_fwd_f32")
             ctx.save_for_backward(qp, kp, o, lse, ws)
-            ctx.scale = scale
+            ctx.scale, ctx.dn = scale, dn
             return o[:, :T]
         f32 = vp.dtype == torch.float32
         vpp = _prep(vp if f32 else vp.to(torch.bfloat16), tp)
         o = torch.empty(B, tp, Hq, D, dtype=torch.bfloat16, device=dev)
         lse = torch.empty(B, Hq, tp, dtype=torch.float32, device=dev)
-        ws = torch.empty(lib.lucid_attn_vp_fwd_workspace_bytes(B, Hq, Hkv, tp, D), dtype=torch.uint8, device=dev)
+        ws = torch.empty(lib.lucid_attn_vp_fwd_workspace_bytes(B, Hq, Hkv, tp, dn), dtype=torch.uint8, device=dev)
         rc = lib.lucid_attn_vp_fwd(_lib.ptr(qp), _lib.strides3(qp, (0, 1, 2)), _lib.ptr(kp), _lib.strides3(kp, (0, 1, 2)),
                                    _lib.ptr(vpp), _lib.strides3(vpp, (0, 1, 2)), int(f32), _lib.ptr(o),
-                                   _lib.strides3(o, (0, 2, 1)), _lib.ptr(lse), _lib.ptr(ws), B, Hq, Hkv, tp, D, scale,
+                                   _lib.strides3(o, (0, 2, 1)), _lib.ptr(lse), _lib.ptr(ws), B, Hq, Hkv, tp, dn, scale,
                                    float(eps), _lib.stream_handle(dev))
         _lib.check(lib, rc, "lucid_attn_vp_fwd")
         ctx.save_for_backward(qp, kp, o, lse, ws)
-        ctx.scale = scale
+        ctx.scale, ctx.dn = scale, dn
         return o[:, :T]
 
     @staticmethod
     def backward(ctx, do):
         qs, ks, vs = ctx.shapes
         if ctx.empty:
-            return do.new_zeros(qs), do.new_zeros(ks), torch.zeros(vs, dtype=ctx.vdtype, device=do.device), None, None
+            return (do.new_zeros(qs), do.new_zeros(ks), torch.zeros(vs, dtype=ctx.vdtype, device=do.device),
+                    None, None, None)
         qp, kp, o, lse, ws = ctx.saved_tensors
         lib = _lib.load()
         B, Hq, tp, D = qp.shape
-        Hkv, t = kp.shape[1], ctx.t
+        Hkv, t, dn = kp.shape[1], ctx.t, ctx.dn
         dt = torch.float32 if ctx.f32in else torch.bfloat16
         if do.dtype != dt:
             do = do.to(dt)
@@ -382,58 +400,65 @@ class AttentionOnVPrimeFunction(torch.autograd.Function):
             dq = torch.empty(B, Hq, tp, D, dtype=torch.float32, device=dev)
             dk = torch.empty(B, Hkv, tp, D, dtype=torch.float32, device=dev)
             dvp = torch.empty(B, Hkv, tp, D, dtype=torch.float32, device=dev)
-            bws = torch.empty(lib.lucid_attn_vp_bwd_f32_workspace_bytes(B, Hq, Hkv, tp, D), dtype=torch.uint8,
+            bws = torch.empty(lib.lucid_attn_vp_bwd_f32_workspace_bytes(B, Hq, Hkv, tp, dn), dtype=torch.uint8,
                               device=dev)
             rc = lib.lucid_attn_vp_bwd_f32(_lib.ptr(do), _lib.strides3(do, (0, 2, 1)), _lib.ptr(o),
                                            _lib.strides3(o, (0, 2, 1)), _lib.ptr(lse), _lib.ptr(ws), _lib.ptr(dq),
                                            _lib.strides3(dq, (0, 1, 2)), _lib.ptr(dk), _lib.strides3(dk, (0, 1, 2)),
                                            _lib.ptr(dvp), _lib.strides3(dvp, (0, 1, 2)), _lib.ptr(bws),
-                                           B, Hq, Hkv, tp, D, ctx.scale, _lib.stream_handle(dev))
+                                           B, Hq, Hkv, tp, dn, ctx.scale, _lib.stream_handle(dev))
             _lib.check(lib, rc, "lucid_attn_vp_bwd_f32")
-            return dq[:, :, :t], dk[:, :, :t], dvp[:, :, :t].to(ctx.vdtype), None, None
+            return dq[:, :, :t], dk[:, :, :t], dvp[:, :, :t].to(ctx.vdtype), None, None, None
         f32 = ctx.vdtype == torch.float32
         dq = torch.empty(B, Hq, tp, D, dtype=torch.bfloat16, device=dev)
         dk = torch.empty(B, Hkv, tp, D, dtype=torch.bfloat16, device=dev)
         dvp = torch.empty(B, Hkv, tp, D, dtype=torch.float32 if f32 else torch.bfloat16, device=dev)
-        bws = torch.empty(lib.lucid_attn_vp_bwd_workspace_bytes(B, Hq, Hkv, tp, D), dtype=torch.uint8, device=dev)
+        bws = torch.empty(lib.lucid_attn_vp_bwd_workspace_bytes(B, Hq, Hkv, tp, dn), dtype=torch.uint8, device=dev)
         rc = lib.lucid_attn_vp_bwd(_lib.ptr(do), _lib.strides3(do, (0, 2, 1)), _lib.ptr(qp), _lib.strides3(qp, (0, 1, 2)),
                                    _lib.ptr(kp), _lib.strides3(kp, (0, 1, 2)), _lib.ptr(o), _lib.strides3(o, (0, 2, 1)),
                                    _lib.ptr(lse), _lib.ptr(ws), _lib.ptr(dq), _lib.strides3(dq, (0, 1, 2)), _lib.ptr(dk),
                                    _lib.strides3(dk, (0, 1, 2)), _lib.ptr(dvp), _lib.strides3(dvp, (0, 1, 2)), int(f32),
-                                   _lib.ptr(bws), B, Hq, Hkv, tp, D, ctx.scale, _lib.stream_handle(dev))
+                                   _lib.ptr(bws), B, Hq, Hkv, tp, dn, ctx.scale, _lib.stream_handle(dev))
         _lib.check(lib, rc, "lucid_attn_vp_bwd")
         dvp = dvp[:, :, :t]
         if dvp.dtype != ctx.vdtype:
             dvp = dvp.to(ctx.vdtype)
-        return dq[:, :, :t], dk[:, :, :t], dvp, None, None
+        return dq[:, :, :t], dk[:, :, :t], dvp, None, None, None
 
 
 def get_v_prime(key, value, scaling=None, attention_mask=None, eps=1e-5):
     """``V' = P^-1 V`` -- ``LucidAttention.get_v_prime(key, value, scaling, attention_mask)``
     (modeling_lucid.py:551-574), differentiable w.r.t. ``key`` and ``value``.
 
-    ``key, value [B, Hkv, T, d]`` (bf16, or fp32 at d = 64); returns V' in ``value``'s dtype.
+    ``key, value [B, Hkv, T, d]`` (bf16 with d <= 128, or fp32 with d <= 64); returns V' in ``value``'s dtype.
     ``eps`` is k_norm's epsilon (``config.rms_norm_eps``).  ``attention_mask``: None or the
     causal mask."""
     _check_inputs(None, key, value, f32_ok=True)
     _check_causal_mask(attention_mask, key.shape[2], key.shape[2])
-    scale = key.shape[-1] ** -0.5 if scaling is None else float(scaling)
-    return GetVPrimeFunction.apply(key, value, scale, eps)
+    d = key.shape[-1]
+    scale = d ** -0.5 if scaling is None else float(scaling)
+    dp = _padded_dim(d)
+    vprime = GetVPrimeFunction.apply(_pad_d(key, dp), _pad_d(value, dp), scale, eps, d)
+    return vprime if dp == d else vprime[..., :d]
 
 
 def eager_lucid_attention_forward(query, key, v_prime, scaling=None, attention_mask=None, eps=1e-5, **kwargs):
     """``LucidAttention.eager_lucid_attention_forward(query, key, v_prime, scaling, attention_mask)``
     (modeling_lucid.py:505-549): causal softmax attention of ``query [B, Hq, T, d]`` and
     ``key [B, Hkv, T, d]`` on a given ``v_prime [B, Hkv, T, d]`` (bf16 or fp32; GQA by index,
-    no repeat_kv copy).  fp32 query and key (d = 64) run the fp32 kernels (fp32 O).  Returns ``(O [B, T, Hq, d], None)``, differentiable w.r.t. all three.
+    no repeat_kv copy).  fp32 query and key (d <= 64) run the fp32 kernels (fp32 O).  Returns
+    ``(O [B, T, Hq, d], None)``, differentiable w.r.t. all three.
     ``attention_mask``: None or the causal mask.  ``eps`` (k_norm's) only serves the per-head
     precision choice (:func:`set_precision`)."""
     _check_inputs(query, key, None, f32_ok=True)
     if v_prime.shape != key.shape or not v_prime.is_cuda or v_prime.dtype not in (torch.bfloat16, torch.float32):
         raise ValueError("lucid_amd: v_prime must be a bf16 or fp32 GPU tensor shaped like key")
     _check_causal_mask(attention_mask, query.shape[2], key.shape[2])
-    scale = query.shape[-1] ** -0.5 if scaling is None else float(scaling)
-    return AttentionOnVPrimeFunction.apply(query, key, v_prime, scale, eps), None
+    d = query.shape[-1]
+    scale = d ** -0.5 if scaling is None else float(scaling)
+    dp = _padded_dim(d)
+    o = AttentionOnVPrimeFunction.apply(_pad_d(query, dp), _pad_d(key, dp), _pad_d(v_prime, dp), scale, eps, d)
+    return (o if dp == d else o[..., :d]), None
 
 
 def causal_attention(query, key, value, scaling=None):
@@ -449,8 +474,9 @@ def lucid_decode(query, key, value, key_cache, vprime_cache, cache_len, scaling=
     attention of LucidAttention.forward, modeling_lucid.py:475-496, 576-598).
 
     ``query [B, Hq, 1, d]``, ``key/value [B, Hkv, 1, d]`` (bf16; keys with RoPE applied);
-    ``key_cache`` / ``vprime_cache`` are bf16 buffers ``[B, Hkv, T_cap, d]`` whose first
-    ``cache_len`` rows are valid.  The token's V' row (exact diagonal:
+    ``key_cache`` / ``vprime_cache`` are bf16 buffers ``[B, Hkv, T_cap, dp]`` whose first
+    ``cache_len`` rows are valid, ``dp`` = 64 for d <= 64 and 128 above (columns beyond d
+    zero: the head rows zero-padded).  The token's V' row (exact diagonal:
     ``v'_t = (v_t - sum_j P_tj v'_j) / P_tt``) and its key are written at row ``cache_len``
     of the caches in place.  Returns ``(O [B, 1, Hq, d], v'_t fp32 [B, Hkv, 1, d])``.
     """
@@ -458,27 +484,29 @@ def lucid_decode(query, key, value, key_cache, vprime_cache, cache_len, scaling=
     for name, t in (("query", query), ("key_cache", key_cache), ("vprime_cache", vprime_cache)):
         if not t.is_cuda or t.dtype != torch.bfloat16 or t.dim() != 4:
             raise TypeError(f"lucid_amd: {name} must be a 4-D bfloat16 GPU tensor")
+    for name, t in (("key_cache", key_cache), ("vprime_cache", vprime_cache)):  # written in place: no copies
         if t.stride(-1) != 1 or any(s % 8 for s in t.stride()[:3]) or t.data_ptr() % 16:
             raise ValueError(f"lucid_amd: {name} needs a contiguous last axis and 8-element aligned strides")
-    B, Hkv, tn, D = key.shape
+    B, Hkv, tn, d = key.shape
     Hq = query.shape[1]
+    D = _padded_dim(d)
     if tn != 1 or query.shape[2] != 1:
         raise ValueError("lucid_amd: lucid_decode takes one new token per sequence")
     if key_cache.shape[:2] != (B, Hkv) or vprime_cache.shape != key_cache.shape or key_cache.shape[3] != D:
-        raise ValueError("lucid_amd: cache shapes disagree with the new key")
+        raise ValueError(f"lucid_amd: cache buffers must be [B, Hkv, T_cap, {D}] for head_dim {d}")
     lib = _lib.load()
     cap = key_cache.shape[2]
-    q, k, v = (_prep(t, 1) for t in (query, key, value))
+    q, k, v = (_prep(_pad_d(t, D), 1) for t in (query, key, value))
     o = torch.empty(B, 1, Hq, D, dtype=torch.bfloat16, device=q.device)
     vp_new = torch.empty(B, Hkv, 1, D, dtype=torch.float32, device=q.device)
-    ws = torch.empty(max(lib.lucid_decode_workspace_bytes(B, Hq, Hkv, cap, D), 256), dtype=torch.uint8,
+    ws = torch.empty(max(lib.lucid_decode_workspace_bytes(B, Hq, Hkv, cap, d), 256), dtype=torch.uint8,
                      device=q.device)
-    scale = D ** -0.5 if scaling is None else float(scaling)
+    scale = d ** -0.5 if scaling is None else float(scaling)
     rc = lib.lucid_decode(
         _lib.ptr(q), _lib.strides3(q, (0, 1, 2)), _lib.ptr(k), _lib.strides3(k, (0, 1, 2)),
         _lib.ptr(v), _lib.strides3(v, (0, 1, 2)), _lib.ptr(key_cache), _lib.strides3(key_cache, (0, 1, 2)),
         _lib.ptr(vprime_cache), _lib.strides3(vprime_cache, (0, 1, 2)), _lib.ptr(o), _lib.strides3(o, (0, 2, 1)),
-        _lib.ptr(vp_new), _lib.ptr(ws), B, Hq, Hkv, int(cache_len), cap, D, scale, float(eps),
+        _lib.ptr(vp_new), _lib.ptr(ws), B, Hq, Hkv, int(cache_len), cap, d, scale, float(eps),
         _lib.stream_handle(q.device))
     _lib.check(lib, rc, "lucid_decode")
-    return o, vp_new
+    return (o, vp_new) if D == d else (o[..., :d], vp_new[..., :d])

@@ -24,7 +24,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from .lucid import lucid_attention, lucid_decode
+from .lucid import _padded_dim, lucid_attention, lucid_decode
 
 
 @dataclass
@@ -110,23 +110,25 @@ class LlamaMLP(nn.Module):
 class LucidCache:
     """Per-layer (K with RoPE applied, V') cache for decoding (the reference keeps the same
     pair in a DynamicCache, modeling_lucid.py:479-481).  Rows live in preallocated bf16
-    buffers [B, Hkv, capacity, d] that grow by doubling, so a decoding step appends in
-    place instead of concatenating the whole cache; ``key_cache`` / ``value_cache`` give
-    the valid rows [B, Hkv, T, d]."""
+    buffers [B, Hkv, capacity, dp] that grow by doubling, so a decoding step appends in
+    place instead of concatenating the whole cache (dp: the head dim d zero-padded to 64 or
+    128, the row width of the decoding kernel); ``key_cache`` / ``value_cache`` give the
+    valid rows [B, Hkv, T, d]."""
 
     def __init__(self, min_capacity: int = 256):
         self._k: list[torch.Tensor] = []
         self._v: list[torch.Tensor] = []
         self._len: list[int] = []
+        self._d: list[int] = []
         self.min_capacity = min_capacity
 
     @property
     def key_cache(self) -> list[torch.Tensor]:
-        return [k[:, :, :n] for k, n in zip(self._k, self._len)]
+        return [k[:, :, :n, :d] for k, n, d in zip(self._k, self._len, self._d)]
 
     @property
     def value_cache(self) -> list[torch.Tensor]:
-        return [v[:, :, :n] for v, n in zip(self._v, self._len)]
+        return [v[:, :, :n, :d] for v, n, d in zip(self._v, self._len, self._d)]
 
     def get_seq_length(self, layer_idx: int = 0) -> int:
         return self._len[layer_idx] if layer_idx < len(self._len) else 0
@@ -136,10 +138,13 @@ class LucidCache:
         n = self.get_seq_length(layer_idx)
         if layer_idx == len(self._k):
             cap = max(self.min_capacity, -(-extra // 256) * 256)
-            shape = (like.shape[0], like.shape[1], cap, like.shape[3])
-            self._k.append(torch.empty(shape, dtype=torch.bfloat16, device=like.device))
-            self._v.append(torch.empty(shape, dtype=torch.bfloat16, device=like.device))
+            d = like.shape[3]
+            shape = (like.shape[0], like.shape[1], cap, _padded_dim(d))
+            alloc = torch.empty if shape[3] == d else torch.zeros  # padded columns stay zero
+            self._k.append(alloc(shape, dtype=torch.bfloat16, device=like.device))
+            self._v.append(alloc(shape, dtype=torch.bfloat16, device=like.device))
             self._len.append(0)
+            self._d.append(d)
             return
         cap = self._k[layer_idx].shape[2]
         if n + extra <= cap:
@@ -147,7 +152,8 @@ class LucidCache:
         new_cap = max(2 * cap, -(-(n + extra) // 256) * 256)
         for bufs in (self._k, self._v):
             old = bufs[layer_idx]
-            grown = torch.empty(old.shape[0], old.shape[1], new_cap, old.shape[3], dtype=old.dtype, device=old.device)
+            alloc = torch.empty if old.shape[3] == self._d[layer_idx] else torch.zeros
+            grown = alloc(old.shape[0], old.shape[1], new_cap, old.shape[3], dtype=old.dtype, device=old.device)
             grown[:, :, :n] = old[:, :, :n]
             bufs[layer_idx] = grown
 
@@ -162,10 +168,11 @@ class LucidCache:
         self.reserve(layer_idx, key, key.shape[2])
         k, v, n = self.buffers(layer_idx)
         t = key.shape[2]
-        k[:, :, n:n + t] = key
-        v[:, :, n:n + t] = v_prime
+        d = self._d[layer_idx]
+        k[:, :, n:n + t, :d] = key
+        v[:, :, n:n + t, :d] = v_prime
         self._len[layer_idx] = n + t
-        return k[:, :, :n + t], v[:, :, :n + t]
+        return k[:, :, :n + t, :d], v[:, :, :n + t, :d]
 
 
 class LucidAttention(nn.Module):

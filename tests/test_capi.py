@@ -71,11 +71,21 @@ def test_argument_validation_without_gpu(built):
     lib = _lib.load()
     s = (ctypes.c_int64 * 3)(64 * 256, 64 * 256, 64)
     dummy = ctypes.c_void_p(1 << 20)
-    # head_dim 96 is rejected before anything is launched
-    rc = lib.lucid_attn_fwd(dummy, s, dummy, s, dummy, s, dummy, s, dummy, dummy, dummy,
-                            1, 1, 1, 256, 96, 0.1, 1e-5, None)
-    assert rc == _lib.LUCID_EINVAL
-    assert b"head_dim" in lib.lucid_last_error()
+    # head dims above 128 (or below 1) are rejected before anything is launched
+    for d in (0, 129, 256):
+        rc = lib.lucid_attn_fwd(dummy, s, dummy, s, dummy, s, dummy, s, dummy, dummy, dummy,
+                                1, 1, 1, 256, d, 0.1, 1e-5, None)
+        assert rc == _lib.LUCID_EINVAL
+        assert b"head_dim" in lib.lucid_last_error()
+    # other head dims run on rows padded to 64 or 128: the workspaces are those of the padded dim
+    for d, dp in ((1, 64), (32, 64), (68, 128), (96, 128)):
+        assert lib.lucid_fwd_workspace_bytes(1, 4, 2, 256, d) == lib.lucid_fwd_workspace_bytes(1, 4, 2, 256, dp)
+        assert lib.lucid_bwd_workspace_bytes(1, 4, 2, 256, d) == lib.lucid_bwd_workspace_bytes(1, 4, 2, 256, dp)
+        assert lib.lucid_decode_workspace_bytes(1, 4, 2, 4096, d) == lib.lucid_decode_workspace_bytes(1, 4, 2, 4096, dp)
+    # fp32 inputs: head dims up to 64
+    rc = lib.lucid_attn_fwd_f32(dummy, s, dummy, s, dummy, s, dummy, s, dummy, dummy, dummy,
+                                1, 1, 1, 256, 68, 0.1, 1e-5, None)
+    assert rc == _lib.LUCID_EINVAL and b"head_dim <= 64" in lib.lucid_last_error()
     rc = lib.lucid_attn_fwd(dummy, s, dummy, s, dummy, s, dummy, s, dummy, dummy, dummy,
                             1, 1, 1, 200, 64, 0.1, 1e-5, None)
     assert rc == _lib.LUCID_EINVAL and b"multiple of 128" in lib.lucid_last_error()

@@ -124,7 +124,7 @@ def _ref32_errors(q, k, v, do, eps=1e-5):
 def test_fp32_rejects_what_it_does_not_cover():
     from lucid_amd import lucid_attention
     q, k, v, _ = (x.cuda() for x in _inputs(1, 2, 2, 128, 128, seed=1))
-    with pytest.raises(ValueError, match="head_dim 64"):
+    with pytest.raises(ValueError, match="head_dim <= 64"):
         lucid_attention(q, k, v)
     q, k, v, _ = (x.cuda() for x in _inputs(1, 2, 2, 128, 64, seed=1))
     with pytest.raises(TypeError, match="share one dtype"):

@@ -216,7 +216,7 @@ def test_auto_precision_picks_exact_for_correlated_heads():
     v = (torch.randn(B, Hkv, T, D, generator=g) / 8).to(torch.bfloat16)
     print("case auto precision", flush=True)
     assert lucid.get_precision() == "auto"
-    o, vp, lse, ws = lucid._fwd(q.cuda(), k.cuda(), v.cuda(), D ** -0.5, 1e-5)
+    o, vp, lse, ws = lucid._fwd(q.cuda(), k.cuda(), v.cuda(), D ** -0.5, 1e-5, D)
     torch.cuda.synchronize()
     mass = lucid.head_row_mass(ws, B, Hq, Hkv, T, D).cpu().numpy()
     kh = R.k_hat(_np(k), 1e-5)
