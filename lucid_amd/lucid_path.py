@@ -14,8 +14,11 @@ reference ships as the kernels ``intra_chunk_preprocess_fwd.py`` and
 
     O_i = sum_{j <= i} softmax_j(s A_ij) v_j
 
-Tensors are bf16 GPU tensors in the reference layout ``[B, T, H, K]``; K = V = 64.
-There is no CPU or Triton fallback.
+Tensors are bf16 GPU tensors in the reference layout ``[B, T, H, K]``; the kernels run at
+K = V = 64, and head dims 16 and 32 (the other sizes the reference's kernels take below
+128) run on rows zero-padded to 64: the reflections ``I - beta w w^T`` act as the identity
+on the padded coordinates, so the logits, O and the gradients of the real coordinates are
+unchanged.  There is no CPU or Triton fallback.
 """
 from __future__ import annotations
 
@@ -156,8 +159,8 @@ def _check(q, k, v, w, beta, g):
     assert beta.shape[:3] == k.shape[:3], 'beta should have the same number of heads as k'
     assert g is None, 'g is not supported'
     assert q.shape[-2] % k.shape[-2] == 0, 'the number of query heads should be divisible by the number of key heads'
-    if q.shape[-1] != 64 or v.shape[-1] != 64:
-        raise NotImplementedError("lucid_amd LUCID-Path kernels support head_dim 64")
+    if q.shape[-1] > _KD or v.shape[-1] > _KD:
+        raise NotImplementedError("lucid_amd LUCID-Path kernels support head_dim 16, 32 and 64")
     for name, x in (("q", q), ("k", k), ("v", v), ("w", w), ("beta", beta)):
         if not x.is_cuda:
             raise RuntimeError(f"lucid_amd: {name} must be a GPU tensor (no CPU path)")
@@ -165,7 +168,19 @@ def _check(q, k, v, w, beta, g):
             raise TypeError(f"lucid_amd: {name} must be bfloat16, got {x.dtype}")
 
 
+_KD = 64  # head dim of the kernels (q, k, w and v rows)
+
+
+def _pad_d(x: torch.Tensor) -> torch.Tensor:
+    """Zero-pad the head axis (last) to the kernels' 64 columns (differentiable)."""
+    return x if x.shape[-1] == _KD else F.pad(x, (0, _KD - x.shape[-1]))
+
+
 def _apply(fn, q, k, v, w, beta, g, scale, cu_seqlens, use_cache):
+    kd, vd = k.shape[-1], v.shape[-1]
+    if kd != _KD or vd != _KD:
+        o, kc = _apply(fn, _pad_d(q), _pad_d(k), _pad_d(v), _pad_d(w), beta, g, scale, cu_seqlens, use_cache)
+        return o[..., :vd], (kc[..., :kd] if kc is not None else None)
     if q.shape[1] == 0 or q.numel() == 0:  # empty: empty results, as the reference's ops give
         o = q.new_zeros(*q.shape[:3], v.shape[-1]) + 0 * (q.sum() + k.sum() + v.sum() + w.sum() + beta.sum())
         return o, (k.new_empty(k.shape) if use_cache else None)
