@@ -39,7 +39,7 @@ extern "C" {
 #define LUCID_PRECISION_FAST 1  /* bf16 products everywhere */
 #define LUCID_PRECISION_EXACT 2 /* hi/lo split products for every head */
 
-/* ABI version of this header (bumped on any signature change). */
+/* ABI version of this header (bumped on any signature change or new entry point): 4. */
 int lucid_abi_version(void);
 
 /* Text of the last error on the calling thread ("" if none). */
@@ -221,6 +221,26 @@ int lucid_decode(const void* q, const int64_t* q_strides, const void* k, const i
                  const int64_t* v_strides, void* k_cache, const int64_t* k_cache_strides, void* vp_cache,
                  const int64_t* vp_cache_strides, void* o, const int64_t* o_strides, float* vp_new, void* ws, int B,
                  int Hq, int Hkv, int T_past, int T_cap, int D, float scale, float eps, void* stream);
+
+/* Bytes of the workspace of lucid_decode_tokens for L new tokens per call and caches of
+ * capacity T_cap (0 on bad sizes). */
+size_t lucid_decode_tokens_workspace_bytes(int B, int Hq, int Hkv, int L, int T_cap, int D);
+
+/* L new tokens per sequence in one call (q [B,Hq,L,D], k and v [B,Hkv,L,D], rows in
+ * order; o [B,L,Hq,D] by its strides {batch, head, time}; vp_new fp32 [B,Hkv,L,D]
+ * contiguous), appended at rows T_past .. T_past+L-1 of the caches (T_past + L <= T_cap).
+ * Each token's V' row is the exact prefill row: it is coupled to the cached rows and to
+ * the earlier new tokens, v'_t = (v_t - sum_{j<t} P_tj v'_j) / P_tt, and each token
+ * attends to the cache and to the new tokens up to itself.  The tokens run in passes of
+ * 32 / (Hq/Hkv + 1) (the columns of one score tile), each pass reading the caches once.
+ * Replaces LucidAttention.get_new_v_prime for L_k new tokens (modeling_lucid.py:576-598,
+ * which couples a new token to the cache only) and the cached attention call
+ * (:475-496).  lucid_decode is this entry with L = 1. */
+int lucid_decode_tokens(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                        const void* v, const int64_t* v_strides, void* k_cache, const int64_t* k_cache_strides,
+                        void* vp_cache, const int64_t* vp_cache_strides, void* o, const int64_t* o_strides,
+                        float* vp_new, void* ws, int B, int Hq, int Hkv, int L, int T_past, int T_cap, int D,
+                        float scale, float eps, void* stream);
 
 /* lucid_decode without a workspace argument: the same decoding step, with its split
  * partials in a static 4 MiB (4194304-byte) device array of the library instead of `ws`,

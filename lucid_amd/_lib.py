@@ -72,6 +72,9 @@ _SIGS = {
                           _int, _int, _int, _int, _int, _int, _flt, _flt, _vp], _int),
         "lucid_decode_noalloc": ([_vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp,
                                   _int, _int, _int, _int, _int, _int, _flt, _flt, _vp], _int),
+        "lucid_decode_tokens_workspace_bytes": ([_int] * 6, _sz),
+        "lucid_decode_tokens": ([_vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _vp,
+                                 _int, _int, _int, _int, _int, _int, _int, _flt, _flt, _vp], _int),
         "lucid_profile_enable": ([_int], None),
         "lucid_profile_collect": ([], _int),
         "lucid_profile_entry": ([_int, ctypes.c_char_p, _int, ctypes.POINTER(ctypes.c_double),

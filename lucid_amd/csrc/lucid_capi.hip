@@ -585,7 +585,10 @@ int decode_splits(int BH, int Tp, int D) {
   return want < most ? want : most;
 }
 
-lucid::DecodePartials carve_decode(void* base, int BH, int G, int nsplit, int D, size_t* bytes) {
+// Tokens per split/combine pass: the L (G + 1) columns of one 32-column score tile.
+int decode_pass_tokens(int G) { return 32 / (G + 1); }
+
+lucid::DecodePartials carve_decode(void* base, int BH, int G, int L, int nsplit, int D, size_t* bytes) {
   D = padded_dim(D);
   lucid::DecodePartials w{};
   size_t off = 0;
@@ -596,55 +599,75 @@ lucid::DecodePartials carve_decode(void* base, int BH, int G, int nsplit, int D,
     return r;
   };
   const size_t ns = nsplit > 0 ? nsplit : 1;
-  w.a = reinterpret_cast<float*>(take(ns * BH * D * 4));
-  w.m = reinterpret_cast<float*>(take(ns * BH * G * 4));
-  w.l = reinterpret_cast<float*>(take(ns * BH * G * 4));
-  w.o = reinterpret_cast<float*>(take(ns * BH * G * D * 4));
+  w.a = reinterpret_cast<float*>(take(ns * BH * L * D * 4));
+  w.m = reinterpret_cast<float*>(take(ns * BH * L * G * 4));
+  w.l = reinterpret_cast<float*>(take(ns * BH * L * G * 4));
+  w.o = reinterpret_cast<float*>(take(ns * BH * L * G * D * 4));
   if (bytes) *bytes = off;
   return w;
 }
 
+// Partials of one pass of at most `L` tokens with a cache that grows to `T_end` rows.
+size_t decode_ws_bytes(int BH, int G, int L, int T_end, int D) {
+  const int Lp = L < decode_pass_tokens(G) ? L : decode_pass_tokens(G);
+  size_t n = 0;
+  carve_decode(nullptr, BH, G, Lp, decode_splits(BH, T_end, D), D, &n);
+  return n;
+}
+
+// L new tokens in passes of at most decode_pass_tokens(G): each pass reads the cache once
+// (split kernel) and appends its tokens (combine kernel), so the next pass sees them.
 template <int D, int G>
 int launch_decode(const void* q, const int64_t* qs, const void* k, const int64_t* ks, const void* v,
                   const int64_t* vs, void* kc, const int64_t* kcs, void* vc, const int64_t* vcs, void* o,
-                  const int64_t* os, float* vp_new, const lucid::DecodePartials& part, int B, int Hkv, int Tp,
-                  float scale, float eps, float dn, hipStream_t st) {
+                  const int64_t* os, float* vp_new, void* ws, int B, int Hkv, int L, int Tp, float scale, float eps,
+                  float dn, hipStream_t st) {
   const int BH = B * Hkv;
-  const int ns = decode_splits(BH, Tp, D);
-  if (ns > 0) {
-    const int KS = (Tp + ns - 1) / ns;
-    LUCID_LAUNCH("lucid_decode_split_kernel", (lucid::lucid_decode_split_kernel<D, G>), dim3(ns, BH), st,
-                 (const bf16*)q, S(qs), (const bf16*)k, S(ks), (const bf16*)kc, S(kcs), (const bf16*)vc, S(vcs), Hkv,
-                 Tp, KS, scale, eps, dn, part);
+  constexpr int LM = lucid::decode_tokens_per_pass<G>();
+  for (int t0 = 0; t0 < L; t0 += LM) {
+    const int Lc = L - t0 < LM ? L - t0 : LM, Tc = Tp + t0;
+    const int ns = decode_splits(BH, Tc, D);
+    const lucid::DecodePartials part = carve_decode(ws, BH, G, Lc, ns, D, nullptr);
+    const bf16* qc = (const bf16*)q + t0 * qs[2];
+    const bf16* kn = (const bf16*)k + t0 * ks[2];
+    const bf16* vn = (const bf16*)v + t0 * vs[2];
+    if (ns > 0) {
+      const int KS = (Tc + ns - 1) / ns;
+      LUCID_LAUNCH("lucid_decode_split_kernel", (lucid::lucid_decode_split_kernel<D, G>), dim3(ns, BH), st, qc,
+                   S(qs), kn, S(ks), (const bf16*)kc, S(kcs), (const bf16*)vc, S(vcs), Hkv, Tc, KS, Lc, scale, eps,
+                   dn, part);
+    }
+    LUCID_LAUNCH("lucid_decode_combine_kernel", (lucid::lucid_decode_combine_kernel<D, G>), dim3(BH, G), st, ns,
+                 Lc, qc, S(qs), kn, S(ks), vn, S(vs), (bf16*)kc, S(kcs), (bf16*)vc, S(vcs),
+                 (bf16*)o + t0 * os[2], S(os), vp_new + (size_t)t0 * D, L, Hkv, Tc, scale, eps, dn, part);
   }
-  LUCID_LAUNCH("lucid_decode_combine_kernel", (lucid::lucid_decode_combine_kernel<D, G>), dim3(BH, G), st, ns,
-               (const bf16*)q, S(qs), (const bf16*)k, S(ks), (const bf16*)v, S(vs), (bf16*)kc, S(kcs), (bf16*)vc,
-               S(vcs), (bf16*)o, S(os), vp_new, Hkv, Tp, scale, eps, dn, part);
   return LUCID_OK;
 }
 
 template <int D>
 int decode_dispatch_g(int G, const void* q, const int64_t* qs, const void* k, const int64_t* ks, const void* v,
                       const int64_t* vs, void* kc, const int64_t* kcs, void* vc, const int64_t* vcs, void* o,
-                      const int64_t* os, float* vp_new, const lucid::DecodePartials& part, int B, int Hkv, int Tp,
-                      float scale, float eps, float dn, hipStream_t st) {
+                      const int64_t* os, float* vp_new, void* ws, int B, int Hkv, int L, int Tp, float scale,
+                      float eps, float dn, hipStream_t st) {
   switch (G) {
-    case 1: return launch_decode<D, 1>(q, qs, k, ks, v, vs, kc, kcs, vc, vcs, o, os, vp_new, part, B, Hkv, Tp, scale, eps, dn, st);
-    case 2: return launch_decode<D, 2>(q, qs, k, ks, v, vs, kc, kcs, vc, vcs, o, os, vp_new, part, B, Hkv, Tp, scale, eps, dn, st);
-    case 4: return launch_decode<D, 4>(q, qs, k, ks, v, vs, kc, kcs, vc, vcs, o, os, vp_new, part, B, Hkv, Tp, scale, eps, dn, st);
-    case 8: return launch_decode<D, 8>(q, qs, k, ks, v, vs, kc, kcs, vc, vcs, o, os, vp_new, part, B, Hkv, Tp, scale, eps, dn, st);
+    case 1: return launch_decode<D, 1>(q, qs, k, ks, v, vs, kc, kcs, vc, vcs, o, os, vp_new, ws, B, Hkv, L, Tp, scale, eps, dn, st);
+    case 2: return launch_decode<D, 2>(q, qs, k, ks, v, vs, kc, kcs, vc, vcs, o, os, vp_new, ws, B, Hkv, L, Tp, scale, eps, dn, st);
+    case 4: return launch_decode<D, 4>(q, qs, k, ks, v, vs, kc, kcs, vc, vcs, o, os, vp_new, ws, B, Hkv, L, Tp, scale, eps, dn, st);
+    case 8: return launch_decode<D, 8>(q, qs, k, ks, v, vs, kc, kcs, vc, vcs, o, os, vp_new, ws, B, Hkv, L, Tp, scale, eps, dn, st);
     default: return fail("decode supports Hq / Hkv in {1, 2, 4, 8}, got " + std::to_string(G));
   }
 }
 
 int check_decode_args(const void* q, const int64_t* qs, const void* k, const int64_t* ks, const void* v,
                       const int64_t* vs, const void* kc, const int64_t* kcs, const void* vc, const int64_t* vcs,
-                      const void* o, const int64_t* os, const float* vp_new, int B, int Hq, int Hkv, int T_past,
-                      int T_cap, int D) {
+                      const void* o, const int64_t* os, const float* vp_new, int B, int Hq, int Hkv, int L,
+                      int T_past, int T_cap, int D) {
   if (B <= 0 || Hq <= 0 || Hkv <= 0) return fail("B, Hq and Hkv must be positive");
+  if (L <= 0) return fail("the number of new tokens must be positive");
   if (D < 1 || D > 128) return fail("head_dim must be in [1, 128], got " + std::to_string(D));
   if (Hq % Hkv != 0) return fail("Hq must be a multiple of Hkv");
-  if (T_past < 0 || T_past >= T_cap) return fail("the cache is full: T_past must be in [0, T_cap)");
+  if (T_past < 0 || (int64_t)T_past + L > T_cap)
+    return fail("the cache is too small: T_past + L must be within T_cap (T_past >= 0)");
   if (int rc = check_tensor("q", q, qs)) return rc;
   if (int rc = check_tensor("k", k, ks)) return rc;
   if (int rc = check_tensor("v", v, vs)) return rc;
@@ -695,16 +718,14 @@ int decode_scratch(void** out) {
 int decode_impl(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides, const void* v,
                 const int64_t* v_strides, void* k_cache, const int64_t* k_cache_strides, void* vp_cache,
                 const int64_t* vp_cache_strides, void* o, const int64_t* o_strides, float* vp_new, void* ws, int B,
-                int Hq, int Hkv, int T_past, int D, float scale, float eps, void* stream) {
-  const lucid::DecodePartials part =
-      carve_decode(ws, B * Hkv, Hq / Hkv, decode_splits(B * Hkv, T_past, D), D, nullptr);
+                int Hq, int Hkv, int L, int T_past, int D, float scale, float eps, void* stream) {
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (padded_dim(D) == 64)
     return decode_dispatch_g<64>(Hq / Hkv, q, q_strides, k, k_strides, v, v_strides, k_cache, k_cache_strides,
-                                 vp_cache, vp_cache_strides, o, o_strides, vp_new, part, B, Hkv, T_past, scale, eps,
+                                 vp_cache, vp_cache_strides, o, o_strides, vp_new, ws, B, Hkv, L, T_past, scale, eps,
                                  (float)D, st);
   return decode_dispatch_g<128>(Hq / Hkv, q, q_strides, k, k_strides, v, v_strides, k_cache, k_cache_strides,
-                                vp_cache, vp_cache_strides, o, o_strides, vp_new, part, B, Hkv, T_past, scale, eps,
+                                vp_cache, vp_cache_strides, o, o_strides, vp_new, ws, B, Hkv, L, T_past, scale, eps,
                                 (float)D, st);
 }
 
@@ -714,23 +735,36 @@ extern "C" {
 
 size_t lucid_decode_workspace_bytes(int B, int Hq, int Hkv, int T_cap, int D) {
   if (B <= 0 || Hkv <= 0 || Hq <= 0 || Hq % Hkv || T_cap < 0) return 0;
-  size_t n = 0;
-  carve_decode(nullptr, B * Hkv, Hq / Hkv, decode_splits(B * Hkv, T_cap, D), D, &n);
-  return n;
+  return decode_ws_bytes(B * Hkv, Hq / Hkv, 1, T_cap, D);
+}
+
+size_t lucid_decode_tokens_workspace_bytes(int B, int Hq, int Hkv, int L, int T_cap, int D) {
+  if (B <= 0 || Hkv <= 0 || Hq <= 0 || Hq % Hkv || T_cap < 0 || L <= 0) return 0;
+  return decode_ws_bytes(B * Hkv, Hq / Hkv, L, T_cap, D);
 }
 
 int lucid_decode(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides, const void* v,
                  const int64_t* v_strides, void* k_cache, const int64_t* k_cache_strides, void* vp_cache,
                  const int64_t* vp_cache_strides, void* o, const int64_t* o_strides, float* vp_new, void* ws, int B,
                  int Hq, int Hkv, int T_past, int T_cap, int D, float scale, float eps, void* stream) {
+  return lucid_decode_tokens(q, q_strides, k, k_strides, v, v_strides, k_cache, k_cache_strides, vp_cache,
+                             vp_cache_strides, o, o_strides, vp_new, ws, B, Hq, Hkv, 1, T_past, T_cap, D, scale, eps,
+                             stream);
+}
+
+int lucid_decode_tokens(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                        const void* v, const int64_t* v_strides, void* k_cache, const int64_t* k_cache_strides,
+                        void* vp_cache, const int64_t* vp_cache_strides, void* o, const int64_t* o_strides,
+                        float* vp_new, void* ws, int B, int Hq, int Hkv, int L, int T_past, int T_cap, int D,
+                        float scale, float eps, void* stream) {
   g_last_error.clear();
   if (int rc = check_decode_args(q, q_strides, k, k_strides, v, v_strides, k_cache, k_cache_strides, vp_cache,
-                                 vp_cache_strides, o, o_strides, vp_new, B, Hq, Hkv, T_past, T_cap, D))
+                                 vp_cache_strides, o, o_strides, vp_new, B, Hq, Hkv, L, T_past, T_cap, D))
     return rc;
   if (!ws) return fail("ws must be non-null");
   if (int rc = check_ws("ws", ws)) return rc;
   return decode_impl(q, q_strides, k, k_strides, v, v_strides, k_cache, k_cache_strides, vp_cache, vp_cache_strides,
-                     o, o_strides, vp_new, ws, B, Hq, Hkv, T_past, D, scale, eps, stream);
+                     o, o_strides, vp_new, ws, B, Hq, Hkv, L, T_past, D, scale, eps, stream);
 }
 
 int lucid_decode_noalloc(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
@@ -740,21 +774,20 @@ int lucid_decode_noalloc(const void* q, const int64_t* q_strides, const void* k,
                          void* stream) {
   g_last_error.clear();
   if (int rc = check_decode_args(q, q_strides, k, k_strides, v, v_strides, k_cache, k_cache_strides, vp_cache,
-                                 vp_cache_strides, o, o_strides, vp_new, B, Hq, Hkv, T_past, T_cap, D))
+                                 vp_cache_strides, o, o_strides, vp_new, B, Hq, Hkv, 1, T_past, T_cap, D))
     return rc;
-  size_t need = 0;
-  carve_decode(nullptr, B * Hkv, Hq / Hkv, decode_splits(B * Hkv, T_past, D), D, &need);
+  const size_t need = decode_ws_bytes(B * Hkv, Hq / Hkv, 1, T_past, D);
   if (need > kDecodeScratchBytes)
     return fail("lucid_decode_noalloc needs " + std::to_string(need) + " bytes of scratch for these sizes, above its " +
                 std::to_string(kDecodeScratchBytes) + "-byte static scratch; call lucid_decode with a workspace");
   void* ws = nullptr;
   if (int rc = decode_scratch(&ws)) return rc;
   return decode_impl(q, q_strides, k, k_strides, v, v_strides, k_cache, k_cache_strides, vp_cache, vp_cache_strides,
-                     o, o_strides, vp_new, ws, B, Hq, Hkv, T_past, D, scale, eps, stream);
+                     o, o_strides, vp_new, ws, B, Hq, Hkv, 1, T_past, D, scale, eps, stream);
 }
 
 
-int lucid_abi_version(void) { return 3; }
+int lucid_abi_version(void) { return 4; }
 
 int lucid_set_precision(int mode) {
   g_last_error.clear();

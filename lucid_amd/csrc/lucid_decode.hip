@@ -1,49 +1,58 @@
-// LUCID decoding step on CDNA4 (gfx950): one new token per sequence against a
-// (K, V') cache, with the exact preconditioner row (modeling_lucid.py:576-598 is
-// the reference seam; its V' update drops the division by the diagonal P_tt, kept
-// here so that a decoded row equals the same row of a prefill):
-//   P_tj = exp(s r_t r_j (k_t . k_j) - 1/s),  r = 1 / rms(k)  (j < t)
+// LUCID decoding step on CDNA4 (gfx950): L new tokens per sequence against a (K, V')
+// cache, with the exact preconditioner rows (modeling_lucid.py:576-598 is the reference
+// seam; its V' update drops the division by the diagonal P_tt and the coupling among the
+// new tokens, both kept here so that decoded rows equal the same rows of a prefill):
+//   P_tj = exp(s r_t r_j (k_t . k_j) - 1/s),  r = 1 / rms(k)  (j < t, cached or new)
 //   v'_t = (v_t - sum_{j<t} P_tj v'_j) / P_tt,  P_tt = exp(s dn ms_t / (ms_t + eps) - 1/s)
-// (dn: the head dim; rows may be zero-padded beyond it, ms = sum k^2 / dn)
-//   o_g  = softmax_j(s q_g . k_j) v'_j over j <= t, for the G query heads of the kv head
-// Both sums read every cached row once (memory bound), so one pass over the cache
-// computes them together, split over the sequence (flash-decoding):
-//   lucid_decode_split_kernel    per (split, kv head): partial sum_j P_tj v'_j and the
-//                                online-softmax state (m, l, O) of every query head, as
-//                                MFMA tiles (the G query heads and the token's key are
-//                                the columns of one score tile)
-//   lucid_decode_combine_kernel  per (kv head, query head): v'_t, the token's own
-//                                softmax term, the output, and the append of (k_t, v'_t)
-//                                to the cache
+//   o_tg = softmax_j(s q_tg . k_j) v'_j over j <= t, for the G query heads of the kv head
+// (dn: the head dim; rows may be zero-padded beyond it, ms = sum k^2 / dn).
+// The cached part of both sums reads every cached row once (memory bound), so one pass
+// over the cache computes it for all L tokens together, split over the sequence
+// (flash-decoding):
+//   lucid_decode_split_kernel    per (split, kv head): partial sum_j P_tj v'_j of every new
+//                                token and the online-softmax state (m, l, O) of every
+//                                (token, query head), as MFMA tiles (the L (G + 1) query
+//                                heads and new keys are the columns of one score tile)
+//   lucid_decode_combine_kernel  per (kv head, query head): merges the splits, solves the
+//                                new tokens' rows in order (their coupling among each
+//                                other), adds the new keys to each token's softmax, writes
+//                                the outputs and appends (k_t, v'_t) to the caches
 #include "lucid_common.h"
 
 namespace lucid {
 
 constexpr float DEC_NEG = -1e30f;  // finite "minus infinity" for empty softmax states
 
+// Tokens of one pass: the L (G + 1) columns of a 32-column score tile.
+template <int G>
+constexpr int decode_tokens_per_pass() {
+  return 32 / (G + 1);
+}
+
 struct DecodePartials {
-  float* a;  // [nsplit][BH][D]     sum_j P_tj v'_j
-  float* m;  // [nsplit][BH][G]     running max (log2 domain)
-  float* l;  // [nsplit][BH][G]     running sum
-  float* o;  // [nsplit][BH][G][D]  unnormalised output
+  float* a;  // [nsplit][BH][L][D]     sum_j P_tj v'_j over the split's cached rows
+  float* m;  // [nsplit][BH][L*G]      running max (log2 domain), column t*G + g
+  float* l;  // [nsplit][BH][L*G]      running sum
+  float* o;  // [nsplit][BH][L*G][D]   unnormalised output
 };
 
 // Split pass on the matrix cores.  Each wave sweeps its own 32-key tiles of the split
 // (tiles w, w+4, ...) and computes, per tile, one MFMA score tile
-//   S^T[j][c] = K_j . X_c,  X_c = q_{hG+c} (c < G),  X_G = k_t,  other columns zero,
-// so the G query heads and the preconditioner row of the new token share one product.
-// Column c < G takes the online softmax p = exp2(s' S - m_c); column G takes
-// p = exp2(s' r_t r_j S - 1/s log2 e), with 1/rms r_j of the cached key from the key
-// registers.  O^T[d][c] += V'^T[d][j] p^T[j][c] (V' rows staged per wave into LDS by
-// direct loads and read transposed) accumulates the G outputs and, in column G, the
-// sum_j P_tj v'_j.  Keys reach registers one tile ahead; no barrier in the sweep.
+//   S^T[j][c] = K_j . X_c,  column c = t (G + 1) + i:  X_c = q_{t, hG+i} (i < G),  k_t (i = G),
+// other columns zero, so every query head and the preconditioner row of every new token
+// share one product.  Query columns take the online softmax p = exp2(s' S - m_c); key
+// columns take p = exp2(s' r_t r_j S - 1/s log2 e), with 1/rms r_j of the cached key from
+// the key registers and r_t of the column's own key.  O^T[d][c] += V'^T[d][j] p^T[j][c]
+// (V' rows staged per wave into LDS by direct loads and read transposed) accumulates the
+// outputs and, in the key columns, sum_j P_tj v'_j.  Keys reach registers one tile ahead;
+// no barrier in the sweep.  Every new token sees every cached row (all are earlier).
 template <int D, int G>
 struct DecodeMfmaSmem {
   union {
     bf16 v[4][2][32 * D];  // per wave, double buffered, swizzled (chunk c of row r at c ^ (r & 7))
     struct {
-      float so[4][G + 1][D];  // per wave: columns 0..G of O^T
-      float m[4][G], l[4][G];
+      float so[4][32][D];  // per wave: the columns of O^T
+      float m[4][32], l[4][32];
     } fin;
   } u;
   float nn[4][32];  // per wave: squared norms of the tile's keys
@@ -53,7 +62,7 @@ template <int D, int G>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void lucid_decode_split_kernel(
     const bf16* __restrict__ q, Strides qs, const bf16* __restrict__ kn, Strides kns,
     const bf16* __restrict__ kc, Strides kcs, const bf16* __restrict__ vc, Strides vcs, int Hkv, int Tp, int KS,
-    float scale, float eps, float dn, DecodePartials part) {
+    int L, float scale, float eps, float dn, DecodePartials part) {
   constexpr int NKS = D / 16, NDT = D / 32, CPR = D / 8, NST = 32 * CPR / 64;  // NST: staging loads per tile
   static_assert(G + 1 <= 32, "query heads + the preconditioner row must fit one 32-column tile");
   __shared__ __attribute__((aligned(16))) DecodeMfmaSmem<D, G> sm;
@@ -61,6 +70,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void l
   const int b = bh / Hkv, h = bh - b * Hkv;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
   const int col = l32;  // score / output column of this lane
+  const int tok = col / (G + 1), hi = col - tok * (G + 1);
+  const bool valid = tok < L, isq = valid && hi < G, isk = valid && hi == G;
   const int j0 = s * KS, j1 = min(Tp, j0 + KS);
 
   // B operand: column col of X^T (k = d), zero for the padding columns
@@ -69,10 +80,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void l
 #pragma unroll
   for (int st = 0; st < NKS; ++st) {
     bf16x8 x;
-    if (col < G) {
-      x = ld8(q + b * qs.b + (h * G + col) * qs.h + 16 * st + 8 * g);
-    } else if (col == G) {
-      x = ld8(kn + b * kns.b + h * kns.h + 16 * st + 8 * g);
+    if (isq) {
+      x = ld8(q + b * qs.b + (h * G + hi) * qs.h + (int64_t)tok * qs.t + 16 * st + 8 * g);
+    } else if (isk) {
+      x = ld8(kn + b * kns.b + h * kns.h + (int64_t)tok * kns.t + 16 * st + 8 * g);
 #pragma unroll
       for (int e = 0; e < 8; ++e) nt = fmaf((float)x[e], (float)x[e], nt);
     } else {
@@ -81,8 +92,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void l
     }
     xb[st] = x;
   }
-  nt = wave_sum32(nt);
-  const float rt = rsqrtf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, nt), G)) / dn + eps);
+  nt = wave_sum32(nt);  // squared norm of this column's key (both lane halves)
+  const float rt = rsqrtf(nt / dn + eps);
   const float sl2 = scale * LOG2E_F, c1 = sl2 * rt, c0 = LOG2E_F / scale;
 
   f32x16 oacc[NDT];
@@ -138,7 +149,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void l
 #pragma unroll
     for (int e = 0; e < 16; ++e)
       if (jb + drow(e, g) < j1) mx = fmaxf(mx, sc[e]);
-    mx = (col < G) ? wave_max32(mx) * sl2 : DEC_NEG;
+    mx = isq ? wave_max32(mx) * sl2 : DEC_NEG;
     if (__builtin_amdgcn_ballot_w64(mx > m + 8.0f)) {
       const float mnew = fmaxf(m, mx);
       const float al = __builtin_amdgcn_exp2f(m - mnew);
@@ -147,14 +158,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void l
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) oacc[dt][e] *= (col < G) ? al : 1.f;
+        for (int e = 0; e < 16; ++e) oacc[dt][e] *= isq ? al : 1.f;
     }
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-      const bool ok = jb + drow(e, g) < j1 && col <= G;
-      const float arg = (col < G) ? fmaf(sc[e], sl2, -m) : fmaf(c1 * rsqrtf(nr[e] / dn + eps), sc[e], -c0);
+      const bool ok = jb + drow(e, g) < j1 && valid;
+      const float arg = isq ? fmaf(sc[e], sl2, -m) : fmaf(c1 * rsqrtf(nr[e] / dn + eps), sc[e], -c0);
       const float p = ok ? __builtin_amdgcn_exp2f(arg) : 0.f;
-      if (col < G) l += p;
+      if (isq) l += p;
       sc[e] = p;
     }
     const bf16x8 p0 = pack_b(sc, 0), p1 = pack_b(sc, 1);
@@ -176,113 +187,170 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void l
   }
   l = wave_sum32(l);
   __syncthreads();  // every wave is done with its staging buffers (aliased below)
-  if (col <= G) {
+  if (valid) {
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
       for (int e = 0; e < 16; ++e) sm.u.fin.so[w][col][dt * 32 + drow(e, g)] = oacc[dt][e];
-    if (col < G && g == 0) {
+    if (isq && g == 0) {
       sm.u.fin.m[w][col] = m;
       sm.u.fin.l[w][col] = l;
     }
   }
   __syncthreads();
-  // combine the 4 waves: thread d of the first D threads owns column d
+  // combine the 4 waves: thread d of the first D threads owns column d of every token
   if (tid < D) {
     const int d = tid;
-    part.a[((int64_t)s * BH + bh) * D + d] =
-        sm.u.fin.so[0][G][d] + sm.u.fin.so[1][G][d] + sm.u.fin.so[2][G][d] + sm.u.fin.so[3][G][d];
+    for (int t = 0; t < L; ++t) {
+      const int ck = t * (G + 1) + G;
+      part.a[(((int64_t)s * BH + bh) * L + t) * D + d] =
+          sm.u.fin.so[0][ck][d] + sm.u.fin.so[1][ck][d] + sm.u.fin.so[2][ck][d] + sm.u.fin.so[3][ck][d];
 #pragma unroll
-    for (int gg = 0; gg < G; ++gg) {
-      const float mn = fmaxf(fmaxf(sm.u.fin.m[0][gg], sm.u.fin.m[1][gg]), fmaxf(sm.u.fin.m[2][gg], sm.u.fin.m[3][gg]));
-      float lt = 0.f, ot = 0.f;
+      for (int gg = 0; gg < G; ++gg) {
+        const int cq = t * (G + 1) + gg;
+        const float mn =
+            fmaxf(fmaxf(sm.u.fin.m[0][cq], sm.u.fin.m[1][cq]), fmaxf(sm.u.fin.m[2][cq], sm.u.fin.m[3][cq]));
+        float lt = 0.f, ot = 0.f;
 #pragma unroll
-      for (int ww = 0; ww < 4; ++ww) {
-        const float al = __builtin_amdgcn_exp2f(sm.u.fin.m[ww][gg] - mn);
-        lt = fmaf(sm.u.fin.l[ww][gg], al, lt);
-        ot = fmaf(sm.u.fin.so[ww][gg][d], al, ot);
-      }
-      part.o[(((int64_t)s * BH + bh) * G + gg) * D + d] = ot;
-      if (d == 0) {
-        part.m[((int64_t)s * BH + bh) * G + gg] = mn;
-        part.l[((int64_t)s * BH + bh) * G + gg] = lt;
+        for (int ww = 0; ww < 4; ++ww) {
+          const float al = __builtin_amdgcn_exp2f(sm.u.fin.m[ww][cq] - mn);
+          lt = fmaf(sm.u.fin.l[ww][cq], al, lt);
+          ot = fmaf(sm.u.fin.so[ww][cq][d], al, ot);
+        }
+        const int64_t pi = ((int64_t)s * BH + bh) * (L * G) + t * G + gg;
+        part.o[pi * D + d] = ot;
+        if (d == 0) {
+          part.m[pi] = mn;
+          part.l[pi] = lt;
+        }
       }
     }
   }
 }
 
-// grid (B*Hkv, G): workgroup (kv head, query head g).  The 256 threads are NSL = 256/D
-// split lanes x D columns; each split lane reduces every NSL-th partial, then the
-// lanes are combined in LDS.  Every workgroup of a kv head computes v'_t; the g = 0
-// one writes it and appends (k_t, v'_t) to the caches.
+// grid (B*Hkv, G): workgroup (kv head, query head g), for the L tokens of the pass.  The
+// 256 threads are NSL = 256/D split lanes x D columns; each split lane reduces every
+// NSL-th partial, then the lanes are combined in LDS.  The new tokens' own rows follow in
+// order: v'_t needs v'_u of the earlier new tokens (u < t), each column d only its own
+// column, so thread d solves column d of every token without a barrier.  Every
+// workgroup of a kv head computes the v'_t; the g = 0 one writes them and appends
+// (k_t, v'_t) to the caches at rows Tp + t.
 template <int D, int G>
 __global__ __launch_bounds__(256) void lucid_decode_combine_kernel(
-    int nsplit, const bf16* __restrict__ q, Strides qs, const bf16* __restrict__ kn, Strides kns,
+    int nsplit, int L, const bf16* __restrict__ q, Strides qs, const bf16* __restrict__ kn, Strides kns,
     const bf16* __restrict__ vn, Strides vns, bf16* __restrict__ kc, Strides kcs, bf16* __restrict__ vc, Strides vcs,
-    bf16* __restrict__ o, Strides os, float* __restrict__ vp_new, int Hkv, int Tp, float scale, float eps, float dn,
-    DecodePartials part) {
+    bf16* __restrict__ o, Strides os, float* __restrict__ vp_new, int vp_rows, int Hkv, int Tp, float scale,
+    float eps, float dn, DecodePartials part) {
   constexpr int NSL = 256 / D;
-  __shared__ float ra[NSL][D], ro[NSL][D], rm[NSL], rl[NSL], dots[2][D];
+  constexpr int LM = decode_tokens_per_pass<G>();
+  __shared__ float ra[NSL][D], ro[NSL][D], rm[NSL], rl[NSL];
+  __shared__ float at[LM][D], ot[LM][D], lt[LM], mt[LM];
+  __shared__ float kk[LM][LM], qk[LM][LM];  // k_t . k_u (u <= t) and q_tg . k_u (u <= t)
   const int bh = blockIdx.x, BH = gridDim.x, g = blockIdx.y;
   const int b = bh / Hkv, h = bh - b * Hkv;
   const int tid = threadIdx.x, sl = tid / D, d = tid - sl * D;
   const int hq = h * G + g;
-  // running max of this query head over the splits
-  float mx = DEC_NEG;
-#pragma unroll 8
-  for (int s = sl; s < nsplit; s += NSL) mx = fmaxf(mx, part.m[((int64_t)s * BH + bh) * G + g]);
-  if (d == 0) rm[sl] = mx;
-  if (sl == 0) {
-    const float kd = (float)kn[b * kns.b + h * kns.h + d];
-    dots[0][d] = kd * kd;
-    dots[1][d] = (float)q[b * qs.b + hq * qs.h + d] * kd;
-  }
-  __syncthreads();
-  float M = rm[0];
+  // the splits' partials of every token: its key column (sum P_tj v'_j) and its query column
+  for (int t = 0; t < L; ++t) {
+    const int64_t c = t * G + g;
+    float mx = DEC_NEG;
+    for (int s = sl; s < nsplit; s += NSL) mx = fmaxf(mx, part.m[((int64_t)s * BH + bh) * (L * G) + c]);
+    if (d == 0) rm[sl] = mx;
+    __syncthreads();
+    float M = rm[0];
 #pragma unroll
-  for (int i = 1; i < NSL; ++i) M = fmaxf(M, rm[i]);
-  float a = 0.f, lt = 0.f, ot = 0.f;
-#pragma unroll 8
-  for (int s = sl; s < nsplit; s += NSL) {
-    const int64_t i = ((int64_t)s * BH + bh) * G + g;
-    const float al = __builtin_amdgcn_exp2f(part.m[i] - M);
-    a += part.a[((int64_t)s * BH + bh) * D + d];
-    lt = fmaf(part.l[i], al, lt);
-    ot = fmaf(part.o[i * D + d], al, ot);
+    for (int i = 1; i < NSL; ++i) M = fmaxf(M, rm[i]);
+    float a = 0.f, lv = 0.f, ov = 0.f;
+    for (int s = sl; s < nsplit; s += NSL) {
+      const int64_t i = ((int64_t)s * BH + bh) * (L * G) + c;
+      const float al = __builtin_amdgcn_exp2f(part.m[i] - M);
+      a += part.a[(((int64_t)s * BH + bh) * L + t) * D + d];
+      lv = fmaf(part.l[i], al, lv);
+      ov = fmaf(part.o[i * D + d], al, ov);
+    }
+    ra[sl][d] = a;
+    ro[sl][d] = ov;
+    if (d == 0) rl[sl] = lv;
+    __syncthreads();
+    if (sl == 0) {
+#pragma unroll
+      for (int i = 1; i < NSL; ++i) {
+        a += ra[i][d];
+        ov += ro[i][d];
+      }
+      at[t][d] = a;
+      ot[t][d] = ov;
+      if (d == 0) {
+        float ls = 0.f;
+#pragma unroll
+        for (int i = 0; i < NSL; ++i) ls += rl[i];
+        lt[t] = ls;
+        mt[t] = M;
+      }
+    }
+    __syncthreads();
   }
-  ra[sl][d] = a;
-  ro[sl][d] = ot;
-  if (d == 0) rl[sl] = lt;
+  // dot products among the new tokens: k_t . k_u and q_tg . k_u for u <= t
+  for (int idx = tid; idx < L * L; idx += 256) {
+    const int t = idx / L, u = idx - t * L;
+    if (u > t) continue;
+    const bf16* kt = kn + b * kns.b + h * kns.h + (int64_t)t * kns.t;
+    const bf16* ku = kn + b * kns.b + h * kns.h + (int64_t)u * kns.t;
+    const bf16* qt = q + b * qs.b + hq * qs.h + (int64_t)t * qs.t;
+    float dkk = 0.f, dqk = 0.f;
+    for (int i = 0; i < D; i += 8) {
+      const bf16x8 a8 = ld8(kt + i), b8 = ld8(ku + i), q8 = ld8(qt + i);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        dkk = fmaf((float)a8[e], (float)b8[e], dkk);
+        dqk = fmaf((float)q8[e], (float)b8[e], dqk);
+      }
+    }
+    kk[t][u] = dkk;
+    qk[t][u] = dqk;
+  }
   __syncthreads();
   if (sl != 0) return;
-  float nk = 0.f, qk = 0.f;
-  for (int i = 0; i < D; ++i) {
-    nk += dots[0][i];
-    qk += dots[1][i];
-  }
+  // the new rows in order: v'_t = (v_t - a_t - sum_{u<t} P_tu v'_u) / P_tt
+  float vpc[LM];  // this column of v'_u (fp32)
+  const float sl2 = scale * LOG2E_F, c0 = LOG2E_F / scale;
 #pragma unroll
-  for (int i = 1; i < NSL; ++i) {
-    a += ra[i][d];
-    ot += ro[i][d];
-  }
-  lt = 0.f;
+  for (int t = 0; t < LM; ++t) {
+    if (t >= L) break;
+    const float rt = rsqrtf(kk[t][t] / dn + eps);
+    float x = (float)vn[b * vns.b + h * vns.h + (int64_t)t * vns.t + d] - at[t][d];
 #pragma unroll
-  for (int i = 0; i < NSL; ++i) lt += rl[i];
-  const float ms = nk / dn;
-  // P_tt = exp(s |K^_t|^2 - 1/s), |K^_t|^2 = dn ms / (ms + eps)
-  const float ptt = __builtin_amdgcn_exp2f(LOG2E_F * (scale * dn * ms / (ms + eps) - 1.f / scale));
-  const float vpt = ((float)vn[b * vns.b + h * vns.h + d] - a) / ptt;
-  const bf16 vpb = (bf16)vpt;
-  if (g == 0) {
-    vp_new[(int64_t)bh * D + d] = vpt;
-    kc[b * kcs.b + h * kcs.h + (int64_t)Tp * kcs.t + d] = kn[b * kns.b + h * kns.h + d];
-    vc[b * vcs.b + h * vcs.h + (int64_t)Tp * vcs.t + d] = vpb;
+    for (int u = 0; u < t; ++u) {
+      const float ru = rsqrtf(kk[u][u] / dn + eps);
+      x = fmaf(-__builtin_amdgcn_exp2f(fmaf(sl2 * rt * ru, kk[t][u], -c0)), vpc[u], x);
+    }
+    // P_tt = exp(s |K^_t|^2 - 1/s), |K^_t|^2 = dn ms / (ms + eps)
+    const float ms = kk[t][t] / dn;
+    const float ptt = __builtin_amdgcn_exp2f(LOG2E_F * (scale * dn * ms / (ms + eps) - 1.f / scale));
+    vpc[t] = x / ptt;
   }
-  // the token's own term joins the softmax
-  const float st = qk * scale * LOG2E_F;
-  const float M2 = fmaxf(M, st);
-  const float c = __builtin_amdgcn_exp2f(M - M2), es = __builtin_amdgcn_exp2f(st - M2);
-  o[b * os.b + hq * os.h + d] = (bf16)((ot * c + es * (float)vpb) / (lt * c + es));
+  // outputs: the cached part merged with the new keys u <= t (values bf16(v'_u), as cached)
+#pragma unroll
+  for (int t = 0; t < LM; ++t) {
+    if (t >= L) break;
+    float M2 = mt[t];
+#pragma unroll
+    for (int u = 0; u <= t; ++u) M2 = fmaxf(M2, qk[t][u] * sl2);
+    const float c = __builtin_amdgcn_exp2f(mt[t] - M2);
+    float num = ot[t][d] * c, den = lt[t] * c;
+#pragma unroll
+    for (int u = 0; u <= t; ++u) {
+      const float es = __builtin_amdgcn_exp2f(fmaf(qk[t][u], sl2, -M2));
+      num = fmaf(es, (float)(bf16)vpc[u], num);
+      den += es;
+    }
+    o[b * os.b + hq * os.h + (int64_t)t * os.t + d] = (bf16)(num / den);
+    if (g == 0) {
+      vp_new[((int64_t)bh * vp_rows + t) * D + d] = vpc[t];
+      kc[b * kcs.b + h * kcs.h + (int64_t)(Tp + t) * kcs.t + d] = kn[b * kns.b + h * kns.h + (int64_t)t * kns.t + d];
+      vc[b * vcs.b + h * vcs.h + (int64_t)(Tp + t) * vcs.t + d] = (bf16)vpc[t];
+    }
+  }
 }
 
 }  // namespace lucid

@@ -470,15 +470,19 @@ def causal_attention(query, key, value, scaling=None):
 
 
 def lucid_decode(query, key, value, key_cache, vprime_cache, cache_len, scaling=None, eps=1e-5):
-    """One decoding step for one new token per sequence (``get_new_v_prime`` and the cached
-    attention of LucidAttention.forward, modeling_lucid.py:475-496, 576-598).
+    """A decoding step for L new tokens per sequence (``get_new_v_prime`` for ``L_k`` new
+    tokens and the cached attention of LucidAttention.forward, modeling_lucid.py:475-496,
+    576-598), in one call.
 
-    ``query [B, Hq, 1, d]``, ``key/value [B, Hkv, 1, d]`` (bf16; keys with RoPE applied);
-    ``key_cache`` / ``vprime_cache`` are bf16 buffers ``[B, Hkv, T_cap, dp]`` whose first
-    ``cache_len`` rows are valid, ``dp`` = 64 for d <= 64 and 128 above (columns beyond d
-    zero: the head rows zero-padded).  The token's V' row (exact diagonal:
-    ``v'_t = (v_t - sum_j P_tj v'_j) / P_tt``) and its key are written at row ``cache_len``
-    of the caches in place.  Returns ``(O [B, 1, Hq, d], v'_t fp32 [B, Hkv, 1, d])``.
+    ``query [B, Hq, L, d]``, ``key/value [B, Hkv, L, d]`` (bf16; keys with RoPE applied;
+    the L tokens in sequence order); ``key_cache`` / ``vprime_cache`` are bf16 buffers
+    ``[B, Hkv, T_cap, dp]`` whose first ``cache_len`` rows are valid, ``dp`` = 64 for
+    d <= 64 and 128 above (columns beyond d zero: the head rows zero-padded).  Each token's
+    V' row is the prefill row (exact diagonal, coupled to the cache and to the earlier new
+    tokens: ``v'_t = (v_t - sum_{j<t} P_tj v'_j) / P_tt``) and each token attends to the
+    cache and to the new tokens up to itself; the keys and V' rows are written at rows
+    ``cache_len .. cache_len + L - 1`` of the caches in place.  Returns
+    ``(O [B, L, Hq, d], V' fp32 [B, Hkv, L, d])``.
     """
     _check_inputs(None, key, value)
     for name, t in (("query", query), ("key_cache", key_cache), ("vprime_cache", vprime_cache)):
@@ -487,26 +491,28 @@ def lucid_decode(query, key, value, key_cache, vprime_cache, cache_len, scaling=
     for name, t in (("key_cache", key_cache), ("vprime_cache", vprime_cache)):  # written in place: no copies
         if t.stride(-1) != 1 or any(s % 8 for s in t.stride()[:3]) or t.data_ptr() % 16:
             raise ValueError(f"lucid_amd: {name} needs a contiguous last axis and 8-element aligned strides")
-    B, Hkv, tn, d = key.shape
+    B, Hkv, L, d = key.shape
     Hq = query.shape[1]
     D = _padded_dim(d)
-    if tn != 1 or query.shape[2] != 1:
-        raise ValueError("lucid_amd: lucid_decode takes one new token per sequence")
+    if query.shape[0] != B or query.shape[2] != L or query.shape[3] != d or Hq % Hkv:
+        raise ValueError("lucid_amd: query [B, Hq, L, d] disagrees with key [B, Hkv, L, d]")
     if key_cache.shape[:2] != (B, Hkv) or vprime_cache.shape != key_cache.shape or key_cache.shape[3] != D:
         raise ValueError(f"lucid_amd: cache buffers must be [B, Hkv, T_cap, {D}] for head_dim {d}")
     lib = _lib.load()
     cap = key_cache.shape[2]
-    q, k, v = (_prep(_pad_d(t, D), 1) for t in (query, key, value))
-    o = torch.empty(B, 1, Hq, D, dtype=torch.bfloat16, device=q.device)
-    vp_new = torch.empty(B, Hkv, 1, D, dtype=torch.float32, device=q.device)
-    ws = torch.empty(max(lib.lucid_decode_workspace_bytes(B, Hq, Hkv, cap, d), 256), dtype=torch.uint8,
+    if L == 0:
+        return (query.new_empty(B, 0, Hq, d), torch.empty(B, Hkv, 0, d, dtype=torch.float32, device=query.device))
+    q, k, v = (_prep(_pad_d(t, D), L) for t in (query, key, value))
+    o = torch.empty(B, L, Hq, D, dtype=torch.bfloat16, device=q.device)
+    vp_new = torch.empty(B, Hkv, L, D, dtype=torch.float32, device=q.device)
+    ws = torch.empty(max(lib.lucid_decode_tokens_workspace_bytes(B, Hq, Hkv, L, cap, d), 256), dtype=torch.uint8,
                      device=q.device)
     scale = d ** -0.5 if scaling is None else float(scaling)
-    rc = lib.lucid_decode(
+    rc = lib.lucid_decode_tokens(
         _lib.ptr(q), _lib.strides3(q, (0, 1, 2)), _lib.ptr(k), _lib.strides3(k, (0, 1, 2)),
         _lib.ptr(v), _lib.strides3(v, (0, 1, 2)), _lib.ptr(key_cache), _lib.strides3(key_cache, (0, 1, 2)),
         _lib.ptr(vprime_cache), _lib.strides3(vprime_cache, (0, 1, 2)), _lib.ptr(o), _lib.strides3(o, (0, 2, 1)),
-        _lib.ptr(vp_new), _lib.ptr(ws), B, Hq, Hkv, int(cache_len), cap, d, scale, float(eps),
+        _lib.ptr(vp_new), _lib.ptr(ws), B, Hq, Hkv, L, int(cache_len), cap, d, scale, float(eps),
         _lib.stream_handle(q.device))
-    _lib.check(lib, rc, "lucid_decode")
+    _lib.check(lib, rc, "lucid_decode_tokens")
     return (o, vp_new) if D == d else (o[..., :d], vp_new[..., :d])

@@ -242,18 +242,15 @@ class LucidAttention(nn.Module):
         return torch.cat(outs, dim=-2)
 
     def _decode(self, q, k, v, cache: LucidCache) -> torch.Tensor:
-        """New tokens one at a time through the HIP decoding step (``lucid_decode``), which
-        computes the V' row exactly as ``get_new_v_prime`` and appends (k_t, v'_t) to the
-        cache in place; returns [B, Tn, Hq, d]."""
-        outs = []
-        for t in range(q.shape[2]):
-            cache.reserve(self.layer_idx, k, 1)
-            kb, vb, n = cache.buffers(self.layer_idx)
-            o, _ = lucid_decode(q[:, :, t:t + 1], k[:, :, t:t + 1], v[:, :, t:t + 1], kb, vb, n,
-                                scaling=self.scaling, eps=self.config.rms_norm_eps)
-            cache.advance(self.layer_idx, 1)
-            outs.append(o)
-        return outs[0] if len(outs) == 1 else torch.cat(outs, dim=1)
+        """The new tokens through one HIP decoding call (``lucid_decode``), which computes
+        their V' rows exactly as ``get_new_v_prime`` (coupled to the cache and to each
+        other) and appends (k_t, v'_t) to the cache in place; returns [B, Tn, Hq, d]."""
+        n_new = q.shape[2]
+        cache.reserve(self.layer_idx, k, n_new)
+        kb, vb, n = cache.buffers(self.layer_idx)
+        o, _ = lucid_decode(q, k, v, kb, vb, n, scaling=self.scaling, eps=self.config.rms_norm_eps)
+        cache.advance(self.layer_idx, n_new)
+        return o
 
 
 class LlamaDecoderLayer(nn.Module):

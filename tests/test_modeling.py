@@ -115,6 +115,32 @@ def test_decode_matches_prefill_logits():
     assert cache.get_seq_length() == T + n_new
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("heads,hkv,head_dim", [(2, 1, 64), (4, 1, 68)])
+def test_decode_several_tokens_in_one_call_matches_prefill_logits(heads, hkv, head_dim):
+    """Prefill, then five new tokens in one forward call (one decoding call per layer): the
+    logits equal those of the whole sequence in one prefill.  head_dim 68 is the reference
+    model's (lucid/config/config.json:9)."""
+    torch.manual_seed(4)
+    cfg = M.LucidConfig(vocab_size=512, hidden_size=heads * head_dim, intermediate_size=256, num_hidden_layers=2,
+                        num_attention_heads=heads, num_key_value_heads=hkv, head_dim=head_dim)
+    model = M.LlamaForCausalLM(cfg).to("cuda", torch.bfloat16).eval()
+    T, n_new = 200, 5
+    ids = torch.randint(0, cfg.vocab_size, (1, T + n_new), generator=torch.Generator().manual_seed(6)).cuda()
+    print(f"case decode tokens model heads={heads} hkv={hkv} head_dim={head_dim}", flush=True)
+    with torch.no_grad():
+        _, full = model(ids)
+        cache = M.LucidCache()
+        model(ids[:, :T], past_key_values=cache)
+        _, dec = model(ids[:, T:], past_key_values=cache)
+    torch.cuda.synchronize()
+    ref = full[:, T:].float()
+    err = (dec.float() - ref).abs().max().item()
+    assert err <= 2e-2 * max(1.0, ref.abs().max().item()), err
+    assert cache.get_seq_length() == T + n_new
+    assert cache.key_cache[0].shape[-1] == head_dim
+
+
 def test_cache_grows_in_place_and_keeps_rows():
     cache = M.LucidCache(min_capacity=256)
     g = torch.Generator().manual_seed(7)
