@@ -185,9 +185,10 @@ def measured_traffic(workload, kernel):
 
 
 def bench_decode(args, dev):
-    """One LUCID decoding step (one layer's attention for one new token per sequence) against
-    a full cache at the long-context shape of config 5: B=1, Hq=32 over Hkv=8, d=128,
-    T=131072 cached rows.  HBM-bound: the K and V' caches are read once per step."""
+    """One LUCID decoding step (one layer's attention for ``--decode-tokens`` L new tokens per
+    sequence, default 1) against a full cache at the long-context shape of config 5: B=1,
+    Hq=32 over Hkv=8, d=128, T=131072 cached rows.  HBM-bound: the K and V' caches are read
+    once per pass of up to 32 / (Hq/Hkv + 1) = 6 tokens."""
     import torch
 
     from lucid_amd import _lib, lucid_decode
@@ -195,14 +196,15 @@ def bench_decode(args, dev):
     B, Hq, Hkv, T, D = 1, 32, 8, 131072, 128
     g = torch.Generator().manual_seed(0)
     s = D ** -0.5
-    kc = (torch.randn(B, Hkv, T + 1, D, generator=g) * s).to(torch.bfloat16).to(dev)
-    vc = (torch.randn(B, Hkv, T + 1, D, generator=g) * s).to(torch.bfloat16).to(dev)
-    q = (torch.randn(B, Hq, 1, D, generator=g) * s).to(torch.bfloat16).to(dev)
-    k = (torch.randn(B, Hkv, 1, D, generator=g) * s).to(torch.bfloat16).to(dev)
-    v = (torch.randn(B, Hkv, 1, D, generator=g) * s).to(torch.bfloat16).to(dev)
+    L = args.decode_tokens
+    kc = (torch.randn(B, Hkv, T + L, D, generator=g) * s).to(torch.bfloat16).to(dev)
+    vc = (torch.randn(B, Hkv, T + L, D, generator=g) * s).to(torch.bfloat16).to(dev)
+    q = (torch.randn(B, Hq, L, D, generator=g) * s).to(torch.bfloat16).to(dev)
+    k = (torch.randn(B, Hkv, L, D, generator=g) * s).to(torch.bfloat16).to(dev)
+    v = (torch.randn(B, Hkv, L, D, generator=g) * s).to(torch.bfloat16).to(dev)
     lib = _lib.load()
 
-    def step():  # every step decodes row T against rows [0, T) (same work each time)
+    def step():  # every step decodes rows T .. T+L-1 against rows [0, T) (same work each time)
         lucid_decode(q, k, v, kc, vc, T)
 
     for _ in range(args.warmup):
@@ -222,12 +224,12 @@ def bench_decode(args, dev):
                sorted(totals.items(), key=lambda kv: -kv[1][0])}
     dom = "lucid_decode_split_kernel"
     dom_avg = totals[dom][0] / totals[dom][1]
-    nbytes = 2.0 * B * Hkv * T * D * 2  # K and V' caches, bf16, read once
+    nbytes = 2.0 * B * Hkv * T * D * 2  # K and V' caches, bf16, read once per split pass
     achieved = nbytes / (dom_avg / 1e3) / 1e9
-    traffic = measured_traffic("decode", dom)
+    traffic = measured_traffic("decode", dom) if L == 1 else None
     out = {
-        "metric": "LUCID decode step (one layer, one new token) tokens/s at T=128K cache (config-5 shape)",
-        "value": round(B / (ms / 1e3), 1),
+        "metric": "LUCID decode step (one layer, L new tokens) tokens/s at T=128K cache (config-5 shape)",
+        "value": round(B * L / (ms / 1e3), 1),
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": args.steps,
@@ -239,7 +241,7 @@ def bench_decode(args, dev):
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1)/sqrt(d) caches and token)",
         "config": {"workload": "lucid_decode_step", "B": B, "Hq": Hq, "Hkv": Hkv, "T_cache": T, "head_dim": D,
-                   "parallelism": "single GPU"},
+                   "new_tokens": L, "parallelism": "single GPU"},
         "roofline": {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "algorithmic_bytes": nbytes},
@@ -369,6 +371,8 @@ def main():
     ap.add_argument("--keys", default="iid", choices=["iid", "correlated"],
                     help="iid: the BASELINE inputs; correlated: every key = a shared direction + 0.1 N(0,1) "
                          "(row mass ~T, the exact chains under --precision auto)")
+    ap.add_argument("--decode-tokens", type=int, default=1,
+                    help="new tokens per decoding call (--workload decode)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-causal", action="store_true")
     ap.add_argument("--copy-bytes", type=int, default=0,

@@ -229,67 +229,33 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void l
 }
 
 // grid (B*Hkv, G): workgroup (kv head, query head g), for the L tokens of the pass.  The
-// 256 threads are NSL = 256/D split lanes x D columns; each split lane reduces every
-// NSL-th partial, then the lanes are combined in LDS.  The new tokens' own rows follow in
-// order: v'_t needs v'_u of the earlier new tokens (u < t), each column d only its own
-// column, so thread d solves column d of every token without a barrier.  Every
-// workgroup of a kv head computes the v'_t; the g = 0 one writes them and appends
-// (k_t, v'_t) to the caches at rows Tp + t.
+// 256 threads are D/4 column groups (4 columns each, 16-byte loads) x NSL = 1024/D split
+// lanes, the lanes of one group adjacent in the wave: each lane merges every NSL-th split
+// of every token at once (online rescaling; the tokens' loads interleave), then the
+// lanes of a group are merged by lane shuffles.  The new tokens' own rows follow in
+// order: v'_t needs v'_u of the earlier new tokens (u < t), each column only its own
+// column, so the first lane of each group solves its 4 columns of every token without a
+// barrier.  Every workgroup of a kv head computes the v'_t; the g = 0 one writes them and
+// appends (k_t, v'_t) to the caches at rows Tp + t.
 template <int D, int G>
 __global__ __launch_bounds__(256) void lucid_decode_combine_kernel(
     int nsplit, int L, const bf16* __restrict__ q, Strides qs, const bf16* __restrict__ kn, Strides kns,
     const bf16* __restrict__ vn, Strides vns, bf16* __restrict__ kc, Strides kcs, bf16* __restrict__ vc, Strides vcs,
     bf16* __restrict__ o, Strides os, float* __restrict__ vp_new, int vp_rows, int Hkv, int Tp, float scale,
     float eps, float dn, DecodePartials part) {
-  constexpr int NSL = 256 / D;
+  constexpr int CG = D / 4, NSL = 256 / CG;
+  static_assert(NSL * CG == 256 && NSL <= 64 && (NSL & (NSL - 1)) == 0, "split lanes of a group within a wave");
   constexpr int LM = decode_tokens_per_pass<G>();
-  __shared__ float ra[NSL][D], ro[NSL][D], rm[NSL], rl[NSL];
-  __shared__ float at[LM][D], ot[LM][D], lt[LM], mt[LM];
   __shared__ float kk[LM][LM], qk[LM][LM];  // k_t . k_u (u <= t) and q_tg . k_u (u <= t)
+  // merged O, sum_j P_tj v'_j and the new v' rows of every token
+  __shared__ __attribute__((aligned(16))) float ovs[LM][D];
+  __shared__ __attribute__((aligned(16))) float avs[LM][D];
+  __shared__ __attribute__((aligned(16))) float vps[LM][D];
+  __shared__ float ms_[LM], ls_[LM];                                              // merged max and sum
   const int bh = blockIdx.x, BH = gridDim.x, g = blockIdx.y;
   const int b = bh / Hkv, h = bh - b * Hkv;
-  const int tid = threadIdx.x, sl = tid / D, d = tid - sl * D;
+  const int tid = threadIdx.x, cg = tid / NSL, sl = tid - cg * NSL, d0 = 4 * cg;
   const int hq = h * G + g;
-  // the splits' partials of every token: its key column (sum P_tj v'_j) and its query column
-  for (int t = 0; t < L; ++t) {
-    const int64_t c = t * G + g;
-    float mx = DEC_NEG;
-    for (int s = sl; s < nsplit; s += NSL) mx = fmaxf(mx, part.m[((int64_t)s * BH + bh) * (L * G) + c]);
-    if (d == 0) rm[sl] = mx;
-    __syncthreads();
-    float M = rm[0];
-#pragma unroll
-    for (int i = 1; i < NSL; ++i) M = fmaxf(M, rm[i]);
-    float a = 0.f, lv = 0.f, ov = 0.f;
-    for (int s = sl; s < nsplit; s += NSL) {
-      const int64_t i = ((int64_t)s * BH + bh) * (L * G) + c;
-      const float al = __builtin_amdgcn_exp2f(part.m[i] - M);
-      a += part.a[(((int64_t)s * BH + bh) * L + t) * D + d];
-      lv = fmaf(part.l[i], al, lv);
-      ov = fmaf(part.o[i * D + d], al, ov);
-    }
-    ra[sl][d] = a;
-    ro[sl][d] = ov;
-    if (d == 0) rl[sl] = lv;
-    __syncthreads();
-    if (sl == 0) {
-#pragma unroll
-      for (int i = 1; i < NSL; ++i) {
-        a += ra[i][d];
-        ov += ro[i][d];
-      }
-      at[t][d] = a;
-      ot[t][d] = ov;
-      if (d == 0) {
-        float ls = 0.f;
-#pragma unroll
-        for (int i = 0; i < NSL; ++i) ls += rl[i];
-        lt[t] = ls;
-        mt[t] = M;
-      }
-    }
-    __syncthreads();
-  }
   // dot products among the new tokens: k_t . k_u and q_tg . k_u for u <= t
   for (int idx = tid; idx < L * L; idx += 256) {
     const int t = idx / L, u = idx - t * L;
@@ -298,6 +264,7 @@ __global__ __launch_bounds__(256) void lucid_decode_combine_kernel(
     const bf16* ku = kn + b * kns.b + h * kns.h + (int64_t)u * kns.t;
     const bf16* qt = q + b * qs.b + hq * qs.h + (int64_t)t * qs.t;
     float dkk = 0.f, dqk = 0.f;
+#pragma unroll
     for (int i = 0; i < D; i += 8) {
       const bf16x8 a8 = ld8(kt + i), b8 = ld8(ku + i), q8 = ld8(qt + i);
 #pragma unroll
@@ -309,46 +276,126 @@ __global__ __launch_bounds__(256) void lucid_decode_combine_kernel(
     kk[t][u] = dkk;
     qk[t][u] = dqk;
   }
-  __syncthreads();
-  if (sl != 0) return;
-  // the new rows in order: v'_t = (v_t - a_t - sum_{u<t} P_tu v'_u) / P_tt
-  float vpc[LM];  // this column of v'_u (fp32)
-  const float sl2 = scale * LOG2E_F, c0 = LOG2E_F / scale;
+  // the splits' partials of every token: its key column (sum P_tj v'_j) and its query
+  // column (t, g), merged with a running max per token
+  float M[LM], lv[LM];
+  f32x4 ov[LM], av[LM];
 #pragma unroll
   for (int t = 0; t < LM; ++t) {
-    if (t >= L) break;
-    const float rt = rsqrtf(kk[t][t] / dn + eps);
-    float x = (float)vn[b * vns.b + h * vns.h + (int64_t)t * vns.t + d] - at[t][d];
+    M[t] = DEC_NEG;
+    lv[t] = 0.f;
+    ov[t] = av[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  for (int s = sl; s < nsplit; s += NSL) {
+    const int64_t base = ((int64_t)s * BH + bh) * (L * G) + g;
 #pragma unroll
+    for (int t = 0; t < LM; ++t) {
+      if (t < L) {
+        const int64_t i = base + t * G;
+        const float mi = part.m[i], li = part.l[i];
+        const f32x4 oi = *reinterpret_cast<const f32x4*>(part.o + i * D + d0);
+        const f32x4 ai = *reinterpret_cast<const f32x4*>(part.a + (((int64_t)s * BH + bh) * L + t) * D + d0);
+        const float mn = fmaxf(M[t], mi);
+        const float c = __builtin_amdgcn_exp2f(M[t] - mn), e = __builtin_amdgcn_exp2f(mi - mn);
+        lv[t] = fmaf(lv[t], c, li * e);
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+          ov[t][x] = fmaf(ov[t][x], c, oi[x] * e);
+          av[t][x] += ai[x];
+        }
+        M[t] = mn;
+      }
+    }
+  }
+  // merge the NSL adjacent split lanes of each column group
+#pragma unroll
+  for (int off = 1; off < NSL; off <<= 1) {
+#pragma unroll
+    for (int t = 0; t < LM; ++t) {
+      if (t < L) {
+        const float mo = __shfl_xor(M[t], off, 64), lo = __shfl_xor(lv[t], off, 64);
+        const float mn = fmaxf(M[t], mo);
+        const float c = __builtin_amdgcn_exp2f(M[t] - mn), co = __builtin_amdgcn_exp2f(mo - mn);
+        lv[t] = fmaf(lv[t], c, lo * co);
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+          ov[t][x] = fmaf(ov[t][x], c, __shfl_xor(ov[t][x], off, 64) * co);
+          av[t][x] += __shfl_xor(av[t][x], off, 64);
+        }
+        M[t] = mn;
+      }
+    }
+  }
+  // the merged state of every token into LDS (the first lane of each column group)
+  if (sl == 0) {
+#pragma unroll
+    for (int t = 0; t < LM; ++t) {
+      if (t < L) {
+        *reinterpret_cast<f32x4*>(&ovs[t][d0]) = ov[t];
+        *reinterpret_cast<f32x4*>(&avs[t][d0]) = av[t];
+        if (cg == 0) {
+          ms_[t] = M[t];
+          ls_[t] = lv[t];
+        }
+      }
+    }
+  }
+  __syncthreads();  // kk, qk and the merged states
+  if (sl != 0) return;
+  // the new rows in order: v'_t = (v_t - a_t - sum_{u<t} P_tu v'_u) / P_tt (columns d0 .. d0+3)
+  const float sl2 = scale * LOG2E_F, c0 = LOG2E_F / scale;
+  for (int t = 0; t < L; ++t) {
+    const float rt = rsqrtf(kk[t][t] / dn + eps);
+    const bf16x4 v4 = *reinterpret_cast<const bf16x4*>(vn + b * vns.b + h * vns.h + (int64_t)t * vns.t + d0);
+    const f32x4 a4 = *reinterpret_cast<const f32x4*>(&avs[t][d0]);
+    f32x4 x;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) x[j] = (float)v4[j] - a4[j];
     for (int u = 0; u < t; ++u) {
       const float ru = rsqrtf(kk[u][u] / dn + eps);
-      x = fmaf(-__builtin_amdgcn_exp2f(fmaf(sl2 * rt * ru, kk[t][u], -c0)), vpc[u], x);
+      const float p = __builtin_amdgcn_exp2f(fmaf(sl2 * rt * ru, kk[t][u], -c0));
+      const f32x4 vu = *reinterpret_cast<const f32x4*>(&vps[u][d0]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x[j] = fmaf(-p, vu[j], x[j]);
     }
     // P_tt = exp(s |K^_t|^2 - 1/s), |K^_t|^2 = dn ms / (ms + eps)
     const float ms = kk[t][t] / dn;
-    const float ptt = __builtin_amdgcn_exp2f(LOG2E_F * (scale * dn * ms / (ms + eps) - 1.f / scale));
-    vpc[t] = x / ptt;
+    const float inv = 1.f / __builtin_amdgcn_exp2f(LOG2E_F * (scale * dn * ms / (ms + eps) - 1.f / scale));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) x[j] *= inv;
+    *reinterpret_cast<f32x4*>(&vps[t][d0]) = x;  // read back only by this thread
   }
   // outputs: the cached part merged with the new keys u <= t (values bf16(v'_u), as cached)
-#pragma unroll
-  for (int t = 0; t < LM; ++t) {
-    if (t >= L) break;
-    float M2 = mt[t];
-#pragma unroll
+  for (int t = 0; t < L; ++t) {
+    float M2 = ms_[t];
     for (int u = 0; u <= t; ++u) M2 = fmaxf(M2, qk[t][u] * sl2);
-    const float c = __builtin_amdgcn_exp2f(mt[t] - M2);
-    float num = ot[t][d] * c, den = lt[t] * c;
+    const float c = __builtin_amdgcn_exp2f(ms_[t] - M2);
+    const f32x4 o4 = *reinterpret_cast<const f32x4*>(&ovs[t][d0]);
+    f32x4 num;
 #pragma unroll
+    for (int j = 0; j < 4; ++j) num[j] = o4[j] * c;
+    float den = ls_[t] * c;
     for (int u = 0; u <= t; ++u) {
       const float es = __builtin_amdgcn_exp2f(fmaf(qk[t][u], sl2, -M2));
-      num = fmaf(es, (float)(bf16)vpc[u], num);
+      const f32x4 vu = *reinterpret_cast<const f32x4*>(&vps[u][d0]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) num[j] = fmaf(es, (float)(bf16)vu[j], num[j]);
       den += es;
     }
-    o[b * os.b + hq * os.h + (int64_t)t * os.t + d] = (bf16)(num / den);
+    const float rden = 1.f / den;
+    const f32x4 vt = *reinterpret_cast<const f32x4*>(&vps[t][d0]);
+    bf16x4 ob, vb;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      ob[j] = (bf16)(num[j] * rden);
+      vb[j] = (bf16)vt[j];
+    }
+    *reinterpret_cast<bf16x4*>(o + b * os.b + hq * os.h + (int64_t)t * os.t + d0) = ob;
     if (g == 0) {
-      vp_new[((int64_t)bh * vp_rows + t) * D + d] = vpc[t];
-      kc[b * kcs.b + h * kcs.h + (int64_t)(Tp + t) * kcs.t + d] = kn[b * kns.b + h * kns.h + (int64_t)t * kns.t + d];
-      vc[b * vcs.b + h * vcs.h + (int64_t)(Tp + t) * vcs.t + d] = (bf16)vpc[t];
+      *reinterpret_cast<f32x4*>(vp_new + ((int64_t)bh * vp_rows + t) * D + d0) = vt;
+      *reinterpret_cast<bf16x4*>(kc + b * kcs.b + h * kcs.h + (int64_t)(Tp + t) * kcs.t + d0) =
+          *reinterpret_cast<const bf16x4*>(kn + b * kns.b + h * kns.h + (int64_t)t * kns.t + d0);
+      *reinterpret_cast<bf16x4*>(vc + b * vcs.b + h * vcs.h + (int64_t)(Tp + t) * vcs.t + d0) = vb;
     }
   }
 }
