@@ -43,6 +43,7 @@ def causal_flops(B, Hq, T, D):
 KERNEL_FLOPS = {
     "lucid_precond_fwd_kernel": lambda B, Hq, Hkv, T, D: 2.0 * T * T * D * B * Hkv,   # K^K^T, P V'
     "lucid_attn_fwd_kernel": lambda B, Hq, Hkv, T, D: 2.0 * T * T * D * B * Hq,       # QK^T, P V'
+    "lucid_attn_fwd_wide_kernel": lambda B, Hq, Hkv, T, D: 2.0 * T * T * D * B * Hq,  # the same at head dim 128
     "lucid_attn_bwd_dkdv_kernel": lambda B, Hq, Hkv, T, D: 4.0 * T * T * D * B * Hq,  # S, dV', dP, dK
     "lucid_attn_bwd_dq_kernel": lambda B, Hq, Hkv, T, D: 1.0 * T * T * D * B * Hq,    # dQ
     "lucid_precond_bwd_col_kernel": lambda B, Hq, Hkv, T, D: 4.0 * T * T * D * B * Hkv,  # P, P^T dV, dV V'^T, M^T K^
@@ -440,8 +441,8 @@ def main():
             o.backward(do)
         if fwd_only:
             flops = 2.0 * T * T * D * B * (Hq + Hkv)
-            kflops = {"lucid_precond_fwd_kernel": KERNEL_FLOPS["lucid_precond_fwd_kernel"](B, Hq, Hkv, T, D),
-                      "lucid_attn_fwd_kernel": KERNEL_FLOPS["lucid_attn_fwd_kernel"](B, Hq, Hkv, T, D)}
+            kflops = {n: KERNEL_FLOPS[n](B, Hq, Hkv, T, D) for n in
+                      ("lucid_precond_fwd_kernel", "lucid_attn_fwd_kernel", "lucid_attn_fwd_wide_kernel")}
         else:
             flops = lucid_flops(B, Hq, Hkv, T, D)
             kflops = {n: f(B, Hq, Hkv, T, D) for n, f in KERNEL_FLOPS.items()}

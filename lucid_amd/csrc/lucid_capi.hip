@@ -185,6 +185,8 @@ int check_tensor(const char* name, const void* p, const int64_t* s) {
 lucid::Strides S(const int64_t* s) { return lucid::Strides{s[0], s[1], s[2]}; }
 
 #define LUCID_LAUNCH(NAME, KERNEL, GRID, ST, ...) LUCID_TIMED_LAUNCH(hip_status, NAME, KERNEL, GRID, ST, __VA_ARGS__)
+#define LUCID_LAUNCH_B(NAME, KERNEL, GRID, BLOCK, ST, ...) \
+  LUCID_TIMED_LAUNCH_B(hip_status, NAME, KERNEL, GRID, BLOCK, ST, __VA_ARGS__)
 
 template <int D>
 int launch_precond_fwd(const void* k, const int64_t* ks, const void* v, const int64_t* vs, float* vprime,
@@ -212,16 +214,30 @@ int launch_precond_fwd(const void* k, const int64_t* ks, const void* v, const in
   return LUCID_OK;
 }
 
+// Causal attention on the V' operands of w (bf16): the 256-thread kernel at head dim 64,
+// the eight-wave kernel at 128.
+template <int D>
+int launch_attn_fwd(const void* q, const int64_t* qs, const void* k, const int64_t* ks, void* o, const int64_t* os,
+                    float* lse, const FwdWs& w, int B, int Hq, int Hkv, int T, float scale, hipStream_t st) {
+  const int BHq = B * Hq;
+  if constexpr (D == 128) {
+    LUCID_LAUNCH_B("lucid_attn_fwd_wide_kernel", lucid::lucid_attn_fwd_wide_kernel<D>, dim3(((T + 255) / 256) * BHq),
+                   dim3(512), st, (const bf16*)q, S(qs), (const bf16*)k, S(ks), w.vpt, (bf16*)o, S(os), lse, w.mass,
+                   w.olo, Hq, Hkv, T, B * Hkv, scale);
+  } else {
+    LUCID_LAUNCH("lucid_attn_fwd_kernel", lucid::lucid_attn_fwd_kernel<D>, dim3(((T + 255) / 256) * BHq), st,
+                 (const bf16*)q, S(qs), (const bf16*)k, S(ks), w.vpt, (bf16*)o, S(os), lse, w.mass, w.olo, Hq, Hkv,
+                 T, BHq, scale, lucid::Lo{}, nullptr);
+  }
+  return LUCID_OK;
+}
+
 template <int D>
 int launch_fwd(const void* q, const int64_t* qs, const void* k, const int64_t* ks, const void* v, const int64_t* vs,
                void* o, const int64_t* os, float* vprime, float* lse, const FwdWs& w, int B, int Hq, int Hkv, int T,
                float scale, float eps, float dn, hipStream_t st) {
   if (int rc = launch_precond_fwd<D>(k, ks, v, vs, vprime, w, B, Hkv, T, scale, eps, dn, st)) return rc;
-  const int BHq = B * Hq;
-  LUCID_LAUNCH("lucid_attn_fwd_kernel", lucid::lucid_attn_fwd_kernel<D>, dim3(((T + 255) / 256) * BHq), st, (const bf16*)q,
-               S(qs), (const bf16*)k, S(ks), w.vpt, (bf16*)o, S(os), lse, w.mass, w.olo, Hq, Hkv, T, BHq, scale,
-               lucid::Lo{}, nullptr);
-  return LUCID_OK;
+  return launch_attn_fwd<D>(q, qs, k, ks, o, os, lse, w, B, Hq, Hkv, T, scale, st);
 }
 
 // The attention part of the backward: delta, dV' and the softmax dK (into w.dvp, w.dka)
@@ -364,10 +380,7 @@ int launch_attn_vp_fwd(const void* q, const int64_t* qs, const void* k, const in
   if (g_precision == LUCID_PRECISION_AUTO)
     LUCID_LAUNCH("lucid_mass_kernel", lucid::lucid_mass_kernel<D>, dim3(T / 64, BH), st, (const bf16*)k, S(ks),
                  Hkv, T, w.rinv, scale, w.mass);
-  LUCID_LAUNCH("lucid_attn_fwd_kernel", lucid::lucid_attn_fwd_kernel<D>, dim3(((T + 255) / 256) * BHq), st,
-               (const bf16*)q, S(qs), (const bf16*)k, S(ks), w.vpt, (bf16*)o, S(os), lse, w.mass, w.olo, Hq, Hkv, T,
-               BHq, scale, lucid::Lo{}, nullptr);
-  return LUCID_OK;
+  return launch_attn_fwd<D>(q, qs, k, ks, o, os, lse, w, B, Hq, Hkv, T, scale, st);
 }
 
 template <int D>

@@ -1144,4 +1144,180 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
   }
 }
 
+// Workgroup id of an attention grid (nblk row blocks x B*Hkv kv heads x G query heads)
+// -> (row block, kv-head row bh = b*Hkv + h, query head g of the group), heavy (late) row
+// blocks first.  Workgroup ids go to the 8 XCDs round robin, so when B*Hkv is a multiple of
+// 8 the ids of one XCD take the kv heads bh = xcd, xcd + 8, ... with all G of their query
+// heads: the query heads that read the same K and V' tiles share one L2.  Otherwise the
+// query head is the fastest index.
+__device__ __forceinline__ void attn_block_of(int id, int nblk, int BH, int G, int& ib, int& bh, int& g) {
+  if ((BH & 7) == 0) {
+    const int xcd = id & 7, kk = id >> 3, per = (BH >> 3) * G;
+    const int ibo = kk / per, rest = kk - ibo * per;
+    ib = nblk - 1 - ibo;
+    bh = xcd + 8 * (rest / G);
+    g = rest - (rest / G) * G;
+  } else {
+    const int BHq = BH * G, bhq = id % BHq;
+    ib = nblk - 1 - id / BHq;
+    bh = bhq / G;
+    g = bhq - bh * G;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Causal attention on V' at head dim 128 (bf16): 256 query rows per workgroup as eight
+// waves of 32 rows (one n-tile each), two waves per SIMD, so that one wave's softmax runs
+// beside the other's MFMAs; every 64-key tile of K and V'^T is staged once per workgroup
+// in LDS (double buffered, register-staged one tile ahead by all 512 threads, padded rows)
+// and read by all eight waves.  Per wave and tile: S^T[j][i] = K_j . Q_i (16 MFMAs), the
+// online softmax (lazy rescale by 2^8), O^T[d][i] += V'^T[d][j] P^T[j][i] (16 MFMAs).
+// Outputs as lucid_attn_fwd_kernel (O, lse2, O's lo part for exact heads).
+// ---------------------------------------------------------------------------
+template <int D>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void lucid_attn_fwd_wide_kernel(
+    const bf16* __restrict__ q, Strides qs, const bf16* __restrict__ k, Strides ks, const bf16* __restrict__ vpt,
+    bf16* __restrict__ o, Strides os, float* __restrict__ lse, const float* __restrict__ mass,
+    bf16* __restrict__ olo, int Hq, int Hkv, int T, int BH, float scale) {
+  constexpr int NDT = D / 32;
+  constexpr int NKS = D / 16;
+  constexpr int CH = D / 64;  // 16-byte chunks per thread for each of the K and V'^T tiles
+  static_assert(D == 128, "the wide attention kernel is the head-dim-128 path");
+  __shared__ __attribute__((aligned(16))) bf16 lk[2][64][D + 8];
+  __shared__ __attribute__((aligned(16))) bf16 lv[2][D][64 + 8];
+
+  const int G = Hq / Hkv;
+  const int nblk = (T + 255) / 256;
+  int ib, bh, gi;
+  attn_block_of(blockIdx.x, nblk, BH, G, ib, bh, gi);
+  const int b = bh / Hkv, h = bh - b * Hkv, hq = h * G + gi, bhq = b * Hq + hq;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int g = lane >> 5, l32 = lane & 31;
+  const int r0 = ib * 256;
+  const int row0 = r0 + w * 32;  // this wave's 32 rows
+  const bf16* qh = q + b * qs.b + hq * qs.h;
+  const bf16* kh = k + b * ks.b + h * ks.h;
+  const bf16* vth = vpt + (int64_t)bh * D * T;
+  const float c = scale * LOG2E_F;
+
+  bf16x8 qb[NKS];
+  {
+    const int rq = min(row0 + l32, T - 1);
+#pragma unroll
+    for (int st = 0; st < NKS; ++st) qb[st] = ld8(qh + (int64_t)rq * qs.t + 16 * st + 8 * g);
+  }
+  f32x16 oacc[NDT];
+#pragma unroll
+  for (int t = 0; t < NDT; ++t) oacc[t] = zero16();
+  float m = -1e30f, lsum = 0.f;
+
+  const int ntile = (min(r0 + 256, T) + 63) / 64;
+  const int last_w = row0 / 64;  // the tile holding this wave's diagonal
+  bf16x8 stg[2 * CH];
+  auto gload = [&](int j0) {
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      const int cidx = tid + 512 * u;
+      const int kr = cidx / (D / 8), kc = cidx % (D / 8);
+      stg[u] = ld8(kh + (int64_t)(j0 + kr) * ks.t + kc * 8);
+      const int vr = cidx >> 3, vc = cidx & 7;
+      stg[CH + u] = ld8(vth + (int64_t)vr * T + j0 + vc * 8);
+    }
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      const int cidx = tid + 512 * u;
+      const int kr = cidx / (D / 8), kc = cidx % (D / 8);
+      *reinterpret_cast<bf16x8*>(&lk[buf][kr][kc * 8]) = stg[u];
+      const int vr = cidx >> 3, vc = cidx & 7;
+      *reinterpret_cast<bf16x8*>(&lv[buf][vr][vc * 8]) = stg[CH + u];
+    }
+  };
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  for (int jt = 0; jt < ntile; ++jt) {
+    const int buf = jt & 1;
+    const bool more = jt + 1 < ntile;
+    if (more) gload((jt + 1) * 64);
+    if (jt <= last_w && row0 < T) {
+      f32x16 s[2];
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        s[mt] = zero16();
+#pragma unroll
+        for (int st = 0; st < NKS; ++st)
+          s[mt] = mfma32(ld8(&lk[buf][mt * 32 + l32][16 * st + 8 * g]), qb[st], s[mt]);
+      }
+      if (jt == last_w) {  // causal mask: key 64 jt + mt 32 + drow > row
+        const int rel = row0 - jt * 64 + l32;  // the lane's row relative to the tile's first key
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+          for (int e = 0; e < 16; ++e)
+            if (mt * 32 + drow(e, g) > rel) s[mt][e] = -INFINITY;
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[mt][e]);
+      mx = wave_max32(mx) * c;
+      if (__builtin_amdgcn_ballot_w64(mx > m + 8.0f)) {
+        const float mnew = fmaxf(m, mx);
+        const float alpha = __builtin_amdgcn_exp2f(m - mnew);
+        m = mnew;
+        lsum *= alpha;
+#pragma unroll
+        for (int t = 0; t < NDT; ++t)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) oacc[t][e] *= alpha;
+      }
+      bf16x8 pb[4];
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const float p = __builtin_amdgcn_exp2f(fmaf(s[mt][e], c, -m));
+          lsum += p;
+          s[mt][e] = p;
+        }
+        pb[2 * mt] = pack_b(s[mt], 0);
+        pb[2 * mt + 1] = pack_b(s[mt], 1);
+      }
+#pragma unroll
+      for (int t = 0; t < NDT; ++t)
+#pragma unroll
+        for (int k4 = 0; k4 < 4; ++k4)
+          oacc[t] = mfma32(ld8(&lv[buf][t * 32 + l32][16 * k4 + 8 * g]), pb[k4], oacc[t]);
+    }
+    if (more) lstore(buf ^ 1);
+    __syncthreads();
+  }
+  const bool exact = mass[bh] > kExactMass;
+  const int irow = row0 + l32;
+  const float ls = wave_sum32(lsum);
+  if (irow < T) {
+    const float inv = 1.0f / ls;
+    bf16* op = o + b * os.b + hq * os.h + (int64_t)irow * os.t;
+    bf16* ol = olo + ((int64_t)bhq * T + irow) * D;
+#pragma unroll
+    for (int t = 0; t < NDT; ++t)
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) {
+        bf16x4 bb, bl;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const float x = oacc[t][4 * qq + u] * inv;
+          bb[u] = (bf16)x;
+          bl[u] = (bf16)(x - (float)bb[u]);
+        }
+        *reinterpret_cast<bf16x4*>(op + t * 32 + 8 * qq + 4 * g) = bb;
+        if (exact) *reinterpret_cast<bf16x4*>(ol + t * 32 + 8 * qq + 4 * g) = bl;
+      }
+    if (g == 0) lse[(int64_t)bhq * T + irow] = m + log2f(ls);
+  }
+}
+
 }  // namespace lucid

@@ -81,9 +81,9 @@ inline void reset() {
 
 }  // namespace lucid_prof
 
-// Launch KERNEL on ST with 256 threads; on failure return the status from the
-// enclosing function (STATUS_FN(name) must yield an int, 0 = ok).
-#define LUCID_TIMED_LAUNCH(STATUS_FN, NAME, KERNEL, GRID, ST, ...)        \
+// Launch KERNEL on ST with BLOCK threads (LUCID_TIMED_LAUNCH: 256); on failure return the
+// status from the enclosing function (STATUS_FN(name) must yield an int, 0 = ok).
+#define LUCID_TIMED_LAUNCH_B(STATUS_FN, NAME, KERNEL, GRID, BLOCK, ST, ...)\
   do {                                                                     \
     hipEvent_t ev_a = nullptr, ev_b = nullptr;                             \
     if (lucid_prof::enabled()) {                                           \
@@ -92,8 +92,10 @@ inline void reset() {
       if (!ev_a || !ev_b || hipEventRecord(ev_a, ST) != hipSuccess)        \
         ev_a = nullptr;                                                    \
     }                                                                      \
-    hipLaunchKernelGGL(KERNEL, GRID, dim3(256), 0, ST, __VA_ARGS__);       \
+    hipLaunchKernelGGL(KERNEL, GRID, BLOCK, 0, ST, __VA_ARGS__);            \
     if (int rc_ = STATUS_FN(NAME)) return rc_;                             \
     if (ev_a && hipEventRecord(ev_b, ST) == hipSuccess)                    \
       lucid_prof::records().push_back(lucid_prof::Rec{NAME, ev_a, ev_b});  \
   } while (0)
+#define LUCID_TIMED_LAUNCH(STATUS_FN, NAME, KERNEL, GRID, ST, ...) \
+  LUCID_TIMED_LAUNCH_B(STATUS_FN, NAME, KERNEL, GRID, dim3(256), ST, __VA_ARGS__)
