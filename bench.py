@@ -360,10 +360,11 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="lucid",
-                    choices=["lucid", "c2", "c3", "c5", "path", "path_softmax", "decode"],
+                    choices=["lucid", "c2", "c3", "c5", "gqa128", "path", "path_softmax", "decode"],
                     help="lucid: north star B1 H16 T32768 d64 fwd+bwd (default); c2: B4 H16 T4096 d64 "
                          "fwd+bwd; c3: 16-layer Llama-LUCID decoder, one training step (fwd+bwd+AdamW) "
-                         "on B1 x T8192; c5: B1 T131072 Hq32/Hkv8 d128 forward only; path: LUCID-Path "
+                         "on B1 x T8192; c5: B1 T131072 Hq32/Hkv8 d128 forward only; gqa128: the config-5 heads "
+                         "(Hq32/Hkv8 d128) at B1 T32768, fwd+bwd; path: LUCID-Path "
                          "B1 H16 T32768 d64 fwd+bwd; path_softmax: PaTH softmax attention on the config-4 "
                          "shape, fwd+bwd; decode: one decoding step against a 128K cache (config-5 heads)")
     ap.add_argument("--precision", default="auto", choices=["auto", "fast", "exact"],
@@ -427,7 +428,7 @@ def main():
             metric = "PaTH softmax attention fwd+bwd tokens/s & TFLOP/s at T=32K bf16 (config-4 shape)"
     else:
         B, Hq, Hkv, T, D = {"lucid": (1, 16, 16, 32768, 64), "c2": (4, 16, 16, 4096, 64),
-                            "c5": (1, 32, 8, 131072, 128)}[wl]
+                            "c5": (1, 32, 8, 131072, 128), "gqa128": (1, 32, 8, 32768, 128)}[wl]
         q, k, v, do = _bench_inputs(B, Hq, Hkv, T, D, dev, grad=not fwd_only, keys=args.keys)
         lib, prefix = _lib.load(), "lucid_"
 
@@ -542,7 +543,8 @@ def main():
                 else "synthetic (seeded N(0,1) q,k,v,w; w L2-normalised; beta=2 sigmoid(N(0,1)); N(0,1) dO)",
         "precision": args.precision, "keys": args.keys,
         "config": {"workload": {"lucid": "lucid_attention_fwd_bwd", "c2": "lucid_attention_fwd_bwd",
-                                "c5": "lucid_attention_fwd", "path": "lucid_path_fwd_bwd",
+                                "c5": "lucid_attention_fwd", "gqa128": "lucid_attention_fwd_bwd",
+                                "path": "lucid_path_fwd_bwd",
                                 "path_softmax": "path_softmax_attention_fwd_bwd"}[wl],
                    "B": B, "Hq": Hq, "Hkv": Hkv, "T": T, "head_dim": D, "causal": True,
                    "parallelism": "single GPU"},

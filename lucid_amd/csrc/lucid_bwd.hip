@@ -284,7 +284,9 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
 
 // ---------------------------------------------------------------------------
 // Row sweep for dQ.  Workgroup = 256 query rows (heavy blocks first), wave w
-// owns rows 64w..64w+63 (lane <-> row i).  Every key tile (K rows, V' rows) is
+// owns rows RW w .. RW w + RW - 1 (lane <-> row i): four waves of 64 rows, or at head
+// dim 128 eight waves of 32 rows (two per SIMD; with 64 rows per wave the Q and dO
+// operands and accumulators of a wave exceed the registers and spill).  Every key tile (K rows, V' rows) is
 // staged once per workgroup in LDS by direct global->LDS loads (three buffers,
 // two tiles ahead); K^T operands come through transposing LDS loads.
 //   S^T[j][i] = K_j . Q_i, dP^T[j][i] = V'_j . dO_i, dS^T = P^T (dP^T - delta_i)
@@ -309,16 +311,19 @@ struct DqSmemF32 {  // fp32 inputs: the lo tiles of K and V' beside the hi tiles
   bf16 vl[3][64 * D];
 };
 
-template <int D, bool EXACT, bool F32 = false>
-__global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void lucid_attn_bwd_dq_kernel(
+template <int D, bool EXACT, bool F32 = false, int RW = 64>
+__global__ __launch_bounds__(16384 / RW) LUCID_TWO_WAVES_IF((D == 64 || RW == 32) && !EXACT) void lucid_attn_bwd_dq_kernel(
     const bf16* __restrict__ q, Strides qs, const bf16* __restrict__ k, Strides ks, const bf16* __restrict__ vpb,
     const bf16* __restrict__ dout, Strides dos, const float* __restrict__ lse,
     const float* __restrict__ delta, const float* __restrict__ mass,
     std::conditional_t<F32, float, bf16>* __restrict__ dq, Strides dqs, int Hq, int Hkv, int T, int BHq,
     float scale, Lo lo, const bf16* __restrict__ vpbl) {
-  static_assert(!F32 || (EXACT && D == 64), "fp32 inputs: exact instance, head dim 64");
+  static_assert(!F32 || (EXACT && D == 64 && RW == 64), "fp32 inputs: exact instance, head dim 64");
+  static_assert(RW == 64 || RW == 32, "rows per wave");
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
+  constexpr int NT = RW / 32;           // 32-row n-tiles per wave
+  constexpr int NTHR = 64 * (256 / RW);  // 256 rows per workgroup
   __shared__ __attribute__((aligned(16))) std::conditional_t<F32, DqSmemF32<D>, DqSmem<D>> sm;
   const int nblk = (T + 255) / 256;
   const int id = blockIdx.x;
@@ -331,15 +336,15 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
   const int r0 = ib * 256;
-  const int row0 = r0 + w * 64;
+  const int row0 = r0 + w * RW;
   const bf16* kh = k + b * ks.b + h * ks.h;
   const bf16* vh = vpb + (int64_t)bh * T * D;
   const float c = scale * LOG2E_F;
 
-  bf16x8 qb[2][NKS], db[2][NKS], qbl[2][NKS], dbl[2][NKS];
-  float li[2], di[2];
+  bf16x8 qb[NT][NKS], db[NT][NKS], qbl[NT][NKS], dbl[NT][NKS];
+  float li[NT], di[NT];
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
+  for (int nt = 0; nt < NT; ++nt) {
     const int ir = min(row0 + nt * 32 + l32, T - 1);
 #pragma unroll
     for (int st = 0; st < NKS; ++st) {
@@ -353,26 +358,27 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
     li[nt] = lse[(int64_t)bhq * T + ir];
     di[nt] = delta[(int64_t)bhq * T + ir];
   }
-  f32x16 acc[NDT][2];
+  f32x16 acc[NDT][NT];
 #pragma unroll
-  for (int t = 0; t < NDT; ++t) {
-    acc[t][0] = zero16();
-    acc[t][1] = zero16();
-  }
+  for (int t = 0; t < NDT; ++t)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[t][nt] = zero16();
   const int ntile = (min(r0 + 256, T) + 63) / 64;
   const int last_w = row0 / 64;
+  const int roff = row0 - last_w * 64;  // this wave's first row within its diagonal tile
   // newest vector-memory ops of a step, per wave
-  constexpr int STAGE_OPS = (F32 ? 4 : 2) * (64 * (D / 8) / 256);
-  int plan_k[64 * (D / 8) / 256], plan_v[64 * (D / 8) / 256];
-  dma_plan<64, D / 8>(ks.t, plan_k);
-  dma_plan<64, D / 8>(D, plan_v);
+  constexpr int PLAN = 64 * (D / 8) / NTHR;
+  constexpr int STAGE_OPS = (F32 ? 4 : 2) * PLAN;
+  int plan_k[PLAN], plan_v[PLAN];
+  dma_plan<64, D / 8, NTHR>(ks.t, plan_k);
+  dma_plan<64, D / 8, NTHR>(D, plan_v);
   auto stage = [&](int jt) {
     const int j0 = jt * 64, buf = jt % 3;
-    dma_stage<64, D / 8>(plan_k, kh + (int64_t)j0 * ks.t, sm.k[buf]);
-    dma_stage<64, D / 8>(plan_v, vh + (int64_t)j0 * D, sm.v[buf]);
+    dma_stage<64, D / 8, NTHR>(plan_k, kh + (int64_t)j0 * ks.t, sm.k[buf]);
+    dma_stage<64, D / 8, NTHR>(plan_v, vh + (int64_t)j0 * D, sm.v[buf]);
     if constexpr (F32) {
-      dma_stage<64, D / 8>(plan_k, lo.k + b * ks.b + h * ks.h + (int64_t)j0 * ks.t, sm.kl[buf]);
-      dma_stage<64, D / 8>(plan_v, vpbl + (int64_t)bh * T * D + (int64_t)j0 * D, sm.vl[buf]);
+      dma_stage<64, D / 8, NTHR>(plan_k, lo.k + b * ks.b + h * ks.h + (int64_t)j0 * ks.t, sm.kl[buf]);
+      dma_stage<64, D / 8, NTHR>(plan_v, vpbl + (int64_t)bh * T * D + (int64_t)j0 * D, sm.vl[buf]);
     }
   };
   stage(0);
@@ -393,37 +399,43 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
   auto tile = [&](const int buf, const bool DIAG) {
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
-      bf16x8 ka[NKS], va[NKS];
+      // the K and V' operands of this key half: held across the n-tiles, or (one n-tile)
+      // read where they are used, which keeps the head-dim-128 instance within its registers
+      bf16x8 ka[NT > 1 ? NKS : 1], va[NT > 1 ? NKS : 1];
+      if constexpr (NT > 1) {
 #pragma unroll
-      for (int st = 0; st < NKS; ++st) {
-        ka[st] = ld8(sm.k[buf] + rdo[st] + mt * 32 * D);
-        va[st] = ld8(sm.v[buf] + rdo[st] + mt * 32 * D);
+        for (int st = 0; st < NKS; ++st) {
+          ka[st] = ld8(sm.k[buf] + rdo[st] + mt * 32 * D);
+          va[st] = ld8(sm.v[buf] + rdo[st] + mt * 32 * D);
+        }
       }
-      bf16x8 dsb[2][2], dsl[2][2];
+      auto kop = [&](int st) { return NT > 1 ? ka[st % (NT > 1 ? NKS : 1)] : ld8(sm.k[buf] + rdo[st] + mt * 32 * D); };
+      auto vop = [&](int st) { return NT > 1 ? va[st % (NT > 1 ? NKS : 1)] : ld8(sm.v[buf] + rdo[st] + mt * 32 * D); };
+      bf16x8 dsb[NT][2], dsl[NT][2];
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
+      for (int nt = 0; nt < NT; ++nt) {
         f32x16 sc = zero16(), dp = zero16();
 #pragma unroll
         for (int st = 0; st < NKS; ++st) {
-          sc = mfma32(ka[st], qb[nt][st], sc);
-          dp = mfma32(va[st], db[nt][st], dp);
+          sc = mfma32(kop(st), qb[nt][st], sc);
+          dp = mfma32(vop(st), db[nt][st], dp);
         }
         if constexpr (F32) {
 #pragma unroll
           for (int st = 0; st < NKS; ++st) {
             const bf16x8 kl8 = ld8(sm.kl[buf] + rdo[st] + mt * 32 * D);
             const bf16x8 vl8 = ld8(sm.vl[buf] + rdo[st] + mt * 32 * D);
-            sc = mfma32(ka[st], qbl[nt][st], sc);
+            sc = mfma32(kop(st), qbl[nt][st], sc);
             sc = mfma32(kl8, qb[nt][st], sc);
             sc = mfma32(kl8, qbl[nt][st], sc);
-            dp = mfma32(va[st], dbl[nt][st], dp);
+            dp = mfma32(vop(st), dbl[nt][st], dp);
             dp = mfma32(vl8, db[nt][st], dp);
           }
         }
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           float p = __builtin_amdgcn_exp2f(fmaf(sc[e], c, -li[nt]));
-          if (DIAG && (mt * 32 + drow(e, g) > nt * 32 + l32)) p = 0.f;
+          if (DIAG && (mt * 32 + drow(e, g) > roff + nt * 32 + l32)) p = 0.f;
           sc[e] = p * (dp[e] + di[nt]);  // di holds -delta
         }
         dsb[nt][0] = pack_b(sc, 0);
@@ -438,7 +450,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
         const bf16x8 a0 = lds_tr_a<D / 8>(sm.k[buf], mt * 32, t * 32);
         const bf16x8 a1 = lds_tr_a<D / 8>(sm.k[buf], mt * 32 + 16, t * 32);
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
+        for (int nt = 0; nt < NT; ++nt) {
           acc[t][nt] = mfma32(a0, dsb[nt][0], acc[t][nt]);
           acc[t][nt] = mfma32(a1, dsb[nt][1], acc[t][nt]);
           if constexpr (EXACT) {
@@ -465,7 +477,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
     __syncthreads();
   }
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
+  for (int nt = 0; nt < NT; ++nt) {
     const int irow = row0 + nt * 32 + l32;
     if (irow >= T) continue;
     auto* op = dq + b * dqs.b + hq * dqs.h + (int64_t)irow * dqs.t;

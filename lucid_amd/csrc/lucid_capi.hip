@@ -252,14 +252,17 @@ int launch_attn_bwd(const void* dout, const int64_t* dos, const void* q, const i
   LUCID_LAUNCH("lucid_attn_bwd_dkdv_kernel", lucid::lucid_attn_bwd_dkdv_kernel<D>, dim3((T / 128) * BH), st,
                (const bf16*)q, S(qs), (const bf16*)k, S(ks), f.vpb, (const bf16*)dout, S(dos), lse,
                w.delta, w.dvp, w.dka, Hq, Hkv, T, BH, scale, lucid::Lo{}, nullptr);
-  LUCID_LAUNCH("lucid_attn_bwd_dq_kernel", (lucid::lucid_attn_bwd_dq_kernel<D, false>),
-               dim3(((T + 255) / 256) * BHq), st, (const bf16*)q, S(qs), (const bf16*)k, S(ks), f.vpb,
-               (const bf16*)dout, S(dos), lse, w.delta, f.mass, (bf16*)dq, S(dqs), Hq, Hkv, T, BHq, scale,
-               lucid::Lo{}, nullptr);
-  LUCID_LAUNCH("lucid_attn_bwd_dq_exact_kernel", (lucid::lucid_attn_bwd_dq_kernel<D, true>),
-               dim3(((T + 255) / 256) * BHq), st, (const bf16*)q, S(qs), (const bf16*)k, S(ks), f.vpb,
-               (const bf16*)dout, S(dos), lse, w.delta, f.mass, (bf16*)dq, S(dqs), Hq, Hkv, T, BHq, scale,
-               lucid::Lo{}, nullptr);
+  // dQ: four waves of 64 rows at head dim 64, eight waves of 32 rows at 128
+  constexpr int RW = D == 128 ? 32 : 64;
+  const dim3 block(64 * (256 / RW));
+  LUCID_LAUNCH_B("lucid_attn_bwd_dq_kernel", (lucid::lucid_attn_bwd_dq_kernel<D, false, false, RW>),
+                 dim3(((T + 255) / 256) * BHq), block, st, (const bf16*)q, S(qs), (const bf16*)k, S(ks), f.vpb,
+                 (const bf16*)dout, S(dos), lse, w.delta, f.mass, (bf16*)dq, S(dqs), Hq, Hkv, T, BHq, scale,
+                 lucid::Lo{}, nullptr);
+  LUCID_LAUNCH_B("lucid_attn_bwd_dq_exact_kernel", (lucid::lucid_attn_bwd_dq_kernel<D, true, false, RW>),
+                 dim3(((T + 255) / 256) * BHq), block, st, (const bf16*)q, S(qs), (const bf16*)k, S(ks), f.vpb,
+                 (const bf16*)dout, S(dos), lse, w.delta, f.mass, (bf16*)dq, S(dqs), Hq, Hkv, T, BHq, scale,
+                 lucid::Lo{}, nullptr);
   return LUCID_OK;
 }
 

@@ -260,11 +260,12 @@ __device__ __forceinline__ void dma_tile(const bf16* __restrict__ src, int64_t s
   }
 }
 // dma_tile split in two: the per-lane element offsets for a fixed row stride
-// (dma_plan, once per kernel) and the loads of one tile (dma_stage).
-template <int ROWS, int CPR>
+// (dma_plan, once per kernel) and the loads of one tile (dma_stage), by a workgroup of
+// NTHR threads.
+template <int ROWS, int CPR, int NTHR = 256>
 __device__ __forceinline__ void dma_plan(int64_t stride, int* off) {
-  constexpr int PER_WAVE = ROWS * CPR / 256;
-  static_assert(PER_WAVE * 256 == ROWS * CPR, "tile must be a whole number of 1 KB pieces per wave");
+  constexpr int PER_WAVE = ROWS * CPR / NTHR;
+  static_assert(PER_WAVE * NTHR == ROWS * CPR, "tile must be a whole number of 1 KB pieces per wave");
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
 #pragma unroll
   for (int i = 0; i < PER_WAVE; ++i) {
@@ -273,9 +274,9 @@ __device__ __forceinline__ void dma_plan(int64_t stride, int* off) {
     off[i] = (int)(r * stride) + c * 8;
   }
 }
-template <int ROWS, int CPR>
+template <int ROWS, int CPR, int NTHR = 256>
 __device__ __forceinline__ void dma_stage(const int* off, const bf16* __restrict__ src, bf16* lds) {
-  constexpr int PER_WAVE = ROWS * CPR / 256;
+  constexpr int PER_WAVE = ROWS * CPR / NTHR;
   const int w = threadIdx.x >> 6;
 #pragma unroll
   for (int i = 0; i < PER_WAVE; ++i)
