@@ -43,6 +43,8 @@ def causal_flops(B, Hq, T, D):
 KERNEL_FLOPS = {
     "lucid_precond_fwd_kernel": lambda B, Hq, Hkv, T, D: 2.0 * T * T * D * B * Hkv,   # K^K^T, P V'
     "lucid_attn_fwd_kernel": lambda B, Hq, Hkv, T, D: 2.0 * T * T * D * B * Hq,       # QK^T, P V'
+    # chain (K^K^T, P V') and attention (QK^T, P V') of each block in one kernel (Hq == Hkv)
+    "lucid_fused_fwd_kernel": lambda B, Hq, Hkv, T, D: 2.0 * T * T * D * B * (Hkv + Hq),
     "lucid_attn_fwd_wide_kernel": lambda B, Hq, Hkv, T, D: 2.0 * T * T * D * B * Hq,  # the same at head dim 128
     "lucid_attn_bwd_dkdv_kernel": lambda B, Hq, Hkv, T, D: 4.0 * T * T * D * B * Hq,  # S, dV', dP, dK
     "lucid_attn_bwd_dq_kernel": lambda B, Hq, Hkv, T, D: 1.0 * T * T * D * B * Hq,    # dQ
@@ -375,6 +377,9 @@ def main():
                          "(row mass ~T, the exact chains under --precision auto)")
     ap.add_argument("--decode-tokens", type=int, default=1,
                     help="new tokens per decoding call (--workload decode)")
+    ap.add_argument("--no-fused-fwd", action="store_true",
+                    help="time the two-kernel forward (chain, then attention) instead of the fused kernel "
+                         "(lucid_amd.set_fused_forward)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-causal", action="store_true")
     ap.add_argument("--copy-bytes", type=int, default=0,
@@ -393,11 +398,12 @@ def main():
 
     import torch
 
-    from lucid_amd import _lib, lucid_attention, set_precision
+    from lucid_amd import _lib, lucid_attention, set_fused_forward, set_precision
 
     dev = torch.device("cuda:0")
     wl = args.workload
     set_precision(args.precision)
+    set_fused_forward(not args.no_fused_fwd)
     if wl == "c3":
         bench_c3(args, dev)
         return
@@ -443,7 +449,8 @@ def main():
         if fwd_only:
             flops = 2.0 * T * T * D * B * (Hq + Hkv)
             kflops = {n: KERNEL_FLOPS[n](B, Hq, Hkv, T, D) for n in
-                      ("lucid_precond_fwd_kernel", "lucid_attn_fwd_kernel", "lucid_attn_fwd_wide_kernel")}
+                      ("lucid_precond_fwd_kernel", "lucid_attn_fwd_kernel", "lucid_attn_fwd_wide_kernel",
+                       "lucid_fused_fwd_kernel")}
         else:
             flops = lucid_flops(B, Hq, Hkv, T, D)
             kflops = {n: f(B, Hq, Hkv, T, D) for n, f in KERNEL_FLOPS.items()}
@@ -541,7 +548,7 @@ def main():
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1)/sqrt(d) q,k,v; N(0,1) dO)" if wl not in ("path", "path_softmax")
                 else "synthetic (seeded N(0,1) q,k,v,w; w L2-normalised; beta=2 sigmoid(N(0,1)); N(0,1) dO)",
-        "precision": args.precision, "keys": args.keys,
+        "precision": args.precision, "keys": args.keys, "fused_forward": not args.no_fused_fwd,
         "config": {"workload": {"lucid": "lucid_attention_fwd_bwd", "c2": "lucid_attention_fwd_bwd",
                                 "c5": "lucid_attention_fwd", "gqa128": "lucid_attention_fwd_bwd",
                                 "path": "lucid_path_fwd_bwd",

@@ -39,7 +39,7 @@ extern "C" {
 #define LUCID_PRECISION_FAST 1  /* bf16 products everywhere */
 #define LUCID_PRECISION_EXACT 2 /* hi/lo split products for every head */
 
-/* ABI version of this header (bumped on any signature change or new entry point): 4. */
+/* ABI version of this header (bumped on any signature change or new entry point): 5. */
 int lucid_abi_version(void);
 
 /* Text of the last error on the calling thread ("" if none). */
@@ -58,6 +58,15 @@ const char* lucid_last_error(void);
  * torch solve_triangular works in the input dtype (modeling_lucid.py:570). */
 int lucid_set_precision(int mode);
 int lucid_get_precision(void);
+
+/* Forward kernel schedule for the calls that follow (process-wide; no counterpart in the
+ * reference).  On (default): at head dim <= 64 with one query head per kv head, the
+ * preconditioner chain and the causal attention of each 128-row block run in one fused
+ * kernel (lucid_fused_fwd_kernel) that feeds every staged key tile to both; off: the chain
+ * kernel, then the attention kernel.  Both give the same O, V' and lse up to the rounding
+ * order of the attention's online softmax.  Any nonzero value means on. */
+int lucid_set_fused_forward(int on);
+int lucid_get_fused_forward(void);
 
 /* Bounded chain waits (no counterpart in the reference, which has no cross-workgroup
  * waits).  The chained solves hand blocks between workgroups through per-head progress

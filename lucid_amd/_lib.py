@@ -33,6 +33,8 @@ _SIGS = {
         "lucid_chain_status": ([], _int),
         "lucid_set_chain_wait_limit": ([ctypes.c_double], _int),
         "lucid_get_precision": ([], _int),
+        "lucid_set_fused_forward": ([_int], _int),
+        "lucid_get_fused_forward": ([], _int),
         "lucid_fwd_workspace_mass_offset": ([_int] * 5, _sz),
         "lucid_bwd_workspace_bytes": ([_int] * 5, _sz),
         "lucid_get_v_prime": ([_vp, _i64p, _vp, _i64p, _vp, _vp, _int, _int, _int, _int, _flt, _flt, _vp], _int),

@@ -21,6 +21,10 @@ thread_local std::string g_last_error;
 // per head from its row mass (lucid_mass_kernel, kExactMass); the others force one kind.
 int g_precision = LUCID_PRECISION_AUTO;
 
+// Forward schedule (lucid_set_fused_forward): the fused chain + attention kernel at head
+// dim 64 with one query head per kv head, or the two-kernel sequence.
+bool g_fused_fwd = true;
+
 int fail(const std::string& msg) {
   g_last_error = msg;
   return LUCID_EINVAL;
@@ -227,7 +231,7 @@ int launch_attn_fwd(const void* q, const int64_t* qs, const void* k, const int64
   } else {
     LUCID_LAUNCH("lucid_attn_fwd_kernel", lucid::lucid_attn_fwd_kernel<D>, dim3(((T + 255) / 256) * BHq), st,
                  (const bf16*)q, S(qs), (const bf16*)k, S(ks), w.vpt, (bf16*)o, S(os), lse, w.mass, w.olo, Hq, Hkv,
-                 T, BHq, scale, lucid::Lo{}, nullptr);
+                 T, BHq, scale, lucid::Lo{}, nullptr, 0);
   }
   return LUCID_OK;
 }
@@ -236,6 +240,33 @@ template <int D>
 int launch_fwd(const void* q, const int64_t* qs, const void* k, const int64_t* ks, const void* v, const int64_t* vs,
                void* o, const int64_t* os, float* vprime, float* lse, const FwdWs& w, int B, int Hq, int Hkv, int T,
                float scale, float eps, float dn, hipStream_t st) {
+  if constexpr (D == 64) {
+    if (Hq == Hkv && g_fused_fwd) {
+      const int BH = B * Hkv;
+      const float mass_init = g_precision == LUCID_PRECISION_EXACT ? 1e30f : 0.f;
+      LUCID_LAUNCH("lucid_prep_kernel", lucid::lucid_prep_kernel<D>, dim3(T / 64, BH), st, (const bf16*)k, S(ks),
+                   Hkv, T, eps, dn, scale, w.rinv, w.kt, w.pinv, w.counters, w.mass, mass_init, lucid::Lo{}, nullptr);
+      if (g_precision == LUCID_PRECISION_AUTO)
+        LUCID_LAUNCH("lucid_mass_kernel", lucid::lucid_mass_kernel<D>, dim3(T / 64, BH), st, (const bf16*)k, S(ks),
+                     Hkv, T, w.rinv, scale, w.mass);
+      LUCID_LAUNCH("lucid_zx_kernel", lucid::lucid_zx_kernel<D>, dim3(T / 128, BH), st, (const bf16*)k, S(ks), Hkv,
+                   T, w.rinv, scale, w.pinv, w.zx, lucid::Lo{});
+      if (g_precision != LUCID_PRECISION_EXACT)
+        LUCID_LAUNCH("lucid_fused_fwd_kernel", lucid::lucid_fused_fwd_kernel<D>, dim3((T / 128) * BH), st,
+                     (const bf16*)q, S(qs), (const bf16*)k, S(ks), (const bf16*)v, S(vs), Hkv, T, BH, w.rinv, scale,
+                     vprime, w.vpb, w.vpt, w.pinv, w.zx, w.mass, w.counters, (bf16*)o, S(os), lse);
+      if (g_precision != LUCID_PRECISION_FAST) {
+        // heads of the exact chains: their chain, then their attention (skip_fast)
+        LUCID_LAUNCH("lucid_precond_fwd_exact_kernel", (lucid::lucid_precond_fwd_kernel<D, true>),
+                     dim3((T / 128) * BH), st, (const bf16*)k, S(ks), (const bf16*)v, S(vs), Hkv, T, BH, w.rinv,
+                     scale, vprime, w.vpb, w.vpt, w.vpbl, w.vptl, w.pinv, w.zx, w.mass, w.counters, lucid::Lo{});
+        LUCID_LAUNCH("lucid_attn_fwd_exact_kernel", lucid::lucid_attn_fwd_kernel<D>, dim3(((T + 255) / 256) * B * Hq),
+                     st, (const bf16*)q, S(qs), (const bf16*)k, S(ks), w.vpt, (bf16*)o, S(os), lse, w.mass, w.olo,
+                     Hq, Hkv, T, B * Hq, scale, lucid::Lo{}, nullptr, 1);
+      }
+      return LUCID_OK;
+    }
+  }
   if (int rc = launch_precond_fwd<D>(k, ks, v, vs, vprime, w, B, Hkv, T, scale, eps, dn, st)) return rc;
   return launch_attn_fwd<D>(q, qs, k, ks, o, os, lse, w, B, Hq, Hkv, T, scale, st);
 }
@@ -483,7 +514,7 @@ int launch_attn_fwd_f32(const void* q, const int64_t* qs, void* o, const int64_t
   lo.k = w.kcl;
   LUCID_LAUNCH("lucid_attn_fwd_f32_kernel", (lucid::lucid_attn_fwd_kernel<D, true>), dim3(((T + 255) / 256) * BHq),
                st, w.qh, rows_strides(Hq, T, D), w.kch, rows_strides(Hkv, T, D), w.vpt, (float*)o, S(os), lse,
-               w.mass, w.olo, Hq, Hkv, T, BHq, scale, lo, w.vptl);
+               w.mass, w.olo, Hq, Hkv, T, BHq, scale, lo, w.vptl, 0);
   return LUCID_OK;
 }
 
@@ -803,7 +834,7 @@ int lucid_decode_noalloc(const void* q, const int64_t* q_strides, const void* k,
 }
 
 
-int lucid_abi_version(void) { return 4; }
+int lucid_abi_version(void) { return 5; }
 
 int lucid_set_precision(int mode) {
   g_last_error.clear();
@@ -814,6 +845,14 @@ int lucid_set_precision(int mode) {
 }
 
 int lucid_get_precision(void) { return g_precision; }
+
+int lucid_set_fused_forward(int on) {
+  g_last_error.clear();
+  g_fused_fwd = on != 0;
+  return LUCID_OK;
+}
+
+int lucid_get_fused_forward(void) { return g_fused_fwd ? 1 : 0; }
 
 int lucid_chain_status(void) {
   g_last_error.clear();

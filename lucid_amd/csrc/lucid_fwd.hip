@@ -844,7 +844,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
     const bf16* __restrict__ q, Strides qs, const bf16* __restrict__ k, Strides ks, const bf16* __restrict__ vpt,
     std::conditional_t<F32, float, bf16>* __restrict__ o, Strides os, float* __restrict__ lse,
     const float* __restrict__ mass, bf16* __restrict__ olo, int Hq, int Hkv, int T, int BHq, float scale, Lo lo,
-    const bf16* __restrict__ vptl) {
+    const bf16* __restrict__ vptl, int skip_fast) {
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
   constexpr int CH = D / 32;  // 16-byte chunks per thread for each of the K and V'^T tiles
@@ -861,6 +861,9 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
   const int b = bhq / Hq, hq = bhq - b * Hq;
   const int h = hq / (Hq / Hkv);
   const int bh = b * Hkv + h;
+  // skip_fast: the fused forward has already written O and lse for the heads of the bf16
+  // chains; this launch covers the heads of the exact chains only
+  if (skip_fast && !(mass[bh] > kExactMass)) return;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
   const int r0 = ib * 256;
@@ -1142,6 +1145,312 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
       if (g == 0) lse[(int64_t)bhq * T + irow] = m[nt] + log2f(ls);
     }
   }
+}
+
+// ---------------------------------------------------------------------------
+// Fused forward at head dim 64 (bf16, one query head per kv head): the chained
+// preconditioner solve of one 128-row block and the causal attention of the same 128
+// query rows in one workgroup, so that every staged key tile and every LDS operand read
+// feeds both.  The chain (ids, counters, staging, finalisation) is lucid_precond_fwd_kernel's;
+// the attention is lucid_attn_fwd_kernel's online softmax.  Wave w owns rows
+// i0 + 32w .. +32 (lane <-> row) of both and sweeps all 128 keys of each staged pair as
+// four 32-key sub-tiles mt:
+//   K_j rows (A operand, one LDS read)  -> S^T = K_j . K_i (chain) and K_j . Q_i (attention)
+//   V'^T (A operand, one LDS read)      -> acc^T += V'^T P^T (chain) and O^T += V'^T A^T
+// The chain's two products and the attention's two are independent, so the exp work of
+// one overlaps the matrix products of the other inside the wave.  After the block's V' is
+// solved and published, the attention finishes on the diagonal pair (the block's own keys,
+// K rows staged again, V'^T from the solve's LDS copy) and writes O and lse2.
+// Heads of the exact chains return at once (lucid_precond_fwd_kernel<D, true> and the
+// attention kernel with skip_fast cover them).
+// ---------------------------------------------------------------------------
+template <int D>
+__global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(true) void lucid_fused_fwd_kernel(
+    const bf16* __restrict__ q, Strides qs, const bf16* __restrict__ k, Strides ks, const bf16* __restrict__ v,
+    Strides vs, int Hkv, int T, int BH, const float* __restrict__ rinv, float scale, float* __restrict__ vp32,
+    bf16* __restrict__ vpb, bf16* __restrict__ vpt, const float* __restrict__ pinv, const float* __restrict__ zx,
+    const float* __restrict__ mass, int* __restrict__ counters, bf16* __restrict__ o, Strides os,
+    float* __restrict__ lse) {
+  static_assert(D == 64, "fused forward: head dim 64");
+  constexpr int NDT = D / 32;
+  constexpr int NKS = D / 16;
+  __shared__ __attribute__((aligned(16))) PfwdSmem<D, false, false> sm;
+
+  const int id = blockIdx.x;
+  const int i2 = id / BH, bh = id - (id / BH) * BH;
+  if (mass[bh] > kExactMass) return;  // the exact chain and attention kernels cover this head
+  const int b = bh / Hkv, h = bh - b * Hkv;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int g = lane >> 5, l32 = lane & 31;
+  const int i0 = i2 * 128;
+  const int NT = T / 64;
+  const int irow = i0 + 32 * w + l32;  // this lane's row (chain and attention)
+  const bf16* kp = k + b * ks.b + h * ks.h;
+  const bf16* vh = v + b * vs.b + h * vs.h;
+  const float* rv = rinv + (int64_t)bh * T;
+  const bf16* vpth = vpt + (int64_t)bh * D * T;
+  const float* pinv_blk = pinv + ((int64_t)bh * NT + 2 * i2) * 4096;
+  int* cnt = counters + bh;
+  const float sl2 = scale * LOG2E_F;
+  const float c0 = LOG2E_F / scale;
+  const float c = sl2;  // attention: P = exp2(c S - m)
+
+  bf16x8 kbi[NKS], qbi[NKS];
+#pragma unroll
+  for (int st = 0; st < NKS; ++st) {
+    kbi[st] = ld8(kp + (int64_t)irow * ks.t + 16 * st + 8 * g);
+    qbi[st] = ld8(q + b * qs.b + h * qs.h + (int64_t)irow * qs.t + 16 * st + 8 * g);
+  }
+  const float ai = sl2 * rv[irow];
+  // chain accumulators start at -V^T (R = -acc after the sweep); attention at zero
+  f32x16 acc[NDT], oacc[NDT];
+#pragma unroll
+  for (int t = 0; t < NDT; ++t) {
+    oacc[t] = zero16();
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd) {
+      const bf16x4 x = *reinterpret_cast<const bf16x4*>(vh + (int64_t)irow * vs.t + t * 32 + 8 * qd + 4 * g);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) acc[t][4 * qd + u] = -(float)x[u];
+    }
+  }
+  float m = -1e30f, lsum = 0.f;
+
+  const int npair = i2;
+  int ready = 0;
+  int plan_k[128 * (D / 8) / 256], plan_v[D * 16 / 256];
+  dma_plan<128, D / 8>(ks.t, plan_k);
+  dma_plan<D, 16>(T, plan_v);
+  auto stage = [&](int pp) {
+    const int buf = pp & 1;
+    if (w < 2) dma_f32x64(rv + pp * 128 + 64 * w, &sm.u.st.r[buf][64 * w]);
+    dma_stage<128, D / 8>(plan_k, kp + (int64_t)pp * 128 * ks.t, sm.u.st.k[buf]);
+    dma_stage<D, 16>(plan_v, vpth + pp * 128, sm.u.st.v[buf]);
+  };
+  f32x4 xr[8];
+  auto xload = [&]() {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int idx = tid + 256 * u;
+      const int sb = idx >> 10, r = (idx >> 4) & 63, c4 = (idx & 15) * 4;
+      xr[u] = *reinterpret_cast<const f32x4*>(pinv_blk + sb * 4096 + r * 64 + c4);
+    }
+  };
+  auto xstore = [&](int sb) {
+#pragma unroll
+    for (int u = 4 * sb; u < 4 * sb + 4; ++u) {
+      const int idx = tid + 256 * u;
+      const int r = (idx >> 4) & 63, c4 = (idx & 15) * 4;
+      *reinterpret_cast<f32x4*>(&sm.u.fin.X[r][c4]) = xr[u];
+    }
+  };
+  // online softmax of one 32-key sub-tile of scores (lazy rescale: the reference max moves
+  // only when a row grows by more than 2^8); returns the two bf16 B operands
+  auto softmax = [&](f32x16& sa, bf16x8& pa0, bf16x8& pa1) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sa[e]);
+    mx = wave_max32(mx) * c;
+    if (__builtin_amdgcn_ballot_w64(mx > m + 8.0f)) {
+      const float mnew = fmaxf(m, mx);
+      const float alpha = __builtin_amdgcn_exp2f(m - mnew);
+      m = mnew;
+      lsum *= alpha;
+#pragma unroll
+      for (int t = 0; t < NDT; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) oacc[t][e] *= alpha;
+    }
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const float p = __builtin_amdgcn_exp2f(fmaf(sa[e], c, -m));
+      lsum += p;
+      sa[e] = p;
+    }
+    pa0 = pack_b(sa, 0);
+    pa1 = pack_b(sa, 1);
+  };
+  // one staged pair: the chain's P V' and the attention, sub-tiles mt = 0..3
+  auto sweep_pair = [&](int buf) {
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      const int key0 = mt * 32;
+      bf16x8 ka[NKS];
+#pragma unroll
+      for (int st = 0; st < NKS; ++st) ka[st] = ld8(swz<D / 8>(sm.u.st.k[buf], key0 + l32, 2 * st + g));
+      float rj[16];
+      lds_rows16(&sm.u.st.r[buf][key0], g, rj);
+      f32x16 sc = zero16(), sa = zero16();
+#pragma unroll
+      for (int st = 0; st < NKS; ++st) {
+        sc = mfma32(ka[st], kbi[st], sc);
+        sa = mfma32(ka[st], qbi[st], sa);
+      }
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sc[e] = __builtin_amdgcn_exp2f(fmaf(sc[e] * ai, rj[e], -c0));
+      const bf16x8 pb0 = pack_b(sc, 0), pb1 = pack_b(sc, 1);
+      bf16x8 pa0, pa1;
+      softmax(sa, pa0, pa1);
+#pragma unroll
+      for (int t = 0; t < NDT; ++t) {
+        const bf16x8 va0 = ld8(swz<16>(sm.u.st.v[buf], t * 32 + l32, key0 / 8 + g));
+        const bf16x8 va1 = ld8(swz<16>(sm.u.st.v[buf], t * 32 + l32, key0 / 8 + 2 + g));
+        acc[t] = mfma32(va0, pb0, acc[t]);
+        acc[t] = mfma32(va1, pb1, acc[t]);
+        oacc[t] = mfma32(va0, pa0, oacc[t]);
+        oacc[t] = mfma32(va1, pa1, oacc[t]);
+      }
+    }
+  };
+  if (npair > 0) {
+    ready = wait_counter_gt(cnt, 1);
+    stage(0);
+    dma_wait();
+  } else {
+    xload();
+  }
+  __syncthreads();
+  for (int pp = 0; pp + 1 < npair; ++pp) {
+    const int need = 2 * pp + 3;  // pair pp + 1 is complete once the counter exceeds this
+    if (need >= ready) {
+      const int seen = poll_counter(cnt);
+      if (seen > need) {
+        chain_acquire();
+        ready = seen;
+      }
+    }
+    const bool early = need < ready;
+    if (early) stage(pp + 1);
+    sweep_pair(pp & 1);
+    if (!early) {
+      ready = wait_counter_gt(cnt, need);
+      stage(pp + 1);
+    }
+    dma_wait();
+    __syncthreads();
+  }
+  if (npair > 0) {
+    xload();  // fetch the inverses while the last pair is processed
+    sweep_pair((npair - 1) & 1);
+    __syncthreads();
+  }
+
+  // ---- the chain's block solve: R^T = -acc, V'_A = X_A R_A, V'_B = X_B R_B + Z V'_A ----
+  float(*Rt)[132] = sm.u.fin.Rt;
+#pragma unroll
+  for (int t = 0; t < NDT; ++t)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][32 * w + l32] = -acc[t][e];
+  xstore(0);
+  f32x4 zr[4][2];
+  {
+    const float* zrow = zx + ((int64_t)bh * (T / 128) + i2) * 4096 + ((w & 1) * 32 + l32) * 64 + 8 * g;
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      zr[st][0] = *reinterpret_cast<const f32x4*>(zrow + 16 * st);
+      zr[st][1] = *reinterpret_cast<const f32x4*>(zrow + 16 * st + 4);
+    }
+  }
+  __syncthreads();
+  auto diag_solve = [&](int sb) {
+    for (int tile = w; tile < NDT * 2; tile += 4) {
+      const int dt = tile >> 1, rh = tile & 1;
+      f32x16 ov = zero16();
+      const int kmax = rh ? 4 : 2;
+      for (int st = 0; st < kmax; ++st) {
+        bf16x8 ah, al, bh8, bl;
+        split8(&Rt[dt * 32 + l32][sb * 64 + 16 * st + 8 * g], ah, al);
+        split8(&sm.u.fin.X[rh * 32 + l32][16 * st + 8 * g], bh8, bl);
+        ov = mfma32(ah, bh8, ov);
+        ov = mfma32(ah, bl, ov);
+        ov = mfma32(al, bh8, ov);
+      }
+      if (sb == 1) {  // + Z V'_A
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+          bf16x8 zh, zl;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float x = zr[st][e >> 2][e & 3];
+            zh[e] = (bf16)x;
+            zl[e] = (bf16)(x - (float)zh[e]);
+          }
+          const bf16x8 va = ld8(&sm.u.fin.vT[dt * 32 + l32][16 * st + 8 * g]);
+          ov = mfma32(va, zh, ov);
+          ov = mfma32(va, zl, ov);
+        }
+      }
+      const int rl = rh * 32 + l32;
+      const int r = i0 + sb * 64 + rl;
+      const int lslot = sb * 64 + ((rl & ~15) | jmap(rl & 15));
+      float* out32 = vp32 + ((int64_t)bh * T + r) * D;
+      bf16* outb = vpb + ((int64_t)bh * T + r) * D;
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd) {
+        const int d0 = dt * 32 + 8 * qd + 4 * g;
+        f32x4 f;
+        bf16x4 bb;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          f[u] = ov[4 * qd + u];
+          bb[u] = (bf16)ov[4 * qd + u];
+          sm.u.fin.vT[d0 + u][lslot] = bb[u];
+        }
+        *reinterpret_cast<f32x4*>(out32 + d0) = f;
+        *reinterpret_cast<bf16x4*>(outb + d0) = bb;
+      }
+    }
+  };
+  diag_solve(0);
+  __syncthreads();
+  xstore(1);
+  __syncthreads();
+  diag_solve(1);
+  __syncthreads();
+  for (int cc = tid; cc < D * 16; cc += 256) {
+    const int dd = cc >> 4, s8 = (cc & 15) * 8;
+    *reinterpret_cast<bf16x8*>(vpt + ((int64_t)bh * D + dd) * T + i0 + s8) = ld8(&sm.u.fin.vT[dd][s8]);
+  }
+  publish_counter(cnt, 2 * i2 + 2);
+
+  // ---- the attention's diagonal pair: keys i0 .. i0 + 127 ----
+  // the block's K rows go to the first staging buffer (its bytes lie inside R^T and X,
+  // both dead now; V'^T of the block stays in fin.vT)
+  static_assert(sizeof(sm.u.st.k[0]) <= offsetof(decltype(sm.u.fin), vT), "diagonal K rows overlap V'^T");
+  dma_stage<128, D / 8>(plan_k, kp + (int64_t)i0 * ks.t, sm.u.st.k[0]);
+  dma_wait();
+  __syncthreads();
+  for (int mt = 0; mt <= w; ++mt) {
+    const int key0 = mt * 32;
+    f32x16 sa = zero16();
+#pragma unroll
+    for (int st = 0; st < NKS; ++st) sa = mfma32(ld8(swz<D / 8>(sm.u.st.k[0], key0 + l32, 2 * st + g)), qbi[st], sa);
+    if (mt == w) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        if (drow(e, g) > l32) sa[e] = -INFINITY;
+    }
+    bf16x8 pa0, pa1;
+    softmax(sa, pa0, pa1);
+#pragma unroll
+    for (int t = 0; t < NDT; ++t) {
+      oacc[t] = mfma32(ld8(&sm.u.fin.vT[t * 32 + l32][key0 + 8 * g]), pa0, oacc[t]);
+      oacc[t] = mfma32(ld8(&sm.u.fin.vT[t * 32 + l32][key0 + 16 + 8 * g]), pa1, oacc[t]);
+    }
+  }
+  const float ls = wave_sum32(lsum);
+  const float inv = 1.0f / ls;
+  bf16* op = o + b * os.b + h * os.h + (int64_t)irow * os.t;
+#pragma unroll
+  for (int t = 0; t < NDT; ++t)
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) {
+      bf16x4 bb;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) bb[u] = (bf16)(oacc[t][4 * qq + u] * inv);
+      *reinterpret_cast<bf16x4*>(op + t * 32 + 8 * qq + 4 * g) = bb;
+    }
+  if (g == 0) lse[(int64_t)bh * T + irow] = m + log2f(ls);
 }
 
 // Workgroup id of an attention grid (nblk row blocks x B*Hkv kv heads x G query heads)

@@ -224,6 +224,22 @@ def get_precision() -> str:
     return {v: k for k, v in _PRECISIONS.items()}[code]
 
 
+def set_fused_forward(on: bool = True) -> None:
+    """Forward kernel schedule for the calls that follow (process-wide).
+
+    On (default): at head dim <= 64 with one query head per kv head the preconditioner chain
+    and the causal attention of each 128-row block run in one fused kernel that feeds every
+    staged key tile to both; off: the chain kernel, then the attention kernel.  The results
+    agree up to the rounding order of the attention's online softmax.
+    """
+    lib = _lib.load()
+    _lib.check(lib, lib.lucid_set_fused_forward(1 if on else 0), "lucid_set_fused_forward")
+
+
+def get_fused_forward() -> bool:
+    return bool(_lib.load().lucid_get_fused_forward())
+
+
 def head_row_mass(ws: torch.Tensor, B: int, Hq: int, Hkv: int, T: int, D: int) -> torch.Tensor:
     """Per-head row mass recorded in a forward workspace (float [B*Hkv]); heads above 4 ran the
     exact chain kernels.  ``T`` is the padded length the forward ran at."""

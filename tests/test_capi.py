@@ -45,7 +45,7 @@ def test_every_declared_symbol_is_exported(built, header):
 def test_abi_version_and_workspace(built):
     from lucid_amd import _lib
     lib = _lib.load()
-    assert lib.lucid_abi_version() == 4
+    assert lib.lucid_abi_version() == 5
     ws = lib.lucid_fwd_workspace_bytes(1, 16, 16, 32768, 64)
     # rinv + K^T + V' (bf16) + V'^T + diagonal inverses + -(X_B P_BA) per 128-row block
     # + lo parts of V' and V'^T + row masses + lo part of O + counters, each 256-byte aligned

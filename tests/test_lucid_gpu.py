@@ -230,3 +230,38 @@ def test_auto_precision_picks_exact_for_correlated_heads():
         scale = float(np.abs(vp_ref[:, h]).max())
         assert _maxerr(vp[:, h], vp_ref[:, h]) <= 2e-3 * scale
     check("o", _maxerr(o, o_ref), float(np.abs(o_ref).max()))
+
+
+@pytest.mark.parametrize("B,H,T,qk_std", [(1, 2, 128, None), (2, 2, 640, None), (1, 3, 1024, 1.0)])
+def test_fused_forward_matches_two_kernel_forward(B, H, T, qk_std):
+    """The fused forward (chain and attention of each 128-row block in one kernel; the default
+    at head dim 64 with Hq == Hkv) against the two-kernel sequence on the same inputs: O, V'
+    and every gradient agree to rounding order, and both meet the oracle bars.  T = 128 is a
+    single block (no earlier pair), T = 640 an odd number of blocks."""
+    from lucid_amd import get_fused_forward, lucid_attention, set_fused_forward
+    D = 64
+    q, k, v, do = _inputs(B, H, H, T, D, seed=7 * T + B, qk_std=qk_std)
+    print(f"case fused forward B={B} H={H} T={T} qk_std={qk_std}", flush=True)
+    assert get_fused_forward()
+    got = {}
+    for fused in (True, False):
+        set_fused_forward(fused)
+        try:
+            qg, kg, vg = (t.cuda().requires_grad_() for t in (q, k, v))
+            o, vp = lucid_attention(qg, kg, vg, return_vprime=True)
+            o.backward(do.cuda())
+            torch.cuda.synchronize()
+        finally:
+            set_fused_forward(True)
+        got[fused] = {"o": o, "vprime": vp, "dq": qg.grad, "dk": kg.grad, "dv": vg.grad}
+    o_ref, vp_ref = R.lucid_attention(_np(q), _np(k), _np(v), D ** -0.5, 1e-5)
+    dq, dk, dv = R.lucid_attention_grads(_np(q), _np(k), _np(v), _np(do), D ** -0.5, 1e-5)
+    refs = {"o": o_ref, "vprime": vp_ref, "dq": dq, "dk": dk, "dv": dv}
+    for name, ref in refs.items():
+        scale = float(np.abs(ref).max())
+        for fused in (True, False):
+            check(f"{name} ({'fused' if fused else 'two kernels'})", _maxerr(got[fused][name], ref), scale)
+        diff = float((got[True][name].float() - got[False][name].float()).abs().max())
+        print(f"  {name}: fused vs two kernels {diff:.2e} (scale {scale:.2e})", flush=True)
+        # the paths differ only in fp32 summation order (and the bf16 rounding that follows)
+        assert diff <= (1e-5 if name == "vprime" else 1e-2) * scale, f"{name}: {diff:.3e}"

@@ -50,7 +50,7 @@ CASES = [
 
 @pytest.mark.parametrize("B,Hq,Hkv,T,D,corr", CASES)
 def test_seams_composed_like_lucid_attention(B, Hq, Hkv, T, D, corr):
-    from lucid_amd import eager_lucid_attention_forward, get_v_prime, lucid_attention
+    from lucid_amd import eager_lucid_attention_forward, get_v_prime, lucid_attention, set_fused_forward
     q, k, v, do = _inputs(B, Hq, Hkv, T, D, seed=T + D + corr, correlated=corr)
     print(f"case seams B={B} Hq={Hq} Hkv={Hkv} T={T} D={D} correlated={corr}", flush=True)
     s = D ** -0.5
@@ -61,15 +61,25 @@ def test_seams_composed_like_lucid_attention(B, Hq, Hkv, T, D, corr):
     o, w = eager_lucid_attention_forward(qg, kg, v_prime, s, mask)
     assert w is None and o.shape == (B, T, Hq, D)
     o.backward(do.cuda())
-    # the fused op on the same inputs
+    # the fused op on the same inputs, with the two-kernel forward (chain, then attention: the
+    # kernels the seams run)
     qf, kf, vf = (t.cuda().requires_grad_() for t in (q, k, v))
-    of, vpf = lucid_attention(qf, kf, vf, s, return_vprime=True)
+    set_fused_forward(False)
+    try:
+        of, vpf = lucid_attention(qf, kf, vf, s, return_vprime=True)
+    finally:
+        set_fused_forward(True)
     of.backward(do.cuda())
+    # and with the default schedule (at Hq == Hkv the fused chain + attention kernel)
+    o_def, vp_def = lucid_attention(q.cuda(), k.cuda(), v.cuda(), s, return_vprime=True)
     torch.cuda.synchronize()
-    # the seam's V' is the fused V' rounded to the value dtype, and the attention kernels read
-    # the same bf16 V' in both, so O agrees exactly
+    # the seam's V' is the fused op's V' rounded to the value dtype, and the attention kernels
+    # read the same bf16 V' in both, so O agrees exactly
     assert torch.equal(v_prime.detach(), vpf.to(torch.bfloat16))
     assert torch.equal(o.detach(), of.detach())
+    # the fused kernel sums in another order: V' to fp32 rounding, O to one bf16 rounding step
+    assert float((vp_def - vpf).abs().max()) <= 1e-5 * float(vpf.abs().max())
+    assert float((o_def.float() - of.float()).abs().max()) <= 1e-2 * float(of.float().abs().max())
     o_ref, vp_ref = R.lucid_attention(_np(q), _np(k), _np(v), s, 1e-5)
     grads = R.lucid_attention_grads(_np(q), _np(k), _np(v), _np(do), s, 1e-5)
     check("o", _err(o, o_ref), float(np.abs(o_ref).max()))
