@@ -49,6 +49,7 @@ KERNEL_FLOPS = {
     "lucid_attn_bwd_dkdv_kernel": lambda B, Hq, Hkv, T, D: 4.0 * T * T * D * B * Hq,  # S, dV', dP, dK
     "lucid_attn_bwd_dq_kernel": lambda B, Hq, Hkv, T, D: 1.0 * T * T * D * B * Hq,    # dQ
     "lucid_precond_bwd_col_kernel": lambda B, Hq, Hkv, T, D: 4.0 * T * T * D * B * Hkv,  # P, P^T dV, dV V'^T, M^T K^
+    "lucid_precond_bwd_col_wide_kernel": lambda B, Hq, Hkv, T, D: 4.0 * T * T * D * B * Hkv,  # the same, 256 columns/WG
     "lucid_precond_bwd_row_kernel": lambda B, Hq, Hkv, T, D: 1.0 * T * T * D * B * Hkv,  # M K^
 }
 

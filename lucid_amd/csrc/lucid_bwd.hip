@@ -980,6 +980,262 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
 }
 
 // ---------------------------------------------------------------------------
+// The column chain with 256 columns per workgroup (head dim 64, bf16 chains; the default
+// when T is a multiple of 256): eight waves, wave w owns columns J0 + 32w .. +32 of the
+// four 64-column sub-blocks A..D (w >> 1), so every staged row tile (K rows, dV rows,
+// 1/rms) serves twice the columns of lucid_precond_bwd_col_kernel and a head's tiles are
+// fetched half as often.  The sweep body is that kernel's.  After the sweep over the
+// rows below the block, the sub-blocks are solved from the last (D) to the first (A):
+//   dV_s = X_s^T R_s  (R_s = dV'_s - acc_s, X_s = P_ss^-1), published as the head's next
+//   64-row block; its dV rows (bf16, from the solve) and K rows are put in LDS in the
+//   sweep layout, and the waves of the earlier sub-blocks take them as one more sweep
+//   step (P^T dV and the M^T K^ column sums), while the two waves of sub-block s add the
+//   strictly lower in-block terms of their column sums (rows r > c of the same block).
+// So the in-block coupling needs no separate cross-term phase and a head has half as many
+// hand-offs.  counters[bh] = n: the last n 64-row blocks of dV are published (as in
+// lucid_precond_bwd_col_kernel).  Heads of the exact chains return at once.
+// ---------------------------------------------------------------------------
+template <int D>
+struct PcolWideSmem {
+  bf16 k[3][64 * D];  // staged row tiles (swizzled, chunk c of row r at c ^ (r & 7))
+  bf16 dv[3][64 * D];
+  float r[3][64];
+  float Rt[D][68];    // R^T of the sub-block being solved
+  float Xt[64][68];   // Xt[c][r] = X[r][c] of that sub-block
+  bf16 sk[64 * D];    // the solved sub-block as a row tile: K rows, dV rows, 1/rms
+  bf16 sdv[64 * D];
+  float sr[64];
+};
+
+template <int D>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void lucid_precond_bwd_col_wide_kernel(
+    const bf16* __restrict__ k, Strides ks, int Hkv, int T, int BH, const float* __restrict__ rinv, float scale,
+    const bf16* __restrict__ vpb, const float* __restrict__ pinv, const float* __restrict__ mass,
+    const float* __restrict__ dvp, bf16* __restrict__ dvb, bf16* __restrict__ dv_out, Strides dvs,
+    float* __restrict__ colsum, int* __restrict__ counters) {
+  static_assert(D == 64, "wide column chain: head dim 64");
+  constexpr int NDT = D / 32;
+  constexpr int NKS = D / 16;
+  constexpr int NTHR = 512;
+  __shared__ __attribute__((aligned(16))) PcolWideSmem<D> sm;
+
+  const int NT = T / 64, NP = T / 256;
+  const int id = blockIdx.x;
+  const int p = NP - 1 - id / BH, bh = id - (id / BH) * BH;
+  if (mass[bh] > kExactMass) return;  // the exact instance of the 128-column chain solves this head
+  const int b = bh / Hkv, h = bh - b * Hkv;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int g = lane >> 5, l32 = lane & 31;
+  const int sbw = w >> 1;         // this wave's sub-block
+  const int J0 = p * 256;
+  const int jc = J0 + 32 * w + l32;  // this lane's column
+  const bf16* kh = k + b * ks.b + h * ks.h;
+  const float* rv = rinv + (int64_t)bh * T;
+  const bf16* dvbh = dvb + (int64_t)bh * T * D;
+  const bf16* vph = vpb + (int64_t)bh * T * D;
+  int* cnt = counters + bh;
+  const float sl2 = scale * LOG2E_F;
+  const float c0 = LOG2E_F / scale;
+
+  bf16x8 kbJ[NKS], vbJ[NKS];
+#pragma unroll
+  for (int st = 0; st < NKS; ++st) {
+    kbJ[st] = ld8(kh + (int64_t)jc * ks.t + 16 * st + 8 * g);
+    vbJ[st] = ld8(vph + (int64_t)jc * D + 16 * st + 8 * g);
+  }
+  const float aJ = sl2 * rv[jc];
+  f32x16 adv[NDT], acs[NDT];
+  {
+    const float* src = dvp + ((int64_t)bh * T + jc) * D;
+#pragma unroll
+    for (int t = 0; t < NDT; ++t) {
+      acs[t] = zero16();
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) {
+        const f32x4 x = *reinterpret_cast<const f32x4*>(src + t * 32 + 8 * qq + 4 * g);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) adv[t][4 * qq + u] = -x[u];
+      }
+    }
+  }
+
+  // one 64-row tile against this wave's columns: acc^T += dV^T P, C^T += K^T (r G P);
+  // DIAG: the rows of this wave's own sub-block, strictly below its columns, C only
+  auto sweep_rows = [&](const bf16* tk, const bf16* tdv, const float* tr, const bool DIAG) {
+#pragma unroll
+    for (int rh = 0; rh < 2; ++rh) {
+      if (DIAG && rh * 32 + 31 <= (w & 1) * 32) continue;  // rows all at or above the columns
+      bf16x8 ka[NKS], da[NKS];
+#pragma unroll
+      for (int st = 0; st < NKS; ++st) {
+        ka[st] = ld8(swz<D / 8>(tk, rh * 32 + l32, 2 * st + g));
+        da[st] = ld8(swz<D / 8>(tdv, rh * 32 + l32, 2 * st + g));
+      }
+      float rI[16];
+      lds_rows16(tr + rh * 32, g, rI);
+      f32x16 sc = zero16(), gg = zero16();
+#pragma unroll
+      for (int st = 0; st < NKS; ++st) {
+        sc = mfma32(ka[st], kbJ[st], sc);
+        gg = mfma32(da[st], vbJ[st], gg);
+      }
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        float pe = __builtin_amdgcn_exp2f(fmaf(sc[e] * aJ, rI[e], -c0));
+        // strictly below the diagonal: the diagonal terms M_jj K^_j are added by the row
+        // kernel in closed form
+        if (DIAG && rh * 32 + drow(e, g) <= (w & 1) * 32 + l32) pe = 0.f;
+        sc[e] = pe;
+        gg[e] = gg[e] * pe * rI[e];
+      }
+      const bf16x8 pb0 = pack_b(sc, 0), pb1 = pack_b(sc, 1);
+      const bf16x8 mb0 = pack_b(gg, 0), mb1 = pack_b(gg, 1);
+#pragma unroll
+      for (int t = 0; t < NDT; ++t) {
+        const bf16x8 k0 = lds_tr_a<D / 8>(tk, rh * 32, t * 32);
+        const bf16x8 k1 = lds_tr_a<D / 8>(tk, rh * 32 + 16, t * 32);
+        if (!DIAG) {
+          const bf16x8 a0 = lds_tr_a<D / 8>(tdv, rh * 32, t * 32);
+          const bf16x8 a1 = lds_tr_a<D / 8>(tdv, rh * 32 + 16, t * 32);
+          adv[t] = mfma32(a0, pb0, adv[t]);
+          adv[t] = mfma32(a1, pb1, adv[t]);
+        }
+        acs[t] = mfma32(k0, mb0, acs[t]);
+        acs[t] = mfma32(k1, mb1, acs[t]);
+      }
+    }
+  };
+
+  // ---- sweep over the 64-row tiles below the block, far (published first) to near ----
+  const int first = NT - 1, last = 4 * p + 4;
+  int ready = 0;
+  constexpr int PER = 64 * (D / 8) / NTHR;  // 16-byte loads per thread for a 64-row tile
+  constexpr int STAGE_OPS = 2 * PER;
+  const int nsteps = first - last + 1;
+  int plan_k[PER], plan_d[PER];
+  dma_plan<64, D / 8, NTHR>(ks.t, plan_k);
+  dma_plan<64, D / 8, NTHR>(D, plan_d);
+  auto stage = [&](int kk) {
+    const int i0 = (first - kk) * 64, buf = kk % 3;
+    if (w == 0) dma_f32x64(rv + i0, sm.r[buf]);
+    dma_stage<64, D / 8, NTHR>(plan_k, kh + (int64_t)i0 * ks.t, sm.k[buf]);
+    dma_stage<64, D / 8, NTHR>(plan_d, dvbh + (int64_t)i0 * D, sm.dv[buf]);
+  };
+  int issued = 0;
+  auto try_issue = [&](int upto) {
+    if (issued <= upto && issued < nsteps) {
+      const int need = NT - 1 - (first - issued);
+      if (need >= ready) {
+        const int seen = poll_counter(cnt);
+        if (seen > need) {
+          chain_acquire();
+          ready = seen;
+        }
+      }
+      if (need < ready) {
+        stage(issued);
+        ++issued;
+      }
+    }
+  };
+  if (nsteps > 0) {
+    ready = wait_counter_gt(cnt, NT - 1 - first);
+    stage(0);
+    issued = 1;
+    try_issue(1);
+    if (issued > 1) dma_wait_but<STAGE_OPS>();
+    else dma_wait();
+  }
+  __syncthreads();
+  for (int ks_ = 0; ks_ < nsteps; ++ks_) {
+    try_issue(ks_ + 2);
+    sweep_rows(sm.k[ks_ % 3], sm.dv[ks_ % 3], sm.r[ks_ % 3], false);
+    if (ks_ + 1 < nsteps && issued == ks_ + 1) {  // the next tile was not published yet: wait for it
+      ready = wait_counter_gt(cnt, NT - 1 - (first - issued));
+      stage(issued);
+      ++issued;
+    }
+    if (issued > ks_ + 2) dma_wait_but<STAGE_OPS>();  // the step after next may stay in flight
+    else dma_wait();
+    __syncthreads();
+  }
+
+  // ---- the block's sub-blocks, last to first ----
+  for (int s = 3; s >= 0; --s) {
+    const int r0 = J0 + 64 * s;  // first row (= column) of sub-block s
+    // its K rows and 1/rms into the solved-tile slots (read only after the barriers below)
+    if (w == 0) dma_f32x64(rv + r0, sm.sr);
+    dma_stage<64, D / 8, NTHR>(plan_k, kh + (int64_t)r0 * ks.t, sm.sk);
+    // R^T of its columns (its two waves) and X^T
+    if (sbw == s) {
+#pragma unroll
+      for (int t = 0; t < NDT; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sm.Rt[t * 32 + drow(e, g)][(w & 1) * 32 + l32] = -adv[t][e];
+    }
+    {
+      const float* xb = pinv + ((int64_t)bh * NT + 4 * p + s) * 4096;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int idx = tid + NTHR * u;  // 1024 chunks of 4
+        const int r = idx >> 4, c4 = (idx & 15) * 4;
+        const f32x4 x = *reinterpret_cast<const f32x4*>(xb + r * 64 + c4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sm.Xt[c4 + e][r] = x[e];
+      }
+    }
+    __syncthreads();
+    // dV^T[d][c] = sum_r R^T[d][r] X[r][c] (X lower: r >= c): four 32x32 tiles, waves 0..3
+    if (w < 4) {
+      const int dt = w >> 1, chh = w & 1;
+      f32x16 o = zero16();
+      for (int st = chh ? 2 : 0; st < 4; ++st) {
+        bf16x8 ah, al, bh8, bl;
+        split8(&sm.Rt[dt * 32 + l32][16 * st + 8 * g], ah, al);
+        split8(&sm.Xt[chh * 32 + l32][16 * st + 8 * g], bh8, bl);
+        o = mfma32(ah, bh8, o);
+        o = mfma32(ah, bl, o);
+        o = mfma32(al, bh8, o);
+      }
+      const int cl = chh * 32 + l32;  // row of dV inside the sub-block
+      const int r = r0 + cl;
+      bf16* ob = dvb + ((int64_t)bh * T + r) * D;
+      bf16* ou = dv_out + b * dvs.b + h * dvs.h + (int64_t)r * dvs.t;
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) {
+        const int d0 = dt * 32 + 8 * qq + 4 * g;
+        bf16x4 bb;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) bb[u] = (bf16)o[4 * qq + u];
+        *reinterpret_cast<bf16x4*>(ob + d0) = bb;
+        *reinterpret_cast<bf16x4*>(ou + d0) = bb;
+        *reinterpret_cast<bf16x4*>(sm.sdv + swz_off<D / 8>(cl, d0 >> 3) + (d0 & 7)) = bb;
+      }
+    }
+    dma_wait();
+    publish_counter(cnt, NT - (4 * p + s));  // waits for every wave's stores, then a barrier
+    // the solved rows against the earlier sub-blocks' columns; the strictly lower in-block
+    // column-sum terms for sub-block s's own columns
+    if (sbw < s) sweep_rows(sm.sk, sm.sdv, sm.sr, false);
+    else if (sbw == s) sweep_rows(sm.sk, sm.sdv, sm.sr, true);
+    __syncthreads();  // before the next sub-block overwrites Rt, Xt and the solved-tile slots
+  }
+  // ---- the column sums of this wave's columns ----
+  {
+    float* dst = colsum + ((int64_t)bh * T + jc) * D;
+#pragma unroll
+    for (int t = 0; t < NDT; ++t)
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) {
+        f32x4 x;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) x[u] = acs[t][4 * qq + u];
+        *reinterpret_cast<f32x4*>(dst + t * 32 + 8 * qq + 4 * g) = x;
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Row sums R_I = sum_{J <= I} M_IJ K^_J, then dK^ = -s (R + C), the RMSNorm
 // backward and the attention dK (dka; null for the preconditioner-only backward).
 // No chain: every dV is known.

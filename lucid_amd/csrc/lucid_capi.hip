@@ -306,9 +306,16 @@ int launch_precond_bwd(const void* k, const int64_t* ks, const FwdWs& f, void* d
   const int BH = B * Hkv;
   // each chain kernel in two instances (bf16 and exact), selected per head by the forward's
   // row mass; the precision forced at the forward call is recorded there
-  LUCID_LAUNCH("lucid_precond_bwd_col_kernel", (lucid::lucid_precond_bwd_col_kernel<D, false>),
-               dim3((T / 128) * BH), st, (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, scale, f.kt, f.vpb, f.vpbl,
-               f.pinv, f.mass, w.dvp, w.dvb, w.dvbl, (bf16*)dv, S(dvs), w.colsum, w.counters, lucid::Lo{});
+  // bf16 chains at head dim 64: 256 columns per workgroup when T allows it
+  if (D == 64 && T % 256 == 0) {
+    LUCID_LAUNCH_B("lucid_precond_bwd_col_wide_kernel", lucid::lucid_precond_bwd_col_wide_kernel<64>,
+                   dim3((T / 256) * BH), dim3(512), st, (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, scale, f.vpb,
+                   f.pinv, f.mass, w.dvp, w.dvb, (bf16*)dv, S(dvs), w.colsum, w.counters);
+  } else {
+    LUCID_LAUNCH("lucid_precond_bwd_col_kernel", (lucid::lucid_precond_bwd_col_kernel<D, false>),
+                 dim3((T / 128) * BH), st, (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, scale, f.kt, f.vpb, f.vpbl,
+                 f.pinv, f.mass, w.dvp, w.dvb, w.dvbl, (bf16*)dv, S(dvs), w.colsum, w.counters, lucid::Lo{});
+  }
   LUCID_LAUNCH("lucid_precond_bwd_col_exact_kernel", (lucid::lucid_precond_bwd_col_kernel<D, true>),
                dim3((T / 128) * BH), st, (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, scale, f.kt, f.vpb, f.vpbl,
                f.pinv, f.mass, w.dvp, w.dvb, w.dvbl, (bf16*)dv, S(dvs), w.colsum, w.counters, lucid::Lo{});
