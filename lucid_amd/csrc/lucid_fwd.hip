@@ -299,8 +299,10 @@ __global__ __launch_bounds__(256) void lucid_rows_in_kernel(const IT* __restrict
 // block: the keys of its own block are summed exactly (j < i), the earlier keys are
 // sampled, at most 128 keys spread evenly over the earlier 64-blocks (one key per block
 // at a row offset that varies with the row block), each weighted by the number of
-// earlier keys it stands for.  Each wave takes 32-key chunks:
-//   S[i][j] = K_i . K_j (lane <-> key j, rows i in the D layout), P = exp(s r_i r_j S - 1/s)
+// earlier keys it stands for.  Each wave takes 32-key chunks as the transposed score tile
+//   S^T[j][i] = K_j . K_i (lane <-> row i, the 16 values of a lane over keys j),
+//   P = exp(s r_i r_j S - 1/s),
+// so that a row's sum is taken inside its lanes (16 values, then the two lane halves).
 // The block's largest row total goes to mass[bh] by an integer max of the (non-negative)
 // float bits.  grid (T/64, B*Hkv), after lucid_prep_kernel (1/rms, mass[bh] = 0).
 // ---------------------------------------------------------------------------
@@ -310,6 +312,8 @@ __global__ __launch_bounds__(256) void lucid_mass_kernel(const bf16* __restrict_
                                                          float* __restrict__ mass) {
   constexpr int NKS = D / 16;
   __shared__ float part[4][64];
+  __shared__ float kr[4][32];  // 1/rms of each wave's current 32 keys
+  __shared__ float kw[4][32];  // their weights
   const int blk = blockIdx.x, bh = blockIdx.y;
   const int b = bh / Hkv, h = bh - b * Hkv;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -318,58 +322,56 @@ __global__ __launch_bounds__(256) void lucid_mass_kernel(const bf16* __restrict_
   const float* rv = rinv + (int64_t)bh * T;
   const int i0 = blk * 64;
   const float c0 = LOG2E_F / scale;
-  bf16x8 ka[2][NKS];  // A operand: the block's rows (m-tiles of 32)
-  float ri[2][16];    // s log2e / rms of the D-layout rows
+  bf16x8 kb[2][NKS];  // B operand: the block's rows (n-tiles of 32)
+  float ri[2];        // s log2e / rms of this lane's rows
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt) {
+  for (int nt = 0; nt < 2; ++nt) {
 #pragma unroll
-    for (int st = 0; st < NKS; ++st) ka[mt][st] = ld8(kp + (int64_t)(i0 + mt * 32 + l32) * ks.t + 16 * st + 8 * g);
-    load_rows16(rv + i0 + mt * 32, g, ri[mt]);
-#pragma unroll
-    for (int e = 0; e < 16; ++e) ri[mt][e] *= scale * LOG2E_F;
+    for (int st = 0; st < NKS; ++st) kb[nt][st] = ld8(kp + (int64_t)(i0 + nt * 32 + l32) * ks.t + 16 * st + 8 * g);
+    ri[nt] = rv[i0 + nt * 32 + l32] * scale * LOG2E_F;
   }
-  float acc[2][16];
-#pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) acc[mt][e] = 0.f;
+  float acc[2] = {0.f, 0.f};
   const int off = (blk * 29) & 63;           // sampled row inside a sampled block
   const int ns = min(blk, 128);              // sampled keys
   const int nchunk = 2 + (ns + 31) / 32;     // chunks 0, 1: own block; 2..: sampled
   const float wsample = ns ? 64.f * (float)blk / (float)ns : 0.f;
   for (int c = w; c < nchunk; c += 4) {
     const bool own = c < 2;
-    const int n = 32 * (c - 2) + l32;        // this lane's sample
+    const int n = 32 * (c - 2) + l32;        // this lane's sample (A-operand lane <-> key)
     const bool valid = own || n < ns;
     const int key = own ? i0 + 32 * c + l32 : (valid ? (int)(((int64_t)n * blk) / ns) : 0) * 64 + off;
-    const float wgt = own ? 1.f : (valid ? wsample : 0.f);
-    bf16x8 kb[NKS];
+    bf16x8 ka[NKS];
 #pragma unroll
-    for (int st = 0; st < NKS; ++st) kb[st] = ld8(kp + (int64_t)key * ks.t + 16 * st + 8 * g);
-    const float rj = rv[key];
+    for (int st = 0; st < NKS; ++st) ka[st] = ld8(kp + (int64_t)key * ks.t + 16 * st + 8 * g);
+    if (g == 0) {
+      kr[w][l32] = rv[key];
+      kw[w][l32] = own ? 1.f : (valid ? wsample : 0.f);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
+    float rj[16], wj[16];
+    lds_rows16(kr[w], g, rj);
+    lds_rows16(kw[w], g, wj);
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
+    for (int nt = 0; nt < 2; ++nt) {
       f32x16 sd = zero16();
 #pragma unroll
-      for (int st = 0; st < NKS; ++st) sd = mfma32(ka[mt][st], kb[st], sd);
+      for (int st = 0; st < NKS; ++st) sd = mfma32(ka[st], kb[nt][st], sd);
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        float p = __builtin_amdgcn_exp2f(fmaf(sd[e] * ri[mt][e], rj, -c0));
-        if (own && 32 * c + l32 >= mt * 32 + drow(e, g)) p = 0.f;  // keys j < i only
-        acc[mt][e] = fmaf(wgt * p, p, acc[mt][e]);
+        float p = __builtin_amdgcn_exp2f(fmaf(sd[e] * ri[nt], rj[e], -c0));
+        if (own && 32 * c + drow(e, g) >= nt * 32 + l32) p = 0.f;  // keys j < i only
+        acc[nt] = fmaf(wj[e] * p, p, acc[nt]);
       }
     }
+    __builtin_amdgcn_wave_barrier();  // every lane has read kr, kw before the next chunk writes them
   }
-  // sum over the 32 keys of a lane half, then over the waves
+  // the two lane halves hold the two halves of each row's keys; then the sum over the waves
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      float x = acc[mt][e];
-#pragma unroll
-      for (int m = 16; m >= 1; m >>= 1) x += __shfl_xor(x, m, 32);
-      if (l32 == 0) part[w][mt * 32 + drow(e, g)] = x;
-    }
+  for (int nt = 0; nt < 2; ++nt) {
+    const float x = wave_sum32(acc[nt]);
+    if (g == 0) part[w][nt * 32 + l32] = x;
+  }
   __syncthreads();
   if (tid < 64) {
     float x = part[0][tid] + part[1][tid] + part[2][tid] + part[3][tid];
