@@ -225,7 +225,8 @@ int launch_attn_fwd(const void* q, const int64_t* qs, const void* k, const int64
                     float* lse, const FwdWs& w, int B, int Hq, int Hkv, int T, float scale, hipStream_t st) {
   const int BHq = B * Hq;
   if constexpr (D == 128) {
-    LUCID_LAUNCH_B("lucid_attn_fwd_wide_kernel", lucid::lucid_attn_fwd_wide_kernel<D>, dim3(((T + 255) / 256) * BHq),
+    // 128 keys per staged tile: half the barriers and row-max updates of 64 (1 % at config 5)
+    LUCID_LAUNCH_B("lucid_attn_fwd_wide_kernel", (lucid::lucid_attn_fwd_wide_kernel<D, 128>), dim3(((T + 255) / 256) * BHq),
                    dim3(512), st, (const bf16*)q, S(qs), (const bf16*)k, S(ks), w.vpt, (bf16*)o, S(os), lse, w.mass,
                    w.olo, Hq, Hkv, T, B * Hkv, scale);
   } else {

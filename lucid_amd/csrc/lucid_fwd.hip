@@ -1479,23 +1479,26 @@ __device__ __forceinline__ void attn_block_of(int id, int nblk, int BH, int G, i
 // ---------------------------------------------------------------------------
 // Causal attention on V' at head dim 128 (bf16): 256 query rows per workgroup as eight
 // waves of 32 rows (one n-tile each), two waves per SIMD, so that one wave's softmax runs
-// beside the other's MFMAs; every 64-key tile of K and V'^T is staged once per workgroup
-// in LDS (double buffered, register-staged one tile ahead by all 512 threads, padded rows)
-// and read by all eight waves.  Per wave and tile: S^T[j][i] = K_j . Q_i (16 MFMAs), the
-// online softmax (lazy rescale by 2^8), O^T[d][i] += V'^T[d][j] P^T[j][i] (16 MFMAs).
+// beside the other's MFMAs; every KT-key tile of K and V'^T (KT = 64 or 128; the launch uses
+// 128) is staged once per workgroup in LDS (double buffered, register-staged one tile ahead
+// by all 512 threads, padded rows) and read by all eight waves.  Per wave and 64 keys:
+// S^T[j][i] = K_j . Q_i (16 MFMAs), the online softmax (one row max per staged tile, lazy
+// rescale by 2^8), O^T[d][i] += V'^T[d][j] P^T[j][i] (16 MFMAs).
 // Outputs as lucid_attn_fwd_kernel (O, lse2, O's lo part for exact heads).
 // ---------------------------------------------------------------------------
-template <int D>
+template <int D, int KT = 64>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void lucid_attn_fwd_wide_kernel(
     const bf16* __restrict__ q, Strides qs, const bf16* __restrict__ k, Strides ks, const bf16* __restrict__ vpt,
     bf16* __restrict__ o, Strides os, float* __restrict__ lse, const float* __restrict__ mass,
     bf16* __restrict__ olo, int Hq, int Hkv, int T, int BH, float scale) {
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
-  constexpr int CH = D / 64;  // 16-byte chunks per thread for each of the K and V'^T tiles
+  constexpr int NMT = KT / 32;        // 32-key sub-tiles per staged tile
+  constexpr int CH = D * KT / 4096;   // 16-byte chunks per thread for each of the K and V'^T tiles
   static_assert(D == 128, "the wide attention kernel is the head-dim-128 path");
-  __shared__ __attribute__((aligned(16))) bf16 lk[2][64][D + 8];
-  __shared__ __attribute__((aligned(16))) bf16 lv[2][D][64 + 8];
+  static_assert(KT == 64 || KT == 128, "keys per staged tile");
+  __shared__ __attribute__((aligned(16))) bf16 lk[2][KT][D + 8];
+  __shared__ __attribute__((aligned(16))) bf16 lv[2][D][KT + 8];
 
   const int G = Hq / Hkv;
   const int nblk = (T + 255) / 256;
@@ -1522,17 +1525,17 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void l
   for (int t = 0; t < NDT; ++t) oacc[t] = zero16();
   float m = -1e30f, lsum = 0.f;
 
-  const int ntile = (min(r0 + 256, T) + 63) / 64;
-  const int last_w = row0 / 64;  // the tile holding this wave's diagonal
+  const int ntile = (min(r0 + 256, T) + KT - 1) / KT;
+  const int last_w = row0 / KT;  // the tile holding this wave's diagonal
   bf16x8 stg[2 * CH];
   auto gload = [&](int j0) {
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
       const int cidx = tid + 512 * u;
       const int kr = cidx / (D / 8), kc = cidx % (D / 8);
-      stg[u] = ld8(kh + (int64_t)(j0 + kr) * ks.t + kc * 8);
-      const int vr = cidx >> 3, vc = cidx & 7;
-      stg[CH + u] = ld8(vth + (int64_t)vr * T + j0 + vc * 8);
+      stg[u] = ld8(kh + (int64_t)min(j0 + kr, T - 1) * ks.t + kc * 8);
+      const int vr = cidx / (KT / 8), vc = cidx % (KT / 8);
+      stg[CH + u] = ld8(vth + (int64_t)vr * T + min(j0 + vc * 8, T - 8));
     }
   };
   auto lstore = [&](int buf) {
@@ -1541,7 +1544,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void l
       const int cidx = tid + 512 * u;
       const int kr = cidx / (D / 8), kc = cidx % (D / 8);
       *reinterpret_cast<bf16x8*>(&lk[buf][kr][kc * 8]) = stg[u];
-      const int vr = cidx >> 3, vc = cidx & 7;
+      const int vr = cidx / (KT / 8), vc = cidx % (KT / 8);
       *reinterpret_cast<bf16x8*>(&lv[buf][vr][vc * 8]) = stg[CH + u];
     }
   };
@@ -1551,27 +1554,27 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void l
   for (int jt = 0; jt < ntile; ++jt) {
     const int buf = jt & 1;
     const bool more = jt + 1 < ntile;
-    if (more) gload((jt + 1) * 64);
+    if (more) gload((jt + 1) * KT);
     if (jt <= last_w && row0 < T) {
-      f32x16 s[2];
+      f32x16 s[NMT];
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
+      for (int mt = 0; mt < NMT; ++mt) {
         s[mt] = zero16();
 #pragma unroll
         for (int st = 0; st < NKS; ++st)
           s[mt] = mfma32(ld8(&lk[buf][mt * 32 + l32][16 * st + 8 * g]), qb[st], s[mt]);
       }
-      if (jt == last_w) {  // causal mask: key 64 jt + mt 32 + drow > row
-        const int rel = row0 - jt * 64 + l32;  // the lane's row relative to the tile's first key
+      if (jt == last_w) {  // causal mask: key KT jt + mt 32 + drow > row
+        const int rel = row0 - jt * KT + l32;  // the lane's row relative to the tile's first key
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
+        for (int mt = 0; mt < NMT; ++mt)
 #pragma unroll
           for (int e = 0; e < 16; ++e)
             if (mt * 32 + drow(e, g) > rel) s[mt][e] = -INFINITY;
       }
       float mx = -INFINITY;
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
+      for (int mt = 0; mt < NMT; ++mt)
 #pragma unroll
         for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[mt][e]);
       mx = wave_max32(mx) * c;
@@ -1585,9 +1588,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void l
 #pragma unroll
           for (int e = 0; e < 16; ++e) oacc[t][e] *= alpha;
       }
-      bf16x8 pb[4];
+      bf16x8 pb[2 * NMT];
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
+      for (int mt = 0; mt < NMT; ++mt) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           const float p = __builtin_amdgcn_exp2f(fmaf(s[mt][e], c, -m));
@@ -1600,7 +1603,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void l
 #pragma unroll
       for (int t = 0; t < NDT; ++t)
 #pragma unroll
-        for (int k4 = 0; k4 < 4; ++k4)
+        for (int k4 = 0; k4 < 2 * NMT; ++k4)
           oacc[t] = mfma32(ld8(&lv[buf][t * 32 + l32][16 * k4 + 8 * g]), pb[k4], oacc[t]);
     }
     if (more) lstore(buf ^ 1);
