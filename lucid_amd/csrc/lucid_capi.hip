@@ -207,10 +207,17 @@ int launch_precond_fwd(const void* k, const int64_t* ks, const void* v, const in
                w.rinv, scale, w.pinv, w.zx, lucid::Lo{});
   // both instances of the chain: each solves the heads of its precision and returns at
   // once for the others
-  if (g_precision != LUCID_PRECISION_EXACT)
-    LUCID_LAUNCH("lucid_precond_fwd_kernel", (lucid::lucid_precond_fwd_kernel<D, false>), dim3((T / 128) * BH),
-                 st, (const bf16*)k, S(ks), (const bf16*)v, S(vs), Hkv, T, BH, w.rinv, scale, vprime, w.vpb,
-                 w.vpt, w.vpbl, w.vptl, w.pinv, w.zx, w.mass, w.counters, lucid::Lo{});
+  if (g_precision != LUCID_PRECISION_EXACT) {
+    if (D == 128)  // eight waves (two per SIMD) at head dim 128
+      LUCID_LAUNCH_B("lucid_precond_fwd_kernel", (lucid::lucid_precond_fwd_kernel<128, false, false, 8>),
+                     dim3((T / 128) * BH), dim3(512), st, (const bf16*)k, S(ks), (const bf16*)v, S(vs), Hkv, T, BH,
+                     w.rinv, scale, vprime, w.vpb, w.vpt, w.vpbl, w.vptl, w.pinv, w.zx, w.mass, w.counters,
+                     lucid::Lo{});
+    else
+      LUCID_LAUNCH("lucid_precond_fwd_kernel", (lucid::lucid_precond_fwd_kernel<D, false>), dim3((T / 128) * BH),
+                   st, (const bf16*)k, S(ks), (const bf16*)v, S(vs), Hkv, T, BH, w.rinv, scale, vprime, w.vpb,
+                   w.vpt, w.vpbl, w.vptl, w.pinv, w.zx, w.mass, w.counters, lucid::Lo{});
+  }
   if (g_precision != LUCID_PRECISION_FAST)
     LUCID_LAUNCH("lucid_precond_fwd_exact_kernel", (lucid::lucid_precond_fwd_kernel<D, true>),
                  dim3((T / 128) * BH), st, (const bf16*)k, S(ks), (const bf16*)v, S(vs), Hkv, T, BH, w.rinv,

@@ -469,7 +469,9 @@ __global__ __launch_bounds__(256) void lucid_zx_kernel(const bf16* __restrict__ 
 // Z through a 2-term split against bf16 V'_A.  The chain's critical path is the work
 // after the last pair becomes visible, so everything that does not depend on it (V,
 // the two inverses, Z) is loaded earlier.  At d = 64 two workgroups share a CU (LDS <= 80 KB,
-// <= 256 registers per lane) so that one's MFMA work overlaps the other's exp.
+// <= 256 registers per lane) so that one's MFMA work overlaps the other's exp.  At d = 128
+// the bf16 chain runs NW = 8 waves (two per SIMD, 220 registers): wave w owns the 32 rows
+// i0 + 32 (w % 4) .. of key half w / 4 (one n-tile instead of two), one solve tile each.
 //
 // EXACT (heads whose row mass exceeds kExactMass; the other instance returns at once for
 // them and vice versa): V' is also kept as its bf16 residual lo = bf16(V' - bf16(V'))
@@ -515,15 +517,19 @@ struct PfwdSmem<D, true, F32> {
   } u;
 };
 
-template <int D, bool EXACT, bool F32 = false>
-__global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void lucid_precond_fwd_kernel(
+template <int D, bool EXACT, bool F32 = false, int NW = 4>
+__global__ __launch_bounds__(64 * NW) LUCID_TWO_WAVES_IF((D == 64 || NW == 8) && !EXACT) void lucid_precond_fwd_kernel(
     const bf16* __restrict__ k, Strides ks, const bf16* __restrict__ v, Strides vs, int Hkv, int T, int BH,
     const float* __restrict__ rinv, float scale, float* __restrict__ vp32, bf16* __restrict__ vpb,
     bf16* __restrict__ vpt, bf16* __restrict__ vpbl, bf16* __restrict__ vptl, float* __restrict__ pinv,
     const float* __restrict__ zx, const float* __restrict__ mass, int* __restrict__ counters, Lo lo) {
   static_assert(EXACT || !F32, "fp32 inputs run the exact chains");
+  static_assert(NW == 4 || (NW == 8 && D == 128 && !EXACT), "eight waves: the bf16 chain at head dim 128");
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
+  constexpr int NTHR = 64 * NW;
+  constexpr int NTW = 8 / NW;            // 32-row n-tiles per wave (two with four waves, one with eight)
+  constexpr int RQ = NW / 2;             // row groups (waves per key half)
   constexpr bool SINGLE = EXACT && D == 128;  // one staging buffer
   __shared__ __attribute__((aligned(16))) PfwdSmem<D, EXACT, F32> sm;
 
@@ -533,7 +539,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
   const int b = bh / Hkv, h = bh - b * Hkv;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
-  const int ih = w & 1, kh = w >> 1;
+  const int ih = w % RQ, kh = w / RQ;  // rows i0 + 32 NTW ih .. (+32 NTW), key half kh of each pair
   const int i0 = i2 * 128;
   const int NT = T / 64;
   const bf16* kp = k + b * ks.b + h * ks.h;
@@ -547,11 +553,11 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
   const float c0 = LOG2E_F / scale;
 
   const bf16* klh = F32 ? lo.k + b * ks.b + h * ks.h : nullptr;
-  bf16x8 kbi[2][NKS], kbil[2][NKS];
-  float ai[2];
+  bf16x8 kbi[NTW][NKS], kbil[NTW][NKS];
+  float ai[NTW];
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
-    const int row = i0 + ih * 64 + nt * 32 + l32;
+  for (int nt = 0; nt < NTW; ++nt) {
+    const int row = i0 + ih * 32 * NTW + nt * 32 + l32;
 #pragma unroll
     for (int st = 0; st < NKS; ++st) {
       kbi[nt][st] = ld8(kp + (int64_t)row * ks.t + 16 * st + 8 * g);
@@ -560,10 +566,10 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
     ai[nt] = sl2 * rv[row];
   }
   // accumulators: -V^T for the kh = 0 waves, zero for the others
-  f32x16 acc[NDT][2];
+  f32x16 acc[NDT][NTW];
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
-    const int64_t roff = (int64_t)(i0 + ih * 64 + nt * 32 + l32) * vs.t;
+  for (int nt = 0; nt < NTW; ++nt) {
+    const int64_t roff = (int64_t)(i0 + ih * 32 * NTW + nt * 32 + l32) * vs.t;
     const bf16* vrow = vh + roff;
 #pragma unroll
     for (int t = 0; t < NDT; ++t)
@@ -589,31 +595,32 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
   // it is staged into buffer pp & 1 by direct global->LDS loads
   const int npair = i2;
   int ready = 0;
-  int plan_k[128 * (D / 8) / 256], plan_v[D * 16 / 256];
-  dma_plan<128, D / 8>(ks.t, plan_k);
-  dma_plan<D, 16>(T, plan_v);
+  int plan_k[128 * (D / 8) / NTHR], plan_v[D * 16 / NTHR];
+  dma_plan<128, D / 8, NTHR>(ks.t, plan_k);
+  dma_plan<D, 16, NTHR>(T, plan_v);
   auto stage = [&](int pp) {
     const int buf = SINGLE ? 0 : pp & 1;
     if (w < 2) dma_f32x64(rv + pp * 128 + 64 * w, &sm.u.st.r[buf][64 * w]);
-    dma_stage<128, D / 8>(plan_k, kp + (int64_t)pp * 128 * ks.t, sm.u.st.k[buf]);
-    if constexpr (F32) dma_stage<128, D / 8>(plan_k, klh + (int64_t)pp * 128 * ks.t, sm.u.st.kl[buf]);
-    dma_stage<D, 16>(plan_v, vpth + pp * 128, sm.u.st.v[buf]);
-    if constexpr (EXACT) dma_stage<D, 16>(plan_v, vptlh + pp * 128, sm.u.st.vl[buf]);
+    dma_stage<128, D / 8, NTHR>(plan_k, kp + (int64_t)pp * 128 * ks.t, sm.u.st.k[buf]);
+    if constexpr (F32) dma_stage<128, D / 8, NTHR>(plan_k, klh + (int64_t)pp * 128 * ks.t, sm.u.st.kl[buf]);
+    dma_stage<D, 16, NTHR>(plan_v, vpth + pp * 128, sm.u.st.v[buf]);
+    if constexpr (EXACT) dma_stage<D, 16, NTHR>(plan_v, vptlh + pp * 128, sm.u.st.vl[buf]);
   };
-  // the two inverses X_A, X_B (2 x 64 x 64 fp32): chunk u -> sub-block u >> 2
-  f32x4 xr[8];
+  // the two inverses X_A, X_B (2 x 64 x 64 fp32): chunk u -> sub-block u / XH
+  constexpr int XPER = 2048 / NTHR, XH = XPER / 2;  // 16-byte chunks per thread, per sub-block
+  f32x4 xr[XPER];
   auto xload = [&]() {
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int idx = tid + 256 * u;
+    for (int u = 0; u < XPER; ++u) {
+      const int idx = tid + NTHR * u;
       const int sb = idx >> 10, r = (idx >> 4) & 63, c4 = (idx & 15) * 4;
       xr[u] = *reinterpret_cast<const f32x4*>(pinv_blk + sb * 4096 + r * 64 + c4);
     }
   };
   auto xstore = [&](int sb) {
 #pragma unroll
-    for (int u = 4 * sb; u < 4 * sb + 4; ++u) {
-      const int idx = tid + 256 * u;
+    for (int u = XH * sb; u < XH * sb + XH; ++u) {
+      const int idx = tid + NTHR * u;
       const int r = (idx >> 4) & 63, c4 = (idx & 15) * 4;
       *reinterpret_cast<f32x4*>(&sm.u.fin.X[r][c4]) = xr[u];
     }
@@ -627,9 +634,9 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
       for (int st = 0; st < NKS; ++st) ka[st] = ld8(swz<D / 8>(sm.u.st.k[buf], key0 + l32, 2 * st + g));
       float rj[16];
       lds_rows16(&sm.u.st.r[buf][key0], g, rj);
-      bf16x8 pb[2][2], pbl[2][2];
+      bf16x8 pb[NTW][2], pbl[NTW][2];
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
+      for (int nt = 0; nt < NTW; ++nt) {
         f32x16 sc = zero16();
 #pragma unroll
         for (int st = 0; st < NKS; ++st) sc = mfma32(ka[st], kbi[nt][st], sc);
@@ -656,7 +663,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
         const bf16x8 va0 = ld8(swz<16>(sm.u.st.v[buf], t * 32 + l32, key0 / 8 + g));
         const bf16x8 va1 = ld8(swz<16>(sm.u.st.v[buf], t * 32 + l32, key0 / 8 + 2 + g));
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
+        for (int nt = 0; nt < NTW; ++nt) {
           acc[t][nt] = mfma32(va0, pb[nt][0], acc[t][nt]);
           acc[t][nt] = mfma32(va1, pb[nt][1], acc[t][nt]);
         }
@@ -664,7 +671,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
           const bf16x8 vl0 = ld8(swz<16>(sm.u.st.vl[buf], t * 32 + l32, key0 / 8 + g));
           const bf16x8 vl1 = ld8(swz<16>(sm.u.st.vl[buf], t * 32 + l32, key0 / 8 + 2 + g));
 #pragma unroll
-          for (int nt = 0; nt < 2; ++nt) {
+          for (int nt = 0; nt < NTW; ++nt) {
             acc[t][nt] = mfma32(va0, pbl[nt][0], acc[t][nt]);
             acc[t][nt] = mfma32(va1, pbl[nt][1], acc[t][nt]);
             acc[t][nt] = mfma32(vl0, pb[nt][0], acc[t][nt]);
@@ -724,9 +731,9 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
 #pragma unroll
     for (int t = 0; t < NDT; ++t)
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt)
+      for (int nt = 0; nt < NTW; ++nt)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][ih * 64 + nt * 32 + l32] = acc[t][nt][e];
+        for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][ih * 32 * NTW + nt * 32 + l32] = acc[t][nt][e];
   }
   xstore(0);
   __syncthreads();
@@ -734,10 +741,10 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
 #pragma unroll
     for (int t = 0; t < NDT; ++t)
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt)
+      for (int nt = 0; nt < NTW; ++nt)
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-          float& x = Rt[t * 32 + drow(e, g)][ih * 64 + nt * 32 + l32];
+          float& x = Rt[t * 32 + drow(e, g)][ih * 32 * NTW + nt * 32 + l32];
           x = -(acc[t][nt][e] + x);
         }
   }
@@ -756,7 +763,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
 
   // V'^T[d][r] = sum_c R^T[d][c] X[r][c] for sub-block sb (X lower triangular)
   auto diag_solve = [&](int sb) {
-    for (int tile = w; tile < NDT * 2; tile += 4) {
+    for (int tile = w; tile < NDT * 2; tile += NW) {
       const int dt = tile >> 1, rh = tile & 1;
       f32x16 o = zero16();
       const int kmax = rh ? 4 : 2;
@@ -817,7 +824,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
   diag_solve(1);
   __syncthreads();
   // V'^T of the whole block to the T-perm operand copy: 16-byte stores
-  for (int c = tid; c < D * 16; c += 256) {
+  for (int c = tid; c < D * 16; c += NTHR) {
     const int dd = c >> 4, s8 = (c & 15) * 8;
     *reinterpret_cast<bf16x8*>(vpt + ((int64_t)bh * D + dd) * T + i0 + s8) = ld8(&sm.u.fin.vT[dd][s8]);
     if constexpr (EXACT)
