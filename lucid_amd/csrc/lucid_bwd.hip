@@ -509,13 +509,16 @@ __global__ __launch_bounds__(16384 / RW) LUCID_TWO_WAVES_IF((D == 64 || RW == 32
 // last n 64-blocks of dV are published.
 // wave w owns columns J0 + 32w .. +32 (one n-tile, lane <-> column) and sweeps
 // all 64 rows of every later row tile I, so its column accumulators need no
-// cross-wave reduction.  Each later row tile (K rows, dV rows, 1/rms) is
+// cross-wave reduction.  Each later row tile (K^ rows in bf16, dV rows) is
 // staged once in LDS by direct global->LDS loads (three buffers, two tiles
-// ahead, swizzled, no registers); the transposed operands dV^T and K^T are read
+// ahead, swizzled, no registers); the transposed operands dV^T and K^^T are read
 // from the same tiles with transposing LDS loads:
-//   S[I][J] = K_I . K_J, P = exp(s r_I r_J S - 1/s), G[I][J] = dV_I . V'_J
-//   acc^T[d][J] += dV^T[d][I] P[I][J];  C^T[d][J] += K^T[d][I] (r_I G P)[I][J]
-// (acc starts at -dV'^T).  Then dV_B = X_B^T R_B, dV_A = X_A^T (R_A - P_BA^T dV_B),
+//   S[I][J] = K^_I . K_J, P = exp(s r_J S - 1/s), G[I][J] = dV_I . V'_J
+//   acc^T[d][J] += dV^T[d][I] P[I][J];  C^T[d][J] += K^^T[d][I] (G P)[I][J]
+// (acc starts at -dV'^T).  Only the swept rows' K^ is rounded to bf16: its rounding
+// differs from row to row, so it does not add up over the sums over I, while the
+// column's own key stays exact (scaled by r_J in fp32).  The EXACT instance stages raw
+// K rows and 1/rms instead and scales by r_I r_J in fp32.  Then dV_B = X_B^T R_B, dV_A = X_A^T (R_A - P_BA^T dV_B),
 // R = dV' - acc, and the diagonal-block terms of C.  The chain's critical path
 // is the work after the last tile becomes visible, so dV' and both inverses
 // are loaded earlier.  At
@@ -568,9 +571,10 @@ struct PcolSmem<D, true, F32> {
 
 template <int D, bool EXACT, bool F32 = false>
 __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void lucid_precond_bwd_col_kernel(
-    const bf16* __restrict__ k, Strides ks, int Hkv, int T, int BH, const float* __restrict__ rinv, float scale,
-    const bf16* __restrict__ kt, const bf16* __restrict__ vpb, const bf16* __restrict__ vpbl,
-    const float* __restrict__ pinv, const float* __restrict__ mass, const float* __restrict__ dvp,
+    const bf16* __restrict__ k, Strides ks, int Hkv, int T, int BH, const float* __restrict__ rinv,
+    const bf16* __restrict__ khat, float scale, const bf16* __restrict__ kt, const bf16* __restrict__ vpb,
+    const bf16* __restrict__ vpbl, const float* __restrict__ pinv, const float* __restrict__ mass,
+    const float* __restrict__ dvp,
     bf16* __restrict__ dvb, bf16* __restrict__ dvbl, std::conditional_t<F32, float, bf16>* __restrict__ dv_out,
     Strides dvs, float* __restrict__ colsum, int* __restrict__ counters, Lo lo) {
   static_assert(!F32 || (EXACT && D == 64), "fp32 inputs: exact instance, head dim 64");
@@ -599,8 +603,16 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
 
   const bf16* klh = F32 ? lo.k + b * ks.b + h * ks.h : nullptr;
   const bf16* ktlh = F32 ? lo.kt + (int64_t)bh * D * T : nullptr;
-  bf16x8 kbJ[NKS], vbJ[NKS], vbJl[NKS], kbJl[NKS];
+  // bf16 chains: the sweep stages K^ tiles (khat, rounded to bf16 once per row) against the
+  // column's raw key, so an MFMA times a_j = s log2(e) r_j gives the exponent E = s log2(e)
+  // r_i r_j K_i.K_j; P = exp2(E - c0) = C exp2(E) with C = 2^-c0: the sweep takes exp2(E),
+  // adv starts at -dV' / C, and adv and acs are multiplied by C after the sweep.  The exact
+  // instance keeps raw K tiles and the fp32 factors r_i r_j.
+  const bf16* khh = EXACT ? nullptr : khat + (int64_t)bh * T * D;
+  const float invC = EXACT ? 1.f : __builtin_amdgcn_exp2f(c0);
   const int jc = J0 + cw + l32;
+  const float aJ = sl2 * rv[jc];
+  bf16x8 kbJ[NKS], vbJ[NKS], vbJl[NKS], kbJl[NKS];
 #pragma unroll
   for (int st = 0; st < NKS; ++st) {
     kbJ[st] = ld8(kh + (int64_t)jc * ks.t + 16 * st + 8 * g);
@@ -608,7 +620,6 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
     if constexpr (EXACT) vbJl[st] = ld8(vpbl + ((int64_t)bh * T + jc) * D + 16 * st + 8 * g);
     if constexpr (F32) kbJl[st] = ld8(klh + (int64_t)jc * ks.t + 16 * st + 8 * g);
   }
-  const float aJ = sl2 * rv[jc];
   f32x16 adv[NDT], acs[NDT];
   {
     const float* src = dvp + ((int64_t)bh * T + jc) * D;
@@ -619,7 +630,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
       for (int qq = 0; qq < 4; ++qq) {
         const f32x4 x = *reinterpret_cast<const f32x4*>(src + t * 32 + 8 * qq + 4 * g);
 #pragma unroll
-        for (int u = 0; u < 4; ++u) adv[t][4 * qq + u] = -x[u];
+        for (int u = 0; u < 4; ++u) adv[t][4 * qq + u] = -x[u] * invC;
       }
     }
   }
@@ -636,8 +647,12 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
   dma_plan<64, D / 8>(D, plan_d);
   auto stage = [&](int k) {
     const int i0 = (first - k) * 64, buf = k % 3;
-    if (w == 0) dma_f32x64(rv + i0, sm.u.st.r[buf]);
-    dma_stage<64, D / 8>(plan_k, kh + (int64_t)i0 * ks.t, sm.u.st.k[buf]);
+    if constexpr (EXACT) {
+      if (w == 0) dma_f32x64(rv + i0, sm.u.st.r[buf]);
+      dma_stage<64, D / 8>(plan_k, kh + (int64_t)i0 * ks.t, sm.u.st.k[buf]);
+    } else {
+      dma_stage<64, D / 8>(plan_d, khh + (int64_t)i0 * D, sm.u.st.k[buf]);
+    }
     dma_stage<64, D / 8>(plan_d, dvbh + (int64_t)i0 * D, sm.u.st.dv[buf]);
     if constexpr (EXACT) dma_stage<64, D / 8>(plan_d, dvblh + (int64_t)i0 * D, sm.u.st.dvl[buf]);
     if constexpr (F32) dma_stage<64, D / 8>(plan_k, klh + (int64_t)i0 * ks.t, sm.u.st.kl[buf]);
@@ -704,7 +719,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
         da[st] = ld8(swz<D / 8>(sm.u.st.dv[buf], rh * 32 + l32, 2 * st + g));
       }
       float rI[16];
-      lds_rows16(&sm.u.st.r[buf][rh * 32], g, rI);
+      if constexpr (EXACT) lds_rows16(&sm.u.st.r[buf][rh * 32], g, rI);
       f32x16 sc = zero16(), gg = zero16();
 #pragma unroll
       for (int st = 0; st < NKS; ++st) {
@@ -729,9 +744,9 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
       }
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const float pe = __builtin_amdgcn_exp2f(fmaf(sc[e] * aJ, rI[e], -c0));
+        const float pe = __builtin_amdgcn_exp2f(EXACT ? fmaf(sc[e] * aJ, rI[e], -c0) : sc[e] * aJ);
         sc[e] = pe;
-        gg[e] = gg[e] * pe * rI[e];
+        gg[e] = EXACT ? gg[e] * pe * rI[e] : gg[e] * pe;
       }
       const bf16x8 pb0 = pack_b(sc, 0), pb1 = pack_b(sc, 1);
       const bf16x8 mb0 = pack_b(gg, 0), mb1 = pack_b(gg, 1);
@@ -788,6 +803,16 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
     __syncthreads();
   }
 
+  if constexpr (!EXACT) {  // the sweep's factor 1/C
+    const float Cf = __builtin_amdgcn_exp2f(-c0);
+#pragma unroll
+    for (int t = 0; t < NDT; ++t)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        adv[t][e] *= Cf;
+        acs[t][e] *= Cf;
+      }
+  }
   // ---- R = dV' - acc = -adv for this wave's columns; X^T of sub-block B ----
   float(*Rt)[132] = sm.u.fin.Rt;
 #pragma unroll
@@ -982,12 +1007,12 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
 // ---------------------------------------------------------------------------
 // The column chain with 256 columns per workgroup (head dim 64, bf16 chains; the default
 // when T is a multiple of 256): eight waves, wave w owns columns J0 + 32w .. +32 of the
-// four 64-column sub-blocks A..D (w >> 1), so every staged row tile (K rows, dV rows,
-// 1/rms) serves twice the columns of lucid_precond_bwd_col_kernel and a head's tiles are
+// four 64-column sub-blocks A..D (w >> 1), so every staged row tile (K^ rows, dV rows)
+// serves twice the columns of lucid_precond_bwd_col_kernel and a head's tiles are
 // fetched half as often.  The sweep body is that kernel's.  After the sweep over the
 // rows below the block, the sub-blocks are solved from the last (D) to the first (A):
 //   dV_s = X_s^T R_s  (R_s = dV'_s - acc_s, X_s = P_ss^-1), published as the head's next
-//   64-row block; its dV rows (bf16, from the solve) and K rows are put in LDS in the
+//   64-row block; its dV rows (bf16, from the solve) and K^ rows are put in LDS in the
 //   sweep layout, and the waves of the earlier sub-blocks take them as one more sweep
 //   step (P^T dV and the M^T K^ column sums), while the two waves of sub-block s add the
 //   strictly lower in-block terms of their column sums (rows r > c of the same block).
@@ -997,20 +1022,19 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
 // ---------------------------------------------------------------------------
 template <int D>
 struct PcolWideSmem {
-  bf16 k[3][64 * D];  // staged row tiles (swizzled, chunk c of row r at c ^ (r & 7))
+  bf16 k[3][64 * D];  // staged row tiles, K^ and dV (swizzled, chunk c of row r at c ^ (r & 7))
   bf16 dv[3][64 * D];
-  float r[3][64];
   float Rt[D][68];    // R^T of the sub-block being solved
   float Xt[64][68];   // Xt[c][r] = X[r][c] of that sub-block
-  bf16 sk[64 * D];    // the solved sub-block as a row tile: K rows, dV rows, 1/rms
+  bf16 sk[64 * D];    // the solved sub-block as a row tile: K^ rows, dV rows
   bf16 sdv[64 * D];
-  float sr[64];
 };
 
 template <int D>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void lucid_precond_bwd_col_wide_kernel(
-    const bf16* __restrict__ k, Strides ks, int Hkv, int T, int BH, const float* __restrict__ rinv, float scale,
-    const bf16* __restrict__ vpb, const float* __restrict__ pinv, const float* __restrict__ mass,
+    const bf16* __restrict__ k, Strides ks, int Hkv, int T, int BH, const float* __restrict__ rinv,
+    const bf16* __restrict__ khat, float scale, const bf16* __restrict__ vpb, const float* __restrict__ pinv,
+    const float* __restrict__ mass,
     const float* __restrict__ dvp, bf16* __restrict__ dvb, bf16* __restrict__ dv_out, Strides dvs,
     float* __restrict__ colsum, int* __restrict__ counters) {
   static_assert(D == 64, "wide column chain: head dim 64");
@@ -1030,6 +1054,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void l
   const int J0 = p * 256;
   const int jc = J0 + 32 * w + l32;  // this lane's column
   const bf16* kh = k + b * ks.b + h * ks.h;
+  const bf16* khh = khat + (int64_t)bh * T * D;
   const float* rv = rinv + (int64_t)bh * T;
   const bf16* dvbh = dvb + (int64_t)bh * T * D;
   const bf16* vph = vpb + (int64_t)bh * T * D;
@@ -1037,13 +1062,18 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void l
   const float sl2 = scale * LOG2E_F;
   const float c0 = LOG2E_F / scale;
 
+  // the staged K^_i rows (rounded to bf16 once per row) against the column's raw key: an
+  // MFMA times aJ gives E = s log2(e) r_i r_j K_i.K_j, and P = exp2(E - c0) = C exp2(E) with
+  // C = 2^-c0, so the sweep takes exp2(E) and the accumulators carry a factor 1/C (adv
+  // starts at -dV' / C; both are multiplied by C where they are read)
+  const float aJ = sl2 * rv[jc];
+  const float Cf = __builtin_amdgcn_exp2f(-c0), invC = __builtin_amdgcn_exp2f(c0);
   bf16x8 kbJ[NKS], vbJ[NKS];
 #pragma unroll
   for (int st = 0; st < NKS; ++st) {
     kbJ[st] = ld8(kh + (int64_t)jc * ks.t + 16 * st + 8 * g);
     vbJ[st] = ld8(vph + (int64_t)jc * D + 16 * st + 8 * g);
   }
-  const float aJ = sl2 * rv[jc];
   f32x16 adv[NDT], acs[NDT];
   {
     const float* src = dvp + ((int64_t)bh * T + jc) * D;
@@ -1054,14 +1084,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void l
       for (int qq = 0; qq < 4; ++qq) {
         const f32x4 x = *reinterpret_cast<const f32x4*>(src + t * 32 + 8 * qq + 4 * g);
 #pragma unroll
-        for (int u = 0; u < 4; ++u) adv[t][4 * qq + u] = -x[u];
+        for (int u = 0; u < 4; ++u) adv[t][4 * qq + u] = -x[u] * invC;
       }
     }
   }
 
-  // one 64-row tile against this wave's columns: acc^T += dV^T P, C^T += K^T (r G P);
-  // DIAG: the rows of this wave's own sub-block, strictly below its columns, C only
-  auto sweep_rows = [&](const bf16* tk, const bf16* tdv, const float* tr, const bool DIAG) {
+  // one 64-row tile (K^ rows, dV rows) against this wave's columns: acc^T += dV^T P,
+  // C^T += K^^T (G P); DIAG: the rows of this wave's own sub-block, strictly below its
+  // columns, C only
+  auto sweep_rows = [&](const bf16* tk, const bf16* tdv, const bool DIAG) {
 #pragma unroll
     for (int rh = 0; rh < 2; ++rh) {
       if (DIAG && rh * 32 + 31 <= (w & 1) * 32) continue;  // rows all at or above the columns
@@ -1071,8 +1102,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void l
         ka[st] = ld8(swz<D / 8>(tk, rh * 32 + l32, 2 * st + g));
         da[st] = ld8(swz<D / 8>(tdv, rh * 32 + l32, 2 * st + g));
       }
-      float rI[16];
-      lds_rows16(tr + rh * 32, g, rI);
       f32x16 sc = zero16(), gg = zero16();
 #pragma unroll
       for (int st = 0; st < NKS; ++st) {
@@ -1081,12 +1110,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void l
       }
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        float pe = __builtin_amdgcn_exp2f(fmaf(sc[e] * aJ, rI[e], -c0));
+        float pe = __builtin_amdgcn_exp2f(sc[e] * aJ);
         // strictly below the diagonal: the diagonal terms M_jj K^_j are added by the row
         // kernel in closed form
         if (DIAG && rh * 32 + drow(e, g) <= (w & 1) * 32 + l32) pe = 0.f;
         sc[e] = pe;
-        gg[e] = gg[e] * pe * rI[e];
+        gg[e] = gg[e] * pe;
       }
       const bf16x8 pb0 = pack_b(sc, 0), pb1 = pack_b(sc, 1);
       const bf16x8 mb0 = pack_b(gg, 0), mb1 = pack_b(gg, 1);
@@ -1112,13 +1141,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void l
   constexpr int PER = 64 * (D / 8) / NTHR;  // 16-byte loads per thread for a 64-row tile
   constexpr int STAGE_OPS = 2 * PER;
   const int nsteps = first - last + 1;
-  int plan_k[PER], plan_d[PER];
-  dma_plan<64, D / 8, NTHR>(ks.t, plan_k);
+  int plan_d[PER];  // K^ and dV rows: row stride D
   dma_plan<64, D / 8, NTHR>(D, plan_d);
   auto stage = [&](int kk) {
     const int i0 = (first - kk) * 64, buf = kk % 3;
-    if (w == 0) dma_f32x64(rv + i0, sm.r[buf]);
-    dma_stage<64, D / 8, NTHR>(plan_k, kh + (int64_t)i0 * ks.t, sm.k[buf]);
+    dma_stage<64, D / 8, NTHR>(plan_d, khh + (int64_t)i0 * D, sm.k[buf]);
     dma_stage<64, D / 8, NTHR>(plan_d, dvbh + (int64_t)i0 * D, sm.dv[buf]);
   };
   int issued = 0;
@@ -1149,7 +1176,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void l
   __syncthreads();
   for (int ks_ = 0; ks_ < nsteps; ++ks_) {
     try_issue(ks_ + 2);
-    sweep_rows(sm.k[ks_ % 3], sm.dv[ks_ % 3], sm.r[ks_ % 3], false);
+    sweep_rows(sm.k[ks_ % 3], sm.dv[ks_ % 3], false);
     if (ks_ + 1 < nsteps && issued == ks_ + 1) {  // the next tile was not published yet: wait for it
       ready = wait_counter_gt(cnt, NT - 1 - (first - issued));
       stage(issued);
@@ -1163,15 +1190,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void l
   // ---- the block's sub-blocks, last to first ----
   for (int s = 3; s >= 0; --s) {
     const int r0 = J0 + 64 * s;  // first row (= column) of sub-block s
-    // its K rows and 1/rms into the solved-tile slots (read only after the barriers below)
-    if (w == 0) dma_f32x64(rv + r0, sm.sr);
-    dma_stage<64, D / 8, NTHR>(plan_k, kh + (int64_t)r0 * ks.t, sm.sk);
+    // its K^ rows into the solved-tile slot (read only after the barriers below)
+    dma_stage<64, D / 8, NTHR>(plan_d, khh + (int64_t)r0 * D, sm.sk);
     // R^T of its columns (its two waves) and X^T
     if (sbw == s) {
 #pragma unroll
       for (int t = 0; t < NDT; ++t)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) sm.Rt[t * 32 + drow(e, g)][(w & 1) * 32 + l32] = -adv[t][e];
+        for (int e = 0; e < 16; ++e) sm.Rt[t * 32 + drow(e, g)][(w & 1) * 32 + l32] = -Cf * adv[t][e];
     }
     {
       const float* xb = pinv + ((int64_t)bh * NT + 4 * p + s) * 4096;
@@ -1216,8 +1242,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void l
     publish_counter(cnt, NT - (4 * p + s));  // waits for every wave's stores, then a barrier
     // the solved rows against the earlier sub-blocks' columns; the strictly lower in-block
     // column-sum terms for sub-block s's own columns
-    if (sbw < s) sweep_rows(sm.sk, sm.sdv, sm.sr, false);
-    else if (sbw == s) sweep_rows(sm.sk, sm.sdv, sm.sr, true);
+    if (sbw < s) sweep_rows(sm.sk, sm.sdv, false);
+    else if (sbw == s) sweep_rows(sm.sk, sm.sdv, true);
     __syncthreads();  // before the next sub-block overwrites Rt, Xt and the solved-tile slots
   }
   // ---- the column sums of this wave's columns ----
@@ -1229,7 +1255,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void l
       for (int qq = 0; qq < 4; ++qq) {
         f32x4 x;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) x[u] = acs[t][4 * qq + u];
+        for (int u = 0; u < 4; ++u) x[u] = Cf * acs[t][4 * qq + u];
         *reinterpret_cast<f32x4*>(dst + t * 32 + 8 * qq + 4 * g) = x;
       }
   }
@@ -1241,19 +1267,23 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void l
 // No chain: every dV is known.
 // Workgroup = 256 rows (heavy, late blocks first); wave w owns rows 64w .. +64
 // (two 32-row n-tiles, lane <-> row) and sweeps both 32-key halves of every
-// staged 64-key tile J (K rows, V' rows, 1/rms; direct global->LDS loads, three
+// staged 64-key tile J (K^ rows in bf16, V' rows; direct global->LDS loads, three
 // buffers, two tiles ahead; K^T operands through transposing LDS loads):
-//   S^T[J][I] = K_J . K_I, G^T[J][I] = V'_J . dV_I, R^T[d][I] += K^T[d][J] (r_J G P)^T[J][I]
+//   E^T[J][I] = s log2(e) r_I (K^_J . K_I), G^T[J][I] = V'_J . dV_I,
+//   R^T[d][I] += K^^T[d][J] (G exp2(E))^T[J][I]   (P = exp2(E - c0) = 2^-c0 exp2(E): R is
+//   multiplied by 2^-c0 after the sweep)
+// Only the swept keys' K^ is rounded to bf16 (a rounding that differs from key to key and
+// does not add up over the sum over J); the row's own key stays exact.
 // Each wave finishes its own rows, so no cross-wave reduction is needed.
 // EXACT (heads whose row mass exceeds kExactMass; each instance returns at once for the
-// other heads): G = V' dV^T and M K are split into hi*hi + hi*lo + lo*hi with the lo
-// parts of V' (staged beside V') and dV (held beside dV); one workgroup per CU.
+// other heads): the exponents come from raw K tiles times fp32 factors r_I r_J, and
+// G = V' dV^T and M K are split into hi*hi + hi*lo + lo*hi with the lo parts of V'
+// (staged beside V') and dV (held beside dV); one workgroup per CU.
 // ---------------------------------------------------------------------------
 template <int D, bool EXACT, bool F32 = false>
 struct ProwSmem {
-  bf16 k[3][64 * D];  // swizzled tiles (chunk c of row r at c ^ (r & 7))
+  bf16 k[3][64 * D];  // swizzled K^ tiles (chunk c of row r at c ^ (r & 7))
   bf16 v[3][64 * D];
-  float r[3][64];
 };
 template <int D, bool F32>
 struct ProwSmem<D, true, F32> {
@@ -1266,8 +1296,9 @@ struct ProwSmem<D, true, F32> {
 
 template <int D, bool EXACT, bool F32 = false>
 __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void lucid_precond_bwd_row_kernel(
-    const bf16* __restrict__ k, Strides ks, int Hkv, int T, int BH, const float* __restrict__ rinv, float scale,
-    float dn, const bf16* __restrict__ vpb, const bf16* __restrict__ vpbl, const bf16* __restrict__ dvb,
+    const bf16* __restrict__ k, Strides ks, int Hkv, int T, int BH, const float* __restrict__ rinv,
+    const bf16* __restrict__ khat, float scale, float dn, const bf16* __restrict__ vpb,
+    const bf16* __restrict__ vpbl, const bf16* __restrict__ dvb,
     const bf16* __restrict__ dvbl, const float* __restrict__ mass, const float* __restrict__ colsum,
     const float* __restrict__ dka, std::conditional_t<F32, float, bf16>* __restrict__ dk_out, Strides dks, Lo lo) {
   static_assert(!F32 || (EXACT && D == 64), "fp32 inputs: exact instance, head dim 64");
@@ -1286,6 +1317,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
   const bf16* kh = k + b * ks.b + h * ks.h;
   const float* rv = rinv + (int64_t)bh * T;
   const bf16* vh = vpb + (int64_t)bh * T * D;
+  const bf16* khh = EXACT ? nullptr : khat + (int64_t)bh * T * D;  // the exact instance reads raw K
   const float sl2 = scale * LOG2E_F;
   const float c0 = LOG2E_F / scale;
 
@@ -1295,6 +1327,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
     const int ir = active ? row0 + nt * 32 + l32 : 0;
+    aI[nt] = sl2 * rv[ir];
 #pragma unroll
     for (int st = 0; st < NKS; ++st) {
       kbI[nt][st] = ld8(kh + (int64_t)ir * ks.t + 16 * st + 8 * g);
@@ -1302,7 +1335,6 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
       dbI[nt][st] = ld8(dvb + ((int64_t)bh * T + ir) * D + 16 * st + 8 * g);
       if constexpr (EXACT) dbIl[nt][st] = ld8(dvbl + ((int64_t)bh * T + ir) * D + 16 * st + 8 * g);
     }
-    aI[nt] = sl2 * rv[ir];
   }
   f32x16 acc[NDT][2];
 #pragma unroll
@@ -1318,8 +1350,12 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
   dma_plan<64, D / 8>(D, plan_v);
   auto stage = [&](int J) {
     const int j0 = J * 64, buf = J % 3;
-    if (w == 0) dma_f32x64(rv + j0, sm.r[buf]);
-    dma_stage<64, D / 8>(plan_k, kh + (int64_t)j0 * ks.t, sm.k[buf]);
+    if constexpr (EXACT) {
+      if (w == 0) dma_f32x64(rv + j0, sm.r[buf]);
+      dma_stage<64, D / 8>(plan_k, kh + (int64_t)j0 * ks.t, sm.k[buf]);
+    } else {
+      dma_stage<64, D / 8>(plan_v, khh + (int64_t)j0 * D, sm.k[buf]);
+    }
     dma_stage<64, D / 8>(plan_v, vh + (int64_t)j0 * D, sm.v[buf]);
     if constexpr (EXACT) dma_stage<64, D / 8>(plan_v, vpbl + (int64_t)bh * T * D + (int64_t)j0 * D, sm.vl[buf]);
     if constexpr (F32) dma_stage<64, D / 8>(plan_k, klh + (int64_t)j0 * ks.t, sm.kl[buf]);
@@ -1340,7 +1376,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
         va[st] = ld8(swz<D / 8>(sm.v[buf], jh * 32 + l32, 2 * st + g));
       }
       float rJ[16];
-      lds_rows16(&sm.r[buf][jh * 32], g, rJ);
+      if constexpr (EXACT) lds_rows16(&sm.r[buf][jh * 32], g, rJ);
       bf16x8 mb[2][2], ml[2][2];
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt) {
@@ -1368,10 +1404,10 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
         }
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-          float pe = __builtin_amdgcn_exp2f(fmaf(sc[e] * aI[nt], rJ[e], -c0));
+          float pe = __builtin_amdgcn_exp2f(EXACT ? fmaf(sc[e] * aI[nt], rJ[e], -c0) : sc[e] * aI[nt]);
           // j >= i masked: the diagonal term is added in closed form after the sweep
           if (diag && jh * 32 + drow(e, g) >= nt * 32 + l32) pe = 0.f;
-          gg[e] = gg[e] * pe * rJ[e];
+          gg[e] = EXACT ? gg[e] * pe * rJ[e] : gg[e] * pe;
         }
         mb[nt][0] = pack_b(gg, 0);
         mb[nt][1] = pack_b(gg, 1);
@@ -1412,6 +1448,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
     __syncthreads();
   }
   if (!active) return;
+  const float accf = EXACT ? 1.f : __builtin_amdgcn_exp2f(-c0);  // the bf16 sweep's 2^-c0
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
     const int irow = row0 + nt * 32 + l32;
@@ -1442,7 +1479,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           const int e = 4 * qq + u;
-          const float x = -scale * (acc[t][nt][e] + cv[u]);
+          const float x = -scale * (accf * acc[t][nt][e] + cv[u]);
           const float kk = ri * ((float)kv[u] + (F32 ? (float)kvl[u] : 0.f));
           dkh[t][e] = x;
           khat[t][e] = kk;

@@ -61,6 +61,7 @@ int chain_check() {
 struct FwdWs {
   float* rinv;   // [BH][T]
   bf16* kt;      // [BH][D][T]  K^T, T-perm
+  bf16* khat;    // [BH][T][D]  K^ = r K rounded to bf16 (the bf16 chains' key tiles)
   bf16* vpb;     // [BH][T][D]  V' bf16
   bf16* vpt;     // [BH][D][T]  V'^T, T-perm
   float* pinv;   // [BH][T/64][64][64]  inverses of the diagonal blocks of P
@@ -97,6 +98,7 @@ FwdWs carve_fwd(void* base, int B, int Hq, int Hkv, int T, int D, bool f32 = fal
   };
   w.rinv = reinterpret_cast<float*>(take(BH * T * 4));
   w.kt = reinterpret_cast<bf16*>(take(BH * D * T * 2));
+  w.khat = reinterpret_cast<bf16*>(take(BH * T * D * 2));
   w.vpb = reinterpret_cast<bf16*>(take(BH * T * D * 2));
   w.vpt = reinterpret_cast<bf16*>(take(BH * D * T * 2));
   w.pinv = reinterpret_cast<float*>(take(BH * (T / 64) * 4096 * 4));
@@ -199,7 +201,8 @@ int launch_precond_fwd(const void* k, const int64_t* ks, const void* v, const in
   // a forced precision is written straight into the head masses (no mass pass)
   const float mass_init = g_precision == LUCID_PRECISION_EXACT ? 1e30f : 0.f;
   LUCID_LAUNCH("lucid_prep_kernel", lucid::lucid_prep_kernel<D>, dim3(T / 64, BH), st, (const bf16*)k, S(ks), Hkv,
-               T, eps, dn, scale, w.rinv, w.kt, w.pinv, w.counters, w.mass, mass_init, lucid::Lo{}, nullptr);
+               T, eps, dn, scale, w.rinv, w.kt, w.pinv, w.counters, w.mass, mass_init, lucid::Lo{}, nullptr,
+               w.khat);
   if (g_precision == LUCID_PRECISION_AUTO)
     LUCID_LAUNCH("lucid_mass_kernel", lucid::lucid_mass_kernel<D>, dim3(T / 64, BH), st, (const bf16*)k, S(ks),
                  Hkv, T, w.rinv, scale, w.mass);
@@ -211,16 +214,16 @@ int launch_precond_fwd(const void* k, const int64_t* ks, const void* v, const in
     if (D == 128)  // eight waves (two per SIMD) at head dim 128
       LUCID_LAUNCH_B("lucid_precond_fwd_kernel", (lucid::lucid_precond_fwd_kernel<128, false, false, 8>),
                      dim3((T / 128) * BH), dim3(512), st, (const bf16*)k, S(ks), (const bf16*)v, S(vs), Hkv, T, BH,
-                     w.rinv, scale, vprime, w.vpb, w.vpt, w.vpbl, w.vptl, w.pinv, w.zx, w.mass, w.counters,
+                     w.rinv, w.khat, scale, vprime, w.vpb, w.vpt, w.vpbl, w.vptl, w.pinv, w.zx, w.mass, w.counters,
                      lucid::Lo{});
     else
       LUCID_LAUNCH("lucid_precond_fwd_kernel", (lucid::lucid_precond_fwd_kernel<D, false>), dim3((T / 128) * BH),
-                   st, (const bf16*)k, S(ks), (const bf16*)v, S(vs), Hkv, T, BH, w.rinv, scale, vprime, w.vpb,
-                   w.vpt, w.vpbl, w.vptl, w.pinv, w.zx, w.mass, w.counters, lucid::Lo{});
+                   st, (const bf16*)k, S(ks), (const bf16*)v, S(vs), Hkv, T, BH, w.rinv, w.khat, scale, vprime,
+                   w.vpb, w.vpt, w.vpbl, w.vptl, w.pinv, w.zx, w.mass, w.counters, lucid::Lo{});
   }
   if (g_precision != LUCID_PRECISION_FAST)
     LUCID_LAUNCH("lucid_precond_fwd_exact_kernel", (lucid::lucid_precond_fwd_kernel<D, true>),
-                 dim3((T / 128) * BH), st, (const bf16*)k, S(ks), (const bf16*)v, S(vs), Hkv, T, BH, w.rinv,
+                 dim3((T / 128) * BH), st, (const bf16*)k, S(ks), (const bf16*)v, S(vs), Hkv, T, BH, w.rinv, w.khat,
                  scale, vprime, w.vpb, w.vpt, w.vpbl, w.vptl, w.pinv, w.zx, w.mass, w.counters, lucid::Lo{});
   return LUCID_OK;
 }
@@ -253,7 +256,8 @@ int launch_fwd(const void* q, const int64_t* qs, const void* k, const int64_t* k
       const int BH = B * Hkv;
       const float mass_init = g_precision == LUCID_PRECISION_EXACT ? 1e30f : 0.f;
       LUCID_LAUNCH("lucid_prep_kernel", lucid::lucid_prep_kernel<D>, dim3(T / 64, BH), st, (const bf16*)k, S(ks),
-                   Hkv, T, eps, dn, scale, w.rinv, w.kt, w.pinv, w.counters, w.mass, mass_init, lucid::Lo{}, nullptr);
+                   Hkv, T, eps, dn, scale, w.rinv, w.kt, w.pinv, w.counters, w.mass, mass_init, lucid::Lo{}, nullptr,
+                   w.khat);
       if (g_precision == LUCID_PRECISION_AUTO)
         LUCID_LAUNCH("lucid_mass_kernel", lucid::lucid_mass_kernel<D>, dim3(T / 64, BH), st, (const bf16*)k, S(ks),
                      Hkv, T, w.rinv, scale, w.mass);
@@ -267,7 +271,8 @@ int launch_fwd(const void* q, const int64_t* qs, const void* k, const int64_t* k
         // heads of the exact chains: their chain, then their attention (skip_fast)
         LUCID_LAUNCH("lucid_precond_fwd_exact_kernel", (lucid::lucid_precond_fwd_kernel<D, true>),
                      dim3((T / 128) * BH), st, (const bf16*)k, S(ks), (const bf16*)v, S(vs), Hkv, T, BH, w.rinv,
-                     scale, vprime, w.vpb, w.vpt, w.vpbl, w.vptl, w.pinv, w.zx, w.mass, w.counters, lucid::Lo{});
+                     w.khat, scale, vprime, w.vpb, w.vpt, w.vpbl, w.vptl, w.pinv, w.zx, w.mass, w.counters,
+                     lucid::Lo{});
         LUCID_LAUNCH("lucid_attn_fwd_exact_kernel", lucid::lucid_attn_fwd_kernel<D>, dim3(((T + 255) / 256) * B * Hq),
                      st, (const bf16*)q, S(qs), (const bf16*)k, S(ks), w.vpt, (bf16*)o, S(os), lse, w.mass, w.olo,
                      Hq, Hkv, T, B * Hq, scale, lucid::Lo{}, nullptr, 1);
@@ -317,22 +322,22 @@ int launch_precond_bwd(const void* k, const int64_t* ks, const FwdWs& f, void* d
   // bf16 chains at head dim 64: 256 columns per workgroup when T allows it
   if (D == 64 && T % 256 == 0) {
     LUCID_LAUNCH_B("lucid_precond_bwd_col_wide_kernel", lucid::lucid_precond_bwd_col_wide_kernel<64>,
-                   dim3((T / 256) * BH), dim3(512), st, (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, scale, f.vpb,
-                   f.pinv, f.mass, w.dvp, w.dvb, (bf16*)dv, S(dvs), w.colsum, w.counters);
+                   dim3((T / 256) * BH), dim3(512), st, (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, f.khat, scale,
+                   f.vpb, f.pinv, f.mass, w.dvp, w.dvb, (bf16*)dv, S(dvs), w.colsum, w.counters);
   } else {
     LUCID_LAUNCH("lucid_precond_bwd_col_kernel", (lucid::lucid_precond_bwd_col_kernel<D, false>),
-                 dim3((T / 128) * BH), st, (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, scale, f.kt, f.vpb, f.vpbl,
-                 f.pinv, f.mass, w.dvp, w.dvb, w.dvbl, (bf16*)dv, S(dvs), w.colsum, w.counters, lucid::Lo{});
+                 dim3((T / 128) * BH), st, (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, f.khat, scale, f.kt, f.vpb,
+                 f.vpbl, f.pinv, f.mass, w.dvp, w.dvb, w.dvbl, (bf16*)dv, S(dvs), w.colsum, w.counters, lucid::Lo{});
   }
   LUCID_LAUNCH("lucid_precond_bwd_col_exact_kernel", (lucid::lucid_precond_bwd_col_kernel<D, true>),
-               dim3((T / 128) * BH), st, (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, scale, f.kt, f.vpb, f.vpbl,
-               f.pinv, f.mass, w.dvp, w.dvb, w.dvbl, (bf16*)dv, S(dvs), w.colsum, w.counters, lucid::Lo{});
+               dim3((T / 128) * BH), st, (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, f.khat, scale, f.kt, f.vpb,
+               f.vpbl, f.pinv, f.mass, w.dvp, w.dvb, w.dvbl, (bf16*)dv, S(dvs), w.colsum, w.counters, lucid::Lo{});
   LUCID_LAUNCH("lucid_precond_bwd_row_kernel", (lucid::lucid_precond_bwd_row_kernel<D, false>),
-               dim3(((T + 255) / 256) * BH), st, (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, scale, dn, f.vpb, f.vpbl,
-               w.dvb, w.dvbl, f.mass, w.colsum, dka, (bf16*)dk, S(dks), lucid::Lo{});
+               dim3(((T + 255) / 256) * BH), st, (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, f.khat, scale, dn,
+               f.vpb, f.vpbl, w.dvb, w.dvbl, f.mass, w.colsum, dka, (bf16*)dk, S(dks), lucid::Lo{});
   LUCID_LAUNCH("lucid_precond_bwd_row_exact_kernel", (lucid::lucid_precond_bwd_row_kernel<D, true>),
-               dim3(((T + 255) / 256) * BH), st, (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, scale, dn, f.vpb, f.vpbl,
-               w.dvb, w.dvbl, f.mass, w.colsum, dka, (bf16*)dk, S(dks), lucid::Lo{});
+               dim3(((T + 255) / 256) * BH), st, (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, f.khat, scale, dn,
+               f.vpb, f.vpbl, w.dvb, w.dvbl, f.mass, w.colsum, dka, (bf16*)dk, S(dks), lucid::Lo{});
   return LUCID_OK;
 }
 
@@ -507,13 +512,13 @@ int launch_precond_fwd_f32(const void* k, const int64_t* ks, const void* v, cons
   lo.kt = w.ktl;
   lo.v = static_cast<const float*>(v);
   LUCID_LAUNCH("lucid_prep_f32_kernel", (lucid::lucid_prep_kernel<D, true>), dim3(T / 64, BH), st, w.kh, ck, Hkv,
-               T, eps, dn, scale, w.rinv, w.kt, w.pinv, w.counters, w.mass, kForceExact, lo, w.ktl);
+               T, eps, dn, scale, w.rinv, w.kt, w.pinv, w.counters, w.mass, kForceExact, lo, w.ktl, nullptr);
   LUCID_LAUNCH("lucid_zx_f32_kernel", (lucid::lucid_zx_kernel<D, true>), dim3(T / 128, BH), st, w.kh, ck, Hkv, T,
                w.rinv, scale, w.pinv, w.zx, lo);
   // the chain reads V as fp32 through lo.v with V's own strides (its bf16 operand is unused)
   LUCID_LAUNCH("lucid_precond_fwd_f32_kernel", (lucid::lucid_precond_fwd_kernel<D, true, true>),
-               dim3((T / 128) * BH), st, w.kh, ck, (const bf16*)v, S(vs), Hkv, T, BH, w.rinv, scale, vprime, w.vpb,
-               w.vpt, w.vpbl, w.vptl, w.pinv, w.zx, w.mass, w.counters, lo);
+               dim3((T / 128) * BH), st, w.kh, ck, (const bf16*)v, S(vs), Hkv, T, BH, w.rinv, nullptr, scale, vprime,
+               w.vpb, w.vpt, w.vpbl, w.vptl, w.pinv, w.zx, w.mass, w.counters, lo);
   return LUCID_OK;
 }
 
@@ -581,11 +586,11 @@ int launch_precond_bwd_f32(const FwdWs& f, void* dk, const int64_t* dks, void* d
   lo.k = f.kl;
   lo.kt = f.ktl;
   LUCID_LAUNCH("lucid_precond_bwd_col_f32_kernel", (lucid::lucid_precond_bwd_col_kernel<D, true, true>),
-               dim3((T / 128) * BH), st, f.kh, ck, Hkv, T, BH, f.rinv, scale, f.kt, f.vpb, f.vpbl, f.pinv, f.mass,
-               w.dvp, w.dvb, w.dvbl, (float*)dv, S(dvs), w.colsum, w.counters, lo);
+               dim3((T / 128) * BH), st, f.kh, ck, Hkv, T, BH, f.rinv, nullptr, scale, f.kt, f.vpb, f.vpbl, f.pinv,
+               f.mass, w.dvp, w.dvb, w.dvbl, (float*)dv, S(dvs), w.colsum, w.counters, lo);
   LUCID_LAUNCH("lucid_precond_bwd_row_f32_kernel", (lucid::lucid_precond_bwd_row_kernel<D, true, true>),
-               dim3(((T + 255) / 256) * BH), st, f.kh, ck, Hkv, T, BH, f.rinv, scale, dn, f.vpb, f.vpbl, w.dvb, w.dvbl,
-               f.mass, w.colsum, dka, (float*)dk, S(dks), lo);
+               dim3(((T + 255) / 256) * BH), st, f.kh, ck, Hkv, T, BH, f.rinv, nullptr, scale, dn, f.vpb, f.vpbl,
+               w.dvb, w.dvbl, f.mass, w.colsum, dka, (float*)dk, S(dks), lo);
   return LUCID_OK;
 }
 

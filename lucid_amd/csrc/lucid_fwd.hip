@@ -6,8 +6,8 @@
 //   O   = softmax(s Q K^T, causal) V'                     (:520-530)
 //
 // Kernels (all 256 threads = 4 waves, MFMA 32x32x16 bf16, fp32 accumulate):
-//   lucid_prep_kernel        per-row 1/rms of K, K^T in T-perm layout, inverses of the 64x64
-//                            diagonal blocks of P, zero chain counters
+//   lucid_prep_kernel        per-row 1/rms of K, K^ rows in bf16, K^T in T-perm layout,
+//                            inverses of the 64x64 diagonal blocks of P, zero chain counters
 //   lucid_zx_kernel          the in-block coupling -X_B P_BA of every 128-row chain block
 //   lucid_precond_fwd_kernel chained solve, one workgroup per (128-row block, kv head);
 //                            it waits on a per-head progress counter for V'_j, j < i and
@@ -23,7 +23,8 @@ namespace lucid {
 // prep: rinv[bh][t] = 1/sqrt(sum K^2 / dn + eps) (dn: the head dim, rows zero-padded beyond it); kt[bh][d][perm(t)] = K[t][d];
 // pinv[bh][blk] = inverse of the 64x64 diagonal block of P (fp32 forward
 // substitution by wave 0); zero the chain counter and set the head's row mass
-// to mass_init (0 before lucid_mass_kernel; a forced precision sets it directly).
+// to mass_init (0 before lucid_mass_kernel; a forced precision sets it directly);
+// khat (if not null): khat[bh][t] = K^_t = r_t K_t rounded to bf16.
 // grid (T/64, B*Hkv)
 // ---------------------------------------------------------------------------
 template <int D, bool F32 = false>
@@ -31,7 +32,8 @@ __global__ __launch_bounds__(256) void lucid_prep_kernel(const bf16* __restrict_
                                                          float eps, float dn, float scale, float* __restrict__ rinv,
                                                          bf16* __restrict__ kt, float* __restrict__ pinv,
                                                          int* __restrict__ counters, float* __restrict__ mass,
-                                                         float mass_init, Lo lo, bf16* __restrict__ ktl) {
+                                                         float mass_init, Lo lo, bf16* __restrict__ ktl,
+                                                         bf16* __restrict__ khat) {
   constexpr int SEG = D / 4;
   constexpr int NKS = D / 16;
   __shared__ bf16 tile[F32 ? 2 : 1][D][64 + 8];
@@ -45,9 +47,11 @@ __global__ __launch_bounds__(256) void lucid_prep_kernel(const bf16* __restrict_
   const bf16* klp = F32 ? lo.k + b * ks.b + h * ks.h + (int64_t)blk * 64 * ks.t : nullptr;
   const int row = tid >> 2, seg = tid & 3;
   float ss = 0.f;
+  bf16x8 xs[SEG / 8];
 #pragma unroll
   for (int c = 0; c < SEG; c += 8) {
-    bf16x8 x = ld8(kp + row * ks.t + seg * SEG + c);
+    const bf16x8 x = ld8(kp + row * ks.t + seg * SEG + c);
+    xs[c / 8] = x;
     bf16x8 xl;
     if constexpr (F32) xl = ld8(klp + row * ks.t + seg * SEG + c);
 #pragma unroll
@@ -63,10 +67,15 @@ __global__ __launch_bounds__(256) void lucid_prep_kernel(const bf16* __restrict_
   }
   ss += __shfl_xor(ss, 1, 64);
   ss += __shfl_xor(ss, 2, 64);
+  const float ri = 1.0f / sqrtf(ss / dn + eps);
   if (seg == 0) {
-    const float ri = 1.0f / sqrtf(ss / dn + eps);
     rinv[(int64_t)bh * T + blk * 64 + row] = ri;
     rr[row] = ri;
+  }
+  if (khat) {  // K^ rows in bf16 (the bf16 chains' staged key tiles)
+    bf16* dst = khat + ((int64_t)bh * T + blk * 64 + row) * D + seg * SEG;
+#pragma unroll
+    for (int c = 0; c < SEG; c += 8) *reinterpret_cast<bf16x8*>(dst + c) = scale8(xs[c / 8], ri);
   }
   if (blk == 0 && tid == 0) {
     counters[bh] = 0;
@@ -458,8 +467,9 @@ __global__ __launch_bounds__(256) void lucid_zx_kernel(const bf16* __restrict__ 
 // of 64-row blocks of V' already published (whole 128-row blocks at a time).
 //
 // The earlier keys are swept in pairs of 64-key tiles (128 keys per barrier):
-// K rows, V'^T (T-perm) and 1/rms of the pair are staged once per workgroup in
-// LDS by direct global->LDS loads (double buffered, swizzled, no registers).
+// K^ rows (bf16, the bf16 chains; raw K rows and 1/rms, the exact ones) and V'^T (T-perm)
+// of the pair are staged once per workgroup in LDS by direct global->LDS loads (double
+// buffered, swizzled, no registers).
 // wave w: ih = w & 1 -> rows i0 + 64*ih .. +64 (two 32-row n-tiles, lane <-> row)
 //         kh = w >> 1 -> the 64-key tile 2*pair + kh of every staged pair
 //   acc^T[d][i] += V'^T[d][j] P^T[j][i],  P^T[j][i] = exp(s r_i r_j K_j.K_i - 1/s)
@@ -520,7 +530,8 @@ struct PfwdSmem<D, true, F32> {
 template <int D, bool EXACT, bool F32 = false, int NW = 4>
 __global__ __launch_bounds__(64 * NW) LUCID_TWO_WAVES_IF((D == 64 || NW == 8) && !EXACT) void lucid_precond_fwd_kernel(
     const bf16* __restrict__ k, Strides ks, const bf16* __restrict__ v, Strides vs, int Hkv, int T, int BH,
-    const float* __restrict__ rinv, float scale, float* __restrict__ vp32, bf16* __restrict__ vpb,
+    const float* __restrict__ rinv, const bf16* __restrict__ khat, float scale, float* __restrict__ vp32,
+    bf16* __restrict__ vpb,
     bf16* __restrict__ vpt, bf16* __restrict__ vpbl, bf16* __restrict__ vptl, float* __restrict__ pinv,
     const float* __restrict__ zx, const float* __restrict__ mass, int* __restrict__ counters, Lo lo) {
   static_assert(EXACT || !F32, "fp32 inputs run the exact chains");
@@ -552,20 +563,29 @@ __global__ __launch_bounds__(64 * NW) LUCID_TWO_WAVES_IF((D == 64 || NW == 8) &&
   const float sl2 = scale * LOG2E_F;
   const float c0 = LOG2E_F / scale;
 
+  // bf16 chain: K^ tiles (khat) against the row keys scaled by s log2(e) r_i (one bf16
+  // rounding), so that an MFMA gives the exponent E = s log2(e) r_i r_j K_i.K_j; P = exp2(E - c0)
+  // = C exp2(E) with C = 2^-c0, so the sweep takes exp2(E) and the accumulators carry a factor
+  // 1/C (they start at -V / C; R is multiplied by C).  The exact instance keeps raw K tiles and
+  // the fp32 factors r_i r_j.
+  const bf16* khh = EXACT ? nullptr : khat + (int64_t)bh * T * D;
+  const float Cf = EXACT ? 1.f : __builtin_amdgcn_exp2f(-c0);
+  const float invC = EXACT ? 1.f : __builtin_amdgcn_exp2f(c0);
   const bf16* klh = F32 ? lo.k + b * ks.b + h * ks.h : nullptr;
   bf16x8 kbi[NTW][NKS], kbil[NTW][NKS];
   float ai[NTW];
 #pragma unroll
   for (int nt = 0; nt < NTW; ++nt) {
     const int row = i0 + ih * 32 * NTW + nt * 32 + l32;
+    ai[nt] = sl2 * rv[row];
 #pragma unroll
     for (int st = 0; st < NKS; ++st) {
-      kbi[nt][st] = ld8(kp + (int64_t)row * ks.t + 16 * st + 8 * g);
+      const bf16x8 kr = ld8(kp + (int64_t)row * ks.t + 16 * st + 8 * g);
+      kbi[nt][st] = EXACT ? kr : scale8(kr, ai[nt]);
       if constexpr (F32) kbil[nt][st] = ld8(klh + (int64_t)row * ks.t + 16 * st + 8 * g);
     }
-    ai[nt] = sl2 * rv[row];
   }
-  // accumulators: -V^T for the kh = 0 waves, zero for the others
+  // accumulators: -V^T (/ C) for the kh = 0 waves, zero for the others
   f32x16 acc[NDT][NTW];
 #pragma unroll
   for (int nt = 0; nt < NTW; ++nt) {
@@ -586,7 +606,7 @@ __global__ __launch_bounds__(64 * NW) LUCID_TWO_WAVES_IF((D == 64 || NW == 8) &&
           for (int u = 0; u < 4; ++u) vv[u] = (float)x[u];
         }
 #pragma unroll
-        for (int u = 0; u < 4; ++u) acc[t][nt][4 * qd + u] = kh ? 0.f : -vv[u];
+        for (int u = 0; u < 4; ++u) acc[t][nt][4 * qd + u] = kh ? 0.f : -vv[u] * invC;
       }
   }
 
@@ -596,12 +616,16 @@ __global__ __launch_bounds__(64 * NW) LUCID_TWO_WAVES_IF((D == 64 || NW == 8) &&
   const int npair = i2;
   int ready = 0;
   int plan_k[128 * (D / 8) / NTHR], plan_v[D * 16 / NTHR];
-  dma_plan<128, D / 8, NTHR>(ks.t, plan_k);
+  dma_plan<128, D / 8, NTHR>(EXACT ? ks.t : (int64_t)D, plan_k);
   dma_plan<D, 16, NTHR>(T, plan_v);
   auto stage = [&](int pp) {
     const int buf = SINGLE ? 0 : pp & 1;
-    if (w < 2) dma_f32x64(rv + pp * 128 + 64 * w, &sm.u.st.r[buf][64 * w]);
-    dma_stage<128, D / 8, NTHR>(plan_k, kp + (int64_t)pp * 128 * ks.t, sm.u.st.k[buf]);
+    if constexpr (EXACT) {
+      if (w < 2) dma_f32x64(rv + pp * 128 + 64 * w, &sm.u.st.r[buf][64 * w]);
+      dma_stage<128, D / 8, NTHR>(plan_k, kp + (int64_t)pp * 128 * ks.t, sm.u.st.k[buf]);
+    } else {
+      dma_stage<128, D / 8, NTHR>(plan_k, khh + (int64_t)pp * 128 * D, sm.u.st.k[buf]);
+    }
     if constexpr (F32) dma_stage<128, D / 8, NTHR>(plan_k, klh + (int64_t)pp * 128 * ks.t, sm.u.st.kl[buf]);
     dma_stage<D, 16, NTHR>(plan_v, vpth + pp * 128, sm.u.st.v[buf]);
     if constexpr (EXACT) dma_stage<D, 16, NTHR>(plan_v, vptlh + pp * 128, sm.u.st.vl[buf]);
@@ -633,7 +657,7 @@ __global__ __launch_bounds__(64 * NW) LUCID_TWO_WAVES_IF((D == 64 || NW == 8) &&
 #pragma unroll
       for (int st = 0; st < NKS; ++st) ka[st] = ld8(swz<D / 8>(sm.u.st.k[buf], key0 + l32, 2 * st + g));
       float rj[16];
-      lds_rows16(&sm.u.st.r[buf][key0], g, rj);
+      if constexpr (EXACT) lds_rows16(&sm.u.st.r[buf][key0], g, rj);
       bf16x8 pb[NTW][2], pbl[NTW][2];
 #pragma unroll
       for (int nt = 0; nt < NTW; ++nt) {
@@ -650,7 +674,8 @@ __global__ __launch_bounds__(64 * NW) LUCID_TWO_WAVES_IF((D == 64 || NW == 8) &&
           }
         }
 #pragma unroll
-        for (int e = 0; e < 16; ++e) sc[e] = __builtin_amdgcn_exp2f(fmaf(sc[e] * ai[nt], rj[e], -c0));
+        for (int e = 0; e < 16; ++e)
+          sc[e] = __builtin_amdgcn_exp2f(EXACT ? fmaf(sc[e] * ai[nt], rj[e], -c0) : sc[e]);
         pb[nt][0] = pack_b(sc, 0);
         pb[nt][1] = pack_b(sc, 1);
         if constexpr (EXACT) {
@@ -745,7 +770,7 @@ __global__ __launch_bounds__(64 * NW) LUCID_TWO_WAVES_IF((D == 64 || NW == 8) &&
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           float& x = Rt[t * 32 + drow(e, g)][ih * 32 * NTW + nt * 32 + l32];
-          x = -(acc[t][nt][e] + x);
+          x = -Cf * (acc[t][nt][e] + x);
         }
   }
   // Z rows of this wave's B output tiles (row half rh = w & 1), 8 columns per lane half and
@@ -1204,13 +1229,15 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(true) void lucid_fused_fwd_
   const float c0 = LOG2E_F / scale;
   const float c = sl2;  // attention: P = exp2(c S - m)
 
+  // the row's key scaled by s log2(e) r_i (one bf16 rounding): with the staged raw K_j rows
+  // (shared with the attention) the chain's exponent is r_j times the product, minus c0
+  const float ai = sl2 * rv[irow];
   bf16x8 kbi[NKS], qbi[NKS];
 #pragma unroll
   for (int st = 0; st < NKS; ++st) {
-    kbi[st] = ld8(kp + (int64_t)irow * ks.t + 16 * st + 8 * g);
+    kbi[st] = scale8(ld8(kp + (int64_t)irow * ks.t + 16 * st + 8 * g), ai);
     qbi[st] = ld8(q + b * qs.b + h * qs.h + (int64_t)irow * qs.t + 16 * st + 8 * g);
   }
-  const float ai = sl2 * rv[irow];
   // chain accumulators start at -V^T (R = -acc after the sweep); attention at zero
   f32x16 acc[NDT], oacc[NDT];
 #pragma unroll
@@ -1296,7 +1323,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(true) void lucid_fused_fwd_
         sa = mfma32(ka[st], qbi[st], sa);
       }
 #pragma unroll
-      for (int e = 0; e < 16; ++e) sc[e] = __builtin_amdgcn_exp2f(fmaf(sc[e] * ai, rj[e], -c0));
+      for (int e = 0; e < 16; ++e) sc[e] = __builtin_amdgcn_exp2f(fmaf(sc[e], rj[e], -c0));
       const bf16x8 pb0 = pack_b(sc, 0), pb1 = pack_b(sc, 1);
       bf16x8 pa0, pa1;
       softmax(sa, pa0, pa1);

@@ -43,6 +43,14 @@ __device__ __forceinline__ f32x16 zero16() {
   return z;
 }
 
+// accumulator with every element x (an MFMA then adds its product to x)
+__device__ __forceinline__ f32x16 splat16(float x) {
+  f32x16 z;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) z[e] = x;
+  return z;
+}
+
 // position of sequence index j inside a T-perm row (involution on the low 4 bits)
 __host__ __device__ __forceinline__ int jmap(int j) {
   return (j & ~0xC) | ((j & 4) << 1) | ((j & 8) >> 1);
@@ -52,6 +60,14 @@ __host__ __device__ __forceinline__ int jmap(int j) {
 __device__ __forceinline__ int drow(int e, int g) { return 8 * (e >> 2) + 4 * g + (e & 3); }
 
 __device__ __forceinline__ bf16x8 ld8(const bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
+
+// eight bf16 values times a in fp32, rounded once to bf16
+__device__ __forceinline__ bf16x8 scale8(const bf16x8& x, float a) {
+  bf16x8 r;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r[e] = (bf16)(a * (float)x[e]);
+  return r;
+}
 
 // Pack D-layout fp32 values e = 8h .. 8h+7 into a bf16 B operand (k-step h of the tile)
 __device__ __forceinline__ bf16x8 pack_b(const f32x16& x, int h) {

@@ -47,9 +47,9 @@ def test_abi_version_and_workspace(built):
     lib = _lib.load()
     assert lib.lucid_abi_version() == 5
     ws = lib.lucid_fwd_workspace_bytes(1, 16, 16, 32768, 64)
-    # rinv + K^T + V' (bf16) + V'^T + diagonal inverses + -(X_B P_BA) per 128-row block
-    # + lo parts of V' and V'^T + row masses + lo part of O + counters, each 256-byte aligned
-    expect = (16 * 32768 * 4 + 3 * 16 * 64 * 32768 * 2 + 16 * 512 * 4096 * 4 + 16 * 256 * 4096 * 4
+    # rinv + K^T + K^ (bf16) + V' (bf16) + V'^T + diagonal inverses + -(X_B P_BA) per 128-row
+    # block + lo parts of V' and V'^T + row masses + lo part of O + counters, each 256-byte aligned
+    expect = (16 * 32768 * 4 + 4 * 16 * 64 * 32768 * 2 + 16 * 512 * 4096 * 4 + 16 * 256 * 4096 * 4
               + 2 * 16 * 64 * 32768 * 2 + 256 + 16 * 32768 * 64 * 2 + 256)
     assert ws == expect
     assert lib.lucid_fwd_workspace_mass_offset(1, 16, 16, 32768, 64) == expect - 512 - 16 * 32768 * 64 * 2

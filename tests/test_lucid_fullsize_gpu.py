@@ -15,7 +15,11 @@ Inputs:
   * "unit":        q, k ~ N(0,1) so that s q.k is O(1) and the softmax is far from uniform
   * "correlated":  every key = a shared direction + 0.1 N(0,1) noise, so P_ij ~ 0.93 below the
                    diagonal (no damping along the chain)
+  * "moderate":    a shared direction (|base|^2 = d) + 1.2 N(0,1) noise: at T = 4096 the
+                   largest row mass max_i sum_{j<i} P_ij^2 is ~3.2, just under the limit (4) up
+                   to which the bf16 chain kernels run, with off-diagonal row sums of P up to ~90
 """
+import numpy as np
 import pytest
 import torch
 
@@ -28,11 +32,13 @@ pytestmark = pytest.mark.gpu
 def _inputs(B, Hq, Hkv, T, D, seed, kind):
     g = torch.Generator().manual_seed(seed)
     s = D ** -0.5
-    qk = 1.0 if kind in ("unit", "correlated") else s
+    qk = 1.0 if kind in ("unit", "correlated", "moderate") else s
     q = torch.randn(B, Hq, T, D, generator=g) * qk
-    if kind == "correlated":
+    if kind in ("correlated", "moderate"):
         base = torch.randn(B, Hkv, 1, D, generator=g)
-        k = base + 0.1 * torch.randn(B, Hkv, T, D, generator=g)
+        if kind == "moderate":  # |base|^2 = D, so that every head has about the same row mass
+            base = base * (D ** 0.5) / base.norm(dim=-1, keepdim=True)
+        k = base + (0.1 if kind == "correlated" else 1.2) * torch.randn(B, Hkv, T, D, generator=g)
     else:
         k = torch.randn(B, Hkv, T, D, generator=g) * qk
     v = torch.randn(B, Hkv, T, D, generator=g) * s
@@ -108,3 +114,46 @@ def test_correlated_keys(T):
 def test_gqa_d128_long_backward():
     """GQA 4:1 at head dim 128, T = 8192, forward and backward."""
     _run(1, 8, 2, 8192, 128, seed=104, kind="config")
+
+
+def test_bf16_chains_at_the_mass_limit():
+    """The bf16 chain kernels (forced) on keys whose largest row mass is just under the limit up
+    to which the automatic selection runs them: the hardest inputs they are used for."""
+    from lucid_amd import lucid
+    B, H, T, D = 1, 2, 4096, 64
+    q, k, _, _ = _inputs(B, H, H, T, D, 105, "moderate")
+    kh = R.k_hat(k.double().numpy(), 1e-5)
+    for h in range(H):
+        p = np.tril(R.precond_matrix(kh[0, h], D ** -0.5), -1)
+        mass = float((p ** 2).sum(1).max())
+        print(f"head {h}: exact row mass {mass:.2f}", flush=True)
+        assert 2.0 < mass <= 4.0
+    lucid.set_precision("fast")
+    try:
+        _run(B, H, H, T, D, seed=105, kind="moderate")
+        # the preconditioner's own gradient (get_v_prime alone: dV = P^-T W and the k_norm
+        # backward of -s (M K^ + M^T K^)), where the chains' rounding is not masked by the
+        # attention's terms of dK
+        from lucid_amd import get_v_prime
+        v = torch.randn(B, H, T, D, generator=torch.Generator().manual_seed(6)).to(torch.bfloat16) / 8
+        wgt = torch.randn(B, H, T, D, generator=torch.Generator().manual_seed(7))
+        kg, vg = k.cuda().requires_grad_(), v.cuda().requires_grad_()
+        vp = get_v_prime(kg, vg)
+        (vp.float() * wgt.cuda()).sum().backward()
+        torch.cuda.synchronize()
+        s = D ** -0.5
+        kn, vn, wn = (x.detach().float().cpu().double().numpy() for x in (k, v, wgt))
+        for h in range(H):
+            vp_ref = R.vprime_dense(kn[:, h:h + 1], vn[:, h:h + 1], s, 1e-5)[0, 0]
+            dkh, dv_ref = R.precond_backward(kh[0, h], vp_ref, wn[0, h], s)
+            dk_ref = R.rmsnorm_backward(kn[0, h], dkh, 1e-5)
+            errs = {}
+            for name, got, ref in (("vprime", vp[0, h], vp_ref), ("dk", kg.grad[0, h], dk_ref),
+                                   ("dv", vg.grad[0, h], dv_ref)):
+                errs[name] = (float(np.abs(got.detach().double().cpu().numpy() - ref).max()), float(np.abs(ref).max()))
+            print(f"get_v_prime head {h} (err, max|ref|):", {n: (f"{e:.2e}", f"{m:.2e}") for n, (e, m) in errs.items()},
+                  flush=True)
+            for name, (err, scale) in errs.items():
+                check(name, err, scale)
+    finally:
+        lucid.set_precision("auto")

@@ -263,5 +263,7 @@ def test_fused_forward_matches_two_kernel_forward(B, H, T, qk_std):
             check(f"{name} ({'fused' if fused else 'two kernels'})", _maxerr(got[fused][name], ref), scale)
         diff = float((got[True][name].float() - got[False][name].float()).abs().max())
         print(f"  {name}: fused vs two kernels {diff:.2e} (scale {scale:.2e})", flush=True)
-        # the paths differ only in fp32 summation order (and the bf16 rounding that follows)
-        assert diff <= (1e-5 if name == "vprime" else 1e-2) * scale, f"{name}: {diff:.3e}"
+        # the paths differ in fp32 summation order (and the bf16 rounding that follows) and in
+        # the chain's exponent operands: the fused kernel rounds the scaled row key to bf16
+        # against raw K tiles, the chain kernel stages K^ tiles rounded to bf16 as well
+        assert diff <= (5e-4 if name == "vprime" else 1e-2) * scale, f"{name}: {diff:.3e}"

@@ -77,8 +77,10 @@ def test_seams_composed_like_lucid_attention(B, Hq, Hkv, T, D, corr):
     # read the same bf16 V' in both, so O agrees exactly
     assert torch.equal(v_prime.detach(), vpf.to(torch.bfloat16))
     assert torch.equal(o.detach(), of.detach())
-    # the fused kernel sums in another order: V' to fp32 rounding, O to one bf16 rounding step
-    assert float((vp_def - vpf).abs().max()) <= 1e-5 * float(vpf.abs().max())
+    # the fused kernel sums in another order and rounds only the scaled row key of the chain's
+    # exponents to bf16 (the chain kernel also the staged K^ rows): V' agrees to ~1e-4
+    # relative, O to one bf16 rounding step
+    assert float((vp_def - vpf).abs().max()) <= 5e-4 * float(vpf.abs().max())
     assert float((o_def.float() - of.float()).abs().max()) <= 1e-2 * float(of.float().abs().max())
     o_ref, vp_ref = R.lucid_attention(_np(q), _np(k), _np(v), s, 1e-5)
     grads = R.lucid_attention_grads(_np(q), _np(k), _np(v), _np(do), s, 1e-5)
