@@ -171,8 +171,11 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
   for (int st = 0; st < NKS; ++st) rdo[st] = swz_off<D / 8>(l32, 2 * st + g);
   const bf16x8 ones = seed_ones(g);
   const float cinv = 1.f / c;
-  // one 64-row query tile; DIAG: the tile holding this wave's keys (causal mask)
-  auto tile = [&](const int buf, const bool DIAG) {
+  // one 64-row query tile in buffer buf (a compile-time index, so that every LDS operand
+  // address is a lane offset plus an immediate); DIAG: the tile holding this wave's keys
+  // (causal mask)
+  auto tile = [&](auto bufc, const bool DIAG) {
+    constexpr int buf = decltype(bufc)::value;
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
       if (DIAG && mt * 32 + 31 < kloc - l32) continue;  // rows all above this wave's keys
@@ -255,15 +258,20 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
       }
     }
   };
-  for (int s = 0; s < nsteps; ++s) {
-    const int buf = s % 3;
+  // step s works on buffer s % 3: the loop is unrolled by three so that it is a constant
+  auto step = [&](auto bufc, const int s) {
     if (s + 2 < nsteps) stage(s + 2);
     const int it = it_first + s % ntile;
-    if (it > it_w) tile(buf, false);
-    else if (it == it_w) tile(buf, true);
+    if (it > it_w) tile(bufc, false);
+    else if (it == it_w) tile(bufc, true);
     if (s + 2 < nsteps) dma_wait_but<STAGE_OPS>();  // the step after next may stay in flight
     else dma_wait();
     __syncthreads();
+  };
+  for (int s = 0; s < nsteps; s += 3) {
+    step(std::integral_constant<int, 0>{}, s);
+    if (s + 1 < nsteps) step(std::integral_constant<int, 1>{}, s + 1);
+    if (s + 2 < nsteps) step(std::integral_constant<int, 2>{}, s + 2);
   }
   float* ov = dvp + ((int64_t)bh * T + jrow) * D;
   float* ok = dka + ((int64_t)bh * T + jrow) * D;
