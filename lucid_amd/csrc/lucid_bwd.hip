@@ -174,8 +174,8 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
   // one 64-row query tile in buffer buf (a compile-time index, so that every LDS operand
   // address is a lane offset plus an immediate); DIAG: the tile holding this wave's keys
   // (causal mask)
-  auto tile = [&](auto bufc, const bool DIAG) {
-    constexpr int buf = decltype(bufc)::value;
+  auto tile = [&](auto bufc, const bool DIAG) __attribute__((always_inline)) {
+    const int buf = bufc;
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
       if (DIAG && mt * 32 + 31 < kloc - l32) continue;  // rows all above this wave's keys
@@ -259,7 +259,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
     }
   };
   // step s works on buffer s % 3: the loop is unrolled by three so that it is a constant
-  auto step = [&](auto bufc, const int s) {
+  auto step = [&](auto bufc, const int s) __attribute__((always_inline)) {
     if (s + 2 < nsteps) stage(s + 2);
     const int it = it_first + s % ntile;
     if (it > it_w) tile(bufc, false);
@@ -403,8 +403,10 @@ __global__ __launch_bounds__(16384 / RW) LUCID_TWO_WAVES_IF((D == 64 || RW == 32
   int rdo[NKS];
 #pragma unroll
   for (int st = 0; st < NKS; ++st) rdo[st] = swz_off<D / 8>(l32, 2 * st + g);
-  // one 64-key tile; DIAG: the tile holding this wave's rows (causal mask)
-  auto tile = [&](const int buf, const bool DIAG) {
+  // one 64-key tile in buffer buf (a compile-time index: LDS operand addresses are lane
+  // offsets plus immediates); DIAG: the tile holding this wave's rows (causal mask)
+  auto tile = [&](auto bufc, const bool DIAG) __attribute__((always_inline)) {
+    const int buf = bufc;
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
       // the K and V' operands of this key half: held across the n-tiles, or (one n-tile)
@@ -473,16 +475,36 @@ __global__ __launch_bounds__(16384 / RW) LUCID_TWO_WAVES_IF((D == 64 || RW == 32
       }
     }
   };
-  for (int jt = 0; jt < ntile; ++jt) {
-    const int buf = jt % 3;
+  // step jt works on buffer jt % 3: the bf16 instances unroll the loop by three so that it
+  // is a constant
+  auto step = [&](auto bufc, const int jt) __attribute__((always_inline)) {
     if (jt + 2 < ntile) stage(jt + 2);
     if (row0 < T) {
-      if (jt < last_w) tile(buf, false);
-      else if (jt == last_w) tile(buf, true);
+      if (jt < last_w) tile(bufc, false);
+      else if (jt == last_w) tile(bufc, true);
     }
     if (jt + 2 < ntile) dma_wait_but<STAGE_OPS>();  // the step after next may stay in flight
     else dma_wait();
     __syncthreads();
+  };
+  if constexpr (EXACT) {  // the exact instances keep the rolled loop (registers)
+    for (int jt = 0; jt < ntile; ++jt) {
+      const int buf = jt % 3;
+      if (jt + 2 < ntile) stage(jt + 2);
+      if (row0 < T) {
+        if (jt < last_w) tile(buf, false);
+        else if (jt == last_w) tile(buf, true);
+      }
+      if (jt + 2 < ntile) dma_wait_but<STAGE_OPS>();
+      else dma_wait();
+      __syncthreads();
+    }
+  } else {
+    for (int jt = 0; jt < ntile; jt += 3) {
+      step(std::integral_constant<int, 0>{}, jt);
+      if (jt + 1 < ntile) step(std::integral_constant<int, 1>{}, jt + 1);
+      if (jt + 2 < ntile) step(std::integral_constant<int, 2>{}, jt + 2);
+    }
   }
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
