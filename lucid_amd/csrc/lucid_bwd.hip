@@ -19,17 +19,19 @@
 
 namespace lucid {
 
-// delta[bhq][t] = -(dO_t . O_t) (stored negated: it seeds the dP accumulators of the
-// column sweep); zero the chain counters.  Heads of the exact chains (row mass above
-// kExactMass) take O as its bf16 pair O + olo (written by the attention forward).
-// grid (T/64, B*Hq)
+// delta[bhq][t] = -(dO_t . O_t) (stored negated); zero the chain counters.  Heads of the
+// exact chains (row mass above kExactMass) take O as its bf16 pair O + olo (written by the
+// attention forward).  seeds[bhq][t]: the two MFMA A-operand rows (8 bf16 each) that seed
+// the column sweep's accumulators with the row terms, -lse2_t / c (c = s log2(e)) and
+// -delta_t, each split into three bf16 terms (seed_a).  grid (T/64, B*Hq)
 template <int D, bool F32 = false>
 __global__ __launch_bounds__(256) void lucid_bwd_prep_kernel(const bf16* __restrict__ dout, Strides dos,
                                                              const bf16* __restrict__ o, Strides os,
                                                              const bf16* __restrict__ olo,
                                                              const float* __restrict__ mass, int Hq, int Hkv, int T,
                                                              float* __restrict__ delta, int* __restrict__ counters,
-                                                             int BH, Lo lo) {
+                                                             int BH, Lo lo, const float* __restrict__ lse,
+                                                             float cinv, bf16* __restrict__ seeds) {
   constexpr int SEG = D / 4;
   const int blk = blockIdx.x, bhq = blockIdx.y;
   const int b = bhq / Hq, hq = bhq - b * Hq;
@@ -67,7 +69,12 @@ __global__ __launch_bounds__(256) void lucid_bwd_prep_kernel(const bf16* __restr
   }
   acc += __shfl_xor(acc, 1, 64);
   acc += __shfl_xor(acc, 2, 64);
-  if (seg == 0) delta[(int64_t)bhq * T + t] = -acc;
+  if (seg == 0) {
+    const int64_t r = (int64_t)bhq * T + t;
+    delta[r] = -acc;
+    *reinterpret_cast<bf16x8*>(seeds + r * 16) = seed_a(-lse[r] * cinv, 0);
+    *reinterpret_cast<bf16x8*>(seeds + r * 16 + 8) = seed_a(-acc, 0);
+  }
   if (blk == 0 && tid == 0 && bhq < BH) counters[bhq] = 0;
 }
 
@@ -89,8 +96,7 @@ struct DkdvSmem {
   bf16 dO[3][64 * D];
   bf16 ql[F32 ? 3 : 1][F32 ? 64 * D : 8];   // lo tiles (fp32 inputs)
   bf16 dOl[F32 ? 3 : 1][F32 ? 64 * D : 8];
-  float lse[3][64];
-  float dl[3][64];
+  bf16 seed[3][64][16];  // per row: the seed operands of -lse2 / c and -delta (seeds)
 };
 
 // F32 (fp32 inputs, head dim 64): the lo tiles of Q and dO are staged beside the hi tiles,
@@ -99,8 +105,7 @@ struct DkdvSmem {
 template <int D, bool F32 = false>
 __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid_attn_bwd_dkdv_kernel(
     const bf16* __restrict__ q, Strides qs, const bf16* __restrict__ k, Strides ks, const bf16* __restrict__ vpb,
-    const bf16* __restrict__ dout, Strides dos, const float* __restrict__ lse, const float* __restrict__ delta,
-    float* __restrict__ dvp, float* __restrict__ dka, int Hq, int Hkv, int T, int BH, float scale, Lo lo,
+    const bf16* __restrict__ dout, Strides dos, const bf16* __restrict__ seeds, float* __restrict__ dvp, float* __restrict__ dka, int Hq, int Hkv, int T, int BH, float scale, Lo lo,
     const bf16* __restrict__ vpbl) {
   static_assert(!F32 || D == 64, "fp32 inputs: head dim 64");
   constexpr int NDT = D / 32;
@@ -147,8 +152,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
   auto stage = [&](int s) {
     const int gi = s / ntile, it = it_first + s - gi * ntile, buf = s % 3;
     const int hq = h * G + gi, bhq = b * Hq + hq, i0 = it * 64;
-    if (w == 0) dma_f32x64(lse + (int64_t)bhq * T + i0, sm.lse[buf]);
-    if (w == 1) dma_f32x64(delta + (int64_t)bhq * T + i0, sm.dl[buf]);
+    if (w < 2) dma_1k(seeds + ((int64_t)bhq * T + i0 + 32 * w) * 16, &sm.seed[buf][32 * w][0]);  // 2 KB of seed rows
     dma_stage<64, D / 8>(plan_q, q + b * qs.b + hq * qs.h + (int64_t)i0 * qs.t, sm.q[buf]);
     dma_stage<64, D / 8>(plan_o, dout + b * dos.b + hq * dos.h + (int64_t)i0 * dos.t, sm.dO[buf]);
     if constexpr (F32) {
@@ -170,7 +174,6 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
 #pragma unroll
   for (int st = 0; st < NKS; ++st) rdo[st] = swz_off<D / 8>(l32, 2 * st + g);
   const bf16x8 ones = seed_ones(g);
-  const float cinv = 1.f / c;
   // one 64-row query tile in buffer buf (a compile-time index, so that every LDS operand
   // address is a lane offset plus an immediate); DIAG: the tile holding this wave's keys
   // (causal mask)
@@ -180,15 +183,17 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
     for (int mt = 0; mt < 2; ++mt) {
       if (DIAG && mt * 32 + 31 < kloc - l32) continue;  // rows all above this wave's keys
       // the per-row terms enter through the matrix cores: a rank-3 product with `ones`
-      // seeds the score accumulator with -lse_i / c and the dP accumulator with -delta_i,
-      // from the one value of this lane's own row (no per-element row reads)
+      // seeds the score accumulator with -lse_i / c and the dP accumulator with -delta_i
+      // (the three-term splits come staged from lucid_bwd_prep_kernel; no per-element row
+      // reads and no VALU work here)
       f32x16 pv;
       bf16x8 pb0, pb1;
       {
         bf16x8 qa[NKS];
 #pragma unroll
         for (int st = 0; st < NKS; ++st) qa[st] = ld8(sm.q[buf] + rdo[st] + mt * 32 * D);
-        f32x16 sc = mfma32(seed_a(-sm.lse[buf][mt * 32 + l32] * cinv, g), ones, zero16());
+        // (lanes 32..63 read the same row: they meet the zero rows of `ones`)
+        f32x16 sc = mfma32(ld8(&sm.seed[buf][mt * 32 + l32][0]), ones, zero16());
 #pragma unroll
         for (int st = 0; st < NKS; ++st) sc = mfma32(qa[st], kb[st], sc);
         if constexpr (F32) {
@@ -228,7 +233,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
 #pragma unroll
         for (int st = 0; st < NKS; ++st) da[st] = ld8(sm.dO[buf] + rdo[st] + mt * 32 * D);
         // dP - delta: the accumulator starts at -delta (stored negated)
-        f32x16 dp = mfma32(seed_a(sm.dl[buf][mt * 32 + l32], g), ones, zero16());
+        f32x16 dp = mfma32(ld8(&sm.seed[buf][mt * 32 + l32][8]), ones, zero16());
 #pragma unroll
         for (int st = 0; st < NKS; ++st) dp = mfma32(da[st], vb[st], dp);
         if constexpr (F32) {

@@ -128,6 +128,7 @@ FwdWs carve_fwd(void* base, int B, int Hq, int Hkv, int T, int D, bool f32 = fal
 
 struct BwdWs {
   float* delta;  // [BHq][T]
+  bf16* seeds;   // [BHq][T][16] the dK/dV' sweep's seed operands of -lse2 / c and -delta
   float* dvp;    // [BH][T][D]   dV' (summed over the group)
   float* dka;    // [BH][T][D]   dK from the softmax part (scaled)
   bf16* dvb;     // [BH][T][D]   dV bf16
@@ -150,6 +151,7 @@ BwdWs carve_bwd(void* base, int B, int Hq, int Hkv, int T, int D, bool f32 = fal
     return r;
   };
   w.delta = reinterpret_cast<float*>(take(BHq * T * 4));
+  w.seeds = reinterpret_cast<bf16*>(take(BHq * T * 32));
   w.dvp = reinterpret_cast<float*>(take(BH * T * D * 4));
   w.dka = reinterpret_cast<float*>(take(BH * T * D * 4));
   w.dvb = reinterpret_cast<bf16*>(take(BH * T * D * 2));
@@ -291,11 +293,13 @@ int launch_attn_bwd(const void* dout, const int64_t* dos, const void* q, const i
                     const int64_t* ks, const void* o, const int64_t* os, const float* lse, const FwdWs& f, void* dq,
                     const int64_t* dqs, const BwdWs& w, int B, int Hq, int Hkv, int T, float scale, hipStream_t st) {
   const int BH = B * Hkv, BHq = B * Hq;
+  const float cinv = 1.f / (scale * LOG2E_F);
   LUCID_LAUNCH("lucid_bwd_prep_kernel", lucid::lucid_bwd_prep_kernel<D>, dim3(T / 64, BHq), st, (const bf16*)dout,
-               S(dos), (const bf16*)o, S(os), f.olo, f.mass, Hq, Hkv, T, w.delta, w.counters, BH, lucid::Lo{});
+               S(dos), (const bf16*)o, S(os), f.olo, f.mass, Hq, Hkv, T, w.delta, w.counters, BH, lucid::Lo{}, lse,
+               cinv, w.seeds);
   LUCID_LAUNCH("lucid_attn_bwd_dkdv_kernel", lucid::lucid_attn_bwd_dkdv_kernel<D>, dim3((T / 128) * BH), st,
-               (const bf16*)q, S(qs), (const bf16*)k, S(ks), f.vpb, (const bf16*)dout, S(dos), lse,
-               w.delta, w.dvp, w.dka, Hq, Hkv, T, BH, scale, lucid::Lo{}, nullptr);
+               (const bf16*)q, S(qs), (const bf16*)k, S(ks), f.vpb, (const bf16*)dout, S(dos), w.seeds, w.dvp,
+               w.dka, Hq, Hkv, T, BH, scale, lucid::Lo{}, nullptr);
   // dQ: four waves of 64 rows at head dim 64, eight waves of 32 rows at 128
   constexpr int RW = D == 128 ? 32 : 64;
   const dim3 block(64 * (256 / RW));
@@ -402,6 +406,7 @@ BwdWs carve_seam_bwd(void* base, int B, int Hq, int Hkv, int T, int D, bool attn
   w.dvp = reinterpret_cast<float*>(take(BH * T * D * 4));
   if (attn) {
     w.delta = reinterpret_cast<float*>(take(BHq * T * 4));
+    w.seeds = reinterpret_cast<bf16*>(take(BHq * T * 32));
     w.dka = reinterpret_cast<float*>(take(BH * T * D * 4));
     if (f32) {
       w.doh = reinterpret_cast<bf16*>(take(BHq * T * D * 2));
@@ -564,10 +569,9 @@ int launch_attn_bwd_f32(const void* dout, const int64_t* dos, const void* o, con
   // delta reads fp32 dO and O with their own strides (the bf16 operands are unused)
   LUCID_LAUNCH("lucid_bwd_prep_f32_kernel", (lucid::lucid_bwd_prep_kernel<D, true>), dim3(T / 64, BHq), st,
                (const bf16*)dout, S(dos), (const bf16*)o, S(os), f.olo, f.mass, Hq, Hkv, T, w.delta, w.counters, BH,
-               lo);
+               lo, lse, 1.f / (scale * LOG2E_F), w.seeds);
   LUCID_LAUNCH("lucid_attn_bwd_dkdv_f32_kernel", (lucid::lucid_attn_bwd_dkdv_kernel<D, true>), dim3((T / 128) * BH),
-               st, f.qh, cq, f.kch, ck, f.vpb, w.doh, cq, lse, w.delta, w.dvp, w.dka, Hq, Hkv, T, BH, scale, lo,
-               f.vpbl);
+               st, f.qh, cq, f.kch, ck, f.vpb, w.doh, cq, w.seeds, w.dvp, w.dka, Hq, Hkv, T, BH, scale, lo, f.vpbl);
   LUCID_LAUNCH("lucid_attn_bwd_dq_f32_kernel", (lucid::lucid_attn_bwd_dq_kernel<D, true, true>),
                dim3(((T + 255) / 256) * BHq), st, f.qh, cq, f.kch, ck, f.vpb, w.doh, cq, lse, w.delta, f.mass,
                (float*)dq, S(dqs), Hq, Hkv, T, BHq, scale, lo, f.vpbl);

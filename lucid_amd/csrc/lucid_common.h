@@ -286,6 +286,10 @@ __device__ __forceinline__ void dma_stage(const int* off, const bf16* __restrict
 __device__ __forceinline__ void dma_f32x64(const float* __restrict__ src, float* lds) {
   __builtin_amdgcn_global_load_lds(src + (threadIdx.x & 63), lds, 4, 0, 0);
 }
+// 1 KB (512 consecutive bf16) into LDS by one wave (call from a single wave)
+__device__ __forceinline__ void dma_1k(const bf16* __restrict__ src, bf16* lds) {
+  __builtin_amdgcn_global_load_lds(src + 8 * (threadIdx.x & 63), lds, 16, 0, 0);
+}
 // Wait until this wave's staging loads have landed in LDS.
 __device__ __forceinline__ void dma_wait() { __builtin_amdgcn_s_waitcnt(0); }
 // Wait until at most N of this wave's vector memory operations are outstanding
