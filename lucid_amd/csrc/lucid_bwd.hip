@@ -22,9 +22,8 @@ namespace lucid {
 // delta[bhq][t] = -(dO_t . O_t) (stored negated); zero the chain counters.  Heads of the
 // exact chains (row mass above kExactMass) take O as its bf16 pair O + olo (written by the
 // attention forward).  seeds[bhq][t]: the two MFMA A-operand rows (8 bf16 each) that seed
-// the column sweep's accumulators with the row terms, -lse2_t * cinv (cinv = 1 for bf16
-// inputs, whose sweep scales the keys by c = s log2(e); 1 / c for fp32 inputs) and -delta_t,
-// each split into three bf16 terms (seed_a).  grid (T/64, B*Hq)
+// the column sweep's accumulators with the row terms, -lse2_t / c (c = s log2(e)) and
+// -delta_t, each split into three bf16 terms (seed_a).  grid (T/64, B*Hq)
 template <int D, bool F32 = false>
 __global__ __launch_bounds__(256) void lucid_bwd_prep_kernel(const bf16* __restrict__ dout, Strides dos,
                                                              const bf16* __restrict__ o, Strides os,
@@ -128,10 +127,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
   bf16x8 kb[NKS], vb[NKS], kbl[NKS], vbl[NKS];
 #pragma unroll
   for (int st = 0; st < NKS; ++st) {
-    // bf16 inputs: the key scaled by c = s log2(e) (one bf16 rounding, which differs from
-    // query row to query row in the exponents), so that the seeded score is the exponent
-    kb[st] = F32 ? ld8(kh + (int64_t)jrow * ks.t + 16 * st + 8 * g)
-                 : scale8(ld8(kh + (int64_t)jrow * ks.t + 16 * st + 8 * g), c);
+    kb[st] = ld8(kh + (int64_t)jrow * ks.t + 16 * st + 8 * g);
     vb[st] = ld8(vpb + ((int64_t)bh * T + jrow) * D + 16 * st + 8 * g);
     if constexpr (F32) {
       kbl[st] = ld8(lo.k + b * ks.b + h * ks.h + (int64_t)jrow * ks.t + 16 * st + 8 * g);
@@ -187,8 +183,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
     for (int mt = 0; mt < 2; ++mt) {
       if (DIAG && mt * 32 + 31 < kloc - l32) continue;  // rows all above this wave's keys
       // the per-row terms enter through the matrix cores: a rank-3 product with `ones`
-      // seeds the score accumulator with -lse_i (-lse_i / c for fp32 inputs, whose keys are
-      // not scaled) and the dP accumulator with -delta_i
+      // seeds the score accumulator with -lse_i / c and the dP accumulator with -delta_i
       // (the three-term splits come staged from lucid_bwd_prep_kernel; no per-element row
       // reads and no VALU work here)
       f32x16 pv;
@@ -212,7 +207,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
         }
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-          float p = __builtin_amdgcn_exp2f(F32 ? sc[e] * c : sc[e]);
+          float p = __builtin_amdgcn_exp2f(sc[e] * c);
           if (DIAG && (mt * 32 + drow(e, g) < kloc)) p = 0.f;
           pv[e] = p;
         }

@@ -293,10 +293,10 @@ int launch_attn_bwd(const void* dout, const int64_t* dos, const void* q, const i
                     const int64_t* ks, const void* o, const int64_t* os, const float* lse, const FwdWs& f, void* dq,
                     const int64_t* dqs, const BwdWs& w, int B, int Hq, int Hkv, int T, float scale, hipStream_t st) {
   const int BH = B * Hkv, BHq = B * Hq;
-  // the bf16 dK/dV' sweep scales its keys by s log2(e): its lse seed is -lse2 itself
+  const float cinv = 1.f / (scale * LOG2E_F);
   LUCID_LAUNCH("lucid_bwd_prep_kernel", lucid::lucid_bwd_prep_kernel<D>, dim3(T / 64, BHq), st, (const bf16*)dout,
                S(dos), (const bf16*)o, S(os), f.olo, f.mass, Hq, Hkv, T, w.delta, w.counters, BH, lucid::Lo{}, lse,
-               1.f, w.seeds);
+               cinv, w.seeds);
   LUCID_LAUNCH("lucid_attn_bwd_dkdv_kernel", lucid::lucid_attn_bwd_dkdv_kernel<D>, dim3((T / 128) * BH), st,
                (const bf16*)q, S(qs), (const bf16*)k, S(ks), f.vpb, (const bf16*)dout, S(dos), w.seeds, w.dvp,
                w.dka, Hq, Hkv, T, BH, scale, lucid::Lo{}, nullptr);
