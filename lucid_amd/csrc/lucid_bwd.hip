@@ -147,8 +147,11 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
   const int it_w = jw / 64;               // this wave's diagonal tile
   const int kloc = jw - it_w * 64 + l32;  // this lane's key inside its diagonal tile
   int plan_q[64 * (D / 8) / 256], plan_o[64 * (D / 8) / 256];
-  dma_plan<64, D / 8>(qs.t, plan_q);
-  dma_plan<64, D / 8>(dos.t, plan_o);
+  // head dim 64: the conflict-free swizzle (every staged tile is read twice per wave, in rows
+  // and transposed, so the LDS bandwidth matters here)
+  constexpr int SW = D == 64 ? 1 : 0;
+  dma_plan<64, D / 8, 256, SW>(qs.t, plan_q);
+  dma_plan<64, D / 8, 256, SW>(dos.t, plan_o);
   auto stage = [&](int s) {
     const int gi = s / ntile, it = it_first + s - gi * ntile, buf = s % 3;
     const int hq = h * G + gi, bhq = b * Hq + hq, i0 = it * 64;
@@ -168,11 +171,11 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
     dma_wait();
   }
   __syncthreads();
-  int tro[NDT], rdo[NKS];  // lane offsets of the transposing and the row reads
+  int tro[NDT], tro2[NDT], rdo[NKS];  // lane offsets of the transposing (two loads) and the row reads
 #pragma unroll
-  for (int t = 0; t < NDT; ++t) tro[t] = lds_tr_lane_off<D / 8>(t * 32);
+  for (int t = 0; t < NDT; ++t) lds_tr_lane_offs<D / 8, SW>(t * 32, tro[t], tro2[t]);
 #pragma unroll
-  for (int st = 0; st < NKS; ++st) rdo[st] = swz_off<D / 8>(l32, 2 * st + g);
+  for (int st = 0; st < NKS; ++st) rdo[st] = swz_off<D / 8, SW>(l32, 2 * st + g);
   const bf16x8 ones = seed_ones(g);
   // one 64-row query tile in buffer buf (a compile-time index, so that every LDS operand
   // address is a lane offset plus an immediate); DIAG: the tile holding this wave's keys
@@ -216,15 +219,15 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
       }
 #pragma unroll
       for (int t = 0; t < NDT; ++t) {
-        const bf16x8 o0 = lds_tr_a_at<D / 8>(sm.dO[buf] + tro[t], mt * 32);
-        const bf16x8 o1 = lds_tr_a_at<D / 8>(sm.dO[buf] + tro[t], mt * 32 + 16);
+        const bf16x8 o0 = lds_tr_a_at2<D / 8>(sm.dO[buf], tro[t], tro2[t], mt * 32);
+        const bf16x8 o1 = lds_tr_a_at2<D / 8>(sm.dO[buf], tro[t], tro2[t], mt * 32 + 16);
         adv[t] = mfma32(o0, pb0, adv[t]);
         adv[t] = mfma32(o1, pb1, adv[t]);
         if constexpr (F32) {
           adv[t] = mfma32(o0, pack_lo(pv, 0, pb0), adv[t]);
           adv[t] = mfma32(o1, pack_lo(pv, 1, pb1), adv[t]);
-          adv[t] = mfma32(lds_tr_a_at<D / 8>(sm.dOl[buf] + tro[t], mt * 32), pb0, adv[t]);
-          adv[t] = mfma32(lds_tr_a_at<D / 8>(sm.dOl[buf] + tro[t], mt * 32 + 16), pb1, adv[t]);
+          adv[t] = mfma32(lds_tr_a_at2<D / 8>(sm.dOl[buf], tro[t], tro2[t], mt * 32), pb0, adv[t]);
+          adv[t] = mfma32(lds_tr_a_at2<D / 8>(sm.dOl[buf], tro[t], tro2[t], mt * 32 + 16), pb1, adv[t]);
         }
       }
       f32x16 ds;
@@ -250,15 +253,15 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
       }
 #pragma unroll
       for (int t = 0; t < NDT; ++t) {
-        const bf16x8 q0 = lds_tr_a_at<D / 8>(sm.q[buf] + tro[t], mt * 32);
-        const bf16x8 q1 = lds_tr_a_at<D / 8>(sm.q[buf] + tro[t], mt * 32 + 16);
+        const bf16x8 q0 = lds_tr_a_at2<D / 8>(sm.q[buf], tro[t], tro2[t], mt * 32);
+        const bf16x8 q1 = lds_tr_a_at2<D / 8>(sm.q[buf], tro[t], tro2[t], mt * 32 + 16);
         adk[t] = mfma32(q0, pb0, adk[t]);
         adk[t] = mfma32(q1, pb1, adk[t]);
         if constexpr (F32) {
           adk[t] = mfma32(q0, pack_lo(ds, 0, pb0), adk[t]);
           adk[t] = mfma32(q1, pack_lo(ds, 1, pb1), adk[t]);
-          adk[t] = mfma32(lds_tr_a_at<D / 8>(sm.ql[buf] + tro[t], mt * 32), pb0, adk[t]);
-          adk[t] = mfma32(lds_tr_a_at<D / 8>(sm.ql[buf] + tro[t], mt * 32 + 16), pb1, adk[t]);
+          adk[t] = mfma32(lds_tr_a_at2<D / 8>(sm.ql[buf], tro[t], tro2[t], mt * 32), pb0, adk[t]);
+          adk[t] = mfma32(lds_tr_a_at2<D / 8>(sm.ql[buf], tro[t], tro2[t], mt * 32 + 16), pb1, adk[t]);
         }
       }
     }

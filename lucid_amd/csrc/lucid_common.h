@@ -262,7 +262,21 @@ __device__ __forceinline__ void dma_tile(const bf16* __restrict__ src, int64_t s
 // dma_tile split in two: the per-lane element offsets for a fixed row stride
 // (dma_plan, once per kernel) and the loads of one tile (dma_stage), by a workgroup of
 // NTHR threads.
-template <int ROWS, int CPR, int NTHR = 256>
+// Swizzle key of row r: chunk c of row r is stored at chunk c ^ swz_key<SW>(r).
+//   SW = 0: r & 7.  With 128-byte rows, rows r and r + 8 of one 16-lane pass of 16-byte
+//     reads land on the same banks (2-way), as do rows r and r + 2 of a transposing read.
+//   SW = 1: bitrev3((r >> 1) & 7), conflict-free for both reads of 128-byte rows; rows r and
+//     r + 8 then differ in the key, so a transposing read needs a second lane offset.
+template <int SW>
+__device__ __forceinline__ int swz_key(int r) {
+  if constexpr (SW == 0) {
+    return r & 7;
+  } else {
+    const int x = (r >> 1) & 7;
+    return ((x & 1) << 2) | (x & 2) | (x >> 2);
+  }
+}
+template <int ROWS, int CPR, int NTHR = 256, int SW = 0>
 __device__ __forceinline__ void dma_plan(int64_t stride, int* off) {
   constexpr int PER_WAVE = ROWS * CPR / NTHR;
   static_assert(PER_WAVE * NTHR == ROWS * CPR, "tile must be a whole number of 1 KB pieces per wave");
@@ -270,7 +284,7 @@ __device__ __forceinline__ void dma_plan(int64_t stride, int* off) {
 #pragma unroll
   for (int i = 0; i < PER_WAVE; ++i) {
     const int q = (w * PER_WAVE + i) * 64 + lane;
-    const int r = q / CPR, c = (q % CPR) ^ (r & 7);
+    const int r = q / CPR, c = (q % CPR) ^ swz_key<SW>(r);
     off[i] = (int)(r * stride) + c * 8;
   }
 }
@@ -301,9 +315,9 @@ __device__ __forceinline__ void dma_wait_but() {
 }
 // Element offset of logical chunk c (8 bf16) of row r in a swizzled tile with CPR
 // chunks per row, and its address.
-template <int CPR>
+template <int CPR, int SW = 0>
 __device__ __forceinline__ int swz_off(int r, int c) {
-  return r * (CPR * 8) + ((c ^ (r & 7)) << 3);
+  return r * (CPR * 8) + ((c ^ swz_key<SW>(r)) << 3);
 }
 template <int CPR>
 __device__ __forceinline__ const bf16* swz(const bf16* tile, int r, int c) {
@@ -342,6 +356,23 @@ __device__ __forceinline__ int lds_tr_lane_off(int col0) {
   const int col = col0 + 16 * ((lane >> 4) & 1) + 4 * (s & 3);
   const int r1 = 4 * (lane >> 5) + (s >> 2);
   return r1 * (CPR * 8) + ((((col >> 3) ^ (r1 & 7)) << 3) | (col & 7));
+}
+// The same for a tile with swizzle SW: the lane offsets of the two loads (rows r1 and
+// r1 + 8, whose keys differ for SW = 1); rows row0 (a multiple of 16) add row0 * CPR * 8.
+template <int CPR, int SW>
+__device__ __forceinline__ void lds_tr_lane_offs(int col0, int& o1, int& o2) {
+  const int lane = threadIdx.x & 63, s = lane & 15;
+  const int col = col0 + 16 * ((lane >> 4) & 1) + 4 * (s & 3);
+  const int r1 = 4 * (lane >> 5) + (s >> 2);
+  o1 = r1 * (CPR * 8) + ((((col >> 3) ^ swz_key<SW>(r1)) << 3) | (col & 7));
+  o2 = (r1 + 8) * (CPR * 8) + ((((col >> 3) ^ swz_key<SW>(r1 + 8)) << 3) | (col & 7));
+}
+template <int CPR>
+__device__ __forceinline__ bf16x8 lds_tr_a_at2(const bf16* tile, int o1, int o2, int row0) {
+  typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+  const bf16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(tile + o1 + row0 * (CPR * 8)));
+  const bf16x4 v2 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(tile + o2 + row0 * (CPR * 8)));
+  return bf16x8{v1[0], v1[1], v1[2], v1[3], v2[0], v2[1], v2[2], v2[3]};
 }
 template <int CPR>
 __device__ __forceinline__ bf16x8 lds_tr_a_at(const bf16* tile_lane, int row0) {
