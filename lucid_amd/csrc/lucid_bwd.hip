@@ -1079,6 +1079,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void l
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
   constexpr int NTHR = 512;
+  constexpr int SW = 0;  // (the conflict-free swizzle, SW = 1, costs more VALU address work here than it saves)
   __shared__ __attribute__((aligned(16))) PcolWideSmem<D> sm;
 
   const int NT = T / 64, NP = T / 256;
@@ -1137,8 +1138,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void l
       bf16x8 ka[NKS], da[NKS];
 #pragma unroll
       for (int st = 0; st < NKS; ++st) {
-        ka[st] = ld8(swz<D / 8>(tk, rh * 32 + l32, 2 * st + g));
-        da[st] = ld8(swz<D / 8>(tdv, rh * 32 + l32, 2 * st + g));
+        ka[st] = ld8(swz<D / 8, SW>(tk, rh * 32 + l32, 2 * st + g));
+        da[st] = ld8(swz<D / 8, SW>(tdv, rh * 32 + l32, 2 * st + g));
       }
       f32x16 sc = zero16(), gg = zero16();
 #pragma unroll
@@ -1159,11 +1160,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void l
       const bf16x8 mb0 = pack_b(gg, 0), mb1 = pack_b(gg, 1);
 #pragma unroll
       for (int t = 0; t < NDT; ++t) {
-        const bf16x8 k0 = lds_tr_a<D / 8>(tk, rh * 32, t * 32);
-        const bf16x8 k1 = lds_tr_a<D / 8>(tk, rh * 32 + 16, t * 32);
+        const bf16x8 k0 = lds_tr_a<D / 8, SW>(tk, rh * 32, t * 32);
+        const bf16x8 k1 = lds_tr_a<D / 8, SW>(tk, rh * 32 + 16, t * 32);
         if (!DIAG) {
-          const bf16x8 a0 = lds_tr_a<D / 8>(tdv, rh * 32, t * 32);
-          const bf16x8 a1 = lds_tr_a<D / 8>(tdv, rh * 32 + 16, t * 32);
+          const bf16x8 a0 = lds_tr_a<D / 8, SW>(tdv, rh * 32, t * 32);
+          const bf16x8 a1 = lds_tr_a<D / 8, SW>(tdv, rh * 32 + 16, t * 32);
           adv[t] = mfma32(a0, pb0, adv[t]);
           adv[t] = mfma32(a1, pb1, adv[t]);
         }
@@ -1180,7 +1181,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void l
   constexpr int STAGE_OPS = 2 * PER;
   const int nsteps = first - last + 1;
   int plan_d[PER];  // K^ and dV rows: row stride D
-  dma_plan<64, D / 8, NTHR>(D, plan_d);
+  dma_plan<64, D / 8, NTHR, SW>(D, plan_d);
   auto stage = [&](int kk) {
     const int i0 = (first - kk) * 64, buf = kk % 3;
     dma_stage<64, D / 8, NTHR>(plan_d, khh + (int64_t)i0 * D, sm.k[buf]);
@@ -1273,7 +1274,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void l
         for (int u = 0; u < 4; ++u) bb[u] = (bf16)o[4 * qq + u];
         *reinterpret_cast<bf16x4*>(ob + d0) = bb;
         *reinterpret_cast<bf16x4*>(ou + d0) = bb;
-        *reinterpret_cast<bf16x4*>(sm.sdv + swz_off<D / 8>(cl, d0 >> 3) + (d0 & 7)) = bb;
+        *reinterpret_cast<bf16x4*>(sm.sdv + swz_off<D / 8, SW>(cl, d0 >> 3) + (d0 & 7)) = bb;
       }
     }
     dma_wait();

@@ -319,9 +319,9 @@ template <int CPR, int SW = 0>
 __device__ __forceinline__ int swz_off(int r, int c) {
   return r * (CPR * 8) + ((c ^ swz_key<SW>(r)) << 3);
 }
-template <int CPR>
+template <int CPR, int SW = 0>
 __device__ __forceinline__ const bf16* swz(const bf16* tile, int r, int c) {
-  return tile + swz_off<CPR>(r, c);
+  return tile + swz_off<CPR, SW>(r, c);
 }
 
 // MFMA A operand [m = col0 + lane%32][k = 16 rows from row0] read from a
@@ -334,15 +334,17 @@ __device__ __forceinline__ const bf16* swz(const bf16* tile, int r, int c) {
 // slot 8g + e therefore holds row jmap(8g + e) -- the order in which the D
 // layout of a score tile delivers its keys -- so the result pairs with
 // pack_b() exactly like a 16-byte read from a T-perm tile.
-template <int CPR>
+template <int CPR, int SW = 0>
 __device__ __forceinline__ bf16x8 lds_tr_a(const bf16* tile, int row0, int col0) {
   typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
   const int lane = threadIdx.x & 63, s = lane & 15;
   const int col = col0 + 16 * ((lane >> 4) & 1) + 4 * (s & 3);
   const int r1 = row0 + 4 * (lane >> 5) + (s >> 2);
-  const int off = (((col >> 3) ^ (r1 & 7)) << 3) | (col & 7);  // rows r1 and r1 + 8 share the swizzle
-  const bf16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(tile + r1 * (CPR * 8) + off));
-  const bf16x4 v2 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(tile + (r1 + 8) * (CPR * 8) + off));
+  // (with SW = 0 rows r1 and r1 + 8 share the swizzle key)
+  const int off1 = (((col >> 3) ^ swz_key<SW>(r1)) << 3) | (col & 7);
+  const int off2 = (((col >> 3) ^ swz_key<SW>(r1 + 8)) << 3) | (col & 7);
+  const bf16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(tile + r1 * (CPR * 8) + off1));
+  const bf16x4 v2 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(tile + (r1 + 8) * (CPR * 8) + off2));
   return bf16x8{v1[0], v1[1], v1[2], v1[3], v2[0], v2[1], v2[2], v2[3]};
 }
 
