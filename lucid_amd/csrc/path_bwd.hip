@@ -393,6 +393,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
   // exponent offset and delta of this lane's row (LUCID-Path: the constant 1/s, no delta)
   const float ci = SM ? ws.lse[(int64_t)bhq * T + iw0 + l32] : cc0;
   const float di = SM ? bw.delta[(int64_t)bhq * T + iw0 + l32] : 0.f;
+  // LUCID-Path: dA = -s dP exp2(sl2 S - cc0) = F dP exp2(sl2 S) with the constant
+  // F = -s 2^-cc0, which G carries out of the sweep (applied to dM and to d q~)
+  const float F = SM ? 1.f : -scale * __builtin_amdgcn_exp2f(-cc0);
   f32x16 acc[2] = {zero16(), zero16()};
 
   int plan_k[2], plan_o[2];
@@ -431,7 +434,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
         dm = mfma32(xa, gl, dm);
       }
 #pragma unroll
-      for (int e = 0; e < 16; ++e) unsafeAtomicAdd(dM + (at * 32 + drow(e, g)) * 64 + bt * 32 + l32, dm[e]);
+      for (int e = 0; e < 16; ++e) unsafeAtomicAdd(dM + (at * 32 + drow(e, g)) * 64 + bt * 32 + l32, F * dm[e]);
     }
     if (act) {
 #pragma unroll
@@ -493,8 +496,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
         }
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-          const float ex = __builtin_amdgcn_exp2f(fmaf(sc[e], sl2, -ci));
-          sc[e] = SM ? scale * ex * (dp[e] - di) : -scale * dp[e] * ex;
+          const float ex = __builtin_amdgcn_exp2f(SM ? fmaf(sc[e], sl2, -ci) : sc[e] * sl2);
+          sc[e] = SM ? scale * ex * (dp[e] - di) : dp[e] * ex;
         }
         const bf16x8 d0 = pack_b(sc, 0), d1 = pack_b(sc, 1);
 #pragma unroll
@@ -515,7 +518,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
       for (int qq = 0; qq < 4; ++qq) {
         f32x4 v;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) v[u] = acc[t][4 * qq + u];
+        for (int u = 0; u < 4; ++u) v[u] = F * acc[t][4 * qq + u];
         *reinterpret_cast<f32x4*>(dst + t * 32 + 8 * qq + 4 * g) = v;
       }
   }
@@ -571,6 +574,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
   const bool live = Jw < NT;           // NT odd: the last pair has one chunk
   const int sJ = J1 / PR, cb = sJ * PR, ceJ = min(cb + PR, NT) - 1;
   const float sl2 = scale * LOG2E_F, cc0 = LOG2E_F / scale;
+  // LUCID-Path: dA = -s dP exp2(sl2 S - cc0) = F dP exp2(sl2 S) with the constant
+  // F = -s 2^-cc0, applied to the accumulators where the sweep hands them on
+  const float F = SM ? 1.f : -scale * __builtin_amdgcn_exp2f(-cc0);
 
   bf16x8 kbs[4], kbf[4], ob[4];
   {
@@ -686,7 +692,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
           for (int e = 0; e < 16; ++e) sc[e] = dp[e];
         } else {
 #pragma unroll
-          for (int e = 0; e < 16; ++e) sc[e] = -scale * dp[e] * __builtin_amdgcn_exp2f(fmaf(sc[e], sl2, -cc0));
+          for (int e = 0; e < 16; ++e) sc[e] = dp[e] * __builtin_amdgcn_exp2f(sc[e] * sl2);
         }
         const bf16x8 d0 = pack_b(sc, 0), d1 = pack_b(sc, 1);
 #pragma unroll
@@ -734,8 +740,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-          if (!SM) sm.u.fin.a[(w & 1) * 32 + l32][t * 32 + drow(e, g)] = as_[t][e];
-          sm.u.fin.f[(w & 1) * 32 + l32][t * 32 + drow(e, g)] = SM ? as_[t][e] : af[t][e];
+          if (!SM) sm.u.fin.a[(w & 1) * 32 + l32][t * 32 + drow(e, g)] = F * as_[t][e];
+          sm.u.fin.f[(w & 1) * 32 + l32][t * 32 + drow(e, g)] = SM ? as_[t][e] : F * af[t][e];
         }
     }
     load_mat64<false>(sm.u.fin.m, ws.suf + ((int64_t)bh * NT + J) * 4096);
