@@ -393,9 +393,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
   // exponent offset and delta of this lane's row (LUCID-Path: the constant 1/s, no delta)
   const float ci = SM ? ws.lse[(int64_t)bhq * T + iw0 + l32] : cc0;
   const float di = SM ? bw.delta[(int64_t)bhq * T + iw0 + l32] : 0.f;
-  // LUCID-Path: dA = -s dP exp2(sl2 S - cc0) = F dP exp2(sl2 S) with the constant
-  // F = -s 2^-cc0, which G carries out of the sweep (applied to dM and to d q~)
-  const float F = SM ? 1.f : -scale * __builtin_amdgcn_exp2f(-cc0);
+  // dA = F dP exp2(sl2 S) (LUCID-Path, F = -s 2^-cc0) or F P (dP - delta) (PaTH softmax,
+  // F = s): the constant F is carried out of the sweep by G (applied to dM and to d q~)
+  const float F = SM ? scale : -scale * __builtin_amdgcn_exp2f(-cc0);
   f32x16 acc[2] = {zero16(), zero16()};
 
   int plan_k[2], plan_o[2];
@@ -497,7 +497,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           const float ex = __builtin_amdgcn_exp2f(SM ? fmaf(sc[e], sl2, -ci) : sc[e] * sl2);
-          sc[e] = SM ? scale * ex * (dp[e] - di) : dp[e] * ex;
+          sc[e] = SM ? ex * (dp[e] - di) : dp[e] * ex;
         }
         const bf16x8 d0 = pack_b(sc, 0), d1 = pack_b(sc, 1);
 #pragma unroll
@@ -574,9 +574,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
   const bool live = Jw < NT;           // NT odd: the last pair has one chunk
   const int sJ = J1 / PR, cb = sJ * PR, ceJ = min(cb + PR, NT) - 1;
   const float sl2 = scale * LOG2E_F, cc0 = LOG2E_F / scale;
-  // LUCID-Path: dA = -s dP exp2(sl2 S - cc0) = F dP exp2(sl2 S) with the constant
-  // F = -s 2^-cc0, applied to the accumulators where the sweep hands them on
-  const float F = SM ? 1.f : -scale * __builtin_amdgcn_exp2f(-cc0);
+  // dA = F dP exp2(sl2 S) (LUCID-Path, F = -s 2^-cc0) or F P (dP - delta) (PaTH softmax,
+  // F = s): the constant F is applied to the dK accumulators where the sweep hands them on
+  const float F = SM ? scale : -scale * __builtin_amdgcn_exp2f(-cc0);
 
   bf16x8 kbs[4], kbf[4], ob[4];
   {
@@ -646,7 +646,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
         for (int qq = 0; qq < 4; ++qq) {
           f32x4 x;
 #pragma unroll
-          for (int u = 0; u < 4; ++u) x[u] = as_[t][4 * qq + u];
+          for (int u = 0; u < 4; ++u) x[u] = F * as_[t][4 * qq + u];
           *reinterpret_cast<f32x4*>(dst + t * 32 + 8 * qq + 4 * g) = x;
         }
       as_[0] = zero16();
@@ -679,7 +679,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
             for (int u = 0; u < 4; ++u) {
               const int e = 4 * qq + u;
               sc[e] = __builtin_amdgcn_exp2f(fmaf(sc[e], sl2, -c4[u]));  // P
-              dp[e] = scale * sc[e] * (dp[e] - d4[u]);                   // dA
+              dp[e] = sc[e] * (dp[e] - d4[u]);                           // dA / F
             }
           }
           const bf16x8 p0 = pack_b(sc, 0), p1 = pack_b(sc, 1);
@@ -741,7 +741,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           if (!SM) sm.u.fin.a[(w & 1) * 32 + l32][t * 32 + drow(e, g)] = F * as_[t][e];
-          sm.u.fin.f[(w & 1) * 32 + l32][t * 32 + drow(e, g)] = SM ? as_[t][e] : F * af[t][e];
+          sm.u.fin.f[(w & 1) * 32 + l32][t * 32 + drow(e, g)] = F * (SM ? as_[t][e] : af[t][e]);
         }
     }
     load_mat64<false>(sm.u.fin.m, ws.suf + ((int64_t)bh * NT + J) * 4096);
