@@ -1626,13 +1626,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void l
 #pragma unroll
       for (int mt = 0; mt < NMT; ++mt) {
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const float p = __builtin_amdgcn_exp2f(fmaf(s[mt][e], c, -m));
-          lsum += p;
-          s[mt][e] = p;
-        }
+        for (int e = 0; e < 16; ++e) s[mt][e] = __builtin_amdgcn_exp2f(fmaf(s[mt][e], c, -m));
         pb[2 * mt] = pack_b(s[mt], 0);
         pb[2 * mt + 1] = pack_b(s[mt], 1);
+        lsum = add_sum8(pb[2 * mt + 1], add_sum8(pb[2 * mt], lsum));  // sum of the bf16 P of P V'
       }
 #pragma unroll
       for (int t = 0; t < NDT; ++t)

@@ -61,6 +61,17 @@ __device__ __forceinline__ int drow(int e, int g) { return 8 * (e >> 2) + 4 * g 
 
 __device__ __forceinline__ bf16x8 ld8(const bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
 
+// acc + the sum of eight bf16 values (four v_dot2 against (1, 1)): the row sums of a
+// softmax taken from the same bf16 values that enter its P V product
+__device__ __forceinline__ float add_sum8(const bf16x8& p, float acc) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  const bf16x2 ones = {(bf16)1.0f, (bf16)1.0f};
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    acc = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{p[2 * k], p[2 * k + 1]}, ones, acc, false);
+  return acc;
+}
+
 // eight bf16 values times a in fp32, rounded once to bf16
 __device__ __forceinline__ bf16x8 scale8(const bf16x8& x, float a) {
   bf16x8 r;
