@@ -213,7 +213,11 @@ int launch_precond_fwd(const void* k, const int64_t* ks, const void* v, const in
   // both instances of the chain: each solves the heads of its precision and returns at
   // once for the others
   if (g_precision != LUCID_PRECISION_EXACT) {
-    if (D == 128)  // eight waves (two per SIMD) at head dim 128
+    if (D == 128 && T % 256 == 0)  // 256 rows per workgroup: each staged pair serves twice the rows
+      LUCID_LAUNCH_B("lucid_precond_fwd_wide_kernel", (lucid::lucid_precond_fwd_wide_kernel<128>),
+                     dim3((T / 256) * BH), dim3(512), st, (const bf16*)k, S(ks), (const bf16*)v, S(vs), Hkv, T, BH,
+                     w.rinv, w.khat, scale, vprime, w.vpb, w.vpt, w.pinv, w.zx, w.mass, w.counters);
+    else if (D == 128)  // eight waves (two per SIMD) at head dim 128
       LUCID_LAUNCH_B("lucid_precond_fwd_kernel", (lucid::lucid_precond_fwd_kernel<128, false, false, 8>),
                      dim3((T / 128) * BH), dim3(512), st, (const bf16*)k, S(ks), (const bf16*)v, S(vs), Hkv, T, BH,
                      w.rinv, w.khat, scale, vprime, w.vpb, w.vpt, w.vpbl, w.vptl, w.pinv, w.zx, w.mass, w.counters,

@@ -1182,6 +1182,264 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
 }
 
 // ---------------------------------------------------------------------------
+// The bf16 forward chain at head dim 128 with 256 rows (two 128-row blocks 2p, 2p + 1) per
+// workgroup, for T a multiple of 256: eight waves, wave w owns rows i0 + 32w .. +32 (block
+// 2p: waves 0..3, block 2p + 1: waves 4..7) and sweeps all 128 keys of every staged pair, so
+// that each staged pair (K^ rows, V'^T) serves 256 rows and a head's earlier pairs are
+// fetched half as often (at this head dim the chain streams them from HBM).  After the sweep
+// over the pairs before block 2p, block 2p is solved and published as in
+// lucid_precond_fwd_kernel; then its K^ rows are staged and, with its V'^T from the solve's
+// LDS copy, swept once more by the waves of block 2p + 1, which is solved and published in
+// turn.  Heads of the exact chains return at once (lucid_precond_fwd_kernel<D, true>).
+// ---------------------------------------------------------------------------
+template <int D>
+struct PfwdWideSmem {
+  union {
+    struct {
+      bf16 k[2][128 * D];  // staged K^ rows of a pair (swizzled, chunk c of row r at c ^ (r & 7))
+      bf16 v[2][D * 128];  // staged V'^T of a pair (T-perm rows, swizzled)
+    } st;
+    struct {
+      float Rt[D][132];     // R^T of the block being solved (cols 0..63 = first sub-block)
+      float X[64][68];      // inverse of the diagonal sub-block being solved
+      bf16 vT[D][128 + 8];  // V'^T of the block just solved (bf16, T-perm within 16-groups)
+    } fin;
+  } u;
+};
+
+template <int D>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void lucid_precond_fwd_wide_kernel(
+    const bf16* __restrict__ k, Strides ks, const bf16* __restrict__ v, Strides vs, int Hkv, int T, int BH,
+    const float* __restrict__ rinv, const bf16* __restrict__ khat, float scale, float* __restrict__ vp32,
+    bf16* __restrict__ vpb, bf16* __restrict__ vpt, const float* __restrict__ pinv, const float* __restrict__ zx,
+    const float* __restrict__ mass, int* __restrict__ counters) {
+  static_assert(D == 128, "wide forward chain: head dim 128");
+  constexpr int NDT = D / 32;
+  constexpr int NKS = D / 16;
+  constexpr int NTHR = 512;
+  __shared__ __attribute__((aligned(16))) PfwdWideSmem<D> sm;
+  static_assert(sizeof(bf16) * 128 * D <= sizeof(sm.u.fin.Rt), "block K^ rows must fit in R^T's bytes");
+
+  const int id = blockIdx.x;
+  const int p = id / BH, bh = id - (id / BH) * BH;  // ids grow with p: every wait is on a lower id
+  if (mass[bh] > kExactMass) return;  // the exact instance of lucid_precond_fwd_kernel solves this head
+  const int b = bh / Hkv, h = bh - b * Hkv;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int g = lane >> 5, l32 = lane & 31;
+  const int i0 = p * 256;
+  const int NT = T / 64;
+  const int row = i0 + 32 * w + l32;  // this lane's row
+  const bf16* kp = k + b * ks.b + h * ks.h;
+  const bf16* vh = v + b * vs.b + h * vs.h;
+  const float* rv = rinv + (int64_t)bh * T;
+  const bf16* khh = khat + (int64_t)bh * T * D;
+  const bf16* vpth = vpt + (int64_t)bh * D * T;
+  int* cnt = counters + bh;
+  const float sl2 = scale * LOG2E_F;
+  const float c0 = LOG2E_F / scale;
+  // as in lucid_precond_fwd_kernel's bf16 instance: K^ tiles against the row key scaled by
+  // s log2(e) r_i, and P = exp2(E - c0) = C exp2(E): the accumulators carry a factor 1/C
+  const float Cf = __builtin_amdgcn_exp2f(-c0), invC = __builtin_amdgcn_exp2f(c0);
+  const float ai = sl2 * rv[row];
+  bf16x8 kbi[NKS];
+#pragma unroll
+  for (int st = 0; st < NKS; ++st) kbi[st] = scale8(ld8(kp + (int64_t)row * ks.t + 16 * st + 8 * g), ai);
+  f32x16 acc[NDT];  // -V^T / C
+#pragma unroll
+  for (int t = 0; t < NDT; ++t)
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd) {
+      const bf16x4 x = *reinterpret_cast<const bf16x4*>(vh + (int64_t)row * vs.t + t * 32 + 8 * qd + 4 * g);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) acc[t][4 * qd + u] = -(float)x[u] * invC;
+    }
+
+  int plan_k[128 * (D / 8) / NTHR], plan_v[D * 16 / NTHR];
+  dma_plan<128, D / 8, NTHR>(D, plan_k);
+  dma_plan<D, 16, NTHR>(T, plan_v);
+  auto stage = [&](int pp) {
+    const int buf = pp & 1;
+    dma_stage<128, D / 8, NTHR>(plan_k, khh + (int64_t)pp * 128 * D, sm.u.st.k[buf]);
+    dma_stage<D, 16, NTHR>(plan_v, vpth + pp * 128, sm.u.st.v[buf]);
+  };
+  // all 128 keys of a pair: K^ rows tk (staged layout), V'^T through vop(t, chunk)
+  auto sweep_keys = [&](const bf16* tk, auto vop) {
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      const int key0 = mt * 32;
+      f32x16 sc = zero16();
+#pragma unroll
+      for (int st = 0; st < NKS; ++st) sc = mfma32(ld8(swz<D / 8>(tk, key0 + l32, 2 * st + g)), kbi[st], sc);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sc[e] = __builtin_amdgcn_exp2f(sc[e]);
+      const bf16x8 pb0 = pack_b(sc, 0), pb1 = pack_b(sc, 1);
+#pragma unroll
+      for (int t = 0; t < NDT; ++t) {
+        acc[t] = mfma32(vop(t, key0 / 8 + g), pb0, acc[t]);
+        acc[t] = mfma32(vop(t, key0 / 8 + 2 + g), pb1, acc[t]);
+      }
+    }
+  };
+
+  // ---- sweep over the 2p pairs before block 2p (pair pp is complete once the counter
+  // exceeds 2pp + 1), double buffered ----
+  const int npair = 2 * p;
+  int ready = 0;
+  if (npair > 0) {
+    ready = wait_counter_gt(cnt, 1);
+    stage(0);
+    dma_wait();
+  }
+  __syncthreads();
+  for (int pp = 0; pp < npair; ++pp) {
+    const int buf = pp & 1;
+    const bool more = pp + 1 < npair;
+    const int need = 2 * pp + 3;  // pair pp + 1 is complete once the counter exceeds this
+    bool early = false;
+    if (more) {
+      if (need >= ready) {
+        const int seen = poll_counter(cnt);
+        if (seen > need) {
+          chain_acquire();
+          ready = seen;
+        }
+      }
+      early = need < ready;
+      if (early) stage(pp + 1);
+    }
+    sweep_keys(sm.u.st.k[buf], [&](int t, int c) { return ld8(swz<16>(sm.u.st.v[buf], t * 32 + l32, c)); });
+    if (more && !early) {
+      ready = wait_counter_gt(cnt, need);
+      stage(pp + 1);
+    }
+    dma_wait();
+    __syncthreads();
+  }
+
+  // ---- solve one 128-row block q (2p or 2p + 1) whose R^T is in Rt: V'_A = X_A R_A,
+  // V'_B = X_B R_B + Z V'_A, written out and kept as V'^T in LDS; then published ----
+  f32x4 xr[4];
+  auto xload = [&](int q) {
+    const float* pinv_blk = pinv + ((int64_t)bh * NT + 2 * q) * 4096;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int idx = tid + NTHR * u;
+      const int sb = idx >> 10, r = (idx >> 4) & 63, c4 = (idx & 15) * 4;
+      xr[u] = *reinterpret_cast<const f32x4*>(pinv_blk + sb * 4096 + r * 64 + c4);
+    }
+  };
+  auto xstore = [&](int sb) {
+#pragma unroll
+    for (int u = 2 * sb; u < 2 * sb + 2; ++u) {
+      const int idx = tid + NTHR * u;
+      const int r = (idx >> 4) & 63, c4 = (idx & 15) * 4;
+      *reinterpret_cast<f32x4*>(&sm.u.fin.X[r][c4]) = xr[u];
+    }
+  };
+  auto solve_block = [&](int q) {
+    const int r0 = q * 128;
+    // Z rows of this wave's B output tiles (row half rh = w & 1)
+    f32x4 zr[4][2];
+    {
+      const float* zrow = zx + ((int64_t)bh * (T / 128) + q) * 4096 + ((w & 1) * 32 + l32) * 64 + 8 * g;
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        zr[st][0] = *reinterpret_cast<const f32x4*>(zrow + 16 * st);
+        zr[st][1] = *reinterpret_cast<const f32x4*>(zrow + 16 * st + 4);
+      }
+    }
+    float(*Rt)[132] = sm.u.fin.Rt;
+    // V'^T[d][r] = sum_c R^T[d][c] X[r][c] for sub-block sb (X lower triangular); tile w
+    auto diag_solve = [&](int sb) {
+      const int dt = w >> 1, rh = w & 1;
+      f32x16 o = zero16();
+      const int kmax = rh ? 4 : 2;
+      for (int st = 0; st < kmax; ++st) {
+        bf16x8 ah, al, bh8, bl;
+        split8(&Rt[dt * 32 + l32][sb * 64 + 16 * st + 8 * g], ah, al);
+        split8(&sm.u.fin.X[rh * 32 + l32][16 * st + 8 * g], bh8, bl);
+        o = mfma32(ah, bh8, o);
+        o = mfma32(ah, bl, o);
+        o = mfma32(al, bh8, o);
+      }
+      if (sb == 1) {  // + Z V'_A: V'_A^T from the bf16 T-perm tile, Z split into hi + lo
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+          bf16x8 zh, zl;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float x = zr[st][e >> 2][e & 3];
+            zh[e] = (bf16)x;
+            zl[e] = (bf16)(x - (float)zh[e]);
+          }
+          const bf16x8 va = ld8(&sm.u.fin.vT[dt * 32 + l32][16 * st + 8 * g]);
+          o = mfma32(va, zh, o);
+          o = mfma32(va, zl, o);
+        }
+      }
+      const int rl = rh * 32 + l32;
+      const int r = r0 + sb * 64 + rl;
+      const int lslot = sb * 64 + ((rl & ~15) | jmap(rl & 15));
+      float* out32 = vp32 + ((int64_t)bh * T + r) * D;
+      bf16* outb = vpb + ((int64_t)bh * T + r) * D;
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd) {
+        const int d0 = dt * 32 + 8 * qd + 4 * g;
+        f32x4 f;
+        bf16x4 bb;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          f[u] = o[4 * qd + u];
+          bb[u] = (bf16)o[4 * qd + u];
+          sm.u.fin.vT[d0 + u][lslot] = bb[u];
+        }
+        *reinterpret_cast<f32x4*>(out32 + d0) = f;
+        *reinterpret_cast<bf16x4*>(outb + d0) = bb;
+      }
+    };
+    xstore(0);
+    __syncthreads();
+    diag_solve(0);
+    __syncthreads();
+    xstore(1);
+    __syncthreads();
+    diag_solve(1);
+    __syncthreads();
+    // V'^T of the block to the T-perm operand copy: 16-byte stores
+    for (int c = tid; c < D * 16; c += NTHR) {
+      const int dd = c >> 4, s8 = (c & 15) * 8;
+      *reinterpret_cast<bf16x8*>(vpt + ((int64_t)bh * D + dd) * T + r0 + s8) = ld8(&sm.u.fin.vT[dd][s8]);
+    }
+    publish_counter(cnt, 2 * q + 2);
+  };
+  // R^T = -C acc for the waves of block half `half` (waves 4 half .. 4 half + 3)
+  auto store_r = [&](int half) {
+    if ((w >> 2) == half) {
+#pragma unroll
+      for (int t = 0; t < NDT; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sm.u.fin.Rt[t * 32 + drow(e, g)][32 * (w & 3) + l32] = -Cf * acc[t][e];
+    }
+  };
+
+  // ---- block 2p ----
+  xload(2 * p);
+  store_r(0);
+  solve_block(2 * p);  // (its first barrier orders the R^T stores before the solve)
+  // ---- block 2p + 1: block 2p's keys (K^ rows staged into R^T's bytes, V'^T from the
+  // solve's copy), then its own solve ----
+  bf16* kx = reinterpret_cast<bf16*>(&sm.u.fin.Rt[0][0]);
+  dma_stage<128, D / 8, NTHR>(plan_k, khh + (int64_t)i0 * D, kx);
+  xload(2 * p + 1);
+  dma_wait();
+  __syncthreads();
+  if (w >= 4) sweep_keys(kx, [&](int t, int c) { return ld8(&sm.u.fin.vT[t * 32 + l32][8 * c]); });
+  __syncthreads();
+  store_r(1);
+  solve_block(2 * p + 1);
+}
+
+// ---------------------------------------------------------------------------
 // Fused forward at head dim 64 (bf16, one query head per kv head): the chained
 // preconditioner solve of one 128-row block and the causal attention of the same 128
 // query rows in one workgroup, so that every staged key tile and every LDS operand read

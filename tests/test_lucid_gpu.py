@@ -51,6 +51,8 @@ CASES = [
     (1, 2, 2, 256, 64, 1.0),
     (2, 4, 2, 384, 64, 1.0),
     (1, 2, 1, 200, 128, 1.0),
+    (1, 4, 2, 768, 128, None),    # d = 128 chain over 256-row workgroups with earlier pairs
+    (1, 2, 1, 640, 128, 1.0),     # d = 128, T not a multiple of 256 (128-row workgroups)
 ]
 
 
