@@ -1880,20 +1880,20 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void l
 #pragma unroll
           for (int e = 0; e < 16; ++e) oacc[t][e] *= alpha;
       }
-      bf16x8 pb[2 * NMT];
+      // per 32-key sub-tile: its exps, then its P V' products (key order within each O tile
+      // as before), so that the exps of the next sub-tile can issue beside these MFMAs
 #pragma unroll
       for (int mt = 0; mt < NMT; ++mt) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) s[mt][e] = __builtin_amdgcn_exp2f(fmaf(s[mt][e], c, -m));
-        pb[2 * mt] = pack_b(s[mt], 0);
-        pb[2 * mt + 1] = pack_b(s[mt], 1);
-        lsum = add_sum8(pb[2 * mt + 1], add_sum8(pb[2 * mt], lsum));  // sum of the bf16 P of P V'
+        const bf16x8 pb0 = pack_b(s[mt], 0), pb1 = pack_b(s[mt], 1);
+        lsum = add_sum8(pb1, add_sum8(pb0, lsum));  // sum of the bf16 P of P V'
+#pragma unroll
+        for (int t = 0; t < NDT; ++t) {
+          oacc[t] = mfma32(ld8(&lv[buf][t * 32 + l32][32 * mt + 8 * g]), pb0, oacc[t]);
+          oacc[t] = mfma32(ld8(&lv[buf][t * 32 + l32][32 * mt + 16 + 8 * g]), pb1, oacc[t]);
+        }
       }
-#pragma unroll
-      for (int t = 0; t < NDT; ++t)
-#pragma unroll
-        for (int k4 = 0; k4 < 2 * NMT; ++k4)
-          oacc[t] = mfma32(ld8(&lv[buf][t * 32 + l32][16 * k4 + 8 * g]), pb[k4], oacc[t]);
     }
     if (more) lstore(buf ^ 1);
     __syncthreads();

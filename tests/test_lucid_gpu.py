@@ -206,17 +206,19 @@ def _correlated_keys(T, D, g, noise=0.1):
     return base + noise * torch.randn(T, D, generator=g)
 
 
-def test_auto_precision_picks_exact_for_correlated_heads():
+@pytest.mark.parametrize("D", [64, 128])
+def test_auto_precision_picks_exact_for_correlated_heads(D):
     """AUTO: a head whose keys share a direction (row mass ~T) runs the exact chains, a head of
     N(0,1)-like keys the bf16 ones; the sampled mass agrees with the exact row mass
-    max_i sum_{j<i} P_ij^2 of the float64 oracle, and both heads meet the parity bars."""
+    max_i sum_{j<i} P_ij^2 of the float64 oracle, and both heads meet the parity bars.  At
+    head dim 128 the two instances are the 256-row bf16 chain and the exact chain."""
     from lucid_amd import lucid
-    B, Hq, Hkv, T, D = 1, 2, 2, 1024, 64
+    B, Hq, Hkv, T = 1, 2, 2, 1024
     g = torch.Generator().manual_seed(21)
     q = torch.randn(B, Hq, T, D, generator=g).to(torch.bfloat16)
     k = torch.stack([torch.randn(T, D, generator=g), _correlated_keys(T, D, g)])[None].to(torch.bfloat16)
     v = (torch.randn(B, Hkv, T, D, generator=g) / 8).to(torch.bfloat16)
-    print("case auto precision", flush=True)
+    print(f"case auto precision D={D}", flush=True)
     assert lucid.get_precision() == "auto"
     o, vp, lse, ws = lucid._fwd(q.cuda(), k.cuda(), v.cuda(), D ** -0.5, 1e-5, D)
     torch.cuda.synchronize()
