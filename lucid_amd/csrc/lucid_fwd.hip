@@ -1772,8 +1772,8 @@ __device__ __forceinline__ void attn_block_of(int id, int nblk, int BH, int G, i
 // Causal attention on V' at head dim 128 (bf16): 256 query rows per workgroup as eight
 // waves of 32 rows (one n-tile each), two waves per SIMD, so that one wave's softmax runs
 // beside the other's MFMAs; every KT-key tile of K and V'^T (KT = 64 or 128; the launch uses
-// 128) is staged once per workgroup in LDS (double buffered, register-staged one tile ahead
-// by all 512 threads, padded rows) and read by all eight waves.  Per wave and 64 keys:
+// 128) is staged once per workgroup in LDS (double buffered, loaded one tile ahead by direct
+// global -> LDS loads of all 512 threads, swizzled rows) and read by all eight waves.  Per wave and 64 keys:
 // S^T[j][i] = K_j . Q_i (16 MFMAs), the online softmax (one row max per staged tile, lazy
 // rescale by 2^8), O^T[d][i] += V'^T[d][j] P^T[j][i] (16 MFMAs).
 // Outputs as lucid_attn_fwd_kernel (O, lse2, O's lo part for exact heads).
@@ -1786,11 +1786,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void l
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
   constexpr int NMT = KT / 32;        // 32-key sub-tiles per staged tile
-  constexpr int CH = D * KT / 4096;   // 16-byte chunks per thread for each of the K and V'^T tiles
   static_assert(D == 128, "the wide attention kernel is the head-dim-128 path");
   static_assert(KT == 64 || KT == 128, "keys per staged tile");
-  __shared__ __attribute__((aligned(16))) bf16 lk[2][KT][D + 8];
-  __shared__ __attribute__((aligned(16))) bf16 lv[2][D][KT + 8];
+  // staged tiles, unpadded and swizzled (chunk c of row r at c ^ (r & 7)), filled by direct
+  // global -> LDS loads
+  __shared__ __attribute__((aligned(16))) bf16 lk[2][KT * D];
+  __shared__ __attribute__((aligned(16))) bf16 lv[2][D * KT];
 
   const int G = Hq / Hkv;
   const int nblk = (T + 255) / 256;
@@ -1819,34 +1820,21 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void l
 
   const int ntile = (min(r0 + 256, T) + KT - 1) / KT;
   const int last_w = row0 / KT;  // the tile holding this wave's diagonal
-  bf16x8 stg[2 * CH];
-  auto gload = [&](int j0) {
-#pragma unroll
-    for (int u = 0; u < CH; ++u) {
-      const int cidx = tid + 512 * u;
-      const int kr = cidx / (D / 8), kc = cidx % (D / 8);
-      stg[u] = ld8(kh + (int64_t)min(j0 + kr, T - 1) * ks.t + kc * 8);
-      const int vr = cidx / (KT / 8), vc = cidx % (KT / 8);
-      stg[CH + u] = ld8(vth + (int64_t)vr * T + min(j0 + vc * 8, T - 8));
-    }
+  // T is a multiple of KT (checked by the launch), so every staged tile lies inside the rows
+  int plan_k[KT * (D / 8) / 512], plan_v[D * (KT / 8) / 512];
+  dma_plan<KT, D / 8, 512>(ks.t, plan_k);
+  dma_plan<D, KT / 8, 512>(T, plan_v);
+  auto stage = [&](int j0, int buf) {
+    dma_stage<KT, D / 8, 512>(plan_k, kh + (int64_t)j0 * ks.t, lk[buf]);
+    dma_stage<D, KT / 8, 512>(plan_v, vth + j0, lv[buf]);
   };
-  auto lstore = [&](int buf) {
-#pragma unroll
-    for (int u = 0; u < CH; ++u) {
-      const int cidx = tid + 512 * u;
-      const int kr = cidx / (D / 8), kc = cidx % (D / 8);
-      *reinterpret_cast<bf16x8*>(&lk[buf][kr][kc * 8]) = stg[u];
-      const int vr = cidx / (KT / 8), vc = cidx % (KT / 8);
-      *reinterpret_cast<bf16x8*>(&lv[buf][vr][vc * 8]) = stg[CH + u];
-    }
-  };
-  gload(0);
-  lstore(0);
+  stage(0, 0);
+  dma_wait();
   __syncthreads();
   for (int jt = 0; jt < ntile; ++jt) {
     const int buf = jt & 1;
     const bool more = jt + 1 < ntile;
-    if (more) gload((jt + 1) * KT);
+    if (more) stage((jt + 1) * KT, buf ^ 1);
     if (jt <= last_w && row0 < T) {
       f32x16 s[NMT];
 #pragma unroll
@@ -1854,7 +1842,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void l
         s[mt] = zero16();
 #pragma unroll
         for (int st = 0; st < NKS; ++st)
-          s[mt] = mfma32(ld8(&lk[buf][mt * 32 + l32][16 * st + 8 * g]), qb[st], s[mt]);
+          s[mt] = mfma32(ld8(swz<D / 8>(lk[buf], mt * 32 + l32, 2 * st + g)), qb[st], s[mt]);
       }
       if (jt == last_w) {  // causal mask: key KT jt + mt 32 + drow > row
         const int rel = row0 - jt * KT + l32;  // the lane's row relative to the tile's first key
@@ -1890,12 +1878,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void l
         lsum = add_sum8(pb1, add_sum8(pb0, lsum));  // sum of the bf16 P of P V'
 #pragma unroll
         for (int t = 0; t < NDT; ++t) {
-          oacc[t] = mfma32(ld8(&lv[buf][t * 32 + l32][32 * mt + 8 * g]), pb0, oacc[t]);
-          oacc[t] = mfma32(ld8(&lv[buf][t * 32 + l32][32 * mt + 16 + 8 * g]), pb1, oacc[t]);
+          oacc[t] = mfma32(ld8(swz<KT / 8>(lv[buf], t * 32 + l32, 4 * mt + g)), pb0, oacc[t]);
+          oacc[t] = mfma32(ld8(swz<KT / 8>(lv[buf], t * 32 + l32, 4 * mt + 2 + g)), pb1, oacc[t]);
         }
       }
     }
-    if (more) lstore(buf ^ 1);
+    dma_wait();
     __syncthreads();
   }
   const bool exact = mass[bh] > kExactMass;
