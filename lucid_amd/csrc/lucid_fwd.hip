@@ -1789,9 +1789,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void l
   static_assert(D == 128, "the wide attention kernel is the head-dim-128 path");
   static_assert(KT == 64 || KT == 128, "keys per staged tile");
   // staged tiles, unpadded and swizzled (chunk c of row r at c ^ (r & 7)), filled by direct
-  // global -> LDS loads
-  __shared__ __attribute__((aligned(16))) bf16 lk[2][KT * D];
-  __shared__ __attribute__((aligned(16))) bf16 lv[2][D * KT];
+  // global -> LDS loads.  One LDS variable: with the K and V'^T tiles in two, the compiler
+  // waits for the next tile's loads before the first read of the current tile.
+  __shared__ __attribute__((aligned(16))) struct {
+    bf16 k[2][KT * D];
+    bf16 v[2][D * KT];
+  } sm;
+  auto& lk = sm.k;
+  auto& lv = sm.v;
 
   const int G = Hq / Hkv;
   const int nblk = (T + 255) / 256;
@@ -1829,6 +1834,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void l
     dma_stage<D, KT / 8, 512>(plan_v, vth + j0, lv[buf]);
   };
   stage(0, 0);
+  // the Q rows are consumed here, so that they have landed before the loop: otherwise the
+  // compiler moves their loads past this point and then waits for all loads (vmcnt(0)),
+  // the next tile's direct loads included, before the first product of every tile
+#pragma unroll
+  for (int st = 0; st < NKS; ++st) asm volatile("" ::"v"(qb[st]));
   dma_wait();
   __syncthreads();
   for (int jt = 0; jt < ntile; ++jt) {
