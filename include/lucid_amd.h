@@ -1,8 +1,12 @@
 /*
  * lucid_amd -- C ABI of the MI355X (gfx950) LUCID attention kernels.
  *
- * Plain pointers and sizes only; every buffer is caller-owned device memory
- * (the library never allocates).  Tensors are bf16 (fp32 for the _f32 entry
+ * Plain pointers and sizes only; every buffer is caller-owned device memory (the
+ * library allocates no device memory; its only allocation is the 4-byte pinned flag of the
+ * bounded chain waits, made with a per-device set-up -- hipHostMalloc once per process,
+ * hipMemcpyToSymbol once per device -- by the first chain call on a device and again after
+ * lucid_set_chain_wait_limit; code that captures HIP graphs calls lucid_chain_status() once per
+ * device before capture, which does that set-up).  Tensors are bf16 (fp32 for the _f32 entry
  * points) with the last (head_dim) axis contiguous; the other axes are described by element strides
  * {batch, head, time}.  All launches go on `stream` (a hipStream_t, NULL =
  * default stream); calls are asynchronous.  Return value: 0 on success,
@@ -29,6 +33,9 @@
 extern "C" {
 #endif
 
+/* The libraries are built with hidden symbol visibility; only these entry points are exported. */
+#pragma GCC visibility push(default)
+
 #define LUCID_OK 0
 #define LUCID_EINVAL 1
 #define LUCID_ECHAIN 2 /* a chain wait gave up in an earlier launch (lucid_chain_status) */
@@ -39,14 +46,15 @@ extern "C" {
 #define LUCID_PRECISION_FAST 1  /* bf16 products everywhere */
 #define LUCID_PRECISION_EXACT 2 /* hi/lo split products for every head */
 
-/* ABI version of this header (bumped on any signature change or new entry point): 5. */
+/* ABI version of this header (bumped on any signature change or new entry point): 6. */
 int lucid_abi_version(void);
 
 /* Text of the last error on the calling thread ("" if none). */
 const char* lucid_last_error(void);
 
-/* Chain precision for the forward calls that follow (process-wide; the backward uses the
- * choice recorded in the forward workspace).  The off-diagonal products of the chained
+/* Chain precision for the forward calls that follow on the calling thread (thread-local:
+ * another thread's calls keep their own mode; the backward uses the choice recorded in the
+ * forward workspace, so it may run on any thread).  The off-diagonal products of the chained
  * solves (P V', P^T dV, (dV V'^T) * P and its sums with K) accumulate over every earlier
  * key of a row; with bf16 operands their error grows like 2^-8 |V'| sqrt(m), m = the
  * row mass sum_{j<i} P_ij^2, which is ~1e-2 for keys with no common direction but ~T for
@@ -59,8 +67,8 @@ const char* lucid_last_error(void);
 int lucid_set_precision(int mode);
 int lucid_get_precision(void);
 
-/* Forward kernel schedule for the calls that follow (process-wide; no counterpart in the
- * reference).  On (default): at head dim <= 64 with one query head per kv head, the
+/* Forward kernel schedule for the calls that follow on the calling thread (thread-local;
+ * no counterpart in the reference).  On (default): at head dim <= 64 with one query head per kv head, the
  * preconditioner chain and the causal attention of each 128-row block run in one fused
  * kernel (lucid_fused_fwd_kernel) that feeds every staged key tile to both; off: the chain
  * kernel, then the attention kernel.  Both give the same O, V' and lse up to the rounding
@@ -210,6 +218,29 @@ int lucid_precond_bwd(const void* k, const int64_t* k_strides, const void* dvpri
                       const int64_t* dv_strides, void* bwd_ws, int B, int Hkv, int T, int D, float scale,
                       void* stream);
 
+/* ---- Lucid_Tril_Solver: the solve on keys that are already normalised ----
+ * V' = P(K^)^-1 V with P_ij = exp(s K^_i . K^_j - 1/s) (j <= i) for a caller's K^ (no k_norm
+ * inside: 1/rms is taken as 1), and its gradient dV = P^-T dV', dK^ = -s (M K^ + M^T K^),
+ * M = tril((dV V'^T) * P), diagonal included -- dK^ itself, with no RMSNorm backward.
+ * Replace Lucid_Tril_Solver.forward / .backward (modeling_lucid.py:284-312, :314-382), which
+ * take key = K^ and return (grad_k, grad_v).  The result does not depend on the reference's
+ * block size BS (a blocking of the same solve), and value is not modified (the reference's
+ * forward subtracts from value's rows in place, :296-299).  Same arguments, layouts and
+ * workspaces (lucid_fwd_workspace_bytes(B, Hkv, Hkv, T, D), lucid_precond_bwd_workspace_bytes)
+ * as lucid_get_v_prime / lucid_precond_bwd; the _f32 variants those of lucid_get_v_prime_f32 /
+ * lucid_precond_bwd_f32 (lucid_v_prime_f32_workspace_bytes). */
+int lucid_tril_solve(const void* key_hat, const int64_t* k_strides, const void* v, const int64_t* v_strides,
+                     float* vprime, void* fwd_ws, int B, int Hkv, int T, int D, float scale, void* stream);
+int lucid_tril_solve_bwd(const void* key_hat, const int64_t* k_strides, const void* dvprime,
+                         const int64_t* dvprime_strides, int dvprime_f32, const void* fwd_ws, void* dk,
+                         const int64_t* dk_strides, void* dv, const int64_t* dv_strides, void* bwd_ws, int B, int Hkv,
+                         int T, int D, float scale, void* stream);
+int lucid_tril_solve_f32(const float* key_hat, const int64_t* k_strides, const float* v, const int64_t* v_strides,
+                         float* vprime, void* fwd_ws, int B, int Hkv, int T, int D, float scale, void* stream);
+int lucid_tril_solve_bwd_f32(const float* dvprime, const int64_t* dvprime_strides, const void* fwd_ws, float* dk,
+                             const int64_t* dk_strides, float* dv, const int64_t* dv_strides, void* bwd_ws, int B,
+                             int Hkv, int T, int D, float scale, void* stream);
+
 /* Bytes of the decoding workspace for caches of capacity T_cap (0 on bad sizes). */
 size_t lucid_decode_workspace_bytes(int B, int Hq, int Hkv, int T_cap, int D);
 
@@ -221,7 +252,8 @@ size_t lucid_decode_workspace_bytes(int B, int Hq, int Hkv, int T_cap, int D);
  *   v'_t = (v_t - sum_{j<t} P_tj v'_j) / P_tt,
  * writes it to vp_new (fp32 [B,Hkv,D]) and appends (k_t, v'_t) at row T_past of the
  * caches, then o (strides {batch, head, -}, [B,1,Hq,D] in the reference layout) =
- * softmax over j <= t of s q.k_j times v'_j.  Hq / Hkv in {1, 2, 4, 8}.
+ * softmax over j <= t of s q.k_j times v'_j.  Any Hq / Hkv (groups above 31 query heads per kv
+ * head run in chunks of query heads).
  * Replaces LucidAttention.get_new_v_prime (modeling_lucid.py:576-598, which omits the
  * division by P_tt) and the cached attention call of LucidAttention.forward
  * (:475-496); a decoded row equals the same row of lucid_attn_fwd on the whole
@@ -277,6 +309,8 @@ void lucid_profile_enable(int on);
 int lucid_profile_collect(void);
 int lucid_profile_entry(int idx, char* name, int name_len, double* total_ms, long* count);
 void lucid_profile_reset(void);
+
+#pragma GCC visibility pop
 
 #ifdef __cplusplus
 }

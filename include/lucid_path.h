@@ -8,7 +8,9 @@
  * o [B,T,HQ,V]; element strides {batch, head, time}, last axis contiguous.
  * bf16 tensors; K = V = 64; T a multiple of 64 (the Python layer zero-pads the
  * sequence end, exact for every real row since L is strictly lower triangular).
- * Buffers are caller-owned (the library never allocates); launches go on `stream`.
+ * Buffers are caller-owned (no device allocation; the bounded chain waits set up a 4-byte
+ * pinned flag on the first chain call per device, as in lucid_amd.h -- call
+ * lucid_path_chain_status() once before HIP graph capture); launches go on `stream`.
  * Return codes as in lucid_amd.h (0 ok, 1 bad argument, 1000 + hipError_t).
  */
 #ifndef LUCID_PATH_H
@@ -20,6 +22,9 @@
 #ifdef __cplusplus
 extern "C" {
 #endif
+
+/* The libraries are built with hidden symbol visibility; only these entry points are exported. */
+#pragma GCC visibility push(default)
 
 /* ABI version of this header. */
 int lucid_path_abi_version(void);
@@ -107,6 +112,8 @@ void lucid_path_profile_enable(int on);
 int lucid_path_profile_collect(void);
 int lucid_path_profile_entry(int idx, char* name, int name_len, double* total_ms, long* count);
 void lucid_path_profile_reset(void);
+
+#pragma GCC visibility pop
 
 #ifdef __cplusplus
 }

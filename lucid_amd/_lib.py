@@ -69,6 +69,12 @@ _SIGS = {
         "lucid_precond_bwd_workspace_bytes": ([_int] * 4, _sz),
         "lucid_precond_bwd": ([_vp, _i64p, _vp, _i64p, _int, _vp, _vp, _i64p, _vp, _i64p, _vp,
                                _int, _int, _int, _int, _flt, _vp], _int),
+        "lucid_tril_solve": ([_vp, _i64p, _vp, _i64p, _vp, _vp, _int, _int, _int, _int, _flt, _vp], _int),
+        "lucid_tril_solve_bwd": ([_vp, _i64p, _vp, _i64p, _int, _vp, _vp, _i64p, _vp, _i64p, _vp,
+                                  _int, _int, _int, _int, _flt, _vp], _int),
+        "lucid_tril_solve_f32": ([_vp, _i64p, _vp, _i64p, _vp, _vp, _int, _int, _int, _int, _flt, _vp], _int),
+        "lucid_tril_solve_bwd_f32": ([_vp, _i64p, _vp, _vp, _i64p, _vp, _i64p, _vp, _int, _int, _int, _int, _flt,
+                                      _vp], _int),
         "lucid_decode_workspace_bytes": ([_int] * 5, _sz),
         "lucid_decode": ([_vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _vp,
                           _int, _int, _int, _int, _int, _int, _flt, _flt, _vp], _int),

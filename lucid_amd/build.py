@@ -12,10 +12,14 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 ARCH = os.environ.get("LUCID_OFFLOAD_ARCH", "gfx950")
 
-# Every HIP translation unit is compiled with packed-fp32 instructions disabled.
+# Every HIP translation unit is compiled with packed-fp32 instructions disabled.  Host code
+# gets hidden symbol visibility: each library exports only the extern "C" entry points its
+# header declares, so two libraries loaded into one process (RTLD_GLOBAL included) never
+# bind each other's internal helpers or their static state.
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-shared", "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Xarch_host", "-fvisibility=hidden", "-Xarch_host", "-fvisibility-inlines-hidden",
 ]
 
 TARGETS = {

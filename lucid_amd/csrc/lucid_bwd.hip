@@ -1532,12 +1532,15 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
     dotp = wave_sum32(dotp);
     kss = wave_sum32(kss);
     gdot = wave_sum32(gdot);
-    const float f = dotp / dn;
+    // dn <= 0: the keys arrived normalised (the Lucid_Tril_Solver seam): dK^ itself is the
+    // output (r = 1, no RMSNorm backward)
+    const bool knorm = dn > 0.f;
+    const float f = knorm ? dotp / dn : 0.f;
     // The diagonal terms of M K^ + M^T K^ (excluded from both sums), -2 s M_ii K^_i with
     // M_ii = (dV_i . V'_i) P_ii, P_ii = exp(s |K^_i|^2 - 1/s), lie along K^_i, which the
     // RMSNorm backward keeps only to the fraction 1 - |K^_i|^2 / dn (= eps r_i^2): added here
     // as fd * K^_i rather than as two large terms that cancel down to that fraction.
-    const float fd = -2.f * scale * gdot * __builtin_amdgcn_exp2f(fmaf(sl2, kss, -c0)) * (1.f - kss / dn);
+    const float fd = -2.f * scale * gdot * __builtin_amdgcn_exp2f(fmaf(sl2, kss, -c0)) * (knorm ? 1.f - kss / dn : 1.f);
     auto* op = dk_out + b * dks.b + h * dks.h + (int64_t)irow * dks.t;
 #pragma unroll
     for (int t = 0; t < NDT; ++t)

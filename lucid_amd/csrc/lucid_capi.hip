@@ -19,11 +19,12 @@ thread_local std::string g_last_error;
 
 // Precision of the preconditioner chains (lucid_set_precision): LUCID_PRECISION_AUTO picks
 // per head from its row mass (lucid_mass_kernel, kExactMass); the others force one kind.
-int g_precision = LUCID_PRECISION_AUTO;
+// Per calling thread: a mode set on one thread never changes how another thread's calls run.
+thread_local int g_precision = LUCID_PRECISION_AUTO;
 
 // Forward schedule (lucid_set_fused_forward): the fused chain + attention kernel at head
-// dim 64 with one query head per kv head, or the two-kernel sequence.
-bool g_fused_fwd = true;
+// dim 64 with one query head per kv head, or the two-kernel sequence.  Per calling thread.
+thread_local bool g_fused_fwd = true;
 
 int fail(const std::string& msg) {
   g_last_error = msg;
@@ -663,6 +664,18 @@ int decode_splits(int BH, int Tp, int D) {
 // Tokens per split/combine pass: the L (G + 1) columns of one 32-column score tile.
 int decode_pass_tokens(int G) { return 32 / (G + 1); }
 
+// Query heads per kv head are decoded in chunks of at most 31 (a chunk's query columns and
+// the preconditioner row of each token share one 32-column score tile): G <= 31 is one
+// chunk, larger groups split into equal chunks (the last may be smaller), all run with the
+// token passes of the largest so that every chunk computes the same V' rows.
+struct DecodeGroups {
+  int chunks, gs;  // number of chunks, query heads per chunk (the largest)
+};
+DecodeGroups decode_groups(int G) {
+  const int n = (G + 30) / 31;
+  return DecodeGroups{n, (G + n - 1) / n};
+}
+
 lucid::DecodePartials carve_decode(void* base, int BH, int G, int L, int nsplit, int D, size_t* bytes) {
   D = padded_dim(D);
   lucid::DecodePartials w{};
@@ -682,27 +695,29 @@ lucid::DecodePartials carve_decode(void* base, int BH, int G, int L, int nsplit,
   return w;
 }
 
-// Partials of one pass of at most `L` tokens with a cache that grows to `T_end` rows.
+// Partials of one pass of at most `L` tokens with a cache that grows to `T_end` rows (one
+// chunk of query heads at a time: the chunks run in turn on the same partials).
 size_t decode_ws_bytes(int BH, int G, int L, int T_end, int D) {
-  const int Lp = L < decode_pass_tokens(G) ? L : decode_pass_tokens(G);
+  const int Gs = decode_groups(G).gs;
+  const int Lp = L < decode_pass_tokens(Gs) ? L : decode_pass_tokens(Gs);
   size_t n = 0;
-  carve_decode(nullptr, BH, G, Lp, decode_splits(BH, T_end, D), D, &n);
+  carve_decode(nullptr, BH, Gs, Lp, decode_splits(BH, T_end, D), D, &n);
   return n;
 }
 
-// L new tokens in passes of at most decode_pass_tokens(G): each pass reads the cache once
-// (split kernel) and appends its tokens (combine kernel), so the next pass sees them.
+// L new tokens in passes of LM tokens: each pass reads the cache once (split kernel) and
+// appends its tokens (combine kernel), so the next pass sees them.  The Gs query heads
+// g0 .. g0+Gs-1 of each kv head's Gt; G > 0: the instance for Gs = G.
 template <int D, int G>
 int launch_decode(const void* q, const int64_t* qs, const void* k, const int64_t* ks, const void* v,
                   const int64_t* vs, void* kc, const int64_t* kcs, void* vc, const int64_t* vcs, void* o,
                   const int64_t* os, float* vp_new, void* ws, int B, int Hkv, int L, int Tp, float scale, float eps,
-                  float dn, hipStream_t st) {
+                  float dn, hipStream_t st, int Gs, int Gt, int g0, int LM, int write_cache) {
   const int BH = B * Hkv;
-  constexpr int LM = lucid::decode_tokens_per_pass<G>();
   for (int t0 = 0; t0 < L; t0 += LM) {
     const int Lc = L - t0 < LM ? L - t0 : LM, Tc = Tp + t0;
     const int ns = decode_splits(BH, Tc, D);
-    const lucid::DecodePartials part = carve_decode(ws, BH, G, Lc, ns, D, nullptr);
+    const lucid::DecodePartials part = carve_decode(ws, BH, Gs, Lc, ns, D, nullptr);
     const bf16* qc = (const bf16*)q + t0 * qs[2];
     const bf16* kn = (const bf16*)k + t0 * ks[2];
     const bf16* vn = (const bf16*)v + t0 * vs[2];
@@ -710,11 +725,12 @@ int launch_decode(const void* q, const int64_t* qs, const void* k, const int64_t
       const int KS = (Tc + ns - 1) / ns;
       LUCID_LAUNCH("lucid_decode_split_kernel", (lucid::lucid_decode_split_kernel<D, G>), dim3(ns, BH), st, qc,
                    S(qs), kn, S(ks), (const bf16*)kc, S(kcs), (const bf16*)vc, S(vcs), Hkv, Tc, KS, Lc, scale, eps,
-                   dn, part);
+                   dn, part, Gs, Gt, g0);
     }
-    LUCID_LAUNCH("lucid_decode_combine_kernel", (lucid::lucid_decode_combine_kernel<D, G>), dim3(BH, G), st, ns,
+    LUCID_LAUNCH("lucid_decode_combine_kernel", (lucid::lucid_decode_combine_kernel<D, G>), dim3(BH, Gs), st, ns,
                  Lc, qc, S(qs), kn, S(ks), vn, S(vs), (bf16*)kc, S(kcs), (bf16*)vc, S(vcs),
-                 (bf16*)o + t0 * os[2], S(os), vp_new + (size_t)t0 * D, L, Hkv, Tc, scale, eps, dn, part);
+                 (bf16*)o + t0 * os[2], S(os), vp_new + (size_t)t0 * D, L, Hkv, Tc, scale, eps, dn, part, Gs, Gt, g0,
+                 write_cache);
   }
   return LUCID_OK;
 }
@@ -724,13 +740,27 @@ int decode_dispatch_g(int G, const void* q, const int64_t* qs, const void* k, co
                       const int64_t* vs, void* kc, const int64_t* kcs, void* vc, const int64_t* vcs, void* o,
                       const int64_t* os, float* vp_new, void* ws, int B, int Hkv, int L, int Tp, float scale,
                       float eps, float dn, hipStream_t st) {
-  switch (G) {
-    case 1: return launch_decode<D, 1>(q, qs, k, ks, v, vs, kc, kcs, vc, vcs, o, os, vp_new, ws, B, Hkv, L, Tp, scale, eps, dn, st);
-    case 2: return launch_decode<D, 2>(q, qs, k, ks, v, vs, kc, kcs, vc, vcs, o, os, vp_new, ws, B, Hkv, L, Tp, scale, eps, dn, st);
-    case 4: return launch_decode<D, 4>(q, qs, k, ks, v, vs, kc, kcs, vc, vcs, o, os, vp_new, ws, B, Hkv, L, Tp, scale, eps, dn, st);
-    case 8: return launch_decode<D, 8>(q, qs, k, ks, v, vs, kc, kcs, vc, vcs, o, os, vp_new, ws, B, Hkv, L, Tp, scale, eps, dn, st);
-    default: return fail("decode supports Hq / Hkv in {1, 2, 4, 8}, got " + std::to_string(G));
+#define LUCID_DECODE_G(GI) \
+  launch_decode<D, GI>(q, qs, k, ks, v, vs, kc, kcs, vc, vcs, o, os, vp_new, ws, B, Hkv, L, Tp, scale, eps, dn, st, G, G, 0, \
+                       decode_pass_tokens(G), 1)
+  switch (G) {  // the common groupings as their own instances
+    case 1: return LUCID_DECODE_G(1);
+    case 2: return LUCID_DECODE_G(2);
+    case 4: return LUCID_DECODE_G(4);
+    case 8: return LUCID_DECODE_G(8);
+    default: break;
   }
+#undef LUCID_DECODE_G
+  // any other group: the generic instance, in chunks of query heads above 31
+  const DecodeGroups dg = decode_groups(G);
+  const int LM = decode_pass_tokens(dg.gs);
+  for (int c = 0; c < dg.chunks; ++c) {
+    const int g0 = c * dg.gs, gs = G - g0 < dg.gs ? G - g0 : dg.gs;
+    if (int rc = launch_decode<D, 0>(q, qs, k, ks, v, vs, kc, kcs, vc, vcs, o, os, vp_new, ws, B, Hkv, L, Tp, scale,
+                                     eps, dn, st, gs, G, g0, LM, c == 0))
+      return rc;
+  }
+  return LUCID_OK;
 }
 
 int check_decode_args(const void* q, const int64_t* qs, const void* k, const int64_t* ks, const void* v,
@@ -804,6 +834,82 @@ int decode_impl(const void* q, const int64_t* q_strides, const void* k, const in
                                 (float)D, st);
 }
 
+// get_v_prime with k_norm (dn = the head dim) or on keys already normalised (dn = 0, the
+// Lucid_Tril_Solver seam: 1/rms is 1 and the backward returns dK^ itself).
+int get_v_prime_impl(const void* k, const int64_t* k_strides, const void* v, const int64_t* v_strides, float* vprime,
+                     void* fwd_ws, int B, int Hkv, int T, int D, float scale, float eps, float dn, void* stream) {
+  g_last_error.clear();
+  if (int rc = check_dims(B, Hkv, Hkv, T, D)) return rc;
+  if (int rc = check_tensor("k", k, k_strides)) return rc;
+  if (int rc = check_tensor("v", v, v_strides)) return rc;
+  if (!vprime || !fwd_ws) return fail("vprime and fwd_ws must be non-null");
+  if (int rc = check_ws("fwd_ws", fwd_ws)) return rc;
+  if (int rc = chain_check()) return rc;
+  const FwdWs w = carve_fwd(fwd_ws, B, Hkv, Hkv, T, D);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (padded_dim(D) == 64) return launch_precond_fwd<64>(k, k_strides, v, v_strides, vprime, w, B, Hkv, T, scale, eps, dn, st);
+  return launch_precond_fwd<128>(k, k_strides, v, v_strides, vprime, w, B, Hkv, T, scale, eps, dn, st);
+}
+
+int precond_bwd_impl(const void* k, const int64_t* k_strides, const void* dvprime, const int64_t* dvprime_strides,
+                     int dvprime_f32, const void* fwd_ws, void* dk, const int64_t* dk_strides, void* dv,
+                     const int64_t* dv_strides, void* bwd_ws, int B, int Hkv, int T, int D, float scale, float dn,
+                     void* stream) {
+  g_last_error.clear();
+  if (int rc = check_dims(B, Hkv, Hkv, T, D)) return rc;
+  if (int rc = check_tensor("k", k, k_strides)) return rc;
+  if (int rc = check_tensor("dvprime", dvprime, dvprime_strides)) return rc;
+  if (int rc = check_tensor("dk", dk, dk_strides)) return rc;
+  if (int rc = check_tensor("dv", dv, dv_strides)) return rc;
+  if (!fwd_ws || !bwd_ws) return fail("fwd_ws and bwd_ws must be non-null");
+  if (int rc = check_ws("fwd_ws", fwd_ws)) return rc;
+  if (int rc = check_ws("bwd_ws", bwd_ws)) return rc;
+  if (int rc = chain_check()) return rc;
+  const FwdWs f = carve_fwd(const_cast<void*>(fwd_ws), B, Hkv, Hkv, T, D);
+  const BwdWs w = carve_seam_bwd(bwd_ws, B, Hkv, Hkv, T, D, false);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (padded_dim(D) == 64)
+    return launch_precond_only_bwd<64>(k, k_strides, dvprime, dvprime_strides, dvprime_f32, f, dk, dk_strides, dv,
+                                       dv_strides, w, B, Hkv, T, scale, dn, st);
+  return launch_precond_only_bwd<128>(k, k_strides, dvprime, dvprime_strides, dvprime_f32, f, dk, dk_strides, dv,
+                                      dv_strides, w, B, Hkv, T, scale, dn, st);
+}
+
+int get_v_prime_f32_impl(const float* k, const int64_t* k_strides, const float* v, const int64_t* v_strides,
+                         float* vprime, void* fwd_ws, int B, int Hkv, int T, int D, float scale, float eps, float dn,
+                         void* stream) {
+  g_last_error.clear();
+  if (int rc = check_dims(B, Hkv, Hkv, T, D)) return rc;
+  if (padded_dim(D) != kF32D) return fail("fp32 inputs are supported at head_dim <= 64, got " + std::to_string(D));
+  if (int rc = check_tensor("k", k, k_strides)) return rc;
+  if (int rc = check_tensor("v", v, v_strides)) return rc;
+  if (!vprime || !fwd_ws) return fail("vprime and fwd_ws must be non-null");
+  if (int rc = check_ws("fwd_ws", fwd_ws)) return rc;
+  if (int rc = chain_check()) return rc;
+  const FwdWs w = carve_fwd(fwd_ws, B, Hkv, Hkv, T, D, true, false);
+  return launch_precond_fwd_f32(k, k_strides, v, v_strides, vprime, w, B, Hkv, T, scale, eps, dn,
+                                static_cast<hipStream_t>(stream));
+}
+
+int precond_bwd_f32_impl(const float* dvprime, const int64_t* dvprime_strides, const void* fwd_ws, float* dk,
+                         const int64_t* dk_strides, float* dv, const int64_t* dv_strides, void* bwd_ws, int B, int Hkv,
+                         int T, int D, float scale, float dn, void* stream) {
+  g_last_error.clear();
+  if (int rc = check_dims(B, Hkv, Hkv, T, D)) return rc;
+  if (padded_dim(D) != kF32D) return fail("fp32 inputs are supported at head_dim <= 64, got " + std::to_string(D));
+  if (int rc = check_tensor("dvprime", dvprime, dvprime_strides)) return rc;
+  if (int rc = check_tensor("dk", dk, dk_strides)) return rc;
+  if (int rc = check_tensor("dv", dv, dv_strides)) return rc;
+  if (!fwd_ws || !bwd_ws) return fail("fwd_ws and bwd_ws must be non-null");
+  if (int rc = check_ws("fwd_ws", fwd_ws)) return rc;
+  if (int rc = check_ws("bwd_ws", bwd_ws)) return rc;
+  if (int rc = chain_check()) return rc;
+  const FwdWs f = carve_fwd(const_cast<void*>(fwd_ws), B, Hkv, Hkv, T, D, true, false);
+  const BwdWs w = carve_seam_bwd(bwd_ws, B, Hkv, Hkv, T, D, false);
+  return launch_precond_only_bwd_f32(dvprime, dvprime_strides, f, dk, dk_strides, dv, dv_strides, w, B, Hkv, T,
+                                     scale, dn, static_cast<hipStream_t>(stream));
+}
+
 }  // namespace
 
 extern "C" {
@@ -862,7 +968,7 @@ int lucid_decode_noalloc(const void* q, const int64_t* q_strides, const void* k,
 }
 
 
-int lucid_abi_version(void) { return 5; }
+int lucid_abi_version(void) { return 6; }
 
 int lucid_set_precision(int mode) {
   g_last_error.clear();
@@ -912,17 +1018,33 @@ size_t lucid_bwd_workspace_bytes(int B, int Hq, int Hkv, int T, int D) {
 int lucid_get_v_prime(const void* k, const int64_t* k_strides, const void* v, const int64_t* v_strides,
                       float* vprime, void* fwd_ws, int B, int Hkv, int T, int D, float scale, float eps,
                       void* stream) {
-  g_last_error.clear();
-  if (int rc = check_dims(B, Hkv, Hkv, T, D)) return rc;
-  if (int rc = check_tensor("k", k, k_strides)) return rc;
-  if (int rc = check_tensor("v", v, v_strides)) return rc;
-  if (!vprime || !fwd_ws) return fail("vprime and fwd_ws must be non-null");
-  if (int rc = check_ws("fwd_ws", fwd_ws)) return rc;
-  if (int rc = chain_check()) return rc;
-  const FwdWs w = carve_fwd(fwd_ws, B, Hkv, Hkv, T, D);
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  if (padded_dim(D) == 64) return launch_precond_fwd<64>(k, k_strides, v, v_strides, vprime, w, B, Hkv, T, scale, eps, (float)D, st);
-  return launch_precond_fwd<128>(k, k_strides, v, v_strides, vprime, w, B, Hkv, T, scale, eps, (float)D, st);
+  return get_v_prime_impl(k, k_strides, v, v_strides, vprime, fwd_ws, B, Hkv, T, D, scale, eps, (float)D, stream);
+}
+
+int lucid_tril_solve(const void* key_hat, const int64_t* k_strides, const void* v, const int64_t* v_strides,
+                     float* vprime, void* fwd_ws, int B, int Hkv, int T, int D, float scale, void* stream) {
+  return get_v_prime_impl(key_hat, k_strides, v, v_strides, vprime, fwd_ws, B, Hkv, T, D, scale, 0.f, 0.f, stream);
+}
+
+int lucid_tril_solve_bwd(const void* key_hat, const int64_t* k_strides, const void* dvprime,
+                         const int64_t* dvprime_strides, int dvprime_f32, const void* fwd_ws, void* dk,
+                         const int64_t* dk_strides, void* dv, const int64_t* dv_strides, void* bwd_ws, int B, int Hkv,
+                         int T, int D, float scale, void* stream) {
+  return precond_bwd_impl(key_hat, k_strides, dvprime, dvprime_strides, dvprime_f32, fwd_ws, dk, dk_strides, dv,
+                          dv_strides, bwd_ws, B, Hkv, T, D, scale, 0.f, stream);
+}
+
+int lucid_tril_solve_f32(const float* key_hat, const int64_t* k_strides, const float* v, const int64_t* v_strides,
+                         float* vprime, void* fwd_ws, int B, int Hkv, int T, int D, float scale, void* stream) {
+  return get_v_prime_f32_impl(key_hat, k_strides, v, v_strides, vprime, fwd_ws, B, Hkv, T, D, scale, 0.f, 0.f,
+                              stream);
+}
+
+int lucid_tril_solve_bwd_f32(const float* dvprime, const int64_t* dvprime_strides, const void* fwd_ws, float* dk,
+                             const int64_t* dk_strides, float* dv, const int64_t* dv_strides, void* bwd_ws, int B,
+                             int Hkv, int T, int D, float scale, void* stream) {
+  return precond_bwd_f32_impl(dvprime, dvprime_strides, fwd_ws, dk, dk_strides, dv, dv_strides, bwd_ws, B, Hkv, T, D,
+                              scale, 0.f, stream);
 }
 
 int lucid_attn_fwd(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
@@ -1032,36 +1154,14 @@ size_t lucid_v_prime_f32_workspace_bytes(int B, int Hkv, int T, int D) {
 int lucid_get_v_prime_f32(const float* k, const int64_t* k_strides, const float* v, const int64_t* v_strides,
                           float* vprime, void* fwd_ws, int B, int Hkv, int T, int D, float scale, float eps,
                           void* stream) {
-  g_last_error.clear();
-  if (int rc = check_dims(B, Hkv, Hkv, T, D)) return rc;
-  if (padded_dim(D) != kF32D) return fail("fp32 inputs are supported at head_dim <= 64, got " + std::to_string(D));
-  if (int rc = check_tensor("k", k, k_strides)) return rc;
-  if (int rc = check_tensor("v", v, v_strides)) return rc;
-  if (!vprime || !fwd_ws) return fail("vprime and fwd_ws must be non-null");
-  if (int rc = check_ws("fwd_ws", fwd_ws)) return rc;
-  if (int rc = chain_check()) return rc;
-  const FwdWs w = carve_fwd(fwd_ws, B, Hkv, Hkv, T, D, true, false);
-  return launch_precond_fwd_f32(k, k_strides, v, v_strides, vprime, w, B, Hkv, T, scale, eps,
-                                (float)D, static_cast<hipStream_t>(stream));
+  return get_v_prime_f32_impl(k, k_strides, v, v_strides, vprime, fwd_ws, B, Hkv, T, D, scale, eps, (float)D, stream);
 }
 
 int lucid_precond_bwd_f32(const float* dvprime, const int64_t* dvprime_strides, const void* fwd_ws, float* dk,
                           const int64_t* dk_strides, float* dv, const int64_t* dv_strides, void* bwd_ws, int B,
                           int Hkv, int T, int D, float scale, void* stream) {
-  g_last_error.clear();
-  if (int rc = check_dims(B, Hkv, Hkv, T, D)) return rc;
-  if (padded_dim(D) != kF32D) return fail("fp32 inputs are supported at head_dim <= 64, got " + std::to_string(D));
-  if (int rc = check_tensor("dvprime", dvprime, dvprime_strides)) return rc;
-  if (int rc = check_tensor("dk", dk, dk_strides)) return rc;
-  if (int rc = check_tensor("dv", dv, dv_strides)) return rc;
-  if (!fwd_ws || !bwd_ws) return fail("fwd_ws and bwd_ws must be non-null");
-  if (int rc = check_ws("fwd_ws", fwd_ws)) return rc;
-  if (int rc = check_ws("bwd_ws", bwd_ws)) return rc;
-  if (int rc = chain_check()) return rc;
-  const FwdWs f = carve_fwd(const_cast<void*>(fwd_ws), B, Hkv, Hkv, T, D, true, false);
-  const BwdWs w = carve_seam_bwd(bwd_ws, B, Hkv, Hkv, T, D, false);
-  return launch_precond_only_bwd_f32(dvprime, dvprime_strides, f, dk, dk_strides, dv, dv_strides, w, B, Hkv, T,
-                                     scale, (float)D, static_cast<hipStream_t>(stream));
+  return precond_bwd_f32_impl(dvprime, dvprime_strides, fwd_ws, dk, dk_strides, dv, dv_strides, bwd_ws, B, Hkv, T, D,
+                              scale, (float)D, stream);
 }
 
 size_t lucid_attn_vp_fwd_f32_workspace_bytes(int B, int Hq, int Hkv, int T, int D) {
@@ -1176,24 +1276,8 @@ int lucid_precond_bwd(const void* k, const int64_t* k_strides, const void* dvpri
                       int dvprime_f32, const void* fwd_ws, void* dk, const int64_t* dk_strides, void* dv,
                       const int64_t* dv_strides, void* bwd_ws, int B, int Hkv, int T, int D, float scale,
                       void* stream) {
-  g_last_error.clear();
-  if (int rc = check_dims(B, Hkv, Hkv, T, D)) return rc;
-  if (int rc = check_tensor("k", k, k_strides)) return rc;
-  if (int rc = check_tensor("dvprime", dvprime, dvprime_strides)) return rc;
-  if (int rc = check_tensor("dk", dk, dk_strides)) return rc;
-  if (int rc = check_tensor("dv", dv, dv_strides)) return rc;
-  if (!fwd_ws || !bwd_ws) return fail("fwd_ws and bwd_ws must be non-null");
-  if (int rc = check_ws("fwd_ws", fwd_ws)) return rc;
-  if (int rc = check_ws("bwd_ws", bwd_ws)) return rc;
-  if (int rc = chain_check()) return rc;
-  const FwdWs f = carve_fwd(const_cast<void*>(fwd_ws), B, Hkv, Hkv, T, D);
-  const BwdWs w = carve_seam_bwd(bwd_ws, B, Hkv, Hkv, T, D, false);
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  if (padded_dim(D) == 64)
-    return launch_precond_only_bwd<64>(k, k_strides, dvprime, dvprime_strides, dvprime_f32, f, dk, dk_strides, dv,
-                                       dv_strides, w, B, Hkv, T, scale, (float)D, st);
-  return launch_precond_only_bwd<128>(k, k_strides, dvprime, dvprime_strides, dvprime_f32, f, dk, dk_strides, dv,
-                                      dv_strides, w, B, Hkv, T, scale, (float)D, st);
+  return precond_bwd_impl(k, k_strides, dvprime, dvprime_strides, dvprime_f32, fwd_ws, dk, dk_strides, dv, dv_strides,
+                          bwd_ws, B, Hkv, T, D, scale, (float)D, stream);
 }
 
 void lucid_profile_enable(int on) { lucid_prof::enabled() = on != 0; }

@@ -23,17 +23,19 @@ namespace lucid {
 
 constexpr float DEC_NEG = -1e30f;  // finite "minus infinity" for empty softmax states
 
-// Tokens of one pass: the L (G + 1) columns of a 32-column score tile.
+// Tokens of one pass: the L (G + 1) columns of a 32-column score tile.  G = 0 is the
+// generic instance (the group size Gs a runtime argument, 3 <= Gs <= 31): its per-token
+// arrays hold the 8 tokens of its smallest group.
 template <int G>
 constexpr int decode_tokens_per_pass() {
-  return 32 / (G + 1);
+  return G > 0 ? 32 / (G + 1) : 8;
 }
 
 struct DecodePartials {
   float* a;  // [nsplit][BH][L][D]     sum_j P_tj v'_j over the split's cached rows
-  float* m;  // [nsplit][BH][L*G]      running max (log2 domain), column t*G + g
-  float* l;  // [nsplit][BH][L*G]      running sum
-  float* o;  // [nsplit][BH][L*G][D]   unnormalised output
+  float* m;  // [nsplit][BH][L*Gs]     running max (log2 domain), column t*Gs + g
+  float* l;  // [nsplit][BH][L*Gs]     running sum
+  float* o;  // [nsplit][BH][L*Gs][D]  unnormalised output
 };
 
 // Split pass on the matrix cores.  Each wave sweeps its own 32-key tiles of the split
@@ -46,6 +48,9 @@ struct DecodePartials {
 // (V' rows staged per wave into LDS by direct loads and read transposed) accumulates the
 // outputs and, in the key columns, sum_j P_tj v'_j.  Keys reach registers one tile ahead;
 // no barrier in the sweep.  Every new token sees every cached row (all are earlier).
+// The columns hold the Gs query heads g0 .. g0+Gs-1 of the kv head's Gt (query head
+// h Gt + g0 + i); G > 0 fixes Gs = G at compile time, G = 0 takes Gs at run time.  A key
+// column's partials do not depend on the other columns of the tile.
 template <int D, int G>
 struct DecodeMfmaSmem {
   union {
@@ -62,16 +67,17 @@ template <int D, int G>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void lucid_decode_split_kernel(
     const bf16* __restrict__ q, Strides qs, const bf16* __restrict__ kn, Strides kns,
     const bf16* __restrict__ kc, Strides kcs, const bf16* __restrict__ vc, Strides vcs, int Hkv, int Tp, int KS,
-    int L, float scale, float eps, float dn, DecodePartials part) {
+    int L, float scale, float eps, float dn, DecodePartials part, int Gs, int Gt, int g0) {
   constexpr int NKS = D / 16, NDT = D / 32, CPR = D / 8, NST = 32 * CPR / 64;  // NST: staging loads per tile
   static_assert(G + 1 <= 32, "query heads + the preconditioner row must fit one 32-column tile");
+  const int GG = G > 0 ? G : Gs;  // query columns per token (GG + 1 <= 32, checked by the host)
   __shared__ __attribute__((aligned(16))) DecodeMfmaSmem<D, G> sm;
   const int s = blockIdx.x, bh = blockIdx.y, BH = gridDim.y;
   const int b = bh / Hkv, h = bh - b * Hkv;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
   const int col = l32;  // score / output column of this lane
-  const int tok = col / (G + 1), hi = col - tok * (G + 1);
-  const bool valid = tok < L, isq = valid && hi < G, isk = valid && hi == G;
+  const int tok = col / (GG + 1), hi = col - tok * (GG + 1);
+  const bool valid = tok < L, isq = valid && hi < GG, isk = valid && hi == GG;
   const int j0 = s * KS, j1 = min(Tp, j0 + KS);
 
   // B operand: column col of X^T (k = d), zero for the padding columns
@@ -81,7 +87,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void l
   for (int st = 0; st < NKS; ++st) {
     bf16x8 x;
     if (isq) {
-      x = ld8(q + b * qs.b + (h * G + hi) * qs.h + (int64_t)tok * qs.t + 16 * st + 8 * g);
+      x = ld8(q + b * qs.b + (h * Gt + g0 + hi) * qs.h + (int64_t)tok * qs.t + 16 * st + 8 * g);
     } else if (isk) {
       x = ld8(kn + b * kns.b + h * kns.h + (int64_t)tok * kns.t + 16 * st + 8 * g);
 #pragma unroll
@@ -202,12 +208,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void l
   if (tid < D) {
     const int d = tid;
     for (int t = 0; t < L; ++t) {
-      const int ck = t * (G + 1) + G;
+      const int ck = t * (GG + 1) + GG;
       part.a[(((int64_t)s * BH + bh) * L + t) * D + d] =
           sm.u.fin.so[0][ck][d] + sm.u.fin.so[1][ck][d] + sm.u.fin.so[2][ck][d] + sm.u.fin.so[3][ck][d];
-#pragma unroll
-      for (int gg = 0; gg < G; ++gg) {
-        const int cq = t * (G + 1) + gg;
+      for (int gg = 0; gg < GG; ++gg) {
+        const int cq = t * (GG + 1) + gg;
         const float mn =
             fmaxf(fmaxf(sm.u.fin.m[0][cq], sm.u.fin.m[1][cq]), fmaxf(sm.u.fin.m[2][cq], sm.u.fin.m[3][cq]));
         float lt = 0.f, ot = 0.f;
@@ -217,7 +222,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void l
           lt = fmaf(sm.u.fin.l[ww][cq], al, lt);
           ot = fmaf(sm.u.fin.so[ww][cq][d], al, ot);
         }
-        const int64_t pi = ((int64_t)s * BH + bh) * (L * G) + t * G + gg;
+        const int64_t pi = ((int64_t)s * BH + bh) * (L * GG) + t * GG + gg;
         part.o[pi * D + d] = ot;
         if (d == 0) {
           part.m[pi] = mn;
@@ -228,7 +233,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void l
   }
 }
 
-// grid (B*Hkv, G): workgroup (kv head, query head g), for the L tokens of the pass.  The
+// grid (B*Hkv, Gs): workgroup (kv head, query head g0 + g of the kv head's Gt), for the L
+// tokens of the pass (G and Gs as in the split kernel; L <= its token capacity).  The
 // 256 threads are D/4 column groups (4 columns each, 16-byte loads) x NSL = 1024/D split
 // lanes, the lanes of one group adjacent in the wave: each lane merges every NSL-th split
 // of every token at once (online rescaling; the tokens' loads interleave), then the
@@ -236,13 +242,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void l
 // order: v'_t needs v'_u of the earlier new tokens (u < t), each column only its own
 // column, so the first lane of each group solves its 4 columns of every token without a
 // barrier.  Every workgroup of a kv head computes the v'_t; the g = 0 one writes them and
-// appends (k_t, v'_t) to the caches at rows Tp + t.
+// appends (k_t, v'_t) to the caches at rows Tp + t (if write_cache: a group split into
+// chunks of query heads runs this once per chunk, and only the first writes).
 template <int D, int G>
 __global__ __launch_bounds__(256) void lucid_decode_combine_kernel(
     int nsplit, int L, const bf16* __restrict__ q, Strides qs, const bf16* __restrict__ kn, Strides kns,
     const bf16* __restrict__ vn, Strides vns, bf16* __restrict__ kc, Strides kcs, bf16* __restrict__ vc, Strides vcs,
     bf16* __restrict__ o, Strides os, float* __restrict__ vp_new, int vp_rows, int Hkv, int Tp, float scale,
-    float eps, float dn, DecodePartials part) {
+    float eps, float dn, DecodePartials part, int Gs, int Gt, int g0, int write_cache) {
   constexpr int CG = D / 4, NSL = 256 / CG;
   static_assert(NSL * CG == 256 && NSL <= 64 && (NSL & (NSL - 1)) == 0, "split lanes of a group within a wave");
   constexpr int LM = decode_tokens_per_pass<G>();
@@ -255,7 +262,8 @@ __global__ __launch_bounds__(256) void lucid_decode_combine_kernel(
   const int bh = blockIdx.x, BH = gridDim.x, g = blockIdx.y;
   const int b = bh / Hkv, h = bh - b * Hkv;
   const int tid = threadIdx.x, cg = tid / NSL, sl = tid - cg * NSL, d0 = 4 * cg;
-  const int hq = h * G + g;
+  const int GG = G > 0 ? G : Gs;
+  const int hq = h * Gt + g0 + g;
   // dot products among the new tokens: k_t . k_u and q_tg . k_u for u <= t
   for (int idx = tid; idx < L * L; idx += 256) {
     const int t = idx / L, u = idx - t * L;
@@ -287,11 +295,11 @@ __global__ __launch_bounds__(256) void lucid_decode_combine_kernel(
     ov[t] = av[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
   for (int s = sl; s < nsplit; s += NSL) {
-    const int64_t base = ((int64_t)s * BH + bh) * (L * G) + g;
+    const int64_t base = ((int64_t)s * BH + bh) * (L * GG) + g;
 #pragma unroll
     for (int t = 0; t < LM; ++t) {
       if (t < L) {
-        const int64_t i = base + t * G;
+        const int64_t i = base + t * GG;
         const float mi = part.m[i], li = part.l[i];
         const f32x4 oi = *reinterpret_cast<const f32x4*>(part.o + i * D + d0);
         const f32x4 ai = *reinterpret_cast<const f32x4*>(part.a + (((int64_t)s * BH + bh) * L + t) * D + d0);
@@ -391,7 +399,7 @@ __global__ __launch_bounds__(256) void lucid_decode_combine_kernel(
       vb[j] = (bf16)vt[j];
     }
     *reinterpret_cast<bf16x4*>(o + b * os.b + hq * os.h + (int64_t)t * os.t + d0) = ob;
-    if (g == 0) {
+    if (g == 0 && write_cache) {
       *reinterpret_cast<f32x4*>(vp_new + ((int64_t)bh * vp_rows + t) * D + d0) = vt;
       *reinterpret_cast<bf16x4*>(kc + b * kcs.b + h * kcs.h + (int64_t)(Tp + t) * kcs.t + d0) =
           *reinterpret_cast<const bf16x4*>(kn + b * kns.b + h * kns.h + (int64_t)t * kns.t + d0);

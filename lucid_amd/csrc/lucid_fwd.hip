@@ -20,7 +20,8 @@
 namespace lucid {
 
 // ---------------------------------------------------------------------------
-// prep: rinv[bh][t] = 1/sqrt(sum K^2 / dn + eps) (dn: the head dim, rows zero-padded beyond it); kt[bh][d][perm(t)] = K[t][d];
+// prep: rinv[bh][t] = 1/sqrt(sum K^2 / dn + eps) (dn: the head dim, rows zero-padded beyond it;
+// dn <= 0: keys already normalised, rinv = 1); kt[bh][d][perm(t)] = K[t][d];
 // pinv[bh][blk] = inverse of the 64x64 diagonal block of P (fp32 forward
 // substitution by wave 0); zero the chain counter and set the head's row mass
 // to mass_init (0 before lucid_mass_kernel; a forced precision sets it directly);
@@ -67,7 +68,8 @@ __global__ __launch_bounds__(256) void lucid_prep_kernel(const bf16* __restrict_
   }
   ss += __shfl_xor(ss, 1, 64);
   ss += __shfl_xor(ss, 2, 64);
-  const float ri = 1.0f / sqrtf(ss / dn + eps);
+  // dn <= 0: the keys arrive normalised (the Lucid_Tril_Solver seam takes K^ itself): r = 1
+  const float ri = dn > 0.f ? 1.0f / sqrtf(ss / dn + eps) : 1.0f;
   if (seg == 0) {
     rinv[(int64_t)bh * T + blk * 64 + row] = ri;
     rr[row] = ri;

@@ -22,6 +22,8 @@ leaves every dot product unchanged; the RMS of k_norm divides by the true d.
 """
 from __future__ import annotations
 
+import contextlib
+
 import torch
 import torch.nn.functional as F
 
@@ -205,7 +207,10 @@ _PRECISIONS = {"auto": 0, "fast": 1, "exact": 2}
 
 
 def set_precision(mode: str = "auto") -> None:
-    """Precision of the preconditioner chains for the calls that follow (process-wide).
+    """Precision of the preconditioner chains for the forward calls that follow on this thread.
+
+    The mode is per thread (other threads keep theirs); a backward uses the choice its
+    forward recorded, whatever thread it runs on.  :func:`precision` sets it for a block.
 
     ``"auto"`` (default) measures each head's row mass ``max_i sum_{j<i} P_ij^2`` (sampled)
     and runs heads above 4 -- keys along a shared direction, where the chain products
@@ -225,7 +230,8 @@ def get_precision() -> str:
 
 
 def set_fused_forward(on: bool = True) -> None:
-    """Forward kernel schedule for the calls that follow (process-wide).
+    """Forward kernel schedule for the calls that follow on this thread (per thread, like
+    :func:`set_precision`; :func:`fused_forward` sets it for a block).
 
     On (default): at head dim <= 64 with one query head per kv head the preconditioner chain
     and the causal attention of each 128-row block run in one fused kernel that feeds every
@@ -238,6 +244,28 @@ def set_fused_forward(on: bool = True) -> None:
 
 def get_fused_forward() -> bool:
     return bool(_lib.load().lucid_get_fused_forward())
+
+
+@contextlib.contextmanager
+def precision(mode: str):
+    """``with precision("exact"): ...`` -- :func:`set_precision` for the block, restored after."""
+    old = get_precision()
+    set_precision(mode)
+    try:
+        yield
+    finally:
+        set_precision(old)
+
+
+@contextlib.contextmanager
+def fused_forward(on: bool):
+    """``with fused_forward(False): ...`` -- :func:`set_fused_forward` for the block, restored after."""
+    old = get_fused_forward()
+    set_fused_forward(on)
+    try:
+        yield
+    finally:
+        set_fused_forward(old)
 
 
 def head_row_mass(ws: torch.Tensor, B: int, Hq: int, Hkv: int, T: int, D: int) -> torch.Tensor:
@@ -289,9 +317,9 @@ class GetVPrimeFunction(torch.autograd.Function):
     ``solve_triangular``; the backward uses the forward's fp32 solve state."""
 
     @staticmethod
-    def forward(ctx, key, value, scale, eps, dn):
+    def forward(ctx, key, value, scale, eps, dn, knorm=True):
         B, Hkv, T, D = key.shape
-        ctx.shape, ctx.t = key.shape, T
+        ctx.shape, ctx.t, ctx.knorm = key.shape, T, knorm
         if T == 0 or key.numel() == 0:
             ctx.empty = True
             return value.new_empty(B, Hkv, T, D)
@@ -304,12 +332,15 @@ class GetVPrimeFunction(torch.autograd.Function):
         if ctx.f32:
             ws = torch.empty(lib.lucid_v_prime_f32_workspace_bytes(B, Hkv, tp, dn), dtype=torch.uint8,
                              device=key.device)
-            fn, name = lib.lucid_get_v_prime_f32, "lucid_get_v_prime_f32"
+            name = "lucid_get_v_prime_f32" if knorm else "lucid_tril_solve_f32"
         else:
             ws = torch.empty(lib.lucid_fwd_workspace_bytes(B, Hkv, Hkv, tp, dn), dtype=torch.uint8, device=key.device)
-            fn, name = lib.lucid_get_v_prime, "lucid_get_v_prime"
-        rc = fn(_lib.ptr(k), _lib.strides3(k, (0, 1, 2)), _lib.ptr(v), _lib.strides3(v, (0, 1, 2)),
-                _lib.ptr(vprime), _lib.ptr(ws), B, Hkv, tp, dn, scale, float(eps), _lib.stream_handle(key.device))
+            name = "lucid_get_v_prime" if knorm else "lucid_tril_solve"
+        args = [_lib.ptr(k), _lib.strides3(k, (0, 1, 2)), _lib.ptr(v), _lib.strides3(v, (0, 1, 2)),
+                _lib.ptr(vprime), _lib.ptr(ws), B, Hkv, tp, dn, scale]
+        if knorm:  # k_norm's epsilon (the solver seam takes normalised keys)
+            args.append(float(eps))
+        rc = getattr(lib, name)(*args, _lib.stream_handle(key.device))
         _lib.check(lib, rc, name)
         ctx.save_for_backward(k, ws)
         ctx.scale, ctx.dn = scale, dn
@@ -318,7 +349,7 @@ class GetVPrimeFunction(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dvp):
         if ctx.empty:
-            return dvp.new_zeros(ctx.shape), dvp.new_zeros(ctx.shape), None, None, None
+            return dvp.new_zeros(ctx.shape), dvp.new_zeros(ctx.shape), None, None, None, None
         k, ws = ctx.saved_tensors
         lib = _lib.load()
         B, Hkv, tp, D = k.shape
@@ -328,23 +359,25 @@ class GetVPrimeFunction(torch.autograd.Function):
             dvp = _prep(dvp.float(), tp)
             dk = torch.empty(B, Hkv, tp, D, dtype=torch.float32, device=k.device)
             dv = torch.empty_like(dk)
-            rc = lib.lucid_precond_bwd_f32(_lib.ptr(dvp), _lib.strides3(dvp, (0, 1, 2)), _lib.ptr(ws), _lib.ptr(dk),
-                                           _lib.strides3(dk, (0, 1, 2)), _lib.ptr(dv), _lib.strides3(dv, (0, 1, 2)),
-                                           _lib.ptr(bws), B, Hkv, tp, dn, ctx.scale, _lib.stream_handle(k.device))
-            _lib.check(lib, rc, "lucid_precond_bwd_f32")
-            return dk[:, :, :t], dv[:, :, :t], None, None, None
+            name = "lucid_precond_bwd_f32" if ctx.knorm else "lucid_tril_solve_bwd_f32"
+            rc = getattr(lib, name)(_lib.ptr(dvp), _lib.strides3(dvp, (0, 1, 2)), _lib.ptr(ws), _lib.ptr(dk),
+                                    _lib.strides3(dk, (0, 1, 2)), _lib.ptr(dv), _lib.strides3(dv, (0, 1, 2)),
+                                    _lib.ptr(bws), B, Hkv, tp, dn, ctx.scale, _lib.stream_handle(k.device))
+            _lib.check(lib, rc, name)
+            return dk[:, :, :t], dv[:, :, :t], None, None, None, None
         f32 = dvp.dtype == torch.float32
         if not f32 and dvp.dtype != torch.bfloat16:
             dvp = dvp.to(torch.bfloat16)
         dvp = _prep(dvp, tp)
         dk = torch.empty(B, Hkv, tp, D, dtype=torch.bfloat16, device=k.device)
         dv = torch.empty_like(dk)
-        rc = lib.lucid_precond_bwd(_lib.ptr(k), _lib.strides3(k, (0, 1, 2)), _lib.ptr(dvp), _lib.strides3(dvp, (0, 1, 2)),
-                                   int(f32), _lib.ptr(ws), _lib.ptr(dk), _lib.strides3(dk, (0, 1, 2)), _lib.ptr(dv),
-                                   _lib.strides3(dv, (0, 1, 2)), _lib.ptr(bws), B, Hkv, tp, dn, ctx.scale,
-                                   _lib.stream_handle(k.device))
-        _lib.check(lib, rc, "lucid_precond_bwd")
-        return dk[:, :, :t], dv[:, :, :t], None, None, None
+        name = "lucid_precond_bwd" if ctx.knorm else "lucid_tril_solve_bwd"
+        rc = getattr(lib, name)(_lib.ptr(k), _lib.strides3(k, (0, 1, 2)), _lib.ptr(dvp), _lib.strides3(dvp, (0, 1, 2)),
+                                int(f32), _lib.ptr(ws), _lib.ptr(dk), _lib.strides3(dk, (0, 1, 2)), _lib.ptr(dv),
+                                _lib.strides3(dv, (0, 1, 2)), _lib.ptr(bws), B, Hkv, tp, dn, ctx.scale,
+                                _lib.stream_handle(k.device))
+        _lib.check(lib, rc, name)
+        return dk[:, :, :t], dv[:, :, :t], None, None, None, None
 
 
 class AttentionOnVPrimeFunction(torch.autograd.Function):
@@ -456,6 +489,34 @@ def get_v_prime(key, value, scaling=None, attention_mask=None, eps=1e-5):
     dp = _padded_dim(d)
     vprime = GetVPrimeFunction.apply(_pad_d(key, dp), _pad_d(value, dp), scale, eps, d)
     return vprime if dp == d else vprime[..., :d]
+
+
+class Lucid_Tril_Solver:  # noqa: N801  (the reference's class name)
+    """Drop-in for ``Lucid_Tril_Solver`` (modeling_lucid.py:284-382): ``Lucid_Tril_Solver.apply(key,
+    value, scaling, BS=2**14)`` solves ``P V' = V`` for keys that are already normalised
+    (``key`` is K^: the reference's get_v_prime applies k_norm before calling it, :562-565), with
+    ``P_ij = exp(scaling K^_i . K^_j - 1/scaling)`` for j <= i.  Differentiable w.r.t. ``key``
+    and ``value``; the gradient is the reference backward's ``(grad_k, grad_v, None, None)``:
+    ``dV = P^-T dV'``, ``dK^ = -scaling (M K^ + M^T K^)``, ``M = tril((dV V'^T) * P)`` (no
+    RMSNorm backward).  C ``lucid_tril_solve`` / ``lucid_tril_solve_bwd`` (``_f32`` for fp32).
+
+    ``BS`` is the reference's block size; as there, ``T`` must exceed it and be a multiple of it
+    (``AssertionError`` otherwise, :287-288).  The solve itself is the library's chained
+    blockwise one, so the result does not depend on ``BS``; ``value`` is left unmodified (the
+    reference subtracts from its rows in place, :296-299).  Layouts ``[B, Hkv, T, d]``, bf16
+    with d <= 128 or fp32 with d <= 64; V' comes back in ``value``'s dtype.
+    """
+
+    @staticmethod
+    def apply(key, value, scaling, BS=2 ** 14):
+        L = key.shape[-2]
+        assert L > BS, f"Sequence length {L} must be greater than block size {BS}."
+        assert L % BS == 0, f"Sequence length {L} must be divisible by block size {BS}."
+        _check_inputs(None, key, value, f32_ok=True)
+        d = key.shape[-1]
+        dp = _padded_dim(d)
+        vprime = GetVPrimeFunction.apply(_pad_d(key, dp), _pad_d(value, dp), float(scaling), 0.0, d, False)
+        return vprime if dp == d else vprime[..., :d]
 
 
 def eager_lucid_attention_forward(query, key, v_prime, scaling=None, attention_mask=None, eps=1e-5, **kwargs):

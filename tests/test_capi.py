@@ -45,7 +45,7 @@ def test_every_declared_symbol_is_exported(built, header):
 def test_abi_version_and_workspace(built):
     from lucid_amd import _lib
     lib = _lib.load()
-    assert lib.lucid_abi_version() == 5
+    assert lib.lucid_abi_version() == 6
     ws = lib.lucid_fwd_workspace_bytes(1, 16, 16, 32768, 64)
     # rinv + K^T + K^ (bf16) + V' (bf16) + V'^T + diagonal inverses + -(X_B P_BA) per 128-row
     # block + lo parts of V' and V'^T + row masses + lo part of O + counters, each 256-byte aligned
@@ -143,3 +143,43 @@ def test_product_path_fails_loudly_without_gpu_tensors():
     q = torch.zeros(1, 1, 128, 64, dtype=torch.bfloat16)
     with pytest.raises(RuntimeError, match="GPU tensor"):
         lucid_attention(q, q, q)
+
+
+def test_tril_solver_asserts_like_the_reference():
+    """Lucid_Tril_Solver.forward asserts T > BS and T % BS == 0 (modeling_lucid.py:287-288)
+    before anything else, so these raise on the CPU as in the reference."""
+    import torch
+    from lucid_amd.lucid import Lucid_Tril_Solver
+    k = torch.zeros(1, 1, 4096, 64, dtype=torch.bfloat16)
+    with pytest.raises(AssertionError, match="greater than block size"):
+        Lucid_Tril_Solver.apply(k, k, 0.125)  # default BS = 2**14
+    with pytest.raises(AssertionError, match="divisible by block size"):
+        Lucid_Tril_Solver.apply(k, k, 0.125, 3000)
+    with pytest.raises(RuntimeError, match="GPU tensor"):
+        Lucid_Tril_Solver.apply(k, k, 0.125, 1024)
+
+
+def test_only_the_declared_entry_points_are_exported(built):
+    """Each library exports the extern "C" entry points its header declares and no internal host
+    helper: chain_guard (the bounded-wait flag and its per-device set-up) and lucid_prof (event
+    records) stay hidden, so two libraries in one process, loaded RTLD_GLOBAL or linked, never
+    bind each other's copies or their static state.  What else is visible is the HIP kernel
+    handles (namespace lucid, names distinct between the two libraries), libstdc++'s own template
+    instances (namespace std, stateless) and HIP's module marker."""
+    import subprocess
+    from lucid_amd import _lib
+    kernels = {}
+    for header in HEADERS:
+        libname = LIB_FOR_HEADER[os.path.basename(header)]
+        out = subprocess.run(["nm", "-D", "--defined-only", _lib.lib_path(libname)], capture_output=True,
+                             text=True, check=True).stdout
+        names = {ln.split()[-1] for ln in out.splitlines() if len(ln.split()) == 3}
+        plain = sorted(n for n in names if not n.startswith("_Z") and not n.startswith("__hip_cuid_"))
+        assert plain == _declared(header), f"{libname}: {set(plain) ^ set(_declared(header))}"
+        mangled = {n for n in names if n.startswith("_Z")}
+        stray = sorted(n for n in mangled if not n.startswith(("_ZN5lucid", "_ZNSt", "_ZSt")))
+        assert not stray, f"{libname} exports internal helpers {stray}"
+        assert not any("11chain_guard" in n or "10lucid_prof" in n for n in names)
+        kernels[libname] = {n for n in mangled if n.startswith("_ZN5lucid")}
+    a, b = kernels.values()
+    assert not (a & b), f"kernel handles exported by both libraries: {sorted(a & b)}"

@@ -101,6 +101,13 @@ def test_decode_rejects_full_cache():
     (1, 8, 1, 1000, 7, 128),   # G = 8: 3 tokens per pass
     (1, 4, 2, 0, 9, 64),       # empty cache: the first pass has no split partials
     (1, 2, 1, 77, 5, 68),      # a padded head dim
+    # groupings without their own instance: the generic one (group size at run time)
+    (1, 6, 2, 200, 10, 64),    # G = 3: 8 tokens per pass
+    (1, 12, 2, 65, 5, 128),    # G = 6: 4 tokens per pass
+    (2, 12, 1, 300, 4, 64),    # G = 12: 2 tokens per pass
+    (1, 40, 1, 129, 3, 64),    # G = 40: two chunks of 20 query heads, 1 token per pass
+    (2, 64, 2, 70, 2, 68),     # G = 32 (multi-query with 32 heads per kv head): chunks of 16
+    (1, 33, 1, 90, 2, 64),     # G = 33: chunks of 17 and 16 with the passes of the larger
 ])
 def test_decode_several_tokens_in_one_call(B, Hq, Hkv, T0, n, D):
     """n new tokens in one call (get_new_v_prime with L_k = n): every decoded O and V' row
