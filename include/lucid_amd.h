@@ -13,7 +13,7 @@
  * LUCID_EINVAL for a rejected argument (text in lucid_last_error()), or
  * LUCID_EHIP + hipError_t for a HIP launch failure.
  *
- * Supported: head_dim D in [1, 128] (fp32 entry points: [1, 64]); T a multiple of
+ * Supported: head_dim D in [1, 128] (bf16 and fp32 entry points); T a multiple of
  * 128 (the Python layer zero-pads the sequence end, which leaves every real row
  * unchanged because both P and the attention mask are causal); Hq a multiple of
  * Hkv (GQA).  Head dims other than 64 and 128 (the reference model's is 68,
@@ -131,7 +131,7 @@ int lucid_attn_bwd(const void* dout, const int64_t* do_strides, const void* q, c
                    const int64_t* dk_strides, void* dv, const int64_t* dv_strides, void* bwd_ws, int B, int Hq,
                    int Hkv, int T, int D, float scale, float eps, void* stream);
 
-/* ---- fp32 inputs (head dim 64) ----
+/* ---- fp32 inputs (head dims up to 128) ----
  * The reference computes in the dtype of its inputs (modeling_lucid.py:461-496, :284-382 run
  * on whatever q/k/v hold); these are lucid_attn_fwd / lucid_attn_bwd for fp32 tensors, with
  * fp32 outputs (o, dq, dk, dv) and the same layouts and strides.  Q, K and dO are carried as
@@ -151,7 +151,7 @@ int lucid_attn_bwd_f32(const float* dout, const int64_t* do_strides, const float
                        int Hkv, int T, int D, float scale, void* stream);
 
 /* The two seams below (get_v_prime and eager_lucid_attention_forward) on fp32 tensors, head
- * dim 64: the same contracts as lucid_get_v_prime / lucid_precond_bwd and lucid_attn_vp_fwd /
+ * dims up to 128: the same contracts as lucid_get_v_prime / lucid_precond_bwd and lucid_attn_vp_fwd /
  * lucid_attn_vp_bwd, with fp32 inputs (v_prime included) and fp32 outputs.  Workspaces:
  * lucid_v_prime_f32_workspace_bytes for lucid_get_v_prime_f32 (kept until
  * lucid_precond_bwd_f32, whose own workspace is lucid_precond_bwd_workspace_bytes), and the

@@ -92,11 +92,12 @@ __global__ __launch_bounds__(256) void lucid_bwd_prep_kernel(const bf16* __restr
 // ---------------------------------------------------------------------------
 template <int D, bool F32 = false>
 struct DkdvSmem {
-  bf16 q[3][64 * D];   // swizzled tiles (chunk c of row r at c ^ (r & 7))
-  bf16 dO[3][64 * D];
-  bf16 ql[F32 ? 3 : 1][F32 ? 64 * D : 8];   // lo tiles (fp32 inputs)
-  bf16 dOl[F32 ? 3 : 1][F32 ? 64 * D : 8];
-  bf16 seed[3][64][16];  // per row: the seed operands of -lse2 / c and -delta (seeds)
+  static constexpr int NB = stage_bufs(D, F32);
+  bf16 q[NB][64 * D];   // swizzled tiles (chunk c of row r at c ^ (r & 7))
+  bf16 dO[NB][64 * D];
+  bf16 ql[F32 ? NB : 1][F32 ? 64 * D : 8];   // lo tiles (fp32 inputs)
+  bf16 dOl[F32 ? NB : 1][F32 ? 64 * D : 8];
+  bf16 seed[NB][64][16];  // per row: the seed operands of -lse2 / c and -delta (seeds)
 };
 
 // F32 (fp32 inputs, head dim 64): the lo tiles of Q and dO are staged beside the hi tiles,
@@ -107,12 +108,13 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
     const bf16* __restrict__ q, Strides qs, const bf16* __restrict__ k, Strides ks, const bf16* __restrict__ vpb,
     const bf16* __restrict__ dout, Strides dos, const bf16* __restrict__ seeds, float* __restrict__ dvp, float* __restrict__ dka, int Hq, int Hkv, int T, int BH, float scale, Lo lo,
     const bf16* __restrict__ vpbl) {
-  static_assert(!F32 || D == 64, "fp32 inputs: head dim 64");
+  static_assert(!F32 || D == 64 || D == 128, "fp32 inputs: head dim 64 or 128");
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
   // newest vector-memory ops of a step, per wave
   constexpr int STAGE_OPS = (F32 ? 4 : 2) * (64 * (D / 8) / 256);
   __shared__ __attribute__((aligned(16))) DkdvSmem<D, F32> sm;
+  constexpr int NB = stage_bufs(D, F32);
   const int id = blockIdx.x;
   const int jb = id / BH, bh = id - (id / BH) * BH;
   const int b = bh / Hkv, h = bh - b * Hkv;
@@ -153,7 +155,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
   dma_plan<64, D / 8, 256, SW>(qs.t, plan_q);
   dma_plan<64, D / 8, 256, SW>(dos.t, plan_o);
   auto stage = [&](int s) {
-    const int gi = s / ntile, it = it_first + s - gi * ntile, buf = s % 3;
+    const int gi = s / ntile, it = it_first + s - gi * ntile, buf = s % NB;
     const int hq = h * G + gi, bhq = b * Hq + hq, i0 = it * 64;
     if (w < 2) dma_1k(seeds + ((int64_t)bhq * T + i0 + 32 * w) * 16, &sm.seed[buf][32 * w][0]);  // 2 KB of seed rows
     dma_stage<64, D / 8>(plan_q, q + b * qs.b + hq * qs.h + (int64_t)i0 * qs.t, sm.q[buf]);
@@ -164,7 +166,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
     }
   };
   stage(0);
-  if (nsteps > 1) {
+  if (NB == 3 && nsteps > 1) {
     stage(1);
     dma_wait_but<STAGE_OPS>();
   } else {
@@ -266,20 +268,22 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
       }
     }
   };
-  // step s works on buffer s % 3: the loop is unrolled by three so that it is a constant
+  // step s works on buffer s % NB: the loop is unrolled by NB so that it is a constant
   auto step = [&](auto bufc, const int s) __attribute__((always_inline)) {
-    if (s + 2 < nsteps) stage(s + 2);
+    if (s + NB - 1 < nsteps) stage(s + NB - 1);
     const int it = it_first + s % ntile;
     if (it > it_w) tile(bufc, false);
     else if (it == it_w) tile(bufc, true);
-    if (s + 2 < nsteps) dma_wait_but<STAGE_OPS>();  // the step after next may stay in flight
+    if (NB == 3 && s + 2 < nsteps) dma_wait_but<STAGE_OPS>();  // the step after next may stay in flight
     else dma_wait();
     __syncthreads();
   };
-  for (int s = 0; s < nsteps; s += 3) {
+  for (int s = 0; s < nsteps; s += NB) {
     step(std::integral_constant<int, 0>{}, s);
     if (s + 1 < nsteps) step(std::integral_constant<int, 1>{}, s + 1);
-    if (s + 2 < nsteps) step(std::integral_constant<int, 2>{}, s + 2);
+    if constexpr (NB == 3) {
+      if (s + 2 < nsteps) step(std::integral_constant<int, 2>{}, s + 2);
+    }
   }
   float* ov = dvp + ((int64_t)bh * T + jrow) * D;
   float* ok = dka + ((int64_t)bh * T + jrow) * D;
@@ -321,10 +325,11 @@ struct DqSmem {
 };
 template <int D>
 struct DqSmemF32 {  // fp32 inputs: the lo tiles of K and V' beside the hi tiles
-  bf16 k[3][64 * D];
-  bf16 v[3][64 * D];
-  bf16 kl[3][64 * D];
-  bf16 vl[3][64 * D];
+  static constexpr int NB = stage_bufs(D, true);
+  bf16 k[NB][64 * D];
+  bf16 v[NB][64 * D];
+  bf16 kl[NB][64 * D];
+  bf16 vl[NB][64 * D];
 };
 
 template <int D, bool EXACT, bool F32 = false, int RW = 64>
@@ -334,13 +339,14 @@ __global__ __launch_bounds__(16384 / RW) LUCID_TWO_WAVES_IF((D == 64 || RW == 32
     const float* __restrict__ delta, const float* __restrict__ mass,
     std::conditional_t<F32, float, bf16>* __restrict__ dq, Strides dqs, int Hq, int Hkv, int T, int BHq,
     float scale, Lo lo, const bf16* __restrict__ vpbl) {
-  static_assert(!F32 || (EXACT && D == 64 && RW == 64), "fp32 inputs: exact instance, head dim 64");
+  static_assert(!F32 || EXACT, "fp32 inputs: exact instance");
   static_assert(RW == 64 || RW == 32, "rows per wave");
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
   constexpr int NT = RW / 32;           // 32-row n-tiles per wave
   constexpr int NTHR = 64 * (256 / RW);  // 256 rows per workgroup
   __shared__ __attribute__((aligned(16))) std::conditional_t<F32, DqSmemF32<D>, DqSmem<D>> sm;
+  constexpr int NB = stage_bufs(D, F32);
   const int nblk = (T + 255) / 256;
   const int id = blockIdx.x;
   const int bhq = id % BHq;
@@ -389,7 +395,7 @@ __global__ __launch_bounds__(16384 / RW) LUCID_TWO_WAVES_IF((D == 64 || RW == 32
   dma_plan<64, D / 8, NTHR>(ks.t, plan_k);
   dma_plan<64, D / 8, NTHR>(D, plan_v);
   auto stage = [&](int jt) {
-    const int j0 = jt * 64, buf = jt % 3;
+    const int j0 = jt * 64, buf = jt % NB;
     dma_stage<64, D / 8, NTHR>(plan_k, kh + (int64_t)j0 * ks.t, sm.k[buf]);
     dma_stage<64, D / 8, NTHR>(plan_v, vh + (int64_t)j0 * D, sm.v[buf]);
     if constexpr (F32) {
@@ -398,7 +404,7 @@ __global__ __launch_bounds__(16384 / RW) LUCID_TWO_WAVES_IF((D == 64 || RW == 32
     }
   };
   stage(0);
-  if (ntile > 1) {
+  if (NB == 3 && ntile > 1) {
     stage(1);
     dma_wait_but<STAGE_OPS>();
   } else {
@@ -497,17 +503,18 @@ __global__ __launch_bounds__(16384 / RW) LUCID_TWO_WAVES_IF((D == 64 || RW == 32
   };
   if constexpr (EXACT) {  // the exact instances keep the rolled loop (registers)
     for (int jt = 0; jt < ntile; ++jt) {
-      const int buf = jt % 3;
-      if (jt + 2 < ntile) stage(jt + 2);
+      const int buf = jt % NB;
+      if (jt + NB - 1 < ntile) stage(jt + NB - 1);
       if (row0 < T) {
         if (jt < last_w) tile(buf, false);
         else if (jt == last_w) tile(buf, true);
       }
-      if (jt + 2 < ntile) dma_wait_but<STAGE_OPS>();
+      if (NB == 3 && jt + 2 < ntile) dma_wait_but<STAGE_OPS>();
       else dma_wait();
       __syncthreads();
     }
   } else {
+    static_assert(EXACT || NB == 3, "the bf16 instances stage three deep");
     for (int jt = 0; jt < ntile; jt += 3) {
       step(std::integral_constant<int, 0>{}, jt);
       if (jt + 1 < ntile) step(std::integral_constant<int, 1>{}, jt + 1);
@@ -590,13 +597,14 @@ struct PcolSmem<D, false, false> {
 };
 template <int D, bool F32>
 struct PcolSmem<D, true, F32> {
+  static constexpr int NB = stage_bufs(D, F32);
   union {
     struct {
-      bf16 k[3][64 * D];
-      bf16 dv[3][64 * D];
-      bf16 dvl[3][64 * D];  // lo part of dV
-      bf16 kl[F32 ? 3 : 1][F32 ? 64 * D : 8];  // lo part of K (fp32 inputs)
-      float r[3][64];
+      bf16 k[NB][64 * D];
+      bf16 dv[NB][64 * D];
+      bf16 dvl[NB][64 * D];  // lo part of dV
+      bf16 kl[F32 ? NB : 1][F32 ? 64 * D : 8];  // lo part of K (fp32 inputs)
+      float r[NB][64];
     } st;
     struct {
       float Rt[D][132];
@@ -615,10 +623,11 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
     const float* __restrict__ dvp,
     bf16* __restrict__ dvb, bf16* __restrict__ dvbl, std::conditional_t<F32, float, bf16>* __restrict__ dv_out,
     Strides dvs, float* __restrict__ colsum, int* __restrict__ counters, Lo lo) {
-  static_assert(!F32 || (EXACT && D == 64), "fp32 inputs: exact instance, head dim 64");
+  static_assert(!F32 || EXACT, "fp32 inputs: exact instance");
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
   __shared__ __attribute__((aligned(16))) PcolSmem<D, EXACT, F32> sm;
+  constexpr int NB = stage_bufs(D, F32);
 
   const int NT = T / 64, NP = T / 128;
   const int id = blockIdx.x;
@@ -676,7 +685,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
   // ---- sweep over the later 64-row tiles, far (published first) to near ----
   const int first = NT - 1, last = 2 * p + 2;  // tiles first, first-1, ..., last
   int ready = 0;
-  // step k of the sweep stages tile first - k into buffer k % 3; the newest
+  // step k of the sweep stages tile first - k into buffer k % NB; the newest
   // STAGE_OPS vector memory operations of a wave are the tiles of a step
   constexpr int STAGE_OPS = (F32 ? 4 : EXACT ? 3 : 2) * (64 * (D / 8) / 256);
   const int nsteps = first - last + 1;
@@ -684,7 +693,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
   dma_plan<64, D / 8>(ks.t, plan_k);
   dma_plan<64, D / 8>(D, plan_d);
   auto stage = [&](int k) {
-    const int i0 = (first - k) * 64, buf = k % 3;
+    const int i0 = (first - k) * 64, buf = k % NB;
     if constexpr (EXACT) {
       if (w == 0) dma_f32x64(rv + i0, sm.u.st.r[buf]);
       dma_stage<64, D / 8>(plan_k, kh + (int64_t)i0 * ks.t, sm.u.st.k[buf]);
@@ -739,7 +748,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
     ready = wait_counter_gt(cnt, NT - 1 - first);
     stage(0);
     issued = 1;
-    try_issue(1);
+    if (NB == 3) try_issue(1);
     if (issued > 1) dma_wait_but<STAGE_OPS>();
     else dma_wait();
   } else {
@@ -823,8 +832,8 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
   // all steps but the last; the last one is peeled so that the inverses it
   // prefetches do not hold registers through the loop
   for (int ks_ = 0; ks_ + 1 < nsteps; ++ks_) {
-    try_issue(ks_ + 2);
-    sweep_tile(ks_ % 3);
+    try_issue(ks_ + NB - 1);
+    sweep_tile(ks_ % NB);
     if (issued == ks_ + 1) {  // the next tile was not published yet: wait for it
       ready = wait_counter_gt(cnt, NT - 1 - (first - issued));
       stage(issued);
@@ -836,7 +845,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
   }
   if (nsteps > 0) {
     xload();  // fetch the inverses while the last tile is processed
-    sweep_tile((nsteps - 1) % 3);
+    sweep_tile((nsteps - 1) % NB);
     dma_wait();
     __syncthreads();
   }
@@ -1326,11 +1335,12 @@ struct ProwSmem {
 };
 template <int D, bool F32>
 struct ProwSmem<D, true, F32> {
-  bf16 k[3][64 * D];
-  bf16 v[3][64 * D];
-  bf16 vl[3][64 * D];  // lo part of V'
-  bf16 kl[F32 ? 3 : 1][F32 ? 64 * D : 8];  // lo part of K (fp32 inputs)
-  float r[3][64];
+  static constexpr int NB = stage_bufs(D, F32);
+  bf16 k[NB][64 * D];
+  bf16 v[NB][64 * D];
+  bf16 vl[NB][64 * D];  // lo part of V'
+  bf16 kl[F32 ? NB : 1][F32 ? 64 * D : 8];  // lo part of K (fp32 inputs)
+  float r[NB][64];
 };
 
 template <int D, bool EXACT, bool F32 = false>
@@ -1340,10 +1350,11 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
     const bf16* __restrict__ vpbl, const bf16* __restrict__ dvb,
     const bf16* __restrict__ dvbl, const float* __restrict__ mass, const float* __restrict__ colsum,
     const float* __restrict__ dka, std::conditional_t<F32, float, bf16>* __restrict__ dk_out, Strides dks, Lo lo) {
-  static_assert(!F32 || (EXACT && D == 64), "fp32 inputs: exact instance, head dim 64");
+  static_assert(!F32 || EXACT, "fp32 inputs: exact instance");
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
   __shared__ __attribute__((aligned(16))) ProwSmem<D, EXACT, F32> sm;
+  constexpr int NB = stage_bufs(D, F32);
   const int nblk = (T + 255) / 256;
   const int id = blockIdx.x;
   const int ib = nblk - 1 - id / BH, bh = id - (id / BH) * BH;  // heavy (late) blocks first
@@ -1388,7 +1399,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
   dma_plan<64, D / 8>(ks.t, plan_k);
   dma_plan<64, D / 8>(D, plan_v);
   auto stage = [&](int J) {
-    const int j0 = J * 64, buf = J % 3;
+    const int j0 = J * 64, buf = J % NB;
     if constexpr (EXACT) {
       if (w == 0) dma_f32x64(rv + j0, sm.r[buf]);
       dma_stage<64, D / 8>(plan_k, kh + (int64_t)j0 * ks.t, sm.k[buf]);
@@ -1400,8 +1411,12 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
     if constexpr (F32) dma_stage<64, D / 8>(plan_k, klh + (int64_t)j0 * ks.t, sm.kl[buf]);
   };
   stage(0);
-  stage(1);
-  dma_wait_but<STAGE_OPS>();
+  if (NB == 3) {  // ntile >= 2 (T >= 128)
+    stage(1);
+    dma_wait_but<STAGE_OPS>();
+  } else {
+    dma_wait();
+  }
   __syncthreads();
   // this wave's rows are the 64-block row0 / 64; key tiles after it are fully masked
   const int last_w = row0 / 64;
@@ -1476,13 +1491,13 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
     }
   };
   for (int J = 0; J < ntile; ++J) {
-    const int buf = J % 3;
-    if (J + 2 < ntile) stage(J + 2);
+    const int buf = J % NB;
+    if (J + NB - 1 < ntile) stage(J + NB - 1);
     if (active) {
       if (J < last_w) tile(buf, false);
       else if (J == last_w) tile(buf, true);
     }
-    if (J + 2 < ntile) dma_wait_but<STAGE_OPS>();  // the step after next may stay in flight
+    if (NB == 3 && J + 2 < ntile) dma_wait_but<STAGE_OPS>();  // the step after next may stay in flight
     else dma_wait();
     __syncthreads();
   }

@@ -487,7 +487,6 @@ int launch_precond_only_bwd(const void* k, const int64_t* ks, const void* dvp, c
 // run the exact chain instances (their row mass is forced above kExactMass); outputs are
 // fp32.  The launchers mirror the bf16 ones above piece by piece.
 
-constexpr int kF32D = 64;
 constexpr float kForceExact = 1e30f;
 
 // Element strides of the contiguous [B][H][T][D] rows of a split copy.
@@ -495,28 +494,30 @@ lucid::Strides rows_strides(int H, int T, int D) {
   return lucid::Strides{(int64_t)H * T * D, (int64_t)T * D, (int64_t)D};
 }
 
+template <int D>
 int launch_split(const void* x, const int64_t* xs, int B, int H, int T, bf16* hi, bf16* lo, hipStream_t st,
                  const float* center = nullptr) {
-  LUCID_LAUNCH("lucid_split_kernel", lucid::lucid_split_kernel<kF32D>, dim3(T / 64, B * H), st, (const float*)x,
+  LUCID_LAUNCH("lucid_split_kernel", lucid::lucid_split_kernel<D>, dim3(T / 64, B * H), st, (const float*)x,
                S(xs), H, T, hi, lo, center);
   return LUCID_OK;
 }
 
 // The attention's keys: K - (mean key of the head) as a bf16 pair in w.kch / w.kcl.
+template <int D>
 int launch_centered_keys(const void* k, const int64_t* ks, const FwdWs& w, int B, int Hkv, int T, hipStream_t st) {
-  LUCID_LAUNCH("lucid_key_mean_kernel", lucid::lucid_key_mean_kernel<kF32D>, dim3(B * Hkv), st, (const float*)k,
+  LUCID_LAUNCH("lucid_key_mean_kernel", lucid::lucid_key_mean_kernel<D>, dim3(B * Hkv), st, (const float*)k,
                S(ks), Hkv, T, w.kmean);
-  return launch_split(k, ks, B, Hkv, T, w.kch, w.kcl, st, w.kmean);
+  return launch_split<D>(k, ks, B, Hkv, T, w.kch, w.kcl, st, w.kmean);
 }
 
 // V' = P^-1 V from fp32 K and V (K split into w.kh / w.kl).
+template <int D>
 int launch_precond_fwd_f32(const void* k, const int64_t* ks, const void* v, const int64_t* vs, float* vprime,
                            const FwdWs& w, int B, int Hkv, int T, float scale, float eps, float dn,
                            hipStream_t st) {
-  constexpr int D = kF32D;
   const int BH = B * Hkv;
   const lucid::Strides ck = rows_strides(Hkv, T, D);
-  if (int rc = launch_split(k, ks, B, Hkv, T, w.kh, w.kl, st)) return rc;
+  if (int rc = launch_split<D>(k, ks, B, Hkv, T, w.kh, w.kl, st)) return rc;
   lucid::Lo lo{};
   lo.k = w.kl;
   lo.kt = w.ktl;
@@ -534,11 +535,11 @@ int launch_precond_fwd_f32(const void* k, const int64_t* ks, const void* v, cons
 
 // O = softmax(s Q K^T, causal) V' on the split Q (split here), the centred keys and V' in
 // w.  lse is the row normaliser of the scores against the centred keys.
+template <int D>
 int launch_attn_fwd_f32(const void* q, const int64_t* qs, void* o, const int64_t* os, float* lse, const FwdWs& w,
                         int B, int Hq, int Hkv, int T, float scale, hipStream_t st) {
-  constexpr int D = kF32D;
   const int BHq = B * Hq;
-  if (int rc = launch_split(q, qs, B, Hq, T, w.qh, w.ql, st)) return rc;
+  if (int rc = launch_split<D>(q, qs, B, Hq, T, w.qh, w.ql, st)) return rc;
   lucid::Lo lo{};
   lo.q = w.ql;
   lo.k = w.kcl;
@@ -548,23 +549,25 @@ int launch_attn_fwd_f32(const void* q, const int64_t* qs, void* o, const int64_t
   return LUCID_OK;
 }
 
+template <int D>
 int launch_fwd_f32(const void* q, const int64_t* qs, const void* k, const int64_t* ks, const void* v,
                    const int64_t* vs, void* o, const int64_t* os, float* vprime, float* lse, const FwdWs& w, int B,
                    int Hq, int Hkv, int T, float scale, float eps, float dn, hipStream_t st) {
-  if (int rc = launch_precond_fwd_f32(k, ks, v, vs, vprime, w, B, Hkv, T, scale, eps, dn, st)) return rc;
-  if (int rc = launch_centered_keys(k, ks, w, B, Hkv, T, st)) return rc;
-  return launch_attn_fwd_f32(q, qs, o, os, lse, w, B, Hq, Hkv, T, scale, st);
+  if (int rc = launch_precond_fwd_f32<D>(k, ks, v, vs, vprime, w, B, Hkv, T, scale, eps, dn, st)) return rc;
+  if (int rc = launch_centered_keys<D>(k, ks, w, B, Hkv, T, st)) return rc;
+  return launch_attn_fwd_f32<D>(q, qs, o, os, lse, w, B, Hq, Hkv, T, scale, st);
 }
 
 // The attention part of the backward: delta (from fp32 dO and O), dV' and the softmax dK
 // (into w.dvp, w.dka) and dQ (fp32).  Reads the split Q, centred K and V' of the forward.
+// dQ: four waves of 64 rows at head dim 64, eight waves of 32 rows at 128.
+template <int D>
 int launch_attn_bwd_f32(const void* dout, const int64_t* dos, const void* o, const int64_t* os, const float* lse,
                         const FwdWs& f, void* dq, const int64_t* dqs, const BwdWs& w, int B, int Hq, int Hkv, int T,
                         float scale, hipStream_t st) {
-  constexpr int D = kF32D;
   const int BH = B * Hkv, BHq = B * Hq;
   const lucid::Strides cq = rows_strides(Hq, T, D), ck = rows_strides(Hkv, T, D);
-  if (int rc = launch_split(dout, dos, B, Hq, T, w.doh, w.dol, st)) return rc;
+  if (int rc = launch_split<D>(dout, dos, B, Hq, T, w.doh, w.dol, st)) return rc;
   lucid::Lo lo{};
   lo.q = f.ql;
   lo.k = f.kcl;
@@ -577,18 +580,19 @@ int launch_attn_bwd_f32(const void* dout, const int64_t* dos, const void* o, con
                lo, lse, 1.f / (scale * LOG2E_F), w.seeds);
   LUCID_LAUNCH("lucid_attn_bwd_dkdv_f32_kernel", (lucid::lucid_attn_bwd_dkdv_kernel<D, true>), dim3((T / 128) * BH),
                st, f.qh, cq, f.kch, ck, f.vpb, w.doh, cq, w.seeds, w.dvp, w.dka, Hq, Hkv, T, BH, scale, lo, f.vpbl);
-  LUCID_LAUNCH("lucid_attn_bwd_dq_f32_kernel", (lucid::lucid_attn_bwd_dq_kernel<D, true, true>),
-               dim3(((T + 255) / 256) * BHq), st, f.qh, cq, f.kch, ck, f.vpb, w.doh, cq, lse, w.delta, f.mass,
-               (float*)dq, S(dqs), Hq, Hkv, T, BHq, scale, lo, f.vpbl);
+  constexpr int RW = D == 128 ? 32 : 64;
+  LUCID_LAUNCH_B("lucid_attn_bwd_dq_f32_kernel", (lucid::lucid_attn_bwd_dq_kernel<D, true, true, RW>),
+                 dim3(((T + 255) / 256) * BHq), dim3(64 * (256 / RW)), st, f.qh, cq, f.kch, ck, f.vpb, w.doh, cq, lse,
+                 w.delta, f.mass, (float*)dq, S(dqs), Hq, Hkv, T, BHq, scale, lo, f.vpbl);
   return LUCID_OK;
 }
 
 // The preconditioner part: dV = P^-T dV' (w.dvp, counters zeroed), then dK (fp32) with the
 // softmax part dka added (null: none).
+template <int D>
 int launch_precond_bwd_f32(const FwdWs& f, void* dk, const int64_t* dks, void* dv, const int64_t* dvs,
                            const BwdWs& w, const float* dka, int B, int Hkv, int T, float scale, float dn,
                            hipStream_t st) {
-  constexpr int D = kF32D;
   const int BH = B * Hkv;
   const lucid::Strides ck = rows_strides(Hkv, T, D);
   lucid::Lo lo{};
@@ -603,36 +607,37 @@ int launch_precond_bwd_f32(const FwdWs& f, void* dk, const int64_t* dks, void* d
   return LUCID_OK;
 }
 
+template <int D>
 int launch_bwd_f32(const void* dout, const int64_t* dos, const void* o, const int64_t* os, const float* lse,
                    const FwdWs& f, void* dq, const int64_t* dqs, void* dk, const int64_t* dks, void* dv,
                    const int64_t* dvs, const BwdWs& w, int B, int Hq, int Hkv, int T, float scale, float dn,
                    hipStream_t st) {
-  if (int rc = launch_attn_bwd_f32(dout, dos, o, os, lse, f, dq, dqs, w, B, Hq, Hkv, T, scale, st)) return rc;
-  return launch_precond_bwd_f32(f, dk, dks, dv, dvs, w, w.dka, B, Hkv, T, scale, dn, st);
+  if (int rc = launch_attn_bwd_f32<D>(dout, dos, o, os, lse, f, dq, dqs, w, B, Hq, Hkv, T, scale, st)) return rc;
+  return launch_precond_bwd_f32<D>(f, dk, dks, dv, dvs, w, w.dka, B, Hkv, T, scale, dn, st);
 }
 
 // eager_lucid_attention_forward on fp32 Q, K and V': the centred keys, the V' pair and
 // layouts, then the attention (the layout pass's 1/rms, read only by the row-mass pass,
 // which the forced precision skips, comes from the centred keys).
+template <int D>
 int launch_attn_vp_fwd_f32(const void* q, const int64_t* qs, const void* k, const int64_t* ks, const void* vp,
                            const int64_t* vs, void* o, const int64_t* os, float* lse, const FwdWs& w, int B, int Hq,
                            int Hkv, int T, float eps, float scale, float dn, hipStream_t st) {
-  constexpr int D = kF32D;
   const int BH = B * Hkv;
-  if (int rc = launch_centered_keys(k, ks, w, B, Hkv, T, st)) return rc;
+  if (int rc = launch_centered_keys<D>(k, ks, w, B, Hkv, T, st)) return rc;
   LUCID_LAUNCH("lucid_vp_layout_f32_kernel", (lucid::lucid_vp_layout_kernel<D, float, true>), dim3(T / 64, BH), st,
                w.kch, rows_strides(Hkv, T, D), (const float*)vp, S(vs), Hkv, T, eps, dn, w.rinv, w.vpb, w.vpt, w.mass,
                kForceExact, w.vpbl, w.vptl);
-  return launch_attn_fwd_f32(q, qs, o, os, lse, w, B, Hq, Hkv, T, scale, st);
+  return launch_attn_fwd_f32<D>(q, qs, o, os, lse, w, B, Hq, Hkv, T, scale, st);
 }
 
+template <int D>
 int launch_attn_vp_bwd_f32(const void* dout, const int64_t* dos, const void* o, const int64_t* os, const float* lse,
                            const FwdWs& f, void* dq, const int64_t* dqs, void* dk, const int64_t* dks, void* dvp,
                            const int64_t* dvps, const BwdWs& w, int B, int Hq, int Hkv, int T, float scale,
                            hipStream_t st) {
-  constexpr int D = kF32D;
   const int BH = B * Hkv;
-  if (int rc = launch_attn_bwd_f32(dout, dos, o, os, lse, f, dq, dqs, w, B, Hq, Hkv, T, scale, st)) return rc;
+  if (int rc = launch_attn_bwd_f32<D>(dout, dos, o, os, lse, f, dq, dqs, w, B, Hq, Hkv, T, scale, st)) return rc;
   LUCID_LAUNCH("lucid_rows_out_kernel", (lucid::lucid_rows_out_kernel<D, float>), dim3(T / 64, BH), st, w.dka,
                (float*)dk, S(dks), Hkv, T, 1.f);
   LUCID_LAUNCH("lucid_rows_out_kernel", (lucid::lucid_rows_out_kernel<D, float>), dim3(T / 64, BH), st, w.dvp,
@@ -641,13 +646,13 @@ int launch_attn_vp_bwd_f32(const void* dout, const int64_t* dos, const void* o, 
 }
 
 // Gradient of get_v_prime on fp32 inputs: dV' (fp32, strided) in, fp32 dK and dV out.
+template <int D>
 int launch_precond_only_bwd_f32(const void* dvp, const int64_t* dvps, const FwdWs& f, void* dk, const int64_t* dks,
                                 void* dv, const int64_t* dvs, const BwdWs& w, int B, int Hkv, int T, float scale,
                                 float dn, hipStream_t st) {
-  constexpr int D = kF32D;
   LUCID_LAUNCH("lucid_rows_in_kernel", (lucid::lucid_rows_in_kernel<D, float>), dim3(T / 64, B * Hkv), st,
                (const float*)dvp, S(dvps), w.dvp, Hkv, T, w.counters);
-  return launch_precond_bwd_f32(f, dk, dks, dv, dvs, w, nullptr, B, Hkv, T, scale, dn, st);
+  return launch_precond_bwd_f32<D>(f, dk, dks, dv, dvs, w, nullptr, B, Hkv, T, scale, dn, st);
 }
 
 // Decoding: split the cached sequence so that one resident round of split workgroups
@@ -880,14 +885,13 @@ int get_v_prime_f32_impl(const float* k, const int64_t* k_strides, const float* 
                          void* stream) {
   g_last_error.clear();
   if (int rc = check_dims(B, Hkv, Hkv, T, D)) return rc;
-  if (padded_dim(D) != kF32D) return fail("fp32 inputs are supported at head_dim <= 64, got " + std::to_string(D));
   if (int rc = check_tensor("k", k, k_strides)) return rc;
   if (int rc = check_tensor("v", v, v_strides)) return rc;
   if (!vprime || !fwd_ws) return fail("vprime and fwd_ws must be non-null");
   if (int rc = check_ws("fwd_ws", fwd_ws)) return rc;
   if (int rc = chain_check()) return rc;
   const FwdWs w = carve_fwd(fwd_ws, B, Hkv, Hkv, T, D, true, false);
-  return launch_precond_fwd_f32(k, k_strides, v, v_strides, vprime, w, B, Hkv, T, scale, eps, dn,
+  return (padded_dim(D) == 64 ? launch_precond_fwd_f32<64> : launch_precond_fwd_f32<128>)(k, k_strides, v, v_strides, vprime, w, B, Hkv, T, scale, eps, dn,
                                 static_cast<hipStream_t>(stream));
 }
 
@@ -896,7 +900,6 @@ int precond_bwd_f32_impl(const float* dvprime, const int64_t* dvprime_strides, c
                          int T, int D, float scale, float dn, void* stream) {
   g_last_error.clear();
   if (int rc = check_dims(B, Hkv, Hkv, T, D)) return rc;
-  if (padded_dim(D) != kF32D) return fail("fp32 inputs are supported at head_dim <= 64, got " + std::to_string(D));
   if (int rc = check_tensor("dvprime", dvprime, dvprime_strides)) return rc;
   if (int rc = check_tensor("dk", dk, dk_strides)) return rc;
   if (int rc = check_tensor("dv", dv, dv_strides)) return rc;
@@ -906,7 +909,7 @@ int precond_bwd_f32_impl(const float* dvprime, const int64_t* dvprime_strides, c
   if (int rc = chain_check()) return rc;
   const FwdWs f = carve_fwd(const_cast<void*>(fwd_ws), B, Hkv, Hkv, T, D, true, false);
   const BwdWs w = carve_seam_bwd(bwd_ws, B, Hkv, Hkv, T, D, false);
-  return launch_precond_only_bwd_f32(dvprime, dvprime_strides, f, dk, dk_strides, dv, dv_strides, w, B, Hkv, T,
+  return (padded_dim(D) == 64 ? launch_precond_only_bwd_f32<64> : launch_precond_only_bwd_f32<128>)(dvprime, dvprime_strides, f, dk, dk_strides, dv, dv_strides, w, B, Hkv, T,
                                      scale, dn, static_cast<hipStream_t>(stream));
 }
 
@@ -1112,7 +1115,6 @@ int lucid_attn_fwd_f32(const float* q, const int64_t* q_strides, const float* k,
                        void* stream) {
   g_last_error.clear();
   if (int rc = check_dims(B, Hq, Hkv, T, D)) return rc;
-  if (padded_dim(D) != kF32D) return fail("fp32 inputs are supported at head_dim <= 64, got " + std::to_string(D));
   if (int rc = check_tensor("q", q, q_strides)) return rc;
   if (int rc = check_tensor("k", k, k_strides)) return rc;
   if (int rc = check_tensor("v", v, v_strides)) return rc;
@@ -1121,7 +1123,7 @@ int lucid_attn_fwd_f32(const float* q, const int64_t* q_strides, const float* k,
   if (int rc = check_ws("fwd_ws", fwd_ws)) return rc;
   if (int rc = chain_check()) return rc;
   const FwdWs w = carve_fwd(fwd_ws, B, Hq, Hkv, T, D, true);
-  return launch_fwd_f32(q, q_strides, k, k_strides, v, v_strides, o, o_strides, vprime, lse, w, B, Hq, Hkv, T,
+  return (padded_dim(D) == 64 ? launch_fwd_f32<64> : launch_fwd_f32<128>)(q, q_strides, k, k_strides, v, v_strides, o, o_strides, vprime, lse, w, B, Hq, Hkv, T,
                         scale, eps, (float)D, static_cast<hipStream_t>(stream));
 }
 
@@ -1131,7 +1133,6 @@ int lucid_attn_bwd_f32(const float* dout, const int64_t* do_strides, const float
                        int Hkv, int T, int D, float scale, void* stream) {
   g_last_error.clear();
   if (int rc = check_dims(B, Hq, Hkv, T, D)) return rc;
-  if (padded_dim(D) != kF32D) return fail("fp32 inputs are supported at head_dim <= 64, got " + std::to_string(D));
   if (int rc = check_tensor("dout", dout, do_strides)) return rc;
   if (int rc = check_tensor("o", o, o_strides)) return rc;
   if (int rc = check_tensor("dq", dq, dq_strides)) return rc;
@@ -1143,7 +1144,7 @@ int lucid_attn_bwd_f32(const float* dout, const int64_t* do_strides, const float
   if (int rc = chain_check()) return rc;
   const FwdWs f = carve_fwd(const_cast<void*>(fwd_ws), B, Hq, Hkv, T, D, true);
   const BwdWs w = carve_bwd(bwd_ws, B, Hq, Hkv, T, D, true);
-  return launch_bwd_f32(dout, do_strides, o, o_strides, lse, f, dq, dq_strides, dk, dk_strides, dv, dv_strides, w,
+  return (padded_dim(D) == 64 ? launch_bwd_f32<64> : launch_bwd_f32<128>)(dout, do_strides, o, o_strides, lse, f, dq, dq_strides, dk, dk_strides, dv, dv_strides, w,
                         B, Hq, Hkv, T, scale, (float)D, static_cast<hipStream_t>(stream));
 }
 
@@ -1174,7 +1175,6 @@ int lucid_attn_vp_fwd_f32(const float* q, const int64_t* q_strides, const float*
                           void* stream) {
   g_last_error.clear();
   if (int rc = check_dims(B, Hq, Hkv, T, D)) return rc;
-  if (padded_dim(D) != kF32D) return fail("fp32 inputs are supported at head_dim <= 64, got " + std::to_string(D));
   if (int rc = check_tensor("q", q, q_strides)) return rc;
   if (int rc = check_tensor("k", k, k_strides)) return rc;
   if (int rc = check_tensor("vprime", vprime, vprime_strides)) return rc;
@@ -1182,7 +1182,7 @@ int lucid_attn_vp_fwd_f32(const float* q, const int64_t* q_strides, const float*
   if (!lse || !ws) return fail("lse and ws must be non-null");
   if (int rc = check_ws("ws", ws)) return rc;
   const FwdWs w = carve_attn_vp(ws, B, Hq, Hkv, T, D, true);
-  return launch_attn_vp_fwd_f32(q, q_strides, k, k_strides, vprime, vprime_strides, o, o_strides, lse, w, B, Hq, Hkv,
+  return (padded_dim(D) == 64 ? launch_attn_vp_fwd_f32<64> : launch_attn_vp_fwd_f32<128>)(q, q_strides, k, k_strides, vprime, vprime_strides, o, o_strides, lse, w, B, Hq, Hkv,
                                 T, eps, scale, (float)D, static_cast<hipStream_t>(stream));
 }
 
@@ -1196,7 +1196,6 @@ int lucid_attn_vp_bwd_f32(const float* dout, const int64_t* do_strides, const fl
                           int B, int Hq, int Hkv, int T, int D, float scale, void* stream) {
   g_last_error.clear();
   if (int rc = check_dims(B, Hq, Hkv, T, D)) return rc;
-  if (padded_dim(D) != kF32D) return fail("fp32 inputs are supported at head_dim <= 64, got " + std::to_string(D));
   if (int rc = check_tensor("dout", dout, do_strides)) return rc;
   if (int rc = check_tensor("o", o, o_strides)) return rc;
   if (int rc = check_tensor("dq", dq, dq_strides)) return rc;
@@ -1207,7 +1206,7 @@ int lucid_attn_vp_bwd_f32(const float* dout, const int64_t* do_strides, const fl
   if (int rc = check_ws("bwd_ws", bwd_ws)) return rc;
   const FwdWs f = carve_attn_vp(const_cast<void*>(fwd_ws), B, Hq, Hkv, T, D, true);
   const BwdWs w = carve_seam_bwd(bwd_ws, B, Hq, Hkv, T, D, true, true);
-  return launch_attn_vp_bwd_f32(dout, do_strides, o, o_strides, lse, f, dq, dq_strides, dk, dk_strides, dvprime,
+  return (padded_dim(D) == 64 ? launch_attn_vp_bwd_f32<64> : launch_attn_vp_bwd_f32<128>)(dout, do_strides, o, o_strides, lse, f, dq, dq_strides, dk, dk_strides, dvprime,
                                 dvprime_strides, w, B, Hq, Hkv, T, scale, static_cast<hipStream_t>(stream));
 }
 

@@ -21,6 +21,12 @@ struct Strides {
 // (N(0,1)-like) give m ~ 1e-2; keys along a shared direction give m ~ T.
 constexpr float kExactMass = 4.0f;
 
+// Staged tiles in flight in the backward sweeps: three buffers (the tile in use, the next
+// one landed, the one after in flight), two for the fp32-input instances at head dim 128,
+// whose hi and lo tiles would not fit three deep in the 160 KB of LDS (the next tile is
+// then waited for at the end of each step).
+constexpr int stage_bufs(int D, bool F32) { return (F32 && D == 128) ? 2 : 3; }
+
 // fp32 inputs (F32 kernel instances): each fp32 input X reaches the kernels as two bf16
 // tensors, X ~= X_hi + X_lo (lucid_split_kernel: 16 significant bits), and every product
 // with an input operand takes three MFMAs (hi*hi + hi*lo + lo*hi).  The score products

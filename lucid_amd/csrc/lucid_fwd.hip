@@ -255,18 +255,19 @@ __global__ __launch_bounds__(256) void lucid_split_kernel(const float* __restric
 // and dK does not involve K.  Keys along a shared direction then reach the split products
 // as their small deviations, so the 16-bit rounding of dS, dP and the scores no longer
 // multiplies the shared part (a ~6-10x smaller dQ error there).  One workgroup per head:
-// 16 row phases x 16 four-column groups, fixed summation order.  grid (B*H), D == 64
+// 256 / (D/4) row phases x D/4 four-column groups, fixed summation order.  grid (B*H)
 template <int D>
 __global__ __launch_bounds__(256) void lucid_key_mean_kernel(const float* __restrict__ k, Strides ks, int H, int T,
                                                              float* __restrict__ mean) {
-  static_assert(D == 64, "16 four-column groups");
-  __shared__ f32x4 part[16][16];
+  constexpr int CG = D / 4, PH = 256 / CG;
+  static_assert(CG * PH == 256, "four-column groups x row phases = 256 threads");
+  __shared__ f32x4 part[PH][CG];
   const int bh = blockIdx.x, b = bh / H, h = bh - b * H;
-  const int ph = threadIdx.x >> 4, c4 = threadIdx.x & 15;
+  const int ph = threadIdx.x / CG, c4 = threadIdx.x % CG;
   const float* kp = k + b * ks.b + h * ks.h + 4 * c4;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll 8
-  for (int t = ph; t < T; t += 16) {
+  for (int t = ph; t < T; t += PH) {
     const f32x4 x = *reinterpret_cast<const f32x4*>(kp + (int64_t)t * ks.t);
 #pragma unroll
     for (int u = 0; u < 4; ++u) acc[u] += x[u];
@@ -275,7 +276,7 @@ __global__ __launch_bounds__(256) void lucid_key_mean_kernel(const float* __rest
   __syncthreads();
   if (ph == 0) {
     f32x4 tot = part[0][c4];
-    for (int r = 1; r < 16; ++r)
+    for (int r = 1; r < PH; ++r)
 #pragma unroll
       for (int u = 0; u < 4; ++u) tot[u] += part[r][c4][u];
 #pragma unroll

@@ -12,10 +12,9 @@ Python mirror of the reference operator seams in ``modeling_lucid.py``:
 
 Layouts follow the reference: ``query [B, Hq, T, d]``, ``key/value [B, Hkv, T, d]``
 (any strides with a contiguous last axis, e.g. the ``.view(...).transpose(1, 2)``
-views LucidAttention builds), output ``[B, T, Hq, d]``.  Inputs must be bf16
-CUDA(HIP) tensors with d <= 128, or fp32 tensors with d <= 64 (computed on bf16 hi/lo
-pairs to ~1e-4 relative, fp32 outputs); anything else raises (there is no CPU or eager
-fallback).  T that is not a multiple of 128 is zero-padded at the end, which is exact for
+views LucidAttention builds), output ``[B, T, Hq, d]``.  Inputs must be bf16 or fp32
+CUDA(HIP) tensors with d <= 128 (fp32 is computed on bf16 hi/lo pairs to ~1e-4 relative,
+fp32 outputs); anything else raises (there is no CPU or eager fallback).  T that is not a multiple of 128 is zero-padded at the end, which is exact for
 every real row because P and the attention mask are causal.  Head dims other than 64 and
 128 (the reference model's is 68) run on rows zero-padded to the next of the two, which
 leaves every dot product unchanged; the RMS of k_norm divides by the true d.
@@ -31,7 +30,6 @@ from . import _lib
 
 _T_ALIGN = 128
 _MAX_D = 128  # head dims up to 128: rows are zero-padded to 64 or 128 columns
-_F32_MAX_D = 64  # the fp32-input kernels run at 64 columns
 
 
 def _padded_dim(d: int) -> int:
@@ -44,8 +42,8 @@ def _pad_d(t: torch.Tensor, dp: int) -> torch.Tensor:
 
 
 def _check_inputs(q, k, v, f32_ok=False):
-    """Shapes, device and dtype of the operands; ``f32_ok``: fp32 operands (head dim 64) are
-    accepted, all of one dtype."""
+    """Shapes, device and dtype of the operands; ``f32_ok``: fp32 operands are accepted, all of
+    one dtype."""
     for name, t in (("query", q), ("key", k), ("value", v)):
         if t is None:
             continue
@@ -62,8 +60,6 @@ def _check_inputs(q, k, v, f32_ok=False):
     d = k.shape[-1]
     if not 1 <= d <= _MAX_D:
         raise ValueError(f"lucid_amd: head_dim {d} not supported (supported: 1 .. {_MAX_D})")
-    if k.dtype == torch.float32 and d > _F32_MAX_D:
-        raise ValueError(f"lucid_amd: fp32 inputs are supported at head_dim <= {_F32_MAX_D}, got {d} (use bf16)")
     if q is not None:
         if q.shape[0] != k.shape[0] or q.shape[2] != k.shape[2] or q.shape[3] != d:
             raise ValueError("lucid_amd: query/key shapes disagree")
@@ -280,7 +276,7 @@ def lucid_attention(query, key, value, scaling=None, eps=1e-5, return_vprime=Fal
     """LUCID attention: ``softmax(s Q K^T, causal) P^-1 V``; returns O ``[B, T, Hq, d]``.
 
     ``eps`` is the k_norm epsilon (``config.rms_norm_eps``, modeling_lucid.py:409).
-    bf16 inputs give bf16 O; fp32 inputs (head dim <= 64) give fp32 O and gradients.
+    bf16 inputs give bf16 O; fp32 inputs give fp32 O and gradients.
     """
     _check_inputs(query, key, value, f32_ok=True)
     d = query.shape[-1]
@@ -479,7 +475,7 @@ def get_v_prime(key, value, scaling=None, attention_mask=None, eps=1e-5):
     """``V' = P^-1 V`` -- ``LucidAttention.get_v_prime(key, value, scaling, attention_mask)``
     (modeling_lucid.py:551-574), differentiable w.r.t. ``key`` and ``value``.
 
-    ``key, value [B, Hkv, T, d]`` (bf16 with d <= 128, or fp32 with d <= 64); returns V' in ``value``'s dtype.
+    ``key, value [B, Hkv, T, d]`` (bf16 or fp32, d <= 128); returns V' in ``value``'s dtype.
     ``eps`` is k_norm's epsilon (``config.rms_norm_eps``).  ``attention_mask``: None or the
     causal mask."""
     _check_inputs(None, key, value, f32_ok=True)
@@ -504,7 +500,7 @@ class Lucid_Tril_Solver:  # noqa: N801  (the reference's class name)
     (``AssertionError`` otherwise, :287-288).  The solve itself is the library's chained
     blockwise one, so the result does not depend on ``BS``; ``value`` is left unmodified (the
     reference subtracts from its rows in place, :296-299).  Layouts ``[B, Hkv, T, d]``, bf16
-    with d <= 128 or fp32 with d <= 64; V' comes back in ``value``'s dtype.
+    or fp32 with d <= 128; V' comes back in ``value``'s dtype.
     """
 
     @staticmethod
@@ -523,7 +519,7 @@ def eager_lucid_attention_forward(query, key, v_prime, scaling=None, attention_m
     """``LucidAttention.eager_lucid_attention_forward(query, key, v_prime, scaling, attention_mask)``
     (modeling_lucid.py:505-549): causal softmax attention of ``query [B, Hq, T, d]`` and
     ``key [B, Hkv, T, d]`` on a given ``v_prime [B, Hkv, T, d]`` (bf16 or fp32; GQA by index,
-    no repeat_kv copy).  fp32 query and key (d <= 64) run the fp32 kernels (fp32 O).  Returns
+    no repeat_kv copy).  fp32 query and key run the fp32 kernels (fp32 O).  Returns
     ``(O [B, T, Hq, d], None)``, differentiable w.r.t. all three.
     ``attention_mask``: None or the causal mask.  ``eps`` (k_norm's) only serves the per-head
     precision choice (:func:`set_precision`)."""

@@ -82,10 +82,11 @@ def test_argument_validation_without_gpu(built):
         assert lib.lucid_fwd_workspace_bytes(1, 4, 2, 256, d) == lib.lucid_fwd_workspace_bytes(1, 4, 2, 256, dp)
         assert lib.lucid_bwd_workspace_bytes(1, 4, 2, 256, d) == lib.lucid_bwd_workspace_bytes(1, 4, 2, 256, dp)
         assert lib.lucid_decode_workspace_bytes(1, 4, 2, 4096, d) == lib.lucid_decode_workspace_bytes(1, 4, 2, 4096, dp)
-    # fp32 inputs: head dims up to 64
+    # fp32 inputs: head dims up to 128 as well (workspaces of the padded dim), above rejected
     rc = lib.lucid_attn_fwd_f32(dummy, s, dummy, s, dummy, s, dummy, s, dummy, dummy, dummy,
-                                1, 1, 1, 256, 68, 0.1, 1e-5, None)
-    assert rc == _lib.LUCID_EINVAL and b"head_dim <= 64" in lib.lucid_last_error()
+                                1, 1, 1, 256, 129, 0.1, 1e-5, None)
+    assert rc == _lib.LUCID_EINVAL and b"head_dim" in lib.lucid_last_error()
+    assert lib.lucid_fwd_f32_workspace_bytes(1, 4, 2, 256, 68) == lib.lucid_fwd_f32_workspace_bytes(1, 4, 2, 256, 128)
     rc = lib.lucid_attn_fwd(dummy, s, dummy, s, dummy, s, dummy, s, dummy, dummy, dummy,
                             1, 1, 1, 200, 64, 0.1, 1e-5, None)
     assert rc == _lib.LUCID_EINVAL and b"multiple of 128" in lib.lucid_last_error()

@@ -1,4 +1,4 @@
-"""GPU parity of LUCID attention on fp32 inputs (head dim 64): O, V' and the gradients of the
+"""GPU parity of LUCID attention on fp32 inputs (head dims up to 128): O, V' and the gradients of the
 fp32 kernels against float64 ground truth, at the north star's fp32 bar (tests/bars.py):
 
     max |x - ref| <= 1e-4 * max |ref|   for O, V', dQ, dK and dV
@@ -65,6 +65,11 @@ CASES = [
     (1, 2, 1, 1024, 64, "correlated"), # keys along a shared direction
     (1, 2, 2, 4096, 64, "correlated"),
     (1, 2, 2, 32768, 64, "unit"),      # the headline length
+    # the reference's shipped LUCID model: fp32, 32 query heads over 4 kv heads, head dim 68,
+    # T up to max_position_embeddings 2048 (lucid/config/config.json:9,13,17,18,25)
+    (1, 32, 4, 2048, 68, "unit"),
+    (1, 2, 2, 4096, 128, "unit"),
+    (1, 2, 1, 1024, 96, "correlated"),
 ]
 
 
@@ -123,23 +128,22 @@ def _ref32_errors(q, k, v, do, eps=1e-5):
 
 def test_fp32_rejects_what_it_does_not_cover():
     from lucid_amd import lucid_attention
-    q, k, v, _ = (x.cuda() for x in _inputs(1, 2, 2, 128, 128, seed=1))
-    with pytest.raises(ValueError, match="head_dim <= 64"):
+    q, k, v, _ = (x.cuda() for x in _inputs(1, 2, 2, 128, 129, seed=1))
+    with pytest.raises(ValueError, match="head_dim 129"):
         lucid_attention(q, k, v)
     q, k, v, _ = (x.cuda() for x in _inputs(1, 2, 2, 128, 64, seed=1))
     with pytest.raises(TypeError, match="share one dtype"):
         lucid_attention(q, k.bfloat16(), v)
 
 
-@pytest.mark.parametrize("B,Hq,Hkv,T", [(1, 1, 1, 512), (2, 4, 2, 320)])
-def test_fp32_seams_composed_like_lucid_attention(B, Hq, Hkv, T):
+@pytest.mark.parametrize("B,Hq,Hkv,T,D", [(1, 1, 1, 512, 64), (2, 4, 2, 320, 64), (1, 8, 1, 384, 68), (1, 2, 2, 256, 128)])
+def test_fp32_seams_composed_like_lucid_attention(B, Hq, Hkv, T, D):
     """get_v_prime and eager_lucid_attention_forward on fp32 tensors, composed as
     LucidAttention.forward composes them (modeling_lucid.py:461-496): fp32 V', O and gradients
     at the fp32 bar against the numpy oracle, and against the fused fp32 call."""
     from lucid_amd import eager_lucid_attention_forward, get_v_prime, lucid_attention
-    D = 64
     q, k, v, do = _inputs(B, Hq, Hkv, T, D, seed=11 + T)
-    print(f"case fp32 seams B={B} Hq={Hq} Hkv={Hkv} T={T}", flush=True)
+    print(f"case fp32 seams B={B} Hq={Hq} Hkv={Hkv} T={T} D={D}", flush=True)
     s = D ** -0.5
     qg, kg, vg = (x.cuda().requires_grad_() for x in (q, k, v))
     vp = get_v_prime(kg, vg, s)
