@@ -4,6 +4,7 @@
 #include "../../include/lucid_path.h"
 #include "path_fwd.hip"
 #include "path_bwd.hip"
+#include "path_wide.hip"
 #include "chain_guard.h"
 #include "profiling.h"
 
@@ -44,10 +45,12 @@ int pchain_check() {
 }
 
 // softmax = true: the PaTH softmax layout (row log-sum-exp instead of the solve's
-// diagonal inverses and O^T chain operand)
-lucid::PathFwdWs carve_path_fwd(void* base, int B, int T, int H, int HQ, size_t* bytes, bool softmax = false) {
+// diagonal inverses and O^T chain operand).  KD: the kernels' head dim (64 or 128): rows
+// of KD values, KD x KD transport matrices, C x C (64 x 64) in-chunk matrices.
+lucid::PathFwdWs carve_path_fwd(void* base, int B, int T, int H, int HQ, size_t* bytes, bool softmax = false,
+                                int KD = 64) {
   const size_t BH = (size_t)B * H, BHq = (size_t)B * HQ;
-  const size_t NT = T / 64, NS = (NT + 7) / 8;
+  const size_t NT = T / 64, NS = (NT + 7) / 8, KK = (size_t)KD * KD;
   lucid::PathFwdWs w{};
   size_t off = 0;
   char* p = static_cast<char*>(base);
@@ -56,18 +59,18 @@ lucid::PathFwdWs carve_path_fwd(void* base, int B, int T, int H, int HQ, size_t*
     off += a256(n);
     return r;
   };
-  w.w2 = reinterpret_cast<float*>(take(BH * T * 64 * 4));
-  w.hc = reinterpret_cast<float*>(take(BH * NT * 4096 * 4));
-  w.kt = reinterpret_cast<bf16*>(take(BH * T * 64 * 2));
-  w.suf = reinterpret_cast<float*>(take(BH * NT * 4096 * 4));
-  w.hl = reinterpret_cast<float*>(take(BH * NS * 4096 * 4));
-  w.kl = reinterpret_cast<bf16*>(take(BH * T * 64 * 2));
-  w.qt = reinterpret_cast<float*>(take(BHq * T * 64 * 4));
+  w.w2 = reinterpret_cast<float*>(take(BH * T * KD * 4));
+  w.hc = reinterpret_cast<float*>(take(BH * NT * KK * 4));
+  w.kt = reinterpret_cast<bf16*>(take(BH * T * KD * 2));
+  w.suf = reinterpret_cast<float*>(take(BH * NT * KK * 4));
+  w.hl = reinterpret_cast<float*>(take(BH * NS * KK * 4));
+  w.kl = reinterpret_cast<bf16*>(take(BH * T * KD * 2));
+  w.qt = reinterpret_cast<float*>(take(BHq * T * KD * 4));
   w.ld = reinterpret_cast<float*>(take(BHq * NT * 4096 * 4));
   if (!softmax) w.y = reinterpret_cast<float*>(take(BHq * NT * 4096 * 4));
-  w.qs = reinterpret_cast<bf16*>(take(BHq * 8 * T * 64 * 2));
-  w.qb = reinterpret_cast<bf16*>(take(BHq * NS * T * 64 * 2));
-  if (!softmax) w.oT = reinterpret_cast<bf16*>(take(BHq * T * 64 * 2));
+  w.qs = reinterpret_cast<bf16*>(take(BHq * 8 * T * KD * 2));
+  w.qb = reinterpret_cast<bf16*>(take(BHq * NS * T * KD * 2));
+  if (!softmax) w.oT = reinterpret_cast<bf16*>(take(BHq * T * KD * 2));
   w.counters = reinterpret_cast<int*>(take(BHq * 4));
   if (softmax) w.lse = reinterpret_cast<float*>(take(BHq * T * 4));
   if (bytes) *bytes = off;
@@ -90,9 +93,9 @@ int pcheck_vec(const char* name, const void* p, const int64_t* s) {
 
 lucid::Strides PS(const int64_t* s) { return lucid::Strides{s[0], s[1], s[2]}; }
 
-lucid::PathBwdWs carve_path_bwd(void* base, int B, int T, int HQ, size_t* bytes, bool softmax = false) {
+lucid::PathBwdWs carve_path_bwd(void* base, int B, int T, int HQ, size_t* bytes, bool softmax = false, int KD = 64) {
   const size_t BHq = (size_t)B * HQ;
-  const size_t NT = T / 64, NS = (NT + 7) / 8;
+  const size_t NT = T / 64, NS = (NT + 7) / 8, KK = (size_t)KD * KD;
   lucid::PathBwdWs w{};
   size_t off = 0;
   char* p = static_cast<char*>(base);
@@ -101,20 +104,20 @@ lucid::PathBwdWs carve_path_bwd(void* base, int B, int T, int HQ, size_t* bytes,
     off += a256(n);
     return r;
   };
-  w.dvf = reinterpret_cast<float*>(take(BHq * T * 64 * 4));
+  w.dvf = reinterpret_cast<float*>(take(BHq * T * KD * 4));
   if (!softmax) {
-    w.dvb = reinterpret_cast<bf16*>(take(BHq * T * 64 * 2));
-    w.dvT = reinterpret_cast<bf16*>(take(BHq * T * 64 * 2));
+    w.dvb = reinterpret_cast<bf16*>(take(BHq * T * KD * 2));
+    w.dvT = reinterpret_cast<bf16*>(take(BHq * T * KD * 2));
   }
   w.dad = reinterpret_cast<float*>(take(BHq * NT * 4096 * 4));
-  w.dqt = reinterpret_cast<float*>(take(BHq * T * 64 * 4));
-  w.dkt = reinterpret_cast<float*>(take(BHq * T * 64 * 4));
-  w.dsuf = reinterpret_cast<float*>(take(BHq * NT * 4096 * 4));
-  w.dhl = reinterpret_cast<float*>(take(BHq * NS * 4096 * 4));
-  w.dhc = reinterpret_cast<float*>(take(BHq * NT * 4096 * 4));
-  w.dq = reinterpret_cast<float*>(take(BHq * T * 64 * 4));
-  w.dk = reinterpret_cast<float*>(take(BHq * T * 64 * 4));
-  w.dw = reinterpret_cast<float*>(take(BHq * T * 64 * 4));
+  w.dqt = reinterpret_cast<float*>(take(BHq * T * KD * 4));
+  w.dkt = reinterpret_cast<float*>(take(BHq * T * KD * 4));
+  w.dsuf = reinterpret_cast<float*>(take(BHq * NT * KK * 4));
+  w.dhl = reinterpret_cast<float*>(take(BHq * NS * KK * 4));
+  w.dhc = reinterpret_cast<float*>(take(BHq * NT * KK * 4));
+  w.dq = reinterpret_cast<float*>(take(BHq * T * KD * 4));
+  w.dk = reinterpret_cast<float*>(take(BHq * T * KD * 4));
+  w.dw = reinterpret_cast<float*>(take(BHq * T * KD * 4));
   w.db = reinterpret_cast<float*>(take(BHq * T * 4));
   w.counters = reinterpret_cast<int*>(take(BHq * 4));
   if (softmax) w.delta = reinterpret_cast<float*>(take(BHq * T * 4));
@@ -124,7 +127,7 @@ lucid::PathBwdWs carve_path_bwd(void* base, int B, int T, int HQ, size_t* bytes,
 
 int check_shapes(int B, int T, int H, int HQ, int K) {
   if (B <= 0 || T <= 0 || H <= 0 || HQ <= 0) return pfail("B, T, H and HQ must be positive");
-  if (K != 64) return pfail("head_dim must be 64, got " + std::to_string(K));
+  if (K != 64 && K != 128) return pfail("head_dim must be 64 or 128, got " + std::to_string(K));
   if (T % 64) return pfail("T must be a multiple of 64, got " + std::to_string(T));
   if (HQ % H) return pfail("the number of query heads must be a multiple of the key heads");
   return 0;
@@ -134,9 +137,19 @@ int check_shapes(int B, int T, int H, int HQ, int K) {
 // decode key cache
 int launch_front(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
                  const void* w, const int64_t* w_strides, const void* beta, const int64_t* beta_strides,
-                 int B, int T, int H, int HQ, float scale, int softmax, const lucid::PathFwdWs& ws, hipStream_t st) {
+                 int B, int T, int H, int HQ, float scale, int softmax, const lucid::PathFwdWs& ws, hipStream_t st,
+                 int KD = 64) {
   const int NT = T / 64, NS = (NT + 7) / 8;
   const int BH = B * H, BHq = B * HQ;
+  if (KD == 128) {
+    LUCID_TIMED_LAUNCH(phip, "path_chunk128_kernel", lucid::path_chunk128_kernel, dim3(NT, BHq), st, (const bf16*)q,
+                       PS(q_strides), (const bf16*)k, PS(k_strides), (const bf16*)w, PS(w_strides), (const bf16*)beta,
+                       PS(beta_strides), HQ, H, T, scale, softmax, ws);
+    LUCID_TIMED_LAUNCH(phip, "path_large128_kernel", lucid::path_large128_kernel, dim3(NS, BH), st, T, ws);
+    LUCID_TIMED_LAUNCH(phip, "path_transport128_kernel", lucid::path_transport128_kernel, dim3(BHq, (NT + 1) / 2), st,
+                       HQ, H, T, ws);
+    return 0;
+  }
   LUCID_TIMED_LAUNCH(phip, "path_chunk_kernel", lucid::path_chunk_kernel, dim3(NT, BHq), st, (const bf16*)q, PS(q_strides),
                      (const bf16*)k, PS(k_strides), (const bf16*)w, PS(w_strides), (const bf16*)beta,
                      PS(beta_strides), HQ, H, T, scale, softmax, ws);
@@ -146,8 +159,13 @@ int launch_front(const void* q, const int64_t* q_strides, const void* k, const i
 }
 
 int launch_kcache(void* kcache, const int64_t* kcache_strides, int B, int T, int H, const lucid::PathFwdWs& ws,
-                  hipStream_t st) {
+                  hipStream_t st, int KD = 64) {
   const int NT = T / 64;
+  if (KD == 128) {
+    LUCID_TIMED_LAUNCH(phip, "path_kcache128_kernel", lucid::path_kcache128_kernel, dim3(NT, B * H), st, T,
+                       (bf16*)kcache, PS(kcache_strides), H, ws);
+    return 0;
+  }
   LUCID_TIMED_LAUNCH(phip, "path_kcache_kernel", lucid::path_kcache_kernel, dim3(NT, B * H), st, T, (bf16*)kcache,
                      PS(kcache_strides), H, ws);
   return 0;
@@ -193,9 +211,8 @@ int lucid_path_set_chain_wait_limit(double seconds) {
 }
 
 size_t lucid_path_fwd_workspace_bytes(int B, int T, int H, int HQ, int K) {
-  (void)K;
   size_t n = 0;
-  carve_path_fwd(nullptr, B, T, H, HQ, &n);
+  carve_path_fwd(nullptr, B, T, H, HQ, &n, false, K > 64 ? 128 : 64);
   return n;
 }
 
@@ -217,16 +234,21 @@ int lucid_path_fwd(const void* q, const int64_t* q_strides, const void* k, const
   if (!fwd_ws) return pfail("fwd_ws is null");
   if (reinterpret_cast<uintptr_t>(fwd_ws) % 256) return pfail("fwd_ws must be 256-byte aligned");
   if (int rc = pchain_check()) return rc;
-  const lucid::PathFwdWs ws = carve_path_fwd(fwd_ws, B, T, H, HQ, nullptr);
+  const lucid::PathFwdWs ws = carve_path_fwd(fwd_ws, B, T, H, HQ, nullptr, false, K);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int NT = T / 64;
   const int BHq = B * HQ;
-  if (int rc = launch_front(q, q_strides, k, k_strides, w, w_strides, beta, beta_strides, B, T, H, HQ, scale, 0, ws, st))
+  if (int rc = launch_front(q, q_strides, k, k_strides, w, w_strides, beta, beta_strides, B, T, H, HQ, scale, 0, ws, st,
+                            K))
     return rc;
-  LUCID_TIMED_LAUNCH(phip, "path_solve_fwd_kernel", lucid::path_solve_fwd_kernel, dim3(((NT + 1) / 2) * BHq), st, (const bf16*)v,
-                     PS(v_strides), (bf16*)o, PS(o_strides), HQ, H, T, BHq, scale, ws);
+  if (K == 128)
+    LUCID_TIMED_LAUNCH(phip, "path_solve_fwd_kernel", lucid::path_solve_fwd_kernel<128>, dim3(((NT + 1) / 2) * BHq), st,
+                       (const bf16*)v, PS(v_strides), (bf16*)o, PS(o_strides), HQ, H, T, BHq, scale, ws);
+  else
+    LUCID_TIMED_LAUNCH(phip, "path_solve_fwd_kernel", lucid::path_solve_fwd_kernel<64>, dim3(((NT + 1) / 2) * BHq), st,
+                       (const bf16*)v, PS(v_strides), (bf16*)o, PS(o_strides), HQ, H, T, BHq, scale, ws);
   if (kcache)
-    if (int rc = launch_kcache(kcache, kcache_strides, B, T, H, ws, st)) return rc;
+    if (int rc = launch_kcache(kcache, kcache_strides, B, T, H, ws, st, K)) return rc;
   return 0;
 }
 
@@ -247,6 +269,7 @@ int lucid_path_bwd(const void* dout, const int64_t* do_strides, const void* q, c
                    void* stream) {
   g_path_error.clear();
   if (int rc = check_shapes(B, T, H, HQ, K)) return rc;
+  if (K != 64) return pfail("the backward runs at head_dim 64 only, got " + std::to_string(K));
   if (int rc = pcheck_vec("dout", dout, do_strides)) return rc;
   if (int rc = pcheck_vec("q", q, q_strides)) return rc;
   if (int rc = pcheck_vec("k", k, k_strides)) return rc;
@@ -294,6 +317,7 @@ int lucid_path_softmax_fwd(const void* q, const int64_t* q_strides, const void* 
                            int K, float scale, void* stream) {
   g_path_error.clear();
   if (int rc = check_shapes(B, T, H, HQ, K)) return rc;
+  if (K != 64) return pfail("the softmax path runs at head_dim 64 only, got " + std::to_string(K));
   if (int rc = pcheck_vec("q", q, q_strides)) return rc;
   if (int rc = pcheck_vec("k", k, k_strides)) return rc;
   if (int rc = pcheck_vec("v", v, v_strides)) return rc;
@@ -334,6 +358,7 @@ int lucid_path_softmax_bwd(const void* dout, const int64_t* do_strides, const vo
                            float scale, void* stream) {
   g_path_error.clear();
   if (int rc = check_shapes(B, T, H, HQ, K)) return rc;
+  if (K != 64) return pfail("the backward runs at head_dim 64 only, got " + std::to_string(K));
   if (int rc = pcheck_vec("dout", dout, do_strides)) return rc;
   if (int rc = pcheck_vec("q", q, q_strides)) return rc;
   if (int rc = pcheck_vec("k", k, k_strides)) return rc;

@@ -338,25 +338,28 @@ __global__ __launch_bounds__(256) void path_transport_kernel(int HQ, int H, int 
 // bf16 split.  L_BA depends on the key operands only and is computed before the sweep.
 // The fp32 buffers of the final step reuse the staging space.
 // ---------------------------------------------------------------------------
+template <int KD>
 struct SolveFwdSmem {
   union {
     struct {
-      bf16 k[2][2][64 * 64];  // [buffer][chunk of the pair], swizzled (chunk c of row r at c ^ (r & 7))
-      bf16 o[2][2][64 * 64];
+      bf16 k[2][2][64 * KD];  // [buffer][chunk of the pair], swizzled (chunk c of row r at c ^ (r & 7))
+      bf16 o[2][2][KD * 64];
     } st;
     struct {
-      float Rt[64][132];    // R^T for the 128 rows (0..63 = A, 64..127 = B)
+      float Rt[KD][132];    // R^T for the 128 rows (0..63 = A, 64..127 = B)
       float Ys[64][68];     // Y of the chunk being solved
-      bf16 ot[64][128 + 8];  // O^T of both chunks, T-perm within 16-groups
+      bf16 ot[KD][128 + 8];  // O^T of both chunks, T-perm within 16-groups
     } fin;
   } u;
   bf16x8 lba[4][64][2];  // L_BA as MFMA B operands, per wave and lane
 };
 
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void path_solve_fwd_kernel(const bf16* __restrict__ v, Strides vs,
+template <int KD>
+__global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_solve_fwd_kernel(const bf16* __restrict__ v, Strides vs,
                                                              bf16* __restrict__ o, Strides os, int HQ, int H,
                                                              int T, int BHq, float scale, PathFwdWs ws) {
-  __shared__ __attribute__((aligned(16))) SolveFwdSmem sm;
+  constexpr int NKS = KD / 16, NVT = KD / 32;  // k-steps of a logit product, 32-column value tiles
+  __shared__ __attribute__((aligned(16))) SolveFwdSmem<KD> sm;
   const int NT = T / PC, NS = (NT + PR - 1) / PR;
   const int id = blockIdx.x;
   const int p = id / BHq, bhq = id - (id / BHq) * BHq;
@@ -370,19 +373,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
   const int i0 = A * PC;
   int* cnt = ws.counters + bhq;
   const float sl2 = scale * LOG2E_F, cc0 = LOG2E_F / scale;
-  const bf16* oTh = ws.oT + (int64_t)bhq * 64 * T;
+  const bf16* oTh = ws.oT + (int64_t)bhq * KD * T;
   const int npair = p;  // key chunks 0 .. A - 1
   // this wave's rows (chunk A or B); a missing chunk B reads chunk A's rows, unused
   const bool myrows = ih == 0 || hasB;
   const int r0 = i0 + (myrows ? ih * 64 : 0);
 
   // accumulators: -V^T for the kh = 0 waves (R = V - acc = -(acc_0 + acc_1)), zero for the others
-  f32x16 acc[2][2];
+  f32x16 acc[NVT][2];
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
     const bf16* vrow = v + b * vs.b + h * vs.h + (int64_t)(r0 + nt * 32 + l32) * vs.t;
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < NVT; ++t)
 #pragma unroll
       for (int qq = 0; qq < 4; ++qq) {
         const bf16x4 vv = *reinterpret_cast<const bf16x4*>(vrow + t * 32 + 8 * qq + 4 * g);
@@ -393,16 +396,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
   // query operand of key chunk J for this wave's rows: QB^(J/PR) below the large chunk,
   // QS slot J - cb inside it
   auto qbase = [&](int J) {
-    return (J < cb) ? ws.qb + ((int64_t)bhq * NS + J / PR) * T * 64 : ws.qs + ((int64_t)bhq * PR + (J - cb)) * T * 64;
+    return (J < cb) ? ws.qb + ((int64_t)bhq * NS + J / PR) * T * KD : ws.qs + ((int64_t)bhq * PR + (J - cb)) * T * KD;
   };
   // L_BA (rows of B half nb, keys of A half ka): Kop_A = k~_A, Qop = QS slot A - cb of B's rows
   if (hasB) {
     const int nb = w & 1, ka = w >> 1;
-    const bf16* kr = ws.kt + ((int64_t)bh * T + i0 + ka * 32 + l32) * 64;
-    const bf16* qr = qbase(A) + (int64_t)(i0 + 64 + nb * 32 + l32) * 64;
+    const bf16* kr = ws.kt + ((int64_t)bh * T + i0 + ka * 32 + l32) * KD;
+    const bf16* qr = qbase(A) + (int64_t)(i0 + 64 + nb * 32 + l32) * KD;
     f32x16 sc = zero16();
 #pragma unroll
-    for (int st = 0; st < 4; ++st) sc = mfma32(ld8(kr + 16 * st + 8 * g), ld8(qr + 16 * st + 8 * g), sc);
+    for (int st = 0; st < NKS; ++st) sc = mfma32(ld8(kr + 16 * st + 8 * g), ld8(qr + 16 * st + 8 * g), sc);
 #pragma unroll
     for (int e = 0; e < 16; ++e) sc[e] = __builtin_amdgcn_exp2f(fmaf(sc[e], sl2, -cc0));
     sm.lba[w][lane][0] = pack_b(sc, 0);
@@ -410,7 +413,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
   }
   // below the large chunk the operand changes only every PR key chunks, so it stays in
   // registers across pairs; inside it every chunk has its own slot
-  bf16x8 qop[2][4];
+  bf16x8 qop[2][NKS];
   int qsrc = -1;
   auto load_q = [&](int J) {
     const int src = (J < cb) ? J / PR : NS + J;
@@ -420,18 +423,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
-      for (int st = 0; st < 4; ++st) qop[nt][st] = ld8(base + (int64_t)(r0 + nt * 32 + l32) * 64 + 16 * st + 8 * g);
+      for (int st = 0; st < NKS; ++st) qop[nt][st] = ld8(base + (int64_t)(r0 + nt * 32 + l32) * KD + 16 * st + 8 * g);
   };
-  int plan_k[2], plan_t[2];
-  dma_plan<64, 8>(64, plan_k);
-  dma_plan<64, 8>(T, plan_t);
+  int plan_k[64 * (KD / 8) / 256], plan_t[KD * 8 / 256];
+  dma_plan<64, KD / 8>(KD, plan_k);
+  dma_plan<KD, 8>(T, plan_t);
   auto stage = [&](int pp) {  // key chunks 2pp, 2pp + 1 into buffer pp & 1
     const int buf = pp & 1;
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int J = 2 * pp + u;
-      dma_stage<64, 8>(plan_k, ((J < cb) ? ws.kl : ws.kt) + ((int64_t)bh * T + J * PC) * 64, sm.u.st.k[buf][u]);
-      dma_stage<64, 8>(plan_t, oTh + J * PC, sm.u.st.o[buf][u]);
+      dma_stage<64, KD / 8>(plan_k, ((J < cb) ? ws.kl : ws.kt) + ((int64_t)bh * T + J * PC) * KD, sm.u.st.k[buf][u]);
+      dma_stage<KD, 8>(plan_t, oTh + J * PC, sm.u.st.o[buf][u]);
     }
   };
   // Y_A, Y_B (fp32) are fetched into registers during the last pair
@@ -454,22 +457,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
   auto sweep_pair = [&](int buf) {
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
-      bf16x8 ka[4];
+      bf16x8 ka[NKS];
 #pragma unroll
-      for (int st = 0; st < 4; ++st) ka[st] = ld8(swz<8>(sm.u.st.k[buf][kh], mt * 32 + l32, 2 * st + g));
+      for (int st = 0; st < NKS; ++st) ka[st] = ld8(swz<KD / 8>(sm.u.st.k[buf][kh], mt * 32 + l32, 2 * st + g));
       bf16x8 pb[2][2];
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt) {
         f32x16 sc = zero16();
 #pragma unroll
-        for (int st = 0; st < 4; ++st) sc = mfma32(ka[st], qop[nt][st], sc);
+        for (int st = 0; st < NKS; ++st) sc = mfma32(ka[st], qop[nt][st], sc);
 #pragma unroll
         for (int e = 0; e < 16; ++e) sc[e] = __builtin_amdgcn_exp2f(fmaf(sc[e], sl2, -cc0));
         pb[nt][0] = pack_b(sc, 0);
         pb[nt][1] = pack_b(sc, 1);
       }
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
+      for (int t = 0; t < NVT; ++t) {
         const bf16x8 va0 = ld8(swz<8>(sm.u.st.o[buf][kh], t * 32 + l32, 4 * mt + g));
         const bf16x8 va1 = ld8(swz<8>(sm.u.st.o[buf][kh], t * 32 + l32, 4 * mt + 2 + g));
 #pragma unroll
@@ -521,7 +524,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
   float(*Rt)[132] = sm.u.fin.Rt;
   if (kh == 1 && myrows) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < NVT; ++t)
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
@@ -531,7 +534,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
   __syncthreads();
   if (kh == 0 && myrows) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < NVT; ++t)
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
@@ -541,9 +544,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
         }
   }
   __syncthreads();
-  // O^T[d][r] = sum_c R^T[d][c] Y[r][c] for chunk c (Y lower triangular)
+  // O^T[d][r] = sum_c R^T[d][c] Y[r][c] for chunk c (Y lower triangular); wave w -> value
+  // tiles dt = w >> 1 (+ 2, + 4 .. at KD > 64), row half rh = w & 1
   auto diag_solve = [&](int c) {
-    const int dt = w >> 1, rh = w & 1;
+   const int rh = w & 1;
+   for (int dt = w >> 1; dt < NVT; dt += 2) {
     f32x16 oo = zero16();
     for (int st = 0; st < (rh ? 4 : 2); ++st) {
       bf16x8 ah, al, bh8, bl;
@@ -567,6 +572,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
       }
       *reinterpret_cast<bf16x4*>(orow + d0) = bb;
     }
+   }
   };
   diag_solve(0);
   __syncthreads();
@@ -575,23 +581,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
     // ---- R_B -= L_BA O_A: wave -> (B rows half nb, A keys half ka) ----
     const int nb = w & 1, ka = w >> 1;
     const bf16x8 l0 = sm.lba[w][lane][0], l1 = sm.lba[w][lane][1];
-    f32x16 cr[2];
+    f32x16 cr[NVT];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
+    for (int t = 0; t < NVT; ++t) {
       cr[t] = mfma32(ld8(&sm.u.fin.ot[t * 32 + l32][ka * 32 + 8 * g]), l0, zero16());
       cr[t] = mfma32(ld8(&sm.u.fin.ot[t * 32 + l32][ka * 32 + 16 + 8 * g]), l1, cr[t]);
     }
     const int col = 64 + nb * 32 + l32;
     if (ka == 1) {
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+      for (int t = 0; t < NVT; ++t)
 #pragma unroll
         for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][col] -= cr[t][e];
     }
     __syncthreads();
     if (ka == 0) {
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+      for (int t = 0; t < NVT; ++t)
 #pragma unroll
         for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][col] -= cr[t][e];
     }
@@ -601,9 +607,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
   }
   // O^T of the workgroup's chunks to the chain operand with 16-byte stores
   const int nch = hasB ? 2 : 1;
-  for (int c = tid; c < 64 * 8 * nch; c += 256) {
+  for (int c = tid; c < KD * 8 * nch; c += 256) {
     const int dd = c / (8 * nch), s8 = (c - dd * 8 * nch) * 8;
-    *reinterpret_cast<bf16x8*>(ws.oT + ((int64_t)bhq * 64 + dd) * T + i0 + s8) = ld8(&sm.u.fin.ot[dd][s8]);
+    *reinterpret_cast<bf16x8*>(ws.oT + ((int64_t)bhq * KD + dd) * T + i0 + s8) = ld8(&sm.u.fin.ot[dd][s8]);
   }
   publish_counter(cnt, A + nch);
 }

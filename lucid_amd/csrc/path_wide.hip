@@ -1,0 +1,376 @@
+// LUCID-Path (and PaTH softmax) at head dim 128: the stages whose operands are 64 x K or
+// K x K fp32 matrices (the WY form of a chunk, the Householder products of a large chunk,
+// the query transport, the decode key cache, and their backward), with every 128-wide
+// matrix held as 64 x 64 fp32 LDS blocks and every product taken block by block on the
+// matrix cores (mgemm64: 3-term bf16 split, ~fp32 accuracy).  The algebra is that of the
+// head-dim-64 kernels in path_fwd.hip / path_bwd.hip (reference parallel.py:27-177,
+// cumprod_householder_fwd.py:13-79, transform_q.py:15-61, prepare_k_cache.py:12-74,
+// cumprod_householder_bwd.py:13-95, intra_chunk_preprocess_bwd.py:14-110); only the
+// staging differs, so that the operands fit the 160 KB of LDS.
+//
+// Workspace layouts at K = V = 128 (PathFwdWs / PathBwdWs): rows [..][T][128], K x K
+// matrices row-major [..][128 * 128], in-chunk C x C matrices [..][64 * 64] as at 64.
+#pragma once
+#include "path_common.h"
+
+namespace lucid {
+
+constexpr int WK = 128;  // head dim of this file's kernels
+
+// 64 x 64 block of an fp32 row-major matrix (row stride ld) into an LDS block, and back
+__device__ __forceinline__ void load_blk(float (*dst)[68], const float* __restrict__ src, int ld) {
+  for (int idx = threadIdx.x; idx < 1024; idx += 256) {
+    const int r = idx >> 4, c4 = (idx & 15) * 4;
+    *reinterpret_cast<f32x4*>(&dst[r][c4]) = *reinterpret_cast<const f32x4*>(src + (int64_t)r * ld + c4);
+  }
+}
+__device__ __forceinline__ void store_blk(float* __restrict__ dst, int ld, const float (*src)[68]) {
+  for (int idx = threadIdx.x; idx < 1024; idx += 256) {
+    const int r = idx >> 4, c4 = (idx & 15) * 4;
+    *reinterpret_cast<f32x4*>(dst + (int64_t)r * ld + c4) = *reinterpret_cast<const f32x4*>(&src[r][c4]);
+  }
+}
+// D-layout tile (this wave's 32 x 32 of a 64 x 64 block) to a row-major fp32 / bf16 matrix
+__device__ __forceinline__ void dl_put(float* __restrict__ dst, int ld, const f32x16& x) {
+  const int cl = dl_col();
+  DL_FOR_E dst[(int64_t)dl_row(e) * ld + cl] = x[e];
+}
+
+// ---------------------------------------------------------------------------
+// WY form and in-chunk transforms at K = 128 (path_chunk_kernel's algebra).  grid (NT, B*HQ)
+//   phase 1 (K halves h = 0, 1 accumulated): a = Wb W^T, WBK = Wb K^T, QW = Q W^T, QK = Q K^T
+//   Tm = (I + stril a)^-1, TW = Tm stril(WBK), A_diag = tril(QK - tril(QW) TW), L_diag, Y
+//   phase 2: Tmb = Tm diag(beta); W2_h = Tmb W_h; k~_h = K_h - TW^T W_h; q~_h = Q_h - QW W2_h;
+//   Hc blocks (a, b) = delta_ab I - W_a^T W2_b
+// LDS: seven 64 x 64 fp32 blocks.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void path_chunk128_kernel(const bf16* __restrict__ q, Strides qs,
+                                                            const bf16* __restrict__ k, Strides ks,
+                                                            const bf16* __restrict__ w, Strides wst,
+                                                            const bf16* __restrict__ beta, Strides bst, int HQ, int H,
+                                                            int T, float scale, int softmax, PathFwdWs ws) {
+  __shared__ __attribute__((aligned(16))) float Bm[7][64][68];
+  __shared__ float bsh[64];
+  const int c = blockIdx.x, bhq = blockIdx.y;
+  const int NT = T / PC;
+  const int G = HQ / H;
+  const int b = bhq / HQ, hq = bhq - b * HQ, h = hq / G;
+  const int bh = b * H + h;
+  const bool kvw = (hq % G) == 0;
+  const int tid = threadIdx.x;
+  const int t0 = c * PC;
+  const f32x16 z = zero16();
+  const int cl = dl_col();
+  if (c == 0 && tid == 0) ws.counters[bhq] = 0;
+  const bf16* wp = w + b * wst.b + h * wst.h + (int64_t)t0 * wst.t;
+  const bf16* qp = q + b * qs.b + hq * qs.h + (int64_t)t0 * qs.t;
+  const bf16* kp = k + b * ks.b + h * ks.h + (int64_t)t0 * ks.t;
+  if (tid < 64) bsh[tid] = (float)beta[b * bst.b + h * bst.h + (int64_t)(t0 + tid) * bst.t];
+  f32x16 aA = z, aWBK = z, aQW = z, aQK = z;
+#pragma unroll 1
+  for (int hh = 0; hh < 2; ++hh) {
+    load_rows64_f32(Bm[0], wp + 64 * hh, wst.t);
+    load_rows64_f32(Bm[1], qp + 64 * hh, qs.t);
+    load_rows64_f32(Bm[2], kp + 64 * hh, ks.t);
+    __syncthreads();
+    {
+      const int r = tid >> 2, cc = (tid & 3) * 16;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) Bm[3][r][cc + e] = bsh[r] * Bm[0][r][cc + e];
+    }
+    __syncthreads();
+    aA = mgemm64<false, true>(Bm[3], Bm[0], aA);
+    aWBK = mgemm64<false, true>(Bm[3], Bm[2], aWBK);
+    aQW = mgemm64<false, true>(Bm[1], Bm[0], aQW);
+    aQK = mgemm64<false, true>(Bm[1], Bm[2], aQK);
+    __syncthreads();
+  }
+  float(*Tm)[68] = Bm[4];
+  float(*QW)[68] = Bm[5];
+  float(*TW)[68] = Bm[6];
+  dl_store(Tm, aA, 2);
+  dl_store(QW, aWBK, 2);  // stril(WBK), until TW is formed
+  __syncthreads();
+  invert_unit_lower64(Tm);
+  dl_store(TW, mgemm64<false, false>(Tm, QW, z), 0);
+  __syncthreads();
+  dl_store(QW, aQW, 1);  // tril(Q W^T)
+  __syncthreads();
+  {
+    const f32x16 qt_ = mgemm64<false, false>(QW, TW, z);
+    float* dst = ws.ld + ((int64_t)bhq * NT + c) * 4096;
+    if (softmax) {
+      DL_FOR_E {
+        const int r = dl_row(e);
+        dst[r * 64 + cl] = cl <= r ? aQK[e] - qt_[e] : 0.f;
+      }
+    } else {
+      const float sl2 = scale * LOG2E_F, cc0 = LOG2E_F / scale;
+      DL_FOR_E {
+        const int r = dl_row(e);
+        const float v = cl < r ? __builtin_amdgcn_exp2f(fmaf(aQK[e] - qt_[e], sl2, -cc0)) : 0.f;
+        Bm[0][r][cl] = v;
+        dst[r * 64 + cl] = v;
+      }
+      __syncthreads();
+      invert_unit_lower64(Bm[0]);
+      store_blk(ws.y + ((int64_t)bhq * NT + c) * 4096, 64, Bm[0]);
+    }
+  }
+  __syncthreads();
+  // Tmb = Tm diag(beta) in place (Tm is read only by the W2 products from here on)
+  for (int idx = tid; idx < 4096; idx += 256) Tm[idx >> 6][idx & 63] *= bsh[idx & 63];
+  load_rows64_f32(Bm[1], wp, wst.t);
+  load_rows64_f32(Bm[2], wp + 64, wst.t);
+  __syncthreads();
+  const f32x16 w2a = mgemm64<false, false>(Tm, Bm[1], z), w2b = mgemm64<false, false>(Tm, Bm[2], z);
+  dl_store(Bm[0], w2a, 0);
+  dl_store(Bm[3], w2b, 0);
+  if (kvw) {
+    float* dst = ws.w2 + ((int64_t)bh * T + t0) * WK;
+    dl_put(dst, WK, w2a);
+    dl_put(dst + 64, WK, w2b);
+  }
+  __syncthreads();
+#pragma unroll 1
+  for (int hh = 0; hh < 2; ++hh) {
+    float(*Wh)[68] = Bm[1 + hh];
+    float(*W2h)[68] = hh ? Bm[3] : Bm[0];
+    if (kvw) {  // k~_h = K_h - TW^T W_h
+      const f32x16 a = mgemm64<true, false>(TW, Wh, z);
+      bf16* dst = ws.kt + ((int64_t)bh * T + t0) * WK + 64 * hh;
+      DL_FOR_E {
+        const int r = dl_row(e);
+        dst[r * WK + cl] = (bf16)((float)kp[(int64_t)r * ks.t + 64 * hh + cl] - a[e]);
+      }
+    }
+    {  // q~_h = Q_h - QW W2_h
+      const f32x16 a = mgemm64<false, false>(QW, W2h, z);
+      float* dst = ws.qt + ((int64_t)bhq * T + t0) * WK + 64 * hh;
+      DL_FOR_E {
+        const int r = dl_row(e);
+        dst[r * WK + cl] = (float)qp[(int64_t)r * qs.t + 64 * hh + cl] - a[e];
+      }
+    }
+  }
+  if (kvw) {  // Hc = I - W^T W2, block (ra, cb_)
+    float* dst = ws.hc + ((int64_t)bh * NT + c) * (WK * WK);
+#pragma unroll 1
+    for (int blk = 0; blk < 4; ++blk) {
+      const int ra = blk >> 1, cb_ = blk & 1;
+      const f32x16 a = mgemm64<true, false>(Bm[1 + ra], cb_ ? Bm[3] : Bm[0], z);
+      DL_FOR_E {
+        const int r = dl_row(e);
+        dst[(int64_t)(64 * ra + r) * WK + 64 * cb_ + cl] = (ra == cb_ && r == cl ? 1.f : 0.f) - a[e];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Per large chunk at K = 128 (path_large_kernel's algebra): SUF_c from the top down,
+// KL_c = k~_c SUF_c^T, SUF_{c-1} = SUF_c Hc_c, HL = the last.  grid (NS, B*H)
+// LDS: SUF as four blocks, and four operand blocks holding k~_c, then Hc_c.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void path_large128_kernel(int T, PathFwdWs ws) {
+  __shared__ __attribute__((aligned(16))) float Sf[4][64][68];  // block (r, c) at 2 r + c
+  __shared__ __attribute__((aligned(16))) float Op[4][64][68];
+  const int s = blockIdx.x, bh = blockIdx.y;
+  const int NT = T / PC, NS = (NT + PR - 1) / PR;
+  const int tid = threadIdx.x;
+  const int cb = s * PR, ce = min(cb + PR, NT) - 1;
+  const f32x16 z = zero16();
+  for (int idx = tid; idx < 4 * 4096; idx += 256) {
+    const int blk = idx >> 12, r = (idx >> 6) & 63, cc = idx & 63;
+    Sf[blk][r][cc] = ((blk == 0 || blk == 3) && r == cc) ? 1.f : 0.f;
+  }
+  __syncthreads();
+#pragma unroll 1
+  for (int c = ce; c >= cb; --c) {
+    float* suf = ws.suf + ((int64_t)bh * NT + c) * (WK * WK);
+#pragma unroll 1
+    for (int blk = 0; blk < 4; ++blk) store_blk(suf + (blk >> 1) * 64 * WK + (blk & 1) * 64, WK, Sf[blk]);
+    load_rows64_f32(Op[0], ws.kt + ((int64_t)bh * T + c * PC) * WK, WK);
+    load_rows64_f32(Op[1], ws.kt + ((int64_t)bh * T + c * PC) * WK + 64, WK);
+    __syncthreads();
+    // KL_c[r][d] = sum_e k~[r][e] SUF[d][e]
+#pragma unroll 1
+    for (int dh = 0; dh < 2; ++dh) {
+      f32x16 a = mgemm64<false, true>(Op[0], Sf[2 * dh], z);
+      a = mgemm64<false, true>(Op[1], Sf[2 * dh + 1], a);
+      bf16* dst = ws.kl + ((int64_t)bh * T + c * PC) * WK + 64 * dh;
+      const int cl = dl_col();
+      DL_FOR_E dst[dl_row(e) * WK + cl] = (bf16)a[e];
+    }
+    __syncthreads();
+    const float* hc = ws.hc + ((int64_t)bh * NT + c) * (WK * WK);
+#pragma unroll 1
+    for (int blk = 0; blk < 4; ++blk) load_blk(Op[blk], hc + (blk >> 1) * 64 * WK + (blk & 1) * 64, WK);
+    __syncthreads();
+    f32x16 nb[4];
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk) {
+      const int ra = blk >> 1, cb_ = blk & 1;
+      nb[blk] = mgemm64<false, false>(Sf[2 * ra], Op[cb_], z);
+      nb[blk] = mgemm64<false, false>(Sf[2 * ra + 1], Op[2 + cb_], nb[blk]);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk) dl_store(Sf[blk], nb[blk], 0);
+    __syncthreads();
+  }
+  float* hl = ws.hl + ((int64_t)bh * NS + s) * (WK * WK);
+#pragma unroll 1
+  for (int blk = 0; blk < 4; ++blk) store_blk(hl + (blk >> 1) * 64 * WK + (blk & 1) * 64, WK, Sf[blk]);
+}
+
+// x <- x M for rows [r0, r0 + 32 nrt) of X [rows][128] (fp32 LDS) with M^T in MT
+// (MT[n][k] = M[k][n]): output tile (value tile dt, row tile rt) in D layout (m = column
+// of the product, lane <-> row), 3-term bf16 split products over the 128 columns
+__device__ __forceinline__ f32x16 mat_xM128_tile(const float (*X)[132], const float (*MT)[132], int dt, int rt) {
+  const int lane = threadIdx.x & 63, g = lane >> 5, l32 = lane & 31;
+  f32x16 o = zero16();
+#pragma unroll
+  for (int st = 0; st < 8; ++st) {
+    bf16x8 ah, al, bh8, bl;
+    split8(&MT[dt * 32 + l32][16 * st + 8 * g], ah, al);
+    split8(&X[rt * 32 + l32][16 * st + 8 * g], bh8, bl);
+    o = mfma32(ah, bh8, o);
+    o = mfma32(ah, bl, o);
+    o = mfma32(al, bh8, o);
+  }
+  return o;
+}
+
+// M^T of a 128 x 128 fp32 row-major matrix into LDS (MT[c][r] = M[r][c]); TR = false: M itself
+template <bool TR>
+__device__ __forceinline__ void load_mat128(float (*dst)[132], const float* __restrict__ src) {
+  for (int idx = threadIdx.x; idx < WK * WK / 4; idx += 256) {
+    const int r = idx >> 5, c4 = (idx & 31) * 4;
+    const f32x4 v = *reinterpret_cast<const f32x4*>(src + r * WK + c4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (TR)
+        dst[c4 + e][r] = v[e];
+      else
+        dst[r][c4 + e] = v[e];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Query transport at K = 128 (path_transport_kernel's algebra: QS slots inside the large
+// chunk, then QB for every earlier large chunk), one workgroup per pair of chunks
+// A = 2p, B = 2p + 1; wave w computes value tile w of every row tile.  grid (B*HQ, ceil(NT/2))
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void path_transport128_kernel(int HQ, int H, int T, PathFwdWs ws) {
+  __shared__ __attribute__((aligned(16))) float X[128][132];  // rows 0..63 = chunk A, 64..127 = chunk B
+  __shared__ __attribute__((aligned(16))) float MT[128][132];
+  const int p = (int)gridDim.y - 1 - (int)blockIdx.y, bhq = blockIdx.x;
+  const int NT = T / PC, NS = (NT + PR - 1) / PR;
+  const int G = HQ / H;
+  const int b = bhq / HQ, hq = bhq - b * HQ, bh = b * H + hq / G;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 5, l32 = lane & 31;
+  const int A = 2 * p;
+  const bool hasB = A + 1 < NT;
+  const int sI = A / PR, cb = sI * PR;
+  {
+    const float* src = ws.qt + ((int64_t)bhq * T + A * PC) * WK;  // A's and B's rows are adjacent
+    for (int idx = tid; idx < (hasB ? 128 : 64) * 32; idx += 256) {
+      const int r = idx >> 5, c4 = (idx & 31) * 4;
+      *reinterpret_cast<f32x4*>(&X[r][c4]) = *reinterpret_cast<const f32x4*>(src + (int64_t)r * WK + c4);
+    }
+  }
+  auto emit = [&](bf16* dst, int r0, int nblk) {  // rows r0 .. r0 + 64 nblk of X -> bf16 rows (stride 128)
+    for (int idx = tid; idx < 64 * nblk * 16; idx += 256) {
+      const int r = r0 + (idx >> 4), c8 = (idx & 15) * 8;
+      bf16x8 v;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = (bf16)X[r][c8 + e];
+      *reinterpret_cast<bf16x8*>(dst + (int64_t)r * WK + c8) = v;
+    }
+  };
+  const int nq = A - cb, nsteps = nq + sI;
+  auto mat = [&](int j) {  // j = -1: Hc_A, B's own first step
+    return (j < nq) ? ws.hc + ((int64_t)bh * NT + (A - 1 - j)) * (WK * WK)
+                    : ws.hl + ((int64_t)bh * NS + (sI - 1 - (j - nq))) * (WK * WK);
+  };
+  auto slot = [&](int j) {  // destination of the rows emitted before step j (row 0 = chunk A's first row)
+    return ((j < nq) ? ws.qs + (((int64_t)bhq * PR + (A - 1 - j - cb)) * T) * WK
+                     : ws.qb + (((int64_t)bhq * NS + (sI - 1 - (j - nq))) * T) * WK) +
+           (int64_t)A * PC * WK;
+  };
+  // rows [rt0, rt0 + 32 nrt) of X <- X M (every wave: value tile w)
+  auto step = [&](int rt0, int nrt) {
+    f32x16 o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (i < nrt) o[i] = mat_xM128_tile(X, MT, w, rt0 + i);
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (i < nrt) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) X[(rt0 + i) * 32 + l32][w * 32 + drow(e, g)] = o[i][e];
+      }
+    __syncthreads();
+  };
+  if (hasB) {  // B's own first step: emit to QS slot A - cb, then X_B <- X_B Hc_A
+    load_mat128<true>(MT, mat(-1));
+    __syncthreads();
+    emit(ws.qs + (((int64_t)bhq * PR + (A - cb)) * T) * WK + (int64_t)A * PC * WK, 64, 1);
+    step(2, 2);
+  }
+  const int nblk = hasB ? 2 : 1;
+#pragma unroll 1
+  for (int j = 0; j < nsteps; ++j) {
+    load_mat128<true>(MT, mat(j));
+    emit(slot(j), 0, nblk);
+    __syncthreads();
+    step(0, 2 * nblk);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// k_cache at K = 128 (path_kcache_kernel's algebra): x = KL_J; x <- x HL_s^T for every
+// later large chunk.  grid (NT, B*H)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void path_kcache128_kernel(int T, bf16* __restrict__ kc, Strides kcs, int H,
+                                                             PathFwdWs ws) {
+  __shared__ __attribute__((aligned(16))) float X[64][132];
+  __shared__ __attribute__((aligned(16))) float MT[128][132];
+  const int J = blockIdx.x, bh = blockIdx.y;
+  const int b = bh / H, h = bh - b * H;
+  const int NT = T / PC, NS = (NT + PR - 1) / PR;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 5, l32 = lane & 31;
+  for (int idx = tid; idx < 64 * 16; idx += 256) {
+    const int r = idx >> 4, c8 = (idx & 15) * 8;
+    const bf16x8 v = ld8(ws.kl + ((int64_t)bh * T + J * PC + r) * WK + c8);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) X[r][c8 + e] = (float)v[e];
+  }
+  __syncthreads();
+#pragma unroll 1
+  for (int s = J / PR + 1; s < NS; ++s) {
+    load_mat128<false>(MT, ws.hl + ((int64_t)bh * NS + s) * (WK * WK));  // (HL^T)^T = HL
+    __syncthreads();
+    f32x16 o[2];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) o[rt] = mat_xM128_tile(X, MT, w, rt);
+    __syncthreads();
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) X[rt * 32 + l32][w * 32 + drow(e, g)] = o[rt][e];
+    __syncthreads();
+  }
+  for (int idx = tid; idx < 64 * 16; idx += 256) {
+    const int r = idx >> 4, c8 = (idx & 15) * 8;
+    bf16x8 v;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = (bf16)X[r][c8 + e];
+    *reinterpret_cast<bf16x8*>(kc + b * kcs.b + h * kcs.h + (int64_t)(J * PC + r) * kcs.t + c8) = v;
+  }
+}
+
+}  // namespace lucid

@@ -15,10 +15,10 @@ reference ships as the kernels ``intra_chunk_preprocess_fwd.py`` and
     O_i = sum_{j <= i} softmax_j(s A_ij) v_j
 
 Tensors are bf16 GPU tensors in the reference layout ``[B, T, H, K]``; the kernels run at
-K = V = 64, and head dims 16 and 32 (the other sizes the reference's kernels take below
-128) run on rows zero-padded to 64: the reflections ``I - beta w w^T`` act as the identity
-on the padded coordinates, so the logits, O and the gradients of the real coordinates are
-unchanged.  There is no CPU or Triton fallback.
+K = V = 64 and K = V = 128, and the other head dims the reference's kernels take (16, 32;
+a K/V pair that differs) run on rows zero-padded to the next of the two: the reflections
+``I - beta w w^T`` act as the identity on the padded coordinates, so the logits, O and the
+gradients of the real coordinates are unchanged.  There is no CPU or Triton fallback.
 """
 from __future__ import annotations
 
@@ -159,8 +159,6 @@ def _check(q, k, v, w, beta, g):
     assert beta.shape[:3] == k.shape[:3], 'beta should have the same number of heads as k'
     assert g is None, 'g is not supported'
     assert q.shape[-2] % k.shape[-2] == 0, 'the number of query heads should be divisible by the number of key heads'
-    if q.shape[-1] > _KD or v.shape[-1] > _KD:
-        raise NotImplementedError("lucid_amd LUCID-Path kernels support head_dim 16, 32 and 64")
     for name, x in (("q", q), ("k", k), ("v", v), ("w", w), ("beta", beta)):
         if not x.is_cuda:
             raise RuntimeError(f"lucid_amd: {name} must be a GPU tensor (no CPU path)")
@@ -168,18 +166,20 @@ def _check(q, k, v, w, beta, g):
             raise TypeError(f"lucid_amd: {name} must be bfloat16, got {x.dtype}")
 
 
-_KD = 64  # head dim of the kernels (q, k, w and v rows)
+_KDS = (64, 128)  # head dims of the kernels (q, k, w and v rows share one)
 
 
-def _pad_d(x: torch.Tensor) -> torch.Tensor:
-    """Zero-pad the head axis (last) to the kernels' 64 columns (differentiable)."""
-    return x if x.shape[-1] == _KD else F.pad(x, (0, _KD - x.shape[-1]))
+def _pad_d(x: torch.Tensor, kd: int) -> torch.Tensor:
+    """Zero-pad the head axis (last) to the kernels' kd columns (differentiable)."""
+    return x if x.shape[-1] == kd else F.pad(x, (0, kd - x.shape[-1]))
 
 
 def _apply(fn, q, k, v, w, beta, g, scale, cu_seqlens, use_cache):
     kd, vd = k.shape[-1], v.shape[-1]
-    if kd != _KD or vd != _KD:
-        o, kc = _apply(fn, _pad_d(q), _pad_d(k), _pad_d(v), _pad_d(w), beta, g, scale, cu_seqlens, use_cache)
+    kk = _KDS[0] if max(kd, vd) <= _KDS[0] else _KDS[1]
+    if kd != kk or vd != kk:
+        pd = lambda x: _pad_d(x, kk)  # noqa: E731
+        o, kc = _apply(fn, pd(q), pd(k), pd(v), pd(w), beta, g, scale, cu_seqlens, use_cache)
         return o[..., :vd], (kc[..., :kd] if kc is not None else None)
     if q.shape[1] == 0 or q.numel() == 0:  # empty: empty results, as the reference's ops give
         o = q.new_zeros(*q.shape[:3], v.shape[-1]) + 0 * (q.sum() + k.sum() + v.sum() + w.sum() + beta.sum())

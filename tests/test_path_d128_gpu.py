@@ -1,0 +1,79 @@
+"""GPU parity of LUCID-Path and PaTH softmax attention on the head-dim-128 kernels.
+
+The reference entry point takes head dim 128 for q/k/w and for v
+(lucid_path/triton_code/parallel.py:230-232).  Here K = V = 128 runs on its own kernels
+(128 x 128 transport products, 128-wide query transport and solve), and a K/V pair whose
+larger member exceeds 64 runs on rows zero-padded to 128.  Oracles: the float64 chunked
+restatement (oracle/path_ref.py) on the CPU for short sequences, the float64 dense oracle
+(oracle/path_dense.py, pinned in tests/test_oracle_path_dense.py) on the GPU for long ones;
+the decode key cache against the brute-force reflection product.  Bars: tests/bars.py
+(bf16 against float64 on the same bf16-rounded inputs).
+"""
+import pytest
+import torch
+
+from bars import check
+from oracle import path_dense as PD
+from oracle import path_ref as P
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(B, T, H, G, K, V, seed):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, T, H * G, K, generator=g)
+    k = torch.randn(B, T, H, K, generator=g)
+    v = torch.randn(B, T, H, V, generator=g)
+    w = torch.randn(B, T, H, K, generator=g)
+    w = w / w.norm(dim=-1, keepdim=True)
+    beta = 2 * torch.sigmoid(torch.randn(B, T, H, generator=g))
+    do = torch.randn(B, T, H * G, V, generator=g)
+    return [x.to(torch.bfloat16) for x in (q, k, v, w, beta, do)]
+
+
+def _f64(x):
+    return x.detach().cpu().double()
+
+
+def _pad_t(x, Tp):
+    return torch.nn.functional.pad(_f64(x), [0, 0] * (x.dim() - 2) + [0, Tp - x.shape[1]])
+
+
+@pytest.mark.parametrize("B,T,H,G,K,V", [(1, 256, 1, 1, 128, 128), (2, 192, 2, 2, 128, 128),
+                                         (1, 200, 1, 1, 64, 128), (1, 128, 2, 1, 128, 32)])
+def test_lucid_path_d128_forward_short(B, T, H, G, K, V):
+    from lucid_amd.lucid_path import parallel_lucid_path_attention
+    q, k, v, w, beta, _ = _inputs(B, T, H, G, K, V, seed=11 * T + K + V)
+    print(f"case path d128 fwd B={B} T={T} H={H} G={G} K={K} V={V}", flush=True)
+    with torch.no_grad():
+        o, kc = parallel_lucid_path_attention(k.cuda(), v.cuda(), w.cuda(), beta.cuda(), q=q.cuda(),
+                                              use_cache=True)
+    torch.cuda.synchronize()
+    assert o.shape == (B, T, H * G, V) and kc.shape == (B, T, H, K)
+    Tp = (T + 63) // 64 * 64
+    ref = P.path_attention_chunked(*(_pad_t(x, Tp) for x in (q, k, v, w, beta)), scale=K ** -0.5, C=64)[:, :T]
+    err = (o.cpu().double() - ref).abs().max().item()
+    print(f"  o: max err {err:.2e} max|ref| {ref.abs().max().item():.2e}", flush=True)
+    check("o", err, ref.abs().max().item())
+    kc_ref = P.path_kcache_bruteforce(_f64(k), _f64(w), _f64(beta))
+    err = (kc.cpu().double() - kc_ref).abs().max().item()
+    print(f"  k_cache: max err {err:.2e} max|ref| {kc_ref.abs().max().item():.2e}", flush=True)
+    check("k_cache", err, kc_ref.abs().max().item())
+
+
+@pytest.mark.parametrize("B,T,H,G", [(1, 1024, 2, 2), (1, 8192, 1, 1)])
+def test_lucid_path_d128_forward_long(B, T, H, G):
+    """Several super-chunks (S = 512 positions): the large-chunk products, the query transport
+    across super-chunks and the chained solve over up to 128 chunks."""
+    from lucid_amd.lucid_path import parallel_lucid_path_attention
+    q, k, v, w, beta, _ = (x.cuda() for x in _inputs(B, T, H, G, 128, 128, seed=T + G))
+    print(f"case path d128 fwd long B={B} T={T} H={H} G={G}", flush=True)
+    with torch.no_grad():
+        o, _ = parallel_lucid_path_attention(k, v, w, beta, q=q)
+    torch.cuda.synchronize()
+    heads = range(H * G) if T <= 1024 else [0]
+    ref = PD.path_attention_dense(q, k, v, w, beta, scale=128 ** -0.5, heads=heads)
+    for hq in heads:
+        err = (o[:, :, hq].double() - ref[:, :, hq]).abs().max().item()
+        print(f"  head {hq} o: max err {err:.2e} max|ref| {ref[:, :, hq].abs().max().item():.2e}", flush=True)
+        check(f"o[{hq}]", err, ref[:, :, hq].abs().max().item())

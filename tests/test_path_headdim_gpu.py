@@ -87,11 +87,9 @@ def test_path_softmax_small_head_dims(B, T, H, G, K, V):
         check(name, err, r.abs().max().item())
 
 
-def test_lucid_path_rejects_head_dim_128():
-    """Head dim 128 passes the reference's asserts but has no kernels here: it raises."""
+def test_lucid_path_rejects_unsupported_head_dim():
+    """A head dim outside the reference's [16, 32, 64, 128] fails its assert."""
     from lucid_amd.lucid_path import parallel_lucid_path_attention
-    q, k, v, w, beta, _ = _inputs(1, 64, 1, 1, 128, 128, seed=1)
-    with pytest.raises(NotImplementedError, match="head_dim"):
-        parallel_lucid_path_attention(k.cuda(), v.cuda(), w.cuda(), beta.cuda(), q=q.cuda())
+    q, k, v, w, beta, _ = _inputs(1, 64, 1, 1, 48, 48, seed=1)
     with pytest.raises(AssertionError, match="only support head_dim"):
-        parallel_lucid_path_attention(k[..., :48].cuda(), v[..., :48].cuda(), w[..., :48].cuda(), beta.cuda())
+        parallel_lucid_path_attention(k.cuda(), v.cuda(), w.cuda(), beta.cuda(), q=q.cuda())
