@@ -6,7 +6,7 @@
  *   A_ij = q_i^T H_i ... H_{j+1} k_j,  H_t = I - beta_t w_t w_t^T.
  * Layouts as the reference: q [B,T,HQ,K], k/w [B,T,H,K], v [B,T,H,V], beta [B,T,H],
  * o [B,T,HQ,V]; element strides {batch, head, time}, last axis contiguous.
- * bf16 tensors; K = V = 64, or K = V = 128 (LUCID-Path forward); T a multiple of 64
+ * bf16 tensors; K = V = 64, or K = V = 128 (LUCID-Path); T a multiple of 64
  * (the Python layer zero-pads the
  * sequence end, exact for every real row since L is strictly lower triangular).
  * Buffers are caller-owned (no device allocation; the bounded chain waits set up a 4-byte

@@ -19,19 +19,20 @@
 
 namespace lucid {
 
+// K: the kernels' head dim (64 or 128)
 struct PathBwdWs {
-  float* dvf;   // [BHq][T][64]       dV (fp32)
-  bf16* dvb;    // [BHq][T][64]       dV rows (bf16)
-  bf16* dvT;    // [BHq][64][T]       dV^T, T-perm (chain operand)
+  float* dvf;   // [BHq][T][K]        dV (fp32)
+  bf16* dvb;    // [BHq][T][K]        dV rows (bf16)
+  bf16* dvT;    // [BHq][K][T]        dV^T, T-perm (chain operand)
   float* dad;   // [BHq][NT][64][64]  dA_diag
-  float* dqt;   // [BHq][T][64]       d q~
-  float* dkt;   // [BHq][T][64]       d k~
-  float* dsuf;  // [BHq][NT][64][64]  d SUF
-  float* dhl;   // [BHq][NS][64][64]  d HL  (atomics)
-  float* dhc;   // [BHq][NT][64][64]  d Hc  (atomics + products backward)
-  float* dq;    // [BHq][T][64]
-  float* dk;    // [BHq][T][64]       per query head, summed over the group at the end
-  float* dw;    // [BHq][T][64]
+  float* dqt;   // [BHq][T][K]        d q~
+  float* dkt;   // [BHq][T][K]        d k~
+  float* dsuf;  // [BHq][NT][K][K]    d SUF
+  float* dhl;   // [BHq][NS][K][K]    d HL  (atomics)
+  float* dhc;   // [BHq][NT][K][K]    d Hc  (atomics + products backward)
+  float* dq;    // [BHq][T][K]
+  float* dk;    // [BHq][T][K]        per query head, summed over the group at the end
+  float* dw;    // [BHq][T][K]
   float* db;    // [BHq][T]
   int* counters;  // [BHq]
   float* delta; // [BHq][T]           PaTH softmax only: rowsum(dO * O)
@@ -63,25 +64,30 @@ __global__ __launch_bounds__(256) void path_bwd_zero_kernel(int64_t n_hl, int64_
 // depends on the operands only and is computed before the sweep; the fp32 buffers
 // of the final step reuse the staging space.
 // ---------------------------------------------------------------------------
+template <int KD>
 struct DvSmem {
   union {
     struct {
-      bf16 q[2][2][64 * 64];  // [buffer][tile of the pair, or column chunk], swizzled (chunk c of row r at c ^ (r & 7))
-      bf16 d[2][2][64 * 64];
+      bf16 q[2][2][64 * KD];  // [buffer][tile of the pair, or column chunk], swizzled (chunk c of row r at c ^ (r & 7))
+      bf16 d[2][2][KD * 64];
     } st;
     struct {
-      float Rt[64][132];    // R^T for the 128 columns (0..63 = A), then dV rows of one chunk
+      float Rt[KD][132];    // R^T for the 128 columns (0..63 = A), then dV rows of one chunk
       float Yt[64][68];     // Yt[c][r] = Y[r][c] of the chunk being solved, then O rows
-      bf16 dt[64][128 + 8];  // dV^T of both chunks, T-perm within 16-groups
+      bf16 dt[KD][128 + 8];  // dV^T of both chunks, T-perm within 16-groups
     } fin;
   } u;
   bf16x8 lba[4][64][2];  // L_BA as MFMA B operands, per wave and lane
 };
 
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void path_dv_kernel(const bf16* __restrict__ dout, Strides dos,
+// KD: head dim (64 or 128); at 128 a wave owns value tiles w >> 1 and (w >> 1) + 2 of the
+// final solve, and dA_diag is summed over the two 64-column halves of dV and O
+template <int KD>
+__global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_dv_kernel(const bf16* __restrict__ dout, Strides dos,
                                                       const bf16* __restrict__ o, Strides os, int HQ, int H, int T,
                                                       int BHq, float scale, PathFwdWs ws, PathBwdWs bw) {
-  __shared__ __attribute__((aligned(16))) DvSmem sm;
+  constexpr int NKS = KD / 16, NVT = KD / 32;  // k-steps of a logit product, 32-column value tiles
+  __shared__ __attribute__((aligned(16))) DvSmem<KD> sm;
   const int NT = T / PC, NS = (NT + PR - 1) / PR, NQ = (NT + 1) / 2;
   const int id = blockIdx.x;
   const int q = NQ - 1 - id / BHq, bhq = id - (id / BHq) * BHq;
@@ -99,18 +105,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
   int* cnt = bw.counters + bhq;
   const float sl2 = scale * LOG2E_F, cc0 = LOG2E_F / scale;
 
-  bf16x8 kbs[4], kbf[4];
+  bf16x8 kbs[NKS], kbf[NKS];
 #pragma unroll
-  for (int st = 0; st < 4; ++st) {
-    kbs[st] = ld8(ws.kt + ((int64_t)bh * T + jc) * 64 + 16 * st + 8 * g);
-    kbf[st] = ld8(ws.kl + ((int64_t)bh * T + jc) * 64 + 16 * st + 8 * g);
+  for (int st = 0; st < NKS; ++st) {
+    kbs[st] = ld8(ws.kt + ((int64_t)bh * T + jc) * KD + 16 * st + 8 * g);
+    kbf[st] = ld8(ws.kl + ((int64_t)bh * T + jc) * KD + 16 * st + 8 * g);
   }
   // accumulators start at -dO^T (R = dO - acc = -acc)
-  f32x16 acc[2];
+  f32x16 acc[NVT];
   {
     const bf16* drow_ = dout + b * dos.b + hq * dos.h + (int64_t)jc * dos.t;
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < NVT; ++t)
 #pragma unroll
       for (int qq = 0; qq < 4; ++qq) {
         const bf16x4 x = *reinterpret_cast<const bf16x4*>(drow_ + t * 32 + 8 * qq + 4 * g);
@@ -119,15 +125,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
       }
   }
   // QS slot of column chunk c (relative to the large chunk) for row chunk I inside it
-  auto qs_slot = [&](int c) { return ws.qs + ((int64_t)bhq * PR + (A + c - cb)) * T * 64; };
+  auto qs_slot = [&](int c) { return ws.qs + ((int64_t)bhq * PR + (A + c - cb)) * T * KD; };
   // L_BA (rows of B half kb, columns of A half na): Qop = QS slot A - cb of B's rows, Kop_A = k~_A
   if (hasB) {
     const int na = w & 1, kb = w >> 1;
-    const bf16* qr = qs_slot(0) + (int64_t)((A + 1) * PC + kb * 32 + l32) * 64;
-    const bf16* kr = ws.kt + ((int64_t)bh * T + j0 + na * 32 + l32) * 64;
+    const bf16* qr = qs_slot(0) + (int64_t)((A + 1) * PC + kb * 32 + l32) * KD;
+    const bf16* kr = ws.kt + ((int64_t)bh * T + j0 + na * 32 + l32) * KD;
     f32x16 sc = zero16();
 #pragma unroll
-    for (int st = 0; st < 4; ++st) sc = mfma32(ld8(qr + 16 * st + 8 * g), ld8(kr + 16 * st + 8 * g), sc);
+    for (int st = 0; st < NKS; ++st) sc = mfma32(ld8(qr + 16 * st + 8 * g), ld8(kr + 16 * st + 8 * g), sc);
 #pragma unroll
     for (int e = 0; e < 16; ++e) sc[e] = __builtin_amdgcn_exp2f(fmaf(sc[e], sl2, -cc0));
     sm.lba[w][lane][0] = pack_b(sc, 0);
@@ -139,9 +145,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
   const int nfs = (nfar + 1) / 2, nsteps = nfs + (n - nfar);
   auto first_tile = [&](int s) { return s < nfs ? 2 * s : nfar + (s - nfs); };
   auto need = [&](int s) { return s < nfs ? min(2 * s + 1, nfar - 1) : first_tile(s); };
-  int plan_q[2], plan_t[2];
-  dma_plan<64, 8>(64, plan_q);
-  dma_plan<64, 8>(T, plan_t);
+  int plan_q[64 * (KD / 8) / 256], plan_t[KD * 8 / 256];
+  dma_plan<64, KD / 8>(KD, plan_q);
+  dma_plan<KD, 8>(T, plan_t);
   auto stage = [&](int s) {
     const int buf = s & 1, k0 = first_tile(s);
     if (s < nfs) {
@@ -150,16 +156,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
         const int k = k0 + u;
         if (k < nfar) {
           const int I = NT - 1 - k;
-          dma_stage<64, 8>(plan_q, ws.qb + (((int64_t)bhq * NS + sJ) * T + (int64_t)I * PC) * 64, sm.u.st.q[buf][u]);
-          dma_stage<64, 8>(plan_t, bw.dvT + (int64_t)bhq * 64 * T + I * PC, sm.u.st.d[buf][u]);
+          dma_stage<64, KD / 8>(plan_q, ws.qb + (((int64_t)bhq * NS + sJ) * T + (int64_t)I * PC) * KD,
+                                sm.u.st.q[buf][u]);
+          dma_stage<KD, 8>(plan_t, bw.dvT + (int64_t)bhq * KD * T + I * PC, sm.u.st.d[buf][u]);
         }
       }
     } else {
       const int I = NT - 1 - k0;
 #pragma unroll
       for (int c = 0; c < 2; ++c)
-        if (c == 0 || hasB) dma_stage<64, 8>(plan_q, qs_slot(c) + (int64_t)I * PC * 64, sm.u.st.q[buf][c]);
-      dma_stage<64, 8>(plan_t, bw.dvT + (int64_t)bhq * 64 * T + I * PC, sm.u.st.d[buf][0]);
+        if (c == 0 || hasB) dma_stage<64, KD / 8>(plan_q, qs_slot(c) + (int64_t)I * PC * KD, sm.u.st.q[buf][c]);
+      dma_stage<KD, 8>(plan_t, bw.dvT + (int64_t)bhq * KD * T + I * PC, sm.u.st.d[buf][0]);
     }
   };
   // Y_A, Y_B (fp32) are fetched into registers during the last step
@@ -186,12 +193,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
     for (int rh = 0; rh < 2; ++rh) {
       f32x16 sc = zero16();
 #pragma unroll
-      for (int st = 0; st < 4; ++st) sc = mfma32(ld8(swz<8>(qt, rh * 32 + l32, 2 * st + g)), same ? kbs[st] : kbf[st], sc);
+      for (int st = 0; st < NKS; ++st)
+        sc = mfma32(ld8(swz<KD / 8>(qt, rh * 32 + l32, 2 * st + g)), same ? kbs[st] : kbf[st], sc);
 #pragma unroll
       for (int e = 0; e < 16; ++e) sc[e] = __builtin_amdgcn_exp2f(fmaf(sc[e], sl2, -cc0));
       const bf16x8 p0 = pack_b(sc, 0), p1 = pack_b(sc, 1);
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
+      for (int t = 0; t < NVT; ++t) {
         acc[t] = mfma32(ld8(swz<8>(dtl, t * 32 + l32, 4 * rh + g)), p0, acc[t]);
         acc[t] = mfma32(ld8(swz<8>(dtl, t * 32 + l32, 4 * rh + 2 + g)), p1, acc[t]);
       }
@@ -242,15 +250,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
   float(*Yt)[68] = sm.u.fin.Yt;
   if (mycols) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < NVT; ++t)
 #pragma unroll
       for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][w * 32 + l32] = -acc[t][e];
   }
   ystore_t(hasB ? 1 : 0);
   __syncthreads();
-  // dV^T[d][c] = sum_r R^T[d][r] Y[r][c] for chunk cc (Y lower: r >= c); wave -> (d tile, column half)
-  const int dt = w >> 1, chh = w & 1;
-  auto diag_solve = [&](int cc) {
+  // dV^T[d][c] = sum_r R^T[d][r] Y[r][c] for chunk cc (Y lower: r >= c); wave -> (d tiles
+  // dt0 + 2 i, column half); returns the wave's tiles in D layout
+  const int dt0 = w >> 1, chh = w & 1;
+  auto diag_solve = [&](int cc, f32x16* dvs) {
+#pragma unroll
+   for (int i = 0; i < NVT / 2; ++i) {
+    const int dt = dt0 + 2 * i;
     f32x16 dvo = zero16();
     for (int st = chh ? 2 : 0; st < 4; ++st) {
       bf16x8 ah, al, bh8, bl;
@@ -263,8 +275,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
     const int cl = chh * 32 + l32;
     const int r = j0 + cc * 64 + cl;
     const int lslot = cc * 64 + ((cl & ~15) | jmap(cl & 15));
-    float* of = bw.dvf + ((int64_t)bhq * T + r) * 64;
-    bf16* ob = bw.dvb + ((int64_t)bhq * T + r) * 64;
+    float* of = bw.dvf + ((int64_t)bhq * T + r) * KD;
+    bf16* ob = bw.dvb + ((int64_t)bhq * T + r) * KD;
 #pragma unroll
     for (int qq = 0; qq < 4; ++qq) {
       const int d0 = dt * 32 + 8 * qq + 4 * g;
@@ -279,35 +291,36 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
       *reinterpret_cast<f32x4*>(of + d0) = f;
       *reinterpret_cast<bf16x4*>(ob + d0) = bb;
     }
-    return dvo;
+    dvs[i] = dvo;
+   }
   };
   // dV^T of chunk cc to the chain operand with 16-byte stores, then publish it
   auto publish_chunk = [&](int cc) {
     __syncthreads();
-    for (int c = tid; c < 64 * 8; c += 256) {
+    for (int c = tid; c < KD * 8; c += 256) {
       const int dd = c >> 3, s8 = (c & 7) * 8;
-      *reinterpret_cast<bf16x8*>(bw.dvT + ((int64_t)bhq * 64 + dd) * T + j0 + cc * 64 + s8) =
+      *reinterpret_cast<bf16x8*>(bw.dvT + ((int64_t)bhq * KD + dd) * T + j0 + cc * 64 + s8) =
           ld8(&sm.u.fin.dt[dd][cc * 64 + s8]);
     }
     publish_counter(cnt, NT - (A + cc));
   };
-  f32x16 dvoB = zero16();
+  f32x16 dvoB[NVT / 2], dvoA[NVT / 2];
   if (hasB) {
-    dvoB = diag_solve(1);
+    diag_solve(1, dvoB);
     publish_chunk(1);
     // ---- R_A -= L_BA^T dV_B: wave -> (A columns half na, B rows half kb); Y_A^T to LDS ----
     const int na = w & 1, kb = w >> 1;
     const bf16x8 l0 = sm.lba[w][lane][0], l1 = sm.lba[w][lane][1];
-    f32x16 cr[2];
+    f32x16 cr[NVT];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
+    for (int t = 0; t < NVT; ++t) {
       cr[t] = mfma32(ld8(&sm.u.fin.dt[t * 32 + l32][64 + kb * 32 + 8 * g]), l0, zero16());
       cr[t] = mfma32(ld8(&sm.u.fin.dt[t * 32 + l32][64 + kb * 32 + 16 + 8 * g]), l1, cr[t]);
     }
     const int col = na * 32 + l32;
     if (kb == 1) {
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+      for (int t = 0; t < NVT; ++t)
 #pragma unroll
         for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][col] -= cr[t][e];
     }
@@ -315,23 +328,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
     __syncthreads();
     if (kb == 0) {
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+      for (int t = 0; t < NVT; ++t)
 #pragma unroll
         for (int e = 0; e < 16; ++e) Rt[t * 32 + drow(e, g)][col] -= cr[t][e];
     }
     __syncthreads();
   }
-  const f32x16 dvoA = diag_solve(0);
+  diag_solve(0, dvoA);
   publish_chunk(0);
-  // ---- dA_diag = -s (dV_J O_J^T) * L_diag per chunk (every read of Rt / Yt came before the last barrier) ----
+  // ---- dA_diag = -s (dV_J O_J^T) * L_diag per chunk (every read of Rt / Yt came before the last
+  // barrier), summed over the 64-column halves of dV and O ----
   float(*Dr)[68] = reinterpret_cast<float(*)[68]>(&sm.u.fin.Rt[0][0]);  // dV rows of the chunk
   for (int cc = 0; cc < (hasB ? 2 : 1); ++cc) {
-    const f32x16 dvo = cc ? dvoB : dvoA;
+    f32x16 a = zero16();
 #pragma unroll
-    for (int e = 0; e < 16; ++e) Dr[chh * 32 + l32][dt * 32 + drow(e, g)] = dvo[e];
-    load_rows64_f32(Yt, o + b * os.b + hq * os.h + (int64_t)(j0 + cc * 64) * os.t, os.t);  // Yt <- O rows
-    __syncthreads();
-    const f32x16 a = mgemm64<false, true>(Dr, Yt, zero16());
+    for (int i = 0; i < NVT / 2; ++i) {
+      const f32x16 dvo = cc ? dvoB[i] : dvoA[i];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) Dr[chh * 32 + l32][dt0 * 32 + drow(e, g)] = dvo[e];
+      load_rows64_f32(Yt, o + b * os.b + hq * os.h + (int64_t)(j0 + cc * 64) * os.t + 64 * i, os.t);  // O rows
+      __syncthreads();
+      a = mgemm64<false, true>(Dr, Yt, a);
+      if (i + 1 < NVT / 2) __syncthreads();
+    }
     const float* ldp = ws.ld + ((int64_t)bhq * NT + A + cc) * 4096;
     float* dst = bw.dad + ((int64_t)bhq * NT + A + cc) * 4096;
     const int cl = dl_col();
@@ -360,17 +379,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
 // with X = dV, Y = O (rows of the same query head); PaTH softmax (SM = true)
 // dA = s P (X_I Y_J^T - delta_i), P = exp2(s' S - lse_i), X = dO, Y = V (kv head).
 // ---------------------------------------------------------------------------
+template <int KD>
 struct RowSmem {
-  bf16 k[2][64 * 64];  // swizzled (chunk c of row r at c ^ (r & 7))
-  bf16 o[2][64 * 64];
-  float g[128][68];    // G rows of the pair at a transport step
+  bf16 k[2][64 * KD];  // swizzled (chunk c of row r at c ^ (r & 7))
+  bf16 o[2][64 * KD];
+  float g[128][KD + 4];  // G rows of the pair at a transport step
 };
 
-template <bool SM>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void path_bwd_row_kernel(
+// KD: head dim (64 or 128); the KD x KD transport matrices and their gradients are row-major
+template <bool SM, int KD>
+__global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_bwd_row_kernel(
     const bf16* __restrict__ xsrc, Strides xs, const bf16* __restrict__ ysrc, Strides ys, int HQ, int H, int T,
     float scale, PathFwdWs ws, PathBwdWs bw) {
-  __shared__ __attribute__((aligned(16))) RowSmem sm;
+  constexpr int NKS = KD / 16, NVT = KD / 32, CPR = KD / 8;  // k-steps, 32-column tiles, 16-byte chunks per row
+  __shared__ __attribute__((aligned(16))) RowSmem<KD> sm;
   const int NT = T / PC, NS = (NT + PR - 1) / PR;
   const int I1 = 2 * ((int)gridDim.y - 1 - (int)blockIdx.y), bhq = blockIdx.x;  // heaviest pairs of all heads first
   const int G_ = HQ / H;
@@ -384,11 +406,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
   const int nJ = pair ? I1 + 1 : I1;                // key tiles needed by the pair
   const float sl2 = scale * LOG2E_F, cc0 = LOG2E_F / scale;
 
-  bf16x8 dvr[4];
+  bf16x8 dvr[NKS];
   {
     const bf16* xrow = xsrc + b * xs.b + hq * xs.h + (int64_t)(iw0 + l32) * xs.t;
 #pragma unroll
-    for (int st = 0; st < 4; ++st) dvr[st] = ld8(xrow + 16 * st + 8 * g);
+    for (int st = 0; st < NKS; ++st) dvr[st] = ld8(xrow + 16 * st + 8 * g);
   }
   // exponent offset and delta of this lane's row (LUCID-Path: the constant 1/s, no delta)
   const float ci = SM ? ws.lse[(int64_t)bhq * T + iw0 + l32] : cc0;
@@ -396,11 +418,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
   // dA = F dP exp2(sl2 S) (LUCID-Path, F = -s 2^-cc0) or F P (dP - delta) (PaTH softmax,
   // F = s): the constant F is carried out of the sweep by G (applied to dM and to d q~)
   const float F = SM ? scale : -scale * __builtin_amdgcn_exp2f(-cc0);
-  f32x16 acc[2] = {zero16(), zero16()};
+  f32x16 acc[NVT];
+#pragma unroll
+  for (int t = 0; t < NVT; ++t) acc[t] = zero16();
 
-  int plan_k[2], plan_o[2];
-  dma_plan<64, 8>(64, plan_k);
-  dma_plan<64, 8>(ys.t, plan_o);
+  int plan_k[64 * CPR / 256], plan_o[64 * CPR / 256];
+  dma_plan<64, CPR>(KD, plan_k);
+  dma_plan<64, CPR>(ys.t, plan_o);
   // ---- dM += X^T G over the pair's rows (atomic) and G <- G M^T for each wave's rows ----
   // X (rows of the query operand, row-major) is staged into the idle half of the double
   // buffer (tile J+1 is staged only after the transition); X^T comes from transposing reads
@@ -408,21 +432,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
     const bool act = Iw < NT && J < Iw;
     bf16* xa_t = sm.k[(J + 1) & 1];  // X rows of chunk I1
     bf16* xb_t = sm.o[(J + 1) & 1];  // X rows of chunk I1 + 1
-    dma_stage<64, 8>(plan_k, X + (int64_t)I1 * PC * 64, xa_t);
-    if (pair) dma_stage<64, 8>(plan_k, X + (int64_t)(I1 + 1) * PC * 64, xb_t);
+    dma_stage<64, CPR>(plan_k, X + (int64_t)I1 * PC * KD, xa_t);
+    if (pair) dma_stage<64, CPR>(plan_k, X + (int64_t)(I1 + 1) * PC * KD, xb_t);
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < NVT; ++t)
 #pragma unroll
       for (int e = 0; e < 16; ++e) sm.g[32 * w + l32][t * 32 + drow(e, g)] = act ? acc[t][e] : 0.f;
     dma_wait();
     __syncthreads();
-    {
-      const int at = w >> 1, bt = w & 1;  // dM tile (a rows, b cols)
+#pragma unroll 1
+    for (int tt = w; tt < NVT * NVT; tt += 4) {
+      const int at = tt / NVT, bt = tt % NVT;  // dM tile (a rows, b cols)
       f32x16 dm = zero16();
       // rows of a chunk that has left the sweep are skipped: its X rows may be undefined
       const int ks0 = (J < I1) ? 0 : 4, ks1 = (pair && J < I1 + 1) ? 8 : 4;
       for (int ks = ks0; ks < ks1; ++ks) {
-        const bf16x8 xa = lds_tr_a<8>(ks < 4 ? xa_t : xb_t, 16 * (ks & 3), at * 32);
+        const bf16x8 xa = lds_tr_a<CPR>(ks < 4 ? xa_t : xb_t, 16 * (ks & 3), at * 32);
         bf16x8 gh, gl;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -434,16 +459,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
         dm = mfma32(xa, gl, dm);
       }
 #pragma unroll
-      for (int e = 0; e < 16; ++e) unsafeAtomicAdd(dM + (at * 32 + drow(e, g)) * 64 + bt * 32 + l32, F * dm[e]);
+      for (int e = 0; e < 16; ++e) unsafeAtomicAdd(dM + (at * 32 + drow(e, g)) * KD + bt * 32 + l32, F * dm[e]);
     }
     if (act) {
 #pragma unroll
-      for (int bt = 0; bt < 2; ++bt) {
+      for (int bt = 0; bt < NVT; ++bt) {
         f32x16 gn = zero16();
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
+        for (int ks = 0; ks < NKS; ++ks) {
           bf16x8 ah, al, bh8, bl;
-          split8(M + (bt * 32 + l32) * 64 + 16 * ks + 8 * g, ah, al);
+          split8(M + (bt * 32 + l32) * KD + 16 * ks + 8 * g, ah, al);
           split8(&sm.g[32 * w + l32][16 * ks + 8 * g], bh8, bl);
           gn = mfma32(ah, bh8, gn);
           gn = mfma32(ah, bl, gn);
@@ -457,42 +482,42 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
 
   auto stage = [&](int J) {
     const int buf = J & 1;
-    const bf16* kr = ((J < cb) ? ws.kl : ws.kt) + ((int64_t)bh * T + J * PC) * 64;
-    dma_stage<64, 8>(plan_k, kr, sm.k[buf]);
-    dma_stage<64, 8>(plan_o, yh + (int64_t)J * PC * ys.t, sm.o[buf]);
+    const bf16* kr = ((J < cb) ? ws.kl : ws.kt) + ((int64_t)bh * T + J * PC) * KD;
+    dma_stage<64, CPR>(plan_k, kr, sm.k[buf]);
+    dma_stage<64, CPR>(plan_o, yh + (int64_t)J * PC * ys.t, sm.o[buf]);
   };
   if (nJ > 0) stage(0);
   dma_wait();
   __syncthreads();
-  bf16x8 qb[4];
+  bf16x8 qb[NKS];
   for (int J = 0; J < nJ; ++J) {
     const int buf = J & 1;
     // transport step before the first tile that uses a new query operand
     if (J < cb) {
       if (J % PR == 0 && J > 0) {
         const int s = J / PR;
-        transition(J, ws.qb + ((int64_t)bhq * NS + s) * T * 64, ws.hl + ((int64_t)bh * NS + s) * 4096,
-                   bw.dhl + ((int64_t)bhq * NS + s) * 4096);
+        transition(J, ws.qb + ((int64_t)bhq * NS + s) * T * KD, ws.hl + ((int64_t)bh * NS + s) * (KD * KD),
+                   bw.dhl + ((int64_t)bhq * NS + s) * (KD * KD));
       }
     } else if (sI > 0 || J > cb) {
-      transition(J, ws.qs + ((int64_t)bhq * PR + (J - cb)) * T * 64, ws.hc + ((int64_t)bh * NT + J) * 4096,
-                 bw.dhc + ((int64_t)bhq * NT + J) * 4096);
+      transition(J, ws.qs + ((int64_t)bhq * PR + (J - cb)) * T * KD, ws.hc + ((int64_t)bh * NT + J) * (KD * KD),
+                 bw.dhc + ((int64_t)bhq * NT + J) * (KD * KD));
     }
     if (J + 1 < nJ) stage(J + 1);
     if (J >= cb || J % PR == 0) {  // the query operand changes
-      const bf16* qsrc = (J < cb) ? ws.qb + ((int64_t)bhq * NS + J / PR) * T * 64
-                                  : ws.qs + ((int64_t)bhq * PR + (J - cb)) * T * 64;
+      const bf16* qsrc = (J < cb) ? ws.qb + ((int64_t)bhq * NS + J / PR) * T * KD
+                                  : ws.qs + ((int64_t)bhq * PR + (J - cb)) * T * KD;
 #pragma unroll
-      for (int st = 0; st < 4; ++st) qb[st] = ld8(qsrc + (int64_t)(iw0 + l32) * 64 + 16 * st + 8 * g);
+      for (int st = 0; st < NKS; ++st) qb[st] = ld8(qsrc + (int64_t)(iw0 + l32) * KD + 16 * st + 8 * g);
     }
     if (Iw < NT && J < Iw) {
 #pragma unroll
       for (int jh = 0; jh < 2; ++jh) {
         f32x16 sc = zero16(), dp = zero16();
 #pragma unroll
-        for (int st = 0; st < 4; ++st) {
-          sc = mfma32(ld8(swz<8>(sm.k[buf], jh * 32 + l32, 2 * st + g)), qb[st], sc);
-          dp = mfma32(ld8(swz<8>(sm.o[buf], jh * 32 + l32, 2 * st + g)), dvr[st], dp);
+        for (int st = 0; st < NKS; ++st) {
+          sc = mfma32(ld8(swz<CPR>(sm.k[buf], jh * 32 + l32, 2 * st + g)), qb[st], sc);
+          dp = mfma32(ld8(swz<CPR>(sm.o[buf], jh * 32 + l32, 2 * st + g)), dvr[st], dp);
         }
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
@@ -501,9 +526,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
         }
         const bf16x8 d0 = pack_b(sc, 0), d1 = pack_b(sc, 1);
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          acc[t] = mfma32(lds_tr_a<8>(sm.k[buf], jh * 32, t * 32), d0, acc[t]);
-          acc[t] = mfma32(lds_tr_a<8>(sm.k[buf], jh * 32 + 16, t * 32), d1, acc[t]);
+        for (int t = 0; t < NVT; ++t) {
+          acc[t] = mfma32(lds_tr_a<CPR>(sm.k[buf], jh * 32, t * 32), d0, acc[t]);
+          acc[t] = mfma32(lds_tr_a<CPR>(sm.k[buf], jh * 32 + 16, t * 32), d1, acc[t]);
         }
       }
     }
@@ -511,9 +536,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
     __syncthreads();
   }
   if (Iw < NT) {
-    float* dst = bw.dqt + ((int64_t)bhq * T + iw0 + l32) * 64;
+    float* dst = bw.dqt + ((int64_t)bhq * T + iw0 + l32) * KD;
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < NVT; ++t)
 #pragma unroll
       for (int qq = 0; qq < 4; ++qq) {
         f32x4 v;
@@ -541,29 +566,86 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
 // delta are staged beside each query tile, and dV_J^T[d][j] += dO_I^T[d][i] P[i][j]
 // is accumulated too and added to the diagonal block's part in dvf.
 // ---------------------------------------------------------------------------
-template <bool SM>
+template <bool SM, int KD>
 struct ColSmem {
   union {
     struct {
-      bf16 qa[3][64 * 64];  // swizzled (chunk c of row r at c ^ (r & 7))
-      bf16 qb[3][64 * 64];
-      bf16 dv[3][64 * 64];
+      bf16 qa[3][64 * KD];  // swizzled (chunk c of row r at c ^ (r & 7))
+      bf16 qb[3][64 * KD];
+      bf16 dv[3][64 * KD];
     } st;
-    struct {
-      float a[64][68];  // d k~ (same large chunk), then the result
-      float f[64][68];  // dKL
-      float m[64][68];  // SUF_J, then k~_J
+    struct {  // 64-column halves at KD = 128
+      float a[KD / 64][64][68];  // d k~ (same large chunk), then the result
+      float f[KD / 64][64][68];  // dKL
+      float m[KD / 64][64][68];  // SUF_J blocks, then k~_J
     } fin;
   } u;
   float lse[SM ? 3 : 1][64];  // softmax: lse and delta of the staged query rows
   float dl[SM ? 3 : 1][64];
 };
 
+// The column sweep's last step at KD = 128, per chunk J of the pair, on 64 x 64 fp32 LDS
+// blocks (a, f: 64-column halves of d k~ (same) and dKL; m: operand blocks):
+//   d k~_J[:, c] = d k~(same)[:, c] + sum_k dKL[:, k] SUF_J(k, c)   (block (k, c) of SUF_J)
+//   dSUF_J(r, c) = dKL[:, r]^T k~_J[:, c]
+// Softmax mode: the same-chunk part was parked in dkt and dKL is in as_.
 template <bool SM>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void path_bwd_col_kernel(
+__device__ __forceinline__ void col_finish128(float (*a)[64][68], float (*f)[64][68], float (*m)[64][68],
+                                              const f32x16 (&as_)[4], const f32x16 (&af)[4], float F, int J1, int NT,
+                                              int T, int bh, int bhq, const PathFwdWs& ws, const PathBwdWs& bw) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
+  const int cl = dl_col();
+  for (int half = 0; half < 2; ++half) {
+    const int J = J1 + half;
+    if (J >= NT) break;
+    if ((w >> 1) == half) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int r = (w & 1) * 32 + l32, c = (t & 1) * 32 + drow(e, g);
+          if (!SM) a[t >> 1][r][c] = F * as_[t][e];
+          f[t >> 1][r][c] = F * (SM ? as_[t][e] : af[t][e]);
+        }
+    }
+    const float* suf = ws.suf + ((int64_t)bh * NT + J) * (128 * 128);
+    float* dkt = bw.dkt + ((int64_t)bhq * T + J * PC) * 128;
+#pragma unroll 1
+    for (int ch = 0; ch < 2; ++ch) {
+      load_blk(m[0], suf + 64 * ch, 128);
+      load_blk(m[1], suf + 64 * 128 + 64 * ch, 128);
+      __syncthreads();
+      f32x16 r = mgemm64<false, false>(f[0], m[0], zero16());
+      r = mgemm64<false, false>(f[1], m[1], r);
+      DL_FOR_E {
+        const int rr = dl_row(e);
+        float* p = dkt + (int64_t)rr * 128 + 64 * ch + cl;
+        *p = r[e] + (SM ? *p : a[ch][rr][cl]);
+      }
+      __syncthreads();
+    }
+    load_rows64_f32(m[0], ws.kt + ((int64_t)bh * T + J * PC) * 128, 128);
+    load_rows64_f32(m[1], ws.kt + ((int64_t)bh * T + J * PC) * 128 + 64, 128);
+    __syncthreads();
+    float* dsuf = bw.dsuf + ((int64_t)bhq * NT + J) * (128 * 128);
+#pragma unroll 1
+    for (int blk = 0; blk < 4; ++blk) {
+      const int ra = blk >> 1, cb_ = blk & 1;
+      const f32x16 r = mgemm64<true, false>(f[ra], m[cb_], zero16());
+      DL_FOR_E dsuf[(int64_t)(64 * ra + dl_row(e)) * 128 + 64 * cb_ + cl] = r[e];
+    }
+    __syncthreads();
+  }
+}
+
+// KD: head dim (64 or 128)
+template <bool SM, int KD>
+__global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_bwd_col_kernel(
     const bf16* __restrict__ xsrc, Strides xs, const bf16* __restrict__ ysrc, Strides ys, int HQ, int H, int T,
     float scale, PathFwdWs ws, PathBwdWs bw) {
-  __shared__ __attribute__((aligned(16))) ColSmem<SM> sm;
+  constexpr int NKS = KD / 16, NVT = KD / 32, CPR = KD / 8;  // k-steps, 32-column tiles, 16-byte chunks per row
+  constexpr int PT = 64 * CPR / 256;  // direct loads per wave for one staged tile
+  __shared__ __attribute__((aligned(16))) ColSmem<SM, KD> sm;
   const int NT = T / PC, NS = (NT + PR - 1) / PR;
   const int J1 = 2 * blockIdx.y, bhq = blockIdx.x;  // heaviest (earliest) key pairs of all heads first
   const int G_ = HQ / H;
@@ -578,37 +660,43 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
   // F = s): the constant F is applied to the dK accumulators where the sweep hands them on
   const float F = SM ? scale : -scale * __builtin_amdgcn_exp2f(-cc0);
 
-  bf16x8 kbs[4], kbf[4], ob[4];
+  bf16x8 kbs[NKS], kbf[NKS], ob[NKS];
   {
     const int jr = min(J1 * PC + 32 * w + l32, T - 1);
     const bf16* yrow = ysrc + b * ys.b + (SM ? hq / G_ : hq) * ys.h + (int64_t)jr * ys.t;
 #pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      kbs[st] = ld8(ws.kt + ((int64_t)bh * T + jr) * 64 + 16 * st + 8 * g);
-      kbf[st] = ld8(ws.kl + ((int64_t)bh * T + jr) * 64 + 16 * st + 8 * g);
+    for (int st = 0; st < NKS; ++st) {
+      kbs[st] = ld8(ws.kt + ((int64_t)bh * T + jr) * KD + 16 * st + 8 * g);
+      kbf[st] = ld8(ws.kl + ((int64_t)bh * T + jr) * KD + 16 * st + 8 * g);
       ob[st] = ld8(yrow + 16 * st + 8 * g);
     }
   }
-  f32x16 as_[2] = {zero16(), zero16()}, af[2] = {zero16(), zero16()};
-  f32x16 dva[2] = {zero16(), zero16()};  // softmax: dV^T of this wave's keys
+  f32x16 as_[NVT], af[NVT];
+  f32x16 dva[SM ? NVT : 1];  // softmax: dV^T of this wave's keys
+#pragma unroll
+  for (int t = 0; t < NVT; ++t) {
+    as_[t] = zero16();
+    af[t] = zero16();
+    if (SM) dva[t] = zero16();
+  }
 
   // step k stages query tile I = J1 + 1 + k
   const int nsteps = NT - 1 - J1;
   // newest vector-memory ops of a step, per wave: 3 tiles inside J's large chunk, 2 beyond
   auto near = [&](int k) { return J1 + 1 + k <= ceJ; };
-  int plan_r[2], plan_x[2];
-  dma_plan<64, 8>(64, plan_r);
-  if (SM) dma_plan<64, 8>(xs.t, plan_x);
+  int plan_r[PT], plan_x[PT];
+  dma_plan<64, CPR>(KD, plan_r);
+  if (SM) dma_plan<64, CPR>(xs.t, plan_x);
   auto stage = [&](int k) {
     const int I = J1 + 1 + k, buf = k % 3;
     const bool same = I <= ceJ;
-    const bf16* q1 = same ? ws.qs + ((int64_t)bhq * PR + (J1 - cb)) * T * 64
-                          : ws.qb + ((int64_t)bhq * NS + sJ) * T * 64;
-    dma_stage<64, 8>(plan_r, q1 + (int64_t)I * PC * 64, sm.u.st.qa[buf]);
-    dma_stage<64, 8>(SM ? plan_x : plan_r, xh + (int64_t)I * PC * xs.t, sm.u.st.dv[buf]);
+    const bf16* q1 = same ? ws.qs + ((int64_t)bhq * PR + (J1 - cb)) * T * KD
+                          : ws.qb + ((int64_t)bhq * NS + sJ) * T * KD;
+    dma_stage<64, CPR>(plan_r, q1 + (int64_t)I * PC * KD, sm.u.st.qa[buf]);
+    dma_stage<64, CPR>(SM ? plan_x : plan_r, xh + (int64_t)I * PC * xs.t, sm.u.st.dv[buf]);
     if (same)  // the second chunk of the pair has its own query operand inside the large chunk
-      dma_stage<64, 8>(plan_r, ws.qs + ((int64_t)bhq * PR + (J1 + 1 - cb)) * T * 64 + (int64_t)I * PC * 64,
-                       sm.u.st.qb[buf]);
+      dma_stage<64, CPR>(plan_r, ws.qs + ((int64_t)bhq * PR + (J1 + 1 - cb)) * T * KD + (int64_t)I * PC * KD,
+                         sm.u.st.qb[buf]);
     if (SM) {  // one more load for waves 0 and 1
       if (w == 0) dma_f32x64(ws.lse + (int64_t)bhq * T + I * PC, sm.lse[buf]);
       if (w == 1) dma_f32x64(bw.delta + (int64_t)bhq * T + I * PC, sm.dl[buf]);
@@ -617,11 +705,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
   // wait until the step after the next one is the only one in flight
   auto wait_next = [&](bool nr) {
     if (SM && w < 2) {
-      if (nr) dma_wait_but<7>();
-      else dma_wait_but<5>();
+      if (nr) dma_wait_but<3 * PT + 1>();
+      else dma_wait_but<2 * PT + 1>();
     } else {
-      if (nr) dma_wait_but<6>();
-      else dma_wait_but<4>();
+      if (nr) dma_wait_but<3 * PT>();
+      else dma_wait_but<2 * PT>();
     }
   };
   if (nsteps > 0) {
@@ -639,9 +727,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
   bool parked = false;
   auto park = [&]() {
     if (live) {
-      float* dst = bw.dkt + ((int64_t)bhq * T + Jw * PC + (w & 1) * 32 + l32) * 64;
+      float* dst = bw.dkt + ((int64_t)bhq * T + Jw * PC + (w & 1) * 32 + l32) * KD;
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+      for (int t = 0; t < NVT; ++t)
 #pragma unroll
         for (int qq = 0; qq < 4; ++qq) {
           f32x4 x;
@@ -649,8 +737,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
           for (int u = 0; u < 4; ++u) x[u] = F * as_[t][4 * qq + u];
           *reinterpret_cast<f32x4*>(dst + t * 32 + 8 * qq + 4 * g) = x;
         }
-      as_[0] = zero16();
-      as_[1] = zero16();
+#pragma unroll
+      for (int t = 0; t < NVT; ++t) as_[t] = zero16();
     }
     parked = true;
   };
@@ -666,9 +754,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
       for (int rh = 0; rh < 2; ++rh) {
         f32x16 sc = zero16(), dp = zero16();
 #pragma unroll
-        for (int st = 0; st < 4; ++st) {
-          sc = mfma32(ld8(swz<8>(qt, rh * 32 + l32, 2 * st + g)), same ? kbs[st] : kbf[st], sc);
-          dp = mfma32(ld8(swz<8>(sm.u.st.dv[buf], rh * 32 + l32, 2 * st + g)), ob[st], dp);
+        for (int st = 0; st < NKS; ++st) {
+          sc = mfma32(ld8(swz<CPR>(qt, rh * 32 + l32, 2 * st + g)), same ? kbs[st] : kbf[st], sc);
+          dp = mfma32(ld8(swz<CPR>(sm.u.st.dv[buf], rh * 32 + l32, 2 * st + g)), ob[st], dp);
         }
         if (SM) {
 #pragma unroll
@@ -684,9 +772,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
           }
           const bf16x8 p0 = pack_b(sc, 0), p1 = pack_b(sc, 1);
 #pragma unroll
-          for (int t = 0; t < 2; ++t) {
-            dva[t] = mfma32(lds_tr_a<8>(sm.u.st.dv[buf], rh * 32, t * 32), p0, dva[t]);
-            dva[t] = mfma32(lds_tr_a<8>(sm.u.st.dv[buf], rh * 32 + 16, t * 32), p1, dva[t]);
+          for (int t = 0; t < NVT; ++t) {
+            dva[t] = mfma32(lds_tr_a<CPR>(sm.u.st.dv[buf], rh * 32, t * 32), p0, dva[t]);
+            dva[t] = mfma32(lds_tr_a<CPR>(sm.u.st.dv[buf], rh * 32 + 16, t * 32), p1, dva[t]);
           }
 #pragma unroll
           for (int e = 0; e < 16; ++e) sc[e] = dp[e];
@@ -696,9 +784,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
         }
         const bf16x8 d0 = pack_b(sc, 0), d1 = pack_b(sc, 1);
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const bf16x8 a0 = lds_tr_a<8>(qt, rh * 32, t * 32);
-          const bf16x8 a1 = lds_tr_a<8>(qt, rh * 32 + 16, t * 32);
+        for (int t = 0; t < NVT; ++t) {
+          const bf16x8 a0 = lds_tr_a<CPR>(qt, rh * 32, t * 32);
+          const bf16x8 a1 = lds_tr_a<CPR>(qt, rh * 32 + 16, t * 32);
           if (same || SM) {  // softmax: one accumulator, the same-chunk part is parked in dkt
             as_[t] = mfma32(a0, d0, as_[t]);
             as_[t] = mfma32(a1, d1, as_[t]);
@@ -718,9 +806,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
   }
   if (SM && !parked) park();
   if (SM && live) {  // dV_J rows: the diagonal block's part is already in dvf
-    float* dst = bw.dvf + ((int64_t)bhq * T + Jw * PC + (w & 1) * 32 + l32) * 64;
+    float* dst = bw.dvf + ((int64_t)bhq * T + Jw * PC + (w & 1) * 32 + l32) * KD;
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < NVT; ++t)
 #pragma unroll
       for (int qq = 0; qq < 4; ++qq) {
         f32x4* p = reinterpret_cast<f32x4*>(dst + t * 32 + 8 * qq + 4 * g);
@@ -731,6 +819,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
       }
   }
   // ---- per chunk of the pair: d k~_J = dk~(same) + dKL SUF_J, dSUF_J = dKL^T k~_J ----
+  if constexpr (KD == 128) {
+    col_finish128<SM>(sm.u.fin.a, sm.u.fin.f, sm.u.fin.m, as_, af, F, J1, NT, T, bh, bhq, ws, bw);
+  } else {
   const int r0 = (tid >> 4) * 4, c0 = (tid & 15) * 4;
   for (int half = 0; half < 2; ++half) {
     const int J = J1 + half;
@@ -740,15 +831,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-          if (!SM) sm.u.fin.a[(w & 1) * 32 + l32][t * 32 + drow(e, g)] = F * as_[t][e];
-          sm.u.fin.f[(w & 1) * 32 + l32][t * 32 + drow(e, g)] = F * (SM ? as_[t][e] : af[t][e]);
+          if (!SM) sm.u.fin.a[0][(w & 1) * 32 + l32][t * 32 + drow(e, g)] = F * as_[t][e];
+          sm.u.fin.f[0][(w & 1) * 32 + l32][t * 32 + drow(e, g)] = F * (SM ? as_[t][e] : af[t][e]);
         }
     }
-    load_mat64<false>(sm.u.fin.m, ws.suf + ((int64_t)bh * NT + J) * 4096);
+    load_mat64<false>(sm.u.fin.m[0], ws.suf + ((int64_t)bh * NT + J) * 4096);
     __syncthreads();
     float acc4[4][4];
     zero44(acc4);
-    lds_gemm64<false, false>(sm.u.fin.f, sm.u.fin.m, acc4);  // dKL SUF
+    lds_gemm64<false, false>(sm.u.fin.f[0], sm.u.fin.m[0], acc4);  // dKL SUF
     {
       float* dst = bw.dkt + ((int64_t)bhq * T + J * PC) * 64;
 #pragma unroll
@@ -756,15 +847,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
         f32x4 v;
         if (SM) v = *reinterpret_cast<const f32x4*>(dst + (r0 + i) * 64 + c0);  // parked part
 #pragma unroll
-        for (int j = 0; j < 4; ++j) v[j] = acc4[i][j] + (SM ? v[j] : sm.u.fin.a[r0 + i][c0 + j]);
+        for (int j = 0; j < 4; ++j) v[j] = acc4[i][j] + (SM ? v[j] : sm.u.fin.a[0][r0 + i][c0 + j]);
         *reinterpret_cast<f32x4*>(dst + (r0 + i) * 64 + c0) = v;
       }
     }
     __syncthreads();
-    load_rows64_f32(sm.u.fin.m, ws.kt + ((int64_t)bh * T + J * PC) * 64, 64);
+    load_rows64_f32(sm.u.fin.m[0], ws.kt + ((int64_t)bh * T + J * PC) * 64, 64);
     __syncthreads();
     zero44(acc4);
-    lds_gemm64<true, false>(sm.u.fin.f, sm.u.fin.m, acc4);  // dSUF = dKL^T k~
+    lds_gemm64<true, false>(sm.u.fin.f[0], sm.u.fin.m[0], acc4);  // dSUF = dKL^T k~
     {
       float* dst = bw.dsuf + ((int64_t)bhq * NT + J) * 4096;
 #pragma unroll
@@ -776,6 +867,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
       }
     }
     __syncthreads();
+  }
   }
 }
 
@@ -1057,32 +1149,35 @@ __global__ __launch_bounds__(256) void path_wy_bwd_kernel(const bf16* __restrict
 
 // ---------------------------------------------------------------------------
 // GQA sums over the query heads of each kv head (parallel.py:165-171) and casts
-// to the caller's bf16 gradients.  grid (T/4, B*H), thread = (row, column)
+// to the caller's bf16 gradients.  grid (T/4, B*H), thread = (row, column), KD / 64 columns
+// per thread (KD: head dim of the fp32 rows)
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void path_reduce_kernel(int HQ, int H, int T, PathBwdWs bw, bf16* __restrict__ dq,
+__global__ __launch_bounds__(256) void path_reduce_kernel(int HQ, int H, int T, int KD, PathBwdWs bw, bf16* __restrict__ dq,
                                                           Strides dqs, bf16* __restrict__ dk, Strides dks,
                                                           bf16* __restrict__ dv, Strides dvs, bf16* __restrict__ dw,
                                                           Strides dws, bf16* __restrict__ db, Strides dbs) {
   const int bh = blockIdx.y;
   const int b = bh / H, h = bh - b * H;
   const int G_ = HQ / H;
-  const int t = blockIdx.x * 4 + (threadIdx.x >> 6), col = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
-  float sk = 0.f, sv = 0.f, sw = 0.f, sb = 0.f;
-  for (int gi = 0; gi < G_; ++gi) {
-    const int hq = h * G_ + gi;
-    const int64_t bhq = (int64_t)b * HQ + hq;
-    const int64_t off = (bhq * T + t) * 64 + col;
-    sk += bw.dk[off];
-    sv += bw.dvf[off];
-    sw += bw.dw[off];
-    if (col == 0) sb += bw.db[bhq * T + t];
-    dq[b * dqs.b + hq * dqs.h + (int64_t)t * dqs.t + col] = (bf16)bw.dq[off];
+  for (int col = threadIdx.x & 63; col < KD; col += 64) {
+    float sk = 0.f, sv = 0.f, sw = 0.f, sb = 0.f;
+    for (int gi = 0; gi < G_; ++gi) {
+      const int hq = h * G_ + gi;
+      const int64_t bhq = (int64_t)b * HQ + hq;
+      const int64_t off = (bhq * T + t) * KD + col;
+      sk += bw.dk[off];
+      sv += bw.dvf[off];
+      sw += bw.dw[off];
+      if (col == 0) sb += bw.db[bhq * T + t];
+      dq[b * dqs.b + hq * dqs.h + (int64_t)t * dqs.t + col] = (bf16)bw.dq[off];
+    }
+    dk[b * dks.b + h * dks.h + (int64_t)t * dks.t + col] = (bf16)sk;
+    dv[b * dvs.b + h * dvs.h + (int64_t)t * dvs.t + col] = (bf16)sv;
+    dw[b * dws.b + h * dws.h + (int64_t)t * dws.t + col] = (bf16)sw;
+    if (col == 0) db[b * dbs.b + h * dbs.h + (int64_t)t * dbs.t] = (bf16)sb;
   }
-  dk[b * dks.b + h * dks.h + (int64_t)t * dks.t + col] = (bf16)sk;
-  dv[b * dvs.b + h * dvs.h + (int64_t)t * dvs.t + col] = (bf16)sv;
-  dw[b * dws.b + h * dws.h + (int64_t)t * dws.t + col] = (bf16)sw;
-  if (col == 0) db[b * dbs.b + h * dbs.h + (int64_t)t * dbs.t] = (bf16)sb;
 }
 
 }  // namespace lucid

@@ -3,8 +3,7 @@
 
 #include "../../include/lucid_path.h"
 #include "path_fwd.hip"
-#include "path_bwd.hip"
-#include "path_wide.hip"
+#include "path_wide.hip"  // includes path_bwd.hip
 #include "chain_guard.h"
 #include "profiling.h"
 
@@ -177,14 +176,23 @@ int launch_back(const void* q, const int64_t* q_strides, const void* k, const in
                 const int64_t* w_strides, const void* beta, const int64_t* beta_strides, void* dq,
                 const int64_t* dq_strides, void* dk, const int64_t* dk_strides, void* dv, const int64_t* dv_strides,
                 void* dw, const int64_t* dw_strides, void* dbeta, const int64_t* dbeta_strides, int B, int T, int H,
-                int HQ, const lucid::PathFwdWs& ws, const lucid::PathBwdWs& bw, hipStream_t st) {
+                int HQ, const lucid::PathFwdWs& ws, const lucid::PathBwdWs& bw, hipStream_t st, int KD = 64) {
   const int NT = T / 64, NS = (NT + 7) / 8;
   const int BH = B * H, BHq = B * HQ;
-  LUCID_TIMED_LAUNCH(phip, "path_products_bwd_kernel", lucid::path_products_bwd_kernel, dim3(NS, BHq), st, HQ, H, T, ws, bw);
-  LUCID_TIMED_LAUNCH(phip, "path_wy_bwd_kernel", lucid::path_wy_bwd_kernel, dim3(NT, BHq), st, (const bf16*)q, PS(q_strides),
-                     (const bf16*)k, PS(k_strides), (const bf16*)w, PS(w_strides), (const bf16*)beta,
-                     PS(beta_strides), HQ, H, T, ws, bw);
-  LUCID_TIMED_LAUNCH(phip, "path_reduce_kernel", lucid::path_reduce_kernel, dim3((T + 3) / 4, BH), st, HQ, H, T, bw,
+  if (KD == 128) {
+    LUCID_TIMED_LAUNCH(phip, "path_products_bwd128_kernel", lucid::path_products_bwd128_kernel, dim3(NS, BHq), st, HQ,
+                       H, T, ws, bw);
+    LUCID_TIMED_LAUNCH(phip, "path_wy_bwd128_kernel", lucid::path_wy_bwd128_kernel, dim3(NT, BHq), st, (const bf16*)q,
+                       PS(q_strides), (const bf16*)k, PS(k_strides), (const bf16*)w, PS(w_strides), (const bf16*)beta,
+                       PS(beta_strides), HQ, H, T, ws, bw);
+  } else {
+    LUCID_TIMED_LAUNCH(phip, "path_products_bwd_kernel", lucid::path_products_bwd_kernel, dim3(NS, BHq), st, HQ, H, T,
+                       ws, bw);
+    LUCID_TIMED_LAUNCH(phip, "path_wy_bwd_kernel", lucid::path_wy_bwd_kernel, dim3(NT, BHq), st, (const bf16*)q,
+                       PS(q_strides), (const bf16*)k, PS(k_strides), (const bf16*)w, PS(w_strides), (const bf16*)beta,
+                       PS(beta_strides), HQ, H, T, ws, bw);
+  }
+  LUCID_TIMED_LAUNCH(phip, "path_reduce_kernel", lucid::path_reduce_kernel, dim3((T + 3) / 4, BH), st, HQ, H, T, KD, bw,
                      (bf16*)dq, PS(dq_strides), (bf16*)dk, PS(dk_strides), (bf16*)dv, PS(dv_strides), (bf16*)dw,
                      PS(dw_strides), (bf16*)dbeta, PS(dbeta_strides));
   return 0;
@@ -254,9 +262,8 @@ int lucid_path_fwd(const void* q, const int64_t* q_strides, const void* k, const
 
 size_t lucid_path_bwd_workspace_bytes(int B, int T, int H, int HQ, int K) {
   (void)H;
-  (void)K;
   size_t n = 0;
-  carve_path_bwd(nullptr, B, T, HQ, &n);
+  carve_path_bwd(nullptr, B, T, HQ, &n, false, K > 64 ? 128 : 64);
   return n;
 }
 
@@ -269,7 +276,6 @@ int lucid_path_bwd(const void* dout, const int64_t* do_strides, const void* q, c
                    void* stream) {
   g_path_error.clear();
   if (int rc = check_shapes(B, T, H, HQ, K)) return rc;
-  if (K != 64) return pfail("the backward runs at head_dim 64 only, got " + std::to_string(K));
   if (int rc = pcheck_vec("dout", dout, do_strides)) return rc;
   if (int rc = pcheck_vec("q", q, q_strides)) return rc;
   if (int rc = pcheck_vec("k", k, k_strides)) return rc;
@@ -285,22 +291,31 @@ int lucid_path_bwd(const void* dout, const int64_t* do_strides, const void* q, c
   if (reinterpret_cast<uintptr_t>(fwd_ws) % 256 || reinterpret_cast<uintptr_t>(bwd_ws) % 256)
     return pfail("fwd_ws and bwd_ws must be 256-byte aligned");
   if (int rc = pchain_check()) return rc;
-  const lucid::PathFwdWs ws = carve_path_fwd(const_cast<void*>(fwd_ws), B, T, H, HQ, nullptr);
-  const lucid::PathBwdWs bw = carve_path_bwd(bwd_ws, B, T, HQ, nullptr);
+  const lucid::PathFwdWs ws = carve_path_fwd(const_cast<void*>(fwd_ws), B, T, H, HQ, nullptr, false, K);
+  const lucid::PathBwdWs bw = carve_path_bwd(bwd_ws, B, T, HQ, nullptr, false, K);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int NT = T / 64, NS = (NT + 7) / 8;
   const int BHq = B * HQ;
-  const int64_t n_hl = (int64_t)BHq * NS * 4096, n_hc = (int64_t)BHq * NT * 4096;
-  const lucid::Strides dvs{(int64_t)HQ * T * 64, (int64_t)T * 64, 64};  // dV rows [B][HQ][T][64]
+  const int64_t n_hl = (int64_t)BHq * NS * K * K, n_hc = (int64_t)BHq * NT * K * K;
+  const lucid::Strides dvs{(int64_t)HQ * T * K, (int64_t)T * K, K};  // dV rows [B][HQ][T][K]
   LUCID_TIMED_LAUNCH(phip, "path_bwd_zero_kernel", lucid::path_bwd_zero_kernel, dim3(1024), st, n_hl, n_hc, BHq, bw);
-  LUCID_TIMED_LAUNCH(phip, "path_dv_kernel", lucid::path_dv_kernel, dim3(((NT + 1) / 2) * BHq), st, (const bf16*)dout, PS(do_strides),
-                     (const bf16*)o, PS(o_strides), HQ, H, T, BHq, scale, ws, bw);
-  LUCID_TIMED_LAUNCH(phip, "path_bwd_row_kernel", lucid::path_bwd_row_kernel<false>, dim3(BHq, (NT + 1) / 2), st,
-                     (const bf16*)bw.dvb, dvs, (const bf16*)o, PS(o_strides), HQ, H, T, scale, ws, bw);
-  LUCID_TIMED_LAUNCH(phip, "path_bwd_col_kernel", lucid::path_bwd_col_kernel<false>, dim3(BHq, (NT + 1) / 2), st,
-                     (const bf16*)bw.dvb, dvs, (const bf16*)o, PS(o_strides), HQ, H, T, scale, ws, bw);
+  if (K == 128) {
+    LUCID_TIMED_LAUNCH(phip, "path_dv_kernel", lucid::path_dv_kernel<128>, dim3(((NT + 1) / 2) * BHq), st,
+                       (const bf16*)dout, PS(do_strides), (const bf16*)o, PS(o_strides), HQ, H, T, BHq, scale, ws, bw);
+    LUCID_TIMED_LAUNCH(phip, "path_bwd_row_kernel", (lucid::path_bwd_row_kernel<false, 128>), dim3(BHq, (NT + 1) / 2),
+                       st, (const bf16*)bw.dvb, dvs, (const bf16*)o, PS(o_strides), HQ, H, T, scale, ws, bw);
+    LUCID_TIMED_LAUNCH(phip, "path_bwd_col_kernel", (lucid::path_bwd_col_kernel<false, 128>), dim3(BHq, (NT + 1) / 2),
+                       st, (const bf16*)bw.dvb, dvs, (const bf16*)o, PS(o_strides), HQ, H, T, scale, ws, bw);
+  } else {
+    LUCID_TIMED_LAUNCH(phip, "path_dv_kernel", lucid::path_dv_kernel<64>, dim3(((NT + 1) / 2) * BHq), st,
+                       (const bf16*)dout, PS(do_strides), (const bf16*)o, PS(o_strides), HQ, H, T, BHq, scale, ws, bw);
+    LUCID_TIMED_LAUNCH(phip, "path_bwd_row_kernel", (lucid::path_bwd_row_kernel<false, 64>), dim3(BHq, (NT + 1) / 2),
+                       st, (const bf16*)bw.dvb, dvs, (const bf16*)o, PS(o_strides), HQ, H, T, scale, ws, bw);
+    LUCID_TIMED_LAUNCH(phip, "path_bwd_col_kernel", (lucid::path_bwd_col_kernel<false, 64>), dim3(BHq, (NT + 1) / 2),
+                       st, (const bf16*)bw.dvb, dvs, (const bf16*)o, PS(o_strides), HQ, H, T, scale, ws, bw);
+  }
   return launch_back(q, q_strides, k, k_strides, w, w_strides, beta, beta_strides, dq, dq_strides, dk, dk_strides, dv,
-                     dv_strides, dw, dw_strides, dbeta, dbeta_strides, B, T, H, HQ, ws, bw, st);
+                     dv_strides, dw, dw_strides, dbeta, dbeta_strides, B, T, H, HQ, ws, bw, st, K);
 }
 
 size_t lucid_path_softmax_fwd_workspace_bytes(int B, int T, int H, int HQ, int K) {
@@ -384,9 +399,9 @@ int lucid_path_softmax_bwd(const void* dout, const int64_t* do_strides, const vo
   LUCID_TIMED_LAUNCH(phip, "path_softmax_diag_bwd_kernel", lucid::path_softmax_diag_bwd_kernel, dim3(NT, BHq), st,
                      (const bf16*)dout, PS(do_strides), (const bf16*)o, PS(o_strides), (const bf16*)v, PS(v_strides),
                      HQ, H, T, scale, ws, bw);
-  LUCID_TIMED_LAUNCH(phip, "path_softmax_bwd_row_kernel", lucid::path_bwd_row_kernel<true>, dim3(BHq, (NT + 1) / 2), st,
+  LUCID_TIMED_LAUNCH(phip, "path_softmax_bwd_row_kernel", (lucid::path_bwd_row_kernel<true, 64>), dim3(BHq, (NT + 1) / 2), st,
                      (const bf16*)dout, PS(do_strides), (const bf16*)v, PS(v_strides), HQ, H, T, scale, ws, bw);
-  LUCID_TIMED_LAUNCH(phip, "path_softmax_bwd_col_kernel", lucid::path_bwd_col_kernel<true>, dim3(BHq, (NT + 1) / 2), st,
+  LUCID_TIMED_LAUNCH(phip, "path_softmax_bwd_col_kernel", (lucid::path_bwd_col_kernel<true, 64>), dim3(BHq, (NT + 1) / 2), st,
                      (const bf16*)dout, PS(do_strides), (const bf16*)v, PS(v_strides), HQ, H, T, scale, ws, bw);
   return launch_back(q, q_strides, k, k_strides, w, w_strides, beta, beta_strides, dq, dq_strides, dk, dk_strides, dv,
                      dv_strides, dw, dw_strides, dbeta, dbeta_strides, B, T, H, HQ, ws, bw, st);

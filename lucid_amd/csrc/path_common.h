@@ -256,6 +256,25 @@ __device__ __forceinline__ f32x16 dl_load(const float (*S)[68]) {
   DL_FOR_E x[e] = S[dl_row(e)][cl];
   return x;
 }
+// 64 x 64 block of an fp32 row-major matrix (row stride ld) into an LDS block, and back
+__device__ __forceinline__ void load_blk(float (*dst)[68], const float* __restrict__ src, int ld) {
+  for (int idx = threadIdx.x; idx < 1024; idx += 256) {
+    const int r = idx >> 4, c4 = (idx & 15) * 4;
+    *reinterpret_cast<f32x4*>(&dst[r][c4]) = *reinterpret_cast<const f32x4*>(src + (int64_t)r * ld + c4);
+  }
+}
+__device__ __forceinline__ void store_blk(float* __restrict__ dst, int ld, const float (*src)[68]) {
+  for (int idx = threadIdx.x; idx < 1024; idx += 256) {
+    const int r = idx >> 4, c4 = (idx & 15) * 4;
+    *reinterpret_cast<f32x4*>(dst + (int64_t)r * ld + c4) = *reinterpret_cast<const f32x4*>(&src[r][c4]);
+  }
+}
+// D-layout tile (this wave's 32 x 32 of a 64 x 64 block) to a row-major fp32 / bf16 matrix
+__device__ __forceinline__ void dl_put(float* __restrict__ dst, int ld, const f32x16& x) {
+  const int cl = dl_col();
+  DL_FOR_E dst[(int64_t)dl_row(e) * ld + cl] = x[e];
+}
+
 // 64x64 fp32 row-major matrix: thread t holds rows (t + 256 i) / 16, 4 columns each
 __device__ __forceinline__ void mat_fetch(f32x4 v[4], const float* __restrict__ src) {
 #pragma unroll

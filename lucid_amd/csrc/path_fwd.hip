@@ -20,19 +20,20 @@
 
 namespace lucid {
 
+// K: the kernels' head dim (64 or 128); in-chunk C x C matrices are 64 x 64 at either
 struct PathFwdWs {
-  float* w2;    // [BH][T][64]        W2 = T_inv (beta W)
-  float* hc;    // [BH][NT][64][64]   Hc = I - W^T W2
-  bf16* kt;     // [BH][T][64]        k~ rows
-  float* suf;   // [BH][NT][64][64]   SUF_c
-  float* hl;    // [BH][NS][64][64]   HL_s
-  bf16* kl;     // [BH][T][64]        KL rows
-  float* qt;    // [BHq][T][64]       q~
+  float* w2;    // [BH][T][K]         W2 = T_inv (beta W)
+  float* hc;    // [BH][NT][K][K]     Hc = I - W^T W2
+  bf16* kt;     // [BH][T][K]         k~ rows
+  float* suf;   // [BH][NT][K][K]     SUF_c
+  float* hl;    // [BH][NS][K][K]     HL_s
+  bf16* kl;     // [BH][T][K]         KL rows
+  float* qt;    // [BHq][T][K]        q~
   float* ld;    // [BHq][NT][64][64]  L_diag (strictly lower)
   float* y;     // [BHq][NT][64][64]  (I + L_diag)^-1
-  bf16* qs;     // [BHq][8][T][64]    QS rows, slot = c - (first chunk of I's large chunk)
-  bf16* qb;     // [BHq][NS][T][64]   QB rows
-  bf16* oT;     // [BHq][64][T]       O^T, T-perm (chain operand)
+  bf16* qs;     // [BHq][8][T][K]     QS rows, slot = c - (first chunk of I's large chunk)
+  bf16* qb;     // [BHq][NS][T][K]    QB rows
+  bf16* oT;     // [BHq][K][T]        O^T, T-perm (chain operand)
   int* counters;  // [BHq]
   float* lse;   // [BHq][T]           PaTH softmax only: row log-sum-exp, exp2 domain (log2(l) + m)
 };

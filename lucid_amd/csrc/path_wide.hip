@@ -12,29 +12,11 @@
 // matrices row-major [..][128 * 128], in-chunk C x C matrices [..][64 * 64] as at 64.
 #pragma once
 #include "path_common.h"
+#include "path_bwd.hip"  // PathBwdWs (path_bwd.hip has no include guard: included here only)
 
 namespace lucid {
 
 constexpr int WK = 128;  // head dim of this file's kernels
-
-// 64 x 64 block of an fp32 row-major matrix (row stride ld) into an LDS block, and back
-__device__ __forceinline__ void load_blk(float (*dst)[68], const float* __restrict__ src, int ld) {
-  for (int idx = threadIdx.x; idx < 1024; idx += 256) {
-    const int r = idx >> 4, c4 = (idx & 15) * 4;
-    *reinterpret_cast<f32x4*>(&dst[r][c4]) = *reinterpret_cast<const f32x4*>(src + (int64_t)r * ld + c4);
-  }
-}
-__device__ __forceinline__ void store_blk(float* __restrict__ dst, int ld, const float (*src)[68]) {
-  for (int idx = threadIdx.x; idx < 1024; idx += 256) {
-    const int r = idx >> 4, c4 = (idx & 15) * 4;
-    *reinterpret_cast<f32x4*>(dst + (int64_t)r * ld + c4) = *reinterpret_cast<const f32x4*>(&src[r][c4]);
-  }
-}
-// D-layout tile (this wave's 32 x 32 of a 64 x 64 block) to a row-major fp32 / bf16 matrix
-__device__ __forceinline__ void dl_put(float* __restrict__ dst, int ld, const f32x16& x) {
-  const int cl = dl_col();
-  DL_FOR_E dst[(int64_t)dl_row(e) * ld + cl] = x[e];
-}
 
 // ---------------------------------------------------------------------------
 // WY form and in-chunk transforms at K = 128 (path_chunk_kernel's algebra).  grid (NT, B*HQ)
@@ -371,6 +353,253 @@ __global__ __launch_bounds__(256) void path_kcache128_kernel(int T, bf16* __rest
     for (int e = 0; e < 8; ++e) v[e] = (bf16)X[r][c8 + e];
     *reinterpret_cast<bf16x8*>(kc + b * kcs.b + h * kcs.h + (int64_t)(J * PC + r) * kcs.t + c8) = v;
   }
+}
+
+// ---------------------------------------------------------------------------
+// Products backward at K = 128 (path_products_bwd_kernel's algebra) inside one large chunk:
+//   F = dHL_s; for c from the bottom up: dHc_c += SUF_c^T F; F <- F Hc_c^T + dSUF_c
+// F as four 64 x 64 blocks, SUF_c and then Hc_c as four more.  grid (NS, B*HQ)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void path_products_bwd128_kernel(int HQ, int H, int T, PathFwdWs ws, PathBwdWs bw) {
+  __shared__ __attribute__((aligned(16))) float Fb[4][64][68];  // block (r, c) at 2 r + c
+  __shared__ __attribute__((aligned(16))) float Ob[4][64][68];
+  const int NT = T / PC, NS = (NT + PR - 1) / PR;
+  const int s = blockIdx.x, bhq = blockIdx.y;
+  const int G_ = HQ / H;
+  const int b = bhq / HQ, hq = bhq - b * HQ, bh = b * H + hq / G_;
+  const int cb = s * PR, ce = min(cb + PR, NT) - 1;
+  const int cl = dl_col();
+  const f32x16 z = zero16();
+  constexpr int KK = WK * WK;
+  const float* dhl = bw.dhl + ((int64_t)bhq * NS + s) * KK;
+#pragma unroll 1
+  for (int blk = 0; blk < 4; ++blk) load_blk(Fb[blk], dhl + (blk >> 1) * 64 * WK + (blk & 1) * 64, WK);
+#pragma unroll 1
+  for (int c = cb; c <= ce; ++c) {
+    const float* suf = ws.suf + ((int64_t)bh * NT + c) * KK;
+#pragma unroll 1
+    for (int blk = 0; blk < 4; ++blk) load_blk(Ob[blk], suf + (blk >> 1) * 64 * WK + (blk & 1) * 64, WK);
+    __syncthreads();
+    {  // dHc_c(a, b) += sum_k SUF_c(k, a)^T F(k, b)
+      float* dhc = bw.dhc + ((int64_t)bhq * NT + c) * KK;
+#pragma unroll 1
+      for (int blk = 0; blk < 4; ++blk) {
+        const int ra = blk >> 1, cb_ = blk & 1;
+        f32x16 a = mgemm64<true, false>(Ob[ra], Fb[cb_], z);
+        a = mgemm64<true, false>(Ob[2 + ra], Fb[2 + cb_], a);
+        DL_FOR_E dhc[(int64_t)(64 * ra + dl_row(e)) * WK + 64 * cb_ + cl] += a[e];
+      }
+    }
+    __syncthreads();
+    const float* hc = ws.hc + ((int64_t)bh * NT + c) * KK;
+#pragma unroll 1
+    for (int blk = 0; blk < 4; ++blk) load_blk(Ob[blk], hc + (blk >> 1) * 64 * WK + (blk & 1) * 64, WK);
+    __syncthreads();
+    f32x16 nb[4];  // F(a, b) <- sum_k F(a, k) Hc_c(b, k)^T + dSUF_c(a, b)
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk) {
+      const int ra = blk >> 1, cb_ = blk & 1;
+      nb[blk] = mgemm64<false, true>(Fb[2 * ra], Ob[2 * cb_], z);
+      nb[blk] = mgemm64<false, true>(Fb[2 * ra + 1], Ob[2 * cb_ + 1], nb[blk]);
+    }
+    __syncthreads();
+    const float* ds = bw.dsuf + ((int64_t)bhq * NT + c) * KK;
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk) {
+      const int ra = blk >> 1, cb_ = blk & 1;
+      DL_FOR_E {
+        const int r = dl_row(e);
+        Fb[blk][r][cl] = nb[blk][e] + ds[(int64_t)(64 * ra + r) * WK + 64 * cb_ + cl];
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward of the WY form of one chunk at K = 128 (path_wy_bwd_kernel's algebra), with the
+// 64 x 128 operands and results taken as 64-column halves and beta folded into row / column
+// scalings of the products (Wb = diag(beta) W is formed only where it is an operand):
+//   A: Tm = (I + stril(diag(b) W W^T))^-1, QW = tril(Q W^T), WBK = stril(diag(b) W K^T), TW = Tm WBK
+//   B: dQW = -(dq~ W2^T + dA TW^T), dW2 = -(QW^T dq~ + W dHc), dTW = -(W dk~^T + QW^T dA),
+//      dW = -(TW dk~ + W2 dHc^T) + ...
+//   C: dTm = dTW WBK^T + dW2 Wb^T, dWBK = stril(Tm^T dTW), dWb = Tm^T dW2 + ...,
+//      da = -stril((Tm^T dTm) Tm^T)
+//   D (per half): dq = dq~ + dA K + tril(dQW) W, dk = dk~ + dA^T Q + dWBK^T Wb,
+//      dWb += dWBK K + da W, dW += tril(dQW)^T Q + da^T Wb + diag(b) dWb, db = rowsum(dWb * W)
+// LDS: nine 64 x 64 fp32 blocks.  grid (NT, B*HQ)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void path_wy_bwd128_kernel(const bf16* __restrict__ q, Strides qs,
+                                                             const bf16* __restrict__ k, Strides ks,
+                                                             const bf16* __restrict__ w, Strides wst,
+                                                             const bf16* __restrict__ beta, Strides bst, int HQ, int H,
+                                                             int T, PathFwdWs ws, PathBwdWs bw) {
+  __shared__ __attribute__((aligned(16))) float S[9][64][68];
+  __shared__ float bsh[64];
+  __shared__ float dbs[2][64];
+  const int NT = T / PC;
+  const int c = blockIdx.x, bhq = blockIdx.y;
+  const int G_ = HQ / H;
+  const int b = bhq / HQ, hq = bhq - b * HQ, h = hq / G_, bh = b * H + h;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, g = lane >> 5;
+  const int t0 = c * PC;
+  const f32x16 z = zero16();
+  const int cl = dl_col();
+  const bf16* wp = w + b * wst.b + h * wst.h + (int64_t)t0 * wst.t;
+  const bf16* qp = q + b * qs.b + hq * qs.h + (int64_t)t0 * qs.t;
+  const bf16* kp = k + b * ks.b + h * ks.h + (int64_t)t0 * ks.t;
+  const float* w2p = ws.w2 + ((int64_t)bh * T + t0) * WK;
+  const float* dqp = bw.dqt + ((int64_t)bhq * T + t0) * WK;
+  const float* dkp = bw.dkt + ((int64_t)bhq * T + t0) * WK;
+  if (tid < 64) bsh[tid] = (float)beta[b * bst.b + h * bst.h + (int64_t)(t0 + tid) * bst.t];
+  // ---- A: the forward's in-chunk matrices ----
+  f32x16 aA = z, aQW = z, aWK = z;
+#pragma unroll 1
+  for (int hh = 0; hh < 2; ++hh) {
+    load_rows64_f32(S[0], wp + 64 * hh, wst.t);
+    load_rows64_f32(S[1], qp + 64 * hh, qs.t);
+    load_rows64_f32(S[2], kp + 64 * hh, ks.t);
+    __syncthreads();
+    aA = mgemm64<false, true>(S[0], S[0], aA);
+    aQW = mgemm64<false, true>(S[1], S[0], aQW);
+    aWK = mgemm64<false, true>(S[0], S[2], aWK);
+    __syncthreads();
+  }
+  DL_FOR_E {
+    const float br = bsh[dl_row(e)];
+    aA[e] *= br;
+    aWK[e] *= br;
+  }
+  float(*Tm)[68] = S[3];
+  float(*QW)[68] = S[4];
+  float(*WBK)[68] = S[5];
+  float(*TW)[68] = S[6];
+  float(*dA)[68] = S[7];
+  dl_store(Tm, aA, 2);
+  dl_store(QW, aQW, 1);
+  dl_store(WBK, aWK, 2);
+  __syncthreads();
+  invert_unit_lower64(Tm);
+  dl_store(TW, mgemm64<false, false>(Tm, WBK, z), 0);
+  load_blk(dA, bw.dad + ((int64_t)bhq * NT + c) * 4096, 64);
+  __syncthreads();
+  // ---- B ----
+  f32x16 aW2[2], aW[2], dQW = z, dTW = z;
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+    load_blk(S[0], w2p + 64 * hh, WK);
+    load_blk(S[1], dqp + 64 * hh, WK);
+    __syncthreads();
+    dQW = mgemm64<false, true>(S[1], S[0], dQW);          // dq~_h W2_h^T
+    aW2[hh] = dl_neg(mgemm64<true, false>(QW, S[1], z));  // -QW^T dq~_h
+    __syncthreads();
+  }
+  dQW = dl_neg(mgemm64<false, true>(dA, TW, dQW));  // -(dq~ W2^T + dA TW^T)
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+    load_rows64_f32(S[0], wp + 64 * hh, wst.t);
+    load_blk(S[1], dkp + 64 * hh, WK);
+    __syncthreads();
+    dTW = mgemm64<false, true>(S[0], S[1], dTW);         // W_h dk~_h^T
+    aW[hh] = dl_neg(mgemm64<false, false>(TW, S[1], z));  // -TW dk~_h
+    __syncthreads();
+  }
+  dTW = dl_neg(mgemm64<true, false>(QW, dA, dTW));  // -(W dk~^T + QW^T dA)
+  __syncthreads();
+  // dW2(:, b) -= W_a dHc(a, b), dW(:, a) -= W2_b dHc(a, b)^T
+  load_rows64_f32(S[0], wp, wst.t);
+  load_rows64_f32(S[1], wp + 64, wst.t);
+  load_blk(S[2], w2p, WK);
+  load_blk(S[4], w2p + 64, WK);
+  {
+    const float* dhc = bw.dhc + ((int64_t)bhq * NT + c) * (WK * WK);
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk) {
+      const int ra = blk >> 1, cb_ = blk & 1;
+      load_blk(S[6], dhc + (int64_t)64 * ra * WK + 64 * cb_, WK);
+      __syncthreads();
+      const f32x16 t1 = mgemm64<false, true>(cb_ ? S[4] : S[2], S[6], z);
+      const f32x16 t2 = mgemm64<false, false>(ra ? S[1] : S[0], S[6], z);
+      DL_FOR_E {
+        aW[ra][e] -= t1[e];
+        aW2[cb_][e] -= t2[e];
+      }
+      __syncthreads();
+    }
+  }
+  // ---- C ----
+  dl_store(S[8], dTW, 0);
+  dl_store(S[2], aW2[0], 0);
+  dl_store(S[4], aW2[1], 0);
+  __syncthreads();
+  f32x16 dTm = mgemm64<false, true>(S[8], WBK, z);  // dTW WBK^T
+  {
+    f32x16 t = mgemm64<false, true>(S[2], S[0], z);  // dW2 W^T, then the column scaling by beta
+    t = mgemm64<false, true>(S[4], S[1], t);
+    const float bc = bsh[cl];
+    DL_FOR_E dTm[e] = fmaf(t[e], bc, dTm[e]);
+  }
+  f32x16 aWb[2];
+  aWb[0] = mgemm64<true, false>(Tm, S[2], z);  // Tm^T dW2
+  aWb[1] = mgemm64<true, false>(Tm, S[4], z);
+  const f32x16 dWBK = mgemm64<true, false>(Tm, S[8], z);  // Tm^T dTW
+  __syncthreads();
+  dl_store(S[5], dWBK, 2);
+  dl_store(S[6], dTm, 0);
+  __syncthreads();
+  dl_store(S[8], mgemm64<true, false>(Tm, S[6], z), 0);  // Tm^T dTm
+  __syncthreads();
+  const f32x16 da = dl_neg(mgemm64<false, true>(S[8], Tm, z));
+  __syncthreads();
+  dl_store(S[6], da, 2);
+  dl_store(S[8], dQW, 1);
+  // ---- D: per 64-column half ----
+  float rs[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) rs[e] = 0.f;
+#pragma unroll 1
+  for (int hh = 0; hh < 2; ++hh) {
+    float(*Wh)[68] = hh ? S[1] : S[0];
+    load_rows64_f32(S[4], qp + 64 * hh, qs.t);
+    load_rows64_f32(S[3], kp + 64 * hh, ks.t);
+    for (int idx = tid; idx < 4096; idx += 256) S[2][idx >> 6][idx & 63] = bsh[idx >> 6] * Wh[idx >> 6][idx & 63];
+    __syncthreads();
+    f32x16 aq = mgemm64<false, false>(dA, S[3], z);  // dA K_h
+    aq = mgemm64<false, false>(S[8], Wh, aq);        // + tril(dQW) W_h
+    f32x16 ak = mgemm64<true, false>(dA, S[4], z);   // dA^T Q_h
+    ak = mgemm64<true, false>(S[5], S[2], ak);       // + dWBK^T Wb_h
+    f32x16 wb = mgemm64<false, false>(S[5], S[3], aWb[hh]);  // + dWBK K_h
+    wb = mgemm64<false, false>(S[6], Wh, wb);                 // + da W_h
+    f32x16 dw = mgemm64<true, false>(S[8], S[4], aW[hh]);     // + tril(dQW)^T Q_h
+    dw = mgemm64<true, false>(S[6], S[2], dw);                // + da^T Wb_h
+    const int64_t rowbase = ((int64_t)bhq * T + t0) * WK + 64 * hh;
+    DL_FOR_E {
+      const int r = dl_row(e);
+      const int64_t off = rowbase + (int64_t)r * WK + cl;
+      bw.dq[off] = aq[e] + dqp[r * WK + 64 * hh + cl];
+      bw.dk[off] = ak[e] + dkp[r * WK + 64 * hh + cl];
+      bw.dw[off] = fmaf(bsh[r], wb[e], dw[e]);
+      rs[e] = fmaf(wb[e], Wh[r][cl], rs[e]);
+    }
+    __syncthreads();
+  }
+  // db_r = sum over the 128 columns: the 32 lanes of a half-wave, then the two column-half waves
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    float x = rs[e];
+    x += __shfl_xor(x, 1, 64);
+    x += __shfl_xor(x, 2, 64);
+    x += __shfl_xor(x, 4, 64);
+    x += __shfl_xor(x, 8, 64);
+    x += __shfl_xor(x, 16, 64);
+    rs[e] = x;
+  }
+  if ((lane & 31) == 0) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) dbs[wv & 1][32 * (wv >> 1) + drow(e, g)] = rs[e];
+  }
+  __syncthreads();
+  if (tid < 64) bw.db[(int64_t)bhq * T + t0 + tid] = dbs[0][tid] + dbs[1][tid];
 }
 
 }  // namespace lucid

@@ -77,3 +77,45 @@ def test_lucid_path_d128_forward_long(B, T, H, G):
         err = (o[:, :, hq].double() - ref[:, :, hq]).abs().max().item()
         print(f"  head {hq} o: max err {err:.2e} max|ref| {ref[:, :, hq].abs().max().item():.2e}", flush=True)
         check(f"o[{hq}]", err, ref[:, :, hq].abs().max().item())
+
+
+@pytest.mark.parametrize("B,T,H,G,K,V", [(1, 256, 1, 1, 128, 128), (2, 192, 2, 2, 128, 128),
+                                         (1, 200, 1, 1, 64, 128), (1, 128, 2, 1, 128, 32)])
+def test_lucid_path_d128_backward_short(B, T, H, G, K, V):
+    from lucid_amd.lucid_path import parallel_lucid_path_attention
+    q, k, v, w, beta, do = _inputs(B, T, H, G, K, V, seed=13 * T + K + V)
+    print(f"case path d128 bwd B={B} T={T} H={H} G={G} K={K} V={V}", flush=True)
+    leaves = [x.cuda().requires_grad_() for x in (q, k, v, w, beta)]
+    o, _ = parallel_lucid_path_attention(leaves[1], leaves[2], leaves[3], leaves[4], q=leaves[0])
+    o.backward(do.cuda())
+    torch.cuda.synchronize()
+    Tp = (T + 63) // 64 * 64
+    s = K ** -0.5
+    ref = P.path_attention_chunked(*(_pad_t(x, Tp) for x in (q, k, v, w, beta)), scale=s, C=64)[:, :T]
+    check("o", (o.detach().cpu().double() - ref).abs().max().item(), ref.abs().max().item())
+    grads = P.path_attention_grads(*(_pad_t(x, Tp) for x in (q, k, v, w, beta)), _pad_t(do, Tp), scale=s, C=64)
+    for name, got, r in zip(("dq", "dk", "dv", "dw", "dbeta"), leaves, grads):
+        r = r[:, :T]
+        assert got.grad.shape == r.shape, name
+        err = (got.grad.cpu().double() - r).abs().max().item()
+        print(f"  {name}: max err {err:.2e} max|ref| {r.abs().max().item():.2e}", flush=True)
+        check(name, err, r.abs().max().item())
+
+
+@pytest.mark.parametrize("B,T,H,G", [(1, 1024, 2, 2), (1, 8192, 1, 1)])
+def test_lucid_path_d128_backward_long(B, T, H, G):
+    """Gradients across super-chunks: the row and column sweeps over QB / QS operands, the
+    128 x 128 transport gradients (dHL, dHc) and the products backward."""
+    from lucid_amd.lucid_path import parallel_lucid_path_attention
+    q, k, v, w, beta, do = (x.cuda() for x in _inputs(B, T, H, G, 128, 128, seed=3 * T + G))
+    print(f"case path d128 bwd long B={B} T={T} H={H} G={G}", flush=True)
+    leaves = [x.clone().requires_grad_() for x in (q, k, v, w, beta)]
+    o, _ = parallel_lucid_path_attention(leaves[1], leaves[2], leaves[3], leaves[4], q=leaves[0])
+    o.backward(do)
+    torch.cuda.synchronize()
+    ref_o, ref_g = PD.path_attention_dense(q, k, v, w, beta, do=do, scale=128 ** -0.5)
+    check("o", (o.detach().double() - ref_o).abs().max().item(), ref_o.abs().max().item())
+    for name, got, r in zip(("dq", "dk", "dv", "dw", "dbeta"), leaves, ref_g):
+        err = (got.grad.double() - r).abs().max().item()
+        print(f"  {name}: max err {err:.2e} max|ref| {r.abs().max().item():.2e}", flush=True)
+        check(name, err, r.abs().max().item())
