@@ -875,15 +875,17 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_bwd_col
 // PaTH softmax backward of the diagonal blocks, per (chunk c, query head):
 //   delta_i = dO_i . O_i,  P = exp2(s' A_diag - lse_i) (j <= i),
 //   dA_diag = s P (dO V^T - delta_i),  dV_c = P^T dO_c   (the column sweep adds the rest)
-// fp32 on LDS.  grid (NT, B*HQ)
+// fp32 on LDS, dO and V rows as 64-column halves at KD = 128.  grid (NT, B*HQ)
 // ---------------------------------------------------------------------------
+template <int KD>
 __global__ __launch_bounds__(256) void path_softmax_diag_bwd_kernel(const bf16* __restrict__ dout, Strides dos,
                                                                     const bf16* __restrict__ o, Strides os,
                                                                     const bf16* __restrict__ v, Strides vs, int HQ,
                                                                     int H, int T, float scale, PathFwdWs ws,
                                                                     PathBwdWs bw) {
-  __shared__ __attribute__((aligned(16))) float Dm[64][68];
-  __shared__ __attribute__((aligned(16))) float Vm[64][68];
+  constexpr int NH = KD / 64;
+  __shared__ __attribute__((aligned(16))) float Dm[NH][64][68];
+  __shared__ __attribute__((aligned(16))) float Vm[NH][64][68];
   __shared__ __attribute__((aligned(16))) float Pm[64][68];
   __shared__ float dls[64], lss[64];
   const int NT = T / PC;
@@ -893,16 +895,20 @@ __global__ __launch_bounds__(256) void path_softmax_diag_bwd_kernel(const bf16* 
   const int tid = threadIdx.x;
   const int r0 = (tid >> 4) * 4, c0 = (tid & 15) * 4;
   const int t0 = c * PC;
-  load_rows64_f32(Dm, dout + b * dos.b + hq * dos.h + (int64_t)t0 * dos.t, dos.t);
-  load_rows64_f32(Vm, v + b * vs.b + h * vs.h + (int64_t)t0 * vs.t, vs.t);
-  {  // delta of row r: 4 threads x 16 columns
+#pragma unroll
+  for (int hh = 0; hh < NH; ++hh) {
+    load_rows64_f32(Dm[hh], dout + b * dos.b + hq * dos.h + (int64_t)t0 * dos.t + 64 * hh, dos.t);
+    load_rows64_f32(Vm[hh], v + b * vs.b + h * vs.h + (int64_t)t0 * vs.t + 64 * hh, vs.t);
+  }
+  {  // delta of row r: 4 threads x 16 columns per 64-column half
     const int r = tid >> 2, cc = (tid & 3) * 16;
     const bf16* orow = o + b * os.b + hq * os.h + (int64_t)(t0 + r) * os.t + cc;
     const bf16* drow_ = dout + b * dos.b + hq * dos.h + (int64_t)(t0 + r) * dos.t + cc;
     float acc = 0.f;
 #pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-      const bf16x8 x = ld8(orow + 8 * hh), y = ld8(drow_ + 8 * hh);
+    for (int hh = 0; hh < 2 * NH; ++hh) {
+      const int off = 64 * (hh >> 1) + 8 * (hh & 1);
+      const bf16x8 x = ld8(orow + off), y = ld8(drow_ + off);
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc = fmaf((float)x[e], (float)y[e], acc);
     }
@@ -929,7 +935,8 @@ __global__ __launch_bounds__(256) void path_softmax_diag_bwd_kernel(const bf16* 
   __syncthreads();
   float acc[4][4];
   zero44(acc);
-  lds_gemm64<false, true>(Dm, Vm, acc);  // dP = dO V^T
+#pragma unroll
+  for (int hh = 0; hh < NH; ++hh) lds_gemm64<false, true>(Dm[hh], Vm[hh], acc);  // dP = dO V^T
   {
     float* dst = bw.dad + ((int64_t)bhq * NT + c) * 4096;
 #pragma unroll
@@ -940,16 +947,17 @@ __global__ __launch_bounds__(256) void path_softmax_diag_bwd_kernel(const bf16* 
       *reinterpret_cast<f32x4*>(dst + (r0 + i) * 64 + c0) = x;
     }
   }
-  zero44(acc);
-  lds_gemm64<true, false>(Pm, Dm, acc);  // dV_c = P^T dO
-  {
-    float* dst = bw.dvf + ((int64_t)bhq * T + t0) * 64;
+#pragma unroll
+  for (int hh = 0; hh < NH; ++hh) {
+    zero44(acc);
+    lds_gemm64<true, false>(Pm, Dm[hh], acc);  // dV_c = P^T dO
+    float* dst = bw.dvf + ((int64_t)bhq * T + t0) * KD + 64 * hh;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       f32x4 x;
 #pragma unroll
       for (int j = 0; j < 4; ++j) x[j] = acc[i][j];
-      *reinterpret_cast<f32x4*>(dst + (r0 + i) * 64 + c0) = x;
+      *reinterpret_cast<f32x4*>(dst + (r0 + i) * KD + c0) = x;
     }
   }
 }

@@ -319,9 +319,8 @@ int lucid_path_bwd(const void* dout, const int64_t* do_strides, const void* q, c
 }
 
 size_t lucid_path_softmax_fwd_workspace_bytes(int B, int T, int H, int HQ, int K) {
-  (void)K;
   size_t n = 0;
-  carve_path_fwd(nullptr, B, T, H, HQ, &n, true);
+  carve_path_fwd(nullptr, B, T, H, HQ, &n, true, K > 64 ? 128 : 64);
   return n;
 }
 
@@ -332,7 +331,6 @@ int lucid_path_softmax_fwd(const void* q, const int64_t* q_strides, const void* 
                            int K, float scale, void* stream) {
   g_path_error.clear();
   if (int rc = check_shapes(B, T, H, HQ, K)) return rc;
-  if (K != 64) return pfail("the softmax path runs at head_dim 64 only, got " + std::to_string(K));
   if (int rc = pcheck_vec("q", q, q_strides)) return rc;
   if (int rc = pcheck_vec("k", k, k_strides)) return rc;
   if (int rc = pcheck_vec("v", v, v_strides)) return rc;
@@ -343,23 +341,27 @@ int lucid_path_softmax_fwd(const void* q, const int64_t* q_strides, const void* 
     if (int rc = pcheck_vec("kcache", kcache, kcache_strides)) return rc;
   if (!fwd_ws) return pfail("fwd_ws is null");
   if (reinterpret_cast<uintptr_t>(fwd_ws) % 256) return pfail("fwd_ws must be 256-byte aligned");
-  const lucid::PathFwdWs ws = carve_path_fwd(fwd_ws, B, T, H, HQ, nullptr, true);
+  const lucid::PathFwdWs ws = carve_path_fwd(fwd_ws, B, T, H, HQ, nullptr, true, K);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int NT = T / 64;
-  if (int rc = launch_front(q, q_strides, k, k_strides, w, w_strides, beta, beta_strides, B, T, H, HQ, scale, 1, ws, st))
+  if (int rc = launch_front(q, q_strides, k, k_strides, w, w_strides, beta, beta_strides, B, T, H, HQ, scale, 1, ws, st,
+                            K))
     return rc;
-  LUCID_TIMED_LAUNCH(phip, "path_softmax_fwd_kernel", lucid::path_softmax_fwd_kernel, dim3(B * HQ, (NT + 3) / 4), st,
-                     (const bf16*)v, PS(v_strides), (bf16*)o, PS(o_strides), HQ, H, T, scale, ws);
+  if (K == 128)
+    LUCID_TIMED_LAUNCH(phip, "path_softmax_fwd_kernel", lucid::path_softmax_fwd_kernel<128>, dim3(B * HQ, (NT + 3) / 4),
+                       st, (const bf16*)v, PS(v_strides), (bf16*)o, PS(o_strides), HQ, H, T, scale, ws);
+  else
+    LUCID_TIMED_LAUNCH(phip, "path_softmax_fwd_kernel", lucid::path_softmax_fwd_kernel<64>, dim3(B * HQ, (NT + 3) / 4),
+                       st, (const bf16*)v, PS(v_strides), (bf16*)o, PS(o_strides), HQ, H, T, scale, ws);
   if (kcache)
-    if (int rc = launch_kcache(kcache, kcache_strides, B, T, H, ws, st)) return rc;
+    if (int rc = launch_kcache(kcache, kcache_strides, B, T, H, ws, st, K)) return rc;
   return 0;
 }
 
 size_t lucid_path_softmax_bwd_workspace_bytes(int B, int T, int H, int HQ, int K) {
   (void)H;
-  (void)K;
   size_t n = 0;
-  carve_path_bwd(nullptr, B, T, HQ, &n, true);
+  carve_path_bwd(nullptr, B, T, HQ, &n, true, K > 64 ? 128 : 64);
   return n;
 }
 
@@ -373,7 +375,6 @@ int lucid_path_softmax_bwd(const void* dout, const int64_t* do_strides, const vo
                            float scale, void* stream) {
   g_path_error.clear();
   if (int rc = check_shapes(B, T, H, HQ, K)) return rc;
-  if (K != 64) return pfail("the backward runs at head_dim 64 only, got " + std::to_string(K));
   if (int rc = pcheck_vec("dout", dout, do_strides)) return rc;
   if (int rc = pcheck_vec("q", q, q_strides)) return rc;
   if (int rc = pcheck_vec("k", k, k_strides)) return rc;
@@ -389,22 +390,36 @@ int lucid_path_softmax_bwd(const void* dout, const int64_t* do_strides, const vo
   if (!fwd_ws || !bwd_ws) return pfail("fwd_ws and bwd_ws must be non-null");
   if (reinterpret_cast<uintptr_t>(fwd_ws) % 256 || reinterpret_cast<uintptr_t>(bwd_ws) % 256)
     return pfail("fwd_ws and bwd_ws must be 256-byte aligned");
-  const lucid::PathFwdWs ws = carve_path_fwd(const_cast<void*>(fwd_ws), B, T, H, HQ, nullptr, true);
-  const lucid::PathBwdWs bw = carve_path_bwd(bwd_ws, B, T, HQ, nullptr, true);
+  const lucid::PathFwdWs ws = carve_path_fwd(const_cast<void*>(fwd_ws), B, T, H, HQ, nullptr, true, K);
+  const lucid::PathBwdWs bw = carve_path_bwd(bwd_ws, B, T, HQ, nullptr, true, K);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int NT = T / 64, NS = (NT + 7) / 8;
   const int BHq = B * HQ;
-  const int64_t n_hl = (int64_t)BHq * NS * 4096, n_hc = (int64_t)BHq * NT * 4096;
+  const int64_t n_hl = (int64_t)BHq * NS * K * K, n_hc = (int64_t)BHq * NT * K * K;
   LUCID_TIMED_LAUNCH(phip, "path_bwd_zero_kernel", lucid::path_bwd_zero_kernel, dim3(1024), st, n_hl, n_hc, BHq, bw);
-  LUCID_TIMED_LAUNCH(phip, "path_softmax_diag_bwd_kernel", lucid::path_softmax_diag_bwd_kernel, dim3(NT, BHq), st,
-                     (const bf16*)dout, PS(do_strides), (const bf16*)o, PS(o_strides), (const bf16*)v, PS(v_strides),
-                     HQ, H, T, scale, ws, bw);
-  LUCID_TIMED_LAUNCH(phip, "path_softmax_bwd_row_kernel", (lucid::path_bwd_row_kernel<true, 64>), dim3(BHq, (NT + 1) / 2), st,
-                     (const bf16*)dout, PS(do_strides), (const bf16*)v, PS(v_strides), HQ, H, T, scale, ws, bw);
-  LUCID_TIMED_LAUNCH(phip, "path_softmax_bwd_col_kernel", (lucid::path_bwd_col_kernel<true, 64>), dim3(BHq, (NT + 1) / 2), st,
-                     (const bf16*)dout, PS(do_strides), (const bf16*)v, PS(v_strides), HQ, H, T, scale, ws, bw);
+  if (K == 128) {
+    LUCID_TIMED_LAUNCH(phip, "path_softmax_diag_bwd_kernel", lucid::path_softmax_diag_bwd_kernel<128>, dim3(NT, BHq),
+                       st, (const bf16*)dout, PS(do_strides), (const bf16*)o, PS(o_strides), (const bf16*)v,
+                       PS(v_strides), HQ, H, T, scale, ws, bw);
+    LUCID_TIMED_LAUNCH(phip, "path_softmax_bwd_row_kernel", (lucid::path_bwd_row_kernel<true, 128>),
+                       dim3(BHq, (NT + 1) / 2), st, (const bf16*)dout, PS(do_strides), (const bf16*)v, PS(v_strides),
+                       HQ, H, T, scale, ws, bw);
+    LUCID_TIMED_LAUNCH(phip, "path_softmax_bwd_col_kernel", (lucid::path_bwd_col_kernel<true, 128>),
+                       dim3(BHq, (NT + 1) / 2), st, (const bf16*)dout, PS(do_strides), (const bf16*)v, PS(v_strides),
+                       HQ, H, T, scale, ws, bw);
+  } else {
+    LUCID_TIMED_LAUNCH(phip, "path_softmax_diag_bwd_kernel", lucid::path_softmax_diag_bwd_kernel<64>, dim3(NT, BHq),
+                       st, (const bf16*)dout, PS(do_strides), (const bf16*)o, PS(o_strides), (const bf16*)v,
+                       PS(v_strides), HQ, H, T, scale, ws, bw);
+    LUCID_TIMED_LAUNCH(phip, "path_softmax_bwd_row_kernel", (lucid::path_bwd_row_kernel<true, 64>),
+                       dim3(BHq, (NT + 1) / 2), st, (const bf16*)dout, PS(do_strides), (const bf16*)v, PS(v_strides),
+                       HQ, H, T, scale, ws, bw);
+    LUCID_TIMED_LAUNCH(phip, "path_softmax_bwd_col_kernel", (lucid::path_bwd_col_kernel<true, 64>),
+                       dim3(BHq, (NT + 1) / 2), st, (const bf16*)dout, PS(do_strides), (const bf16*)v, PS(v_strides),
+                       HQ, H, T, scale, ws, bw);
+  }
   return launch_back(q, q_strides, k, k_strides, w, w_strides, beta, beta_strides, dq, dq_strides, dk, dk_strides, dv,
-                     dv_strides, dw, dw_strides, dbeta, dbeta_strides, B, T, H, HQ, ws, bw, st);
+                     dv_strides, dw, dw_strides, dbeta, dbeta_strides, B, T, H, HQ, ws, bw, st, K);
 }
 
 void lucid_path_profile_enable(int on) { lucid_prof::enabled() = on != 0; }

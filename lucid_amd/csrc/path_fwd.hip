@@ -629,16 +629,20 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_solve_f
 // (exp2 domain) is kept for the backward.  grid (B*HQ, ceil(NT/4)), the groups with the
 // most key chunks (of all heads) first.
 // ---------------------------------------------------------------------------
+template <int KD>
 struct SoftmaxFwdSmem {
-  bf16 k[2][64 * 64];   // swizzled (chunk c of row r at c ^ (r & 7))
-  bf16 v[2][64 * 64];
-  bf16 vd[4][64 * 64];  // V rows of the group's own chunks (diagonal blocks)
+  bf16 k[2][64 * KD];   // swizzled (chunk c of row r at c ^ (r & 7))
+  bf16 v[2][64 * KD];
+  bf16 vd[4][64 * KD];  // V rows of the group's own chunks (diagonal blocks)
 };
 
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void path_softmax_fwd_kernel(
+// KD: head dim (64 or 128)
+template <int KD>
+__global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_softmax_fwd_kernel(
     const bf16* __restrict__ v, Strides vs, bf16* __restrict__ o, Strides os, int HQ, int H, int T, float scale,
     PathFwdWs ws) {
-  __shared__ __attribute__((aligned(16))) SoftmaxFwdSmem sm;
+  constexpr int NKS = KD / 16, NVT = KD / 32, CPR = KD / 8;  // k-steps, 32-column tiles, 16-byte chunks per row
+  __shared__ __attribute__((aligned(16))) SoftmaxFwdSmem<KD> sm;
   const int NT = T / PC, NS = (NT + PR - 1) / PR, NQ = (NT + 3) / 4;
   const int I1 = 4 * (NQ - 1 - (int)blockIdx.y), bhq = blockIdx.x;  // heaviest groups of all heads first
   const int G_ = HQ / H;
@@ -652,20 +656,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
   const float sl2 = scale * LOG2E_F;
   const bf16* vh = v + b * vs.b + h * vs.h;
 
-  int plan_k[2], plan_v[2];
-  dma_plan<64, 8>(64, plan_k);
-  dma_plan<64, 8>(vs.t, plan_v);
+  int plan_k[64 * CPR / 256], plan_v[64 * CPR / 256];
+  dma_plan<64, CPR>(KD, plan_k);
+  dma_plan<64, CPR>(vs.t, plan_v);
   auto stage = [&](int J) {
     const int buf = J & 1;
-    dma_stage<64, 8>(plan_k, ((J < cb) ? ws.kl : ws.kt) + ((int64_t)bh * T + J * PC) * 64, sm.k[buf]);
-    dma_stage<64, 8>(plan_v, vh + (int64_t)J * PC * vs.t, sm.v[buf]);
+    dma_stage<64, CPR>(plan_k, ((J < cb) ? ws.kl : ws.kt) + ((int64_t)bh * T + J * PC) * KD, sm.k[buf]);
+    dma_stage<64, CPR>(plan_v, vh + (int64_t)J * PC * vs.t, sm.v[buf]);
   };
 #pragma unroll
   for (int c = 0; c < 4; ++c)
-    if (I1 + c < NT) dma_stage<64, 8>(plan_v, vh + (int64_t)(I1 + c) * PC * vs.t, sm.vd[c]);
+    if (I1 + c < NT) dma_stage<64, CPR>(plan_v, vh + (int64_t)(I1 + c) * PC * vs.t, sm.vd[c]);
   if (nJ > 0) stage(0);
 
-  f32x16 acc[2][2];
+  f32x16 acc[2][NVT];
   float m[2] = {0.f, 0.f}, l[2] = {0.f, 0.f};
   dma_wait();
   __syncthreads();
@@ -673,8 +677,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
   // j = 32 jh + drow(e, g); keys j > rl are masked
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
-    acc[nt][0] = zero16();
-    acc[nt][1] = zero16();
+#pragma unroll
+    for (int t = 0; t < NVT; ++t) acc[nt][t] = zero16();
     if (!live) continue;
     const int rl = nt * 32 + l32;
     const float* ad = ws.ld + ((int64_t)bhq * NT + Iw) * 4096 + rl * 64;
@@ -706,23 +710,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
       }
       const bf16x8 p0 = pack_b(sd[jh], 0), p1 = pack_b(sd[jh], 1);
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        acc[nt][t] = mfma32(lds_tr_a<8>(vt, jh * 32, t * 32), p0, acc[nt][t]);
-        acc[nt][t] = mfma32(lds_tr_a<8>(vt, jh * 32 + 16, t * 32), p1, acc[nt][t]);
+      for (int t = 0; t < NVT; ++t) {
+        acc[nt][t] = mfma32(lds_tr_a<CPR>(vt, jh * 32, t * 32), p0, acc[nt][t]);
+        acc[nt][t] = mfma32(lds_tr_a<CPR>(vt, jh * 32 + 16, t * 32), p1, acc[nt][t]);
       }
     }
   }
-  bf16x8 qb[2][4];
+  bf16x8 qb[2][NKS];
   for (int J = 0; J < nJ; ++J) {
     const int buf = J & 1;
     if (J + 1 < nJ) stage(J + 1);
     if (J >= cb || J % PR == 0) {  // the query operand changes
-      const bf16* qsrc = (J < cb) ? ws.qb + ((int64_t)bhq * NS + J / PR) * T * 64
-                                  : ws.qs + ((int64_t)bhq * PR + (J - cb)) * T * 64;
+      const bf16* qsrc = (J < cb) ? ws.qb + ((int64_t)bhq * NS + J / PR) * T * KD
+                                  : ws.qs + ((int64_t)bhq * PR + (J - cb)) * T * KD;
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
-        for (int st = 0; st < 4; ++st) qb[nt][st] = ld8(qsrc + (int64_t)(iw0 + nt * 32 + l32) * 64 + 16 * st + 8 * g);
+        for (int st = 0; st < NKS; ++st)
+          qb[nt][st] = ld8(qsrc + (int64_t)(iw0 + nt * 32 + l32) * KD + 16 * st + 8 * g);
     }
     if (live && J < Iw) {
 #pragma unroll
@@ -732,8 +737,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
         for (int jh = 0; jh < 2; ++jh) {
           sc[jh] = zero16();
 #pragma unroll
-          for (int st = 0; st < 4; ++st)
-            sc[jh] = mfma32(ld8(swz<8>(sm.k[buf], jh * 32 + l32, 2 * st + g)), qb[nt][st], sc[jh]);
+          for (int st = 0; st < NKS; ++st)
+            sc[jh] = mfma32(ld8(swz<CPR>(sm.k[buf], jh * 32 + l32, 2 * st + g)), qb[nt][st], sc[jh]);
         }
         float mx = -INFINITY;
 #pragma unroll
@@ -746,7 +751,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
         m[nt] = mn;
         l[nt] *= alpha;
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+        for (int t = 0; t < NVT; ++t)
 #pragma unroll
           for (int e = 0; e < 16; ++e) acc[nt][t][e] *= alpha;
 #pragma unroll
@@ -758,9 +763,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
           }
           const bf16x8 p0 = pack_b(sc[jh], 0), p1 = pack_b(sc[jh], 1);
 #pragma unroll
-          for (int t = 0; t < 2; ++t) {
-            acc[nt][t] = mfma32(lds_tr_a<8>(sm.v[buf], jh * 32, t * 32), p0, acc[nt][t]);
-            acc[nt][t] = mfma32(lds_tr_a<8>(sm.v[buf], jh * 32 + 16, t * 32), p1, acc[nt][t]);
+          for (int t = 0; t < NVT; ++t) {
+            acc[nt][t] = mfma32(lds_tr_a<CPR>(sm.v[buf], jh * 32, t * 32), p0, acc[nt][t]);
+            acc[nt][t] = mfma32(lds_tr_a<CPR>(sm.v[buf], jh * 32 + 16, t * 32), p1, acc[nt][t]);
           }
         }
       }
@@ -776,7 +781,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
       const int i = iw0 + nt * 32 + l32;
       bf16* orow = o + b * os.b + hq * os.h + (int64_t)i * os.t;
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+      for (int t = 0; t < NVT; ++t)
 #pragma unroll
         for (int qq = 0; qq < 4; ++qq) {
           bf16x4 bb;

@@ -119,3 +119,45 @@ def test_lucid_path_d128_backward_long(B, T, H, G):
         err = (got.grad.double() - r).abs().max().item()
         print(f"  {name}: max err {err:.2e} max|ref| {r.abs().max().item():.2e}", flush=True)
         check(name, err, r.abs().max().item())
+
+
+@pytest.mark.parametrize("B,T,H,G,K,V", [(1, 256, 1, 1, 128, 128), (1, 192, 1, 2, 128, 128), (1, 128, 2, 1, 64, 128)])
+def test_path_softmax_d128_short(B, T, H, G, K, V):
+    """PaTH softmax attention on the head-dim-128 kernels against the brute-force float64
+    oracle (explicit Householder products), forward and backward."""
+    from lucid_amd.lucid_path import parallel_path_attention
+    q, k, v, w, beta, do = _inputs(B, T, H, G, K, V, seed=17 * T + K + V)
+    print(f"case path softmax d128 B={B} T={T} H={H} G={G} K={K} V={V}", flush=True)
+    leaves = [x.cuda().requires_grad_() for x in (q, k, v, w, beta)]
+    o, _ = parallel_path_attention(*leaves)
+    o.backward(do.cuda())
+    torch.cuda.synchronize()
+    s = K ** -0.5
+    ref = P.path_softmax_bruteforce(*(_f64(x) for x in (q, k, v, w, beta)), scale=s)
+    err = (o.detach().cpu().double() - ref).abs().max().item()
+    print(f"  o: max err {err:.2e} max|ref| {ref.abs().max().item():.2e}", flush=True)
+    check("o", err, ref.abs().max().item())
+    grads = P.path_softmax_grads(*(_f64(x) for x in (q, k, v, w, beta)), _f64(do), scale=s)
+    for name, got, r in zip(("dq", "dk", "dv", "dw", "dbeta"), leaves, grads):
+        err = (got.grad.cpu().double() - r).abs().max().item()
+        print(f"  {name}: max err {err:.2e} max|ref| {r.abs().max().item():.2e}", flush=True)
+        check(name, err, r.abs().max().item())
+
+
+@pytest.mark.parametrize("B,T,H,G", [(1, 1024, 2, 2), (1, 4096, 1, 1)])
+def test_path_softmax_d128_long(B, T, H, G):
+    from lucid_amd.lucid_path import parallel_path_attention
+    q, k, v, w, beta, do = (x.cuda() for x in _inputs(B, T, H, G, 128, 128, seed=5 * T + G))
+    print(f"case path softmax d128 long B={B} T={T} H={H} G={G}", flush=True)
+    leaves = [x.clone().requires_grad_() for x in (q, k, v, w, beta)]
+    o, _ = parallel_path_attention(*leaves)
+    o.backward(do)
+    torch.cuda.synchronize()
+    ref_o, ref_g = PD.path_attention_dense(q, k, v, w, beta, do=do, scale=128 ** -0.5, softmax=True)
+    err = (o.detach().double() - ref_o).abs().max().item()
+    print(f"  o: max err {err:.2e} max|ref| {ref_o.abs().max().item():.2e}", flush=True)
+    check("o", err, ref_o.abs().max().item())
+    for name, got, r in zip(("dq", "dk", "dv", "dw", "dbeta"), leaves, ref_g):
+        err = (got.grad.double() - r).abs().max().item()
+        print(f"  {name}: max err {err:.2e} max|ref| {r.abs().max().item():.2e}", flush=True)
+        check(name, err, r.abs().max().item())
