@@ -6,9 +6,9 @@
  *   A_ij = q_i^T H_i ... H_{j+1} k_j,  H_t = I - beta_t w_t w_t^T.
  * Layouts as the reference: q [B,T,HQ,K], k/w [B,T,H,K], v [B,T,H,V], beta [B,T,H],
  * o [B,T,HQ,V]; element strides {batch, head, time}, last axis contiguous.
- * bf16 tensors; K = V = 64, or K = V = 128 (LUCID-Path); T a multiple of 64
- * (the Python layer zero-pads the
- * sequence end, exact for every real row since L is strictly lower triangular).
+ * bf16 tensors with K = V = 64 or K = V = 128, or fp32 tensors (the _f32 entry points) with
+ * K = V = 64; T a multiple of 64 (the Python layer zero-pads the sequence end, exact for every
+ * real row since L is strictly lower triangular, and smaller head dims to 64 or 128).
  * Buffers are caller-owned (no device allocation; the bounded chain waits set up a 4-byte
  * pinned flag on the first chain call per device, as in lucid_amd.h -- call
  * lucid_path_chain_status() once before HIP graph capture); launches go on `stream`.
@@ -106,6 +106,44 @@ int lucid_path_softmax_bwd(const void* dout, const int64_t* do_strides, const vo
                            const int64_t* dv_strides, void* dw, const int64_t* dw_strides, void* dbeta,
                            const int64_t* dbeta_strides, void* bwd_ws, int B, int T, int H, int HQ, int K,
                            float scale, void* stream);
+
+/*
+ * fp32 tensors (the reference's LUCID-Path model is fp32: lucid_path/config/config.json:5).
+ * Same contracts as the bf16 entry points above, K = V = 64 (smaller head dims zero-padded
+ * by the caller); every product of the sweeps runs as a 3-term bf16 split (hi.hi + hi.lo +
+ * lo.hi) on hi / lo copies of its operands, ~fp32 accuracy.  The workspaces are larger
+ * (the lo copies): size them with the _f32 workspace functions.  The reference's Triton
+ * kernels take fp32 tensors through the same entry points (parallel.py:180-241).
+ */
+size_t lucid_path_fwd_f32_workspace_bytes(int B, int T, int H, int HQ, int K);
+int lucid_path_fwd_f32(const float* q, const int64_t* q_strides, const float* k, const int64_t* k_strides,
+                       const float* v, const int64_t* v_strides, const float* w, const int64_t* w_strides,
+                       const float* beta, const int64_t* beta_strides, float* o, const int64_t* o_strides,
+                       float* kcache, const int64_t* kcache_strides, void* fwd_ws, int B, int T, int H, int HQ, int K,
+                       float scale, void* stream);
+size_t lucid_path_bwd_f32_workspace_bytes(int B, int T, int H, int HQ, int K);
+int lucid_path_bwd_f32(const float* dout, const int64_t* do_strides, const float* q, const int64_t* q_strides,
+                       const float* k, const int64_t* k_strides, const float* w, const int64_t* w_strides,
+                       const float* beta, const int64_t* beta_strides, const float* o, const int64_t* o_strides,
+                       const void* fwd_ws, float* dq, const int64_t* dq_strides, float* dk, const int64_t* dk_strides,
+                       float* dv, const int64_t* dv_strides, float* dw, const int64_t* dw_strides, float* dbeta,
+                       const int64_t* dbeta_strides, void* bwd_ws, int B, int T, int H, int HQ, int K, float scale,
+                       void* stream);
+size_t lucid_path_softmax_fwd_f32_workspace_bytes(int B, int T, int H, int HQ, int K);
+int lucid_path_softmax_fwd_f32(const float* q, const int64_t* q_strides, const float* k, const int64_t* k_strides,
+                               const float* v, const int64_t* v_strides, const float* w, const int64_t* w_strides,
+                               const float* beta, const int64_t* beta_strides, float* o, const int64_t* o_strides,
+                               float* kcache, const int64_t* kcache_strides, void* fwd_ws, int B, int T, int H,
+                               int HQ, int K, float scale, void* stream);
+size_t lucid_path_softmax_bwd_f32_workspace_bytes(int B, int T, int H, int HQ, int K);
+int lucid_path_softmax_bwd_f32(const float* dout, const int64_t* do_strides, const float* q,
+                               const int64_t* q_strides, const float* k, const int64_t* k_strides, const float* v,
+                               const int64_t* v_strides, const float* w, const int64_t* w_strides, const float* beta,
+                               const int64_t* beta_strides, const float* o, const int64_t* o_strides,
+                               const void* fwd_ws, float* dq, const int64_t* dq_strides, float* dk,
+                               const int64_t* dk_strides, float* dv, const int64_t* dv_strides, float* dw,
+                               const int64_t* dw_strides, float* dbeta, const int64_t* dbeta_strides, void* bwd_ws,
+                               int B, int T, int H, int HQ, int K, float scale, void* stream);
 
 /* Per-kernel timing with HIP events (no counterpart in the reference; used by
  * bench.py), same contract as lucid_profile_* in lucid_amd.h. */

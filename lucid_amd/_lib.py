@@ -108,6 +108,20 @@ _SIGS = {
         "lucid_path_softmax_bwd": ([_vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p,
                                     _vp, _i64p, _vp, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p,
                                     _vp, _int, _int, _int, _int, _int, _flt, _vp], _int),
+        "lucid_path_fwd_f32_workspace_bytes": ([_int] * 5, _sz),
+        "lucid_path_fwd_f32": ([_vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p,
+                                _vp, _i64p, _vp, _int, _int, _int, _int, _int, _flt, _vp], _int),
+        "lucid_path_bwd_f32_workspace_bytes": ([_int] * 5, _sz),
+        "lucid_path_bwd_f32": ([_vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp,
+                                _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp,
+                                _int, _int, _int, _int, _int, _flt, _vp], _int),
+        "lucid_path_softmax_fwd_f32_workspace_bytes": ([_int] * 5, _sz),
+        "lucid_path_softmax_fwd_f32": ([_vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p,
+                                        _vp, _i64p, _vp, _int, _int, _int, _int, _int, _flt, _vp], _int),
+        "lucid_path_softmax_bwd_f32_workspace_bytes": ([_int] * 5, _sz),
+        "lucid_path_softmax_bwd_f32": ([_vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p,
+                                        _vp, _i64p, _vp, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp,
+                                        _i64p, _vp, _int, _int, _int, _int, _int, _flt, _vp], _int),
         "lucid_path_profile_enable": ([_int], None),
         "lucid_path_profile_collect": ([], _int),
         "lucid_path_profile_entry": ([_int, ctypes.c_char_p, _int, ctypes.POINTER(ctypes.c_double),

@@ -36,7 +36,36 @@ struct PathBwdWs {
   float* db;    // [BHq][T]
   int* counters;  // [BHq]
   float* delta; // [BHq][T]           PaTH softmax only: rowsum(dO * O)
+  // fp32 inputs: element offsets of the lo planes of dvb, dvT (0 with bf16 inputs)
+  int64_t lo_dvb, lo_dvT;
+  // fp32 inputs: split copies (hi plane, lo plane at + lo_*) of the rows the sweeps stage
+  // from the caller: xsp = dO [BHq][T][K] (PaTH softmax), ysp = O [BHq][T][K] (LUCID-Path)
+  // or V [BH][T][K] (PaTH softmax)
+  bf16* xsp;
+  bf16* ysp;
+  int64_t lo_xsp, lo_ysp;
 };
+
+// fp32 rows x [B][T][HH][K] (element strides xs: batch, head, time) -> bf16 hi and lo planes,
+// contiguous [B][HH][T][K], the lo plane at dst + lo.  4 values per thread; grid
+// (ceil(T K / 1024), B*HH)
+__global__ __launch_bounds__(256) void path_split_kernel(const float* __restrict__ x, Strides xs, bf16* __restrict__ dst,
+                                                         int64_t lo, int HH, int T, int K) {
+  const int bhh = blockIdx.y, b = bhh / HH, hh = bhh - b * HH;
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i >= (int64_t)T * K) return;
+  const int t = (int)(i / K), c = (int)(i - (int64_t)t * K);
+  const f32x4 v = *reinterpret_cast<const f32x4*>(x + b * xs.b + hh * xs.h + (int64_t)t * xs.t + c);
+  bf16x4 h4, l4;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    h4[u] = (bf16)v[u];
+    l4[u] = (bf16)(v[u] - (float)h4[u]);
+  }
+  bf16* d = dst + (int64_t)bhh * T * K + i;
+  *reinterpret_cast<bf16x4*>(d) = h4;
+  *reinterpret_cast<bf16x4*>(d + lo) = l4;
+}
 
 __global__ __launch_bounds__(256) void path_bwd_zero_kernel(int64_t n_hl, int64_t n_hc, int n_cnt, PathBwdWs bw) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -64,30 +93,33 @@ __global__ __launch_bounds__(256) void path_bwd_zero_kernel(int64_t n_hl, int64_
 // depends on the operands only and is computed before the sweep; the fp32 buffers
 // of the final step reuse the staging space.
 // ---------------------------------------------------------------------------
-template <int KD>
+template <int KD, int NP>
 struct DvSmem {
   union {
     struct {
-      bf16 q[2][2][64 * KD];  // [buffer][tile of the pair, or column chunk], swizzled (chunk c of row r at c ^ (r & 7))
-      bf16 d[2][2][KD * 64];
+      // [buffer][tile of the pair, or column chunk][plane], swizzled (chunk c of row r at c ^ (r & 7))
+      bf16 q[2][2][NP][64 * KD];
+      bf16 d[2][2][NP][KD * 64];
     } st;
     struct {
       float Rt[KD][132];    // R^T for the 128 columns (0..63 = A), then dV rows of one chunk
       float Yt[64][68];     // Yt[c][r] = Y[r][c] of the chunk being solved, then O rows
-      bf16 dt[KD][128 + 8];  // dV^T of both chunks, T-perm within 16-groups
+      bf16 dt[NP][KD][128 + 8];  // dV^T of both chunks, T-perm within 16-groups
     } fin;
   } u;
-  bf16x8 lba[4][64][2];  // L_BA as MFMA B operands, per wave and lane
+  bf16x8 lba[4][64][2 * NP];  // L_BA as MFMA B operands, per wave and lane ([2 + h]: lo)
 };
 
 // KD: head dim (64 or 128); at 128 a wave owns value tiles w >> 1 and (w >> 1) + 2 of the
 // final solve, and dA_diag is summed over the two 64-column halves of dV and O
-template <int KD>
-__global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_dv_kernel(const bf16* __restrict__ dout, Strides dos,
-                                                      const bf16* __restrict__ o, Strides os, int HQ, int H, int T,
-                                                      int BHq, float scale, PathFwdWs ws, PathBwdWs bw) {
+// F32: fp32 dO and O; every operand product is a 3-term split over hi / lo planes (mm3)
+template <int KD, bool F32>
+__global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64 && !F32) void path_dv_kernel(
+    const pin_t<F32>* __restrict__ dout, Strides dos, const pin_t<F32>* __restrict__ o, Strides os, int HQ, int H,
+    int T, int BHq, float scale, PathFwdWs ws, PathBwdWs bw) {
   constexpr int NKS = KD / 16, NVT = KD / 32;  // k-steps of a logit product, 32-column value tiles
-  __shared__ __attribute__((aligned(16))) DvSmem<KD> sm;
+  constexpr int NP = F32 ? 2 : 1;
+  __shared__ __attribute__((aligned(16))) DvSmem<KD, NP> sm;
   const int NT = T / PC, NS = (NT + PR - 1) / PR, NQ = (NT + 1) / 2;
   const int id = blockIdx.x;
   const int q = NQ - 1 - id / BHq, bhq = id - (id / BHq) * BHq;
@@ -105,23 +137,35 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_dv_kern
   int* cnt = bw.counters + bhq;
   const float sl2 = scale * LOG2E_F, cc0 = LOG2E_F / scale;
 
-  bf16x8 kbs[NKS], kbf[NKS];
+  bf16x8 kbs[NKS][NP], kbf[NKS][NP];
 #pragma unroll
   for (int st = 0; st < NKS; ++st) {
-    kbs[st] = ld8(ws.kt + ((int64_t)bh * T + jc) * KD + 16 * st + 8 * g);
-    kbf[st] = ld8(ws.kl + ((int64_t)bh * T + jc) * KD + 16 * st + 8 * g);
+    const bf16* ps = ws.kt + ((int64_t)bh * T + jc) * KD + 16 * st + 8 * g;
+    const bf16* pf = ws.kl + ((int64_t)bh * T + jc) * KD + 16 * st + 8 * g;
+    kbs[st][0] = ld8(ps);
+    kbf[st][0] = ld8(pf);
+    if constexpr (F32) {
+      kbs[st][1] = ld8(ps + ws.lo_kt);
+      kbf[st][1] = ld8(pf + ws.lo_kl);
+    }
   }
   // accumulators start at -dO^T (R = dO - acc = -acc)
   f32x16 acc[NVT];
   {
-    const bf16* drow_ = dout + b * dos.b + hq * dos.h + (int64_t)jc * dos.t;
+    const pin_t<F32>* drow_ = dout + b * dos.b + hq * dos.h + (int64_t)jc * dos.t;
 #pragma unroll
     for (int t = 0; t < NVT; ++t)
 #pragma unroll
       for (int qq = 0; qq < 4; ++qq) {
-        const bf16x4 x = *reinterpret_cast<const bf16x4*>(drow_ + t * 32 + 8 * qq + 4 * g);
+        if constexpr (F32) {
+          const f32x4 x = *reinterpret_cast<const f32x4*>(drow_ + t * 32 + 8 * qq + 4 * g);
 #pragma unroll
-        for (int u = 0; u < 4; ++u) acc[t][4 * qq + u] = -(float)x[u];
+          for (int u = 0; u < 4; ++u) acc[t][4 * qq + u] = -x[u];
+        } else {
+          const bf16x4 x = *reinterpret_cast<const bf16x4*>(drow_ + t * 32 + 8 * qq + 4 * g);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) acc[t][4 * qq + u] = -(float)x[u];
+        }
       }
   }
   // QS slot of column chunk c (relative to the large chunk) for row chunk I inside it
@@ -133,11 +177,23 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_dv_kern
     const bf16* kr = ws.kt + ((int64_t)bh * T + j0 + na * 32 + l32) * KD;
     f32x16 sc = zero16();
 #pragma unroll
-    for (int st = 0; st < NKS; ++st) sc = mfma32(ld8(qr + 16 * st + 8 * g), ld8(kr + 16 * st + 8 * g), sc);
+    for (int st = 0; st < NKS; ++st) {
+      bf16x8 qa8[NP], ka8[NP];
+      qa8[0] = ld8(qr + 16 * st + 8 * g);
+      ka8[0] = ld8(kr + 16 * st + 8 * g);
+      if constexpr (F32) {
+        qa8[1] = ld8(qr + ws.lo_qs + 16 * st + 8 * g);
+        ka8[1] = ld8(kr + ws.lo_kt + 16 * st + 8 * g);
+      }
+      sc = mm3<NP>(qa8, ka8, sc);
+    }
 #pragma unroll
     for (int e = 0; e < 16; ++e) sc[e] = __builtin_amdgcn_exp2f(fmaf(sc[e], sl2, -cc0));
-    sm.lba[w][lane][0] = pack_b(sc, 0);
-    sm.lba[w][lane][1] = pack_b(sc, 1);
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      sm.lba[w][lane][hh] = pack_b(sc, hh);
+      if constexpr (F32) sm.lba[w][lane][2 + hh] = pack_lo(sc, hh, sm.lba[w][lane][hh]);
+    }
   }
   // row tile k (k = 0 .. n-1) is chunk I = NT-1-k, published once the counter exceeds k.
   // Tiles k < nfar lie beyond the large chunk (swept in pairs); the rest one per step.
@@ -156,17 +212,24 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_dv_kern
         const int k = k0 + u;
         if (k < nfar) {
           const int I = NT - 1 - k;
-          dma_stage<64, KD / 8>(plan_q, ws.qb + (((int64_t)bhq * NS + sJ) * T + (int64_t)I * PC) * KD,
-                                sm.u.st.q[buf][u]);
-          dma_stage<KD, 8>(plan_t, bw.dvT + (int64_t)bhq * KD * T + I * PC, sm.u.st.d[buf][u]);
+#pragma unroll
+          for (int pl = 0; pl < NP; ++pl) {
+            dma_stage<64, KD / 8>(plan_q, ws.qb + pl * ws.lo_qb + (((int64_t)bhq * NS + sJ) * T + (int64_t)I * PC) * KD,
+                                  sm.u.st.q[buf][u][pl]);
+            dma_stage<KD, 8>(plan_t, bw.dvT + pl * bw.lo_dvT + (int64_t)bhq * KD * T + I * PC, sm.u.st.d[buf][u][pl]);
+          }
         }
       }
     } else {
       const int I = NT - 1 - k0;
 #pragma unroll
-      for (int c = 0; c < 2; ++c)
-        if (c == 0 || hasB) dma_stage<64, KD / 8>(plan_q, qs_slot(c) + (int64_t)I * PC * KD, sm.u.st.q[buf][c]);
-      dma_stage<KD, 8>(plan_t, bw.dvT + (int64_t)bhq * KD * T + I * PC, sm.u.st.d[buf][0]);
+      for (int pl = 0; pl < NP; ++pl) {
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+          if (c == 0 || hasB)
+            dma_stage<64, KD / 8>(plan_q, qs_slot(c) + pl * ws.lo_qs + (int64_t)I * PC * KD, sm.u.st.q[buf][c][pl]);
+        dma_stage<KD, 8>(plan_t, bw.dvT + pl * bw.lo_dvT + (int64_t)bhq * KD * T + I * PC, sm.u.st.d[buf][0][pl]);
+      }
     }
   };
   // Y_A, Y_B (fp32) are fetched into registers during the last step
@@ -187,22 +250,35 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_dv_kern
       for (int e = 0; e < 4; ++e) sm.u.fin.Yt[c4 + e][r] = yr[u][e];
     }
   };
-  // one staged 64-row tile against this wave's 32 columns
-  auto tile = [&](const bf16* qt, const bf16* dtl, bool same) {
+  // one staged 64-row tile (planes qt[pl], dtl[pl]) against this wave's 32 columns
+  auto tile = [&](bf16* const* qt, bf16* const* dtl, bool same) {
 #pragma unroll
     for (int rh = 0; rh < 2; ++rh) {
       f32x16 sc = zero16();
 #pragma unroll
-      for (int st = 0; st < NKS; ++st)
-        sc = mfma32(ld8(swz<KD / 8>(qt, rh * 32 + l32, 2 * st + g)), same ? kbs[st] : kbf[st], sc);
+      for (int st = 0; st < NKS; ++st) {
+        bf16x8 qa[NP];
+#pragma unroll
+        for (int pl = 0; pl < NP; ++pl) qa[pl] = ld8(swz<KD / 8>(qt[pl], rh * 32 + l32, 2 * st + g));
+        sc = mm3<NP>(qa, same ? kbs[st] : kbf[st], sc);
+      }
 #pragma unroll
       for (int e = 0; e < 16; ++e) sc[e] = __builtin_amdgcn_exp2f(fmaf(sc[e], sl2, -cc0));
-      const bf16x8 p0 = pack_b(sc, 0), p1 = pack_b(sc, 1);
+      bf16x8 p[2][NP];
 #pragma unroll
-      for (int t = 0; t < NVT; ++t) {
-        acc[t] = mfma32(ld8(swz<8>(dtl, t * 32 + l32, 4 * rh + g)), p0, acc[t]);
-        acc[t] = mfma32(ld8(swz<8>(dtl, t * 32 + l32, 4 * rh + 2 + g)), p1, acc[t]);
+      for (int hh = 0; hh < 2; ++hh) {
+        p[hh][0] = pack_b(sc, hh);
+        if constexpr (F32) p[hh][1] = pack_lo(sc, hh, p[hh][0]);
       }
+#pragma unroll
+      for (int t = 0; t < NVT; ++t)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          bf16x8 da[NP];
+#pragma unroll
+          for (int pl = 0; pl < NP; ++pl) da[pl] = ld8(swz<8>(dtl[pl], t * 32 + l32, 4 * rh + 2 * hh + g));
+          acc[t] = mm3<NP>(da, p[hh], acc[t]);
+        }
     }
   };
   int ready = 0;
@@ -232,11 +308,25 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_dv_kern
     } else {
       yload();
     }
+    auto planes = [&](bf16 (*x)[KD * 64], bf16** out) {
+#pragma unroll
+      for (int pl = 0; pl < NP; ++pl) out[pl] = x[pl];
+    };
+    bf16* qp_[NP];
+    bf16* dp_[NP];
     if (s < nfs) {
-      tile(sm.u.st.q[buf][0], sm.u.st.d[buf][0], false);
-      if (2 * s + 1 < nfar) tile(sm.u.st.q[buf][1], sm.u.st.d[buf][1], false);
+      planes(sm.u.st.q[buf][0], qp_);
+      planes(sm.u.st.d[buf][0], dp_);
+      tile(qp_, dp_, false);
+      if (2 * s + 1 < nfar) {
+        planes(sm.u.st.q[buf][1], qp_);
+        planes(sm.u.st.d[buf][1], dp_);
+        tile(qp_, dp_, false);
+      }
     } else {
-      tile(sm.u.st.q[buf][mycols ? wc : 0], sm.u.st.d[buf][0], true);
+      planes(sm.u.st.q[buf][mycols ? wc : 0], qp_);
+      planes(sm.u.st.d[buf][0], dp_);
+      tile(qp_, dp_, true);
     }
     if (more && !early) {
       ready = wait_counter_gt(cnt, need(s + 1));
@@ -281,15 +371,20 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_dv_kern
     for (int qq = 0; qq < 4; ++qq) {
       const int d0 = dt * 32 + 8 * qq + 4 * g;
       f32x4 f;
-      bf16x4 bb;
+      bf16x4 bb, bl;
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         f[u] = dvo[4 * qq + u];
         bb[u] = (bf16)f[u];
-        sm.u.fin.dt[d0 + u][lslot] = bb[u];
+        sm.u.fin.dt[0][d0 + u][lslot] = bb[u];
+        if constexpr (F32) {
+          bl[u] = (bf16)(f[u] - (float)bb[u]);
+          sm.u.fin.dt[NP - 1][d0 + u][lslot] = bl[u];
+        }
       }
       *reinterpret_cast<f32x4*>(of + d0) = f;
       *reinterpret_cast<bf16x4*>(ob + d0) = bb;
+      if constexpr (F32) *reinterpret_cast<bf16x4*>(ob + bw.lo_dvb + d0) = bl;
     }
     dvs[i] = dvo;
    }
@@ -299,8 +394,9 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_dv_kern
     __syncthreads();
     for (int c = tid; c < KD * 8; c += 256) {
       const int dd = c >> 3, s8 = (c & 7) * 8;
-      *reinterpret_cast<bf16x8*>(bw.dvT + ((int64_t)bhq * KD + dd) * T + j0 + cc * 64 + s8) =
-          ld8(&sm.u.fin.dt[dd][cc * 64 + s8]);
+      bf16* dst = bw.dvT + ((int64_t)bhq * KD + dd) * T + j0 + cc * 64 + s8;
+      *reinterpret_cast<bf16x8*>(dst) = ld8(&sm.u.fin.dt[0][dd][cc * 64 + s8]);
+      if constexpr (F32) *reinterpret_cast<bf16x8*>(dst + bw.lo_dvT) = ld8(&sm.u.fin.dt[NP - 1][dd][cc * 64 + s8]);
     }
     publish_counter(cnt, NT - (A + cc));
   };
@@ -310,12 +406,23 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_dv_kern
     publish_chunk(1);
     // ---- R_A -= L_BA^T dV_B: wave -> (A columns half na, B rows half kb); Y_A^T to LDS ----
     const int na = w & 1, kb = w >> 1;
-    const bf16x8 l0 = sm.lba[w][lane][0], l1 = sm.lba[w][lane][1];
+    bf16x8 lb[2][NP];
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      lb[hh][0] = sm.lba[w][lane][hh];
+      if constexpr (F32) lb[hh][1] = sm.lba[w][lane][2 + hh];
+    }
     f32x16 cr[NVT];
 #pragma unroll
     for (int t = 0; t < NVT; ++t) {
-      cr[t] = mfma32(ld8(&sm.u.fin.dt[t * 32 + l32][64 + kb * 32 + 8 * g]), l0, zero16());
-      cr[t] = mfma32(ld8(&sm.u.fin.dt[t * 32 + l32][64 + kb * 32 + 16 + 8 * g]), l1, cr[t]);
+      cr[t] = zero16();
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        bf16x8 da[NP];
+#pragma unroll
+        for (int pl = 0; pl < NP; ++pl) da[pl] = ld8(&sm.u.fin.dt[pl][t * 32 + l32][64 + kb * 32 + 16 * hh + 8 * g]);
+        cr[t] = mm3<NP>(da, lb[hh], cr[t]);
+      }
     }
     const int col = na * 32 + l32;
     if (kb == 1) {
@@ -379,20 +486,23 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_dv_kern
 // with X = dV, Y = O (rows of the same query head); PaTH softmax (SM = true)
 // dA = s P (X_I Y_J^T - delta_i), P = exp2(s' S - lse_i), X = dO, Y = V (kv head).
 // ---------------------------------------------------------------------------
-template <int KD>
+template <int KD, int NP>
 struct RowSmem {
-  bf16 k[2][64 * KD];  // swizzled (chunk c of row r at c ^ (r & 7))
-  bf16 o[2][64 * KD];
+  bf16 k[2][NP][64 * KD];  // [buffer][plane], swizzled (chunk c of row r at c ^ (r & 7))
+  bf16 o[2][NP][64 * KD];
   float g[128][KD + 4];  // G rows of the pair at a transport step
 };
 
-// KD: head dim (64 or 128); the KD x KD transport matrices and their gradients are row-major
-template <bool SM, int KD>
-__global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_bwd_row_kernel(
-    const bf16* __restrict__ xsrc, Strides xs, const bf16* __restrict__ ysrc, Strides ys, int HQ, int H, int T,
-    float scale, PathFwdWs ws, PathBwdWs bw) {
+// KD: head dim (64 or 128); the KD x KD transport matrices and their gradients are row-major.
+// F32: X and Y rows are bf16 hi planes with their lo planes at xsrc + x_lo, ysrc + y_lo, and
+// every operand product is a 3-term split (mm3)
+template <bool SM, int KD, bool F32>
+__global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64 && !F32) void path_bwd_row_kernel(
+    const bf16* __restrict__ xsrc, Strides xs, int64_t x_lo, const bf16* __restrict__ ysrc, Strides ys, int64_t y_lo,
+    int HQ, int H, int T, float scale, PathFwdWs ws, PathBwdWs bw) {
   constexpr int NKS = KD / 16, NVT = KD / 32, CPR = KD / 8;  // k-steps, 32-column tiles, 16-byte chunks per row
-  __shared__ __attribute__((aligned(16))) RowSmem<KD> sm;
+  constexpr int NP = F32 ? 2 : 1;
+  __shared__ __attribute__((aligned(16))) RowSmem<KD, NP> sm;
   const int NT = T / PC, NS = (NT + PR - 1) / PR;
   const int I1 = 2 * ((int)gridDim.y - 1 - (int)blockIdx.y), bhq = blockIdx.x;  // heaviest pairs of all heads first
   const int G_ = HQ / H;
@@ -406,11 +516,14 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_bwd_row
   const int nJ = pair ? I1 + 1 : I1;                // key tiles needed by the pair
   const float sl2 = scale * LOG2E_F, cc0 = LOG2E_F / scale;
 
-  bf16x8 dvr[NKS];
+  bf16x8 dvr[NKS][NP];
   {
     const bf16* xrow = xsrc + b * xs.b + hq * xs.h + (int64_t)(iw0 + l32) * xs.t;
 #pragma unroll
-    for (int st = 0; st < NKS; ++st) dvr[st] = ld8(xrow + 16 * st + 8 * g);
+    for (int st = 0; st < NKS; ++st) {
+      dvr[st][0] = ld8(xrow + 16 * st + 8 * g);
+      if constexpr (F32) dvr[st][1] = ld8(xrow + x_lo + 16 * st + 8 * g);
+    }
   }
   // exponent offset and delta of this lane's row (LUCID-Path: the constant 1/s, no delta)
   const float ci = SM ? ws.lse[(int64_t)bhq * T + iw0 + l32] : cc0;
@@ -428,12 +541,14 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_bwd_row
   // ---- dM += X^T G over the pair's rows (atomic) and G <- G M^T for each wave's rows ----
   // X (rows of the query operand, row-major) is staged into the idle half of the double
   // buffer (tile J+1 is staged only after the transition); X^T comes from transposing reads
-  auto transition = [&](int J, const bf16* X, const float* M, float* dM) {
+  auto transition = [&](int J, const bf16* X, int64_t xlo, const float* M, float* dM) {
     const bool act = Iw < NT && J < Iw;
-    bf16* xa_t = sm.k[(J + 1) & 1];  // X rows of chunk I1
-    bf16* xb_t = sm.o[(J + 1) & 1];  // X rows of chunk I1 + 1
-    dma_stage<64, CPR>(plan_k, X + (int64_t)I1 * PC * KD, xa_t);
-    if (pair) dma_stage<64, CPR>(plan_k, X + (int64_t)(I1 + 1) * PC * KD, xb_t);
+    // planes of the X rows of chunk I1 (in k) and I1 + 1 (in o)
+#pragma unroll
+    for (int pl = 0; pl < NP; ++pl) {
+      dma_stage<64, CPR>(plan_k, X + pl * xlo + (int64_t)I1 * PC * KD, sm.k[(J + 1) & 1][pl]);
+      if (pair) dma_stage<64, CPR>(plan_k, X + pl * xlo + (int64_t)(I1 + 1) * PC * KD, sm.o[(J + 1) & 1][pl]);
+    }
 #pragma unroll
     for (int t = 0; t < NVT; ++t)
 #pragma unroll
@@ -447,7 +562,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_bwd_row
       // rows of a chunk that has left the sweep are skipped: its X rows may be undefined
       const int ks0 = (J < I1) ? 0 : 4, ks1 = (pair && J < I1 + 1) ? 8 : 4;
       for (int ks = ks0; ks < ks1; ++ks) {
-        const bf16x8 xa = lds_tr_a<CPR>(ks < 4 ? xa_t : xb_t, 16 * (ks & 3), at * 32);
+        const bf16x8 xa = lds_tr_a<CPR>(ks < 4 ? sm.k[(J + 1) & 1][0] : sm.o[(J + 1) & 1][0], 16 * (ks & 3), at * 32);
         bf16x8 gh, gl;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -457,6 +572,9 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_bwd_row
         }
         dm = mfma32(xa, gh, dm);
         dm = mfma32(xa, gl, dm);
+        if constexpr (F32)
+          dm = mfma32(lds_tr_a<CPR>(ks < 4 ? sm.k[(J + 1) & 1][1] : sm.o[(J + 1) & 1][1], 16 * (ks & 3), at * 32), gh,
+                      dm);
       }
 #pragma unroll
       for (int e = 0; e < 16; ++e) unsafeAtomicAdd(dM + (at * 32 + drow(e, g)) * KD + bt * 32 + l32, F * dm[e]);
@@ -483,32 +601,40 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_bwd_row
   auto stage = [&](int J) {
     const int buf = J & 1;
     const bf16* kr = ((J < cb) ? ws.kl : ws.kt) + ((int64_t)bh * T + J * PC) * KD;
-    dma_stage<64, CPR>(plan_k, kr, sm.k[buf]);
-    dma_stage<64, CPR>(plan_o, yh + (int64_t)J * PC * ys.t, sm.o[buf]);
+    const int64_t klo = (J < cb) ? ws.lo_kl : ws.lo_kt;
+#pragma unroll
+    for (int pl = 0; pl < NP; ++pl) {
+      dma_stage<64, CPR>(plan_k, kr + pl * klo, sm.k[buf][pl]);
+      dma_stage<64, CPR>(plan_o, yh + pl * y_lo + (int64_t)J * PC * ys.t, sm.o[buf][pl]);
+    }
   };
   if (nJ > 0) stage(0);
   dma_wait();
   __syncthreads();
-  bf16x8 qb[NKS];
+  bf16x8 qb[NKS][NP];
   for (int J = 0; J < nJ; ++J) {
     const int buf = J & 1;
     // transport step before the first tile that uses a new query operand
     if (J < cb) {
       if (J % PR == 0 && J > 0) {
         const int s = J / PR;
-        transition(J, ws.qb + ((int64_t)bhq * NS + s) * T * KD, ws.hl + ((int64_t)bh * NS + s) * (KD * KD),
+        transition(J, ws.qb + ((int64_t)bhq * NS + s) * T * KD, ws.lo_qb, ws.hl + ((int64_t)bh * NS + s) * (KD * KD),
                    bw.dhl + ((int64_t)bhq * NS + s) * (KD * KD));
       }
     } else if (sI > 0 || J > cb) {
-      transition(J, ws.qs + ((int64_t)bhq * PR + (J - cb)) * T * KD, ws.hc + ((int64_t)bh * NT + J) * (KD * KD),
-                 bw.dhc + ((int64_t)bhq * NT + J) * (KD * KD));
+      transition(J, ws.qs + ((int64_t)bhq * PR + (J - cb)) * T * KD, ws.lo_qs,
+                 ws.hc + ((int64_t)bh * NT + J) * (KD * KD), bw.dhc + ((int64_t)bhq * NT + J) * (KD * KD));
     }
     if (J + 1 < nJ) stage(J + 1);
     if (J >= cb || J % PR == 0) {  // the query operand changes
       const bf16* qsrc = (J < cb) ? ws.qb + ((int64_t)bhq * NS + J / PR) * T * KD
                                   : ws.qs + ((int64_t)bhq * PR + (J - cb)) * T * KD;
+      const int64_t qlo = (J < cb) ? ws.lo_qb : ws.lo_qs;
 #pragma unroll
-      for (int st = 0; st < NKS; ++st) qb[st] = ld8(qsrc + (int64_t)(iw0 + l32) * KD + 16 * st + 8 * g);
+      for (int st = 0; st < NKS; ++st) {
+        qb[st][0] = ld8(qsrc + (int64_t)(iw0 + l32) * KD + 16 * st + 8 * g);
+        if constexpr (F32) qb[st][1] = ld8(qsrc + qlo + (int64_t)(iw0 + l32) * KD + 16 * st + 8 * g);
+      }
     }
     if (Iw < NT && J < Iw) {
 #pragma unroll
@@ -516,20 +642,35 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_bwd_row
         f32x16 sc = zero16(), dp = zero16();
 #pragma unroll
         for (int st = 0; st < NKS; ++st) {
-          sc = mfma32(ld8(swz<CPR>(sm.k[buf], jh * 32 + l32, 2 * st + g)), qb[st], sc);
-          dp = mfma32(ld8(swz<CPR>(sm.o[buf], jh * 32 + l32, 2 * st + g)), dvr[st], dp);
+          bf16x8 ka[NP], oa[NP];
+#pragma unroll
+          for (int pl = 0; pl < NP; ++pl) {
+            ka[pl] = ld8(swz<CPR>(sm.k[buf][pl], jh * 32 + l32, 2 * st + g));
+            oa[pl] = ld8(swz<CPR>(sm.o[buf][pl], jh * 32 + l32, 2 * st + g));
+          }
+          sc = mm3<NP>(ka, qb[st], sc);
+          dp = mm3<NP>(oa, dvr[st], dp);
         }
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           const float ex = __builtin_amdgcn_exp2f(SM ? fmaf(sc[e], sl2, -ci) : sc[e] * sl2);
           sc[e] = SM ? ex * (dp[e] - di) : dp[e] * ex;
         }
-        const bf16x8 d0 = pack_b(sc, 0), d1 = pack_b(sc, 1);
+        bf16x8 dd[2][NP];
 #pragma unroll
-        for (int t = 0; t < NVT; ++t) {
-          acc[t] = mfma32(lds_tr_a<CPR>(sm.k[buf], jh * 32, t * 32), d0, acc[t]);
-          acc[t] = mfma32(lds_tr_a<CPR>(sm.k[buf], jh * 32 + 16, t * 32), d1, acc[t]);
+        for (int hh = 0; hh < 2; ++hh) {
+          dd[hh][0] = pack_b(sc, hh);
+          if constexpr (F32) dd[hh][1] = pack_lo(sc, hh, dd[hh][0]);
         }
+#pragma unroll
+        for (int t = 0; t < NVT; ++t)
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) {
+            bf16x8 ka[NP];
+#pragma unroll
+            for (int pl = 0; pl < NP; ++pl) ka[pl] = lds_tr_a<CPR>(sm.k[buf][pl], jh * 32 + 16 * hh, t * 32);
+            acc[t] = mm3<NP>(ka, dd[hh], acc[t]);
+          }
       }
     }
     dma_wait();
@@ -566,13 +707,13 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_bwd_row
 // delta are staged beside each query tile, and dV_J^T[d][j] += dO_I^T[d][i] P[i][j]
 // is accumulated too and added to the diagonal block's part in dvf.
 // ---------------------------------------------------------------------------
-template <bool SM, int KD>
+template <bool SM, int KD, int NP>
 struct ColSmem {
   union {
     struct {
-      bf16 qa[3][64 * KD];  // swizzled (chunk c of row r at c ^ (r & 7))
-      bf16 qb[3][64 * KD];
-      bf16 dv[3][64 * KD];
+      bf16 qa[3][NP][64 * KD];  // [buffer][plane], swizzled (chunk c of row r at c ^ (r & 7))
+      bf16 qb[3][NP][64 * KD];
+      bf16 dv[3][NP][64 * KD];
     } st;
     struct {  // 64-column halves at KD = 128
       float a[KD / 64][64][68];  // d k~ (same large chunk), then the result
@@ -638,14 +779,16 @@ __device__ __forceinline__ void col_finish128(float (*a)[64][68], float (*f)[64]
   }
 }
 
-// KD: head dim (64 or 128)
-template <bool SM, int KD>
-__global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_bwd_col_kernel(
-    const bf16* __restrict__ xsrc, Strides xs, const bf16* __restrict__ ysrc, Strides ys, int HQ, int H, int T,
-    float scale, PathFwdWs ws, PathBwdWs bw) {
+// KD: head dim (64 or 128).  F32: X and Y rows are bf16 hi planes with their lo planes at
+// xsrc + x_lo, ysrc + y_lo, and every operand product is a 3-term split (mm3)
+template <bool SM, int KD, bool F32>
+__global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64 && !F32) void path_bwd_col_kernel(
+    const bf16* __restrict__ xsrc, Strides xs, int64_t x_lo, const bf16* __restrict__ ysrc, Strides ys, int64_t y_lo,
+    int HQ, int H, int T, float scale, PathFwdWs ws, PathBwdWs bw) {
   constexpr int NKS = KD / 16, NVT = KD / 32, CPR = KD / 8;  // k-steps, 32-column tiles, 16-byte chunks per row
-  constexpr int PT = 64 * CPR / 256;  // direct loads per wave for one staged tile
-  __shared__ __attribute__((aligned(16))) ColSmem<SM, KD> sm;
+  constexpr int NP = F32 ? 2 : 1;
+  constexpr int PT = NP * 64 * CPR / 256;  // direct loads per wave for one staged tile (all planes)
+  __shared__ __attribute__((aligned(16))) ColSmem<SM, KD, NP> sm;
   const int NT = T / PC, NS = (NT + PR - 1) / PR;
   const int J1 = 2 * blockIdx.y, bhq = blockIdx.x;  // heaviest (earliest) key pairs of all heads first
   const int G_ = HQ / H;
@@ -660,15 +803,22 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_bwd_col
   // F = s): the constant F is applied to the dK accumulators where the sweep hands them on
   const float F = SM ? scale : -scale * __builtin_amdgcn_exp2f(-cc0);
 
-  bf16x8 kbs[NKS], kbf[NKS], ob[NKS];
+  bf16x8 kbs[NKS][NP], kbf[NKS][NP], ob[NKS][NP];
   {
     const int jr = min(J1 * PC + 32 * w + l32, T - 1);
     const bf16* yrow = ysrc + b * ys.b + (SM ? hq / G_ : hq) * ys.h + (int64_t)jr * ys.t;
 #pragma unroll
     for (int st = 0; st < NKS; ++st) {
-      kbs[st] = ld8(ws.kt + ((int64_t)bh * T + jr) * KD + 16 * st + 8 * g);
-      kbf[st] = ld8(ws.kl + ((int64_t)bh * T + jr) * KD + 16 * st + 8 * g);
-      ob[st] = ld8(yrow + 16 * st + 8 * g);
+      const bf16* ps = ws.kt + ((int64_t)bh * T + jr) * KD + 16 * st + 8 * g;
+      const bf16* pf = ws.kl + ((int64_t)bh * T + jr) * KD + 16 * st + 8 * g;
+      kbs[st][0] = ld8(ps);
+      kbf[st][0] = ld8(pf);
+      ob[st][0] = ld8(yrow + 16 * st + 8 * g);
+      if constexpr (F32) {
+        kbs[st][1] = ld8(ps + ws.lo_kt);
+        kbf[st][1] = ld8(pf + ws.lo_kl);
+        ob[st][1] = ld8(yrow + y_lo + 16 * st + 8 * g);
+      }
     }
   }
   f32x16 as_[NVT], af[NVT];
@@ -692,11 +842,16 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_bwd_col
     const bool same = I <= ceJ;
     const bf16* q1 = same ? ws.qs + ((int64_t)bhq * PR + (J1 - cb)) * T * KD
                           : ws.qb + ((int64_t)bhq * NS + sJ) * T * KD;
-    dma_stage<64, CPR>(plan_r, q1 + (int64_t)I * PC * KD, sm.u.st.qa[buf]);
-    dma_stage<64, CPR>(SM ? plan_x : plan_r, xh + (int64_t)I * PC * xs.t, sm.u.st.dv[buf]);
-    if (same)  // the second chunk of the pair has its own query operand inside the large chunk
-      dma_stage<64, CPR>(plan_r, ws.qs + ((int64_t)bhq * PR + (J1 + 1 - cb)) * T * KD + (int64_t)I * PC * KD,
-                         sm.u.st.qb[buf]);
+    const int64_t qlo = same ? ws.lo_qs : ws.lo_qb;
+#pragma unroll
+    for (int pl = 0; pl < NP; ++pl) {
+      dma_stage<64, CPR>(plan_r, q1 + pl * qlo + (int64_t)I * PC * KD, sm.u.st.qa[buf][pl]);
+      dma_stage<64, CPR>(SM ? plan_x : plan_r, xh + pl * x_lo + (int64_t)I * PC * xs.t, sm.u.st.dv[buf][pl]);
+      if (same)  // the second chunk of the pair has its own query operand inside the large chunk
+        dma_stage<64, CPR>(plan_r,
+                           ws.qs + pl * ws.lo_qs + ((int64_t)bhq * PR + (J1 + 1 - cb)) * T * KD + (int64_t)I * PC * KD,
+                           sm.u.st.qb[buf][pl]);
+    }
     if (SM) {  // one more load for waves 0 and 1
       if (w == 0) dma_f32x64(ws.lse + (int64_t)bhq * T + I * PC, sm.lse[buf]);
       if (w == 1) dma_f32x64(bw.delta + (int64_t)bhq * T + I * PC, sm.dl[buf]);
@@ -749,14 +904,20 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_bwd_col
     if (SM && I == ceJ + 1) park();
     if (live && I > Jw) {
       const bool same = I <= ceJ;
-      const bf16* qt = (w >= 2 && same) ? sm.u.st.qb[buf] : sm.u.st.qa[buf];
+      bf16 (*qt)[64 * KD] = (w >= 2 && same) ? sm.u.st.qb[buf] : sm.u.st.qa[buf];  // planes
 #pragma unroll
       for (int rh = 0; rh < 2; ++rh) {
         f32x16 sc = zero16(), dp = zero16();
 #pragma unroll
         for (int st = 0; st < NKS; ++st) {
-          sc = mfma32(ld8(swz<CPR>(qt, rh * 32 + l32, 2 * st + g)), same ? kbs[st] : kbf[st], sc);
-          dp = mfma32(ld8(swz<CPR>(sm.u.st.dv[buf], rh * 32 + l32, 2 * st + g)), ob[st], dp);
+          bf16x8 qa8[NP], da8[NP];
+#pragma unroll
+          for (int pl = 0; pl < NP; ++pl) {
+            qa8[pl] = ld8(swz<CPR>(qt[pl], rh * 32 + l32, 2 * st + g));
+            da8[pl] = ld8(swz<CPR>(sm.u.st.dv[buf][pl], rh * 32 + l32, 2 * st + g));
+          }
+          sc = mm3<NP>(qa8, same ? kbs[st] : kbf[st], sc);
+          dp = mm3<NP>(da8, ob[st], dp);
         }
         if (SM) {
 #pragma unroll
@@ -770,29 +931,47 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_bwd_col
               dp[e] = sc[e] * (dp[e] - d4[u]);                           // dA / F
             }
           }
-          const bf16x8 p0 = pack_b(sc, 0), p1 = pack_b(sc, 1);
+          bf16x8 pp[2][NP];
 #pragma unroll
-          for (int t = 0; t < NVT; ++t) {
-            dva[t] = mfma32(lds_tr_a<CPR>(sm.u.st.dv[buf], rh * 32, t * 32), p0, dva[t]);
-            dva[t] = mfma32(lds_tr_a<CPR>(sm.u.st.dv[buf], rh * 32 + 16, t * 32), p1, dva[t]);
+          for (int hh = 0; hh < 2; ++hh) {
+            pp[hh][0] = pack_b(sc, hh);
+            if constexpr (F32) pp[hh][1] = pack_lo(sc, hh, pp[hh][0]);
           }
+#pragma unroll
+          for (int t = 0; t < NVT; ++t)
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+              bf16x8 xa[NP];
+#pragma unroll
+              for (int pl = 0; pl < NP; ++pl) xa[pl] = lds_tr_a<CPR>(sm.u.st.dv[buf][pl], rh * 32 + 16 * hh, t * 32);
+              dva[t] = mm3<NP>(xa, pp[hh], dva[t]);
+            }
 #pragma unroll
           for (int e = 0; e < 16; ++e) sc[e] = dp[e];
         } else {
 #pragma unroll
           for (int e = 0; e < 16; ++e) sc[e] = dp[e] * __builtin_amdgcn_exp2f(sc[e] * sl2);
         }
-        const bf16x8 d0 = pack_b(sc, 0), d1 = pack_b(sc, 1);
+        bf16x8 dd[2][NP];
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          dd[hh][0] = pack_b(sc, hh);
+          if constexpr (F32) dd[hh][1] = pack_lo(sc, hh, dd[hh][0]);
+        }
 #pragma unroll
         for (int t = 0; t < NVT; ++t) {
-          const bf16x8 a0 = lds_tr_a<CPR>(qt, rh * 32, t * 32);
-          const bf16x8 a1 = lds_tr_a<CPR>(qt, rh * 32 + 16, t * 32);
+          bf16x8 a0[NP], a1[NP];
+#pragma unroll
+          for (int pl = 0; pl < NP; ++pl) {
+            a0[pl] = lds_tr_a<CPR>(qt[pl], rh * 32, t * 32);
+            a1[pl] = lds_tr_a<CPR>(qt[pl], rh * 32 + 16, t * 32);
+          }
           if (same || SM) {  // softmax: one accumulator, the same-chunk part is parked in dkt
-            as_[t] = mfma32(a0, d0, as_[t]);
-            as_[t] = mfma32(a1, d1, as_[t]);
+            as_[t] = mm3<NP>(a0, dd[0], as_[t]);
+            as_[t] = mm3<NP>(a1, dd[1], as_[t]);
           } else {
-            af[t] = mfma32(a0, d0, af[t]);
-            af[t] = mfma32(a1, d1, af[t]);
+            af[t] = mm3<NP>(a0, dd[0], af[t]);
+            af[t] = mm3<NP>(a1, dd[1], af[t]);
           }
         }
       }
@@ -852,7 +1031,10 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_bwd_col
       }
     }
     __syncthreads();
-    load_rows64_f32(sm.u.fin.m[0], ws.kt + ((int64_t)bh * T + J * PC) * 64, 64);
+    if constexpr (F32)
+      load_rows64_split(sm.u.fin.m[0], ws.kt + ((int64_t)bh * T + J * PC) * 64, 64, ws.lo_kt);
+    else
+      load_rows64_f32(sm.u.fin.m[0], ws.kt + ((int64_t)bh * T + J * PC) * 64, 64);
     __syncthreads();
     zero44(acc4);
     lds_gemm64<true, false>(sm.u.fin.f[0], sm.u.fin.m[0], acc4);  // dSUF = dKL^T k~
@@ -877,11 +1059,11 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_bwd_col
 //   dA_diag = s P (dO V^T - delta_i),  dV_c = P^T dO_c   (the column sweep adds the rest)
 // fp32 on LDS, dO and V rows as 64-column halves at KD = 128.  grid (NT, B*HQ)
 // ---------------------------------------------------------------------------
-template <int KD>
-__global__ __launch_bounds__(256) void path_softmax_diag_bwd_kernel(const bf16* __restrict__ dout, Strides dos,
-                                                                    const bf16* __restrict__ o, Strides os,
-                                                                    const bf16* __restrict__ v, Strides vs, int HQ,
-                                                                    int H, int T, float scale, PathFwdWs ws,
+template <int KD, bool F32>
+__global__ __launch_bounds__(256) void path_softmax_diag_bwd_kernel(const pin_t<F32>* __restrict__ dout, Strides dos,
+                                                                    const pin_t<F32>* __restrict__ o, Strides os,
+                                                                    const pin_t<F32>* __restrict__ v, Strides vs,
+                                                                    int HQ, int H, int T, float scale, PathFwdWs ws,
                                                                     PathBwdWs bw) {
   constexpr int NH = KD / 64;
   __shared__ __attribute__((aligned(16))) float Dm[NH][64][68];
@@ -902,15 +1084,14 @@ __global__ __launch_bounds__(256) void path_softmax_diag_bwd_kernel(const bf16* 
   }
   {  // delta of row r: 4 threads x 16 columns per 64-column half
     const int r = tid >> 2, cc = (tid & 3) * 16;
-    const bf16* orow = o + b * os.b + hq * os.h + (int64_t)(t0 + r) * os.t + cc;
-    const bf16* drow_ = dout + b * dos.b + hq * dos.h + (int64_t)(t0 + r) * dos.t + cc;
+    const pin_t<F32>* orow = o + b * os.b + hq * os.h + (int64_t)(t0 + r) * os.t + cc;
+    const pin_t<F32>* drow_ = dout + b * dos.b + hq * dos.h + (int64_t)(t0 + r) * dos.t + cc;
     float acc = 0.f;
 #pragma unroll
     for (int hh = 0; hh < 2 * NH; ++hh) {
       const int off = 64 * (hh >> 1) + 8 * (hh & 1);
-      const bf16x8 x = ld8(orow + off), y = ld8(drow_ + off);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc = fmaf((float)x[e], (float)y[e], acc);
+      for (int e = 0; e < 8; ++e) acc = fmaf((float)orow[off + e], (float)drow_[off + e], acc);
     }
     acc += __shfl_xor(acc, 1, 64);
     acc += __shfl_xor(acc, 2, 64);
@@ -1019,11 +1200,12 @@ __global__ __launch_bounds__(256) void path_products_bwd_kernel(int HQ, int H, i
 // (rows dl_row(e), column dl_col()).  Operands live in 9 fp32 LDS buffers.
 // grid (NT, B*HQ)
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void path_wy_bwd_kernel(const bf16* __restrict__ q, Strides qs,
-                                                          const bf16* __restrict__ k, Strides ks,
-                                                          const bf16* __restrict__ w, Strides wst,
-                                                          const bf16* __restrict__ beta, Strides bst, int HQ, int H,
-                                                          int T, PathFwdWs ws, PathBwdWs bw) {
+template <bool F32>
+__global__ __launch_bounds__(256) void path_wy_bwd_kernel(const pin_t<F32>* __restrict__ q, Strides qs,
+                                                          const pin_t<F32>* __restrict__ k, Strides ks,
+                                                          const pin_t<F32>* __restrict__ w, Strides wst,
+                                                          const pin_t<F32>* __restrict__ beta, Strides bst, int HQ,
+                                                          int H, int T, PathFwdWs ws, PathBwdWs bw) {
   __shared__ __attribute__((aligned(16))) float W[64][68];
   __shared__ __attribute__((aligned(16))) float Wb[64][68];
   __shared__ __attribute__((aligned(16))) float Q[64][68];
@@ -1160,10 +1342,13 @@ __global__ __launch_bounds__(256) void path_wy_bwd_kernel(const bf16* __restrict
 // to the caller's bf16 gradients.  grid (T/4, B*H), thread = (row, column), KD / 64 columns
 // per thread (KD: head dim of the fp32 rows)
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void path_reduce_kernel(int HQ, int H, int T, int KD, PathBwdWs bw, bf16* __restrict__ dq,
-                                                          Strides dqs, bf16* __restrict__ dk, Strides dks,
-                                                          bf16* __restrict__ dv, Strides dvs, bf16* __restrict__ dw,
-                                                          Strides dws, bf16* __restrict__ db, Strides dbs) {
+template <bool F32>
+__global__ __launch_bounds__(256) void path_reduce_kernel(int HQ, int H, int T, int KD, PathBwdWs bw,
+                                                          pin_t<F32>* __restrict__ dq, Strides dqs,
+                                                          pin_t<F32>* __restrict__ dk, Strides dks,
+                                                          pin_t<F32>* __restrict__ dv, Strides dvs,
+                                                          pin_t<F32>* __restrict__ dw, Strides dws,
+                                                          pin_t<F32>* __restrict__ db, Strides dbs) {
   const int bh = blockIdx.y;
   const int b = bh / H, h = bh - b * H;
   const int G_ = HQ / H;
@@ -1179,12 +1364,12 @@ __global__ __launch_bounds__(256) void path_reduce_kernel(int HQ, int H, int T, 
       sv += bw.dvf[off];
       sw += bw.dw[off];
       if (col == 0) sb += bw.db[bhq * T + t];
-      dq[b * dqs.b + hq * dqs.h + (int64_t)t * dqs.t + col] = (bf16)bw.dq[off];
+      dq[b * dqs.b + hq * dqs.h + (int64_t)t * dqs.t + col] = (pin_t<F32>)bw.dq[off];
     }
-    dk[b * dks.b + h * dks.h + (int64_t)t * dks.t + col] = (bf16)sk;
-    dv[b * dvs.b + h * dvs.h + (int64_t)t * dvs.t + col] = (bf16)sv;
-    dw[b * dws.b + h * dws.h + (int64_t)t * dws.t + col] = (bf16)sw;
-    if (col == 0) db[b * dbs.b + h * dbs.h + (int64_t)t * dbs.t] = (bf16)sb;
+    dk[b * dks.b + h * dks.h + (int64_t)t * dks.t + col] = (pin_t<F32>)sk;
+    dv[b * dvs.b + h * dvs.h + (int64_t)t * dvs.t + col] = (pin_t<F32>)sv;
+    dw[b * dws.b + h * dws.h + (int64_t)t * dws.t + col] = (pin_t<F32>)sw;
+    if (col == 0) db[b * dbs.b + h * dbs.h + (int64_t)t * dbs.t] = (pin_t<F32>)sb;
   }
 }
 

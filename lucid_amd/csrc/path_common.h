@@ -1,12 +1,42 @@
-// Shared helpers of the LUCID-Path kernels (head_dim K = V = 64, small chunk 64,
+// Shared helpers of the LUCID-Path kernels (head dim K = V = 64 or 128, small chunk 64,
 // large chunk 8 small chunks = 512 positions).
+//
+// fp32 inputs (template flag F32): the caller's tensors are fp32, and every bf16 MFMA
+// operand buffer of the workspace holds two bf16 planes, hi = bf16(x) and lo = bf16(x - hi),
+// the lo plane at a fixed element offset from the hi plane (PathFwdWs / PathBwdWs lo_*).
+// Each product then takes hi.hi + hi.lo + lo.hi (~fp32 accuracy, mm3 below).
 #pragma once
+#include <type_traits>
 #include "lucid_common.h"
 
 namespace lucid {
 
 constexpr int PC = 64;  // small chunk (positions)
 constexpr int PR = 8;   // small chunks per large chunk
+
+// element type of the caller's tensors
+template <bool F32>
+using pin_t = std::conditional_t<F32, float, bf16>;
+
+// acc + a b over the NP planes of each operand: a[0] b[0] (NP = 1), or the 3-term split
+// a[0] b[0] + a[0] b[1] + a[1] b[0] (NP = 2)
+template <int NP>
+__device__ __forceinline__ f32x16 mm3(const bf16x8* a, const bf16x8* b, f32x16 acc) {
+  acc = mfma32(a[0], b[0], acc);
+  if constexpr (NP == 2) {
+    acc = mfma32(a[0], b[1], acc);
+    acc = mfma32(a[1], b[0], acc);
+  }
+  return acc;
+}
+
+// x as bf16 into hi[i], and (NP = 2) its residual into hi[i + lo]
+template <int NP>
+__device__ __forceinline__ void put_split(bf16* hi, int64_t lo, int64_t i, float x) {
+  const bf16 h = (bf16)x;
+  hi[i] = h;
+  if constexpr (NP == 2) hi[i + lo] = (bf16)(x - (float)h);
+}
 
 // acc[i][j] += sum_k opA(A)[r0+i][k] * opB(B)[k][c0+j] for 64x64 fp32 LDS matrices
 // (row stride 68); thread t owns the 4x4 block r0 = 4*(t/16), c0 = 4*(t%16).
@@ -132,6 +162,28 @@ __device__ __forceinline__ void invert_unit_lower64(float (*M)[68]) {
   merge_lower_blocks<32>(M);
 }
 
+// Load a 64x64 block of fp32 rows (row stride st elements) into an fp32 LDS matrix.
+__device__ __forceinline__ void load_rows64_f32(float (*dst)[68], const float* __restrict__ src, int64_t st) {
+  const int tid = threadIdx.x;
+  const int r = tid >> 2, c = (tid & 3) * 16;
+#pragma unroll
+  for (int q4 = 0; q4 < 4; ++q4)
+    *reinterpret_cast<f32x4*>(&dst[r][c + 4 * q4]) = *reinterpret_cast<const f32x4*>(src + (int64_t)r * st + c + 4 * q4);
+}
+// The same from bf16 hi / lo planes (lo = element offset of the lo plane; 0: none).
+__device__ __forceinline__ void load_rows64_split(float (*dst)[68], const bf16* __restrict__ src, int64_t st,
+                                                  int64_t lo) {
+  const int tid = threadIdx.x;
+  const int r = tid >> 2, c = (tid & 3) * 16;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const bf16x8 x = ld8(src + (int64_t)r * st + c + 8 * h);
+    bf16x8 y{};
+    if (lo) y = ld8(src + lo + (int64_t)r * st + c + 8 * h);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dst[r][c + 8 * h + e] = (float)x[e] + (lo ? (float)y[e] : 0.f);
+  }
+}
 // Load a 64x64 block of bf16 rows (row stride st elements) into an fp32 LDS matrix.
 __device__ __forceinline__ void load_rows64_f32(float (*dst)[68], const bf16* __restrict__ src, int64_t st) {
   const int tid = threadIdx.x;

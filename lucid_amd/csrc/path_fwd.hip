@@ -36,16 +36,23 @@ struct PathFwdWs {
   bf16* oT;     // [BHq][K][T]        O^T, T-perm (chain operand)
   int* counters;  // [BHq]
   float* lse;   // [BHq][T]           PaTH softmax only: row log-sum-exp, exp2 domain (log2(l) + m)
+  // fp32 inputs: element offsets of the lo planes of kt, kl, qs, qb, oT (0 with bf16 inputs)
+  int64_t lo_kt, lo_kl, lo_qs, lo_qb, lo_oT;
+  // fp32 inputs, PaTH softmax: split copy of V [BH][T][K] (hi plane, lo plane at + lo_vsp)
+  bf16* vsp;
+  int64_t lo_vsp;
 };
 
 // ---------------------------------------------------------------------------
 // WY form and in-chunk transforms (triangular_solve_fwd.py:118-148, parallel.py:39-51)
 // grid (NT, B*HQ).  kv-head outputs are written by the first query head of each group.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void path_chunk_kernel(const bf16* __restrict__ q, Strides qs,
-                                                         const bf16* __restrict__ k, Strides ks,
-                                                         const bf16* __restrict__ w, Strides wst,
-                                                         const bf16* __restrict__ beta, Strides bst, int HQ, int H,
+// F32: fp32 inputs; k~ is written as hi / lo planes
+template <bool F32>
+__global__ __launch_bounds__(256) void path_chunk_kernel(const pin_t<F32>* __restrict__ q, Strides qs,
+                                                         const pin_t<F32>* __restrict__ k, Strides ks,
+                                                         const pin_t<F32>* __restrict__ w, Strides wst,
+                                                         const pin_t<F32>* __restrict__ beta, Strides bst, int HQ, int H,
                                                          int T, float scale, int softmax, PathFwdWs ws) {
   __shared__ __attribute__((aligned(16))) float Wm[64][68];
   __shared__ __attribute__((aligned(16))) float Wb[64][68];
@@ -113,7 +120,7 @@ __global__ __launch_bounds__(256) void path_chunk_kernel(const bf16* __restrict_
     bf16* dst = ws.kt + ((int64_t)bh * T + t0) * 64;
     DL_FOR_E {
       const int r = dl_row(e);
-      dst[r * 64 + cl] = (bf16)(Ks[r][cl] - acc[e]);
+      put_split<F32 ? 2 : 1>(dst, ws.lo_kt, r * 64 + cl, Ks[r][cl] - acc[e]);
     }
   }
   // QW = tril(Q W^T) -> X (every read of WBK came before the last barrier)
@@ -165,6 +172,7 @@ __global__ __launch_bounds__(256) void path_chunk_kernel(const bf16* __restrict_
 // Per large chunk: SUF_c (c from the top down), HL_s, KL = k~ SUF^T
 // (cumprod_householder_fwd.py:13-79).  grid (NS, B*H)
 // ---------------------------------------------------------------------------
+template <bool F32>
 __global__ __launch_bounds__(256) void path_large_kernel(int T, PathFwdWs ws) {
   __shared__ __attribute__((aligned(16))) float Sf[64][68];
   __shared__ __attribute__((aligned(16))) float Hs[64][68];
@@ -178,12 +186,16 @@ __global__ __launch_bounds__(256) void path_large_kernel(int T, PathFwdWs ws) {
   // products on the matrix cores (mgemm64, D layout); k~_c and Hc_c of the next chunk
   // are fetched into registers while the current one is processed
   const int kr = tid >> 2, kc = (tid & 3) * 16;
-  bf16x8 pk[2];
+  bf16x8 pk[2], pl[2];
   f32x4 ph[4];
   auto fetch = [&](int c) {
     const bf16* src = ws.kt + ((int64_t)bh * T + c * PC + kr) * 64 + kc;
     pk[0] = ld8(src);
     pk[1] = ld8(src + 8);
+    if constexpr (F32) {
+      pl[0] = ld8(src + ws.lo_kt);
+      pl[1] = ld8(src + ws.lo_kt + 8);
+    }
     mat_fetch(ph, ws.hc + ((int64_t)bh * NT + c) * 4096);
   };
   fetch(ce);
@@ -191,7 +203,7 @@ __global__ __launch_bounds__(256) void path_large_kernel(int T, PathFwdWs ws) {
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) Kt[kr][kc + 8 * hh + e] = (float)pk[hh][e];
+      for (int e = 0; e < 8; ++e) Kt[kr][kc + 8 * hh + e] = (float)pk[hh][e] + (F32 ? (float)pl[hh][e] : 0.f);
     mat_put(Hs, ph);
     __syncthreads();
     if (c > cb) fetch(c - 1);
@@ -206,7 +218,7 @@ __global__ __launch_bounds__(256) void path_large_kernel(int T, PathFwdWs ws) {
     {
       const f32x16 a = mgemm64<false, true>(Kt, Sf, zero16());
       bf16* dst = ws.kl + ((int64_t)bh * T + c * PC) * 64;
-      DL_FOR_E dst[dl_row(e) * 64 + cl] = (bf16)a[e];
+      DL_FOR_E put_split<F32 ? 2 : 1>(dst, ws.lo_kl, dl_row(e) * 64 + cl, a[e]);
     }
     // SUF_{c-1} = SUF_c Hc_c
     const f32x16 sn = mgemm64<false, false>(Sf, Hs, zero16());
@@ -231,6 +243,7 @@ __global__ __launch_bounds__(256) void path_large_kernel(int T, PathFwdWs ws) {
 // the same slot.  grid (B*HQ, ceil(NT/2)): the work of a pair grows with p, so the
 // late pairs of every head are dispatched first.
 // ---------------------------------------------------------------------------
+template <bool F32>
 __global__ __launch_bounds__(256) void path_transport_kernel(int HQ, int H, int T, PathFwdWs ws) {
   __shared__ __attribute__((aligned(16))) float X[128][68];  // rows 0..63 = chunk A, 64..127 = chunk B
   __shared__ __attribute__((aligned(16))) float MT[64][68];
@@ -246,16 +259,21 @@ __global__ __launch_bounds__(256) void path_transport_kernel(int HQ, int H, int 
     const float* src = ws.qt + ((int64_t)bhq * T + A * PC) * 64;  // A's and B's rows are adjacent
     for (int idx = tid; idx < (hasB ? 8192 : 4096); idx += 256) X[idx >> 6][idx & 63] = src[idx];
   }
-  // rows r0 .. r0 + 64 * nblk of X -> bf16 rows at dst (row stride 64)
-  auto emit = [&](bf16* dst, int r0, int nblk) {
+  // rows r0 .. r0 + 64 * nblk of X -> bf16 rows at dst (row stride 64), and (F32) their
+  // residuals at dst + lo
+  auto emit = [&](bf16* dst, int64_t lo, int r0, int nblk) {
     const int cc = (tid & 3) * 16;
     for (int r = r0 + (tid >> 2); r < r0 + 64 * nblk; r += 64) {
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
-        bf16x8 v;
+        bf16x8 v, vl;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = (bf16)X[r][cc + 8 * hh + e];
+        for (int e = 0; e < 8; ++e) {
+          v[e] = (bf16)X[r][cc + 8 * hh + e];
+          if constexpr (F32) vl[e] = (bf16)(X[r][cc + 8 * hh + e] - (float)v[e]);
+        }
         *reinterpret_cast<bf16x8*>(dst + (int64_t)r * 64 + cc + 8 * hh) = v;
+        if constexpr (F32) *reinterpret_cast<bf16x8*>(dst + lo + (int64_t)r * 64 + cc + 8 * hh) = vl;
       }
     }
   };
@@ -292,7 +310,7 @@ __global__ __launch_bounds__(256) void path_transport_kernel(int HQ, int H, int 
     mload(-1);
     mstore_t();
     __syncthreads();
-    emit(ws.qs + (((int64_t)bhq * PR + (A - cb)) * T) * 64 + (int64_t)A * PC * 64, 64, 1);
+    emit(ws.qs + (((int64_t)bhq * PR + (A - cb)) * T) * 64 + (int64_t)A * PC * 64, ws.lo_qs, 64, 1);
     if (nsteps > 0) mload(0);
     const f32x16 o = mat_xM_tile(X, MT, dt, rt + 2);
     __syncthreads();
@@ -308,7 +326,7 @@ __global__ __launch_bounds__(256) void path_transport_kernel(int HQ, int H, int 
   const int nblk = hasB ? 2 : 1;
   for (int j = 0; j < nsteps; ++j) {
     if (j + 1 < nsteps) mload(j + 1);
-    emit(slot(j), 0, nblk);
+    emit(slot(j), (j < nq) ? ws.lo_qs : ws.lo_qb, 0, nblk);
     const f32x16 o0 = mat_xM_tile(X, MT, dt, rt);
     f32x16 o1 = zero16();
     if (hasB) o1 = mat_xM_tile(X, MT, dt, rt + 2);
@@ -339,28 +357,31 @@ __global__ __launch_bounds__(256) void path_transport_kernel(int HQ, int H, int 
 // bf16 split.  L_BA depends on the key operands only and is computed before the sweep.
 // The fp32 buffers of the final step reuse the staging space.
 // ---------------------------------------------------------------------------
-template <int KD>
+// NP: bf16 planes per operand (2: fp32 inputs, hi and lo)
+template <int KD, int NP>
 struct SolveFwdSmem {
   union {
     struct {
-      bf16 k[2][2][64 * KD];  // [buffer][chunk of the pair], swizzled (chunk c of row r at c ^ (r & 7))
-      bf16 o[2][2][KD * 64];
+      bf16 k[2][2][NP][64 * KD];  // [buffer][chunk of the pair][plane], swizzled (chunk c of row r at c ^ (r & 7))
+      bf16 o[2][2][NP][KD * 64];
     } st;
     struct {
       float Rt[KD][132];    // R^T for the 128 rows (0..63 = A, 64..127 = B)
       float Ys[64][68];     // Y of the chunk being solved
-      bf16 ot[KD][128 + 8];  // O^T of both chunks, T-perm within 16-groups
+      bf16 ot[NP][KD][128 + 8];  // O^T of both chunks, T-perm within 16-groups
     } fin;
   } u;
-  bf16x8 lba[4][64][2];  // L_BA as MFMA B operands, per wave and lane
+  bf16x8 lba[4][64][2 * NP];  // L_BA as MFMA B operands, per wave and lane ([2 + h]: lo)
 };
 
-template <int KD>
-__global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_solve_fwd_kernel(const bf16* __restrict__ v, Strides vs,
-                                                             bf16* __restrict__ o, Strides os, int HQ, int H,
-                                                             int T, int BHq, float scale, PathFwdWs ws) {
+// F32: fp32 V and O; every operand product is a 3-term split over hi / lo planes (mm3)
+template <int KD, bool F32>
+__global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64 && !F32) void path_solve_fwd_kernel(
+    const pin_t<F32>* __restrict__ v, Strides vs, pin_t<F32>* __restrict__ o, Strides os, int HQ, int H, int T, int BHq,
+    float scale, PathFwdWs ws) {
   constexpr int NKS = KD / 16, NVT = KD / 32;  // k-steps of a logit product, 32-column value tiles
-  __shared__ __attribute__((aligned(16))) SolveFwdSmem<KD> sm;
+  constexpr int NP = F32 ? 2 : 1;
+  __shared__ __attribute__((aligned(16))) SolveFwdSmem<KD, NP> sm;
   const int NT = T / PC, NS = (NT + PR - 1) / PR;
   const int id = blockIdx.x;
   const int p = id / BHq, bhq = id - (id / BHq) * BHq;
@@ -384,14 +405,23 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_solve_f
   f32x16 acc[NVT][2];
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
-    const bf16* vrow = v + b * vs.b + h * vs.h + (int64_t)(r0 + nt * 32 + l32) * vs.t;
+    const pin_t<F32>* vrow = v + b * vs.b + h * vs.h + (int64_t)(r0 + nt * 32 + l32) * vs.t;
 #pragma unroll
     for (int t = 0; t < NVT; ++t)
 #pragma unroll
       for (int qq = 0; qq < 4; ++qq) {
-        const bf16x4 vv = *reinterpret_cast<const bf16x4*>(vrow + t * 32 + 8 * qq + 4 * g);
+        float vv[4];
+        if constexpr (F32) {
+          const f32x4 x = *reinterpret_cast<const f32x4*>(vrow + t * 32 + 8 * qq + 4 * g);
 #pragma unroll
-        for (int u = 0; u < 4; ++u) acc[t][nt][4 * qq + u] = kh ? 0.f : -(float)vv[u];
+          for (int u = 0; u < 4; ++u) vv[u] = x[u];
+        } else {
+          const bf16x4 x = *reinterpret_cast<const bf16x4*>(vrow + t * 32 + 8 * qq + 4 * g);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) vv[u] = (float)x[u];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc[t][nt][4 * qq + u] = kh ? 0.f : -vv[u];
       }
   }
   // query operand of key chunk J for this wave's rows: QB^(J/PR) below the large chunk,
@@ -399,6 +429,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_solve_f
   auto qbase = [&](int J) {
     return (J < cb) ? ws.qb + ((int64_t)bhq * NS + J / PR) * T * KD : ws.qs + ((int64_t)bhq * PR + (J - cb)) * T * KD;
   };
+  auto qlo = [&](int J) { return (J < cb) ? ws.lo_qb : ws.lo_qs; };  // lo plane offset of qbase(J)
   // L_BA (rows of B half nb, keys of A half ka): Kop_A = k~_A, Qop = QS slot A - cb of B's rows
   if (hasB) {
     const int nb = w & 1, ka = w >> 1;
@@ -406,25 +437,42 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_solve_f
     const bf16* qr = qbase(A) + (int64_t)(i0 + 64 + nb * 32 + l32) * KD;
     f32x16 sc = zero16();
 #pragma unroll
-    for (int st = 0; st < NKS; ++st) sc = mfma32(ld8(kr + 16 * st + 8 * g), ld8(qr + 16 * st + 8 * g), sc);
+    for (int st = 0; st < NKS; ++st) {
+      bf16x8 ka8[NP], qa8[NP];
+      ka8[0] = ld8(kr + 16 * st + 8 * g);
+      qa8[0] = ld8(qr + 16 * st + 8 * g);
+      if constexpr (F32) {
+        ka8[1] = ld8(kr + ws.lo_kt + 16 * st + 8 * g);
+        qa8[1] = ld8(qr + ws.lo_qs + 16 * st + 8 * g);
+      }
+      sc = mm3<NP>(ka8, qa8, sc);
+    }
 #pragma unroll
     for (int e = 0; e < 16; ++e) sc[e] = __builtin_amdgcn_exp2f(fmaf(sc[e], sl2, -cc0));
-    sm.lba[w][lane][0] = pack_b(sc, 0);
-    sm.lba[w][lane][1] = pack_b(sc, 1);
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      sm.lba[w][lane][hh] = pack_b(sc, hh);
+      if constexpr (F32) sm.lba[w][lane][2 + hh] = pack_lo(sc, hh, sm.lba[w][lane][hh]);
+    }
   }
   // below the large chunk the operand changes only every PR key chunks, so it stays in
   // registers across pairs; inside it every chunk has its own slot
-  bf16x8 qop[2][NKS];
+  bf16x8 qop[2][NKS][NP];
   int qsrc = -1;
   auto load_q = [&](int J) {
     const int src = (J < cb) ? J / PR : NS + J;
     if (src == qsrc) return;
     qsrc = src;
     const bf16* base = qbase(J);
+    const int64_t lo = qlo(J);
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
-      for (int st = 0; st < NKS; ++st) qop[nt][st] = ld8(base + (int64_t)(r0 + nt * 32 + l32) * KD + 16 * st + 8 * g);
+      for (int st = 0; st < NKS; ++st) {
+        const bf16* p = base + (int64_t)(r0 + nt * 32 + l32) * KD + 16 * st + 8 * g;
+        qop[nt][st][0] = ld8(p);
+        if constexpr (F32) qop[nt][st][1] = ld8(p + lo);
+      }
   };
   int plan_k[64 * (KD / 8) / 256], plan_t[KD * 8 / 256];
   dma_plan<64, KD / 8>(KD, plan_k);
@@ -434,8 +482,13 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_solve_f
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int J = 2 * pp + u;
-      dma_stage<64, KD / 8>(plan_k, ((J < cb) ? ws.kl : ws.kt) + ((int64_t)bh * T + J * PC) * KD, sm.u.st.k[buf][u]);
-      dma_stage<KD, 8>(plan_t, oTh + J * PC, sm.u.st.o[buf][u]);
+      const bf16* kp = ((J < cb) ? ws.kl : ws.kt) + ((int64_t)bh * T + J * PC) * KD;
+      dma_stage<64, KD / 8>(plan_k, kp, sm.u.st.k[buf][u][0]);
+      dma_stage<KD, 8>(plan_t, oTh + J * PC, sm.u.st.o[buf][u][0]);
+      if constexpr (F32) {
+        dma_stage<64, KD / 8>(plan_k, kp + ((J < cb) ? ws.lo_kl : ws.lo_kt), sm.u.st.k[buf][u][1]);
+        dma_stage<KD, 8>(plan_t, oTh + ws.lo_oT + J * PC, sm.u.st.o[buf][u][1]);
+      }
     }
   };
   // Y_A, Y_B (fp32) are fetched into registers during the last pair
@@ -458,28 +511,37 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_solve_f
   auto sweep_pair = [&](int buf) {
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
-      bf16x8 ka[NKS];
+      bf16x8 ka[NKS][NP];
 #pragma unroll
-      for (int st = 0; st < NKS; ++st) ka[st] = ld8(swz<KD / 8>(sm.u.st.k[buf][kh], mt * 32 + l32, 2 * st + g));
-      bf16x8 pb[2][2];
+      for (int st = 0; st < NKS; ++st)
+#pragma unroll
+        for (int pl = 0; pl < NP; ++pl) ka[st][pl] = ld8(swz<KD / 8>(sm.u.st.k[buf][kh][pl], mt * 32 + l32, 2 * st + g));
+      bf16x8 pb[2][2][NP];
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt) {
         f32x16 sc = zero16();
 #pragma unroll
-        for (int st = 0; st < NKS; ++st) sc = mfma32(ka[st], qop[nt][st], sc);
+        for (int st = 0; st < NKS; ++st) sc = mm3<NP>(ka[st], qop[nt][st], sc);
 #pragma unroll
         for (int e = 0; e < 16; ++e) sc[e] = __builtin_amdgcn_exp2f(fmaf(sc[e], sl2, -cc0));
-        pb[nt][0] = pack_b(sc, 0);
-        pb[nt][1] = pack_b(sc, 1);
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          pb[nt][hh][0] = pack_b(sc, hh);
+          if constexpr (F32) pb[nt][hh][1] = pack_lo(sc, hh, pb[nt][hh][0]);
+        }
       }
 #pragma unroll
       for (int t = 0; t < NVT; ++t) {
-        const bf16x8 va0 = ld8(swz<8>(sm.u.st.o[buf][kh], t * 32 + l32, 4 * mt + g));
-        const bf16x8 va1 = ld8(swz<8>(sm.u.st.o[buf][kh], t * 32 + l32, 4 * mt + 2 + g));
+        bf16x8 va[2][NP];
+#pragma unroll
+        for (int pl = 0; pl < NP; ++pl) {
+          va[0][pl] = ld8(swz<8>(sm.u.st.o[buf][kh][pl], t * 32 + l32, 4 * mt + g));
+          va[1][pl] = ld8(swz<8>(sm.u.st.o[buf][kh][pl], t * 32 + l32, 4 * mt + 2 + g));
+        }
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) {
-          acc[t][nt] = mfma32(va0, pb[nt][0], acc[t][nt]);
-          acc[t][nt] = mfma32(va1, pb[nt][1], acc[t][nt]);
+          acc[t][nt] = mm3<NP>(va[0], pb[nt][0], acc[t][nt]);
+          acc[t][nt] = mm3<NP>(va[1], pb[nt][1], acc[t][nt]);
         }
       }
     }
@@ -561,7 +623,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_solve_f
     }
     const int rl = rh * 32 + l32;
     const int lslot = c * 64 + ((rl & ~15) | jmap(rl & 15));
-    bf16* orow = o + b * os.b + hq * os.h + (int64_t)(i0 + c * 64 + rl) * os.t;
+    pin_t<F32>* orow = o + b * os.b + hq * os.h + (int64_t)(i0 + c * 64 + rl) * os.t;
 #pragma unroll
     for (int qq = 0; qq < 4; ++qq) {
       const int d0 = dt * 32 + 8 * qq + 4 * g;
@@ -569,9 +631,17 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_solve_f
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         bb[u] = (bf16)oo[4 * qq + u];
-        sm.u.fin.ot[d0 + u][lslot] = bb[u];
+        sm.u.fin.ot[0][d0 + u][lslot] = bb[u];
+        if constexpr (F32) sm.u.fin.ot[NP - 1][d0 + u][lslot] = (bf16)(oo[4 * qq + u] - (float)bb[u]);
       }
-      *reinterpret_cast<bf16x4*>(orow + d0) = bb;
+      if constexpr (F32) {
+        f32x4 f;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) f[u] = oo[4 * qq + u];
+        *reinterpret_cast<f32x4*>(orow + d0) = f;
+      } else {
+        *reinterpret_cast<bf16x4*>(orow + d0) = bb;
+      }
     }
    }
   };
@@ -581,12 +651,23 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_solve_f
     ystore(1);
     // ---- R_B -= L_BA O_A: wave -> (B rows half nb, A keys half ka) ----
     const int nb = w & 1, ka = w >> 1;
-    const bf16x8 l0 = sm.lba[w][lane][0], l1 = sm.lba[w][lane][1];
+    bf16x8 lb[2][NP];
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      lb[hh][0] = sm.lba[w][lane][hh];
+      if constexpr (F32) lb[hh][1] = sm.lba[w][lane][2 + hh];
+    }
     f32x16 cr[NVT];
 #pragma unroll
     for (int t = 0; t < NVT; ++t) {
-      cr[t] = mfma32(ld8(&sm.u.fin.ot[t * 32 + l32][ka * 32 + 8 * g]), l0, zero16());
-      cr[t] = mfma32(ld8(&sm.u.fin.ot[t * 32 + l32][ka * 32 + 16 + 8 * g]), l1, cr[t]);
+      cr[t] = zero16();
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        bf16x8 oa[NP];
+#pragma unroll
+        for (int pl = 0; pl < NP; ++pl) oa[pl] = ld8(&sm.u.fin.ot[pl][t * 32 + l32][ka * 32 + 16 * hh + 8 * g]);
+        cr[t] = mm3<NP>(oa, lb[hh], cr[t]);
+      }
     }
     const int col = 64 + nb * 32 + l32;
     if (ka == 1) {
@@ -610,7 +691,9 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_solve_f
   const int nch = hasB ? 2 : 1;
   for (int c = tid; c < KD * 8 * nch; c += 256) {
     const int dd = c / (8 * nch), s8 = (c - dd * 8 * nch) * 8;
-    *reinterpret_cast<bf16x8*>(ws.oT + ((int64_t)bhq * KD + dd) * T + i0 + s8) = ld8(&sm.u.fin.ot[dd][s8]);
+    bf16* dst = ws.oT + ((int64_t)bhq * KD + dd) * T + i0 + s8;
+    *reinterpret_cast<bf16x8*>(dst) = ld8(&sm.u.fin.ot[0][dd][s8]);
+    if constexpr (F32) *reinterpret_cast<bf16x8*>(dst + ws.lo_oT) = ld8(&sm.u.fin.ot[NP - 1][dd][s8]);
   }
   publish_counter(cnt, A + nch);
 }
@@ -629,20 +712,22 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_solve_f
 // (exp2 domain) is kept for the backward.  grid (B*HQ, ceil(NT/4)), the groups with the
 // most key chunks (of all heads) first.
 // ---------------------------------------------------------------------------
-template <int KD>
+template <int KD, int NP>
 struct SoftmaxFwdSmem {
-  bf16 k[2][64 * KD];   // swizzled (chunk c of row r at c ^ (r & 7))
-  bf16 v[2][64 * KD];
-  bf16 vd[4][64 * KD];  // V rows of the group's own chunks (diagonal blocks)
+  bf16 k[2][NP][64 * KD];   // [buffer][plane], swizzled (chunk c of row r at c ^ (r & 7))
+  bf16 v[2][NP][64 * KD];
+  bf16 vd[4][NP][64 * KD];  // V rows of the group's own chunks (diagonal blocks)
 };
 
-// KD: head dim (64 or 128)
-template <int KD>
-__global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_softmax_fwd_kernel(
-    const bf16* __restrict__ v, Strides vs, bf16* __restrict__ o, Strides os, int HQ, int H, int T, float scale,
-    PathFwdWs ws) {
+// KD: head dim (64 or 128).  F32: v is the hi plane of a split fp32 V (lo plane at v + v_lo),
+// o is fp32, and every product is a 3-term split (mm3)
+template <int KD, bool F32>
+__global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64 && !F32) void path_softmax_fwd_kernel(
+    const bf16* __restrict__ v, Strides vs, int64_t v_lo, pin_t<F32>* __restrict__ o, Strides os, int HQ, int H, int T,
+    float scale, PathFwdWs ws) {
   constexpr int NKS = KD / 16, NVT = KD / 32, CPR = KD / 8;  // k-steps, 32-column tiles, 16-byte chunks per row
-  __shared__ __attribute__((aligned(16))) SoftmaxFwdSmem<KD> sm;
+  constexpr int NP = F32 ? 2 : 1;
+  __shared__ __attribute__((aligned(16))) SoftmaxFwdSmem<KD, NP> sm;
   const int NT = T / PC, NS = (NT + PR - 1) / PR, NQ = (NT + 3) / 4;
   const int I1 = 4 * (NQ - 1 - (int)blockIdx.y), bhq = blockIdx.x;  // heaviest groups of all heads first
   const int G_ = HQ / H;
@@ -661,12 +746,21 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_softmax
   dma_plan<64, CPR>(vs.t, plan_v);
   auto stage = [&](int J) {
     const int buf = J & 1;
-    dma_stage<64, CPR>(plan_k, ((J < cb) ? ws.kl : ws.kt) + ((int64_t)bh * T + J * PC) * KD, sm.k[buf]);
-    dma_stage<64, CPR>(plan_v, vh + (int64_t)J * PC * vs.t, sm.v[buf]);
+    const bf16* kp = ((J < cb) ? ws.kl : ws.kt) + ((int64_t)bh * T + J * PC) * KD;
+    dma_stage<64, CPR>(plan_k, kp, sm.k[buf][0]);
+    dma_stage<64, CPR>(plan_v, vh + (int64_t)J * PC * vs.t, sm.v[buf][0]);
+    if constexpr (F32) {
+      dma_stage<64, CPR>(plan_k, kp + ((J < cb) ? ws.lo_kl : ws.lo_kt), sm.k[buf][1]);
+      dma_stage<64, CPR>(plan_v, vh + v_lo + (int64_t)J * PC * vs.t, sm.v[buf][1]);
+    }
   };
 #pragma unroll
   for (int c = 0; c < 4; ++c)
-    if (I1 + c < NT) dma_stage<64, CPR>(plan_v, vh + (int64_t)(I1 + c) * PC * vs.t, sm.vd[c]);
+    if (I1 + c < NT) {
+#pragma unroll
+      for (int pl = 0; pl < NP; ++pl)
+        dma_stage<64, CPR>(plan_v, vh + pl * v_lo + (int64_t)(I1 + c) * PC * vs.t, sm.vd[c][pl]);
+    }
   if (nJ > 0) stage(0);
 
   f32x16 acc[2][NVT];
@@ -700,7 +794,6 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_softmax
 #pragma unroll
       for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sd[jh][e]);
     m[nt] = wave_max32(mx);  // finite: the diagonal key is always present
-    const bf16* vt = sm.vd[w];
 #pragma unroll
     for (int jh = 0; jh < 2; ++jh) {
 #pragma unroll
@@ -708,26 +801,39 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_softmax
         sd[jh][e] = __builtin_amdgcn_exp2f(sd[jh][e] - m[nt]);
         l[nt] += sd[jh][e];
       }
-      const bf16x8 p0 = pack_b(sd[jh], 0), p1 = pack_b(sd[jh], 1);
+      bf16x8 p[2][NP];
 #pragma unroll
-      for (int t = 0; t < NVT; ++t) {
-        acc[nt][t] = mfma32(lds_tr_a<CPR>(vt, jh * 32, t * 32), p0, acc[nt][t]);
-        acc[nt][t] = mfma32(lds_tr_a<CPR>(vt, jh * 32 + 16, t * 32), p1, acc[nt][t]);
+      for (int hh = 0; hh < 2; ++hh) {
+        p[hh][0] = pack_b(sd[jh], hh);
+        if constexpr (F32) p[hh][1] = pack_lo(sd[jh], hh, p[hh][0]);
       }
+#pragma unroll
+      for (int t = 0; t < NVT; ++t)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          bf16x8 va[NP];
+#pragma unroll
+          for (int pl = 0; pl < NP; ++pl) va[pl] = lds_tr_a<CPR>(sm.vd[w][pl], jh * 32 + 16 * hh, t * 32);
+          acc[nt][t] = mm3<NP>(va, p[hh], acc[nt][t]);
+        }
     }
   }
-  bf16x8 qb[2][NKS];
+  bf16x8 qb[2][NKS][NP];
   for (int J = 0; J < nJ; ++J) {
     const int buf = J & 1;
     if (J + 1 < nJ) stage(J + 1);
     if (J >= cb || J % PR == 0) {  // the query operand changes
       const bf16* qsrc = (J < cb) ? ws.qb + ((int64_t)bhq * NS + J / PR) * T * KD
                                   : ws.qs + ((int64_t)bhq * PR + (J - cb)) * T * KD;
+      const int64_t qlo = (J < cb) ? ws.lo_qb : ws.lo_qs;
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
-        for (int st = 0; st < NKS; ++st)
-          qb[nt][st] = ld8(qsrc + (int64_t)(iw0 + nt * 32 + l32) * KD + 16 * st + 8 * g);
+        for (int st = 0; st < NKS; ++st) {
+          const bf16* p = qsrc + (int64_t)(iw0 + nt * 32 + l32) * KD + 16 * st + 8 * g;
+          qb[nt][st][0] = ld8(p);
+          if constexpr (F32) qb[nt][st][1] = ld8(p + qlo);
+        }
     }
     if (live && J < Iw) {
 #pragma unroll
@@ -737,8 +843,12 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_softmax
         for (int jh = 0; jh < 2; ++jh) {
           sc[jh] = zero16();
 #pragma unroll
-          for (int st = 0; st < NKS; ++st)
-            sc[jh] = mfma32(ld8(swz<CPR>(sm.k[buf], jh * 32 + l32, 2 * st + g)), qb[nt][st], sc[jh]);
+          for (int st = 0; st < NKS; ++st) {
+            bf16x8 ka[NP];
+#pragma unroll
+            for (int pl = 0; pl < NP; ++pl) ka[pl] = ld8(swz<CPR>(sm.k[buf][pl], jh * 32 + l32, 2 * st + g));
+            sc[jh] = mm3<NP>(ka, qb[nt][st], sc[jh]);
+          }
         }
         float mx = -INFINITY;
 #pragma unroll
@@ -761,12 +871,21 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_softmax
             sc[jh][e] = __builtin_amdgcn_exp2f(fmaf(sc[jh][e], sl2, -mn));
             l[nt] += sc[jh][e];
           }
-          const bf16x8 p0 = pack_b(sc[jh], 0), p1 = pack_b(sc[jh], 1);
+          bf16x8 p[2][NP];
 #pragma unroll
-          for (int t = 0; t < NVT; ++t) {
-            acc[nt][t] = mfma32(lds_tr_a<CPR>(sm.v[buf], jh * 32, t * 32), p0, acc[nt][t]);
-            acc[nt][t] = mfma32(lds_tr_a<CPR>(sm.v[buf], jh * 32 + 16, t * 32), p1, acc[nt][t]);
+          for (int hh = 0; hh < 2; ++hh) {
+            p[hh][0] = pack_b(sc[jh], hh);
+            if constexpr (F32) p[hh][1] = pack_lo(sc[jh], hh, p[hh][0]);
           }
+#pragma unroll
+          for (int t = 0; t < NVT; ++t)
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+              bf16x8 va[NP];
+#pragma unroll
+              for (int pl = 0; pl < NP; ++pl) va[pl] = lds_tr_a<CPR>(sm.v[buf][pl], jh * 32 + 16 * hh, t * 32);
+              acc[nt][t] = mm3<NP>(va, p[hh], acc[nt][t]);
+            }
         }
       }
     }
@@ -779,15 +898,22 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_softmax
       const float ls = wave_sum32(l[nt]);
       const float inv = 1.f / ls;
       const int i = iw0 + nt * 32 + l32;
-      bf16* orow = o + b * os.b + hq * os.h + (int64_t)i * os.t;
+      pin_t<F32>* orow = o + b * os.b + hq * os.h + (int64_t)i * os.t;
 #pragma unroll
       for (int t = 0; t < NVT; ++t)
 #pragma unroll
         for (int qq = 0; qq < 4; ++qq) {
-          bf16x4 bb;
+          if constexpr (F32) {
+            f32x4 f;
 #pragma unroll
-          for (int u = 0; u < 4; ++u) bb[u] = (bf16)(acc[nt][t][4 * qq + u] * inv);
-          *reinterpret_cast<bf16x4*>(orow + t * 32 + 8 * qq + 4 * g) = bb;
+            for (int u = 0; u < 4; ++u) f[u] = acc[nt][t][4 * qq + u] * inv;
+            *reinterpret_cast<f32x4*>(orow + t * 32 + 8 * qq + 4 * g) = f;
+          } else {
+            bf16x4 bb;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) bb[u] = (bf16)(acc[nt][t][4 * qq + u] * inv);
+            *reinterpret_cast<bf16x4*>(orow + t * 32 + 8 * qq + 4 * g) = bb;
+          }
         }
       if (g == 0) ws.lse[(int64_t)bhq * T + i] = m[nt] + log2f(ls);
     }
@@ -798,7 +924,8 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64) void path_softmax
 // k_cache_j = keys carried to the sequence end (prepare_k_cache.py:12-74):
 // x = KL_J; x <- x HL_s^T for every later large chunk.  grid (NT, B*H)
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void path_kcache_kernel(int T, bf16* __restrict__ kc, Strides kcs, int H,
+template <bool F32>
+__global__ __launch_bounds__(256) void path_kcache_kernel(int T, pin_t<F32>* __restrict__ kc, Strides kcs, int H,
                                                           PathFwdWs ws) {
   __shared__ __attribute__((aligned(16))) float X[64][68];
   __shared__ __attribute__((aligned(16))) float MT[64][68];
@@ -806,7 +933,10 @@ __global__ __launch_bounds__(256) void path_kcache_kernel(int T, bf16* __restric
   const int b = bh / H, h = bh - b * H;
   const int NT = T / PC, NS = (NT + PR - 1) / PR;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 5, l32 = lane & 31;
-  load_rows64_f32(X, ws.kl + ((int64_t)bh * T + J * PC) * 64, 64);
+  if constexpr (F32)
+    load_rows64_split(X, ws.kl + ((int64_t)bh * T + J * PC) * 64, 64, ws.lo_kl);
+  else
+    load_rows64_f32(X, ws.kl + ((int64_t)bh * T + J * PC) * 64, 64);
   __syncthreads();
   for (int s = J / PR + 1; s < NS; ++s) {
     load_mat64<false>(MT, ws.hl + ((int64_t)bh * NS + s) * 4096);  // (HL^T)^T = HL
@@ -819,13 +949,19 @@ __global__ __launch_bounds__(256) void path_kcache_kernel(int T, bf16* __restric
     __syncthreads();
   }
   const int r = tid >> 2, cc = (tid & 3) * 16;
-  bf16* dst = kc + b * kcs.b + h * kcs.h + (int64_t)(J * PC + r) * kcs.t + cc;
+  pin_t<F32>* dst = kc + b * kcs.b + h * kcs.h + (int64_t)(J * PC + r) * kcs.t + cc;
 #pragma unroll
   for (int hh = 0; hh < 2; ++hh) {
-    bf16x8 vv;
+    if constexpr (F32) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) vv[e] = (bf16)X[r][cc + 8 * hh + e];
-    *reinterpret_cast<bf16x8*>(dst + 8 * hh) = vv;
+      for (int q4 = 0; q4 < 2; ++q4)
+        *reinterpret_cast<f32x4*>(dst + 8 * hh + 4 * q4) = *reinterpret_cast<const f32x4*>(&X[r][cc + 8 * hh + 4 * q4]);
+    } else {
+      bf16x8 vv;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) vv[e] = (bf16)X[r][cc + 8 * hh + e];
+      *reinterpret_cast<bf16x8*>(dst + 8 * hh) = vv;
+    }
   }
 }
 

@@ -14,11 +14,13 @@ reference ships as the kernels ``intra_chunk_preprocess_fwd.py`` and
 
     O_i = sum_{j <= i} softmax_j(s A_ij) v_j
 
-Tensors are bf16 GPU tensors in the reference layout ``[B, T, H, K]``; the kernels run at
-K = V = 64 and K = V = 128, and the other head dims the reference's kernels take (16, 32;
-a K/V pair that differs) run on rows zero-padded to the next of the two: the reflections
-``I - beta w w^T`` act as the identity on the padded coordinates, so the logits, O and the
-gradients of the real coordinates are unchanged.  There is no CPU or Triton fallback.
+Tensors are GPU tensors in the reference layout ``[B, T, H, K]``, all bf16 or all fp32 (the
+reference's LUCID-Path model is fp32, lucid_path/config/config.json:5).  bf16 runs at
+K = V = 64 and K = V = 128, fp32 at K = V = 64 (3-term bf16 split products on hi / lo copies
+of every operand, ~fp32 accuracy), and the other head dims the reference's kernels take
+(16, 32; a K/V pair that differs) run on rows zero-padded to the next supported one: the
+reflections ``I - beta w w^T`` act as the identity on the padded coordinates, so the logits,
+O and the gradients of the real coordinates are unchanged.  There is no CPU or Triton fallback.
 """
 from __future__ import annotations
 
@@ -47,24 +49,30 @@ def _ready(x: torch.Tensor) -> torch.Tensor:
     return x
 
 
+def _entry(softmax: bool, fwd: bool, dtype: torch.dtype) -> str:
+    """C entry point name: lucid_path[_softmax]_{fwd,bwd}[_f32]."""
+    return ("lucid_path_softmax_" if softmax else "lucid_path_") + ("fwd" if fwd else "bwd") + (
+        "_f32" if dtype == torch.float32 else "")
+
+
 def _fwd(q, k, v, w, beta, scale, use_cache, softmax=False):
     lib = _lib.load(_LIB)
-    pre = "lucid_path_softmax_" if softmax else "lucid_path_"
+    name = _entry(softmax, True, q.dtype)
     B, T, HQ, K = q.shape
     H = k.shape[2]
     dev = q.device
-    o = torch.empty(B, T, HQ, v.shape[-1], dtype=torch.bfloat16, device=dev)
-    kc = torch.empty(B, T, H, K, dtype=torch.bfloat16, device=dev) if use_cache else None
-    ws = torch.empty(getattr(lib, pre + "fwd_workspace_bytes")(B, T, H, HQ, K), dtype=torch.uint8, device=dev)
+    o = torch.empty(B, T, HQ, v.shape[-1], dtype=q.dtype, device=dev)
+    kc = torch.empty(B, T, H, K, dtype=q.dtype, device=dev) if use_cache else None
+    ws = torch.empty(getattr(lib, name + "_workspace_bytes")(B, T, H, HQ, K), dtype=torch.uint8, device=dev)
     beta = beta.contiguous()
     st3 = lambda t: _lib.strides3(t, (0, 2, 1))  # noqa: E731  (batch, head, time)
     beta_strides = (ctypes.c_int64 * 3)(beta.stride(0), beta.stride(2), beta.stride(1))
-    rc = getattr(lib, pre + "fwd")(
+    rc = getattr(lib, name)(
         _lib.ptr(q), st3(q), _lib.ptr(k), st3(k), _lib.ptr(v), st3(v), _lib.ptr(w), st3(w),
         _lib.ptr(beta), beta_strides, _lib.ptr(o), st3(o),
         _lib.ptr(kc) if kc is not None else None, st3(kc) if kc is not None else None,
         _lib.ptr(ws), B, T, H, HQ, K, float(scale), _lib.stream_handle(dev))
-    _lib.check(lib, rc, pre + "fwd")
+    _lib.check(lib, rc, name)
     return o, kc, ws
 
 
@@ -89,23 +97,25 @@ class ParallelLUCIDPathAttentionFunction(torch.autograd.Function):
         # the k_cache output carries no gradient (parallel.py:78-81 ignores dk_new)
         q, k, v, w, beta, o, ws = ctx.saved_tensors
         t, tp = ctx.t, q.shape[1]
-        if do.dtype != torch.bfloat16:
-            do = do.to(torch.bfloat16)
+        if do.dtype != q.dtype:
+            do = do.to(q.dtype)
         do = _ready(_pad_t(do, tp))
         lib = _lib.load(_LIB)
+        name = _entry(False, False, q.dtype)
         B, T, HQ, K = q.shape
         H = k.shape[2]
         dq, dk, dv, dw = (torch.empty_like(x) for x in (q, k, v, w))
-        db = torch.empty(B, T, H, dtype=torch.bfloat16, device=q.device)
-        bws = torch.empty(lib.lucid_path_bwd_workspace_bytes(B, T, H, HQ, K), dtype=torch.uint8, device=q.device)
+        db = torch.empty(B, T, H, dtype=q.dtype, device=q.device)
+        bws = torch.empty(getattr(lib, name + "_workspace_bytes")(B, T, H, HQ, K), dtype=torch.uint8,
+                          device=q.device)
         st3 = lambda x: _lib.strides3(x, (0, 2, 1))  # noqa: E731
         bst = lambda x: (ctypes.c_int64 * 3)(x.stride(0), x.stride(2), x.stride(1))  # noqa: E731
-        rc = lib.lucid_path_bwd(
+        rc = getattr(lib, name)(
             _lib.ptr(do), st3(do), _lib.ptr(q), st3(q), _lib.ptr(k), st3(k), _lib.ptr(w), st3(w),
             _lib.ptr(beta), bst(beta), _lib.ptr(o), st3(o), _lib.ptr(ws),
             _lib.ptr(dq), st3(dq), _lib.ptr(dk), st3(dk), _lib.ptr(dv), st3(dv), _lib.ptr(dw), st3(dw),
             _lib.ptr(db), bst(db), _lib.ptr(bws), B, T, H, HQ, K, float(ctx.scale), _lib.stream_handle(q.device))
-        _lib.check(lib, rc, "lucid_path_bwd")
+        _lib.check(lib, rc, name)
         return (dq[:, :t], dk[:, :t], dv[:, :t], dw[:, :t], db[:, :t], None, None, None, None)
 
 
@@ -130,24 +140,25 @@ class ParallelPathAttentionFunction(torch.autograd.Function):
     def backward(ctx, do, dk_cache):
         q, k, v, w, beta, o, ws = ctx.saved_tensors
         t, tp = ctx.t, q.shape[1]
-        if do.dtype != torch.bfloat16:
-            do = do.to(torch.bfloat16)
+        if do.dtype != q.dtype:
+            do = do.to(q.dtype)
         do = _ready(_pad_t(do, tp))
         lib = _lib.load(_LIB)
+        name = _entry(True, False, q.dtype)
         B, T, HQ, K = q.shape
         H = k.shape[2]
         dq, dk, dv, dw = (torch.empty_like(x) for x in (q, k, v, w))
-        db = torch.empty(B, T, H, dtype=torch.bfloat16, device=q.device)
-        bws = torch.empty(lib.lucid_path_softmax_bwd_workspace_bytes(B, T, H, HQ, K), dtype=torch.uint8,
+        db = torch.empty(B, T, H, dtype=q.dtype, device=q.device)
+        bws = torch.empty(getattr(lib, name + "_workspace_bytes")(B, T, H, HQ, K), dtype=torch.uint8,
                           device=q.device)
         st3 = lambda x: _lib.strides3(x, (0, 2, 1))  # noqa: E731
         bst = lambda x: (ctypes.c_int64 * 3)(x.stride(0), x.stride(2), x.stride(1))  # noqa: E731
-        rc = lib.lucid_path_softmax_bwd(
+        rc = getattr(lib, name)(
             _lib.ptr(do), st3(do), _lib.ptr(q), st3(q), _lib.ptr(k), st3(k), _lib.ptr(v), st3(v),
             _lib.ptr(w), st3(w), _lib.ptr(beta), bst(beta), _lib.ptr(o), st3(o), _lib.ptr(ws),
             _lib.ptr(dq), st3(dq), _lib.ptr(dk), st3(dk), _lib.ptr(dv), st3(dv), _lib.ptr(dw), st3(dw),
             _lib.ptr(db), bst(db), _lib.ptr(bws), B, T, H, HQ, K, float(ctx.scale), _lib.stream_handle(q.device))
-        _lib.check(lib, rc, "lucid_path_softmax_bwd")
+        _lib.check(lib, rc, name)
         return (dq[:, :t], dk[:, :t], dv[:, :t], dw[:, :t], db[:, :t], None, None, None, None)
 
 
@@ -159,11 +170,15 @@ def _check(q, k, v, w, beta, g):
     assert beta.shape[:3] == k.shape[:3], 'beta should have the same number of heads as k'
     assert g is None, 'g is not supported'
     assert q.shape[-2] % k.shape[-2] == 0, 'the number of query heads should be divisible by the number of key heads'
+    if q.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"lucid_amd: q must be bfloat16 or float32, got {q.dtype}")
     for name, x in (("q", q), ("k", k), ("v", v), ("w", w), ("beta", beta)):
         if not x.is_cuda:
             raise RuntimeError(f"lucid_amd: {name} must be a GPU tensor (no CPU path)")
-        if x.dtype != torch.bfloat16:
-            raise TypeError(f"lucid_amd: {name} must be bfloat16, got {x.dtype}")
+        if x.dtype != q.dtype:
+            raise TypeError(f"lucid_amd: {name} must have q's dtype {q.dtype}, got {x.dtype}")
+    if q.dtype == torch.float32 and max(q.shape[-1], v.shape[-1]) > _KDS[0]:
+        raise NotImplementedError("lucid_amd: fp32 LUCID-Path runs at head dims up to 64 (bf16 up to 128)")
 
 
 _KDS = (64, 128)  # head dims of the kernels (q, k, w and v rows share one)

@@ -107,9 +107,20 @@ def test_argument_validation_without_gpu(built):
     rc = plib.lucid_path_softmax_fwd(dummy, s4, dummy, s4, dummy, s4, dummy, s4, dummy, sb, dummy, s4, None, None,
                                      misaligned, 1, 256, 1, 1, 64, 0.125, None)
     assert rc == _lib.LUCID_EINVAL and b"256-byte aligned" in plib.lucid_path_last_error()
+    # the path kernels run at head dims 64 and 128 (the Python layer pads the others)
     rc = plib.lucid_path_softmax_fwd(dummy, s4, dummy, s4, dummy, s4, dummy, s4, dummy, sb, dummy, s4, None, None,
-                                     dummy, 1, 256, 1, 1, 128, 0.125, None)
+                                     dummy, 1, 256, 1, 1, 96, 0.125, None)
     assert rc == _lib.LUCID_EINVAL and b"head_dim" in plib.lucid_path_last_error()
+    # fp32: head dim 64 only; its workspaces add the lo planes of the bf16 operand copies
+    rc = plib.lucid_path_fwd_f32(dummy, s4, dummy, s4, dummy, s4, dummy, s4, dummy, sb, dummy, s4, None, None,
+                                 dummy, 1, 256, 1, 1, 128, 0.125, None)
+    assert rc == _lib.LUCID_EINVAL and b"fp32" in plib.lucid_path_last_error()
+    for kind in ("fwd", "bwd", "softmax_fwd", "softmax_bwd"):
+        n16 = getattr(plib, f"lucid_path_{kind}_workspace_bytes")(1, 4096, 2, 4, 64)
+        n32 = getattr(plib, f"lucid_path_{kind}_f32_workspace_bytes")(1, 4096, 2, 4, 64)
+        assert n32 > n16, kind
+    # head dim 128: the KD x KD transport matrices and 128-wide rows
+    assert plib.lucid_path_fwd_workspace_bytes(1, 4096, 2, 4, 128) > 2 * plib.lucid_path_fwd_workspace_bytes(1, 4096, 2, 4, 64)
     # the softmax forward workspace drops the solve's inverses and O^T and adds the row lse
     B, T, H, HQ = 1, 4096, 2, 4
     d = plib.lucid_path_fwd_workspace_bytes(B, T, H, HQ, 64) - plib.lucid_path_softmax_fwd_workspace_bytes(B, T, H, HQ, 64)
