@@ -42,6 +42,7 @@ def causal_flops(B, Hq, T, D):
 # scores and the preprocessing kernels count zero)
 KERNEL_FLOPS = {
     "lucid_precond_fwd_kernel": lambda B, Hq, Hkv, T, D: 2.0 * T * T * D * B * Hkv,   # K^K^T, P V'
+    "lucid_precond_fwd_wide_kernel": lambda B, Hq, Hkv, T, D: 2.0 * T * T * D * B * Hkv,  # the same, 256 rows/WG
     "lucid_attn_fwd_kernel": lambda B, Hq, Hkv, T, D: 2.0 * T * T * D * B * Hq,       # QK^T, P V'
     # chain (K^K^T, P V') and attention (QK^T, P V') of each block in one kernel (Hq == Hkv)
     "lucid_fused_fwd_kernel": lambda B, Hq, Hkv, T, D: 2.0 * T * T * D * B * (Hkv + Hq),
@@ -134,7 +135,7 @@ def _bench_inputs(B, Hq, Hkv, T, D, dev, grad=True, keys="iid"):
     return q, k, v, do
 
 
-def _path_inputs(B, H, T, D, dev):
+def _path_inputs(B, H, T, D, dev, dtype=None):
     import torch
     g = torch.Generator().manual_seed(0)
     q, k, v = (torch.randn(B, T, H, D, generator=g) for _ in range(3))
@@ -142,7 +143,7 @@ def _path_inputs(B, H, T, D, dev):
     w = w / w.norm(dim=-1, keepdim=True)
     beta = 2 * torch.sigmoid(torch.randn(B, T, H, generator=g))
     do = torch.randn(B, T, H, D, generator=g)
-    xs = [x.to(torch.bfloat16).to(dev) for x in (q, k, v, w, beta, do)]
+    xs = [x.to(dtype or torch.bfloat16).to(dev) for x in (q, k, v, w, beta, do)]
     for x in xs[:5]:
         x.requires_grad_()
     return xs
@@ -150,6 +151,10 @@ def _path_inputs(B, H, T, D, dev):
 
 # LUCID-Path kernel FLOPs of this implementation's algorithm (per query head, in T^2 d,
 # causal halves): the two-level transport makes every inter-chunk logit block one GEMM.
+# Executed per step: LUCID-Path 10 T^2 d per query head (solve 2 + dV 2 + row 3 + col 3),
+# PaTH softmax 9 (2 + 3 + 4), against the reference algorithm's 16 T^2 d (the bench's
+# headline count, which also charges the per-pair query propagation).
+PATH_EXECUTED = {"path": 10.0, "path_softmax": 9.0}
 PATH_KERNEL_FLOPS = {
     "path_solve_fwd_kernel": 2.0,  # A = Q K^T, L O
     "path_dv_kernel": 2.0,         # A, L^T dV
@@ -363,12 +368,14 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="lucid",
-                    choices=["lucid", "c2", "c3", "c5", "gqa128", "path", "path_softmax", "decode"],
+                    choices=["lucid", "c2", "c3", "c5", "gqa128", "path", "path128", "path_f32", "path_softmax",
+                             "decode"],
                     help="lucid: north star B1 H16 T32768 d64 fwd+bwd (default); c2: B4 H16 T4096 d64 "
                          "fwd+bwd; c3: 16-layer Llama-LUCID decoder, one training step (fwd+bwd+AdamW) "
                          "on B1 x T8192; c5: B1 T131072 Hq32/Hkv8 d128 forward only; gqa128: the config-5 heads "
                          "(Hq32/Hkv8 d128) at B1 T32768, fwd+bwd; path: LUCID-Path "
-                         "B1 H16 T32768 d64 fwd+bwd; path_softmax: PaTH softmax attention on the config-4 "
+                         "B1 H16 T32768 d64 fwd+bwd; path128: the same at head dim 128; path_f32: config 4 on fp32 "
+                         "inputs; path_softmax: PaTH softmax attention on the config-4 "
                          "shape, fwd+bwd; decode: one decoding step against a 128K cache (config-5 heads)")
     ap.add_argument("--precision", default="auto", choices=["auto", "fast", "exact"],
                     help="LUCID chain precision (lucid_amd.set_precision): auto picks per head from the row "
@@ -412,16 +419,18 @@ def main():
         bench_decode(args, dev)
         return
     fwd_only = wl == "c5"
-    if wl in ("path", "path_softmax"):
+    path_kind = {"path": "path", "path128": "path", "path_f32": "path", "path_softmax": "path_softmax"}.get(wl)
+    executed = None
+    if path_kind:
         from lucid_amd.lucid_path import parallel_lucid_path_attention, parallel_path_attention
-        B, Hq, Hkv, T, D = 1, 16, 16, 32768, 64
-        q, k, v, w, beta, do = _path_inputs(B, Hq, T, D, dev)
+        B, Hq, Hkv, T, D = 1, 16, 16, 32768, (128 if wl == "path128" else 64)
+        q, k, v, w, beta, do = _path_inputs(B, Hq, T, D, dev, torch.float32 if wl == "path_f32" else None)
         lib, prefix = _lib.load("liblucid_path.so"), "lucid_path_"
 
         def step():
             for x in (q, k, v, w, beta):
                 x.grad = None
-            if wl == "path":
+            if path_kind == "path":
                 o, _ = parallel_lucid_path_attention(k, v, w, beta, q=q)
             else:
                 o, _ = parallel_path_attention(q, k, v, w, beta)
@@ -429,10 +438,13 @@ def main():
         # count of the reference algorithm (query propagated through every chunk pair):
         # fwd 4 T^2 d (A, L O, 2x propagation) + bwd 12 T^2 d per query head
         flops = 16.0 * T * T * D * B * Hq
+        executed = PATH_EXECUTED[path_kind] * T * T * D * B * Hq
         kflops = {n: f * T * T * D * B * Hq for n, f in PATH_KERNEL_FLOPS.items()}
-        metric = "LUCID-Path fwd+bwd tokens/s & TFLOP/s at T=32K bf16 (config 4)"
-        if wl == "path_softmax":
-            metric = "PaTH softmax attention fwd+bwd tokens/s & TFLOP/s at T=32K bf16 (config-4 shape)"
+        metric = {"path": "LUCID-Path fwd+bwd tokens/s & TFLOP/s at T=32K bf16 (config 4)",
+                  "path128": "LUCID-Path fwd+bwd tokens/s & TFLOP/s at T=32K bf16, head dim 128",
+                  "path_f32": "LUCID-Path fwd+bwd tokens/s & TFLOP/s at T=32K fp32 (config 4, fp32 inputs)",
+                  "path_softmax": "PaTH softmax attention fwd+bwd tokens/s & TFLOP/s at T=32K bf16 "
+                                  "(config-4 shape)"}[wl]
     else:
         B, Hq, Hkv, T, D = {"lucid": (1, 16, 16, 32768, 64), "c2": (4, 16, 16, 4096, 64),
                             "c5": (1, 32, 8, 131072, 128), "gqa128": (1, 32, 8, 32768, 128)}[wl]
@@ -450,8 +462,8 @@ def main():
         if fwd_only:
             flops = 2.0 * T * T * D * B * (Hq + Hkv)
             kflops = {n: KERNEL_FLOPS[n](B, Hq, Hkv, T, D) for n in
-                      ("lucid_precond_fwd_kernel", "lucid_attn_fwd_kernel", "lucid_attn_fwd_wide_kernel",
-                       "lucid_fused_fwd_kernel")}
+                      ("lucid_precond_fwd_kernel", "lucid_precond_fwd_wide_kernel", "lucid_attn_fwd_kernel",
+                       "lucid_attn_fwd_wide_kernel", "lucid_fused_fwd_kernel")}
         else:
             flops = lucid_flops(B, Hq, Hkv, T, D)
             kflops = {n: f(B, Hq, Hkv, T, D) for n, f in KERNEL_FLOPS.items()}
@@ -546,18 +558,24 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic (seeded N(0,1)/sqrt(d) q,k,v; N(0,1) dO)" if wl not in ("path", "path_softmax")
+        "dtype": "f32" if wl == "path_f32" else "bf16",
+        "data": "synthetic (seeded N(0,1)/sqrt(d) q,k,v; N(0,1) dO)" if not path_kind
                 else "synthetic (seeded N(0,1) q,k,v,w; w L2-normalised; beta=2 sigmoid(N(0,1)); N(0,1) dO)",
         "precision": args.precision, "keys": args.keys, "fused_forward": not args.no_fused_fwd,
         "config": {"workload": {"lucid": "lucid_attention_fwd_bwd", "c2": "lucid_attention_fwd_bwd",
                                 "c5": "lucid_attention_fwd", "gqa128": "lucid_attention_fwd_bwd",
-                                "path": "lucid_path_fwd_bwd",
+                                "path": "lucid_path_fwd_bwd", "path128": "lucid_path_fwd_bwd",
+                                "path_f32": "lucid_path_fwd_bwd",
                                 "path_softmax": "path_softmax_attention_fwd_bwd"}[wl],
                    "B": B, "Hq": Hq, "Hkv": Hkv, "T": T, "head_dim": D, "causal": True,
                    "parallelism": "single GPU"},
         "tflops": round(flops / (ms / 1e3) / 1e12, 1),
         "frac_mfma_peak": round(flops / (ms / 1e3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+        # path workloads: the work this implementation executes (see PATH_EXECUTED), beside the
+        # reference algorithm's count above
+        "tflops_executed": round(executed / (ms / 1e3) / 1e12, 1) if executed else None,
+        "frac_mfma_peak_executed": (round(executed / (ms / 1e3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)
+                                    if executed else None),
         "roofline": {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": traffic},
         "kernels": kernels,
