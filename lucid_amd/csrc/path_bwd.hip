@@ -85,7 +85,7 @@ __global__ __launch_bounds__(256) void path_bwd_zero_kernel(int64_t n_hl, int64_
 // reduction:
 //   S[I][J] = Qop_I . Kop_J, L = exp(s S - 1/s), acc^T[d][j] += dV^T[d][i] L[i][j]
 // Row tiles beyond the large chunk share one query operand (QB) for both chunks and
-// are swept in pairs, one barrier and one staging round per pair; the (at most six)
+// are swept in pairs, one barrier and one staging round per pair; the (at most PR - 2)
 // row tiles inside the large chunk need a query slot per column chunk (QS) and are
 // swept one per step with both slots staged.  Then dV_B = Y_B^T R_B (published),
 // R_A -= L_BA^T dV_B, dV_A = Y_A^T R_A (published), R = dO - acc, and

@@ -51,7 +51,7 @@ lucid::PathFwdWs carve_path_fwd(void* base, int B, int T, int H, int HQ, size_t*
                                 int KD = 64, bool f32 = false) {
   const size_t NP = f32 ? 2 : 1;
   const size_t BH = (size_t)B * H, BHq = (size_t)B * HQ;
-  const size_t NT = T / 64, NS = (NT + 7) / 8, KK = (size_t)KD * KD;
+  const size_t NT = T / 64, NS = (NT + lucid::PR - 1) / lucid::PR, KK = (size_t)KD * KD;
   lucid::PathFwdWs w{};
   size_t off = 0;
   char* p = static_cast<char*>(base);
@@ -74,7 +74,7 @@ lucid::PathFwdWs carve_path_fwd(void* base, int B, int T, int H, int HQ, size_t*
   w.qt = reinterpret_cast<float*>(take(BHq * T * KD * 4));
   w.ld = reinterpret_cast<float*>(take(BHq * NT * 4096 * 4));
   if (!softmax) w.y = reinterpret_cast<float*>(take(BHq * NT * 4096 * 4));
-  w.qs = take_b(BHq * 8 * T * KD, w.lo_qs);
+  w.qs = take_b(BHq * lucid::PR * T * KD, w.lo_qs);
   w.qb = take_b(BHq * NS * T * KD, w.lo_qb);
   if (!softmax) w.oT = take_b(BHq * T * KD, w.lo_oT);
   if (softmax && f32) w.vsp = take_b(BH * T * KD, w.lo_vsp);
@@ -104,7 +104,7 @@ lucid::PathBwdWs carve_path_bwd(void* base, int B, int T, int HQ, size_t* bytes,
                                 bool f32 = false) {
   const size_t NP = f32 ? 2 : 1;
   const size_t BHq = (size_t)B * HQ;
-  const size_t NT = T / 64, NS = (NT + 7) / 8, KK = (size_t)KD * KD;
+  const size_t NT = T / 64, NS = (NT + lucid::PR - 1) / lucid::PR, KK = (size_t)KD * KD;
   lucid::PathBwdWs w{};
   size_t off = 0;
   char* p = static_cast<char*>(base);
@@ -159,7 +159,7 @@ int launch_front(const void* q, const int64_t* q_strides, const void* k, const i
                  int B, int T, int H, int HQ, float scale, int softmax, const lucid::PathFwdWs& ws, hipStream_t st,
                  int KD) {
   using TI = lucid::pin_t<F32>;
-  const int NT = T / 64, NS = (NT + 7) / 8;
+  const int NT = T / 64, NS = (NT + lucid::PR - 1) / lucid::PR;
   const int BH = B * H, BHq = B * HQ;
   if (KD == 128) {
     LUCID_TIMED_LAUNCH(phip, "path_chunk128_kernel", lucid::path_chunk128_kernel, dim3(NT, BHq), st, (const bf16*)q,
@@ -215,7 +215,7 @@ int launch_back(const void* q, const int64_t* q_strides, const void* k, const in
                 void* dw, const int64_t* dw_strides, void* dbeta, const int64_t* dbeta_strides, int B, int T, int H,
                 int HQ, const lucid::PathFwdWs& ws, const lucid::PathBwdWs& bw, hipStream_t st, int KD) {
   using TI = lucid::pin_t<F32>;
-  const int NT = T / 64, NS = (NT + 7) / 8;
+  const int NT = T / 64, NS = (NT + lucid::PR - 1) / lucid::PR;
   const int BH = B * H, BHq = B * HQ;
   if (KD == 128) {
     LUCID_TIMED_LAUNCH(phip, "path_products_bwd128_kernel", lucid::path_products_bwd128_kernel, dim3(NS, BHq), st, HQ,
@@ -351,7 +351,7 @@ int path_bwd_impl(int softmax, const void* dout, const int64_t* do_strides, cons
   const lucid::PathFwdWs ws = carve_path_fwd(const_cast<void*>(fwd_ws), B, T, H, HQ, nullptr, softmax != 0, K, F32);
   const lucid::PathBwdWs bw = carve_path_bwd(bwd_ws, B, T, HQ, nullptr, softmax != 0, K, F32);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const int NT = T / 64, NS = (NT + 7) / 8;
+  const int NT = T / 64, NS = (NT + lucid::PR - 1) / lucid::PR;
   const int BHq = B * HQ;
   const int64_t n_hl = (int64_t)BHq * NS * K * K, n_hc = (int64_t)BHq * NT * K * K;
   LUCID_TIMED_LAUNCH(phip, "path_bwd_zero_kernel", lucid::path_bwd_zero_kernel, dim3(1024), st, n_hl, n_hc, BHq, bw);

@@ -1,5 +1,5 @@
 // Shared helpers of the LUCID-Path kernels (head dim K = V = 64 or 128, small chunk 64,
-// large chunk 8 small chunks = 512 positions).
+// large chunk PR = 16 small chunks = 1024 positions).
 //
 // fp32 inputs (template flag F32): the caller's tensors are fp32, and every bf16 MFMA
 // operand buffer of the workspace holds two bf16 planes, hi = bf16(x) and lo = bf16(x - hi),
@@ -12,7 +12,7 @@
 namespace lucid {
 
 constexpr int PC = 64;  // small chunk (positions)
-constexpr int PR = 8;   // small chunks per large chunk
+constexpr int PR = 16;  // small chunks per large chunk (S = 1024 positions)
 
 // element type of the caller's tensors
 template <bool F32>
