@@ -541,19 +541,72 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64 && !F32) void path
   // ---- dM += X^T G over the pair's rows (atomic) and G <- G M^T for each wave's rows ----
   // X (rows of the query operand, row-major) is staged into the idle half of the double
   // buffer (tile J+1 is staged only after the transition); X^T comes from transposing reads
-  auto transition = [&](int J, const bf16* X, int64_t xlo, const float* M, float* dM) {
-    const bool act = Iw < NT && J < Iw;
-    // planes of the X rows of chunk I1 (in k) and I1 + 1 (in o)
+  bf16x8 qb[NKS][NP];  // this wave's rows of the current query operand (MFMA B operands)
+  // the query operand of key tile J (QB^(J/PR) below the large chunk, QS slot J - cb inside
+  // it), and whether a transport step precedes tile J (the operand differs from tile J - 1's)
+  auto opnd = [&](int J) {
+    return (J < cb) ? ws.qb + ((int64_t)bhq * NS + J / PR) * T * KD : ws.qs + ((int64_t)bhq * PR + (J - cb)) * T * KD;
+  };
+  auto opnd_lo = [&](int J) { return (J < cb) ? ws.lo_qb : ws.lo_qs; };
+  auto trans_at = [&](int J) { return (J < cb) ? (J % PR == 0 && J > 0) : (sI > 0 || J > cb); };
+  // KD = 64: a transition's X rows (the new operand's rows of chunks I1, I1 + 1) are fetched
+  // into registers one key tile ahead, so that no transition waits for them; at KD = 128 they
+  // are staged by direct loads in the transition (registers)
+  constexpr bool XPRE = KD == 64;
+  constexpr int XPT = XPRE ? 2 * 64 * CPR / 256 : 1;  // 16-byte chunks per thread and plane
+  bf16x8 xr[NP][XPT];
+  auto xprefetch = [&](int J) {
+    const bf16* X = opnd(J) + (int64_t)I1 * PC * KD;
+    const int64_t xlo = opnd_lo(J);
 #pragma unroll
-    for (int pl = 0; pl < NP; ++pl) {
-      dma_stage<64, CPR>(plan_k, X + pl * xlo + (int64_t)I1 * PC * KD, sm.k[(J + 1) & 1][pl]);
-      if (pair) dma_stage<64, CPR>(plan_k, X + pl * xlo + (int64_t)(I1 + 1) * PC * KD, sm.o[(J + 1) & 1][pl]);
+    for (int u = 0; u < XPT; ++u) {
+      const int idx = tid + 256 * u, r = idx / CPR, c = idx - (idx / CPR) * CPR;
+      if (r < 64 || pair) {
+#pragma unroll
+        for (int pl = 0; pl < NP; ++pl) xr[pl][u] = ld8(X + pl * xlo + (int64_t)r * KD + 8 * c);
+      }
+    }
+  };
+  auto transition = [&](int J, const float* M, float* dM) {
+    const bool act = Iw < NT && J < Iw;
+    // the M rows of this wave's G M^T (KD = 64), loaded before the barrier so that their
+    // latency overlaps the dM products
+    f32x4 mv[XPRE ? NVT : 1][XPRE ? NKS : 1][2];
+    if constexpr (XPRE) {
+      if (act) {
+#pragma unroll
+        for (int bt = 0; bt < NVT; ++bt)
+#pragma unroll
+          for (int ks = 0; ks < NKS; ++ks)
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh)
+              mv[bt][ks][hh] = *reinterpret_cast<const f32x4*>(M + (bt * 32 + l32) * KD + 16 * ks + 8 * g + 4 * hh);
+      }
+      // planes of the X rows of chunk I1 (in k) and I1 + 1 (in o), swizzled as the direct loads
+#pragma unroll
+      for (int u = 0; u < XPT; ++u) {
+        const int idx = tid + 256 * u, r = idx / CPR, c = idx - (idx / CPR) * CPR, rr = r & 63;
+        if (r < 64 || pair) {
+#pragma unroll
+          for (int pl = 0; pl < NP; ++pl)
+            *reinterpret_cast<bf16x8*>((r < 64 ? sm.k[(J + 1) & 1][pl] : sm.o[(J + 1) & 1][pl]) + swz_off<CPR>(rr, c)) =
+                xr[pl][u];
+        }
+      }
+    } else {
+      const bf16* X = opnd(J);
+      const int64_t xlo = opnd_lo(J);
+#pragma unroll
+      for (int pl = 0; pl < NP; ++pl) {
+        dma_stage<64, CPR>(plan_k, X + pl * xlo + (int64_t)I1 * PC * KD, sm.k[(J + 1) & 1][pl]);
+        if (pair) dma_stage<64, CPR>(plan_k, X + pl * xlo + (int64_t)(I1 + 1) * PC * KD, sm.o[(J + 1) & 1][pl]);
+      }
     }
 #pragma unroll
     for (int t = 0; t < NVT; ++t)
 #pragma unroll
       for (int e = 0; e < 16; ++e) sm.g[32 * w + l32][t * 32 + drow(e, g)] = act ? acc[t][e] : 0.f;
-    dma_wait();
+    if constexpr (!XPRE) dma_wait();
     __syncthreads();
 #pragma unroll 1
     for (int tt = w; tt < NVT * NVT; tt += 4) {
@@ -586,7 +639,17 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64 && !F32) void path
 #pragma unroll
         for (int ks = 0; ks < NKS; ++ks) {
           bf16x8 ah, al, bh8, bl;
-          split8(M + (bt * 32 + l32) * KD + 16 * ks + 8 * g, ah, al);
+          if constexpr (XPRE) {
+            float m8[8];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              m8[e] = mv[bt][ks][0][e];
+              m8[4 + e] = mv[bt][ks][1][e];
+            }
+            split_vals(m8, ah, al);
+          } else {
+            split8(M + (bt * 32 + l32) * KD + 16 * ks + 8 * g, ah, al);
+          }
           split8(&sm.g[32 * w + l32][16 * ks + 8 * g], bh8, bl);
           gn = mfma32(ah, bh8, gn);
           gn = mfma32(ah, bl, gn);
@@ -594,6 +657,15 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64 && !F32) void path
         }
         acc[bt] = gn;
       }
+    }
+    // this wave's rows of the new operand (the sweep's query registers), from the staged X
+    {
+#pragma unroll
+      for (int st = 0; st < NKS; ++st)
+#pragma unroll
+        for (int pl = 0; pl < NP; ++pl)
+          qb[st][pl] = ld8(swz<CPR>((pair && (w >> 1)) ? sm.o[(J + 1) & 1][pl] : sm.k[(J + 1) & 1][pl],
+                                    (w & 1) * 32 + l32, 2 * st + g));
     }
     __syncthreads();
   };
@@ -611,30 +683,31 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64 && !F32) void path
   if (nJ > 0) stage(0);
   dma_wait();
   __syncthreads();
-  bf16x8 qb[NKS][NP];
   for (int J = 0; J < nJ; ++J) {
     const int buf = J & 1;
-    // transport step before the first tile that uses a new query operand
-    if (J < cb) {
-      if (J % PR == 0 && J > 0) {
+    // transport step before the first tile that uses a new query operand (it also loads the
+    // new operand's rows into qb)
+    const bool tr = trans_at(J);
+    if (tr) {
+      if (J < cb) {
         const int s = J / PR;
-        transition(J, ws.qb + ((int64_t)bhq * NS + s) * T * KD, ws.lo_qb, ws.hl + ((int64_t)bh * NS + s) * (KD * KD),
-                   bw.dhl + ((int64_t)bhq * NS + s) * (KD * KD));
+        transition(J, ws.hl + ((int64_t)bh * NS + s) * (KD * KD), bw.dhl + ((int64_t)bhq * NS + s) * (KD * KD));
+      } else {
+        transition(J, ws.hc + ((int64_t)bh * NT + J) * (KD * KD), bw.dhc + ((int64_t)bhq * NT + J) * (KD * KD));
       }
-    } else if (sI > 0 || J > cb) {
-      transition(J, ws.qs + ((int64_t)bhq * PR + (J - cb)) * T * KD, ws.lo_qs,
-                 ws.hc + ((int64_t)bh * NT + J) * (KD * KD), bw.dhc + ((int64_t)bhq * NT + J) * (KD * KD));
     }
     if (J + 1 < nJ) stage(J + 1);
-    if (J >= cb || J % PR == 0) {  // the query operand changes
-      const bf16* qsrc = (J < cb) ? ws.qb + ((int64_t)bhq * NS + J / PR) * T * KD
-                                  : ws.qs + ((int64_t)bhq * PR + (J - cb)) * T * KD;
-      const int64_t qlo = (J < cb) ? ws.lo_qb : ws.lo_qs;
+    if (!tr && (J >= cb || J % PR == 0)) {  // the query operand changes without a transport step (J = 0)
+      const bf16* qsrc = opnd(J);
+      const int64_t qlo = opnd_lo(J);
 #pragma unroll
       for (int st = 0; st < NKS; ++st) {
         qb[st][0] = ld8(qsrc + (int64_t)(iw0 + l32) * KD + 16 * st + 8 * g);
         if constexpr (F32) qb[st][1] = ld8(qsrc + qlo + (int64_t)(iw0 + l32) * KD + 16 * st + 8 * g);
       }
+    }
+    if constexpr (XPRE) {
+      if (J + 1 < nJ && trans_at(J + 1)) xprefetch(J + 1);  // in flight during this tile's sweep
     }
     if (Iw < NT && J < Iw) {
 #pragma unroll
