@@ -161,3 +161,42 @@ def test_path_softmax_d128_long(B, T, H, G):
         err = (got.grad.double() - r).abs().max().item()
         print(f"  {name}: max err {err:.2e} max|ref| {r.abs().max().item():.2e}", flush=True)
         check(name, err, r.abs().max().item())
+
+
+@pytest.mark.parametrize("softmax", [False, True])
+def test_path_d128_varlen_packed_sequences(softmax):
+    """cu_seqlens at head dim 128: every packed sequence against its own float64 oracle."""
+    from lucid_amd.lucid_path import parallel_lucid_path_attention, parallel_path_attention
+    bounds = [0, 90, 218, 300]
+    T = bounds[-1]
+    q, k, v, w, beta, do = _inputs(1, T, 2, 1, 128, 128, seed=41 + softmax)
+    print(f"case path d128 varlen softmax={softmax} bounds={bounds}", flush=True)
+    leaves = [x.cuda().requires_grad_() for x in (q, k, v, w, beta)]
+    cu = torch.tensor(bounds, dtype=torch.int32, device="cuda")
+    if softmax:
+        o, kc = parallel_path_attention(*leaves, cu_seqlens=cu, use_cache=True)
+    else:
+        o, kc = parallel_lucid_path_attention(leaves[1], leaves[2], leaves[3], leaves[4], q=leaves[0], cu_seqlens=cu,
+                                              use_cache=True)
+    o.backward(do.cuda())
+    torch.cuda.synchronize()
+    s = 128 ** -0.5
+    for s0, s1 in zip(bounds[:-1], bounds[1:]):
+        seg = [_f64(x[:, s0:s1]) for x in (q, k, v, w, beta)]
+        if softmax:
+            o_ref = P.path_softmax_bruteforce(*seg, scale=s)
+            g_ref = P.path_softmax_grads(*seg, _f64(do[:, s0:s1]), scale=s)
+        else:
+            n = s1 - s0
+            tp = (n + 63) // 64 * 64
+            segp = [_pad_t(x, tp) for x in seg]
+            o_ref = P.path_attention_chunked(*segp, scale=s, C=64)[:, :n]
+            g_ref = [r[:, :n] for r in P.path_attention_grads(*segp, _pad_t(do[:, s0:s1], tp), scale=s, C=64)]
+        check(f"seq [{s0},{s1}) o", (o[:, s0:s1].detach().cpu().double() - o_ref).abs().max().item(),
+              o_ref.abs().max().item())
+        kc_ref = P.path_kcache_bruteforce(seg[1], seg[3], seg[4])
+        check(f"seq [{s0},{s1}) k_cache", (kc[:, s0:s1].cpu().double() - kc_ref).abs().max().item(),
+              kc_ref.abs().max().item())
+        for name, x, r in zip(("dq", "dk", "dv", "dw", "dbeta"), leaves, g_ref):
+            check(f"seq [{s0},{s1}) {name}", (x.grad[:, s0:s1].cpu().double() - r).abs().max().item(),
+                  r.abs().max().item())

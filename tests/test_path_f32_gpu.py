@@ -125,3 +125,49 @@ def test_path_f32_rejects_wide_heads_and_mixed_dtypes():
     q, k, v, w, beta, _ = (x.cuda() for x in _inputs(1, 64, 1, 1, 64, 64, seed=1))
     with pytest.raises(TypeError, match="dtype"):
         parallel_lucid_path_attention(k, v.bfloat16(), w, beta, q=q)
+
+
+@pytest.mark.parametrize("softmax", [False, True])
+def test_path_f32_varlen_packed_sequences(softmax):
+    """cu_seqlens on fp32 inputs: every packed sequence against its own float64 oracle at the
+    fp32 bar (lengths in three 64-position buckets, one ragged)."""
+    from lucid_amd.lucid_path import parallel_lucid_path_attention, parallel_path_attention
+    bounds = [0, 70, 198, 262]
+    T = bounds[-1]
+    q, k, v, w, beta, do = _inputs(1, T, 2, 1, 64, 64, seed=31 + softmax)
+    print(f"case path f32 varlen softmax={softmax} bounds={bounds}", flush=True)
+    leaves = [x.cuda().requires_grad_() for x in (q, k, v, w, beta)]
+    cu = torch.tensor(bounds, dtype=torch.int32, device="cuda")
+    if softmax:
+        o, kc = parallel_path_attention(*leaves, cu_seqlens=cu, use_cache=True)
+    else:
+        o, kc = parallel_lucid_path_attention(leaves[1], leaves[2], leaves[3], leaves[4], q=leaves[0], cu_seqlens=cu,
+                                              use_cache=True)
+    o.backward(do.cuda())
+    torch.cuda.synchronize()
+    for s0, s1 in zip(bounds[:-1], bounds[1:]):
+        seg = [_f64(x[:, s0:s1]) for x in (q, k, v, w, beta)]
+        if softmax:
+            o_ref = P.path_softmax_bruteforce(*seg, scale=0.125)
+            g_ref = P.path_softmax_grads(*seg, _f64(do[:, s0:s1]), scale=0.125)
+        else:
+            n = s1 - s0
+            tp = (n + 63) // 64 * 64
+            segp = [_pad_t(x, tp) for x in seg]
+            o_ref = P.path_attention_chunked(*segp, scale=0.125, C=64)[:, :n]
+            g_ref = [r[:, :n] for r in P.path_attention_grads(*segp, _pad_t(do[:, s0:s1], tp), scale=0.125, C=64)]
+        _cmp(f"seq [{s0},{s1}) o", o[:, s0:s1], o_ref)
+        _cmp(f"seq [{s0},{s1}) k_cache", kc[:, s0:s1], P.path_kcache_bruteforce(*seg[1:2], seg[3], seg[4]))
+        for name, x, r in zip(("dq", "dk", "dv", "dw", "dbeta"), leaves, g_ref):
+            _cmp(f"seq [{s0},{s1}) {name}", x.grad[:, s0:s1], r)
+
+
+def test_path_f32_empty_sequence():
+    from lucid_amd.lucid_path import parallel_lucid_path_attention, parallel_path_attention
+    leaves = [x.cuda().requires_grad_() for x in _inputs(1, 0, 2, 1, 64, 64, seed=1)[:5]]
+    o, kc = parallel_path_attention(*leaves, use_cache=True)
+    assert o.shape == (1, 0, 2, 64) and o.dtype == torch.float32 and kc.shape == (1, 0, 2, 64)
+    o.sum().backward()
+    assert all(x.grad is not None and x.grad.shape == x.shape for x in leaves)
+    o2, kc2 = parallel_lucid_path_attention(*leaves[1:], q=leaves[0])
+    assert o2.shape == (1, 0, 2, 64) and kc2 is None
