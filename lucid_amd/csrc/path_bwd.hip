@@ -490,7 +490,9 @@ template <int KD, int NP>
 struct RowSmem {
   bf16 k[2][NP][64 * KD];  // [buffer][plane], swizzled (chunk c of row r at c ^ (r & 7))
   bf16 o[2][NP][64 * KD];
-  float g[128][KD + 4];  // G rows of the pair at a transport step
+  // G rows of the pair at a transport step as bf16 hi and lo planes, swizzled (chunk c of
+  // row r at c ^ (r & 7)): split once when stored, read directly by both transition products
+  bf16 gs[2][128 * KD];
 };
 
 // KD: head dim (64 or 128); the KD x KD transport matrices and their gradients are row-major.
@@ -567,11 +569,12 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64 && !F32) void path
       }
     }
   };
-  auto transition = [&](int J, const float* M, float* dM) {
+  // Ms: M as bf16 hi and lo planes (the lo plane KD * KD elements after the hi plane)
+  auto transition = [&](int J, const bf16* Ms, float* dM) {
     const bool act = Iw < NT && J < Iw;
-    // the M rows of this wave's G M^T (KD = 64), loaded before the barrier so that their
-    // latency overlaps the dM products
-    f32x4 mv[XPRE ? NVT : 1][XPRE ? NKS : 1][2];
+    // the M rows of this wave's G M^T (KD = 64; hi, lo), loaded before the barrier so that
+    // their latency overlaps the dM products
+    bf16x8 mv[XPRE ? NVT : 1][XPRE ? NKS : 1][2];
     if constexpr (XPRE) {
       if (act) {
 #pragma unroll
@@ -580,7 +583,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64 && !F32) void path
           for (int ks = 0; ks < NKS; ++ks)
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh)
-              mv[bt][ks][hh] = *reinterpret_cast<const f32x4*>(M + (bt * 32 + l32) * KD + 16 * ks + 8 * g + 4 * hh);
+              mv[bt][ks][hh] = ld8(Ms + hh * (KD * KD) + (bt * 32 + l32) * KD + 16 * ks + 8 * g);
       }
       // planes of the X rows of chunk I1 (in k) and I1 + 1 (in o), swizzled as the direct loads
 #pragma unroll
@@ -605,7 +608,18 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64 && !F32) void path
 #pragma unroll
     for (int t = 0; t < NVT; ++t)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) sm.g[32 * w + l32][t * 32 + drow(e, g)] = act ? acc[t][e] : 0.f;
+      for (int qd = 0; qd < 4; ++qd) {  // elements 4 qd .. 4 qd + 3: columns t*32 + 8 qd + 4 g + u
+        bf16x4 hi, lo;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const float x = act ? acc[t][4 * qd + u] : 0.f;
+          hi[u] = (bf16)x;
+          lo[u] = (bf16)(x - (float)hi[u]);
+        }
+        const int off = swz_off<CPR>(32 * w + l32, 4 * t + qd) + 4 * g;
+        *reinterpret_cast<bf16x4*>(sm.gs[0] + off) = hi;
+        *reinterpret_cast<bf16x4*>(sm.gs[1] + off) = lo;
+      }
     if constexpr (!XPRE) dma_wait();
     __syncthreads();
 #pragma unroll 1
@@ -616,13 +630,9 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64 && !F32) void path
       const int ks0 = (J < I1) ? 0 : 4, ks1 = (pair && J < I1 + 1) ? 8 : 4;
       for (int ks = ks0; ks < ks1; ++ks) {
         const bf16x8 xa = lds_tr_a<CPR>(ks < 4 ? sm.k[(J + 1) & 1][0] : sm.o[(J + 1) & 1][0], 16 * (ks & 3), at * 32);
-        bf16x8 gh, gl;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float x = sm.g[16 * ks + jmap(8 * g + e)][bt * 32 + l32];
-          gh[e] = (bf16)x;
-          gl[e] = (bf16)(x - (float)gh[e]);
-        }
+        // G rows 16 ks + jmap(slot), column bt * 32 + lane: the transposing read's slot order
+        const bf16x8 gh = lds_tr_a<CPR>(sm.gs[0], 16 * ks, bt * 32);
+        const bf16x8 gl = lds_tr_a<CPR>(sm.gs[1], 16 * ks, bt * 32);
         dm = mfma32(xa, gh, dm);
         dm = mfma32(xa, gl, dm);
         if constexpr (F32)
@@ -638,19 +648,16 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64 && !F32) void path
         f32x16 gn = zero16();
 #pragma unroll
         for (int ks = 0; ks < NKS; ++ks) {
-          bf16x8 ah, al, bh8, bl;
+          bf16x8 ah, al;
           if constexpr (XPRE) {
-            float m8[8];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              m8[e] = mv[bt][ks][0][e];
-              m8[4 + e] = mv[bt][ks][1][e];
-            }
-            split_vals(m8, ah, al);
+            ah = mv[bt][ks][0];
+            al = mv[bt][ks][1];
           } else {
-            split8(M + (bt * 32 + l32) * KD + 16 * ks + 8 * g, ah, al);
+            ah = ld8(Ms + (bt * 32 + l32) * KD + 16 * ks + 8 * g);
+            al = ld8(Ms + KD * KD + (bt * 32 + l32) * KD + 16 * ks + 8 * g);
           }
-          split8(&sm.g[32 * w + l32][16 * ks + 8 * g], bh8, bl);
+          const bf16x8 bh8 = ld8(swz<CPR>(sm.gs[0], 32 * w + l32, 2 * ks + g));
+          const bf16x8 bl = ld8(swz<CPR>(sm.gs[1], 32 * w + l32, 2 * ks + g));
           gn = mfma32(ah, bh8, gn);
           gn = mfma32(ah, bl, gn);
           gn = mfma32(al, bh8, gn);
@@ -691,9 +698,9 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(KD == 64 && !F32) void path
     if (tr) {
       if (J < cb) {
         const int s = J / PR;
-        transition(J, ws.hl + ((int64_t)bh * NS + s) * (KD * KD), bw.dhl + ((int64_t)bhq * NS + s) * (KD * KD));
+        transition(J, ws.hls + ((int64_t)bh * NS + s) * (2 * KD * KD), bw.dhl + ((int64_t)bhq * NS + s) * (KD * KD));
       } else {
-        transition(J, ws.hc + ((int64_t)bh * NT + J) * (KD * KD), bw.dhc + ((int64_t)bhq * NT + J) * (KD * KD));
+        transition(J, ws.hcs + ((int64_t)bh * NT + J) * (2 * KD * KD), bw.dhc + ((int64_t)bhq * NT + J) * (KD * KD));
       }
     }
     if (J + 1 < nJ) stage(J + 1);

@@ -70,6 +70,8 @@ lucid::PathFwdWs carve_path_fwd(void* base, int B, int T, int H, int HQ, size_t*
   w.kt = take_b(BH * T * KD, w.lo_kt);
   w.suf = reinterpret_cast<float*>(take(BH * NT * KK * 4));
   w.hl = reinterpret_cast<float*>(take(BH * NS * KK * 4));
+  w.hcs = reinterpret_cast<bf16*>(take(BH * NT * KK * 2 * 2));
+  w.hls = reinterpret_cast<bf16*>(take(BH * NS * KK * 2 * 2));
   w.kl = take_b(BH * T * KD, w.lo_kl);
   w.qt = reinterpret_cast<float*>(take(BHq * T * KD * 4));
   w.ld = reinterpret_cast<float*>(take(BHq * NT * 4096 * 4));

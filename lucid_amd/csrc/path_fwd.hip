@@ -28,6 +28,8 @@ struct PathFwdWs {
   bf16* kt;     // [BH][T][K]         k~ rows
   float* suf;   // [BH][NT][K][K]     SUF_c
   float* hl;    // [BH][NS][K][K]     HL_s
+  bf16* hcs;    // [BH][NT][2][K][K]  Hc as bf16 hi and lo planes (the backward transport operand)
+  bf16* hls;    // [BH][NS][2][K][K]  HL_s as bf16 hi and lo planes
   bf16* kl;     // [BH][T][K]         KL rows
   float* qt;    // [BHq][T][K]        q~
   float* ld;    // [BHq][NT][64][64]  L_diag (strictly lower)
@@ -104,9 +106,12 @@ __global__ __launch_bounds__(256) void path_chunk_kernel(const pin_t<F32>* __res
   if (kvw) {
     const f32x16 acc = mgemm64<true, false>(Wm, W2s, z);
     float* dst = ws.hc + ((int64_t)bh * NT + c) * 4096;
+    bf16* dsts = ws.hcs + ((int64_t)bh * NT + c) * 8192;
     DL_FOR_E {
       const int r = dl_row(e);
-      dst[r * 64 + cl] = (r == cl ? 1.f : 0.f) - acc[e];
+      const float x = (r == cl ? 1.f : 0.f) - acc[e];
+      dst[r * 64 + cl] = x;
+      put_split<2>(dsts, 4096, r * 64 + cl, x);
     }
   }
   // WBK = stril(beta W K^T) -> X
@@ -228,9 +233,13 @@ __global__ __launch_bounds__(256) void path_large_kernel(int T, PathFwdWs ws) {
   }
   __syncthreads();
   float* dst = ws.hl + ((int64_t)bh * ((NT + PR - 1) / PR) + s) * 4096;
+  bf16* dsts = ws.hls + ((int64_t)bh * ((NT + PR - 1) / PR) + s) * 8192;
   for (int i = 0; i < 4; ++i) {
     const int f = 4 * (tid + 256 * i);
-    *reinterpret_cast<f32x4*>(dst + f) = *reinterpret_cast<const f32x4*>(&Sf[f >> 6][f & 63]);
+    const f32x4 x = *reinterpret_cast<const f32x4*>(&Sf[f >> 6][f & 63]);
+    *reinterpret_cast<f32x4*>(dst + f) = x;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) put_split<2>(dsts, 4096, f + u, x[u]);
   }
 }
 

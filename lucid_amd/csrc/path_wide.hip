@@ -137,13 +137,17 @@ __global__ __launch_bounds__(256) void path_chunk128_kernel(const bf16* __restri
   }
   if (kvw) {  // Hc = I - W^T W2, block (ra, cb_)
     float* dst = ws.hc + ((int64_t)bh * NT + c) * (WK * WK);
+    bf16* dsts = ws.hcs + ((int64_t)bh * NT + c) * (2 * WK * WK);
 #pragma unroll 1
     for (int blk = 0; blk < 4; ++blk) {
       const int ra = blk >> 1, cb_ = blk & 1;
       const f32x16 a = mgemm64<true, false>(Bm[1 + ra], cb_ ? Bm[3] : Bm[0], z);
       DL_FOR_E {
         const int r = dl_row(e);
-        dst[(int64_t)(64 * ra + r) * WK + 64 * cb_ + cl] = (ra == cb_ && r == cl ? 1.f : 0.f) - a[e];
+        const int i = (64 * ra + r) * WK + 64 * cb_ + cl;
+        const float x = (ra == cb_ && r == cl ? 1.f : 0.f) - a[e];
+        dst[i] = x;
+        put_split<2>(dsts, WK * WK, i, x);
       }
     }
   }
@@ -202,8 +206,16 @@ __global__ __launch_bounds__(256) void path_large128_kernel(int T, PathFwdWs ws)
     __syncthreads();
   }
   float* hl = ws.hl + ((int64_t)bh * NS + s) * (WK * WK);
+  bf16* hls = ws.hls + ((int64_t)bh * NS + s) * (2 * WK * WK);
 #pragma unroll 1
-  for (int blk = 0; blk < 4; ++blk) store_blk(hl + (blk >> 1) * 64 * WK + (blk & 1) * 64, WK, Sf[blk]);
+  for (int blk = 0; blk < 4; ++blk) {
+    const int o = (blk >> 1) * 64 * WK + (blk & 1) * 64;
+    store_blk(hl + o, WK, Sf[blk]);
+    for (int idx = threadIdx.x; idx < 4096; idx += 256) {
+      const int r = idx >> 6, cc = idx & 63;
+      put_split<2>(hls, WK * WK, o + r * WK + cc, Sf[blk][r][cc]);
+    }
+  }
 }
 
 // x <- x M for rows [r0, r0 + 32 nrt) of X [rows][128] (fp32 LDS) with M^T in MT
