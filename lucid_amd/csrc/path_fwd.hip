@@ -256,7 +256,10 @@ __global__ __launch_bounds__(256) void path_large_kernel(int T, PathFwdWs ws) {
 template <bool F32>
 __global__ __launch_bounds__(256) void path_transport_kernel(int HQ, int H, int T, PathFwdWs ws) {
   __shared__ __attribute__((aligned(16))) float X[128][68];  // rows 0..63 = chunk A, 64..127 = chunk B
-  __shared__ __attribute__((aligned(16))) float MT[64][68];
+  // the step's transition matrix M as bf16 hi and lo planes, row-major, swizzled (chunk c of
+  // row r at c ^ (r & 7)); its columns (the A operand of D^T = M^T X^T) come through
+  // transposing reads
+  __shared__ __attribute__((aligned(16))) bf16 Ms[2][64 * 64];
   const int p = (int)gridDim.y - 1 - (int)blockIdx.y, bhq = blockIdx.x;
   const int NT = T / PC, NS = (NT + PR - 1) / PR;
   const int G = HQ / H;
@@ -269,6 +272,7 @@ __global__ __launch_bounds__(256) void path_transport_kernel(int HQ, int H, int 
     const float* src = ws.qt + ((int64_t)bhq * T + A * PC) * 64;  // A's and B's rows are adjacent
     for (int idx = tid; idx < (hasB ? 8192 : 4096); idx += 256) X[idx >> 6][idx & 63] = src[idx];
   }
+  __syncthreads();
   // rows r0 .. r0 + 64 * nblk of X -> bf16 rows at dst (row stride 64), and (F32) their
   // residuals at dst + lo
   auto emit = [&](bf16* dst, int64_t lo, int r0, int nblk) {
@@ -288,58 +292,82 @@ __global__ __launch_bounds__(256) void path_transport_kernel(int HQ, int H, int 
     }
   };
   // joint steps j = 0 .. nq-1 carry X through Hc_{A-1} .. Hc_cb (emitting QS), steps
-  // nq .. nq+sI-1 through HL_{sI-1} .. HL_0 (emitting QB).  The transition matrix of the
-  // next step is loaded into registers while a step computes, so no step waits for it.
+  // nq .. nq+sI-1 through HL_{sI-1} .. HL_0 (emitting QB).  Each step emits X, then
+  // multiplies it by the step's matrix; after the last emit X is not used, so the last step
+  // only emits.  The matrix of the next step is loaded into registers while a step computes,
+  // so no step waits for it.
   const int nq = A - cb, nsteps = nq + sI;
-  auto mat = [&](int j) {  // j = -1: Hc_A, B's own first step
-    return (j < nq) ? ws.hc + ((int64_t)bh * NT + (A - 1 - j)) * 4096
-                    : ws.hl + ((int64_t)bh * NS + (sI - 1 - (j - nq))) * 4096;
+  auto mat = [&](int j) {  // hi plane (lo plane 4096 elements on); j = -1: Hc_A, B's own first step
+    return (j < nq) ? ws.hcs + ((int64_t)bh * NT + (A - 1 - j)) * 8192
+                    : ws.hls + ((int64_t)bh * NS + (sI - 1 - (j - nq))) * 8192;
   };
   auto slot = [&](int j) {  // destination of the rows emitted before step j (row 0 = chunk A's first row)
     return ((j < nq) ? ws.qs + (((int64_t)bhq * PR + (A - 1 - j - cb)) * T) * 64
                      : ws.qb + (((int64_t)bhq * NS + (sI - 1 - (j - nq))) * T) * 64) +
            (int64_t)A * PC * 64;
   };
-  f32x4 mr[4];  // thread t holds M[r][c4 .. c4+3], r = (t + 256 u) / 16, c4 = 4 ((t + 256 u) % 16)
+  bf16x8 mr[4];  // thread t: plane u >> 1, 16-byte chunk q = t + 256 (u & 1) (row q >> 3, chunk q & 7)
   auto mload = [&](int j) {
-    const float* M = mat(j);
+    const bf16* M = mat(j);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) mr[u] = *reinterpret_cast<const f32x4*>(M + 4 * (tid + 256 * u));
+    for (int u = 0; u < 4; ++u) mr[u] = ld8(M + (u >> 1) * 4096 + 8 * (tid + 256 * (u & 1)));
   };
-  auto mstore_t = [&]() {  // MT[c][r] = M[r][c]
+  auto mstore = [&]() {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int idx = tid + 256 * u, r = idx >> 4, c4 = (idx & 15) * 4;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) MT[c4 + e][r] = mr[u][e];
+      const int q = tid + 256 * (u & 1);
+      *reinterpret_cast<bf16x8*>(Ms[u >> 1] + swz_off<8>(q >> 3, q & 7)) = mr[u];
     }
   };
   const int dt = w >> 1, rt = w & 1;  // this wave's output tiles: (dt, rt) of A and (dt, rt + 2) of B
-  if (hasB) {
-    // B's own first step: emit to QS slot A - cb, then X_B <- X_B Hc_A
-    mload(-1);
-    mstore_t();
-    __syncthreads();
-    emit(ws.qs + (((int64_t)bhq * PR + (A - cb)) * T) * 64 + (int64_t)A * PC * 64, ws.lo_qs, 64, 1);
-    if (nsteps > 0) mload(0);
-    const f32x16 o = mat_xM_tile(X, MT, dt, rt + 2);
-    __syncthreads();
+  // tile (dt, xr) of X M in D layout (m = column of the product, lane <-> row), 3-term split:
+  // A operand = M^T rows = columns dt*32 + lane of M, k slots in the transposing read's order
+  // (rows 16 st + jmap(slot)); B operand = the same k of X row xr*32 + lane
+  auto xm_tile = [&](int xr) {
+    f32x16 o = zero16();
 #pragma unroll
-    for (int e = 0; e < 16; ++e) X[(rt + 2) * 32 + l32][dt * 32 + drow(e, g)] = o[e];
-    if (nsteps > 0) mstore_t();
-    __syncthreads();
-  } else if (nsteps > 0) {
+    for (int st = 0; st < 4; ++st) {
+      const bf16x8 ah = lds_tr_a<8>(Ms[0], 16 * st, dt * 32);
+      const bf16x8 al = lds_tr_a<8>(Ms[1], 16 * st, dt * 32);
+      const f32x4 x0 = *reinterpret_cast<const f32x4*>(&X[xr * 32 + l32][16 * st + 4 * g]);
+      const f32x4 x1 = *reinterpret_cast<const f32x4*>(&X[xr * 32 + l32][16 * st + 8 + 4 * g]);
+      const float v[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+      bf16x8 bh8, bl;
+      split_vals(v, bh8, bl);
+      o = mfma32(ah, bh8, o);
+      o = mfma32(ah, bl, o);
+      o = mfma32(al, bh8, o);
+    }
+    return o;
+  };
+  if (hasB) {
+    // B's own first step: emit to QS slot A - cb, then X_B <- X_B Hc_A (if an emit follows)
+    emit(ws.qs + (((int64_t)bhq * PR + (A - cb)) * T) * 64 + (int64_t)A * PC * 64, ws.lo_qs, 64, 1);
+    if (nsteps > 0) {
+      mload(-1);
+      mstore();
+      __syncthreads();
+      if (nsteps > 1) mload(0);
+      const f32x16 o = xm_tile(rt + 2);
+      __syncthreads();
+#pragma unroll
+      for (int e = 0; e < 16; ++e) X[(rt + 2) * 32 + l32][dt * 32 + drow(e, g)] = o[e];
+      if (nsteps > 1) mstore();
+      __syncthreads();
+    }
+  } else if (nsteps > 1) {
     mload(0);
-    mstore_t();
+    mstore();
     __syncthreads();
   }
   const int nblk = hasB ? 2 : 1;
   for (int j = 0; j < nsteps; ++j) {
-    if (j + 1 < nsteps) mload(j + 1);
     emit(slot(j), (j < nq) ? ws.lo_qs : ws.lo_qb, 0, nblk);
-    const f32x16 o0 = mat_xM_tile(X, MT, dt, rt);
+    if (j + 1 == nsteps) break;
+    if (j + 2 < nsteps) mload(j + 1);
+    const f32x16 o0 = xm_tile(rt);
     f32x16 o1 = zero16();
-    if (hasB) o1 = mat_xM_tile(X, MT, dt, rt + 2);
+    if (hasB) o1 = xm_tile(rt + 2);
     __syncthreads();
 #pragma unroll
     for (int e = 0; e < 16; ++e) X[rt * 32 + l32][dt * 32 + drow(e, g)] = o0[e];
@@ -347,7 +375,7 @@ __global__ __launch_bounds__(256) void path_transport_kernel(int HQ, int H, int 
 #pragma unroll
       for (int e = 0; e < 16; ++e) X[(rt + 2) * 32 + l32][dt * 32 + drow(e, g)] = o1[e];
     }
-    if (j + 1 < nsteps) mstore_t();
+    if (j + 2 < nsteps) mstore();
     __syncthreads();
   }
 }
