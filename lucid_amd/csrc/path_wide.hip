@@ -259,7 +259,10 @@ __device__ __forceinline__ void load_mat128(float (*dst)[132], const float* __re
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void path_transport128_kernel(int HQ, int H, int T, PathFwdWs ws) {
   __shared__ __attribute__((aligned(16))) float X[128][132];  // rows 0..63 = chunk A, 64..127 = chunk B
-  __shared__ __attribute__((aligned(16))) float MT[128][132];
+  // the step's transition matrix M as bf16 hi and lo planes, row-major, swizzled (chunk c of
+  // row r at c ^ (r & 7)); its columns (the A operand of D^T = M^T X^T) come through
+  // transposing reads
+  __shared__ __attribute__((aligned(16))) bf16 Ms[2][WK * WK];
   const int p = (int)gridDim.y - 1 - (int)blockIdx.y, bhq = blockIdx.x;
   const int NT = T / PC, NS = (NT + PR - 1) / PR;
   const int G = HQ / H;
@@ -275,6 +278,7 @@ __global__ __launch_bounds__(256) void path_transport128_kernel(int HQ, int H, i
       *reinterpret_cast<f32x4*>(&X[r][c4]) = *reinterpret_cast<const f32x4*>(src + (int64_t)r * WK + c4);
     }
   }
+  __syncthreads();
   auto emit = [&](bf16* dst, int r0, int nblk) {  // rows r0 .. r0 + 64 nblk of X -> bf16 rows (stride 128)
     for (int idx = tid; idx < 64 * nblk * 16; idx += 256) {
       const int r = r0 + (idx >> 4), c8 = (idx & 15) * 8;
@@ -284,22 +288,59 @@ __global__ __launch_bounds__(256) void path_transport128_kernel(int HQ, int H, i
       *reinterpret_cast<bf16x8*>(dst + (int64_t)r * WK + c8) = v;
     }
   };
+  // Each step emits X, then multiplies it by the step's matrix; after the last emit X is not
+  // used, so the last step only emits.  The next step's matrix is loaded into registers while
+  // a step computes.
   const int nq = A - cb, nsteps = nq + sI;
-  auto mat = [&](int j) {  // j = -1: Hc_A, B's own first step
-    return (j < nq) ? ws.hc + ((int64_t)bh * NT + (A - 1 - j)) * (WK * WK)
-                    : ws.hl + ((int64_t)bh * NS + (sI - 1 - (j - nq))) * (WK * WK);
+  auto mat = [&](int j) {  // hi plane (lo plane WK * WK elements on); j = -1: Hc_A, B's own first step
+    return (j < nq) ? ws.hcs + ((int64_t)bh * NT + (A - 1 - j)) * (2 * WK * WK)
+                    : ws.hls + ((int64_t)bh * NS + (sI - 1 - (j - nq))) * (2 * WK * WK);
   };
   auto slot = [&](int j) {  // destination of the rows emitted before step j (row 0 = chunk A's first row)
     return ((j < nq) ? ws.qs + (((int64_t)bhq * PR + (A - 1 - j - cb)) * T) * WK
                      : ws.qb + (((int64_t)bhq * NS + (sI - 1 - (j - nq))) * T) * WK) +
            (int64_t)A * PC * WK;
   };
-  // rows [rt0, rt0 + 32 nrt) of X <- X M (every wave: value tile w)
-  auto step = [&](int rt0, int nrt) {
+  bf16x8 mr[16];  // thread t: plane u >> 3, 16-byte chunk q = t + 256 (u & 7) (row q >> 4, chunk q & 15)
+  auto mload = [&](int j) {
+    const bf16* M = mat(j);
+#pragma unroll
+    for (int u = 0; u < 16; ++u) mr[u] = ld8(M + (u >> 3) * (WK * WK) + 8 * (tid + 256 * (u & 7)));
+  };
+  auto mstore = [&]() {
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int q = tid + 256 * (u & 7);
+      *reinterpret_cast<bf16x8*>(Ms[u >> 3] + swz_off<16>(q >> 4, q & 15)) = mr[u];
+    }
+  };
+  // tile (value tile w, row tile xr) of X M in D layout (m = column of the product, lane <->
+  // row), 3-term split: A operand = columns w*32 + lane of M, k slots in the transposing
+  // read's order (rows 16 st + jmap(slot)); B operand = the same k of X row xr*32 + lane
+  auto xm_tile = [&](int xr) {
+    f32x16 o = zero16();
+#pragma unroll
+    for (int st = 0; st < 8; ++st) {
+      const bf16x8 ah = lds_tr_a<16>(Ms[0], 16 * st, w * 32);
+      const bf16x8 al = lds_tr_a<16>(Ms[1], 16 * st, w * 32);
+      const f32x4 x0 = *reinterpret_cast<const f32x4*>(&X[xr * 32 + l32][16 * st + 4 * g]);
+      const f32x4 x1 = *reinterpret_cast<const f32x4*>(&X[xr * 32 + l32][16 * st + 8 + 4 * g]);
+      const float v[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+      bf16x8 bh8, bl;
+      split_vals(v, bh8, bl);
+      o = mfma32(ah, bh8, o);
+      o = mfma32(ah, bl, o);
+      o = mfma32(al, bh8, o);
+    }
+    return o;
+  };
+  // rows [rt0, rt0 + 32 nrt) of X <- X M (every wave: value tile w); next: store the
+  // prefetched matrix of the next step once every wave has read this one
+  auto step = [&](int rt0, int nrt, bool next) {
     f32x16 o[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      if (i < nrt) o[i] = mat_xM128_tile(X, MT, w, rt0 + i);
+      if (i < nrt) o[i] = xm_tile(rt0 + i);
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -307,21 +348,31 @@ __global__ __launch_bounds__(256) void path_transport128_kernel(int HQ, int H, i
 #pragma unroll
         for (int e = 0; e < 16; ++e) X[(rt0 + i) * 32 + l32][w * 32 + drow(e, g)] = o[i][e];
       }
+    if (next) mstore();
     __syncthreads();
   };
-  if (hasB) {  // B's own first step: emit to QS slot A - cb, then X_B <- X_B Hc_A
-    load_mat128<true>(MT, mat(-1));
-    __syncthreads();
+  if (hasB) {  // B's own first step: emit to QS slot A - cb, then X_B <- X_B Hc_A (if an emit follows)
     emit(ws.qs + (((int64_t)bhq * PR + (A - cb)) * T) * WK + (int64_t)A * PC * WK, 64, 1);
-    step(2, 2);
+    if (nsteps > 0) {
+      mload(-1);
+      mstore();
+      __syncthreads();
+      if (nsteps > 1) mload(0);
+      step(2, 2, nsteps > 1);
+    }
+  } else if (nsteps > 1) {
+    mload(0);
+    mstore();
+    __syncthreads();
   }
   const int nblk = hasB ? 2 : 1;
 #pragma unroll 1
   for (int j = 0; j < nsteps; ++j) {
-    load_mat128<true>(MT, mat(j));
     emit(slot(j), 0, nblk);
-    __syncthreads();
-    step(0, 2 * nblk);
+    if (j + 1 == nsteps) break;
+    const bool next = j + 2 < nsteps;
+    if (next) mload(j + 1);
+    step(0, 2 * nblk, next);
   }
 }
 
