@@ -9,7 +9,10 @@ with the inputs already resident in HBM.
 Reported: tokens/s (whole job), TFLOP/s by the frozen algorithmic count
 7*T^2*d*B*(Hq+Hkv) (causal halves, 1 FMA = 2 flop; exp, RMSNorm and the
 diagonal-block inverses excluded), the roofline of the dominant kernel timed
-with HIP events on its launch stream inside the timed region, plain causal
+with HIP events on its launch stream inside the timed region (events around that
+kernel only; the per-kernel breakdown "kernels" comes from K untimed steps before
+it with events around every launch, which would otherwise add two event records
+per launch to the timed steps), plain causal
 attention at the same shape as a comparator (this build's own attention kernels
 with V' = V, and torch SDPA; the ratio is taken against the faster), and a CPU
 baseline (the float32 torch restatement of the reference's dense path, one head
@@ -53,6 +56,61 @@ KERNEL_FLOPS = {
     "lucid_precond_bwd_col_wide_kernel": lambda B, Hq, Hkv, T, D: 4.0 * T * T * D * B * Hkv,  # the same, 256 columns/WG
     "lucid_precond_bwd_row_kernel": lambda B, Hq, Hkv, T, D: 1.0 * T * T * D * B * Hkv,  # M K^
 }
+
+
+def warm_up(step, warmup):
+    """Untimed warmup: exactly `warmup` steps when given; by default at least 3 steps and at
+    least 0.5 s of GPU work (the clocks of an idle GPU take that long to come up: a 2 ms step
+    timed after three warmup steps reads ~2 % slow).  Returns the number of steps run."""
+    import torch
+    if warmup is not None:
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        return warmup
+    n, t0 = 0, time.perf_counter()
+    while n < 3 or time.perf_counter() - t0 < 0.5:
+        step()
+        torch.cuda.synchronize()
+        n += 1
+    return n
+
+
+def profiled_timing(lib, prefix, step, steps, dom=None):
+    """Per-kernel breakdown and the timed region, kept apart so that the events do not slow the
+    step they time: K untimed steps with every launch bracketed by HIP events (the breakdown;
+    the dominant kernel = the largest total unless `dom` names it), then the timed region of
+    K steps (barrier + synchronize on both sides) with events around the dominant kernel's
+    launches only (one pair per launch, on its own stream).  Returns (ms per step, breakdown
+    totals {name: (total_ms, launches)}, dominant kernel, its average ms in the timed region)."""
+    import torch
+
+    from lucid_amd import _lib
+    getattr(lib, prefix + "profile_reset")()
+    getattr(lib, prefix + "profile_only")(None)
+    getattr(lib, prefix + "profile_enable")(1)
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    getattr(lib, prefix + "profile_enable")(0)
+    totals = _lib.profile_totals(lib, prefix)
+    if dom is None:
+        dom = max(totals.items(), key=lambda kv: kv[1][0])[0]
+    getattr(lib, prefix + "profile_reset")()
+    getattr(lib, prefix + "profile_only")(dom.encode())
+    getattr(lib, prefix + "profile_enable")(1)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / steps * 1e3
+    getattr(lib, prefix + "profile_enable")(0)
+    getattr(lib, prefix + "profile_only")(None)
+    timed = _lib.profile_totals(lib, prefix)
+    getattr(lib, prefix + "profile_reset")()
+    tot, cnt = timed[dom]
+    return ms, totals, dom, tot / cnt
 
 
 def _cpu_info():
@@ -216,23 +274,10 @@ def bench_decode(args, dev):
     def step():  # every step decodes rows T .. T+L-1 against rows [0, T) (same work each time)
         lucid_decode(q, k, v, kc, vc, T)
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    lib.lucid_profile_reset()
-    lib.lucid_profile_enable(1)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    ms = (time.perf_counter() - t0) / args.steps * 1e3
-    lib.lucid_profile_enable(0)
-    totals = _lib.profile_totals(lib, "lucid_")
+    args.warmup = warm_up(step, args.warmup)
+    ms, totals, dom, dom_avg = profiled_timing(lib, "lucid_", step, args.steps, "lucid_decode_split_kernel")
     kernels = {n: {"avg_ms": round(tot / cnt, 4), "launches": cnt} for n, (tot, cnt) in
                sorted(totals.items(), key=lambda kv: -kv[1][0])}
-    dom = "lucid_decode_split_kernel"
-    dom_avg = totals[dom][0] / totals[dom][1]
     nbytes = 2.0 * B * Hkv * T * D * 2  # K and V' caches, bf16, read once per split pass
     achieved = nbytes / (dom_avg / 1e3) / 1e9
     traffic = measured_traffic("decode", dom) if L == 1 else None
@@ -286,24 +331,11 @@ def bench_c3(args, dev):
         return loss
 
     first = step().item()
-    for _ in range(max(0, args.warmup - 1)):
-        step()
-    torch.cuda.synchronize()
-    lib.lucid_profile_reset()
-    lib.lucid_profile_enable(1)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        losses.append(step())
-    torch.cuda.synchronize()
-    ms = (time.perf_counter() - t0) / args.steps * 1e3
-    lib.lucid_profile_enable(0)
-    totals = _lib.profile_totals(lib, "lucid_")
+    args.warmup = 1 + warm_up(step, None if args.warmup is None else max(0, args.warmup - 1))
+    ms, totals, dom, dom_avg = profiled_timing(lib, "lucid_", lambda: losses.append(step()), args.steps)
     attn_ms = sum(tot for tot, _ in totals.values()) / args.steps
     kernels = {n: {"avg_ms": round(tot / cnt, 4), "launches": cnt} for n, (tot, cnt) in
                sorted(totals.items(), key=lambda kv: -kv[1][0])}
-    dom = max(totals.items(), key=lambda kv: kv[1][0])[0]
-    dom_avg = totals[dom][0] / totals[dom][1]
     H, D = cfg.num_attention_heads, cfg.head_dim
     achieved = KERNEL_FLOPS[dom](B, H, H, T, D) / (dom_avg / 1e3) / 1e12
     n_params = M.count_parameters(model)
@@ -366,7 +398,8 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=None,
+                    help="untimed warmup steps (default: at least 3 steps and 0.5 s of GPU work)")
     ap.add_argument("--workload", default="lucid",
                     choices=["lucid", "c2", "c3", "c5", "gqa128", "path", "path128", "path_f32", "path_softmax",
                              "decode"],
@@ -471,20 +504,8 @@ def main():
         if wl != "lucid":
             metric = f"LUCID attention {'forward' if fwd_only else 'fwd+bwd'} tokens/s & TFLOP/s ({wl})"
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    getattr(lib, prefix + "profile_reset")()
-    getattr(lib, prefix + "profile_enable")(1)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    getattr(lib, prefix + "profile_enable")(0)
-    totals = _lib.profile_totals(lib, prefix)
-    ms = (t1 - t0) / args.steps * 1e3
+    args.warmup = warm_up(step, args.warmup)
+    ms, totals, dom, dom_avg = profiled_timing(lib, prefix, step, args.steps)
     tokens_s = B * T / (ms / 1e3)
 
     kernels = {}
@@ -493,8 +514,6 @@ def main():
         kf = kflops.get(name, 0.0)
         kernels[name] = {"avg_ms": round(avg, 4), "launches": cnt,
                          "tflops": round(kf / (avg / 1e3) / 1e12, 1) if kf else None}
-    dom = max(totals.items(), key=lambda kv: kv[1][0])[0]
-    dom_avg = totals[dom][0] / totals[dom][1]
     achieved = kflops.get(dom, 0.0) / (dom_avg / 1e3) / 1e12
     traffic = measured_traffic(wl, dom)
 

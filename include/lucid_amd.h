@@ -304,8 +304,11 @@ int lucid_decode_noalloc(const void* q, const int64_t* q_strides, const void* k,
  * lucid_profile_collect() waits for the recorded events, folds them into
  * per-kernel totals and returns the number of distinct kernels;
  * lucid_profile_entry(i, ...) reads total milliseconds and launch count of
- * kernel i; lucid_profile_reset() clears the totals.  Not thread safe. */
+ * kernel i; lucid_profile_reset() clears the totals.  lucid_profile_only(name) times only
+ * the launches of the named kernel (null or "": every kernel), so that a timed region
+ * carries one kernel's events instead of two per launch.  Not thread safe. */
 void lucid_profile_enable(int on);
+void lucid_profile_only(const char* name);
 int lucid_profile_collect(void);
 int lucid_profile_entry(int idx, char* name, int name_len, double* total_ms, long* count);
 void lucid_profile_reset(void);

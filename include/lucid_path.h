@@ -148,6 +148,7 @@ int lucid_path_softmax_bwd_f32(const float* dout, const int64_t* do_strides, con
 /* Per-kernel timing with HIP events (no counterpart in the reference; used by
  * bench.py), same contract as lucid_profile_* in lucid_amd.h. */
 void lucid_path_profile_enable(int on);
+void lucid_path_profile_only(const char* name);
 int lucid_path_profile_collect(void);
 int lucid_path_profile_entry(int idx, char* name, int name_len, double* total_ms, long* count);
 void lucid_path_profile_reset(void);

@@ -88,6 +88,7 @@ _SIGS = {
         "lucid_profile_entry": ([_int, ctypes.c_char_p, _int, ctypes.POINTER(ctypes.c_double),
                                  ctypes.POINTER(ctypes.c_long)], _int),
         "lucid_profile_reset": ([], None),
+        "lucid_profile_only": ([ctypes.c_char_p], None),
     },
     "liblucid_path.so": {
         "lucid_path_abi_version": ([], _int),
@@ -127,6 +128,7 @@ _SIGS = {
         "lucid_path_profile_entry": ([_int, ctypes.c_char_p, _int, ctypes.POINTER(ctypes.c_double),
                                       ctypes.POINTER(ctypes.c_long)], _int),
         "lucid_path_profile_reset": ([], None),
+        "lucid_path_profile_only": ([ctypes.c_char_p], None),
     },
 }
 

@@ -1281,6 +1281,8 @@ int lucid_precond_bwd(const void* k, const int64_t* k_strides, const void* dvpri
 
 void lucid_profile_enable(int on) { lucid_prof::enabled() = on != 0; }
 
+void lucid_profile_only(const char* name) { lucid_prof::only() = name ? name : ""; }
+
 int lucid_profile_collect(void) { return lucid_prof::collect(); }
 
 int lucid_profile_entry(int idx, char* name, int name_len, double* total_ms, long* count) {

@@ -575,6 +575,8 @@ int lucid_path_softmax_bwd_f32(const float* dout, const int64_t* do_strides, con
 
 void lucid_path_profile_enable(int on) { lucid_prof::enabled() = on != 0; }
 
+void lucid_path_profile_only(const char* name) { lucid_prof::only() = name ? name : ""; }
+
 int lucid_path_profile_collect(void) { return lucid_prof::collect(); }
 
 int lucid_path_profile_entry(int idx, char* name, int name_len, double* total_ms, long* count) {

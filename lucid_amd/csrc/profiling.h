@@ -21,6 +21,13 @@ inline bool& enabled() {
   static bool on = false;
   return on;
 }
+// Optional filter: when not empty, only launches of the kernel with this name are timed
+// (so that a timed region carries the events of one kernel, not two per launch).
+inline std::string& only() {
+  static std::string s;
+  return s;
+}
+inline bool wanted(const char* name) { return enabled() && (only().empty() || only() == name); }
 inline std::vector<Rec>& records() {
   static std::vector<Rec> r;
   return r;
@@ -86,7 +93,7 @@ inline void reset() {
 #define LUCID_TIMED_LAUNCH_B(STATUS_FN, NAME, KERNEL, GRID, BLOCK, ST, ...)\
   do {                                                                     \
     hipEvent_t ev_a = nullptr, ev_b = nullptr;                             \
-    if (lucid_prof::enabled()) {                                           \
+    if (lucid_prof::wanted(NAME)) {                                        \
       ev_a = lucid_prof::pool_event();                                     \
       ev_b = lucid_prof::pool_event();                                     \
       if (!ev_a || !ev_b || hipEventRecord(ev_a, ST) != hipSuccess)        \
