@@ -176,10 +176,15 @@ class LucidAttentionFunction(torch.autograd.Function):
         ctx.save_for_backward(qp, kp, o, lse, ws)
         ctx.scale, ctx.eps, ctx.t, ctx.dn = scale, eps, t, dn
         ctx.mark_non_differentiable(vprime)
+        # no zero-filled gradient for the V' output, which the backward ignores (a T x d fp32
+        # fill per call otherwise)
+        ctx.set_materialize_grads(False)
         return o[:, :t], vprime[:, :, :t]
 
     @staticmethod
     def backward(ctx, do, _dvprime):
+        if do is None:  # O took no part in the loss (gradients are not materialised)
+            return None, None, None, None, None, None
         if ctx.empty:
             return (do.new_zeros(ctx.shapes[0]), do.new_zeros(ctx.shapes[1]), do.new_zeros(ctx.shapes[1]),
                     None, None, None)
