@@ -206,11 +206,9 @@ int launch_precond_fwd(const void* k, const int64_t* ks, const void* v, const in
   LUCID_LAUNCH("lucid_prep_kernel", lucid::lucid_prep_kernel<D>, dim3(T / 64, BH), st, (const bf16*)k, S(ks), Hkv,
                T, eps, dn, scale, w.rinv, w.kt, w.pinv, w.counters, w.mass, mass_init, lucid::Lo{}, nullptr,
                w.khat);
-  if (g_precision == LUCID_PRECISION_AUTO)
-    LUCID_LAUNCH("lucid_mass_kernel", lucid::lucid_mass_kernel<D>, dim3(T / 64, BH), st, (const bf16*)k, S(ks),
-                 Hkv, T, w.rinv, scale, w.mass);
+  // the in-block coupling of every 128-row chain block and (AUTO) the heads' row masses
   LUCID_LAUNCH("lucid_zx_kernel", lucid::lucid_zx_kernel<D>, dim3(T / 128, BH), st, (const bf16*)k, S(ks), Hkv, T,
-               w.rinv, scale, w.pinv, w.zx, lucid::Lo{});
+               w.rinv, scale, w.pinv, w.zx, lucid::Lo{}, g_precision == LUCID_PRECISION_AUTO ? w.mass : nullptr);
   // both instances of the chain: each solves the heads of its precision and returns at
   // once for the others
   if (g_precision != LUCID_PRECISION_EXACT) {
@@ -265,11 +263,8 @@ int launch_fwd(const void* q, const int64_t* qs, const void* k, const int64_t* k
       LUCID_LAUNCH("lucid_prep_kernel", lucid::lucid_prep_kernel<D>, dim3(T / 64, BH), st, (const bf16*)k, S(ks),
                    Hkv, T, eps, dn, scale, w.rinv, w.kt, w.pinv, w.counters, w.mass, mass_init, lucid::Lo{}, nullptr,
                    w.khat);
-      if (g_precision == LUCID_PRECISION_AUTO)
-        LUCID_LAUNCH("lucid_mass_kernel", lucid::lucid_mass_kernel<D>, dim3(T / 64, BH), st, (const bf16*)k, S(ks),
-                     Hkv, T, w.rinv, scale, w.mass);
       LUCID_LAUNCH("lucid_zx_kernel", lucid::lucid_zx_kernel<D>, dim3(T / 128, BH), st, (const bf16*)k, S(ks), Hkv,
-                   T, w.rinv, scale, w.pinv, w.zx, lucid::Lo{});
+                   T, w.rinv, scale, w.pinv, w.zx, lucid::Lo{}, g_precision == LUCID_PRECISION_AUTO ? w.mass : nullptr);
       if (g_precision != LUCID_PRECISION_EXACT)
         LUCID_LAUNCH("lucid_fused_fwd_kernel", lucid::lucid_fused_fwd_kernel<D>, dim3((T / 128) * BH), st,
                      (const bf16*)q, S(qs), (const bf16*)k, S(ks), (const bf16*)v, S(vs), Hkv, T, BH, w.rinv, scale,

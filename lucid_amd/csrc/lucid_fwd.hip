@@ -8,7 +8,8 @@
 // Kernels (all 256 threads = 4 waves, MFMA 32x32x16 bf16, fp32 accumulate):
 //   lucid_prep_kernel        per-row 1/rms of K, K^ rows in bf16, K^T in T-perm layout,
 //                            inverses of the 64x64 diagonal blocks of P, zero chain counters
-//   lucid_zx_kernel          the in-block coupling -X_B P_BA of every 128-row chain block
+//   lucid_zx_kernel          the in-block coupling -X_B P_BA of every 128-row chain block and
+//                            (precision "auto") the heads' row masses, lucid_mass_kernel's work
 //   lucid_precond_fwd_kernel chained solve, one workgroup per (128-row block, kv head);
 //                            it waits on a per-head progress counter for V'_j, j < i and
 //                            sweeps the earlier keys 128 at a time
@@ -316,17 +317,18 @@ __global__ __launch_bounds__(256) void lucid_rows_in_kernel(const IT* __restrict
 //   P = exp(s r_i r_j S - 1/s),
 // so that a row's sum is taken inside its lanes (16 values, then the two lane halves).
 // The block's largest row total goes to mass[bh] by an integer max of the (non-negative)
-// float bits.  grid (T/64, B*Hkv), after lucid_prep_kernel (1/rms, mass[bh] = 0).
+// float bits.  After lucid_prep_kernel (1/rms, mass[bh] = 0); run per 64-row block by the
+// 256 threads of a workgroup (lucid_mass_kernel: grid (T/64, B*Hkv); lucid_zx_kernel runs
+// it for the two blocks of its 128 rows when given `mass`).
 // ---------------------------------------------------------------------------
 template <int D>
-__global__ __launch_bounds__(256) void lucid_mass_kernel(const bf16* __restrict__ k, Strides ks, int Hkv, int T,
-                                                         const float* __restrict__ rinv, float scale,
-                                                         float* __restrict__ mass) {
+__device__ __forceinline__ void row_mass_block(const bf16* __restrict__ k, Strides ks, int Hkv, int T,
+                                               const float* __restrict__ rinv, float scale, float* __restrict__ mass,
+                                               int blk, int bh) {
   constexpr int NKS = D / 16;
   __shared__ float part[4][64];
   __shared__ float kr[4][32];  // 1/rms of each wave's current 32 keys
   __shared__ float kw[4][32];  // their weights
-  const int blk = blockIdx.x, bh = blockIdx.y;
   const int b = bh / Hkv, h = bh - b * Hkv;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
@@ -393,6 +395,13 @@ __global__ __launch_bounds__(256) void lucid_mass_kernel(const bf16* __restrict_
   }
 }
 
+template <int D>
+__global__ __launch_bounds__(256) void lucid_mass_kernel(const bf16* __restrict__ k, Strides ks, int Hkv, int T,
+                                                         const float* __restrict__ rinv, float scale,
+                                                         float* __restrict__ mass) {
+  row_mass_block<D>(k, ks, Hkv, T, rinv, scale, mass, blockIdx.x, blockIdx.y);
+}
+
 // ---------------------------------------------------------------------------
 // zx = -(X_B P_BA) for every 128-row chain block (A = its first 64 rows, B = the
 // last 64; X_B = the inverse of P's diagonal block B from lucid_prep_kernel,
@@ -404,7 +413,8 @@ __global__ __launch_bounds__(256) void lucid_mass_kernel(const bf16* __restrict_
 template <int D, bool F32 = false>
 __global__ __launch_bounds__(256) void lucid_zx_kernel(const bf16* __restrict__ k, Strides ks, int Hkv, int T,
                                                        const float* __restrict__ rinv, float scale,
-                                                       const float* __restrict__ pinv, float* __restrict__ zx, Lo lo) {
+                                                       const float* __restrict__ pinv, float* __restrict__ zx, Lo lo,
+                                                       float* __restrict__ mass = nullptr) {
   constexpr int NKS = D / 16;
   __shared__ __attribute__((aligned(16))) float Xb[64][68];
   __shared__ __attribute__((aligned(16))) float PT[64][68];  // PT[c][m] = P_BA[m][c]
@@ -459,6 +469,13 @@ __global__ __launch_bounds__(256) void lucid_zx_kernel(const bf16* __restrict__ 
   float* zo = zx + ((int64_t)bh * (T / 128) + blk) * 4096 + slot;
 #pragma unroll
   for (int e = 0; e < 16; ++e) zo[(tm * 32 + drow(e, g)) * 64] = -z[e];
+  if constexpr (!F32) {
+    if (mass) {  // the row masses of the two 64-row blocks (one launch less than lucid_mass_kernel)
+      row_mass_block<D>(k, ks, Hkv, T, rinv, scale, mass, 2 * blk, bh);
+      __syncthreads();
+      row_mass_block<D>(k, ks, Hkv, T, rinv, scale, mass, 2 * blk + 1, bh);
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
