@@ -56,6 +56,11 @@ KERNEL_FLOPS = {
     "lucid_precond_bwd_col_wide_kernel": lambda B, Hq, Hkv, T, D: 4.0 * T * T * D * B * Hkv,  # the same, 256 columns/WG
     "lucid_precond_bwd_row_kernel": lambda B, Hq, Hkv, T, D: 1.0 * T * T * D * B * Hkv,  # M K^
 }
+# fp32 inputs: the same algorithmic counts (at the caller's head dim; the kernels run on rows
+# padded to 64 or 128 and take every product as three or four bf16 MFMAs)
+for _n in ("lucid_precond_fwd", "lucid_attn_fwd", "lucid_attn_bwd_dkdv", "lucid_attn_bwd_dq", "lucid_precond_bwd_col",
+           "lucid_precond_bwd_row"):
+    KERNEL_FLOPS[_n + "_f32_kernel"] = KERNEL_FLOPS[_n + "_kernel"]
 
 
 def warm_up(step, warmup):
@@ -178,18 +183,19 @@ def cpu_baseline(T=32768, H_full=16, D=64):
     }
 
 
-def _bench_inputs(B, Hq, Hkv, T, D, dev, grad=True, keys="iid"):
+def _bench_inputs(B, Hq, Hkv, T, D, dev, grad=True, keys="iid", dtype=None):
     import torch
+    dt = dtype or torch.bfloat16
     g = torch.Generator().manual_seed(0)
-    mk = lambda *shape: (torch.randn(*shape, generator=g) / D ** 0.5).to(torch.bfloat16).to(dev)  # noqa: E731
+    mk = lambda *shape: (torch.randn(*shape, generator=g) / D ** 0.5).to(dt).to(dev)  # noqa: E731
     q, k, v = mk(B, Hq, T, D), mk(B, Hkv, T, D), mk(B, Hkv, T, D)
     if keys == "correlated":  # a shared direction per head + 0.1 N(0,1) noise
         base = torch.randn(B, Hkv, 1, D, generator=g)
-        k = ((base + 0.1 * torch.randn(B, Hkv, T, D, generator=g)) / D ** 0.5).to(torch.bfloat16).to(dev)
+        k = ((base + 0.1 * torch.randn(B, Hkv, T, D, generator=g)) / D ** 0.5).to(dt).to(dev)
     if grad:
         for x in (q, k, v):
             x.requires_grad_()
-    do = torch.randn(B, T, Hq, D, generator=g).to(torch.bfloat16).to(dev)
+    do = torch.randn(B, T, Hq, D, generator=g).to(dt).to(dev)
     return q, k, v, do
 
 
@@ -401,12 +407,13 @@ def main():
     ap.add_argument("--warmup", type=int, default=None,
                     help="untimed warmup steps (default: at least 3 steps and 0.5 s of GPU work)")
     ap.add_argument("--workload", default="lucid",
-                    choices=["lucid", "c2", "c3", "c5", "gqa128", "path", "path128", "path_f32", "path_softmax",
-                             "decode"],
+                    choices=["lucid", "c2", "c3", "c5", "gqa128", "ref_f32", "path", "path128", "path_f32",
+                             "path_softmax", "decode"],
                     help="lucid: north star B1 H16 T32768 d64 fwd+bwd (default); c2: B4 H16 T4096 d64 "
                          "fwd+bwd; c3: 16-layer Llama-LUCID decoder, one training step (fwd+bwd+AdamW) "
                          "on B1 x T8192; c5: B1 T131072 Hq32/Hkv8 d128 forward only; gqa128: the config-5 heads "
-                         "(Hq32/Hkv8 d128) at B1 T32768, fwd+bwd; path: LUCID-Path "
+                         "(Hq32/Hkv8 d128) at B1 T32768, fwd+bwd; ref_f32: the attention layer of the reference's shipped "
+                         "LUCID model config (fp32, head dim 68, 32 query / 4 kv heads) at B8 T2048, fwd+bwd; path: LUCID-Path "
                          "B1 H16 T32768 d64 fwd+bwd; path128: the same at head dim 128; path_f32: config 4 on fp32 "
                          "inputs; path_softmax: PaTH softmax attention on the config-4 "
                          "shape, fwd+bwd; decode: one decoding step against a 128K cache (config-5 heads)")
@@ -480,8 +487,10 @@ def main():
                                   "(config-4 shape)"}[wl]
     else:
         B, Hq, Hkv, T, D = {"lucid": (1, 16, 16, 32768, 64), "c2": (4, 16, 16, 4096, 64),
-                            "c5": (1, 32, 8, 131072, 128), "gqa128": (1, 32, 8, 32768, 128)}[wl]
-        q, k, v, do = _bench_inputs(B, Hq, Hkv, T, D, dev, grad=not fwd_only, keys=args.keys)
+                            "c5": (1, 32, 8, 131072, 128), "gqa128": (1, 32, 8, 32768, 128),
+                            "ref_f32": (8, 32, 4, 2048, 68)}[wl]
+        q, k, v, do = _bench_inputs(B, Hq, Hkv, T, D, dev, grad=not fwd_only, keys=args.keys,
+                                    dtype=torch.float32 if wl == "ref_f32" else None)
         lib, prefix = _lib.load(), "lucid_"
 
         def step():
@@ -577,12 +586,13 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32" if wl == "path_f32" else "bf16",
+        "dtype": "f32" if wl in ("path_f32", "ref_f32") else "bf16",
         "data": "synthetic (seeded N(0,1)/sqrt(d) q,k,v; N(0,1) dO)" if not path_kind
                 else "synthetic (seeded N(0,1) q,k,v,w; w L2-normalised; beta=2 sigmoid(N(0,1)); N(0,1) dO)",
         "precision": args.precision, "keys": args.keys, "fused_forward": not args.no_fused_fwd,
         "config": {"workload": {"lucid": "lucid_attention_fwd_bwd", "c2": "lucid_attention_fwd_bwd",
                                 "c5": "lucid_attention_fwd", "gqa128": "lucid_attention_fwd_bwd",
+                                "ref_f32": "lucid_attention_fwd_bwd",
                                 "path": "lucid_path_fwd_bwd", "path128": "lucid_path_fwd_bwd",
                                 "path_f32": "lucid_path_fwd_bwd",
                                 "path_softmax": "path_softmax_attention_fwd_bwd"}[wl],

@@ -332,8 +332,10 @@ struct DqSmemF32 {  // fp32 inputs: the lo tiles of K and V' beside the hi tiles
   bf16 vl[NB][64 * D];
 };
 
-template <int D, bool EXACT, bool F32 = false, int RW = 64>
-__global__ __launch_bounds__(16384 / RW) LUCID_TWO_WAVES_IF((D == 64 || RW == 32) && !EXACT) void lucid_attn_bwd_dq_kernel(
+// WGR: rows per workgroup (256; 128 for the fp32 instance at head dim 128, whose hi/lo
+// operands need one wave per SIMD to stay in registers)
+template <int D, bool EXACT, bool F32 = false, int RW = 64, int WGR = 256>
+__global__ __launch_bounds__(64 * (WGR / RW)) LUCID_TWO_WAVES_IF((D == 64 || RW == 32) && !EXACT) void lucid_attn_bwd_dq_kernel(
     const bf16* __restrict__ q, Strides qs, const bf16* __restrict__ k, Strides ks, const bf16* __restrict__ vpb,
     const bf16* __restrict__ dout, Strides dos, const float* __restrict__ lse,
     const float* __restrict__ delta, const float* __restrict__ mass,
@@ -344,10 +346,10 @@ __global__ __launch_bounds__(16384 / RW) LUCID_TWO_WAVES_IF((D == 64 || RW == 32
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
   constexpr int NT = RW / 32;           // 32-row n-tiles per wave
-  constexpr int NTHR = 64 * (256 / RW);  // 256 rows per workgroup
+  constexpr int NTHR = 64 * (WGR / RW);  // WGR rows per workgroup
   __shared__ __attribute__((aligned(16))) std::conditional_t<F32, DqSmemF32<D>, DqSmem<D>> sm;
   constexpr int NB = stage_bufs(D, F32);
-  const int nblk = (T + 255) / 256;
+  const int nblk = (T + WGR - 1) / WGR;
   const int id = blockIdx.x;
   const int bhq = id % BHq;
   const int ib = nblk - 1 - id / BHq;
@@ -357,7 +359,7 @@ __global__ __launch_bounds__(16384 / RW) LUCID_TWO_WAVES_IF((D == 64 || RW == 32
   if ((mass[bh] > kExactMass) != EXACT) return;  // the other instance handles this head
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
-  const int r0 = ib * 256;
+  const int r0 = ib * WGR;
   const int row0 = r0 + w * RW;
   const bf16* kh = k + b * ks.b + h * ks.h;
   const bf16* vh = vpb + (int64_t)bh * T * D;
@@ -385,7 +387,7 @@ __global__ __launch_bounds__(16384 / RW) LUCID_TWO_WAVES_IF((D == 64 || RW == 32
   for (int t = 0; t < NDT; ++t)
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) acc[t][nt] = zero16();
-  const int ntile = (min(r0 + 256, T) + 63) / 64;
+  const int ntile = (min(r0 + WGR, T) + 63) / 64;
   const int last_w = row0 / 64;
   const int roff = row0 - last_w * 64;  // this wave's first row within its diagonal tile
   // newest vector-memory ops of a step, per wave
@@ -1343,7 +1345,9 @@ struct ProwSmem<D, true, F32> {
   float r[NB][64];
 };
 
-template <int D, bool EXACT, bool F32 = false>
+// NT: 32-row n-tiles per wave (2: 256 rows per workgroup; 1: 128 rows, for the fp32 instance
+// at head dim 128, whose hi/lo row operands of two n-tiles do not fit the registers)
+template <int D, bool EXACT, bool F32 = false, int NT = 2>
 __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void lucid_precond_bwd_row_kernel(
     const bf16* __restrict__ k, Strides ks, int Hkv, int T, int BH, const float* __restrict__ rinv,
     const bf16* __restrict__ khat, float scale, float dn, const bf16* __restrict__ vpb,
@@ -1355,14 +1359,15 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
   constexpr int NKS = D / 16;
   __shared__ __attribute__((aligned(16))) ProwSmem<D, EXACT, F32> sm;
   constexpr int NB = stage_bufs(D, F32);
-  const int nblk = (T + 255) / 256;
+  constexpr int WGR = 128 * NT;  // rows per workgroup
+  const int nblk = (T + WGR - 1) / WGR;
   const int id = blockIdx.x;
   const int ib = nblk - 1 - id / BH, bh = id - (id / BH) * BH;  // heavy (late) blocks first
   if ((mass[bh] > kExactMass) != EXACT) return;  // the other instance handles this head
   const int b = bh / Hkv, h = bh - b * Hkv;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
-  const int row0 = ib * 256 + w * 64;  // this wave's rows (T is a multiple of 128, so all 64 or none are < T)
+  const int row0 = ib * WGR + w * 32 * NT;  // this wave's rows (T is a multiple of 128: all or none are < T)
   const bool active = row0 < T;
   const bf16* kh = k + b * ks.b + h * ks.h;
   const float* rv = rinv + (int64_t)bh * T;
@@ -1372,10 +1377,10 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
   const float c0 = LOG2E_F / scale;
 
   const bf16* klh = F32 ? lo.k + b * ks.b + h * ks.h : nullptr;
-  bf16x8 kbI[2][NKS], dbI[2][NKS], dbIl[2][NKS], kbIl[2][NKS];
-  float aI[2];
+  bf16x8 kbI[NT][NKS], dbI[NT][NKS], dbIl[NT][NKS], kbIl[NT][NKS];
+  float aI[NT];
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
+  for (int nt = 0; nt < NT; ++nt) {
     const int ir = active ? row0 + nt * 32 + l32 : 0;
     aI[nt] = sl2 * rv[ir];
 #pragma unroll
@@ -1386,13 +1391,12 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
       if constexpr (EXACT) dbIl[nt][st] = ld8(dvbl + ((int64_t)bh * T + ir) * D + 16 * st + 8 * g);
     }
   }
-  f32x16 acc[NDT][2];
+  f32x16 acc[NDT][NT];
 #pragma unroll
-  for (int t = 0; t < NDT; ++t) {
-    acc[t][0] = zero16();
-    acc[t][1] = zero16();
-  }
-  const int ntile = min(4 * ib + 4, T / 64);  // key tiles 0 .. ntile-1 (>= 2 since T >= 128)
+  for (int t = 0; t < NDT; ++t)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[t][nt] = zero16();
+  const int ntile = min((ib + 1) * (WGR / 64), T / 64);  // key tiles 0 .. ntile-1 (>= 2 since T >= 128)
   // newest vector-memory ops of a step, per wave
   constexpr int STAGE_OPS = (F32 ? 4 : EXACT ? 3 : 2) * (64 * (D / 8) / 256);
   int plan_k[64 * (D / 8) / 256], plan_v[64 * (D / 8) / 256];
@@ -1420,6 +1424,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
   __syncthreads();
   // this wave's rows are the 64-block row0 / 64; key tiles after it are fully masked
   const int last_w = row0 / 64;
+  const int roff = row0 - last_w * 64;  // the wave's first row inside that block (32 at NT = 1 for odd waves)
   auto tile = [&](int buf, bool diag) {
 #pragma unroll 1
     for (int jh = 0; jh < 2; ++jh) {
@@ -1431,9 +1436,9 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
       }
       float rJ[16];
       if constexpr (EXACT) lds_rows16(&sm.r[buf][jh * 32], g, rJ);
-      bf16x8 mb[2][2], ml[2][2];
+      bf16x8 mb[NT][2], ml[NT][2];
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
+      for (int nt = 0; nt < NT; ++nt) {
         f32x16 sc = zero16(), gg = zero16();
 #pragma unroll
         for (int st = 0; st < NKS; ++st) {
@@ -1460,7 +1465,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
         for (int e = 0; e < 16; ++e) {
           float pe = __builtin_amdgcn_exp2f(EXACT ? fmaf(sc[e] * aI[nt], rJ[e], -c0) : sc[e] * aI[nt]);
           // j >= i masked: the diagonal term is added in closed form after the sweep
-          if (diag && jh * 32 + drow(e, g) >= nt * 32 + l32) pe = 0.f;
+          if (diag && jh * 32 + drow(e, g) >= roff + nt * 32 + l32) pe = 0.f;
           gg[e] = EXACT ? gg[e] * pe * rJ[e] : gg[e] * pe;
         }
         mb[nt][0] = pack_b(gg, 0);
@@ -1475,7 +1480,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
         const bf16x8 k0 = lds_tr_a<D / 8>(sm.k[buf], jh * 32, t * 32);
         const bf16x8 k1 = lds_tr_a<D / 8>(sm.k[buf], jh * 32 + 16, t * 32);
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
+        for (int nt = 0; nt < NT; ++nt) {
           acc[t][nt] = mfma32(k0, mb[nt][0], acc[t][nt]);
           acc[t][nt] = mfma32(k1, mb[nt][1], acc[t][nt]);
           if constexpr (EXACT) {
@@ -1504,7 +1509,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
   if (!active) return;
   const float accf = EXACT ? 1.f : __builtin_amdgcn_exp2f(-c0);  // the bf16 sweep's 2^-c0
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
+  for (int nt = 0; nt < NT; ++nt) {
     const int irow = row0 + nt * 32 + l32;
     const float ri = rv[irow];
     const float* cs = colsum + ((int64_t)bh * T + irow) * D;

@@ -307,8 +307,11 @@ int launch_attn_bwd(const void* dout, const int64_t* dos, const void* q, const i
                  dim3(((T + 255) / 256) * BHq), block, st, (const bf16*)q, S(qs), (const bf16*)k, S(ks), f.vpb,
                  (const bf16*)dout, S(dos), lse, w.delta, f.mass, (bf16*)dq, S(dqs), Hq, Hkv, T, BHq, scale,
                  lucid::Lo{}, nullptr);
-  LUCID_LAUNCH_B("lucid_attn_bwd_dq_exact_kernel", (lucid::lucid_attn_bwd_dq_kernel<D, true, false, RW>),
-                 dim3(((T + 255) / 256) * BHq), block, st, (const bf16*)q, S(qs), (const bf16*)k, S(ks), f.vpb,
+  // the exact instance at head dim 128: 128 rows per workgroup, one wave per SIMD (its hi/lo
+  // operands need the registers)
+  constexpr int XWGR = D == 128 ? 128 : 256;
+  LUCID_LAUNCH_B("lucid_attn_bwd_dq_exact_kernel", (lucid::lucid_attn_bwd_dq_kernel<D, true, false, RW, XWGR>),
+                 dim3(((T + XWGR - 1) / XWGR) * BHq), dim3(64 * (XWGR / RW)), st, (const bf16*)q, S(qs), (const bf16*)k, S(ks), f.vpb,
                  (const bf16*)dout, S(dos), lse, w.delta, f.mass, (bf16*)dq, S(dqs), Hq, Hkv, T, BHq, scale,
                  lucid::Lo{}, nullptr);
   return LUCID_OK;
@@ -339,9 +342,12 @@ int launch_precond_bwd(const void* k, const int64_t* ks, const FwdWs& f, void* d
   LUCID_LAUNCH("lucid_precond_bwd_row_kernel", (lucid::lucid_precond_bwd_row_kernel<D, false>),
                dim3(((T + 255) / 256) * BH), st, (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, f.khat, scale, dn,
                f.vpb, f.vpbl, w.dvb, w.dvbl, f.mass, w.colsum, dka, (bf16*)dk, S(dks), lucid::Lo{});
-  LUCID_LAUNCH("lucid_precond_bwd_row_exact_kernel", (lucid::lucid_precond_bwd_row_kernel<D, true>),
-               dim3(((T + 255) / 256) * BH), st, (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, f.khat, scale, dn,
-               f.vpb, f.vpbl, w.dvb, w.dvbl, f.mass, w.colsum, dka, (bf16*)dk, S(dks), lucid::Lo{});
+  // the exact instance at head dim 128: one n-tile per wave (128 rows per workgroup), so that
+  // its hi/lo row operands stay in registers
+  constexpr int XNT = D == 128 ? 1 : 2;
+  LUCID_LAUNCH("lucid_precond_bwd_row_exact_kernel", (lucid::lucid_precond_bwd_row_kernel<D, true, false, XNT>),
+               dim3(((T + 128 * XNT - 1) / (128 * XNT)) * BH), st, (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, f.khat,
+               scale, dn, f.vpb, f.vpbl, w.dvb, w.dvbl, f.mass, w.colsum, dka, (bf16*)dk, S(dks), lucid::Lo{});
   return LUCID_OK;
 }
 
@@ -538,9 +544,13 @@ int launch_attn_fwd_f32(const void* q, const int64_t* qs, void* o, const int64_t
   lucid::Lo lo{};
   lo.q = w.ql;
   lo.k = w.kcl;
-  LUCID_LAUNCH("lucid_attn_fwd_f32_kernel", (lucid::lucid_attn_fwd_kernel<D, true>), dim3(((T + 255) / 256) * BHq),
-               st, w.qh, rows_strides(Hq, T, D), w.kch, rows_strides(Hkv, T, D), w.vpt, (float*)o, S(os), lse,
-               w.mass, w.olo, Hq, Hkv, T, BHq, scale, lo, w.vptl, 0);
+  // head dim 128: one 32-row n-tile per wave (128 rows per workgroup), so that the hi/lo
+  // operands stay in registers
+  constexpr int NT = D == 128 ? 1 : 2;
+  LUCID_LAUNCH("lucid_attn_fwd_f32_kernel", (lucid::lucid_attn_fwd_kernel<D, true, NT>),
+               dim3(((T + 128 * NT - 1) / (128 * NT)) * BHq), st, w.qh, rows_strides(Hq, T, D), w.kch,
+               rows_strides(Hkv, T, D), w.vpt, (float*)o, S(os), lse, w.mass, w.olo, Hq, Hkv, T, BHq, scale, lo,
+               w.vptl, 0);
   return LUCID_OK;
 }
 
@@ -575,10 +585,12 @@ int launch_attn_bwd_f32(const void* dout, const int64_t* dos, const void* o, con
                lo, lse, 1.f / (scale * LOG2E_F), w.seeds);
   LUCID_LAUNCH("lucid_attn_bwd_dkdv_f32_kernel", (lucid::lucid_attn_bwd_dkdv_kernel<D, true>), dim3((T / 128) * BH),
                st, f.qh, cq, f.kch, ck, f.vpb, w.doh, cq, w.seeds, w.dvp, w.dka, Hq, Hkv, T, BH, scale, lo, f.vpbl);
-  constexpr int RW = D == 128 ? 32 : 64;
-  LUCID_LAUNCH_B("lucid_attn_bwd_dq_f32_kernel", (lucid::lucid_attn_bwd_dq_kernel<D, true, true, RW>),
-                 dim3(((T + 255) / 256) * BHq), dim3(64 * (256 / RW)), st, f.qh, cq, f.kch, ck, f.vpb, w.doh, cq, lse,
-                 w.delta, f.mass, (float*)dq, S(dqs), Hq, Hkv, T, BHq, scale, lo, f.vpbl);
+  // head dim 128: four waves of 32 rows (128 rows per workgroup, one wave per SIMD), so that
+  // the hi/lo operands of a wave stay in registers
+  constexpr int RW = D == 128 ? 32 : 64, WGR = D == 128 ? 128 : 256;
+  LUCID_LAUNCH_B("lucid_attn_bwd_dq_f32_kernel", (lucid::lucid_attn_bwd_dq_kernel<D, true, true, RW, WGR>),
+                 dim3(((T + WGR - 1) / WGR) * BHq), dim3(64 * (WGR / RW)), st, f.qh, cq, f.kch, ck, f.vpb, w.doh, cq,
+                 lse, w.delta, f.mass, (float*)dq, S(dqs), Hq, Hkv, T, BHq, scale, lo, f.vpbl);
   return LUCID_OK;
 }
 
@@ -596,9 +608,10 @@ int launch_precond_bwd_f32(const FwdWs& f, void* dk, const int64_t* dks, void* d
   LUCID_LAUNCH("lucid_precond_bwd_col_f32_kernel", (lucid::lucid_precond_bwd_col_kernel<D, true, true>),
                dim3((T / 128) * BH), st, f.kh, ck, Hkv, T, BH, f.rinv, nullptr, scale, f.kt, f.vpb, f.vpbl, f.pinv,
                f.mass, w.dvp, w.dvb, w.dvbl, (float*)dv, S(dvs), w.colsum, w.counters, lo);
-  LUCID_LAUNCH("lucid_precond_bwd_row_f32_kernel", (lucid::lucid_precond_bwd_row_kernel<D, true, true>),
-               dim3(((T + 255) / 256) * BH), st, f.kh, ck, Hkv, T, BH, f.rinv, nullptr, scale, dn, f.vpb, f.vpbl,
-               w.dvb, w.dvbl, f.mass, w.colsum, dka, (float*)dk, S(dks), lo);
+  constexpr int NT = D == 128 ? 1 : 2;  // head dim 128: one n-tile per wave (registers)
+  LUCID_LAUNCH("lucid_precond_bwd_row_f32_kernel", (lucid::lucid_precond_bwd_row_kernel<D, true, true, NT>),
+               dim3(((T + 128 * NT - 1) / (128 * NT)) * BH), st, f.kh, ck, Hkv, T, BH, f.rinv, nullptr, scale, dn,
+               f.vpb, f.vpbl, w.dvb, w.dvbl, f.mass, w.colsum, dka, (float*)dk, S(dks), lo);
   return LUCID_OK;
 }
 

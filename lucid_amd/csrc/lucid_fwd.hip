@@ -893,7 +893,9 @@ __global__ __launch_bounds__(64 * NW) LUCID_TWO_WAVES_IF((D == 64 || NW == 8) &&
 // backward's delta_i = dO_i . O_i enters dQ_i = s sum_j dS_ij K_j multiplied by the
 // attention-weighted mean key, which is large when keys share a direction.
 // ---------------------------------------------------------------------------
-template <int D, bool F32 = false>
+// NT: 32-row n-tiles per wave (2: 256 rows per workgroup; 1: 128 rows, for the fp32
+// instance at head dim 128, whose hi/lo operands of two n-tiles do not fit the registers)
+template <int D, bool F32 = false, int NT = 2>
 __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid_attn_fwd_kernel(
     const bf16* __restrict__ q, Strides qs, const bf16* __restrict__ k, Strides ks, const bf16* __restrict__ vpt,
     std::conditional_t<F32, float, bf16>* __restrict__ o, Strides os, float* __restrict__ lse,
@@ -908,7 +910,9 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
   __shared__ __attribute__((aligned(16))) bf16 lkl[F32 ? 2 : 1][F32 ? 64 : 1][D + 8];  // lo tiles (fp32 inputs)
   __shared__ __attribute__((aligned(16))) bf16 lvl[F32 ? 2 : 1][F32 ? D : 1][64 + 8];
 
-  const int nblk = (T + 255) / 256;
+  static_assert(NT == 2 || (NT == 1 && (D == 128 || F32)), "one n-tile per wave: the generic tile body only");
+  constexpr int WGR = 128 * NT;  // rows per workgroup
+  const int nblk = (T + WGR - 1) / WGR;
   const int id = blockIdx.x;
   const int bhq = id % BHq;
   const int ib = nblk - 1 - id / BHq;
@@ -920,8 +924,8 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
   if (skip_fast && !(mass[bh] > kExactMass)) return;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
-  const int r0 = ib * 256;
-  const int row0 = r0 + w * 64;
+  const int r0 = ib * WGR;
+  const int row0 = r0 + w * 32 * NT;
   const bf16* qh = q + b * qs.b + hq * qs.h;
   const bf16* kh = k + b * ks.b + h * ks.h;
   const bf16* vth = vpt + (int64_t)bh * D * T;
@@ -930,9 +934,9 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
   const bf16* vtlh = F32 ? vptl + (int64_t)bh * D * T : nullptr;
   const float c = scale * LOG2E_F;
 
-  bf16x8 qb[2][NKS], qbl[2][NKS];
+  bf16x8 qb[NT][NKS], qbl[NT][NKS];
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
+  for (int nt = 0; nt < NT; ++nt) {
     const int rq = min(row0 + nt * 32 + l32, T - 1);
 #pragma unroll
     for (int st = 0; st < NKS; ++st) {
@@ -940,16 +944,19 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
       if constexpr (F32) qbl[nt][st] = ld8(qlh + (int64_t)rq * qs.t + 16 * st + 8 * g);
     }
   }
-  f32x16 oacc[NDT][2];
+  f32x16 oacc[NDT][NT];
+  float m[NT], lsum[NT];
 #pragma unroll
-  for (int t = 0; t < NDT; ++t) {
-    oacc[t][0] = zero16();
-    oacc[t][1] = zero16();
+  for (int nt = 0; nt < NT; ++nt) {
+    m[nt] = -1e30f;
+    lsum[nt] = 0.f;
+#pragma unroll
+    for (int t = 0; t < NDT; ++t) oacc[t][nt] = zero16();
   }
-  float m[2] = {-1e30f, -1e30f}, lsum[2] = {0.f, 0.f};
 
-  const int ntile = (min(r0 + 256, T) + 63) / 64;
-  const int last_w = row0 / 64;  // this wave's diagonal tile
+  const int ntile = (min(r0 + WGR, T) + 63) / 64;
+  const int last_w = row0 / 64;         // this wave's diagonal tile
+  const int roff = row0 - last_w * 64;  // this wave's first row inside it (32 at NT = 1 for odd waves)
   bf16x8 stg[NST];
   auto gload = [&](int j0) {
 #pragma unroll
@@ -987,7 +994,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
     const bool more = jt + 1 < ntile;
     if (more) gload((jt + 1) * 64);
     if (jt <= last_w && row0 < T) {
-      if constexpr (D == 64 && !F32) {
+      if constexpr (D == 64 && !F32 && NT == 2) {
         // Two 32-row halves (nt) per 64-key tile, staggered so that each half's softmax
         // VALU work overlaps the other half's MFMA work inside this wave:
         //   S(nt 0) | max(0) | S(nt 1) + exp(0) | max(1) | PV(nt 0) + exp(1) | PV(nt 1)
@@ -1070,7 +1077,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
         softmax(1);
         pv(1);
       } else {  // D = 128 and fp32 inputs: both halves' products first (the staggered order spills)
-        f32x16 s[2][2];
+        f32x16 s[2][NT];
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
           bf16x8 ka[NKS], kal[NKS];
@@ -1080,7 +1087,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
             if constexpr (F32) kal[st] = ld8(&lkl[buf][mt * 32 + l32][16 * st + 8 * g]);
           }
 #pragma unroll
-          for (int nt = 0; nt < 2; ++nt) {
+          for (int nt = 0; nt < NT; ++nt) {
             s[mt][nt] = zero16();
 #pragma unroll
             for (int st = 0; st < NKS; ++st) {
@@ -1097,14 +1104,14 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
 #pragma unroll
           for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt)
+            for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
               for (int e = 0; e < 16; ++e)
-                if (mt * 32 + drow(e, g) > nt * 32 + l32) s[mt][nt][e] = -INFINITY;
+                if (mt * 32 + drow(e, g) > roff + nt * 32 + l32) s[mt][nt][e] = -INFINITY;
         }
-        bf16x8 pb[2][4], pbl[2][4];
+        bf16x8 pb[NT][4], pbl[NT][4];
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
+        for (int nt = 0; nt < NT; ++nt) {
           float mx = -INFINITY;
 #pragma unroll
           for (int mt = 0; mt < 2; ++mt)
@@ -1146,7 +1153,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
 #pragma unroll
           for (int k4 = 0; k4 < 4; ++k4) va[k4] = ld8(&lv[buf][t * 32 + l32][16 * k4 + 8 * g]);
 #pragma unroll
-          for (int nt = 0; nt < 2; ++nt)
+          for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
             for (int k4 = 0; k4 < 4; ++k4) oacc[t][nt] = mfma32(va[k4], pb[nt][k4], oacc[t][nt]);
           if constexpr (F32) {
@@ -1154,7 +1161,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
             for (int k4 = 0; k4 < 4; ++k4) {
               const bf16x8 val = ld8(&lvl[buf][t * 32 + l32][16 * k4 + 8 * g]);
 #pragma unroll
-              for (int nt = 0; nt < 2; ++nt) {
+              for (int nt = 0; nt < NT; ++nt) {
                 oacc[t][nt] = mfma32(va[k4], pbl[nt][k4], oacc[t][nt]);
                 oacc[t][nt] = mfma32(val, pb[nt][k4], oacc[t][nt]);
               }
@@ -1168,7 +1175,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
   }
   const bool exact = !F32 && mass[bh] > kExactMass;  // fp32 O needs no lo part
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
+  for (int nt = 0; nt < NT; ++nt) {
     const int irow = row0 + nt * 32 + l32;
     const float ls = wave_sum32(lsum[nt]);
     if (irow < T) {
