@@ -339,7 +339,9 @@ def bench_c3(args, dev):
     first = step().item()
     args.warmup = 1 + warm_up(step, None if args.warmup is None else max(0, args.warmup - 1))
     ms, totals, dom, dom_avg = profiled_timing(lib, "lucid_", lambda: losses.append(step()), args.steps)
-    attn_ms = sum(tot for tot, _ in totals.values()) / args.steps
+    model_ops = ("lucid_rmsnorm", "lucid_rope")  # the fused RMSNorm / RoPE layers, not attention
+    attn_ms = sum(tot for n, (tot, _) in totals.items() if not n.startswith(model_ops)) / args.steps
+    norm_rope_ms = sum(tot for n, (tot, _) in totals.items() if n.startswith(model_ops)) / args.steps
     kernels = {n: {"avg_ms": round(tot / cnt, 4), "launches": cnt} for n, (tot, cnt) in
                sorted(totals.items(), key=lambda kv: -kv[1][0])}
     H, D = cfg.num_attention_heads, cfg.head_dim
@@ -390,6 +392,7 @@ def bench_c3(args, dev):
         "loss_last_step": round(losses[-1].item(), 4),
         "tflops": round(flops / (ms / 1e3) / 1e12, 1),
         "attention_ms_per_step": round(attn_ms, 3),
+        "rmsnorm_rope_ms_per_step": round(norm_rope_ms, 3),
         "roofline": {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None},
         "kernels": kernels,

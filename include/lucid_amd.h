@@ -299,6 +299,23 @@ int lucid_decode_noalloc(const void* q, const int64_t* q_strides, const void* k,
                          float* vp_new, int B, int Hq, int Hkv, int T_past, int T_cap, int D, float scale, float eps,
                          void* stream);
 
+/* The decoder's elementwise layers, one pass each (the Llama-LUCID model around the attention
+ * core; the reference computes them as chains of torch ops).  bf16 tensors, rows contiguous.
+ * lucid_rmsnorm_fwd: y[N][H] = w * bf16(x * rstd), rstd[n] = 1/sqrt(mean(x[n]^2) + eps) (fp32;
+ * saved for the backward), replacing LlamaRMSNorm.forward (modeling_lucid.py:58-75).
+ * lucid_rmsnorm_bwd: dx and dw (summed over the rows in a fixed order) from dy, with a
+ * caller-owned fp32 workspace of lucid_rmsnorm_bwd_workspace_bytes(N, H).  H must be 512, 1024,
+ * 2048 or 4096.  lucid_rope: out[R][64] = x cos + rotate_half(x) sin (transpose = 1: the
+ * adjoint, for the backward) for rows of head dim 64 in [B, T, H] order (row r uses the
+ * cos / sin row r / Hn, bf16 [B*T][64]), x rows at x_row_stride elements, out contiguous,
+ * replacing apply_rotary_pos_emb (modeling_lucid.py:118-145). */
+int lucid_rmsnorm_fwd(const void* x, const void* w, void* y, float* rstd, int N, int H, float eps, void* stream);
+size_t lucid_rmsnorm_bwd_workspace_bytes(int N, int H);
+int lucid_rmsnorm_bwd(const void* x, const void* w, const void* dy, const float* rstd, void* dx, void* dw,
+                      void* workspace, int N, int H, void* stream);
+int lucid_rope(const void* x, int64_t x_row_stride, int R, int Hn, const void* cos, const void* sin, void* out, int D,
+               int transpose, void* stream);
+
 /* Per-kernel timing (no counterpart in the reference; used by bench.py).
  * When enabled, every launch is bracketed by two HIP events on its stream.
  * lucid_profile_collect() waits for the recorded events, folds them into

@@ -81,6 +81,10 @@ _SIGS = {
         "lucid_decode_noalloc": ([_vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp,
                                   _int, _int, _int, _int, _int, _int, _flt, _flt, _vp], _int),
         "lucid_decode_tokens_workspace_bytes": ([_int] * 6, _sz),
+        "lucid_rmsnorm_fwd": ([_vp, _vp, _vp, _vp, _int, _int, _flt, _vp], _int),
+        "lucid_rmsnorm_bwd_workspace_bytes": ([_int, _int], _sz),
+        "lucid_rmsnorm_bwd": ([_vp, _vp, _vp, _vp, _vp, _vp, _vp, _int, _int, _vp], _int),
+        "lucid_rope": ([_vp, ctypes.c_int64, _int, _int, _vp, _vp, _vp, _int, _int, _vp], _int),
         "lucid_decode_tokens": ([_vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _vp,
                                  _int, _int, _int, _int, _int, _int, _int, _flt, _flt, _vp], _int),
         "lucid_profile_enable": ([_int], None),

@@ -10,6 +10,7 @@
 #include "lucid_bwd.hip"
 #include "lucid_decode.hip"
 #include "lucid_fwd.hip"
+#include "model_ops.hip"
 #include "chain_guard.h"
 #include "profiling.h"
 
@@ -1298,5 +1299,73 @@ int lucid_profile_entry(int idx, char* name, int name_len, double* total_ms, lon
 }
 
 void lucid_profile_reset(void) { lucid_prof::reset(); }
+
+// ---- the decoder's elementwise layers (modeling_lucid.py:58-75, 118-145) ----
+
+int lucid_rmsnorm_fwd(const void* x, const void* w, void* y, float* rstd, int N, int H, float eps, void* stream) {
+  g_last_error.clear();
+  if (N < 0 || (H != 512 && H != 1024 && H != 2048 && H != 4096))
+    return fail("lucid_rmsnorm_fwd: H must be 512, 1024, 2048 or 4096 and N >= 0, got H=" + std::to_string(H));
+  if (N == 0) return LUCID_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 grid((N + 3) / 4);
+#define LUCID_NORM_FWD(NC)                                                                                      \
+  LUCID_LAUNCH("lucid_rmsnorm_fwd_kernel", lucid::lucid_rmsnorm_fwd_kernel<NC>, grid, st, (const bf16*)x,   \
+               (const bf16*)w, (bf16*)y, rstd, N, eps)
+  switch (H) {
+    case 512: LUCID_NORM_FWD(1); break;
+    case 1024: LUCID_NORM_FWD(2); break;
+    case 2048: LUCID_NORM_FWD(4); break;
+    default: LUCID_NORM_FWD(8); break;
+  }
+#undef LUCID_NORM_FWD
+  return LUCID_OK;
+}
+
+size_t lucid_rmsnorm_bwd_workspace_bytes(int N, int H) {
+  return (size_t)((N + lucid::kNormRowsPerBlock - 1) / lucid::kNormRowsPerBlock) * (size_t)H * sizeof(float);
+}
+
+int lucid_rmsnorm_bwd(const void* x, const void* w, const void* dy, const float* rstd, void* dx, void* dw,
+                      void* workspace, int N, int H, void* stream) {
+  g_last_error.clear();
+  if (N < 0 || (H != 512 && H != 1024 && H != 2048 && H != 4096))
+    return fail("lucid_rmsnorm_bwd: H must be 512, 1024, 2048 or 4096 and N >= 0, got H=" + std::to_string(H));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int nb = (N + lucid::kNormRowsPerBlock - 1) / lucid::kNormRowsPerBlock;
+  float* part = static_cast<float*>(workspace);
+  if (nb > 0) {
+#define LUCID_NORM_BWD(NC)                                                                                       \
+  LUCID_LAUNCH("lucid_rmsnorm_bwd_kernel", lucid::lucid_rmsnorm_bwd_kernel<NC>, dim3(nb), st, (const bf16*)x,  \
+               (const bf16*)w, (const bf16*)dy, rstd, (bf16*)dx, part, N)
+    switch (H) {
+      case 512: LUCID_NORM_BWD(1); break;
+      case 1024: LUCID_NORM_BWD(2); break;
+      case 2048: LUCID_NORM_BWD(4); break;
+      default: LUCID_NORM_BWD(8); break;
+    }
+#undef LUCID_NORM_BWD
+  }
+  LUCID_LAUNCH("lucid_rmsnorm_dw_kernel", lucid::lucid_rmsnorm_dw_kernel, dim3((H + 255) / 256), st, part, nb, H,
+               (bf16*)dw);
+  return LUCID_OK;
+}
+
+int lucid_rope(const void* x, int64_t x_row_stride, int R, int Hn, const void* cos, const void* sin, void* out, int D,
+               int transpose, void* stream) {
+  g_last_error.clear();
+  if (D != 64 || R < 0 || Hn <= 0 || x_row_stride < D)
+    return fail("lucid_rope: head dim 64, R >= 0, Hn > 0 and a row stride >= 64, got D=" + std::to_string(D));
+  if (R == 0) return LUCID_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)(((int64_t)R * (D / 2) + 255) / 256));
+  if (transpose)
+    LUCID_LAUNCH("lucid_rope_kernel", lucid::lucid_rope_kernel<-1>, grid, st, (const bf16*)x, x_row_stride, R, Hn,
+                 (const bf16*)cos, (const bf16*)sin, (bf16*)out);
+  else
+    LUCID_LAUNCH("lucid_rope_kernel", lucid::lucid_rope_kernel<1>, grid, st, (const bf16*)x, x_row_stride, R, Hn,
+                 (const bf16*)cos, (const bf16*)sin, (bf16*)out);
+  return LUCID_OK;
+}
 
 }  // extern "C"

@@ -5,8 +5,9 @@ parameter names follow it (``model.layers.N.self_attn.q_proj`` ...), so its stat
 dicts load unchanged, and ``LucidAttention.forward`` keeps the reference signature
 (``modeling_lucid.py:421-503``).  The attention core -- K^ = RMSNorm(K), the
 preconditioner solve V' = P^-1 V and causal softmax attention on V' -- runs in
-``lucid_amd.lucid_attention`` (HIP); embeddings, RMSNorm, RoPE, the SwiGLU MLP and
-the LM head are plain PyTorch (hipBLASLt GEMMs).
+``lucid_amd.lucid_attention`` (HIP); RMSNorm and RoPE on bf16 GPU activations run as one
+HIP kernel pass each way (``lucid_amd.model_ops``; the torch expressions otherwise);
+embeddings, the SwiGLU MLP and the LM head are plain PyTorch (hipBLASLt GEMMs).
 
 Decoding with a cache (``get_new_v_prime``, ``modeling_lucid.py:576-598``) keeps
 (K, V') per layer and runs the HIP decoding step ``lucid_decode``.  The new rows of V'
@@ -25,6 +26,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from .lucid import _padded_dim, lucid_attention, lucid_decode
+from .model_ops import apply_rope, rms_norm, rms_norm_supported, rope_supported
 
 
 @dataclass
@@ -61,6 +63,8 @@ class LlamaRMSNorm(nn.Module):
         self.variance_epsilon = eps
 
     def forward(self, hidden_states: torch.Tensor) -> torch.Tensor:
+        if rms_norm_supported(hidden_states, self.weight):
+            return rms_norm(hidden_states, self.weight, self.variance_epsilon)  # one HIP pass each way
         input_dtype = hidden_states.dtype
         x = hidden_states.to(torch.float32)
         x = x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + self.variance_epsilon)
@@ -90,6 +94,8 @@ def rotate_half(x: torch.Tensor) -> torch.Tensor:
 
 def apply_rotary_pos_emb(q, k, cos, sin, unsqueeze_dim: int = 1):
     """modeling_lucid.py:118-145."""
+    if unsqueeze_dim == 1 and rope_supported(q, cos) and rope_supported(k, cos):
+        return apply_rope(q, cos, sin), apply_rope(k, cos, sin)  # one HIP pass each way
     cos, sin = cos.unsqueeze(unsqueeze_dim), sin.unsqueeze(unsqueeze_dim)
     return (q * cos) + (rotate_half(q) * sin), (k * cos) + (rotate_half(k) * sin)
 

@@ -1,0 +1,142 @@
+"""GPU parity of the fused decoder layers (lucid_amd.model_ops) against float32 PyTorch
+restatements of the reference expressions (modeling_lucid.py:58-75 RMSNorm, :112-145 RoPE):
+
+    RMSNorm  y = w * bf16(x rstd), rstd = 1/sqrt(mean(x^2) + eps), and its gradients dx, dw
+    RoPE     x cos + rotate_half(x) sin, rotate_half(x) = (-x2, x1), and its gradient
+
+Outputs are bf16, so the bar is bf16 rounding: max |ours - ref| <= 1e-2 * max |ref| against the
+float32 reference (on bf16-rounded inputs), and the forward of RMSNorm also within two bf16
+ulps of the reference's own bf16 torch expression.  A tiny decoder whose norms and rotary
+embedding take the fused path matches the same model on the torch expressions.
+"""
+import pytest
+import torch
+
+from lucid_amd import model_ops as O
+from lucid_amd import modeling_lucid as M
+
+pytestmark = pytest.mark.gpu
+
+BAR = 1e-2
+
+
+def _rel(a, b):
+    return ((a.float() - b.float()).abs().max() / b.float().abs().max().clamp_min(1e-30)).item()
+
+
+def _rmsnorm_ref(x, w, eps):
+    """float32 restatement of LlamaRMSNorm (the rounding of x rstd to bf16 kept)."""
+    xf = x.float()
+    xn = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+    return w.float() * xn.to(torch.bfloat16).float()
+
+
+@pytest.mark.parametrize("N,H", [(1, 512), (130, 1024), (600, 2048), (77, 4096)])
+def test_rmsnorm_forward_backward(N, H):
+    print(f"case rmsnorm N={N} H={H}", flush=True)
+    g = torch.Generator().manual_seed(N + H)
+    x = (torch.randn(2, N, H, generator=g) * 3).to(torch.bfloat16).cuda().requires_grad_()
+    w = (1 + 0.1 * torch.randn(H, generator=g)).to(torch.bfloat16).cuda().requires_grad_()
+    dy = torch.randn(2, N, H, generator=g).to(torch.bfloat16).cuda()
+    eps = 1e-5
+    y = O.rms_norm(x, w, eps)
+    y.backward(dy)
+    torch.cuda.synchronize()
+
+    xr = x.detach().float().requires_grad_()
+    wr = w.detach().float().requires_grad_()
+    yr = _rmsnorm_ref(xr, wr, eps)
+    yr.backward(dy.float())
+    assert y.dtype == torch.bfloat16 and y.shape == x.shape
+    assert _rel(y, yr) <= BAR
+    assert _rel(x.grad, xr.grad) <= BAR, _rel(x.grad, xr.grad)
+    assert _rel(w.grad, wr.grad) <= BAR, _rel(w.grad, wr.grad)
+    # the reference's bf16 torch expression: two bf16 ulps at most (rstd's last bit may differ)
+    with torch.no_grad():
+        xf = x.float()
+        ye = w * (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)).to(torch.bfloat16)
+    ulp = 2.0 ** -6 * ye.float().abs()
+    assert bool(((y.float() - ye.float()).abs() <= ulp + 1e-30).all())
+
+
+def test_rmsnorm_rejects_unsupported():
+    x = torch.randn(4, 96, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(TypeError):
+        O.rms_norm(x, torch.ones(96, dtype=torch.bfloat16, device="cuda"), 1e-5)
+    assert not O.rms_norm_supported(x.float(), torch.ones(96, device="cuda"))
+
+
+def _rope_ref(x, cos, sin):
+    c, s = cos.float().unsqueeze(1), sin.float().unsqueeze(1)
+    x1, x2 = x[..., :32], x[..., 32:]
+    return x * c + torch.cat((-x2, x1), dim=-1) * s
+
+
+@pytest.mark.parametrize("B,H,T,layout", [(1, 4, 37, "proj"), (2, 3, 129, "proj"), (2, 2, 64, "dense")])
+def test_rope_forward_backward(B, H, T, layout):
+    print(f"case rope B={B} H={H} T={T} {layout}", flush=True)
+    g = torch.Generator().manual_seed(B * 100 + H * 10 + T)
+    if layout == "proj":  # the model's q_proj(...).view(B, T, H, d).transpose(1, 2)
+        base = torch.randn(B, T, H * 64, generator=g).to(torch.bfloat16).cuda()
+        x = base.view(B, T, H, 64).transpose(1, 2).detach().requires_grad_()
+    else:  # a dense [B, H, T, d] tensor (copied to rows by the wrapper)
+        x = torch.randn(B, H, T, 64, generator=g).to(torch.bfloat16).cuda().requires_grad_()
+    pos = torch.arange(T)[None].expand(B, -1).cuda()
+    emb = M.LlamaRotaryEmbedding(M.LucidConfig(hidden_size=H * 64, num_attention_heads=H, head_dim=64),
+                                 device="cuda")
+    cos, sin = emb(x, pos)
+    dout = torch.randn(B, H, T, 64, generator=g).to(torch.bfloat16).cuda()
+    out = O.apply_rope(x, cos, sin)
+    out.backward(dout)
+    torch.cuda.synchronize()
+
+    xr = x.detach().float().requires_grad_()
+    ref = _rope_ref(xr, cos, sin)
+    ref.backward(dout.float())
+    assert out.shape == x.shape and out.dtype == torch.bfloat16
+    assert _rel(out, ref) <= BAR
+    assert _rel(x.grad, xr.grad) <= BAR
+
+
+def test_rope_cos_broadcast_over_batch():
+    """cos / sin given for one sequence ([1, T, 64]) apply to every batch row."""
+    B, H, T = 3, 2, 50
+    x = torch.randn(B, H, T, 64, dtype=torch.bfloat16, device="cuda")
+    emb = M.LlamaRotaryEmbedding(M.LucidConfig(hidden_size=H * 64, num_attention_heads=H, head_dim=64),
+                                 device="cuda")
+    cos, sin = emb(x, torch.arange(T, device="cuda")[None])
+    out = O.apply_rope(x, cos, sin)
+    assert _rel(out, _rope_ref(x.float(), cos.expand(B, -1, -1), sin.expand(B, -1, -1))) <= BAR
+
+
+def test_tiny_decoder_fused_layers_match_torch_expressions(monkeypatch):
+    """A decoder with hidden size 512 (fused RMSNorm) and head dim 64 (fused RoPE) against the
+    same weights on the torch expressions: loss and gradients."""
+    torch.manual_seed(3)
+    cfg = M.LucidConfig(vocab_size=512, hidden_size=512, intermediate_size=1024, num_hidden_layers=2,
+                        num_attention_heads=8, num_key_value_heads=2, head_dim=64)
+    model = M.LlamaForCausalLM(cfg).to("cuda", torch.bfloat16)
+    for p in model.parameters():  # norms away from 1 so that dw matters
+        if p.dim() == 1:
+            p.data.uniform_(0.5, 1.5)
+    ids = torch.randint(0, cfg.vocab_size, (2, 160), generator=torch.Generator().manual_seed(4)).cuda()
+
+    def run():
+        model.zero_grad(set_to_none=True)
+        loss, _ = model(ids, labels=ids)
+        loss.backward()
+        torch.cuda.synchronize()
+        return loss.item(), {n: p.grad.float().clone() for n, p in model.named_parameters()}
+
+    loss_f, grads_f = run()
+    monkeypatch.setattr(M, "rms_norm_supported", lambda *a: False)
+    monkeypatch.setattr(M, "rope_supported", lambda *a: False)
+    loss_t, grads_t = run()
+    assert abs(loss_f - loss_t) <= 1e-2 * abs(loss_t), (loss_f, loss_t)
+    for name in ("model.layers.0.input_layernorm.weight", "model.layers.1.post_attention_layernorm.weight",
+                 "model.norm.weight", "model.layers.0.self_attn.q_proj.weight",
+                 "model.layers.0.self_attn.k_proj.weight", "model.embed_tokens.weight"):
+        a, b = grads_f[name], grads_t[name]
+        cos = torch.nn.functional.cosine_similarity(a.flatten(), b.flatten(), dim=0).item()
+        rel = ((a - b).norm() / b.norm()).item()
+        assert cos > 0.99 and rel < 0.1, (name, cos, rel)
