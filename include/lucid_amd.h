@@ -305,16 +305,34 @@ int lucid_decode_noalloc(const void* q, const int64_t* q_strides, const void* k,
  * saved for the backward), replacing LlamaRMSNorm.forward (modeling_lucid.py:58-75).
  * lucid_rmsnorm_bwd: dx and dw (summed over the rows in a fixed order) from dy, with a
  * caller-owned fp32 workspace of lucid_rmsnorm_bwd_workspace_bytes(N, H).  H must be 512, 1024,
- * 2048 or 4096.  lucid_rope: out[R][64] = x cos + rotate_half(x) sin (transpose = 1: the
- * adjoint, for the backward) for rows of head dim 64 in [B, T, H] order (row r uses the
- * cos / sin row r / Hn, bf16 [B*T][64]), x rows at x_row_stride elements, out contiguous,
+ * 2048 or 4096.  lucid_rope: out[B][T][Hn][64] = x cos + rotate_half(x) sin (transpose = 1:
+ * the adjoint, for the backward) for x [B, Hn, T, 64] at element strides x_strides = (b, h, t),
+ * multiples of 8, with cos / sin bf16 [B*T][64] (one row per token), pointers 16-byte aligned,
  * replacing apply_rotary_pos_emb (modeling_lucid.py:118-145). */
 int lucid_rmsnorm_fwd(const void* x, const void* w, void* y, float* rstd, int N, int H, float eps, void* stream);
 size_t lucid_rmsnorm_bwd_workspace_bytes(int N, int H);
 int lucid_rmsnorm_bwd(const void* x, const void* w, const void* dy, const float* rstd, void* dx, void* dw,
                       void* workspace, int N, int H, void* stream);
-int lucid_rope(const void* x, int64_t x_row_stride, int R, int Hn, const void* cos, const void* sin, void* out, int D,
-               int transpose, void* stream);
+int lucid_rope(const void* x, const int64_t x_strides[3], int B, int Hn, int T, const void* cos, const void* sin,
+               void* out, int D, int transpose, void* stream);
+
+/* lucid_swiglu_fwd: h = silu(g) * u over n bf16 values, replacing the act_fn(gate) * up of
+ * LlamaMLP.forward (modeling_lucid.py:155-167); lucid_swiglu_bwd: dg = dh u silu'(g),
+ * du = dh silu(g).  Pointers 16-byte aligned.
+ * lucid_causal_lm_loss_fwd / _bwd: the causal-LM cross entropy of LlamaForCausalLM.forward
+ * (modeling_lucid.py:847-967; F.cross_entropy on logits[:, :-1] in fp32 against labels[:, 1:],
+ * ignore index -100) over bf16 logits [R = B*T][V] at row_stride elements (V and the stride
+ * multiples of 8), labels int64 [R].  The forward writes per row lse, loss (lse - logit of the
+ * target; 0 where the row does not count, NaN for a target outside [0, V) other than -100) and
+ * valid (1 or 0): the loss is sum(loss) / sum(valid).  The backward writes dlogits [R][V]
+ * = (softmax - onehot) * scale[0] on counted rows and 0 elsewhere (scale: a device float,
+ * dloss / sum(valid)). */
+int lucid_swiglu_fwd(const void* g, const void* u, void* h, int64_t n, void* stream);
+int lucid_swiglu_bwd(const void* g, const void* u, const void* dh, void* dg, void* du, int64_t n, void* stream);
+int lucid_causal_lm_loss_fwd(const void* logits, int64_t row_stride, const int64_t* labels, int R, int T, int V,
+                             float* lse, float* loss, float* valid, void* stream);
+int lucid_causal_lm_loss_bwd(const void* logits, int64_t row_stride, const int64_t* labels, int R, int T, int V,
+                             const float* lse, const float* valid, const float* scale, void* dlogits, void* stream);
 
 /* Per-kernel timing (no counterpart in the reference; used by bench.py).
  * When enabled, every launch is bracketed by two HIP events on its stream.

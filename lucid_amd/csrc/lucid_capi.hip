@@ -1346,25 +1346,89 @@ int lucid_rmsnorm_bwd(const void* x, const void* w, const void* dy, const float*
     }
 #undef LUCID_NORM_BWD
   }
-  LUCID_LAUNCH("lucid_rmsnorm_dw_kernel", lucid::lucid_rmsnorm_dw_kernel, dim3((H + 255) / 256), st, part, nb, H,
-               (bf16*)dw);
+  LUCID_LAUNCH_B("lucid_rmsnorm_dw_kernel", lucid::lucid_rmsnorm_dw_kernel, dim3(H / 256), dim3(64 * lucid::kDwWaves),
+                 st, part, nb, H, (bf16*)dw);
   return LUCID_OK;
 }
 
-int lucid_rope(const void* x, int64_t x_row_stride, int R, int Hn, const void* cos, const void* sin, void* out, int D,
-               int transpose, void* stream) {
+int lucid_rope(const void* x, const int64_t x_strides[3], int B, int Hn, int T, const void* cos, const void* sin,
+               void* out, int D, int transpose, void* stream) {
   g_last_error.clear();
-  if (D != 64 || R < 0 || Hn <= 0 || x_row_stride < D)
-    return fail("lucid_rope: head dim 64, R >= 0, Hn > 0 and a row stride >= 64, got D=" + std::to_string(D));
+  if (D != 64 || B < 0 || T < 0 || Hn <= 0)
+    return fail("lucid_rope: head dim 64, B >= 0, T >= 0 and Hn > 0, got D=" + std::to_string(D));
+  if (x_strides[0] % 8 || x_strides[1] % 8 || x_strides[2] % 8 || reinterpret_cast<uintptr_t>(x) % 16 ||
+      reinterpret_cast<uintptr_t>(cos) % 16 || reinterpret_cast<uintptr_t>(sin) % 16 ||
+      reinterpret_cast<uintptr_t>(out) % 16)
+    return fail("lucid_rope: strides must be multiples of 8 elements and pointers 16-byte aligned");
+  const int64_t R = (int64_t)B * T * Hn;
   if (R == 0) return LUCID_OK;
+  if (R > INT32_MAX / 4) return fail("lucid_rope: too many rows");
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const dim3 grid((unsigned)(((int64_t)R * (D / 2) + 255) / 256));
+  const dim3 grid((unsigned)((R * 4 + 255) / 256));
   if (transpose)
-    LUCID_LAUNCH("lucid_rope_kernel", lucid::lucid_rope_kernel<-1>, grid, st, (const bf16*)x, x_row_stride, R, Hn,
-                 (const bf16*)cos, (const bf16*)sin, (bf16*)out);
+    LUCID_LAUNCH("lucid_rope_kernel", lucid::lucid_rope_kernel<-1>, grid, st, (const bf16*)x, x_strides[0],
+                 x_strides[1], x_strides[2], (int)R, Hn, T, (const bf16*)cos, (const bf16*)sin, (bf16*)out);
   else
-    LUCID_LAUNCH("lucid_rope_kernel", lucid::lucid_rope_kernel<1>, grid, st, (const bf16*)x, x_row_stride, R, Hn,
-                 (const bf16*)cos, (const bf16*)sin, (bf16*)out);
+    LUCID_LAUNCH("lucid_rope_kernel", lucid::lucid_rope_kernel<1>, grid, st, (const bf16*)x, x_strides[0],
+                 x_strides[1], x_strides[2], (int)R, Hn, T, (const bf16*)cos, (const bf16*)sin, (bf16*)out);
+  return LUCID_OK;
+}
+
+static bool misaligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 != 0; }
+
+int lucid_swiglu_fwd(const void* g, const void* u, void* h, int64_t n, void* stream) {
+  g_last_error.clear();
+  if (n < 0) return fail("lucid_swiglu_fwd: n must be >= 0");
+  if (misaligned16(g) || misaligned16(u) || misaligned16(h))
+    return fail("lucid_swiglu_fwd: pointers must be 16-byte aligned");
+  if (n == 0) return LUCID_OK;
+  const int64_t blocks = (n + 2047) / 2048;
+  if (blocks > INT32_MAX) return fail("lucid_swiglu_fwd: too many elements");
+  LUCID_LAUNCH("lucid_swiglu_fwd_kernel", lucid::lucid_swiglu_fwd_kernel, dim3((unsigned)blocks),
+               static_cast<hipStream_t>(stream), (const bf16*)g, (const bf16*)u, (bf16*)h, n);
+  return LUCID_OK;
+}
+
+int lucid_swiglu_bwd(const void* g, const void* u, const void* dh, void* dg, void* du, int64_t n, void* stream) {
+  g_last_error.clear();
+  if (n < 0) return fail("lucid_swiglu_bwd: n must be >= 0");
+  if (misaligned16(g) || misaligned16(u) || misaligned16(dh) || misaligned16(dg) || misaligned16(du))
+    return fail("lucid_swiglu_bwd: pointers must be 16-byte aligned");
+  if (n == 0) return LUCID_OK;
+  const int64_t blocks = (n + 2047) / 2048;
+  if (blocks > INT32_MAX) return fail("lucid_swiglu_bwd: too many elements");
+  LUCID_LAUNCH("lucid_swiglu_bwd_kernel", lucid::lucid_swiglu_bwd_kernel, dim3((unsigned)blocks),
+               static_cast<hipStream_t>(stream), (const bf16*)g, (const bf16*)u, (const bf16*)dh, (bf16*)dg,
+               (bf16*)du, n);
+  return LUCID_OK;
+}
+
+static int check_ce(const char* what, const void* logits, int64_t ls, int R, int T, int V) {
+  if (R < 0 || T < 1 || R % T || V < 1 || V % 8 || ls < V || ls % 8 || misaligned16(logits))
+    return fail(std::string(what) + ": R a multiple of T >= 1, V and the row stride multiples of 8, logits "
+                "16-byte aligned; got R=" + std::to_string(R) + " T=" + std::to_string(T) + " V=" +
+                std::to_string(V));
+  return LUCID_OK;
+}
+
+int lucid_causal_lm_loss_fwd(const void* logits, int64_t row_stride, const int64_t* labels, int R, int T, int V,
+                             float* lse, float* loss, float* valid, void* stream) {
+  g_last_error.clear();
+  if (int rc = check_ce("lucid_causal_lm_loss_fwd", logits, row_stride, R, T, V)) return rc;
+  if (R == 0) return LUCID_OK;
+  LUCID_LAUNCH("lucid_ce_fwd_kernel", lucid::lucid_ce_fwd_kernel, dim3(R), static_cast<hipStream_t>(stream),
+               (const bf16*)logits, row_stride, labels, T, V, lse, loss, valid);
+  return LUCID_OK;
+}
+
+int lucid_causal_lm_loss_bwd(const void* logits, int64_t row_stride, const int64_t* labels, int R, int T, int V,
+                             const float* lse, const float* valid, const float* scale, void* dlogits, void* stream) {
+  g_last_error.clear();
+  if (int rc = check_ce("lucid_causal_lm_loss_bwd", logits, row_stride, R, T, V)) return rc;
+  if (misaligned16(dlogits)) return fail("lucid_causal_lm_loss_bwd: dlogits must be 16-byte aligned");
+  if (R == 0) return LUCID_OK;
+  LUCID_LAUNCH("lucid_ce_bwd_kernel", lucid::lucid_ce_bwd_kernel, dim3(R), static_cast<hipStream_t>(stream),
+               (const bf16*)logits, row_stride, labels, T, V, lse, valid, scale, (bf16*)dlogits);
   return LUCID_OK;
 }
 

@@ -11,11 +11,18 @@
 //                                 order: deterministic)
 //   lucid_rope_kernel             out = x cos + rotate_half(x) sin over [B, T, H, d] rows (and
 //                                 its transpose for the backward), one rounding to bf16
+//   lucid_swiglu_fwd/bwd_kernel   h = silu(g) u (modeling_lucid.py:155-167 between the gate / up
+//                                 and down projections) and its gradients, fp32 inside
+//   lucid_ce_fwd/bwd_kernel       the shifted causal-LM cross entropy on bf16 logits
+//                                 (modeling_lucid.py:847-967: labels shifted by one, -100
+//                                 ignored): per-row logsumexp and loss in one read of the row;
+//                                 backward (softmax - onehot) scale written as bf16
 #include "lucid_common.h"
 
 namespace lucid {
 
-constexpr int kNormRowsPerBlock = 64;  // rows per workgroup of the backward (one dw partial each)
+constexpr int kNormRowsPerBlock = 16;  // rows per workgroup of the backward (one dw partial each)
+constexpr int kDwWaves = 16;           // waves of the dw reduction workgroup (256 columns each)
 
 // One wave per row; H = 64 * 8 * NC (a lane holds NC chunks of 8 consecutive values).
 template <int NC>
@@ -106,45 +113,231 @@ __global__ __launch_bounds__(256) void lucid_rmsnorm_bwd_kernel(const bf16* __re
     part[(int64_t)blockIdx.x * H + j] = (red[0][j] + red[1][j]) + (red[2][j] + red[3][j]);
 }
 
-// dw[j] = sum over the row blocks of part[b][j], in block order; grid H / 256.
-__global__ __launch_bounds__(256) void lucid_rmsnorm_dw_kernel(const float* __restrict__ part, int nb, int H,
-                                                               bf16* __restrict__ dw) {
-  const int j = blockIdx.x * 256 + threadIdx.x;
-  if (j >= H) return;
-  float s = 0.f;
-  for (int b = 0; b < nb; ++b) s += part[(int64_t)b * H + j];
-  dw[j] = (bf16)s;
+// dw[j] = sum over the row blocks of part[b][j]: a workgroup of kDwWaves waves per 256 columns
+// (4 per lane, one 16-byte load); wave w sums the blocks b = w, w + kDwWaves, ... in order, and
+// the waves' sums are added in a fixed tree order (deterministic).  Grid H / 256.
+__global__ __launch_bounds__(64 * kDwWaves) void lucid_rmsnorm_dw_kernel(const float* __restrict__ part, int nb,
+                                                                         int H, bf16* __restrict__ dw) {
+  __shared__ float4 red[kDwWaves][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int j = blockIdx.x * 256 + lane * 4;
+  float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 8
+  for (int b = w; b < nb; b += kDwWaves) {
+    const float4 p = *reinterpret_cast<const float4*>(part + (int64_t)b * H + j);
+    s.x += p.x;
+    s.y += p.y;
+    s.z += p.z;
+    s.w += p.w;
+  }
+  red[w][lane] = s;
+  __syncthreads();
+#pragma unroll
+  for (int h = kDwWaves / 2; h >= 1; h >>= 1) {
+    if (w < h) {
+      const float4 o = red[w + h][lane];
+      s.x += o.x;
+      s.y += o.y;
+      s.z += o.z;
+      s.w += o.w;
+      red[w][lane] = s;
+    }
+    __syncthreads();
+  }
+  if (w == 0) {
+    bf16 o[4] = {(bf16)s.x, (bf16)s.y, (bf16)s.z, (bf16)s.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) dw[j + e] = o[e];
+  }
 }
 
-// Rotary embedding over rows of head dim D = 64 (the model's): x [R][D] with row stride
-// xs (elements) and head index h = row % Hn, token t = row / Hn (the [B, T, H, D] layout of
-// the projections, B folded into t); cos / sin [Tt][D] rows of the token.  SIGN = +1: the
-// forward out = x cos + rotate_half(x) sin; SIGN = -1: its transpose (the backward),
-// out = x cos + rotate_half^T(x sin).  One lane per pair (i, i + D/2).
+// Rotary embedding over rows of head dim D = 64 (the model's).  Output rows are [B, T, Hn]
+// ordered, out[row][64] contiguous; row (b, t, h) reads x + b sb + h sh + t st (element strides,
+// multiples of 8) and the cos / sin row of token b T + t ([B T][64]).  SIGN = +1: the forward
+// out = x cos + rotate_half(x) sin, rotate_half(x) = (-x2, x1); SIGN = -1: its transpose (the
+// backward), out = x cos + rotate_half^T(x sin), rotate_half^T(y) = (y2, -y1).  Four lanes per
+// row, each holding 8 pairs (i, i + 32) in 16-byte loads.
 template <int SIGN>
-__global__ __launch_bounds__(256) void lucid_rope_kernel(const bf16* __restrict__ x, int64_t xs, int R, int Hn,
+__global__ __launch_bounds__(256) void lucid_rope_kernel(const bf16* __restrict__ x, int64_t sb, int64_t sh,
+                                                         int64_t st, int R, int Hn, int T,
                                                          const bf16* __restrict__ cs, const bf16* __restrict__ sn,
                                                          bf16* __restrict__ out) {
   constexpr int D = 64, HD = D / 2;
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;  // (row, pair)
-  const int row = (int)(idx / HD), i = (int)(idx % HD);
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int row = (int)(idx >> 2), i0 = (int)(idx & 3) * 8;
   if (row >= R) return;
-  const int t = row / Hn;
-  const bf16* xr = x + (int64_t)row * xs;
-  const float x1 = (float)xr[i], x2 = (float)xr[i + HD];
-  const float c1 = (float)cs[(int64_t)t * D + i], c2 = (float)cs[(int64_t)t * D + i + HD];
-  const float s1 = (float)sn[(int64_t)t * D + i], s2 = (float)sn[(int64_t)t * D + i + HD];
-  float o1, o2;
-  if constexpr (SIGN > 0) {  // rotate_half(x) = (-x2, x1)
-    o1 = x1 * c1 - x2 * s1;
-    o2 = x2 * c2 + x1 * s2;
-  } else {  // rotate_half^T(y) = (y2, -y1) with y = x sin
-    o1 = x1 * c1 + x2 * s2;
-    o2 = x2 * c2 - x1 * s1;
+  const int h = row % Hn, bt = row / Hn;
+  const int t = bt % T, b = bt / T;
+  const bf16* xr = x + b * sb + h * sh + t * st;
+  const bf16x8 x1 = ld8(xr + i0), x2 = ld8(xr + HD + i0);
+  const bf16x8 c1 = ld8(cs + (int64_t)bt * D + i0), c2 = ld8(cs + (int64_t)bt * D + HD + i0);
+  const bf16x8 s1 = ld8(sn + (int64_t)bt * D + i0), s2 = ld8(sn + (int64_t)bt * D + HD + i0);
+  bf16x8 o1, o2;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float a = (float)x1[e], c = (float)x2[e];
+    if constexpr (SIGN > 0) {
+      o1[e] = (bf16)(a * (float)c1[e] - c * (float)s1[e]);
+      o2[e] = (bf16)(c * (float)c2[e] + a * (float)s2[e]);
+    } else {
+      o1[e] = (bf16)(a * (float)c1[e] + c * (float)s2[e]);
+      o2[e] = (bf16)(c * (float)c2[e] - a * (float)s1[e]);
+    }
   }
   bf16* orow = out + (int64_t)row * D;
-  orow[i] = (bf16)o1;
-  orow[i + HD] = (bf16)o2;
+  *reinterpret_cast<bf16x8*>(orow + i0) = o1;
+  *reinterpret_cast<bf16x8*>(orow + HD + i0) = o2;
+}
+
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
+
+// h = silu(g) u elementwise over n values; 8 per lane (16-byte accesses) and a scalar tail.
+__global__ __launch_bounds__(256) void lucid_swiglu_fwd_kernel(const bf16* __restrict__ g, const bf16* __restrict__ u,
+                                                               bf16* __restrict__ h, int64_t n) {
+  const int64_t c = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
+  if (c + 8 <= n) {
+    const bf16x8 gv = ld8(g + c), uv = ld8(u + c);
+    bf16x8 o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float x = (float)gv[e];
+      o[e] = (bf16)(x * sigmoidf_(x) * (float)uv[e]);
+    }
+    *reinterpret_cast<bf16x8*>(h + c) = o;
+  } else {
+    for (int64_t i = c; i < n; ++i) {
+      const float x = (float)g[i];
+      h[i] = (bf16)(x * sigmoidf_(x) * (float)u[i]);
+    }
+  }
+}
+
+// dg = dh u silu'(g), du = dh silu(g); silu'(x) = sig(x) (1 + x (1 - sig(x))).
+__global__ __launch_bounds__(256) void lucid_swiglu_bwd_kernel(const bf16* __restrict__ g, const bf16* __restrict__ u,
+                                                               const bf16* __restrict__ dh, bf16* __restrict__ dg,
+                                                               bf16* __restrict__ du, int64_t n) {
+  const int64_t c = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
+  auto one = [](float x, float uu, float d, float& og, float& ou) {
+    const float sg = sigmoidf_(x);
+    og = d * uu * sg * (1.0f + x * (1.0f - sg));
+    ou = d * x * sg;
+  };
+  if (c + 8 <= n) {
+    const bf16x8 gv = ld8(g + c), uv = ld8(u + c), dv = ld8(dh + c);
+    bf16x8 og, ou;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float a, b;
+      one((float)gv[e], (float)uv[e], (float)dv[e], a, b);
+      og[e] = (bf16)a;
+      ou[e] = (bf16)b;
+    }
+    *reinterpret_cast<bf16x8*>(dg + c) = og;
+    *reinterpret_cast<bf16x8*>(du + c) = ou;
+  } else {
+    for (int64_t i = c; i < n; ++i) {
+      float a, b;
+      one((float)g[i], (float)u[i], (float)dh[i], a, b);
+      dg[i] = (bf16)a;
+      du[i] = (bf16)b;
+    }
+  }
+}
+
+constexpr int kIgnoreIndex = -100;  // F.cross_entropy's default ignore_index
+
+// Workgroup-wide (max, sum of exp) merge of the 256 lanes' running pairs; every lane returns
+// the row's logsumexp.
+__device__ __forceinline__ float block_lse(float m, float s) {
+  __shared__ float sm[4], ss[4];
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const float m2 = __shfl_xor(m, o, 64), s2 = __shfl_xor(s, o, 64);
+    const float mm = fmaxf(m, m2);
+    s = s * __expf(m - mm) + s2 * __expf(m2 - mm);
+    m = mm;
+  }
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    sm[w] = m;
+    ss[w] = s;
+  }
+  __syncthreads();
+  float mm = fmaxf(fmaxf(sm[0], sm[1]), fmaxf(sm[2], sm[3]));
+  float st = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) st += ss[i] * __expf(sm[i] - mm);
+  return mm + __logf(st);
+}
+
+// Row r of logits [R][V] (row stride ls, V and ls multiples of 8) is position t = r % T of its
+// sequence; its target is labels[r + 1] for t < T - 1 (the shift of the causal-LM loss), and the
+// last position of each sequence has none.  Writes lse[r], loss[r] = lse - logit[target] and
+// valid[r] (1 when the row counts, else 0 with loss 0); a target outside [0, V) other than the
+// ignore index gives a NaN loss.
+__global__ __launch_bounds__(256) void lucid_ce_fwd_kernel(const bf16* __restrict__ logits, int64_t ls,
+                                                           const int64_t* __restrict__ labels, int T, int V,
+                                                           float* __restrict__ lse, float* __restrict__ loss,
+                                                           float* __restrict__ valid) {
+  const int r = blockIdx.x;
+  const bf16* row = logits + (int64_t)r * ls;
+  float m = -3.0e38f, s = 0.f;
+  for (int j = threadIdx.x * 8; j < V; j += 256 * 8) {
+    const bf16x8 xv = ld8(row + j);
+    float cm = (float)xv[0];
+#pragma unroll
+    for (int e = 1; e < 8; ++e) cm = fmaxf(cm, (float)xv[e]);
+    if (cm > m) {
+      s *= __expf(m - cm);
+      m = cm;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s += __expf((float)xv[e] - m);
+  }
+  const float l = block_lse(m, s);
+  if (threadIdx.x == 0) {
+    lse[r] = l;
+    const bool has = (r % T) != T - 1;
+    const int64_t tgt = has ? labels[r + 1] : kIgnoreIndex;
+    if (tgt == kIgnoreIndex) {
+      loss[r] = 0.f;
+      valid[r] = 0.f;
+    } else if (tgt < 0 || tgt >= V) {
+      loss[r] = __int_as_float(0x7fc00000);
+      valid[r] = 1.f;
+    } else {
+      loss[r] = l - (float)row[tgt];
+      valid[r] = 1.f;
+    }
+  }
+}
+
+// dlogits[r][j] = (exp(logit - lse[r]) - [j == target]) * scale[0] for counted rows, 0 for the
+// others (dlogits [R][V] contiguous).
+__global__ __launch_bounds__(256) void lucid_ce_bwd_kernel(const bf16* __restrict__ logits, int64_t ls,
+                                                           const int64_t* __restrict__ labels, int T, int V,
+                                                           const float* __restrict__ lse,
+                                                           const float* __restrict__ valid,
+                                                           const float* __restrict__ scale,
+                                                           bf16* __restrict__ dlogits) {
+  const int r = blockIdx.x;
+  const bf16* row = logits + (int64_t)r * ls;
+  bf16* drow = dlogits + (int64_t)r * V;
+  const bool on = valid[r] != 0.f;
+  const float sc = on ? scale[0] : 0.f, l = lse[r];
+  const int64_t tgt = on ? labels[r + 1] : -1;
+  for (int j = threadIdx.x * 8; j < V; j += 256 * 8) {
+    bf16x8 o;
+    if (on) {
+      const bf16x8 xv = ld8(row + j);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = (bf16)((__expf((float)xv[e] - l) - (j + e == tgt ? 1.f : 0.f)) * sc);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = (bf16)0.f;
+    }
+    *reinterpret_cast<bf16x8*>(drow + j) = o;
+  }
 }
 
 }  // namespace lucid

@@ -1,19 +1,26 @@
-"""Fused RMSNorm and rotary-embedding layers of the Llama-LUCID decoder on HIP kernels.
+"""Fused elementwise layers of the Llama-LUCID decoder on HIP kernels.
 
 The reference model (``modeling_lucid.py:58-75`` RMSNorm, ``:112-145`` rotate_half /
-apply_rotary_pos_emb) writes both as chains of torch elementwise ops, each a full pass over
-the activations in HBM.  Here each is one kernel pass forward and one backward:
+apply_rotary_pos_emb, ``:155-167`` the SwiGLU MLP, ``:847-967`` the loss) writes these as
+chains of torch elementwise ops, each a full pass over the activations in HBM.  Here each is
+one kernel pass forward and one backward:
 
 * :func:`rms_norm` -- y = w * bf16(x * rstd) with rstd = 1 / sqrt(mean(x^2) + eps) in fp32
   (the reference's statistics and rounding points); backward dx = rstd (g - xn mean(g xn)),
   g = bf16(dy w), and dw summed over row blocks in a fixed order (deterministic).
 * :func:`apply_rope` -- x cos + rotate_half(x) sin on a ``[B, H, T, 64]`` view of the
-  ``[B, T, H, 64]`` projection output, written as ``[B, T, H, 64]`` (returned as the same
-  transposed view), rounded to bf16 once; backward applies the transposed rotation.
+  ``[B, T, H, 64]`` projection output (any strides that are multiples of 8), written as
+  ``[B, T, H, 64]`` (returned as the same transposed view), rounded to bf16 once; backward
+  applies the transposed rotation.
 
-Both take bf16 GPU tensors only (hidden sizes 512, 1024, 2048 or 4096; head dim 64) and
-raise otherwise; :func:`rms_norm_supported` / :func:`rope_supported` tell the model which
-inputs they cover.
+* :func:`swiglu` -- silu(g) * u of the MLP, one pass each way with fp32 inside (the
+  reference rounds silu(g) to bf16 before the product).
+* :func:`causal_lm_loss` -- the shifted cross entropy on bf16 logits, one read of the logits
+  forward (per-row logsumexp) and one read + write backward, instead of fp32 copies of them.
+
+All take bf16 GPU tensors only (RMSNorm: hidden sizes 512, 1024, 2048 or 4096; RoPE: head
+dim 64; the loss: a vocabulary that is a multiple of 8) and raise otherwise; the
+``*_supported`` predicates tell the model which inputs they cover.
 """
 from __future__ import annotations
 
@@ -81,31 +88,28 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
     return RMSNormFunction.apply(x, weight, eps)
 
 
-def _rows(t: torch.Tensor):
-    """``t`` [B, H, T, 64] viewed as rows in [B, T, H] order: (tensor, row stride); copies
-    when the three leading axes do not collapse into one stride."""
-    B, Hn, T, _ = t.shape
-    s = t.stride()
-    if s[3] == 1 and s[1] % 8 == 0 and s[2] == Hn * s[1] and (B == 1 or s[0] == T * s[2]) \
-            and t.data_ptr() % 16 == 0:
-        return t, s[1]
-    return t.transpose(1, 2).contiguous().transpose(1, 2), 64
+def _strided(t: torch.Tensor) -> torch.Tensor:
+    """``t`` [B, H, T, 64] as the kernel reads it: unit stride on the head axis, the other
+    strides multiples of 8 elements, a 16-byte aligned base (copied otherwise)."""
+    if t.stride(3) == 1 and all(s % 8 == 0 for s in t.stride()[:3]) and t.data_ptr() % 16 == 0:
+        return t
+    return t.contiguous()
 
 
 def _tokens(c: torch.Tensor, B: int, T: int) -> torch.Tensor:
     """cos / sin [B or 1, T, 64] as B*T contiguous token rows."""
     if c.dim() == 2:
         c = c.unsqueeze(0)
-    return c.expand(B, T, c.shape[-1]).contiguous()
+    return _aligned(c.expand(B, T, c.shape[-1]))
 
 
 def _rope_launch(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, transpose: int) -> torch.Tensor:
     B, Hn, T, D = x.shape
-    xr, xs = _rows(x)
+    xr = _strided(x)
     out = torch.empty(B, T, Hn, D, dtype=x.dtype, device=x.device)
     lib = _lib.load()
-    rc = lib.lucid_rope(_lib.ptr(xr), xs, B * T * Hn, Hn, _lib.ptr(cos), _lib.ptr(sin), _lib.ptr(out), D, transpose,
-                        _lib.stream_handle(x.device))
+    rc = lib.lucid_rope(_lib.ptr(xr), _lib.strides3(xr, (0, 1, 2)), B, Hn, T, _lib.ptr(cos), _lib.ptr(sin),
+                        _lib.ptr(out), D, transpose, _lib.stream_handle(x.device))
     _lib.check(lib, rc, "lucid_rope")
     return out.transpose(1, 2)
 
@@ -130,3 +134,85 @@ def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.T
     """x cos + rotate_half(x) sin for x [B, H, T, 64] and cos / sin [B or 1, T, 64]
     (modeling_lucid.py:118-145 with unsqueeze_dim 1)."""
     return RopeFunction.apply(x, cos, sin)
+
+
+def swiglu_supported(g: torch.Tensor, u: torch.Tensor) -> bool:
+    return g.is_cuda and g.dtype == torch.bfloat16 and u.dtype == torch.bfloat16 and g.shape == u.shape
+
+
+class SwiGLUFunction(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, g: torch.Tensor, u: torch.Tensor):
+        if not swiglu_supported(g, u):
+            raise TypeError(f"lucid_amd.swiglu: bf16 GPU gate and up of one shape, got {g.dtype} {tuple(g.shape)} / "
+                            f"{u.dtype} {tuple(u.shape)}")
+        g2, u2 = _aligned(g), _aligned(u)
+        h = torch.empty_like(g2)
+        lib = _lib.load()
+        rc = lib.lucid_swiglu_fwd(_lib.ptr(g2), _lib.ptr(u2), _lib.ptr(h), g2.numel(), _lib.stream_handle(g.device))
+        _lib.check(lib, rc, "lucid_swiglu_fwd")
+        ctx.save_for_backward(g2, u2)
+        return h
+
+    @staticmethod
+    def backward(ctx, dh: torch.Tensor):
+        g2, u2 = ctx.saved_tensors
+        dh2 = _aligned(dh)
+        dg, du = torch.empty_like(g2), torch.empty_like(u2)
+        lib = _lib.load()
+        rc = lib.lucid_swiglu_bwd(_lib.ptr(g2), _lib.ptr(u2), _lib.ptr(dh2), _lib.ptr(dg), _lib.ptr(du), g2.numel(),
+                                  _lib.stream_handle(g2.device))
+        _lib.check(lib, rc, "lucid_swiglu_bwd")
+        return dg, du
+
+
+def swiglu(g: torch.Tensor, u: torch.Tensor) -> torch.Tensor:
+    """silu(g) * u (the gated activation of ``LlamaMLP.forward``, modeling_lucid.py:155-167)."""
+    return SwiGLUFunction.apply(g, u)
+
+
+IGNORE_INDEX = -100
+
+
+def causal_lm_loss_supported(logits: torch.Tensor, labels: torch.Tensor) -> bool:
+    return (logits.is_cuda and logits.dtype == torch.bfloat16 and logits.dim() == 3 and logits.shape[-1] % 8 == 0
+            and labels.shape == logits.shape[:2] and labels.dtype == torch.int64)
+
+
+class CausalLMLossFunction(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, logits: torch.Tensor, labels: torch.Tensor):
+        if not causal_lm_loss_supported(logits, labels):
+            raise TypeError("lucid_amd.causal_lm_loss: bf16 GPU logits [B, T, V] (V a multiple of 8) and int64 "
+                            f"labels [B, T], got {logits.dtype} {tuple(logits.shape)} / {labels.dtype}")
+        B, T, V = logits.shape
+        lg = _aligned(logits.reshape(B * T, V))
+        lb = labels.reshape(-1).contiguous()
+        R = B * T
+        lse, per_row, valid = (torch.empty(R, dtype=torch.float32, device=logits.device) for _ in range(3))
+        lib = _lib.load()
+        rc = lib.lucid_causal_lm_loss_fwd(_lib.ptr(lg), V, _lib.ptr(lb), R, T, V, _lib.ptr(lse), _lib.ptr(per_row),
+                                          _lib.ptr(valid), _lib.stream_handle(logits.device))
+        _lib.check(lib, rc, "lucid_causal_lm_loss_fwd")
+        count = valid.sum()
+        ctx.save_for_backward(lg, lb, lse, valid, count)
+        ctx.dims = (B, T, V)
+        return per_row.sum() / count
+
+    @staticmethod
+    def backward(ctx, dloss: torch.Tensor):
+        lg, lb, lse, valid, count = ctx.saved_tensors
+        B, T, V = ctx.dims
+        scale = (dloss.float() / count).reshape(1).contiguous()
+        dlogits = torch.empty(B * T, V, dtype=torch.bfloat16, device=lg.device)
+        lib = _lib.load()
+        rc = lib.lucid_causal_lm_loss_bwd(_lib.ptr(lg), V, _lib.ptr(lb), B * T, T, V, _lib.ptr(lse), _lib.ptr(valid),
+                                          _lib.ptr(scale), _lib.ptr(dlogits), _lib.stream_handle(lg.device))
+        _lib.check(lib, rc, "lucid_causal_lm_loss_bwd")
+        return dlogits.view(B, T, V), None
+
+
+def causal_lm_loss(logits: torch.Tensor, labels: torch.Tensor) -> torch.Tensor:
+    """Mean cross entropy of logits[:, :-1] against labels[:, 1:] with -100 ignored, computed in
+    fp32 (``LlamaForCausalLM.forward``'s loss, modeling_lucid.py:847-967); a float32 scalar."""
+    return CausalLMLossFunction.apply(logits, labels)

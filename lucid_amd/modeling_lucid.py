@@ -5,9 +5,10 @@ parameter names follow it (``model.layers.N.self_attn.q_proj`` ...), so its stat
 dicts load unchanged, and ``LucidAttention.forward`` keeps the reference signature
 (``modeling_lucid.py:421-503``).  The attention core -- K^ = RMSNorm(K), the
 preconditioner solve V' = P^-1 V and causal softmax attention on V' -- runs in
-``lucid_amd.lucid_attention`` (HIP); RMSNorm and RoPE on bf16 GPU activations run as one
-HIP kernel pass each way (``lucid_amd.model_ops``; the torch expressions otherwise);
-embeddings, the SwiGLU MLP and the LM head are plain PyTorch (hipBLASLt GEMMs).
+``lucid_amd.lucid_attention`` (HIP); RMSNorm, RoPE, the SwiGLU gate and the loss on bf16
+GPU activations run as one HIP kernel pass each way (``lucid_amd.model_ops``; the torch
+expressions otherwise); embeddings and the projections / LM head are plain PyTorch (hipBLASLt
+GEMMs).
 
 Decoding with a cache (``get_new_v_prime``, ``modeling_lucid.py:576-598``) keeps
 (K, V') per layer and runs the HIP decoding step ``lucid_decode``.  The new rows of V'
@@ -26,7 +27,8 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from .lucid import _padded_dim, lucid_attention, lucid_decode
-from .model_ops import apply_rope, rms_norm, rms_norm_supported, rope_supported
+from .model_ops import (apply_rope, causal_lm_loss, causal_lm_loss_supported, rms_norm, rms_norm_supported,
+                        rope_supported, swiglu, swiglu_supported)
 
 
 @dataclass
@@ -110,7 +112,10 @@ class LlamaMLP(nn.Module):
         self.down_proj = nn.Linear(config.intermediate_size, config.hidden_size, bias=config.mlp_bias)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
+        g, u = self.gate_proj(x), self.up_proj(x)
+        if swiglu_supported(g, u):
+            return self.down_proj(swiglu(g, u))  # one HIP pass each way
+        return self.down_proj(F.silu(g) * u)
 
 
 class LucidCache:
@@ -181,6 +186,9 @@ class LucidCache:
         return k[:, :, :n + t, :d], v[:, :, :n + t, :d]
 
 
+_STACKED_QKV_MIN_NUMEL = 1 << 20  # activations at least this large take one stacked q/k/v GEMM
+
+
 class LucidAttention(nn.Module):
     """LUCID attention module (modeling_lucid.py:385-503) on the HIP kernels."""
 
@@ -208,9 +216,18 @@ class LucidAttention(nn.Module):
                 cache_position: Optional[torch.Tensor] = None, **kwargs):
         input_shape = hidden_states.shape[:-1]
         hidden_shape = (*input_shape, -1, self.head_dim)
-        q = self.q_proj(hidden_states).view(hidden_shape).transpose(1, 2)
-        k = self.k_proj(hidden_states).view(hidden_shape).transpose(1, 2)
-        v = self.v_proj(hidden_states).view(hidden_shape).transpose(1, 2)
+        if hidden_states.is_cuda and hidden_states.numel() >= _STACKED_QKV_MIN_NUMEL:
+            # one GEMM over the stacked q / k / v weights (the parameters stay separate): on
+            # long inputs its weight gradient runs at ~1.5x the rate of three narrow ones
+            qkv = F.linear(hidden_states, torch.cat((self.q_proj.weight, self.k_proj.weight, self.v_proj.weight)),
+                           None if self.q_proj.bias is None else
+                           torch.cat((self.q_proj.bias, self.k_proj.bias, self.v_proj.bias)))
+            nq, nk = self.q_proj.out_features, self.k_proj.out_features
+            q, k, v = (t.view(hidden_shape).transpose(1, 2) for t in qkv.split((nq, nk, nk), dim=-1))
+        else:
+            q = self.q_proj(hidden_states).view(hidden_shape).transpose(1, 2)
+            k = self.k_proj(hidden_states).view(hidden_shape).transpose(1, 2)
+            v = self.v_proj(hidden_states).view(hidden_shape).transpose(1, 2)
         cos, sin = position_embeddings
         if self.use_rope:
             q, k = apply_rotary_pos_emb(q, k, cos, sin)
@@ -325,7 +342,9 @@ class LlamaForCausalLM(nn.Module):
         hidden = self.model(input_ids, past_key_values=past_key_values)
         logits = self.lm_head(hidden)
         loss = None
-        if labels is not None:
+        if labels is not None and causal_lm_loss_supported(logits, labels):
+            loss = causal_lm_loss(logits, labels)  # fused on the HIP kernels (no fp32 copy of the logits)
+        elif labels is not None:
             loss = F.cross_entropy(logits[:, :-1].float().reshape(-1, logits.shape[-1]), labels[:, 1:].reshape(-1))
         return loss, logits
 

@@ -3,6 +3,8 @@ restatements of the reference expressions (modeling_lucid.py:58-75 RMSNorm, :112
 
     RMSNorm  y = w * bf16(x rstd), rstd = 1/sqrt(mean(x^2) + eps), and its gradients dx, dw
     RoPE     x cos + rotate_half(x) sin, rotate_half(x) = (-x2, x1), and its gradient
+    SwiGLU   silu(g) u (:155-167) and its gradients
+    loss     cross entropy of logits[:, :-1] (fp32) against labels[:, 1:], -100 ignored (:847-967)
 
 Outputs are bf16, so the bar is bf16 rounding: max |ours - ref| <= 1e-2 * max |ref| against the
 float32 reference (on bf16-rounded inputs), and the forward of RMSNorm also within two bf16
@@ -72,15 +74,19 @@ def _rope_ref(x, cos, sin):
     return x * c + torch.cat((-x2, x1), dim=-1) * s
 
 
-@pytest.mark.parametrize("B,H,T,layout", [(1, 4, 37, "proj"), (2, 3, 129, "proj"), (2, 2, 64, "dense")])
+@pytest.mark.parametrize("B,H,T,layout", [(1, 4, 37, "proj"), (2, 3, 129, "proj"), (2, 2, 64, "dense"),
+                                           (2, 3, 33, "sliced")])
 def test_rope_forward_backward(B, H, T, layout):
     print(f"case rope B={B} H={H} T={T} {layout}", flush=True)
     g = torch.Generator().manual_seed(B * 100 + H * 10 + T)
     if layout == "proj":  # the model's q_proj(...).view(B, T, H, d).transpose(1, 2)
         base = torch.randn(B, T, H * 64, generator=g).to(torch.bfloat16).cuda()
         x = base.view(B, T, H, 64).transpose(1, 2).detach().requires_grad_()
-    else:  # a dense [B, H, T, d] tensor (copied to rows by the wrapper)
+    elif layout == "dense":  # a dense [B, H, T, d] tensor
         x = torch.randn(B, H, T, 64, generator=g).to(torch.bfloat16).cuda().requires_grad_()
+    else:  # rows 68 apart: strides not multiples of 8 (the wrapper copies)
+        base = torch.randn(B, H, T, 68, generator=g).to(torch.bfloat16).cuda()
+        x = base[..., :64].detach().requires_grad_()
     pos = torch.arange(T)[None].expand(B, -1).cuda()
     emb = M.LlamaRotaryEmbedding(M.LucidConfig(hidden_size=H * 64, num_attention_heads=H, head_dim=64),
                                  device="cuda")
@@ -110,8 +116,8 @@ def test_rope_cos_broadcast_over_batch():
 
 
 def test_tiny_decoder_fused_layers_match_torch_expressions(monkeypatch):
-    """A decoder with hidden size 512 (fused RMSNorm) and head dim 64 (fused RoPE) against the
-    same weights on the torch expressions: loss and gradients."""
+    """A decoder with hidden size 512 (fused RMSNorm), head dim 64 (fused RoPE), the fused SwiGLU
+    gate and loss against the same weights on the torch expressions: loss and gradients."""
     torch.manual_seed(3)
     cfg = M.LucidConfig(vocab_size=512, hidden_size=512, intermediate_size=1024, num_hidden_layers=2,
                         num_attention_heads=8, num_key_value_heads=2, head_dim=64)
@@ -129,8 +135,8 @@ def test_tiny_decoder_fused_layers_match_torch_expressions(monkeypatch):
         return loss.item(), {n: p.grad.float().clone() for n, p in model.named_parameters()}
 
     loss_f, grads_f = run()
-    monkeypatch.setattr(M, "rms_norm_supported", lambda *a: False)
-    monkeypatch.setattr(M, "rope_supported", lambda *a: False)
+    for name in ("rms_norm_supported", "rope_supported", "swiglu_supported", "causal_lm_loss_supported"):
+        monkeypatch.setattr(M, name, lambda *a: False)
     loss_t, grads_t = run()
     assert abs(loss_f - loss_t) <= 1e-2 * abs(loss_t), (loss_f, loss_t)
     for name in ("model.layers.0.input_layernorm.weight", "model.layers.1.post_attention_layernorm.weight",
@@ -140,3 +146,84 @@ def test_tiny_decoder_fused_layers_match_torch_expressions(monkeypatch):
         cos = torch.nn.functional.cosine_similarity(a.flatten(), b.flatten(), dim=0).item()
         rel = ((a - b).norm() / b.norm()).item()
         assert cos > 0.99 and rel < 0.1, (name, cos, rel)
+
+
+@pytest.mark.parametrize("shape", [(3005,), (2, 37, 5632)])
+def test_swiglu_forward_backward(shape):
+    print(f"case swiglu {shape}", flush=True)
+    g = torch.Generator().manual_seed(len(shape))
+    gate = (2 * torch.randn(*shape, generator=g)).to(torch.bfloat16).cuda().requires_grad_()
+    up = torch.randn(*shape, generator=g).to(torch.bfloat16).cuda().requires_grad_()
+    dh = torch.randn(*shape, generator=g).to(torch.bfloat16).cuda()
+    h = O.swiglu(gate, up)
+    h.backward(dh)
+    torch.cuda.synchronize()
+    gr, ur = gate.detach().float().requires_grad_(), up.detach().float().requires_grad_()
+    hr = torch.nn.functional.silu(gr) * ur
+    hr.backward(dh.float())
+    assert h.dtype == torch.bfloat16 and h.shape == gate.shape
+    assert _rel(h, hr) <= BAR
+    assert _rel(gate.grad, gr.grad) <= BAR
+    assert _rel(up.grad, ur.grad) <= BAR
+
+
+def _ce_ref(logits, labels):
+    V = logits.shape[-1]
+    return torch.nn.functional.cross_entropy(logits[:, :-1].float().reshape(-1, V), labels[:, 1:].reshape(-1))
+
+
+@pytest.mark.parametrize("B,T,V", [(2, 33, 1000), (1, 9, 32000)])
+def test_causal_lm_loss_forward_backward(B, T, V):
+    print(f"case loss B={B} T={T} V={V}", flush=True)
+    g = torch.Generator().manual_seed(T)
+    logits = (3 * torch.randn(B, T, V, generator=g)).to(torch.bfloat16).cuda().requires_grad_()
+    labels = torch.randint(0, V, (B, T), generator=g)
+    labels[0, 5:9] = -100  # ignored targets
+    labels = labels.cuda()
+    loss = O.causal_lm_loss(logits, labels)
+    loss.backward(torch.tensor(2.0, device="cuda"))
+    torch.cuda.synchronize()
+    lr = logits.detach().float().requires_grad_()
+    ref = _ce_ref(lr, labels)
+    (2 * ref).backward()
+    assert loss.dtype == torch.float32 and loss.dim() == 0
+    assert abs(loss.item() - ref.item()) <= 1e-4 * abs(ref.item()), (loss.item(), ref.item())
+    assert _rel(logits.grad, lr.grad) <= BAR
+    assert bool((logits.grad[:, -1] == 0).all())  # the last position has no target
+
+
+def test_causal_lm_loss_flags_bad_targets_and_empty_batches():
+    logits = torch.randn(1, 4, 64, dtype=torch.bfloat16, device="cuda")
+    bad = torch.tensor([[0, 1, 64, 2]], device="cuda")
+    assert torch.isnan(O.causal_lm_loss(logits, bad)).item()
+    none = torch.full((1, 4), -100, dtype=torch.int64, device="cuda")
+    assert torch.isnan(O.causal_lm_loss(logits, none)).item()  # as torch: a mean over no targets
+    assert torch.isnan(_ce_ref(logits, none)).item()
+
+
+def test_stacked_qkv_projection_matches_separate_projections(monkeypatch):
+    """Long inputs take one GEMM over the stacked q / k / v weights; the loss and the gradients
+    of the three separate parameters match the per-projection GEMMs."""
+    torch.manual_seed(5)
+    cfg = M.LucidConfig(vocab_size=512, hidden_size=512, intermediate_size=1024, num_hidden_layers=1,
+                        num_attention_heads=8, num_key_value_heads=4, head_dim=64)
+    model = M.LlamaForCausalLM(cfg).to("cuda", torch.bfloat16)
+    ids = torch.randint(0, cfg.vocab_size, (2, 1024), generator=torch.Generator().manual_seed(6)).cuda()
+    assert 2 * 1024 * 512 >= M._STACKED_QKV_MIN_NUMEL
+
+    def run():
+        model.zero_grad(set_to_none=True)
+        loss, _ = model(ids, labels=ids)
+        loss.backward()
+        torch.cuda.synchronize()
+        return loss.item(), {n: p.grad.float().clone() for n, p in model.named_parameters()}
+
+    loss_s, grads_s = run()
+    monkeypatch.setattr(M, "_STACKED_QKV_MIN_NUMEL", 1 << 62)
+    loss_p, grads_p = run()
+    assert abs(loss_s - loss_p) <= 1e-3 * abs(loss_p), (loss_s, loss_p)
+    for name in ("q_proj", "k_proj", "v_proj"):
+        a, b = grads_s[f"model.layers.0.self_attn.{name}.weight"], grads_p[f"model.layers.0.self_attn.{name}.weight"]
+        assert a.shape == b.shape
+        rel = ((a - b).norm() / b.norm()).item()
+        assert rel < 2e-2, (name, rel)
