@@ -38,6 +38,10 @@ extern "C" {
 
 #define LUCID_OK 0
 #define LUCID_EINVAL 1
+
+/* element types of lucid_adamw_step */
+#define LUCID_DTYPE_BF16 0
+#define LUCID_DTYPE_F32 1
 #define LUCID_ECHAIN 2 /* a chain wait gave up in an earlier launch (lucid_chain_status) */
 #define LUCID_EHIP 1000
 
@@ -333,6 +337,19 @@ int lucid_causal_lm_loss_fwd(const void* logits, int64_t row_stride, const int64
                              float* lse, float* loss, float* valid, void* stream);
 int lucid_causal_lm_loss_bwd(const void* logits, int64_t row_stride, const int64_t* labels, int R, int T, int V,
                              const float* lse, const float* valid, const float* scale, void* dlogits, void* stream);
+
+/* One AdamW step (decoupled weight decay) over n parameter tensors, the update of
+ * torch.optim.AdamW, the default optimizer of the HF Trainer that the reference's training
+ * script builds (run_clm_chunk.py:776; no counterpart in modeling_lucid.py):
+ *   p <- p (1 - lr wd);  m <- m + (1 - beta1)(g - m);  v <- beta2 v + (1 - beta2) g^2;
+ *   p <- p - lr / (1 - beta1^step) * m / (sqrt(v) / sqrt(1 - beta2^step) + eps)
+ * in fp32, each stored value rounded once.  params / grads / exp_avgs / exp_avg_sqs are host
+ * arrays of n device pointers to contiguous tensors of numels[i] elements, all of one dtype
+ * (LUCID_DTYPE_BF16 or LUCID_DTYPE_F32), each aligned to 8 elements; step (>= 1) is the
+ * count after this update.  One launch per 48 tensors. */
+int lucid_adamw_step(int n, void* const* params, const void* const* grads, void* const* exp_avgs,
+                     void* const* exp_avg_sqs, const int64_t* numels, int dtype, float lr, float beta1, float beta2,
+                     float eps, float weight_decay, int64_t step, void* stream);
 
 /* Per-kernel timing (no counterpart in the reference; used by bench.py).
  * When enabled, every launch is bracketed by two HIP events on its stream.

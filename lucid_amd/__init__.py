@@ -8,6 +8,8 @@ Operator entry points (drop-ins for the reference seams):
 * :func:`lucid_amd.lucid.set_precision` (bf16 or hi/lo-split chain products, chosen per head by default)
 * :func:`lucid_amd.lucid.set_fused_forward` (one fused chain + attention kernel, or two kernels)
 * :mod:`lucid_amd.modeling_lucid` (the reference model file's classes on these operators)
+* :mod:`lucid_amd.model_ops` (fused RMSNorm, RoPE, SwiGLU gate and causal-LM loss of the decoder)
+* :mod:`lucid_amd.optim` (AdamW on one HIP pass per step)
 * :mod:`lucid_amd.lucid_path` (LUCID-Path and PaTH softmax attention)
 """
 from .lucid import (LucidAttentionFunction, causal_attention, eager_lucid_attention_forward, get_fused_forward,

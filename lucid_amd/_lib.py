@@ -89,6 +89,8 @@ _SIGS = {
         "lucid_swiglu_bwd": ([_vp, _vp, _vp, _vp, _vp, ctypes.c_int64, _vp], _int),
         "lucid_causal_lm_loss_fwd": ([_vp, ctypes.c_int64, _vp, _int, _int, _int, _vp, _vp, _vp, _vp], _int),
         "lucid_causal_lm_loss_bwd": ([_vp, ctypes.c_int64, _vp, _int, _int, _int, _vp, _vp, _vp, _vp, _vp], _int),
+        "lucid_adamw_step": ([_int, _vp, _vp, _vp, _vp, _i64p, _int, _flt, _flt, _flt, _flt, _flt, ctypes.c_int64,
+                              _vp], _int),
         "lucid_decode_tokens": ([_vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _vp,
                                  _int, _int, _int, _int, _int, _int, _int, _flt, _flt, _vp], _int),
         "lucid_profile_enable": ([_int], None),

@@ -1432,4 +1432,57 @@ int lucid_causal_lm_loss_bwd(const void* logits, int64_t row_stride, const int64
   return LUCID_OK;
 }
 
+int lucid_adamw_step(int n, void* const* params, const void* const* grads, void* const* exp_avgs,
+                     void* const* exp_avg_sqs, const int64_t* numels, int dtype, float lr, float beta1, float beta2,
+                     float eps, float weight_decay, int64_t step, void* stream) {
+  g_last_error.clear();
+  if (n < 0 || (dtype != LUCID_DTYPE_BF16 && dtype != LUCID_DTYPE_F32) || step < 1)
+    return fail("lucid_adamw_step: n >= 0, dtype LUCID_DTYPE_BF16 or LUCID_DTYPE_F32 and step >= 1");
+  if (!(lr >= 0.f) || !(beta1 >= 0.f && beta1 < 1.f) || !(beta2 >= 0.f && beta2 < 1.f) || !(eps >= 0.f) ||
+      !(weight_decay >= 0.f))
+    return fail("lucid_adamw_step: lr, eps and weight_decay >= 0, betas in [0, 1)");
+  const size_t es = dtype == LUCID_DTYPE_F32 ? 4 : 2;
+  for (int i = 0; i < n; ++i) {
+    if (numels[i] < 0 || numels[i] > (int64_t)INT32_MAX * lucid::kAdamChunk / 2)
+      return fail("lucid_adamw_step: tensor " + std::to_string(i) + " has a bad element count");
+    for (const void* ptr : {(const void*)params[i], grads[i], (const void*)exp_avgs[i], (const void*)exp_avg_sqs[i]})
+      if (reinterpret_cast<uintptr_t>(ptr) % (8 * es))
+        return fail("lucid_adamw_step: tensor " + std::to_string(i) + " is not aligned to 8 elements");
+  }
+  lucid::AdamWScalars c;
+  c.decay = 1.0f - lr * weight_decay;
+  c.b1 = beta1;
+  c.b2 = beta2;
+  c.eps = eps;
+  c.step_size = (float)((double)lr / (1.0 - std::pow((double)beta1, (double)step)));
+  c.inv_bc2 = (float)(1.0 / std::sqrt(1.0 - std::pow((double)beta2, (double)step)));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  lucid::AdamWBatch batch;
+  int i = 0;
+  while (i < n) {
+    batch.n = 0;
+    int64_t chunks = 0;
+    for (; i < n && batch.n < lucid::kAdamMaxTensors; ++i) {
+      if (numels[i] == 0) continue;
+      const int64_t nc = (numels[i] + lucid::kAdamChunk - 1) / lucid::kAdamChunk;
+      if (batch.n > 0 && chunks + nc > INT32_MAX) break;
+      const int k = batch.n++;
+      batch.p[k] = params[i];
+      batch.g[k] = grads[i];
+      batch.m[k] = exp_avgs[i];
+      batch.v[k] = exp_avg_sqs[i];
+      batch.numel[k] = numels[i];
+      batch.chunk0[k] = (int)chunks;
+      chunks += nc;
+    }
+    if (batch.n == 0) continue;
+    batch.chunk0[batch.n] = (int)chunks;
+    if (dtype == LUCID_DTYPE_F32)
+      LUCID_LAUNCH("lucid_adamw_kernel", lucid::lucid_adamw_kernel<float>, dim3((unsigned)chunks), st, batch, c);
+    else
+      LUCID_LAUNCH("lucid_adamw_kernel", lucid::lucid_adamw_kernel<bf16>, dim3((unsigned)chunks), st, batch, c);
+  }
+  return LUCID_OK;
+}
+
 }  // extern "C"

@@ -13,13 +13,19 @@
 //                                 its transpose for the backward), one rounding to bf16
 //   lucid_swiglu_fwd/bwd_kernel   h = silu(g) u (modeling_lucid.py:155-167 between the gate / up
 //                                 and down projections) and its gradients, fp32 inside
+//   lucid_adamw_kernel            one AdamW update over up to kAdamMaxTensors parameter
+//                                 tensors per launch (p, grad, exp_avg, exp_avg_sq; fp32 math)
 //   lucid_ce_fwd/bwd_kernel       the shifted causal-LM cross entropy on bf16 logits
 //                                 (modeling_lucid.py:847-967: labels shifted by one, -100
 //                                 ignored): per-row logsumexp and loss in one read of the row;
 //                                 backward (softmax - onehot) scale written as bf16
+#include <type_traits>
+
 #include "lucid_common.h"
 
 namespace lucid {
+
+typedef float f32x8_t __attribute__((ext_vector_type(8)));
 
 constexpr int kNormRowsPerBlock = 16;  // rows per workgroup of the backward (one dw partial each)
 constexpr int kDwWaves = 16;           // waves of the dw reduction workgroup (256 columns each)
@@ -337,6 +343,81 @@ __global__ __launch_bounds__(256) void lucid_ce_bwd_kernel(const bf16* __restric
       for (int e = 0; e < 8; ++e) o[e] = (bf16)0.f;
     }
     *reinterpret_cast<bf16x8*>(drow + j) = o;
+  }
+}
+
+// AdamW (decoupled weight decay, Loshchilov & Hutter), the update of torch.optim.AdamW:
+//   p <- p (1 - lr wd);  m <- m + (1 - b1) (g - m);  v <- b2 v + (1 - b2) g^2
+//   p <- p - step_size m / (sqrt(v) / sqrt(1 - b2^t) + eps),  step_size = lr / (1 - b1^t)
+// in fp32 with one rounding per stored value.  A launch covers up to kAdamMaxTensors tensors
+// (pointers in the kernel argument), cut into chunks of kAdamChunk elements: workgroup c
+// finds its tensor in the chunk prefix sums.  8 elements per lane (16- or 32-byte accesses
+// when the tensor's base is aligned, which the host checks), a scalar tail.
+constexpr int kAdamMaxTensors = 48;
+constexpr int kAdamChunk = 256 * 8;
+
+struct AdamWBatch {
+  void* p[kAdamMaxTensors];
+  const void* g[kAdamMaxTensors];
+  void* m[kAdamMaxTensors];
+  void* v[kAdamMaxTensors];
+  int64_t numel[kAdamMaxTensors];
+  int chunk0[kAdamMaxTensors + 1];  // first chunk of each tensor; chunk0[n] = the grid size
+  int n;
+};
+
+struct AdamWScalars {
+  float decay;       // 1 - lr wd
+  float b1, b2, eps;
+  float step_size;   // lr / (1 - b1^t)
+  float inv_bc2;     // 1 / sqrt(1 - b2^t)
+};
+
+template <typename T>
+__device__ __forceinline__ void adamw_one(T& p, float g, T& m, T& v, const AdamWScalars& c) {
+  float pf = (float)p * c.decay;
+  const float mf = (float)m + (1.0f - c.b1) * (g - (float)m);
+  const float vf = c.b2 * (float)v + (1.0f - c.b2) * g * g;
+  pf -= c.step_size * mf / (sqrtf(vf) * c.inv_bc2 + c.eps);
+  p = (T)pf;
+  m = (T)mf;
+  v = (T)vf;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void lucid_adamw_kernel(const AdamWBatch batch, const AdamWScalars c) {
+  const int chunk = blockIdx.x;
+  int lo = 0, hi = batch.n - 1;  // the tensor i with chunk0[i] <= chunk < chunk0[i + 1]
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (batch.chunk0[mid] <= chunk) lo = mid;
+    else hi = mid - 1;
+  }
+  const int i = lo;
+  T* p = static_cast<T*>(batch.p[i]);
+  const T* g = static_cast<const T*>(batch.g[i]);
+  T* m = static_cast<T*>(batch.m[i]);
+  T* v = static_cast<T*>(batch.v[i]);
+  const int64_t n = batch.numel[i];
+  const int64_t e0 = (int64_t)(chunk - batch.chunk0[i]) * kAdamChunk + threadIdx.x * 8;
+  if (e0 + 8 <= n) {
+    using V8 = std::conditional_t<std::is_same_v<T, float>, f32x8_t, bf16x8>;
+    V8 pv = *reinterpret_cast<const V8*>(p + e0), mv = *reinterpret_cast<const V8*>(m + e0);
+    V8 vv = *reinterpret_cast<const V8*>(v + e0);
+    const V8 gv = *reinterpret_cast<const V8*>(g + e0);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      T pe = pv[e], me = mv[e], ve = vv[e];
+      adamw_one<T>(pe, (float)gv[e], me, ve, c);
+      pv[e] = pe;
+      mv[e] = me;
+      vv[e] = ve;
+    }
+    *reinterpret_cast<V8*>(p + e0) = pv;
+    *reinterpret_cast<V8*>(m + e0) = mv;
+    *reinterpret_cast<V8*>(v + e0) = vv;
+  } else {
+    for (int64_t e = e0; e < n; ++e) adamw_one<T>(p[e], (float)g[e], m[e], v[e], c);
   }
 }
 

@@ -66,6 +66,39 @@ def test_precision_mode_roundtrip_and_validation(built):
     assert b"precision" in lib.lucid_last_error() and lib.lucid_get_precision() == 0
 
 
+def test_decoder_layer_and_optimizer_validation_without_gpu(built):
+    """The fused decoder layers and the AdamW step reject bad shapes, pointers and
+    hyper-parameters before anything is launched."""
+    from lucid_amd import _lib
+    lib = _lib.load()
+    dummy = ctypes.c_void_p(1 << 20)
+    rc = lib.lucid_rmsnorm_fwd(dummy, dummy, dummy, dummy, 4, 768, 1e-5, None)
+    assert rc == _lib.LUCID_EINVAL and b"H must be" in lib.lucid_last_error()
+    s = (ctypes.c_int64 * 3)(64, 64, 64)
+    rc = lib.lucid_rope(dummy, s, 1, 1, 1, dummy, dummy, dummy, 128, 0, None)
+    assert rc == _lib.LUCID_EINVAL and b"head dim 64" in lib.lucid_last_error()
+    odd = (ctypes.c_int64 * 3)(68, 68, 68)
+    rc = lib.lucid_rope(dummy, odd, 1, 1, 1, dummy, dummy, dummy, 64, 0, None)
+    assert rc == _lib.LUCID_EINVAL and b"multiples of 8" in lib.lucid_last_error()
+    rc = lib.lucid_swiglu_fwd(ctypes.c_void_p((1 << 20) + 2), dummy, dummy, 64, None)
+    assert rc == _lib.LUCID_EINVAL and b"aligned" in lib.lucid_last_error()
+    rc = lib.lucid_causal_lm_loss_fwd(dummy, 100, dummy, 4, 4, 100, dummy, dummy, dummy, None)
+    assert rc == _lib.LUCID_EINVAL and b"multiples of 8" in lib.lucid_last_error()
+    rc = lib.lucid_causal_lm_loss_fwd(dummy, 64, dummy, 6, 4, 64, dummy, dummy, dummy, None)
+    assert rc == _lib.LUCID_EINVAL and b"multiple of T" in lib.lucid_last_error()
+
+    def adamw(ptr, numel, dtype=0, beta2=0.999, step=1):
+        arrs = [(ctypes.c_void_p * 1)(ptr) for _ in range(4)]
+        return lib.lucid_adamw_step(1, *arrs, (ctypes.c_int64 * 1)(numel), dtype, 1e-3, 0.9, beta2, 1e-8, 0.01,
+                                    step, None)
+    assert adamw(1 << 20, 8, dtype=2) == _lib.LUCID_EINVAL
+    assert adamw(1 << 20, 8, step=0) == _lib.LUCID_EINVAL
+    assert adamw(1 << 20, 8, beta2=1.0) == _lib.LUCID_EINVAL and b"betas" in lib.lucid_last_error()
+    assert adamw((1 << 20) + 16, 8, dtype=1) == _lib.LUCID_EINVAL and b"aligned" in lib.lucid_last_error()
+    assert adamw(1 << 20, -1) == _lib.LUCID_EINVAL and b"element count" in lib.lucid_last_error()
+    assert lib.lucid_adamw_step(0, None, None, None, None, None, 0, 1e-3, 0.9, 0.999, 1e-8, 0.0, 1, None) == 0
+
+
 def test_argument_validation_without_gpu(built):
     from lucid_amd import _lib
     lib = _lib.load()
