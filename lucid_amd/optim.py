@@ -41,6 +41,10 @@ class AdamW(torch.optim.Optimizer):
                 loss = closure()
         lib = _lib.load()
         for group in self.param_groups:
+            # groups loaded from a torch.optim.AdamW state dict carry its flags: refuse the
+            # variants this update does not implement rather than ignore them
+            if group.get("amsgrad") or group.get("maximize"):
+                raise ValueError("lucid_amd.optim.AdamW: amsgrad and maximize are not supported")
             # one C call per (device, dtype, step count): the bias corrections are per call
             batches: dict[tuple, list] = {}
             for p in group["params"]:

@@ -100,6 +100,16 @@ def test_adamw_bf16_matches_torch_fused():
         assert e_ours <= 1.05 * e_torch, (key, e_ours, e_torch)
 
 
+def test_adamw_refuses_amsgrad_groups_from_torch_state_dicts():
+    p = torch.nn.Parameter(torch.randn(16, device="cuda"))
+    p.grad = torch.randn(16, device="cuda")
+    opt = AdamW([p])
+    sd = torch.optim.AdamW([torch.nn.Parameter(torch.randn(16, device="cuda"))], amsgrad=True).state_dict()
+    opt.load_state_dict(sd)
+    with pytest.raises(ValueError):
+        opt.step()
+
+
 def test_adamw_rejects_cpu_and_fp16_parameters():
     p = torch.nn.Parameter(torch.randn(8))
     p.grad = torch.randn(8)
