@@ -227,3 +227,23 @@ def test_stacked_qkv_projection_matches_separate_projections(monkeypatch):
         assert a.shape == b.shape
         rel = ((a - b).norm() / b.norm()).item()
         assert rel < 2e-2, (name, rel)
+
+
+def test_empty_and_single_position_inputs():
+    """Empty batches and one-position sequences: the same shapes and values as the torch
+    expressions (an empty RMSNorm batch has a zero weight gradient; a one-position sequence
+    has no loss targets, so the mean is NaN as in torch)."""
+    x = torch.zeros(0, 512, dtype=torch.bfloat16, device="cuda", requires_grad=True)
+    w = torch.ones(512, dtype=torch.bfloat16, device="cuda", requires_grad=True)
+    y = O.rms_norm(x, w, 1e-5)
+    y.sum().backward()
+    assert y.shape == (0, 512) and x.grad.shape == (0, 512) and bool((w.grad == 0).all())
+    g = torch.zeros(0, 64, dtype=torch.bfloat16, device="cuda")
+    assert O.swiglu(g, g).shape == (0, 64)
+    xr = torch.randn(2, 3, 1, 64, dtype=torch.bfloat16, device="cuda")
+    emb = M.LlamaRotaryEmbedding(M.LucidConfig(hidden_size=192, num_attention_heads=3, head_dim=64), device="cuda")
+    cos, sin = emb(xr, torch.zeros(2, 1, dtype=torch.int64, device="cuda"))
+    assert _rel(O.apply_rope(xr, cos, sin), xr.float()) <= BAR  # position 0: the identity
+    logits = torch.randn(2, 1, 64, dtype=torch.bfloat16, device="cuda")
+    labels = torch.zeros(2, 1, dtype=torch.int64, device="cuda")
+    assert torch.isnan(O.causal_lm_loss(logits, labels)).item() and torch.isnan(_ce_ref(logits, labels)).item()

@@ -119,3 +119,14 @@ def test_adamw_rejects_cpu_and_fp16_parameters():
     q.grad = torch.randn(8, dtype=torch.float16, device="cuda")
     with pytest.raises(TypeError):
         AdamW([q]).step()
+
+
+def test_adamw_skips_empty_and_gradless_parameters():
+    empty = torch.nn.Parameter(torch.zeros(0, device="cuda"))
+    empty.grad = torch.zeros(0, device="cuda")
+    idle = torch.nn.Parameter(torch.ones(8, device="cuda"))
+    opt = AdamW([empty, idle], lr=0.1)
+    opt.step()
+    torch.cuda.synchronize()
+    assert bool((idle.detach() == 1).all()) and idle not in opt.state
+    assert int(opt.state[empty]["step"]) == 1
