@@ -116,14 +116,27 @@ def _fwd_f32(q, k, v, scale, eps, dn):
     return o, vprime, lse, ws
 
 
-def _bwd_f32(do, q, k, o, lse, ws, scale, dn):
+def _grad_buf(B, H, T, D, dtype, dev, time_major):
+    """A [B, H, T, D] gradient buffer; time_major: stored as [B, T, H, D] (the layout of the
+    usual ``proj(x).view(B, T, H, D).transpose(1, 2)`` operands, whose view backward then
+    needs no copy)."""
+    if time_major:
+        return torch.empty(B, T, H, D, dtype=dtype, device=dev).transpose(1, 2)
+    return torch.empty(B, H, T, D, dtype=dtype, device=dev)
+
+
+def _time_major(x: torch.Tensor) -> bool:
+    return x.dim() == 4 and x.shape[1] > 1 and x.stride(1) < x.stride(2)
+
+
+def _bwd_f32(do, q, k, o, lse, ws, scale, dn, layouts=(False, False, False)):
     lib = _lib.load()
     B, Hq, T, D = q.shape
     Hkv = k.shape[1]
     dev = q.device
-    dq = torch.empty(B, Hq, T, D, dtype=torch.float32, device=dev)
-    dk = torch.empty(B, Hkv, T, D, dtype=torch.float32, device=dev)
-    dv = torch.empty(B, Hkv, T, D, dtype=torch.float32, device=dev)
+    dq = _grad_buf(B, Hq, T, D, torch.float32, dev, layouts[0])
+    dk = _grad_buf(B, Hkv, T, D, torch.float32, dev, layouts[1])
+    dv = _grad_buf(B, Hkv, T, D, torch.float32, dev, layouts[2])
     bws = torch.empty(lib.lucid_bwd_f32_workspace_bytes(B, Hq, Hkv, T, dn), dtype=torch.uint8, device=dev)
     rc = lib.lucid_attn_bwd_f32(
         _lib.ptr(do), _lib.strides3(do, (0, 2, 1)), _lib.ptr(o), _lib.strides3(o, (0, 2, 1)),
@@ -134,14 +147,14 @@ def _bwd_f32(do, q, k, o, lse, ws, scale, dn):
     return dq, dk, dv
 
 
-def _bwd(do, q, k, o, lse, ws, scale, eps, dn):
+def _bwd(do, q, k, o, lse, ws, scale, eps, dn, layouts=(False, False, False)):
     lib = _lib.load()
     B, Hq, T, D = q.shape
     Hkv = k.shape[1]
     dev = q.device
-    dq = torch.empty(B, Hq, T, D, dtype=torch.bfloat16, device=dev)
-    dk = torch.empty(B, Hkv, T, D, dtype=torch.bfloat16, device=dev)
-    dv = torch.empty(B, Hkv, T, D, dtype=torch.bfloat16, device=dev)
+    dq = _grad_buf(B, Hq, T, D, torch.bfloat16, dev, layouts[0])
+    dk = _grad_buf(B, Hkv, T, D, torch.bfloat16, dev, layouts[1])
+    dv = _grad_buf(B, Hkv, T, D, torch.bfloat16, dev, layouts[2])
     bws = torch.empty(lib.lucid_bwd_workspace_bytes(B, Hq, Hkv, T, dn), dtype=torch.uint8, device=dev)
     rc = lib.lucid_attn_bwd(
         _lib.ptr(do), _lib.strides3(do, (0, 2, 1)), _lib.ptr(q), _lib.strides3(q, (0, 1, 2)),
@@ -175,6 +188,8 @@ class LucidAttentionFunction(torch.autograd.Function):
         o, vprime, lse, ws = (_fwd_f32 if ctx.f32 else _fwd)(qp, kp, vp_, scale, eps, dn)
         ctx.save_for_backward(qp, kp, o, lse, ws)
         ctx.scale, ctx.eps, ctx.t, ctx.dn = scale, eps, t, dn
+        # the gradients are written in the memory order of the operands they belong to
+        ctx.layouts = (_time_major(q), _time_major(k), _time_major(v))
         ctx.mark_non_differentiable(vprime)
         # no zero-filled gradient for the V' output, which the backward ignores (a T x d fp32
         # fill per call otherwise)
@@ -198,9 +213,9 @@ class LucidAttentionFunction(torch.autograd.Function):
         if do.stride(-1) != 1 or any(s % 8 for s in do.stride()) or do.data_ptr() % 16:
             do = do.contiguous()
         if ctx.f32:
-            dq, dk, dv = _bwd_f32(do, qp, kp, o, lse, ws, ctx.scale, ctx.dn)
+            dq, dk, dv = _bwd_f32(do, qp, kp, o, lse, ws, ctx.scale, ctx.dn, ctx.layouts)
         else:
-            dq, dk, dv = _bwd(do, qp, kp, o, lse, ws, ctx.scale, ctx.eps, ctx.dn)
+            dq, dk, dv = _bwd(do, qp, kp, o, lse, ws, ctx.scale, ctx.eps, ctx.dn, ctx.layouts)
         return dq[:, :, :t], dk[:, :, :t], dv[:, :, :t], None, None, None
 
 

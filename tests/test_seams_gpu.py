@@ -153,3 +153,32 @@ def test_seams_reject_a_non_causal_mask():
     get_v_prime(k, v, None, causal)
     with pytest.raises(NotImplementedError):
         eager_lucid_attention_forward(q, k, v, None, 1e-5)
+
+
+@pytest.mark.parametrize("dtype,B,Hq,Hkv,T,D", [(torch.bfloat16, 2, 4, 2, 200, 64),
+                                                (torch.bfloat16, 1, 4, 4, 256, 128),
+                                                (torch.float32, 1, 4, 2, 256, 68)])
+def test_gradients_follow_the_operand_layout(dtype, B, Hq, Hkv, T, D):
+    """Operands given as [B, T, H, d] memory (the projections' view(...).transpose(1, 2)) get
+    their gradients in that memory order (head dims 64 and 128, which are not copied into a
+    padded buffer), and the values are those of the same call on contiguous [B, H, T, d]
+    operands, bit for bit (the same kernels, other output strides)."""
+    from lucid_amd import lucid_attention
+    print(f"case layouts {dtype} B={B} Hq={Hq} Hkv={Hkv} T={T} D={D}", flush=True)
+    q, k, v, do = (x.to(dtype).cuda() for x in _inputs(B, Hq, Hkv, T, D, 11))
+    grads = {}
+    for tm in (False, True):
+        leaves = [(x.transpose(1, 2).contiguous() if tm else x.clone()).requires_grad_() for x in (q, k, v)]
+        ops = [x.transpose(1, 2) if tm else x.view(x.shape) for x in leaves]  # non-leaf views
+        seen = []
+        for x in ops:  # the gradient as the attention backward returns it
+            x.register_hook(lambda g_: seen.append((g_.stride(1) < g_.stride(2), g_.clone())))
+        o = lucid_attention(*ops)
+        o.backward(do)
+        torch.cuda.synchronize()
+        assert len(seen) == 3
+        if D in (64, 128):  # other head dims pass through a zero-padded copy of the operands
+            assert all(s_[0] == tm for s_ in seen), [s_[0] for s_ in seen]
+        grads[tm] = [o.detach()] + [s_[1] for s_ in seen]
+    for a, b in zip(grads[False], grads[True]):
+        assert torch.equal(a, b)
