@@ -156,6 +156,7 @@ def test_seams_reject_a_non_causal_mask():
 
 
 @pytest.mark.parametrize("dtype,B,Hq,Hkv,T,D", [(torch.bfloat16, 2, 4, 2, 200, 64),
+                                                (torch.bfloat16, 3, 2, 2, 384, 64),
                                                 (torch.bfloat16, 1, 4, 4, 256, 128),
                                                 (torch.float32, 1, 4, 2, 256, 68)])
 def test_gradients_follow_the_operand_layout(dtype, B, Hq, Hkv, T, D):
