@@ -103,7 +103,9 @@ struct DkdvSmem {
 // F32 (fp32 inputs, head dim 64): the lo tiles of Q and dO are staged beside the hi tiles,
 // K and V' carry their lo parts in registers, and every product (dV', dP, dK) takes
 // three MFMAs (S = Q.K four, lo*lo included); P and dS are split into hi and lo.
-template <int D, bool F32 = false>
+// DA: the head-dim columns that can be nonzero (zero-padded rows of a smaller head dim; the
+// products skip the k-steps and tiles that would only meet zero columns, whose outputs stay 0)
+template <int D, bool F32 = false, int DA = D>
 __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid_attn_bwd_dkdv_kernel(
     const bf16* __restrict__ q, Strides qs, const bf16* __restrict__ k, Strides ks, const bf16* __restrict__ vpb,
     const bf16* __restrict__ dout, Strides dos, const bf16* __restrict__ seeds, float* __restrict__ dvp, float* __restrict__ dka, int Hq, int Hkv, int T, int BH, float scale, Lo lo,
@@ -111,6 +113,8 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
   static_assert(!F32 || D == 64 || D == 128, "fp32 inputs: head dim 64 or 128");
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
+  constexpr int NDT_A = DA / 32, NKS_A = DA / 16;
+  static_assert(DA % 32 == 0 && DA <= D, "active head dim");
   // newest vector-memory ops of a step, per wave
   constexpr int STAGE_OPS = (F32 ? 4 : 2) * (64 * (D / 8) / 256);
   __shared__ __attribute__((aligned(16))) DkdvSmem<D, F32> sm;
@@ -128,7 +132,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
 
   bf16x8 kb[NKS], vb[NKS], kbl[NKS], vbl[NKS];
 #pragma unroll
-  for (int st = 0; st < NKS; ++st) {
+  for (int st = 0; st < NKS_A; ++st) {
     kb[st] = ld8(kh + (int64_t)jrow * ks.t + 16 * st + 8 * g);
     vb[st] = ld8(vpb + ((int64_t)bh * T + jrow) * D + 16 * st + 8 * g);
     if constexpr (F32) {
@@ -196,14 +200,14 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
       {
         bf16x8 qa[NKS];
 #pragma unroll
-        for (int st = 0; st < NKS; ++st) qa[st] = ld8(sm.q[buf] + rdo[st] + mt * 32 * D);
+        for (int st = 0; st < NKS_A; ++st) qa[st] = ld8(sm.q[buf] + rdo[st] + mt * 32 * D);
         // (lanes 32..63 read the same row: they meet the zero rows of `ones`)
         f32x16 sc = mfma32(ld8(&sm.seed[buf][mt * 32 + l32][0]), ones, zero16());
 #pragma unroll
-        for (int st = 0; st < NKS; ++st) sc = mfma32(qa[st], kb[st], sc);
+        for (int st = 0; st < NKS_A; ++st) sc = mfma32(qa[st], kb[st], sc);
         if constexpr (F32) {
 #pragma unroll
-          for (int st = 0; st < NKS; ++st) {
+          for (int st = 0; st < NKS_A; ++st) {
             const bf16x8 qal = ld8(sm.ql[buf] + rdo[st] + mt * 32 * D);
             sc = mfma32(qa[st], kbl[st], sc);
             sc = mfma32(qal, kb[st], sc);
@@ -220,7 +224,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
         pb1 = pack_b(pv, 1);
       }
 #pragma unroll
-      for (int t = 0; t < NDT; ++t) {
+      for (int t = 0; t < NDT_A; ++t) {
         const bf16x8 o0 = lds_tr_a_at2<D / 8>(sm.dO[buf], tro[t], tro2[t], mt * 32);
         const bf16x8 o1 = lds_tr_a_at2<D / 8>(sm.dO[buf], tro[t], tro2[t], mt * 32 + 16);
         adv[t] = mfma32(o0, pb0, adv[t]);
@@ -236,14 +240,14 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
       {
         bf16x8 da[NKS];
 #pragma unroll
-        for (int st = 0; st < NKS; ++st) da[st] = ld8(sm.dO[buf] + rdo[st] + mt * 32 * D);
+        for (int st = 0; st < NKS_A; ++st) da[st] = ld8(sm.dO[buf] + rdo[st] + mt * 32 * D);
         // dP - delta: the accumulator starts at -delta (stored negated)
         f32x16 dp = mfma32(ld8(&sm.seed[buf][mt * 32 + l32][8]), ones, zero16());
 #pragma unroll
-        for (int st = 0; st < NKS; ++st) dp = mfma32(da[st], vb[st], dp);
+        for (int st = 0; st < NKS_A; ++st) dp = mfma32(da[st], vb[st], dp);
         if constexpr (F32) {
 #pragma unroll
-          for (int st = 0; st < NKS; ++st) {
+          for (int st = 0; st < NKS_A; ++st) {
             dp = mfma32(da[st], vbl[st], dp);
             dp = mfma32(ld8(sm.dOl[buf] + rdo[st] + mt * 32 * D), vb[st], dp);
           }
@@ -254,7 +258,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
         pb1 = pack_b(ds, 1);
       }
 #pragma unroll
-      for (int t = 0; t < NDT; ++t) {
+      for (int t = 0; t < NDT_A; ++t) {
         const bf16x8 q0 = lds_tr_a_at2<D / 8>(sm.q[buf], tro[t], tro2[t], mt * 32);
         const bf16x8 q1 = lds_tr_a_at2<D / 8>(sm.q[buf], tro[t], tro2[t], mt * 32 + 16);
         adk[t] = mfma32(q0, pb0, adk[t]);
@@ -334,7 +338,8 @@ struct DqSmemF32 {  // fp32 inputs: the lo tiles of K and V' beside the hi tiles
 
 // WGR: rows per workgroup (256; 128 for the fp32 instance at head dim 128, whose hi/lo
 // operands need one wave per SIMD to stay in registers)
-template <int D, bool EXACT, bool F32 = false, int RW = 64, int WGR = 256>
+// DA: the head-dim columns that can be nonzero (as in lucid_attn_bwd_dkdv_kernel)
+template <int D, bool EXACT, bool F32 = false, int RW = 64, int WGR = 256, int DA = D>
 __global__ __launch_bounds__(64 * (WGR / RW)) LUCID_TWO_WAVES_IF((D == 64 || RW == 32) && !EXACT) void lucid_attn_bwd_dq_kernel(
     const bf16* __restrict__ q, Strides qs, const bf16* __restrict__ k, Strides ks, const bf16* __restrict__ vpb,
     const bf16* __restrict__ dout, Strides dos, const float* __restrict__ lse,
@@ -345,6 +350,8 @@ __global__ __launch_bounds__(64 * (WGR / RW)) LUCID_TWO_WAVES_IF((D == 64 || RW 
   static_assert(RW == 64 || RW == 32, "rows per wave");
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
+  constexpr int NDT_A = DA / 32, NKS_A = DA / 16;
+  static_assert(DA % 32 == 0 && DA <= D && (DA == D || RW == 32), "active head dim");
   constexpr int NT = RW / 32;           // 32-row n-tiles per wave
   constexpr int NTHR = 64 * (WGR / RW);  // WGR rows per workgroup
   __shared__ __attribute__((aligned(16))) std::conditional_t<F32, DqSmemF32<D>, DqSmem<D>> sm;
@@ -371,7 +378,7 @@ __global__ __launch_bounds__(64 * (WGR / RW)) LUCID_TWO_WAVES_IF((D == 64 || RW 
   for (int nt = 0; nt < NT; ++nt) {
     const int ir = min(row0 + nt * 32 + l32, T - 1);
 #pragma unroll
-    for (int st = 0; st < NKS; ++st) {
+    for (int st = 0; st < NKS_A; ++st) {
       qb[nt][st] = ld8(q + b * qs.b + hq * qs.h + (int64_t)ir * qs.t + 16 * st + 8 * g);
       db[nt][st] = ld8(dout + b * dos.b + hq * dos.h + (int64_t)ir * dos.t + 16 * st + 8 * g);
       if constexpr (F32) {
@@ -442,13 +449,13 @@ __global__ __launch_bounds__(64 * (WGR / RW)) LUCID_TWO_WAVES_IF((D == 64 || RW 
       for (int nt = 0; nt < NT; ++nt) {
         f32x16 sc = zero16(), dp = zero16();
 #pragma unroll
-        for (int st = 0; st < NKS; ++st) {
+        for (int st = 0; st < NKS_A; ++st) {
           sc = mfma32(kop(st), qb[nt][st], sc);
           dp = mfma32(vop(st), db[nt][st], dp);
         }
         if constexpr (F32) {
 #pragma unroll
-          for (int st = 0; st < NKS; ++st) {
+          for (int st = 0; st < NKS_A; ++st) {
             const bf16x8 kl8 = ld8(sm.kl[buf] + rdo[st] + mt * 32 * D);
             const bf16x8 vl8 = ld8(sm.vl[buf] + rdo[st] + mt * 32 * D);
             sc = mfma32(kop(st), qbl[nt][st], sc);
@@ -472,7 +479,7 @@ __global__ __launch_bounds__(64 * (WGR / RW)) LUCID_TWO_WAVES_IF((D == 64 || RW 
         }
       }
 #pragma unroll
-      for (int t = 0; t < NDT; ++t) {
+      for (int t = 0; t < NDT_A; ++t) {
         const bf16x8 a0 = lds_tr_a<D / 8>(sm.k[buf], mt * 32, t * 32);
         const bf16x8 a1 = lds_tr_a<D / 8>(sm.k[buf], mt * 32 + 16, t * 32);
 #pragma unroll

@@ -535,11 +535,19 @@ int launch_precond_fwd_f32(const void* k, const int64_t* ks, const void* v, cons
   return LUCID_OK;
 }
 
+// The head-dim columns the attention products of the fp32 kernels run over: rows of a head
+// dim in (64, 96] are zero-padded to 128 and only the first 96 columns can be nonzero.
+// dn: the caller's head dim (<= 0: unknown, all of D).
+template <int D>
+bool narrow_dims(float dn) {
+  return D == 128 && dn > 0.f && dn <= 96.f;
+}
+
 // O = softmax(s Q K^T, causal) V' on the split Q (split here), the centred keys and V' in
 // w.  lse is the row normaliser of the scores against the centred keys.
 template <int D>
 int launch_attn_fwd_f32(const void* q, const int64_t* qs, void* o, const int64_t* os, float* lse, const FwdWs& w,
-                        int B, int Hq, int Hkv, int T, float scale, hipStream_t st) {
+                        int B, int Hq, int Hkv, int T, float scale, float dn, hipStream_t st) {
   const int BHq = B * Hq;
   if (int rc = launch_split<D>(q, qs, B, Hq, T, w.qh, w.ql, st)) return rc;
   lucid::Lo lo{};
@@ -548,10 +556,18 @@ int launch_attn_fwd_f32(const void* q, const int64_t* qs, void* o, const int64_t
   // head dim 128: one 32-row n-tile per wave (128 rows per workgroup), so that the hi/lo
   // operands stay in registers
   constexpr int NT = D == 128 ? 1 : 2;
-  LUCID_LAUNCH("lucid_attn_fwd_f32_kernel", (lucid::lucid_attn_fwd_kernel<D, true, NT>),
-               dim3(((T + 128 * NT - 1) / (128 * NT)) * BHq), st, w.qh, rows_strides(Hq, T, D), w.kch,
-               rows_strides(Hkv, T, D), w.vpt, (float*)o, S(os), lse, w.mass, w.olo, Hq, Hkv, T, BHq, scale, lo,
-               w.vptl, 0);
+  const dim3 grid(((T + 128 * NT - 1) / (128 * NT)) * BHq);
+  if constexpr (D == 128) {
+    if (narrow_dims<D>(dn)) {
+      LUCID_LAUNCH("lucid_attn_fwd_f32_kernel", (lucid::lucid_attn_fwd_kernel<D, true, NT, 96>), grid, st, w.qh,
+                   rows_strides(Hq, T, D), w.kch, rows_strides(Hkv, T, D), w.vpt, (float*)o, S(os), lse, w.mass,
+                   w.olo, Hq, Hkv, T, BHq, scale, lo, w.vptl, 0);
+      return LUCID_OK;
+    }
+  }
+  LUCID_LAUNCH("lucid_attn_fwd_f32_kernel", (lucid::lucid_attn_fwd_kernel<D, true, NT>), grid, st, w.qh,
+               rows_strides(Hq, T, D), w.kch, rows_strides(Hkv, T, D), w.vpt, (float*)o, S(os), lse, w.mass, w.olo,
+               Hq, Hkv, T, BHq, scale, lo, w.vptl, 0);
   return LUCID_OK;
 }
 
@@ -561,7 +577,7 @@ int launch_fwd_f32(const void* q, const int64_t* qs, const void* k, const int64_
                    int Hq, int Hkv, int T, float scale, float eps, float dn, hipStream_t st) {
   if (int rc = launch_precond_fwd_f32<D>(k, ks, v, vs, vprime, w, B, Hkv, T, scale, eps, dn, st)) return rc;
   if (int rc = launch_centered_keys<D>(k, ks, w, B, Hkv, T, st)) return rc;
-  return launch_attn_fwd_f32<D>(q, qs, o, os, lse, w, B, Hq, Hkv, T, scale, st);
+  return launch_attn_fwd_f32<D>(q, qs, o, os, lse, w, B, Hq, Hkv, T, scale, dn, st);
 }
 
 // The attention part of the backward: delta (from fp32 dO and O), dV' and the softmax dK
@@ -570,7 +586,7 @@ int launch_fwd_f32(const void* q, const int64_t* qs, const void* k, const int64_
 template <int D>
 int launch_attn_bwd_f32(const void* dout, const int64_t* dos, const void* o, const int64_t* os, const float* lse,
                         const FwdWs& f, void* dq, const int64_t* dqs, const BwdWs& w, int B, int Hq, int Hkv, int T,
-                        float scale, hipStream_t st) {
+                        float scale, float dn, hipStream_t st) {
   const int BH = B * Hkv, BHq = B * Hq;
   const lucid::Strides cq = rows_strides(Hq, T, D), ck = rows_strides(Hkv, T, D);
   if (int rc = launch_split<D>(dout, dos, B, Hq, T, w.doh, w.dol, st)) return rc;
@@ -584,14 +600,25 @@ int launch_attn_bwd_f32(const void* dout, const int64_t* dos, const void* o, con
   LUCID_LAUNCH("lucid_bwd_prep_f32_kernel", (lucid::lucid_bwd_prep_kernel<D, true>), dim3(T / 64, BHq), st,
                (const bf16*)dout, S(dos), (const bf16*)o, S(os), f.olo, f.mass, Hq, Hkv, T, w.delta, w.counters, BH,
                lo, lse, 1.f / (scale * LOG2E_F), w.seeds);
-  LUCID_LAUNCH("lucid_attn_bwd_dkdv_f32_kernel", (lucid::lucid_attn_bwd_dkdv_kernel<D, true>), dim3((T / 128) * BH),
-               st, f.qh, cq, f.kch, ck, f.vpb, w.doh, cq, w.seeds, w.dvp, w.dka, Hq, Hkv, T, BH, scale, lo, f.vpbl);
-  // head dim 128: four waves of 32 rows (128 rows per workgroup, one wave per SIMD), so that
-  // the hi/lo operands of a wave stay in registers
+  // head dim 128: four waves of 32 rows for dQ (128 rows per workgroup, one wave per SIMD),
+  // so that the hi/lo operands of a wave stay in registers
   constexpr int RW = D == 128 ? 32 : 64, WGR = D == 128 ? 128 : 256;
-  LUCID_LAUNCH_B("lucid_attn_bwd_dq_f32_kernel", (lucid::lucid_attn_bwd_dq_kernel<D, true, true, RW, WGR>),
-                 dim3(((T + WGR - 1) / WGR) * BHq), dim3(64 * (WGR / RW)), st, f.qh, cq, f.kch, ck, f.vpb, w.doh, cq,
-                 lse, w.delta, f.mass, (float*)dq, S(dqs), Hq, Hkv, T, BHq, scale, lo, f.vpbl);
+  const dim3 gkv((T / 128) * BH), gq(((T + WGR - 1) / WGR) * BHq), bq(64 * (WGR / RW));
+  if constexpr (D == 128) {
+    if (narrow_dims<D>(dn)) {
+      LUCID_LAUNCH("lucid_attn_bwd_dkdv_f32_kernel", (lucid::lucid_attn_bwd_dkdv_kernel<D, true, 96>), gkv, st,
+                   f.qh, cq, f.kch, ck, f.vpb, w.doh, cq, w.seeds, w.dvp, w.dka, Hq, Hkv, T, BH, scale, lo, f.vpbl);
+      LUCID_LAUNCH_B("lucid_attn_bwd_dq_f32_kernel", (lucid::lucid_attn_bwd_dq_kernel<D, true, true, RW, WGR, 96>),
+                     gq, bq, st, f.qh, cq, f.kch, ck, f.vpb, w.doh, cq, lse, w.delta, f.mass, (float*)dq, S(dqs), Hq,
+                     Hkv, T, BHq, scale, lo, f.vpbl);
+      return LUCID_OK;
+    }
+  }
+  LUCID_LAUNCH("lucid_attn_bwd_dkdv_f32_kernel", (lucid::lucid_attn_bwd_dkdv_kernel<D, true>), gkv, st, f.qh, cq,
+               f.kch, ck, f.vpb, w.doh, cq, w.seeds, w.dvp, w.dka, Hq, Hkv, T, BH, scale, lo, f.vpbl);
+  LUCID_LAUNCH_B("lucid_attn_bwd_dq_f32_kernel", (lucid::lucid_attn_bwd_dq_kernel<D, true, true, RW, WGR>), gq, bq,
+                 st, f.qh, cq, f.kch, ck, f.vpb, w.doh, cq, lse, w.delta, f.mass, (float*)dq, S(dqs), Hq, Hkv, T,
+                 BHq, scale, lo, f.vpbl);
   return LUCID_OK;
 }
 
@@ -621,7 +648,7 @@ int launch_bwd_f32(const void* dout, const int64_t* dos, const void* o, const in
                    const FwdWs& f, void* dq, const int64_t* dqs, void* dk, const int64_t* dks, void* dv,
                    const int64_t* dvs, const BwdWs& w, int B, int Hq, int Hkv, int T, float scale, float dn,
                    hipStream_t st) {
-  if (int rc = launch_attn_bwd_f32<D>(dout, dos, o, os, lse, f, dq, dqs, w, B, Hq, Hkv, T, scale, st)) return rc;
+  if (int rc = launch_attn_bwd_f32<D>(dout, dos, o, os, lse, f, dq, dqs, w, B, Hq, Hkv, T, scale, dn, st)) return rc;
   return launch_precond_bwd_f32<D>(f, dk, dks, dv, dvs, w, w.dka, B, Hkv, T, scale, dn, st);
 }
 
@@ -637,16 +664,16 @@ int launch_attn_vp_fwd_f32(const void* q, const int64_t* qs, const void* k, cons
   LUCID_LAUNCH("lucid_vp_layout_f32_kernel", (lucid::lucid_vp_layout_kernel<D, float, true>), dim3(T / 64, BH), st,
                w.kch, rows_strides(Hkv, T, D), (const float*)vp, S(vs), Hkv, T, eps, dn, w.rinv, w.vpb, w.vpt, w.mass,
                kForceExact, w.vpbl, w.vptl);
-  return launch_attn_fwd_f32<D>(q, qs, o, os, lse, w, B, Hq, Hkv, T, scale, st);
+  return launch_attn_fwd_f32<D>(q, qs, o, os, lse, w, B, Hq, Hkv, T, scale, dn, st);
 }
 
 template <int D>
 int launch_attn_vp_bwd_f32(const void* dout, const int64_t* dos, const void* o, const int64_t* os, const float* lse,
                            const FwdWs& f, void* dq, const int64_t* dqs, void* dk, const int64_t* dks, void* dvp,
                            const int64_t* dvps, const BwdWs& w, int B, int Hq, int Hkv, int T, float scale,
-                           hipStream_t st) {
+                           float dn, hipStream_t st) {
   const int BH = B * Hkv;
-  if (int rc = launch_attn_bwd_f32<D>(dout, dos, o, os, lse, f, dq, dqs, w, B, Hq, Hkv, T, scale, st)) return rc;
+  if (int rc = launch_attn_bwd_f32<D>(dout, dos, o, os, lse, f, dq, dqs, w, B, Hq, Hkv, T, scale, dn, st)) return rc;
   LUCID_LAUNCH("lucid_rows_out_kernel", (lucid::lucid_rows_out_kernel<D, float>), dim3(T / 64, BH), st, w.dka,
                (float*)dk, S(dks), Hkv, T, 1.f);
   LUCID_LAUNCH("lucid_rows_out_kernel", (lucid::lucid_rows_out_kernel<D, float>), dim3(T / 64, BH), st, w.dvp,
@@ -1216,7 +1243,7 @@ int lucid_attn_vp_bwd_f32(const float* dout, const int64_t* do_strides, const fl
   const FwdWs f = carve_attn_vp(const_cast<void*>(fwd_ws), B, Hq, Hkv, T, D, true);
   const BwdWs w = carve_seam_bwd(bwd_ws, B, Hq, Hkv, T, D, true, true);
   return (padded_dim(D) == 64 ? launch_attn_vp_bwd_f32<64> : launch_attn_vp_bwd_f32<128>)(dout, do_strides, o, o_strides, lse, f, dq, dq_strides, dk, dk_strides, dvprime,
-                                dvprime_strides, w, B, Hq, Hkv, T, scale, static_cast<hipStream_t>(stream));
+                                dvprime_strides, w, B, Hq, Hkv, T, scale, (float)D, static_cast<hipStream_t>(stream));
 }
 
 size_t lucid_attn_vp_fwd_workspace_bytes(int B, int Hq, int Hkv, int T, int D) {

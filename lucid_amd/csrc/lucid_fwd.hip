@@ -895,7 +895,10 @@ __global__ __launch_bounds__(64 * NW) LUCID_TWO_WAVES_IF((D == 64 || NW == 8) &&
 // ---------------------------------------------------------------------------
 // NT: 32-row n-tiles per wave (2: 256 rows per workgroup; 1: 128 rows, for the fp32
 // instance at head dim 128, whose hi/lo operands of two n-tiles do not fit the registers)
-template <int D, bool F32 = false, int NT = 2>
+// DA: the head-dim columns that can be nonzero (a multiple of 32, <= D): rows of a smaller
+// head dim are zero-padded to D, and the products skip the k-steps and value tiles that
+// would only meet the zero columns (the outputs there stay 0)
+template <int D, bool F32 = false, int NT = 2, int DA = D>
 __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid_attn_fwd_kernel(
     const bf16* __restrict__ q, Strides qs, const bf16* __restrict__ k, Strides ks, const bf16* __restrict__ vpt,
     std::conditional_t<F32, float, bf16>* __restrict__ o, Strides os, float* __restrict__ lse,
@@ -903,6 +906,8 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
     const bf16* __restrict__ vptl, int skip_fast) {
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
+  constexpr int NDT_A = DA / 32, NKS_A = DA / 16;  // value tiles and k-steps that can be nonzero
+  static_assert(DA % 32 == 0 && DA <= D && (DA == D || NT == 1), "active head dim");
   constexpr int CH = D / 32;  // 16-byte chunks per thread for each of the K and V'^T tiles
   constexpr int NST = F32 ? 4 * CH : 2 * CH;  // staging registers (fp32 inputs: hi and lo tiles)
   __shared__ __attribute__((aligned(16))) bf16 lk[2][64][D + 8];
@@ -939,7 +944,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
   for (int nt = 0; nt < NT; ++nt) {
     const int rq = min(row0 + nt * 32 + l32, T - 1);
 #pragma unroll
-    for (int st = 0; st < NKS; ++st) {
+    for (int st = 0; st < NKS_A; ++st) {
       qb[nt][st] = ld8(qh + (int64_t)rq * qs.t + 16 * st + 8 * g);
       if constexpr (F32) qbl[nt][st] = ld8(qlh + (int64_t)rq * qs.t + 16 * st + 8 * g);
     }
@@ -1082,7 +1087,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
         for (int mt = 0; mt < 2; ++mt) {
           bf16x8 ka[NKS], kal[NKS];
 #pragma unroll
-          for (int st = 0; st < NKS; ++st) {
+          for (int st = 0; st < NKS_A; ++st) {
             ka[st] = ld8(&lk[buf][mt * 32 + l32][16 * st + 8 * g]);
             if constexpr (F32) kal[st] = ld8(&lkl[buf][mt * 32 + l32][16 * st + 8 * g]);
           }
@@ -1090,7 +1095,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
           for (int nt = 0; nt < NT; ++nt) {
             s[mt][nt] = zero16();
 #pragma unroll
-            for (int st = 0; st < NKS; ++st) {
+            for (int st = 0; st < NKS_A; ++st) {
               s[mt][nt] = mfma32(ka[st], qb[nt][st], s[mt][nt]);
               if constexpr (F32) {
                 s[mt][nt] = mfma32(ka[st], qbl[nt][st], s[mt][nt]);
@@ -1124,7 +1129,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
             m[nt] = mnew;
             lsum[nt] *= alpha;
 #pragma unroll
-            for (int t = 0; t < NDT; ++t)
+            for (int t = 0; t < NDT_A; ++t)
 #pragma unroll
               for (int e = 0; e < 16; ++e) oacc[t][nt][e] *= alpha;
           }
@@ -1148,7 +1153,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
           }
         }
 #pragma unroll
-        for (int t = 0; t < NDT; ++t) {
+        for (int t = 0; t < NDT_A; ++t) {
           bf16x8 va[4];
 #pragma unroll
           for (int k4 = 0; k4 < 4; ++k4) va[k4] = ld8(&lv[buf][t * 32 + l32][16 * k4 + 8 * g]);
