@@ -113,8 +113,8 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
   static_assert(!F32 || D == 64 || D == 128, "fp32 inputs: head dim 64 or 128");
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
-  constexpr int NDT_A = DA / 32, NKS_A = DA / 16;
-  static_assert(DA % 32 == 0 && DA <= D, "active head dim");
+  constexpr int NDT_A = (DA + 31) / 32, NKS_A = DA / 16;
+  static_assert(DA % 16 == 0 && DA <= D, "active head dim");
   // newest vector-memory ops of a step, per wave
   constexpr int STAGE_OPS = (F32 ? 4 : 2) * (64 * (D / 8) / 256);
   __shared__ __attribute__((aligned(16))) DkdvSmem<D, F32> sm;
@@ -350,8 +350,8 @@ __global__ __launch_bounds__(64 * (WGR / RW)) LUCID_TWO_WAVES_IF((D == 64 || RW 
   static_assert(RW == 64 || RW == 32, "rows per wave");
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
-  constexpr int NDT_A = DA / 32, NKS_A = DA / 16;
-  static_assert(DA % 32 == 0 && DA <= D && (DA == D || RW == 32), "active head dim");
+  constexpr int NDT_A = (DA + 31) / 32, NKS_A = DA / 16;
+  static_assert(DA % 16 == 0 && DA <= D && (DA == D || RW == 32), "active head dim");
   constexpr int NT = RW / 32;           // 32-row n-tiles per wave
   constexpr int NTHR = 64 * (WGR / RW);  // WGR rows per workgroup
   __shared__ __attribute__((aligned(16))) std::conditional_t<F32, DqSmemF32<D>, DqSmem<D>> sm;

@@ -536,11 +536,13 @@ int launch_precond_fwd_f32(const void* k, const int64_t* ks, const void* v, cons
 }
 
 // The head-dim columns the attention products of the fp32 kernels run over: rows of a head
-// dim in (64, 96] are zero-padded to 128 and only the first 96 columns can be nonzero.
-// dn: the caller's head dim (<= 0: unknown, all of D).
+// dim in (64, 96] are zero-padded to 128 and only the first 80 (d <= 80) or 96 columns can
+// be nonzero (k-steps of 16, value tiles of 32).  dn: the caller's head dim (<= 0: unknown,
+// all of D).  Returns 80, 96 or D.
 template <int D>
-bool narrow_dims(float dn) {
-  return D == 128 && dn > 0.f && dn <= 96.f;
+int active_dims(float dn) {
+  if (D != 128 || !(dn > 0.f)) return D;
+  return dn <= 80.f ? 80 : dn <= 96.f ? 96 : D;
 }
 
 // O = softmax(s Q K^T, causal) V' on the split Q (split here), the centred keys and V' in
@@ -558,12 +560,20 @@ int launch_attn_fwd_f32(const void* q, const int64_t* qs, void* o, const int64_t
   constexpr int NT = D == 128 ? 1 : 2;
   const dim3 grid(((T + 128 * NT - 1) / (128 * NT)) * BHq);
   if constexpr (D == 128) {
-    if (narrow_dims<D>(dn)) {
-      LUCID_LAUNCH("lucid_attn_fwd_f32_kernel", (lucid::lucid_attn_fwd_kernel<D, true, NT, 96>), grid, st, w.qh,
-                   rows_strides(Hq, T, D), w.kch, rows_strides(Hkv, T, D), w.vpt, (float*)o, S(os), lse, w.mass,
-                   w.olo, Hq, Hkv, T, BHq, scale, lo, w.vptl, 0);
+    const int da = active_dims<D>(dn);
+#define LUCID_ATTN_FWD_NARROW(DA)                                                                                    \
+  LUCID_LAUNCH("lucid_attn_fwd_f32_kernel", (lucid::lucid_attn_fwd_kernel<D, true, NT, DA>), grid, st, w.qh,        \
+               rows_strides(Hq, T, D), w.kch, rows_strides(Hkv, T, D), w.vpt, (float*)o, S(os), lse, w.mass, w.olo, \
+               Hq, Hkv, T, BHq, scale, lo, w.vptl, 0)
+    if (da == 80) {
+      LUCID_ATTN_FWD_NARROW(80);
       return LUCID_OK;
     }
+    if (da == 96) {
+      LUCID_ATTN_FWD_NARROW(96);
+      return LUCID_OK;
+    }
+#undef LUCID_ATTN_FWD_NARROW
   }
   LUCID_LAUNCH("lucid_attn_fwd_f32_kernel", (lucid::lucid_attn_fwd_kernel<D, true, NT>), grid, st, w.qh,
                rows_strides(Hq, T, D), w.kch, rows_strides(Hkv, T, D), w.vpt, (float*)o, S(os), lse, w.mass, w.olo,
@@ -605,14 +615,22 @@ int launch_attn_bwd_f32(const void* dout, const int64_t* dos, const void* o, con
   constexpr int RW = D == 128 ? 32 : 64, WGR = D == 128 ? 128 : 256;
   const dim3 gkv((T / 128) * BH), gq(((T + WGR - 1) / WGR) * BHq), bq(64 * (WGR / RW));
   if constexpr (D == 128) {
-    if (narrow_dims<D>(dn)) {
-      LUCID_LAUNCH("lucid_attn_bwd_dkdv_f32_kernel", (lucid::lucid_attn_bwd_dkdv_kernel<D, true, 96>), gkv, st,
-                   f.qh, cq, f.kch, ck, f.vpb, w.doh, cq, w.seeds, w.dvp, w.dka, Hq, Hkv, T, BH, scale, lo, f.vpbl);
-      LUCID_LAUNCH_B("lucid_attn_bwd_dq_f32_kernel", (lucid::lucid_attn_bwd_dq_kernel<D, true, true, RW, WGR, 96>),
-                     gq, bq, st, f.qh, cq, f.kch, ck, f.vpb, w.doh, cq, lse, w.delta, f.mass, (float*)dq, S(dqs), Hq,
-                     Hkv, T, BHq, scale, lo, f.vpbl);
+    const int da = active_dims<D>(dn);
+#define LUCID_ATTN_BWD_NARROW(DA)                                                                                   \
+  LUCID_LAUNCH("lucid_attn_bwd_dkdv_f32_kernel", (lucid::lucid_attn_bwd_dkdv_kernel<D, true, DA>), gkv, st, f.qh,  \
+               cq, f.kch, ck, f.vpb, w.doh, cq, w.seeds, w.dvp, w.dka, Hq, Hkv, T, BH, scale, lo, f.vpbl);          \
+  LUCID_LAUNCH_B("lucid_attn_bwd_dq_f32_kernel", (lucid::lucid_attn_bwd_dq_kernel<D, true, true, RW, WGR, DA>), gq, \
+                 bq, st, f.qh, cq, f.kch, ck, f.vpb, w.doh, cq, lse, w.delta, f.mass, (float*)dq, S(dqs), Hq, Hkv, T,  \
+                 BHq, scale, lo, f.vpbl)
+    if (da == 80) {
+      LUCID_ATTN_BWD_NARROW(80);
       return LUCID_OK;
     }
+    if (da == 96) {
+      LUCID_ATTN_BWD_NARROW(96);
+      return LUCID_OK;
+    }
+#undef LUCID_ATTN_BWD_NARROW
   }
   LUCID_LAUNCH("lucid_attn_bwd_dkdv_f32_kernel", (lucid::lucid_attn_bwd_dkdv_kernel<D, true>), gkv, st, f.qh, cq,
                f.kch, ck, f.vpb, w.doh, cq, w.seeds, w.dvp, w.dka, Hq, Hkv, T, BH, scale, lo, f.vpbl);

@@ -895,7 +895,7 @@ __global__ __launch_bounds__(64 * NW) LUCID_TWO_WAVES_IF((D == 64 || NW == 8) &&
 // ---------------------------------------------------------------------------
 // NT: 32-row n-tiles per wave (2: 256 rows per workgroup; 1: 128 rows, for the fp32
 // instance at head dim 128, whose hi/lo operands of two n-tiles do not fit the registers)
-// DA: the head-dim columns that can be nonzero (a multiple of 32, <= D): rows of a smaller
+// DA: the head-dim columns that can be nonzero (a multiple of 16, <= D): rows of a smaller
 // head dim are zero-padded to D, and the products skip the k-steps and value tiles that
 // would only meet the zero columns (the outputs there stay 0)
 template <int D, bool F32 = false, int NT = 2, int DA = D>
@@ -906,8 +906,8 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !F32) void lucid
     const bf16* __restrict__ vptl, int skip_fast) {
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
-  constexpr int NDT_A = DA / 32, NKS_A = DA / 16;  // value tiles and k-steps that can be nonzero
-  static_assert(DA % 32 == 0 && DA <= D && (DA == D || NT == 1), "active head dim");
+  constexpr int NDT_A = (DA + 31) / 32, NKS_A = DA / 16;  // value tiles and k-steps that can be nonzero
+  static_assert(DA % 16 == 0 && DA <= D && (DA == D || NT == 1), "active head dim");
   constexpr int CH = D / 32;  // 16-byte chunks per thread for each of the K and V'^T tiles
   constexpr int NST = F32 ? 4 * CH : 2 * CH;  // staging registers (fp32 inputs: hi and lo tiles)
   __shared__ __attribute__((aligned(16))) bf16 lk[2][64][D + 8];
