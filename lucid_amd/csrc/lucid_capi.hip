@@ -234,17 +234,35 @@ int launch_precond_fwd(const void* k, const int64_t* ks, const void* v, const in
   return LUCID_OK;
 }
 
+// The head-dim columns the attention products run over: rows of a head
+// dim in (64, 96] are zero-padded to 128 and only the first 80 (d <= 80) or 96 columns can
+// be nonzero (k-steps of 16, value tiles of 32).  dn: the caller's head dim (<= 0: unknown,
+// all of D).  Returns 80, 96 or D.
+template <int D>
+int active_dims(float dn) {
+  if (D != 128 || !(dn > 0.f)) return D;
+  return dn <= 80.f ? 80 : dn <= 96.f ? 96 : D;
+}
+
 // Causal attention on the V' operands of w (bf16): the 256-thread kernel at head dim 64,
 // the eight-wave kernel at 128.
 template <int D>
 int launch_attn_fwd(const void* q, const int64_t* qs, const void* k, const int64_t* ks, void* o, const int64_t* os,
-                    float* lse, const FwdWs& w, int B, int Hq, int Hkv, int T, float scale, hipStream_t st) {
+                    float* lse, const FwdWs& w, int B, int Hq, int Hkv, int T, float scale, float dn,
+                    hipStream_t st) {
   const int BHq = B * Hq;
   if constexpr (D == 128) {
     // 128 keys per staged tile: half the barriers and row-max updates of 64 (1 % at config 5)
-    LUCID_LAUNCH_B("lucid_attn_fwd_wide_kernel", (lucid::lucid_attn_fwd_wide_kernel<D, 128>), dim3(((T + 255) / 256) * BHq),
-                   dim3(512), st, (const bf16*)q, S(qs), (const bf16*)k, S(ks), w.vpt, (bf16*)o, S(os), lse, w.mass,
-                   w.olo, Hq, Hkv, T, B * Hkv, scale);
+    auto wide = [&](auto dac) -> int {
+      LUCID_LAUNCH_B("lucid_attn_fwd_wide_kernel", (lucid::lucid_attn_fwd_wide_kernel<D, 128, decltype(dac)::value>),
+                     dim3(((T + 255) / 256) * BHq), dim3(512), st, (const bf16*)q, S(qs), (const bf16*)k, S(ks),
+                     w.vpt, (bf16*)o, S(os), lse, w.mass, w.olo, Hq, Hkv, T, B * Hkv, scale);
+      return LUCID_OK;
+    };
+    const int da = active_dims<D>(dn);
+    if (da == 80) return wide(std::integral_constant<int, 80>{});
+    if (da == 96) return wide(std::integral_constant<int, 96>{});
+    return wide(std::integral_constant<int, D>{});
   } else {
     LUCID_LAUNCH("lucid_attn_fwd_kernel", lucid::lucid_attn_fwd_kernel<D>, dim3(((T + 255) / 256) * BHq), st,
                  (const bf16*)q, S(qs), (const bf16*)k, S(ks), w.vpt, (bf16*)o, S(os), lse, w.mass, w.olo, Hq, Hkv,
@@ -284,7 +302,7 @@ int launch_fwd(const void* q, const int64_t* qs, const void* k, const int64_t* k
     }
   }
   if (int rc = launch_precond_fwd<D>(k, ks, v, vs, vprime, w, B, Hkv, T, scale, eps, dn, st)) return rc;
-  return launch_attn_fwd<D>(q, qs, k, ks, o, os, lse, w, B, Hq, Hkv, T, scale, st);
+  return launch_attn_fwd<D>(q, qs, k, ks, o, os, lse, w, B, Hq, Hkv, T, scale, dn, st);
 }
 
 // The attention part of the backward: delta, dV' and the softmax dK (into w.dvp, w.dka)
@@ -292,30 +310,39 @@ int launch_fwd(const void* q, const int64_t* qs, const void* k, const int64_t* k
 template <int D>
 int launch_attn_bwd(const void* dout, const int64_t* dos, const void* q, const int64_t* qs, const void* k,
                     const int64_t* ks, const void* o, const int64_t* os, const float* lse, const FwdWs& f, void* dq,
-                    const int64_t* dqs, const BwdWs& w, int B, int Hq, int Hkv, int T, float scale, hipStream_t st) {
+                    const int64_t* dqs, const BwdWs& w, int B, int Hq, int Hkv, int T, float scale, float dn,
+                    hipStream_t st) {
   const int BH = B * Hkv, BHq = B * Hq;
   const float cinv = 1.f / (scale * LOG2E_F);
   LUCID_LAUNCH("lucid_bwd_prep_kernel", lucid::lucid_bwd_prep_kernel<D>, dim3(T / 64, BHq), st, (const bf16*)dout,
                S(dos), (const bf16*)o, S(os), f.olo, f.mass, Hq, Hkv, T, w.delta, w.counters, BH, lucid::Lo{}, lse,
                cinv, w.seeds);
-  LUCID_LAUNCH("lucid_attn_bwd_dkdv_kernel", lucid::lucid_attn_bwd_dkdv_kernel<D>, dim3((T / 128) * BH), st,
-               (const bf16*)q, S(qs), (const bf16*)k, S(ks), f.vpb, (const bf16*)dout, S(dos), w.seeds, w.dvp,
-               w.dka, Hq, Hkv, T, BH, scale, lucid::Lo{}, nullptr);
-  // dQ: four waves of 64 rows at head dim 64, eight waves of 32 rows at 128
+  // dQ: four waves of 64 rows at head dim 64, eight waves of 32 rows at 128; the exact
+  // instance at 128: 128 rows per workgroup, one wave per SIMD (its hi/lo operands need the
+  // registers).  DA: the active head-dim columns (zero-padded rows of a smaller head dim)
   constexpr int RW = D == 128 ? 32 : 64;
-  const dim3 block(64 * (256 / RW));
-  LUCID_LAUNCH_B("lucid_attn_bwd_dq_kernel", (lucid::lucid_attn_bwd_dq_kernel<D, false, false, RW>),
-                 dim3(((T + 255) / 256) * BHq), block, st, (const bf16*)q, S(qs), (const bf16*)k, S(ks), f.vpb,
-                 (const bf16*)dout, S(dos), lse, w.delta, f.mass, (bf16*)dq, S(dqs), Hq, Hkv, T, BHq, scale,
-                 lucid::Lo{}, nullptr);
-  // the exact instance at head dim 128: 128 rows per workgroup, one wave per SIMD (its hi/lo
-  // operands need the registers)
   constexpr int XWGR = D == 128 ? 128 : 256;
-  LUCID_LAUNCH_B("lucid_attn_bwd_dq_exact_kernel", (lucid::lucid_attn_bwd_dq_kernel<D, true, false, RW, XWGR>),
-                 dim3(((T + XWGR - 1) / XWGR) * BHq), dim3(64 * (XWGR / RW)), st, (const bf16*)q, S(qs), (const bf16*)k, S(ks), f.vpb,
-                 (const bf16*)dout, S(dos), lse, w.delta, f.mass, (bf16*)dq, S(dqs), Hq, Hkv, T, BHq, scale,
-                 lucid::Lo{}, nullptr);
-  return LUCID_OK;
+  auto sweeps = [&](auto dac) -> int {
+    constexpr int DA = decltype(dac)::value;
+    LUCID_LAUNCH("lucid_attn_bwd_dkdv_kernel", (lucid::lucid_attn_bwd_dkdv_kernel<D, false, DA>),
+                 dim3((T / 128) * BH), st, (const bf16*)q, S(qs), (const bf16*)k, S(ks), f.vpb, (const bf16*)dout,
+                 S(dos), w.seeds, w.dvp, w.dka, Hq, Hkv, T, BH, scale, lucid::Lo{}, nullptr);
+    LUCID_LAUNCH_B("lucid_attn_bwd_dq_kernel", (lucid::lucid_attn_bwd_dq_kernel<D, false, false, RW, 256, DA>),
+                   dim3(((T + 255) / 256) * BHq), dim3(64 * (256 / RW)), st, (const bf16*)q, S(qs), (const bf16*)k,
+                   S(ks), f.vpb, (const bf16*)dout, S(dos), lse, w.delta, f.mass, (bf16*)dq, S(dqs), Hq, Hkv, T, BHq,
+                   scale, lucid::Lo{}, nullptr);
+    LUCID_LAUNCH_B("lucid_attn_bwd_dq_exact_kernel", (lucid::lucid_attn_bwd_dq_kernel<D, true, false, RW, XWGR, DA>),
+                   dim3(((T + XWGR - 1) / XWGR) * BHq), dim3(64 * (XWGR / RW)), st, (const bf16*)q, S(qs),
+                   (const bf16*)k, S(ks), f.vpb, (const bf16*)dout, S(dos), lse, w.delta, f.mass, (bf16*)dq, S(dqs),
+                   Hq, Hkv, T, BHq, scale, lucid::Lo{}, nullptr);
+    return LUCID_OK;
+  };
+  if constexpr (D == 128) {
+    const int da = active_dims<D>(dn);
+    if (da == 80) return sweeps(std::integral_constant<int, 80>{});
+    if (da == 96) return sweeps(std::integral_constant<int, 96>{});
+  }
+  return sweeps(std::integral_constant<int, D>{});
 }
 
 // The preconditioner part: dV = P^-T dV' (w.dvp, counters zeroed), then dK with the softmax
@@ -357,7 +384,7 @@ int launch_bwd(const void* dout, const int64_t* dos, const void* q, const int64_
                const int64_t* ks, const void* o, const int64_t* os, const float* lse, const FwdWs& f, void* dq,
                const int64_t* dqs, void* dk, const int64_t* dks, void* dv, const int64_t* dvs, const BwdWs& w, int B,
                int Hq, int Hkv, int T, float scale, float dn, hipStream_t st) {
-  if (int rc = launch_attn_bwd<D>(dout, dos, q, qs, k, ks, o, os, lse, f, dq, dqs, w, B, Hq, Hkv, T, scale, st))
+  if (int rc = launch_attn_bwd<D>(dout, dos, q, qs, k, ks, o, os, lse, f, dq, dqs, w, B, Hq, Hkv, T, scale, dn, st))
     return rc;
   return launch_precond_bwd<D>(k, ks, f, dk, dks, dv, dvs, w, w.dka, B, Hkv, T, scale, dn, st);
 }
@@ -446,16 +473,17 @@ int launch_attn_vp_fwd(const void* q, const int64_t* qs, const void* k, const in
   if (g_precision == LUCID_PRECISION_AUTO)
     LUCID_LAUNCH("lucid_mass_kernel", lucid::lucid_mass_kernel<D>, dim3(T / 64, BH), st, (const bf16*)k, S(ks),
                  Hkv, T, w.rinv, scale, w.mass);
-  return launch_attn_fwd<D>(q, qs, k, ks, o, os, lse, w, B, Hq, Hkv, T, scale, st);
+  return launch_attn_fwd<D>(q, qs, k, ks, o, os, lse, w, B, Hq, Hkv, T, scale, dn, st);
 }
 
 template <int D>
 int launch_attn_vp_bwd(const void* dout, const int64_t* dos, const void* q, const int64_t* qs, const void* k,
                        const int64_t* ks, const void* o, const int64_t* os, const float* lse, const FwdWs& f,
                        void* dq, const int64_t* dqs, void* dk, const int64_t* dks, void* dvp, const int64_t* dvps,
-                       int dvp_f32, const BwdWs& w, int B, int Hq, int Hkv, int T, float scale, hipStream_t st) {
+                       int dvp_f32, const BwdWs& w, int B, int Hq, int Hkv, int T, float scale, float dn,
+                       hipStream_t st) {
   const int BH = B * Hkv;
-  if (int rc = launch_attn_bwd<D>(dout, dos, q, qs, k, ks, o, os, lse, f, dq, dqs, w, B, Hq, Hkv, T, scale, st))
+  if (int rc = launch_attn_bwd<D>(dout, dos, q, qs, k, ks, o, os, lse, f, dq, dqs, w, B, Hq, Hkv, T, scale, dn, st))
     return rc;
   LUCID_LAUNCH("lucid_rows_out_kernel", (lucid::lucid_rows_out_kernel<D, bf16>), dim3(T / 64, BH), st, w.dka,
                (bf16*)dk, S(dks), Hkv, T, 1.f);
@@ -533,16 +561,6 @@ int launch_precond_fwd_f32(const void* k, const int64_t* ks, const void* v, cons
                dim3((T / 128) * BH), st, w.kh, ck, (const bf16*)v, S(vs), Hkv, T, BH, w.rinv, nullptr, scale, vprime,
                w.vpb, w.vpt, w.vpbl, w.vptl, w.pinv, w.zx, w.mass, w.counters, lo);
   return LUCID_OK;
-}
-
-// The head-dim columns the attention products of the fp32 kernels run over: rows of a head
-// dim in (64, 96] are zero-padded to 128 and only the first 80 (d <= 80) or 96 columns can
-// be nonzero (k-steps of 16, value tiles of 32).  dn: the caller's head dim (<= 0: unknown,
-// all of D).  Returns 80, 96 or D.
-template <int D>
-int active_dims(float dn) {
-  if (D != 128 || !(dn > 0.f)) return D;
-  return dn <= 80.f ? 80 : dn <= 96.f ? 96 : D;
 }
 
 // O = softmax(s Q K^T, causal) V' on the split Q (split here), the centred keys and V' in
@@ -1316,9 +1334,10 @@ int lucid_attn_vp_bwd(const void* dout, const int64_t* do_strides, const void* q
   if (padded_dim(D) == 64)
     return launch_attn_vp_bwd<64>(dout, do_strides, q, q_strides, k, k_strides, o, o_strides, lse, f, dq,
                                   dq_strides, dk, dk_strides, dvprime, dvprime_strides, dvprime_f32, w, B, Hq, Hkv,
-                                  T, scale, st);
+                                  T, scale, (float)D, st);
   return launch_attn_vp_bwd<128>(dout, do_strides, q, q_strides, k, k_strides, o, o_strides, lse, f, dq, dq_strides,
-                                 dk, dk_strides, dvprime, dvprime_strides, dvprime_f32, w, B, Hq, Hkv, T, scale, st);
+                                 dk, dk_strides, dvprime, dvprime_strides, dvprime_f32, w, B, Hq, Hkv, T, scale,
+                                 (float)D, st);
 }
 
 size_t lucid_precond_bwd_workspace_bytes(int B, int Hkv, int T, int D) {

@@ -1810,13 +1810,16 @@ __device__ __forceinline__ void attn_block_of(int id, int nblk, int BH, int G, i
 // rescale by 2^8), O^T[d][i] += V'^T[d][j] P^T[j][i] (16 MFMAs).
 // Outputs as lucid_attn_fwd_kernel (O, lse2, O's lo part for exact heads).
 // ---------------------------------------------------------------------------
-template <int D, int KT = 64>
+// DA: the head-dim columns that can be nonzero (as in lucid_attn_fwd_kernel)
+template <int D, int KT = 64, int DA = D>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void lucid_attn_fwd_wide_kernel(
     const bf16* __restrict__ q, Strides qs, const bf16* __restrict__ k, Strides ks, const bf16* __restrict__ vpt,
     bf16* __restrict__ o, Strides os, float* __restrict__ lse, const float* __restrict__ mass,
     bf16* __restrict__ olo, int Hq, int Hkv, int T, int BH, float scale) {
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
+  constexpr int NDT_A = (DA + 31) / 32, NKS_A = DA / 16;
+  static_assert(DA % 16 == 0 && DA <= D, "active head dim");
   constexpr int NMT = KT / 32;        // 32-key sub-tiles per staged tile
   static_assert(D == 128, "the wide attention kernel is the head-dim-128 path");
   static_assert(KT == 64 || KT == 128, "keys per staged tile");
@@ -1848,7 +1851,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void l
   {
     const int rq = min(row0 + l32, T - 1);
 #pragma unroll
-    for (int st = 0; st < NKS; ++st) qb[st] = ld8(qh + (int64_t)rq * qs.t + 16 * st + 8 * g);
+    for (int st = 0; st < NKS_A; ++st) qb[st] = ld8(qh + (int64_t)rq * qs.t + 16 * st + 8 * g);
   }
   f32x16 oacc[NDT];
 #pragma unroll
@@ -1870,7 +1873,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void l
   // compiler moves their loads past this point and then waits for all loads (vmcnt(0)),
   // the next tile's direct loads included, before the first product of every tile
 #pragma unroll
-  for (int st = 0; st < NKS; ++st) asm volatile("" ::"v"(qb[st]));
+  for (int st = 0; st < NKS_A; ++st) asm volatile("" ::"v"(qb[st]));
   dma_wait();
   __syncthreads();
   for (int jt = 0; jt < ntile; ++jt) {
@@ -1883,7 +1886,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void l
       for (int mt = 0; mt < NMT; ++mt) {
         s[mt] = zero16();
 #pragma unroll
-        for (int st = 0; st < NKS; ++st)
+        for (int st = 0; st < NKS_A; ++st)
           s[mt] = mfma32(ld8(swz<D / 8>(lk[buf], mt * 32 + l32, 2 * st + g)), qb[st], s[mt]);
       }
       if (jt == last_w) {  // causal mask: key KT jt + mt 32 + drow > row
@@ -1906,7 +1909,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void l
         m = mnew;
         lsum *= alpha;
 #pragma unroll
-        for (int t = 0; t < NDT; ++t)
+        for (int t = 0; t < NDT_A; ++t)
 #pragma unroll
           for (int e = 0; e < 16; ++e) oacc[t][e] *= alpha;
       }
@@ -1919,7 +1922,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void l
         const bf16x8 pb0 = pack_b(s[mt], 0), pb1 = pack_b(s[mt], 1);
         lsum = add_sum8(pb1, add_sum8(pb0, lsum));  // sum of the bf16 P of P V'
 #pragma unroll
-        for (int t = 0; t < NDT; ++t) {
+        for (int t = 0; t < NDT_A; ++t) {
           oacc[t] = mfma32(ld8(swz<KT / 8>(lv[buf], t * 32 + l32, 4 * mt + g)), pb0, oacc[t]);
           oacc[t] = mfma32(ld8(swz<KT / 8>(lv[buf], t * 32 + l32, 4 * mt + 2 + g)), pb1, oacc[t]);
         }
