@@ -416,13 +416,14 @@ def main():
     ap.add_argument("--warmup", type=int, default=None,
                     help="untimed warmup steps (default: at least 3 steps and 0.5 s of GPU work)")
     ap.add_argument("--workload", default="lucid",
-                    choices=["lucid", "c2", "c3", "c5", "gqa128", "ref_f32", "path", "path128", "path_f32",
+                    choices=["lucid", "c2", "c3", "c5", "gqa128", "ref_f32", "ref_bf16", "path", "path128", "path_f32",
                              "path_softmax", "decode"],
                     help="lucid: north star B1 H16 T32768 d64 fwd+bwd (default); c2: B4 H16 T4096 d64 "
                          "fwd+bwd; c3: 16-layer Llama-LUCID decoder, one training step (fwd+bwd+AdamW) "
                          "on B1 x T8192; c5: B1 T131072 Hq32/Hkv8 d128 forward only; gqa128: the config-5 heads "
                          "(Hq32/Hkv8 d128) at B1 T32768, fwd+bwd; ref_f32: the attention layer of the reference's shipped "
-                         "LUCID model config (fp32, head dim 68, 32 query / 4 kv heads) at B8 T2048, fwd+bwd; path: LUCID-Path "
+                         "LUCID model config (fp32, head dim 68, 32 query / 4 kv heads) at B8 T2048, fwd+bwd; ref_bf16: "
+                         "the same shape in bf16; path: LUCID-Path "
                          "B1 H16 T32768 d64 fwd+bwd; path128: the same at head dim 128; path_f32: config 4 on fp32 "
                          "inputs; path_softmax: PaTH softmax attention on the config-4 "
                          "shape, fwd+bwd; decode: one decoding step against a 128K cache (config-5 heads)")
@@ -497,7 +498,7 @@ def main():
     else:
         B, Hq, Hkv, T, D = {"lucid": (1, 16, 16, 32768, 64), "c2": (4, 16, 16, 4096, 64),
                             "c5": (1, 32, 8, 131072, 128), "gqa128": (1, 32, 8, 32768, 128),
-                            "ref_f32": (8, 32, 4, 2048, 68)}[wl]
+                            "ref_f32": (8, 32, 4, 2048, 68), "ref_bf16": (8, 32, 4, 2048, 68)}[wl]
         q, k, v, do = _bench_inputs(B, Hq, Hkv, T, D, dev, grad=not fwd_only, keys=args.keys,
                                     dtype=torch.float32 if wl == "ref_f32" else None)
         lib, prefix = _lib.load(), "lucid_"
@@ -601,7 +602,7 @@ def main():
         "precision": args.precision, "keys": args.keys, "fused_forward": not args.no_fused_fwd,
         "config": {"workload": {"lucid": "lucid_attention_fwd_bwd", "c2": "lucid_attention_fwd_bwd",
                                 "c5": "lucid_attention_fwd", "gqa128": "lucid_attention_fwd_bwd",
-                                "ref_f32": "lucid_attention_fwd_bwd",
+                                "ref_f32": "lucid_attention_fwd_bwd", "ref_bf16": "lucid_attention_fwd_bwd",
                                 "path": "lucid_path_fwd_bwd", "path128": "lucid_path_fwd_bwd",
                                 "path_f32": "lucid_path_fwd_bwd",
                                 "path_softmax": "path_softmax_attention_fwd_bwd"}[wl],
