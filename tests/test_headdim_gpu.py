@@ -42,6 +42,11 @@ CASES = [
     (1, 4, 2, 384, 96, None),
     (1, 2, 1, 256, 16, 1.0),
     (1, 2, 2, 128, 127, None),
+    # edges of the active-column instances (80 columns up to d = 80, 96 up to 96, else 128),
+    # the first with the reference model's 32 / 4 grouping
+    (1, 32, 4, 256, 80, None),
+    (1, 4, 2, 256, 81, 1.0),
+    (1, 2, 1, 256, 97, None),
 ]
 
 
@@ -66,7 +71,8 @@ def test_padded_head_dim_matches_oracle(B, Hq, Hkv, T, D, qk_std):
         check(name, err, float(np.abs(ref).max()))
 
 
-@pytest.mark.parametrize("B,Hq,Hkv,T,D", [(1, 2, 1, 512, 48), (1, 2, 2, 384, 20)])
+@pytest.mark.parametrize("B,Hq,Hkv,T,D", [(1, 2, 1, 512, 48), (1, 2, 2, 384, 20),
+                                           (1, 4, 2, 256, 80), (1, 2, 2, 256, 81), (1, 2, 1, 256, 96)])
 def test_padded_head_dim_fp32(B, Hq, Hkv, T, D):
     from lucid_amd import lucid_attention
     q, k, v, do = _inputs(B, Hq, Hkv, T, D, seed=5 * T + D, qk_std=1.0, dtype=torch.float32)
