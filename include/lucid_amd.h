@@ -20,8 +20,9 @@
  * lucid/config/config.json:9) run on zero-padded rows: every [.., D] operand then
  * has Dp = 64 (D <= 64) or 128 (D > 64) elements per row, columns D .. Dp-1 zero in
  * the inputs (dout included) and written zero in the outputs; the dot products are
- * unchanged and the RMS of k_norm divides by D itself.  Workspace sizes take D and
- * are those of Dp.
+ * unchanged and the RMS of k_norm divides by D itself (the attention sweeps of D in
+ * 65 .. 96 leave out the columns beyond 80 or 96, whose products are zero).  Workspace
+ * sizes take D and are those of Dp.
  */
 #ifndef LUCID_AMD_H
 #define LUCID_AMD_H
