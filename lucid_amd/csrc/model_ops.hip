@@ -1,7 +1,9 @@
 // Fused elementwise layers of the Llama-LUCID decoder (the model around the attention core,
-// modeling_lucid.py:58-75 and 118-145) on CDNA4 (gfx950).  As torch ops each of them is a
-// chain of memory-bound passes (RMSNorm: fp32 copy, square, mean, rsqrt, two products and a
-// cast, each reading and writing the whole activation); here each is one pass over its rows.
+// modeling_lucid.py:58-75, 118-145, 155-167 and the loss of 847-967) and the AdamW step of its
+// training (run_clm_chunk.py:776, the Trainer's default optimizer) on CDNA4 (gfx950).  As
+// torch ops each of them is a chain of memory-bound passes (RMSNorm: fp32 copy, square, mean,
+// rsqrt, two products and a cast, each reading and writing the whole activation); here each
+// is one pass over its data.
 //
 //   lucid_rmsnorm_fwd_kernel      y = w * bf16(x rstd), rstd = 1/sqrt(mean(x^2) + eps) (fp32
 //                                 statistics, the weight applied in bf16 as in the reference)
