@@ -624,7 +624,10 @@ struct PcolSmem<D, true, F32> {
   } u;
 };
 
-template <int D, bool EXACT, bool F32 = false>
+// DA: the head-dim columns that can be nonzero (zero-padded rows of a smaller head dim): the
+// sweeps' products skip the rest; the solve and the cross term stay full width (their padded
+// columns are zero because dV' and V' are)
+template <int D, bool EXACT, bool F32 = false, int DA = D>
 __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void lucid_precond_bwd_col_kernel(
     const bf16* __restrict__ k, Strides ks, int Hkv, int T, int BH, const float* __restrict__ rinv,
     const bf16* __restrict__ khat, float scale, const bf16* __restrict__ kt, const bf16* __restrict__ vpb,
@@ -635,6 +638,8 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
   static_assert(!F32 || EXACT, "fp32 inputs: exact instance");
   constexpr int NDT = D / 32;
   constexpr int NKS = D / 16;
+  constexpr int NDT_A = (DA + 31) / 32, NKS_A = DA / 16;
+  static_assert(DA % 16 == 0 && DA <= D, "active head dim");
   __shared__ __attribute__((aligned(16))) PcolSmem<D, EXACT, F32> sm;
   constexpr int NB = stage_bufs(D, F32);
 
@@ -670,7 +675,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
   const float aJ = sl2 * rv[jc];
   bf16x8 kbJ[NKS], vbJ[NKS], vbJl[NKS], kbJl[NKS];
 #pragma unroll
-  for (int st = 0; st < NKS; ++st) {
+  for (int st = 0; st < NKS_A; ++st) {
     kbJ[st] = ld8(kh + (int64_t)jc * ks.t + 16 * st + 8 * g);
     vbJ[st] = ld8(vph + (int64_t)jc * D + 16 * st + 8 * g);
     if constexpr (EXACT) vbJl[st] = ld8(vpbl + ((int64_t)bh * T + jc) * D + 16 * st + 8 * g);
@@ -770,7 +775,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
     for (int rh = 0; rh < 2; ++rh) {
       bf16x8 ka[NKS], da[NKS];
 #pragma unroll
-      for (int st = 0; st < NKS; ++st) {
+      for (int st = 0; st < NKS_A; ++st) {
         ka[st] = ld8(swz<D / 8>(sm.u.st.k[buf], rh * 32 + l32, 2 * st + g));
         da[st] = ld8(swz<D / 8>(sm.u.st.dv[buf], rh * 32 + l32, 2 * st + g));
       }
@@ -778,20 +783,20 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
       if constexpr (EXACT) lds_rows16(&sm.u.st.r[buf][rh * 32], g, rI);
       f32x16 sc = zero16(), gg = zero16();
 #pragma unroll
-      for (int st = 0; st < NKS; ++st) {
+      for (int st = 0; st < NKS_A; ++st) {
         sc = mfma32(ka[st], kbJ[st], sc);
         gg = mfma32(da[st], vbJ[st], gg);
       }
       if constexpr (EXACT) {
 #pragma unroll
-        for (int st = 0; st < NKS; ++st) {
+        for (int st = 0; st < NKS_A; ++st) {
           gg = mfma32(da[st], vbJl[st], gg);
           gg = mfma32(ld8(swz<D / 8>(sm.u.st.dvl[buf], rh * 32 + l32, 2 * st + g)), vbJ[st], gg);
         }
       }
       if constexpr (F32) {
 #pragma unroll
-        for (int st = 0; st < NKS; ++st) {
+        for (int st = 0; st < NKS_A; ++st) {
           const bf16x8 kal = ld8(swz<D / 8>(sm.u.st.kl[buf], rh * 32 + l32, 2 * st + g));
           sc = mfma32(ka[st], kbJl[st], sc);
           sc = mfma32(kal, kbJ[st], sc);
@@ -814,7 +819,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
         ml1 = pack_lo(gg, 1, mb1);
       }
 #pragma unroll
-      for (int t = 0; t < NDT; ++t) {
+      for (int t = 0; t < NDT_A; ++t) {
         const bf16x8 a0 = lds_tr_a<D / 8>(sm.u.st.dv[buf], rh * 32, t * 32);
         const bf16x8 a1 = lds_tr_a<D / 8>(sm.u.st.dv[buf], rh * 32 + 16, t * 32);
         const bf16x8 k0 = lds_tr_a<D / 8>(sm.u.st.k[buf], rh * 32, t * 32);
@@ -991,7 +996,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
       const int rbase = J0 + rb * 64 + rh * 32;
       bf16x8 ka[NKS], da[NKS];
 #pragma unroll
-      for (int st = 0; st < NKS; ++st) {
+      for (int st = 0; st < NKS_A; ++st) {
         ka[st] = ld8(kh + (int64_t)(rbase + l32) * ks.t + 16 * st + 8 * g);
         da[st] = ld8(dvbh + (int64_t)(rbase + l32) * D + 16 * st + 8 * g);
       }
@@ -999,20 +1004,20 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
       load_rows16(rv + rbase, g, rr);
       f32x16 sc = zero16(), gg = zero16();
 #pragma unroll
-      for (int st = 0; st < NKS; ++st) {
+      for (int st = 0; st < NKS_A; ++st) {
         sc = mfma32(ka[st], kbJ[st], sc);
         gg = mfma32(da[st], vbJ[st], gg);
       }
       if constexpr (EXACT) {
 #pragma unroll
-        for (int st = 0; st < NKS; ++st) {
+        for (int st = 0; st < NKS_A; ++st) {
           gg = mfma32(da[st], vbJl[st], gg);
           gg = mfma32(ld8(dvblh + (int64_t)(rbase + l32) * D + 16 * st + 8 * g), vbJ[st], gg);
         }
       }
       if constexpr (F32) {
 #pragma unroll
-        for (int st = 0; st < NKS; ++st) {
+        for (int st = 0; st < NKS_A; ++st) {
           const bf16x8 kal = ld8(klh + (int64_t)(rbase + l32) * ks.t + 16 * st + 8 * g);
           sc = mfma32(ka[st], kbJl[st], sc);
           sc = mfma32(kal, kbJ[st], sc);
@@ -1029,7 +1034,7 @@ __global__ __launch_bounds__(256) LUCID_TWO_WAVES_IF(D == 64 && !EXACT) void luc
       }
       const bf16x8 mb0 = pack_b(gg, 0), mb1 = pack_b(gg, 1);
 #pragma unroll
-      for (int t = 0; t < NDT; ++t) {
+      for (int t = 0; t < NDT_A; ++t) {
         const bf16* kp = kth + (int64_t)(t * 32 + l32) * T + rbase + 8 * g;
         acs[t] = mfma32(ld8(kp), mb0, acs[t]);
         acs[t] = mfma32(ld8(kp + 16), mb1, acs[t]);

@@ -359,14 +359,31 @@ int launch_precond_bwd(const void* k, const int64_t* ks, const FwdWs& f, void* d
     LUCID_LAUNCH_B("lucid_precond_bwd_col_wide_kernel", lucid::lucid_precond_bwd_col_wide_kernel<64>,
                    dim3((T / 256) * BH), dim3(512), st, (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, f.khat, scale,
                    f.vpb, f.pinv, f.mass, w.dvp, w.dvb, (bf16*)dv, S(dvs), w.colsum, w.counters);
-  } else {
-    LUCID_LAUNCH("lucid_precond_bwd_col_kernel", (lucid::lucid_precond_bwd_col_kernel<D, false>),
+  }
+  // the 128-column chains (bf16 unless the wide one ran, and the exact instance) over the
+  // active head-dim columns
+  auto col_chains = [&](auto dac) -> int {
+    constexpr int DA = decltype(dac)::value;
+    if (!(D == 64 && T % 256 == 0))
+      LUCID_LAUNCH("lucid_precond_bwd_col_kernel", (lucid::lucid_precond_bwd_col_kernel<D, false, false, DA>),
+                   dim3((T / 128) * BH), st, (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, f.khat, scale, f.kt, f.vpb,
+                   f.vpbl, f.pinv, f.mass, w.dvp, w.dvb, w.dvbl, (bf16*)dv, S(dvs), w.colsum, w.counters,
+                   lucid::Lo{});
+    LUCID_LAUNCH("lucid_precond_bwd_col_exact_kernel", (lucid::lucid_precond_bwd_col_kernel<D, true, false, DA>),
                  dim3((T / 128) * BH), st, (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, f.khat, scale, f.kt, f.vpb,
                  f.vpbl, f.pinv, f.mass, w.dvp, w.dvb, w.dvbl, (bf16*)dv, S(dvs), w.colsum, w.counters, lucid::Lo{});
+    return LUCID_OK;
+  };
+  int rc_col;
+  if constexpr (D == 128) {
+    const int da = active_dims<D>(dn);
+    rc_col = da == 80   ? col_chains(std::integral_constant<int, 80>{})
+             : da == 96 ? col_chains(std::integral_constant<int, 96>{})
+                        : col_chains(std::integral_constant<int, D>{});
+  } else {
+    rc_col = col_chains(std::integral_constant<int, D>{});
   }
-  LUCID_LAUNCH("lucid_precond_bwd_col_exact_kernel", (lucid::lucid_precond_bwd_col_kernel<D, true>),
-               dim3((T / 128) * BH), st, (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, f.khat, scale, f.kt, f.vpb,
-               f.vpbl, f.pinv, f.mass, w.dvp, w.dvb, w.dvbl, (bf16*)dv, S(dvs), w.colsum, w.counters, lucid::Lo{});
+  if (rc_col) return rc_col;
   LUCID_LAUNCH("lucid_precond_bwd_row_kernel", (lucid::lucid_precond_bwd_row_kernel<D, false>),
                dim3(((T + 255) / 256) * BH), st, (const bf16*)k, S(ks), Hkv, T, BH, f.rinv, f.khat, scale, dn,
                f.vpb, f.vpbl, w.dvb, w.dvbl, f.mass, w.colsum, dka, (bf16*)dk, S(dks), lucid::Lo{});
@@ -669,9 +686,23 @@ int launch_precond_bwd_f32(const FwdWs& f, void* dk, const int64_t* dks, void* d
   lucid::Lo lo{};
   lo.k = f.kl;
   lo.kt = f.ktl;
-  LUCID_LAUNCH("lucid_precond_bwd_col_f32_kernel", (lucid::lucid_precond_bwd_col_kernel<D, true, true>),
-               dim3((T / 128) * BH), st, f.kh, ck, Hkv, T, BH, f.rinv, nullptr, scale, f.kt, f.vpb, f.vpbl, f.pinv,
-               f.mass, w.dvp, w.dvb, w.dvbl, (float*)dv, S(dvs), w.colsum, w.counters, lo);
+  auto col_chain = [&](auto dac) -> int {  // over the active head-dim columns
+    LUCID_LAUNCH("lucid_precond_bwd_col_f32_kernel",
+                 (lucid::lucid_precond_bwd_col_kernel<D, true, true, decltype(dac)::value>), dim3((T / 128) * BH), st,
+                 f.kh, ck, Hkv, T, BH, f.rinv, nullptr, scale, f.kt, f.vpb, f.vpbl, f.pinv, f.mass, w.dvp, w.dvb,
+                 w.dvbl, (float*)dv, S(dvs), w.colsum, w.counters, lo);
+    return LUCID_OK;
+  };
+  int rc_col;
+  if constexpr (D == 128) {
+    const int da = active_dims<D>(dn);
+    rc_col = da == 80   ? col_chain(std::integral_constant<int, 80>{})
+             : da == 96 ? col_chain(std::integral_constant<int, 96>{})
+                        : col_chain(std::integral_constant<int, D>{});
+  } else {
+    rc_col = col_chain(std::integral_constant<int, D>{});
+  }
+  if (rc_col) return rc_col;
   constexpr int NT = D == 128 ? 1 : 2;  // head dim 128: one n-tile per wave (registers)
   LUCID_LAUNCH("lucid_precond_bwd_row_f32_kernel", (lucid::lucid_precond_bwd_row_kernel<D, true, true, NT>),
                dim3(((T + 128 * NT - 1) / (128 * NT)) * BH), st, f.kh, ck, Hkv, T, BH, f.rinv, nullptr, scale, dn,
