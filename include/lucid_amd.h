@@ -310,16 +310,16 @@ int lucid_decode_noalloc(const void* q, const int64_t* q_strides, const void* k,
  * saved for the backward), replacing LlamaRMSNorm.forward (modeling_lucid.py:58-75).
  * lucid_rmsnorm_bwd: dx and dw (summed over the rows in a fixed order) from dy, with a
  * caller-owned fp32 workspace of lucid_rmsnorm_bwd_workspace_bytes(N, H).  H must be 512, 1024,
- * 2048 or 4096.  lucid_rope: out[B][T][Hn][64] = x cos + rotate_half(x) sin (transpose = 1:
- * the adjoint, for the backward) for x [B, Hn, T, 64] at element strides x_strides = (b, h, t),
- * multiples of 8, with cos / sin bf16 [B*T][64] (one row per token), pointers 16-byte aligned,
- * replacing apply_rotary_pos_emb (modeling_lucid.py:118-145). */
+ * 2048 or 4096.  lucid_rope: out = x cos + rotate_half(x) sin (transpose = 1: the adjoint, for
+ * the backward) for x and out [B, Hn, T, 64] at element strides x_strides / out_strides =
+ * (b, h, t), multiples of 8, with cos / sin bf16 [B*T][64] (one row per token), pointers
+ * 16-byte aligned, replacing apply_rotary_pos_emb (modeling_lucid.py:118-145). */
 int lucid_rmsnorm_fwd(const void* x, const void* w, void* y, float* rstd, int N, int H, float eps, void* stream);
 size_t lucid_rmsnorm_bwd_workspace_bytes(int N, int H);
 int lucid_rmsnorm_bwd(const void* x, const void* w, const void* dy, const float* rstd, void* dx, void* dw,
                       void* workspace, int N, int H, void* stream);
 int lucid_rope(const void* x, const int64_t x_strides[3], int B, int Hn, int T, const void* cos, const void* sin,
-               void* out, int D, int transpose, void* stream);
+               void* out, const int64_t out_strides[3], int D, int transpose, void* stream);
 
 /* lucid_swiglu_fwd: h = silu(g) * u over n bf16 values, replacing the act_fn(gate) * up of
  * LlamaMLP.forward (modeling_lucid.py:155-167); lucid_swiglu_bwd: dg = dh u silu'(g),

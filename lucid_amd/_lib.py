@@ -84,7 +84,7 @@ _SIGS = {
         "lucid_rmsnorm_fwd": ([_vp, _vp, _vp, _vp, _int, _int, _flt, _vp], _int),
         "lucid_rmsnorm_bwd_workspace_bytes": ([_int, _int], _sz),
         "lucid_rmsnorm_bwd": ([_vp, _vp, _vp, _vp, _vp, _vp, _vp, _int, _int, _vp], _int),
-        "lucid_rope": ([_vp, _vp, _int, _int, _int, _vp, _vp, _vp, _int, _int, _vp], _int),
+        "lucid_rope": ([_vp, _vp, _int, _int, _int, _vp, _vp, _vp, _vp, _int, _int, _vp], _int),
         "lucid_swiglu_fwd": ([_vp, _vp, _vp, ctypes.c_int64, _vp], _int),
         "lucid_swiglu_bwd": ([_vp, _vp, _vp, _vp, _vp, ctypes.c_int64, _vp], _int),
         "lucid_causal_lm_loss_fwd": ([_vp, ctypes.c_int64, _vp, _int, _int, _int, _vp, _vp, _vp, _vp], _int),

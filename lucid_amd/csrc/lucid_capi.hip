@@ -1447,13 +1447,16 @@ int lucid_rmsnorm_bwd(const void* x, const void* w, const void* dy, const float*
 }
 
 int lucid_rope(const void* x, const int64_t x_strides[3], int B, int Hn, int T, const void* cos, const void* sin,
-               void* out, int D, int transpose, void* stream) {
+               void* out, const int64_t out_strides[3], int D, int transpose, void* stream) {
   g_last_error.clear();
   if (D != 64 || B < 0 || T < 0 || Hn <= 0)
     return fail("lucid_rope: head dim 64, B >= 0, T >= 0 and Hn > 0, got D=" + std::to_string(D));
-  if (x_strides[0] % 8 || x_strides[1] % 8 || x_strides[2] % 8 || reinterpret_cast<uintptr_t>(x) % 16 ||
-      reinterpret_cast<uintptr_t>(cos) % 16 || reinterpret_cast<uintptr_t>(sin) % 16 ||
-      reinterpret_cast<uintptr_t>(out) % 16)
+  if (!x_strides || !out_strides) return fail("lucid_rope: strides are null");
+  for (int i = 0; i < 3; ++i)
+    if (x_strides[i] % 8 || out_strides[i] % 8)
+      return fail("lucid_rope: strides must be multiples of 8 elements and pointers 16-byte aligned");
+  if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(cos) % 16 ||
+      reinterpret_cast<uintptr_t>(sin) % 16 || reinterpret_cast<uintptr_t>(out) % 16)
     return fail("lucid_rope: strides must be multiples of 8 elements and pointers 16-byte aligned");
   const int64_t R = (int64_t)B * T * Hn;
   if (R == 0) return LUCID_OK;
@@ -1462,10 +1465,12 @@ int lucid_rope(const void* x, const int64_t x_strides[3], int B, int Hn, int T, 
   const dim3 grid((unsigned)((R * 4 + 255) / 256));
   if (transpose)
     LUCID_LAUNCH("lucid_rope_kernel", lucid::lucid_rope_kernel<-1>, grid, st, (const bf16*)x, x_strides[0],
-                 x_strides[1], x_strides[2], (int)R, Hn, T, (const bf16*)cos, (const bf16*)sin, (bf16*)out);
+                 x_strides[1], x_strides[2], (int)R, Hn, T, (const bf16*)cos, (const bf16*)sin, (bf16*)out,
+                 out_strides[0], out_strides[1], out_strides[2]);
   else
     LUCID_LAUNCH("lucid_rope_kernel", lucid::lucid_rope_kernel<1>, grid, st, (const bf16*)x, x_strides[0],
-                 x_strides[1], x_strides[2], (int)R, Hn, T, (const bf16*)cos, (const bf16*)sin, (bf16*)out);
+                 x_strides[1], x_strides[2], (int)R, Hn, T, (const bf16*)cos, (const bf16*)sin, (bf16*)out,
+                 out_strides[0], out_strides[1], out_strides[2]);
   return LUCID_OK;
 }
 

@@ -159,9 +159,9 @@ __global__ __launch_bounds__(64 * kDwWaves) void lucid_rmsnorm_dw_kernel(const f
   }
 }
 
-// Rotary embedding over rows of head dim D = 64 (the model's).  Output rows are [B, T, Hn]
-// ordered, out[row][64] contiguous; row (b, t, h) reads x + b sb + h sh + t st (element strides,
-// multiples of 8) and the cos / sin row of token b T + t ([B T][64]).  SIGN = +1: the forward
+// Rotary embedding over rows of head dim D = 64 (the model's).  Row (b, t, h) reads
+// x + b sb + h sh + t st and writes out + b ob + h oh + t ot (element strides, multiples of 8),
+// with the cos / sin row of token b T + t ([B T][64]).  SIGN = +1: the forward
 // out = x cos + rotate_half(x) sin, rotate_half(x) = (-x2, x1); SIGN = -1: its transpose (the
 // backward), out = x cos + rotate_half^T(x sin), rotate_half^T(y) = (y2, -y1).  Four lanes per
 // row, each holding 8 pairs (i, i + 32) in 16-byte loads.
@@ -169,7 +169,7 @@ template <int SIGN>
 __global__ __launch_bounds__(256) void lucid_rope_kernel(const bf16* __restrict__ x, int64_t sb, int64_t sh,
                                                          int64_t st, int R, int Hn, int T,
                                                          const bf16* __restrict__ cs, const bf16* __restrict__ sn,
-                                                         bf16* __restrict__ out) {
+                                                         bf16* __restrict__ out, int64_t ob, int64_t oh, int64_t ot) {
   constexpr int D = 64, HD = D / 2;
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int row = (int)(idx >> 2), i0 = (int)(idx & 3) * 8;
@@ -192,7 +192,7 @@ __global__ __launch_bounds__(256) void lucid_rope_kernel(const bf16* __restrict_
       o2[e] = (bf16)(c * (float)c2[e] - a * (float)s1[e]);
     }
   }
-  bf16* orow = out + (int64_t)row * D;
+  bf16* orow = out + b * ob + h * oh + t * ot;
   *reinterpret_cast<bf16x8*>(orow + i0) = o1;
   *reinterpret_cast<bf16x8*>(orow + HD + i0) = o2;
 }

@@ -103,15 +103,19 @@ def _tokens(c: torch.Tensor, B: int, T: int) -> torch.Tensor:
     return _aligned(c.expand(B, T, c.shape[-1]))
 
 
-def _rope_launch(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, transpose: int) -> torch.Tensor:
+def _rope_launch(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, transpose: int,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+    """x [B, H, T, 64] rotated into ``out`` ([B, H, T, 64], strides multiples of 8; default: a
+    new [B, T, H, 64] buffer seen as [B, H, T, 64])."""
     B, Hn, T, D = x.shape
     xr = _strided(x)
-    out = torch.empty(B, T, Hn, D, dtype=x.dtype, device=x.device)
+    if out is None:
+        out = torch.empty(B, T, Hn, D, dtype=x.dtype, device=x.device).transpose(1, 2)
     lib = _lib.load()
     rc = lib.lucid_rope(_lib.ptr(xr), _lib.strides3(xr, (0, 1, 2)), B, Hn, T, _lib.ptr(cos), _lib.ptr(sin),
-                        _lib.ptr(out), D, transpose, _lib.stream_handle(x.device))
+                        _lib.ptr(out), _lib.strides3(out, (0, 1, 2)), D, transpose, _lib.stream_handle(x.device))
     _lib.check(lib, rc, "lucid_rope")
-    return out.transpose(1, 2)
+    return out
 
 
 class RopeFunction(torch.autograd.Function):
@@ -134,6 +138,59 @@ def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.T
     """x cos + rotate_half(x) sin for x [B, H, T, 64] and cos / sin [B or 1, T, 64]
     (modeling_lucid.py:118-145 with unsqueeze_dim 1)."""
     return RopeFunction.apply(x, cos, sin)
+
+
+class QKVRopeFunction(torch.autograd.Function):
+    """The stacked projection output qkv [B, T, (Hq + 2 Hkv) 64] split into q, k, v, with the
+    rotary embedding applied to q and k.  Its backward writes the rotated-back dq, dk and dv
+    straight into one [B, T, (Hq + 2 Hkv) 64] gradient, so that no concatenation of the three
+    follows (the split's own backward would concatenate them)."""
+
+    @staticmethod
+    def forward(ctx, qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, nq: int, nk: int):
+        B, T, N = qkv.shape
+        if not (qkv.is_cuda and qkv.dtype == torch.bfloat16 and cos.dtype == torch.bfloat16
+                and nq % 64 == 0 and nk % 64 == 0 and N == nq + 2 * nk):
+            raise TypeError("lucid_amd.qkv_rope: bf16 GPU [B, T, (Hq + 2 Hkv) 64] projections")
+        hq, hk = nq // 64, nk // 64
+
+        def heads(t, h):
+            return t.view(B, T, h, 64).transpose(1, 2)
+
+        c, s = _tokens(cos, B, T), _tokens(sin, B, T)
+        q = _rope_launch(heads(qkv[..., :nq], hq), c, s, 0)
+        k = _rope_launch(heads(qkv[..., nq:nq + nk], hk), c, s, 0)
+        v = heads(qkv[..., nq + nk:], hk)
+        ctx.save_for_backward(c, s)
+        ctx.dims = (B, T, N, nq, nk)
+        return q, k, v
+
+    @staticmethod
+    def backward(ctx, dq, dk, dv):
+        c, s = ctx.saved_tensors
+        B, T, N, nq, nk = ctx.dims
+        dev = c.device
+        g = torch.empty(B, T, N, dtype=torch.bfloat16, device=dev)
+
+        def heads(t, h):
+            return t.view(B, T, h, 64).transpose(1, 2)
+
+        for grad, lo, n in ((dq, 0, nq), (dk, nq, nk)):
+            if grad is None:
+                g[..., lo:lo + n].zero_()
+            else:
+                _rope_launch(grad, c, s, 1, out=heads(g[..., lo:lo + n], n // 64))
+        if dv is None:
+            g[..., nq + nk:].zero_()
+        else:
+            heads(g[..., nq + nk:], nk // 64).copy_(dv)
+        return g, None, None, None, None
+
+
+def qkv_rope(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, nq: int, nk: int):
+    """(q, k, v) [B, H, T, 64] from the stacked projection output, q and k rotated
+    (apply_rotary_pos_emb, modeling_lucid.py:118-145)."""
+    return QKVRopeFunction.apply(qkv, cos, sin, nq, nk)
 
 
 def swiglu_supported(g: torch.Tensor, u: torch.Tensor) -> bool:

@@ -27,8 +27,8 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from .lucid import _padded_dim, lucid_attention, lucid_decode
-from .model_ops import (apply_rope, causal_lm_loss, causal_lm_loss_supported, rms_norm, rms_norm_supported,
-                        rope_supported, swiglu, swiglu_supported)
+from .model_ops import (apply_rope, causal_lm_loss, causal_lm_loss_supported, qkv_rope, rms_norm,
+                        rms_norm_supported, rope_supported, swiglu, swiglu_supported)
 
 
 @dataclass
@@ -223,14 +223,22 @@ class LucidAttention(nn.Module):
                            None if self.q_proj.bias is None else
                            torch.cat((self.q_proj.bias, self.k_proj.bias, self.v_proj.bias)))
             nq, nk = self.q_proj.out_features, self.k_proj.out_features
-            q, k, v = (t.view(hidden_shape).transpose(1, 2) for t in qkv.split((nq, nk, nk), dim=-1))
+            cos, sin = position_embeddings
+            if self.use_rope and self.head_dim == 64 and rope_supported(qkv.view(*hidden_shape).transpose(1, 2), cos):
+                # split + rotary embedding in one autograd step: the backward writes dq, dk and
+                # dv into one gradient of qkv instead of concatenating them
+                q, k, v = qkv_rope(qkv, cos, sin, nq, nk)
+            else:
+                q, k, v = (t.view(hidden_shape).transpose(1, 2) for t in qkv.split((nq, nk, nk), dim=-1))
+                if self.use_rope:
+                    q, k = apply_rotary_pos_emb(q, k, cos, sin)
         else:
             q = self.q_proj(hidden_states).view(hidden_shape).transpose(1, 2)
             k = self.k_proj(hidden_states).view(hidden_shape).transpose(1, 2)
             v = self.v_proj(hidden_states).view(hidden_shape).transpose(1, 2)
-        cos, sin = position_embeddings
-        if self.use_rope:
-            q, k = apply_rotary_pos_emb(q, k, cos, sin)
+            cos, sin = position_embeddings
+            if self.use_rope:
+                q, k = apply_rotary_pos_emb(q, k, cos, sin)
         past = 0 if past_key_value is None else past_key_value.get_seq_length(self.layer_idx)
         if past == 0:
             # training / prefill: the fused HIP op (P never materialised, causal mask implicit)

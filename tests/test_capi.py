@@ -75,10 +75,12 @@ def test_decoder_layer_and_optimizer_validation_without_gpu(built):
     rc = lib.lucid_rmsnorm_fwd(dummy, dummy, dummy, dummy, 4, 768, 1e-5, None)
     assert rc == _lib.LUCID_EINVAL and b"H must be" in lib.lucid_last_error()
     s = (ctypes.c_int64 * 3)(64, 64, 64)
-    rc = lib.lucid_rope(dummy, s, 1, 1, 1, dummy, dummy, dummy, 128, 0, None)
+    rc = lib.lucid_rope(dummy, s, 1, 1, 1, dummy, dummy, dummy, s, 128, 0, None)
     assert rc == _lib.LUCID_EINVAL and b"head dim 64" in lib.lucid_last_error()
     odd = (ctypes.c_int64 * 3)(68, 68, 68)
-    rc = lib.lucid_rope(dummy, odd, 1, 1, 1, dummy, dummy, dummy, 64, 0, None)
+    rc = lib.lucid_rope(dummy, odd, 1, 1, 1, dummy, dummy, dummy, s, 64, 0, None)
+    assert rc == _lib.LUCID_EINVAL and b"multiples of 8" in lib.lucid_last_error()
+    rc = lib.lucid_rope(dummy, s, 1, 1, 1, dummy, dummy, dummy, odd, 64, 0, None)
     assert rc == _lib.LUCID_EINVAL and b"multiples of 8" in lib.lucid_last_error()
     rc = lib.lucid_swiglu_fwd(ctypes.c_void_p((1 << 20) + 2), dummy, dummy, 64, None)
     assert rc == _lib.LUCID_EINVAL and b"aligned" in lib.lucid_last_error()

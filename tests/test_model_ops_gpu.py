@@ -247,3 +247,28 @@ def test_empty_and_single_position_inputs():
     logits = torch.randn(2, 1, 64, dtype=torch.bfloat16, device="cuda")
     labels = torch.zeros(2, 1, dtype=torch.int64, device="cuda")
     assert torch.isnan(O.causal_lm_loss(logits, labels)).item() and torch.isnan(_ce_ref(logits, labels)).item()
+
+
+def test_qkv_rope_matches_split_and_rope():
+    """The fused split + rotary step gives the outputs and the qkv gradient of the split
+    followed by apply_rope, bit for bit (the same kernels; the gradient written in place)."""
+    B, T, Hq, Hkv = 2, 96, 4, 2
+    g = torch.Generator().manual_seed(21)
+    base = torch.randn(B, T, (Hq + 2 * Hkv) * 64, generator=g).to(torch.bfloat16).cuda()
+    emb = M.LlamaRotaryEmbedding(M.LucidConfig(hidden_size=Hq * 64, num_attention_heads=Hq, head_dim=64),
+                                 device="cuda")
+    cos, sin = emb(base, torch.arange(T, device="cuda")[None].expand(B, -1))
+    grads = [torch.randn(B, h, T, 64, generator=g).to(torch.bfloat16).cuda() for h in (Hq, Hkv, Hkv)]
+    outs = {}
+    for fused in (True, False):
+        qkv = base.clone().requires_grad_()
+        if fused:
+            q, k, v = O.qkv_rope(qkv, cos, sin, Hq * 64, Hkv * 64)
+        else:
+            q, k, v = (t.view(B, T, -1, 64).transpose(1, 2) for t in qkv.split((Hq * 64, Hkv * 64, Hkv * 64), -1))
+            q, k = O.apply_rope(q, cos, sin), O.apply_rope(k, cos, sin)
+        torch.autograd.backward((q, k, v), grads)
+        torch.cuda.synchronize()
+        outs[fused] = [q.detach(), k.detach(), v.detach(), qkv.grad]
+    for a, b in zip(outs[True], outs[False]):
+        assert torch.equal(a, b)
