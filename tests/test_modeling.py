@@ -92,6 +92,38 @@ def test_tiny_model_matches_float32_reference(hkv):
 
 
 @pytest.mark.gpu
+def test_fused_layers_model_matches_float32_reference():
+    """A decoder wide and long enough to take every fused path (hidden 512: the fused RMSNorm;
+    B T hidden >= 2^20: the stacked q/k/v GEMM with the fused split + rotary step; the fused
+    SwiGLU gate and loss) against the float32 reference model on the CPU, loss and gradients."""
+    torch.manual_seed(7)
+    cfg = M.LucidConfig(vocab_size=512, hidden_size=512, intermediate_size=1024, num_hidden_layers=2,
+                        num_attention_heads=8, num_key_value_heads=2, head_dim=64)
+    ref = M.LlamaForCausalLM(cfg)  # float32, CPU
+    ours = M.LlamaForCausalLM(cfg)
+    ours.load_state_dict(ref.state_dict())
+    ours = ours.to("cuda", torch.bfloat16)
+    T = 2048
+    assert T * cfg.hidden_size >= M._STACKED_QKV_MIN_NUMEL
+    ids = torch.randint(0, cfg.vocab_size, (1, T), generator=torch.Generator().manual_seed(8))
+    print(f"case fused-layer model T={T}", flush=True)
+    loss_ref, _ = _reference_forward(ref, ids, ids)
+    loss_ref.backward()
+    loss, _ = ours(ids.cuda(), labels=ids.cuda())
+    loss.backward()
+    torch.cuda.synchronize()
+    assert abs(loss.item() - loss_ref.item()) <= 1e-2 * abs(loss_ref.item()), (loss.item(), loss_ref.item())
+    for name in ("model.layers.0.self_attn.q_proj.weight", "model.layers.1.self_attn.k_proj.weight",
+                 "model.layers.0.self_attn.v_proj.weight", "model.layers.1.mlp.gate_proj.weight",
+                 "model.layers.0.input_layernorm.weight", "model.norm.weight", "model.embed_tokens.weight"):
+        gr = dict(ref.named_parameters())[name].grad.double()
+        go = dict(ours.named_parameters())[name].grad.double().cpu()
+        cos = torch.nn.functional.cosine_similarity(gr.flatten(), go.flatten(), dim=0).item()
+        rel = ((go - gr).norm() / gr.norm()).item()
+        assert cos > 0.99 and rel < 0.1, (name, cos, rel)
+
+
+@pytest.mark.gpu
 def test_decode_matches_prefill_logits():
     torch.manual_seed(3)
     cfg = _tiny(1)
